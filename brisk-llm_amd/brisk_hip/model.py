@@ -1,0 +1,159 @@
+"""Model configuration and tensor table from a GGUF file (host side).
+
+Restates the part of the reference's loader the HIP session needs:
+``Model::parse_config`` (src/model.cpp:161-301) for the families on the
+benchmark path (qwen3, llama, bitnet), the tensor names and shapes of
+``Model::Model`` (src/model.cpp:303-423) and the tied output projection
+(src/model.cpp:328-330).  The session takes the weights as GGUF-layout bytes,
+as the reference's ``Model(file, repack = false)`` hands them to a GPU session.
+"""
+from __future__ import annotations
+
+from dataclasses import dataclass
+
+from . import gguf as G
+
+ARCH_QWEN3, ARCH_LLAMA, ARCH_BITNET = 0, 1, 2
+_ARCH = {"qwen3": ARCH_QWEN3, "llama": ARCH_LLAMA, "bitnet": ARCH_BITNET, "bitnet-b1.58": ARCH_BITNET}
+QUANT_TYPES = (G.T_Q4_0, G.T_Q8_0, G.T_Q4_K, G.T_Q6_K, G.T_TQ2_0)
+
+
+class ModelError(RuntimeError):
+    pass
+
+
+def fail(what: str):
+    raise ModelError("model: " + what)  # src/model.cpp:18
+
+
+@dataclass
+class ModelConfig:
+    arch: int
+    arch_name: str
+    vocab: int
+    embd: int
+    layers: int
+    heads: int
+    kv_heads: int
+    head_dim: int
+    ff: int
+    context: int
+    rope_base: float
+    eps: float
+
+    @property
+    def rope_neox(self) -> bool:  # src/model.cpp:167
+        return self.arch != ARCH_LLAMA
+
+    @property
+    def query_dim(self) -> int:
+        return self.heads * self.head_dim
+
+    @property
+    def kv_dim(self) -> int:
+        return self.kv_heads * self.head_dim
+
+
+def parse_config(f: G.GgufFile) -> ModelConfig:
+    name = f.get("general.architecture")
+    if name not in _ARCH:
+        fail(f"unsupported architecture '{name}'; the HIP session runs qwen3, llama and bitnet")
+    p = name + "."
+
+    def u32(key):
+        v = f.get(p + key)
+        if v is None:
+            fail(f"missing metadata '{p + key}'")
+        return int(v)
+
+    def f32(key):
+        v = f.get(p + key)
+        if v is None:
+            fail(f"missing metadata '{p + key}'")
+        return float(v)
+
+    embd, layers, heads = u32("embedding_length"), u32("block_count"), u32("attention.head_count")
+    kv, ff, ctx = u32("attention.head_count_kv"), u32("feed_forward_length"), u32("context_length")
+    if 0 in (embd, layers, heads, kv, ff, ctx):
+        fail("a model dimension is zero")
+    if heads % kv:
+        fail("head_count is not a multiple of head_count_kv")
+    if heads // kv > 16:
+        fail("more than 16 query heads per key/value head is not supported")
+    head_dim = int(f.get(p + "attention.key_length", embd // heads))
+    if head_dim == 0 or head_dim % 32:
+        fail("head size must be a non-zero multiple of 32")
+    if int(f.get(p + "attention.value_length", head_dim)) != head_dim:
+        fail("key and value head sizes differ")
+    emb = f.tensor("token_embd.weight")
+    if emb is None or len(emb.dims) != 2 or emb.dims[0] != embd:
+        fail("missing or misshapen token_embd.weight")
+    return ModelConfig(_ARCH[name], name, int(emb.dims[1]), embd, layers, heads, kv, head_dim, ff, ctx,
+                       f32("rope.freq_base"), f32("attention.layer_norm_rms_epsilon"))
+
+
+@dataclass
+class TensorRef:
+    name: str
+    type: int
+    rows: int
+    cols: int
+    data: object  # numpy uint8 view of the GGUF bytes
+
+
+def tensor_table(f: G.GgufFile, cfg: ModelConfig) -> list:
+    """Every tensor the forward step reads, shape-checked as src/model.cpp:426-478 does."""
+    out = []
+
+    def vec(name, n):
+        t = f.tensor(name)
+        if t is None:
+            fail(f"missing tensor '{name}'")
+        if t.n_elements() != n:
+            fail(f"tensor '{name}' has an unexpected size")
+        if t.type != G.T_F32:
+            fail(f"tensor '{name}' has type {G.TYPE_NAMES.get(t.type, t.type)}; only F32 is supported here")
+        out.append(TensorRef(name, t.type, 1, n, t.data))
+
+    def mat(name, rows, cols):
+        t = f.tensor(name)
+        if t is None:
+            fail(f"missing tensor '{name}'")
+        if len(t.dims) != 2 or t.dims[0] != cols or t.dims[1] != rows:
+            fail(f"tensor '{name}' has an unexpected shape")
+        if t.type not in QUANT_TYPES:
+            fail(f"tensor '{name}' has type {G.TYPE_NAMES.get(t.type, t.type)}, which the HIP session does not take")
+        if cols % G.BLOCK[t.type][0]:
+            fail(f"tensor '{name}' row length is not a multiple of its block size")
+        out.append(TensorRef(name, t.type, rows, cols, t.data))
+
+    e, qd, kvd = cfg.embd, cfg.query_dim, cfg.kv_dim
+    mat("token_embd.weight", cfg.vocab, e)
+    vec("output_norm.weight", e)
+    if f.tensor("output.weight") is not None:
+        mat("output.weight", cfg.vocab, e)
+    for l in range(cfg.layers):
+        b = f"blk.{l}."
+        vec(b + "attn_norm.weight", e)
+        mat(b + "attn_q.weight", qd, e)
+        mat(b + "attn_k.weight", kvd, e)
+        mat(b + "attn_v.weight", kvd, e)
+        if cfg.arch == ARCH_QWEN3:
+            vec(b + "attn_q_norm.weight", cfg.head_dim)
+            vec(b + "attn_k_norm.weight", cfg.head_dim)
+        if cfg.arch == ARCH_BITNET:
+            vec(b + "attn_sub_norm.weight", e)
+            vec(b + "ffn_sub_norm.weight", cfg.ff)
+        mat(b + "attn_output.weight", e, qd)
+        vec(b + "ffn_norm.weight", e)
+        mat(b + "ffn_gate.weight", cfg.ff, e)
+        mat(b + "ffn_up.weight", cfg.ff, e)
+        mat(b + "ffn_down.weight", e, cfg.ff)
+    return out
+
+
+def load(path: str):
+    """(GgufFile, ModelConfig, tensor table) of a model file."""
+    f = G.GgufFile(path)
+    cfg = parse_config(f)
+    return f, cfg, tensor_table(f, cfg)

@@ -1,0 +1,280 @@
+"""Seeded random-weight GGUF models of the benchmark shapes.
+
+Every byte comes from a counter-based splitmix64 stream (integer arithmetic
+only) and exact float64 operations, so a file is byte-identical on every
+machine: the reference's CPU engine and the HIP session read the very same
+weights here and on the GPU host.  Tensor names, shapes and metadata keys are
+the ones the reference's loader reads (src/model.cpp:161-301, :303-423): GGUF
+dims innermost first, so a rows x cols matrix is stored as {cols, rows}
+(src/model.cpp:462).
+
+Distributions (where a config leaves a scale open it is
+pinned here so activations stay O(1) through the layers):
+  Q4_0  d = half(U(0.001, 0.02)), nibbles uniform 0..15
+  Q8_0  d = half(U(0.0002, 0.004)), values uniform -127..127
+  Q4_K  d, dmin = half(U(0.0001, 0.001)), 6-bit scales/mins and nibbles uniform
+  Q6_K  d = half(U(0.00002, 0.0002)), int8 sub-block scales uniform -32..31, 6-bit values uniform
+  TQ2_0 codes uniform over {0, 1, 2} (weights -1, 0, 1), one fp16 scale per tensor U(0.01, 0.03)
+  norm weights f32 U(0.8, 1.2)
+"""
+from __future__ import annotations
+
+import os
+from dataclasses import dataclass, field
+
+import numpy as np
+
+from . import gguf as G
+
+_GOLDEN = np.uint64(0x9E3779B97F4A7C15)
+_M1 = np.uint64(0xBF58476D1CE4E5B9)
+_M2 = np.uint64(0x94D049BB133111EB)
+
+
+def splitmix64(seed: int, n: int) -> np.ndarray:
+    """n outputs of splitmix64 started at ``seed`` (counter form: output i mixes seed + (i+1)*golden)."""
+    with np.errstate(over="ignore"):
+        z = np.arange(1, n + 1, dtype=np.uint64) * _GOLDEN + np.uint64(seed & 0xFFFFFFFFFFFFFFFF)
+        z = (z ^ (z >> np.uint64(30))) * _M1
+        z = (z ^ (z >> np.uint64(27))) * _M2
+        return z ^ (z >> np.uint64(31))
+
+
+def fnv1a64(text: str) -> int:
+    h = 0xCBF29CE484222325
+    for b in text.encode():
+        h = ((h ^ b) * 0x100000001B3) & 0xFFFFFFFFFFFFFFFF
+    return h
+
+
+def stream_seed(model_seed: int, name: str) -> int:
+    return (fnv1a64(name) ^ (model_seed * 0xD1B54A32D192ED03)) & 0xFFFFFFFFFFFFFFFF
+
+
+def random_bytes(seed: int, n: int) -> np.ndarray:
+    return splitmix64(seed, (n + 7) // 8).view(np.uint8)[:n]
+
+
+def random_unit(seed: int, n: int) -> np.ndarray:
+    """Uniform [0, 1) float64 with 53 random bits (exact)."""
+    return (splitmix64(seed, n) >> np.uint64(11)).astype(np.float64) * (1.0 / 9007199254740992.0)
+
+
+def random_uniform(seed: int, n: int, lo: float, hi: float) -> np.ndarray:
+    return lo + random_unit(seed, n) * (hi - lo)
+
+
+def random_normalish(seed: int, n: int) -> np.ndarray:
+    """Approximately N(0, 1): Irwin-Hall sum of four uniforms, centred and scaled (exact float64 ops only)."""
+    u = random_unit(seed, 4 * n).reshape(n, 4)
+    return (u.sum(axis=1) - 2.0) * 1.7320508075688772
+
+
+def half_bits(x: np.ndarray) -> np.ndarray:
+    """float64 -> float32 -> IEEE half (round to nearest even) as uint16."""
+    return x.astype(np.float32).astype(np.float16).view(np.uint16)
+
+
+# --------------------------------------------------------------------------- blocks
+
+def q4_0_blocks(seed: int, nblocks: int) -> np.ndarray:
+    out = np.empty((nblocks, 18), np.uint8)
+    out[:, 0:2] = half_bits(random_uniform(seed, nblocks, 0.001, 0.02)).view(np.uint8).reshape(nblocks, 2)
+    out[:, 2:18] = random_bytes(seed ^ 0x5151, nblocks * 16).reshape(nblocks, 16)
+    return out
+
+
+def q8_0_blocks(seed: int, nblocks: int, lo=0.0002, hi=0.004) -> np.ndarray:
+    out = np.empty((nblocks, 34), np.uint8)
+    out[:, 0:2] = half_bits(random_uniform(seed, nblocks, lo, hi)).view(np.uint8).reshape(nblocks, 2)
+    raw = random_bytes(seed ^ 0x5252, nblocks * 32).astype(np.int16)
+    out[:, 2:34] = ((raw % 255) - 127).astype(np.int8).view(np.uint8).reshape(nblocks, 32)
+    return out
+
+
+def q4_k_blocks(seed: int, nblocks: int) -> np.ndarray:
+    out = np.empty((nblocks, 144), np.uint8)
+    out[:, 0:2] = half_bits(random_uniform(seed, nblocks, 0.0001, 0.001)).view(np.uint8).reshape(nblocks, 2)
+    out[:, 2:4] = half_bits(random_uniform(seed ^ 0x1, nblocks, 0.0001, 0.001)).view(np.uint8).reshape(nblocks, 2)
+    out[:, 4:144] = random_bytes(seed ^ 0x5353, nblocks * 140).reshape(nblocks, 140)
+    return out
+
+
+def q6_k_blocks(seed: int, nblocks: int) -> np.ndarray:
+    out = np.empty((nblocks, 210), np.uint8)
+    out[:, 0:192] = random_bytes(seed ^ 0x5454, nblocks * 192).reshape(nblocks, 192)       # ql, qh
+    sc = (random_bytes(seed ^ 0x5555, nblocks * 16).astype(np.int16) % 64) - 32
+    out[:, 192:208] = sc.astype(np.int8).view(np.uint8).reshape(nblocks, 16)
+    out[:, 208:210] = half_bits(random_uniform(seed, nblocks, 0.00002, 0.0002)).view(np.uint8).reshape(nblocks, 2)
+    return out
+
+
+def tq2_0_blocks(seed: int, nblocks: int) -> np.ndarray:
+    out = np.empty((nblocks, 66), np.uint8)
+    codes = (splitmix64(seed ^ 0x5656, nblocks * 256) % np.uint64(3)).astype(np.uint8).reshape(nblocks, 4, 64)
+    # byte m of the 64 holds elements in bit pairs 2l (src/quant.h:123-130): we only need uniform
+    # codes, so pack four independent codes per byte.
+    packed = codes[:, 0] | (codes[:, 1] << 2) | (codes[:, 2] << 4) | (codes[:, 3] << 6)
+    out[:, 0:64] = packed
+    d = half_bits(random_uniform(seed ^ 0x77, 1, 0.01, 0.03))  # one scale per tensor
+    out[:, 64:66] = np.broadcast_to(d.view(np.uint8), (nblocks, 2))
+    return out
+
+
+BLOCK_MAKERS = {G.T_Q4_0: q4_0_blocks, G.T_Q8_0: q8_0_blocks, G.T_Q4_K: q4_k_blocks,
+                G.T_Q6_K: q6_k_blocks, G.T_TQ2_0: tq2_0_blocks}
+
+
+# --------------------------------------------------------------------------- models
+
+@dataclass
+class ModelSpec:
+    name: str
+    arch: str                 # general.architecture
+    embd: int
+    layers: int
+    heads: int
+    kv_heads: int
+    head_dim: int
+    ff: int
+    vocab: int
+    rope_base: float
+    eps: float = 1e-6
+    context: int = 40960
+    fmt: dict = field(default_factory=dict)   # role -> tensor type; roles: q k v o gate up down
+    embd_fmt: int = G.T_Q8_0
+    out_fmt: int | None = G.T_Q8_0            # None: tied to token_embd (src/model.cpp:328-330)
+    seed: int = 1
+
+    @property
+    def query_dim(self):
+        return self.heads * self.head_dim
+
+    @property
+    def kv_dim(self):
+        return self.kv_heads * self.head_dim
+
+    def layer_weight_bytes(self) -> int:
+        """Quantised bytes of one layer's seven matrices."""
+        shapes = {"q": (self.query_dim, self.embd), "k": (self.kv_dim, self.embd), "v": (self.kv_dim, self.embd),
+                  "o": (self.embd, self.query_dim), "gate": (self.ff, self.embd), "up": (self.ff, self.embd),
+                  "down": (self.embd, self.ff)}
+        total = 0
+        for role, (r, c) in shapes.items():
+            be, bb = G.BLOCK[self.fmt[role]]
+            total += r * c // be * bb
+        return total
+
+    def output_bytes(self) -> int:
+        t = self.out_fmt if self.out_fmt is not None else self.embd_fmt
+        be, bb = G.BLOCK[t]
+        return self.vocab * self.embd // be * bb
+
+    def decode_bytes(self, position: int) -> int:
+        """Algorithmic HBM bytes of one decode step at context length ``position`` (weights + norms + KV)."""
+        be, bb = G.BLOCK[self.embd_fmt]
+        norms = 4 * (2 * self.embd + (2 * self.head_dim if self.arch == "qwen3" else 0)) * self.layers + 4 * self.embd
+        if self.arch.startswith("bitnet"):
+            norms += 4 * (self.embd + self.ff) * self.layers
+        kv = 2 * 2 * self.kv_dim * self.layers * (position + 1)
+        return self.layers * self.layer_weight_bytes() + self.output_bytes() + self.embd // be * bb + norms + kv
+
+
+def _uniform4(t):
+    return {r: t for r in ("q", "k", "v", "o", "gate", "up", "down")}
+
+
+SPECS = {
+    # Qwen3-0.6B shape, Q4_0 layers, Q8_0 embeddings and output.
+    "qwen3-0.6b": ModelSpec("qwen3-0.6b", "qwen3", 1024, 28, 16, 8, 128, 3072, 151936, 1e6, fmt=_uniform4(G.T_Q4_0)),
+    # Llama-3.2-1B shape in a Q4_K_M mix; tied Q6_K embedding.
+    "llama-3.2-1b": ModelSpec("llama-3.2-1b", "llama", 2048, 16, 32, 8, 64, 8192, 128256, 5e5, eps=1e-5, context=131072,
+                              fmt={**_uniform4(G.T_Q4_K), "v": G.T_Q6_K, "down": G.T_Q6_K},
+                              embd_fmt=G.T_Q6_K, out_fmt=None),
+    # Qwen3-1.7B shape, all Q8_0.
+    "qwen3-1.7b": ModelSpec("qwen3-1.7b", "qwen3", 2048, 28, 16, 8, 128, 6144, 151936, 1e6, fmt=_uniform4(G.T_Q8_0)),
+    # BitNet b1.58 2B4T shape, TQ2_0 layers; tied Q4_0 embedding.
+    "bitnet-2b": ModelSpec("bitnet-2b", "bitnet-b1.58", 2560, 30, 20, 5, 128, 6912, 128256, 5e5, eps=1e-5, context=4096,
+                           fmt=_uniform4(G.T_TQ2_0), embd_fmt=G.T_Q4_0, out_fmt=None),
+    # Small shapes of each family for the parity tests (the oracle finishes them in well under a second).
+    "tiny-qwen3": ModelSpec("tiny-qwen3", "qwen3", 256, 2, 4, 2, 64, 512, 1000, 1e6, context=1024, fmt=_uniform4(G.T_Q4_0)),
+    "tiny-llama": ModelSpec("tiny-llama", "llama", 512, 2, 8, 2, 64, 768, 1000, 5e5, eps=1e-5, context=1024,
+                            fmt={**_uniform4(G.T_Q4_K), "v": G.T_Q6_K, "down": G.T_Q6_K}, embd_fmt=G.T_Q6_K, out_fmt=None),
+    "tiny-q8": ModelSpec("tiny-q8", "qwen3", 256, 2, 4, 2, 64, 512, 1000, 1e6, context=1024, fmt=_uniform4(G.T_Q8_0)),
+    "tiny-bitnet": ModelSpec("tiny-bitnet", "bitnet-b1.58", 512, 2, 4, 1, 128, 768, 1000, 5e5, eps=1e-5, context=1024,
+                             fmt=_uniform4(G.T_TQ2_0), embd_fmt=G.T_Q4_0, out_fmt=None),
+}
+
+
+def _matrix(w: G.GgufWriter, spec: ModelSpec, name: str, rows: int, cols: int, ttype: int):
+    be, _ = G.BLOCK[ttype]
+    nblocks = rows * cols // be
+    seed = stream_seed(spec.seed, name)
+    w.add_tensor(name, (cols, rows), ttype, lambda: BLOCK_MAKERS[ttype](seed, nblocks))
+
+
+def _vector(w: G.GgufWriter, spec: ModelSpec, name: str, n: int):
+    seed = stream_seed(spec.seed, name)
+    w.add_tensor(name, (n,), G.T_F32, lambda: random_uniform(seed, n, 0.8, 1.2).astype(np.float32).view(np.uint8))
+
+
+def write_model(spec: ModelSpec, path: str) -> str:
+    """Writes ``spec`` as a GGUF file at ``path`` (skipped when the file already exists)."""
+    if os.path.exists(path):
+        return path
+    a = spec.arch
+    w = G.GgufWriter()
+    w.add("general.architecture", G.STRING, a)
+    w.add("general.name", G.STRING, f"brisk-synthetic-{spec.name}")
+    w.add(f"{a}.embedding_length", G.U32, spec.embd)
+    w.add(f"{a}.block_count", G.U32, spec.layers)
+    w.add(f"{a}.attention.head_count", G.U32, spec.heads)
+    w.add(f"{a}.attention.head_count_kv", G.U32, spec.kv_heads)
+    w.add(f"{a}.attention.key_length", G.U32, spec.head_dim)
+    w.add(f"{a}.attention.value_length", G.U32, spec.head_dim)
+    w.add(f"{a}.feed_forward_length", G.U32, spec.ff)
+    w.add(f"{a}.context_length", G.U32, spec.context)
+    w.add(f"{a}.rope.freq_base", G.F32, spec.rope_base)
+    w.add(f"{a}.attention.layer_norm_rms_epsilon", G.F32, spec.eps)
+    _matrix(w, spec, "token_embd.weight", spec.vocab, spec.embd, spec.embd_fmt)
+    _vector(w, spec, "output_norm.weight", spec.embd)
+    if spec.out_fmt is not None:
+        _matrix(w, spec, "output.weight", spec.vocab, spec.embd, spec.out_fmt)
+    for l in range(spec.layers):
+        b = f"blk.{l}."
+        _vector(w, spec, b + "attn_norm.weight", spec.embd)
+        _matrix(w, spec, b + "attn_q.weight", spec.query_dim, spec.embd, spec.fmt["q"])
+        _matrix(w, spec, b + "attn_k.weight", spec.kv_dim, spec.embd, spec.fmt["k"])
+        _matrix(w, spec, b + "attn_v.weight", spec.kv_dim, spec.embd, spec.fmt["v"])
+        if a == "qwen3":
+            _vector(w, spec, b + "attn_q_norm.weight", spec.head_dim)
+            _vector(w, spec, b + "attn_k_norm.weight", spec.head_dim)
+        if a.startswith("bitnet"):
+            _vector(w, spec, b + "attn_sub_norm.weight", spec.embd)
+            _vector(w, spec, b + "ffn_sub_norm.weight", spec.ff)
+        _matrix(w, spec, b + "attn_output.weight", spec.embd, spec.query_dim, spec.fmt["o"])
+        _vector(w, spec, b + "ffn_norm.weight", spec.embd)
+        _matrix(w, spec, b + "ffn_gate.weight", spec.ff, spec.embd, spec.fmt["gate"])
+        _matrix(w, spec, b + "ffn_up.weight", spec.ff, spec.embd, spec.fmt["up"])
+        _matrix(w, spec, b + "ffn_down.weight", spec.embd, spec.ff, spec.fmt["down"])
+    tmp = path + ".part"
+    w.write(tmp)
+    os.replace(tmp, path)
+    return path
+
+
+def model_dir() -> str:
+    d = os.environ.get("BRISK_MODEL_DIR") or os.path.join(os.environ.get("TMPDIR", "/tmp"), "brisk_models")
+    os.makedirs(d, exist_ok=True)
+    return d
+
+
+def model_path(name: str) -> str:
+    """Path of the seeded model ``name``, written on first use."""
+    spec = SPECS[name]
+    return write_model(spec, os.path.join(model_dir(), f"{name}-s{spec.seed}.gguf"))
+
+
+def prompt_ids(n: int, vocab: int, seed: int = 7) -> np.ndarray:
+    """``n`` seeded random token ids in [0, vocab)."""
+    return (splitmix64(seed * 0x2545F4914F6CDD1D + 3, n) % np.uint64(vocab)).astype(np.int32)

@@ -1,0 +1,691 @@
+/* TEST INFRASTRUCTURE ONLY — the CPU oracle (see oracle.h).
+ *
+ * Plain C restatement of roticv/brisk-llm's x86 CPU path.  Each function cites
+ * the reference lines it follows.  Floating-point expressions keep the
+ * reference's evaluation order and types (float products and sums, double
+ * accumulators where it has them) so that, compiled like the reference
+ * (gcc -O3, no -march: no FMA contraction on x86-64), results are bit-identical
+ * to it.
+ */
+#include "oracle.h"
+
+#include <math.h>
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+
+static __thread char g_err[256];
+const char* or_last_error(void) { return g_err; }
+static int fail(const char* msg) {
+    snprintf(g_err, sizeof g_err, "%s", msg);
+    return -1;
+}
+
+/* ------------------------------------------------------------------ halves */
+
+/* src/quant.cpp:61-85 */
+float or_half_to_float(uint16_t half) {
+    uint32_t h = half, sign = (h & 0x8000u) << 16, exponent = (h >> 10) & 0x1F, mantissa = h & 0x3FF, bits;
+    if (exponent == 0x1F) {
+        bits = sign | 0x7F800000u | (mantissa << 13);
+    } else if (exponent != 0) {
+        bits = sign | ((exponent + 112) << 23) | (mantissa << 13);
+    } else if (mantissa != 0) {
+        exponent = 113;
+        while ((mantissa & 0x400) == 0) {
+            mantissa <<= 1;
+            --exponent;
+        }
+        bits = sign | (exponent << 23) | ((mantissa & 0x3FF) << 13);
+    } else {
+        bits = sign;
+    }
+    float out;
+    memcpy(&out, &bits, 4);
+    return out;
+}
+
+/* src/quant.cpp:87-113: round to nearest, ties to even. */
+uint16_t or_float_to_half(float f) {
+    uint32_t bits;
+    memcpy(&bits, &f, 4);
+    const uint32_t sign = (bits >> 16) & 0x8000u;
+    const int32_t exponent = (int32_t)((bits >> 23) & 0xFF) - 127 + 15;
+    uint32_t mantissa = bits & 0x7FFFFF;
+    if (((bits >> 23) & 0xFF) == 0xFF) return (uint16_t)(sign | 0x7C00u | (mantissa ? 0x200u : 0u));
+    if (exponent >= 0x1F) return (uint16_t)(sign | 0x7C00u);
+    if (exponent <= 0) {
+        if (exponent < -10) return (uint16_t)sign;
+        mantissa |= 0x800000u;
+        const uint32_t shift = (uint32_t)(14 - exponent);
+        uint32_t half = mantissa >> shift;
+        const uint32_t rem = mantissa & ((1u << shift) - 1), halfway = 1u << (shift - 1);
+        if (rem > halfway || (rem == halfway && (half & 1))) ++half;
+        return (uint16_t)(sign | half);
+    }
+    uint32_t half = ((uint32_t)exponent << 10) | (mantissa >> 13);
+    const uint32_t rem = mantissa & 0x1FFF;
+    if (rem > 0x1000 || (rem == 0x1000 && (half & 1))) ++half;
+    return (uint16_t)(sign | half);
+}
+
+static inline uint16_t rd16(const uint8_t* p) { return (uint16_t)(p[0] | (p[1] << 8)); }
+
+/* ------------------------------------------------------------------ activation quantisation */
+
+/* src/quant.cpp:115-142 (portable branch).  Block = {u16 d, i8 qs[32]} (34 bytes). */
+void or_quantize_q8_0(const float* x, void* out_, size_t count) {
+    uint8_t* out = (uint8_t*)out_;
+    for (size_t b = 0; b < count / 32; ++b) {
+        const float* block = x + b * 32;
+        float amax = 0.0f;
+        for (int i = 0; i < 32; ++i) amax = fmaxf(amax, fabsf(block[i]));
+        const float d = amax / 127.0f;
+        const float inverse = d != 0.0f ? 1.0f / d : 0.0f;
+        const uint16_t dh = or_float_to_half(d);
+        uint8_t* o = out + b * 34;
+        o[0] = (uint8_t)dh;
+        o[1] = (uint8_t)(dh >> 8);
+        for (int i = 0; i < 32; ++i) o[2 + i] = (uint8_t)(int8_t)nearbyintf(block[i] * inverse);
+    }
+}
+
+/* src/quant.cpp:146-194 (portable branch).  Block = {f32 d, i8 qs[256], i16 bsums[16]} (292 bytes). */
+void or_quantize_q8_k(const float* x, void* out_, size_t count, int bits) {
+    uint8_t* out = (uint8_t*)out_;
+    for (size_t b = 0; b < count / 256; ++b) {
+        const float* block = x + b * 256;
+        uint8_t* y = out + b * 292;
+        float max = 0.0f, amax = 0.0f;
+        for (int i = 0; i < 256; ++i) {
+            const float ax = fabsf(block[i]);
+            if (ax > amax) {
+                amax = ax;
+                max = block[i];
+            }
+        }
+        if (amax == 0.0f) {
+            memset(y, 0, 292);
+            continue;
+        }
+        const float extreme = bits == 7 ? 63.0f : 127.0f;
+        const float inverse = -extreme / max;
+        const float d = 1.0f / inverse;
+        memcpy(y, &d, 4);
+        int8_t* qs = (int8_t*)(y + 4);
+        for (int i = 0; i < 256; ++i) qs[i] = (int8_t)fminf(127.0f, nearbyintf(inverse * block[i]));
+        for (int g = 0; g < 16; ++g) {
+            int sum = 0;
+            for (int i = 0; i < 16; ++i) sum += qs[g * 16 + i];
+            const int16_t s16 = (int16_t)sum;
+            memcpy(y + 260 + 2 * g, &s16, 2);
+        }
+    }
+}
+
+/* ------------------------------------------------------------------ dots */
+
+/* src/quant.cpp:445-456.  Q4_0 = {u16 d, u8 qs[16]}: low nibbles elements 0-15, high 16-31. */
+static float dot_q4_0(const uint8_t* w, const uint8_t* x, size_t blocks) {
+    float sum = 0.0f;
+    for (size_t b = 0; b < blocks; ++b) {
+        const uint8_t* wb = w + b * 18;
+        const uint8_t* xb = x + b * 34;
+        const int8_t* xq = (const int8_t*)(xb + 2);
+        int32_t acc = 0;
+        for (int i = 0; i < 16; ++i) {
+            acc += ((wb[2 + i] & 0x0F) - 8) * xq[i];
+            acc += ((wb[2 + i] >> 4) - 8) * xq[i + 16];
+        }
+        sum += (float)acc * or_half_to_float(rd16(wb)) * or_half_to_float(rd16(xb));
+    }
+    return sum;
+}
+
+/* src/quant.cpp:474-482 */
+static float dot_q8_0(const uint8_t* w, const uint8_t* x, size_t blocks) {
+    float sum = 0.0f;
+    for (size_t b = 0; b < blocks; ++b) {
+        const uint8_t* wb = w + b * 34;
+        const uint8_t* xb = x + b * 34;
+        const int8_t* wq = (const int8_t*)(wb + 2);
+        const int8_t* xq = (const int8_t*)(xb + 2);
+        int32_t acc = 0;
+        for (int i = 0; i < 32; ++i) acc += wq[i] * xq[i];
+        sum += (float)acc * or_half_to_float(rd16(wb)) * or_half_to_float(rd16(xb));
+    }
+    return sum;
+}
+
+/* src/quant.h:256-264 */
+static void q4_k_scale_min(const uint8_t* scales, int j, uint8_t* scale, uint8_t* min) {
+    if (j < 4) {
+        *scale = scales[j] & 63;
+        *min = scales[j + 4] & 63;
+    } else {
+        *scale = (uint8_t)((scales[j + 4] & 0xF) | ((scales[j - 4] >> 6) << 4));
+        *min = (uint8_t)((scales[j + 4] >> 4) | ((scales[j] >> 6) << 4));
+    }
+}
+
+static inline float q8k_d(const uint8_t* xb) {
+    float d;
+    memcpy(&d, xb, 4);
+    return d;
+}
+static inline int16_t q8k_bsum(const uint8_t* xb, int g) {
+    int16_t s;
+    memcpy(&s, xb + 260 + 2 * g, 2);
+    return s;
+}
+
+/* src/quant.cpp:500-521.  Q4_K = {u16 d, u16 dmin, u8 scales[12], u8 qs[128]}. */
+static float dot_q4_k(const uint8_t* w, const uint8_t* x, size_t blocks) {
+    float sum = 0.0f;
+    for (size_t b = 0; b < blocks; ++b) {
+        const uint8_t* wb = w + b * 144;
+        const uint8_t* xb = x + b * 292;
+        const int8_t* xqs = (const int8_t*)(xb + 4);
+        int32_t weighted = 0, offsets = 0;
+        for (int sb = 0; sb < 8; ++sb) {
+            uint8_t scale, min;
+            q4_k_scale_min(wb + 4, sb, &scale, &min);
+            const uint8_t* q = wb + 16 + (sb / 2) * 32;
+            const int8_t* xq = xqs + sb * 32;
+            int32_t dot = 0;
+            for (int i = 0; i < 32; ++i) dot += ((sb % 2 == 0) ? (q[i] & 0xF) : (q[i] >> 4)) * xq[i];
+            weighted += scale * dot;
+            offsets += min * (q8k_bsum(xb, 2 * sb) + q8k_bsum(xb, 2 * sb + 1));
+        }
+        sum += q8k_d(xb) * (or_half_to_float(rd16(wb)) * (float)weighted - or_half_to_float(rd16(wb + 2)) * (float)offsets);
+    }
+    return sum;
+}
+
+/* src/quant.cpp:285-297.  Q6_K = {u8 ql[128], u8 qh[64], i8 scales[16], u16 d}. */
+static void unpack_q6_k(const uint8_t* block, int8_t* q) {
+    for (int half = 0; half < 2; ++half) {
+        const uint8_t* ql = block + half * 64;
+        const uint8_t* qh = block + 128 + half * 32;
+        int8_t* y = q + half * 128;
+        for (int l = 0; l < 32; ++l) {
+            y[l] = (int8_t)(((ql[l] & 0xF) | (((qh[l] >> 0) & 3) << 4)) - 32);
+            y[l + 32] = (int8_t)(((ql[l + 32] & 0xF) | (((qh[l] >> 2) & 3) << 4)) - 32);
+            y[l + 64] = (int8_t)(((ql[l] >> 4) | (((qh[l] >> 4) & 3) << 4)) - 32);
+            y[l + 96] = (int8_t)(((ql[l + 32] >> 4) | (((qh[l] >> 6) & 3) << 4)) - 32);
+        }
+    }
+}
+
+/* src/quant.cpp:549-563 */
+static float dot_q6_k(const uint8_t* w, const uint8_t* x, size_t blocks) {
+    int8_t q[256];
+    float sum = 0.0f;
+    for (size_t b = 0; b < blocks; ++b) {
+        const uint8_t* wb = w + b * 210;
+        const uint8_t* xb = x + b * 292;
+        const int8_t* xq = (const int8_t*)(xb + 4);
+        const int8_t* scales = (const int8_t*)(wb + 192);
+        unpack_q6_k(wb, q);
+        int32_t weighted = 0;
+        for (int g = 0; g < 16; ++g) {
+            int32_t dot = 0;
+            for (int i = 0; i < 16; ++i) dot += q[g * 16 + i] * xq[g * 16 + i];
+            weighted += scales[g] * dot;
+        }
+        sum += q8k_d(xb) * or_half_to_float(rd16(wb + 208)) * (float)weighted;
+    }
+    return sum;
+}
+
+/* Element e of a TQ2_0 block {u8 qs[64], u16 d}: byte j + m (j in {0, 32}) holds elements
+ * 128 (j/32) + 32 l + m at bit pair 2l (src/quant.h:123-130, src/quant.cpp:566-578). */
+static inline int tq2_code(const uint8_t* wb, int e) {
+    const int j = (e / 128) * 32, l = (e % 128) / 32, m = e % 32;
+    return (wb[j + m] >> (2 * l)) & 3;
+}
+
+/* src/quant.cpp:580-596: the generic TQ2_0 dot (8-bit activations). */
+static float dot_tq2_0(const uint8_t* w, const uint8_t* x, size_t blocks) {
+    float sum = 0.0f;
+    for (size_t b = 0; b < blocks; ++b) {
+        const uint8_t* wb = w + b * 66;
+        const uint8_t* xb = x + b * 292;
+        const int8_t* xq = (const int8_t*)(xb + 4);
+        int32_t acc = 0;
+        for (int e = 0; e < 256; ++e) acc += tq2_code(wb, e) * xq[e];
+        int32_t xsum = 0;
+        for (int g = 0; g < 16; ++g) xsum += q8k_bsum(xb, g);
+        sum += q8k_d(xb) * or_half_to_float(rd16(wb + 64)) * (float)(acc - xsum);
+    }
+    return sum;
+}
+
+/* src/quant.cpp:789-802 on the TQ2_0x16 layout, restated on the GGUF block: the pair
+ * index idx = c0 * 3 + c1 gives weights idx/3 - 1 and idx%3 - 1, i.e. the two codes
+ * minus one, so acc is the same integer; the float order is acc * d_w * d_x. */
+static float dot_tq2_0x16(const uint8_t* w, const uint8_t* x, size_t blocks) {
+    float sum = 0.0f;
+    for (size_t b = 0; b < blocks; ++b) {
+        const uint8_t* wb = w + b * 66;
+        const uint8_t* xb = x + b * 292;
+        const int8_t* xq = (const int8_t*)(xb + 4);
+        int32_t acc = 0;
+        for (int e = 0; e < 256; ++e) acc += (tq2_code(wb, e) - 1) * xq[e];
+        sum += (float)acc * or_half_to_float(rd16(wb + 64)) * q8k_d(xb);
+    }
+    return sum;
+}
+
+float or_dot(int type, int lut16, const void* w, const void* x, size_t blocks) {
+    switch (type) {
+        case OR_Q4_0: return dot_q4_0((const uint8_t*)w, (const uint8_t*)x, blocks);
+        case OR_Q8_0: return dot_q8_0((const uint8_t*)w, (const uint8_t*)x, blocks);
+        case OR_Q4_K: return dot_q4_k((const uint8_t*)w, (const uint8_t*)x, blocks);
+        case OR_Q6_K: return dot_q6_k((const uint8_t*)w, (const uint8_t*)x, blocks);
+        case OR_TQ2_0: return lut16 ? dot_tq2_0x16((const uint8_t*)w, (const uint8_t*)x, blocks)
+                                    : dot_tq2_0((const uint8_t*)w, (const uint8_t*)x, blocks);
+    }
+    return NAN;
+}
+
+static size_t block_elems(int type) { return (type == OR_Q4_0 || type == OR_Q8_0) ? 32 : 256; }
+static size_t block_bytes(int type) {
+    switch (type) {
+        case OR_Q4_0: return 18;
+        case OR_Q8_0: return 34;
+        case OR_Q4_K: return 144;
+        case OR_Q6_K: return 210;
+        case OR_TQ2_0: return 66;
+    }
+    return 0;
+}
+
+/* src/model.cpp:496-503 + src/quant.cpp:144: on x86, TQ2_0 matrices with rows % 16 == 0 are
+ * repacked to TQ2_0x16, whose kernels take 7-bit activations. */
+int or_activation_bits(int type, size_t rows) { return (type == OR_TQ2_0 && rows % 16 == 0) ? 7 : 8; }
+static int takes_q8_k(int type) { return type == OR_Q4_K || type == OR_Q6_K || type == OR_TQ2_0; }
+
+/* matvec_generic (src/kernels.cpp:13-19) */
+void or_matvec(int type, const void* w, size_t rows, size_t cols, const void* x, float* out) {
+    const size_t blocks = cols / block_elems(type), rb = blocks * block_bytes(type);
+    const int lut16 = type == OR_TQ2_0 && rows % 16 == 0;
+    for (size_t r = 0; r < rows; ++r) out[r] = or_dot(type, lut16, (const uint8_t*)w + r * rb, x, blocks);
+}
+
+/* src/quant.cpp:196-239, :299-307, :566-578 */
+void or_dequantize(int type, const void* blocks_, float* out, size_t count) {
+    const uint8_t* blocks = (const uint8_t*)blocks_;
+    const size_t nb = count / block_elems(type);
+    for (size_t b = 0; b < nb; ++b) {
+        float* y = out + b * block_elems(type);
+        const uint8_t* wb = blocks + b * block_bytes(type);
+        switch (type) {
+            case OR_Q4_0: {
+                const float d = or_half_to_float(rd16(wb));
+                for (int i = 0; i < 16; ++i) {
+                    y[i] = (float)((wb[2 + i] & 0x0F) - 8) * d;
+                    y[i + 16] = (float)((wb[2 + i] >> 4) - 8) * d;
+                }
+                break;
+            }
+            case OR_Q8_0: {
+                const float d = or_half_to_float(rd16(wb));
+                for (int i = 0; i < 32; ++i) y[i] = (float)((const int8_t*)(wb + 2))[i] * d;
+                break;
+            }
+            case OR_Q4_K: {
+                const float d = or_half_to_float(rd16(wb)), dmin = or_half_to_float(rd16(wb + 2));
+                for (int chunk = 0; chunk < 4; ++chunk) {
+                    uint8_t scale, min;
+                    q4_k_scale_min(wb + 4, 2 * chunk, &scale, &min);
+                    const float d1 = d * scale, m1 = dmin * min;
+                    q4_k_scale_min(wb + 4, 2 * chunk + 1, &scale, &min);
+                    const float d2 = d * scale, m2 = dmin * min;
+                    const uint8_t* q = wb + 16 + chunk * 32;
+                    for (int i = 0; i < 32; ++i) {
+                        y[chunk * 64 + i] = d1 * (float)(q[i] & 0xF) - m1;
+                        y[chunk * 64 + 32 + i] = d2 * (float)(q[i] >> 4) - m2;
+                    }
+                }
+                break;
+            }
+            case OR_Q6_K: {
+                int8_t q[256];
+                const float d = or_half_to_float(rd16(wb + 208));
+                const int8_t* scales = (const int8_t*)(wb + 192);
+                unpack_q6_k(wb, q);
+                for (int i = 0; i < 256; ++i) y[i] = d * scales[i / 16] * q[i];
+                break;
+            }
+            case OR_TQ2_0: {
+                const float d = or_half_to_float(rd16(wb + 64));
+                for (int e = 0; e < 256; ++e) y[e] = (float)(tq2_code(wb, e) - 1) * d;
+                break;
+            }
+        }
+    }
+}
+
+/* tq2_0_pair_indices + repack_tq2_0x16_scalar (src/quant.cpp:636-672): 16 rows per group,
+ * byte (p/2)*16 + r holds row r's pair indices 2k (low nibble) and 2k+1 (high), then d[16]. */
+void or_repack_tq2_0x16(const void* in_, size_t rows, size_t blocks, void* out_) {
+    const uint8_t* in = (const uint8_t*)in_;
+    uint8_t* out = (uint8_t*)out_;
+    for (size_t g = 0; g < rows / 16; ++g) {
+        for (size_t b = 0; b < blocks; ++b) {
+            uint8_t* packed = out + (g * blocks + b) * 1056;
+            memset(packed, 0, 1024);
+            for (size_t r = 0; r < 16; ++r) {
+                const uint8_t* block = in + ((g * 16 + r) * blocks + b) * 66;
+                memcpy(packed + 1024 + 2 * r, block + 64, 2);
+                for (int p = 0; p < 128; p += 2) {
+                    const int i0 = tq2_code(block, 2 * p) * 3 + tq2_code(block, 2 * p + 1);
+                    const int i1 = tq2_code(block, 2 * p + 2) * 3 + tq2_code(block, 2 * p + 3);
+                    packed[(p / 2) * 16 + r] = (uint8_t)(i0 | (i1 << 4));
+                }
+            }
+        }
+    }
+}
+
+/* ------------------------------------------------------------------ float kernels */
+
+/* dot_f32, portable branch (src/kernels_f32.cpp:231-243): 16 lane partials, tail, then lanes in order. */
+float or_dot_f32(const float* a, const float* b, size_t n) {
+    float lanes[16] = {0};
+    size_t i = 0;
+    for (; i + 16 <= n; i += 16)
+        for (int j = 0; j < 16; ++j) lanes[j] += a[i + j] * b[i + j];
+    float sum = 0.0f;
+    for (; i < n; ++i) sum += a[i] * b[i];
+    for (int j = 0; j < 16; ++j) sum += lanes[j];
+    return sum;
+}
+
+/* softmax_f32 (src/kernels_f32.cpp:276-284) */
+void or_softmax(float* x, size_t n) {
+    float max = x[0];
+    for (size_t i = 1; i < n; ++i)
+        if (x[i] > max) max = x[i];
+    double sum = 0.0;
+    for (size_t i = 0; i < n; ++i) {
+        x[i] = expf(x[i] - max);
+        sum += x[i];
+    }
+    const float scale = (float)(1.0 / sum);
+    for (size_t i = 0; i < n; ++i) x[i] *= scale;
+}
+
+/* rms_norm (src/model.cpp:87-97): squares in float, summed in double. x and out may alias. */
+void or_rms_norm(const float* x, const float* w, float eps, float* out, size_t n) {
+    double sum = 0.0;
+    for (size_t i = 0; i < n; ++i) sum += (double)(x[i] * x[i]);
+    const float mean = (float)(sum / (double)n);
+    const float scale = 1.0f / sqrtf(mean + eps);
+    for (size_t i = 0; i < n; ++i) out[i] = x[i] * scale * w[i];
+}
+
+/* apply_rope (src/model.cpp:104-115) */
+static void apply_rope(float* head, const float* rope, size_t dim, int neox) {
+    const size_t half = dim / 2;
+    for (size_t i = 0; i < half; ++i) {
+        const float c = rope[2 * i], s = rope[2 * i + 1];
+        float* a = &head[neox ? i : 2 * i];
+        float* b = &head[neox ? i + half : 2 * i + 1];
+        const float x0 = *a, x1 = *b;
+        *a = x0 * c - x1 * s;
+        *b = x0 * s + x1 * c;
+    }
+}
+
+/* ------------------------------------------------------------------ session */
+
+typedef struct {
+    int type;
+    size_t rows, cols;
+    const uint8_t* data;
+} matrix;
+
+typedef struct {
+    const float *attn_norm, *q_norm, *k_norm, *attn_sub_norm, *ffn_norm, *ffn_sub_norm;
+    matrix q, k, v, o, gate, up, down;
+} layer_t;
+
+struct oracle_session {
+    oracle_config c;
+    matrix embd, out;
+    const float* out_norm;
+    layer_t* layers;
+    uint16_t **kcache, **vcache;
+    size_t position;
+    /* scratch */
+    float *h, *normed, *q, *k, *v, *att, *proj, *gate, *up, *scores, *rope;
+    uint8_t* xq;
+};
+
+static const oracle_tensor* find(const oracle_tensor* t, size_t n, const char* name) {
+    for (size_t i = 0; i < n; ++i)
+        if (strcmp(t[i].name, name) == 0) return &t[i];
+    return NULL;
+}
+
+oracle_session* or_session_create(const oracle_config* cfg, const oracle_tensor* t, size_t n) {
+    oracle_session* s = (oracle_session*)calloc(1, sizeof *s);
+    s->c = *cfg;
+    const oracle_config* c = cfg;
+    char name[128];
+#define GETM(dst, nm)                                                                    \
+    do {                                                                                 \
+        const oracle_tensor* x_ = find(t, n, nm);                                        \
+        if (!x_) { snprintf(g_err, sizeof g_err, "missing tensor '%s'", nm); goto bad; } \
+        (dst).type = x_->type; (dst).rows = x_->rows; (dst).cols = x_->cols;              \
+        (dst).data = (const uint8_t*)x_->data;                                           \
+    } while (0)
+#define GETV(dst, nm)                                                                    \
+    do {                                                                                 \
+        const oracle_tensor* x_ = find(t, n, nm);                                        \
+        if (!x_) { snprintf(g_err, sizeof g_err, "missing tensor '%s'", nm); goto bad; } \
+        (dst) = (const float*)x_->data;                                                  \
+    } while (0)
+    GETM(s->embd, "token_embd.weight");
+    if (find(t, n, "output.weight")) GETM(s->out, "output.weight");
+    else s->out = s->embd;  /* src/model.cpp:328-330 */
+    GETV(s->out_norm, "output_norm.weight");
+    s->layers = (layer_t*)calloc((size_t)c->layers, sizeof(layer_t));
+    for (int l = 0; l < c->layers; ++l) {
+        layer_t* L = &s->layers[l];
+#define LN(sfx) (snprintf(name, sizeof name, "blk.%d.%s", l, sfx), name)
+        GETV(L->attn_norm, LN("attn_norm.weight"));
+        GETM(L->q, LN("attn_q.weight"));
+        GETM(L->k, LN("attn_k.weight"));
+        GETM(L->v, LN("attn_v.weight"));
+        GETM(L->o, LN("attn_output.weight"));
+        GETV(L->ffn_norm, LN("ffn_norm.weight"));
+        GETM(L->gate, LN("ffn_gate.weight"));
+        GETM(L->up, LN("ffn_up.weight"));
+        GETM(L->down, LN("ffn_down.weight"));
+        if (c->arch == OR_QWEN3) {
+            GETV(L->q_norm, LN("attn_q_norm.weight"));
+            GETV(L->k_norm, LN("attn_k_norm.weight"));
+        }
+        if (c->arch == OR_BITNET) {
+            GETV(L->attn_sub_norm, LN("attn_sub_norm.weight"));
+            GETV(L->ffn_sub_norm, LN("ffn_sub_norm.weight"));
+        }
+    }
+    {
+        const size_t kvsz = (size_t)c->kv_heads * c->max_context * c->head_dim;
+        s->kcache = (uint16_t**)calloc((size_t)c->layers, sizeof(uint16_t*));
+        s->vcache = (uint16_t**)calloc((size_t)c->layers, sizeof(uint16_t*));
+        for (int l = 0; l < c->layers; ++l) {
+            s->kcache[l] = (uint16_t*)calloc(kvsz, 2);
+            s->vcache[l] = (uint16_t*)calloc(kvsz, 2);
+        }
+        const size_t qd = (size_t)c->heads * c->head_dim, kvd = (size_t)c->kv_heads * c->head_dim;
+        const size_t wide = (size_t)(c->embd > c->ff ? c->embd : c->ff) + qd;
+        s->h = (float*)calloc(c->embd, 4);
+        s->normed = (float*)calloc(c->embd, 4);
+        s->q = (float*)calloc(qd, 4);
+        s->k = (float*)calloc(kvd, 4);
+        s->v = (float*)calloc(kvd, 4);
+        s->att = (float*)calloc(qd, 4);
+        s->proj = (float*)calloc(c->embd, 4);
+        s->gate = (float*)calloc(c->ff, 4);
+        s->up = (float*)calloc(c->ff, 4);
+        s->scores = (float*)calloc((size_t)c->max_context, 4);
+        s->rope = (float*)calloc(c->head_dim, 4);
+        s->xq = (uint8_t*)calloc(wide / 32 * 34 + wide / 256 * 292 + 1024, 1);
+    }
+    return s;
+bad:
+    or_session_destroy(s);
+    return NULL;
+#undef GETM
+#undef GETV
+#undef LN
+}
+
+void or_session_destroy(oracle_session* s) {
+    if (!s) return;
+    if (s->kcache)
+        for (int l = 0; l < s->c.layers; ++l) free(s->kcache[l]);
+    if (s->vcache)
+        for (int l = 0; l < s->c.layers; ++l) free(s->vcache[l]);
+    free(s->kcache);
+    free(s->vcache);
+    free(s->layers);
+    free(s->h); free(s->normed); free(s->q); free(s->k); free(s->v); free(s->att);
+    free(s->proj); free(s->gate); free(s->up); free(s->scores); free(s->rope); free(s->xq);
+    free(s);
+}
+
+size_t or_session_position(const oracle_session* s) { return s->position; }
+void or_session_set_position(oracle_session* s, size_t p) { s->position = p; }
+uint16_t* or_session_kv(oracle_session* s, int layer, int value) { return value ? s->vcache[layer] : s->kcache[layer]; }
+
+int or_session_rollback(oracle_session* s, size_t position) {
+    if (position > s->position) return fail("model: cannot roll forward"); /* src/model.cpp:736 */
+    s->position = position;
+    return 0;
+}
+
+/* Session::multiply (src/model.cpp:546-653) for one token: quantise x to the matrix's
+ * activation format, then the generic matvec. */
+static void multiply(oracle_session* s, const matrix* m, const float* x, float* out) {
+    if (takes_q8_k(m->type)) or_quantize_q8_k(x, s->xq, m->cols, or_activation_bits(m->type, m->rows));
+    else or_quantize_q8_0(x, s->xq, m->cols);
+    or_matvec(m->type, m->data, m->rows, m->cols, s->xq, out);
+}
+
+/* embedding_row (src/model.cpp:27-70) */
+static void embedding_row(const matrix* m, size_t r, float* out) {
+    const size_t rb = m->cols / block_elems(m->type) * block_bytes(m->type);
+    or_dequantize(m->type, m->data + r * rb, out, m->cols);
+}
+
+/* One token of Session::eval_batch (src/model.cpp:867-1212) at position s->position.  Every
+ * computation of eval_batch is per token (matmul_generic runs the matvec dot per token,
+ * attention rows only see their own visible range), so a batch equals its tokens in order. */
+static void forward_token(oracle_session* s, int32_t token, float* logits) {
+    const oracle_config* c = &s->c;
+    const size_t embd = c->embd, hd = c->head_dim, qd = (size_t)c->heads * hd, kvd = (size_t)c->kv_heads * hd;
+    const size_t hpk = (size_t)(c->heads / c->kv_heads), pos = s->position, ctx = (size_t)c->max_context;
+    const int neox = c->arch != OR_LLAMA; /* src/model.cpp:167 */
+    const float attention_scale = 1.0f / sqrtf((float)hd);
+
+    /* build_rope (src/model.cpp:880-894), scale 1, attn factor 1, no factors */
+    {
+        const float theta_scale = powf(c->rope_base, -2.0f / (float)hd);
+        float theta = (float)pos * 1.0f;
+        for (size_t i = 0; i < hd / 2; ++i) {
+            s->rope[2 * i] = cosf(theta) * 1.0f;
+            s->rope[2 * i + 1] = sinf(theta) * 1.0f;
+            theta *= theta_scale;
+        }
+    }
+    embedding_row(&s->embd, (size_t)token, s->h);
+
+    for (int l = 0; l < c->layers; ++l) {
+        const layer_t* L = &s->layers[l];
+        or_rms_norm(s->h, L->attn_norm, c->eps, s->normed, embd);
+        multiply(s, &L->q, s->normed, s->q);
+        multiply(s, &L->k, s->normed, s->k);
+        multiply(s, &L->v, s->normed, s->v);
+        for (int h = 0; h < c->heads; ++h) {
+            float* q = s->q + h * hd;
+            if (L->q_norm) or_rms_norm(q, L->q_norm, c->eps, q, hd);
+            apply_rope(q, s->rope, hd, neox);
+        }
+        for (int h = 0; h < c->kv_heads; ++h) {
+            float* k = s->k + h * hd;
+            const float* v = s->v + h * hd;
+            if (L->k_norm) or_rms_norm(k, L->k_norm, c->eps, k, hd);
+            apply_rope(k, s->rope, hd, neox);
+            uint16_t* kr = s->kcache[l] + ((size_t)h * ctx + pos) * hd;
+            uint16_t* vr = s->vcache[l] + ((size_t)h * ctx + pos) * hd;
+            for (size_t i = 0; i < hd; ++i) {
+                kr[i] = or_float_to_half(k[i]);
+                vr[i] = or_float_to_half(v[i]);
+            }
+        }
+        /* attention (src/model.cpp:1050-1093, src/kernels_f32.cpp:256-284) */
+        {
+            const size_t visible = pos + 1;
+            float* key = s->proj; /* free until the output projection */
+            for (int h = 0; h < c->heads; ++h) {
+                const size_t kv = (size_t)h / hpk;
+                const float* q = s->q + h * hd;
+                for (size_t p = 0; p < visible; ++p) {
+                    const uint16_t* kr = s->kcache[l] + (kv * ctx + p) * hd;
+                    for (size_t i = 0; i < hd; ++i) key[i] = or_half_to_float(kr[i]);
+                    s->scores[p] = or_dot_f32(q, key, hd) * attention_scale;
+                }
+                or_softmax(s->scores, visible);
+                float* out = s->att + h * hd;
+                for (size_t i = 0; i < hd; ++i) out[i] = 0.0f;
+                for (size_t p = 0; p < visible; ++p) {
+                    const uint16_t* vr = s->vcache[l] + (kv * ctx + p) * hd;
+                    const float w = s->scores[p];
+                    for (size_t i = 0; i < hd; ++i) out[i] += w * or_half_to_float(vr[i]);
+                }
+            }
+        }
+        if (L->attn_sub_norm) or_rms_norm(s->att, L->attn_sub_norm, c->eps, s->att, qd);
+        multiply(s, &L->o, s->att, s->proj);
+        for (size_t i = 0; i < embd; ++i) s->h[i] += s->proj[i];
+        or_rms_norm(s->h, L->ffn_norm, c->eps, s->normed, embd);
+        multiply(s, &L->gate, s->normed, s->gate);
+        multiply(s, &L->up, s->normed, s->up);
+        for (int i = 0; i < c->ff; ++i) { /* src/model.cpp:1128-1143, src/kernels_f32.cpp:287-289 */
+            const float g = s->gate[i];
+            if (c->arch == OR_BITNET) {
+                const float r = g > 0.0f ? g : 0.0f;
+                s->gate[i] = r * r * s->up[i];
+            } else {
+                s->gate[i] = g / (1.0f + expf(-g)) * s->up[i];
+            }
+        }
+        if (L->ffn_sub_norm) or_rms_norm(s->gate, L->ffn_sub_norm, c->eps, s->gate, c->ff);
+        multiply(s, &L->down, s->gate, s->proj);
+        for (size_t i = 0; i < embd; ++i) s->h[i] += s->proj[i];
+        (void)kvd;
+    }
+    if (logits) {
+        or_rms_norm(s->h, s->out_norm, c->eps, s->normed, embd);
+        multiply(s, &s->out, s->normed, logits);
+    }
+    s->position += 1;
+}
+
+int or_session_eval(oracle_session* s, const int32_t* tokens, size_t n, int all_logits, float* out) {
+    if (n == 0) return fail("model: no tokens to evaluate");
+    for (size_t i = 0; i < n; ++i)
+        if (tokens[i] < 0 || tokens[i] >= s->c.vocab) return fail("model: token id out of range");
+    if (n > (size_t)s->c.max_context - s->position) return fail("model: context length exceeded");
+    for (size_t i = 0; i < n; ++i) {
+        float* row = all_logits ? out + i * (size_t)s->c.vocab : (i + 1 == n ? out : NULL);
+        forward_token(s, tokens[i], row);
+    }
+    return 0;
+}

@@ -1,0 +1,236 @@
+"""TEST INFRASTRUCTURE ONLY: ctypes access to the CPU oracle.
+
+``Oracle`` wraps oracle/_build/liboracle.so (the C restatement in oracle.c);
+``Reference`` wraps oracle/_ref/libbrisk_ref.so (the reference's own engine,
+compiled from its sources by oracle/Makefile).  Only tests/, the smoke check and
+bench.py's cpu_baseline leg import this module.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+ORACLE_SO = os.path.join(HERE, "_build", "liboracle.so")
+REF_SO = os.path.join(HERE, "_ref", "libbrisk_ref.so")
+
+_vp, _sz, _i, _f, _u16 = C.c_void_p, C.c_size_t, C.c_int, C.c_float, C.c_uint16
+
+
+class OracleConfig(C.Structure):
+    _fields_ = [("arch", C.c_int), ("embd", C.c_int), ("layers", C.c_int), ("heads", C.c_int),
+                ("kv_heads", C.c_int), ("head_dim", C.c_int), ("ff", C.c_int), ("vocab", C.c_int),
+                ("rope_base", C.c_float), ("eps", C.c_float), ("max_context", C.c_int)]
+
+
+class OracleTensor(C.Structure):
+    _fields_ = [("name", C.c_char_p), ("type", C.c_int), ("rows", C.c_uint64), ("cols", C.c_uint64),
+                ("data", C.c_void_p)]
+
+
+def ptr(a: np.ndarray):
+    return a.ctypes.data_as(_vp)
+
+
+_oracle = None
+_ref = None
+
+
+def build():
+    """Builds the oracle (and, where the reference tree exists, oracle/_ref)."""
+    import subprocess
+    subprocess.run(["make", "-s", "-C", HERE, "all"], check=True)
+
+
+def oracle_lib():
+    global _oracle
+    if _oracle is None:
+        if not os.path.exists(ORACLE_SO):
+            build()
+        L = C.CDLL(ORACLE_SO)
+        L.or_half_to_float.argtypes = [_u16]
+        L.or_half_to_float.restype = _f
+        L.or_float_to_half.argtypes = [_f]
+        L.or_float_to_half.restype = _u16
+        L.or_quantize_q8_0.argtypes = [_vp, _vp, _sz]
+        L.or_quantize_q8_k.argtypes = [_vp, _vp, _sz, _i]
+        L.or_dot.argtypes = [_i, _i, _vp, _vp, _sz]
+        L.or_dot.restype = _f
+        L.or_matvec.argtypes = [_i, _vp, _sz, _sz, _vp, _vp]
+        L.or_dequantize.argtypes = [_i, _vp, _vp, _sz]
+        L.or_repack_tq2_0x16.argtypes = [_vp, _sz, _sz, _vp]
+        L.or_dot_f32.argtypes = [_vp, _vp, _sz]
+        L.or_dot_f32.restype = _f
+        L.or_softmax.argtypes = [_vp, _sz]
+        L.or_rms_norm.argtypes = [_vp, _vp, _f, _vp, _sz]
+        L.or_activation_bits.argtypes = [_i, _sz]
+        L.or_activation_bits.restype = _i
+        L.or_session_create.argtypes = [C.POINTER(OracleConfig), C.POINTER(OracleTensor), _sz]
+        L.or_session_create.restype = _vp
+        L.or_session_destroy.argtypes = [_vp]
+        L.or_session_eval.argtypes = [_vp, _vp, _sz, _i, _vp]
+        L.or_session_position.argtypes = [_vp]
+        L.or_session_position.restype = _sz
+        L.or_session_rollback.argtypes = [_vp, _sz]
+        L.or_session_kv.argtypes = [_vp, _i, _i]
+        L.or_session_kv.restype = C.POINTER(C.c_uint16)
+        L.or_session_set_position.argtypes = [_vp, _sz]
+        L.or_last_error.restype = C.c_char_p
+        _oracle = L
+    return _oracle
+
+
+def ref_available() -> bool:
+    return os.path.exists(REF_SO)
+
+
+def ref_lib():
+    global _ref
+    if _ref is None:
+        L = C.CDLL(REF_SO)
+        L.ref_open.argtypes = [C.c_char_p, _i, _sz]
+        L.ref_open.restype = _vp
+        L.ref_close.argtypes = [_vp]
+        L.ref_vocab.argtypes = [_vp]
+        L.ref_vocab.restype = C.c_uint32
+        L.ref_position.argtypes = [_vp]
+        L.ref_position.restype = _sz
+        L.ref_rollback.argtypes = [_vp, _sz]
+        L.ref_eval.argtypes = [_vp, _vp, _sz, _vp]
+        L.ref_eval_all.argtypes = [_vp, _vp, _sz, _vp]
+        L.ref_generate.argtypes = [_vp, _vp, _sz, _sz, _vp, _vp, C.POINTER(C.c_double), C.POINTER(C.c_double)]
+        L.ref_last_error.restype = C.c_char_p
+        L.ref_half_to_float.argtypes = [_u16]
+        L.ref_half_to_float.restype = _f
+        L.ref_float_to_half.argtypes = [_f]
+        L.ref_float_to_half.restype = _u16
+        L.ref_quantize_q8_0.argtypes = [_vp, _vp, _sz]
+        L.ref_quantize_q8_k.argtypes = [_vp, _vp, _sz, _i]
+        L.ref_matvec.argtypes = [_i, _vp, _sz, _sz, _vp, _vp]
+        L.ref_matmul.argtypes = [_i, _vp, _sz, _sz, _vp, _sz, _vp, _sz]
+        L.ref_repack_tq2_0x16.argtypes = [_vp, _sz, _sz, _vp]
+        L.ref_dequantize.argtypes = [_i, _vp, _vp, _sz]
+        L.ref_softmax.argtypes = [_vp, _sz]
+        L.ref_dot_f32.argtypes = [_vp, _vp, _sz]
+        L.ref_dot_f32.restype = _f
+        _ref = L
+    return _ref
+
+
+class Oracle:
+    """The C restatement's session over a tensor table (brisk_hip.model.tensor_table)."""
+
+    def __init__(self, cfg, table, max_context: int):
+        L = oracle_lib()
+        self.L, self.cfg, self.max_context = L, cfg, max_context
+        c = OracleConfig(cfg.arch, cfg.embd, cfg.layers, cfg.heads, cfg.kv_heads, cfg.head_dim, cfg.ff, cfg.vocab,
+                         cfg.rope_base, cfg.eps, max_context)
+        self._names = [t.name.encode() for t in table]
+        arr = (OracleTensor * len(table))()
+        for i, t in enumerate(table):
+            arr[i] = OracleTensor(self._names[i], t.type, t.rows, t.cols, t.data.ctypes.data)
+        self._keep = (table, arr)
+        self.h = L.or_session_create(C.byref(c), arr, len(table))
+        if not self.h:
+            raise RuntimeError(L.or_last_error().decode())
+
+    def close(self):
+        if self.h:
+            self.L.or_session_destroy(self.h)
+            self.h = None
+
+    __del__ = close
+
+    def eval(self, tokens, all_logits=False) -> np.ndarray:
+        tokens = np.ascontiguousarray(tokens, dtype=np.int32)
+        out = np.empty((len(tokens) if all_logits else 1, self.cfg.vocab), np.float32)
+        if self.L.or_session_eval(self.h, ptr(tokens), len(tokens), int(all_logits), ptr(out)) != 0:
+            raise RuntimeError(self.L.or_last_error().decode())
+        return out if all_logits else out[0]
+
+    @property
+    def position(self) -> int:
+        return self.L.or_session_position(self.h)
+
+    def rollback(self, p: int):
+        if self.L.or_session_rollback(self.h, p) != 0:
+            raise RuntimeError(self.L.or_last_error().decode())
+
+    def kv(self, layer: int, value: bool) -> np.ndarray:
+        """Layer ``layer``'s fp16-bit cache [kv_heads][max_context][head_dim], writable in place."""
+        n = self.cfg.kv_heads * self.max_context * self.cfg.head_dim
+        p = self.L.or_session_kv(self.h, layer, int(value))
+        return np.ctypeslib.as_array(p, shape=(n,)).reshape(self.cfg.kv_heads, self.max_context, self.cfg.head_dim)
+
+    def set_position(self, p: int):
+        self.L.or_session_set_position(self.h, p)
+
+    def generate(self, prompt, n_gen: int):
+        """Greedy ids and top-1 minus top-2 gaps, as the reference's generate loop."""
+        logits = self.eval(prompt)
+        ids, gaps = [], []
+        for i in range(n_gen):
+            nxt = int(np.argmax(logits))
+            ids.append(nxt)
+            gaps.append(_gap(logits, nxt))
+            if i + 1 == n_gen:
+                break
+            logits = self.eval([nxt])
+        return np.array(ids, np.int32), np.array(gaps, np.float32)
+
+
+def _gap(logits, best):
+    second = np.max(np.delete(logits, best))
+    return float(logits[best] - second)
+
+
+class Reference:
+    """The reference's own CPU Session (oracle/_ref), opened on a GGUF path."""
+
+    def __init__(self, path: str, threads: int = 1, max_context: int = 1024):
+        L = ref_lib()
+        self.L = L
+        self.h = L.ref_open(path.encode(), threads, max_context)
+        if not self.h:
+            raise RuntimeError(L.ref_last_error().decode())
+        self.vocab = L.ref_vocab(self.h)
+
+    def close(self):
+        if self.h:
+            self.L.ref_close(self.h)
+            self.h = None
+
+    __del__ = close
+
+    def eval(self, tokens) -> np.ndarray:
+        tokens = np.ascontiguousarray(tokens, dtype=np.int32)
+        out = np.empty(self.vocab, np.float32)
+        if self.L.ref_eval(self.h, ptr(tokens), len(tokens), ptr(out)) != 0:
+            raise RuntimeError(self.L.ref_last_error().decode())
+        return out
+
+    def eval_all(self, tokens) -> np.ndarray:
+        tokens = np.ascontiguousarray(tokens, dtype=np.int32)
+        out = np.empty((len(tokens), self.vocab), np.float32)
+        if self.L.ref_eval_all(self.h, ptr(tokens), len(tokens), ptr(out)) != 0:
+            raise RuntimeError(self.L.ref_last_error().decode())
+        return out
+
+    @property
+    def position(self) -> int:
+        return self.L.ref_position(self.h)
+
+    def rollback(self, p: int):
+        if self.L.ref_rollback(self.h, p) != 0:
+            raise RuntimeError(self.L.ref_last_error().decode())
+
+    def generate(self, prompt, n_gen: int):
+        prompt = np.ascontiguousarray(prompt, dtype=np.int32)
+        ids = np.zeros(n_gen, np.int32)
+        gaps = np.zeros(n_gen, np.float32)
+        a, b = C.c_double(), C.c_double()
+        if self.L.ref_generate(self.h, ptr(prompt), len(prompt), n_gen, ptr(ids), ptr(gaps), C.byref(a), C.byref(b)) != 0:
+            raise RuntimeError(self.L.ref_last_error().decode())
+        return ids, gaps, a.value, b.value

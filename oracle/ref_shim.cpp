@@ -1,0 +1,193 @@
+// TEST INFRASTRUCTURE ONLY — never part of the product path.
+//
+// A C-ABI shim over the reference's own CPU engine, built from the reference's
+// sources where they lie (/root/reference/src) by oracle/Makefile into
+// oracle/_ref/libbrisk_ref.so.  Only tests/, tests/golden/ scripts,
+// __graft_entry__.smoke() and bench.py's cpu_baseline leg load it, as the
+// checker or as the timed CPU baseline.
+//
+// The calls mirror what the reference's CLI does:
+//   ref_open      ~ cmd_generate's MappedFile + GgufFile::parse + Model(file, repack = !gpu)
+//                   + Session(model, threads, max_context)   (src/main.cpp:178-212)
+//   ref_generate  ~ the greedy loop of cmd_generate           (src/main.cpp:220-299)
+//   ref_eval / ref_eval_all / ref_rollback ~ Engine           (src/engine.h:13-37)
+// plus the kernel-level entry points of src/quant.h and src/kernels.h that the
+// parity tests pin the HIP kernels against.
+#include <algorithm>
+#include <cmath>
+#include <chrono>
+#include <cstdint>
+#include <cstring>
+#include <memory>
+#include <stdexcept>
+#include <string>
+#include <vector>
+
+#include "engine.h"
+#include "gguf.h"
+#include "kernels.h"
+#include "kernels_f32.h"
+#include "mapped_file.h"
+#include "model.h"
+#include "quant.h"
+
+namespace {
+
+thread_local std::string g_error;
+
+struct RefHandle {
+    brisk::MappedFile mapped;
+    brisk::GgufFile file;
+    std::unique_ptr<brisk::Model> model;
+    std::unique_ptr<brisk::Session> session;
+    explicit RefHandle(const std::string& path) : mapped(path), file(brisk::GgufFile::parse(mapped.bytes())) {}
+};
+
+template <typename F>
+int guarded(F&& f) {
+    try {
+        f();
+        return 0;
+    } catch (const std::exception& e) {
+        g_error = e.what();
+        return -1;
+    }
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* ref_last_error(void) { return g_error.c_str(); }
+
+void* ref_open(const char* path, int threads, size_t max_context) {
+    RefHandle* h = nullptr;
+    const int rc = guarded([&] {
+        auto owned = std::make_unique<RefHandle>(path);
+        owned->model = std::make_unique<brisk::Model>(owned->file, /*repack=*/true);
+        owned->session = std::make_unique<brisk::Session>(*owned->model, static_cast<std::size_t>(std::max(threads, 1)), max_context);
+        h = owned.release();
+    });
+    return rc == 0 ? h : nullptr;
+}
+
+void ref_close(void* handle) { delete static_cast<RefHandle*>(handle); }
+
+uint32_t ref_vocab(void* handle) { return static_cast<RefHandle*>(handle)->model->config().vocab_size; }
+
+size_t ref_position(void* handle) { return static_cast<RefHandle*>(handle)->session->position(); }
+
+int ref_rollback(void* handle, size_t position) {
+    return guarded([&] { static_cast<RefHandle*>(handle)->session->rollback(position); });
+}
+
+// Last-token logits of eval(tokens) into out[vocab].
+int ref_eval(void* handle, const int32_t* tokens, size_t n, float* out) {
+    return guarded([&] {
+        auto* h = static_cast<RefHandle*>(handle);
+        const auto logits = h->session->eval(std::span<const brisk::Token>(tokens, n));
+        std::memcpy(out, logits.data(), logits.size() * sizeof(float));
+    });
+}
+
+// All n rows of eval_all(tokens) into out[n * vocab].
+int ref_eval_all(void* handle, const int32_t* tokens, size_t n, float* out) {
+    return guarded([&] {
+        auto* h = static_cast<RefHandle*>(handle);
+        const auto logits = h->session->eval_all(std::span<const brisk::Token>(tokens, n));
+        std::memcpy(out, logits.data(), logits.size() * sizeof(float));
+    });
+}
+
+// The greedy loop of cmd_generate (src/main.cpp:220-299) on token ids:
+// logits = eval(prompt); then n_gen times: next = first index of the max
+// (Sampler::sample at temperature 0, src/sampler.cpp:11-13), record it, and
+// evaluate it unless it is the last one.  gaps[i] = top-1 minus top-2 logit of
+// the distribution token i was picked from (may be null).  Timing fields as
+// src/main.cpp:312-318: prefill seconds and generation seconds.
+int ref_generate(void* handle, const int32_t* prompt, size_t n_prompt, size_t n_gen, int32_t* out_ids, float* gaps,
+                 double* prefill_s, double* gen_s) {
+    return guarded([&] {
+        auto* h = static_cast<RefHandle*>(handle);
+        using Clock = std::chrono::steady_clock;
+        const auto t0 = Clock::now();
+        std::span<const float> logits = h->session->eval(std::span<const brisk::Token>(prompt, n_prompt));
+        const auto t1 = Clock::now();
+        for (size_t i = 0; i < n_gen; ++i) {
+            const auto best = std::max_element(logits.begin(), logits.end());
+            const auto next = static_cast<brisk::Token>(best - logits.begin());
+            out_ids[i] = next;
+            if (gaps != nullptr) {
+                float second = -INFINITY;
+                for (size_t v = 0; v < logits.size(); ++v) {
+                    if (static_cast<brisk::Token>(v) != next) second = std::max(second, logits[v]);
+                }
+                gaps[i] = *best - second;
+            }
+            if (i + 1 == n_gen) break;
+            logits = h->session->eval(next);
+        }
+        const auto t2 = Clock::now();
+        *prefill_s = std::chrono::duration<double>(t1 - t0).count();
+        *gen_s = std::chrono::duration<double>(t2 - t1).count();
+    });
+}
+
+// --- kernel level (src/quant.h, src/kernels.h) ---
+
+float ref_half_to_float(uint16_t h) { return brisk::half_to_float(h); }
+uint16_t ref_float_to_half(float f) { return brisk::float_to_half(f); }
+
+void ref_quantize_q8_0(const float* x, void* out, size_t count) {
+    brisk::quantize_q8_0(x, static_cast<brisk::BlockQ8_0*>(out), count);
+}
+void ref_quantize_q8_k(const float* x, void* out, size_t count, int bits) {
+    brisk::quantize_q8_k(x, static_cast<brisk::BlockQ8_K*>(out), count, bits);
+}
+
+// Formats by the ggml tensor-type numbers a GGUF file uses (src/gguf.h:22-27);
+// 1016 stands for the load-time TQ2_0x16 layout.
+static brisk::WeightFormat format_of(int type) {
+    switch (type) {
+        case 2: return brisk::WeightFormat::Q4_0;
+        case 8: return brisk::WeightFormat::Q8_0;
+        case 12: return brisk::WeightFormat::Q4_K;
+        case 14: return brisk::WeightFormat::Q6_K;
+        case 35: return brisk::WeightFormat::TQ2_0;
+        case 1016: return brisk::WeightFormat::TQ2_0x16;
+        default: throw std::runtime_error("ref shim: unsupported format " + std::to_string(type));
+    }
+}
+
+// KernelSet::matvec / matmul of the generic kernels (src/kernels.cpp:129-163) on
+// pre-quantised activations.
+int ref_matvec(int type, const void* w, size_t rows, size_t cols, const void* x, float* out) {
+    return guarded([&] { brisk::kernels::kernels_for(format_of(type)).matvec(w, rows, cols, x, out); });
+}
+int ref_matmul(int type, const void* w, size_t rows, size_t cols, const void* x, size_t n, float* out, size_t out_stride) {
+    return guarded([&] { brisk::kernels::kernels_for(format_of(type)).matmul(w, rows, cols, x, n, out, out_stride); });
+}
+
+void ref_repack_tq2_0x16(const void* in, size_t rows, size_t blocks, void* out) {
+    brisk::repack_tq2_0x16_scalar(static_cast<const brisk::BlockTQ2_0*>(in), rows, blocks, static_cast<brisk::BlockTQ2_0x16*>(out));
+}
+
+// Dequantised rows (src/quant.h:209-218), for the tolerance checks.
+int ref_dequantize(int type, const void* blocks, float* out, size_t count) {
+    return guarded([&] {
+        switch (format_of(type)) {
+            case brisk::WeightFormat::Q4_0: brisk::dequantize_q4_0(static_cast<const brisk::BlockQ4_0*>(blocks), out, count); break;
+            case brisk::WeightFormat::Q8_0: brisk::dequantize_q8_0(static_cast<const brisk::BlockQ8_0*>(blocks), out, count); break;
+            case brisk::WeightFormat::Q4_K: brisk::dequantize_q4_k(static_cast<const brisk::BlockQ4_K*>(blocks), out, count); break;
+            case brisk::WeightFormat::Q6_K: brisk::dequantize_q6_k(static_cast<const brisk::BlockQ6_K*>(blocks), out, count); break;
+            case brisk::WeightFormat::TQ2_0: brisk::dequantize_tq2_0(static_cast<const brisk::BlockTQ2_0*>(blocks), out, count); break;
+            default: throw std::runtime_error("ref shim: no dequantiser");
+        }
+    });
+}
+
+// The attention kernels of src/kernels_f32.h (portable branch) for one query.
+void ref_softmax(float* x, size_t n) { brisk::kernels::softmax_f32(std::span<float>(x, n)); }
+float ref_dot_f32(const float* a, const float* b, size_t n) { return brisk::kernels::dot_f32(a, b, n); }
+
+}  // extern "C"
