@@ -1,0 +1,128 @@
+"""HipSession: the Engine interface (src/engine.h:13-37) over the C ABI.
+
+Mirrors the reference's ``Session`` / ``MetalSession``: ``eval`` returns the
+last token's logits, ``eval_all`` every token's (1..64 tokens), ``rollback``
+forgets from a position on, ``position`` is the sequence length so far, and
+``log_likelihood`` is ``Engine::log_likelihood`` (src/engine.cpp:10-33).
+Errors raise ``BriskHipError`` (a RuntimeError) with the reference's messages.
+"""
+from __future__ import annotations
+
+import ctypes as C
+
+import numpy as np
+
+from . import lib as _lib
+from . import model as _model
+
+
+def _ptr(a: np.ndarray):
+    return a.ctypes.data_as(C.c_void_p)
+
+
+class HipSession:
+    """One sequence on one GPU.  ``source`` is a GGUF path or a (GgufFile, ModelConfig, table) triple."""
+
+    max_scored_tokens = 64  # Engine::kMaxScoredTokens
+
+    def __init__(self, source, max_context: int = 0, device: int = 0):
+        L = _lib.load()
+        self._L = L
+        if isinstance(source, str):
+            source = _model.load(source)
+        self.file, self.config, table = source
+        c = self.config
+        hc = _lib.HipConfig(c.arch, c.vocab, c.embd, c.layers, c.heads, c.kv_heads, c.head_dim, c.ff, c.context,
+                            c.rope_base, c.eps)
+        names = [t.name.encode() for t in table]
+        arr = (_lib.HipTensor * len(table))()
+        for i, t in enumerate(table):
+            arr[i] = _lib.HipTensor(names[i], t.type, t.rows, t.cols, t.data.ctypes.data)
+        h = C.c_void_p()
+        _lib.check(L.brisk_hip_session_create(C.byref(hc), arr, len(table), max_context, device, C.byref(h)))
+        self._h = h
+        self.vocab = c.vocab
+
+    def close(self):
+        if getattr(self, "_h", None):
+            self._L.brisk_hip_session_destroy(self._h)
+            self._h = None
+
+    def __del__(self):
+        self.close()
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    @staticmethod
+    def _tokens(tokens) -> np.ndarray:
+        return np.ascontiguousarray(np.atleast_1d(np.asarray(tokens)), dtype=np.int32)
+
+    def eval(self, tokens, logits: bool = True):
+        t = self._tokens(tokens)
+        out = np.empty(self.vocab, np.float32) if logits else None
+        _lib.check(self._L.brisk_hip_session_eval(self._h, _ptr(t), len(t), _ptr(out) if logits else None))
+        return out
+
+    def eval_all(self, tokens) -> np.ndarray:
+        t = self._tokens(tokens)
+        out = np.empty((len(t), self.vocab), np.float32)
+        _lib.check(self._L.brisk_hip_session_eval_all(self._h, _ptr(t), len(t), _ptr(out)))
+        return out
+
+    def eval_greedy(self, tokens) -> int:
+        t = self._tokens(tokens)
+        nxt = C.c_int32()
+        _lib.check(self._L.brisk_hip_session_eval_greedy(self._h, _ptr(t), len(t), C.byref(nxt)))
+        return int(nxt.value)
+
+    def generate(self, prompt, n_gen: int) -> np.ndarray:
+        p = self._tokens(prompt)
+        out = np.zeros(n_gen, np.int32)
+        _lib.check(self._L.brisk_hip_session_generate(self._h, _ptr(p), len(p), n_gen, _ptr(out)))
+        return out
+
+    def rollback(self, position: int):
+        _lib.check(self._L.brisk_hip_session_rollback(self._h, position))
+
+    @property
+    def position(self) -> int:
+        return self._L.brisk_hip_session_position(self._h)
+
+    @property
+    def max_context(self) -> int:
+        return self._L.brisk_hip_session_max_context(self._h)
+
+    def kv_cache(self, layer: int, value: bool):
+        """(device pointer, bytes) of a layer's fp16 cache [kv_heads][max_context][head_dim]."""
+        p, n = C.c_void_p(), C.c_size_t()
+        _lib.check(self._L.brisk_hip_session_kv_cache(self._h, layer, int(value), C.byref(p), C.byref(n)))
+        return p.value, n.value
+
+    def set_position(self, position: int):
+        _lib.check(self._L.brisk_hip_session_set_position(self._h, position))
+
+    @property
+    def stream(self) -> int:
+        return self._L.brisk_hip_session_stream(self._h)
+
+    def log_likelihood(self, tokens, chunk: int = 64) -> float:
+        """Engine::log_likelihood (src/engine.cpp:10-33): sum of log p(tokens[i] | tokens[:i]), i >= 1."""
+        t = self._tokens(tokens)
+        if len(t) < 2:
+            raise RuntimeError("need at least two tokens to score")
+        chunk = max(1, min(chunk, self.max_scored_tokens))
+        total = 0.0
+        for begin in range(0, len(t), chunk):
+            n = min(chunk, len(t) - begin)
+            logits = self.eval_all(t[begin:begin + n])
+            for i in range(n):
+                if begin + i + 1 >= len(t):
+                    break
+                row = logits[i].astype(np.float64)
+                mx = row.max()
+                total += (row[t[begin + i + 1]] - mx) - np.log(np.exp(row - mx).sum())
+        return total

@@ -1,0 +1,191 @@
+// The extern "C" surface declared in include/brisk_hip.h.
+#include <hip/hip_runtime.h>
+
+#include <exception>
+#include <new>
+#include <string>
+
+#include "session.h"
+
+struct brisk_hip_session {
+    bh::Session impl;
+    template <typename... A>
+    explicit brisk_hip_session(A&&... a) : impl(static_cast<A&&>(a)...) {}
+};
+
+namespace {
+
+thread_local std::string g_error;
+
+int set_error(int code, const std::string& what) {
+    g_error = what;
+    return code;
+}
+
+template <typename F>
+int guarded(F&& f) {
+    try {
+        f();
+        return BRISK_HIP_OK;
+    } catch (const bh::Error& e) {
+        return set_error(e.code, e.what());
+    } catch (const std::bad_alloc&) {
+        return set_error(BRISK_HIP_ENOMEM, "out of host memory");
+    } catch (const std::exception& e) {
+        return set_error(BRISK_HIP_EINVAL, e.what());
+    }
+}
+
+void hip_check(hipError_t e, const char* what) {
+    if (e != hipSuccess) throw bh::Error(BRISK_HIP_EHIP, std::string("hip: ") + what + ": " + hipGetErrorString(e));
+}
+
+bool known_type(int type) {
+    return type == BRISK_HIP_Q4_0 || type == BRISK_HIP_Q8_0 || type == BRISK_HIP_Q4_K || type == BRISK_HIP_Q6_K ||
+           type == BRISK_HIP_TQ2_0;
+}
+
+bh::Packed packed_view(int type, int flags, const void* packed, size_t rows, size_t cols) {
+    if (!known_type(type)) throw bh::Error(BRISK_HIP_EINVAL, "kernels: unsupported weight type " + std::to_string(type));
+    if (cols == 0 || cols % bh::block_elems(static_cast<uint32_t>(type)) != 0)
+        throw bh::Error(BRISK_HIP_EINVAL, "kernels: cols must be a non-zero multiple of the block size");
+    if (cols > static_cast<size_t>(bh::kMaxCols)) throw bh::Error(BRISK_HIP_EINVAL, "kernels: rows wider than 8192 are not supported");
+    if (rows == 0 || rows > 0xFFFFFFFFu) throw bh::Error(BRISK_HIP_EINVAL, "kernels: bad row count");
+    if (packed == nullptr) throw bh::Error(BRISK_HIP_EINVAL, "kernels: null weights");
+    size_t planes[3];
+    bh::plane_bytes(static_cast<uint32_t>(type), rows, cols, planes);
+    const uint8_t* base = static_cast<const uint8_t*>(packed);
+    bh::Packed p{base, base + bh::align256(planes[0]), base + bh::align256(planes[0]) + bh::align256(planes[1]),
+                 static_cast<uint32_t>(rows), static_cast<uint32_t>(cols), static_cast<uint32_t>(type),
+                 static_cast<uint32_t>(flags) & bh::kFlagLut16};
+    if (type != BRISK_HIP_TQ2_0) p.flags = 0;
+    return p;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* brisk_hip_last_error(void) { return g_error.c_str(); }
+
+int brisk_hip_abi_version(void) { return BRISK_HIP_ABI_VERSION; }
+
+int brisk_hip_device_count(int* count) {
+    return guarded([&] {
+        int n = 0;
+        const hipError_t e = hipGetDeviceCount(&n);
+        *count = e == hipSuccess ? n : 0;
+    });
+}
+
+size_t brisk_hip_packed_bytes(int type, size_t rows, size_t cols) {
+    if (!known_type(type) || cols % bh::block_elems(static_cast<uint32_t>(type)) != 0) return 0;
+    return bh::packed_bytes(static_cast<uint32_t>(type), rows, cols);
+}
+
+int brisk_hip_pack(int type, const void* gguf_blocks, size_t rows, size_t cols, void* packed, void* stream) {
+    return guarded([&] {
+        const bh::Packed p = packed_view(type, 0, packed, rows, cols);
+        if (gguf_blocks == nullptr) throw bh::Error(BRISK_HIP_EINVAL, "kernels: null source");
+        hip_check(bh::launch_pack(static_cast<uint32_t>(type), gguf_blocks, rows, cols, p, static_cast<hipStream_t>(stream)), "pack");
+    });
+}
+
+int brisk_hip_quantize_q8_0(const float* x, void* out, size_t count, void* stream) {
+    return guarded([&] {
+        if (count % 32 != 0) throw bh::Error(BRISK_HIP_EINVAL, "kernels: count must be a multiple of 32");
+        hip_check(bh::launch_quantize(0, x, out, count, 8, static_cast<hipStream_t>(stream)), "quantize_q8_0");
+    });
+}
+
+int brisk_hip_quantize_q8_k(const float* x, void* out, size_t count, int bits, void* stream) {
+    return guarded([&] {
+        if (count % 256 != 0) throw bh::Error(BRISK_HIP_EINVAL, "kernels: count must be a multiple of 256");
+        if (bits != 7 && bits != 8) throw bh::Error(BRISK_HIP_EINVAL, "kernels: bits must be 7 or 8");
+        hip_check(bh::launch_quantize(1, x, out, count, bits, static_cast<hipStream_t>(stream)), "quantize_q8_k");
+    });
+}
+
+int brisk_hip_matvec(int type, int flags, const void* packed, size_t rows, size_t cols, const void* xq, float* out, void* stream) {
+    return brisk_hip_matmul(type, flags, packed, rows, cols, xq, 1, out, rows, stream);
+}
+
+int brisk_hip_matmul(int type, int flags, const void* packed, size_t rows, size_t cols, const void* xq, size_t n, float* out,
+                     size_t out_stride, void* stream) {
+    return guarded([&] {
+        const bh::Packed p = packed_view(type, flags, packed, rows, cols);
+        if (n == 0 || n > 65535) throw bh::Error(BRISK_HIP_EINVAL, "kernels: n must be 1..65535");
+        if (out_stride < rows) throw bh::Error(BRISK_HIP_EINVAL, "kernels: out_stride < rows");
+        hip_check(bh::launch_matvec_q8(p, xq, n, out, out_stride, static_cast<hipStream_t>(stream)), "matmul");
+    });
+}
+
+int brisk_hip_gemv(int type, int flags, const void* packed, size_t rows, size_t cols, const float* x, const float* norm_w, float eps,
+                   float* out, int accumulate, void* stream) {
+    return guarded([&] {
+        bh::GemvArgs g{};
+        g.n = 1;
+        g.t[0].m = packed_view(type, flags, packed, rows, cols);
+        g.t[0].out = out;
+        g.x = x;
+        g.normw = norm_w;
+        g.eps = eps;
+        g.add = accumulate != 0;
+        hip_check(bh::launch_gemv(g, static_cast<hipStream_t>(stream)), "gemv");
+    });
+}
+
+int brisk_hip_expf(const float* x, float* y, size_t n, void* stream) {
+    return guarded([&] { hip_check(bh::launch_expf(x, y, n, static_cast<hipStream_t>(stream)), "expf"); });
+}
+
+int brisk_hip_session_create(const brisk_hip_config* config, const brisk_hip_tensor* tensors, size_t n_tensors, size_t max_context,
+                             int device, brisk_hip_session** out) {
+    return guarded([&] {
+        if (config == nullptr || out == nullptr || (tensors == nullptr && n_tensors != 0))
+            throw bh::Error(BRISK_HIP_EINVAL, "session: null argument");
+        *out = nullptr;
+        *out = new brisk_hip_session(*config, tensors, n_tensors, max_context, device);
+    });
+}
+
+void brisk_hip_session_destroy(brisk_hip_session* s) { delete s; }
+
+int brisk_hip_session_eval(brisk_hip_session* s, const int32_t* tokens, size_t n, float* logits) {
+    return guarded([&] { s->impl.eval(tokens, n, logits); });
+}
+
+int brisk_hip_session_eval_all(brisk_hip_session* s, const int32_t* tokens, size_t n, float* logits) {
+    return guarded([&] {
+        if (logits == nullptr) throw bh::Error(BRISK_HIP_EINVAL, "session: null logits");
+        s->impl.eval_all(tokens, n, logits);
+    });
+}
+
+int brisk_hip_session_eval_greedy(brisk_hip_session* s, const int32_t* tokens, size_t n, int32_t* next) {
+    return guarded([&] { *next = s->impl.eval_greedy(tokens, n); });
+}
+
+int brisk_hip_session_generate(brisk_hip_session* s, const int32_t* prompt, size_t n_prompt, size_t n_gen, int32_t* out) {
+    return guarded([&] { s->impl.generate(prompt, n_prompt, n_gen, out); });
+}
+
+int brisk_hip_session_rollback(brisk_hip_session* s, size_t position) {
+    return guarded([&] { s->impl.rollback(position); });
+}
+
+size_t brisk_hip_session_position(const brisk_hip_session* s) { return s->impl.position(); }
+
+size_t brisk_hip_session_max_context(const brisk_hip_session* s) { return s->impl.max_context(); }
+
+int brisk_hip_session_kv_cache(brisk_hip_session* s, int layer, int value, void** device_ptr, size_t* bytes) {
+    return guarded([&] { s->impl.kv_cache(layer, value, device_ptr, bytes); });
+}
+
+int brisk_hip_session_set_position(brisk_hip_session* s, size_t position) {
+    return guarded([&] { s->impl.set_position(position); });
+}
+
+void* brisk_hip_session_stream(brisk_hip_session* s) { return static_cast<void*>(s->impl.stream()); }
+
+}  // extern "C"

@@ -1,0 +1,453 @@
+// Device-side building blocks of the token loop: half conversion, activation
+// quantisation into LDS, and the per-format integer block dots.
+//
+// Arithmetic contract (checked by the parity tests against the reference's
+// scalar code): every integer block dot is exact, and the per-block float term
+// is formed with the same operations in the same order as the reference's
+// dot_* functions (src/quant.cpp:445-596, :789-802).  The whole library is
+// compiled with -ffp-contract=off and IEEE-correct fp32 division/sqrt, so no
+// product/sum pair is fused into an FMA the x86 reference does not have.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "layout.h"
+
+namespace bh {
+
+constexpr int kThreads = 256;        // every token-loop kernel runs 256-thread workgroups (4 waves of 64)
+constexpr int kMaxCols = 8192;       // widest activation row a matvec takes (Llama-3.2-1B FFN)
+
+// ---------------------------------------------------------------- halves
+
+// IEEE half -> float; exact (src/quant.cpp:61-85 is the same conversion).
+__device__ __forceinline__ float h2f(uint16_t h) { return static_cast<float>(__builtin_bit_cast(_Float16, h)); }
+
+// float -> IEEE half, round to nearest even, with the reference's handling of
+// overflow (infinity), underflow (signed zero) and NaN (quiet, payload
+// dropped): src/quant.cpp:87-113, written out on the bits.
+__device__ __forceinline__ uint16_t f2h(float f) {
+    const uint32_t bits = __float_as_uint(f);
+    const uint32_t sign = (bits >> 16) & 0x8000u;
+    const int32_t exponent = static_cast<int32_t>((bits >> 23) & 0xFF) - 127 + 15;
+    uint32_t mantissa = bits & 0x7FFFFFu;
+    if (((bits >> 23) & 0xFF) == 0xFF) return static_cast<uint16_t>(sign | 0x7C00u | (mantissa ? 0x200u : 0u));
+    if (exponent >= 0x1F) return static_cast<uint16_t>(sign | 0x7C00u);
+    if (exponent <= 0) {
+        if (exponent < -10) return static_cast<uint16_t>(sign);
+        mantissa |= 0x800000u;
+        const uint32_t shift = static_cast<uint32_t>(14 - exponent);
+        uint32_t half = mantissa >> shift;
+        const uint32_t rem = mantissa & ((1u << shift) - 1), halfway = 1u << (shift - 1);
+        if (rem > halfway || (rem == halfway && (half & 1))) ++half;
+        return static_cast<uint16_t>(sign | half);
+    }
+    uint32_t half = (static_cast<uint32_t>(exponent) << 10) | (mantissa >> 13);
+    const uint32_t rem = mantissa & 0x1FFFu;
+    if (rem > 0x1000u || (rem == 0x1000u && (half & 1))) ++half;
+    return static_cast<uint16_t>(sign | half);
+}
+
+// ---------------------------------------------------------------- exp
+
+// expf as the reference's host libm computes it.  The reference calls std::exp
+// on floats (softmax_f32, silu_mul_f32: src/kernels_f32.cpp:276-289), i.e.
+// glibc's expf, whose x86-64 build picks its FMA variant at run time.  That
+// routine (the table-driven design of ARM's optimized-routines, also in
+// glibc's sysdeps/ieee754/flt-32/e_expf.c) works in double: k = round(x * 32 /
+// ln 2), r = x * 32 / ln 2 - k (one fused multiply-add), 2^(k/32) from a
+// 32-entry table of 2^(i/32) with the exponent bits of i folded out, times a
+// degree-3 polynomial in r.  This restatement reproduces glibc's results on
+// every one of the 2^32 float inputs (checked exhaustively on the host).
+__constant__ const unsigned long long kExp2Table[32] = {  // bits(2^(i/32)) - (i << 52) / 32
+    0x3ff0000000000000ull, 0x3fefd9b0d3158574ull, 0x3fefb5586cf9890full, 0x3fef9301d0125b51ull,
+    0x3fef72b83c7d517bull, 0x3fef54873168b9aaull, 0x3fef387a6e756238ull, 0x3fef1e9df51fdee1ull,
+    0x3fef06fe0a31b715ull, 0x3feef1a7373aa9cbull, 0x3feedea64c123422ull, 0x3feece086061892dull,
+    0x3feebfdad5362a27ull, 0x3feeb42b569d4f82ull, 0x3feeab07dd485429ull, 0x3feea47eb03a5585ull,
+    0x3feea09e667f3bcdull, 0x3fee9f75e8ec5f74ull, 0x3feea11473eb0187ull, 0x3feea589994cce13ull,
+    0x3feeace5422aa0dbull, 0x3feeb737b0cdc5e5ull, 0x3feec49182a3f090ull, 0x3feed503b23e255dull,
+    0x3feee89f995ad3adull, 0x3feeff76f2fb5e47ull, 0x3fef199bdd85529cull, 0x3fef3720dcef9069ull,
+    0x3fef5818dcfba487ull, 0x3fef7c97337b9b5full, 0x3fefa4afa2a490daull, 0x3fefd0765b6e4540ull,
+};
+
+__device__ inline float ref_expf(float x) {
+    const uint32_t ux = __float_as_uint(x);
+    const uint32_t abstop = (ux >> 20) & 0x7FF;
+    if (abstop >= 0x42Bu) {  // |x| >= 88 (top 12 bits of 88.0f), or inf / nan
+        if (ux == 0xFF800000u) return 0.0f;
+        if (abstop >= 0x7F8u) return x + x;
+        if (x > 0x1.62e42ep6f) return __uint_as_float(0x7F800000u);
+        if (x < -0x1.9fe368p6f) return 0.0f;
+    }
+    const double inv_ln2_n = 0x1.71547652b82fep+0 * 32.0;
+    const double shift = 0x1.8p+52;
+    const double c0 = 0x1.c6af84b912394p-5 / 32.0 / 32.0 / 32.0;
+    const double c1 = 0x1.ebfce50fac4f3p-3 / 32.0 / 32.0;
+    const double c2 = 0x1.62e42ff0c52d6p-1 / 32.0;
+    const double xd = static_cast<double>(x);
+    const double z = inv_ln2_n * xd;
+    double kd = z + shift;
+    const unsigned long long ki = static_cast<unsigned long long>(__double_as_longlong(kd));
+    kd -= shift;
+    const double r = __fma_rn(inv_ln2_n, xd, -kd);
+    const unsigned long long t = kExp2Table[ki % 32] + (ki << 47);
+    const double s = __longlong_as_double(static_cast<long long>(t));
+    const double p = __fma_rn(c0, r, c1);
+    const double r2 = r * r;
+    double y = __fma_rn(c2, r, 1.0);
+    y = __fma_rn(p, r2, y);
+    y = y * s;
+    return static_cast<float>(y);
+}
+
+__device__ __forceinline__ int dot4(int a, int b, int c) { return __builtin_amdgcn_sdot4(a, b, c, false); }
+
+// ---------------------------------------------------------------- reductions
+
+template <typename T>
+__device__ __forceinline__ T wave_sum(T v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    return v;
+}
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+    return v;
+}
+
+// Sum of float squares in double over a workgroup (the accumulator of rms_norm,
+// src/model.cpp:89-90).  The double sum of float squares is exact unless the
+// squares span more than ~29 binades, so the grouping rarely matters; every
+// workgroup uses the same grouping, so all of them agree bit for bit.
+__device__ __forceinline__ double block_sumsq(const float* x, int n, double* red /* LDS [4] */) {
+    double s = 0.0;
+    for (int i = threadIdx.x; i < n; i += kThreads) {
+        const float v = x[i];
+        s += static_cast<double>(v * v);
+    }
+    s = wave_sum(s);
+    const int wave = threadIdx.x >> 6;
+    __syncthreads();
+    if ((threadIdx.x & 63) == 0) red[wave] = s;
+    __syncthreads();
+    return ((red[0] + red[1]) + red[2]) + red[3];
+}
+
+// rms_norm's scale (src/model.cpp:91-92).
+__device__ __forceinline__ float rms_scale(double sum, int n, float eps) {
+    const float mean = static_cast<float>(sum / static_cast<double>(n));
+    return 1.0f / sqrtf(mean + eps);
+}
+
+// ---------------------------------------------------------------- activations in LDS
+
+// One activation row, quantised, resident in LDS for the whole tile.
+// Q8_0 family: xs = 32-value blocks, xd = half-rounded scale as float, xsum = sum of a block's values.
+// Q8_K family: xs = 256-value blocks, xd = float scale, xsum = the 16 bsums of each block.
+struct ActLds {
+    int32_t xs[kMaxCols / 4];
+    float xd[kMaxCols / 32];
+    int32_t xsum[kMaxCols / 16];
+};
+
+// quantize_q8_0 (src/quant.cpp:115-142) of v = x (or rms_norm(x) * w when `w`
+// is given) into LDS.  Each thread takes 4 consecutive values, so a 32-value
+// block is 8 adjacent lanes.  Exact: IEEE division, round-half-even rint.
+__device__ inline void act_q8_0(const float* x, const float* w, float scale, int cols, ActLds& a) {
+    for (int base = threadIdx.x * 4; base < cols; base += kThreads * 4) {
+        float v[4];
+        const float4 xv = *reinterpret_cast<const float4*>(x + base);
+        v[0] = xv.x; v[1] = xv.y; v[2] = xv.z; v[3] = xv.w;
+        if (w != nullptr) {
+            const float4 wv = *reinterpret_cast<const float4*>(w + base);
+            v[0] = v[0] * scale * wv.x; v[1] = v[1] * scale * wv.y;
+            v[2] = v[2] * scale * wv.z; v[3] = v[3] * scale * wv.w;
+        }
+        float amax = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
+        amax = fmaxf(amax, __shfl_xor(amax, 1, 64));
+        amax = fmaxf(amax, __shfl_xor(amax, 2, 64));
+        amax = fmaxf(amax, __shfl_xor(amax, 4, 64));
+        const float d = amax / 127.0f;
+        const float inv = d != 0.0f ? 1.0f / d : 0.0f;
+        int q[4], sum = 0;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            q[i] = static_cast<int>(rintf(v[i] * inv));
+            sum += q[i];
+        }
+        sum += __shfl_xor(sum, 1, 64);
+        sum += __shfl_xor(sum, 2, 64);
+        sum += __shfl_xor(sum, 4, 64);
+        a.xs[base / 4] = (q[0] & 0xFF) | ((q[1] & 0xFF) << 8) | ((q[2] & 0xFF) << 16) | (q[3] << 24);
+        if ((threadIdx.x & 7) == 0) {
+            a.xd[base / 32] = h2f(f2h(d));
+            a.xsum[base / 32] = sum;
+        }
+    }
+}
+
+// quantize_q8_k (src/quant.cpp:146-194) with `bits` 8 or 7, into LDS.  One
+// wave per 256-value block (4 values a lane).  The scale comes from the first
+// value of largest magnitude, signed, as the reference's scan picks it.
+__device__ inline void act_q8_k(const float* x, const float* w, float scale, int cols, int bits, ActLds& a) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    for (int blk = wave; blk < cols / 256; blk += kThreads / 64) {
+        const int base = blk * 256 + lane * 4;
+        float v[4];
+        const float4 xv = *reinterpret_cast<const float4*>(x + base);
+        v[0] = xv.x; v[1] = xv.y; v[2] = xv.z; v[3] = xv.w;
+        if (w != nullptr) {
+            const float4 wv = *reinterpret_cast<const float4*>(w + base);
+            v[0] = v[0] * scale * wv.x; v[1] = v[1] * scale * wv.y;
+            v[2] = v[2] * scale * wv.z; v[3] = v[3] * scale * wv.w;
+        }
+        // first index of the largest |v|
+        float amax = -1.0f;
+        int idx = 0;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const float av = fabsf(v[i]);
+            if (av > amax) { amax = av; idx = lane * 4 + i; }
+        }
+        float sel = v[idx - lane * 4 < 0 ? 0 : (idx & 3)];
+#pragma unroll
+        for (int o = 1; o < 64; o <<= 1) {
+            const float oa = __shfl_xor(amax, o, 64);
+            const int oi = __shfl_xor(idx, o, 64);
+            const float os = __shfl_xor(sel, o, 64);
+            if (oa > amax || (oa == amax && oi < idx)) { amax = oa; idx = oi; sel = os; }
+        }
+        int q[4];
+        float d;
+        if (amax == 0.0f) {
+            d = 0.0f;
+            q[0] = q[1] = q[2] = q[3] = 0;
+        } else {
+            const float extreme = bits == 7 ? 63.0f : 127.0f;
+            const float inv = -extreme / sel;
+            d = 1.0f / inv;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) q[i] = static_cast<int>(fminf(127.0f, rintf(inv * v[i])));
+        }
+        int s = q[0] + q[1] + q[2] + q[3];
+        s += __shfl_xor(s, 1, 64);
+        s += __shfl_xor(s, 2, 64);
+        a.xs[base / 4] = (q[0] & 0xFF) | ((q[1] & 0xFF) << 8) | ((q[2] & 0xFF) << 16) | (q[3] << 24);
+        if ((lane & 3) == 0) a.xsum[blk * 16 + lane / 4] = static_cast<int16_t>(s);  // bsums are int16
+        if (lane == 0) a.xd[blk] = d;
+    }
+}
+
+// Same LDS image from already-quantised GGUF activation blocks (the KernelSet
+// matvec contract: x is BlockQ8_0 / BlockQ8_K rows, src/kernels.h:19-21).
+__device__ inline void act_from_q8_0(const uint8_t* xq, int cols, ActLds& a) {
+    for (int b = threadIdx.x; b < cols / 32; b += kThreads) {
+        const uint8_t* blk = xq + b * 34;
+        a.xd[b] = h2f(static_cast<uint16_t>(blk[0] | (blk[1] << 8)));
+        int s = 0;
+        for (int j = 0; j < 8; ++j) {
+            const int v = blk[2 + 4 * j] | (blk[3 + 4 * j] << 8) | (blk[4 + 4 * j] << 16) | (blk[5 + 4 * j] << 24);
+            a.xs[b * 8 + j] = v;
+            s = dot4(v, 0x01010101, s);
+        }
+        a.xsum[b] = s;
+    }
+}
+
+__device__ inline void act_from_q8_k(const uint8_t* xq, int cols, ActLds& a) {
+    for (int b = threadIdx.x; b < cols / 256; b += kThreads) {
+        const uint8_t* blk = xq + b * 292;
+        a.xd[b] = *reinterpret_cast<const float*>(blk);
+        for (int j = 0; j < 64; ++j) a.xs[b * 64 + j] = *reinterpret_cast<const int32_t*>(blk + 4 + 4 * j);
+        for (int j = 0; j < 16; ++j) a.xsum[b * 16 + j] = *reinterpret_cast<const int16_t*>(blk + 260 + 2 * j);
+    }
+}
+
+// ---------------------------------------------------------------- block dots
+
+// dot_q4_0_q8_0 block term (src/quant.cpp:445-456): acc = sum((q - 8) x), exact;
+// term = (float)acc * d_w * d_x.  Nibble bytes hold values 0..15, valid as
+// signed int8, so sum(q x) runs on sdot4 and the -8 comes off via the block sum.
+__device__ __forceinline__ float term_q4_0(const Packed& m, uint32_t row, uint32_t b, const ActLds& a) {
+    const uint32_t nb = m.cols / 32;
+    const size_t blk = static_cast<size_t>(row) * nb + b;
+    const uint4 q = *reinterpret_cast<const uint4*>(m.p0 + blk * 16);
+    const uint16_t dw = reinterpret_cast<const uint16_t*>(m.p1)[blk];
+    const int32_t* x = a.xs + b * 8;
+    int acc = 0;
+    const uint32_t qw[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        acc = dot4(static_cast<int>(qw[j] & 0x0F0F0F0Fu), x[j], acc);
+        acc = dot4(static_cast<int>((qw[j] >> 4) & 0x0F0F0F0Fu), x[4 + j], acc);
+    }
+    acc -= 8 * a.xsum[b];
+    return static_cast<float>(acc) * h2f(dw) * a.xd[b];
+}
+
+// dot_q8_0_q8_0 block term (src/quant.cpp:474-482).
+__device__ __forceinline__ float term_q8_0(const Packed& m, uint32_t row, uint32_t b, const ActLds& a) {
+    const uint32_t nb = m.cols / 32;
+    const size_t blk = static_cast<size_t>(row) * nb + b;
+    const uint4* qp = reinterpret_cast<const uint4*>(m.p0 + blk * 32);
+    const uint4 q0 = qp[0], q1 = qp[1];
+    const uint16_t dw = reinterpret_cast<const uint16_t*>(m.p1)[blk];
+    const int32_t* x = a.xs + b * 8;
+    int acc = 0;
+    acc = dot4(q0.x, x[0], acc); acc = dot4(q0.y, x[1], acc); acc = dot4(q0.z, x[2], acc); acc = dot4(q0.w, x[3], acc);
+    acc = dot4(q1.x, x[4], acc); acc = dot4(q1.y, x[5], acc); acc = dot4(q1.z, x[6], acc); acc = dot4(q1.w, x[7], acc);
+    return static_cast<float>(acc) * h2f(dw) * a.xd[b];
+}
+
+// q4_k_scale_min (src/quant.h:256-264)
+__device__ __forceinline__ void q4k_scale_min(const uint8_t* s, int j, int& scale, int& min) {
+    if (j < 4) {
+        scale = s[j] & 63;
+        min = s[j + 4] & 63;
+    } else {
+        scale = (s[j + 4] & 0xF) | ((s[j - 4] >> 6) << 4);
+        min = (s[j + 4] >> 4) | ((s[j] >> 6) << 4);
+    }
+}
+
+// dot_q4_k_q8_k super-block term (src/quant.cpp:500-521): weighted and offsets
+// are exact int32; term = x.d * (d * weighted - dmin * offsets).
+__device__ __forceinline__ float term_q4_k(const Packed& m, uint32_t row, uint32_t b, const ActLds& a) {
+    const uint32_t nsb = m.cols / 256;
+    const size_t blk = static_cast<size_t>(row) * nsb + b;
+    const uint4* qp = reinterpret_cast<const uint4*>(m.p0 + blk * 128);
+    const uint4 meta = *reinterpret_cast<const uint4*>(m.p1 + blk * 16);
+    const uint8_t* mb = reinterpret_cast<const uint8_t*>(&meta);
+    const uint16_t d = static_cast<uint16_t>(meta.x & 0xFFFF), dmin = static_cast<uint16_t>(meta.x >> 16);
+    const int32_t* x = a.xs + b * 64;
+    int weighted = 0, offsets = 0;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {  // chunk c: 32 bytes, low nibbles = sub-block 2c, high = 2c+1
+        const uint4 q0 = qp[2 * c], q1 = qp[2 * c + 1];
+        const uint32_t qw[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
+        int lo = 0, hi = 0;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            lo = dot4(static_cast<int>(qw[j] & 0x0F0F0F0Fu), x[c * 16 + j], lo);
+            hi = dot4(static_cast<int>((qw[j] >> 4) & 0x0F0F0F0Fu), x[c * 16 + 8 + j], hi);
+        }
+        int s0, m0, s1, m1;
+        q4k_scale_min(mb + 4, 2 * c, s0, m0);
+        q4k_scale_min(mb + 4, 2 * c + 1, s1, m1);
+        weighted += s0 * lo + s1 * hi;
+        const int* bs = a.xsum + b * 16 + 4 * c;
+        offsets += m0 * (bs[0] + bs[1]) + m1 * (bs[2] + bs[3]);
+    }
+    return a.xd[b] * (h2f(d) * static_cast<float>(weighted) - h2f(dmin) * static_cast<float>(offsets));
+}
+
+// dot_q6_k_q8_k super-block term (src/quant.cpp:549-563, unpack_q6_k :285-297):
+// per 16-value group g, dot = sum((v - 32) x) = sum(v x) - 32 bsum[g] with v in
+// 0..63; weighted = sum scale_g dot_g, exact; term = x.d * d * weighted.
+__device__ __forceinline__ float term_q6_k(const Packed& m, uint32_t row, uint32_t b, const ActLds& a) {
+    const uint32_t nsb = m.cols / 256;
+    const size_t blk = static_cast<size_t>(row) * nsb + b;
+    const uint32_t* ql = reinterpret_cast<const uint32_t*>(m.p0 + blk * 128);
+    const uint32_t* qh = reinterpret_cast<const uint32_t*>(m.p1 + blk * 64);
+    const uint8_t* meta = m.p2 + blk * 20;  // int8 scales[16], u16 d, pad
+    const int32_t* x = a.xs + b * 64;
+    const int* bs = a.xsum + b * 16;
+    int weighted = 0;
+#pragma unroll
+    for (int half = 0; half < 2; ++half) {
+        int g4[4][2];  // [quarter][sub-group of 16] sums of v x
+#pragma unroll
+        for (int qi = 0; qi < 4; ++qi) g4[qi][0] = g4[qi][1] = 0;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {  // values l = 4j..4j+3 of this half
+            const uint32_t l0 = ql[half * 16 + j], l1 = ql[half * 16 + 8 + j], h = qh[half * 8 + j];
+            const int v0 = static_cast<int>((l0 & 0x0F0F0F0Fu) | (((h >> 0) & 0x03030303u) << 4));
+            const int v1 = static_cast<int>((l1 & 0x0F0F0F0Fu) | (((h >> 2) & 0x03030303u) << 4));
+            const int v2 = static_cast<int>(((l0 >> 4) & 0x0F0F0F0Fu) | (((h >> 4) & 0x03030303u) << 4));
+            const int v3 = static_cast<int>(((l1 >> 4) & 0x0F0F0F0Fu) | (((h >> 6) & 0x03030303u) << 4));
+            const int sg = j >> 2;  // values 0-15 or 16-31 of each quarter
+            g4[0][sg] = dot4(v0, x[half * 32 + 0 + j], g4[0][sg]);
+            g4[1][sg] = dot4(v1, x[half * 32 + 8 + j], g4[1][sg]);
+            g4[2][sg] = dot4(v2, x[half * 32 + 16 + j], g4[2][sg]);
+            g4[3][sg] = dot4(v3, x[half * 32 + 24 + j], g4[3][sg]);
+        }
+#pragma unroll
+        for (int qi = 0; qi < 4; ++qi) {
+#pragma unroll
+            for (int sg = 0; sg < 2; ++sg) {
+                const int g = half * 8 + qi * 2 + sg;
+                const int dot = g4[qi][sg] - 32 * bs[g];
+                weighted += static_cast<int>(static_cast<int8_t>(meta[g])) * dot;
+            }
+        }
+    }
+    const uint16_t d = static_cast<uint16_t>(meta[16] | (meta[17] << 8));
+    return a.xd[b] * h2f(d) * static_cast<float>(weighted);
+}
+
+// Ternary super-block term.  Element e of a TQ2_0 block sits in byte
+// 32 (e / 128) + e % 32 at bit pair 2 ((e % 128) / 32) (src/quant.h:123-130), so
+// bit pair l of bytes 32j..32j+31 is 32 consecutive values.  acc = sum((c - 1) x)
+// is exact.  With `lut16` the float order is the x86 load-time layout's,
+// acc * d_w * x.d (dot_tq2_0x16_q8_k, src/quant.cpp:789-802); else the generic
+// x.d * d_w * acc (dot_tq2_0_q8_k, :580-596).
+__device__ __forceinline__ float term_tq2_0(const Packed& m, uint32_t row, uint32_t b, const ActLds& a, bool lut16) {
+    const uint32_t nsb = m.cols / 256;
+    const size_t blk = static_cast<size_t>(row) * nsb + b;
+    const uint4* qp = reinterpret_cast<const uint4*>(m.p0 + blk * 64);
+    const uint16_t dw = reinterpret_cast<const uint16_t*>(m.p1)[blk];
+    const int32_t* x = a.xs + b * 64;
+    int acc = 0;
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+        const uint4 q0 = qp[2 * j], q1 = qp[2 * j + 1];
+        const uint32_t qw[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
+#pragma unroll
+        for (int l = 0; l < 4; ++l) {
+#pragma unroll
+            for (int k = 0; k < 8; ++k) acc = dot4(static_cast<int>((qw[k] >> (2 * l)) & 0x03030303u), x[j * 32 + l * 8 + k], acc);
+        }
+    }
+    int xsum = 0;
+#pragma unroll
+    for (int g = 0; g < 16; ++g) xsum += a.xsum[b * 16 + g];
+    acc -= xsum;
+    return lut16 ? static_cast<float>(acc) * h2f(dw) * a.xd[b] : a.xd[b] * h2f(dw) * static_cast<float>(acc);
+}
+
+__device__ __forceinline__ float block_term(const Packed& m, uint32_t row, uint32_t b, const ActLds& a) {
+    switch (m.type) {
+        case kQ4_0: return term_q4_0(m, row, b, a);
+        case kQ8_0: return term_q8_0(m, row, b, a);
+        case kQ4_K: return term_q4_k(m, row, b, a);
+        case kQ6_K: return term_q6_k(m, row, b, a);
+        default: return term_tq2_0(m, row, b, a, (m.flags & kFlagLut16) != 0);
+    }
+}
+
+// Row sums of rows [row0, row0 + R) into sums[0..R): the per-block terms go to
+// LDS, then one lane per row adds them in block order, as the reference's
+// sequential `sum +=` does, so each row sum is bit-identical to it.
+// `terms` is LDS of R * (units + 1) floats.  Ends with a barrier.
+__device__ inline void tile_rowsums(const Packed& m, uint32_t row0, int R, const ActLds& a, float* terms, float* sums) {
+    const uint32_t units = m.cols / block_elems(m.type);
+    const uint32_t stride = units + 1;
+    const uint32_t total = static_cast<uint32_t>(R) * units;
+    for (uint32_t u = threadIdx.x; u < total; u += kThreads) {
+        const uint32_t r = u / units, b = u - r * units;
+        const uint32_t row = row0 + r;
+        if (row < m.rows) terms[r * stride + b] = block_term(m, row, b, a);
+    }
+    __syncthreads();
+    if (threadIdx.x < static_cast<uint32_t>(R)) {
+        const float* t = terms + threadIdx.x * stride;
+        float s = 0.0f;
+        for (uint32_t b = 0; b < units; ++b) s += t[b];
+        sums[threadIdx.x] = s;
+    }
+    __syncthreads();
+}
+
+}  // namespace bh

@@ -1,0 +1,95 @@
+// Host-side launchers of the token-loop kernels and their argument blocks.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include "device.h"
+#include "layout.h"
+
+namespace bh {
+
+struct GemvTarget {
+    Packed m;
+    float* out;
+    int R;      // rows per tile (set by the launcher)
+    int tiles;  // tiles of this target (set by the launcher)
+};
+
+struct GemvArgs {
+    GemvTarget t[3];
+    int n;                // targets
+    const float* x;       // activation row (f32)
+    const float* normw;   // rms_norm weight applied to x first, or null
+    float eps;
+    int add;              // 1: out += W x (residual), 0: out = W x
+};
+
+struct QkvArgs {
+    Packed q, k, v;
+    const float* x;
+    const float* normw;   // attn_norm
+    float eps;
+    const float* qnorm;   // per-head q/k RMS weights (Qwen3) or null
+    const float* knorm;
+    const float* rope;    // [max_context][head_dim] cos, sin pairs
+    const int* pos;       // device position of the token
+    float* qout;          // [heads][head_dim]
+    uint16_t* kcache;     // this layer's [kv_heads][ctx][head_dim]
+    uint16_t* vcache;
+    int ctx, head_dim, heads, kv_heads, neox;
+};
+
+struct GateUpArgs {
+    Packed gate, up;
+    int R;
+    const float* x;
+    const float* normw;   // ffn_norm
+    float eps;
+    int relu2;            // BitNet squared-ReLU gate
+    float* act;
+};
+
+struct AttnArgs {
+    const float* q;
+    const uint16_t* kcache;
+    const uint16_t* vcache;
+    const int* pos;
+    int ctx, head_dim, heads, kv_heads;
+    float scale;
+    float* part_acc;      // [heads][max_splits][head_dim]
+    float* part_ml;       // [heads][max_splits][2]
+    int max_splits;
+    unsigned* tickets;    // [kv_heads], zero between launches (the merging workgroup re-arms its own)
+    float* out;           // [heads][head_dim]
+};
+
+constexpr int kArgmaxBlocks = 256;
+
+struct ArgmaxArgs {
+    const float* logits;
+    int n;
+    float* part_v;        // [kArgmaxBlocks]
+    int* part_i;
+    unsigned* ticket;     // zero between launches (the last workgroup re-arms it)
+    int* pos;
+    int advance;          // 1: *pos += 1 after the pick
+    int* seq;             // token sequence by position: seq[*pos + 1] = pick
+    int seq_len;
+    const int* fixed;     // seq[0, *fixed) are caller tokens the pick must not overwrite
+};
+
+hipError_t launch_pack(uint32_t type, const void* src, size_t rows, size_t cols, const Packed& dst, hipStream_t s);
+hipError_t launch_quantize(int kind, const float* x, void* out, size_t count, int bits, hipStream_t s);
+hipError_t launch_matvec_q8(const Packed& m, const void* xq, size_t n, float* out, size_t out_stride, hipStream_t s);
+hipError_t launch_gemv(GemvArgs g, hipStream_t s);
+hipError_t launch_qkv(const QkvArgs& g, hipStream_t s);
+hipError_t launch_gateup(GateUpArgs g, hipStream_t s);
+hipError_t launch_attention(const AttnArgs& g, hipStream_t s);
+hipError_t launch_embed(const Packed& m, const int* seq, const int* pos, float* h, hipStream_t s);
+hipError_t launch_argmax(const ArgmaxArgs& g, hipStream_t s);
+hipError_t launch_advance(int* pos, hipStream_t s);
+hipError_t launch_expf(const float* x, float* y, size_t n, hipStream_t s);
+int attention_max_splits(int ctx);
+int pick_rows_per_tile(uint32_t type, size_t rows, size_t cols);
+
+}  // namespace bh

@@ -1,0 +1,384 @@
+// HipSession: the device-resident token loop behind the C ABI.
+//
+// Counterpart of the reference's Session / MetalSession (src/model.h:223-310,
+// src/metal/metal_session.h:21-37).  Differences in mechanism, not in result:
+//  * weights are copied once to HBM and repacked into planes (layout.h);
+//  * the token sequence and the position live in device memory: the embedding
+//    kernel reads seq[pos], the argmax kernel writes seq[pos + 1] and advances
+//    pos, so one decode step is a fixed launch sequence, captured once as a
+//    hipGraph and replayed per token with no host round trip;
+//  * two step graphs: "layers" (a prompt token whose logits nobody reads, as
+//    eval_batch computes only the last token's logits, src/model.cpp:1201-1205)
+//    and "full" (layers + output projection + greedy pick).
+#include "session.h"
+
+#include <algorithm>
+#include <cmath>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <string>
+#include <vector>
+
+namespace bh {
+
+namespace {
+
+[[noreturn]] void model_fail(const std::string& what) { throw Error(BRISK_HIP_EINVAL, "model: " + what); }
+
+void check(hipError_t e, const char* what) {
+    if (e != hipSuccess) {
+        throw Error(e == hipErrorOutOfMemory || e == hipErrorMemoryAllocation ? BRISK_HIP_ENOMEM : BRISK_HIP_EHIP,
+                    std::string("hip: ") + what + ": " + hipGetErrorString(e));
+    }
+}
+
+}  // namespace
+
+DeviceMatrix::~DeviceMatrix() {
+    if (mem != nullptr) (void)hipFree(mem);
+}
+
+Session::Session(const brisk_hip_config& cfg, const brisk_hip_tensor* tensors, size_t n, size_t max_context, int device)
+    : cfg_(cfg), device_(device) {
+    int count = 0;
+    if (hipGetDeviceCount(&count) != hipSuccess || count == 0) throw Error(BRISK_HIP_ENODEV, "hip: no GPU device available");
+    if (device < 0 || device >= count) throw Error(BRISK_HIP_ENODEV, "hip: no GPU device " + std::to_string(device));
+    if (cfg.arch < BRISK_HIP_ARCH_QWEN3 || cfg.arch > BRISK_HIP_ARCH_BITNET) model_fail("unsupported architecture");
+    if (cfg.embd == 0 || cfg.layers == 0 || cfg.heads == 0 || cfg.kv_heads == 0 || cfg.ff == 0 || cfg.context_length == 0 ||
+        cfg.vocab == 0)
+        model_fail("a model dimension is zero");
+    if (cfg.heads % cfg.kv_heads != 0) model_fail("head_count is not a multiple of head_count_kv");
+    if (cfg.heads / cfg.kv_heads > 16) model_fail("more than 16 query heads per key/value head is not supported");
+    if (cfg.kv_heads > 1000) model_fail("more than 1000 key/value heads is not supported");
+    if (cfg.head_dim == 0 || cfg.head_dim % 32 != 0 || cfg.head_dim > 128) model_fail("head size must be 32, 64, 96 or 128");
+    if (cfg.embd > kMaxCols || cfg.ff > kMaxCols || cfg.heads * cfg.head_dim > kMaxCols) model_fail("a row wider than 8192 is not supported");
+    check(hipSetDevice(device), "hipSetDevice");
+    check(hipStreamCreateWithFlags(&stream_, hipStreamNonBlocking), "hipStreamCreate");
+    max_ctx_ = max_context == 0 ? cfg.context_length : std::min<size_t>(max_context, cfg.context_length);
+
+    auto find = [&](const std::string& name) -> const brisk_hip_tensor* {
+        for (size_t i = 0; i < n; ++i)
+            if (tensors[i].name != nullptr && name == tensors[i].name) return &tensors[i];
+        return nullptr;
+    };
+    // staging for the GGUF bytes of one matrix before its repack
+    size_t staging_bytes = 0;
+    for (size_t i = 0; i < n; ++i) {
+        const brisk_hip_tensor& t = tensors[i];
+        if (t.type != BRISK_HIP_F32) staging_bytes = std::max<size_t>(staging_bytes, t.rows * (t.cols / block_elems(t.type)) * gguf_block_bytes(t.type));
+    }
+    void* staging = nullptr;
+    if (staging_bytes) check(hipMalloc(&staging, staging_bytes), "hipMalloc(staging)");
+
+    auto load_matrix = [&](const std::string& name, size_t rows, size_t cols, DeviceMatrix& m) {
+        const brisk_hip_tensor* t = find(name);
+        if (t == nullptr) model_fail("missing tensor '" + name + "'");
+        if (t->rows != rows || t->cols != cols) model_fail("tensor '" + name + "' has an unexpected shape");
+        const uint32_t type = static_cast<uint32_t>(t->type);
+        if (gguf_block_bytes(type) == 0) model_fail("tensor '" + name + "' has a type the HIP session does not take");
+        if (cols % block_elems(type) != 0) model_fail("tensor '" + name + "' row length is not a multiple of its block size");
+        size_t planes[3];
+        plane_bytes(type, rows, cols, planes);
+        check(hipMalloc(&m.mem, packed_bytes(type, rows, cols)), "hipMalloc(weights)");
+        uint8_t* base = static_cast<uint8_t*>(m.mem);
+        m.p = Packed{base, base + align256(planes[0]), base + align256(planes[0]) + align256(planes[1]),
+                     static_cast<uint32_t>(rows), static_cast<uint32_t>(cols), type, 0u};
+        // x86's load-time TQ2_0x16 layout (rows % 16 == 0) takes 7-bit activations (src/model.cpp:496-503)
+        if (type == kTQ2_0 && rows % 16 == 0) m.p.flags |= kFlagLut16;
+        const size_t bytes = rows * (cols / block_elems(type)) * gguf_block_bytes(type);
+        check(hipMemcpyAsync(staging, t->data, bytes, hipMemcpyHostToDevice, stream_), "hipMemcpy(weights)");
+        check(launch_pack(type, staging, rows, cols, m.p, stream_), "pack");
+        check(hipStreamSynchronize(stream_), "pack sync");
+        weight_bytes_ += bytes;
+    };
+    auto load_vector = [&](const std::string& name, size_t count) -> float* {
+        const brisk_hip_tensor* t = find(name);
+        if (t == nullptr) model_fail("missing tensor '" + name + "'");
+        if (t->rows * t->cols != count) model_fail("tensor '" + name + "' has an unexpected size");
+        if (t->type != BRISK_HIP_F32) model_fail("tensor '" + name + "' is not F32");
+        float* p = static_cast<float*>(alloc(count * sizeof(float)));
+        check(hipMemcpyAsync(p, t->data, count * sizeof(float), hipMemcpyHostToDevice, stream_), "hipMemcpy(vector)");
+        return p;
+    };
+
+    const size_t e = cfg.embd, hd = cfg.head_dim, qd = static_cast<size_t>(cfg.heads) * hd, kvd = static_cast<size_t>(cfg.kv_heads) * hd;
+    load_matrix("token_embd.weight", cfg.vocab, e, embd_);
+    if (find("output.weight") != nullptr) {
+        load_matrix("output.weight", cfg.vocab, e, out_own_);
+        out_ = &out_own_;
+    } else {
+        out_ = &embd_;  // tied (src/model.cpp:328-330)
+    }
+    out_norm_ = load_vector("output_norm.weight", e);
+    layers_.resize(cfg.layers);
+    for (uint32_t l = 0; l < cfg.layers; ++l) {
+        const std::string b = "blk." + std::to_string(l) + ".";
+        Layer& L = layers_[l];
+        L.attn_norm = load_vector(b + "attn_norm.weight", e);
+        load_matrix(b + "attn_q.weight", qd, e, L.q);
+        load_matrix(b + "attn_k.weight", kvd, e, L.k);
+        load_matrix(b + "attn_v.weight", kvd, e, L.v);
+        load_matrix(b + "attn_output.weight", e, qd, L.o);
+        L.ffn_norm = load_vector(b + "ffn_norm.weight", e);
+        load_matrix(b + "ffn_gate.weight", cfg.ff, e, L.gate);
+        load_matrix(b + "ffn_up.weight", cfg.ff, e, L.up);
+        load_matrix(b + "ffn_down.weight", e, cfg.ff, L.down);
+        if (cfg.arch == BRISK_HIP_ARCH_QWEN3) {
+            L.q_norm = load_vector(b + "attn_q_norm.weight", hd);
+            L.k_norm = load_vector(b + "attn_k_norm.weight", hd);
+        }
+        if (cfg.arch == BRISK_HIP_ARCH_BITNET) {
+            L.attn_sub_norm = load_vector(b + "attn_sub_norm.weight", e);
+            L.ffn_sub_norm = load_vector(b + "ffn_sub_norm.weight", cfg.ff);
+        }
+        // one activation row feeds Q, K and V: they must take the same width (src/model.cpp:584-590)
+        if (takes_q8_k(L.q.p.type) != takes_q8_k(L.k.p.type) || takes_q8_k(L.q.p.type) != takes_q8_k(L.v.p.type) ||
+            act_bits(L.q.p) != act_bits(L.k.p) || act_bits(L.q.p) != act_bits(L.v.p) ||
+            takes_q8_k(L.gate.p.type) != takes_q8_k(L.up.p.type) || act_bits(L.gate.p) != act_bits(L.up.p))
+            model_fail("fused multiply mixes activation widths");
+    }
+    if (staging) check(hipFree(staging), "hipFree(staging)");
+
+    // activations and state
+    h_ = static_cast<float*>(alloc(e * 4));
+    q_ = static_cast<float*>(alloc(qd * 4));
+    att_ = static_cast<float*>(alloc(qd * 4));
+    act_ = static_cast<float*>(alloc(static_cast<size_t>(cfg.ff) * 4));
+    logits_ = static_cast<float*>(alloc(static_cast<size_t>(cfg.vocab) * 4));
+    max_splits_ = attention_max_splits(static_cast<int>(max_ctx_));
+    part_acc_ = static_cast<float*>(alloc(static_cast<size_t>(cfg.heads) * max_splits_ * hd * 4));
+    part_ml_ = static_cast<float*>(alloc(static_cast<size_t>(cfg.heads) * max_splits_ * 2 * 4));
+    arg_v_ = static_cast<float*>(alloc(kArgmaxBlocks * 4));
+    arg_i_ = static_cast<int*>(alloc(kArgmaxBlocks * 4));
+    ticket_ = static_cast<unsigned*>(alloc(4096));
+    pos_ = static_cast<int*>(alloc(64));
+    seq_ = static_cast<int*>(alloc((max_ctx_ + 1) * 4));
+    check(hipMemsetAsync(ticket_, 0, 4096, stream_), "memset");
+    check(hipMemsetAsync(pos_, 0, 64, stream_), "memset");
+    check(hipMemsetAsync(seq_, 0, (max_ctx_ + 1) * 4, stream_), "memset");
+    const size_t kv_bytes = static_cast<size_t>(cfg.kv_heads) * max_ctx_ * hd * 2;
+    kcache_.resize(cfg.layers);
+    vcache_.resize(cfg.layers);
+    for (uint32_t l = 0; l < cfg.layers; ++l) {
+        kcache_[l] = static_cast<uint16_t*>(alloc(kv_bytes));
+        vcache_[l] = static_cast<uint16_t*>(alloc(kv_bytes));
+        check(hipMemsetAsync(kcache_[l], 0, kv_bytes, stream_), "memset");
+        check(hipMemsetAsync(vcache_[l], 0, kv_bytes, stream_), "memset");
+    }
+    kv_bytes_ = kv_bytes;
+
+    // RoPE table, built on the host exactly as build_rope does (src/model.cpp:880-894):
+    // theta_scale = base^(-2/dim); theta = pos * scale, multiplied by theta_scale per pair.
+    {
+        std::vector<float> rope(max_ctx_ * hd);
+        const float theta_scale = std::pow(cfg.rope_base, -2.0f / static_cast<float>(hd));
+        for (size_t p = 0; p < max_ctx_; ++p) {
+            float theta = static_cast<float>(p) * 1.0f;
+            float* r = rope.data() + p * hd;
+            for (size_t i = 0; i < hd / 2; ++i) {
+                r[2 * i] = std::cos(theta) * 1.0f;
+                r[2 * i + 1] = std::sin(theta) * 1.0f;
+                theta *= theta_scale;
+            }
+        }
+        rope_ = static_cast<float*>(alloc(rope.size() * 4));
+        check(hipMemcpy(rope_, rope.data(), rope.size() * 4, hipMemcpyHostToDevice), "hipMemcpy(rope)");
+    }
+    check(hipStreamSynchronize(stream_), "init sync");
+    debug_ = std::getenv("BRISK_HIP_DEBUG") != nullptr;
+    use_graphs_ = std::getenv("BRISK_HIP_NO_GRAPH") == nullptr && !debug_;
+    if (use_graphs_) {
+        graph_layers_ = capture(false);
+        graph_full_ = capture(true);
+    }
+}
+
+Session::~Session() {
+    if (graph_layers_) (void)hipGraphExecDestroy(graph_layers_);
+    if (graph_full_) (void)hipGraphExecDestroy(graph_full_);
+    for (void* p : owned_) (void)hipFree(p);
+    if (stream_) (void)hipStreamDestroy(stream_);
+}
+
+void* Session::alloc(size_t bytes) {
+    void* p = nullptr;
+    check(hipMalloc(&p, bytes < 64 ? 64 : bytes), "hipMalloc");
+    owned_.push_back(p);
+    return p;
+}
+
+// One decode step at *pos_: embed seq[*pos_], every layer, then either the
+// output projection + greedy pick (which advances *pos_) or a bare advance.
+void Session::record_step(bool full) {
+    check(launch_embed(embd_.p, seq_, pos_, h_, stream_), "embed");
+    const float scale = 1.0f / std::sqrt(static_cast<float>(cfg_.head_dim));  // src/model.cpp:978
+    for (uint32_t l = 0; l < cfg_.layers; ++l) {
+        const Layer& L = layers_[l];
+        QkvArgs qa{};
+        qa.q = L.q.p; qa.k = L.k.p; qa.v = L.v.p;
+        qa.x = h_; qa.normw = L.attn_norm; qa.eps = cfg_.rms_epsilon;
+        qa.qnorm = L.q_norm; qa.knorm = L.k_norm; qa.rope = rope_; qa.pos = pos_;
+        qa.qout = q_; qa.kcache = kcache_[l]; qa.vcache = vcache_[l];
+        qa.ctx = static_cast<int>(max_ctx_); qa.head_dim = static_cast<int>(cfg_.head_dim);
+        qa.heads = static_cast<int>(cfg_.heads); qa.kv_heads = static_cast<int>(cfg_.kv_heads);
+        qa.neox = cfg_.arch != BRISK_HIP_ARCH_LLAMA;  // src/model.cpp:167
+        check(launch_qkv(qa, stream_), "qkv");
+
+        AttnArgs aa{};
+        aa.q = q_; aa.kcache = kcache_[l]; aa.vcache = vcache_[l]; aa.pos = pos_;
+        aa.ctx = qa.ctx; aa.head_dim = qa.head_dim; aa.heads = qa.heads; aa.kv_heads = qa.kv_heads;
+        aa.scale = scale; aa.part_acc = part_acc_; aa.part_ml = part_ml_; aa.max_splits = max_splits_; aa.tickets = ticket_ + 1; aa.out = att_;
+        check(launch_attention(aa, stream_), "attention");
+
+        GemvArgs oa{};
+        oa.n = 1; oa.t[0].m = L.o.p; oa.t[0].out = h_;
+        oa.x = att_; oa.normw = L.attn_sub_norm; oa.eps = cfg_.rms_epsilon; oa.add = 1;
+        check(launch_gemv(oa, stream_), "attn_output");
+
+        GateUpArgs ga{};
+        ga.gate = L.gate.p; ga.up = L.up.p; ga.x = h_; ga.normw = L.ffn_norm; ga.eps = cfg_.rms_epsilon;
+        ga.relu2 = cfg_.arch == BRISK_HIP_ARCH_BITNET; ga.act = act_;
+        check(launch_gateup(ga, stream_), "gate_up");
+
+        GemvArgs da{};
+        da.n = 1; da.t[0].m = L.down.p; da.t[0].out = h_;
+        da.x = act_; da.normw = L.ffn_sub_norm; da.eps = cfg_.rms_epsilon; da.add = 1;
+        check(launch_gemv(da, stream_), "ffn_down");
+        if (debug_) debug_layer(l);
+    }
+    if (full) {
+        GemvArgs oa{};
+        oa.n = 1; oa.t[0].m = out_->p; oa.t[0].out = logits_;
+        oa.x = h_; oa.normw = out_norm_; oa.eps = cfg_.rms_epsilon; oa.add = 0;
+        check(launch_gemv(oa, stream_), "output");
+        ArgmaxArgs ar{};
+        ar.logits = logits_; ar.n = static_cast<int>(cfg_.vocab); ar.part_v = arg_v_; ar.part_i = arg_i_;
+        ar.ticket = ticket_; ar.pos = pos_; ar.advance = 1; ar.seq = seq_; ar.seq_len = static_cast<int>(max_ctx_) + 1;
+        ar.fixed = pos_ + 1;
+        check(launch_argmax(ar, stream_), "argmax");
+    } else {
+        check(launch_advance(pos_, stream_), "advance");
+    }
+}
+
+hipGraphExec_t Session::capture(bool full) {
+    hipGraph_t graph = nullptr;
+    check(hipStreamBeginCapture(stream_, hipStreamCaptureModeThreadLocal), "hipStreamBeginCapture");
+    try {
+        record_step(full);
+    } catch (...) {
+        (void)hipStreamEndCapture(stream_, &graph);
+        if (graph) (void)hipGraphDestroy(graph);
+        throw;
+    }
+    check(hipStreamEndCapture(stream_, &graph), "hipStreamEndCapture");
+    hipGraphExec_t exec = nullptr;
+    check(hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0), "hipGraphInstantiate");
+    check(hipGraphDestroy(graph), "hipGraphDestroy");
+    return exec;
+}
+
+void Session::step(bool full) {
+    if (use_graphs_) check(hipGraphLaunch(full ? graph_full_ : graph_layers_, stream_), "hipGraphLaunch");
+    else record_step(full);
+}
+
+// BRISK_HIP_DEBUG: the reference's BRISK_CPU_DEBUG line (src/model.cpp:1183-1192) after
+// each layer, for a layer-by-layer comparison with the CPU (steps then run uncaptured).
+void Session::debug_layer(uint32_t l) {
+    std::vector<float> h(cfg_.embd);
+    int pos = 0;
+    check(hipStreamSynchronize(stream_), "debug sync");
+    check(hipMemcpy(h.data(), h_, h.size() * 4, hipMemcpyDeviceToHost), "debug copy");
+    check(hipMemcpy(&pos, pos_, 4, hipMemcpyDeviceToHost), "debug copy");
+    double sum = 0.0;
+    float peak = 0.0f;
+    for (const float v : h) {
+        sum += std::fabs(v);
+        peak = std::max(peak, std::fabs(v));
+    }
+    std::fprintf(stderr, "layer %u pos %d: max|h| %.4f mean|h| %.6f  h[0..3] %.5f %.5f %.5f %.5f\n", l, pos, peak,
+                 sum / cfg_.embd, h[0], h[1], h[2], h[3]);
+}
+
+void Session::validate(const int32_t* tokens, size_t n) const {
+    if (n == 0) throw Error(BRISK_HIP_EINVAL, "model: no tokens to evaluate");
+    for (size_t i = 0; i < n; ++i)
+        if (tokens[i] < 0 || static_cast<uint32_t>(tokens[i]) >= cfg_.vocab) throw Error(BRISK_HIP_EINVAL, "model: token id out of range");
+    if (n > max_ctx_ - position_) throw Error(BRISK_HIP_EINVAL, "model: context length exceeded");
+}
+
+// Writes tokens to seq[position_ ..], syncs the device position to the host's and
+// marks seq[0, position_ + n) as caller tokens (pos_[1]).
+void Session::stage(const int32_t* tokens, size_t n) {
+    check(hipMemcpyAsync(seq_ + position_, tokens, n * 4, hipMemcpyHostToDevice, stream_), "hipMemcpy(tokens)");
+    const int p[2] = {static_cast<int>(position_), static_cast<int>(position_ + n)};
+    check(hipMemcpyAsync(pos_, p, 8, hipMemcpyHostToDevice, stream_), "hipMemcpy(pos)");
+    check(hipStreamSynchronize(stream_), "stage sync");  // the host copies above read stack memory
+}
+
+void Session::eval(const int32_t* tokens, size_t n, float* logits) {
+    validate(tokens, n);
+    stage(tokens, n);
+    for (size_t i = 0; i + 1 < n; ++i) step(false);
+    step(true);
+    if (logits != nullptr) check(hipMemcpyAsync(logits, logits_, static_cast<size_t>(cfg_.vocab) * 4, hipMemcpyDeviceToHost, stream_), "hipMemcpy(logits)");
+    check(hipStreamSynchronize(stream_), "eval sync");
+    position_ += n;
+}
+
+void Session::eval_all(const int32_t* tokens, size_t n, float* logits) {
+    if (n == 0 || n > 64) throw Error(BRISK_HIP_EINVAL, "model: eval_all takes 1 to 64 tokens");
+    validate(tokens, n);
+    stage(tokens, n);
+    for (size_t i = 0; i < n; ++i) {
+        step(true);
+        check(hipMemcpyAsync(logits + i * cfg_.vocab, logits_, static_cast<size_t>(cfg_.vocab) * 4, hipMemcpyDeviceToHost, stream_),
+              "hipMemcpy(logits)");
+    }
+    check(hipStreamSynchronize(stream_), "eval_all sync");
+    position_ += n;
+}
+
+int32_t Session::picked() {
+    int32_t next = 0;
+    check(hipMemcpy(&next, seq_ + position_, 4, hipMemcpyDeviceToHost), "hipMemcpy(next)");
+    return next;
+}
+
+int32_t Session::eval_greedy(const int32_t* tokens, size_t n) {
+    eval(tokens, n, nullptr);
+    return picked();  // the argmax of the last step wrote seq[position_]
+}
+
+void Session::generate(const int32_t* prompt, size_t n_prompt, size_t n_gen, int32_t* out) {
+    if (n_gen == 0) return;
+    validate(prompt, n_prompt);
+    if (n_gen - 1 > max_ctx_ - position_ - n_prompt) throw Error(BRISK_HIP_EINVAL, "model: context length exceeded");
+    eval(prompt, n_prompt, nullptr);
+    const size_t first = position_;  // seq[first] holds the first pick
+    // each further step embeds the previous pick (seq[pos]) and writes the next one
+    for (size_t i = 1; i < n_gen; ++i) step(true);
+    check(hipMemcpyAsync(out, seq_ + first, n_gen * 4, hipMemcpyDeviceToHost, stream_), "hipMemcpy(ids)");
+    check(hipStreamSynchronize(stream_), "generate sync");
+    position_ += n_gen - 1;
+}
+
+void Session::rollback(size_t position) {
+    if (position > position_) throw Error(BRISK_HIP_EINVAL, "model: cannot roll forward");  // src/model.cpp:736
+    position_ = position;  // the caches keep their storage; later entries are overwritten
+}
+
+void Session::set_position(size_t position) {
+    if (position > max_ctx_) throw Error(BRISK_HIP_EINVAL, "model: context length exceeded");
+    position_ = position;
+}
+
+void Session::kv_cache(int layer, int value, void** ptr, size_t* bytes) {
+    if (layer < 0 || static_cast<uint32_t>(layer) >= cfg_.layers) throw Error(BRISK_HIP_EINVAL, "model: layer out of range");
+    *ptr = value ? static_cast<void*>(vcache_[layer]) : static_cast<void*>(kcache_[layer]);
+    *bytes = kv_bytes_;
+}
+
+}  // namespace bh

@@ -1,0 +1,95 @@
+// Host-side state of one device-resident sequence (see session.cpp).
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <stdexcept>
+#include <string>
+#include <vector>
+
+#include "../../include/brisk_hip.h"
+#include "launch.h"
+
+namespace bh {
+
+// An error with the C ABI status it maps to.
+struct Error : std::runtime_error {
+    int code;
+    Error(int c, const std::string& what) : std::runtime_error(what), code(c) {}
+};
+
+struct DeviceMatrix {
+    Packed p{};
+    void* mem = nullptr;
+    DeviceMatrix() = default;
+    DeviceMatrix(const DeviceMatrix&) = delete;
+    DeviceMatrix& operator=(const DeviceMatrix&) = delete;
+    DeviceMatrix(DeviceMatrix&& o) noexcept : p(o.p), mem(o.mem) { o.mem = nullptr; }
+    ~DeviceMatrix();
+};
+
+struct Layer {
+    DeviceMatrix q, k, v, o, gate, up, down;
+    const float* attn_norm = nullptr;
+    const float* q_norm = nullptr;
+    const float* k_norm = nullptr;
+    const float* attn_sub_norm = nullptr;
+    const float* ffn_norm = nullptr;
+    const float* ffn_sub_norm = nullptr;
+};
+
+class Session {
+public:
+    Session(const brisk_hip_config& cfg, const brisk_hip_tensor* tensors, size_t n, size_t max_context, int device);
+    ~Session();
+    Session(const Session&) = delete;
+    Session& operator=(const Session&) = delete;
+
+    void eval(const int32_t* tokens, size_t n, float* logits);
+    void eval_all(const int32_t* tokens, size_t n, float* logits);
+    int32_t eval_greedy(const int32_t* tokens, size_t n);
+    void generate(const int32_t* prompt, size_t n_prompt, size_t n_gen, int32_t* out);
+    void rollback(size_t position);
+    void set_position(size_t position);
+    size_t position() const { return position_; }
+    size_t max_context() const { return max_ctx_; }
+    void kv_cache(int layer, int value, void** ptr, size_t* bytes);
+    hipStream_t stream() const { return stream_; }
+    int device() const { return device_; }
+
+private:
+    void* alloc(size_t bytes);
+    void record_step(bool full);
+    hipGraphExec_t capture(bool full);
+    void step(bool full);
+    void validate(const int32_t* tokens, size_t n) const;
+    void stage(const int32_t* tokens, size_t n);
+    int32_t picked();
+    void debug_layer(uint32_t l);
+
+    brisk_hip_config cfg_;
+    int device_;
+    hipStream_t stream_ = nullptr;
+    size_t max_ctx_ = 0;
+    size_t position_ = 0;
+    size_t weight_bytes_ = 0;
+    std::vector<void*> owned_;
+    DeviceMatrix embd_, out_own_;
+    const DeviceMatrix* out_ = nullptr;
+    const float* out_norm_ = nullptr;
+    std::vector<Layer> layers_;
+    std::vector<uint16_t*> kcache_, vcache_;
+    size_t kv_bytes_ = 0;
+    float *h_ = nullptr, *q_ = nullptr, *att_ = nullptr, *act_ = nullptr, *logits_ = nullptr, *rope_ = nullptr;
+    float *part_acc_ = nullptr, *part_ml_ = nullptr, *arg_v_ = nullptr;
+    int* arg_i_ = nullptr;
+    unsigned* ticket_ = nullptr;
+    int* pos_ = nullptr;
+    int* seq_ = nullptr;
+    int max_splits_ = 0;
+    bool use_graphs_ = true;
+    bool debug_ = false;
+    hipGraphExec_t graph_layers_ = nullptr, graph_full_ = nullptr;
+};
+
+}  // namespace bh

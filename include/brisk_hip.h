@@ -1,0 +1,161 @@
+/* brisk_hip — the C ABI of the MI355X (gfx950) token loop for brisk-llm.
+ *
+ * Plain pointers and sizes only.  Two layers:
+ *
+ *  1. Kernel level: the counterpart of the reference's kernel dispatch ABI,
+ *     `KernelSet{Matvec, Matmul, Prepare, PreparedBytes}` (src/kernels.h:19-39),
+ *     on device memory and a HIP stream (passed as void*; NULL = default stream).
+ *     Used by the parity tests to pin the HIP arithmetic against the reference's
+ *     scalar dot products (src/quant.cpp:445-596).
+ *
+ *  2. Session level: the counterpart of `class Engine` (src/engine.h:13-37) as
+ *     the reference's `Session` (src/model.h:223-310) and `MetalSession`
+ *     (src/metal/metal_session.h:21-37) implement it: eval / eval_all /
+ *     rollback / position, over the weights of a `Model(file, repack = false)`
+ *     (src/model.cpp:303-530) passed as a table of GGUF-layout tensors.
+ *
+ * Every call returns 0 on success or a negative BRISK_HIP_E* code; the message,
+ * worded as the reference words the same failure where it has one (e.g.
+ * "model: context length exceeded", src/model.cpp:704-736), is then available
+ * from brisk_hip_last_error() on the calling thread.  Session calls are
+ * synchronous: results are in host memory when they return.  A session is not
+ * reentrant (like Engine): one caller at a time.
+ */
+#ifndef BRISK_HIP_H
+#define BRISK_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define BRISK_HIP_ABI_VERSION 1
+
+enum {
+    BRISK_HIP_OK = 0,
+    BRISK_HIP_EINVAL = -1,    /* bad argument, shape or model (std::runtime_error in the reference) */
+    BRISK_HIP_ENODEV = -2,    /* no usable GPU */
+    BRISK_HIP_EHIP = -3,      /* a HIP runtime call failed */
+    BRISK_HIP_ENOMEM = -4     /* device allocation failed */
+};
+
+/* Tensor types: the ggml numbers a GGUF file uses (src/gguf.h:22-27). */
+enum {
+    BRISK_HIP_F32 = 0,
+    BRISK_HIP_Q4_0 = 2,
+    BRISK_HIP_Q8_0 = 8,
+    BRISK_HIP_Q4_K = 12,
+    BRISK_HIP_Q6_K = 14,
+    BRISK_HIP_TQ2_0 = 35
+};
+
+/* Model families on this path (Architecture, src/model.h:21-32). */
+enum { BRISK_HIP_ARCH_QWEN3 = 0, BRISK_HIP_ARCH_LLAMA = 1, BRISK_HIP_ARCH_BITNET = 2 };
+
+/* The fields of ModelConfig (src/model.h:36-60) this path reads. */
+typedef struct {
+    int arch;
+    uint32_t vocab, embd, layers, heads, kv_heads, head_dim, ff, context_length;
+    float rope_base, rms_epsilon;
+} brisk_hip_config;
+
+/* One model tensor in GGUF layout (host memory, e.g. the file's mmap):
+ * matrices are rows x cols blocks as stored (GGUF dims {cols, rows}),
+ * vectors have rows = 1 and type BRISK_HIP_F32.  Names are the GGUF names the
+ * reference's loader reads (token_embd.weight, blk.N.attn_q.weight, ...). */
+typedef struct {
+    const char* name;
+    int type;
+    uint64_t rows, cols;
+    const void* data;
+} brisk_hip_tensor;
+
+typedef struct brisk_hip_session brisk_hip_session;
+
+const char* brisk_hip_last_error(void);
+int brisk_hip_abi_version(void);
+int brisk_hip_device_count(int* count);
+
+/* ---------------------------------------------------------------- kernel level */
+
+/* Device bytes of a matrix after the load-time repack (counterpart of
+ * KernelSet::PreparedBytes, src/kernels.h:31-32, for weights). */
+size_t brisk_hip_packed_bytes(int type, size_t rows, size_t cols);
+
+/* Repacks rows x cols GGUF blocks (device memory) into the coalesced HBM layout
+ * at `packed` (brisk_hip_packed_bytes bytes).  Replaces the reference's
+ * load-time repacks (src/model.cpp:481-525). */
+int brisk_hip_pack(int type, const void* gguf_blocks, size_t rows, size_t cols, void* packed, void* stream);
+
+/* quantize_q8_0 / quantize_q8_k(bits) (src/quant.h:202-203, src/quant.cpp:115-194):
+ * `count` floats -> GGUF BlockQ8_0 (34 B) / BlockQ8_K (292 B) rows, bit-exact. */
+int brisk_hip_quantize_q8_0(const float* x, void* out, size_t count, void* stream);
+int brisk_hip_quantize_q8_k(const float* x, void* out, size_t count, int bits, void* stream);
+
+/* KernelSet::matvec and ::matmul (src/kernels.h:19-25): out[t*out_stride + r] =
+ * dot(row r, activation row t) over a packed matrix and pre-quantised
+ * activations (Q8_0 rows for Q4_0/Q8_0, Q8_K rows for Q4_K/Q6_K/TQ2_0).  Each
+ * output is bit-identical to the reference's generic kernels. `flags`: bit 0
+ * selects, for TQ2_0, the x86 TQ2_0x16 arithmetic (src/quant.cpp:789-802). */
+int brisk_hip_matvec(int type, int flags, const void* packed, size_t rows, size_t cols, const void* xq, float* out,
+                     void* stream);
+int brisk_hip_matmul(int type, int flags, const void* packed, size_t rows, size_t cols, const void* xq, size_t n,
+                     float* out, size_t out_stride, void* stream);
+
+/* The decode GEMV of the token loop: quantises the f32 row x in-kernel (after
+ * rms_norm with weight `norm_w` and `eps` when norm_w is non-null), then
+ * out = W x, or out += W x when `accumulate` (the residual update). */
+int brisk_hip_gemv(int type, int flags, const void* packed, size_t rows, size_t cols, const float* x,
+                   const float* norm_w, float eps, float* out, int accumulate, void* stream);
+
+/* expf exactly as the reference's host libm computes it (glibc's expf, which
+ * softmax_f32 and silu_mul_f32 call: src/kernels_f32.cpp:276-289); the token
+ * loop's softmax and SiLU use the same device routine.  y[i] = expf(x[i]). */
+int brisk_hip_expf(const float* x, float* y, size_t n, void* stream);
+
+/* ---------------------------------------------------------------- session level */
+
+/* Engine construction, as `MetalSession(model, file bytes, max_context)`
+ * (src/main.cpp:206): copies and repacks every tensor to the GPU `device`.
+ * max_context 0 = the model's context length; otherwise min of both. */
+int brisk_hip_session_create(const brisk_hip_config* config, const brisk_hip_tensor* tensors, size_t n_tensors,
+                             size_t max_context, int device, brisk_hip_session** out);
+void brisk_hip_session_destroy(brisk_hip_session* s);
+
+/* Engine::eval (src/engine.h:17-21): appends tokens, writes the last token's
+ * vocab logits to `logits` (host; may be NULL to skip the copy). */
+int brisk_hip_session_eval(brisk_hip_session* s, const int32_t* tokens, size_t n, float* logits);
+
+/* Engine::eval_all (src/engine.h:23-26): 1..64 tokens, logits of every token ([n][vocab], host). */
+int brisk_hip_session_eval_all(brisk_hip_session* s, const int32_t* tokens, size_t n, float* logits);
+
+/* eval followed by the greedy pick on the device (Sampler::sample at
+ * temperature 0, src/sampler.cpp:11-13: first index of the max); no logits copy. */
+int brisk_hip_session_eval_greedy(brisk_hip_session* s, const int32_t* tokens, size_t n, int32_t* next);
+
+/* cmd_generate's greedy loop (src/main.cpp:220-299) with the loop on the
+ * device: eval(prompt), then n_gen picks, each evaluated but the last.
+ * out[n_gen] receives the picked ids. */
+int brisk_hip_session_generate(brisk_hip_session* s, const int32_t* prompt, size_t n_prompt, size_t n_gen, int32_t* out);
+
+/* Engine::rollback / position (src/engine.h:28-31). */
+int brisk_hip_session_rollback(brisk_hip_session* s, size_t position);
+size_t brisk_hip_session_position(const brisk_hip_session* s);
+size_t brisk_hip_session_max_context(const brisk_hip_session* s);
+
+/* Device pointer and size of layer `layer`'s fp16 key (value = 0) or value (1)
+ * cache, laid out [kv_head][max_context][head_dim] as the reference's
+ * (src/model.cpp:984-991).  With brisk_hip_session_set_position it lets a
+ * caller install a pre-filled cache (no Engine counterpart). */
+int brisk_hip_session_kv_cache(brisk_hip_session* s, int layer, int value, void** device_ptr, size_t* bytes);
+int brisk_hip_session_set_position(brisk_hip_session* s, size_t position);
+
+/* The session's HIP stream (hipStream_t), for timing with events. */
+void* brisk_hip_session_stream(brisk_hip_session* s);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -439,6 +439,69 @@ static void apply_rope(float* head, const float* rope, size_t dim, int neox) {
     }
 }
 
+/* ------------------------------------------------------------------ expf */
+
+/* glibc's expf, as the reference calls it (std::exp on float). */
+void or_expf_batch(const float* x, float* y, size_t n) {
+    for (size_t i = 0; i < n; ++i) y[i] = expf(x[i]);
+}
+
+/* The restatement of glibc's expf that the HIP token loop runs (its table-driven
+ * double-precision algorithm, with the x86-64 FMA variant's fused reduction
+ * r = x * 32/ln2 - k).  or_expf_check compares it with the host's expf on every
+ * `stride`-th 32-bit pattern and returns the number of differing results. */
+static uint64_t g_exp_tab[32];
+static float expf_restated(float x) {
+    uint32_t ux;
+    memcpy(&ux, &x, 4);
+    const uint32_t abstop = (ux >> 20) & 0x7FF;
+    if (abstop >= 0x42Bu) {
+        if (ux == 0xFF800000u) return 0.0f;
+        if (abstop >= 0x7F8u) return x + x;
+        if (x > 0x1.62e42ep6f) return INFINITY;
+        if (x < -0x1.9fe368p6f) return 0.0f;
+    }
+    const double inv_ln2_n = 0x1.71547652b82fep+0 * 32.0, shift = 0x1.8p+52;
+    const double c0 = 0x1.c6af84b912394p-5 / 32.0 / 32.0 / 32.0, c1 = 0x1.ebfce50fac4f3p-3 / 32.0 / 32.0,
+                 c2 = 0x1.62e42ff0c52d6p-1 / 32.0;
+    const double xd = (double)x, z = inv_ln2_n * xd;
+    double kd = z + shift;
+    uint64_t ki;
+    memcpy(&ki, &kd, 8);
+    kd -= shift;
+    const double r = fma(inv_ln2_n, xd, -kd);
+    const uint64_t t = g_exp_tab[ki % 32] + (ki << 47);
+    double s;
+    memcpy(&s, &t, 8);
+    const double p = fma(c0, r, c1), r2 = r * r;
+    double y = fma(c2, r, 1.0);
+    y = fma(p, r2, y);
+    return (float)(y * s);
+}
+
+uint64_t or_expf_check(uint32_t stride, uint64_t* checked) {
+    for (int i = 0; i < 32; ++i) {
+        const double d = exp2((double)i / 32.0);
+        memcpy(&g_exp_tab[i], &d, 8);
+        g_exp_tab[i] -= ((uint64_t)i << 52) / 32;
+    }
+    uint64_t bad = 0, n = 0;
+    for (uint64_t b = 0; b <= 0xFFFFFFFFull; b += stride) {
+        const uint32_t bits = (uint32_t)b;
+        float x;
+        memcpy(&x, &bits, 4);
+        if (isnan(x)) continue;
+        const float a = expf(x), e = expf_restated(x);
+        uint32_t ua, ue;
+        memcpy(&ua, &a, 4);
+        memcpy(&ue, &e, 4);
+        bad += ua != ue;
+        ++n;
+    }
+    if (checked) *checked = n;
+    return bad;
+}
+
 /* ------------------------------------------------------------------ session */
 
 typedef struct {
@@ -670,6 +733,16 @@ static void forward_token(oracle_session* s, int32_t token, float* logits) {
         multiply(s, &L->down, s->gate, s->proj);
         for (size_t i = 0; i < embd; ++i) s->h[i] += s->proj[i];
         (void)kvd;
+        if (getenv("BRISK_CPU_DEBUG") != NULL) { /* the reference's per-layer line, src/model.cpp:1183-1192 */
+            double sum = 0.0;
+            float peak = 0.0f;
+            for (size_t i = 0; i < embd; ++i) {
+                sum += fabs(s->h[i]);
+                if (fabsf(s->h[i]) > peak) peak = fabsf(s->h[i]);
+            }
+            fprintf(stderr, "layer %d pos %zu: max|h| %.4f mean|h| %.6f  h[0..3] %.5f %.5f %.5f %.5f\n", l, pos, peak,
+                    sum / (double)embd, s->h[0], s->h[1], s->h[2], s->h[3]);
+        }
     }
     if (logits) {
         or_rms_norm(s->h, s->out_norm, c->eps, s->normed, embd);

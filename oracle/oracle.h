@@ -55,6 +55,9 @@ void or_repack_tq2_0x16(const void* in, size_t rows, size_t blocks, void* out);
 float or_dot_f32(const float* a, const float* b, size_t n);
 void or_softmax(float* x, size_t n);
 void or_rms_norm(const float* x, const float* w, float eps, float* out, size_t n);
+/* glibc expf over a batch, and the check of the HIP loop's restatement of it. */
+void or_expf_batch(const float* x, float* y, size_t n);
+uint64_t or_expf_check(uint32_t stride, uint64_t* checked);
 /* Activation bits a matrix of `type` with `rows` rows takes on x86 (src/model.cpp:496-503, src/quant.cpp:144). */
 int or_activation_bits(int type, size_t rows);
 

@@ -65,6 +65,9 @@ def oracle_lib():
         L.or_dot_f32.restype = _f
         L.or_softmax.argtypes = [_vp, _sz]
         L.or_rms_norm.argtypes = [_vp, _vp, _f, _vp, _sz]
+        L.or_expf_batch.argtypes = [_vp, _vp, _sz]
+        L.or_expf_check.argtypes = [C.c_uint32, C.POINTER(C.c_uint64)]
+        L.or_expf_check.restype = C.c_uint64
         L.or_activation_bits.argtypes = [_i, _sz]
         L.or_activation_bits.restype = _i
         L.or_session_create.argtypes = [C.POINTER(OracleConfig), C.POINTER(OracleTensor), _sz]

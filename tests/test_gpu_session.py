@@ -1,0 +1,77 @@
+"""GPU parity of the HIP session (Engine counterpart) against the oracle.
+
+Tiny models of each family the benchmark configs use, seeded: prompt logits
+within 2e-2 (fp32 accumulation-order tolerance of the north star), greedy ids
+identical, eval_all rows, rollback, and the reference's error messages.
+"""
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+torch = pytest.importorskip("torch")
+
+from brisk_hip import BriskHipError, HipSession, model, synth  # noqa: E402
+import pyoracle  # noqa: E402
+
+TOL = 2e-2
+FAMILIES = ["tiny-qwen3", "tiny-llama", "tiny-q8", "tiny-bitnet"]
+
+
+@pytest.fixture(scope="module", params=FAMILIES)
+def pair(request):
+    assert torch.cuda.is_available()
+    name = request.param
+    f, cfg, table = model.load(synth.model_path(name))
+    print(f"[session] {name}", flush=True)
+    s = HipSession((f, cfg, table), max_context=256)
+    o = pyoracle.Oracle(cfg, table, 256)
+    yield name, cfg, s, o
+    s.close()
+    o.close()
+
+
+def test_prompt_logits_and_greedy(pair):
+    name, cfg, s, o = pair
+    s.rollback(0)
+    o.rollback(0)
+    prompt = synth.prompt_ids(12, cfg.vocab)
+    got, want = s.eval(prompt), o.eval(prompt)
+    assert np.abs(got - want).max() <= TOL, name
+    assert int(np.argmax(got)) == int(np.argmax(want))
+    ids = s.generate([int(np.argmax(got))], 24)
+    o_ids, gaps = o.generate([int(np.argmax(want))], 24)
+    np.testing.assert_array_equal(ids, o_ids, err_msg=f"{name}: gaps {gaps}")
+    assert s.position == o.position == 12 + 24
+
+
+def test_eval_all_and_rollback(pair):
+    name, cfg, s, o = pair
+    s.rollback(0)
+    o.rollback(0)
+    toks = synth.prompt_ids(5, cfg.vocab, seed=3)
+    got, want = s.eval_all(toks), o.eval(toks, all_logits=True)
+    assert got.shape == (5, cfg.vocab)
+    assert np.abs(got - want).max() <= TOL
+    # roll back to 2 and continue: the same as evaluating from there in one go
+    s.rollback(2)
+    o.rollback(2)
+    g2, w2 = s.eval(toks[2:]), o.eval(toks[2:])
+    assert np.abs(g2 - w2).max() <= TOL
+    assert np.abs(g2 - got[-1]).max() <= 1e-5
+    assert s.eval_greedy([7]) == int(np.argmax(o.eval([7])))
+
+
+def test_errors(pair):
+    name, cfg, s, o = pair
+    with pytest.raises(BriskHipError, match="token id out of range"):
+        s.eval([cfg.vocab])
+    with pytest.raises(BriskHipError, match="no tokens to evaluate"):
+        s.eval(np.zeros(0, np.int32))
+    with pytest.raises(BriskHipError, match="cannot roll forward"):
+        s.rollback(s.position + 1)
+    with pytest.raises(BriskHipError, match="eval_all takes 1 to 64 tokens"):
+        s.eval_all(np.zeros(65, np.int32))
+    s.rollback(0)
+    with pytest.raises(BriskHipError, match="context length exceeded"):
+        s.eval(np.zeros(257, np.int32))
