@@ -1,0 +1,230 @@
+#!/usr/bin/env python3
+"""Benchmark of the brisk-llm token loop on one MI355X.
+
+Workload: the Qwen3-0.6B-shaped decoder, Q4_0 layers with
+Q8_0 embeddings and output, random weights from a seeded GGUF; 32 random prompt
+ids, then greedy decode.  A "step" is one decode token: the full forward pass
+(28 layers + output projection + on-device greedy pick), replayed from a
+captured hipGraph.  Inputs (weights, KV cache, token sequence) are resident in
+HBM when the timed region starts.
+
+Printed (one JSON line): decode tok/s as `value`, plus
+  roofline      the dominant kernel (the output-projection GEMV, 151936 x 1024
+                Q8_0: the largest launch of the step) timed with HIP events on
+                the stream it runs on, against MI355X's 8 TB/s HBM peak;
+  decode_roofline  bytes per token (weights + norms + KV) x tok/s / 8 TB/s;
+  q4_0_gemv     config 1's 2048 x 2048 Q4_0 matvec streamed over 128 distinct
+                copies (302 MB, beyond the 256 MB Infinity Cache);
+  prefill       tok/s of a 512-token prompt on the Llama-3.2-1B Q4_K_M shape;
+  cpu_baseline  the reference's own CPU engine (built from its sources with its
+                portable kernels, oracle/_ref) on this host: a bounded sample of
+                the same decode workload.
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path[:0] = [os.path.join(ROOT, "brisk-llm_amd"), os.path.join(ROOT, "oracle")]
+
+HBM_PEAK = 8.0e12
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def time_events(torch, stream_ptr, fn, reps):
+    """Average ms of fn() over reps, with HIP events recorded on the given stream."""
+    st = torch.cuda.ExternalStream(stream_ptr) if stream_ptr else torch.cuda.current_stream()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record(st)
+    for i in range(reps):
+        fn(i)
+    end.record(st)
+    end.synchronize()
+    return start.elapsed_time(end) / reps
+
+
+def gemv_roofline(torch, lib, L, rows, cols, ttype, block_bytes, copies, reps, norm):
+    """Streams the GEMV over `copies` distinct packed matrices; returns (ms per launch, bytes per launch)."""
+    import ctypes as C
+    import numpy as np
+    from brisk_hip import synth
+    be = 32 if ttype in (2, 8) else 256
+    nb = rows * cols // be
+    raw = synth.BLOCK_MAKERS[ttype](12345, nb).reshape(-1)
+    src = torch.from_numpy(raw.copy()).cuda()
+    nbytes = lib.brisk_hip_packed_bytes(ttype, rows, cols)
+    mats = []
+    for _ in range(copies):
+        d = torch.empty(nbytes, dtype=torch.uint8, device="cuda")
+        L.check(lib.brisk_hip_pack(ttype, C.c_void_p(src.data_ptr()), rows, cols, C.c_void_p(d.data_ptr()), None))
+        mats.append(d)
+    del src
+    x = torch.randn(cols, device="cuda")
+    w = torch.ones(cols, device="cuda") if norm else None
+    out = torch.empty(rows, device="cuda")
+    stream = torch.cuda.current_stream().cuda_stream
+
+    def launch(i):
+        L.check(lib.brisk_hip_gemv(ttype, 0, C.c_void_p(mats[i % copies].data_ptr()), rows, cols, C.c_void_p(x.data_ptr()),
+                                   C.c_void_p(w.data_ptr()) if w is not None else None, 1e-6, C.c_void_p(out.data_ptr()), 0,
+                                   C.c_void_p(stream)))
+
+    for i in range(copies):
+        launch(i)
+    torch.cuda.synchronize()
+    ms = time_events(torch, stream, launch, reps)
+    algo = rows * cols // be * block_bytes + cols * 4 * (2 if norm else 1) + rows * 4
+    del mats
+    torch.cuda.empty_cache()
+    return ms, algo
+
+
+def cpu_baseline(path, prompt, n_gen):
+    import pyoracle
+    if not pyoracle.ref_available():
+        return None
+    threads = max(1, min(16, os.cpu_count() or 1))
+    ref = pyoracle.Reference(path, threads=threads, max_context=len(prompt) + n_gen + 8)
+    ids, gaps, pre_s, gen_s = ref.generate(prompt, n_gen)
+    ref.close()
+    model = ""
+    try:
+        with open("/proc/cpuinfo") as f:
+            model = next((l.split(":", 1)[1].strip() for l in f if l.startswith("model name")), "")
+    except OSError:
+        pass
+    return {"value": round((n_gen - 1) / gen_s, 3), "unit": "tok/s", "cores": threads, "kind": "reference",
+            "sample": f"qwen3-0.6b-shape decode, {len(prompt)}-token prompt then {n_gen} greedy tokens "
+                      f"(generation tok/s as src/main.cpp:312-318; {threads} threads of {model or 'host CPU'}); "
+                      f"prompt {len(prompt) / pre_s:.1f} tok/s",
+            "ids": ids}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=256)
+    ap.add_argument("--warmup", type=int, default=16)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-prefill", action="store_true")
+    ap.add_argument("--no-kernels", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this build runs on one GPU; --gpus {args.gpus} is not supported "
+              "(the token loop is single-device; see the multi-GPU note in DESIGN.md)", file=sys.stderr)
+        sys.exit(2)
+
+    import numpy as np
+    import torch
+    from brisk_hip import HipSession, lib as L, model, synth
+
+    assert torch.cuda.is_available(), "bench.py needs a GPU"
+    lib = L.load()
+    name = "qwen3-0.6b"
+    spec = synth.SPECS[name]
+    t0 = time.time()
+    path = synth.model_path(name)
+    log(f"model {name}: {path} ({time.time() - t0:.1f}s)")
+    f, cfg, table = model.load(path)
+    prompt = synth.prompt_ids(32, cfg.vocab)
+    K, W = args.steps, args.warmup
+    t0 = time.time()
+    s = HipSession((f, cfg, table), max_context=len(prompt) + max(K, W) + 64)
+    log(f"session load {time.time() - t0:.1f}s")
+
+    # warmup: prompt + W steps, then back to the start of the workload
+    s.eval(prompt, logits=False)
+    s.decode(W, ids=False)
+    s.rollback(0)
+    first = s.eval_greedy(prompt)          # prompt evaluated (untimed), first pick pending
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    ids = s.decode(K)                      # K decode steps, graph replays, one sync at the end
+    torch.cuda.synchronize()
+    dt = time.perf_counter() - t0
+    tok_s = K / dt
+    ms_step = dt / K * 1e3
+    gen = np.concatenate([[first], ids])
+    mean_pos = len(prompt) + K / 2
+    step_bytes = spec.decode_bytes(int(mean_pos))
+    log(f"decode: {K} steps in {dt * 1e3:.1f} ms -> {tok_s:.1f} tok/s, {ms_step * 1e3:.1f} us/step, "
+        f"{step_bytes / 1e6:.1f} MB/step -> {step_bytes * tok_s / 1e9:.1f} GB/s")
+    s.close()
+    del s
+    torch.cuda.empty_cache()
+
+    result = {
+        "metric": "decode tok/s (Qwen3-0.6B-shape Q4_0, greedy, on-device sampling)",
+        "value": round(tok_s, 2), "unit": "tok/s", "n_gpus": 1, "steps": K, "warmup": W,
+        "ms_per_step": round(ms_step, 4), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "q4_0 x q8_0 int8 dot, f32 accumulate", "data": "synthetic (seeded random-weight GGUF)",
+        "config": {"workload": "qwen3-0.6b-shape decode: 32 random prompt ids then greedy steps", "hidden": 1024,
+                   "layers": 28, "heads": 16, "kv_heads": 8, "head_dim": 128, "ffn": 3072, "vocab": 151936,
+                   "weights": "Q4_0 layers, Q8_0 embedding/output", "prompt": 32, "decode_steps": K},
+        "decode_roofline": {"bound": "hbm", "bytes_per_token": step_bytes,
+                            "achieved": round(step_bytes * tok_s / 1e9, 2), "peak": 8000.0, "unit": "GB/s",
+                            "frac": round(step_bytes * tok_s / HBM_PEAK, 4)},
+    }
+    golden = os.path.join(ROOT, "tests", "golden", "qwen3-0.6b_greedy.json")
+    if os.path.exists(golden):
+        with open(golden) as fh:
+            want = json.load(fh)["ids"]
+        n = min(len(gen), len(want))
+        result["greedy_matches_reference"] = bool(list(map(int, gen[:n])) == want[:n])
+        result["greedy_compared"] = n
+
+    if not args.no_kernels:
+        # dominant kernel: the output projection GEMV (151936 x 1024 Q8_0 + output_norm), 2 copies (330 MB > MALL)
+        ms, algo = gemv_roofline(torch, lib, L, cfg.vocab, cfg.embd, 8, 34, copies=2, reps=40, norm=True)
+        ach = algo / (ms * 1e-3) / 1e9
+        result["roofline"] = {"kernel": "k_gemv (output projection, 151936x1024 Q8_0, fused output_norm)",
+                              "bound": "hbm", "achieved": round(ach, 1), "peak": 8000.0, "unit": "GB/s",
+                              "frac": round(ach / 8000.0, 4), "traffic": None, "algorithmic_bytes": algo,
+                              "ms_per_launch": round(ms, 4)}
+        log(f"output gemv: {ms * 1e3:.1f} us, {ach:.0f} GB/s")
+        ms1, algo1 = gemv_roofline(torch, lib, L, 2048, 2048, 2, 18, copies=128, reps=512, norm=False)
+        ach1 = algo1 / (ms1 * 1e-3) / 1e9
+        result["q4_0_gemv"] = {"config": "2048x2048 Q4_0, 128 distinct copies", "us_per_launch": round(ms1 * 1e3, 2),
+                               "achieved": round(ach1, 1), "unit": "GB/s", "frac": round(ach1 / 8000.0, 4),
+                               "algorithmic_bytes": algo1}
+        log(f"q4_0 gemv 2048x2048: {ms1 * 1e3:.2f} us, {ach1:.0f} GB/s")
+
+    if not args.no_prefill:
+        lname = "llama-3.2-1b"
+        t0 = time.time()
+        lpath = synth.model_path(lname)
+        log(f"model {lname}: ({time.time() - t0:.1f}s)")
+        lf, lcfg, ltable = model.load(lpath)
+        lp = synth.prompt_ids(512, lcfg.vocab, seed=11)
+        ls = HipSession((lf, lcfg, ltable), max_context=1024)
+        ls.eval(lp[:64], logits=False)
+        ls.rollback(0)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        ls.eval(lp, logits=True)
+        dtp = time.perf_counter() - t0
+        result["prefill"] = {"workload": "llama-3.2-1b-shape Q4_K_M, 512 random prompt ids (eval, last-token logits)",
+                             "value": round(512 / dtp, 2), "unit": "tok/s", "ms": round(dtp * 1e3, 2)}
+        log(f"prefill 512: {dtp * 1e3:.1f} ms -> {512 / dtp:.1f} tok/s")
+        ls.close()
+
+    if not args.no_cpu_baseline:
+        t0 = time.time()
+        cb = cpu_baseline(path, prompt, 32)
+        if cb is not None:
+            ref_ids = cb.pop("ids")
+            cb["greedy_matches_gpu"] = bool(np.array_equal(ref_ids, gen[:len(ref_ids)]))
+            result["cpu_baseline"] = cb
+            log(f"cpu baseline ({time.time() - t0:.1f}s): {cb['value']} tok/s on {cb['cores']} threads")
+        else:
+            result["cpu_baseline"] = None
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

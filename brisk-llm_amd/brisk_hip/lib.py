@@ -19,7 +19,7 @@ EXPORTS = (
     "brisk_hip_last_error", "brisk_hip_abi_version", "brisk_hip_device_count", "brisk_hip_packed_bytes", "brisk_hip_pack",
     "brisk_hip_quantize_q8_0", "brisk_hip_quantize_q8_k", "brisk_hip_matvec", "brisk_hip_matmul", "brisk_hip_gemv", "brisk_hip_expf",
     "brisk_hip_session_create", "brisk_hip_session_destroy", "brisk_hip_session_eval", "brisk_hip_session_eval_all",
-    "brisk_hip_session_eval_greedy", "brisk_hip_session_generate", "brisk_hip_session_rollback",
+    "brisk_hip_session_eval_greedy", "brisk_hip_session_generate", "brisk_hip_session_decode", "brisk_hip_session_rollback",
     "brisk_hip_session_position", "brisk_hip_session_max_context", "brisk_hip_session_kv_cache",
     "brisk_hip_session_set_position", "brisk_hip_session_stream",
 )
@@ -69,6 +69,7 @@ def load():
     L.brisk_hip_session_eval_all.argtypes = [_vp, _vp, _sz, _vp]
     L.brisk_hip_session_eval_greedy.argtypes = [_vp, _vp, _sz, C.POINTER(C.c_int32)]
     L.brisk_hip_session_generate.argtypes = [_vp, _vp, _sz, _sz, _vp]
+    L.brisk_hip_session_decode.argtypes = [_vp, _sz, _vp]
     L.brisk_hip_session_rollback.argtypes = [_vp, _sz]
     L.brisk_hip_session_position.argtypes = [_vp]
     L.brisk_hip_session_position.restype = _sz

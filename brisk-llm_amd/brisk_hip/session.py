@@ -85,6 +85,12 @@ class HipSession:
         _lib.check(self._L.brisk_hip_session_generate(self._h, _ptr(p), len(p), n_gen, _ptr(out)))
         return out
 
+    def decode(self, n: int, ids: bool = True):
+        """n more greedy steps from the pending pick; returns the n new ids (or None)."""
+        out = np.zeros(n, np.int32) if ids else None
+        _lib.check(self._L.brisk_hip_session_decode(self._h, n, _ptr(out) if ids else None))
+        return out
+
     def rollback(self, position: int):
         _lib.check(self._L.brisk_hip_session_rollback(self._h, position))
 

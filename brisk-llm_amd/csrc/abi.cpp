@@ -170,6 +170,10 @@ int brisk_hip_session_generate(brisk_hip_session* s, const int32_t* prompt, size
     return guarded([&] { s->impl.generate(prompt, n_prompt, n_gen, out); });
 }
 
+int brisk_hip_session_decode(brisk_hip_session* s, size_t n, int32_t* out) {
+    return guarded([&] { s->impl.decode(n, out); });
+}
+
 int brisk_hip_session_rollback(brisk_hip_session* s, size_t position) {
     return guarded([&] { s->impl.rollback(position); });
 }

@@ -365,6 +365,21 @@ void Session::generate(const int32_t* prompt, size_t n_prompt, size_t n_gen, int
     position_ += n_gen - 1;
 }
 
+void Session::decode(size_t n, int32_t* out) {
+    if (n == 0) return;
+    if (position_ == 0) throw Error(BRISK_HIP_EINVAL, "model: decode needs an evaluated token first");
+    if (n > max_ctx_ - position_) throw Error(BRISK_HIP_EINVAL, "model: context length exceeded");
+    const size_t first = position_ + 1;
+    // the device position follows the host's (a rollback may have moved it); seq[position_] is the pending pick
+    const int p[2] = {static_cast<int>(position_), static_cast<int>(position_ + 1)};
+    check(hipMemcpyAsync(pos_, p, 8, hipMemcpyHostToDevice, stream_), "hipMemcpy(pos)");
+    check(hipStreamSynchronize(stream_), "decode stage sync");  // the copy above reads stack memory
+    for (size_t i = 0; i < n; ++i) step(true);
+    if (out != nullptr) check(hipMemcpyAsync(out, seq_ + first, n * 4, hipMemcpyDeviceToHost, stream_), "hipMemcpy(ids)");
+    check(hipStreamSynchronize(stream_), "decode sync");
+    position_ += n;
+}
+
 void Session::rollback(size_t position) {
     if (position > position_) throw Error(BRISK_HIP_EINVAL, "model: cannot roll forward");  // src/model.cpp:736
     position_ = position;  // the caches keep their storage; later entries are overwritten

@@ -49,6 +49,7 @@ public:
     void eval_all(const int32_t* tokens, size_t n, float* logits);
     int32_t eval_greedy(const int32_t* tokens, size_t n);
     void generate(const int32_t* prompt, size_t n_prompt, size_t n_gen, int32_t* out);
+    void decode(size_t n, int32_t* out);
     void rollback(size_t position);
     void set_position(size_t position);
     size_t position() const { return position_; }

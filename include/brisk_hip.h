@@ -140,6 +140,12 @@ int brisk_hip_session_eval_greedy(brisk_hip_session* s, const int32_t* tokens, s
  * out[n_gen] receives the picked ids. */
 int brisk_hip_session_generate(brisk_hip_session* s, const int32_t* prompt, size_t n_prompt, size_t n_gen, int32_t* out);
 
+/* The body of that loop on its own: n more greedy steps, each evaluating the
+ * pending pick (the one the previous eval / decode chose) and picking the next;
+ * out[n] (may be NULL) receives the n new picks.  No host round trip between
+ * steps.  Needs a prior eval; advances position() by n. */
+int brisk_hip_session_decode(brisk_hip_session* s, size_t n, int32_t* out);
+
 /* Engine::rollback / position (src/engine.h:28-31). */
 int brisk_hip_session_rollback(brisk_hip_session* s, size_t position);
 size_t brisk_hip_session_position(const brisk_hip_session* s);
