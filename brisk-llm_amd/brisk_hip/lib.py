@@ -21,7 +21,7 @@ EXPORTS = (
     "brisk_hip_session_create", "brisk_hip_session_destroy", "brisk_hip_session_eval", "brisk_hip_session_eval_all",
     "brisk_hip_session_eval_greedy", "brisk_hip_session_generate", "brisk_hip_session_decode", "brisk_hip_session_rollback",
     "brisk_hip_session_position", "brisk_hip_session_max_context", "brisk_hip_session_kv_cache",
-    "brisk_hip_session_set_position", "brisk_hip_session_stream",
+    "brisk_hip_session_set_position", "brisk_hip_session_stream", "brisk_hip_session_trace",
 )
 
 
@@ -79,6 +79,8 @@ def load():
     L.brisk_hip_session_set_position.argtypes = [_vp, _sz]
     L.brisk_hip_session_stream.argtypes = [_vp]
     L.brisk_hip_session_stream.restype = _vp
+    L.brisk_hip_session_trace.argtypes = [_vp, C.POINTER(C.c_ulonglong), _sz]
+    L.brisk_hip_session_trace.restype = _sz
     _lib = L
     return L
 

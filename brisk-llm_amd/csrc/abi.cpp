@@ -192,4 +192,13 @@ int brisk_hip_session_set_position(brisk_hip_session* s, size_t position) {
 
 void* brisk_hip_session_stream(brisk_hip_session* s) { return static_cast<void*>(s->impl.stream()); }
 
+size_t brisk_hip_session_trace(brisk_hip_session* s, unsigned long long* out, size_t n) {
+    try {
+        return s->impl.trace(out, n);
+    } catch (const std::exception& e) {
+        set_error(BRISK_HIP_EHIP, e.what());
+        return 0;
+    }
+}
+
 }  // extern "C"

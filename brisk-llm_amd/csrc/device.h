@@ -18,6 +18,7 @@ namespace bh {
 
 constexpr int kThreads = 256;        // every token-loop kernel runs 256-thread workgroups (4 waves of 64)
 constexpr int kMaxCols = 8192;       // widest activation row a matvec takes (Llama-3.2-1B FFN)
+constexpr int kTermCap = 8448;       // floats of LDS for the per-block terms of one tile
 
 // ---------------------------------------------------------------- halves
 
@@ -141,6 +142,30 @@ __device__ __forceinline__ float rms_scale(double sum, int n, float eps) {
     return 1.0f / sqrtf(mean + eps);
 }
 
+// ---------------------------------------------------------------- memory policies
+
+// How a phase reads and writes the small activation vectors it shares with
+// other workgroups.  PlainIO: ordinary accesses, for the one-kernel-per-phase
+// path (kernel boundaries make them visible).  CoherentIO: system-scope
+// relaxed atomics, which go past the per-XCD L2 caches, so a persistent
+// kernel can hand vectors between workgroups on different XCDs with a
+// counter-based barrier and no cache writeback/invalidate.
+struct PlainIO {
+    static __device__ __forceinline__ float ld(const float* p) { return *p; }
+    static __device__ __forceinline__ float4 ld4(const float* p) { return *reinterpret_cast<const float4*>(p); }
+    static __device__ __forceinline__ void st(float* p, float v) { *p = v; }
+};
+
+struct CoherentIO {
+    static __device__ __forceinline__ float ld(const float* p) {
+        return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+    }
+    static __device__ __forceinline__ float4 ld4(const float* p) { return make_float4(ld(p), ld(p + 1), ld(p + 2), ld(p + 3)); }
+    static __device__ __forceinline__ void st(float* p, float v) {
+        __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+    }
+};
+
 // ---------------------------------------------------------------- activations in LDS
 
 // One activation row, quantised, resident in LDS for the whole tile.
@@ -240,6 +265,149 @@ __device__ inline void act_q8_k(const float* x, const float* w, float scale, int
     }
 }
 
+// ---- the decode path's activation prologue, split in two so that its loads go
+// out before the weight loads of the tile (a wave's loads complete in order) and
+// its arithmetic overlaps the weight stream.  Element mapping: chunk c of a
+// thread covers values c * 1024 + 4 * threadIdx.x .. + 3, so a Q8_0 block is 8
+// adjacent lanes and a Q8_K block is one wave.
+
+constexpr int kActRegChunks = 4;  // chunks held in registers (rows up to 4096 values); wider rows load late
+
+struct ActRegs {
+    float4 x[kActRegChunks];
+    float4 w[kActRegChunks];
+};
+
+__device__ __forceinline__ float4 ld4(const float* p) { return *reinterpret_cast<const float4*>(p); }
+
+template <class IO = PlainIO>
+__device__ __forceinline__ void act_issue(ActRegs& r, const float* x, const float* w, int cols) {
+#pragma unroll
+    for (int c = 0; c < kActRegChunks; ++c) {
+        const int base = (c * kThreads + static_cast<int>(threadIdx.x)) * 4;
+        if (base < cols) {
+            r.x[c] = IO::ld4(x + base);
+            if (w != nullptr) r.w[c] = ld4(w + base);
+        }
+    }
+}
+
+// quantize_q8_0 of one 4-value piece (src/quant.cpp:115-142): amax over the
+// block's 8 lanes, d = amax / 127, q = rint(v / d), the half-rounded d and the
+// block sum to LDS.
+__device__ __forceinline__ void quant_piece_q8_0(const float v[4], int base, ActLds& a) {
+    float amax = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
+    amax = fmaxf(amax, __shfl_xor(amax, 1, 64));
+    amax = fmaxf(amax, __shfl_xor(amax, 2, 64));
+    amax = fmaxf(amax, __shfl_xor(amax, 4, 64));
+    const float d = amax / 127.0f;
+    const float inv = d != 0.0f ? 1.0f / d : 0.0f;
+    int q[4], sum = 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        q[i] = static_cast<int>(rintf(v[i] * inv));
+        sum += q[i];
+    }
+    sum += __shfl_xor(sum, 1, 64);
+    sum += __shfl_xor(sum, 2, 64);
+    sum += __shfl_xor(sum, 4, 64);
+    a.xs[base / 4] = (q[0] & 0xFF) | ((q[1] & 0xFF) << 8) | ((q[2] & 0xFF) << 16) | (q[3] << 24);
+    if ((threadIdx.x & 7) == 0) {
+        a.xd[base / 32] = h2f(f2h(d));
+        a.xsum[base / 32] = sum;
+    }
+}
+
+// quantize_q8_k (src/quant.cpp:146-194) of one 4-value piece: the wave is the
+// 256-value block; the scale comes from the first value of largest magnitude.
+__device__ __forceinline__ void quant_piece_q8_k(const float v[4], int base, int bits, ActLds& a) {
+    const int lane = threadIdx.x & 63;
+    float amax = -1.0f, sel = 0.0f;
+    int idx = 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const float av = fabsf(v[i]);
+        if (av > amax) { amax = av; idx = lane * 4 + i; sel = v[i]; }
+    }
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        const float oa = __shfl_xor(amax, o, 64);
+        const int oi = __shfl_xor(idx, o, 64);
+        const float os = __shfl_xor(sel, o, 64);
+        if (oa > amax || (oa == amax && oi < idx)) { amax = oa; idx = oi; sel = os; }
+    }
+    int q[4];
+    float d;
+    if (amax == 0.0f) {
+        d = 0.0f;
+        q[0] = q[1] = q[2] = q[3] = 0;
+    } else {
+        const float extreme = bits == 7 ? 63.0f : 127.0f;
+        const float inv = -extreme / sel;
+        d = 1.0f / inv;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) q[i] = static_cast<int>(fminf(127.0f, rintf(inv * v[i])));
+    }
+    int s = q[0] + q[1] + q[2] + q[3];
+    s += __shfl_xor(s, 1, 64);
+    s += __shfl_xor(s, 2, 64);
+    a.xs[base / 4] = (q[0] & 0xFF) | ((q[1] & 0xFF) << 8) | ((q[2] & 0xFF) << 16) | (q[3] << 24);
+    if ((lane & 3) == 0) a.xsum[base / 16] = static_cast<int16_t>(s);
+    if (lane == 0) a.xd[base / 256] = d;
+}
+
+// rms_norm (when w is given, src/model.cpp:87-97) and quantisation of the row
+// whose first chunks act_issue loaded.  Ends with a barrier.
+template <class IO = PlainIO>
+__device__ inline void act_finish(const ActRegs& r, const float* x, const float* w, float eps, int cols, bool q8k, int bits,
+                                  ActLds& a, double* red) {
+    const int nch = (cols + 4 * kThreads - 1) / (4 * kThreads);
+    float scale = 1.0f;
+    if (w != nullptr) {
+        double s = 0.0;
+#pragma unroll
+        for (int c = 0; c < kActRegChunks; ++c) {
+            const int base = (c * kThreads + static_cast<int>(threadIdx.x)) * 4;
+            if (c < nch && base < cols) {
+                const float4 v = r.x[c];
+                s += static_cast<double>(v.x * v.x); s += static_cast<double>(v.y * v.y);
+                s += static_cast<double>(v.z * v.z); s += static_cast<double>(v.w * v.w);
+            }
+        }
+        for (int c = kActRegChunks; c < nch; ++c) {
+            const int base = (c * kThreads + static_cast<int>(threadIdx.x)) * 4;
+            if (base < cols) {
+                const float4 v = IO::ld4(x + base);
+                s += static_cast<double>(v.x * v.x); s += static_cast<double>(v.y * v.y);
+                s += static_cast<double>(v.z * v.z); s += static_cast<double>(v.w * v.w);
+            }
+        }
+        s = wave_sum(s);
+        if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = s;
+        __syncthreads();
+        scale = rms_scale(((red[0] + red[1]) + red[2]) + red[3], cols, eps);
+    }
+    auto piece = [&](float4 xv, float4 wv, int base) {
+        float v[4] = {xv.x, xv.y, xv.z, xv.w};
+        if (w != nullptr) {
+            v[0] = v[0] * scale * wv.x; v[1] = v[1] * scale * wv.y;
+            v[2] = v[2] * scale * wv.z; v[3] = v[3] * scale * wv.w;
+        }
+        if (q8k) quant_piece_q8_k(v, base, bits, a);
+        else quant_piece_q8_0(v, base, a);
+    };
+#pragma unroll
+    for (int c = 0; c < kActRegChunks; ++c) {
+        const int base = (c * kThreads + static_cast<int>(threadIdx.x)) * 4;
+        if (c < nch && base < cols) piece(r.x[c], r.w[c], base);
+    }
+    for (int c = kActRegChunks; c < nch; ++c) {
+        const int base = (c * kThreads + static_cast<int>(threadIdx.x)) * 4;
+        if (base < cols) piece(IO::ld4(x + base), w != nullptr ? ld4(w + base) : make_float4(0, 0, 0, 0), base);
+    }
+    __syncthreads();
+}
+
 // Same LDS image from already-quantised GGUF activation blocks (the KernelSet
 // matvec contract: x is BlockQ8_0 / BlockQ8_K rows, src/kernels.h:19-21).
 __device__ inline void act_from_q8_0(const uint8_t* xq, int cols, ActLds& a) {
@@ -267,39 +435,61 @@ __device__ inline void act_from_q8_k(const uint8_t* xq, int cols, ActLds& a) {
 
 // ---------------------------------------------------------------- block dots
 
+// A weight unit is one GGUF block (Q4_0, Q8_0: 32 values; K-quants and TQ2_0:
+// 256) of one row.  load() fetches its bytes into registers; term() forms the
+// reference's per-block float term from them and the LDS activation.  Tiles
+// issue every load of a thread before any term (and before the activation
+// prologue), so the memory latency is paid once per tile, not once per block.
+
+__device__ __forceinline__ uint4 ld16(const uint8_t* p) { return *reinterpret_cast<const uint4*>(p); }
+
+template <uint32_t T> struct Unit;
+
 // dot_q4_0_q8_0 block term (src/quant.cpp:445-456): acc = sum((q - 8) x), exact;
 // term = (float)acc * d_w * d_x.  Nibble bytes hold values 0..15, valid as
 // signed int8, so sum(q x) runs on sdot4 and the -8 comes off via the block sum.
-__device__ __forceinline__ float term_q4_0(const Packed& m, uint32_t row, uint32_t b, const ActLds& a) {
-    const uint32_t nb = m.cols / 32;
-    const size_t blk = static_cast<size_t>(row) * nb + b;
-    const uint4 q = *reinterpret_cast<const uint4*>(m.p0 + blk * 16);
-    const uint16_t dw = reinterpret_cast<const uint16_t*>(m.p1)[blk];
-    const int32_t* x = a.xs + b * 8;
-    int acc = 0;
-    const uint32_t qw[4] = {q.x, q.y, q.z, q.w};
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        acc = dot4(static_cast<int>(qw[j] & 0x0F0F0F0Fu), x[j], acc);
-        acc = dot4(static_cast<int>((qw[j] >> 4) & 0x0F0F0F0Fu), x[4 + j], acc);
+template <> struct Unit<kQ4_0> {
+    static constexpr uint32_t kElems = 32;
+    static constexpr int kMaxPerThread = 16;
+    uint4 q;
+    uint32_t d;
+    __device__ __forceinline__ void load(const Packed& m, size_t blk) {
+        q = ld16(m.p0 + blk * 16);
+        d = reinterpret_cast<const uint16_t*>(m.p1)[blk];
     }
-    acc -= 8 * a.xsum[b];
-    return static_cast<float>(acc) * h2f(dw) * a.xd[b];
-}
+    __device__ __forceinline__ float term(uint32_t b, const ActLds& a) const {
+        const int32_t* x = a.xs + b * 8;
+        int acc = 0;
+        const uint32_t qw[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            acc = dot4(static_cast<int>(qw[j] & 0x0F0F0F0Fu), x[j], acc);
+            acc = dot4(static_cast<int>((qw[j] >> 4) & 0x0F0F0F0Fu), x[4 + j], acc);
+        }
+        acc -= 8 * a.xsum[b];
+        return static_cast<float>(acc) * h2f(static_cast<uint16_t>(d)) * a.xd[b];
+    }
+};
 
 // dot_q8_0_q8_0 block term (src/quant.cpp:474-482).
-__device__ __forceinline__ float term_q8_0(const Packed& m, uint32_t row, uint32_t b, const ActLds& a) {
-    const uint32_t nb = m.cols / 32;
-    const size_t blk = static_cast<size_t>(row) * nb + b;
-    const uint4* qp = reinterpret_cast<const uint4*>(m.p0 + blk * 32);
-    const uint4 q0 = qp[0], q1 = qp[1];
-    const uint16_t dw = reinterpret_cast<const uint16_t*>(m.p1)[blk];
-    const int32_t* x = a.xs + b * 8;
-    int acc = 0;
-    acc = dot4(q0.x, x[0], acc); acc = dot4(q0.y, x[1], acc); acc = dot4(q0.z, x[2], acc); acc = dot4(q0.w, x[3], acc);
-    acc = dot4(q1.x, x[4], acc); acc = dot4(q1.y, x[5], acc); acc = dot4(q1.z, x[6], acc); acc = dot4(q1.w, x[7], acc);
-    return static_cast<float>(acc) * h2f(dw) * a.xd[b];
-}
+template <> struct Unit<kQ8_0> {
+    static constexpr uint32_t kElems = 32;
+    static constexpr int kMaxPerThread = 8;
+    uint4 q0, q1;
+    uint32_t d;
+    __device__ __forceinline__ void load(const Packed& m, size_t blk) {
+        q0 = ld16(m.p0 + blk * 32);
+        q1 = ld16(m.p0 + blk * 32 + 16);
+        d = reinterpret_cast<const uint16_t*>(m.p1)[blk];
+    }
+    __device__ __forceinline__ float term(uint32_t b, const ActLds& a) const {
+        const int32_t* x = a.xs + b * 8;
+        int acc = 0;
+        acc = dot4(q0.x, x[0], acc); acc = dot4(q0.y, x[1], acc); acc = dot4(q0.z, x[2], acc); acc = dot4(q0.w, x[3], acc);
+        acc = dot4(q1.x, x[4], acc); acc = dot4(q1.y, x[5], acc); acc = dot4(q1.z, x[6], acc); acc = dot4(q1.w, x[7], acc);
+        return static_cast<float>(acc) * h2f(static_cast<uint16_t>(d)) * a.xd[b];
+    }
+};
 
 // q4_k_scale_min (src/quant.h:256-264)
 __device__ __forceinline__ void q4k_scale_min(const uint8_t* s, int j, int& scale, int& min) {
@@ -314,140 +504,186 @@ __device__ __forceinline__ void q4k_scale_min(const uint8_t* s, int j, int& scal
 
 // dot_q4_k_q8_k super-block term (src/quant.cpp:500-521): weighted and offsets
 // are exact int32; term = x.d * (d * weighted - dmin * offsets).
-__device__ __forceinline__ float term_q4_k(const Packed& m, uint32_t row, uint32_t b, const ActLds& a) {
-    const uint32_t nsb = m.cols / 256;
-    const size_t blk = static_cast<size_t>(row) * nsb + b;
-    const uint4* qp = reinterpret_cast<const uint4*>(m.p0 + blk * 128);
-    const uint4 meta = *reinterpret_cast<const uint4*>(m.p1 + blk * 16);
-    const uint8_t* mb = reinterpret_cast<const uint8_t*>(&meta);
-    const uint16_t d = static_cast<uint16_t>(meta.x & 0xFFFF), dmin = static_cast<uint16_t>(meta.x >> 16);
-    const int32_t* x = a.xs + b * 64;
-    int weighted = 0, offsets = 0;
+template <> struct Unit<kQ4_K> {
+    static constexpr uint32_t kElems = 256;
+    static constexpr int kMaxPerThread = 4;
+    uint4 q[8];
+    uint4 meta;  // d, dmin, scales[12]
+    __device__ __forceinline__ void load(const Packed& m, size_t blk) {
 #pragma unroll
-    for (int c = 0; c < 4; ++c) {  // chunk c: 32 bytes, low nibbles = sub-block 2c, high = 2c+1
-        const uint4 q0 = qp[2 * c], q1 = qp[2 * c + 1];
-        const uint32_t qw[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
-        int lo = 0, hi = 0;
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            lo = dot4(static_cast<int>(qw[j] & 0x0F0F0F0Fu), x[c * 16 + j], lo);
-            hi = dot4(static_cast<int>((qw[j] >> 4) & 0x0F0F0F0Fu), x[c * 16 + 8 + j], hi);
-        }
-        int s0, m0, s1, m1;
-        q4k_scale_min(mb + 4, 2 * c, s0, m0);
-        q4k_scale_min(mb + 4, 2 * c + 1, s1, m1);
-        weighted += s0 * lo + s1 * hi;
-        const int* bs = a.xsum + b * 16 + 4 * c;
-        offsets += m0 * (bs[0] + bs[1]) + m1 * (bs[2] + bs[3]);
+        for (int i = 0; i < 8; ++i) q[i] = ld16(m.p0 + blk * 128 + 16 * i);
+        meta = ld16(m.p1 + blk * 16);
     }
-    return a.xd[b] * (h2f(d) * static_cast<float>(weighted) - h2f(dmin) * static_cast<float>(offsets));
-}
+    __device__ __forceinline__ float term(uint32_t b, const ActLds& a) const {
+        const uint32_t mw[4] = {meta.x, meta.y, meta.z, meta.w};
+        const uint8_t* mb = reinterpret_cast<const uint8_t*>(mw);
+        const int32_t* x = a.xs + b * 64;
+        int weighted = 0, offsets = 0;
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {  // chunk c: 32 bytes, low nibbles = sub-block 2c, high = 2c+1
+            const uint32_t qw[8] = {q[2 * c].x, q[2 * c].y, q[2 * c].z, q[2 * c].w,
+                                    q[2 * c + 1].x, q[2 * c + 1].y, q[2 * c + 1].z, q[2 * c + 1].w};
+            int lo = 0, hi = 0;
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                lo = dot4(static_cast<int>(qw[j] & 0x0F0F0F0Fu), x[c * 16 + j], lo);
+                hi = dot4(static_cast<int>((qw[j] >> 4) & 0x0F0F0F0Fu), x[c * 16 + 8 + j], hi);
+            }
+            int s0, m0, s1, m1;
+            q4k_scale_min(mb + 4, 2 * c, s0, m0);
+            q4k_scale_min(mb + 4, 2 * c + 1, s1, m1);
+            weighted += s0 * lo + s1 * hi;
+            const int* bs = a.xsum + b * 16 + 4 * c;
+            offsets += m0 * (bs[0] + bs[1]) + m1 * (bs[2] + bs[3]);
+        }
+        const uint16_t d = static_cast<uint16_t>(meta.x & 0xFFFF), dmin = static_cast<uint16_t>(meta.x >> 16);
+        return a.xd[b] * (h2f(d) * static_cast<float>(weighted) - h2f(dmin) * static_cast<float>(offsets));
+    }
+};
 
 // dot_q6_k_q8_k super-block term (src/quant.cpp:549-563, unpack_q6_k :285-297):
 // per 16-value group g, dot = sum((v - 32) x) = sum(v x) - 32 bsum[g] with v in
 // 0..63; weighted = sum scale_g dot_g, exact; term = x.d * d * weighted.
-__device__ __forceinline__ float term_q6_k(const Packed& m, uint32_t row, uint32_t b, const ActLds& a) {
-    const uint32_t nsb = m.cols / 256;
-    const size_t blk = static_cast<size_t>(row) * nsb + b;
-    const uint32_t* ql = reinterpret_cast<const uint32_t*>(m.p0 + blk * 128);
-    const uint32_t* qh = reinterpret_cast<const uint32_t*>(m.p1 + blk * 64);
-    const uint8_t* meta = m.p2 + blk * 20;  // int8 scales[16], u16 d, pad
-    const int32_t* x = a.xs + b * 64;
-    const int* bs = a.xsum + b * 16;
-    int weighted = 0;
+template <> struct Unit<kQ6_K> {
+    static constexpr uint32_t kElems = 256;
+    static constexpr int kMaxPerThread = 2;
+    uint4 ql[8], qh[4];
+    uint32_t meta[5];  // int8 scales[16], u16 d, pad
+    __device__ __forceinline__ void load(const Packed& m, size_t blk) {
 #pragma unroll
-    for (int half = 0; half < 2; ++half) {
-        int g4[4][2];  // [quarter][sub-group of 16] sums of v x
+        for (int i = 0; i < 8; ++i) ql[i] = ld16(m.p0 + blk * 128 + 16 * i);
 #pragma unroll
-        for (int qi = 0; qi < 4; ++qi) g4[qi][0] = g4[qi][1] = 0;
+        for (int i = 0; i < 4; ++i) qh[i] = ld16(m.p1 + blk * 64 + 16 * i);
+        const uint32_t* mp = reinterpret_cast<const uint32_t*>(m.p2 + blk * 20);
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {  // values l = 4j..4j+3 of this half
-            const uint32_t l0 = ql[half * 16 + j], l1 = ql[half * 16 + 8 + j], h = qh[half * 8 + j];
-            const int v0 = static_cast<int>((l0 & 0x0F0F0F0Fu) | (((h >> 0) & 0x03030303u) << 4));
-            const int v1 = static_cast<int>((l1 & 0x0F0F0F0Fu) | (((h >> 2) & 0x03030303u) << 4));
-            const int v2 = static_cast<int>(((l0 >> 4) & 0x0F0F0F0Fu) | (((h >> 4) & 0x03030303u) << 4));
-            const int v3 = static_cast<int>(((l1 >> 4) & 0x0F0F0F0Fu) | (((h >> 6) & 0x03030303u) << 4));
-            const int sg = j >> 2;  // values 0-15 or 16-31 of each quarter
-            g4[0][sg] = dot4(v0, x[half * 32 + 0 + j], g4[0][sg]);
-            g4[1][sg] = dot4(v1, x[half * 32 + 8 + j], g4[1][sg]);
-            g4[2][sg] = dot4(v2, x[half * 32 + 16 + j], g4[2][sg]);
-            g4[3][sg] = dot4(v3, x[half * 32 + 24 + j], g4[3][sg]);
-        }
+        for (int i = 0; i < 5; ++i) meta[i] = mp[i];
+    }
+    __device__ __forceinline__ float term(uint32_t b, const ActLds& a) const {
+        const uint32_t* L = reinterpret_cast<const uint32_t*>(ql);
+        const uint32_t* H = reinterpret_cast<const uint32_t*>(qh);
+        const int8_t* sc = reinterpret_cast<const int8_t*>(meta);
+        const int32_t* x = a.xs + b * 64;
+        const int* bs = a.xsum + b * 16;
+        int weighted = 0;
 #pragma unroll
-        for (int qi = 0; qi < 4; ++qi) {
+        for (int half = 0; half < 2; ++half) {
+            int g4[4][2] = {{0, 0}, {0, 0}, {0, 0}, {0, 0}};
 #pragma unroll
-            for (int sg = 0; sg < 2; ++sg) {
-                const int g = half * 8 + qi * 2 + sg;
-                const int dot = g4[qi][sg] - 32 * bs[g];
-                weighted += static_cast<int>(static_cast<int8_t>(meta[g])) * dot;
+            for (int j = 0; j < 8; ++j) {  // values l = 4j..4j+3 of this half
+                const uint32_t l0 = L[half * 16 + j], l1 = L[half * 16 + 8 + j], h = H[half * 8 + j];
+                const int v0 = static_cast<int>((l0 & 0x0F0F0F0Fu) | (((h >> 0) & 0x03030303u) << 4));
+                const int v1 = static_cast<int>((l1 & 0x0F0F0F0Fu) | (((h >> 2) & 0x03030303u) << 4));
+                const int v2 = static_cast<int>(((l0 >> 4) & 0x0F0F0F0Fu) | (((h >> 4) & 0x03030303u) << 4));
+                const int v3 = static_cast<int>(((l1 >> 4) & 0x0F0F0F0Fu) | (((h >> 6) & 0x03030303u) << 4));
+                const int sg = j >> 2;
+                g4[0][sg] = dot4(v0, x[half * 32 + 0 + j], g4[0][sg]);
+                g4[1][sg] = dot4(v1, x[half * 32 + 8 + j], g4[1][sg]);
+                g4[2][sg] = dot4(v2, x[half * 32 + 16 + j], g4[2][sg]);
+                g4[3][sg] = dot4(v3, x[half * 32 + 24 + j], g4[3][sg]);
+            }
+#pragma unroll
+            for (int qi = 0; qi < 4; ++qi) {
+#pragma unroll
+                for (int sg = 0; sg < 2; ++sg) {
+                    const int g = half * 8 + qi * 2 + sg;
+                    weighted += static_cast<int>(sc[g]) * (g4[qi][sg] - 32 * bs[g]);
+                }
             }
         }
+        const uint16_t d = static_cast<uint16_t>(meta[4] & 0xFFFF);
+        return a.xd[b] * h2f(d) * static_cast<float>(weighted);
     }
-    const uint16_t d = static_cast<uint16_t>(meta[16] | (meta[17] << 8));
-    return a.xd[b] * h2f(d) * static_cast<float>(weighted);
-}
+};
 
 // Ternary super-block term.  Element e of a TQ2_0 block sits in byte
 // 32 (e / 128) + e % 32 at bit pair 2 ((e % 128) / 32) (src/quant.h:123-130), so
 // bit pair l of bytes 32j..32j+31 is 32 consecutive values.  acc = sum((c - 1) x)
-// is exact.  With `lut16` the float order is the x86 load-time layout's,
+// is exact.  With lut16 the float order is the x86 load-time layout's,
 // acc * d_w * x.d (dot_tq2_0x16_q8_k, src/quant.cpp:789-802); else the generic
 // x.d * d_w * acc (dot_tq2_0_q8_k, :580-596).
-__device__ __forceinline__ float term_tq2_0(const Packed& m, uint32_t row, uint32_t b, const ActLds& a, bool lut16) {
-    const uint32_t nsb = m.cols / 256;
-    const size_t blk = static_cast<size_t>(row) * nsb + b;
-    const uint4* qp = reinterpret_cast<const uint4*>(m.p0 + blk * 64);
-    const uint16_t dw = reinterpret_cast<const uint16_t*>(m.p1)[blk];
-    const int32_t* x = a.xs + b * 64;
-    int acc = 0;
+template <> struct Unit<kTQ2_0> {
+    static constexpr uint32_t kElems = 256;
+    static constexpr int kMaxPerThread = 4;
+    uint4 q[4];
+    uint32_t d;
+    bool lut16;
+    __device__ __forceinline__ void load(const Packed& m, size_t blk) {
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
-        const uint4 q0 = qp[2 * j], q1 = qp[2 * j + 1];
-        const uint32_t qw[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
+        for (int i = 0; i < 4; ++i) q[i] = ld16(m.p0 + blk * 64 + 16 * i);
+        d = reinterpret_cast<const uint16_t*>(m.p1)[blk];
+        lut16 = (m.flags & kFlagLut16) != 0;
+    }
+    __device__ __forceinline__ float term(uint32_t b, const ActLds& a) const {
+        const int32_t* x = a.xs + b * 64;
+        int acc = 0;
 #pragma unroll
-        for (int l = 0; l < 4; ++l) {
+        for (int j = 0; j < 2; ++j) {
+            const uint32_t qw[8] = {q[2 * j].x, q[2 * j].y, q[2 * j].z, q[2 * j].w,
+                                    q[2 * j + 1].x, q[2 * j + 1].y, q[2 * j + 1].z, q[2 * j + 1].w};
 #pragma unroll
-            for (int k = 0; k < 8; ++k) acc = dot4(static_cast<int>((qw[k] >> (2 * l)) & 0x03030303u), x[j * 32 + l * 8 + k], acc);
+            for (int l = 0; l < 4; ++l) {
+#pragma unroll
+                for (int k = 0; k < 8; ++k) acc = dot4(static_cast<int>((qw[k] >> (2 * l)) & 0x03030303u), x[j * 32 + l * 8 + k], acc);
+            }
+        }
+        int xsum = 0;
+#pragma unroll
+        for (int g = 0; g < 16; ++g) xsum += a.xsum[b * 16 + g];
+        acc -= xsum;
+        const float dw = h2f(static_cast<uint16_t>(d));
+        return lut16 ? static_cast<float>(acc) * dw * a.xd[b] : a.xd[b] * dw * static_cast<float>(acc);
+    }
+};
+
+// A tile: rows [row0, row0 + R) of one matrix, all blocks.  Unit i of the tile
+// (row i / units, block i % units) belongs to thread i % 256, slot i / 256.
+template <uint32_t T, int M = Unit<T>::kMaxPerThread>
+struct Tile {
+    static constexpr int kMax = M;
+    Unit<T> u[kMax];
+    uint32_t row0;
+    int R;
+
+    // Issues the loads of every unit this thread owns.
+    __device__ __forceinline__ void load(const Packed& m, uint32_t first_row, int rows_in_tile) {
+        row0 = first_row;
+        R = rows_in_tile;
+        const uint32_t units = m.cols / Unit<T>::kElems;
+        const uint32_t total = static_cast<uint32_t>(R) * units;
+#pragma unroll
+        for (int k = 0; k < kMax; ++k) {
+            const uint32_t i = threadIdx.x + k * kThreads;
+            if (i < total) {
+                const uint32_t r = i / units, b = i - r * units;
+                if (row0 + r < m.rows) u[k].load(m, static_cast<size_t>(row0 + r) * units + b);
+            }
         }
     }
-    int xsum = 0;
+
+    // Terms to LDS (R rows of units + 1 floats), then one lane per row adds them in
+    // block order, as the reference's sequential `sum +=` does: sums[r] is
+    // bit-identical to the reference's dot.  Ends with a barrier.
+    __device__ __forceinline__ void sums(const Packed& m, const ActLds& a, float* terms, float* out) const {
+        const uint32_t units = m.cols / Unit<T>::kElems;
+        const uint32_t stride = units + 1;
+        const uint32_t total = static_cast<uint32_t>(R) * units;
 #pragma unroll
-    for (int g = 0; g < 16; ++g) xsum += a.xsum[b * 16 + g];
-    acc -= xsum;
-    return lut16 ? static_cast<float>(acc) * h2f(dw) * a.xd[b] : a.xd[b] * h2f(dw) * static_cast<float>(acc);
-}
-
-__device__ __forceinline__ float block_term(const Packed& m, uint32_t row, uint32_t b, const ActLds& a) {
-    switch (m.type) {
-        case kQ4_0: return term_q4_0(m, row, b, a);
-        case kQ8_0: return term_q8_0(m, row, b, a);
-        case kQ4_K: return term_q4_k(m, row, b, a);
-        case kQ6_K: return term_q6_k(m, row, b, a);
-        default: return term_tq2_0(m, row, b, a, (m.flags & kFlagLut16) != 0);
+        for (int k = 0; k < kMax; ++k) {
+            const uint32_t i = threadIdx.x + k * kThreads;
+            if (i < total) {
+                const uint32_t r = i / units, b = i - r * units;
+                if (row0 + r < m.rows) terms[r * stride + b] = u[k].term(b, a);
+            }
+        }
+        __syncthreads();
+        if (threadIdx.x < static_cast<uint32_t>(R)) {
+            const float* t = terms + threadIdx.x * stride;
+            float s = 0.0f;
+            for (uint32_t b = 0; b < units; ++b) s += t[b];
+            out[threadIdx.x] = s;
+        }
+        __syncthreads();
     }
-}
-
-// Row sums of rows [row0, row0 + R) into sums[0..R): the per-block terms go to
-// LDS, then one lane per row adds them in block order, as the reference's
-// sequential `sum +=` does, so each row sum is bit-identical to it.
-// `terms` is LDS of R * (units + 1) floats.  Ends with a barrier.
-__device__ inline void tile_rowsums(const Packed& m, uint32_t row0, int R, const ActLds& a, float* terms, float* sums) {
-    const uint32_t units = m.cols / block_elems(m.type);
-    const uint32_t stride = units + 1;
-    const uint32_t total = static_cast<uint32_t>(R) * units;
-    for (uint32_t u = threadIdx.x; u < total; u += kThreads) {
-        const uint32_t r = u / units, b = u - r * units;
-        const uint32_t row = row0 + r;
-        if (row < m.rows) terms[r * stride + b] = block_term(m, row, b, a);
-    }
-    __syncthreads();
-    if (threadIdx.x < static_cast<uint32_t>(R)) {
-        const float* t = terms + threadIdx.x * stride;
-        float s = 0.0f;
-        for (uint32_t b = 0; b < units; ++b) s += t[b];
-        sums[threadIdx.x] = s;
-    }
-    __syncthreads();
-}
+};
 
 }  // namespace bh

@@ -24,21 +24,6 @@ struct GemvArgs {
     int add;              // 1: out += W x (residual), 0: out = W x
 };
 
-struct QkvArgs {
-    Packed q, k, v;
-    const float* x;
-    const float* normw;   // attn_norm
-    float eps;
-    const float* qnorm;   // per-head q/k RMS weights (Qwen3) or null
-    const float* knorm;
-    const float* rope;    // [max_context][head_dim] cos, sin pairs
-    const int* pos;       // device position of the token
-    float* qout;          // [heads][head_dim]
-    uint16_t* kcache;     // this layer's [kv_heads][ctx][head_dim]
-    uint16_t* vcache;
-    int ctx, head_dim, heads, kv_heads, neox;
-};
-
 struct GateUpArgs {
     Packed gate, up;
     int R;
@@ -50,9 +35,16 @@ struct GateUpArgs {
 };
 
 struct AttnArgs {
-    const float* q;
-    const uint16_t* kcache;
-    const uint16_t* vcache;
+    const float* q;       // this token's raw projections (before norms and RoPE): [heads][head_dim]
+    const float* k;       // [kv_heads][head_dim]
+    const float* v;
+    const float* qnorm;   // per-head q/k RMS weights (Qwen3) or null
+    const float* knorm;
+    const float* rope;    // [max_context][head_dim] cos, sin pairs
+    float eps;
+    int neox;
+    uint16_t* kcache;     // this layer's [kv_heads][ctx][head_dim]
+    uint16_t* vcache;
     const int* pos;
     int ctx, head_dim, heads, kv_heads;
     float scale;
@@ -61,32 +53,37 @@ struct AttnArgs {
     int max_splits;
     unsigned* tickets;    // [kv_heads], zero between launches (the merging workgroup re-arms its own)
     float* out;           // [heads][head_dim]
+    unsigned long long* stamps;  // optional profiling: key/value head 0's wall clock at sub-phase ends
 };
 
-constexpr int kArgmaxBlocks = 256;
-
-struct ArgmaxArgs {
-    const float* logits;
-    int n;
-    float* part_v;        // [kArgmaxBlocks]
-    int* part_i;
-    unsigned* ticket;     // zero between launches (the last workgroup re-arms it)
-    int* pos;
-    int advance;          // 1: *pos += 1 after the pick
-    int* seq;             // token sequence by position: seq[*pos + 1] = pick
+// The pending greedy pick and the sequence state it updates.
+struct PickState {
+    unsigned long long* key;   // 0 = no pick pending; else the ordered (logit, index) key of the best row
+    int* pos;                  // position of the token the current step processes
+    int* seq;                  // token sequence by position
     int seq_len;
-    const int* fixed;     // seq[0, *fixed) are caller tokens the pick must not overwrite
+    const int* fixed;          // seq[0, *fixed) are caller tokens a pick must not overwrite
+};
+
+struct HeadArgs {
+    Packed m;             // output projection
+    int R;
+    const float* x;
+    const float* normw;   // output_norm
+    float eps;
+    float* logits;        // or null
+    unsigned long long* key;   // the step's pick key (PickState::key)
 };
 
 hipError_t launch_pack(uint32_t type, const void* src, size_t rows, size_t cols, const Packed& dst, hipStream_t s);
 hipError_t launch_quantize(int kind, const float* x, void* out, size_t count, int bits, hipStream_t s);
 hipError_t launch_matvec_q8(const Packed& m, const void* xq, size_t n, float* out, size_t out_stride, hipStream_t s);
 hipError_t launch_gemv(GemvArgs g, hipStream_t s);
-hipError_t launch_qkv(const QkvArgs& g, hipStream_t s);
 hipError_t launch_gateup(GateUpArgs g, hipStream_t s);
 hipError_t launch_attention(const AttnArgs& g, hipStream_t s);
-hipError_t launch_embed(const Packed& m, const int* seq, const int* pos, float* h, hipStream_t s);
-hipError_t launch_argmax(const ArgmaxArgs& g, hipStream_t s);
+hipError_t launch_embed(const Packed& m, const PickState& ps, float* h, hipStream_t s);
+hipError_t launch_finalize(const PickState& ps, hipStream_t s);
+hipError_t launch_head(HeadArgs g, hipStream_t s);
 hipError_t launch_advance(int* pos, hipStream_t s);
 hipError_t launch_expf(const float* x, float* y, size_t n, hipStream_t s);
 int attention_max_splits(int ctx);

@@ -1,0 +1,50 @@
+// Arguments of the persistent token loop (loop.hip).
+#pragma once
+
+#include "launch.h"
+
+namespace bh {
+
+struct LayerDev {
+    Packed q, k, v, o, gate, up, down;
+    const float* attn_norm;
+    const float* q_norm;
+    const float* k_norm;
+    const float* attn_sub;
+    const float* ffn_norm;
+    const float* ffn_sub;
+    uint16_t* kc;  // [kv_heads][ctx][head_dim] fp16
+    uint16_t* vc;
+};
+
+struct LoopArgs {
+    const LayerDev* layers;  // device array
+    int n_layers;
+    Packed embd, out;
+    const float* out_norm;
+    int embd_dim, heads, kv_heads, head_dim, ff, neox, relu2;
+    float eps, scale;
+    const float* rope;       // [ctx][head_dim]
+    int ctx;
+    float *h, *q, *k, *v, *att, *act, *logits;
+    float *part_acc, *part_ml;
+    int max_splits;
+    unsigned long long* keys;  // [2] pick keys, by step parity
+    int* pos_out;              // device position after the launch
+    int* seq;                  // token sequence by position
+    int seq_len;
+    int fixed;                 // seq[0, fixed) are caller tokens
+    int pos0, n_steps, first_full;  // steps >= first_full compute the output projection and pick
+    unsigned* bar;             // barrier counters (zeroed before each launch)
+    int* error;                // set when a barrier wait expires
+    unsigned long long* trace; // optional: workgroup 0's wall clock after each barrier
+    int R_qkv[3], tiles_qkv[3];
+    int R_o, tiles_o, R_gu, tiles_gu, R_d, tiles_d, R_h, tiles_h;
+};
+
+constexpr size_t kLoopBarrierWords = 64 * 64 + 128;
+
+const void* find_loop_kernel(uint32_t tq, uint32_t tv, uint32_t to, uint32_t tg, uint32_t td, uint32_t th);
+hipError_t launch_loop(const void* kernel, const LoopArgs& g, int grid, hipStream_t s);
+
+}  // namespace bh

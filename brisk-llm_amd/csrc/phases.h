@@ -1,0 +1,428 @@
+// Phase bodies shared by the one-kernel-per-phase path (kernels.hip) and the
+// persistent token loop (loop.hip): attention and the greedy-pick key.
+#pragma once
+
+#include "launch.h"
+
+namespace bh {
+
+// Element e of row r of a packed matrix, dequantised as embedding_row does
+// (src/model.cpp:27-70, src/quant.cpp:196-239).
+__device__ inline float dequant_elem(const Packed& m, uint32_t r, uint32_t e) {
+    const uint32_t cols = m.cols;
+    switch (m.type) {
+        case kQ8_0: {
+            const size_t blk = static_cast<size_t>(r) * (cols / 32) + e / 32;
+            const float d = h2f(reinterpret_cast<const uint16_t*>(m.p1)[blk]);
+            return static_cast<float>(static_cast<int8_t>(m.p0[blk * 32 + e % 32])) * d;
+        }
+        case kQ4_0: {
+            const size_t blk = static_cast<size_t>(r) * (cols / 32) + e / 32;
+            const float d = h2f(reinterpret_cast<const uint16_t*>(m.p1)[blk]);
+            const uint32_t i = e % 32;
+            const uint8_t q = m.p0[blk * 16 + (i & 15)];
+            return static_cast<float>((i < 16 ? (q & 0x0F) : (q >> 4)) - 8) * d;
+        }
+        case kQ4_K: {
+            const size_t blk = static_cast<size_t>(r) * (cols / 256) + e / 256;
+            const uint8_t* meta = m.p1 + blk * 16;
+            const float d = h2f(static_cast<uint16_t>(meta[0] | (meta[1] << 8)));
+            const float dmin = h2f(static_cast<uint16_t>(meta[2] | (meta[3] << 8)));
+            const int i = e % 256, chunk = i / 64, hi = (i % 64) >= 32, j = i % 32;
+            int sc, mn;
+            q4k_scale_min(meta + 4, 2 * chunk + hi, sc, mn);
+            const float d1 = d * static_cast<float>(sc), m1 = dmin * static_cast<float>(mn);
+            const uint8_t q = m.p0[blk * 128 + chunk * 32 + j];
+            return d1 * static_cast<float>(hi ? (q >> 4) : (q & 0xF)) - m1;
+        }
+        case kQ6_K: {
+            const size_t blk = static_cast<size_t>(r) * (cols / 256) + e / 256;
+            const int i = e % 256, half = i / 128, w = i % 128, quarter = w / 32, l = w % 32;
+            const uint8_t* ql = m.p0 + blk * 128 + half * 64;
+            const uint8_t* qh = m.p1 + blk * 64 + half * 32;
+            const uint8_t* meta = m.p2 + blk * 20;
+            const int lo = (quarter & 1) ? ql[l + 32] : ql[l];
+            const int nib = quarter >= 2 ? (lo >> 4) : (lo & 0xF);
+            const int q = (nib | (((qh[l] >> (2 * quarter)) & 3) << 4)) - 32;
+            const float d = h2f(static_cast<uint16_t>(meta[16] | (meta[17] << 8)));
+            return d * static_cast<float>(static_cast<int8_t>(meta[i / 16])) * static_cast<float>(q);
+        }
+        default: {  // TQ2_0
+            const size_t blk = static_cast<size_t>(r) * (cols / 256) + e / 256;
+            const int i = e % 256;
+            const int c = (m.p0[blk * 64 + (i / 128) * 32 + i % 32] >> (2 * ((i % 128) / 32))) & 3;
+            return static_cast<float>(c - 1) * h2f(reinterpret_cast<const uint16_t*>(m.p1)[blk]);
+        }
+    }
+}
+
+// Ordered 64-bit key of (logit, index): larger logit first, then smaller index,
+// so one atomicMax finds the reference's pick (std::max_element: the first index
+// of the maximum, src/sampler.cpp:11-13).  -0 is keyed as +0 (they compare equal).
+__device__ __forceinline__ unsigned long long pick_key(float v, uint32_t idx) {
+    if (v == 0.0f) v = 0.0f;
+    const uint32_t u = __float_as_uint(v);
+    const uint32_t ord = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+    return (static_cast<unsigned long long>(ord) << 32) | (0xFFFFFFFFu - idx);
+}
+
+
+constexpr int kSplit = 64;         // positions per split / per LDS chunk
+constexpr int kExactMax = 512;     // contexts up to this length take the exact-order path
+constexpr int kExactScores = 4096; // ... when heads-per-kv x length fits this many LDS scores
+
+struct AttnLds {
+    float q[16 * 128];               // the group's query heads, normed and rotated
+    float kcur[128], vcur[128];      // this token's key and value (fp16-rounded)
+    uint16_t kv[kSplit * 128];       // one staged chunk of keys or values
+    float part[4 * kSplit * 16];     // dot_f32 lane partials: [head][position][lane]
+    float sc[kExactScores];          // scores, then weights: [head][position]
+    double red[16][4];
+    float mx[16];
+    float ml[16][2];
+};
+
+// RMS norm over one head (optional weight w) and RoPE, by one wave: the
+// per-head q_norm / k_norm and apply_rope of src/model.cpp:1026-1041, with
+// rms_norm's float squares summed in double (src/model.cpp:87-97).
+__device__ void head_norm_rope(float* v, const float* w, const float* rope, int hd, int neox, float eps) {
+    const int lane = threadIdx.x & 63;
+    if (w != nullptr) {
+        double s = 0.0;
+        for (int i = lane; i < hd; i += 64) s += static_cast<double>(v[i] * v[i]);
+        s = wave_sum(s);
+        const float scale = rms_scale(s, hd, eps);
+        for (int i = lane; i < hd; i += 64) v[i] = v[i] * scale * w[i];
+    }
+    const int half = hd / 2;
+    for (int i = lane; i < half; i += 64) {
+        const float c = rope[2 * i], sn = rope[2 * i + 1];
+        const int ia = neox ? i : 2 * i, ib = neox ? i + half : 2 * i + 1;
+        const float x0 = v[ia], x1 = v[ib];
+        v[ia] = x0 * c - x1 * sn;
+        v[ib] = x0 * sn + x1 * c;
+    }
+}
+
+// This token's query heads of the group, and (for `writer`) its key and value
+// into LDS and the fp16 caches at position pos.
+template <class IO, bool kWriteThrough = false>
+__device__ void attn_prologue(const AttnArgs& g, AttnLds& s, int kv, int pos, bool writer) {
+    const int hd = g.head_dim, hpk = g.heads / g.kv_heads, t = threadIdx.x;
+    for (int i = t; i < hpk * hd; i += kThreads) s.q[i] = IO::ld(g.q + kv * hpk * hd + i);
+    if (writer)
+        for (int i = t; i < hd; i += kThreads) {
+            s.kcur[i] = IO::ld(g.k + kv * hd + i);
+            s.vcur[i] = IO::ld(g.v + kv * hd + i);
+        }
+    __syncthreads();
+    const float* rope = g.rope + static_cast<size_t>(pos) * hd;
+    const int wave = t >> 6;
+    for (int h = wave; h < hpk + (writer ? 1 : 0); h += kThreads / 64) {
+        if (h < hpk) head_norm_rope(s.q + h * hd, g.qnorm, rope, hd, g.neox, g.eps);
+        else head_norm_rope(s.kcur, g.knorm, rope, hd, g.neox, g.eps);
+    }
+    __syncthreads();
+    if (writer) {
+        uint16_t* kr = g.kcache + (static_cast<size_t>(kv) * g.ctx + pos) * hd;
+        uint16_t* vr = g.vcache + (static_cast<size_t>(kv) * g.ctx + pos) * hd;
+        for (int i = 2 * t; i < hd; i += 2 * kThreads) {  // store_f16 (src/kernels_f32.cpp:248-250), in pairs
+            const uint16_t k0 = f2h(s.kcur[i]), k1 = f2h(s.kcur[i + 1]);
+            const uint16_t v0 = f2h(s.vcur[i]), v1 = f2h(s.vcur[i + 1]);
+            const uint32_t kw = k0 | (static_cast<uint32_t>(k1) << 16), vw = v0 | (static_cast<uint32_t>(v1) << 16);
+            if (kWriteThrough) {  // read by other workgroups later in the same launch
+                __hip_atomic_store(reinterpret_cast<uint32_t*>(kr + i), kw, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+                __hip_atomic_store(reinterpret_cast<uint32_t*>(vr + i), vw, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+            } else {
+                *reinterpret_cast<uint32_t*>(kr + i) = kw;
+                *reinterpret_cast<uint32_t*>(vr + i) = vw;
+            }
+            s.kcur[i] = h2f(k0); s.kcur[i + 1] = h2f(k1);
+            s.vcur[i] = h2f(v0); s.vcur[i + 1] = h2f(v1);
+        }
+        __syncthreads();
+    }
+}
+
+// Chunk c of a cache ([kv][ctx][hd] fp16) through registers: every thread
+// issues its 16-byte loads for the chunk at once.
+struct ChunkRegs {
+    uint4 r[4];
+};
+
+__device__ __forceinline__ void chunk_load(ChunkRegs& cr, const uint16_t* base, int p0, int n_pos, int hd) {
+    const int per_pos = hd / 8;  // 16-byte pieces per position
+    const int total = n_pos * per_pos;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        const int i = threadIdx.x + k * kThreads;
+        if (i < total) cr.r[k] = *reinterpret_cast<const uint4*>(base + static_cast<size_t>(p0 + i / per_pos) * hd + (i % per_pos) * 8);
+    }
+}
+
+__device__ __forceinline__ void chunk_store(const ChunkRegs& cr, uint16_t* lds, int n_pos, int hd) {
+    const int total = n_pos * (hd / 8);
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        const int i = threadIdx.x + k * kThreads;
+        if (i < total) *reinterpret_cast<uint4*>(lds + i * 8) = cr.r[k];
+    }
+}
+
+// One chunk of the exact path's scores: stage chunk c's keys (cur) into LDS
+// (the current position's from LDS), start loading chunk c + 1 into nxt, and
+// form dot_f32's 16 lane partials and their in-order sum for every query head.
+__device__ __forceinline__ void score_chunk(const AttnArgs& g, AttnLds& s, const ChunkRegs& cur, ChunkRegs& nxt, int c,
+                                            int nchunks, int L, const uint16_t* kbase) {
+    const int hd = g.head_dim, hpk = g.heads / g.kv_heads, t = threadIdx.x, per = hd / 16, pos = L - 1;
+    const int p0 = c * kSplit;
+    const int n = L - p0 < kSplit ? L - p0 : kSplit;
+    const int ncache = pos - p0 < n ? pos - p0 : n;  // positions of the chunk held in the cache
+    __syncthreads();                                 // the previous chunk is consumed
+    chunk_store(cur, s.kv, ncache, hd);
+    if (ncache < n)
+        for (int i = t; i < hd; i += kThreads) s.kv[ncache * hd + i] = f2h(s.kcur[i]);
+    if (c + 1 < nchunks) {
+        const int q0 = p0 + kSplit;
+        const int nn = pos - q0 < kSplit ? pos - q0 : kSplit;
+        if (nn > 0) chunk_load(nxt, kbase, q0, nn, hd);
+    }
+    __syncthreads();
+    for (int g0 = 0; g0 < hpk; g0 += 4) {
+        const int gn = hpk - g0 < 4 ? hpk - g0 : 4;
+        for (int i = t; i < n * 16; i += kThreads) {
+            const int p = i >> 4, j = i & 15;
+            const uint16_t* kr = s.kv + p * hd;
+            float kf[8];
+#pragma unroll
+            for (int m = 0; m < 8; ++m) kf[m] = m < per ? h2f(kr[j + 16 * m]) : 0.0f;
+            for (int gg = 0; gg < gn; ++gg) {
+                const float* q = s.q + (g0 + gg) * hd;
+                float lane = 0.0f;
+#pragma unroll
+                for (int m = 0; m < 8; ++m)
+                    if (m < per) lane += q[j + 16 * m] * kf[m];
+                s.part[(gg * kSplit + p) * 16 + j] = lane;
+            }
+        }
+        __syncthreads();
+        for (int i = t; i < gn * n; i += kThreads) {
+            const int gg = i / n, p = i % n;
+            const float* pr = s.part + (gg * kSplit + p) * 16;
+            float sum = 0.0f;
+#pragma unroll
+            for (int j = 0; j < 16; ++j) sum += pr[j];
+            s.sc[(g0 + gg) * L + p0 + p] = sum * g.scale;
+        }
+        if (g0 + 4 < hpk) __syncthreads();
+    }
+}
+
+// One chunk of the exact path's value sums: stage chunk c's values, start the
+// next chunk's loads, and extend every (head, dim) chain over the chunk's
+// positions in order.
+__device__ __forceinline__ void value_chunk(const AttnArgs& g, AttnLds& s, const ChunkRegs& cur, ChunkRegs& nxt, int c,
+                                            int nchunks, int L, const uint16_t* vbase, float (&acc)[8]) {
+    const int hd = g.head_dim, hpk = g.heads / g.kv_heads, t = threadIdx.x, pos = L - 1, chains = hpk * hd;
+    const int p0 = c * kSplit;
+    const int n = L - p0 < kSplit ? L - p0 : kSplit;
+    const int ncache = pos - p0 < n ? pos - p0 : n;
+    __syncthreads();  // the previous chunk's values (and the weights) are ready / consumed
+    chunk_store(cur, s.kv, ncache, hd);
+    if (ncache < n)
+        for (int i = t; i < hd; i += kThreads) s.kv[ncache * hd + i] = f2h(s.vcur[i]);
+    if (c + 1 < nchunks) {
+        const int q0 = p0 + kSplit;
+        const int nn = pos - q0 < kSplit ? pos - q0 : kSplit;
+        if (nn > 0) chunk_load(nxt, vbase, q0, nn, hd);
+    }
+    __syncthreads();
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+        const int ch = t + k * kThreads;
+        if (ch < chains) {
+            const int gq = ch / hd, d = ch % hd;
+            const float* w = s.sc + gq * L + p0;
+            const uint16_t* vv = s.kv + d;
+            float a = acc[k];
+            int p = 0;
+            for (; p + 8 <= n; p += 8) {  // loads first, then the adds in position order
+                float wv[8], vf[8];
+#pragma unroll
+                for (int u = 0; u < 8; ++u) {
+                    wv[u] = w[p + u];
+                    vf[u] = h2f(vv[(p + u) * hd]);
+                }
+#pragma unroll
+                for (int u = 0; u < 8; ++u) a += wv[u] * vf[u];
+            }
+            for (; p < n; ++p) a += w[p] * h2f(vv[p * hd]);
+            acc[k] = a;
+        }
+    }
+}
+
+// The reference's attention for one token (src/model.cpp:1050-1093 with the
+// portable kernels of src/kernels_f32.cpp:229-284), operation for operation:
+//   score_p = dot_f32(q, k_p) * scale, dot_f32 being 16 lane partials over
+//             i = j (mod 16) in order, then 0 + lane 0 + ... + lane 15;
+//   softmax: max, e_p = expf(s_p - max), sum of e_p in double, w_p = e_p * (float)(1 / sum);
+//   out    = 0 + w_0 v_0 + w_1 v_1 + ... in position order (weighted_sum_f32's axpy).
+// The one grouping that differs is the double sum, whose rounding can reach the
+// float scale only when terms below 2^-20 of the sum lose bits.
+__device__ __forceinline__ void attn_stamp(const AttnArgs& g, int kv, int i) {
+    if (g.stamps != nullptr && kv == 0 && threadIdx.x == 0) g.stamps[i] = wall_clock64();
+}
+
+template <class IO>
+__device__ void attn_exact(const AttnArgs& g, AttnLds& s, int kv, int L) {
+    const int hd = g.head_dim, hpk = g.heads / g.kv_heads, t = threadIdx.x, per = hd / 16;
+    attn_stamp(g, kv, 1);
+    const int pos = L - 1, nchunks = (L + kSplit - 1) / kSplit;
+    const uint16_t* kbase = g.kcache + static_cast<size_t>(kv) * g.ctx * hd;
+    const uint16_t* vbase = g.vcache + static_cast<size_t>(kv) * g.ctx * hd;
+    ChunkRegs ra, rb;  // two register buffers: chunk c in (c even ? ra : rb), the next one loading meanwhile
+    // ---- scores, chunk by chunk (the current position's key comes from LDS)
+    {
+        const int n0 = pos < kSplit ? pos : kSplit;
+        chunk_load(ra, kbase, 0, n0, hd);
+    }
+    for (int c = 0; c < nchunks; c += 2) {
+        score_chunk(g, s, ra, rb, c, nchunks, L, kbase);
+        if (c + 1 < nchunks) score_chunk(g, s, rb, ra, c + 1, nchunks, L, kbase);
+    }
+    __syncthreads();
+    attn_stamp(g, kv, 2);
+    // ---- softmax per head
+    const int wave = t >> 6, wl = t & 63;
+    for (int gq = 0; gq < hpk; ++gq) {
+        float m = -INFINITY;
+        for (int p = t; p < L; p += kThreads) m = fmaxf(m, s.sc[gq * L + p]);
+        m = wave_max(m);
+        if (wl == 0) s.red[gq][wave] = static_cast<double>(m);
+    }
+    __syncthreads();
+    if (t < hpk) s.mx[t] = static_cast<float>(fmax(fmax(s.red[t][0], s.red[t][1]), fmax(s.red[t][2], s.red[t][3])));
+    __syncthreads();
+    for (int gq = 0; gq < hpk; ++gq) {
+        double part = 0.0;
+        for (int p = t; p < L; p += kThreads) {
+            const float e = ref_expf(s.sc[gq * L + p] - s.mx[gq]);
+            s.sc[gq * L + p] = e;
+            part += static_cast<double>(e);
+        }
+        part = wave_sum(part);
+        if (wl == 0) s.red[gq][wave] = part;
+    }
+    __syncthreads();
+    for (int gq = 0; gq < hpk; ++gq) {
+        const double sum = ((s.red[gq][0] + s.red[gq][1]) + s.red[gq][2]) + s.red[gq][3];
+        const float scale = static_cast<float>(1.0 / sum);
+        for (int p = t; p < L; p += kThreads) s.sc[gq * L + p] *= scale;
+    }
+    attn_stamp(g, kv, 3);
+    // ---- value sums in position order, chunk by chunk
+    float acc[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) acc[k] = 0.0f;
+    const int chains = hpk * hd;
+    {
+        const int n0 = pos < kSplit ? pos : kSplit;
+        chunk_load(ra, vbase, 0, n0, hd);
+    }
+    for (int c = 0; c < nchunks; c += 2) {
+        value_chunk(g, s, ra, rb, c, nchunks, L, vbase, acc);
+        if (c + 1 < nchunks) value_chunk(g, s, rb, ra, c + 1, nchunks, L, vbase, acc);
+    }
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+        const int ch = t + k * kThreads;
+        if (ch < chains) IO::st(g.out + kv * hpk * hd + ch, acc[k]);
+    }
+    attn_stamp(g, kv, 4);
+}
+
+// Split-K (flash-decoding) partials for longer contexts: each workgroup scores
+// kSplit positions for all the key/value head's query heads and keeps (max, sum
+// of exp, exp-weighted value sum); attn_split_combine then merges the splits
+// with the log-sum-exp rescale.  Same mathematics as the reference, different
+// rounding order (tolerance, not bit-exact).
+template <class IO>
+__device__ void attn_split_partial(const AttnArgs& g, AttnLds& s, int kv, int split, int L) {
+    const int hd = g.head_dim, hpk = g.heads / g.kv_heads, t = threadIdx.x;
+    const int pos = L - 1, p0 = split * kSplit;
+    const int n = L - p0 < kSplit ? L - p0 : kSplit;
+    const int ncache = pos - p0 < n ? pos - p0 : n;
+    const uint16_t* kbase = g.kcache + static_cast<size_t>(kv) * g.ctx * hd;
+    const uint16_t* vbase = g.vcache + static_cast<size_t>(kv) * g.ctx * hd;
+    ChunkRegs cr;
+    chunk_load(cr, kbase, p0, ncache, hd);
+    chunk_store(cr, s.kv, ncache, hd);
+    if (ncache < n)
+        for (int i = t; i < hd; i += kThreads) s.kv[ncache * hd + i] = f2h(s.kcur[i]);
+    chunk_load(cr, vbase, p0, ncache, hd);  // values in flight while scoring
+    __syncthreads();
+    float* sc = s.sc;  // [head][kSplit]
+    for (int i = t; i < hpk * kSplit; i += kThreads) {
+        const int gq = i / kSplit, p = i % kSplit;
+        float acc = -INFINITY;
+        if (p < n) {
+            acc = 0.0f;
+            const uint16_t* kr = s.kv + p * hd;
+            const float* q = s.q + gq * hd;
+            for (int d = 0; d < hd; ++d) acc += q[d] * h2f(kr[d]);
+            acc *= g.scale;
+        }
+        sc[gq * kSplit + p] = acc;
+    }
+    __syncthreads();
+    const int wave = t >> 6, lane = t & 63;
+    for (int gq = wave; gq < hpk; gq += 4) {
+        const float sv = sc[gq * kSplit + lane];
+        const float mx = wave_max(sv);
+        const float e = lane < n ? ref_expf(sv - mx) : 0.0f;
+        const float l = wave_sum(e);
+        sc[gq * kSplit + lane] = e;
+        if (lane == 0) { s.ml[gq][0] = mx; s.ml[gq][1] = l; }
+    }
+    __syncthreads();
+    chunk_store(cr, s.kv, ncache, hd);
+    if (ncache < n)
+        for (int i = t; i < hd; i += kThreads) s.kv[ncache * hd + i] = f2h(s.vcur[i]);
+    __syncthreads();
+    for (int i = t; i < hpk * hd; i += kThreads) {
+        const int gq = i / hd, d = i % hd;
+        float acc = 0.0f;
+        for (int p = 0; p < n; ++p) acc += sc[gq * kSplit + p] * h2f(s.kv[p * hd + d]);
+        const size_t slot = static_cast<size_t>(kv * hpk + gq) * g.max_splits + split;
+        IO::st(g.part_acc + slot * hd + d, acc);
+        if (d == 0) {
+            IO::st(g.part_ml + slot * 2, s.ml[gq][0]);
+            IO::st(g.part_ml + slot * 2 + 1, s.ml[gq][1]);
+        }
+    }
+}
+
+// Merges the splits of key/value head kv's query heads into out.
+template <class IO>
+__device__ void attn_split_combine(const AttnArgs& g, int kv, int L) {
+    const int hd = g.head_dim, hpk = g.heads / g.kv_heads, t = threadIdx.x;
+    const int ns = (L + kSplit - 1) / kSplit;
+    for (int i = t; i < hpk * hd; i += kThreads) {
+        const int gq = i / hd, d = i % hd;
+        const size_t base = static_cast<size_t>(kv * hpk + gq) * g.max_splits;
+        float M = -INFINITY;
+        for (int s2 = 0; s2 < ns; ++s2) M = fmaxf(M, IO::ld(g.part_ml + (base + s2) * 2));
+        float num = 0.0f, den = 0.0f;
+        for (int s2 = 0; s2 < ns; ++s2) {
+            const float f = ref_expf(IO::ld(g.part_ml + (base + s2) * 2) - M);
+            den += IO::ld(g.part_ml + (base + s2) * 2 + 1) * f;
+            num += IO::ld(g.part_acc + (base + s2) * hd + d) * f;
+        }
+        IO::st(g.out + (kv * hpk + gq) * hd + d, num / den);
+    }
+}
+
+__device__ __forceinline__ bool attn_is_exact(int L, int hpk) { return L <= kExactMax && L * hpk <= kExactScores; }
+
+}  // namespace bh

@@ -50,7 +50,7 @@ Session::Session(const brisk_hip_config& cfg, const brisk_hip_tensor* tensors, s
         model_fail("a model dimension is zero");
     if (cfg.heads % cfg.kv_heads != 0) model_fail("head_count is not a multiple of head_count_kv");
     if (cfg.heads / cfg.kv_heads > 16) model_fail("more than 16 query heads per key/value head is not supported");
-    if (cfg.kv_heads > 1000) model_fail("more than 1000 key/value heads is not supported");
+    if (cfg.kv_heads > 1000) model_fail("more than 1000 key/value heads is not supported");  // ticket slots
     if (cfg.head_dim == 0 || cfg.head_dim % 32 != 0 || cfg.head_dim > 128) model_fail("head size must be 32, 64, 96 or 128");
     if (cfg.embd > kMaxCols || cfg.ff > kMaxCols || cfg.heads * cfg.head_dim > kMaxCols) model_fail("a row wider than 8192 is not supported");
     check(hipSetDevice(device), "hipSetDevice");
@@ -149,8 +149,10 @@ Session::Session(const brisk_hip_config& cfg, const brisk_hip_tensor* tensors, s
     max_splits_ = attention_max_splits(static_cast<int>(max_ctx_));
     part_acc_ = static_cast<float*>(alloc(static_cast<size_t>(cfg.heads) * max_splits_ * hd * 4));
     part_ml_ = static_cast<float*>(alloc(static_cast<size_t>(cfg.heads) * max_splits_ * 2 * 4));
-    arg_v_ = static_cast<float*>(alloc(kArgmaxBlocks * 4));
-    arg_i_ = static_cast<int*>(alloc(kArgmaxBlocks * 4));
+    k_ = static_cast<float*>(alloc(kvd * 4));
+    v_ = static_cast<float*>(alloc(kvd * 4));
+    key_ = static_cast<unsigned long long*>(alloc(64));  // [0]: graph path; [2], [3]: loop (by step parity)
+    check(hipMemsetAsync(key_, 0, 64, stream_), "memset");
     ticket_ = static_cast<unsigned*>(alloc(4096));
     pos_ = static_cast<int*>(alloc(64));
     seq_ = static_cast<int*>(alloc((max_ctx_ + 1) * 4));
@@ -187,6 +189,7 @@ Session::Session(const brisk_hip_config& cfg, const brisk_hip_tensor* tensors, s
     }
     check(hipStreamSynchronize(stream_), "init sync");
     debug_ = std::getenv("BRISK_HIP_DEBUG") != nullptr;
+    setup_loop();
     use_graphs_ = std::getenv("BRISK_HIP_NO_GRAPH") == nullptr && !debug_;
     if (use_graphs_) {
         graph_layers_ = capture(false);
@@ -211,24 +214,40 @@ void* Session::alloc(size_t bytes) {
 // One decode step at *pos_: embed seq[*pos_], every layer, then either the
 // output projection + greedy pick (which advances *pos_) or a bare advance.
 void Session::record_step(bool full) {
-    check(launch_embed(embd_.p, seq_, pos_, h_, stream_), "embed");
+    check(launch_embed(embd_.p, pick_state(), h_, stream_), "embed");
     const float scale = 1.0f / std::sqrt(static_cast<float>(cfg_.head_dim));  // src/model.cpp:978
     for (uint32_t l = 0; l < cfg_.layers; ++l) {
         const Layer& L = layers_[l];
-        QkvArgs qa{};
-        qa.q = L.q.p; qa.k = L.k.p; qa.v = L.v.p;
-        qa.x = h_; qa.normw = L.attn_norm; qa.eps = cfg_.rms_epsilon;
-        qa.qnorm = L.q_norm; qa.knorm = L.k_norm; qa.rope = rope_; qa.pos = pos_;
-        qa.qout = q_; qa.kcache = kcache_[l]; qa.vcache = vcache_[l];
-        qa.ctx = static_cast<int>(max_ctx_); qa.head_dim = static_cast<int>(cfg_.head_dim);
-        qa.heads = static_cast<int>(cfg_.heads); qa.kv_heads = static_cast<int>(cfg_.kv_heads);
-        qa.neox = cfg_.arch != BRISK_HIP_ARCH_LLAMA;  // src/model.cpp:167
-        check(launch_qkv(qa, stream_), "qkv");
+        // Q, K, V rows from attn_norm(h) (src/model.cpp:996-1015): one launch per weight format
+        {
+            const DeviceMatrix* mats[3] = {&L.q, &L.k, &L.v};
+            float* outs[3] = {q_, k_, v_};
+            GemvArgs qa{};
+            qa.x = h_; qa.normw = L.attn_norm; qa.eps = cfg_.rms_epsilon; qa.add = 0;
+            bool done[3] = {false, false, false};
+            for (int i = 0; i < 3; ++i) {
+                if (done[i]) continue;
+                qa.n = 0;
+                for (int j = i; j < 3; ++j) {
+                    if (!done[j] && mats[j]->p.type == mats[i]->p.type) {
+                        qa.t[qa.n].m = mats[j]->p;
+                        qa.t[qa.n].out = outs[j];
+                        ++qa.n;
+                        done[j] = true;
+                    }
+                }
+                check(launch_gemv(qa, stream_), "qkv");
+            }
+        }
 
         AttnArgs aa{};
-        aa.q = q_; aa.kcache = kcache_[l]; aa.vcache = vcache_[l]; aa.pos = pos_;
-        aa.ctx = qa.ctx; aa.head_dim = qa.head_dim; aa.heads = qa.heads; aa.kv_heads = qa.kv_heads;
-        aa.scale = scale; aa.part_acc = part_acc_; aa.part_ml = part_ml_; aa.max_splits = max_splits_; aa.tickets = ticket_ + 1; aa.out = att_;
+        aa.q = q_; aa.k = k_; aa.v = v_; aa.qnorm = L.q_norm; aa.knorm = L.k_norm; aa.rope = rope_;
+        aa.eps = cfg_.rms_epsilon; aa.neox = cfg_.arch != BRISK_HIP_ARCH_LLAMA;  // src/model.cpp:167
+        aa.kcache = kcache_[l]; aa.vcache = vcache_[l]; aa.pos = pos_;
+        aa.ctx = static_cast<int>(max_ctx_); aa.head_dim = static_cast<int>(cfg_.head_dim);
+        aa.heads = static_cast<int>(cfg_.heads); aa.kv_heads = static_cast<int>(cfg_.kv_heads);
+        aa.scale = scale; aa.part_acc = part_acc_; aa.part_ml = part_ml_; aa.max_splits = max_splits_;
+        aa.tickets = ticket_ + 4; aa.out = att_;
         check(launch_attention(aa, stream_), "attention");
 
         GemvArgs oa{};
@@ -248,19 +267,146 @@ void Session::record_step(bool full) {
         if (debug_) debug_layer(l);
     }
     if (full) {
-        GemvArgs oa{};
-        oa.n = 1; oa.t[0].m = out_->p; oa.t[0].out = logits_;
-        oa.x = h_; oa.normw = out_norm_; oa.eps = cfg_.rms_epsilon; oa.add = 0;
-        check(launch_gemv(oa, stream_), "output");
-        ArgmaxArgs ar{};
-        ar.logits = logits_; ar.n = static_cast<int>(cfg_.vocab); ar.part_v = arg_v_; ar.part_i = arg_i_;
-        ar.ticket = ticket_; ar.pos = pos_; ar.advance = 1; ar.seq = seq_; ar.seq_len = static_cast<int>(max_ctx_) + 1;
-        ar.fixed = pos_ + 1;
-        check(launch_argmax(ar, stream_), "argmax");
+        HeadArgs ha{};
+        ha.m = out_->p; ha.x = h_; ha.normw = out_norm_; ha.eps = cfg_.rms_epsilon; ha.logits = logits_;
+        ha.key = key_;
+        check(launch_head(ha, stream_), "output");
     } else {
         check(launch_advance(pos_, stream_), "advance");
     }
 }
+
+// Rows per tile for a phase of the loop: about one tile per workgroup, within
+// the per-thread register budget and the LDS term buffer of every matrix in it.
+static int loop_rows(const std::vector<const Packed*>& ms, int grid, size_t cols_scale = 1) {
+    size_t rows = 0;
+    for (const Packed* m : ms) rows += m->rows;
+    int R = 1;
+    while (R < 64 && static_cast<size_t>(R) * static_cast<size_t>(grid) < rows) R *= 2;
+    for (const Packed* m : ms) R = std::min(R, pick_rows_per_tile(m->type, 1u << 30, m->cols * cols_scale));
+    return std::max(R, 1);
+}
+
+static int tiles_of(const Packed& m, int R) { return static_cast<int>((m.rows + R - 1) / R); }
+
+void Session::setup_loop() {
+    const char* path = std::getenv("BRISK_HIP_PATH");
+    if (path != nullptr && std::string(path) == "graph") return;
+    if (debug_) return;
+    const Layer& L0 = layers_[0];
+    const void* k = find_loop_kernel(L0.q.p.type, L0.v.p.type, L0.o.p.type, L0.gate.p.type, L0.down.p.type, out_->p.type);
+    if (k == nullptr) return;
+    for (const Layer& L : layers_) {  // every layer must share layer 0's formats
+        if (L.q.p.type != L0.q.p.type || L.k.p.type != L0.q.p.type || L.v.p.type != L0.v.p.type || L.o.p.type != L0.o.p.type ||
+            L.gate.p.type != L0.gate.p.type || L.up.p.type != L0.gate.p.type || L.down.p.type != L0.down.p.type ||
+            L.q.p.flags != L0.q.p.flags || L.v.p.flags != L0.v.p.flags || L.o.p.flags != L0.o.p.flags ||
+            L.gate.p.flags != L0.gate.p.flags || L.down.p.flags != L0.down.p.flags)
+            return;
+    }
+    int cus = 0, per_cu = 0;
+    check(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device_), "hipDeviceGetAttribute");
+    check(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, k, kThreads, 0), "hipOccupancy");
+    if (cus <= 0 || per_cu < 1 || cus < static_cast<int>(cfg_.kv_heads)) return;
+    loop_grid_ = cus;  // one resident workgroup per CU: the barrier needs every workgroup resident
+    loop_kernel_ = k;
+
+    std::vector<LayerDev> ld(cfg_.layers);
+    for (uint32_t l = 0; l < cfg_.layers; ++l) {
+        const Layer& L = layers_[l];
+        ld[l] = LayerDev{L.q.p, L.k.p, L.v.p, L.o.p, L.gate.p, L.up.p, L.down.p, L.attn_norm, L.q_norm, L.k_norm,
+                         L.attn_sub_norm, L.ffn_norm, L.ffn_sub_norm, kcache_[l], vcache_[l]};
+    }
+    layers_dev_ = static_cast<LayerDev*>(alloc(ld.size() * sizeof(LayerDev)));
+    check(hipMemcpy(layers_dev_, ld.data(), ld.size() * sizeof(LayerDev), hipMemcpyHostToDevice), "hipMemcpy(layers)");
+    loop_bar_ = static_cast<unsigned*>(alloc(kLoopBarrierWords * 4));
+    loop_error_ = static_cast<int*>(alloc(64));
+    if (std::getenv("BRISK_HIP_TRACE") != nullptr) trace_ = static_cast<unsigned long long*>(alloc(kTraceSlots * 8));
+    check(hipMemset(loop_error_, 0, 64), "memset");
+
+    LoopArgs& g = loop_;
+    g.layers = layers_dev_;
+    g.n_layers = static_cast<int>(cfg_.layers);
+    g.embd = embd_.p;
+    g.out = out_->p;
+    g.out_norm = out_norm_;
+    g.embd_dim = static_cast<int>(cfg_.embd);
+    g.heads = static_cast<int>(cfg_.heads);
+    g.kv_heads = static_cast<int>(cfg_.kv_heads);
+    g.head_dim = static_cast<int>(cfg_.head_dim);
+    g.ff = static_cast<int>(cfg_.ff);
+    g.neox = cfg_.arch != BRISK_HIP_ARCH_LLAMA;
+    g.relu2 = cfg_.arch == BRISK_HIP_ARCH_BITNET;
+    g.eps = cfg_.rms_epsilon;
+    g.scale = 1.0f / std::sqrt(static_cast<float>(cfg_.head_dim));
+    g.rope = rope_;
+    g.ctx = static_cast<int>(max_ctx_);
+    g.h = h_; g.q = q_; g.k = k_; g.v = v_; g.att = att_; g.act = act_; g.logits = logits_;
+    g.part_acc = part_acc_; g.part_ml = part_ml_; g.max_splits = max_splits_;
+    g.keys = key_ + 2;
+    g.pos_out = pos_;
+    g.seq = seq_;
+    g.seq_len = static_cast<int>(max_ctx_) + 1;
+    g.bar = loop_bar_;
+    g.error = loop_error_;
+    const int G = loop_grid_;
+    if (L0.q.p.type == L0.v.p.type) {
+        const int R = loop_rows({&L0.q.p, &L0.k.p, &L0.v.p}, G);
+        for (int i = 0; i < 3; ++i) g.R_qkv[i] = R;
+    } else {
+        const int R = loop_rows({&L0.q.p, &L0.k.p}, G);
+        g.R_qkv[0] = g.R_qkv[1] = R;
+        g.R_qkv[2] = loop_rows({&L0.v.p}, G);
+    }
+    g.tiles_qkv[0] = tiles_of(L0.q.p, g.R_qkv[0]);
+    g.tiles_qkv[1] = tiles_of(L0.k.p, g.R_qkv[1]);
+    g.tiles_qkv[2] = tiles_of(L0.v.p, g.R_qkv[2]);
+    g.R_o = loop_rows({&L0.o.p}, G);
+    g.tiles_o = tiles_of(L0.o.p, g.R_o);
+    g.R_gu = loop_rows({&L0.gate.p}, G, 2);
+    g.tiles_gu = tiles_of(L0.gate.p, g.R_gu);
+    g.R_d = loop_rows({&L0.down.p}, G);
+    g.tiles_d = tiles_of(L0.down.p, g.R_d);
+    g.R_h = loop_rows({&out_->p}, G);
+    g.tiles_h = tiles_of(out_->p, g.R_h);
+}
+
+// One launch of the persistent loop: n_steps steps from position pos0; steps
+// from first_full on compute the output projection and the pick.
+void Session::run_loop(size_t pos0, size_t n_steps, size_t first_full, size_t fixed) {
+    LoopArgs g = loop_;
+    g.pos0 = static_cast<int>(pos0);
+    g.n_steps = static_cast<int>(n_steps);
+    g.first_full = static_cast<int>(first_full);
+    g.fixed = static_cast<int>(fixed);
+    g.trace = trace_;
+    check(hipMemsetAsync(loop_bar_, 0, kLoopBarrierWords * 4, stream_), "memset(barrier)");
+    check(launch_loop(loop_kernel_, g, loop_grid_, stream_), "loop");
+}
+
+// BRISK_HIP_TRACE: workgroup 0's wall clock (100 MHz) after each barrier of the last loop launch.
+size_t Session::trace(unsigned long long* out, size_t n) {
+    if (trace_ == nullptr) return 0;
+    n = std::min(n, kTraceSlots);
+    check(hipMemcpy(out, trace_, n * 8, hipMemcpyDeviceToHost), "hipMemcpy(trace)");
+    return n;
+}
+
+void Session::check_loop_error() {
+    if (loop_kernel_ == nullptr) return;
+    int err = 0;
+    check(hipMemcpy(&err, loop_error_, 4, hipMemcpyDeviceToHost), "hipMemcpy(error)");
+    if (err != 0) {
+        (void)hipMemset(loop_error_, 0, 4);
+        throw Error(BRISK_HIP_EHIP, "hip: token loop barrier timed out (a workgroup was not resident)");
+    }
+}
+
+PickState Session::pick_state() const {
+    return PickState{key_, pos_, seq_, static_cast<int>(max_ctx_) + 1, pos_ + 1};
+}
+
+// Ends a call: the last step's pick, still pending, becomes seq[pos + 1].
+void Session::finish() { check(launch_finalize(pick_state(), stream_), "finalize"); }
 
 hipGraphExec_t Session::capture(bool full) {
     hipGraph_t graph = nullptr;
@@ -321,10 +467,16 @@ void Session::stage(const int32_t* tokens, size_t n) {
 void Session::eval(const int32_t* tokens, size_t n, float* logits) {
     validate(tokens, n);
     stage(tokens, n);
-    for (size_t i = 0; i + 1 < n; ++i) step(false);
-    step(true);
+    if (uses_loop()) {
+        run_loop(position_, n, n - 1, position_ + n);
+    } else {
+        for (size_t i = 0; i + 1 < n; ++i) step(false);
+        step(true);
+        finish();
+    }
     if (logits != nullptr) check(hipMemcpyAsync(logits, logits_, static_cast<size_t>(cfg_.vocab) * 4, hipMemcpyDeviceToHost, stream_), "hipMemcpy(logits)");
     check(hipStreamSynchronize(stream_), "eval sync");
+    check_loop_error();
     position_ += n;
 }
 
@@ -333,11 +485,17 @@ void Session::eval_all(const int32_t* tokens, size_t n, float* logits) {
     validate(tokens, n);
     stage(tokens, n);
     for (size_t i = 0; i < n; ++i) {
-        step(true);
+        if (uses_loop()) {
+            run_loop(position_ + i, 1, 0, position_ + n);
+        } else {
+            step(true);
+            if (i + 1 == n) finish();
+        }
         check(hipMemcpyAsync(logits + i * cfg_.vocab, logits_, static_cast<size_t>(cfg_.vocab) * 4, hipMemcpyDeviceToHost, stream_),
               "hipMemcpy(logits)");
     }
     check(hipStreamSynchronize(stream_), "eval_all sync");
+    check_loop_error();
     position_ += n;
 }
 
@@ -359,9 +517,15 @@ void Session::generate(const int32_t* prompt, size_t n_prompt, size_t n_gen, int
     eval(prompt, n_prompt, nullptr);
     const size_t first = position_;  // seq[first] holds the first pick
     // each further step embeds the previous pick (seq[pos]) and writes the next one
-    for (size_t i = 1; i < n_gen; ++i) step(true);
+    if (uses_loop()) {
+        if (n_gen > 1) run_loop(position_, n_gen - 1, 0, position_ + 1);
+    } else {
+        for (size_t i = 1; i < n_gen; ++i) step(true);
+        finish();
+    }
     check(hipMemcpyAsync(out, seq_ + first, n_gen * 4, hipMemcpyDeviceToHost, stream_), "hipMemcpy(ids)");
     check(hipStreamSynchronize(stream_), "generate sync");
+    check_loop_error();
     position_ += n_gen - 1;
 }
 
@@ -374,9 +538,15 @@ void Session::decode(size_t n, int32_t* out) {
     const int p[2] = {static_cast<int>(position_), static_cast<int>(position_ + 1)};
     check(hipMemcpyAsync(pos_, p, 8, hipMemcpyHostToDevice, stream_), "hipMemcpy(pos)");
     check(hipStreamSynchronize(stream_), "decode stage sync");  // the copy above reads stack memory
-    for (size_t i = 0; i < n; ++i) step(true);
+    if (uses_loop()) {
+        run_loop(position_, n, 0, position_ + 1);
+    } else {
+        for (size_t i = 0; i < n; ++i) step(true);
+        finish();
+    }
     if (out != nullptr) check(hipMemcpyAsync(out, seq_ + first, n * 4, hipMemcpyDeviceToHost, stream_), "hipMemcpy(ids)");
     check(hipStreamSynchronize(stream_), "decode sync");
+    check_loop_error();
     position_ += n;
 }
 

@@ -9,6 +9,7 @@
 
 #include "../../include/brisk_hip.h"
 #include "launch.h"
+#include "loop.h"
 
 namespace bh {
 
@@ -54,6 +55,8 @@ public:
     void set_position(size_t position);
     size_t position() const { return position_; }
     size_t max_context() const { return max_ctx_; }
+    bool uses_loop() const { return loop_kernel_ != nullptr; }
+    size_t trace(unsigned long long* out, size_t n);
     void kv_cache(int layer, int value, void** ptr, size_t* bytes);
     hipStream_t stream() const { return stream_; }
     int device() const { return device_; }
@@ -67,6 +70,11 @@ private:
     void stage(const int32_t* tokens, size_t n);
     int32_t picked();
     void debug_layer(uint32_t l);
+    PickState pick_state() const;
+    void finish();
+    void setup_loop();
+    void run_loop(size_t pos0, size_t n_steps, size_t first_full, size_t fixed);
+    void check_loop_error();
 
     brisk_hip_config cfg_;
     int device_;
@@ -82,13 +90,22 @@ private:
     std::vector<uint16_t*> kcache_, vcache_;
     size_t kv_bytes_ = 0;
     float *h_ = nullptr, *q_ = nullptr, *att_ = nullptr, *act_ = nullptr, *logits_ = nullptr, *rope_ = nullptr;
-    float *part_acc_ = nullptr, *part_ml_ = nullptr, *arg_v_ = nullptr;
-    int* arg_i_ = nullptr;
+    float *part_acc_ = nullptr, *part_ml_ = nullptr, *k_ = nullptr, *v_ = nullptr;
+    unsigned long long* key_ = nullptr;
     unsigned* ticket_ = nullptr;
     int* pos_ = nullptr;
     int* seq_ = nullptr;
     int max_splits_ = 0;
     bool use_graphs_ = true;
+    // persistent loop
+    const void* loop_kernel_ = nullptr;
+    int loop_grid_ = 0;
+    LoopArgs loop_{};
+    LayerDev* layers_dev_ = nullptr;
+    unsigned* loop_bar_ = nullptr;
+    int* loop_error_ = nullptr;
+    unsigned long long* trace_ = nullptr;
+    static constexpr size_t kTraceSlots = 1 << 16;
     bool debug_ = false;
     hipGraphExec_t graph_layers_ = nullptr, graph_full_ = nullptr;
 };

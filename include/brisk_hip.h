@@ -161,6 +161,12 @@ int brisk_hip_session_set_position(brisk_hip_session* s, size_t position);
 /* The session's HIP stream (hipStream_t), for timing with events. */
 void* brisk_hip_session_stream(brisk_hip_session* s);
 
+/* Profiling: with BRISK_HIP_TRACE set when the session was created, the
+ * persistent loop records a 100 MHz wall-clock stamp at the start and after
+ * every grid barrier of its last launch; copies up to n stamps, returns the
+ * count copied (0 when tracing is off). */
+size_t brisk_hip_session_trace(brisk_hip_session* s, unsigned long long* out, size_t n);
+
 #ifdef __cplusplus
 }
 #endif

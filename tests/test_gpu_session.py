@@ -4,6 +4,8 @@ Tiny models of each family the benchmark configs use, seeded: prompt logits
 within 2e-2 (fp32 accumulation-order tolerance of the north star), greedy ids
 identical, eval_all rows, rollback, and the reference's error messages.
 """
+import os
+
 import numpy as np
 import pytest
 
@@ -18,13 +20,20 @@ TOL = 2e-2
 FAMILIES = ["tiny-qwen3", "tiny-llama", "tiny-q8", "tiny-bitnet"]
 
 
-@pytest.fixture(scope="module", params=FAMILIES)
+PATHS = ["loop", "graph"]  # the persistent token loop, and one kernel per phase replayed from hipGraphs
+
+
+@pytest.fixture(scope="module", params=[(f, p) for p in PATHS for f in FAMILIES], ids=lambda fp: f"{fp[0]}-{fp[1]}")
 def pair(request):
     assert torch.cuda.is_available()
-    name = request.param
+    name, path = request.param
     f, cfg, table = model.load(synth.model_path(name))
-    print(f"[session] {name}", flush=True)
-    s = HipSession((f, cfg, table), max_context=256)
+    print(f"[session] {name} ({path})", flush=True)
+    os.environ["BRISK_HIP_PATH"] = path
+    try:
+        s = HipSession((f, cfg, table), max_context=256)
+    finally:
+        del os.environ["BRISK_HIP_PATH"]
     o = pyoracle.Oracle(cfg, table, 256)
     yield name, cfg, s, o
     s.close()
