@@ -257,11 +257,12 @@ __global__ __launch_bounds__(kThreads) void k_attn(AttnArgs g) {
     const bool exact = attn_is_exact(L, g.heads / g.kv_heads);
     if (exact ? split != 0 : split * kSplit >= L) return;
     attn_prologue<PlainIO>(g, s, kv, pos, exact || split == pos / kSplit);
+    const PlainOut o{g.out, g.part_acc, g.part_ml};
     if (exact) {
-        attn_exact<PlainIO>(g, s, kv, L);
+        attn_exact(g, s, kv, L, o);
         return;
     }
-    attn_split_partial<PlainIO>(g, s, kv, split, L);
+    attn_split_partial(g, s, kv, split, L, o);
     // the last split of this key/value head to finish merges them all
     __threadfence();
     __syncthreads();
@@ -270,7 +271,7 @@ __global__ __launch_bounds__(kThreads) void k_attn(AttnArgs g) {
     __syncthreads();
     if (!last) return;
     __threadfence();
-    attn_split_combine<CoherentIO>(g, kv, L);
+    attn_split_combine(g, kv, L, o);
     if (threadIdx.x == 0) g.tickets[kv] = 0u;
 }
 

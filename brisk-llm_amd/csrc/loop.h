@@ -26,23 +26,25 @@ struct LoopArgs {
     float eps, scale;
     const float* rope;       // [ctx][head_dim]
     int ctx;
-    float *h, *q, *k, *v, *att, *act, *logits;
-    float *part_acc, *part_ml;
+    // tagged hand-off words: (tag << 32) | float bits
+    unsigned long long *ht, *qt, *kt, *vt, *attt, *actt, *pacct, *pmlt;
+    unsigned tag_base;
+    float* logits;
     int max_splits;
     unsigned long long* keys;  // [2] pick keys, by step parity
+    unsigned* done;            // [4] phase-H workgroups done, by step parity (monotonic in a launch)
     int* pos_out;              // device position after the launch
     int* seq;                  // token sequence by position
     int seq_len;
     int fixed;                 // seq[0, fixed) are caller tokens
     int pos0, n_steps, first_full;  // steps >= first_full compute the output projection and pick
-    unsigned* bar;             // barrier counters (zeroed before each launch)
     int* error;                // set when a barrier wait expires
     unsigned long long* trace; // optional: workgroup 0's wall clock after each barrier
     int R_qkv[3], tiles_qkv[3];
     int R_o, tiles_o, R_gu, tiles_gu, R_d, tiles_d, R_h, tiles_h;
 };
 
-constexpr size_t kLoopBarrierWords = 64 * 64 + 128;
+int loop_units_per_thread(uint32_t type, bool head);
 
 const void* find_loop_kernel(uint32_t tq, uint32_t tv, uint32_t to, uint32_t tg, uint32_t td, uint32_t th);
 hipError_t launch_loop(const void* kernel, const LoopArgs& g, int grid, hipStream_t s);

@@ -1,129 +1,328 @@
 // The persistent token loop: one launch runs n_steps forward steps.
 //
-// Every workgroup of the grid (one per CU) stays resident for the whole launch
-// and walks the same phase sequence as the one-kernel-per-phase path:
+// Every workgroup of the grid (one per CU) stays resident for the launch and
+// walks the same phases as the one-kernel-per-phase path:
 //
-//   per step:   E  embed: workgroup 0 turns the previous pick (or the caller's
-//                  token) into seq[pos] and dequantises its embedding row into h
 //   per layer:  A  Q/K/V rows of attn_norm(h)                 (src/model.cpp:996-1015)
 //               B  Q/K norms, RoPE, K/V cache write, attention (:1020-1093)
 //               C  O rows of (sub-normed) att, residual add    (:1095-1111)
 //               D  gate/up rows of ffn_norm(h), SiLU / relu^2  (:1111-1143)
 //               F  down rows of (sub-normed) act, residual add (:1144-1162)
-//   full steps: H  output_norm(h) -> output rows -> logits, pick key
+//   full steps: H  output_norm(h) -> output rows -> logits and the greedy pick
 //
-// with a grid barrier after each phase.  The barrier is two-level (groups of
-// 32 workgroups, then the groups) on relaxed device-scope atomics with no cache
-// maintenance: the vectors handed between phases are written and read with
-// system-scope accesses (CoherentIO), which bypass the per-XCD L2s.  Each
-// waiting workgroup spins a bounded number of times; on expiry it raises the
-// error flag, and every workgroup leaves at its next barrier, so a launch
-// always drains.
+// There are no grid barriers.  Every vector one phase hands to the next (q, k,
+// v, att, h, act, attention partials) is stored as 64-bit words, each holding a
+// value and the tag of the (step, layer, phase) that produced it, written with
+// one system-scope store (which goes past the per-XCD L2s).  A consumer polls
+// the words it needs until their tags match, so a hand-off costs one memory
+// round trip.  A buffer is only rewritten after all its readers are done with
+// it: every producer of a phase has consumed, directly or through the phases in
+// between, the outputs of every reader of the previous contents.  The greedy
+// pick is the one all-to-all wait: each workgroup of phase H folds its best
+// (logit, index) into the step's key, then counts itself done; the next step
+// starts from the key once all have.  Waits are bounded: on expiry a workgroup
+// raises the error flag and every waiter leaves, so a launch always drains.
 #include "phases.h"
 #include "loop.h"
 
 namespace bh {
 
-constexpr int kGroup = 32;          // workgroups per first-level barrier counter
-constexpr int kRootSlot = 64 * 64;  // counters sit 256 bytes apart
-constexpr int kReleaseSlot = kRootSlot + 64;
-constexpr unsigned kSpinLimit = 1u << 22;
+constexpr unsigned kSpinLimit = 1u << 24;
 
-// Grid barrier: returns false when the launch is being abandoned.
-__device__ bool grid_barrier(unsigned* bar, unsigned& gen, int* error, unsigned long long* trace = nullptr) {
-    __shared__ int abandon;
-    __builtin_amdgcn_s_waitcnt(0);  // this wave's stores and atomics are performed
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        gen += 1;
-        const unsigned G = gridDim.x, g = blockIdx.x / kGroup, ngroups = (G + kGroup - 1) / kGroup;
-        const unsigned members = G - g * kGroup < kGroup ? G - g * kGroup : kGroup;
-        const unsigned old = atomicAdd(bar + g * 64, 1u);
-        if (old + 1 == gen * members) {
-            // the root add depends on the group add's result, so it is issued after it completed
-            const unsigned o2 = atomicAdd(bar + kRootSlot + (old == ~0u ? 1 : 0), 1u);
-            if (o2 + 1 == gen * ngroups)
-                __hip_atomic_store(bar + kReleaseSlot + (o2 == ~0u ? 1 : 0), gen, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        }
-        unsigned spins = 0;
-        int bad = 0;
-        while (__hip_atomic_load(bar + kReleaseSlot, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < gen) {
-            __builtin_amdgcn_s_sleep(1);
-            if ((++spins & 255) == 0 && __hip_atomic_load(error, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0) {
-                bad = 1;
-                break;
-            }
-            if (spins > kSpinLimit) {
-                atomicExch(error, 1);
-                bad = 1;
-                break;
-            }
-        }
-        abandon = bad;
-        if (trace != nullptr && blockIdx.x == 0) trace[gen] = wall_clock64();
-    }
-    __syncthreads();
-    return abandon == 0;
+__device__ __forceinline__ bool loop_failed(const LoopArgs& g) {
+    return __hip_atomic_load(g.error, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0;
 }
 
-// Shared memory of the loop: the GEMV phases' and the attention phase's layouts overlap.
+// n tagged values of src into dst (LDS), by the whole workgroup; false when
+// the launch is being abandoned.
+__device__ __forceinline__ bool tget_vec(const LoopArgs& g, const unsigned long long* src, unsigned tag, float* dst, int n) {
+    bool fail = false;
+    for (int base = threadIdx.x; base < n && !fail; base += 4 * kThreads) {
+        unsigned long long w[4];
+        bool have[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const int i = base + u * kThreads;
+            have[u] = i >= n;
+            if (!have[u]) w[u] = tload(src + i);
+        }
+        unsigned spins = 0;
+        while (true) {
+            bool all = true;
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                if (!have[u]) {
+                    if (static_cast<unsigned>(w[u] >> 32) == tag) {
+                        dst[base + u * kThreads] = __uint_as_float(static_cast<unsigned>(w[u]));
+                        have[u] = true;
+                    } else {
+                        all = false;
+                    }
+                }
+            }
+            if (all) break;
+            if (++spins > kSpinLimit) {
+                atomicExch(g.error, 1);
+                fail = true;
+                break;
+            }
+            if ((spins & 63) == 0 && loop_failed(g)) {
+                fail = true;
+                break;
+            }
+            __builtin_amdgcn_s_sleep(1);
+#pragma unroll
+            for (int u = 0; u < 4; ++u)
+                if (!have[u]) w[u] = tload(src + base + u * kThreads);
+        }
+    }
+    return !__syncthreads_or(fail);
+}
+
+// One tagged value (a residual row), by one thread.
+__device__ __forceinline__ bool tget_one(const LoopArgs& g, const unsigned long long* src, unsigned tag, float& v) {
+    unsigned spins = 0;
+    unsigned long long w;
+    while (static_cast<unsigned>((w = tload(src)) >> 32) != tag) {
+        if (++spins > kSpinLimit) {
+            atomicExch(g.error, 1);
+            return false;
+        }
+        if ((spins & 63) == 0 && loop_failed(g)) return false;
+        __builtin_amdgcn_s_sleep(1);
+    }
+    v = __uint_as_float(static_cast<unsigned>(w));
+    return true;
+}
+
+// ---------------------------------------------------------------- shared memory
+
 struct GemvLds {
     ActLds a;
     float terms[kTermCap];
     float sums[64];
     float sums2[64];
     double red[4];
+    float x[kMaxCols];  // the phase's input vector
 };
 union LoopLds {
     GemvLds g;
     AttnLds att;
 };
 
-// Rows [row0, row0 + R) of m into out (add: out += ...), activation already in LDS.
-template <uint32_t T>
-__device__ __forceinline__ void tile_out(const Packed& m, uint32_t row0, int R, GemvLds& s, float* out, bool add) {
-    Tile<T> tile;
-    tile.load(m, row0, R);
-    tile.sums(m, s.a, s.terms, s.sums);
-    const uint32_t r = threadIdx.x, row = row0 + r;
-    if (r < static_cast<uint32_t>(R) && row < m.rows) {
-        const float v = add ? CoherentIO::ld(out + row) + s.sums[r] : s.sums[r];
-        CoherentIO::st(out + row, v);
-    }
+__device__ __forceinline__ unsigned tag_of(const LoopArgs& g, int step, int layer, int phase) {
+    return g.tag_base + static_cast<unsigned>((step * g.n_layers + layer) * 8 + phase);
 }
 
+// Quantised activation of the input vector in s.x (rms_norm'd by w when given).
 template <uint32_t T>
-__device__ __forceinline__ void prologue(const Packed& m, const float* x, const float* w, float eps, GemvLds& s) {
+__device__ __forceinline__ void prologue_lds(const Packed& m, const float* w, float eps, GemvLds& s) {
     ActRegs ar;
     const int cols = static_cast<int>(m.cols);
-    act_issue<CoherentIO>(ar, x, w, cols);
-    act_finish<CoherentIO>(ar, x, w, eps, cols, takes_q8_k(T), act_bits(m), s.a, s.red);
+    act_issue<PlainIO>(ar, s.x, w, cols);
+    act_finish<PlainIO>(ar, s.x, w, eps, cols, takes_q8_k(T), act_bits(m), s.a, s.red);
 }
 
-// One matrix (or up to three, same activation) as a phase: tiles t = blockIdx.x, + G, ...
-template <uint32_t T>
-__device__ void gemv_phase(const Packed* ms, float* const* outs, const int* R, const int* tiles, int n, const float* x,
-                           const float* w, float eps, bool add, GemvLds& s) {
-    int total = 0;
-    for (int i = 0; i < n; ++i) total += tiles[i];
-    if (static_cast<int>(blockIdx.x) >= total) return;
-    prologue<T>(ms[0], x, w, eps, s);
-    for (int t = blockIdx.x; t < total; t += gridDim.x) {
-        int i = 0, tt = t;
-        while (i < n - 1 && tt >= tiles[i]) tt -= tiles[i++];
-        tile_out<T>(ms[i], static_cast<uint32_t>(tt) * R[i], R[i], s, outs[i], add);
+// The embedding row of `token` (embedding_row, src/model.cpp:27-70) into s.x.
+__device__ __forceinline__ void embed_to_lds(const LoopArgs& g, int token, GemvLds& s) {
+    for (uint32_t e = threadIdx.x; e < g.embd.cols; e += kThreads) s.x[e] = dequant_elem(g.embd, static_cast<uint32_t>(token), e);
+    __syncthreads();
+}
+
+constexpr int kLoopUnits = 2;  // units per thread in the loop's tiles (the tile plan keeps to it)
+// ... in the output projection's tiles (fewer for the K-quant formats' larger units)
+__host__ __device__ constexpr int head_units(uint32_t type) { return (type == kQ4_K || type == kQ6_K) ? 2 : 4; }
+
+// The tiles t = blockIdx.x, + G, ... of a phase, streamed one ahead: a tile's
+// weights are requested before the phase's input has arrived and before the
+// previous tile is computed, so their latency overlaps the wait and the work.
+// `row_of(t, m, R)` maps a tile to (matrix, first row); `done(t, sums)` is the
+// epilogue.  `ready()` waits for the input and prepares the activation; it runs
+// once, after the first tile's loads are issued.  Returns false when abandoning.
+template <uint32_t T, int M, class RowOf, class Ready, class Done>
+__device__ __forceinline__ bool run_tiles(int total, GemvLds& s, RowOf row_of, Ready ready, Done done) {
+    const int G = static_cast<int>(gridDim.x);
+    int t = static_cast<int>(blockIdx.x);
+    if (t >= total) return true;
+    Tile<T, M> ta, tb;
+    Packed ma, mb;  // by value: a pointer to a kernel-argument member would force a private copy
+    uint32_t ra, rb = 0;
+    int R;
+    row_of(t, ma, ra, R);
+    ta.load(ma, ra, R);
+    if (!ready()) return false;
+    while (true) {
+        if (t + G < total) {
+            row_of(t + G, mb, rb, R);
+            tb.load(mb, rb, R);
+        }
+        ta.sums(ma, s.a, s.terms, s.sums);
+        if (!done(t, ma, ra, s.sums)) return false;
+        t += G;
+        if (t >= total) break;
+        if (t + G < total) {
+            row_of(t + G, ma, ra, R);
+            ta.load(ma, ra, R);
+        }
+        tb.sums(mb, s.a, s.terms, s.sums);
+        if (!done(t, mb, rb, s.sums)) return false;
+        t += G;
+        if (t >= total) break;
     }
+    return true;
 }
 
+// ---------------------------------------------------------------- phases
+
+// A: Q, K, V rows (one format, or Q/K's and then V's).
+template <uint32_t TQ, uint32_t TV>
+__device__ __forceinline__ bool phase_a(const LoopArgs& g, const LayerDev& L, int step, int l, int token, GemvLds& s) {
+    const int nq = g.tiles_qkv[0] + g.tiles_qkv[1];
+    const int total = nq + g.tiles_qkv[2];
+    const unsigned tag = tag_of(g, step, l, 1);
+    auto input = [&]() -> bool {
+        if (l == 0) {
+            embed_to_lds(g, token, s);
+            return true;
+        }
+        return tget_vec(g, g.ht, tag_of(g, step, l - 1, 5), s.x, g.embd_dim);
+    };
+    auto row_of = [&](int t, Packed& m, uint32_t& row0, int& R) {
+        const int i = t < g.tiles_qkv[0] ? 0 : t < nq ? 1 : 2;
+        const int tt = i == 0 ? t : i == 1 ? t - g.tiles_qkv[0] : t - nq;
+        m = i == 0 ? L.q : i == 1 ? L.k : L.v;
+        R = g.R_qkv[i];
+        row0 = static_cast<uint32_t>(tt) * R;
+    };
+    auto done = [&](int t, const Packed& m, uint32_t row0, const float* sums) -> bool {
+        unsigned long long* out = t < g.tiles_qkv[0] ? g.qt : t < nq ? g.kt : g.vt;
+        const int R = t < g.tiles_qkv[0] ? g.R_qkv[0] : t < nq ? g.R_qkv[1] : g.R_qkv[2];
+        const uint32_t r = threadIdx.x;
+        if (r < static_cast<uint32_t>(R) && row0 + r < m.rows) tput(out + row0 + r, sums[r], tag);
+        return true;
+    };
+    if (TQ == TV) {
+        return run_tiles<TQ, kLoopUnits>(total, s, row_of, [&]() -> bool {
+            if (!input()) return false;
+            prologue_lds<TQ>(L.q, L.attn_norm, g.eps, s);
+            return true;
+        }, done);
+    }
+    // Q and K in their format, then V's tiles (same activation family, its own width)
+    if (static_cast<int>(blockIdx.x) >= total) return true;
+    bool have_input = false;
+    if (!run_tiles<TQ, kLoopUnits>(nq, s, row_of, [&]() -> bool {
+            if (!input()) return false;
+            have_input = true;
+            prologue_lds<TQ>(L.q, L.attn_norm, g.eps, s);
+            return true;
+        }, done))
+        return false;
+    if (!have_input && !input()) return false;
+    // V tiles continue round-robin after Q's and K's
+    const int G = static_cast<int>(gridDim.x);
+    const int first = nq % G, me = (static_cast<int>(blockIdx.x) - first + G) % G;
+    if (me >= g.tiles_qkv[2]) return true;
+    prologue_lds<TV>(L.v, L.attn_norm, g.eps, s);
+    for (int t = me; t < g.tiles_qkv[2]; t += G) {
+        const uint32_t row0 = static_cast<uint32_t>(t) * g.R_qkv[2];
+        Tile<TV, kLoopUnits> tile;
+        tile.load(L.v, row0, g.R_qkv[2]);
+        tile.sums(L.v, s.a, s.terms, s.sums);
+        done(nq + t, L.v, row0, s.sums);
+    }
+    return true;
+}
+
+__device__ __forceinline__ AttnArgs attn_args(const LoopArgs& g, const LayerDev& L) {
+    AttnArgs a{};
+    a.qnorm = L.q_norm; a.knorm = L.k_norm; a.rope = g.rope; a.eps = g.eps; a.neox = g.neox;
+    a.kcache = L.kc; a.vcache = L.vc; a.ctx = g.ctx; a.head_dim = g.head_dim; a.heads = g.heads;
+    a.kv_heads = g.kv_heads; a.scale = g.scale; a.max_splits = g.max_splits;
+    a.stamps = g.trace != nullptr ? g.trace + 60000 : nullptr;
+    return a;
+}
+
+// B: attention, exact (one workgroup per key/value head) or split over (kv, split) slots.
+__device__ __forceinline__ bool phase_b(const LoopArgs& g, const LayerDev& L, int step, int l, int pos, AttnLds& s) {
+    const int kvh = g.kv_heads, hpk = g.heads / kvh, hd = g.head_dim, Lc = pos + 1;
+    const unsigned tin = tag_of(g, step, l, 1), tout = tag_of(g, step, l, 2);
+    const AttnArgs a = attn_args(g, L);
+    const TaggedOut o{g.attt, g.pacct, g.pmlt, tout, g.error};
+    if (attn_is_exact(Lc, hpk)) {
+        if (static_cast<int>(blockIdx.x) >= kvh) return true;
+        const int kv = blockIdx.x;
+        attn_stamp(a, kv, 0);
+        if (!tget_vec(g, g.qt + kv * hpk * hd, tin, s.q, hpk * hd)) return false;
+        if (!tget_vec(g, g.kt + kv * hd, tin, s.kcur, hd)) return false;
+        if (!tget_vec(g, g.vt + kv * hd, tin, s.vcur, hd)) return false;
+        attn_finish_prologue<true>(a, s, kv, pos, true);
+        attn_exact(a, s, kv, Lc, o);
+        return true;
+    }
+    const int ns = (Lc + kSplit - 1) / kSplit;
+    for (int slot = blockIdx.x; slot < kvh * ns; slot += gridDim.x) {
+        const int kv = slot % kvh, sp = slot / kvh;
+        const bool writer = sp == pos / kSplit;
+        if (!tget_vec(g, g.qt + kv * hpk * hd, tin, s.q, hpk * hd)) return false;
+        if (writer) {
+            if (!tget_vec(g, g.kt + kv * hd, tin, s.kcur, hd)) return false;
+            if (!tget_vec(g, g.vt + kv * hd, tin, s.vcur, hd)) return false;
+        }
+        attn_finish_prologue<true>(a, s, kv, pos, writer);
+        attn_split_partial(a, s, kv, sp, Lc, o);
+        __syncthreads();
+    }
+    if (static_cast<int>(blockIdx.x) < kvh) {
+        const bool ok = attn_split_combine(a, static_cast<int>(blockIdx.x), Lc, o);
+        return !__syncthreads_or(!ok);
+    }
+    return true;
+}
+
+// C: O rows of att, h += O att.
+template <uint32_t TO>
+__device__ __forceinline__ bool phase_c(const LoopArgs& g, const LayerDev& L, int step, int l, int token, GemvLds& s) {
+    const unsigned tag = tag_of(g, step, l, 3), tprev = tag_of(g, step, l - 1, 5);
+    auto row_of = [&](int t, Packed& m, uint32_t& row0, int& R) {
+        m = L.o;
+        R = g.R_o;
+        row0 = static_cast<uint32_t>(t) * R;
+    };
+    auto ready = [&]() -> bool {
+        if (!tget_vec(g, g.attt, tag_of(g, step, l, 2), s.x, g.heads * g.head_dim)) return false;
+        prologue_lds<TO>(L.o, L.attn_sub, g.eps, s);
+        return true;
+    };
+    auto done = [&](int, const Packed& m, uint32_t row0, const float* sums) -> bool {
+        const uint32_t r = threadIdx.x, row = row0 + r;
+        bool ok = true;
+        if (r < static_cast<uint32_t>(g.R_o) && row < m.rows) {
+            float prev = 0.0f;
+            if (l == 0) prev = dequant_elem(g.embd, static_cast<uint32_t>(token), row);
+            else ok = tget_one(g, g.ht + row, tprev, prev);
+            if (ok) tput(g.ht + row, prev + sums[r], tag);  // h += proj (src/model.cpp:1111)
+        }
+        return !__syncthreads_or(!ok);
+    };
+    return run_tiles<TO, kLoopUnits>(g.tiles_o, s, row_of, ready, done);
+}
+
+// D: gate/up rows of ffn_norm(h), the gated activation.  Tiles 2t and 2t + 1
+// are a gate tile and the up tile of the same rows.
 template <uint32_t TG>
-__device__ void gateup_phase(const LayerDev& L, const LoopArgs& g, GemvLds& s) {
-    if (static_cast<int>(blockIdx.x) >= g.tiles_gu) return;
-    prologue<TG>(L.gate, g.h, L.ffn_norm, g.eps, s);
-    for (int t = blockIdx.x; t < g.tiles_gu; t += gridDim.x) {
-        const uint32_t row0 = static_cast<uint32_t>(t) * g.R_gu;
-        Tile<TG, (Unit<TG>::kMaxPerThread + 1) / 2> tg, tu;
-        tg.load(L.gate, row0, g.R_gu);
-        tu.load(L.up, row0, g.R_gu);
+__device__ __forceinline__ bool phase_d(const LoopArgs& g, const LayerDev& L, int step, int l, GemvLds& s) {
+    if (static_cast<int>(blockIdx.x) >= g.tiles_gu) return true;
+    const unsigned tag = tag_of(g, step, l, 4);
+    const int G = static_cast<int>(gridDim.x);
+    Tile<TG, kLoopUnits> tg, tu;
+    int t = blockIdx.x;
+    uint32_t row0 = static_cast<uint32_t>(t) * g.R_gu;
+    tg.load(L.gate, row0, g.R_gu);
+    tu.load(L.up, row0, g.R_gu);
+    if (!tget_vec(g, g.ht, tag_of(g, step, l, 3), s.x, g.embd_dim)) return false;
+    prologue_lds<TG>(L.gate, L.ffn_norm, g.eps, s);
+    while (true) {
         tg.sums(L.gate, s.a, s.terms, s.sums);
         tu.sums(L.up, s.a, s.terms, s.sums2);
         const uint32_t r = threadIdx.x;
@@ -136,29 +335,79 @@ __device__ void gateup_phase(const LayerDev& L, const LoopArgs& g, GemvLds& s) {
             } else {
                 out = gv / (1.0f + ref_expf(-gv)) * uv;  // src/kernels_f32.cpp:287-289
             }
-            CoherentIO::st(g.act + row0 + r, out);
+            tput(g.actt + row0 + r, out, tag);
         }
+        t += G;
+        if (t >= g.tiles_gu) break;
+        row0 = static_cast<uint32_t>(t) * g.R_gu;
+        tg.load(L.gate, row0, g.R_gu);
+        tu.load(L.up, row0, g.R_gu);
     }
+    return true;
 }
 
-template <uint32_t TH>
-__device__ void head_phase(const LoopArgs& g, unsigned long long* key, GemvLds& s) {
-    if (static_cast<int>(blockIdx.x) >= g.tiles_h) return;
-    prologue<TH>(g.out, g.h, g.out_norm, g.eps, s);
-    unsigned long long best = 0;
-    for (int t = blockIdx.x; t < g.tiles_h; t += gridDim.x) {
-        const uint32_t row0 = static_cast<uint32_t>(t) * g.R_h;
-        Tile<TH> tile;
-        tile.load(g.out, row0, g.R_h);
-        tile.sums(g.out, s.a, s.terms, s.sums);
+__device__ __forceinline__ void stamp(const LoopArgs& g, int i) {
+    if (g.trace != nullptr && blockIdx.x == 0 && threadIdx.x == 0) g.trace[50000 + i] = wall_clock64();
+}
+
+// F: down rows of act, h += down act.
+template <uint32_t TD>
+__device__ __forceinline__ bool phase_f(const LoopArgs& g, const LayerDev& L, int step, int l, GemvLds& s) {
+    const unsigned tag = tag_of(g, step, l, 5), tprev = tag_of(g, step, l, 3);
+    auto row_of = [&](int t, Packed& m, uint32_t& row0, int& R) {
+        m = L.down;
+        R = g.R_d;
+        row0 = static_cast<uint32_t>(t) * R;
+    };
+    auto ready = [&]() -> bool {
+        stamp(g, 0);
+        if (!tget_vec(g, g.actt, tag_of(g, step, l, 4), s.x, g.ff)) return false;
+        stamp(g, 1);
+        prologue_lds<TD>(L.down, L.ffn_sub, g.eps, s);
+        stamp(g, 2);
+        return true;
+    };
+    auto done = [&](int, const Packed& m, uint32_t row0, const float* sums) -> bool {
         const uint32_t r = threadIdx.x, row = row0 + r;
-        if (r < static_cast<uint32_t>(g.R_h) && row < g.out.rows) {
-            const float v = s.sums[r];
+        bool ok = true;
+        if (r < static_cast<uint32_t>(g.R_d) && row < m.rows) {
+            float prev = 0.0f;
+            ok = tget_one(g, g.ht + row, tprev, prev);
+            if (ok) tput(g.ht + row, prev + sums[r], tag);  // h += proj (src/model.cpp:1162)
+        }
+        stamp(g, 3);
+        return !__syncthreads_or(!ok);
+    };
+    return run_tiles<TD, kLoopUnits>(g.tiles_d, s, row_of, ready, done);
+}
+
+// H: output rows of output_norm(h) -> logits; the workgroup's best key folded
+// into keys[step & 1], then the workgroup counted done.
+template <uint32_t TH>
+__device__ __forceinline__ bool phase_h(const LoopArgs& g, int step, GemvLds& s) {
+    if (static_cast<int>(blockIdx.x) >= g.tiles_h) return true;
+    unsigned long long best = 0;
+    auto row_of = [&](int t, Packed& m, uint32_t& row0, int& R) {
+        m = g.out;
+        R = g.R_h;
+        row0 = static_cast<uint32_t>(t) * R;
+    };
+    auto ready = [&]() -> bool {
+        if (!tget_vec(g, g.ht, tag_of(g, step, g.n_layers - 1, 5), s.x, g.embd_dim)) return false;
+        prologue_lds<TH>(g.out, g.out_norm, g.eps, s);
+        return true;
+    };
+    auto done = [&](int, const Packed& m, uint32_t row0, const float* sums) -> bool {
+        const uint32_t r = threadIdx.x, row = row0 + r;
+        if (r < static_cast<uint32_t>(g.R_h) && row < m.rows) {
+            const float v = sums[r];
             g.logits[row] = v;
             const unsigned long long k = pick_key(v, row);
             best = k > best ? k : best;
         }
-    }
+        return true;
+    };
+    if (!run_tiles<TH, head_units(TH)>(g.tiles_h, s, row_of, ready, done)) return false;
     if (threadIdx.x < 64) {
 #pragma unroll
         for (int o = 32; o > 0; o >>= 1) {
@@ -166,140 +415,93 @@ __device__ void head_phase(const LoopArgs& g, unsigned long long* key, GemvLds& 
             best = other > best ? other : best;
         }
         if (threadIdx.x == 0) {
+            unsigned long long* key = g.keys + (step & 1);
             const unsigned long long cur = __hip_atomic_load(key, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            if (best > cur) atomicMax(key, best);
+            unsigned long long old = 0;
+            if (best > cur) old = atomicMax(key, best);
+            // counted done only once the atomicMax has been performed (the address depends on its result)
+            atomicAdd(g.done + (step & 1) + (old == ~0ull ? 2 : 0), 1u);
         }
     }
+    return true;
 }
 
-// Attention with the cache rows written through (system scope), since a row
-// written by one workgroup may be read by another in a later step.
-__device__ void attn_phase(const LayerDev& L, const LoopArgs& g, int pos, AttnLds& s, unsigned& gen, bool& ok) {
-    AttnArgs a{};
-    a.q = g.q; a.k = g.k; a.v = g.v; a.qnorm = L.q_norm; a.knorm = L.k_norm; a.rope = g.rope;
-    a.eps = g.eps; a.neox = g.neox; a.kcache = L.kc; a.vcache = L.vc; a.pos = nullptr;
-    a.ctx = g.ctx; a.head_dim = g.head_dim; a.heads = g.heads; a.kv_heads = g.kv_heads; a.scale = g.scale;
-    a.part_acc = g.part_acc; a.part_ml = g.part_ml; a.max_splits = g.max_splits; a.tickets = nullptr; a.out = g.att;
-    a.stamps = g.trace != nullptr ? g.trace + 60000 + 8 * (pos % 8) : nullptr;
-    const int L_ = pos + 1, hpk = g.heads / g.kv_heads;
-    const int kv = static_cast<int>(blockIdx.x) % g.kv_heads, split = static_cast<int>(blockIdx.x) / g.kv_heads;
-    if (attn_is_exact(L_, hpk)) {
-        if (split == 0) {
-            attn_stamp(a, kv, 0);
-            attn_prologue<CoherentIO, true>(a, s, kv, pos, true);
-            attn_exact<CoherentIO>(a, s, kv, L_);
+// The pick of step `step` (all of its phase H done), by one thread.
+__device__ __forceinline__ bool wait_pick(const LoopArgs& g, int step, int& token) {
+    const int hw = g.tiles_h < static_cast<int>(gridDim.x) ? g.tiles_h : static_cast<int>(gridDim.x);
+    // full steps of this parity so far: first_full .. step, every other one
+    const unsigned want = static_cast<unsigned>(((step - g.first_full) >> 1) + 1) * static_cast<unsigned>(hw);
+    unsigned spins = 0;
+    while (__hip_atomic_load(g.done + (step & 1), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < want) {
+        if (++spins > kSpinLimit) {
+            atomicExch(g.error, 1);
+            return false;
         }
-        return;
+        if ((spins & 63) == 0 && loop_failed(g)) return false;
+        __builtin_amdgcn_s_sleep(1);
     }
-    const int ns = (L_ + kSplit - 1) / kSplit;
-    // every (kv, split) slot of the grid, round-robin over the workgroups
-    for (int slot = blockIdx.x; slot < g.kv_heads * ns; slot += gridDim.x) {
-        const int kvs = slot % g.kv_heads, sp = slot / g.kv_heads;
-        attn_prologue<CoherentIO, true>(a, s, kvs, pos, sp == pos / kSplit);
-        attn_split_partial<CoherentIO>(a, s, kvs, sp, L_);
-        __syncthreads();
-    }
-    ok = grid_barrier(g.bar, gen, g.error, g.trace);
-    if (!ok) return;
-    if (static_cast<int>(blockIdx.x) < g.kv_heads) attn_split_combine<CoherentIO>(a, static_cast<int>(blockIdx.x), L_);
-}
-
-// embedding_row (src/model.cpp:27-70) of `token` into h, by one workgroup.
-__device__ void embed_row(const Packed& m, uint32_t r, float* h) {
-    const uint32_t cols = m.cols;
-    for (uint32_t e = threadIdx.x; e < cols; e += kThreads) CoherentIO::st(h + e, dequant_elem(m, r, e));
+    const unsigned long long k = __hip_atomic_load(g.keys + (step & 1), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    token = static_cast<int>(0xFFFFFFFFu - static_cast<uint32_t>(k & 0xFFFFFFFFu));
+    return true;
 }
 
 template <uint32_t TQ, uint32_t TV, uint32_t TO, uint32_t TG, uint32_t TD, uint32_t TH>
 __global__ __launch_bounds__(kThreads) void k_loop(LoopArgs g) {
     __shared__ LoopLds lds;
-    __shared__ int s_token;
-    unsigned gen = 0;
-    bool ok = true;
-    if (g.trace != nullptr && blockIdx.x == 0 && threadIdx.x == 0) g.trace[0] = wall_clock64();
-    for (int step = 0; step < g.n_steps && ok; ++step) {
+    __shared__ int s_token, s_ok;
+    for (int step = 0; step < g.n_steps; ++step) {
         const int pos = g.pos0 + step;
         const bool full = step >= g.first_full;
-        unsigned long long* key = g.keys + (step & 1);
-        // ---- E
-        if (blockIdx.x == 0) {
-            if (threadIdx.x == 0) {
-                int token = g.seq[pos];
-                if (step > 0 && pos >= g.fixed) {  // the previous step's pick
-                    const unsigned long long k =
-                        __hip_atomic_load(g.keys + ((step - 1) & 1), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                    token = static_cast<int>(0xFFFFFFFFu - static_cast<uint32_t>(k & 0xFFFFFFFFu));
-                    g.seq[pos] = token;
-                }
-                __hip_atomic_store(key, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                s_token = token;
+        // the token of this step: the caller's, or the previous step's pick
+        if (threadIdx.x == 0) {
+            int token = g.seq[pos];
+            bool ok = true;
+            if (step > 0 && pos >= g.fixed) ok = wait_pick(g, step - 1, token);
+            if (ok && blockIdx.x == 0) {
+                if (step > 0 && pos >= g.fixed) g.seq[pos] = token;
+                // re-arm the key this step's phase H uses: its last readers (the
+                // previous step's starts) are all done, since this step's pick
+                // waits on the previous step's phase H, which needed their outputs
+                if (step >= 2) __hip_atomic_store(g.keys + (step & 1), 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                __builtin_amdgcn_s_waitcnt(0);
             }
-            __syncthreads();
-            embed_row(g.embd, static_cast<uint32_t>(s_token), g.h);
+            s_token = token;
+            s_ok = ok;
         }
-        if (!(ok = grid_barrier(g.bar, gen, g.error, g.trace))) break;
-        for (int l = 0; l < g.n_layers && ok; ++l) {
+        __syncthreads();
+        if (!s_ok) return;
+        const int token = s_token;
+        for (int l = 0; l < g.n_layers; ++l) {
             const LayerDev& L = g.layers[l];
-            // ---- A: Q, K, V (same activation; Q and K share a format, V may differ)
-            {
-                if (TQ == TV) {
-                    const Packed ms[3] = {L.q, L.k, L.v};
-                    float* const outs[3] = {g.q, g.k, g.v};
-                    gemv_phase<TQ>(ms, outs, g.R_qkv, g.tiles_qkv, 3, g.h, L.attn_norm, g.eps, false, lds.g);
-                } else {
-                    const Packed ms[2] = {L.q, L.k};
-                    float* const outs[2] = {g.q, g.k};
-                    gemv_phase<TQ>(ms, outs, g.R_qkv, g.tiles_qkv, 2, g.h, L.attn_norm, g.eps, false, lds.g);
-                    __syncthreads();
-                    // V's tiles after Q's and K's, on the next workgroups round-robin
-                    const int first = (g.tiles_qkv[0] + g.tiles_qkv[1]) % static_cast<int>(gridDim.x);
-                    const int me = (static_cast<int>(blockIdx.x) - first + static_cast<int>(gridDim.x)) % static_cast<int>(gridDim.x);
-                    if (me < g.tiles_qkv[2]) {
-                        prologue<TV>(L.v, g.h, L.attn_norm, g.eps, lds.g);
-                        for (int t = me; t < g.tiles_qkv[2]; t += gridDim.x)
-                            tile_out<TV>(L.v, static_cast<uint32_t>(t) * g.R_qkv[2], g.R_qkv[2], lds.g, g.v, false);
-                    }
-                }
-            }
-            if (!(ok = grid_barrier(g.bar, gen, g.error, g.trace))) break;
-            // ---- B
-            attn_phase(L, g, pos, lds.att, gen, ok);
-            if (!ok) break;
-            if (!(ok = grid_barrier(g.bar, gen, g.error, g.trace))) break;
-            // ---- C
-            {
-                const Packed ms[1] = {L.o};
-                float* const outs[1] = {g.h};
-                gemv_phase<TO>(ms, outs, &g.R_o, &g.tiles_o, 1, g.att, L.attn_sub, g.eps, true, lds.g);
-            }
-            if (!(ok = grid_barrier(g.bar, gen, g.error, g.trace))) break;
-            // ---- D
-            gateup_phase<TG>(L, g, lds.g);
-            if (!(ok = grid_barrier(g.bar, gen, g.error, g.trace))) break;
-            // ---- F
-            {
-                const Packed ms[1] = {L.down};
-                float* const outs[1] = {g.h};
-                gemv_phase<TD>(ms, outs, &g.R_d, &g.tiles_d, 1, g.act, L.ffn_sub, g.eps, true, lds.g);
-            }
-            if (!(ok = grid_barrier(g.bar, gen, g.error, g.trace))) break;
+            if (g.trace != nullptr && blockIdx.x == 0 && threadIdx.x == 0) g.trace[1 + (step * g.n_layers + l) * 5] = wall_clock64();
+            if (!phase_a<TQ, TV>(g, L, step, l, token, lds.g)) return;
+            __syncthreads();
+            if (g.trace != nullptr && blockIdx.x == 0 && threadIdx.x == 0) g.trace[2 + (step * g.n_layers + l) * 5] = wall_clock64();
+            if (!phase_b(g, L, step, l, pos, lds.att)) return;
+            __syncthreads();
+            if (g.trace != nullptr && blockIdx.x == 0 && threadIdx.x == 0) g.trace[3 + (step * g.n_layers + l) * 5] = wall_clock64();
+            if (!phase_c<TO>(g, L, step, l, token, lds.g)) return;
+            __syncthreads();
+            if (g.trace != nullptr && blockIdx.x == 0 && threadIdx.x == 0) g.trace[4 + (step * g.n_layers + l) * 5] = wall_clock64();
+            if (!phase_d<TG>(g, L, step, l, lds.g)) return;
+            __syncthreads();
+            if (g.trace != nullptr && blockIdx.x == 0 && threadIdx.x == 0) g.trace[5 + (step * g.n_layers + l) * 5] = wall_clock64();
+            if (!phase_f<TD>(g, L, step, l, lds.g)) return;
+            __syncthreads();
         }
-        if (!ok) break;
-        if (full) {
-            // ---- H
-            head_phase<TH>(g, key, lds.g);
-            if (!(ok = grid_barrier(g.bar, gen, g.error, g.trace))) break;
-        }
+        if (full && !phase_h<TH>(g, step, lds.g)) return;
+        __syncthreads();
     }
-    if (!ok || blockIdx.x != 0 || threadIdx.x != 0) return;
+    if (blockIdx.x != 0 || threadIdx.x != 0) return;
     // the last step's pick becomes seq[end]; the device position follows
     const int end = g.pos0 + g.n_steps;
     if (g.n_steps > g.first_full && end < g.seq_len && end >= g.fixed) {
-        const unsigned long long k =
-            __hip_atomic_load(g.keys + ((g.n_steps - 1) & 1), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        g.seq[end] = static_cast<int>(0xFFFFFFFFu - static_cast<uint32_t>(k & 0xFFFFFFFFu));
+        int token = 0;
+        if (!wait_pick(g, g.n_steps - 1, token)) return;
+        g.seq[end] = token;
     }
     *g.pos_out = end;
+    if (g.trace != nullptr) g.trace[0] = wall_clock64();
 }
 
 // ---------------------------------------------------------------- host side
@@ -320,6 +522,8 @@ const void* find_loop_kernel(uint32_t tq, uint32_t tv, uint32_t to, uint32_t tg,
     if (is(kTQ2_0, kTQ2_0, kTQ2_0, kTQ2_0, kTQ2_0, kQ4_0)) return loop_kernel<kTQ2_0, kTQ2_0, kTQ2_0, kTQ2_0, kTQ2_0, kQ4_0>();
     return nullptr;
 }
+
+int loop_units_per_thread(uint32_t type, bool head) { return head ? head_units(type) : kLoopUnits; }
 
 hipError_t launch_loop(const void* kernel, const LoopArgs& g, int grid, hipStream_t s) {
     void* args[] = {const_cast<LoopArgs*>(&g)};

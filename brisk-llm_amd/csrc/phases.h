@@ -72,9 +72,9 @@ constexpr int kExactMax = 512;     // contexts up to this length take the exact-
 constexpr int kExactScores = 4096; // ... when heads-per-kv x length fits this many LDS scores
 
 struct AttnLds {
-    float q[16 * 128];               // the group's query heads, normed and rotated
-    float kcur[128], vcur[128];      // this token's key and value (fp16-rounded)
-    uint16_t kv[kSplit * 128];       // one staged chunk of keys or values
+    float q[16 * 128];               // the group's query heads (raw, then normed and rotated)
+    float kcur[128], vcur[128];      // this token's key and value (raw, then fp16-rounded)
+    uint16_t kv[2][kSplit * 128];    // two staged chunks of keys or values
     float part[4 * kSplit * 16];     // dot_f32 lane partials: [head][position][lane]
     float sc[kExactScores];          // scores, then weights: [head][position]
     double red[16][4];
@@ -82,10 +82,63 @@ struct AttnLds {
     float ml[16][2];
 };
 
+// ---------------------------------------------------------------- tagged words
+
+// A 64-bit word holding a float and the tag of the step that produced it,
+// written and read with system-scope accesses (past the per-XCD L2s).
+__device__ __forceinline__ void tput(unsigned long long* p, float v, unsigned tag) {
+    __hip_atomic_store(p, (static_cast<unsigned long long>(tag) << 32) | __float_as_uint(v), __ATOMIC_RELAXED,
+                       __HIP_MEMORY_SCOPE_SYSTEM);
+}
+__device__ __forceinline__ unsigned long long tload(const unsigned long long* p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+}
+
+// Where attention puts its results: plain floats (one kernel per phase) ...
+struct PlainOut {
+    float* out;
+    float* part_acc;
+    float* part_ml;
+    __device__ __forceinline__ void att(int i, float v) const { out[i] = v; }
+    __device__ __forceinline__ void pacc(size_t i, float v) const { part_acc[i] = v; }
+    __device__ __forceinline__ void pml(size_t i, float v) const { part_ml[i] = v; }
+    // read after a device-scope fence by the merging workgroup
+    __device__ __forceinline__ bool get_pacc(size_t i, float& v) const { v = CoherentIO::ld(part_acc + i); return true; }
+    __device__ __forceinline__ bool get_pml(size_t i, float& v) const { v = CoherentIO::ld(part_ml + i); return true; }
+};
+
+// ... or tagged words (the persistent loop); reads wait for the tag.
+struct TaggedOut {
+    unsigned long long* out;
+    unsigned long long* part_acc;
+    unsigned long long* part_ml;
+    unsigned tag;
+    int* error;
+    __device__ __forceinline__ void att(int i, float v) const { tput(out + i, v, tag); }
+    __device__ __forceinline__ void pacc(size_t i, float v) const { tput(part_acc + i, v, tag); }
+    __device__ __forceinline__ void pml(size_t i, float v) const { tput(part_ml + i, v, tag); }
+    __device__ bool wait(const unsigned long long* p, float& v) const {
+        unsigned long long w;
+        unsigned spins = 0;
+        while (static_cast<unsigned>((w = tload(p)) >> 32) != tag) {
+            if (++spins > (1u << 24)) {
+                atomicExch(error, 1);
+                return false;
+            }
+            if ((spins & 63) == 0 && __hip_atomic_load(error, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0) return false;
+            __builtin_amdgcn_s_sleep(1);
+        }
+        v = __uint_as_float(static_cast<unsigned>(w));
+        return true;
+    }
+    __device__ __forceinline__ bool get_pacc(size_t i, float& v) const { return wait(part_acc + i, v); }
+    __device__ __forceinline__ bool get_pml(size_t i, float& v) const { return wait(part_ml + i, v); }
+};
+
 // RMS norm over one head (optional weight w) and RoPE, by one wave: the
 // per-head q_norm / k_norm and apply_rope of src/model.cpp:1026-1041, with
 // rms_norm's float squares summed in double (src/model.cpp:87-97).
-__device__ void head_norm_rope(float* v, const float* w, const float* rope, int hd, int neox, float eps) {
+__device__ __forceinline__ void head_norm_rope(float* v, const float* w, const float* rope, int hd, int neox, float eps) {
     const int lane = threadIdx.x & 63;
     if (w != nullptr) {
         double s = 0.0;
@@ -104,10 +157,9 @@ __device__ void head_norm_rope(float* v, const float* w, const float* rope, int 
     }
 }
 
-// This token's query heads of the group, and (for `writer`) its key and value
-// into LDS and the fp16 caches at position pos.
-template <class IO, bool kWriteThrough = false>
-__device__ void attn_prologue(const AttnArgs& g, AttnLds& s, int kv, int pos, bool writer) {
+// This token's raw query heads of the group, and (writer) its raw key and value, into LDS.
+template <class IO>
+__device__ __forceinline__ void attn_load_raw(const AttnArgs& g, AttnLds& s, int kv, bool writer) {
     const int hd = g.head_dim, hpk = g.heads / g.kv_heads, t = threadIdx.x;
     for (int i = t; i < hpk * hd; i += kThreads) s.q[i] = IO::ld(g.q + kv * hpk * hd + i);
     if (writer)
@@ -116,6 +168,15 @@ __device__ void attn_prologue(const AttnArgs& g, AttnLds& s, int kv, int pos, bo
             s.vcur[i] = IO::ld(g.v + kv * hd + i);
         }
     __syncthreads();
+}
+
+// Norms and RoPE of the raw q (and k), then the writer stores K and V at
+// position pos (store_f16, src/kernels_f32.cpp:248-250) and keeps their
+// fp16-rounded values in LDS.  kWriteThrough: system-scope stores, for rows
+// another workgroup reads later in the same launch.
+template <bool kWriteThrough>
+__device__ __forceinline__ void attn_finish_prologue(const AttnArgs& g, AttnLds& s, int kv, int pos, bool writer) {
+    const int hd = g.head_dim, hpk = g.heads / g.kv_heads, t = threadIdx.x;
     const float* rope = g.rope + static_cast<size_t>(pos) * hd;
     const int wave = t >> 6;
     for (int h = wave; h < hpk + (writer ? 1 : 0); h += kThreads / 64) {
@@ -126,11 +187,11 @@ __device__ void attn_prologue(const AttnArgs& g, AttnLds& s, int kv, int pos, bo
     if (writer) {
         uint16_t* kr = g.kcache + (static_cast<size_t>(kv) * g.ctx + pos) * hd;
         uint16_t* vr = g.vcache + (static_cast<size_t>(kv) * g.ctx + pos) * hd;
-        for (int i = 2 * t; i < hd; i += 2 * kThreads) {  // store_f16 (src/kernels_f32.cpp:248-250), in pairs
+        for (int i = 2 * t; i < hd; i += 2 * kThreads) {
             const uint16_t k0 = f2h(s.kcur[i]), k1 = f2h(s.kcur[i + 1]);
             const uint16_t v0 = f2h(s.vcur[i]), v1 = f2h(s.vcur[i + 1]);
             const uint32_t kw = k0 | (static_cast<uint32_t>(k1) << 16), vw = v0 | (static_cast<uint32_t>(v1) << 16);
-            if (kWriteThrough) {  // read by other workgroups later in the same launch
+            if (kWriteThrough) {
                 __hip_atomic_store(reinterpret_cast<uint32_t*>(kr + i), kw, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
                 __hip_atomic_store(reinterpret_cast<uint32_t*>(vr + i), vw, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
             } else {
@@ -140,126 +201,68 @@ __device__ void attn_prologue(const AttnArgs& g, AttnLds& s, int kv, int pos, bo
             s.kcur[i] = h2f(k0); s.kcur[i + 1] = h2f(k1);
             s.vcur[i] = h2f(v0); s.vcur[i + 1] = h2f(v1);
         }
+        // the rows are in memory before anything this workgroup writes later is
+        if (kWriteThrough) __builtin_amdgcn_s_waitcnt(0);
         __syncthreads();
     }
 }
 
-// Chunk c of a cache ([kv][ctx][hd] fp16) through registers: every thread
-// issues its 16-byte loads for the chunk at once.
-struct ChunkRegs {
-    uint4 r[4];
-};
+template <class IO, bool kWriteThrough = false>
+__device__ __forceinline__ void attn_prologue(const AttnArgs& g, AttnLds& s, int kv, int pos, bool writer) {
+    attn_load_raw<IO>(g, s, kv, writer);
+    attn_finish_prologue<kWriteThrough>(g, s, kv, pos, writer);
+}
 
-__device__ __forceinline__ void chunk_load(ChunkRegs& cr, const uint16_t* base, int p0, int n_pos, int hd) {
-    const int per_pos = hd / 8;  // 16-byte pieces per position
-    const int total = n_pos * per_pos;
-#pragma unroll
-    for (int k = 0; k < 4; ++k) {
-        const int i = threadIdx.x + k * kThreads;
-        if (i < total) cr.r[k] = *reinterpret_cast<const uint4*>(base + static_cast<size_t>(p0 + i / per_pos) * hd + (i % per_pos) * 8);
+// Chunk staging: positions [p0, p0 + n_pos) of one head's cache rows
+// ([ctx][hd] fp16, contiguous) straight from global memory into LDS with
+// gfx950's global_load_lds_dwordx4 (16 bytes a lane, lane i of a wave at the
+// wave's LDS base + 16 i).  Completion: s_waitcnt vmcnt(0) + barrier.
+typedef __attribute__((address_space(3))) void* lds_void_ptr;
+typedef __attribute__((address_space(1))) const void* global_cvoid_ptr;
+
+__device__ __forceinline__ void chunk_issue(uint16_t* lds, const uint16_t* base, int p0, int n_pos, int hd) {
+    const int pieces = n_pos * hd / 8;  // 16-byte pieces
+    const uint8_t* src = reinterpret_cast<const uint8_t*>(base + static_cast<size_t>(p0) * hd);
+    uint8_t* dst = reinterpret_cast<uint8_t*>(lds);
+    const int wave_first = static_cast<int>(threadIdx.x) & ~63;
+    for (int k = 0; k * kThreads < pieces; ++k) {
+        const int i = k * kThreads + static_cast<int>(threadIdx.x);
+        if (i < pieces)
+            __builtin_amdgcn_global_load_lds((global_cvoid_ptr)(src + static_cast<size_t>(i) * 16),
+                                             (lds_void_ptr)(dst + (k * kThreads + wave_first) * 16), 16, 0, 0);
     }
 }
 
-__device__ __forceinline__ void chunk_store(const ChunkRegs& cr, uint16_t* lds, int n_pos, int hd) {
-    const int total = n_pos * (hd / 8);
-#pragma unroll
-    for (int k = 0; k < 4; ++k) {
-        const int i = threadIdx.x + k * kThreads;
-        if (i < total) *reinterpret_cast<uint4*>(lds + i * 8) = cr.r[k];
-    }
+__device__ __forceinline__ void attn_stamp(const AttnArgs& g, int kv, int i) {
+    if (g.stamps != nullptr && kv == 0 && threadIdx.x == 0) g.stamps[i] = wall_clock64();
 }
 
-// One chunk of the exact path's scores: stage chunk c's keys (cur) into LDS
-// (the current position's from LDS), start loading chunk c + 1 into nxt, and
-// form dot_f32's 16 lane partials and their in-order sum for every query head.
-__device__ __forceinline__ void score_chunk(const AttnArgs& g, AttnLds& s, const ChunkRegs& cur, ChunkRegs& nxt, int c,
-                                            int nchunks, int L, const uint16_t* kbase) {
-    const int hd = g.head_dim, hpk = g.heads / g.kv_heads, t = threadIdx.x, per = hd / 16, pos = L - 1;
-    const int p0 = c * kSplit;
+// Positions of chunk c (of kSplit) that come from the cache; the current
+// position (pos) comes from LDS.
+__device__ __forceinline__ int chunk_cached(int c, int L) {
+    const int pos = L - 1, p0 = c * kSplit;
     const int n = L - p0 < kSplit ? L - p0 : kSplit;
-    const int ncache = pos - p0 < n ? pos - p0 : n;  // positions of the chunk held in the cache
-    __syncthreads();                                 // the previous chunk is consumed
-    chunk_store(cur, s.kv, ncache, hd);
-    if (ncache < n)
-        for (int i = t; i < hd; i += kThreads) s.kv[ncache * hd + i] = f2h(s.kcur[i]);
-    if (c + 1 < nchunks) {
-        const int q0 = p0 + kSplit;
-        const int nn = pos - q0 < kSplit ? pos - q0 : kSplit;
-        if (nn > 0) chunk_load(nxt, kbase, q0, nn, hd);
-    }
-    __syncthreads();
-    for (int g0 = 0; g0 < hpk; g0 += 4) {
-        const int gn = hpk - g0 < 4 ? hpk - g0 : 4;
-        for (int i = t; i < n * 16; i += kThreads) {
-            const int p = i >> 4, j = i & 15;
-            const uint16_t* kr = s.kv + p * hd;
-            float kf[8];
-#pragma unroll
-            for (int m = 0; m < 8; ++m) kf[m] = m < per ? h2f(kr[j + 16 * m]) : 0.0f;
-            for (int gg = 0; gg < gn; ++gg) {
-                const float* q = s.q + (g0 + gg) * hd;
-                float lane = 0.0f;
-#pragma unroll
-                for (int m = 0; m < 8; ++m)
-                    if (m < per) lane += q[j + 16 * m] * kf[m];
-                s.part[(gg * kSplit + p) * 16 + j] = lane;
-            }
-        }
-        __syncthreads();
-        for (int i = t; i < gn * n; i += kThreads) {
-            const int gg = i / n, p = i % n;
-            const float* pr = s.part + (gg * kSplit + p) * 16;
-            float sum = 0.0f;
-#pragma unroll
-            for (int j = 0; j < 16; ++j) sum += pr[j];
-            s.sc[(g0 + gg) * L + p0 + p] = sum * g.scale;
-        }
-        if (g0 + 4 < hpk) __syncthreads();
-    }
+    return pos - p0 < n ? pos - p0 : n;
 }
 
-// One chunk of the exact path's value sums: stage chunk c's values, start the
-// next chunk's loads, and extend every (head, dim) chain over the chunk's
-// positions in order.
-__device__ __forceinline__ void value_chunk(const AttnArgs& g, AttnLds& s, const ChunkRegs& cur, ChunkRegs& nxt, int c,
-                                            int nchunks, int L, const uint16_t* vbase, float (&acc)[8]) {
-    const int hd = g.head_dim, hpk = g.heads / g.kv_heads, t = threadIdx.x, pos = L - 1, chains = hpk * hd;
-    const int p0 = c * kSplit;
-    const int n = L - p0 < kSplit ? L - p0 : kSplit;
-    const int ncache = pos - p0 < n ? pos - p0 : n;
-    __syncthreads();  // the previous chunk's values (and the weights) are ready / consumed
-    chunk_store(cur, s.kv, ncache, hd);
-    if (ncache < n)
-        for (int i = t; i < hd; i += kThreads) s.kv[ncache * hd + i] = f2h(s.vcur[i]);
+// Waits for chunk c (staged earlier into buffer c & 1), completes it with the
+// current position's row from `cur` (LDS floats, fp16-rounded already) and
+// starts staging chunk c + 1 into the other buffer, which overlaps chunk c's
+// compute.
+__device__ __forceinline__ uint16_t* chunk_advance(AttnLds& s, const uint16_t* base, const float* cur, int c, int nchunks, int L,
+                                                   int hd) {
+    __builtin_amdgcn_s_waitcnt(0);  // this wave's loads of chunk c have landed
+    __syncthreads();                // ... everyone's, and buffer (c + 1) & 1 (chunk c - 1) is consumed
     if (c + 1 < nchunks) {
-        const int q0 = p0 + kSplit;
-        const int nn = pos - q0 < kSplit ? pos - q0 : kSplit;
-        if (nn > 0) chunk_load(nxt, vbase, q0, nn, hd);
+        const int nn = chunk_cached(c + 1, L);
+        if (nn > 0) chunk_issue(s.kv[(c + 1) & 1], base, (c + 1) * kSplit, nn, hd);
     }
+    uint16_t* buf = s.kv[c & 1];
+    const int p0 = c * kSplit, n = L - p0 < kSplit ? L - p0 : kSplit, ncache = chunk_cached(c, L);
+    if (ncache < n)
+        for (int i = threadIdx.x; i < hd; i += kThreads) buf[ncache * hd + i] = f2h(cur[i]);
     __syncthreads();
-#pragma unroll
-    for (int k = 0; k < 8; ++k) {
-        const int ch = t + k * kThreads;
-        if (ch < chains) {
-            const int gq = ch / hd, d = ch % hd;
-            const float* w = s.sc + gq * L + p0;
-            const uint16_t* vv = s.kv + d;
-            float a = acc[k];
-            int p = 0;
-            for (; p + 8 <= n; p += 8) {  // loads first, then the adds in position order
-                float wv[8], vf[8];
-#pragma unroll
-                for (int u = 0; u < 8; ++u) {
-                    wv[u] = w[p + u];
-                    vf[u] = h2f(vv[(p + u) * hd]);
-                }
-#pragma unroll
-                for (int u = 0; u < 8; ++u) a += wv[u] * vf[u];
-            }
-            for (; p < n; ++p) a += w[p] * h2f(vv[p * hd]);
-            acc[k] = a;
-        }
-    }
+    return buf;
 }
 
 // The reference's attention for one token (src/model.cpp:1050-1093 with the
@@ -270,28 +273,56 @@ __device__ __forceinline__ void value_chunk(const AttnArgs& g, AttnLds& s, const
 //   out    = 0 + w_0 v_0 + w_1 v_1 + ... in position order (weighted_sum_f32's axpy).
 // The one grouping that differs is the double sum, whose rounding can reach the
 // float scale only when terms below 2^-20 of the sum lose bits.
-__device__ __forceinline__ void attn_stamp(const AttnArgs& g, int kv, int i) {
-    if (g.stamps != nullptr && kv == 0 && threadIdx.x == 0) g.stamps[i] = wall_clock64();
-}
-
-template <class IO>
-__device__ void attn_exact(const AttnArgs& g, AttnLds& s, int kv, int L) {
+template <class O>
+__device__ __forceinline__ void attn_exact(const AttnArgs& g, AttnLds& s, int kv, int L, const O& o) {
     const int hd = g.head_dim, hpk = g.heads / g.kv_heads, t = threadIdx.x, per = hd / 16;
-    attn_stamp(g, kv, 1);
-    const int pos = L - 1, nchunks = (L + kSplit - 1) / kSplit;
+    const int nchunks = (L + kSplit - 1) / kSplit;
     const uint16_t* kbase = g.kcache + static_cast<size_t>(kv) * g.ctx * hd;
     const uint16_t* vbase = g.vcache + static_cast<size_t>(kv) * g.ctx * hd;
-    ChunkRegs ra, rb;  // two register buffers: chunk c in (c even ? ra : rb), the next one loading meanwhile
-    // ---- scores, chunk by chunk (the current position's key comes from LDS)
+    attn_stamp(g, kv, 1);
+    // ---- scores, chunk by chunk
     {
-        const int n0 = pos < kSplit ? pos : kSplit;
-        chunk_load(ra, kbase, 0, n0, hd);
+        const int n0 = chunk_cached(0, L);
+        if (n0 > 0) chunk_issue(s.kv[0], kbase, 0, n0, hd);
     }
-    for (int c = 0; c < nchunks; c += 2) {
-        score_chunk(g, s, ra, rb, c, nchunks, L, kbase);
-        if (c + 1 < nchunks) score_chunk(g, s, rb, ra, c + 1, nchunks, L, kbase);
+    for (int c = 0; c < nchunks; ++c) {
+        const uint16_t* kvb = chunk_advance(s, kbase, s.kcur, c, nchunks, L, hd);
+        const int p0 = c * kSplit, n = L - p0 < kSplit ? L - p0 : kSplit;
+        for (int g0 = 0; g0 < hpk; g0 += 4) {
+            const int gn = hpk - g0 < 4 ? hpk - g0 : 4;
+            for (int i = t; i < n * 16; i += kThreads) {
+                const int p = i >> 4, j = i & 15;
+                const uint16_t* kr = kvb + p * hd;
+                float kf[8];
+#pragma unroll
+                for (int m = 0; m < 8; ++m) kf[m] = m < per ? h2f(kr[j + 16 * m]) : 0.0f;
+                for (int gg = 0; gg < gn; ++gg) {
+                    const float* q = s.q + (g0 + gg) * hd;
+                    float lane = 0.0f;
+#pragma unroll
+                    for (int m = 0; m < 8; ++m)
+                        if (m < per) lane += q[j + 16 * m] * kf[m];
+                    s.part[(gg * kSplit + p) * 16 + j] = lane;
+                }
+            }
+            __syncthreads();
+            for (int i = t; i < gn * n; i += kThreads) {
+                const int gg = i / n, p = i % n;
+                const float* pr = s.part + (gg * kSplit + p) * 16;
+                float sum = 0.0f;
+#pragma unroll
+                for (int j = 0; j < 16; ++j) sum += pr[j];
+                s.sc[(g0 + gg) * L + p0 + p] = sum * g.scale;
+            }
+            if (g0 + 4 < hpk) __syncthreads();
+        }
     }
+    // the first value chunk streams in while the softmax runs
     __syncthreads();
+    {
+        const int n0 = chunk_cached(0, L);
+        if (n0 > 0) chunk_issue(s.kv[0], vbase, 0, n0, hd);
+    }
     attn_stamp(g, kv, 2);
     // ---- softmax per head
     const int wave = t >> 6, wl = t & 63;
@@ -326,18 +357,37 @@ __device__ void attn_exact(const AttnArgs& g, AttnLds& s, int kv, int L) {
 #pragma unroll
     for (int k = 0; k < 8; ++k) acc[k] = 0.0f;
     const int chains = hpk * hd;
-    {
-        const int n0 = pos < kSplit ? pos : kSplit;
-        chunk_load(ra, vbase, 0, n0, hd);
-    }
-    for (int c = 0; c < nchunks; c += 2) {
-        value_chunk(g, s, ra, rb, c, nchunks, L, vbase, acc);
-        if (c + 1 < nchunks) value_chunk(g, s, rb, ra, c + 1, nchunks, L, vbase, acc);
+    for (int c = 0; c < nchunks; ++c) {
+        const uint16_t* kvb = chunk_advance(s, vbase, s.vcur, c, nchunks, L, hd);
+        const int p0 = c * kSplit, n = L - p0 < kSplit ? L - p0 : kSplit;
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            const int ch = t + k * kThreads;
+            if (ch < chains) {
+                const int gq = ch / hd, d = ch % hd;
+                const float* w = s.sc + gq * L + p0;
+                const uint16_t* vv = kvb + d;
+                float a = acc[k];
+                int p = 0;
+                for (; p + 8 <= n; p += 8) {  // loads first, then the adds in position order
+                    float wv[8], vf[8];
+#pragma unroll
+                    for (int u = 0; u < 8; ++u) {
+                        wv[u] = w[p + u];
+                        vf[u] = h2f(vv[(p + u) * hd]);
+                    }
+#pragma unroll
+                    for (int u = 0; u < 8; ++u) a += wv[u] * vf[u];
+                }
+                for (; p < n; ++p) a += w[p] * h2f(vv[p * hd]);
+                acc[k] = a;
+            }
+        }
     }
 #pragma unroll
     for (int k = 0; k < 8; ++k) {
         const int ch = t + k * kThreads;
-        if (ch < chains) IO::st(g.out + kv * hpk * hd + ch, acc[k]);
+        if (ch < chains) o.att(kv * hpk * hd + ch, acc[k]);
     }
     attn_stamp(g, kv, 4);
 }
@@ -347,20 +397,25 @@ __device__ void attn_exact(const AttnArgs& g, AttnLds& s, int kv, int L) {
 // of exp, exp-weighted value sum); attn_split_combine then merges the splits
 // with the log-sum-exp rescale.  Same mathematics as the reference, different
 // rounding order (tolerance, not bit-exact).
-template <class IO>
-__device__ void attn_split_partial(const AttnArgs& g, AttnLds& s, int kv, int split, int L) {
+template <class O>
+__device__ __forceinline__ void attn_split_partial(const AttnArgs& g, AttnLds& s, int kv, int split, int L, const O& o) {
     const int hd = g.head_dim, hpk = g.heads / g.kv_heads, t = threadIdx.x;
-    const int pos = L - 1, p0 = split * kSplit;
+    const int p0 = split * kSplit;
     const int n = L - p0 < kSplit ? L - p0 : kSplit;
-    const int ncache = pos - p0 < n ? pos - p0 : n;
+    const int ncache = chunk_cached(split, L);
     const uint16_t* kbase = g.kcache + static_cast<size_t>(kv) * g.ctx * hd;
     const uint16_t* vbase = g.vcache + static_cast<size_t>(kv) * g.ctx * hd;
-    ChunkRegs cr;
-    chunk_load(cr, kbase, p0, ncache, hd);
-    chunk_store(cr, s.kv, ncache, hd);
+    __syncthreads();
+    if (ncache > 0) {
+        chunk_issue(s.kv[0], kbase, p0, ncache, hd);
+        chunk_issue(s.kv[1], vbase, p0, ncache, hd);  // values in flight while scoring
+    }
+    __builtin_amdgcn_s_waitcnt(0);
     if (ncache < n)
-        for (int i = t; i < hd; i += kThreads) s.kv[ncache * hd + i] = f2h(s.kcur[i]);
-    chunk_load(cr, vbase, p0, ncache, hd);  // values in flight while scoring
+        for (int i = t; i < hd; i += kThreads) {
+            s.kv[0][ncache * hd + i] = f2h(s.kcur[i]);
+            s.kv[1][ncache * hd + i] = f2h(s.vcur[i]);
+        }
     __syncthreads();
     float* sc = s.sc;  // [head][kSplit]
     for (int i = t; i < hpk * kSplit; i += kThreads) {
@@ -368,7 +423,7 @@ __device__ void attn_split_partial(const AttnArgs& g, AttnLds& s, int kv, int sp
         float acc = -INFINITY;
         if (p < n) {
             acc = 0.0f;
-            const uint16_t* kr = s.kv + p * hd;
+            const uint16_t* kr = s.kv[0] + p * hd;
             const float* q = s.q + gq * hd;
             for (int d = 0; d < hd; ++d) acc += q[d] * h2f(kr[d]);
             acc *= g.scale;
@@ -386,41 +441,44 @@ __device__ void attn_split_partial(const AttnArgs& g, AttnLds& s, int kv, int sp
         if (lane == 0) { s.ml[gq][0] = mx; s.ml[gq][1] = l; }
     }
     __syncthreads();
-    chunk_store(cr, s.kv, ncache, hd);
-    if (ncache < n)
-        for (int i = t; i < hd; i += kThreads) s.kv[ncache * hd + i] = f2h(s.vcur[i]);
-    __syncthreads();
     for (int i = t; i < hpk * hd; i += kThreads) {
         const int gq = i / hd, d = i % hd;
         float acc = 0.0f;
-        for (int p = 0; p < n; ++p) acc += sc[gq * kSplit + p] * h2f(s.kv[p * hd + d]);
+        for (int p = 0; p < n; ++p) acc += sc[gq * kSplit + p] * h2f(s.kv[1][p * hd + d]);
         const size_t slot = static_cast<size_t>(kv * hpk + gq) * g.max_splits + split;
-        IO::st(g.part_acc + slot * hd + d, acc);
+        o.pacc(slot * hd + d, acc);
         if (d == 0) {
-            IO::st(g.part_ml + slot * 2, s.ml[gq][0]);
-            IO::st(g.part_ml + slot * 2 + 1, s.ml[gq][1]);
+            o.pml(slot * 2, s.ml[gq][0]);
+            o.pml(slot * 2 + 1, s.ml[gq][1]);
         }
     }
 }
 
-// Merges the splits of key/value head kv's query heads into out.
-template <class IO>
-__device__ void attn_split_combine(const AttnArgs& g, int kv, int L) {
+// Merges the splits of key/value head kv's query heads into the output.
+template <class O>
+__device__ __forceinline__ bool attn_split_combine(const AttnArgs& g, int kv, int L, const O& o) {
     const int hd = g.head_dim, hpk = g.heads / g.kv_heads, t = threadIdx.x;
     const int ns = (L + kSplit - 1) / kSplit;
     for (int i = t; i < hpk * hd; i += kThreads) {
         const int gq = i / hd, d = i % hd;
         const size_t base = static_cast<size_t>(kv * hpk + gq) * g.max_splits;
-        float M = -INFINITY;
-        for (int s2 = 0; s2 < ns; ++s2) M = fmaxf(M, IO::ld(g.part_ml + (base + s2) * 2));
+        float M = -INFINITY, v = 0.0f;
+        for (int s2 = 0; s2 < ns; ++s2) {
+            if (!o.get_pml((base + s2) * 2, v)) return false;
+            M = fmaxf(M, v);
+        }
         float num = 0.0f, den = 0.0f;
         for (int s2 = 0; s2 < ns; ++s2) {
-            const float f = ref_expf(IO::ld(g.part_ml + (base + s2) * 2) - M);
-            den += IO::ld(g.part_ml + (base + s2) * 2 + 1) * f;
-            num += IO::ld(g.part_acc + (base + s2) * hd + d) * f;
+            float m = 0.0f, l = 0.0f, a = 0.0f;
+            if (!o.get_pml((base + s2) * 2, m) || !o.get_pml((base + s2) * 2 + 1, l) || !o.get_pacc((base + s2) * hd + d, a))
+                return false;
+            const float f = ref_expf(m - M);
+            den += l * f;
+            num += a * f;
         }
-        IO::st(g.out + (kv * hpk + gq) * hd + d, num / den);
+        o.att((kv * hpk + gq) * hd + d, num / den);
     }
+    return true;
 }
 
 __device__ __forceinline__ bool attn_is_exact(int L, int hpk) { return L <= kExactMax && L * hpk <= kExactScores; }

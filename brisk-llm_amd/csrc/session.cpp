@@ -278,13 +278,18 @@ void Session::record_step(bool full) {
 
 // Rows per tile for a phase of the loop: about one tile per workgroup, within
 // the per-thread register budget and the LDS term buffer of every matrix in it.
-static int loop_rows(const std::vector<const Packed*>& ms, int grid, size_t cols_scale = 1) {
+static int loop_rows(const std::vector<const Packed*>& ms, int grid, bool head = false) {
     size_t rows = 0;
     for (const Packed* m : ms) rows += m->rows;
     int R = 1;
     while (R < 64 && static_cast<size_t>(R) * static_cast<size_t>(grid) < rows) R *= 2;
-    for (const Packed* m : ms) R = std::min(R, pick_rows_per_tile(m->type, 1u << 30, m->cols * cols_scale));
-    return std::max(R, 1);
+    for (const Packed* m : ms) {
+        const size_t units = m->cols / block_elems(m->type);
+        while (R > 1 && (static_cast<size_t>(R) * units > static_cast<size_t>(loop_units_per_thread(m->type, head)) * kThreads ||
+                         static_cast<size_t>(R) * (units + 1) > static_cast<size_t>(kTermCap)))
+            R /= 2;
+    }
+    return R;
 }
 
 static int tiles_of(const Packed& m, int R) { return static_cast<int>((m.rows + R - 1) / R); }
@@ -318,8 +323,24 @@ void Session::setup_loop() {
     }
     layers_dev_ = static_cast<LayerDev*>(alloc(ld.size() * sizeof(LayerDev)));
     check(hipMemcpy(layers_dev_, ld.data(), ld.size() * sizeof(LayerDev), hipMemcpyHostToDevice), "hipMemcpy(layers)");
-    loop_bar_ = static_cast<unsigned*>(alloc(kLoopBarrierWords * 4));
+    loop_done_ = static_cast<unsigned*>(alloc(64));
     loop_error_ = static_cast<int*>(alloc(64));
+    {
+        const size_t qd = static_cast<size_t>(cfg_.heads) * cfg_.head_dim, kvd = static_cast<size_t>(cfg_.kv_heads) * cfg_.head_dim;
+        const size_t parts = static_cast<size_t>(cfg_.heads) * max_splits_;
+        tagged_words_ = cfg_.embd + qd + 2 * kvd + qd + cfg_.ff + parts * cfg_.head_dim + parts * 2;
+        unsigned long long* w = static_cast<unsigned long long*>(alloc(tagged_words_ * 8));
+        tagged_ = w;
+        check(hipMemset(w, 0, tagged_words_ * 8), "memset(tagged)");
+        loop_.ht = w; w += cfg_.embd;
+        loop_.qt = w; w += qd;
+        loop_.kt = w; w += kvd;
+        loop_.vt = w; w += kvd;
+        loop_.attt = w; w += qd;
+        loop_.actt = w; w += cfg_.ff;
+        loop_.pacct = w; w += parts * cfg_.head_dim;
+        loop_.pmlt = w;
+    }
     if (std::getenv("BRISK_HIP_TRACE") != nullptr) trace_ = static_cast<unsigned long long*>(alloc(kTraceSlots * 8));
     check(hipMemset(loop_error_, 0, 64), "memset");
 
@@ -340,13 +361,13 @@ void Session::setup_loop() {
     g.scale = 1.0f / std::sqrt(static_cast<float>(cfg_.head_dim));
     g.rope = rope_;
     g.ctx = static_cast<int>(max_ctx_);
-    g.h = h_; g.q = q_; g.k = k_; g.v = v_; g.att = att_; g.act = act_; g.logits = logits_;
-    g.part_acc = part_acc_; g.part_ml = part_ml_; g.max_splits = max_splits_;
+    g.logits = logits_;
+    g.max_splits = max_splits_;
+    g.done = loop_done_;
     g.keys = key_ + 2;
     g.pos_out = pos_;
     g.seq = seq_;
     g.seq_len = static_cast<int>(max_ctx_) + 1;
-    g.bar = loop_bar_;
     g.error = loop_error_;
     const int G = loop_grid_;
     if (L0.q.p.type == L0.v.p.type) {
@@ -362,11 +383,11 @@ void Session::setup_loop() {
     g.tiles_qkv[2] = tiles_of(L0.v.p, g.R_qkv[2]);
     g.R_o = loop_rows({&L0.o.p}, G);
     g.tiles_o = tiles_of(L0.o.p, g.R_o);
-    g.R_gu = loop_rows({&L0.gate.p}, G, 2);
+    g.R_gu = loop_rows({&L0.gate.p}, G);
     g.tiles_gu = tiles_of(L0.gate.p, g.R_gu);
     g.R_d = loop_rows({&L0.down.p}, G);
     g.tiles_d = tiles_of(L0.down.p, g.R_d);
-    g.R_h = loop_rows({&out_->p}, G);
+    g.R_h = loop_rows({&out_->p}, G, true);
     g.tiles_h = tiles_of(out_->p, g.R_h);
 }
 
@@ -379,7 +400,14 @@ void Session::run_loop(size_t pos0, size_t n_steps, size_t first_full, size_t fi
     g.first_full = static_cast<int>(first_full);
     g.fixed = static_cast<int>(fixed);
     g.trace = trace_;
-    check(hipMemsetAsync(loop_bar_, 0, kLoopBarrierWords * 4, stream_), "memset(barrier)");
+    // tags: 255 launch slots of 2^24 step/layer/phase indices; the words are
+    // cleared each time the slots wrap, so a stale word never carries a live tag
+    if (launches_ % 255 == 0) check(hipMemsetAsync(tagged_, 0, tagged_words_ * 8, stream_), "memset(tagged)");
+    g.tag_base = static_cast<unsigned>(launches_ % 255 + 1) << 24;
+    ++launches_;
+    if (n_steps * cfg_.layers * 8 + 8 >= (1u << 24)) throw Error(BRISK_HIP_EINVAL, "hip: too many steps for one loop launch");
+    check(hipMemsetAsync(loop_done_, 0, 64, stream_), "memset(done)");
+    check(hipMemsetAsync(key_ + 2, 0, 16, stream_), "memset(keys)");
     check(launch_loop(loop_kernel_, g, loop_grid_, stream_), "loop");
 }
 

@@ -102,7 +102,10 @@ private:
     int loop_grid_ = 0;
     LoopArgs loop_{};
     LayerDev* layers_dev_ = nullptr;
-    unsigned* loop_bar_ = nullptr;
+    unsigned* loop_done_ = nullptr;
+    unsigned long long* tagged_ = nullptr;
+    size_t tagged_words_ = 0;
+    size_t launches_ = 0;
     int* loop_error_ = nullptr;
     unsigned long long* trace_ = nullptr;
     static constexpr size_t kTraceSlots = 1 << 16;
