@@ -106,16 +106,89 @@ __device__ __forceinline__ int dot4(int a, int b, int c) { return __builtin_amdg
 
 // ---------------------------------------------------------------- reductions
 
-template <typename T>
-__device__ __forceinline__ T wave_sum(T v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+// Cross-lane exchange on DPP (a VALU operand modifier, no LDS round trip).
+// Patterns: swap neighbours (xor 1), swap pairs (xor 2), mirror within 8 lanes,
+// mirror within 16 lanes.  Applied in that order, each step pairs a lane with
+// one holding the reduction of the other half of its group, so after k steps
+// every lane of an aligned 2^k group holds the group's reduction (the same bits
+// in every lane: each pairwise op is commutative).
+constexpr int kDppXor1 = 0xB1, kDppXor2 = 0x4E, kDppHalfMirror = 0x141, kDppMirror = 0x140;
+
+template <int Ctrl, class T>
+__device__ __forceinline__ T dpp(T v) {
+    if constexpr (sizeof(T) == 4) {
+        return __builtin_bit_cast(T, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), Ctrl, 0xF, 0xF, false));
+    } else {
+        static_assert(sizeof(T) == 8, "dpp: 4- or 8-byte values");
+        const unsigned long long u = __builtin_bit_cast(unsigned long long, v);
+        const unsigned lo = static_cast<unsigned>(__builtin_amdgcn_mov_dpp(static_cast<int>(u), Ctrl, 0xF, 0xF, false));
+        const unsigned hi = static_cast<unsigned>(__builtin_amdgcn_mov_dpp(static_cast<int>(u >> 32), Ctrl, 0xF, 0xF, false));
+        return __builtin_bit_cast(T, (static_cast<unsigned long long>(hi) << 32) | lo);
+    }
+}
+
+template <class T>
+__device__ __forceinline__ T readlane(T v, int lane) {
+    if constexpr (sizeof(T) == 4) {
+        return __builtin_bit_cast(T, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), lane));
+    } else {
+        const unsigned long long u = __builtin_bit_cast(unsigned long long, v);
+        const unsigned lo = static_cast<unsigned>(__builtin_amdgcn_readlane(static_cast<int>(u), lane));
+        const unsigned hi = static_cast<unsigned>(__builtin_amdgcn_readlane(static_cast<int>(u >> 32), lane));
+        return __builtin_bit_cast(T, (static_cast<unsigned long long>(hi) << 32) | lo);
+    }
+}
+
+// Reduction over aligned groups of `Lanes` (2, 4, 8 or 16) lanes; every lane of a group gets the result.
+template <int Lanes, class T, class Op>
+__device__ __forceinline__ T group_reduce(T v, Op op) {
+    static_assert(Lanes == 2 || Lanes == 4 || Lanes == 8 || Lanes == 16, "group_reduce: 2..16 lanes");
+    v = op(v, dpp<kDppXor1>(v));
+    if constexpr (Lanes >= 4) v = op(v, dpp<kDppXor2>(v));
+    if constexpr (Lanes >= 8) v = op(v, dpp<kDppHalfMirror>(v));
+    if constexpr (Lanes >= 16) v = op(v, dpp<kDppMirror>(v));
     return v;
 }
+
+// Reduction over the wave, uniform: the four 16-lane rows reduced, then
+// combined as ((row0 op row1) op row2) op row3.
+template <class T, class Op>
+__device__ __forceinline__ T wave_reduce(T v, Op op) {
+    v = group_reduce<16>(v, op);
+    return op(op(op(readlane(v, 0), readlane(v, 16)), readlane(v, 32)), readlane(v, 48));
+}
+
+template <typename T>
+__device__ __forceinline__ T wave_sum(T v) {
+    return wave_reduce(v, [](T a, T b) { return a + b; });
+}
 __device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
-    return v;
+    return wave_reduce(v, [](float a, float b) { return fmaxf(a, b); });
+}
+__device__ __forceinline__ unsigned long long wave_max_u64(unsigned long long v) {
+    return wave_reduce(v, [](unsigned long long a, unsigned long long b) { return a > b ? a : b; });
+}
+
+// The first index of the largest magnitude over a wave, with its signed value.
+struct AbsMax {
+    float amax;
+    int idx;
+    float sel;
+};
+__device__ __forceinline__ AbsMax absmax_op(const AbsMax& a, const AbsMax& b) {
+    return (b.amax > a.amax || (b.amax == a.amax && b.idx < a.idx)) ? b : a;
+}
+template <int Ctrl>
+__device__ __forceinline__ AbsMax dpp_absmax(const AbsMax& v) {
+    return AbsMax{dpp<Ctrl>(v.amax), dpp<Ctrl>(v.idx), dpp<Ctrl>(v.sel)};
+}
+__device__ __forceinline__ AbsMax wave_absmax(AbsMax v) {
+    v = absmax_op(v, dpp_absmax<kDppXor1>(v));
+    v = absmax_op(v, dpp_absmax<kDppXor2>(v));
+    v = absmax_op(v, dpp_absmax<kDppHalfMirror>(v));
+    v = absmax_op(v, dpp_absmax<kDppMirror>(v));
+    auto row = [&](int lane) { return AbsMax{readlane(v.amax, lane), readlane(v.idx, lane), readlane(v.sel, lane)}; };
+    return absmax_op(absmax_op(absmax_op(row(0), row(16)), row(32)), row(48));
 }
 
 // Sum of float squares in double over a workgroup (the accumulator of rms_norm,
@@ -191,9 +264,7 @@ __device__ inline void act_q8_0(const float* x, const float* w, float scale, int
             v[2] = v[2] * scale * wv.z; v[3] = v[3] * scale * wv.w;
         }
         float amax = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
-        amax = fmaxf(amax, __shfl_xor(amax, 1, 64));
-        amax = fmaxf(amax, __shfl_xor(amax, 2, 64));
-        amax = fmaxf(amax, __shfl_xor(amax, 4, 64));
+        amax = group_reduce<8>(amax, [](float a, float b) { return fmaxf(a, b); });
         const float d = amax / 127.0f;
         const float inv = d != 0.0f ? 1.0f / d : 0.0f;
         int q[4], sum = 0;
@@ -202,9 +273,7 @@ __device__ inline void act_q8_0(const float* x, const float* w, float scale, int
             q[i] = static_cast<int>(rintf(v[i] * inv));
             sum += q[i];
         }
-        sum += __shfl_xor(sum, 1, 64);
-        sum += __shfl_xor(sum, 2, 64);
-        sum += __shfl_xor(sum, 4, 64);
+        sum = group_reduce<8>(sum, [](int a, int b) { return a + b; });
         a.xs[base / 4] = (q[0] & 0xFF) | ((q[1] & 0xFF) << 8) | ((q[2] & 0xFF) << 16) | (q[3] << 24);
         if ((threadIdx.x & 7) == 0) {
             a.xd[base / 32] = h2f(f2h(d));
@@ -237,12 +306,9 @@ __device__ inline void act_q8_k(const float* x, const float* w, float scale, int
             if (av > amax) { amax = av; idx = lane * 4 + i; }
         }
         float sel = v[idx - lane * 4 < 0 ? 0 : (idx & 3)];
-#pragma unroll
-        for (int o = 1; o < 64; o <<= 1) {
-            const float oa = __shfl_xor(amax, o, 64);
-            const int oi = __shfl_xor(idx, o, 64);
-            const float os = __shfl_xor(sel, o, 64);
-            if (oa > amax || (oa == amax && oi < idx)) { amax = oa; idx = oi; sel = os; }
+        {
+            const AbsMax m = wave_absmax(AbsMax{amax, idx, sel});
+            amax = m.amax; idx = m.idx; sel = m.sel;
         }
         int q[4];
         float d;
@@ -257,8 +323,7 @@ __device__ inline void act_q8_k(const float* x, const float* w, float scale, int
             for (int i = 0; i < 4; ++i) q[i] = static_cast<int>(fminf(127.0f, rintf(inv * v[i])));
         }
         int s = q[0] + q[1] + q[2] + q[3];
-        s += __shfl_xor(s, 1, 64);
-        s += __shfl_xor(s, 2, 64);
+        s = group_reduce<4>(s, [](int a, int b) { return a + b; });
         a.xs[base / 4] = (q[0] & 0xFF) | ((q[1] & 0xFF) << 8) | ((q[2] & 0xFF) << 16) | (q[3] << 24);
         if ((lane & 3) == 0) a.xsum[blk * 16 + lane / 4] = static_cast<int16_t>(s);  // bsums are int16
         if (lane == 0) a.xd[blk] = d;
@@ -297,9 +362,7 @@ __device__ __forceinline__ void act_issue(ActRegs& r, const float* x, const floa
 // block sum to LDS.
 __device__ __forceinline__ void quant_piece_q8_0(const float v[4], int base, ActLds& a) {
     float amax = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
-    amax = fmaxf(amax, __shfl_xor(amax, 1, 64));
-    amax = fmaxf(amax, __shfl_xor(amax, 2, 64));
-    amax = fmaxf(amax, __shfl_xor(amax, 4, 64));
+    amax = group_reduce<8>(amax, [](float a, float b) { return fmaxf(a, b); });
     const float d = amax / 127.0f;
     const float inv = d != 0.0f ? 1.0f / d : 0.0f;
     int q[4], sum = 0;
@@ -308,9 +371,7 @@ __device__ __forceinline__ void quant_piece_q8_0(const float v[4], int base, Act
         q[i] = static_cast<int>(rintf(v[i] * inv));
         sum += q[i];
     }
-    sum += __shfl_xor(sum, 1, 64);
-    sum += __shfl_xor(sum, 2, 64);
-    sum += __shfl_xor(sum, 4, 64);
+    sum = group_reduce<8>(sum, [](int a, int b) { return a + b; });
     a.xs[base / 4] = (q[0] & 0xFF) | ((q[1] & 0xFF) << 8) | ((q[2] & 0xFF) << 16) | (q[3] << 24);
     if ((threadIdx.x & 7) == 0) {
         a.xd[base / 32] = h2f(f2h(d));
@@ -329,12 +390,9 @@ __device__ __forceinline__ void quant_piece_q8_k(const float v[4], int base, int
         const float av = fabsf(v[i]);
         if (av > amax) { amax = av; idx = lane * 4 + i; sel = v[i]; }
     }
-#pragma unroll
-    for (int o = 1; o < 64; o <<= 1) {
-        const float oa = __shfl_xor(amax, o, 64);
-        const int oi = __shfl_xor(idx, o, 64);
-        const float os = __shfl_xor(sel, o, 64);
-        if (oa > amax || (oa == amax && oi < idx)) { amax = oa; idx = oi; sel = os; }
+    {
+        const AbsMax m = wave_absmax(AbsMax{amax, idx, sel});
+        amax = m.amax; idx = m.idx; sel = m.sel;
     }
     int q[4];
     float d;
@@ -349,8 +407,7 @@ __device__ __forceinline__ void quant_piece_q8_k(const float v[4], int base, int
         for (int i = 0; i < 4; ++i) q[i] = static_cast<int>(fminf(127.0f, rintf(inv * v[i])));
     }
     int s = q[0] + q[1] + q[2] + q[3];
-    s += __shfl_xor(s, 1, 64);
-    s += __shfl_xor(s, 2, 64);
+    s = group_reduce<4>(s, [](int a, int b) { return a + b; });
     a.xs[base / 4] = (q[0] & 0xFF) | ((q[1] & 0xFF) << 8) | ((q[2] & 0xFF) << 16) | (q[3] << 24);
     if ((lane & 3) == 0) a.xsum[base / 16] = static_cast<int16_t>(s);
     if (lane == 0) a.xd[base / 256] = d;
@@ -660,12 +717,14 @@ struct Tile {
         }
     }
 
-    // Terms to LDS (R rows of units + 1 floats), then one lane per row adds them in
-    // block order, as the reference's sequential `sum +=` does: sums[r] is
-    // bit-identical to the reference's dot.  Ends with a barrier.
+    // Terms to LDS (R rows of term_stride(units) floats), then one lane per row
+    // adds them in block order, as the reference's sequential `sum +=` does:
+    // sums[r] is bit-identical to the reference's dot.  The row is read 32
+    // terms at a time before the adds, so the LDS latency is paid once per 32
+    // terms, not once per term.  Ends with a barrier.
     __device__ __forceinline__ void sums(const Packed& m, const ActLds& a, float* terms, float* out) const {
         const uint32_t units = m.cols / Unit<T>::kElems;
-        const uint32_t stride = units + 1;
+        const uint32_t stride = term_stride(units);
         const uint32_t total = static_cast<uint32_t>(R) * units;
 #pragma unroll
         for (int k = 0; k < kMax; ++k) {
@@ -679,7 +738,17 @@ struct Tile {
         if (threadIdx.x < static_cast<uint32_t>(R)) {
             const float* t = terms + threadIdx.x * stride;
             float s = 0.0f;
-            for (uint32_t b = 0; b < units; ++b) s += t[b];
+            uint32_t b = 0;
+            for (; b + 32 <= units; b += 32) {
+                float4 v[8];
+#pragma unroll
+                for (int j = 0; j < 8; ++j) v[j] = *reinterpret_cast<const float4*>(t + b + 4 * j);
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    s += v[j].x; s += v[j].y; s += v[j].z; s += v[j].w;
+                }
+            }
+            for (; b < units; ++b) s += t[b];
             out[threadIdx.x] = s;
         }
         __syncthreads();

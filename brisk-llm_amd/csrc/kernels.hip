@@ -109,7 +109,7 @@ __global__ __launch_bounds__(kThreads) void k_quant_q8_k(const float* __restrict
 template <uint32_t T>
 __global__ __launch_bounds__(kThreads) void k_matvec_q8(Packed m, int R, const uint8_t* __restrict__ xq, float* __restrict__ out, size_t out_stride) {
     __shared__ ActLds a;
-    __shared__ float terms[kTermCap];
+    __shared__ __align__(16) float terms[kTermCap];
     __shared__ float sums[64];
     Tile<T> tile;
     tile.load(m, blockIdx.x * R, R);
@@ -133,7 +133,7 @@ __global__ __launch_bounds__(kThreads) void k_matvec_q8(Packed m, int R, const u
 template <uint32_t T>
 __global__ __launch_bounds__(kThreads) void k_gemv(GemvArgs g) {
     __shared__ ActLds a;
-    __shared__ float terms[kTermCap];
+    __shared__ __align__(16) float terms[kTermCap];
     __shared__ float sums[64];
     __shared__ double red[4];
     int tile_id = blockIdx.x, i = 0;
@@ -159,7 +159,7 @@ __global__ __launch_bounds__(kThreads) void k_gemv(GemvArgs g) {
 template <uint32_t T>
 __global__ __launch_bounds__(kThreads) void k_gateup(GateUpArgs g) {
     __shared__ ActLds a;
-    __shared__ float terms[kTermCap];
+    __shared__ __align__(16) float terms[kTermCap];
     __shared__ float sg[64], su[64];
     __shared__ double red[4];
     const uint32_t row0 = blockIdx.x * g.R;
@@ -195,7 +195,7 @@ __global__ __launch_bounds__(kThreads) void k_gateup(GateUpArgs g) {
 template <uint32_t T>
 __global__ __launch_bounds__(kThreads) void k_head(HeadArgs g) {
     __shared__ ActLds a;
-    __shared__ float terms[kTermCap];
+    __shared__ __align__(16) float terms[kTermCap];
     __shared__ float sums[64];
     __shared__ double red[4];
     const int cols = static_cast<int>(g.m.cols);
@@ -213,11 +213,7 @@ __global__ __launch_bounds__(kThreads) void k_head(HeadArgs g) {
             if (g.logits != nullptr) g.logits[row] = v;
             key = pick_key(v, row);
         }
-#pragma unroll
-        for (int o = 32; o > 0; o >>= 1) {
-            const unsigned long long other = __shfl_xor(key, o, 64);
-            key = other > key ? other : key;
-        }
+        key = wave_max_u64(key);
         if (threadIdx.x == 0) {
             const unsigned long long cur = __hip_atomic_load(g.key, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             if (key > cur) atomicMax(g.key, key);
@@ -338,7 +334,7 @@ int pick_rows_per_tile(uint32_t type, size_t rows, size_t cols) {
     const size_t units = cols / block_elems(type);
     int R = 64;
     while (R > 1 && (static_cast<size_t>(R) * units > static_cast<size_t>(max_per_thread) * kThreads ||
-                     static_cast<size_t>(R) * (units + 1) > static_cast<size_t>(kTermCap)))
+                     static_cast<size_t>(R) * term_stride(static_cast<uint32_t>(units)) > static_cast<size_t>(kTermCap)))
         R /= 2;
     while (R > 1 && (rows + R - 1) / R < static_cast<size_t>(kMinTiles)) R /= 2;
     return R;

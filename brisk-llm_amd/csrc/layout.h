@@ -41,6 +41,10 @@ __host__ __device__ inline bool takes_q8_k(uint32_t type) { return type == kQ4_K
 // Activation width the matrix takes: 7 bits for the x86 ternary layout (src/quant.cpp:144).
 __host__ __device__ inline int act_bits(const Packed& m) { return (m.flags & kFlagLut16) ? 7 : 8; }
 
+// Floats per row of a tile's LDS term buffer: a multiple of 4 (rows are read
+// as float4), padded so that neighbouring rows start in different banks.
+__host__ __device__ inline uint32_t term_stride(uint32_t units) { return ((units + 3) & ~3u) + 4; }
+
 inline size_t align256(size_t n) { return (n + 255) & ~static_cast<size_t>(255); }
 
 // Plane sizes of a packed matrix.

@@ -42,7 +42,12 @@ struct LoopArgs {
     unsigned long long* trace; // optional: workgroup 0's wall clock after each barrier
     int R_qkv[3], tiles_qkv[3];
     int R_o, tiles_o, R_gu, tiles_gu, R_d, tiles_d, R_h, tiles_h;
+    // O and down tiles cover the same rows of h on the same workgroup, which
+    // then keeps its rows of h in LDS for the residual adds
+    int own_h;
 };
+
+constexpr int kOwnRows = 256;  // rows of h one workgroup can keep
 
 int loop_units_per_thread(uint32_t type, bool head);
 

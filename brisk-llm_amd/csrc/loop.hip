@@ -33,50 +33,81 @@ __device__ __forceinline__ bool loop_failed(const LoopArgs& g) {
     return __hip_atomic_load(g.error, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0;
 }
 
-// n tagged values of src into dst (LDS), by the whole workgroup; false when
-// the launch is being abandoned.
-__device__ __forceinline__ bool tget_vec(const LoopArgs& g, const unsigned long long* src, unsigned tag, float* dst, int n) {
+// Tagged values into LDS, by the whole workgroup: up to three (src, dst, n)
+// segments awaited together; false when the launch is being abandoned.
+struct TSeg {
+    const unsigned long long* src;
+    float* dst;
+    int n;
+};
+
+__device__ __forceinline__ bool tget_segs(const LoopArgs& g, unsigned tag, TSeg s0, TSeg s1 = TSeg{nullptr, nullptr, 0},
+                                          TSeg s2 = TSeg{nullptr, nullptr, 0}) {
+    // every word a thread needs (up to kGetPer * kThreads of them) is requested
+    // before any is checked, so a hand-off costs one memory round trip
+    constexpr int kGetPer = 4;
+    const int n01 = s0.n + s1.n, n = n01 + s2.n;
+    auto at = [&](int i, const unsigned long long*& src, float*& dst) {
+        if (i < s0.n) { src = s0.src + i; dst = s0.dst + i; }
+        else if (i < n01) { src = s1.src + (i - s0.n); dst = s1.dst + (i - s0.n); }
+        else { src = s2.src + (i - n01); dst = s2.dst + (i - n01); }
+    };
     bool fail = false;
-    for (int base = threadIdx.x; base < n && !fail; base += 4 * kThreads) {
-        unsigned long long w[4];
-        bool have[4];
+    for (int base = threadIdx.x; base < n && !fail; base += kGetPer * kThreads) {
+        unsigned long long w[kGetPer];
+        const unsigned long long* src[kGetPer];
+        float* dst[kGetPer];
+        bool have[kGetPer];
 #pragma unroll
-        for (int u = 0; u < 4; ++u) {
+        for (int u = 0; u < kGetPer; ++u) {
             const int i = base + u * kThreads;
             have[u] = i >= n;
-            if (!have[u]) w[u] = tload(src + i);
+            at(i < n ? i : n - 1, src[u], dst[u]);  // unconditional loads (no branches between them)
+            w[u] = tload(src[u]);
         }
         unsigned spins = 0;
         while (true) {
             bool all = true;
+            const unsigned long long* first = nullptr;  // the first word still missing
 #pragma unroll
-            for (int u = 0; u < 4; ++u) {
+            for (int u = 0; u < kGetPer; ++u) {
                 if (!have[u]) {
                     if (static_cast<unsigned>(w[u] >> 32) == tag) {
-                        dst[base + u * kThreads] = __uint_as_float(static_cast<unsigned>(w[u]));
+                        *dst[u] = __uint_as_float(static_cast<unsigned>(w[u]));
                         have[u] = true;
                     } else {
+                        if (all) first = src[u];
                         all = false;
                     }
                 }
             }
             if (all) break;
-            if (++spins > kSpinLimit) {
-                atomicExch(g.error, 1);
-                fail = true;
-                break;
+            // poll only that word (one load per round keeps the polling traffic
+            // low while producers are still running), then fetch the rest again
+            unsigned long long f;
+            while (static_cast<unsigned>((f = tload(first)) >> 32) != tag) {
+                if (++spins > kSpinLimit) {
+                    atomicExch(g.error, 1);
+                    fail = true;
+                    break;
+                }
+                if ((spins & 63) == 0 && loop_failed(g)) {
+                    fail = true;
+                    break;
+                }
+                __builtin_amdgcn_s_sleep(1);
             }
-            if ((spins & 63) == 0 && loop_failed(g)) {
-                fail = true;
-                break;
-            }
-            __builtin_amdgcn_s_sleep(1);
+            if (fail) break;
 #pragma unroll
-            for (int u = 0; u < 4; ++u)
-                if (!have[u]) w[u] = tload(src + base + u * kThreads);
+            for (int u = 0; u < kGetPer; ++u)
+                if (!have[u]) w[u] = tload(src[u]);
         }
     }
     return !__syncthreads_or(fail);
+}
+
+__device__ __forceinline__ bool tget_vec(const LoopArgs& g, const unsigned long long* src, unsigned tag, float* dst, int n) {
+    return tget_segs(g, tag, TSeg{src, dst, n});
 }
 
 // One tagged value (a residual row), by one thread.
@@ -99,7 +130,7 @@ __device__ __forceinline__ bool tget_one(const LoopArgs& g, const unsigned long 
 
 struct GemvLds {
     ActLds a;
-    float terms[kTermCap];
+    alignas(16) float terms[kTermCap];
     float sums[64];
     float sums2[64];
     double red[4];
@@ -253,22 +284,24 @@ __device__ __forceinline__ bool phase_b(const LoopArgs& g, const LayerDev& L, in
         if (static_cast<int>(blockIdx.x) >= kvh) return true;
         const int kv = blockIdx.x;
         attn_stamp(a, kv, 0);
-        if (!tget_vec(g, g.qt + kv * hpk * hd, tin, s.q, hpk * hd)) return false;
-        if (!tget_vec(g, g.kt + kv * hd, tin, s.kcur, hd)) return false;
-        if (!tget_vec(g, g.vt + kv * hd, tin, s.vcur, hd)) return false;
-        attn_finish_prologue<true>(a, s, kv, pos, true);
-        attn_exact(a, s, kv, Lc, o);
+        attn_issue_k0(a, s, kv, Lc);  // the cached keys stream in while q/k/v are awaited
+        if (!tget_segs(g, tin, TSeg{g.qt + kv * hpk * hd, s.q, hpk * hd}, TSeg{g.kt + kv * hd, s.kcur, hd},
+                       TSeg{g.vt + kv * hd, s.vcur, hd})) {
+            __builtin_amdgcn_s_waitcnt(0);
+            return false;
+        }
+        attn_finish_prologue<true>(a, s, kv, pos, true, false);
+        attn_exact(a, s, kv, Lc, o, true, true);
         return true;
     }
     const int ns = (Lc + kSplit - 1) / kSplit;
     for (int slot = blockIdx.x; slot < kvh * ns; slot += gridDim.x) {
         const int kv = slot % kvh, sp = slot / kvh;
         const bool writer = sp == pos / kSplit;
-        if (!tget_vec(g, g.qt + kv * hpk * hd, tin, s.q, hpk * hd)) return false;
-        if (writer) {
-            if (!tget_vec(g, g.kt + kv * hd, tin, s.kcur, hd)) return false;
-            if (!tget_vec(g, g.vt + kv * hd, tin, s.vcur, hd)) return false;
-        }
+        if (!tget_segs(g, tin, TSeg{g.qt + kv * hpk * hd, s.q, hpk * hd},
+                       writer ? TSeg{g.kt + kv * hd, s.kcur, hd} : TSeg{nullptr, nullptr, 0},
+                       writer ? TSeg{g.vt + kv * hd, s.vcur, hd} : TSeg{nullptr, nullptr, 0}))
+            return false;
         attn_finish_prologue<true>(a, s, kv, pos, writer);
         attn_split_partial(a, s, kv, sp, Lc, o);
         __syncthreads();
@@ -280,10 +313,14 @@ __device__ __forceinline__ bool phase_b(const LoopArgs& g, const LayerDev& L, in
     return true;
 }
 
-// C: O rows of att, h += O att.
+// C: O rows of att, h += O att.  With own_h the residual rows come from the
+// workgroup's own copy (it produced them in the previous layer's phase F, or
+// from the embedding at layer 0).
 template <uint32_t TO>
-__device__ __forceinline__ bool phase_c(const LoopArgs& g, const LayerDev& L, int step, int l, int token, GemvLds& s) {
+__device__ __forceinline__ bool phase_c(const LoopArgs& g, const LayerDev& L, int step, int l, int token, GemvLds& s,
+                                        float* hown) {
     const unsigned tag = tag_of(g, step, l, 3), tprev = tag_of(g, step, l - 1, 5);
+    const int G = static_cast<int>(gridDim.x);
     auto row_of = [&](int t, Packed& m, uint32_t& row0, int& R) {
         m = L.o;
         R = g.R_o;
@@ -294,16 +331,20 @@ __device__ __forceinline__ bool phase_c(const LoopArgs& g, const LayerDev& L, in
         prologue_lds<TO>(L.o, L.attn_sub, g.eps, s);
         return true;
     };
-    auto done = [&](int, const Packed& m, uint32_t row0, const float* sums) -> bool {
+    auto done = [&](int t, const Packed& m, uint32_t row0, const float* sums) -> bool {
         const uint32_t r = threadIdx.x, row = row0 + r;
         bool ok = true;
         if (r < static_cast<uint32_t>(g.R_o) && row < m.rows) {
             float prev = 0.0f;
-            if (l == 0) prev = dequant_elem(g.embd, static_cast<uint32_t>(token), row);
+            const int slot = (t - static_cast<int>(blockIdx.x)) / G * g.R_o + static_cast<int>(r);
+            if (g.own_h) prev = hown[slot];
+            else if (l == 0) prev = dequant_elem(g.embd, static_cast<uint32_t>(token), row);
             else ok = tget_one(g, g.ht + row, tprev, prev);
-            if (ok) tput(g.ht + row, prev + sums[r], tag);  // h += proj (src/model.cpp:1111)
+            const float h = prev + sums[r];  // h += proj (src/model.cpp:1111)
+            if (ok) tput(g.ht + row, h, tag);
+            if (g.own_h) hown[slot] = h;
         }
-        return !__syncthreads_or(!ok);
+        return g.own_h || !__syncthreads_or(!ok);
     };
     return run_tiles<TO, kLoopUnits>(g.tiles_o, s, row_of, ready, done);
 }
@@ -350,10 +391,11 @@ __device__ __forceinline__ void stamp(const LoopArgs& g, int i) {
     if (g.trace != nullptr && blockIdx.x == 0 && threadIdx.x == 0) g.trace[50000 + i] = wall_clock64();
 }
 
-// F: down rows of act, h += down act.
+// F: down rows of act, h += down act (residual rows from the own copy with own_h).
 template <uint32_t TD>
-__device__ __forceinline__ bool phase_f(const LoopArgs& g, const LayerDev& L, int step, int l, GemvLds& s) {
+__device__ __forceinline__ bool phase_f(const LoopArgs& g, const LayerDev& L, int step, int l, GemvLds& s, float* hown) {
     const unsigned tag = tag_of(g, step, l, 5), tprev = tag_of(g, step, l, 3);
+    const int G = static_cast<int>(gridDim.x);
     auto row_of = [&](int t, Packed& m, uint32_t& row0, int& R) {
         m = L.down;
         R = g.R_d;
@@ -367,16 +409,20 @@ __device__ __forceinline__ bool phase_f(const LoopArgs& g, const LayerDev& L, in
         stamp(g, 2);
         return true;
     };
-    auto done = [&](int, const Packed& m, uint32_t row0, const float* sums) -> bool {
+    auto done = [&](int t, const Packed& m, uint32_t row0, const float* sums) -> bool {
         const uint32_t r = threadIdx.x, row = row0 + r;
         bool ok = true;
         if (r < static_cast<uint32_t>(g.R_d) && row < m.rows) {
             float prev = 0.0f;
-            ok = tget_one(g, g.ht + row, tprev, prev);
-            if (ok) tput(g.ht + row, prev + sums[r], tag);  // h += proj (src/model.cpp:1162)
+            const int slot = (t - static_cast<int>(blockIdx.x)) / G * g.R_d + static_cast<int>(r);
+            if (g.own_h) prev = hown[slot];
+            else ok = tget_one(g, g.ht + row, tprev, prev);
+            const float h = prev + sums[r];  // h += proj (src/model.cpp:1162)
+            if (ok) tput(g.ht + row, h, tag);
+            if (g.own_h) hown[slot] = h;
         }
         stamp(g, 3);
-        return !__syncthreads_or(!ok);
+        return g.own_h || !__syncthreads_or(!ok);
     };
     return run_tiles<TD, kLoopUnits>(g.tiles_d, s, row_of, ready, done);
 }
@@ -409,11 +455,7 @@ __device__ __forceinline__ bool phase_h(const LoopArgs& g, int step, GemvLds& s)
     };
     if (!run_tiles<TH, head_units(TH)>(g.tiles_h, s, row_of, ready, done)) return false;
     if (threadIdx.x < 64) {
-#pragma unroll
-        for (int o = 32; o > 0; o >>= 1) {
-            const unsigned long long other = __shfl_xor(best, o, 64);
-            best = other > best ? other : best;
-        }
+        best = wave_max_u64(best);
         if (threadIdx.x == 0) {
             unsigned long long* key = g.keys + (step & 1);
             const unsigned long long cur = __hip_atomic_load(key, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -448,6 +490,7 @@ __device__ __forceinline__ bool wait_pick(const LoopArgs& g, int step, int& toke
 template <uint32_t TQ, uint32_t TV, uint32_t TO, uint32_t TG, uint32_t TD, uint32_t TH>
 __global__ __launch_bounds__(kThreads) void k_loop(LoopArgs g) {
     __shared__ LoopLds lds;
+    __shared__ float hown[kOwnRows];
     __shared__ int s_token, s_ok;
     for (int step = 0; step < g.n_steps; ++step) {
         const int pos = g.pos0 + step;
@@ -471,6 +514,13 @@ __global__ __launch_bounds__(kThreads) void k_loop(LoopArgs g) {
         __syncthreads();
         if (!s_ok) return;
         const int token = s_token;
+        if (g.own_h) {  // this workgroup's rows of h: the embedding row (embedding_row, src/model.cpp:27-70)
+            for (int t = blockIdx.x, k = 0; t < g.tiles_o; t += gridDim.x, ++k)
+                for (int r = threadIdx.x; r < g.R_o; r += kThreads) {
+                    const uint32_t row = static_cast<uint32_t>(t * g.R_o + r);
+                    if (row < g.embd.cols) hown[k * g.R_o + r] = dequant_elem(g.embd, static_cast<uint32_t>(token), row);
+                }
+        }
         for (int l = 0; l < g.n_layers; ++l) {
             const LayerDev& L = g.layers[l];
             if (g.trace != nullptr && blockIdx.x == 0 && threadIdx.x == 0) g.trace[1 + (step * g.n_layers + l) * 5] = wall_clock64();
@@ -480,13 +530,13 @@ __global__ __launch_bounds__(kThreads) void k_loop(LoopArgs g) {
             if (!phase_b(g, L, step, l, pos, lds.att)) return;
             __syncthreads();
             if (g.trace != nullptr && blockIdx.x == 0 && threadIdx.x == 0) g.trace[3 + (step * g.n_layers + l) * 5] = wall_clock64();
-            if (!phase_c<TO>(g, L, step, l, token, lds.g)) return;
+            if (!phase_c<TO>(g, L, step, l, token, lds.g, hown)) return;
             __syncthreads();
             if (g.trace != nullptr && blockIdx.x == 0 && threadIdx.x == 0) g.trace[4 + (step * g.n_layers + l) * 5] = wall_clock64();
             if (!phase_d<TG>(g, L, step, l, lds.g)) return;
             __syncthreads();
             if (g.trace != nullptr && blockIdx.x == 0 && threadIdx.x == 0) g.trace[5 + (step * g.n_layers + l) * 5] = wall_clock64();
-            if (!phase_f<TD>(g, L, step, l, lds.g)) return;
+            if (!phase_f<TD>(g, L, step, l, lds.g, hown)) return;
             __syncthreads();
         }
         if (full && !phase_h<TH>(g, step, lds.g)) return;

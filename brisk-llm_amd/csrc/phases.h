@@ -75,7 +75,6 @@ struct AttnLds {
     float q[16 * 128];               // the group's query heads (raw, then normed and rotated)
     float kcur[128], vcur[128];      // this token's key and value (raw, then fp16-rounded)
     uint16_t kv[2][kSplit * 128];    // two staged chunks of keys or values
-    float part[4 * kSplit * 16];     // dot_f32 lane partials: [head][position][lane]
     float sc[kExactScores];          // scores, then weights: [head][position]
     double red[16][4];
     float mx[16];
@@ -170,12 +169,34 @@ __device__ __forceinline__ void attn_load_raw(const AttnArgs& g, AttnLds& s, int
     __syncthreads();
 }
 
-// Norms and RoPE of the raw q (and k), then the writer stores K and V at
-// position pos (store_f16, src/kernels_f32.cpp:248-250) and keeps their
-// fp16-rounded values in LDS.  kWriteThrough: system-scope stores, for rows
-// another workgroup reads later in the same launch.
+// The writer's K and V rows at position pos (store_f16, src/kernels_f32.cpp:248-250),
+// from the fp16-rounded values in LDS.  kWriteThrough: system-scope stores, for
+// rows another workgroup reads later in the same launch; the caller orders them
+// before its later writes (an s_waitcnt before those).
 template <bool kWriteThrough>
-__device__ __forceinline__ void attn_finish_prologue(const AttnArgs& g, AttnLds& s, int kv, int pos, bool writer) {
+__device__ __forceinline__ void attn_store_rows(const AttnArgs& g, const AttnLds& s, int kv, int pos) {
+    const int hd = g.head_dim, t = threadIdx.x;
+    uint16_t* kr = g.kcache + (static_cast<size_t>(kv) * g.ctx + pos) * hd;
+    uint16_t* vr = g.vcache + (static_cast<size_t>(kv) * g.ctx + pos) * hd;
+    for (int i = 2 * t; i < hd; i += 2 * kThreads) {
+        const uint32_t kw = f2h(s.kcur[i]) | (static_cast<uint32_t>(f2h(s.kcur[i + 1])) << 16);
+        const uint32_t vw = f2h(s.vcur[i]) | (static_cast<uint32_t>(f2h(s.vcur[i + 1])) << 16);
+        if (kWriteThrough) {
+            __hip_atomic_store(reinterpret_cast<uint32_t*>(kr + i), kw, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+            __hip_atomic_store(reinterpret_cast<uint32_t*>(vr + i), vw, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+        } else {
+            *reinterpret_cast<uint32_t*>(kr + i) = kw;
+            *reinterpret_cast<uint32_t*>(vr + i) = vw;
+        }
+    }
+}
+
+// Norms and RoPE of the raw q (and k), and the fp16 rounding of the writer's
+// k and v in LDS; with `store`, the writer also stores the rows (waiting for
+// them when kWriteThrough).  Ends with a barrier.
+template <bool kWriteThrough>
+__device__ __forceinline__ void attn_finish_prologue(const AttnArgs& g, AttnLds& s, int kv, int pos, bool writer,
+                                                     bool store = true) {
     const int hd = g.head_dim, hpk = g.heads / g.kv_heads, t = threadIdx.x;
     const float* rope = g.rope + static_cast<size_t>(pos) * hd;
     const int wave = t >> 6;
@@ -185,25 +206,16 @@ __device__ __forceinline__ void attn_finish_prologue(const AttnArgs& g, AttnLds&
     }
     __syncthreads();
     if (writer) {
-        uint16_t* kr = g.kcache + (static_cast<size_t>(kv) * g.ctx + pos) * hd;
-        uint16_t* vr = g.vcache + (static_cast<size_t>(kv) * g.ctx + pos) * hd;
-        for (int i = 2 * t; i < hd; i += 2 * kThreads) {
-            const uint16_t k0 = f2h(s.kcur[i]), k1 = f2h(s.kcur[i + 1]);
-            const uint16_t v0 = f2h(s.vcur[i]), v1 = f2h(s.vcur[i + 1]);
-            const uint32_t kw = k0 | (static_cast<uint32_t>(k1) << 16), vw = v0 | (static_cast<uint32_t>(v1) << 16);
-            if (kWriteThrough) {
-                __hip_atomic_store(reinterpret_cast<uint32_t*>(kr + i), kw, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
-                __hip_atomic_store(reinterpret_cast<uint32_t*>(vr + i), vw, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
-            } else {
-                *reinterpret_cast<uint32_t*>(kr + i) = kw;
-                *reinterpret_cast<uint32_t*>(vr + i) = vw;
-            }
-            s.kcur[i] = h2f(k0); s.kcur[i + 1] = h2f(k1);
-            s.vcur[i] = h2f(v0); s.vcur[i + 1] = h2f(v1);
+        for (int i = t; i < hd; i += kThreads) {
+            s.kcur[i] = h2f(f2h(s.kcur[i]));
+            s.vcur[i] = h2f(f2h(s.vcur[i]));
         }
-        // the rows are in memory before anything this workgroup writes later is
-        if (kWriteThrough) __builtin_amdgcn_s_waitcnt(0);
         __syncthreads();
+        if (store) {
+            attn_store_rows<kWriteThrough>(g, s, kv, pos);
+            // the rows are in memory before anything this workgroup writes later is
+            if (kWriteThrough) __builtin_amdgcn_s_waitcnt(0);
+        }
     }
 }
 
@@ -265,6 +277,47 @@ __device__ __forceinline__ uint16_t* chunk_advance(AttnLds& s, const uint16_t* b
     return buf;
 }
 
+// Starts staging the first key chunk of kv head `kv` (positions before the
+// current one only: they are in the cache already), e.g. before the current
+// token's q/k/v have arrived.
+__device__ __forceinline__ void attn_issue_k0(const AttnArgs& g, AttnLds& s, int kv, int L) {
+    const int n0 = chunk_cached(0, L);
+    if (n0 > 0) chunk_issue(s.kv[0], g.kcache + static_cast<size_t>(kv) * g.ctx * g.head_dim, 0, n0, g.head_dim);
+}
+
+// dot_f32's final reduction over 16 lanes, 0 + l0 + l1 + ... + l15 in that
+// order, as a shift-and-add chain through the 16-lane row on DPP: with
+// v(0) = 0 + l and v(k) = v(k-1) shifted down one lane (0 into lane 0) + l,
+// lane j of v(k) is ((0 + l(j-k)) + ...) + l(j), so lane 15 of v(15) is the
+// ordered sum.  No selects; two independent chains interleave.
+constexpr int kDppRowShr1 = 0x111;
+__device__ __forceinline__ void ordered_sum16x2(float& a, float& b) {
+    const float la = a, lb = b;
+    a = 0.0f + la;
+    b = 0.0f + lb;
+#pragma unroll
+    for (int k = 1; k < 16; ++k) {
+        a = __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, a), kDppRowShr1, 0xF, 0xF, false)) + la;
+        b = __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, b), kDppRowShr1, 0xF, 0xF, false)) + lb;
+    }
+}
+
+// dot_f32's lane partial j over a head of 16 * PER values (q, k offset by j):
+// 0 + q[0] k[0] + q[16] k[16] + ..., the loads issued before the adds.
+template <int PER>
+__device__ __forceinline__ float lane_partial(const float* q, const uint16_t* k) {
+    float qv[PER], kf[PER];
+#pragma unroll
+    for (int m = 0; m < PER; ++m) {
+        qv[m] = q[16 * m];
+        kf[m] = h2f(k[16 * m]);
+    }
+    float lane = 0.0f;
+#pragma unroll
+    for (int m = 0; m < PER; ++m) lane += qv[m] * kf[m];
+    return lane;
+}
+
 // The reference's attention for one token (src/model.cpp:1050-1093 with the
 // portable kernels of src/kernels_f32.cpp:229-284), operation for operation:
 //   score_p = dot_f32(q, k_p) * scale, dot_f32 being 16 lane partials over
@@ -273,83 +326,73 @@ __device__ __forceinline__ uint16_t* chunk_advance(AttnLds& s, const uint16_t* b
 //   out    = 0 + w_0 v_0 + w_1 v_1 + ... in position order (weighted_sum_f32's axpy).
 // The one grouping that differs is the double sum, whose rounding can reach the
 // float scale only when terms below 2^-20 of the sum lose bits.
+// A score is computed by a 16-lane row (lane j: partial j), two scores per row
+// at a time.  store_rows: the writer's K/V rows are stored here, once the first
+// key chunk has landed (so that wait does not also wait for the stores).
 template <class O>
-__device__ __forceinline__ void attn_exact(const AttnArgs& g, AttnLds& s, int kv, int L, const O& o) {
+__device__ __forceinline__ void attn_exact(const AttnArgs& g, AttnLds& s, int kv, int L, const O& o, bool k0_issued = false,
+                                           bool store_rows = false) {
     const int hd = g.head_dim, hpk = g.heads / g.kv_heads, t = threadIdx.x, per = hd / 16;
     const int nchunks = (L + kSplit - 1) / kSplit;
     const uint16_t* kbase = g.kcache + static_cast<size_t>(kv) * g.ctx * hd;
     const uint16_t* vbase = g.vcache + static_cast<size_t>(kv) * g.ctx * hd;
     attn_stamp(g, kv, 1);
     // ---- scores, chunk by chunk
-    {
-        const int n0 = chunk_cached(0, L);
-        if (n0 > 0) chunk_issue(s.kv[0], kbase, 0, n0, hd);
-    }
+    if (!k0_issued) attn_issue_k0(g, s, kv, L);
+    const int row = t >> 4, j = t & 15;
     for (int c = 0; c < nchunks; ++c) {
         const uint16_t* kvb = chunk_advance(s, kbase, s.kcur, c, nchunks, L, hd);
-        const int p0 = c * kSplit, n = L - p0 < kSplit ? L - p0 : kSplit;
-        for (int g0 = 0; g0 < hpk; g0 += 4) {
-            const int gn = hpk - g0 < 4 ? hpk - g0 : 4;
-            for (int i = t; i < n * 16; i += kThreads) {
-                const int p = i >> 4, j = i & 15;
-                const uint16_t* kr = kvb + p * hd;
-                float kf[8];
+        if (c == 0) attn_stamp(g, kv, 5);
+        if (c == 0 && store_rows) attn_store_rows<true>(g, s, kv, L - 1);
+        const int p0 = c * kSplit, n = L - p0 < kSplit ? L - p0 : kSplit, pairs = hpk * n;
+        for (int i0 = 2 * row; i0 < pairs; i0 += 2 * (kThreads / 16)) {
+            float acc[2];
 #pragma unroll
-                for (int m = 0; m < 8; ++m) kf[m] = m < per ? h2f(kr[j + 16 * m]) : 0.0f;
-                for (int gg = 0; gg < gn; ++gg) {
-                    const float* q = s.q + (g0 + gg) * hd;
-                    float lane = 0.0f;
+            for (int u = 0; u < 2; ++u) {
+                const int i = i0 + u < pairs ? i0 + u : i0;  // a row's second pair may repeat its first
+                const int gq = i / n, p = i - gq * n;
+                const float* q = s.q + gq * hd + j;
+                const uint16_t* kr = kvb + p * hd + j;
+                acc[u] = per == 8 ? lane_partial<8>(q, kr) : per == 6 ? lane_partial<6>(q, kr)
+                         : per == 4 ? lane_partial<4>(q, kr) : lane_partial<2>(q, kr);
+            }
+            ordered_sum16x2(acc[0], acc[1]);
+            if (j == 15) {
 #pragma unroll
-                    for (int m = 0; m < 8; ++m)
-                        if (m < per) lane += q[j + 16 * m] * kf[m];
-                    s.part[(gg * kSplit + p) * 16 + j] = lane;
+                for (int u = 0; u < 2; ++u) {
+                    const int i = i0 + u;
+                    if (i < pairs) {
+                        const int gq = i / n, p = i - gq * n;
+                        s.sc[gq * L + p0 + p] = acc[u] * g.scale;
+                    }
                 }
             }
-            __syncthreads();
-            for (int i = t; i < gn * n; i += kThreads) {
-                const int gg = i / n, p = i % n;
-                const float* pr = s.part + (gg * kSplit + p) * 16;
-                float sum = 0.0f;
-#pragma unroll
-                for (int j = 0; j < 16; ++j) sum += pr[j];
-                s.sc[(g0 + gg) * L + p0 + p] = sum * g.scale;
-            }
-            if (g0 + 4 < hpk) __syncthreads();
         }
     }
+    attn_stamp(g, kv, 6);
     // the first value chunk streams in while the softmax runs
     __syncthreads();
+    attn_stamp(g, kv, 7);
     {
         const int n0 = chunk_cached(0, L);
         if (n0 > 0) chunk_issue(s.kv[0], vbase, 0, n0, hd);
     }
     attn_stamp(g, kv, 2);
-    // ---- softmax per head
+    // ---- softmax, a wave per head
     const int wave = t >> 6, wl = t & 63;
-    for (int gq = 0; gq < hpk; ++gq) {
+    for (int gq = wave; gq < hpk; gq += kThreads / 64) {
+        float* sc = s.sc + gq * L;
         float m = -INFINITY;
-        for (int p = t; p < L; p += kThreads) m = fmaxf(m, s.sc[gq * L + p]);
+        for (int p = wl; p < L; p += 64) m = fmaxf(m, sc[p]);
         m = wave_max(m);
-        if (wl == 0) s.red[gq][wave] = static_cast<double>(m);
-    }
-    __syncthreads();
-    if (t < hpk) s.mx[t] = static_cast<float>(fmax(fmax(s.red[t][0], s.red[t][1]), fmax(s.red[t][2], s.red[t][3])));
-    __syncthreads();
-    for (int gq = 0; gq < hpk; ++gq) {
         double part = 0.0;
-        for (int p = t; p < L; p += kThreads) {
-            const float e = ref_expf(s.sc[gq * L + p] - s.mx[gq]);
-            s.sc[gq * L + p] = e;
+        for (int p = wl; p < L; p += 64) {
+            const float e = ref_expf(sc[p] - m);
+            sc[p] = e;
             part += static_cast<double>(e);
         }
-        part = wave_sum(part);
-        if (wl == 0) s.red[gq][wave] = part;
-    }
-    __syncthreads();
-    for (int gq = 0; gq < hpk; ++gq) {
-        const double sum = ((s.red[gq][0] + s.red[gq][1]) + s.red[gq][2]) + s.red[gq][3];
-        const float scale = static_cast<float>(1.0 / sum);
-        for (int p = t; p < L; p += kThreads) s.sc[gq * L + p] *= scale;
+        const float scale = static_cast<float>(1.0 / wave_sum(part));
+        for (int p = wl; p < L; p += 64) sc[p] *= scale;
     }
     attn_stamp(g, kv, 3);
     // ---- value sums in position order, chunk by chunk

@@ -286,7 +286,7 @@ static int loop_rows(const std::vector<const Packed*>& ms, int grid, bool head =
     for (const Packed* m : ms) {
         const size_t units = m->cols / block_elems(m->type);
         while (R > 1 && (static_cast<size_t>(R) * units > static_cast<size_t>(loop_units_per_thread(m->type, head)) * kThreads ||
-                         static_cast<size_t>(R) * (units + 1) > static_cast<size_t>(kTermCap)))
+                         static_cast<size_t>(R) * term_stride(static_cast<uint32_t>(units)) > static_cast<size_t>(kTermCap)))
             R /= 2;
     }
     return R;
@@ -386,6 +386,13 @@ void Session::setup_loop() {
     g.R_gu = loop_rows({&L0.gate.p}, G);
     g.tiles_gu = tiles_of(L0.gate.p, g.R_gu);
     g.R_d = loop_rows({&L0.down.p}, G);
+    {
+        const int R = std::min(g.R_o, g.R_d);
+        const int tiles = tiles_of(L0.o.p, R);
+        g.own_h = ((tiles + G - 1) / G) * R <= kOwnRows ? 1 : 0;
+        if (g.own_h) g.R_o = g.R_d = R;
+    }
+    g.tiles_o = tiles_of(L0.o.p, g.R_o);
     g.tiles_d = tiles_of(L0.down.p, g.R_d);
     g.R_h = loop_rows({&out_->p}, G, true);
     g.tiles_h = tiles_of(out_->p, g.R_h);
