@@ -1,0 +1,107 @@
+"""CPU tests of the host side — no GPU: the C-ABI library's exports, the GGUF
+reader/writer, the model-config parser and the seeded synthetic models."""
+import ctypes as C
+import os
+import re
+
+import numpy as np
+import pytest
+
+from brisk_hip import gguf as G, lib as hiplib, model, synth
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "brisk_hip.h")
+
+
+def declared_symbols():
+    text = open(HEADER).read()
+    return sorted(set(re.findall(r"\b(brisk_hip_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_library_exports_every_declared_symbol():
+    if not os.path.exists(hiplib.LIB_PATH):
+        pytest.skip("libbrisk_hip.so is not built (run __graft_entry__.build())")
+    so = C.CDLL(hiplib.LIB_PATH)
+    names = declared_symbols()
+    assert len(names) >= 20
+    missing = [n for n in names if not hasattr(so, n)]
+    assert not missing, missing
+    assert set(names) == set(hiplib.EXPORTS)
+
+
+def test_library_host_only_calls():
+    """Calls that touch no device: the ABI version and the packed-size arithmetic."""
+    if not os.path.exists(hiplib.LIB_PATH):
+        pytest.skip("libbrisk_hip.so is not built")
+    L = hiplib.load()
+    text = open(HEADER).read()
+    want = int(re.search(r"#define BRISK_HIP_ABI_VERSION (\d+)", text).group(1))
+    assert L.brisk_hip_abi_version() == want
+    # packed planes hold exactly the GGUF bytes of the matrix, each plane 256-byte aligned
+    for t, (be, bb) in ((G.T_Q4_0, (32, 18)), (G.T_Q8_0, (32, 34)), (G.T_Q4_K, (256, 144)), (G.T_Q6_K, (256, 210)),
+                        (G.T_TQ2_0, (256, 66))):
+        rows, cols = 48, 2048
+        n = L.brisk_hip_packed_bytes(t, rows, cols)
+        gguf = rows * cols // be * bb
+        assert gguf <= n <= gguf + 3 * 256 + 64 * rows * cols // be
+    assert L.brisk_hip_packed_bytes(G.T_Q4_0, 4, 33) == 0  # cols not a multiple of the block
+    assert L.brisk_hip_packed_bytes(99, 4, 64) == 0
+
+
+def test_gguf_round_trip(tmp_path):
+    w = G.GgufWriter()
+    w.add("general.architecture", G.STRING, "qwen3")
+    w.add("qwen3.block_count", G.U32, 3)
+    w.add("qwen3.rope.freq_base", G.F32, 1e6)
+    w.add("tokenizer.ggml.tokens", G.ARRAY, (G.STRING, ["a", "bc", "d"]))
+    blocks = synth.q4_0_blocks(5, 8)
+    w.add_tensor("blk.0.attn_q.weight", (64, 4), G.T_Q4_0, lambda: blocks)
+    vec = np.arange(64, dtype=np.float32)
+    w.add_tensor("output_norm.weight", (64,), G.T_F32, lambda: vec.view(np.uint8))
+    path = str(tmp_path / "t.gguf")
+    w.write(path)
+    f = G.GgufFile(path)
+    assert f.metadata["general.architecture"] == "qwen3"
+    assert f.metadata["qwen3.block_count"] == 3
+    assert f.metadata["tokenizer.ggml.tokens"] == ["a", "bc", "d"]
+    t = f.tensors["blk.0.attn_q.weight"]
+    assert t.type == G.T_Q4_0 and tuple(t.dims) == (64, 4)
+    assert np.array_equal(np.asarray(t.data).reshape(-1), blocks.reshape(-1))
+    assert np.array_equal(np.asarray(f.tensors["output_norm.weight"].data).view(np.float32), vec)
+
+
+def test_gguf_rejects_bad_magic(tmp_path):
+    p = tmp_path / "bad.gguf"
+    p.write_bytes(b"XXXX" + b"\0" * 64)
+    with pytest.raises(G.GgufError):
+        G.GgufFile(str(p))
+
+
+def test_synthetic_blocks_are_deterministic_and_in_range():
+    a, b = synth.q4_0_blocks(9, 100), synth.q4_0_blocks(9, 100)
+    assert np.array_equal(a, b)
+    d = a[:, 0:2].copy().view(np.float16).astype(np.float32)
+    assert np.all((d >= 0.0009) & (d <= 0.0201))  # configs[0]: d ~ U(0.001, 0.02)
+    q8 = synth.q8_0_blocks(9, 100)
+    assert np.all(q8[:, 2:].view(np.int8) >= -127)
+    t = synth.tq2_0_blocks(9, 10)
+    codes = np.stack([(t[:, :64] >> (2 * l)) & 3 for l in range(4)])
+    assert codes.max() <= 2  # ternary codes 0..2 only
+
+
+def test_spec_bytes_match_the_measurement_contract():
+    """decode bytes of configs[1] (Qwen3-0.6B Q4_0 + Q8_0 output) at position 0."""
+    s = synth.SPECS["qwen3-0.6b"]
+    assert s.layers * s.layer_weight_bytes() == 247_726_080
+    assert s.output_bytes() == 165_306_368
+
+
+@pytest.mark.parametrize("name", ["tiny-qwen3", "tiny-llama", "tiny-bitnet"])
+def test_model_config_parse(name):
+    spec = synth.SPECS[name]
+    f, cfg, table = model.load(synth.model_path(name))
+    assert (cfg.embd, cfg.layers, cfg.heads, cfg.kv_heads, cfg.head_dim, cfg.ff, cfg.vocab) == \
+        (spec.embd, spec.layers, spec.heads, spec.kv_heads, spec.head_dim, spec.ff, spec.vocab)
+    names = {t.name for t in table}
+    assert "token_embd.weight" in names and "blk.0.ffn_down.weight" in names
+    assert ("output.weight" in names) == (spec.out_fmt is not None)
