@@ -4,21 +4,25 @@
 Workload: the Qwen3-0.6B-shaped decoder, Q4_0 layers with
 Q8_0 embeddings and output, random weights from a seeded GGUF; 32 random prompt
 ids, then greedy decode.  A "step" is one decode token: the full forward pass
-(28 layers + output projection + on-device greedy pick), replayed from a
-captured hipGraph.  Inputs (weights, KV cache, token sequence) are resident in
-HBM when the timed region starts.
+(28 layers + output projection + on-device greedy pick).  All K timed steps run
+in one launch of the persistent token loop (k_loop); inputs (weights, KV cache,
+token sequence) are resident in HBM when the timed region starts.
 
 Printed (one JSON line): decode tok/s as `value`, plus
-  roofline      the dominant kernel (the output-projection GEMV, 151936 x 1024
-                Q8_0: the largest launch of the step) timed with HIP events on
-                the stream it runs on, against MI355X's 8 TB/s HBM peak;
-  decode_roofline  bytes per token (weights + norms + KV) x tok/s / 8 TB/s;
-  q4_0_gemv     config 1's 2048 x 2048 Q4_0 matvec streamed over 128 distinct
-                copies (302 MB, beyond the 256 MB Infinity Cache);
+  roofline      the dominant kernel, k_loop (one launch = the K decode steps),
+                timed with HIP events on the session's stream: algorithmic
+                bytes of the K steps (weights + norms + KV read/write per token)
+                over the launch time, against MI355X's 8 TB/s HBM peak;
+  q4_0_gemv     configs[0]'s 2048 x 2048 Q4_0 matvec (k_gemv): single-launch
+                latency, and streaming GB/s over 128 distinct copies (302 MB,
+                beyond the 256 MB Infinity Cache);
+  output_gemv   the 151936 x 1024 Q8_0 output projection as one k_gemv launch;
   prefill       tok/s of a 512-token prompt on the Llama-3.2-1B Q4_K_M shape (configs[2]);
   cpu_baseline  the reference's own CPU engine (built from its sources with its
-                portable kernels, oracle/_ref) on this host: a bounded sample of
-                the same decode workload.
+                portable kernels, oracle/_ref) on this host, on the same decode
+                workload (32-id prompt, 256 greedy tokens).
+`--copy-calibration MB` instead runs one device-to-device copy of that size (the
+plain copy kernel the rocprofv3 FETCH_SIZE/WRITE_SIZE readings are scaled by).
 """
 import argparse
 import json
@@ -92,6 +96,9 @@ def cpu_baseline(path, prompt, n_gen):
     ref = pyoracle.Reference(path, threads=threads, max_context=len(prompt) + n_gen + 8)
     ids, gaps, pre_s, gen_s = ref.generate(prompt, n_gen)
     ref.close()
+    one = pyoracle.Reference(path, threads=1, max_context=len(prompt) + 16)
+    _, _, pre1, gen1 = one.generate(prompt, 8)
+    one.close()
     model = ""
     try:
         with open("/proc/cpuinfo") as f:
@@ -99,10 +106,22 @@ def cpu_baseline(path, prompt, n_gen):
     except OSError:
         pass
     return {"value": round((n_gen - 1) / gen_s, 3), "unit": "tok/s", "cores": threads, "kind": "reference",
-            "sample": f"qwen3-0.6b-shape decode, {len(prompt)}-token prompt then {n_gen} greedy tokens "
-                      f"(generation tok/s as src/main.cpp:312-318; {threads} threads of {model or 'host CPU'}); "
-                      f"prompt {len(prompt) / pre_s:.1f} tok/s",
+            "sample": f"the full decode workload: qwen3-0.6b-shape, {len(prompt)}-id prompt then {n_gen} greedy tokens "
+                      f"(generation tok/s = (tokens - 1) / generation seconds, as src/main.cpp:312-318; {threads} threads "
+                      f"of {model or 'host CPU'}); prompt {len(prompt) / pre_s:.1f} tok/s",
+            "one_thread_tok_s": round(7 / gen1, 3),
             "ids": ids}
+
+
+def copy_calibration(mb):
+    import torch
+    n = mb * (1 << 20) // 4
+    a = torch.ones(n, device="cuda")
+    b = torch.empty_like(a)
+    torch.cuda.synchronize()
+    b.copy_(a)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_calibration_bytes": n * 4}), flush=True)
 
 
 def main():
@@ -113,11 +132,16 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-prefill", action="store_true")
     ap.add_argument("--no-kernels", action="store_true")
+    ap.add_argument("--copy-calibration", type=int, default=0, metavar="MB")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU; --gpus {args.gpus} is not supported "
               "(the token loop is single-device; see the multi-GPU note in DESIGN.md)", file=sys.stderr)
         sys.exit(2)
+
+    if args.copy_calibration:
+        copy_calibration(args.copy_calibration)
+        return
 
     import numpy as np
     import torch
@@ -142,18 +166,24 @@ def main():
     s.decode(W, ids=False)
     s.rollback(0)
     first = s.eval_greedy(prompt)          # prompt evaluated (untimed), first pick pending
+    st = torch.cuda.ExternalStream(s.stream)
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
-    ids = s.decode(K)                      # K decode steps, graph replays, one sync at the end
+    ev0.record(st)
+    ids = s.decode(K)                      # K decode steps: one k_loop launch, one sync at the end
+    ev1.record(st)
     torch.cuda.synchronize()
     dt = time.perf_counter() - t0
+    loop_ms = ev0.elapsed_time(ev1)
     tok_s = K / dt
     ms_step = dt / K * 1e3
     gen = np.concatenate([[first], ids])
-    mean_pos = len(prompt) + K / 2
-    step_bytes = spec.decode_bytes(int(mean_pos))
-    log(f"decode: {K} steps in {dt * 1e3:.1f} ms -> {tok_s:.1f} tok/s, {ms_step * 1e3:.1f} us/step, "
-        f"{step_bytes / 1e6:.1f} MB/step -> {step_bytes * tok_s / 1e9:.1f} GB/s")
+    step_bytes = [spec.decode_bytes(len(prompt) + i) for i in range(K)]
+    launch_bytes = int(sum(step_bytes))
+    mean_bytes = launch_bytes / K
+    log(f"decode: {K} steps in {dt * 1e3:.1f} ms (k_loop {loop_ms:.1f} ms by events) -> {tok_s:.1f} tok/s, "
+        f"{ms_step * 1e3:.1f} us/step, {mean_bytes / 1e6:.1f} MB/step -> {launch_bytes / (loop_ms * 1e-3) / 1e9:.1f} GB/s")
     s.close()
     del s
     torch.cuda.empty_cache()
@@ -162,13 +192,14 @@ def main():
         "metric": "decode tok/s (Qwen3-0.6B-shape Q4_0, greedy, on-device sampling)",
         "value": round(tok_s, 2), "unit": "tok/s", "n_gpus": 1, "steps": K, "warmup": W,
         "ms_per_step": round(ms_step, 4), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
-        "dtype": "q4_0 x q8_0 int8 dot, f32 accumulate", "data": "synthetic (seeded random-weight GGUF)",
+        "dtype": "int8", "data": "synthetic (seeded random-weight GGUF)",
         "config": {"workload": "qwen3-0.6b-shape decode: 32 random prompt ids then greedy steps", "hidden": 1024,
                    "layers": 28, "heads": 16, "kv_heads": 8, "head_dim": 128, "ffn": 3072, "vocab": 151936,
                    "weights": "Q4_0 layers, Q8_0 embedding/output", "prompt": 32, "decode_steps": K},
-        "decode_roofline": {"bound": "hbm", "bytes_per_token": step_bytes,
-                            "achieved": round(step_bytes * tok_s / 1e9, 2), "peak": 8000.0, "unit": "GB/s",
-                            "frac": round(step_bytes * tok_s / HBM_PEAK, 4)},
+        "roofline": {"kernel": "k_loop (persistent token loop; one launch = the K decode steps)", "bound": "hbm",
+                     "achieved": round(launch_bytes / (loop_ms * 1e-3) / 1e9, 2), "peak": 8000.0, "unit": "GB/s",
+                     "frac": round(launch_bytes / (loop_ms * 1e-3) / HBM_PEAK, 4), "traffic": None,
+                     "algorithmic_bytes_per_launch": launch_bytes, "ms_per_launch": round(loop_ms, 3)},
     }
     golden = os.path.join(ROOT, "tests", "golden", "qwen3-0.6b_greedy.json")
     if os.path.exists(golden):
@@ -179,20 +210,22 @@ def main():
         result["greedy_compared"] = n
 
     if not args.no_kernels:
-        # dominant kernel: the output projection GEMV (151936 x 1024 Q8_0 + output_norm), 2 copies (330 MB > MALL)
-        ms, algo = gemv_roofline(torch, lib, L, cfg.vocab, cfg.embd, 8, 34, copies=2, reps=40, norm=True)
-        ach = algo / (ms * 1e-3) / 1e9
-        result["roofline"] = {"kernel": "k_gemv (output projection, 151936x1024 Q8_0, fused output_norm)",
-                              "bound": "hbm", "achieved": round(ach, 1), "peak": 8000.0, "unit": "GB/s",
-                              "frac": round(ach / 8000.0, 4), "traffic": None, "algorithmic_bytes": algo,
-                              "ms_per_launch": round(ms, 4)}
-        log(f"output gemv: {ms * 1e3:.1f} us, {ach:.0f} GB/s")
+        # 2048 x 2048 Q4_0, single launch (matrix cache-resident) and streamed over 128 copies
+        ms0, algo0 = gemv_roofline(torch, lib, L, 2048, 2048, 2, 18, copies=1, reps=512, norm=False)
         ms1, algo1 = gemv_roofline(torch, lib, L, 2048, 2048, 2, 18, copies=128, reps=512, norm=False)
         ach1 = algo1 / (ms1 * 1e-3) / 1e9
-        result["q4_0_gemv"] = {"config": "2048x2048 Q4_0, 128 distinct copies", "us_per_launch": round(ms1 * 1e3, 2),
+        result["q4_0_gemv"] = {"config": "configs[0]: 2048x2048 Q4_0, x quantised to Q8_0 in-kernel",
+                               "single_launch_us": round(ms0 * 1e3, 2),
+                               "streaming_us_per_launch": round(ms1 * 1e3, 2), "streaming_copies": 128,
                                "achieved": round(ach1, 1), "unit": "GB/s", "frac": round(ach1 / 8000.0, 4),
                                "algorithmic_bytes": algo1}
-        log(f"q4_0 gemv 2048x2048: {ms1 * 1e3:.2f} us, {ach1:.0f} GB/s")
+        log(f"q4_0 gemv 2048x2048: single {ms0 * 1e3:.2f} us, streamed {ms1 * 1e3:.2f} us = {ach1:.0f} GB/s")
+        ms, algo = gemv_roofline(torch, lib, L, cfg.vocab, cfg.embd, 8, 34, copies=2, reps=40, norm=True)
+        ach = algo / (ms * 1e-3) / 1e9
+        result["output_gemv"] = {"config": "151936x1024 Q8_0 with fused output_norm, 2 copies (330 MB)",
+                                 "us_per_launch": round(ms * 1e3, 2), "achieved": round(ach, 1), "unit": "GB/s",
+                                 "frac": round(ach / 8000.0, 4), "algorithmic_bytes": algo}
+        log(f"output gemv: {ms * 1e3:.1f} us, {ach:.0f} GB/s")
 
     if not args.no_prefill:
         lname = "llama-3.2-1b"
@@ -215,7 +248,7 @@ def main():
 
     if not args.no_cpu_baseline:
         t0 = time.time()
-        cb = cpu_baseline(path, prompt, 32)
+        cb = cpu_baseline(path, prompt, 256)
         if cb is not None:
             ref_ids = cb.pop("ids")
             cb["greedy_matches_gpu"] = bool(np.array_equal(ref_ids, gen[:len(ref_ids)]))

@@ -72,9 +72,9 @@ constexpr int kExactMax = 512;     // contexts up to this length take the exact-
 constexpr int kExactScores = 4096; // ... when heads-per-kv x length fits this many LDS scores
 
 struct AttnLds {
-    float q[16 * 128];               // the group's query heads (raw, then normed and rotated)
+    alignas(16) float q[16 * 128];             // the group's query heads (raw, then normed and rotated)
     float kcur[128], vcur[128];      // this token's key and value (raw, then fp16-rounded)
-    uint16_t kv[2][kSplit * 128];    // two staged chunks of keys or values
+    alignas(16) uint16_t kv[2][kSplit * 128];    // two staged chunks of keys or values
     float sc[kExactScores];          // scores, then weights: [head][position]
     double red[16][4];
     float mx[16];
@@ -232,16 +232,29 @@ __device__ __forceinline__ void attn_prologue(const AttnArgs& g, AttnLds& s, int
 typedef __attribute__((address_space(3))) void* lds_void_ptr;
 typedef __attribute__((address_space(1))) const void* global_cvoid_ptr;
 
-__device__ __forceinline__ void chunk_issue(uint16_t* lds, const uint16_t* base, int p0, int n_pos, int hd) {
-    const int pieces = n_pos * hd / 8;  // 16-byte pieces
+// Swizzled key layout: 16-byte piece c of chunk row p sits at piece slot
+// p * P + (c ^ (p & mask)) (P = hd / 8 pieces a row, mask = P - 1 when P is a
+// power of two, else 0), so lanes reading the same piece of different rows hit
+// different LDS banks.
+__device__ __forceinline__ int kv_pieces(int hd) { return hd / 8; }
+__device__ __forceinline__ int kv_mask(int hd) {
+    const int P = hd / 8;
+    return (P & (P - 1)) == 0 ? P - 1 : 0;
+}
+
+__device__ __forceinline__ void chunk_issue(uint16_t* lds, const uint16_t* base, int p0, int n_pos, int hd, bool swz = false) {
+    const int P = kv_pieces(hd), mask = swz ? kv_mask(hd) : 0;
+    const int pieces = n_pos * P;  // 16-byte pieces
     const uint8_t* src = reinterpret_cast<const uint8_t*>(base + static_cast<size_t>(p0) * hd);
     uint8_t* dst = reinterpret_cast<uint8_t*>(lds);
     const int wave_first = static_cast<int>(threadIdx.x) & ~63;
     for (int k = 0; k * kThreads < pieces; ++k) {
-        const int i = k * kThreads + static_cast<int>(threadIdx.x);
-        if (i < pieces)
-            __builtin_amdgcn_global_load_lds((global_cvoid_ptr)(src + static_cast<size_t>(i) * 16),
+        const int i = k * kThreads + static_cast<int>(threadIdx.x);  // the LDS slot this lane fills
+        if (i < pieces) {
+            const int p = i / P, c = (i - p * P) ^ (p & mask);
+            __builtin_amdgcn_global_load_lds((global_cvoid_ptr)(src + (static_cast<size_t>(p) * P + c) * 16),
                                              (lds_void_ptr)(dst + (k * kThreads + wave_first) * 16), 16, 0, 0);
+        }
     }
 }
 
@@ -262,17 +275,20 @@ __device__ __forceinline__ int chunk_cached(int c, int L) {
 // starts staging chunk c + 1 into the other buffer, which overlaps chunk c's
 // compute.
 __device__ __forceinline__ uint16_t* chunk_advance(AttnLds& s, const uint16_t* base, const float* cur, int c, int nchunks, int L,
-                                                   int hd) {
+                                                   int hd, bool swz = false) {
     __builtin_amdgcn_s_waitcnt(0);  // this wave's loads of chunk c have landed
     __syncthreads();                // ... everyone's, and buffer (c + 1) & 1 (chunk c - 1) is consumed
     if (c + 1 < nchunks) {
         const int nn = chunk_cached(c + 1, L);
-        if (nn > 0) chunk_issue(s.kv[(c + 1) & 1], base, (c + 1) * kSplit, nn, hd);
+        if (nn > 0) chunk_issue(s.kv[(c + 1) & 1], base, (c + 1) * kSplit, nn, hd, swz);
     }
     uint16_t* buf = s.kv[c & 1];
     const int p0 = c * kSplit, n = L - p0 < kSplit ? L - p0 : kSplit, ncache = chunk_cached(c, L);
-    if (ncache < n)
-        for (int i = threadIdx.x; i < hd; i += kThreads) buf[ncache * hd + i] = f2h(cur[i]);
+    if (ncache < n) {
+        const int P = kv_pieces(hd), mask = swz ? kv_mask(hd) : 0;
+        for (int i = threadIdx.x; i < hd; i += kThreads)
+            buf[(ncache * P + ((i >> 3) ^ (ncache & mask))) * 8 + (i & 7)] = f2h(cur[i]);
+    }
     __syncthreads();
     return buf;
 }
@@ -282,40 +298,37 @@ __device__ __forceinline__ uint16_t* chunk_advance(AttnLds& s, const uint16_t* b
 // token's q/k/v have arrived.
 __device__ __forceinline__ void attn_issue_k0(const AttnArgs& g, AttnLds& s, int kv, int L) {
     const int n0 = chunk_cached(0, L);
-    if (n0 > 0) chunk_issue(s.kv[0], g.kcache + static_cast<size_t>(kv) * g.ctx * g.head_dim, 0, n0, g.head_dim);
+    if (n0 > 0) chunk_issue(s.kv[0], g.kcache + static_cast<size_t>(kv) * g.ctx * g.head_dim, 0, n0, g.head_dim, true);
 }
 
-// dot_f32's final reduction over 16 lanes, 0 + l0 + l1 + ... + l15 in that
-// order, as a shift-and-add chain through the 16-lane row on DPP: with
-// v(0) = 0 + l and v(k) = v(k-1) shifted down one lane (0 into lane 0) + l,
-// lane j of v(k) is ((0 + l(j-k)) + ...) + l(j), so lane 15 of v(15) is the
-// ordered sum.  No selects; two independent chains interleave.
-constexpr int kDppRowShr1 = 0x111;
-__device__ __forceinline__ void ordered_sum16x2(float& a, float& b) {
-    const float la = a, lb = b;
-    a = 0.0f + la;
-    b = 0.0f + lb;
-#pragma unroll
-    for (int k = 1; k < 16; ++k) {
-        a = __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, a), kDppRowShr1, 0xF, 0xF, false)) + la;
-        b = __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, b), kDppRowShr1, 0xF, 0xF, false)) + lb;
-    }
-}
-
-// dot_f32's lane partial j over a head of 16 * PER values (q, k offset by j):
-// 0 + q[0] k[0] + q[16] k[16] + ..., the loads issued before the adds.
+// One score, dot_f32(q, k_p) (src/kernels_f32.cpp:229-246), by one lane: 16
+// lane partials l_j = 0 + q_j k_j + q_(j+16) k_(j+16) + ... (PER terms each),
+// then 0 + l_0 + ... + l_15.  k_p is row p of a swizzled chunk (P pieces a
+// row); q is in LDS (lanes of one head read the same address: a broadcast).
 template <int PER>
-__device__ __forceinline__ float lane_partial(const float* q, const uint16_t* k) {
-    float qv[PER], kf[PER];
+__device__ __forceinline__ float score_lane(const float* q, const uint16_t* chunk, int p, int P, int mask) {
+    float lane[16];
+#pragma unroll
+    for (int j = 0; j < 16; ++j) lane[j] = 0.0f;
+    const uint4* rows = reinterpret_cast<const uint4*>(chunk);
 #pragma unroll
     for (int m = 0; m < PER; ++m) {
-        qv[m] = q[16 * m];
-        kf[m] = h2f(k[16 * m]);
-    }
-    float lane = 0.0f;
+        const uint4 k0 = rows[p * P + ((2 * m) ^ (p & mask))];
+        const uint4 k1 = rows[p * P + ((2 * m + 1) ^ (p & mask))];
+        const float4* q4 = reinterpret_cast<const float4*>(q + 16 * m);
+        const float4 qa = q4[0], qb = q4[1], qc = q4[2], qd = q4[3];
+        const uint32_t kw[8] = {k0.x, k0.y, k0.z, k0.w, k1.x, k1.y, k1.z, k1.w};
+        const float qv[16] = {qa.x, qa.y, qa.z, qa.w, qb.x, qb.y, qb.z, qb.w, qc.x, qc.y, qc.z, qc.w, qd.x, qd.y, qd.z, qd.w};
 #pragma unroll
-    for (int m = 0; m < PER; ++m) lane += qv[m] * kf[m];
-    return lane;
+        for (int j = 0; j < 16; ++j) {
+            const uint16_t h = static_cast<uint16_t>((j & 1) ? (kw[j >> 1] >> 16) : (kw[j >> 1] & 0xFFFF));
+            lane[j] += qv[j] * h2f(h);
+        }
+    }
+    float sum = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 16; ++j) sum += lane[j];
+    return sum;
 }
 
 // The reference's attention for one token (src/model.cpp:1050-1093 with the
@@ -326,8 +339,7 @@ __device__ __forceinline__ float lane_partial(const float* q, const uint16_t* k)
 //   out    = 0 + w_0 v_0 + w_1 v_1 + ... in position order (weighted_sum_f32's axpy).
 // The one grouping that differs is the double sum, whose rounding can reach the
 // float scale only when terms below 2^-20 of the sum lose bits.
-// A score is computed by a 16-lane row (lane j: partial j), two scores per row
-// at a time.  store_rows: the writer's K/V rows are stored here, once the first
+// A score is computed by one lane.  store_rows: the writer's K/V rows are stored here, once the first
 // key chunk has landed (so that wait does not also wait for the stores).
 template <class O>
 __device__ __forceinline__ void attn_exact(const AttnArgs& g, AttnLds& s, int kv, int L, const O& o, bool k0_issued = false,
@@ -339,37 +351,19 @@ __device__ __forceinline__ void attn_exact(const AttnArgs& g, AttnLds& s, int kv
     attn_stamp(g, kv, 1);
     // ---- scores, chunk by chunk
     if (!k0_issued) attn_issue_k0(g, s, kv, L);
-    const int row = t >> 4, j = t & 15;
+    const int P = kv_pieces(hd), mask = kv_mask(hd);
     for (int c = 0; c < nchunks; ++c) {
-        const uint16_t* kvb = chunk_advance(s, kbase, s.kcur, c, nchunks, L, hd);
-        if (c == 0) attn_stamp(g, kv, 5);
+        const uint16_t* kvb = chunk_advance(s, kbase, s.kcur, c, nchunks, L, hd, true);
         if (c == 0 && store_rows) attn_store_rows<true>(g, s, kv, L - 1);
         const int p0 = c * kSplit, n = L - p0 < kSplit ? L - p0 : kSplit, pairs = hpk * n;
-        for (int i0 = 2 * row; i0 < pairs; i0 += 2 * (kThreads / 16)) {
-            float acc[2];
-#pragma unroll
-            for (int u = 0; u < 2; ++u) {
-                const int i = i0 + u < pairs ? i0 + u : i0;  // a row's second pair may repeat its first
-                const int gq = i / n, p = i - gq * n;
-                const float* q = s.q + gq * hd + j;
-                const uint16_t* kr = kvb + p * hd + j;
-                acc[u] = per == 8 ? lane_partial<8>(q, kr) : per == 6 ? lane_partial<6>(q, kr)
-                         : per == 4 ? lane_partial<4>(q, kr) : lane_partial<2>(q, kr);
-            }
-            ordered_sum16x2(acc[0], acc[1]);
-            if (j == 15) {
-#pragma unroll
-                for (int u = 0; u < 2; ++u) {
-                    const int i = i0 + u;
-                    if (i < pairs) {
-                        const int gq = i / n, p = i - gq * n;
-                        s.sc[gq * L + p0 + p] = acc[u] * g.scale;
-                    }
-                }
-            }
+        for (int i = t; i < pairs; i += kThreads) {  // one (head, position) score a lane
+            const int gq = i / n, p = i - gq * n;
+            const float* q = s.q + gq * hd;
+            const float v = per == 8 ? score_lane<8>(q, kvb, p, P, mask) : per == 6 ? score_lane<6>(q, kvb, p, P, mask)
+                          : per == 4 ? score_lane<4>(q, kvb, p, P, mask) : score_lane<2>(q, kvb, p, P, mask);
+            s.sc[gq * L + p0 + p] = v * g.scale;
         }
     }
-    attn_stamp(g, kv, 6);
     // the first value chunk streams in while the softmax runs
     __syncthreads();
     attn_stamp(g, kv, 7);
