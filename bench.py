@@ -113,6 +113,19 @@ def cpu_baseline(path, prompt, n_gen):
             "ids": ids}
 
 
+def profiled_traffic(steps):
+    """HBM bytes of the decode launch measured by rocprofv3 (FETCH_SIZE + WRITE_SIZE, each scaled by a plain
+    copy's reading) for the default 256-step workload; None for other step counts or without the summary."""
+    p = os.path.join(ROOT, "profiles", "k_loop_qwen3-0.6b_decode.md")
+    if steps != 256 or not os.path.exists(p):
+        return None
+    with open(p) as fh:
+        for line in fh:
+            if line.startswith("traffic_bytes_per_launch:"):
+                return int(line.split(":")[1])
+    return None
+
+
 def copy_calibration(mb):
     import torch
     n = mb * (1 << 20) // 4
@@ -201,6 +214,10 @@ def main():
                      "frac": round(launch_bytes / (loop_ms * 1e-3) / HBM_PEAK, 4), "traffic": None,
                      "algorithmic_bytes_per_launch": launch_bytes, "ms_per_launch": round(loop_ms, 3)},
     }
+    traffic = profiled_traffic(K)
+    if traffic is not None:
+        result["roofline"]["traffic"] = traffic
+        result["roofline"]["traffic_source"] = "profiles/k_loop_qwen3-0.6b_decode.md (rocprofv3 FETCH_SIZE + WRITE_SIZE, copy-calibrated)"
     golden = os.path.join(ROOT, "tests", "golden", "qwen3-0.6b_greedy.json")
     if os.path.exists(golden):
         with open(golden) as fh:
