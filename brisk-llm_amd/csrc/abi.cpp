@@ -5,6 +5,7 @@
 #include <new>
 #include <string>
 
+#include "prefill.h"
 #include "session.h"
 
 struct brisk_hip_session {
@@ -116,7 +117,33 @@ int brisk_hip_matmul(int type, int flags, const void* packed, size_t rows, size_
         const bh::Packed p = packed_view(type, flags, packed, rows, cols);
         if (n == 0 || n > 65535) throw bh::Error(BRISK_HIP_EINVAL, "kernels: n must be 1..65535");
         if (out_stride < rows) throw bh::Error(BRISK_HIP_EINVAL, "kernels: out_stride < rows");
-        hip_check(bh::launch_matvec_q8(p, xq, n, out, out_stride, static_cast<hipStream_t>(stream)), "matmul");
+        const hipStream_t st = static_cast<hipStream_t>(stream);
+        if (n == 1) {
+            hip_check(bh::launch_matvec_q8(p, xq, n, out, out_stride, st), "matmul");
+            return;
+        }
+        // batches take the int8 MFMA path of the prefill: the GGUF activation rows are
+        // converted to its planar layout in a scratch allocation, released when done
+        const int stride = static_cast<int>((cols + 255) / 256 * 256);
+        bh::ActPlanar x{};
+        x.stride = stride;
+        void* mem = nullptr;
+        const size_t qb = n * static_cast<size_t>(stride), db = n * static_cast<size_t>(stride / 32) * 4,
+                     bb = n * static_cast<size_t>(stride / 16) * 4;
+        hip_check(hipMalloc(&mem, qb + db + bb), "hipMalloc");
+        x.qs = static_cast<int8_t*>(mem);
+        x.d = reinterpret_cast<float*>(static_cast<char*>(mem) + qb);
+        x.bs = reinterpret_cast<int32_t*>(static_cast<char*>(mem) + qb + db);
+        hipError_t e = bh::launch_pre_planar(xq, static_cast<int>(cols), static_cast<int>(n), bh::takes_q8_k(p.type), x, st);
+        if (e == hipSuccess) {
+            bh::MmArgs g{};
+            g.m = p; g.x = x; g.ntok = static_cast<int>(n); g.out = out; g.ostride = static_cast<int>(out_stride);
+            e = bh::launch_mm(g, bh::kMmStore, st);
+        }
+        const hipError_t e2 = hipStreamSynchronize(st);
+        (void)hipFree(mem);
+        hip_check(e, "matmul");
+        hip_check(e2, "matmul sync");
     });
 }
 

@@ -8,6 +8,11 @@
 
 namespace bh {
 
+constexpr int kSplit = 64;          // attention positions per split / per LDS chunk
+constexpr int kExactMax = 512;      // contexts up to this length take the exact-order attention
+constexpr int kExactScores = 4096;  // ... when heads-per-kv x length fits this many LDS scores
+__host__ __device__ inline bool attn_is_exact(int L, int hpk) { return L <= kExactMax && L * hpk <= kExactScores; }
+
 struct GemvTarget {
     Packed m;
     float* out;

@@ -67,9 +67,6 @@ __device__ __forceinline__ unsigned long long pick_key(float v, uint32_t idx) {
 }
 
 
-constexpr int kSplit = 64;         // positions per split / per LDS chunk
-constexpr int kExactMax = 512;     // contexts up to this length take the exact-order path
-constexpr int kExactScores = 4096; // ... when heads-per-kv x length fits this many LDS scores
 
 struct AttnLds {
     alignas(16) float q[16 * 128];             // the group's query heads (raw, then normed and rotated)
@@ -518,6 +515,5 @@ __device__ __forceinline__ bool attn_split_combine(const AttnArgs& g, int kv, in
     return true;
 }
 
-__device__ __forceinline__ bool attn_is_exact(int L, int hpk) { return L <= kExactMax && L * hpk <= kExactScores; }
 
 }  // namespace bh

@@ -1,0 +1,49 @@
+// Batched prefill (prefill.hip): argument blocks and launchers.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include "launch.h"
+
+namespace bh {
+
+// Activations quantised per token: int8 values [T][stride], scales
+// [T][stride / 32] (Q8_0: per 32 values; Q8_K: per 256), int32 sums
+// [T][stride / 16] (Q8_0: per 32; Q8_K: the bsums per 16).
+struct ActPlanar {
+    int8_t* qs;
+    float* d;
+    int32_t* bs;
+    int stride;  // values per token row (>= the widest input, a multiple of 256)
+};
+
+enum { kMmStore = 0, kMmAdd = 1, kMmPair = 2 };
+
+struct MmArgs {
+    Packed m;        // the weight matrix (rows x cols)
+    Packed m2;       // kMmPair: the up matrix (same shape and format as m, the gate)
+    ActPlanar x;     // ntok quantised rows of m.cols values
+    int ntok;
+    float* out;      // out[t * ostride + r]
+    int ostride;
+    int relu2;       // kMmPair: BitNet's squared-ReLU gate instead of SiLU
+};
+
+struct PreAttnArgs {
+    AttnArgs a;      // layer, shape and cache (a.q/k/v/pos/out unused)
+    float* q;        // [T][qstride] raw, then normed and rotated by k_pre_rope
+    const float* k;  // [T][kvstride]
+    const float* v;
+    float* out;      // [T][qstride] attention output
+    int qstride, kvstride;
+    int pos0;        // position of token 0
+};
+
+hipError_t launch_mm(const MmArgs& g, int mode, hipStream_t s);
+hipError_t launch_pre_quant(const float* x, int xstride, const float* w, float eps, int cols, int ntok, bool q8k, int bits,
+                            const ActPlanar& out, hipStream_t s);
+hipError_t launch_pre_planar(const void* xq, int cols, int ntok, bool q8k, const ActPlanar& out, hipStream_t s);
+hipError_t launch_pre_embed(const Packed& m, const int* seq, int pos0, int ntok, float* h, hipStream_t s);
+hipError_t launch_pre_attention(const PreAttnArgs& p, int ntok, hipStream_t s);
+
+}  // namespace bh

@@ -189,6 +189,10 @@ Session::Session(const brisk_hip_config& cfg, const brisk_hip_tensor* tensors, s
     }
     check(hipStreamSynchronize(stream_), "init sync");
     debug_ = std::getenv("BRISK_HIP_DEBUG") != nullptr;
+    {
+        const char* pf = std::getenv("BRISK_HIP_PREFILL");
+        prefill_on_ = !(pf != nullptr && std::string(pf) == "0") && !debug_;
+    }
     setup_loop();
     use_graphs_ = std::getenv("BRISK_HIP_NO_GRAPH") == nullptr && !debug_;
     if (use_graphs_) {
@@ -492,15 +496,112 @@ void Session::validate(const int32_t* tokens, size_t n) const {
 
 // Writes tokens to seq[position_ ..], syncs the device position to the host's and
 // marks seq[0, position_ + n) as caller tokens (pos_[1]).
-void Session::stage(const int32_t* tokens, size_t n) {
+void Session::stage(const int32_t* tokens, size_t n) { stage(tokens, n, position_); }
+
+void Session::stage(const int32_t* tokens, size_t n, size_t device_pos) {
     check(hipMemcpyAsync(seq_ + position_, tokens, n * 4, hipMemcpyHostToDevice, stream_), "hipMemcpy(tokens)");
-    const int p[2] = {static_cast<int>(position_), static_cast<int>(position_ + n)};
+    const int p[2] = {static_cast<int>(device_pos), static_cast<int>(position_ + n)};
     check(hipMemcpyAsync(pos_, p, 8, hipMemcpyHostToDevice, stream_), "hipMemcpy(pos)");
     check(hipStreamSynchronize(stream_), "stage sync");  // the host copies above read stack memory
 }
 
+// Prompts of two or more tokens whose attention stays on the exact path go
+// through the batched prefill (BRISK_HIP_PREFILL=0 turns it off).
+bool Session::use_prefill(size_t n) const {
+    return prefill_on_ && n >= 2 && attn_is_exact(static_cast<int>(position_ + n), static_cast<int>(cfg_.heads / cfg_.kv_heads));
+}
+
+void Session::ensure_prefill() {
+    if (pre_h_ != nullptr) return;
+    const size_t T = kPrefillTokens, e = cfg_.embd, qd = static_cast<size_t>(cfg_.heads) * cfg_.head_dim,
+                 kvd = static_cast<size_t>(cfg_.kv_heads) * cfg_.head_dim, ff = cfg_.ff;
+    pre_h_ = static_cast<float*>(alloc(T * e * 4));
+    pre_q_ = static_cast<float*>(alloc(T * qd * 4));
+    pre_k_ = static_cast<float*>(alloc(T * kvd * 4));
+    pre_v_ = static_cast<float*>(alloc(T * kvd * 4));
+    pre_att_ = static_cast<float*>(alloc(T * qd * 4));
+    pre_act_ = static_cast<float*>(alloc(T * ff * 4));
+    const size_t widest = std::max(std::max(e, qd), ff);
+    pre_x_.stride = static_cast<int>((widest + 255) / 256 * 256);
+    pre_x_.qs = static_cast<int8_t*>(alloc(T * pre_x_.stride));
+    pre_x_.d = static_cast<float*>(alloc(T * (pre_x_.stride / 32) * 4));
+    pre_x_.bs = static_cast<int32_t*>(alloc(T * (pre_x_.stride / 16) * 4));
+}
+
+// T rows of x (rms_norm'd by w when given), quantised for `consumer`'s activation format.
+void Session::prefill_quant(const float* x, int xstride, const float* w, int cols, int T, const DeviceMatrix& consumer) {
+    check(launch_pre_quant(x, xstride, w, cfg_.rms_epsilon, cols, T, takes_q8_k(consumer.p.type), act_bits(consumer.p), pre_x_,
+                           stream_),
+          "prefill quantise");
+}
+
+// Every layer for the T tokens seq[pos0 .. pos0 + T), as eval_batch runs a batch
+// (src/model.cpp:867-1162): the hidden rows end in pre_h_.
+void Session::prefill_layers(size_t pos0, int T) {
+    const int e = static_cast<int>(cfg_.embd), qd = static_cast<int>(cfg_.heads * cfg_.head_dim),
+              kvd = static_cast<int>(cfg_.kv_heads * cfg_.head_dim), ff = static_cast<int>(cfg_.ff);
+    check(launch_pre_embed(embd_.p, seq_, static_cast<int>(pos0), T, pre_h_, stream_), "prefill embed");
+    for (uint32_t l = 0; l < cfg_.layers; ++l) {
+        const Layer& L = layers_[l];
+        MmArgs g{};
+        g.x = pre_x_;
+        g.ntok = T;
+        // Q, K, V of attn_norm(h) (src/model.cpp:996-1015)
+        prefill_quant(pre_h_, e, L.attn_norm, e, T, L.q);
+        g.m = L.q.p; g.out = pre_q_; g.ostride = qd;
+        check(launch_mm(g, kMmStore, stream_), "prefill q");
+        g.m = L.k.p; g.out = pre_k_; g.ostride = kvd;
+        check(launch_mm(g, kMmStore, stream_), "prefill k");
+        g.m = L.v.p; g.out = pre_v_; g.ostride = kvd;
+        check(launch_mm(g, kMmStore, stream_), "prefill v");
+        // norms, RoPE, cache rows, attention (:1020-1093)
+        PreAttnArgs pa{};
+        pa.a.qnorm = L.q_norm; pa.a.knorm = L.k_norm; pa.a.rope = rope_; pa.a.eps = cfg_.rms_epsilon;
+        pa.a.neox = cfg_.arch != BRISK_HIP_ARCH_LLAMA;  // src/model.cpp:167
+        pa.a.kcache = kcache_[l]; pa.a.vcache = vcache_[l];
+        pa.a.ctx = static_cast<int>(max_ctx_); pa.a.head_dim = static_cast<int>(cfg_.head_dim);
+        pa.a.heads = static_cast<int>(cfg_.heads); pa.a.kv_heads = static_cast<int>(cfg_.kv_heads);
+        pa.a.scale = 1.0f / std::sqrt(static_cast<float>(cfg_.head_dim));  // src/model.cpp:978
+        pa.q = pre_q_; pa.k = pre_k_; pa.v = pre_v_; pa.out = pre_att_;
+        pa.qstride = qd; pa.kvstride = kvd; pa.pos0 = static_cast<int>(pos0);
+        check(launch_pre_attention(pa, T, stream_), "prefill attention");
+        // h += O (sub-normed) att (:1095-1111)
+        prefill_quant(pre_att_, qd, L.attn_sub_norm, qd, T, L.o);
+        g.m = L.o.p; g.out = pre_h_; g.ostride = e;
+        check(launch_mm(g, kMmAdd, stream_), "prefill o");
+        // act = silu(gate) * up of ffn_norm(h) (:1111-1143)
+        prefill_quant(pre_h_, e, L.ffn_norm, e, T, L.gate);
+        g.m = L.gate.p; g.m2 = L.up.p; g.out = pre_act_; g.ostride = ff; g.relu2 = cfg_.arch == BRISK_HIP_ARCH_BITNET;
+        check(launch_mm(g, kMmPair, stream_), "prefill gate/up");
+        // h += down (sub-normed) act (:1144-1162)
+        prefill_quant(pre_act_, ff, L.ffn_sub_norm, ff, T, L.down);
+        g.m = L.down.p; g.out = pre_h_; g.ostride = e; g.relu2 = 0;
+        check(launch_mm(g, kMmAdd, stream_), "prefill down");
+    }
+}
+
 void Session::eval(const int32_t* tokens, size_t n, float* logits) {
     validate(tokens, n);
+    if (use_prefill(n)) {
+        ensure_prefill();
+        // the device position is the last token's: the head's pick then lands in seq[position_ + n]
+        stage(tokens, n, position_ + n - 1);
+        int T = 0;
+        for (size_t c = 0; c < n; c += kPrefillTokens) {
+            T = static_cast<int>(std::min(n - c, static_cast<size_t>(kPrefillTokens)));
+            prefill_layers(position_ + c, T);
+        }
+        HeadArgs ha{};  // output_norm + output rows of the last token (src/model.cpp:1195-1205)
+        ha.m = out_->p; ha.x = pre_h_ + static_cast<size_t>(T - 1) * cfg_.embd; ha.normw = out_norm_;
+        ha.eps = cfg_.rms_epsilon; ha.logits = logits_; ha.key = key_;
+        check(launch_head(ha, stream_), "output");
+        finish();
+        if (logits != nullptr)
+            check(hipMemcpyAsync(logits, logits_, static_cast<size_t>(cfg_.vocab) * 4, hipMemcpyDeviceToHost, stream_), "hipMemcpy(logits)");
+        check(hipStreamSynchronize(stream_), "eval sync");
+        position_ += n;
+        return;
+    }
     stage(tokens, n);
     if (uses_loop()) {
         run_loop(position_, n, n - 1, position_ + n);

@@ -10,6 +10,7 @@
 #include "../../include/brisk_hip.h"
 #include "launch.h"
 #include "loop.h"
+#include "prefill.h"
 
 namespace bh {
 
@@ -68,6 +69,7 @@ private:
     void step(bool full);
     void validate(const int32_t* tokens, size_t n) const;
     void stage(const int32_t* tokens, size_t n);
+    void stage(const int32_t* tokens, size_t n, size_t device_pos);
     int32_t picked();
     void debug_layer(uint32_t l);
     PickState pick_state() const;
@@ -75,6 +77,10 @@ private:
     void setup_loop();
     void run_loop(size_t pos0, size_t n_steps, size_t first_full, size_t fixed);
     void check_loop_error();
+    bool use_prefill(size_t n) const;
+    void ensure_prefill();
+    void prefill_layers(size_t pos0, int T);
+    void prefill_quant(const float* x, int xstride, const float* w, int cols, int T, const DeviceMatrix& consumer);
 
     brisk_hip_config cfg_;
     int device_;
@@ -110,6 +116,11 @@ private:
     unsigned long long* trace_ = nullptr;
     static constexpr size_t kTraceSlots = 1 << 16;
     bool debug_ = false;
+    // batched prefill (int8 MFMA), buffers for kPrefillTokens tokens, allocated on first use
+    static constexpr int kPrefillTokens = 512;
+    bool prefill_on_ = true;
+    float *pre_h_ = nullptr, *pre_q_ = nullptr, *pre_k_ = nullptr, *pre_v_ = nullptr, *pre_att_ = nullptr, *pre_act_ = nullptr;
+    ActPlanar pre_x_{};
     hipGraphExec_t graph_layers_ = nullptr, graph_full_ = nullptr;
 };
 

@@ -113,12 +113,12 @@ CASES = [
 ]
 
 
+@pytest.mark.parametrize("n", [7, 67])  # batches run on int8 MFMA: 16-token groups, 64-token tiles
 @pytest.mark.parametrize("type_,rows,cols", CASES)
-def test_matvec_matmul_bitexact(lib, orc, type_, rows, cols):
+def test_matvec_matmul_bitexact(lib, orc, type_, rows, cols, n):
     w = weights(type_, rows, cols, rows * 7919 + cols)
     q8k = type_ in (Q4_K, Q6_K, TQ2_0)
     bits = orc.or_activation_bits(type_, rows)
-    n = 7
     xs = [activations(cols, 100 + t) for t in range(n)]
     xq = np.concatenate([quant_ref(orc, x, q8k, bits) for x in xs])
     rb = cols // BLOCK[type_][0] * (292 if q8k else 34)

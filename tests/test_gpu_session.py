@@ -20,7 +20,9 @@ TOL = 2e-2
 FAMILIES = ["tiny-qwen3", "tiny-llama", "tiny-q8", "tiny-bitnet"]
 
 
-PATHS = ["loop", "graph"]  # the persistent token loop, and one kernel per phase replayed from hipGraphs
+# the persistent token loop, one kernel per phase replayed from hipGraphs (both with the
+# batched MFMA prefill for prompts), and the loop with prompts evaluated token by token
+PATHS = ["loop", "graph", "tokenwise"]
 
 
 @pytest.fixture(scope="module", params=[(f, p) for p in PATHS for f in FAMILIES], ids=lambda fp: f"{fp[0]}-{fp[1]}")
@@ -29,11 +31,13 @@ def pair(request):
     name, path = request.param
     f, cfg, table = model.load(synth.model_path(name))
     print(f"[session] {name} ({path})", flush=True)
-    os.environ["BRISK_HIP_PATH"] = path
+    env = {"BRISK_HIP_PATH": path} if path != "tokenwise" else {"BRISK_HIP_PREFILL": "0"}
+    os.environ.update(env)
     try:
         s = HipSession((f, cfg, table), max_context=256)
     finally:
-        del os.environ["BRISK_HIP_PATH"]
+        for k in env:
+            del os.environ[k]
     o = pyoracle.Oracle(cfg, table, 256)
     yield name, cfg, s, o
     s.close()
@@ -47,6 +51,8 @@ def test_prompt_logits_and_greedy(pair):
     prompt = synth.prompt_ids(12, cfg.vocab)
     got, want = s.eval(prompt), o.eval(prompt)
     assert np.abs(got - want).max() <= TOL, name
+    # on these contexts every path repeats the reference's arithmetic: bit for bit
+    np.testing.assert_array_equal(got.view(np.uint32), want.view(np.uint32), err_msg=name)
     assert int(np.argmax(got)) == int(np.argmax(want))
     ids = s.generate([int(np.argmax(got))], 24)
     o_ids, gaps = o.generate([int(np.argmax(want))], 24)
