@@ -139,6 +139,7 @@ struct GemvLds {
 union LoopLds {
     GemvLds g;
     AttnLds att;
+    AttnPoolLds pool;
 };
 
 __device__ __forceinline__ unsigned tag_of(const LoopArgs& g, int step, int layer, int phase) {
@@ -275,23 +276,25 @@ __device__ __forceinline__ AttnArgs attn_args(const LoopArgs& g, const LayerDev&
 }
 
 // B: attention, exact (one workgroup per key/value head) or split over (kv, split) slots.
-__device__ __forceinline__ bool phase_b(const LoopArgs& g, const LayerDev& L, int step, int l, int pos, AttnLds& s) {
+__device__ __forceinline__ bool phase_b(const LoopArgs& g, const LayerDev& L, int step, int l, int pos, LoopLds& lds) {
     const int kvh = g.kv_heads, hpk = g.heads / kvh, hd = g.head_dim, Lc = pos + 1;
     const unsigned tin = tag_of(g, step, l, 1), tout = tag_of(g, step, l, 2);
     const AttnArgs a = attn_args(g, L);
     const TaggedOut o{g.attt, g.pacct, g.pmlt, tout, g.error};
-    if (attn_is_exact(Lc, hpk)) {
+    AttnLds& s = lds.att;
+    if (attn_is_exact(Lc, hpk) && Lc <= kSplit * kPoolChunks) {
         if (static_cast<int>(blockIdx.x) >= kvh) return true;
         const int kv = blockIdx.x;
+        AttnPoolLds& sp = lds.pool;
         attn_stamp(a, kv, 0);
-        attn_issue_k0(a, s, kv, Lc);  // the cached keys stream in while q/k/v are awaited
-        if (!tget_segs(g, tin, TSeg{g.qt + kv * hpk * hd, s.q, hpk * hd}, TSeg{g.kt + kv * hd, s.kcur, hd},
-                       TSeg{g.vt + kv * hd, s.vcur, hd})) {
+        attn_pool_issue(a, sp, kv, Lc);  // the cached keys (and values) stream in while q/k/v are awaited
+        if (!tget_segs(g, tin, TSeg{g.qt + kv * hpk * hd, sp.a.q, hpk * hd}, TSeg{g.kt + kv * hd, sp.a.kcur, hd},
+                       TSeg{g.vt + kv * hd, sp.a.vcur, hd})) {
             __builtin_amdgcn_s_waitcnt(0);
             return false;
         }
-        attn_finish_prologue<true>(a, s, kv, pos, true, false);
-        attn_exact(a, s, kv, Lc, o, true, true);
+        attn_finish_prologue<true>(a, sp.a, kv, pos, true, false);
+        attn_exact_pool(a, sp, kv, Lc, o);
         return true;
     }
     const int ns = (Lc + kSplit - 1) / kSplit;
@@ -527,7 +530,7 @@ __global__ __launch_bounds__(kThreads) void k_loop(LoopArgs g) {
             if (!phase_a<TQ, TV>(g, L, step, l, token, lds.g)) return;
             __syncthreads();
             if (g.trace != nullptr && blockIdx.x == 0 && threadIdx.x == 0) g.trace[2 + (step * g.n_layers + l) * 5] = wall_clock64();
-            if (!phase_b(g, L, step, l, pos, lds.att)) return;
+            if (!phase_b(g, L, step, l, pos, lds)) return;
             __syncthreads();
             if (g.trace != nullptr && blockIdx.x == 0 && threadIdx.x == 0) g.trace[3 + (step * g.n_layers + l) * 5] = wall_clock64();
             if (!phase_c<TO>(g, L, step, l, token, lds.g, hown)) return;

@@ -69,13 +69,23 @@ __device__ __forceinline__ unsigned long long pick_key(float v, uint32_t idx) {
 
 
 struct AttnLds {
-    alignas(16) float q[16 * 128];             // the group's query heads (raw, then normed and rotated)
+    alignas(16) float q[16 * 128];   // the group's query heads (raw, then normed and rotated)
     float kcur[128], vcur[128];      // this token's key and value (raw, then fp16-rounded)
-    alignas(16) uint16_t kv[2][kSplit * 128];    // two staged chunks of keys or values
-    float sc[kExactScores];          // scores, then weights: [head][position]
+    alignas(16) float sc[kExactScores + 64];  // scores, then weights: [head][position] (rows may be padded)
     double red[16][4];
     float mx[16];
     float ml[16][2];
+    alignas(16) uint16_t kv[2][kSplit * 128];  // two staged chunks of keys or values (kept last: see AttnPoolLds)
+};
+
+// The persistent loop's attention space: AttnLds with its chunk buffers
+// extended to kPoolChunks, so that a whole context's keys (and, when they fit,
+// its values) are staged at once.
+constexpr int kPoolChunks = 8;
+struct AttnPoolLds {
+    AttnLds a;
+    alignas(16) uint16_t more[kPoolChunks - 2][kSplit * 128];
+    __device__ __forceinline__ uint16_t* chunk(int i) { return &a.kv[0][0] + static_cast<size_t>(i) * kSplit * 128; }
 };
 
 // ---------------------------------------------------------------- tagged words
@@ -422,6 +432,141 @@ __device__ __forceinline__ void attn_exact(const AttnArgs& g, AttnLds& s, int kv
     for (int k = 0; k < 8; ++k) {
         const int ch = t + k * kThreads;
         if (ch < chains) o.att(kv * hpk * hd + ch, acc[k]);
+    }
+    attn_stamp(g, kv, 4);
+}
+
+// ---------------------------------------------------------------- pooled exact attention (the loop)
+
+// Where the pooled attention stages chunk c of the keys / values for a context of L.
+__device__ __forceinline__ int pool_nchunks(int L) { return (L + kSplit - 1) / kSplit; }
+__device__ __forceinline__ bool pool_values_early(int L) { return 2 * pool_nchunks(L) <= kPoolChunks; }
+
+// Issues the cached rows of every key chunk (and of every value chunk when
+// both fit the pool) of kv head `kv`; the first LDS access after this waits for
+// them, so one memory latency covers the whole context.  Needs L <= kSplit * kPoolChunks.
+__device__ __forceinline__ void attn_pool_issue(const AttnArgs& g, AttnPoolLds& s, int kv, int L) {
+    const int n = pool_nchunks(L), hd = g.head_dim;
+    const uint16_t* kbase = g.kcache + static_cast<size_t>(kv) * g.ctx * hd;
+    const uint16_t* vbase = g.vcache + static_cast<size_t>(kv) * g.ctx * hd;
+    for (int c = 0; c < n; ++c) {
+        const int nn = chunk_cached(c, L);
+        if (nn > 0) chunk_issue(s.chunk(c), kbase, c * kSplit, nn, hd, true);
+    }
+    if (pool_values_early(L))
+        for (int c = 0; c < n; ++c) {
+            const int nn = chunk_cached(c, L);
+            if (nn > 0) chunk_issue(s.chunk(n + c), vbase, c * kSplit, nn, hd, false);
+        }
+}
+
+// The current position's row (cur, fp16-rounded floats) into its chunk buffer.
+__device__ __forceinline__ void pool_put_current(uint16_t* buf, const float* cur, int L, int hd, bool swz) {
+    const int pos = L - 1, r = pos % kSplit, P = kv_pieces(hd), mask = swz ? kv_mask(hd) : 0;
+    for (int i = threadIdx.x; i < hd; i += kThreads) buf[(r * P + ((i >> 3) ^ (r & mask))) * 8 + (i & 7)] = f2h(cur[i]);
+}
+
+// attn_exact's arithmetic (the reference's order, see there) over the pool:
+// keys (and values) were issued by attn_pool_issue; the writer's cache rows
+// are stored here once the keys have landed.
+template <class O>
+__device__ __forceinline__ void attn_exact_pool(const AttnArgs& g, AttnPoolLds& sp, int kv, int L, const O& o) {
+    AttnLds& s = sp.a;
+    const int hd = g.head_dim, hpk = g.heads / g.kv_heads, t = threadIdx.x, per = hd / 16;
+    const int n = pool_nchunks(L), last = (L - 1) / kSplit;
+    const int Ls = (L + 3) & ~3;  // score row stride: rows start 16-byte aligned
+    const bool early = pool_values_early(L);
+    attn_stamp(g, kv, 1);
+    __builtin_amdgcn_s_waitcnt(0);  // this wave's key (and value) loads have landed
+    pool_put_current(sp.chunk(last), s.kcur, L, hd, true);
+    if (early) pool_put_current(sp.chunk(n + last), s.vcur, L, hd, false);
+    __syncthreads();
+    attn_store_rows<true>(g, s, kv, L - 1);
+    attn_stamp(g, kv, 5);
+    // ---- scores
+    const int P = kv_pieces(hd), mask = kv_mask(hd), pairs = hpk * L;
+    for (int i = t; i < pairs; i += kThreads) {  // one (head, position) score a lane
+        const int gq = i / L, pos = i - gq * L, c = pos / kSplit, p = pos - c * kSplit;
+        const float* q = s.q + gq * hd;
+        const uint16_t* buf = sp.chunk(c);
+        const float v = per == 8 ? score_lane<8>(q, buf, p, P, mask) : per == 6 ? score_lane<6>(q, buf, p, P, mask)
+                      : per == 4 ? score_lane<4>(q, buf, p, P, mask) : score_lane<2>(q, buf, p, P, mask);
+        s.sc[gq * Ls + pos] = v * g.scale;
+    }
+    __syncthreads();
+    attn_stamp(g, kv, 2);
+    const int vfirst = early ? n : 0;
+    if (!early) {  // the keys are consumed: the values take their buffers
+        const uint16_t* vbase = g.vcache + static_cast<size_t>(kv) * g.ctx * hd;
+        for (int c = 0; c < n; ++c) {
+            const int nn = chunk_cached(c, L);
+            if (nn > 0) chunk_issue(sp.chunk(c), vbase, c * kSplit, nn, hd, false);
+        }
+    }
+    // ---- softmax, a wave per head
+    const int wave = t >> 6, wl = t & 63;
+    for (int gq = wave; gq < hpk; gq += kThreads / 64) {
+        float* sc = s.sc + gq * Ls;
+        float m = -INFINITY;
+        for (int p = wl; p < L; p += 64) m = fmaxf(m, sc[p]);
+        m = wave_max(m);
+        double part = 0.0;
+        for (int p = wl; p < L; p += 64) {
+            const float e = ref_expf(sc[p] - m);
+            sc[p] = e;
+            part += static_cast<double>(e);
+        }
+        const float scale = static_cast<float>(1.0 / wave_sum(part));
+        for (int p = wl; p < L; p += 64) sc[p] *= scale;
+    }
+    if (!early) {
+        __builtin_amdgcn_s_waitcnt(0);
+        pool_put_current(sp.chunk(last), s.vcur, L, hd, false);
+    }
+    __syncthreads();
+    attn_stamp(g, kv, 3);
+    // ---- value sums in position order, one chain a lane (every SIMD busy).  Positions
+    // go in batches of 16 (a chunk holds 4); the next batch's weights and values are
+    // read before the current batch's adds, so LDS latency overlaps them.
+    const int chains = hpk * hd, full = L & ~15;
+    for (int ch = t; ch < chains; ch += kThreads) {
+        const int gq = ch / hd, d = ch % hd;
+        const float* w = s.sc + gq * Ls;
+        auto vrow = [&](int pos) -> const uint16_t* { return sp.chunk(vfirst + pos / kSplit) + (pos % kSplit) * hd + d; };
+        float a = 0.0f;
+        float4 wb[2][4];
+        uint16_t vb[2][16];
+        auto fetch = [&](int slot, int p) {
+#pragma unroll
+            for (int u = 0; u < 4; ++u) wb[slot][u] = *reinterpret_cast<const float4*>(w + p + 4 * u);
+            const uint16_t* vv = vrow(p);
+#pragma unroll
+            for (int u = 0; u < 16; ++u) vb[slot][u] = vv[u * hd];
+        };
+        auto add = [&](int slot) {
+#pragma unroll
+            for (int u = 0; u < 16; ++u) {
+                const float4 q4 = wb[slot][u >> 2];
+                const float wv = (u & 3) == 0 ? q4.x : (u & 3) == 1 ? q4.y : (u & 3) == 2 ? q4.z : q4.w;
+                a += wv * h2f(vb[slot][u]);
+            }
+        };
+        int p = 0;
+        if (full > 0) {
+            fetch(0, 0);
+            for (; p + 32 <= full; p += 32) {
+                fetch(1, p + 16);
+                add(0);
+                if (p + 32 < full) fetch(0, p + 32);
+                add(1);
+            }
+            if (p < full) {  // one batch left, already in slot 0
+                add(0);
+                p += 16;
+            }
+        }
+        for (; p < L; ++p) a += w[p] * h2f(*vrow(p));
+        o.att(kv * hpk * hd + ch, a);
     }
     attn_stamp(g, kv, 4);
 }
