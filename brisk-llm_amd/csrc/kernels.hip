@@ -37,6 +37,12 @@ __global__ void k_pack(uint32_t type, const uint8_t* __restrict__ src, size_t bl
             const uint8_t* s = src + b * 144;
             for (int i = 0; i < 16; ++i) p1[b * 16 + i] = s[i];
             for (int i = 0; i < 128; ++i) p0[b * 128 + i] = s[16 + i];
+            for (int j = 0; j < 8; ++j) {  // q4_k_scale_min decoded once (src/quant.h:256-264)
+                int sc, mn;
+                q4k_scale_min(s + 4, j, sc, mn);
+                p2[b * 16 + j] = static_cast<uint8_t>(sc);
+                p2[b * 16 + 8 + j] = static_cast<uint8_t>(mn);
+            }
             break;
         }
         case kQ6_K: {  // ql[128], qh[64], scales[16], d

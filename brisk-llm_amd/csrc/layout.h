@@ -8,12 +8,13 @@
 //   Q4_0   p0: nibbles  [rows][cols/32][16]    p1: d [rows][cols/32] (fp16)
 //   Q8_0   p0: int8     [rows][cols/32][32]    p1: d [rows][cols/32] (fp16)
 //   Q4_K   p0: nibbles  [rows][cols/256][128]  p1: {d, dmin, scales[12]} [rows][cols/256][16]
+//          p2: the 8 sub-block scales then the 8 mins, decoded to bytes [rows][cols/256][16]
 //   Q6_K   p0: ql       [rows][cols/256][128]  p1: qh [rows][cols/256][64]
 //          p2: {int8 scales[16], d, pad} [rows][cols/256][20]
 //   TQ2_0  p0: 2-bit    [rows][cols/256][64]   p1: d [rows][cols/256] (fp16)
 //
 // Bytes within each run are unchanged, so the byte total equals the GGUF size
-// (plus 2 pad bytes per Q6_K block and plane alignment).
+// (plus 2 pad bytes per Q6_K block, Q4_K's decoded scale plane, and plane alignment).
 #pragma once
 
 #include <stddef.h>
@@ -54,7 +55,7 @@ inline void plane_bytes(uint32_t type, size_t rows, size_t cols, size_t out[3]) 
     switch (type) {
         case kQ4_0: out[0] = blocks * 16; out[1] = blocks * 2; break;
         case kQ8_0: out[0] = blocks * 32; out[1] = blocks * 2; break;
-        case kQ4_K: out[0] = blocks * 128; out[1] = blocks * 16; break;
+        case kQ4_K: out[0] = blocks * 128; out[1] = blocks * 16; out[2] = blocks * 16; break;
         case kQ6_K: out[0] = blocks * 128; out[1] = blocks * 64; out[2] = blocks * 20; break;
         case kTQ2_0: out[0] = blocks * 64; out[1] = blocks * 2; break;
         default: break;

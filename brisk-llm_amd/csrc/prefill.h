@@ -17,7 +17,7 @@ struct ActPlanar {
     int stride;  // values per token row (>= the widest input, a multiple of 256)
 };
 
-enum { kMmStore = 0, kMmAdd = 1, kMmPair = 2 };
+enum { kMmStore = 0, kMmAdd = 1, kMmPair = 2, kMmGated = 3 };
 
 struct MmArgs {
     Packed m;        // the weight matrix (rows x cols)

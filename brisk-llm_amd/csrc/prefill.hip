@@ -132,182 +132,326 @@ __device__ __forceinline__ v4i mfma(uint64_t a, uint64_t b, v4i c) {
 
 // ---------------------------------------------------------------- the GEMM
 
-// One wave: 16 rows x (16 * kGroups) tokens; a workgroup: 64 rows (4 waves) x the same tokens.
-constexpr int kGroups = 4;
-constexpr int kRowsPerWg = 64, kTokPerWg = 16 * kGroups;
+// A workgroup computes 64 rows (4 waves x 16) x 64 tokens (4 groups of 16).
+// The K dimension goes in chunks of 256 values (8 sub-blocks; one super-block
+// for the K-quants).  Per chunk the workgroup stages the 64 tokens'
+// activations (and their scales) in LDS, and each lane holds its weight
+// fragments and row scales in registers; both are loaded one chunk ahead, so
+// memory latency overlaps the MFMAs and the float epilogue.
+constexpr int kRowsPerWg = 64;
+constexpr int kChunkCols = 256;
+constexpr int kBRow = kChunkCols + 16;  // LDS bytes per token row, padded off the bank period
+// Token groups of 16 a workgroup: 4 (64 tokens), or 2 for the K-quants, whose
+// integer epilogue holds more state per output.
+template <uint32_t T>
+__host__ __device__ constexpr int mm_groups() { return (T == kQ4_K || T == kQ6_K) ? 2 : 4; }
 
-// Per-lane accumulators of one matrix: [token group][row i].
-struct MmAcc {
-    float s[kGroups][4];
+template <int G>
+struct MmLds {
+    alignas(16) int8_t b[16 * G][kBRow];
+    float xd[16 * G][8];     // Q8_0: the chunk's 8 block scales; Q8_K: [0] the super-block's
+    int32_t bs[16 * G][16];  // Q8_K: the super-block's bsums
 };
 
-// The lane's outputs of W x for tokens t0 + 16 g + l % 16 and rows r0 + 4 (l / 16) + i.
-template <uint32_t T>
-__device__ __forceinline__ void mm_tile(const Packed& m, const ActPlanar& x, int ntok, uint32_t r0, int t0, MmAcc& acc) {
-    const int lane = threadIdx.x & 63, kq = (lane >> 4) * 8;
-    const uint32_t arow_raw = r0 + (lane & 15);
-    const bool arow_ok = arow_raw < m.rows;
-    const uint32_t arow = arow_ok ? arow_raw : m.rows - 1;
-    uint32_t orow[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const uint32_t r = r0 + (lane >> 4) * 4 + i;
-        orow[i] = r < m.rows ? r : m.rows - 1;  // clamped for the scale loads; not stored
-    }
-    int tok[kGroups];
-#pragma unroll
-    for (int g = 0; g < kGroups; ++g) {
-        const int t = t0 + 16 * g + (lane & 15);
-        tok[g] = t < ntok ? t : ntok - 1;
-    }
-    const int8_t* xq = x.qs;
-    const size_t xs = x.stride, ds = x.stride / 32, bss = x.stride / 16;
-#pragma unroll
-    for (int g = 0; g < kGroups; ++g)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) acc.s[g][i] = 0.0f;
-    const v4i zero = {0, 0, 0, 0};
+// One thread's share of a chunk's activations, in flight to LDS.
+template <int G>
+struct ActStage {
+    uint4 q[G];
+    float d[2];
+    int32_t bs[4];
+};
 
-    if (T == kQ4_0 || T == kQ8_0) {
-        const uint32_t nsub = m.cols / 32;
-        const uint16_t* dw = reinterpret_cast<const uint16_t*>(m.p1);
-        for (uint32_t j = 0; j < nsub; ++j) {
-            const uint64_t a = arow_ok ? frag_a<T>(m, arow, j, kq) : 0ull;
-            v4i d[kGroups];
+template <int G>
+__device__ __forceinline__ void act_stage_load(ActStage<G>& st, const ActPlanar& x, int ntok, int t0, int c, bool q8k) {
+    constexpr int kTok = 16 * G;
+    const int tid = threadIdx.x;
 #pragma unroll
-            for (int g = 0; g < kGroups; ++g)
-                d[g] = mfma(a, ld8(reinterpret_cast<const uint8_t*>(xq) + tok[g] * xs + j * 32 + kq), zero);
-            float w[4];
+    for (int k = 0; k < G; ++k) {
+        const int idx = k * kThreads + tid, tok = idx >> 4, piece = idx & 15;
+        const int t = t0 + tok < ntok ? t0 + tok : ntok - 1;
+        st.q[k] = *reinterpret_cast<const uint4*>(x.qs + static_cast<size_t>(t) * x.stride + c * kChunkCols + piece * 16);
+    }
+    const size_t ds = x.stride / 32, bss = x.stride / 16;
+    if (!q8k) {  // kTok tokens x 8 scales
 #pragma unroll
-            for (int i = 0; i < 4; ++i) w[i] = h2f(dw[static_cast<size_t>(orow[i]) * nsub + j]);
-#pragma unroll
-            for (int g = 0; g < kGroups; ++g) {
-                const float xd = x.d[tok[g] * ds + j];
-#pragma unroll
-                for (int i = 0; i < 4; ++i) acc.s[g][i] += static_cast<float>(d[g][i]) * w[i] * xd;  // src/quant.cpp:445-482
+        for (int k = 0; k < 2; ++k) {
+            const int idx = k * kThreads + tid, tok = idx >> 3, blk = idx & 7;
+            if (tok < kTok) {
+                const int t = t0 + tok < ntok ? t0 + tok : ntok - 1;
+                st.d[k] = x.d[t * ds + c * 8 + blk];
             }
         }
+    } else {  // kTok tokens x 16 bsums, and kTok scales
+        const int tok = tid >> 2;
+        if (tok < kTok) {
+            const int t = t0 + tok < ntok ? t0 + tok : ntok - 1;
+#pragma unroll
+            for (int k = 0; k < 4; ++k) st.bs[k] = x.bs[t * bss + c * 16 + (tid & 3) * 4 + k];
+        }
+        if (tid < kTok) {
+            const int t2 = t0 + tid < ntok ? t0 + tid : ntok - 1;
+            st.d[0] = x.d[t2 * ds + c];
+        }
+    }
+}
+
+template <int G>
+__device__ __forceinline__ void act_stage_store(const ActStage<G>& st, MmLds<G>& L, bool q8k) {
+    constexpr int kTok = 16 * G;
+    const int tid = threadIdx.x;
+#pragma unroll
+    for (int k = 0; k < G; ++k) {
+        const int idx = k * kThreads + tid, tok = idx >> 4, piece = idx & 15;
+        *reinterpret_cast<uint4*>(&L.b[tok][piece * 16]) = st.q[k];
+    }
+    if (!q8k) {
+#pragma unroll
+        for (int k = 0; k < 2; ++k) {
+            const int idx = k * kThreads + tid;
+            if ((idx >> 3) < kTok) L.xd[idx >> 3][idx & 7] = st.d[k];
+        }
+    } else {
+        if ((tid >> 2) < kTok) {
+#pragma unroll
+            for (int k = 0; k < 4; ++k) L.bs[tid >> 2][(tid & 3) * 4 + k] = st.bs[k];
+        }
+        if (tid < kTok) L.xd[tid][0] = st.d[0];
+    }
+}
+
+// One lane's weights for a chunk: the A fragments of its row (8 sub-blocks) and
+// the scales of its 4 output rows.
+template <uint32_t T>
+struct WChunk {
+    uint64_t a[8];
+    uint4 sc[4];     // Q4_0/Q8_0: 8 fp16 block scales a row; Q4_K: the decoded scales and mins; TQ2_0: .x = d
+    uint32_t s6[4];  // Q6_K: the fp16 d of each row (its int8 scales go in sc); Q4_K: {d, dmin}
+};
+
+template <uint32_t T>
+__device__ __forceinline__ void wchunk_load(WChunk<T>& w, const Packed& m, uint32_t arow, bool arow_ok, const uint32_t orow[4],
+                                            int c, int kq) {
+#pragma unroll
+    for (int jj = 0; jj < 8; ++jj) w.a[jj] = arow_ok ? frag_a<T>(m, arow, c * 8 + jj, kq) : 0ull;
+    if (T == kQ4_0 || T == kQ8_0) {
+        const uint32_t nsub = m.cols / 32;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) w.sc[i] = *reinterpret_cast<const uint4*>(m.p1 + (static_cast<size_t>(orow[i]) * nsub + c * 8) * 2);
     } else if (T == kQ4_K) {
         const uint32_t nsb = m.cols / 256;
-        for (uint32_t sb = 0; sb < nsb; ++sb) {
-            uint4 meta[4];
 #pragma unroll
-            for (int i = 0; i < 4; ++i) meta[i] = *reinterpret_cast<const uint4*>(m.p1 + (static_cast<size_t>(orow[i]) * nsb + sb) * 16);
-            int wsum[kGroups][4], osum[kGroups][4];
-#pragma unroll
-            for (int g = 0; g < kGroups; ++g)
-#pragma unroll
-                for (int i = 0; i < 4; ++i) wsum[g][i] = osum[g][i] = 0;
-            for (uint32_t jj = 0; jj < 8; ++jj) {
-                const uint32_t j = sb * 8 + jj;
-                const uint64_t a = arow_ok ? frag_a<T>(m, arow, j, kq) : 0ull;
-                int sc[4], mn[4];
-#pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    const uint32_t mw[4] = {meta[i].x, meta[i].y, meta[i].z, meta[i].w};
-                    q4k_scale_min(reinterpret_cast<const uint8_t*>(mw) + 4, static_cast<int>(jj), sc[i], mn[i]);
-                }
-#pragma unroll
-                for (int g = 0; g < kGroups; ++g) {
-                    const v4i d = mfma(a, ld8(reinterpret_cast<const uint8_t*>(xq) + tok[g] * xs + j * 32 + kq), zero);
-                    const int32_t* bs = x.bs + tok[g] * bss + sb * 16 + 2 * jj;
-                    const int pair = bs[0] + bs[1];
-#pragma unroll
-                    for (int i = 0; i < 4; ++i) {
-                        wsum[g][i] += sc[i] * d[i];
-                        osum[g][i] += mn[i] * pair;
-                    }
-                }
-            }
-#pragma unroll
-            for (int g = 0; g < kGroups; ++g) {
-                const float xd = x.d[tok[g] * ds + sb];
-#pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    const float d = h2f(static_cast<uint16_t>(meta[i].x & 0xFFFF)), dmin = h2f(static_cast<uint16_t>(meta[i].x >> 16));
-                    acc.s[g][i] += xd * (d * static_cast<float>(wsum[g][i]) - dmin * static_cast<float>(osum[g][i]));  // :500-521
-                }
-            }
+        for (int i = 0; i < 4; ++i) {
+            const size_t blk = static_cast<size_t>(orow[i]) * nsb + c;
+            w.sc[i] = *reinterpret_cast<const uint4*>(m.p2 + blk * 16);
+            w.s6[i] = *reinterpret_cast<const uint32_t*>(m.p1 + blk * 16);
         }
     } else if (T == kQ6_K) {
         const uint32_t nsb = m.cols / 256;
-        const bool lo_half = lane < 32;  // lanes 0..31 hold k 0..15 of a sub-block, 32..63 hold k 16..31
-        for (uint32_t sb = 0; sb < nsb; ++sb) {
-            int wsum[kGroups][4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const uint32_t* mp = reinterpret_cast<const uint32_t*>(m.p2 + (static_cast<size_t>(orow[i]) * nsb + c) * 20);
+            w.sc[i] = make_uint4(mp[0], mp[1], mp[2], mp[3]);
+            w.s6[i] = mp[4];
+        }
+    } else {
+        const uint32_t nsb = m.cols / 256;
+        const uint16_t* dw = reinterpret_cast<const uint16_t*>(m.p1);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) w.sc[i].x = dw[static_cast<size_t>(orow[i]) * nsb + c];
+    }
+}
+
+__device__ __forceinline__ uint32_t u4_word(const uint4& v, int k) { return k == 0 ? v.x : k == 1 ? v.y : k == 2 ? v.z : v.w; }
+
+// Per-lane accumulators: [token group][row i].
+template <int G>
+struct MmAcc {
+    float s[G][4];
+};
+
+// The chunk's contribution to the lane's outputs (tokens 16 g + l % 16, rows 4 (l / 16) + i),
+// in the reference's term and sum order.
+template <uint32_t T, int G>
+__device__ __forceinline__ void wchunk_compute(const WChunk<T>& w, const MmLds<G>& L, MmAcc<G>& acc, bool lut16) {
+    constexpr int kGroups = G;
+    const int lane = threadIdx.x & 63, kq = (lane >> 4) * 8, tl = lane & 15;
+    const v4i zero = {0, 0, 0, 0};
+    if (T == kQ4_0 || T == kQ8_0) {
+#pragma unroll
+        for (int jj = 0; jj < 8; ++jj) {
+            v4i d[kGroups];
 #pragma unroll
             for (int g = 0; g < kGroups; ++g)
+                d[g] = mfma(w.a[jj], *reinterpret_cast<const uint64_t*>(&L.b[16 * g + tl][jj * 32 + kq]), zero);
+            float wd[4];
 #pragma unroll
-                for (int i = 0; i < 4; ++i) wsum[g][i] = 0;
-            for (uint32_t jj = 0; jj < 8; ++jj) {
-                const uint32_t j = sb * 8 + jj;
-                const uint64_t a = arow_ok ? frag_a<T>(m, arow, j, kq) : 0ull;
-                const uint64_t a0 = lo_half ? a : 0ull, a1 = lo_half ? 0ull : a;  // groups 2 jj and 2 jj + 1 of 16
-                int s0[4], s1[4];
-#pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    const int8_t* sc = reinterpret_cast<const int8_t*>(m.p2 + (static_cast<size_t>(orow[i]) * nsb + sb) * 20);
-                    s0[i] = sc[2 * jj];
-                    s1[i] = sc[2 * jj + 1];
-                }
-#pragma unroll
-                for (int g = 0; g < kGroups; ++g) {
-                    const uint64_t b = ld8(reinterpret_cast<const uint8_t*>(xq) + tok[g] * xs + j * 32 + kq);
-                    const v4i d0 = mfma(a0, b, zero), d1 = mfma(a1, b, zero);
-#pragma unroll
-                    for (int i = 0; i < 4; ++i) wsum[g][i] += s0[i] * d0[i] + s1[i] * d1[i];
-                }
+            for (int i = 0; i < 4; ++i) {
+                const uint32_t word = u4_word(w.sc[i], jj >> 1);
+                wd[i] = h2f(static_cast<uint16_t>((jj & 1) ? (word >> 16) : (word & 0xFFFF)));
             }
 #pragma unroll
             for (int g = 0; g < kGroups; ++g) {
-                const float xd = x.d[tok[g] * ds + sb];
+                const float xd = L.xd[16 * g + tl][jj];
+#pragma unroll
+                for (int i = 0; i < 4; ++i) acc.s[g][i] += static_cast<float>(d[g][i]) * wd[i] * xd;  // src/quant.cpp:445-482
+            }
+        }
+    } else if (T == kQ4_K) {
+        int wsum[kGroups][4], osum[kGroups][4];
+#pragma unroll
+        for (int g = 0; g < kGroups; ++g)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) wsum[g][i] = osum[g][i] = 0;
+#pragma unroll
+        for (int jj = 0; jj < 8; ++jj) {
+            int sc[4], mn[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                sc[i] = static_cast<int>((u4_word(w.sc[i], jj >> 2) >> (8 * (jj & 3))) & 0xFF);
+                mn[i] = static_cast<int>((u4_word(w.sc[i], 2 + (jj >> 2)) >> (8 * (jj & 3))) & 0xFF);
+            }
+#pragma unroll
+            for (int g = 0; g < kGroups; ++g) {
+                const int t = 16 * g + tl;
+                const v4i d = mfma(w.a[jj], *reinterpret_cast<const uint64_t*>(&L.b[t][jj * 32 + kq]), zero);
+                const int pair = L.bs[t][2 * jj] + L.bs[t][2 * jj + 1];
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
-                    const uint8_t* mp = m.p2 + (static_cast<size_t>(orow[i]) * nsb + sb) * 20;
-                    const float d = h2f(static_cast<uint16_t>(mp[16] | (mp[17] << 8)));
-                    acc.s[g][i] += xd * d * static_cast<float>(wsum[g][i]);  // src/quant.cpp:549-563
+                    wsum[g][i] += sc[i] * d[i];
+                    osum[g][i] += mn[i] * pair;
                 }
             }
         }
-    } else {  // TQ2_0
-        const uint32_t nsb = m.cols / 256;
-        const bool lut16 = (m.flags & kFlagLut16) != 0;
-        const uint16_t* dw = reinterpret_cast<const uint16_t*>(m.p1);
-        for (uint32_t sb = 0; sb < nsb; ++sb) {
-            v4i d[kGroups];
 #pragma unroll
-            for (int g = 0; g < kGroups; ++g) d[g] = zero;
-            for (uint32_t jj = 0; jj < 8; ++jj) {  // the block's int32 sum over its 8 sub-blocks, exact
-                const uint32_t j = sb * 8 + jj;
-                const uint64_t a = arow_ok ? frag_a<T>(m, arow, j, kq) : 0ull;
+        for (int g = 0; g < kGroups; ++g) {
+            const float xd = L.xd[16 * g + tl][0];
 #pragma unroll
-                for (int g = 0; g < kGroups; ++g)
-                    d[g] = mfma(a, ld8(reinterpret_cast<const uint8_t*>(xq) + tok[g] * xs + j * 32 + kq), d[g]);
+            for (int i = 0; i < 4; ++i) {
+                const float d = h2f(static_cast<uint16_t>(w.s6[i] & 0xFFFF)), dmin = h2f(static_cast<uint16_t>(w.s6[i] >> 16));
+                acc.s[g][i] += xd * (d * static_cast<float>(wsum[g][i]) - dmin * static_cast<float>(osum[g][i]));  // :500-521
+            }
+        }
+    } else if (T == kQ6_K) {
+        const bool lo_half = lane < 32;  // lanes 0..31 hold k 0..15 of a sub-block, 32..63 hold k 16..31
+        int wsum[kGroups][4];
+#pragma unroll
+        for (int g = 0; g < kGroups; ++g)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) wsum[g][i] = 0;
+#pragma unroll
+        for (int jj = 0; jj < 8; ++jj) {
+            const uint64_t a0 = lo_half ? w.a[jj] : 0ull, a1 = lo_half ? 0ull : w.a[jj];  // groups 2 jj and 2 jj + 1 of 16
+            int s0[4], s1[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const uint32_t word = u4_word(w.sc[i], jj >> 1);
+                const int sh = (jj & 1) * 16;
+                s0[i] = static_cast<int8_t>((word >> sh) & 0xFF);
+                s1[i] = static_cast<int8_t>((word >> (sh + 8)) & 0xFF);
             }
 #pragma unroll
             for (int g = 0; g < kGroups; ++g) {
-                const float xd = x.d[tok[g] * ds + sb];
+                const uint64_t b = *reinterpret_cast<const uint64_t*>(&L.b[16 * g + tl][jj * 32 + kq]);
+                const v4i d0 = mfma(a0, b, zero), d1 = mfma(a1, b, zero);
 #pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    const float w = h2f(dw[static_cast<size_t>(orow[i]) * nsb + sb]);
-                    const float a = static_cast<float>(d[g][i]);
-                    acc.s[g][i] += lut16 ? a * w * xd : xd * w * a;  // src/quant.cpp:789-802 / :580-596
-                }
+                for (int i = 0; i < 4; ++i) wsum[g][i] += s0[i] * d0[i] + s1[i] * d1[i];
+            }
+        }
+#pragma unroll
+        for (int g = 0; g < kGroups; ++g) {
+            const float xd = L.xd[16 * g + tl][0];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const float d = h2f(static_cast<uint16_t>(w.s6[i] & 0xFFFF));
+                acc.s[g][i] += xd * d * static_cast<float>(wsum[g][i]);  // src/quant.cpp:549-563
+            }
+        }
+    } else {  // TQ2_0
+        v4i d[kGroups];
+#pragma unroll
+        for (int g = 0; g < kGroups; ++g) d[g] = zero;
+#pragma unroll
+        for (int jj = 0; jj < 8; ++jj)  // the block's int32 sum over its 8 sub-blocks, exact
+#pragma unroll
+            for (int g = 0; g < kGroups; ++g)
+                d[g] = mfma(w.a[jj], *reinterpret_cast<const uint64_t*>(&L.b[16 * g + tl][jj * 32 + kq]), d[g]);
+#pragma unroll
+        for (int g = 0; g < kGroups; ++g) {
+            const float xd = L.xd[16 * g + tl][0];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const float wv = h2f(static_cast<uint16_t>(w.sc[i].x & 0xFFFF));
+                const float a = static_cast<float>(d[g][i]);
+                acc.s[g][i] += lut16 ? a * wv * xd : xd * wv * a;  // src/quant.cpp:789-802 / :580-596
             }
         }
     }
 }
 
-// out[t * ostride + r] (=, += or the gated pair) for a 64-row x 64-token tile.
+// out[t * ostride + r] (=, += or gate(out) * up) for a 64-row x 64-token tile.
 template <uint32_t T, int MODE>
-__global__ __launch_bounds__(kThreads) void k_mm(MmArgs g) {
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 2))) void k_mm(MmArgs g) {
+    constexpr int kGroups = mm_groups<T>(), kTokPerWg = 16 * kGroups;
+    __shared__ MmLds<kGroups> L;
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, kq = (lane >> 4) * 8;
     const uint32_t r0 = blockIdx.x * kRowsPerWg + wave * 16;
     const int t0 = blockIdx.y * kTokPerWg;
-    if (r0 >= g.m.rows) return;
-    MmAcc a;
-    mm_tile<T>(g.m, g.x, g.ntok, r0, t0, a);
-    MmAcc u;
-    if (MODE == kMmPair) mm_tile<T>(g.m2, g.x, g.ntok, r0, t0, u);
+    const bool q8k = takes_q8_k(T);
+    const bool lut16 = (g.m.flags & kFlagLut16) != 0;
+    // rows of this lane: the A fragment's, and the 4 outputs' (clamped for the scale loads; never stored)
+    const uint32_t rmax = g.m.rows - 1;
+    const bool wave_ok = r0 <= rmax;
+    const uint32_t arow_raw = r0 + (lane & 15);
+    const bool arow_ok = arow_raw <= rmax;
+    const uint32_t arow = arow_ok ? arow_raw : rmax;
+    uint32_t orow[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const uint32_t r = r0 + (lane >> 4) * 4 + i;
+        orow[i] = r <= rmax ? r : rmax;
+    }
+    MmAcc<kGroups> a;
+#pragma unroll
+    for (int gi = 0; gi < kGroups; ++gi)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) a.s[gi][i] = 0.0f;
+    const int nc = static_cast<int>(g.m.cols / kChunkCols);
+    ActStage<kGroups> st;
+    WChunk<T> w0, w1;  // two chunks in flight
+    act_stage_load(st, g.x, g.ntok, t0, 0, q8k);
+    if (wave_ok) {
+        wchunk_load<T>(w0, g.m, arow, arow_ok, orow, 0, kq);
+    }
+    for (int c = 0; c < nc; c += 2) {
+        // chunk c (weights in w0/v0)
+        __syncthreads();
+        act_stage_store(st, L, q8k);
+        __syncthreads();
+        if (c + 1 < nc) {
+            act_stage_load(st, g.x, g.ntok, t0, c + 1, q8k);
+            if (wave_ok) {
+                wchunk_load<T>(w1, g.m, arow, arow_ok, orow, c + 1, kq);
+            }
+        }
+        if (wave_ok) {
+            wchunk_compute<T>(w0, L, a, lut16);
+        }
+        if (c + 1 >= nc) break;
+        // chunk c + 1 (weights in w1/v1)
+        __syncthreads();
+        act_stage_store(st, L, q8k);
+        __syncthreads();
+        if (c + 2 < nc) {
+            act_stage_load(st, g.x, g.ntok, t0, c + 2, q8k);
+            if (wave_ok) {
+                wchunk_load<T>(w0, g.m, arow, arow_ok, orow, c + 2, kq);
+            }
+        }
+        if (wave_ok) {
+            wchunk_compute<T>(w1, L, a, lut16);
+        }
+    }
+    if (!wave_ok) return;
 #pragma unroll
     for (int gi = 0; gi < kGroups; ++gi) {
         const int t = t0 + 16 * gi + (lane & 15);
@@ -315,20 +459,20 @@ __global__ __launch_bounds__(kThreads) void k_mm(MmArgs g) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const uint32_t r = r0 + (lane >> 4) * 4 + i;
-            if (r >= g.m.rows) continue;
+            if (r > rmax) continue;
             float* o = g.out + static_cast<size_t>(t) * g.ostride + r;
             const float v = a.s[gi][i];
             if (MODE == kMmStore) {
                 *o = v;
             } else if (MODE == kMmAdd) {
                 *o = *o + v;  // h += proj (src/model.cpp:1111, :1162)
-            } else {
-                const float up = u.s[gi][i];
+            } else {  // kMmGated: out holds the gate row, this is up
+                const float gv = *o;
                 if (g.relu2) {
-                    const float q = v > 0.0f ? v : 0.0f;
-                    *o = q * q * up;  // src/model.cpp:1134-1138
+                    const float q = gv > 0.0f ? gv : 0.0f;
+                    *o = q * q * v;  // src/model.cpp:1134-1138
                 } else {
-                    *o = v / (1.0f + ref_expf(-v)) * up;  // src/kernels_f32.cpp:287-289
+                    *o = gv / (1.0f + ref_expf(-gv)) * v;  // src/kernels_f32.cpp:287-289
                 }
             }
         }
@@ -384,7 +528,8 @@ __global__ __launch_bounds__(kThreads) void k_pre_attn(PreAttnArgs p) {
 
 template <int MODE>
 static hipError_t mm_dispatch(const MmArgs& g, hipStream_t s) {
-    const dim3 grid((g.m.rows + kRowsPerWg - 1) / kRowsPerWg, (g.ntok + kTokPerWg - 1) / kTokPerWg);
+    const int tok = 16 * (g.m.type == kQ4_K || g.m.type == kQ6_K ? mm_groups<kQ4_K>() : mm_groups<kQ4_0>());
+    const dim3 grid((g.m.rows + kRowsPerWg - 1) / kRowsPerWg, (g.ntok + tok - 1) / tok);
     switch (g.m.type) {
         case kQ4_0: hipLaunchKernelGGL((k_mm<kQ4_0, MODE>), grid, dim3(kThreads), 0, s, g); break;
         case kQ8_0: hipLaunchKernelGGL((k_mm<kQ8_0, MODE>), grid, dim3(kThreads), 0, s, g); break;
@@ -398,11 +543,18 @@ static hipError_t mm_dispatch(const MmArgs& g, hipStream_t s) {
 
 hipError_t launch_mm(const MmArgs& g, int mode, hipStream_t s) {
     if (g.ntok <= 0) return hipSuccess;
+    if (g.m.cols % kChunkCols != 0 || g.x.stride % kChunkCols != 0) return hipErrorInvalidValue;
     if (mode == kMmPair && (g.m2.type != g.m.type || g.m2.rows != g.m.rows || g.m2.cols != g.m.cols)) return hipErrorInvalidValue;
     switch (mode) {
         case kMmStore: return mm_dispatch<kMmStore>(g, s);
         case kMmAdd: return mm_dispatch<kMmAdd>(g, s);
-        case kMmPair: return mm_dispatch<kMmPair>(g, s);
+        case kMmPair: {  // the gate rows into out, then up with the gated epilogue
+            const hipError_t e = mm_dispatch<kMmStore>(g, s);
+            if (e != hipSuccess) return e;
+            MmArgs up = g;
+            up.m = g.m2;
+            return mm_dispatch<kMmGated>(up, s);
+        }
         default: return hipErrorInvalidValue;
     }
 }
