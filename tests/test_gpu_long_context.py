@@ -1,0 +1,77 @@
+"""Long contexts (configs[3]: KV cache pre-filled to 4096 positions with fp16
+N(0,1) values, then decode): the split-K attention path, against the oracle
+running on the same pre-filled cache (brisk_hip_session_kv_cache /
+set_position on the GPU, or_session_kv / set_position in the oracle).
+
+Beyond 512 positions the attention is split over 64-position slots and merged
+(flash-decoding), which reorders the value sums: logits are held to the
+north-star tolerance (max-abs 2e-2), greedy ids must match.
+"""
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+torch = pytest.importorskip("torch")
+
+from brisk_hip import HipSession, model, synth  # noqa: E402
+import pyoracle  # noqa: E402
+
+TOL = 2e-2
+
+
+def prefill_kv(s, o, cfg, n_pos, seed):
+    """Seeded fp16 N(0,1) keys and values for positions [0, n_pos) of every layer, into both sessions."""
+    rng = np.random.default_rng(seed)
+    for layer in range(cfg.layers):
+        for value in (False, True):
+            cache = o.kv(layer, value)  # [kv_heads][max_context][head_dim], oracle-owned host memory
+            vals = rng.standard_normal((cfg.kv_heads, n_pos, cfg.head_dim)).astype(np.float16)
+            cache[:, :n_pos, :] = vals.view(np.uint16)
+            ptr, nbytes = s.kv_cache(layer, value)
+            assert cache.nbytes == nbytes
+            _h2d(ptr, np.ascontiguousarray(cache), nbytes)
+    s.set_position(n_pos)
+    o.set_position(n_pos)
+
+
+def _h2d(dst_ptr, host, nbytes):
+    """Host-to-device copy into a raw device pointer (the session's cache)."""
+    import ctypes as C
+    hip = C.CDLL("libamdhip64.so")
+    hip.hipMemcpy.argtypes = [C.c_void_p, C.c_void_p, C.c_size_t, C.c_int]
+    assert hip.hipMemcpy(C.c_void_p(dst_ptr), C.c_void_p(host.ctypes.data), nbytes, 1) == 0  # hipMemcpyHostToDevice
+
+
+@pytest.mark.parametrize("name,n_pos,steps", [("tiny-qwen3", 900, 6), ("tiny-llama", 700, 6)])
+def test_split_attention_tiny(name, n_pos, steps):
+    f, cfg, table = model.load(synth.model_path(name))
+    print(f"[long] {name}: KV pre-filled to {n_pos}", flush=True)
+    with HipSession((f, cfg, table), max_context=n_pos + 16) as s:
+        o = pyoracle.Oracle(cfg, table, n_pos + 16)
+        prefill_kv(s, o, cfg, n_pos, seed=5)
+        tok = [17]
+        got, want = s.eval(tok), o.eval(tok)
+        assert np.abs(got - want).max() <= TOL
+        ids = s.generate([int(np.argmax(got))], steps)
+        o_ids, gaps = o.generate([int(np.argmax(want))], steps)
+        np.testing.assert_array_equal(ids, o_ids, err_msg=f"gaps {gaps}")
+        o.close()
+
+
+@pytest.mark.slow
+def test_qwen3_1_7b_at_4096():
+    """configs[3] at full size: Qwen3-1.7B-shape Q8_0, 4096 pre-filled positions, then decode."""
+    f, cfg, table = model.load(synth.model_path("qwen3-1.7b"))
+    n_pos = 4096
+    print(f"[long] qwen3-1.7b: KV pre-filled to {n_pos}", flush=True)
+    with HipSession((f, cfg, table), max_context=n_pos + 8) as s:
+        o = pyoracle.Oracle(cfg, table, n_pos + 8)
+        prefill_kv(s, o, cfg, n_pos, seed=7)
+        got, want = s.eval([11]), o.eval([11])
+        print(f"  max |logit diff| {np.abs(got - want).max():.3g}", flush=True)
+        assert np.abs(got - want).max() <= TOL
+        ids = s.generate([int(np.argmax(got))], 2)
+        o_ids, gaps = o.generate([int(np.argmax(want))], 2)
+        np.testing.assert_array_equal(ids, o_ids, err_msg=f"gaps {gaps}")
+        o.close()
