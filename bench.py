@@ -113,6 +113,67 @@ def cpu_baseline(path, prompt, n_gen):
             "ids": ids}
 
 
+def other_configs(torch, HipSession, model, synth):
+    """configs[3] (Qwen3-1.7B Q8_0, KV pre-filled to 4096 with fp16 N(0,1), 128 decode steps) and
+    configs[4] (BitNet-2B TQ2_0, 64-id prompt, 256 greedy steps): decode tok/s."""
+    import ctypes as C
+    out = {}
+    hip = C.CDLL("libamdhip64.so")
+    hip.hipMemcpy.argtypes = [C.c_void_p, C.c_void_p, C.c_size_t, C.c_int]
+    f, cfg, table = model.load(synth.model_path("qwen3-1.7b"))
+    s = HipSession((f, cfg, table), max_context=4096 + 160)
+    gen = torch.Generator(device="cuda").manual_seed(7)
+    for layer in range(cfg.layers):
+        for value in (False, True):
+            ptr, nbytes = s.kv_cache(layer, value)
+            fill = torch.randn(nbytes // 2, generator=gen, device="cuda").half()
+            assert hip.hipMemcpy(C.c_void_p(ptr), C.c_void_p(fill.data_ptr()), nbytes, 3) == 0
+    torch.cuda.synchronize()
+    s.set_position(4096)
+    s.eval_greedy([11])
+    s.decode(8, ids=False)             # warm-up
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    s.decode(128, ids=False)
+    dt = time.perf_counter() - t0
+    spec = synth.SPECS["qwen3-1.7b"]
+    b = sum(spec.decode_bytes(4105 + i) for i in range(128))
+    out["qwen3-1.7b_kv4096"] = {"workload": "configs[3]: Qwen3-1.7B-shape Q8_0, KV pre-filled to 4096, 128 greedy decode steps "
+                                            "(split-K attention)", "value": round(128 / dt, 2), "unit": "tok/s",
+                                "hbm_frac": round(b / dt / HBM_PEAK, 4)}
+    log(f"configs[3] decode at 4096: {128 / dt:.1f} tok/s")
+    s.close()
+    del s
+    torch.cuda.empty_cache()
+    f, cfg, table = model.load(synth.model_path("bitnet-2b"))
+    p = synth.prompt_ids(64, cfg.vocab)
+    s = HipSession((f, cfg, table), max_context=64 + 256 + 8)
+    s.eval(p, logits=False)
+    s.decode(8, ids=False)
+    s.rollback(0)
+    s.eval_greedy(p)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    ids = s.decode(255)
+    dt = time.perf_counter() - t0
+    spec = synth.SPECS["bitnet-2b"]
+    b = sum(spec.decode_bytes(64 + i) for i in range(255))
+    entry = {"workload": "configs[4]: BitNet-b1.58-2B-shape TQ2_0 (x86 TQ2_0x16 arithmetic, 7-bit activations), "
+                         "64-id prompt then 256 greedy tokens", "value": round(255 / dt, 2), "unit": "tok/s",
+             "hbm_frac": round(b / dt / HBM_PEAK, 4)}
+    golden = os.path.join(ROOT, "tests", "golden", "bitnet-2b_greedy.json")
+    if os.path.exists(golden):
+        with open(golden) as fh:
+            want = json.load(fh)["ids"]
+        n = min(len(want) - 1, len(ids))
+        entry["greedy_matches_reference"] = bool(list(map(int, ids[:n])) == want[1:n + 1])
+        entry["greedy_compared"] = n + 1
+    out["bitnet-2b"] = entry
+    log(f"configs[4] decode: {255 / dt:.1f} tok/s")
+    s.close()
+    return out
+
+
 def profiled_traffic(steps):
     """HBM bytes of the decode launch measured by rocprofv3 (FETCH_SIZE + WRITE_SIZE, each scaled by a plain
     copy's reading) for the default 256-step workload; None for other step counts or without the summary."""
@@ -145,6 +206,7 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-prefill", action="store_true")
     ap.add_argument("--no-kernels", action="store_true")
+    ap.add_argument("--no-configs", action="store_true", help="skip configs[3] (long context) and configs[4] (BitNet)")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MB")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -245,23 +307,39 @@ def main():
         log(f"output gemv: {ms * 1e3:.1f} us, {ach:.0f} GB/s")
 
     if not args.no_prefill:
+        # Llama-3.2-1B-shape Q4_K_M, 512-id prefill (batched MFMA path), then 128 decode steps
         lname = "llama-3.2-1b"
-        t0 = time.time()
         lpath = synth.model_path(lname)
-        log(f"model {lname}: ({time.time() - t0:.1f}s)")
         lf, lcfg, ltable = model.load(lpath)
         lp = synth.prompt_ids(512, lcfg.vocab, seed=11)
         ls = HipSession((lf, lcfg, ltable), max_context=1024)
-        ls.eval(lp[:64], logits=False)
+        ls.eval(lp[:64], logits=False)     # warm-up (untimed)
         ls.rollback(0)
         torch.cuda.synchronize()
         t0 = time.perf_counter()
         ls.eval(lp, logits=True)
         dtp = time.perf_counter() - t0
-        result["prefill"] = {"workload": "llama-3.2-1b-shape Q4_K_M, 512 random prompt ids (eval, last-token logits)",
-                             "value": round(512 / dtp, 2), "unit": "tok/s", "ms": round(dtp * 1e3, 2)}
-        log(f"prefill 512: {dtp * 1e3:.1f} ms -> {512 / dtp:.1f} tok/s")
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        ls.decode(128, ids=False)
+        dtd = time.perf_counter() - t0
+        # int8 ops of the layer contractions (q, k, v, o, gate, up, down), 2 per multiply-accumulate
+        params = lcfg.layers * (2 * lcfg.embd * lcfg.heads * lcfg.head_dim + 2 * lcfg.embd * lcfg.kv_heads * lcfg.head_dim
+                                + 3 * lcfg.embd * lcfg.ff)
+        ops = 2 * 512 * params
+        result["prefill"] = {"workload": "configs[2]: llama-3.2-1b-shape Q4_K_M, 512 random prompt ids (eval, last-token logits)",
+                             "value": round(512 / dtp, 2), "unit": "tok/s", "ms": round(dtp * 1e3, 2),
+                             "roofline": {"bound": "mfma", "achieved": round(ops / dtp / 1e12, 2), "peak": 5000.0,
+                                          "unit": "TOP/s (int8)", "frac": round(ops / dtp / 5.0e15, 5),
+                                          "ops": ops},
+                             "decode_after_prefill_tok_s": round(128 / dtd, 2)}
+        log(f"prefill 512: {dtp * 1e3:.1f} ms -> {512 / dtp:.1f} tok/s; then 128 decode steps {128 / dtd:.1f} tok/s")
         ls.close()
+        del ls
+        torch.cuda.empty_cache()
+
+    if not args.no_configs:
+        result["configs"] = other_configs(torch, HipSession, model, synth)
 
     if not args.no_cpu_baseline:
         t0 = time.time()
