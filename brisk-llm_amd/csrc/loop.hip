@@ -41,11 +41,11 @@ struct TSeg {
     int n;
 };
 
+template <int kGetPer = 4>
 __device__ __forceinline__ bool tget_segs(const LoopArgs& g, unsigned tag, TSeg s0, TSeg s1 = TSeg{nullptr, nullptr, 0},
                                           TSeg s2 = TSeg{nullptr, nullptr, 0}) {
-    // every word a thread needs (up to kGetPer * kThreads of them) is requested
-    // before any is checked, so a hand-off costs one memory round trip
-    constexpr int kGetPer = 4;
+    // kGetPer words a thread (kGetPer * kThreads a round) are requested before
+    // any is checked, so a round costs one memory round trip
     const int n01 = s0.n + s1.n, n = n01 + s2.n;
     auto at = [&](int i, const unsigned long long*& src, float*& dst) {
         if (i < s0.n) { src = s0.src + i; dst = s0.dst + i; }
@@ -107,7 +107,7 @@ __device__ __forceinline__ bool tget_segs(const LoopArgs& g, unsigned tag, TSeg 
 }
 
 __device__ __forceinline__ bool tget_vec(const LoopArgs& g, const unsigned long long* src, unsigned tag, float* dst, int n) {
-    return tget_segs(g, tag, TSeg{src, dst, n});
+    return tget_segs<>(g, tag, TSeg{src, dst, n});
 }
 
 // One tagged value (a residual row), by one thread.
@@ -275,6 +275,149 @@ __device__ __forceinline__ AttnArgs attn_args(const LoopArgs& g, const LayerDev&
     return a;
 }
 
+// ---------------------------------------------------------------- split attention (long contexts)
+
+constexpr int kSlotPos = 4 * kSplit;  // positions a split slot: four chunks of keys and four of values in the pool
+
+// Word offsets of slot `slot` of kv head `kv` in the partial buffers:
+// values [kv][slot][head][hd], (max, sum) [kv][slot][head][2].
+__device__ __forceinline__ size_t slot_acc(const AttnArgs& a, int kv, int slot) {
+    return static_cast<size_t>(kv * a.max_splits + slot) * (a.heads / a.kv_heads) * a.head_dim;
+}
+__device__ __forceinline__ size_t slot_ml(const AttnArgs& a, int kv, int slot) {
+    return static_cast<size_t>(kv * a.max_splits + slot) * (a.heads / a.kv_heads) * 2;
+}
+
+// Issues the cached key and value rows of the slot's chunks into pool chunks 0..3 and 4..7.
+__device__ __forceinline__ void attn_slot_issue(const AttnArgs& g, AttnPoolLds& s, int kv, int slot, int L) {
+    const int hd = g.head_dim;
+    const uint16_t* kbase = g.kcache + static_cast<size_t>(kv) * g.ctx * hd;
+    const uint16_t* vbase = g.vcache + static_cast<size_t>(kv) * g.ctx * hd;
+    for (int c = 0; c < 4; ++c) {
+        const int gc = slot * 4 + c, nn = chunk_cached(gc, L);
+        if (nn > 0) {
+            chunk_issue(s.chunk(c), kbase, gc * kSplit, nn, hd, true);
+            chunk_issue(s.chunk(4 + c), vbase, gc * kSplit, nn, hd, false);
+        }
+    }
+}
+
+// The slot's partial attention for each query head of the group: m = max score,
+// l = sum of exp(score - m), acc = sum of exp(score - m) v (flash-decoding).
+// The writer (the slot holding position L - 1) also stores the new cache rows.
+template <class O>
+__device__ __forceinline__ void attn_slot_partial(const AttnArgs& g, AttnPoolLds& sp, int kv, int slot, int L, bool writer,
+                                                  const O& o) {
+    AttnLds& s = sp.a;
+    const int hd = g.head_dim, hpk = g.heads / g.kv_heads, t = threadIdx.x, per = hd / 16;
+    const int P0 = slot * kSlotPos, n = L - P0 < kSlotPos ? L - P0 : kSlotPos, Ls = (n + 3) & ~3;
+    __builtin_amdgcn_s_waitcnt(0);
+    if (writer) {
+        const int r = L - 1 - P0;
+        pool_put_current(sp.chunk(r / kSplit), s.kcur, (r % kSplit) + 1, hd, true);
+        pool_put_current(sp.chunk(4 + r / kSplit), s.vcur, (r % kSplit) + 1, hd, false);
+    }
+    __syncthreads();
+    if (writer) attn_store_rows<true>(g, s, kv, L - 1);
+    const int P = kv_pieces(hd), mask = kv_mask(hd);
+    for (int i = t; i < hpk * n; i += kThreads) {
+        const int gq = i / n, p = i - gq * n;
+        const float* q = s.q + gq * hd;
+        const uint16_t* buf = sp.chunk(p / kSplit);
+        const int pr = p % kSplit;
+        const float v = per == 8 ? score_lane<8>(q, buf, pr, P, mask) : per == 6 ? score_lane<6>(q, buf, pr, P, mask)
+                      : per == 4 ? score_lane<4>(q, buf, pr, P, mask) : score_lane<2>(q, buf, pr, P, mask);
+        s.sc[gq * Ls + p] = v * g.scale;
+    }
+    __syncthreads();
+    const int wave = t >> 6, wl = t & 63;
+    for (int gq = wave; gq < hpk; gq += kThreads / 64) {
+        float* sc = s.sc + gq * Ls;
+        float m = -INFINITY;
+        for (int p = wl; p < n; p += 64) m = fmaxf(m, sc[p]);
+        m = wave_max(m);
+        double part = 0.0;
+        for (int p = wl; p < n; p += 64) {
+            const float e = ref_expf(sc[p] - m);
+            sc[p] = e;
+            part += static_cast<double>(e);
+        }
+        const double l = wave_sum(part);
+        if (writer) __builtin_amdgcn_s_waitcnt(0);  // the new cache rows are in memory before any output
+        if (wl == 0) {
+            const size_t ml = slot_ml(g, kv, slot) + gq * 2;
+            o.pml(ml, m);
+            o.pml(ml + 1, static_cast<float>(l));
+        }
+    }
+    __syncthreads();
+    const int chains = hpk * hd;
+    for (int ch = t; ch < chains; ch += kThreads) {
+        const int gq = ch / hd, d = ch % hd;
+        const float* w = s.sc + gq * Ls;
+        float acc = 0.0f;
+        int p = 0;
+        for (; p + 8 <= n; p += 8) {
+            float wv[8], vf[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                wv[u] = w[p + u];
+                vf[u] = h2f(sp.chunk(4 + (p + u) / kSplit)[((p + u) % kSplit) * hd + d]);
+            }
+#pragma unroll
+            for (int u = 0; u < 8; ++u) acc += wv[u] * vf[u];
+        }
+        for (; p < n; ++p) acc += w[p] * h2f(sp.chunk(4 + p / kSplit)[(p % kSplit) * hd + d]);
+        o.pacc(slot_acc(g, kv, slot) + ch, acc);
+    }
+}
+
+// Merges kv head kv's ns slots: out = sum_s acc_s e^(m_s - M) / sum_s l_s e^(m_s - M), M = max_s m_s.
+// The partials are fetched in bulk (batches of slots into the pool) before any arithmetic.
+template <class O>
+__device__ __forceinline__ bool attn_slot_merge(const LoopArgs& lg, const AttnArgs& g, AttnPoolLds& sp, int kv, int ns,
+                                                unsigned tag, const O& o) {
+    const int hd = g.head_dim, hpk = g.heads / g.kv_heads, chains = hpk * hd, t = threadIdx.x;
+    float* buf = reinterpret_cast<float*>(sp.chunk(0));  // the pool as floats
+    constexpr int kPoolFloats = kPoolChunks * kSplit * 128 / 2;
+    const int per_slot = chains + 2 * hpk;
+    const int batch = kPoolFloats / per_slot;
+    // running merge for the outputs this thread owns (chains t, t + 256, ...; at most 4)
+    float M[4], num[4], den[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) { M[k] = -INFINITY; num[k] = 0.0f; den[k] = 0.0f; }
+    for (int s0 = 0; s0 < ns; s0 += batch) {
+        const int nb = ns - s0 < batch ? ns - s0 : batch;
+        __syncthreads();
+        if (!tget_segs<16>(lg, tag, TSeg{lg.pacct + slot_acc(g, kv, s0), buf, nb * chains},
+                           TSeg{lg.pmlt + slot_ml(g, kv, s0), buf + nb * chains, nb * 2 * hpk}))
+            return false;
+        const float* ml = buf + nb * chains;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const int ch = t + k * kThreads;
+            if (ch >= chains) continue;
+            const int gq = ch / hd;
+            float Mn = M[k];
+            for (int j = 0; j < nb; ++j) Mn = fmaxf(Mn, ml[(j * hpk + gq) * 2]);
+            const float r = M[k] == -INFINITY ? 0.0f : ref_expf(M[k] - Mn);
+            float nu = num[k] * r, de = den[k] * r;
+            for (int j = 0; j < nb; ++j) {
+                const float f = ref_expf(ml[(j * hpk + gq) * 2] - Mn);
+                de += ml[(j * hpk + gq) * 2 + 1] * f;
+                nu += buf[j * chains + ch] * f;
+            }
+            M[k] = Mn; num[k] = nu; den[k] = de;
+        }
+    }
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        const int ch = t + k * kThreads;
+        if (ch < chains) o.att(kv * chains + ch, num[k] / den[k]);
+    }
+    return true;
+}
+
 // B: attention, exact (one workgroup per key/value head) or split over (kv, split) slots.
 __device__ __forceinline__ bool phase_b(const LoopArgs& g, const LayerDev& L, int step, int l, int pos, LoopLds& lds) {
     const int kvh = g.kv_heads, hpk = g.heads / kvh, hd = g.head_dim, Lc = pos + 1;
@@ -288,7 +431,7 @@ __device__ __forceinline__ bool phase_b(const LoopArgs& g, const LayerDev& L, in
         AttnPoolLds& sp = lds.pool;
         attn_stamp(a, kv, 0);
         attn_pool_issue(a, sp, kv, Lc);  // the cached keys (and values) stream in while q/k/v are awaited
-        if (!tget_segs(g, tin, TSeg{g.qt + kv * hpk * hd, sp.a.q, hpk * hd}, TSeg{g.kt + kv * hd, sp.a.kcur, hd},
+        if (!tget_segs<>(g, tin, TSeg{g.qt + kv * hpk * hd, sp.a.q, hpk * hd}, TSeg{g.kt + kv * hd, sp.a.kcur, hd},
                        TSeg{g.vt + kv * hd, sp.a.vcur, hd})) {
             __builtin_amdgcn_s_waitcnt(0);
             return false;
@@ -297,21 +440,28 @@ __device__ __forceinline__ bool phase_b(const LoopArgs& g, const LayerDev& L, in
         attn_exact_pool(a, sp, kv, Lc, o);
         return true;
     }
-    const int ns = (Lc + kSplit - 1) / kSplit;
-    for (int slot = blockIdx.x; slot < kvh * ns; slot += gridDim.x) {
-        const int kv = slot % kvh, sp = slot / kvh;
-        const bool writer = sp == pos / kSplit;
-        if (!tget_segs(g, tin, TSeg{g.qt + kv * hpk * hd, s.q, hpk * hd},
-                       writer ? TSeg{g.kt + kv * hd, s.kcur, hd} : TSeg{nullptr, nullptr, 0},
-                       writer ? TSeg{g.vt + kv * hd, s.vcur, hd} : TSeg{nullptr, nullptr, 0}))
+    // split-K: slots of kSlotPos positions a (kv head, slot) task, then one merge a kv head
+    const int ns = (Lc + kSlotPos - 1) / kSlotPos, tasks = ns * kvh, G = static_cast<int>(gridDim.x);
+    AttnPoolLds& sp = lds.pool;
+    for (int task = blockIdx.x; task < tasks; task += G) {
+        const int kv = task % kvh, slot = task / kvh;
+        const bool writer = slot == pos / kSlotPos;
+        attn_slot_issue(a, sp, kv, slot, Lc);  // the slot's cached keys and values stream in while q/k/v are awaited
+        if (!tget_segs<>(g, tin, TSeg{g.qt + kv * hpk * hd, sp.a.q, hpk * hd},
+                         writer ? TSeg{g.kt + kv * hd, sp.a.kcur, hd} : TSeg{nullptr, nullptr, 0},
+                         writer ? TSeg{g.vt + kv * hd, sp.a.vcur, hd} : TSeg{nullptr, nullptr, 0})) {
+            __builtin_amdgcn_s_waitcnt(0);
             return false;
-        attn_finish_prologue<true>(a, s, kv, pos, writer);
-        attn_split_partial(a, s, kv, sp, Lc, o);
+        }
+        attn_finish_prologue<true>(a, sp.a, kv, pos, writer, false);
+        attn_slot_partial(a, sp, kv, slot, Lc, writer, o);
         __syncthreads();
     }
-    if (static_cast<int>(blockIdx.x) < kvh) {
-        const bool ok = attn_split_combine(a, static_cast<int>(blockIdx.x), Lc, o);
-        return !__syncthreads_or(!ok);
+    // the merge of kv head k runs on workgroup G - 1 - k when that one had no slot task
+    for (int kv = 0; kv < kvh; ++kv) {
+        const int wg = G - 1 - kv >= tasks ? G - 1 - kv : kv;
+        if (static_cast<int>(blockIdx.x) != wg) continue;
+        if (!attn_slot_merge(g, a, sp, kv, ns, tout, o)) return false;
     }
     return true;
 }

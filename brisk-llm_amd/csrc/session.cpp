@@ -302,6 +302,8 @@ void Session::setup_loop() {
     const char* path = std::getenv("BRISK_HIP_PATH");
     if (path != nullptr && std::string(path) == "graph") return;
     if (debug_) return;
+    // the loop's split attention merges at most 4 outputs a thread (heads per kv head x head size <= 1024)
+    if ((cfg_.heads / cfg_.kv_heads) * cfg_.head_dim > 4 * kThreads) return;
     const Layer& L0 = layers_[0];
     const void* k = find_loop_kernel(L0.q.p.type, L0.v.p.type, L0.o.p.type, L0.gate.p.type, L0.down.p.type, out_->p.type);
     if (k == nullptr) return;
