@@ -692,6 +692,28 @@ template <> struct Unit<kTQ2_0> {
     }
 };
 
+// Row sums of `nrows` LDS term rows (stride floats apart, `units` terms each),
+// one lane a row, in block order: read 32 terms at a time before the adds, so
+// LDS latency is paid once per 32 terms.  out[r] for r < nrows.
+__device__ __forceinline__ void row_sums(const float* terms, uint32_t stride, uint32_t units, int nrows, float* out) {
+    if (threadIdx.x < static_cast<uint32_t>(nrows)) {
+        const float* t = terms + threadIdx.x * stride;
+        float s = 0.0f;
+        uint32_t b = 0;
+        for (; b + 32 <= units; b += 32) {
+            float4 v[8];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) v[j] = *reinterpret_cast<const float4*>(t + b + 4 * j);
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                s += v[j].x; s += v[j].y; s += v[j].z; s += v[j].w;
+            }
+        }
+        for (; b < units; ++b) s += t[b];
+        out[threadIdx.x] = s;
+    }
+}
+
 // A tile: rows [row0, row0 + R) of one matrix, all blocks.  Unit i of the tile
 // (row i / units, block i % units) belongs to thread i % 256, slot i / 256.
 template <uint32_t T, int M = Unit<T>::kMaxPerThread>
@@ -717,12 +739,8 @@ struct Tile {
         }
     }
 
-    // Terms to LDS (R rows of term_stride(units) floats), then one lane per row
-    // adds them in block order, as the reference's sequential `sum +=` does:
-    // sums[r] is bit-identical to the reference's dot.  The row is read 32
-    // terms at a time before the adds, so the LDS latency is paid once per 32
-    // terms, not once per term.  Ends with a barrier.
-    __device__ __forceinline__ void sums(const Packed& m, const ActLds& a, float* terms, float* out) const {
+    // Terms to LDS (R rows of term_stride(units) floats from `terms`); no barrier.
+    __device__ __forceinline__ void terms(const Packed& m, const ActLds& a, float* terms) const {
         const uint32_t units = m.cols / Unit<T>::kElems;
         const uint32_t stride = term_stride(units);
         const uint32_t total = static_cast<uint32_t>(R) * units;
@@ -734,23 +752,15 @@ struct Tile {
                 if (row0 + r < m.rows) terms[r * stride + b] = u[k].term(b, a);
             }
         }
+    }
+
+    // Terms, then one lane per row adds them in block order, as the reference's
+    // sequential `sum +=` does: sums[r] is bit-identical to the reference's dot.
+    // Ends with a barrier.
+    __device__ __forceinline__ void sums(const Packed& m, const ActLds& a, float* terms_buf, float* out) const {
+        terms(m, a, terms_buf);
         __syncthreads();
-        if (threadIdx.x < static_cast<uint32_t>(R)) {
-            const float* t = terms + threadIdx.x * stride;
-            float s = 0.0f;
-            uint32_t b = 0;
-            for (; b + 32 <= units; b += 32) {
-                float4 v[8];
-#pragma unroll
-                for (int j = 0; j < 8; ++j) v[j] = *reinterpret_cast<const float4*>(t + b + 4 * j);
-#pragma unroll
-                for (int j = 0; j < 8; ++j) {
-                    s += v[j].x; s += v[j].y; s += v[j].z; s += v[j].w;
-                }
-            }
-            for (; b < units; ++b) s += t[b];
-            out[threadIdx.x] = s;
-        }
+        row_sums(terms_buf, term_stride(m.cols / Unit<T>::kElems), m.cols / Unit<T>::kElems, R, out);
         __syncthreads();
     }
 };

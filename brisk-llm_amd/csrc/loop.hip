@@ -128,10 +128,12 @@ __device__ __forceinline__ bool tget_one(const LoopArgs& g, const unsigned long 
 
 // ---------------------------------------------------------------- shared memory
 
+constexpr int kGroupRows = kThreads;  // rows of one tile group (one summing lane each)
+
 struct GemvLds {
     ActLds a;
     alignas(16) float terms[kTermCap];
-    float sums[64];
+    float sums[kGroupRows];
     float sums2[64];
     double red[4];
     float x[kMaxCols];  // the phase's input vector
@@ -179,25 +181,55 @@ __device__ __forceinline__ bool run_tiles(int total, GemvLds& s, RowOf row_of, R
     Tile<T, M> ta, tb;
     Packed ma, mb;  // by value: a pointer to a kernel-argument member would force a private copy
     uint32_t ra, rb = 0;
-    int R;
-    row_of(t, ma, ra, R);
-    ta.load(ma, ra, R);
+    int Ra, Rb = 0;
+    row_of(t, ma, ra, Ra);
+    ta.load(ma, ra, Ra);
     if (!ready()) return false;
+    // Tiles go in groups: their terms side by side in LDS, then one row-sum pass
+    // for all the group's rows (one lane a row), so a workgroup with several
+    // tiles pays the serial block-order sum once, not once a tile.
+    const uint32_t units = ma.cols / Unit<T>::kElems, stride = term_stride(units);
+    int gfirst = t, grows = 0;
+    auto flush = [&]() -> bool {
+        __syncthreads();
+        row_sums(s.terms, stride, units, grows, s.sums);
+        __syncthreads();
+        int off = 0;
+        for (int u = gfirst; off < grows; u += G) {
+            Packed mu;
+            uint32_t r0;
+            int Ru;
+            row_of(u, mu, r0, Ru);
+            if (!done(u, mu, r0, s.sums + off)) return false;
+            off += Ru;
+        }
+        grows = 0;
+        return true;
+    };
+    auto fits = [&](int more) { return (grows + more) * static_cast<int>(stride) <= kTermCap && grows + more <= kGroupRows; };
     while (true) {
         if (t + G < total) {
-            row_of(t + G, mb, rb, R);
-            tb.load(mb, rb, R);
+            row_of(t + G, mb, rb, Rb);
+            tb.load(mb, rb, Rb);
         }
-        ta.sums(ma, s.a, s.terms, s.sums);
-        if (!done(t, ma, ra, s.sums)) return false;
+        ta.terms(ma, s.a, s.terms + grows * stride);
+        grows += Ra;
+        if (t + G >= total || !fits(Rb)) {
+            if (!flush()) return false;
+            gfirst = t + G;
+        }
         t += G;
         if (t >= total) break;
         if (t + G < total) {
-            row_of(t + G, ma, ra, R);
-            ta.load(ma, ra, R);
+            row_of(t + G, ma, ra, Ra);
+            ta.load(ma, ra, Ra);
         }
-        tb.sums(mb, s.a, s.terms, s.sums);
-        if (!done(t, mb, rb, s.sums)) return false;
+        tb.terms(mb, s.a, s.terms + grows * stride);
+        grows += Rb;
+        if (t + G >= total || !fits(Ra)) {
+            if (!flush()) return false;
+            gfirst = t + G;
+        }
         t += G;
         if (t >= total) break;
     }
@@ -502,40 +534,57 @@ __device__ __forceinline__ bool phase_c(const LoopArgs& g, const LayerDev& L, in
     return run_tiles<TO, kLoopUnits>(g.tiles_o, s, row_of, ready, done);
 }
 
-// D: gate/up rows of ffn_norm(h), the gated activation.  Tiles 2t and 2t + 1
-// are a gate tile and the up tile of the same rows.
+// D: gate/up rows of ffn_norm(h), the gated activation.  A tile is R gate rows
+// and the same R up rows; tiles are grouped as in run_tiles (gate terms, then
+// up terms, a tile after the other).
 template <uint32_t TG>
 __device__ __forceinline__ bool phase_d(const LoopArgs& g, const LayerDev& L, int step, int l, GemvLds& s) {
     if (static_cast<int>(blockIdx.x) >= g.tiles_gu) return true;
     const unsigned tag = tag_of(g, step, l, 4);
-    const int G = static_cast<int>(gridDim.x);
+    const int G = static_cast<int>(gridDim.x), R = g.R_gu;
+    const uint32_t units = L.gate.cols / Unit<TG>::kElems, stride = term_stride(units);
     Tile<TG, kLoopUnits> tg, tu;
     int t = blockIdx.x;
-    uint32_t row0 = static_cast<uint32_t>(t) * g.R_gu;
-    tg.load(L.gate, row0, g.R_gu);
-    tu.load(L.up, row0, g.R_gu);
+    uint32_t row0 = static_cast<uint32_t>(t) * R;
+    tg.load(L.gate, row0, R);
+    tu.load(L.up, row0, R);
     if (!tget_vec(g, g.ht, tag_of(g, step, l, 3), s.x, g.embd_dim)) return false;
     prologue_lds<TG>(L.gate, L.ffn_norm, g.eps, s);
+    int gfirst = t, grows = 0;
     while (true) {
-        tg.sums(L.gate, s.a, s.terms, s.sums);
-        tu.sums(L.up, s.a, s.terms, s.sums2);
-        const uint32_t r = threadIdx.x;
-        if (r < static_cast<uint32_t>(g.R_gu) && row0 + r < L.gate.rows) {
-            const float gv = s.sums[r], uv = s.sums2[r];
-            float out;
-            if (g.relu2) {
-                const float q = gv > 0.0f ? gv : 0.0f;
-                out = q * q * uv;  // src/model.cpp:1134-1138
-            } else {
-                out = gv / (1.0f + ref_expf(-gv)) * uv;  // src/kernels_f32.cpp:287-289
-            }
-            tput(g.actt + row0 + r, out, tag);
+        tg.terms(L.gate, s.a, s.terms + grows * stride);
+        tu.terms(L.up, s.a, s.terms + (grows + R) * stride);
+        grows += 2 * R;
+        const int tn = t + G;
+        const bool last = tn >= g.tiles_gu;
+        if (!last) {  // the next tile's weights stream in while this group finishes
+            row0 = static_cast<uint32_t>(tn) * R;
+            tg.load(L.gate, row0, R);
+            tu.load(L.up, row0, R);
         }
-        t += G;
-        if (t >= g.tiles_gu) break;
-        row0 = static_cast<uint32_t>(t) * g.R_gu;
-        tg.load(L.gate, row0, g.R_gu);
-        tu.load(L.up, row0, g.R_gu);
+        if (last || (grows + 2 * R) * static_cast<int>(stride) > kTermCap || grows + 2 * R > kGroupRows) {
+            __syncthreads();
+            row_sums(s.terms, stride, units, grows, s.sums);
+            __syncthreads();
+            for (int u = gfirst, off = 0; off < grows; u += G, off += 2 * R) {
+                const uint32_t r = threadIdx.x, r0 = static_cast<uint32_t>(u) * R;
+                if (r < static_cast<uint32_t>(R) && r0 + r < L.gate.rows) {
+                    const float gv = s.sums[off + r], uv = s.sums[off + R + r];
+                    float out;
+                    if (g.relu2) {
+                        const float q = gv > 0.0f ? gv : 0.0f;
+                        out = q * q * uv;  // src/model.cpp:1134-1138
+                    } else {
+                        out = gv / (1.0f + ref_expf(-gv)) * uv;  // src/kernels_f32.cpp:287-289
+                    }
+                    tput(g.actt + r0 + r, out, tag);
+                }
+            }
+            grows = 0;
+            gfirst = tn;
+        }
+        if (last) break;
+        t = tn;
     }
     return true;
 }
