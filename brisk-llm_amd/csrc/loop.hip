@@ -469,7 +469,9 @@ __device__ __forceinline__ bool phase_b(const LoopArgs& g, const LayerDev& L, in
             return false;
         }
         attn_finish_prologue<true>(a, sp.a, kv, pos, true, false);
-        attn_exact_pool(a, sp, kv, Lc, o);
+        if (hd == 128) attn_exact_pool<128>(a, sp, kv, Lc, o);
+        else if (hd == 64) attn_exact_pool<64>(a, sp, kv, Lc, o);
+        else attn_exact_pool<0>(a, sp, kv, Lc, o);
         return true;
     }
     // split-K: slots of kSlotPos positions a (kv head, slot) task, then one merge a kv head

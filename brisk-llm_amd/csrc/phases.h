@@ -469,10 +469,11 @@ __device__ __forceinline__ void pool_put_current(uint16_t* buf, const float* cur
 // attn_exact's arithmetic (the reference's order, see there) over the pool:
 // keys (and values) were issued by attn_pool_issue; the writer's cache rows
 // are stored here once the keys have landed.
-template <class O>
+// HD: the head size when it is a compile-time constant (64, 128), else 0.
+template <int HD, class O>
 __device__ __forceinline__ void attn_exact_pool(const AttnArgs& g, AttnPoolLds& sp, int kv, int L, const O& o) {
     AttnLds& s = sp.a;
-    const int hd = g.head_dim, hpk = g.heads / g.kv_heads, t = threadIdx.x, per = hd / 16;
+    const int hd = HD != 0 ? HD : g.head_dim, hpk = g.heads / g.kv_heads, t = threadIdx.x, per = hd / 16;
     const int n = pool_nchunks(L), last = (L - 1) / kSplit;
     const int Ls = (L + 3) & ~3;  // score row stride: rows start 16-byte aligned
     const bool early = pool_values_early(L);
@@ -489,8 +490,10 @@ __device__ __forceinline__ void attn_exact_pool(const AttnArgs& g, AttnPoolLds& 
         const int gq = i / L, pos = i - gq * L, c = pos / kSplit, p = pos - c * kSplit;
         const float* q = s.q + gq * hd;
         const uint16_t* buf = sp.chunk(c);
-        const float v = per == 8 ? score_lane<8>(q, buf, p, P, mask) : per == 6 ? score_lane<6>(q, buf, p, P, mask)
-                      : per == 4 ? score_lane<4>(q, buf, p, P, mask) : score_lane<2>(q, buf, p, P, mask);
+        float v;
+        if (HD != 0) v = score_lane<(HD != 0 ? HD : 128) / 16>(q, buf, p, HD / 8, HD / 8 - 1);
+        else v = per == 8 ? score_lane<8>(q, buf, p, P, mask) : per == 6 ? score_lane<6>(q, buf, p, P, mask)
+               : per == 4 ? score_lane<4>(q, buf, p, P, mask) : score_lane<2>(q, buf, p, P, mask);
         s.sc[gq * Ls + pos] = v * g.scale;
     }
     __syncthreads();
@@ -526,46 +529,53 @@ __device__ __forceinline__ void attn_exact_pool(const AttnArgs& g, AttnPoolLds& 
     __syncthreads();
     attn_stamp(g, kv, 3);
     // ---- value sums in position order, one chain a lane (every SIMD busy).  Positions
-    // go in batches of 16 (a chunk holds 4); the next batch's weights and values are
-    // read before the current batch's adds, so LDS latency overlaps them.
-    const int chains = hpk * hd, full = L & ~15;
+    // go in batches of 8 (never across a chunk); the next batch's weights and values
+    // are read before the current batch's adds, so LDS latency overlaps them.
+    const int chains = hpk * hd, full = L & ~7;
+    const uint16_t* vpool = sp.chunk(vfirst);
     for (int ch = t; ch < chains; ch += kThreads) {
         const int gq = ch / hd, d = ch % hd;
         const float* w = s.sc + gq * Ls;
-        auto vrow = [&](int pos) -> const uint16_t* { return sp.chunk(vfirst + pos / kSplit) + (pos % kSplit) * hd + d; };
+        const uint16_t* vcol = vpool + d;
+        auto vat = [&](int pos) -> const uint16_t* { return vcol + (pos >> 6) * (kSplit * 128) + (pos & 63) * hd; };
         float a = 0.0f;
-        float4 wb[2][4];
-        uint16_t vb[2][16];
-        auto fetch = [&](int slot, int p) {
-#pragma unroll
-            for (int u = 0; u < 4; ++u) wb[slot][u] = *reinterpret_cast<const float4*>(w + p + 4 * u);
-            const uint16_t* vv = vrow(p);
-#pragma unroll
-            for (int u = 0; u < 16; ++u) vb[slot][u] = vv[u * hd];
-        };
-        auto add = [&](int slot) {
-#pragma unroll
-            for (int u = 0; u < 16; ++u) {
-                const float4 q4 = wb[slot][u >> 2];
-                const float wv = (u & 3) == 0 ? q4.x : (u & 3) == 1 ? q4.y : (u & 3) == 2 ? q4.z : q4.w;
-                a += wv * h2f(vb[slot][u]);
-            }
-        };
+        float4 wa0, wa1, wb0, wb1;
+        uint16_t va[8], vb[8];
         int p = 0;
         if (full > 0) {
-            fetch(0, 0);
-            for (; p + 32 <= full; p += 32) {
-                fetch(1, p + 16);
-                add(0);
-                if (p + 32 < full) fetch(0, p + 32);
-                add(1);
+            wa0 = *reinterpret_cast<const float4*>(w);
+            wa1 = *reinterpret_cast<const float4*>(w + 4);
+#pragma unroll
+            for (int u = 0; u < 8; ++u) va[u] = vat(0)[u * hd];
+            for (; p + 16 <= full; p += 16) {
+                {
+                    const float* wn = w + p + 8;
+                    wb0 = *reinterpret_cast<const float4*>(wn);
+                    wb1 = *reinterpret_cast<const float4*>(wn + 4);
+                    const uint16_t* vn = vat(p + 8);
+#pragma unroll
+                    for (int u = 0; u < 8; ++u) vb[u] = vn[u * hd];
+                }
+                a += wa0.x * h2f(va[0]); a += wa0.y * h2f(va[1]); a += wa0.z * h2f(va[2]); a += wa0.w * h2f(va[3]);
+                a += wa1.x * h2f(va[4]); a += wa1.y * h2f(va[5]); a += wa1.z * h2f(va[6]); a += wa1.w * h2f(va[7]);
+                if (p + 16 < full) {
+                    const float* wn = w + p + 16;
+                    wa0 = *reinterpret_cast<const float4*>(wn);
+                    wa1 = *reinterpret_cast<const float4*>(wn + 4);
+                    const uint16_t* vn = vat(p + 16);
+#pragma unroll
+                    for (int u = 0; u < 8; ++u) va[u] = vn[u * hd];
+                }
+                a += wb0.x * h2f(vb[0]); a += wb0.y * h2f(vb[1]); a += wb0.z * h2f(vb[2]); a += wb0.w * h2f(vb[3]);
+                a += wb1.x * h2f(vb[4]); a += wb1.y * h2f(vb[5]); a += wb1.z * h2f(vb[6]); a += wb1.w * h2f(vb[7]);
             }
-            if (p < full) {  // one batch left, already in slot 0
-                add(0);
-                p += 16;
+            if (p < full) {  // one batch left, in va / wa
+                a += wa0.x * h2f(va[0]); a += wa0.y * h2f(va[1]); a += wa0.z * h2f(va[2]); a += wa0.w * h2f(va[3]);
+                a += wa1.x * h2f(va[4]); a += wa1.y * h2f(va[5]); a += wa1.z * h2f(va[6]); a += wa1.w * h2f(va[7]);
+                p += 8;
             }
         }
-        for (; p < L; ++p) a += w[p] * h2f(*vrow(p));
+        for (; p < L; ++p) a += w[p] * h2f(*vat(p));
         o.att(kv * hpk * hd + ch, a);
     }
     attn_stamp(g, kv, 4);
