@@ -45,6 +45,8 @@ struct LoopArgs {
     // O and down tiles cover the same rows of h on the same workgroup, which
     // then keeps its rows of h in LDS for the residual adds
     int own_h;
+    // the attention output is handed to phase C quantised (Q8_0 O matrix, no sub-norm)
+    int att_q8;
 };
 
 constexpr int kOwnRows = 256;  // rows of h one workgroup can keep

@@ -455,7 +455,7 @@ __device__ __forceinline__ bool phase_b(const LoopArgs& g, const LayerDev& L, in
     const int kvh = g.kv_heads, hpk = g.heads / kvh, hd = g.head_dim, Lc = pos + 1;
     const unsigned tin = tag_of(g, step, l, 1), tout = tag_of(g, step, l, 2);
     const AttnArgs a = attn_args(g, L);
-    const TaggedOut o{g.attt, g.pacct, g.pmlt, tout, g.error};
+    const TaggedOut o{g.attt, g.pacct, g.pmlt, tout, g.error, g.att_q8, g.heads * g.head_dim};
     AttnLds& s = lds.att;
     if (attn_is_exact(Lc, hpk) && Lc <= kSplit * kPoolChunks) {
         if (static_cast<int>(blockIdx.x) >= kvh) return true;
@@ -514,7 +514,12 @@ __device__ __forceinline__ bool phase_c(const LoopArgs& g, const LayerDev& L, in
         row0 = static_cast<uint32_t>(t) * R;
     };
     auto ready = [&]() -> bool {
-        if (!tget_vec(g, g.attt, tag_of(g, step, l, 2), s.x, g.heads * g.head_dim)) return false;
+        const int n = g.heads * g.head_dim;
+        if (g.att_q8)  // already quantised by the attention: straight into the activation LDS
+            return tget_segs<>(g, tag_of(g, step, l, 2), TSeg{g.attt, reinterpret_cast<float*>(s.a.xs), n / 4},
+                               TSeg{g.attt + n / 4, s.a.xd, n / 32},
+                               TSeg{g.attt + n / 4 + n / 32, reinterpret_cast<float*>(s.a.xsum), n / 32});
+        if (!tget_vec(g, g.attt, tag_of(g, step, l, 2), s.x, n)) return false;
         prologue_lds<TO>(L.o, L.attn_sub, g.eps, s);
         return true;
     };

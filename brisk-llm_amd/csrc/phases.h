@@ -120,7 +120,36 @@ struct TaggedOut {
     unsigned long long* part_ml;
     unsigned tag;
     int* error;
-    __device__ __forceinline__ void att(int i, float v) const { tput(out + i, v, tag); }
+    int q8;      // publish the attention output quantised (Q8_0), see att_q8_0
+    int total;   // values of the whole attention output (heads x head size)
+    __device__ __forceinline__ void att(int i, float v) const {
+        if (q8) att_q8_0(i, v);
+        else tput(out + i, v, tag);
+    }
+    // The consumer (the O projection, no sub-norm) takes the attention output
+    // as quantize_q8_0 makes it (src/quant.cpp:115-142), so the producer
+    // quantises it here and publishes the blocks: words [0, total / 4) hold the
+    // int8 values four a word, then total / 32 fp16-rounded scales (as floats),
+    // then total / 32 block sums.  One value a lane: lanes 32 k .. 32 k + 31 hold
+    // a block, and all of them call together.
+    __device__ __forceinline__ void att_q8_0(int i, float v) const {
+        float amax = group_reduce<16>(fabsf(v), [](float a, float b) { return fmaxf(a, b); });
+        amax = fmaxf(amax, __shfl_xor(amax, 16, 64));
+        const float d = amax / 127.0f;
+        const float inv = d != 0.0f ? 1.0f / d : 0.0f;
+        const int q = static_cast<int>(rintf(v * inv));
+        int sum = group_reduce<16>(q, [](int a, int b) { return a + b; });
+        sum += __shfl_xor(sum, 16, 64);
+        const int q1 = __shfl_down(q, 1, 64), q2 = __shfl_down(q, 2, 64), q3 = __shfl_down(q, 3, 64);
+        if ((i & 3) == 0) {
+            const uint32_t w = (q & 0xFF) | ((q1 & 0xFF) << 8) | ((q2 & 0xFF) << 16) | (static_cast<uint32_t>(q3) << 24);
+            tput(out + i / 4, __uint_as_float(w), tag);
+        }
+        if ((i & 31) == 0) {
+            tput(out + total / 4 + i / 32, h2f(f2h(d)), tag);
+            tput(out + total / 4 + total / 32 + i / 32, __int_as_float(sum), tag);
+        }
+    }
     __device__ __forceinline__ void pacc(size_t i, float v) const { tput(part_acc + i, v, tag); }
     __device__ __forceinline__ void pml(size_t i, float v) const { tput(part_ml + i, v, tag); }
     __device__ bool wait(const unsigned long long* p, float& v) const {
