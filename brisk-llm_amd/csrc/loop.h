@@ -39,7 +39,8 @@ struct LoopArgs {
     int fixed;                 // seq[0, fixed) are caller tokens
     int pos0, n_steps, first_full;  // steps >= first_full compute the output projection and pick
     int* error;                // set when a barrier wait expires
-    unsigned long long* trace; // optional: workgroup 0's wall clock after each barrier
+    unsigned long long* trace; // optional: wall clocks of the phases (workgroup 0; every workgroup at one step/layer)
+    int trace_step, trace_layer;
     int R_qkv[3], tiles_qkv[3];
     int R_o, tiles_o, R_gu, tiles_gu, R_d, tiles_d, R_h, tiles_h;
     // O and down tiles cover the same rows of h on the same workgroup, which

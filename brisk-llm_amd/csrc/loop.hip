@@ -144,6 +144,28 @@ union LoopLds {
     AttnPoolLds pool;
 };
 
+// Trace: workgroup 0's wall clock at point `pt` of phase `ph` of every (step,
+// layer), and every workgroup's at one chosen (step, layer) (trace_step, trace_layer).
+struct Stamps {
+    unsigned long long* w0;
+    unsigned long long* all;
+};
+constexpr int kTraceW0 = 65536, kTraceAll = 1 << 19;
+__device__ __forceinline__ Stamps pst_ptr(const LoopArgs& g, int step, int l, int ph) {
+    Stamps st{nullptr, nullptr};
+    if (g.trace == nullptr) return st;
+    if (blockIdx.x == 0) st.w0 = g.trace + kTraceW0 + (static_cast<size_t>(step * g.n_layers + l) * 8 + ph) * 8;
+    if (step == g.trace_step && l == g.trace_layer) st.all = g.trace + kTraceAll + static_cast<size_t>(ph) * 8 * 1024;
+    return st;
+}
+__device__ __forceinline__ void pst(const Stamps& st, int pt) {
+    if (threadIdx.x == 0 && (st.w0 != nullptr || st.all != nullptr)) {
+        const unsigned long long t = wall_clock64();
+        if (st.w0 != nullptr) st.w0[pt] = t;
+        if (st.all != nullptr) st.all[pt * 1024 + blockIdx.x] = t;
+    }
+}
+
 __device__ __forceinline__ unsigned tag_of(const LoopArgs& g, int step, int layer, int phase) {
     return g.tag_base + static_cast<unsigned>((step * g.n_layers + layer) * 8 + phase);
 }
@@ -174,7 +196,8 @@ __host__ __device__ constexpr int head_units(uint32_t type) { return (type == kQ
 // epilogue.  `ready()` waits for the input and prepares the activation; it runs
 // once, after the first tile's loads are issued.  Returns false when abandoning.
 template <uint32_t T, int M, class RowOf, class Ready, class Done>
-__device__ __forceinline__ bool run_tiles(int total, GemvLds& s, RowOf row_of, Ready ready, Done done) {
+__device__ __forceinline__ bool run_tiles(int total, GemvLds& s, RowOf row_of, Ready ready, Done done,
+                                          Stamps st = Stamps{nullptr, nullptr}) {
     const int G = static_cast<int>(gridDim.x);
     int t = static_cast<int>(blockIdx.x);
     if (t >= total) return true;
@@ -191,9 +214,11 @@ __device__ __forceinline__ bool run_tiles(int total, GemvLds& s, RowOf row_of, R
     const uint32_t units = ma.cols / Unit<T>::kElems, stride = term_stride(units);
     int gfirst = t, grows = 0;
     auto flush = [&]() -> bool {
+        pst(st, 3);
         __syncthreads();
         row_sums(s.terms, stride, units, grows, s.sums);
         __syncthreads();
+        pst(st, 4);
         int off = 0;
         for (int u = gfirst; off < grows; u += G) {
             Packed mu;
@@ -244,12 +269,15 @@ __device__ __forceinline__ bool phase_a(const LoopArgs& g, const LayerDev& L, in
     const int nq = g.tiles_qkv[0] + g.tiles_qkv[1];
     const int total = nq + g.tiles_qkv[2];
     const unsigned tag = tag_of(g, step, l, 1);
+    const Stamps st = pst_ptr(g, step, l, 0);
     auto input = [&]() -> bool {
         if (l == 0) {
             embed_to_lds(g, token, s);
             return true;
         }
-        return tget_vec(g, g.ht, tag_of(g, step, l - 1, 5), s.x, g.embd_dim);
+        const bool ok = tget_vec(g, g.ht, tag_of(g, step, l - 1, 5), s.x, g.embd_dim);
+        pst(st, 1);
+        return ok;
     };
     auto row_of = [&](int t, Packed& m, uint32_t& row0, int& R) {
         const int i = t < g.tiles_qkv[0] ? 0 : t < nq ? 1 : 2;
@@ -269,8 +297,9 @@ __device__ __forceinline__ bool phase_a(const LoopArgs& g, const LayerDev& L, in
         return run_tiles<TQ, kLoopUnits>(total, s, row_of, [&]() -> bool {
             if (!input()) return false;
             prologue_lds<TQ>(L.q, L.attn_norm, g.eps, s);
+            pst(st, 2);
             return true;
-        }, done);
+        }, done, st);
     }
     // Q and K in their format, then V's tiles (same activation family, its own width)
     if (static_cast<int>(blockIdx.x) >= total) return true;
@@ -298,12 +327,12 @@ __device__ __forceinline__ bool phase_a(const LoopArgs& g, const LayerDev& L, in
     return true;
 }
 
-__device__ __forceinline__ AttnArgs attn_args(const LoopArgs& g, const LayerDev& L) {
+__device__ __forceinline__ AttnArgs attn_args(const LoopArgs& g, const LayerDev& L, int step, int l) {
     AttnArgs a{};
     a.qnorm = L.q_norm; a.knorm = L.k_norm; a.rope = g.rope; a.eps = g.eps; a.neox = g.neox;
     a.kcache = L.kc; a.vcache = L.vc; a.ctx = g.ctx; a.head_dim = g.head_dim; a.heads = g.heads;
     a.kv_heads = g.kv_heads; a.scale = g.scale; a.max_splits = g.max_splits;
-    a.stamps = g.trace != nullptr ? g.trace + 60000 : nullptr;
+    a.stamps = g.trace != nullptr ? g.trace + 65536 + (static_cast<size_t>(step * g.n_layers + l) * 8 + 1) * 8 : nullptr;
     return a;
 }
 
@@ -454,7 +483,7 @@ __device__ __forceinline__ bool attn_slot_merge(const LoopArgs& lg, const AttnAr
 __device__ __forceinline__ bool phase_b(const LoopArgs& g, const LayerDev& L, int step, int l, int pos, LoopLds& lds) {
     const int kvh = g.kv_heads, hpk = g.heads / kvh, hd = g.head_dim, Lc = pos + 1;
     const unsigned tin = tag_of(g, step, l, 1), tout = tag_of(g, step, l, 2);
-    const AttnArgs a = attn_args(g, L);
+    const AttnArgs a = attn_args(g, L, step, l);
     const TaggedOut o{g.attt, g.pacct, g.pmlt, tout, g.error, g.att_q8, g.heads * g.head_dim};
     AttnLds& s = lds.att;
     if (attn_is_exact(Lc, hpk) && Lc <= kSplit * kPoolChunks) {
@@ -468,7 +497,9 @@ __device__ __forceinline__ bool phase_b(const LoopArgs& g, const LayerDev& L, in
             __builtin_amdgcn_s_waitcnt(0);
             return false;
         }
+        pst(pst_ptr(g, step, l, 1), 1);
         attn_finish_prologue<true>(a, sp.a, kv, pos, true, false);
+        pst(pst_ptr(g, step, l, 1), 2);
         if (hd == 128) attn_exact_pool<128>(a, sp, kv, Lc, o);
         else if (hd == 64) attn_exact_pool<64>(a, sp, kv, Lc, o);
         else attn_exact_pool<0>(a, sp, kv, Lc, o);
@@ -508,6 +539,7 @@ __device__ __forceinline__ bool phase_c(const LoopArgs& g, const LayerDev& L, in
                                         float* hown) {
     const unsigned tag = tag_of(g, step, l, 3), tprev = tag_of(g, step, l - 1, 5);
     const int G = static_cast<int>(gridDim.x);
+    const Stamps st = pst_ptr(g, step, l, 2);
     auto row_of = [&](int t, Packed& m, uint32_t& row0, int& R) {
         m = L.o;
         R = g.R_o;
@@ -515,10 +547,13 @@ __device__ __forceinline__ bool phase_c(const LoopArgs& g, const LayerDev& L, in
     };
     auto ready = [&]() -> bool {
         const int n = g.heads * g.head_dim;
-        if (g.att_q8)  // already quantised by the attention: straight into the activation LDS
-            return tget_segs<>(g, tag_of(g, step, l, 2), TSeg{g.attt, reinterpret_cast<float*>(s.a.xs), n / 4},
+        if (g.att_q8) {  // already quantised by the attention: straight into the activation LDS
+            const bool ok = tget_segs<>(g, tag_of(g, step, l, 2), TSeg{g.attt, reinterpret_cast<float*>(s.a.xs), n / 4},
                                TSeg{g.attt + n / 4, s.a.xd, n / 32},
                                TSeg{g.attt + n / 4 + n / 32, reinterpret_cast<float*>(s.a.xsum), n / 32});
+            pst(st, 1);
+            return ok;
+        }
         if (!tget_vec(g, g.attt, tag_of(g, step, l, 2), s.x, n)) return false;
         prologue_lds<TO>(L.o, L.attn_sub, g.eps, s);
         return true;
@@ -538,7 +573,7 @@ __device__ __forceinline__ bool phase_c(const LoopArgs& g, const LayerDev& L, in
         }
         return g.own_h || !__syncthreads_or(!ok);
     };
-    return run_tiles<TO, kLoopUnits>(g.tiles_o, s, row_of, ready, done);
+    return run_tiles<TO, kLoopUnits>(g.tiles_o, s, row_of, ready, done, st);
 }
 
 // D: gate/up rows of ffn_norm(h), the gated activation.  A tile is R gate rows
@@ -555,8 +590,11 @@ __device__ __forceinline__ bool phase_d(const LoopArgs& g, const LayerDev& L, in
     uint32_t row0 = static_cast<uint32_t>(t) * R;
     tg.load(L.gate, row0, R);
     tu.load(L.up, row0, R);
+    const Stamps st = pst_ptr(g, step, l, 3);
     if (!tget_vec(g, g.ht, tag_of(g, step, l, 3), s.x, g.embd_dim)) return false;
+    pst(st, 1);
     prologue_lds<TG>(L.gate, L.ffn_norm, g.eps, s);
+    pst(st, 2);
     int gfirst = t, grows = 0;
     while (true) {
         tg.terms(L.gate, s.a, s.terms + grows * stride);
@@ -570,9 +608,11 @@ __device__ __forceinline__ bool phase_d(const LoopArgs& g, const LayerDev& L, in
             tu.load(L.up, row0, R);
         }
         if (last || (grows + 2 * R) * static_cast<int>(stride) > kTermCap || grows + 2 * R > kGroupRows) {
+            pst(st, 3);
             __syncthreads();
             row_sums(s.terms, stride, units, grows, s.sums);
             __syncthreads();
+            pst(st, 4);
             for (int u = gfirst, off = 0; off < grows; u += G, off += 2 * R) {
                 const uint32_t r = threadIdx.x, r0 = static_cast<uint32_t>(u) * R;
                 if (r < static_cast<uint32_t>(R) && r0 + r < L.gate.rows) {
@@ -596,10 +636,6 @@ __device__ __forceinline__ bool phase_d(const LoopArgs& g, const LayerDev& L, in
     return true;
 }
 
-__device__ __forceinline__ void stamp(const LoopArgs& g, int i) {
-    if (g.trace != nullptr && blockIdx.x == 0 && threadIdx.x == 0) g.trace[50000 + i] = wall_clock64();
-}
-
 // F: down rows of act, h += down act (residual rows from the own copy with own_h).
 template <uint32_t TD>
 __device__ __forceinline__ bool phase_f(const LoopArgs& g, const LayerDev& L, int step, int l, GemvLds& s, float* hown) {
@@ -610,12 +646,12 @@ __device__ __forceinline__ bool phase_f(const LoopArgs& g, const LayerDev& L, in
         R = g.R_d;
         row0 = static_cast<uint32_t>(t) * R;
     };
+    const Stamps st = pst_ptr(g, step, l, 4);
     auto ready = [&]() -> bool {
-        stamp(g, 0);
         if (!tget_vec(g, g.actt, tag_of(g, step, l, 4), s.x, g.ff)) return false;
-        stamp(g, 1);
+        pst(st, 1);
         prologue_lds<TD>(L.down, L.ffn_sub, g.eps, s);
-        stamp(g, 2);
+        pst(st, 2);
         return true;
     };
     auto done = [&](int t, const Packed& m, uint32_t row0, const float* sums) -> bool {
@@ -630,10 +666,9 @@ __device__ __forceinline__ bool phase_f(const LoopArgs& g, const LayerDev& L, in
             if (ok) tput(g.ht + row, h, tag);
             if (g.own_h) hown[slot] = h;
         }
-        stamp(g, 3);
         return g.own_h || !__syncthreads_or(!ok);
     };
-    return run_tiles<TD, kLoopUnits>(g.tiles_d, s, row_of, ready, done);
+    return run_tiles<TD, kLoopUnits>(g.tiles_d, s, row_of, ready, done, st);
 }
 
 // H: output rows of output_norm(h) -> logits; the workgroup's best key folded
@@ -733,19 +768,29 @@ __global__ __launch_bounds__(kThreads) void k_loop(LoopArgs g) {
         for (int l = 0; l < g.n_layers; ++l) {
             const LayerDev& L = g.layers[l];
             if (g.trace != nullptr && blockIdx.x == 0 && threadIdx.x == 0) g.trace[1 + (step * g.n_layers + l) * 5] = wall_clock64();
+            pst(pst_ptr(g, step, l, 0), 0);
             if (!phase_a<TQ, TV>(g, L, step, l, token, lds.g)) return;
+            pst(pst_ptr(g, step, l, 0), 7);
             __syncthreads();
             if (g.trace != nullptr && blockIdx.x == 0 && threadIdx.x == 0) g.trace[2 + (step * g.n_layers + l) * 5] = wall_clock64();
+            pst(pst_ptr(g, step, l, 1), 0);
             if (!phase_b(g, L, step, l, pos, lds)) return;
+            pst(pst_ptr(g, step, l, 1), 7);
             __syncthreads();
             if (g.trace != nullptr && blockIdx.x == 0 && threadIdx.x == 0) g.trace[3 + (step * g.n_layers + l) * 5] = wall_clock64();
+            pst(pst_ptr(g, step, l, 2), 0);
             if (!phase_c<TO>(g, L, step, l, token, lds.g, hown)) return;
+            pst(pst_ptr(g, step, l, 2), 7);
             __syncthreads();
             if (g.trace != nullptr && blockIdx.x == 0 && threadIdx.x == 0) g.trace[4 + (step * g.n_layers + l) * 5] = wall_clock64();
+            pst(pst_ptr(g, step, l, 3), 0);
             if (!phase_d<TG>(g, L, step, l, lds.g)) return;
+            pst(pst_ptr(g, step, l, 3), 7);
             __syncthreads();
             if (g.trace != nullptr && blockIdx.x == 0 && threadIdx.x == 0) g.trace[5 + (step * g.n_layers + l) * 5] = wall_clock64();
+            pst(pst_ptr(g, step, l, 4), 0);
             if (!phase_f<TD>(g, L, step, l, lds.g, hown)) return;
+            pst(pst_ptr(g, step, l, 4), 7);
             __syncthreads();
         }
         if (full && !phase_h<TH>(g, step, lds.g)) return;

@@ -419,6 +419,8 @@ void Session::run_loop(size_t pos0, size_t n_steps, size_t first_full, size_t fi
     g.first_full = static_cast<int>(first_full);
     g.fixed = static_cast<int>(fixed);
     g.trace = trace_;
+    g.trace_step = g.trace_layer = -1;
+    if (const char* e = std::getenv("BRISK_HIP_TRACE_AT")) std::sscanf(e, "%d,%d", &g.trace_step, &g.trace_layer);
     // tags: 255 launch slots of 2^24 step/layer/phase indices; the words are
     // cleared each time the slots wrap, so a stale word never carries a live tag
     if (launches_ % 255 == 0) check(hipMemsetAsync(tagged_, 0, tagged_words_ * 8, stream_), "memset(tagged)");

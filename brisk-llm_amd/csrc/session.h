@@ -114,7 +114,7 @@ private:
     size_t launches_ = 0;
     int* loop_error_ = nullptr;
     unsigned long long* trace_ = nullptr;
-    static constexpr size_t kTraceSlots = 1 << 16;
+    static constexpr size_t kTraceSlots = 1 << 20;
     bool debug_ = false;
     // batched prefill (int8 MFMA), buffers for kPrefillTokens tokens, allocated on first use
     static constexpr int kPrefillTokens = 512;
