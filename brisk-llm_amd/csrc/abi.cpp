@@ -166,6 +166,18 @@ int brisk_hip_expf(const float* x, float* y, size_t n, void* stream) {
     return guarded([&] { hip_check(bh::launch_expf(x, y, n, static_cast<hipStream_t>(stream)), "expf"); });
 }
 
+int brisk_hip_div_selftest(unsigned long long* mismatches) {
+    return guarded([&] {
+        unsigned long long* d = nullptr;
+        hip_check(hipMalloc(&d, 24), "hipMalloc");
+        hipError_t e = hipMemset(d, 0, 24);
+        if (e == hipSuccess) e = bh::launch_div_selftest(d, nullptr);
+        if (e == hipSuccess) e = hipMemcpy(mismatches, d, 24, hipMemcpyDeviceToHost);
+        hipFree(d);
+        hip_check(e, "div selftest");
+    });
+}
+
 int brisk_hip_session_create(const brisk_hip_config* config, const brisk_hip_tensor* tensors, size_t n_tensors, size_t max_context,
                              int device, brisk_hip_session** out) {
     return guarded([&] {

@@ -12,6 +12,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <type_traits>
+
 #include "layout.h"
 
 namespace bh {
@@ -27,8 +29,10 @@ __device__ __forceinline__ float h2f(uint16_t h) { return static_cast<float>(__b
 
 // float -> IEEE half, round to nearest even, with the reference's handling of
 // overflow (infinity), underflow (signed zero) and NaN (quiet, payload
-// dropped): src/quant.cpp:87-113, written out on the bits.
-__device__ __forceinline__ uint16_t f2h(float f) {
+// dropped): src/quant.cpp:87-113, written out on the bits.  f2h below is the
+// hardware conversion; brisk_hip_div_selftest checks the two agree on every
+// float.
+__device__ __forceinline__ uint16_t f2h_bits(float f) {
     const uint32_t bits = __float_as_uint(f);
     const uint32_t sign = (bits >> 16) & 0x8000u;
     const int32_t exponent = static_cast<int32_t>((bits >> 23) & 0xFF) - 127 + 15;
@@ -48,6 +52,13 @@ __device__ __forceinline__ uint16_t f2h(float f) {
     const uint32_t rem = mantissa & 0x1FFFu;
     if (rem > 0x1000u || (rem == 0x1000u && (half & 1))) ++half;
     return static_cast<uint16_t>(sign | half);
+}
+
+// The same conversion by v_cvt_f16_f32 (IEEE round to nearest even, half
+// denormals kept), with NaN mapped to the reference's quiet NaN.
+__device__ __forceinline__ uint16_t f2h(float f) {
+    const uint16_t h = __builtin_bit_cast(uint16_t, static_cast<_Float16>(f));
+    return f != f ? static_cast<uint16_t>(((__float_as_uint(f) >> 16) & 0x8000u) | 0x7E00u) : h;
 }
 
 // ---------------------------------------------------------------- exp
@@ -209,10 +220,46 @@ __device__ __forceinline__ double block_sumsq(const float* x, int n, double* red
     return ((red[0] + red[1]) + red[2]) + red[3];
 }
 
-// rms_norm's scale (src/model.cpp:91-92).
+// ---------------------------------------------------------------- short exact divisions
+//
+// IEEE-correct division is a long dependent chain (scale, reciprocal, four
+// FMAs, fix-up).  Two quotients the quantisation chain needs have shorter
+// exact forms; brisk_hip_div_selftest compares both with IEEE division on
+// every input they take.
+
+// a / 127.0f, correctly rounded, for every finite a >= 0: a times RN(1/127),
+// corrected once by the FMA residual.
+__device__ __forceinline__ float div127(float a) {
+    const float c = 0x1.020408p-7f;  // RN(1/127)
+    const float q0 = a * c;
+    return __builtin_fmaf(__builtin_fmaf(-q0, 127.0f, a), c, q0);
+}
+
+// 1.0f / d, correctly rounded: the hardware reciprocal corrected once by the
+// FMA residual, exact for 2^-126 <= |d| < 2^126; other d take IEEE division.
+__device__ __forceinline__ float rcp_rn(float d) {
+    const float ad = fabsf(d);
+    const bool slow = !(ad >= 0x1p-126f && ad < 0x1p126f);
+    const float y0 = __builtin_amdgcn_rcpf(d);
+    float y = __builtin_fmaf(__builtin_fmaf(-d, y0, 1.0f), y0, y0);
+    // a wave-uniform branch, so the long division is not computed beside the short one
+    if (__builtin_expect(__builtin_amdgcn_ballot_w64(slow) != 0, 0)) {
+        if (slow) y = 1.0f / d;
+    }
+    return y;
+}
+
+// max of two non-negative floats (|x| values): their bit patterns order the same way.
+__device__ __forceinline__ float nnmax(float a, float b) {
+    return __uint_as_float(max(__float_as_uint(a), __float_as_uint(b)));
+}
+
+// rms_norm's scale (src/model.cpp:91-92).  sum / n is a multiplication when n
+// is a power of two (exact, so the same double).
 __device__ __forceinline__ float rms_scale(double sum, int n, float eps) {
-    const float mean = static_cast<float>(sum / static_cast<double>(n));
-    return 1.0f / sqrtf(mean + eps);
+    const double m = (n & (n - 1)) == 0 ? sum * (1.0 / static_cast<double>(n)) : sum / static_cast<double>(n);
+    const float mean = static_cast<float>(m);
+    return rcp_rn(sqrtf(mean + eps));
 }
 
 // ---------------------------------------------------------------- memory policies
@@ -265,8 +312,8 @@ __device__ inline void act_q8_0(const float* x, const float* w, float scale, int
         }
         float amax = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
         amax = group_reduce<8>(amax, [](float a, float b) { return fmaxf(a, b); });
-        const float d = amax / 127.0f;
-        const float inv = d != 0.0f ? 1.0f / d : 0.0f;
+        const float d = div127(amax);
+        const float inv = d != 0.0f ? rcp_rn(d) : 0.0f;
         int q[4], sum = 0;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
@@ -318,7 +365,7 @@ __device__ inline void act_q8_k(const float* x, const float* w, float scale, int
         } else {
             const float extreme = bits == 7 ? 63.0f : 127.0f;
             const float inv = -extreme / sel;
-            d = 1.0f / inv;
+            d = rcp_rn(inv);
 #pragma unroll
             for (int i = 0; i < 4; ++i) q[i] = static_cast<int>(fminf(127.0f, rintf(inv * v[i])));
         }
@@ -345,6 +392,23 @@ struct ActRegs {
 
 __device__ __forceinline__ float4 ld4(const float* p) { return *reinterpret_cast<const float4*>(p); }
 
+// The norm weight's chunks alone (before the input is ready), then the input's.
+__device__ __forceinline__ void act_issue_w(ActRegs& r, const float* w, int cols) {
+#pragma unroll
+    for (int c = 0; c < kActRegChunks; ++c) {
+        const int base = (c * kThreads + static_cast<int>(threadIdx.x)) * 4;
+        if (base < cols && w != nullptr) r.w[c] = ld4(w + base);
+    }
+}
+template <class IO = PlainIO>
+__device__ __forceinline__ void act_issue_x(ActRegs& r, const float* x, int cols) {
+#pragma unroll
+    for (int c = 0; c < kActRegChunks; ++c) {
+        const int base = (c * kThreads + static_cast<int>(threadIdx.x)) * 4;
+        if (base < cols) r.x[c] = IO::ld4(x + base);
+    }
+}
+
 template <class IO = PlainIO>
 __device__ __forceinline__ void act_issue(ActRegs& r, const float* x, const float* w, int cols) {
 #pragma unroll
@@ -361,10 +425,10 @@ __device__ __forceinline__ void act_issue(ActRegs& r, const float* x, const floa
 // block's 8 lanes, d = amax / 127, q = rint(v / d), the half-rounded d and the
 // block sum to LDS.
 __device__ __forceinline__ void quant_piece_q8_0(const float v[4], int base, ActLds& a) {
-    float amax = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
-    amax = group_reduce<8>(amax, [](float a, float b) { return fmaxf(a, b); });
-    const float d = amax / 127.0f;
-    const float inv = d != 0.0f ? 1.0f / d : 0.0f;
+    float amax = nnmax(nnmax(fabsf(v[0]), fabsf(v[1])), nnmax(fabsf(v[2]), fabsf(v[3])));
+    amax = group_reduce<8>(amax, [](float a, float b) { return nnmax(a, b); });
+    const float d = div127(amax);
+    const float inv = d != 0.0f ? rcp_rn(d) : 0.0f;
     int q[4], sum = 0;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -376,6 +440,51 @@ __device__ __forceinline__ void quant_piece_q8_0(const float v[4], int base, Act
     if ((threadIdx.x & 7) == 0) {
         a.xd[base / 32] = h2f(f2h(d));
         a.xsum[base / 32] = sum;
+    }
+}
+
+// quant_piece_q8_0 of N pieces at once (their chains interleave).
+template <int N>
+__device__ __forceinline__ void quant_pieces_q8_0(const float (&v)[N][4], const int (&base)[N], int cols, ActLds& a) {
+    float amax[N], d[N], inv[N];
+    int q[N][4], sum[N];
+#pragma unroll
+    for (int k = 0; k < N; ++k) amax[k] = nnmax(nnmax(fabsf(v[k][0]), fabsf(v[k][1])), nnmax(fabsf(v[k][2]), fabsf(v[k][3])));
+#pragma unroll
+    for (int k = 0; k < N; ++k) amax[k] = nnmax(amax[k], dpp<kDppXor1>(amax[k]));
+#pragma unroll
+    for (int k = 0; k < N; ++k) amax[k] = nnmax(amax[k], dpp<kDppXor2>(amax[k]));
+#pragma unroll
+    for (int k = 0; k < N; ++k) amax[k] = nnmax(amax[k], dpp<kDppHalfMirror>(amax[k]));
+#pragma unroll
+    for (int k = 0; k < N; ++k) {
+        d[k] = div127(amax[k]);
+        inv[k] = d[k] != 0.0f ? rcp_rn(d[k]) : 0.0f;
+    }
+#pragma unroll
+    for (int k = 0; k < N; ++k) {
+        sum[k] = 0;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            q[k][i] = static_cast<int>(rintf(v[k][i] * inv[k]));
+            sum[k] += q[k][i];
+        }
+    }
+#pragma unroll
+    for (int k = 0; k < N; ++k) sum[k] += dpp<kDppXor1>(sum[k]);
+#pragma unroll
+    for (int k = 0; k < N; ++k) sum[k] += dpp<kDppXor2>(sum[k]);
+#pragma unroll
+    for (int k = 0; k < N; ++k) sum[k] += dpp<kDppHalfMirror>(sum[k]);
+#pragma unroll
+    for (int k = 0; k < N; ++k) {
+        if (base[k] < cols) {
+            a.xs[base[k] / 4] = (q[k][0] & 0xFF) | ((q[k][1] & 0xFF) << 8) | ((q[k][2] & 0xFF) << 16) | (q[k][3] << 24);
+            if ((threadIdx.x & 7) == 0) {
+                a.xd[base[k] / 32] = h2f(f2h(d[k]));
+                a.xsum[base[k] / 32] = sum[k];
+            }
+        }
     }
 }
 
@@ -402,7 +511,7 @@ __device__ __forceinline__ void quant_piece_q8_k(const float v[4], int base, int
     } else {
         const float extreme = bits == 7 ? 63.0f : 127.0f;
         const float inv = -extreme / sel;
-        d = 1.0f / inv;
+        d = rcp_rn(inv);
 #pragma unroll
         for (int i = 0; i < 4; ++i) q[i] = static_cast<int>(fminf(127.0f, rintf(inv * v[i])));
     }
@@ -443,6 +552,33 @@ __device__ inline void act_finish(const ActRegs& r, const float* x, const float*
         if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = s;
         __syncthreads();
         scale = rms_scale(((red[0] + red[1]) + red[2]) + red[3], cols, eps);
+    }
+    if (!q8k && nch <= kActRegChunks) {  // Q8_0 from registers: all pieces together
+        auto run = [&](auto n_tag) {
+            constexpr int N = decltype(n_tag)::value;
+            float v[N][4];
+            int base[N];
+#pragma unroll
+            for (int k = 0; k < N; ++k) {
+                base[k] = (k * kThreads + static_cast<int>(threadIdx.x)) * 4;
+                const float4 xv = r.x[k];
+                v[k][0] = xv.x; v[k][1] = xv.y; v[k][2] = xv.z; v[k][3] = xv.w;
+                if (w != nullptr) {
+                    const float4 wv = r.w[k];
+                    v[k][0] = v[k][0] * scale * wv.x; v[k][1] = v[k][1] * scale * wv.y;
+                    v[k][2] = v[k][2] * scale * wv.z; v[k][3] = v[k][3] * scale * wv.w;
+                }
+            }
+            quant_pieces_q8_0<N>(v, base, cols, a);
+        };
+        switch (nch) {
+            case 1: run(std::integral_constant<int, 1>{}); break;
+            case 2: run(std::integral_constant<int, 2>{}); break;
+            case 3: run(std::integral_constant<int, 3>{}); break;
+            default: run(std::integral_constant<int, 4>{}); break;
+        }
+        __syncthreads();
+        return;
     }
     auto piece = [&](float4 xv, float4 wv, int base) {
         float v[4] = {xv.x, xv.y, xv.z, xv.w};

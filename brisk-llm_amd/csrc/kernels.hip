@@ -296,6 +296,35 @@ __global__ void k_expf(const float* __restrict__ x, float* __restrict__ y, size_
     if (i < n) y[i] = ref_expf(x[i]);
 }
 
+// The short exact divisions of device.h against IEEE division, over every
+// input: bad[0] counts div127 mismatches (finite a >= 0), bad[1] rcp_rn
+// mismatches (finite d != 0), bad[2] hardware f2h against the bit-level
+// conversion (every float).
+__global__ void k_div_selftest(unsigned long long* bad) {
+    const unsigned long long stride = static_cast<unsigned long long>(gridDim.x) * blockDim.x;
+    unsigned long long n127 = 0, nrcp = 0;
+    for (unsigned long long j = static_cast<unsigned long long>(blockIdx.x) * blockDim.x + threadIdx.x; j < (1ull << 32); j += stride) {
+        const uint32_t i = static_cast<uint32_t>(j);
+        if ((i & 0x7F800000u) == 0x7F800000u) continue;  // inf, NaN
+        const float x = __uint_as_float(i);
+        if ((i >> 31) == 0 && __float_as_uint(div127(x)) != __float_as_uint(__fdiv_rn(x, 127.0f))) ++n127;
+        if ((i & 0x7FFFFFFFu) != 0 && __float_as_uint(rcp_rn(x)) != __float_as_uint(__fdiv_rn(1.0f, x))) ++nrcp;
+    }
+    if (n127 != 0) atomicAdd(bad, n127);
+    if (nrcp != 0) atomicAdd(bad + 1, nrcp);
+    unsigned long long nh = 0;
+    for (unsigned long long j = static_cast<unsigned long long>(blockIdx.x) * blockDim.x + threadIdx.x; j < (1ull << 32); j += stride) {
+        const float x = __uint_as_float(static_cast<uint32_t>(j));
+        if (f2h(x) != f2h_bits(x)) ++nh;
+    }
+    if (nh != 0) atomicAdd(bad + 2, nh);
+}
+
+hipError_t launch_div_selftest(unsigned long long* bad, hipStream_t s) {
+    hipLaunchKernelGGL(k_div_selftest, dim3(8192), dim3(256), 0, s, bad);
+    return hipGetLastError();
+}
+
 hipError_t launch_expf(const float* x, float* y, size_t n, hipStream_t s) {
     if (n == 0) return hipSuccess;
     hipLaunchKernelGGL(k_expf, dim3(static_cast<unsigned>((n + 255) / 256)), dim3(256), 0, s, x, y, n);

@@ -48,6 +48,8 @@ struct LoopArgs {
     int own_h;
     // the attention output is handed to phase C quantised (Q8_0 O matrix, no sub-norm)
     int att_q8;
+    // exact attention one workgroup per query head (else one per key/value head)
+    int head_attn;
 };
 
 constexpr int kOwnRows = 256;  // rows of h one workgroup can keep

@@ -171,11 +171,11 @@ __device__ __forceinline__ unsigned tag_of(const LoopArgs& g, int step, int laye
 }
 
 // Quantised activation of the input vector in s.x (rms_norm'd by w when given).
+// The norm weight chunks are in `ar` already (act_issue_w, before the input wait).
 template <uint32_t T>
-__device__ __forceinline__ void prologue_lds(const Packed& m, const float* w, float eps, GemvLds& s) {
-    ActRegs ar;
+__device__ __forceinline__ void prologue_lds(const Packed& m, ActRegs& ar, const float* w, float eps, GemvLds& s) {
     const int cols = static_cast<int>(m.cols);
-    act_issue<PlainIO>(ar, s.x, w, cols);
+    act_issue_x<PlainIO>(ar, s.x, cols);
     act_finish<PlainIO>(ar, s.x, w, eps, cols, takes_q8_k(T), act_bits(m), s.a, s.red);
 }
 
@@ -295,8 +295,10 @@ __device__ __forceinline__ bool phase_a(const LoopArgs& g, const LayerDev& L, in
     };
     if (TQ == TV) {
         return run_tiles<TQ, kLoopUnits>(total, s, row_of, [&]() -> bool {
+            ActRegs ar;
+            act_issue_w(ar, L.attn_norm, static_cast<int>(L.q.cols));
             if (!input()) return false;
-            prologue_lds<TQ>(L.q, L.attn_norm, g.eps, s);
+            prologue_lds<TQ>(L.q, ar, L.attn_norm, g.eps, s);
             pst(st, 2);
             return true;
         }, done, st);
@@ -305,9 +307,11 @@ __device__ __forceinline__ bool phase_a(const LoopArgs& g, const LayerDev& L, in
     if (static_cast<int>(blockIdx.x) >= total) return true;
     bool have_input = false;
     if (!run_tiles<TQ, kLoopUnits>(nq, s, row_of, [&]() -> bool {
+            ActRegs ar;
+            act_issue_w(ar, L.attn_norm, static_cast<int>(L.q.cols));
             if (!input()) return false;
             have_input = true;
-            prologue_lds<TQ>(L.q, L.attn_norm, g.eps, s);
+            prologue_lds<TQ>(L.q, ar, L.attn_norm, g.eps, s);
             return true;
         }, done))
         return false;
@@ -316,7 +320,11 @@ __device__ __forceinline__ bool phase_a(const LoopArgs& g, const LayerDev& L, in
     const int G = static_cast<int>(gridDim.x);
     const int first = nq % G, me = (static_cast<int>(blockIdx.x) - first + G) % G;
     if (me >= g.tiles_qkv[2]) return true;
-    prologue_lds<TV>(L.v, L.attn_norm, g.eps, s);
+    {
+        ActRegs ar;
+        act_issue_w(ar, L.attn_norm, static_cast<int>(L.v.cols));
+        prologue_lds<TV>(L.v, ar, L.attn_norm, g.eps, s);
+    }
     for (int t = me; t < g.tiles_qkv[2]; t += G) {
         const uint32_t row0 = static_cast<uint32_t>(t) * g.R_qkv[2];
         Tile<TV, kLoopUnits> tile;
@@ -479,6 +487,236 @@ __device__ __forceinline__ bool attn_slot_merge(const LoopArgs& lg, const AttnAr
     return true;
 }
 
+// ---------------------------------------------------------------- per-head exact attention
+
+// Tagged values into LDS by one wave (no barrier): up to K words a lane in
+// flight, every missing word re-polled each round; false when abandoning.
+template <int K>
+__device__ __forceinline__ bool wget_segs(const LoopArgs& g, unsigned tag, TSeg s0, TSeg s1, TSeg s2) {
+    const int lane = static_cast<int>(threadIdx.x & 63);
+    const int n01 = s0.n + s1.n, n = n01 + s2.n;
+    auto at = [&](int i, const unsigned long long*& src, float*& dst) {
+        if (i < s0.n) { src = s0.src + i; dst = s0.dst + i; }
+        else if (i < n01) { src = s1.src + (i - s0.n); dst = s1.dst + (i - s0.n); }
+        else { src = s2.src + (i - n01); dst = s2.dst + (i - n01); }
+    };
+    for (int base = lane; base < n; base += K * 64) {
+        unsigned long long w[K];
+        const unsigned long long* src[K];
+        float* dst[K];
+        bool have[K];
+#pragma unroll
+        for (int u = 0; u < K; ++u) {
+            const int i = base + u * 64;
+            have[u] = i >= n;
+            at(i < n ? i : n - 1, src[u], dst[u]);
+            w[u] = tload(src[u]);
+        }
+        unsigned spins = 0;
+        while (true) {
+            bool all = true;
+#pragma unroll
+            for (int u = 0; u < K; ++u) {
+                if (!have[u]) {
+                    if (static_cast<unsigned>(w[u] >> 32) == tag) {
+                        *dst[u] = __uint_as_float(static_cast<unsigned>(w[u]));
+                        have[u] = true;
+                    } else {
+                        all = false;
+                    }
+                }
+            }
+            if (all) break;
+            if (++spins > kSpinLimit) {
+                atomicExch(g.error, 1);
+                return false;
+            }
+            if ((spins & 63) == 0 && loop_failed(g)) return false;
+            __builtin_amdgcn_s_sleep(1);
+#pragma unroll
+            for (int u = 0; u < K; ++u)
+                if (!have[u]) w[u] = tload(src[u]);
+        }
+    }
+    return true;
+}
+
+// chunk_issue by the `nt` threads of rank 0 .. nt - 1 (nt a multiple of 64).
+__device__ __forceinline__ void chunk_issue_by(uint16_t* lds, const uint16_t* base, int p0, int n_pos, int hd, bool swz, int rank,
+                                               int nt) {
+    const int P = kv_pieces(hd), mask = swz ? kv_mask(hd) : 0;
+    const int pieces = n_pos * P;
+    const uint8_t* src = reinterpret_cast<const uint8_t*>(base + static_cast<size_t>(p0) * hd);
+    uint8_t* dst = reinterpret_cast<uint8_t*>(lds);
+    const int wave_first = rank & ~63;
+    for (int k = 0; k * nt < pieces; ++k) {
+        const int i = k * nt + rank;
+        if (i < pieces) {
+            const int p = i / P, c = (i - p * P) ^ (p & mask);
+            __builtin_amdgcn_global_load_lds((global_cvoid_ptr)(src + (static_cast<size_t>(p) * P + c) * 16),
+                                             (lds_void_ptr)(dst + (k * nt + wave_first) * 16), 16, 0, 0);
+        }
+    }
+}
+
+// Attention of query head h on workgroup h, in the reference's order (scores
+// by dot_f32's 16 lane partials, softmax with a double sum, value sums in
+// position order; see attn_exact_pool).  Wave 0 awaits this token's q (head
+// h), k and v (kv head h / hpk) while waves 1-3 stage the cached keys (and
+// values), so the hand-off polls are not queued behind the cache loads.  Every
+// query head of a kv head normalises and rotates the same k; the first one
+// also stores the new cache rows (system-scope stores, complete before its
+// outputs are published, for the other workgroups that read them in later
+// steps).  Needs L <= kSplit * kPoolChunks.
+template <int HD, class O>
+__device__ __forceinline__ bool attn_head_pool(const LoopArgs& lg, const AttnArgs& g, AttnPoolLds& sp, int h, int pos, unsigned tin,
+                                               const O& o) {
+    AttnLds& s = sp.a;
+    const int hd = HD != 0 ? HD : g.head_dim, hpk = g.heads / g.kv_heads, kv = h / hpk, t = threadIdx.x;
+    const int wave = t >> 6, lane = t & 63, L = pos + 1;
+    const int n = pool_nchunks(L), last = (L - 1) / kSplit;
+    const bool early = pool_values_early(L), writer = h % hpk == 0;
+    const uint16_t* kbase = g.kcache + static_cast<size_t>(kv) * g.ctx * hd;
+    const uint16_t* vbase = g.vcache + static_cast<size_t>(kv) * g.ctx * hd;
+    bool fail = false;
+    attn_stamp(g, h, 0);
+    if (wave == 0) {
+        fail = !wget_segs<8>(lg, tin, TSeg{lg.qt + h * hd, s.q, hd}, TSeg{lg.kt + kv * hd, s.kcur, hd},
+                             TSeg{lg.vt + kv * hd, s.vcur, hd});
+    } else {
+        for (int c = 0; c < n; ++c) {
+            const int nn = chunk_cached(c, L);
+            if (nn > 0) chunk_issue_by(sp.chunk(c), kbase, c * kSplit, nn, hd, true, t - 64, kThreads - 64);
+        }
+        if (early)
+            for (int c = 0; c < n; ++c) {
+                const int nn = chunk_cached(c, L);
+                if (nn > 0) chunk_issue_by(sp.chunk(n + c), vbase, c * kSplit, nn, hd, false, t - 64, kThreads - 64);
+            }
+    }
+    if (__syncthreads_or(fail)) {
+        __builtin_amdgcn_s_waitcnt(0);
+        return false;
+    }
+    attn_stamp(g, h, 1);
+    // q_norm / k_norm and RoPE (src/model.cpp:1026-1041), k and v rounded to fp16 as the cache holds them
+    const float* rope = g.rope + static_cast<size_t>(pos) * hd;
+    if (wave == 0) head_norm_rope(s.q, g.qnorm, rope, hd, g.neox, g.eps);
+    else if (wave == 1) {
+        head_norm_rope(s.kcur, g.knorm, rope, hd, g.neox, g.eps);
+        for (int i = lane; i < hd; i += 64) s.kcur[i] = h2f(f2h(s.kcur[i]));
+    } else if (wave == 2) {
+        for (int i = lane; i < hd; i += 64) s.vcur[i] = h2f(f2h(s.vcur[i]));
+    }
+    __builtin_amdgcn_s_waitcnt(0);  // waves 1-3: the staged keys (and values) have landed
+    __syncthreads();
+    attn_stamp(g, h, 2);
+    pool_put_current(sp.chunk(last), s.kcur, L, hd, true);
+    if (early) pool_put_current(sp.chunk(n + last), s.vcur, L, hd, false);
+    if (writer && t >= 128) {  // waves 2-3 store the new cache rows (store_f16, src/kernels_f32.cpp:248-250)
+        const int i = 2 * (t - 128);
+        if (i < hd) {
+            uint16_t* kr = g.kcache + (static_cast<size_t>(kv) * g.ctx + pos) * hd;
+            uint16_t* vr = g.vcache + (static_cast<size_t>(kv) * g.ctx + pos) * hd;
+            const uint32_t kw = f2h(s.kcur[i]) | (static_cast<uint32_t>(f2h(s.kcur[i + 1])) << 16);
+            const uint32_t vw = f2h(s.vcur[i]) | (static_cast<uint32_t>(f2h(s.vcur[i + 1])) << 16);
+            __hip_atomic_store(reinterpret_cast<uint32_t*>(kr + i), kw, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+            __hip_atomic_store(reinterpret_cast<uint32_t*>(vr + i), vw, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+        }
+    }
+    __syncthreads();
+    // ---- scores, one position a lane
+    for (int p = t; p < L; p += kThreads) {
+        const int c = p / kSplit, r = p - c * kSplit;
+        float v;
+        if (HD != 0) v = score_lane<(HD != 0 ? HD : 128) / 16>(s.q, sp.chunk(c), r, HD / 8, HD / 8 - 1);
+        else {
+            const int per = hd / 16, P = kv_pieces(hd), mask = kv_mask(hd);
+            v = per == 8 ? score_lane<8>(s.q, sp.chunk(c), r, P, mask) : per == 6 ? score_lane<6>(s.q, sp.chunk(c), r, P, mask)
+              : per == 4 ? score_lane<4>(s.q, sp.chunk(c), r, P, mask) : score_lane<2>(s.q, sp.chunk(c), r, P, mask);
+        }
+        s.sc[p] = v * g.scale;
+    }
+    __syncthreads();
+    attn_stamp(g, h, 3);
+    const int vfirst = early ? n : 0;
+    if (!early)  // the keys are consumed: the values take their buffers
+        for (int c = 0; c < n; ++c) {
+            const int nn = chunk_cached(c, L);
+            if (nn > 0) chunk_issue(sp.chunk(c), vbase, c * kSplit, nn, hd, false);
+        }
+    // ---- softmax over the four waves: max, e = expf(s - max), double sum, w = e * (float)(1 / sum)
+    float m = -INFINITY;
+    for (int p = t; p < L; p += kThreads) m = fmaxf(m, s.sc[p]);
+    m = wave_max(m);
+    if (lane == 0) s.mx[wave] = m;
+    __syncthreads();
+    m = fmaxf(fmaxf(s.mx[0], s.mx[1]), fmaxf(s.mx[2], s.mx[3]));
+    double part = 0.0;
+    for (int p = t; p < L; p += kThreads) {
+        const float e = ref_expf(s.sc[p] - m);
+        s.sc[p] = e;
+        part += static_cast<double>(e);
+    }
+    part = wave_sum(part);
+    if (lane == 0) s.red[0][wave] = part;
+    __syncthreads();
+    const float scale = static_cast<float>(1.0 / (((s.red[0][0] + s.red[0][1]) + s.red[0][2]) + s.red[0][3]));
+    for (int p = t; p < L; p += kThreads) s.sc[p] *= scale;
+    __builtin_amdgcn_s_waitcnt(0);  // values staged (late case); the writer's cache rows are in memory
+    if (!early) pool_put_current(sp.chunk(last), s.vcur, L, hd, false);
+    __syncthreads();
+    attn_stamp(g, h, 4);
+    // ---- value sums in position order, one chain a lane
+    if (t < hd) {
+        const int d = t, full = L & ~7;
+        const float* w = s.sc;
+        const uint16_t* vcol = sp.chunk(vfirst) + d;
+        auto vat = [&](int p) -> const uint16_t* { return vcol + (p >> 6) * (kSplit * 128) + (p & 63) * hd; };
+        float a = 0.0f;
+        float4 wa0, wa1, wb0, wb1;
+        uint16_t va[8], vb[8];
+        int p = 0;
+        if (full > 0) {
+            wa0 = *reinterpret_cast<const float4*>(w);
+            wa1 = *reinterpret_cast<const float4*>(w + 4);
+#pragma unroll
+            for (int u = 0; u < 8; ++u) va[u] = vat(0)[u * hd];
+            for (; p + 16 <= full; p += 16) {
+                {
+                    const float* wn = w + p + 8;
+                    wb0 = *reinterpret_cast<const float4*>(wn);
+                    wb1 = *reinterpret_cast<const float4*>(wn + 4);
+                    const uint16_t* vn = vat(p + 8);
+#pragma unroll
+                    for (int u = 0; u < 8; ++u) vb[u] = vn[u * hd];
+                }
+                a += wa0.x * h2f(va[0]); a += wa0.y * h2f(va[1]); a += wa0.z * h2f(va[2]); a += wa0.w * h2f(va[3]);
+                a += wa1.x * h2f(va[4]); a += wa1.y * h2f(va[5]); a += wa1.z * h2f(va[6]); a += wa1.w * h2f(va[7]);
+                if (p + 16 < full) {
+                    const float* wn = w + p + 16;
+                    wa0 = *reinterpret_cast<const float4*>(wn);
+                    wa1 = *reinterpret_cast<const float4*>(wn + 4);
+                    const uint16_t* vn = vat(p + 16);
+#pragma unroll
+                    for (int u = 0; u < 8; ++u) va[u] = vn[u * hd];
+                }
+                a += wb0.x * h2f(vb[0]); a += wb0.y * h2f(vb[1]); a += wb0.z * h2f(vb[2]); a += wb0.w * h2f(vb[3]);
+                a += wb1.x * h2f(vb[4]); a += wb1.y * h2f(vb[5]); a += wb1.z * h2f(vb[6]); a += wb1.w * h2f(vb[7]);
+            }
+            if (p < full) {
+                a += wa0.x * h2f(va[0]); a += wa0.y * h2f(va[1]); a += wa0.z * h2f(va[2]); a += wa0.w * h2f(va[3]);
+                a += wa1.x * h2f(va[4]); a += wa1.y * h2f(va[5]); a += wa1.z * h2f(va[6]); a += wa1.w * h2f(va[7]);
+                p += 8;
+            }
+        }
+        for (; p < L; ++p) a += w[p] * h2f(*vat(p));
+        o.att(h * hd + d, a);
+    }
+    attn_stamp(g, h, 5);
+    return true;
+}
+
 // B: attention, exact (one workgroup per key/value head) or split over (kv, split) slots.
 __device__ __forceinline__ bool phase_b(const LoopArgs& g, const LayerDev& L, int step, int l, int pos, LoopLds& lds) {
     const int kvh = g.kv_heads, hpk = g.heads / kvh, hd = g.head_dim, Lc = pos + 1;
@@ -486,6 +724,14 @@ __device__ __forceinline__ bool phase_b(const LoopArgs& g, const LayerDev& L, in
     const AttnArgs a = attn_args(g, L, step, l);
     const TaggedOut o{g.attt, g.pacct, g.pmlt, tout, g.error, g.att_q8, g.heads * g.head_dim};
     AttnLds& s = lds.att;
+    if (attn_is_exact(Lc, hpk) && Lc <= kSplit * kPoolChunks && g.head_attn) {
+        if (static_cast<int>(blockIdx.x) >= g.heads) return true;
+        const int h = blockIdx.x;
+        AttnPoolLds& sp = lds.pool;
+        if (hd == 128) return attn_head_pool<128>(g, a, sp, h, pos, tin, o);
+        if (hd == 64) return attn_head_pool<64>(g, a, sp, h, pos, tin, o);
+        return attn_head_pool<0>(g, a, sp, h, pos, tin, o);
+    }
     if (attn_is_exact(Lc, hpk) && Lc <= kSplit * kPoolChunks) {
         if (static_cast<int>(blockIdx.x) >= kvh) return true;
         const int kv = blockIdx.x;
@@ -554,8 +800,10 @@ __device__ __forceinline__ bool phase_c(const LoopArgs& g, const LayerDev& L, in
             pst(st, 1);
             return ok;
         }
+        ActRegs ar;
+        act_issue_w(ar, L.attn_sub, n);
         if (!tget_vec(g, g.attt, tag_of(g, step, l, 2), s.x, n)) return false;
-        prologue_lds<TO>(L.o, L.attn_sub, g.eps, s);
+        prologue_lds<TO>(L.o, ar, L.attn_sub, g.eps, s);
         return true;
     };
     auto done = [&](int t, const Packed& m, uint32_t row0, const float* sums) -> bool {
@@ -591,9 +839,11 @@ __device__ __forceinline__ bool phase_d(const LoopArgs& g, const LayerDev& L, in
     tg.load(L.gate, row0, R);
     tu.load(L.up, row0, R);
     const Stamps st = pst_ptr(g, step, l, 3);
+    ActRegs ar;
+    act_issue_w(ar, L.ffn_norm, g.embd_dim);
     if (!tget_vec(g, g.ht, tag_of(g, step, l, 3), s.x, g.embd_dim)) return false;
     pst(st, 1);
-    prologue_lds<TG>(L.gate, L.ffn_norm, g.eps, s);
+    prologue_lds<TG>(L.gate, ar, L.ffn_norm, g.eps, s);
     pst(st, 2);
     int gfirst = t, grows = 0;
     while (true) {
@@ -648,9 +898,11 @@ __device__ __forceinline__ bool phase_f(const LoopArgs& g, const LayerDev& L, in
     };
     const Stamps st = pst_ptr(g, step, l, 4);
     auto ready = [&]() -> bool {
+        ActRegs ar;
+        act_issue_w(ar, L.ffn_sub, g.ff);
         if (!tget_vec(g, g.actt, tag_of(g, step, l, 4), s.x, g.ff)) return false;
         pst(st, 1);
-        prologue_lds<TD>(L.down, L.ffn_sub, g.eps, s);
+        prologue_lds<TD>(L.down, ar, L.ffn_sub, g.eps, s);
         pst(st, 2);
         return true;
     };
@@ -683,8 +935,10 @@ __device__ __forceinline__ bool phase_h(const LoopArgs& g, int step, GemvLds& s)
         row0 = static_cast<uint32_t>(t) * R;
     };
     auto ready = [&]() -> bool {
+        ActRegs ar;
+        act_issue_w(ar, g.out_norm, g.embd_dim);
         if (!tget_vec(g, g.ht, tag_of(g, step, g.n_layers - 1, 5), s.x, g.embd_dim)) return false;
-        prologue_lds<TH>(g.out, g.out_norm, g.eps, s);
+        prologue_lds<TH>(g.out, ar, g.out_norm, g.eps, s);
         return true;
     };
     auto done = [&](int, const Packed& m, uint32_t row0, const float* sums) -> bool {

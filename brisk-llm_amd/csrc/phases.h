@@ -133,10 +133,10 @@ struct TaggedOut {
     // then total / 32 block sums.  One value a lane: lanes 32 k .. 32 k + 31 hold
     // a block, and all of them call together.
     __device__ __forceinline__ void att_q8_0(int i, float v) const {
-        float amax = group_reduce<16>(fabsf(v), [](float a, float b) { return fmaxf(a, b); });
-        amax = fmaxf(amax, __shfl_xor(amax, 16, 64));
-        const float d = amax / 127.0f;
-        const float inv = d != 0.0f ? 1.0f / d : 0.0f;
+        float amax = group_reduce<16>(fabsf(v), [](float a, float b) { return nnmax(a, b); });
+        amax = nnmax(amax, __shfl_xor(amax, 16, 64));
+        const float d = div127(amax);
+        const float inv = d != 0.0f ? rcp_rn(d) : 0.0f;
         const int q = static_cast<int>(rintf(v * inv));
         int sum = group_reduce<16>(q, [](int a, int b) { return a + b; });
         sum += __shfl_xor(sum, 16, 64);

@@ -285,15 +285,19 @@ void Session::record_step(bool full) {
 static int loop_rows(const std::vector<const Packed*>& ms, int grid, bool head = false) {
     size_t rows = 0;
     for (const Packed* m : ms) rows += m->rows;
-    int R = 1;
-    while (R < 64 && static_cast<size_t>(R) * static_cast<size_t>(grid) < rows) R *= 2;
+    // the most rows a tile can take (registers, LDS terms), then the fewest
+    // rounds of tiles over the grid, then rows spread evenly over those rounds
+    // (not rounded to a power of two: 3072 gate rows are 256 tiles of 12)
+    size_t cap = 64;
     for (const Packed* m : ms) {
         const size_t units = m->cols / block_elems(m->type);
-        while (R > 1 && (static_cast<size_t>(R) * units > static_cast<size_t>(loop_units_per_thread(m->type, head)) * kThreads ||
-                         static_cast<size_t>(R) * term_stride(static_cast<uint32_t>(units)) > static_cast<size_t>(kTermCap)))
-            R /= 2;
+        cap = std::min(cap, static_cast<size_t>(loop_units_per_thread(m->type, head)) * kThreads / units);
+        cap = std::min(cap, static_cast<size_t>(kTermCap) / term_stride(static_cast<uint32_t>(units)));
     }
-    return R;
+    cap = std::max<size_t>(cap, 1);
+    const size_t g = static_cast<size_t>(grid);
+    const size_t rounds = (rows + g * cap - 1) / (g * cap);
+    return static_cast<int>(std::max<size_t>(1, (rows + g * rounds - 1) / (g * rounds)));
 }
 
 static int tiles_of(const Packed& m, int R) { return static_cast<int>((m.rows + R - 1) / R); }
@@ -406,6 +410,8 @@ void Session::setup_loop() {
                ((cfg_.heads / cfg_.kv_heads) * cfg_.head_dim) % 32 == 0 ? 1 : 0;
     if (const char* e = std::getenv("BRISK_HIP_ATT_Q8")) g.att_q8 = g.att_q8 && std::string(e) != "0";
     g.tiles_d = tiles_of(L0.down.p, g.R_d);
+    g.head_attn = static_cast<int>(cfg_.heads) <= G ? 1 : 0;
+    if (const char* e = std::getenv("BRISK_HIP_HEAD_ATTN")) g.head_attn = g.head_attn && std::string(e) != "0";
     g.R_h = loop_rows({&out_->p}, G, true);
     g.tiles_h = tiles_of(out_->p, g.R_h);
 }

@@ -115,6 +115,15 @@ int brisk_hip_gemv(int type, int flags, const void* packed, size_t rows, size_t 
  * loop's softmax and SiLU use the same device routine.  y[i] = expf(x[i]). */
 int brisk_hip_expf(const float* x, float* y, size_t n, void* stream);
 
+/* Self-test of the shortcuts the device arithmetic takes: the two short
+ * divisions of the activation quantisation (a / 127 for a >= 0, and 1 / d),
+ * each compared with IEEE division on every finite input it can take, and the
+ * hardware float-to-half conversion, compared with the reference's bit-level
+ * conversion (src/quant.cpp:87-113) on every float.  mismatches[0..2] receive
+ * the counts (all 0 when the shortcuts are exact).  Test support; no
+ * counterpart in the reference. */
+int brisk_hip_div_selftest(unsigned long long* mismatches);
+
 /* ---------------------------------------------------------------- session level */
 
 /* Engine construction, as `MetalSession(model, file bytes, max_context)`

@@ -183,3 +183,12 @@ def test_expf_matches_host_libm(lib, orc):
     got = host(out, np.float32)
     bad = np.flatnonzero(got.view(np.uint32) != want.view(np.uint32))
     assert len(bad) == 0, f"{len(bad)} of {len(x)} differ, e.g. x={x[bad[:3]]} got={got[bad[:3]]} want={want[bad[:3]]}"
+
+
+def test_short_divisions_are_exact(lib):
+    """div127 (a / 127, a >= 0) and rcp_rn (1 / d) equal IEEE division on every finite input, and the
+    hardware float-to-half conversion equals the reference's bit-level one on every float."""
+    import ctypes
+    bad = (ctypes.c_ulonglong * 3)()
+    L.check(lib.brisk_hip_div_selftest(bad))
+    assert bad[0] == 0 and bad[1] == 0 and bad[2] == 0, f"div127: {bad[0]} mismatches, rcp_rn: {bad[1]}, f2h: {bad[2]}"
