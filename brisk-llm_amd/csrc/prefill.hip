@@ -479,6 +479,234 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 2))
     }
 }
 
+// ---------------------------------------------------------------- the K-quant GEMM, staged through LDS
+
+// Q4_K / Q6_K (one 256-value super-block a row per chunk).  A workgroup of 4
+// waves computes 64 rows x 32 tokens; wave w owns rows 16 w .. + 15 for the
+// 32 tokens (2 groups of 16).  Per chunk every operand -- the 64 rows' weight
+// planes and the 32 tokens' int8 values, bsums and scales -- is copied global
+// -> LDS by global_load_lds (16 bytes a lane, no registers held), and the
+// waves read their MFMA fragments from there.  The stage is small (22 KB) and
+// the registers few, so several workgroups share a CU and one's copies overlap
+// the others' MFMAs.  The arithmetic is wchunk_compute's: exact int32 block
+// dots, the reference's float term and sum order.
+constexpr int kKqTok = 32;
+
+struct KqStage {
+    alignas(16) uint8_t w0[64 * 128];      // Q4_K nibbles / Q6_K ql: row r piece p at slot r * 8 + (p ^ (r & 7))
+    alignas(16) uint8_t wk[4096];          // Q4_K: p1 [64][16] then p2 [64][16]; Q6_K: qh, row r piece p at r * 4 + (p ^ (r & 3))
+    alignas(16) uint32_t wm[384];          // Q6_K: the 20-byte meta of row r at dwords 5 r .. 5 r + 4
+    alignas(16) int8_t x[kKqTok * 256];    // token t piece p at slot t * 16 + (p ^ (t & 15))
+    alignas(16) int32_t bs[kKqTok * 16];   // bsums of token t at 16 t
+    alignas(16) float xd[64];              // Q8_K scale of token t (lanes 32..63: a copy)
+};
+
+__device__ __forceinline__ void dma16(const void* src, void* lds_wave_base) {
+    __builtin_amdgcn_global_load_lds((global_cvoid_ptr)src, (lds_void_ptr)lds_wave_base, 16, 0, 0);
+}
+__device__ __forceinline__ void dma4(const void* src, void* lds_wave_base) {
+    __builtin_amdgcn_global_load_lds((global_cvoid_ptr)src, (lds_void_ptr)lds_wave_base, 4, 0, 0);
+}
+
+// Copies chunk c of rows r0 .. r0 + 63 and tokens t0 .. t0 + 31 into the stage
+// (rows and tokens past the ends re-read the last one; their outputs are not stored).
+template <uint32_t T>
+__device__ __forceinline__ void kq_copy(KqStage& st, const Packed& m, const ActPlanar& x, int ntok, uint32_t r0, int t0, int c) {
+    const int tid = threadIdx.x, wave = tid >> 6, wave_first = tid & ~63;
+    const uint32_t nsb = m.cols / 256, rmax = m.rows - 1;
+    auto rowc = [&](int r) -> size_t {
+        const uint32_t rr = r0 + r <= rmax ? r0 + r : rmax;
+        return static_cast<size_t>(rr) * nsb + c;
+    };
+    auto tokc = [&](int t) -> size_t { return static_cast<size_t>(t0 + t < ntok ? t0 + t : ntok - 1); };
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {  // 64 rows x 8 pieces
+        const int slot = k * kThreads + tid, r = slot >> 3, p = (slot & 7) ^ (r & 7);
+        dma16(m.p0 + rowc(r) * 128 + p * 16, st.w0 + (k * kThreads + wave_first) * 16);
+    }
+    if (T == kQ4_K) {  // wave 0: the p1 rows, wave 1: the p2 rows
+        if (wave < 2) {
+            const int r = tid & 63;
+            dma16((wave ? m.p2 : m.p1) + rowc(r) * 16, st.wk + wave_first * 16);
+        }
+    } else {  // qh: 64 rows x 4 pieces; meta: 320 dwords
+        const int r = tid >> 2, p = (tid & 3) ^ (r & 3);
+        dma16(m.p1 + rowc(r) * 64 + p * 16, st.wk + wave_first * 16);
+#pragma unroll
+        for (int k = 0; k < 2; ++k) {
+            const int slot = k * kThreads + tid;
+            if (slot < 384) {  // waves of slots 320..383 copy row 63's meta again into the spare
+                const int sl = slot < 320 ? slot : 319, r2 = sl / 5, j = sl - r2 * 5;
+                dma4(m.p2 + rowc(r2) * 20 + j * 4, st.wm + k * kThreads + wave_first);
+            }
+        }
+    }
+    const size_t bss = x.stride / 16, ds = x.stride / 32;
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {  // 32 tokens x 16 pieces
+        const int slot = k * kThreads + tid, t = slot >> 4, p = (slot & 15) ^ (t & 15);
+        dma16(x.qs + tokc(t) * x.stride + c * 256 + p * 16, st.x + (k * kThreads + wave_first) * 16);
+    }
+    if (wave < 2) dma16(x.bs + tokc(tid >> 2) * bss + c * 16 + (tid & 3) * 4, st.bs + wave_first * 4);  // 32 tokens x 4 pieces
+    if (wave == 0) dma4(x.d + tokc(tid & 31) * ds + c, st.xd);
+}
+
+__device__ __forceinline__ uint64_t lds8(const uint8_t* p) { return *reinterpret_cast<const uint64_t*>(p); }
+
+// The chunk's contribution to the lane's outputs (tokens 16 g + l % 16, rows 16 w + 4 (l / 16) + i).
+template <uint32_t T>
+__device__ __forceinline__ void kq_compute(const KqStage& st, MmAcc<2>& acc) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, kq = (lane >> 4) * 8, tl = lane & 15;
+    const int ar = wave * 16 + tl;  // the A fragment's row within the tile
+    const v4i zero = {0, 0, 0, 0};
+    auto xfrag = [&](int g, int jj) -> uint64_t {
+        const int t = 16 * g + tl, byte = jj * 32 + kq, p = byte >> 4;
+        return lds8(reinterpret_cast<const uint8_t*>(st.x) + (t * 16 + (p ^ (t & 15))) * 16 + (byte & 15));
+    };
+    auto w0frag = [&](int byte) -> uint64_t {
+        const int p = byte >> 4;
+        return lds8(st.w0 + (ar * 8 + (p ^ (ar & 7))) * 16 + (byte & 15));
+    };
+    if (T == kQ4_K) {
+        uint4 scm[4];
+        uint32_t dd[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int orow = wave * 16 + (lane >> 4) * 4 + i;
+            scm[i] = *reinterpret_cast<const uint4*>(st.wk + 1024 + orow * 16);
+            dd[i] = *reinterpret_cast<const uint32_t*>(st.wk + orow * 16);
+        }
+        int wsum[2][4], osum[2][4];
+#pragma unroll
+        for (int g = 0; g < 2; ++g)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) wsum[g][i] = osum[g][i] = 0;
+#pragma unroll
+        for (int jj = 0; jj < 8; ++jj) {
+            const uint64_t w = w0frag((jj >> 1) * 32 + kq);
+            const uint64_t a = (jj & 1) ? ((w >> 4) & (0x0F * kB01)) : (w & (0x0F * kB01));
+            const int sh = 8 * (jj & 3);
+            int sc[4], mn[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                sc[i] = static_cast<int>((((jj >> 2) ? scm[i].y : scm[i].x) >> sh) & 0xFF);
+                mn[i] = static_cast<int>((((jj >> 2) ? scm[i].w : scm[i].z) >> sh) & 0xFF);
+            }
+#pragma unroll
+            for (int g = 0; g < 2; ++g) {
+                const int t = 16 * g + tl;
+                const v4i d = mfma(a, xfrag(g, jj), zero);
+                const int pair = st.bs[t * 16 + 2 * jj] + st.bs[t * 16 + 2 * jj + 1];
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    wsum[g][i] += sc[i] * d[i];
+                    osum[g][i] += mn[i] * pair;
+                }
+            }
+        }
+#pragma unroll
+        for (int g = 0; g < 2; ++g) {
+            const float xd = st.xd[16 * g + tl];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const float d = h2f(static_cast<uint16_t>(dd[i] & 0xFFFF)), dmin = h2f(static_cast<uint16_t>(dd[i] >> 16));
+                acc.s[g][i] += xd * (d * static_cast<float>(wsum[g][i]) - dmin * static_cast<float>(osum[g][i]));  // src/quant.cpp:500-521
+            }
+        }
+    } else {  // Q6_K
+        const bool lo_half = lane < 32;  // lanes 0..31 hold k 0..15 of a sub-block, 32..63 hold k 16..31
+        const int orow0 = wave * 16 + (lane >> 4) * 4;
+        int wsum[2][4];
+#pragma unroll
+        for (int g = 0; g < 2; ++g)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) wsum[g][i] = 0;
+#pragma unroll 2
+        for (int jj = 0; jj < 8; ++jj) {
+            const int half = jj >> 2, quarter = jj & 3;
+            const uint64_t l = w0frag(half * 64 + (quarter & 1) * 32 + kq);
+            const int hb = half * 32 + kq, hp = hb >> 4;
+            const uint64_t h = lds8(st.wk + (ar * 4 + (hp ^ (ar & 3))) * 16 + (hb & 15));
+            const uint64_t nib = quarter >= 2 ? ((l >> 4) & (0x0F * kB01)) : (l & (0x0F * kB01));
+            const uint64_t u = nib | (((h >> (2 * quarter)) & (0x03 * kB01)) << 4);  // 0..63
+            const uint64_t tq = u ^ (0x20 * kB01);                                   // 6-bit two's complement of u - 32
+            const uint64_t a = tq | ((tq & (0x20 * kB01)) * 0x06);
+            const uint64_t a0 = lo_half ? a : 0ull, a1 = lo_half ? 0ull : a;  // groups 2 jj and 2 jj + 1 of 16
+            const int sh = (jj & 1) * 16;
+            int s0[4], s1[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const uint32_t word = st.wm[(orow0 + i) * 5 + (jj >> 1)];
+                s0[i] = static_cast<int8_t>((word >> sh) & 0xFF);
+                s1[i] = static_cast<int8_t>((word >> (sh + 8)) & 0xFF);
+            }
+#pragma unroll
+            for (int g = 0; g < 2; ++g) {
+                const uint64_t b = xfrag(g, jj);
+                const v4i d0 = mfma(a0, b, zero), d1 = mfma(a1, b, zero);
+#pragma unroll
+                for (int i = 0; i < 4; ++i) wsum[g][i] += s0[i] * d0[i] + s1[i] * d1[i];
+            }
+        }
+#pragma unroll
+        for (int g = 0; g < 2; ++g) {
+            const float xd = st.xd[16 * g + tl];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const float d = h2f(static_cast<uint16_t>(st.wm[(orow0 + i) * 5 + 4] & 0xFFFF));
+                acc.s[g][i] += xd * d * static_cast<float>(wsum[g][i]);  // src/quant.cpp:549-563
+            }
+        }
+    }
+}
+
+template <uint32_t T, int MODE>
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(3, 8))) void k_mmk(MmArgs g) {
+    __shared__ KqStage st;
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const uint32_t rt0 = blockIdx.x * 64;
+    const int t0 = blockIdx.y * kKqTok;
+    const int nc = static_cast<int>(g.m.cols / 256);
+    MmAcc<2> a;
+#pragma unroll
+    for (int gi = 0; gi < 2; ++gi)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) a.s[gi][i] = 0.0f;
+    for (int c = 0; c < nc; ++c) {
+        if (c > 0) __syncthreads();  // the previous chunk is consumed
+        kq_copy<T>(st, g.m, g.x, g.ntok, rt0, t0, c);
+        __builtin_amdgcn_s_waitcnt(0);
+        __syncthreads();
+        kq_compute<T>(st, a);
+    }
+    const uint32_t rmax = g.m.rows - 1;
+#pragma unroll
+    for (int gi = 0; gi < 2; ++gi) {
+        const int t = t0 + 16 * gi + (lane & 15);
+        if (t >= g.ntok) continue;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const uint32_t r = rt0 + wave * 16 + (lane >> 4) * 4 + i;
+            if (r > rmax) continue;
+            float* o = g.out + static_cast<size_t>(t) * g.ostride + r;
+            const float v = a.s[gi][i];
+            if (MODE == kMmStore) {
+                *o = v;
+            } else if (MODE == kMmAdd) {
+                *o = *o + v;  // h += proj (src/model.cpp:1111, :1162)
+            } else {  // kMmGated: out holds the gate row, this is up
+                const float gv = *o;
+                if (g.relu2) {
+                    const float q = gv > 0.0f ? gv : 0.0f;
+                    *o = q * q * v;  // src/model.cpp:1134-1138
+                } else {
+                    *o = gv / (1.0f + ref_expf(-gv)) * v;  // src/kernels_f32.cpp:287-289
+                }
+            }
+        }
+    }
+}
+
 // ---------------------------------------------------------------- per-token work
 
 // Embedding rows of seq[pos0 + t] (embedding_row, src/model.cpp:27-70).
@@ -530,11 +758,12 @@ template <int MODE>
 static hipError_t mm_dispatch(const MmArgs& g, hipStream_t s) {
     const int tok = 16 * (g.m.type == kQ4_K || g.m.type == kQ6_K ? mm_groups<kQ4_K>() : mm_groups<kQ4_0>());
     const dim3 grid((g.m.rows + kRowsPerWg - 1) / kRowsPerWg, (g.ntok + tok - 1) / tok);
+    const dim3 kq_grid((g.m.rows + 63) / 64, (g.ntok + kKqTok - 1) / kKqTok);
     switch (g.m.type) {
         case kQ4_0: hipLaunchKernelGGL((k_mm<kQ4_0, MODE>), grid, dim3(kThreads), 0, s, g); break;
         case kQ8_0: hipLaunchKernelGGL((k_mm<kQ8_0, MODE>), grid, dim3(kThreads), 0, s, g); break;
-        case kQ4_K: hipLaunchKernelGGL((k_mm<kQ4_K, MODE>), grid, dim3(kThreads), 0, s, g); break;
-        case kQ6_K: hipLaunchKernelGGL((k_mm<kQ6_K, MODE>), grid, dim3(kThreads), 0, s, g); break;
+        case kQ4_K: hipLaunchKernelGGL((k_mmk<kQ4_K, MODE>), kq_grid, dim3(kThreads), 0, s, g); break;
+        case kQ6_K: hipLaunchKernelGGL((k_mmk<kQ6_K, MODE>), kq_grid, dim3(kThreads), 0, s, g); break;
         case kTQ2_0: hipLaunchKernelGGL((k_mm<kTQ2_0, MODE>), grid, dim3(kThreads), 0, s, g); break;
         default: return hipErrorInvalidValue;
     }
