@@ -83,7 +83,16 @@ __constant__ const unsigned long long kExp2Table[32] = {  // bits(2^(i/32)) - (i
     0x3fef5818dcfba487ull, 0x3fef7c97337b9b5full, 0x3fefa4afa2a490daull, 0x3fefd0765b6e4540ull,
 };
 
-__device__ inline float ref_expf(float x) {
+// The table in LDS: a kernel that calls ref_expf_s fills it first
+// (exp_tab_fill, then a barrier before the first call), so the per-value
+// lookup is an LDS read rather than a dependent global load.
+__shared__ unsigned long long g_exp_tab[32];
+__device__ __forceinline__ void exp_tab_fill() {
+    if (threadIdx.x < 32) g_exp_tab[threadIdx.x] = kExp2Table[threadIdx.x];
+}
+
+template <bool kLds>
+__device__ __forceinline__ float ref_expf_impl(float x) {
     const uint32_t ux = __float_as_uint(x);
     const uint32_t abstop = (ux >> 20) & 0x7FF;
     if (abstop >= 0x42Bu) {  // |x| >= 88 (top 12 bits of 88.0f), or inf / nan
@@ -103,7 +112,7 @@ __device__ inline float ref_expf(float x) {
     const unsigned long long ki = static_cast<unsigned long long>(__double_as_longlong(kd));
     kd -= shift;
     const double r = __fma_rn(inv_ln2_n, xd, -kd);
-    const unsigned long long t = kExp2Table[ki % 32] + (ki << 47);
+    const unsigned long long t = (kLds ? g_exp_tab[ki % 32] : kExp2Table[ki % 32]) + (ki << 47);
     const double s = __longlong_as_double(static_cast<long long>(t));
     const double p = __fma_rn(c0, r, c1);
     const double r2 = r * r;
@@ -112,6 +121,8 @@ __device__ inline float ref_expf(float x) {
     y = y * s;
     return static_cast<float>(y);
 }
+__device__ inline float ref_expf(float x) { return ref_expf_impl<false>(x); }
+__device__ __forceinline__ float ref_expf_s(float x) { return ref_expf_impl<true>(x); }
 
 __device__ __forceinline__ int dot4(int a, int b, int c) { return __builtin_amdgcn_sdot4(a, b, c, false); }
 

@@ -407,7 +407,7 @@ __device__ __forceinline__ void attn_slot_partial(const AttnArgs& g, AttnPoolLds
         m = wave_max(m);
         double part = 0.0;
         for (int p = wl; p < n; p += 64) {
-            const float e = ref_expf(sc[p] - m);
+            const float e = ref_expf_s(sc[p] - m);
             sc[p] = e;
             part += static_cast<double>(e);
         }
@@ -469,10 +469,10 @@ __device__ __forceinline__ bool attn_slot_merge(const LoopArgs& lg, const AttnAr
             const int gq = ch / hd;
             float Mn = M[k];
             for (int j = 0; j < nb; ++j) Mn = fmaxf(Mn, ml[(j * hpk + gq) * 2]);
-            const float r = M[k] == -INFINITY ? 0.0f : ref_expf(M[k] - Mn);
+            const float r = M[k] == -INFINITY ? 0.0f : ref_expf_s(M[k] - Mn);
             float nu = num[k] * r, de = den[k] * r;
             for (int j = 0; j < nb; ++j) {
-                const float f = ref_expf(ml[(j * hpk + gq) * 2] - Mn);
+                const float f = ref_expf_s(ml[(j * hpk + gq) * 2] - Mn);
                 de += ml[(j * hpk + gq) * 2 + 1] * f;
                 nu += buf[j * chains + ch] * f;
             }
@@ -654,7 +654,7 @@ __device__ __forceinline__ bool attn_head_pool(const LoopArgs& lg, const AttnArg
     m = fmaxf(fmaxf(s.mx[0], s.mx[1]), fmaxf(s.mx[2], s.mx[3]));
     double part = 0.0;
     for (int p = t; p < L; p += kThreads) {
-        const float e = ref_expf(s.sc[p] - m);
+        const float e = ref_expf_s(s.sc[p] - m);
         s.sc[p] = e;
         part += static_cast<double>(e);
     }
@@ -872,7 +872,7 @@ __device__ __forceinline__ bool phase_d(const LoopArgs& g, const LayerDev& L, in
                         const float q = gv > 0.0f ? gv : 0.0f;
                         out = q * q * uv;  // src/model.cpp:1134-1138
                     } else {
-                        out = gv / (1.0f + ref_expf(-gv)) * uv;  // src/kernels_f32.cpp:287-289
+                        out = gv / (1.0f + ref_expf_s(-gv)) * uv;  // src/kernels_f32.cpp:287-289
                     }
                     tput(g.actt + r0 + r, out, tag);
                 }
@@ -990,6 +990,7 @@ __global__ __launch_bounds__(kThreads) void k_loop(LoopArgs g) {
     __shared__ LoopLds lds;
     __shared__ float hown[kOwnRows];
     __shared__ int s_token, s_ok;
+    exp_tab_fill();  // ordered before its first use by the barrier after the first token
     for (int step = 0; step < g.n_steps; ++step) {
         const int pos = g.pos0 + step;
         const bool full = step >= g.first_full;

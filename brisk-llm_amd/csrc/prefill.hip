@@ -752,6 +752,190 @@ __global__ __launch_bounds__(kThreads) void k_pre_attn(PreAttnArgs p) {
     attn_exact(g, s, kv, pos + 1, o);
 }
 
+// Attention of a block of tokens over one key/value head, in the reference's
+// order per query row (the same arithmetic as attn_exact): a workgroup takes
+// kPaRows query rows (16 / hpk tokens x the hpk query heads of kv head
+// blockIdx.y), so each staged key or value chunk serves all of them.  Scores
+// for every visible position go to LDS (causal: token t sees positions up to
+// pos0 + t), then softmax a row a wave, then value sums in position order, one
+// (row, dimension) chain a lane.  The cache holds every position (k_pre_rope
+// wrote this prompt's rows).
+constexpr int kPaRows = 16;
+constexpr int kPaMaxL = kExactMax;
+
+struct PaLds {
+    alignas(16) float q[kPaRows * 128];
+    alignas(16) float sc[kPaRows * (kPaMaxL + 4)];
+    alignas(16) uint16_t kv[2][kSplit * 128];
+    double red[kPaRows];
+};
+
+// A cache chunk (kSplit positions of one head) through registers: loaded with
+// ordinary 16-byte loads, then written to LDS in chunk_issue's layout, so the
+// loads of the next chunk are in flight while the current one is computed.
+struct PaChunk {
+    uint4 v0, v1, v2, v3;  // pieces k * kThreads + threadIdx.x, k = 0..3 (kSplit * hd / 8 <= 4 * kThreads)
+};
+__device__ __forceinline__ uint4 pa_piece(const uint8_t* src, int i, int pieces, int P, int mask) {
+    const int j = i < pieces ? i : pieces - 1;  // past the chunk: a copy, not stored
+    const int p = j / P, c = (j - p * P) ^ (p & mask);
+    return *reinterpret_cast<const uint4*>(src + (static_cast<size_t>(p) * P + c) * 16);
+}
+__device__ __forceinline__ void pa_chunk_load(PaChunk& r, const uint16_t* base, int p0, int n_pos, int hd, bool swz) {
+    const int P = kv_pieces(hd), mask = swz ? kv_mask(hd) : 0, pieces = n_pos * P, t = static_cast<int>(threadIdx.x);
+    const uint8_t* src = reinterpret_cast<const uint8_t*>(base + static_cast<size_t>(p0) * hd);
+    r.v0 = pa_piece(src, t, pieces, P, mask);
+    r.v1 = pa_piece(src, kThreads + t, pieces, P, mask);
+    if (kSplit * hd / 8 > 2 * kThreads) {
+        r.v2 = pa_piece(src, 2 * kThreads + t, pieces, P, mask);
+        r.v3 = pa_piece(src, 3 * kThreads + t, pieces, P, mask);
+    }
+}
+__device__ __forceinline__ void pa_chunk_store(const PaChunk& r, uint16_t* lds, int n_pos, int hd) {
+    const int pieces = n_pos * kv_pieces(hd), t = static_cast<int>(threadIdx.x);
+    uint4* dst = reinterpret_cast<uint4*>(lds);
+    if (t < pieces) dst[t] = r.v0;
+    if (kThreads + t < pieces) dst[kThreads + t] = r.v1;
+    if (2 * kThreads + t < pieces) dst[2 * kThreads + t] = r.v2;
+    if (3 * kThreads + t < pieces) dst[3 * kThreads + t] = r.v3;
+}
+
+template <int PER>
+__device__ __forceinline__ void pa_scores(const PreAttnArgs& p, PaLds& s, int rows, int tpb, int hpk, int L, int tb0, int Ls,
+                                          const uint16_t* kbase) {
+    constexpr int hd = PER * 16, P = hd / 8, mask = P - 1;
+    const int nchunks = (L + kSplit - 1) / kSplit;
+    PaChunk r;
+    pa_chunk_load(r, kbase, 0, L < kSplit ? L : kSplit, hd, true);
+    for (int c = 0; c < nchunks; ++c) {
+        // buffer c & 1 last held chunk c - 2, consumed before the barrier of chunk c - 1
+        pa_chunk_store(r, s.kv[c & 1], L - c * kSplit < kSplit ? L - c * kSplit : kSplit, hd);
+        if (c + 1 < nchunks) {
+            const int p1 = (c + 1) * kSplit;
+            pa_chunk_load(r, kbase, p1, L - p1 < kSplit ? L - p1 : kSplit, hd, true);  // in flight during chunk c
+        }
+        __syncthreads();  // chunk c staged
+        const uint16_t* buf = s.kv[c & 1];
+        const int p0 = c * kSplit;
+        for (int i = threadIdx.x; i < rows * kSplit; i += kThreads) {
+            const int row = i / kSplit, pp = i - row * kSplit, pos = p0 + pp;
+            const int tpos = p.pos0 + tb0 + row / hpk;  // the row's token position: it sees 0 .. tpos
+            if (pos <= tpos && pos < L) s.sc[row * Ls + pos] = score_lane<PER>(s.q + row * hd, buf, pp, P, mask) * p.a.scale;
+        }
+    }
+    __syncthreads();
+}
+
+// Value sums of the block's rows: thread t owns dimension d = t % hd of rows
+// t / hd, + kThreads / hd, ... (NCH chains).  The chains run in lockstep
+// over the positions, so each value v[q][d] is read once for all of them and
+// their adds are independent; each chain still adds its terms in position
+// order (0 + w_0 v_0 + w_1 v_1 + ...), stopping at its row's last visible
+// position.
+template <int NCH>
+__device__ __forceinline__ void pa_values(const PreAttnArgs& p, PaLds& s, int rows, int hpk, int L, int tb0, int Ls,
+                                          const uint16_t* vbase, PaChunk& r) {
+    const int hd = p.a.head_dim, t = threadIdx.x, d = t % hd, rstep = kThreads / hd, r0 = t / hd;
+    float acc[NCH];
+    int lr[NCH];
+    const float* wrow[NCH];
+    int lmin = kPaMaxL, lmax = 0;
+#pragma unroll
+    for (int k = 0; k < NCH; ++k) {
+        acc[k] = 0.0f;
+        const int row = r0 + k * rstep < rows ? r0 + k * rstep : rows - 1;  // past the block: a copy, not stored
+        lr[k] = p.pos0 + tb0 + row / hpk + 1;  // positions the row sees
+        wrow[k] = s.sc + row * Ls;
+        lmin = lr[k] < lmin ? lr[k] : lmin;
+        lmax = lr[k] > lmax ? lr[k] : lmax;
+    }
+    const int nchunks = (L + kSplit - 1) / kSplit;
+    for (int c = 0; c < nchunks; ++c) {
+        // r holds value chunk c (chunk 0 was loaded before the softmax)
+        pa_chunk_store(r, s.kv[c & 1], L - c * kSplit < kSplit ? L - c * kSplit : kSplit, hd);
+        if (c + 1 < nchunks) {
+            const int q1 = (c + 1) * kSplit;
+            pa_chunk_load(r, vbase, q1, L - q1 < kSplit ? L - q1 : kSplit, hd, false);
+        }
+        __syncthreads();  // value chunk c staged (and, for c = 0, the weights are final)
+        const uint16_t* vcol = s.kv[c & 1] + d;
+        const int q0 = c * kSplit;
+        const int nall = lmin - q0 < 0 ? 0 : (lmin - q0 < kSplit ? lmin - q0 : kSplit);  // every chain takes these
+        const int nany = lmax - q0 < 0 ? 0 : (lmax - q0 < kSplit ? lmax - q0 : kSplit);
+        int q = 0;
+        for (; q + 4 <= nall; q += 4) {
+            const float v0 = h2f(vcol[(q + 0) * hd]), v1 = h2f(vcol[(q + 1) * hd]);
+            const float v2 = h2f(vcol[(q + 2) * hd]), v3 = h2f(vcol[(q + 3) * hd]);
+#pragma unroll
+            for (int k = 0; k < NCH; ++k) {
+                const float4 w4 = *reinterpret_cast<const float4*>(wrow[k] + q0 + q);
+                float a = acc[k];
+                a += w4.x * v0; a += w4.y * v1; a += w4.z * v2; a += w4.w * v3;
+                acc[k] = a;
+            }
+        }
+        for (; q < nany; ++q) {
+            const float v = h2f(vcol[q * hd]);
+#pragma unroll
+            for (int k = 0; k < NCH; ++k)
+                if (q0 + q < lr[k]) acc[k] += wrow[k][q0 + q] * v;
+        }
+    }
+#pragma unroll
+    for (int k = 0; k < NCH; ++k) {
+        const int row = r0 + k * rstep;
+        if (row < rows) {
+            const int tt = row / hpk, gq = row - tt * hpk;
+            p.out[static_cast<size_t>(tb0 + tt) * p.qstride + (blockIdx.y * hpk + gq) * hd + d] = acc[k];
+        }
+    }
+}
+
+__global__ __launch_bounds__(kThreads) void k_pre_attn_blk(PreAttnArgs p, int ntok) {
+    __shared__ PaLds s;
+    const AttnArgs& g = p.a;
+    const int hpk = g.heads / g.kv_heads, hd = g.head_dim, kv = blockIdx.y;
+    const int tpb = kPaRows / hpk, tb0 = blockIdx.x * tpb;
+    const int ntb = ntok - tb0 < tpb ? ntok - tb0 : tpb, rows = ntb * hpk;
+    const int L = p.pos0 + tb0 + ntb;  // positions the block's last token sees
+    const int Ls = (L + 3) & ~3;
+    const int t = threadIdx.x, wave = t >> 6, wl = t & 63;
+    exp_tab_fill();  // ordered before the softmax by the barriers between
+    for (int i = t; i < rows * hd; i += kThreads) {  // q rows: row = token * hpk + head
+        const int row = i / hd, d = i - row * hd, tt = row / hpk, gq = row - tt * hpk;
+        s.q[i] = p.q[static_cast<size_t>(tb0 + tt) * p.qstride + (kv * hpk + gq) * hd + d];
+    }
+    const uint16_t* kbase = g.kcache + static_cast<size_t>(kv) * g.ctx * hd;
+    const uint16_t* vbase = g.vcache + static_cast<size_t>(kv) * g.ctx * hd;
+    __syncthreads();
+    if (hd == 128) pa_scores<8>(p, s, rows, tpb, hpk, L, tb0, Ls, kbase);
+    else if (hd == 64) pa_scores<4>(p, s, rows, tpb, hpk, L, tb0, Ls, kbase);
+    else pa_scores<2>(p, s, rows, tpb, hpk, L, tb0, Ls, kbase);
+    // first value chunk in flight while the softmax runs
+    PaChunk rv;
+    pa_chunk_load(rv, vbase, 0, L < kSplit ? L : kSplit, hd, false);
+    // ---- softmax, a row a wave: max, e = expf(s - max), double sum, w = e * (float)(1 / sum)
+    for (int row = wave; row < rows; row += kThreads / 64) {
+        const int Lr = p.pos0 + tb0 + row / hpk + 1;
+        float* sc = s.sc + row * Ls;
+        float m = -INFINITY;
+        for (int q = wl; q < Lr; q += 64) m = fmaxf(m, sc[q]);
+        m = wave_max(m);
+        double part = 0.0;
+        for (int q = wl; q < Lr; q += 64) {
+            const float e = ref_expf_s(sc[q] - m);
+            sc[q] = e;
+            part += static_cast<double>(e);
+        }
+        const float scale = static_cast<float>(1.0 / wave_sum(part));
+        for (int q = wl; q < Lr; q += 64) sc[q] *= scale;
+    }
+    // ---- value sums in position order: chains (row, d), kThreads / hd rows a pass
+    if (hd == 128) pa_values<kPaRows * 128 / kThreads>(p, s, rows, hpk, L, tb0, Ls, vbase, rv);
+    else if (hd == 64) pa_values<kPaRows * 64 / kThreads>(p, s, rows, hpk, L, tb0, Ls, vbase, rv);
+    else pa_values<kPaRows * 32 / kThreads>(p, s, rows, hpk, L, tb0, Ls, vbase, rv);
+}
+
 // ---------------------------------------------------------------- launchers
 
 template <int MODE>
@@ -813,7 +997,14 @@ hipError_t launch_pre_attention(const PreAttnArgs& p, int ntok, hipStream_t s) {
     hipLaunchKernelGGL(k_pre_rope, grid, dim3(kThreads), 0, s, p);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    hipLaunchKernelGGL(k_pre_attn, grid, dim3(kThreads), 0, s, p);
+    const int hpk = p.a.heads / p.a.kv_heads;
+    if (hpk <= kPaRows && (p.a.head_dim == 32 || p.a.head_dim == 64 || p.a.head_dim == 128) &&
+        p.pos0 + ntok <= kPaMaxL) {
+        const int tpb = kPaRows / hpk;
+        hipLaunchKernelGGL(k_pre_attn_blk, dim3((ntok + tpb - 1) / tpb, p.a.kv_heads), dim3(kThreads), 0, s, p, ntok);
+    } else {
+        hipLaunchKernelGGL(k_pre_attn, grid, dim3(kThreads), 0, s, p);
+    }
     return hipGetLastError();
 }
 
