@@ -490,14 +490,17 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 2))
 // the registers few, so several workgroups share a CU and one's copies overlap
 // the others' MFMAs.  The arithmetic is wchunk_compute's: exact int32 block
 // dots, the reference's float term and sum order.
-constexpr int kKqTok = 32;
+constexpr int kKqTokMax = 64;
+// tokens a workgroup: 64 for Q4_K (its per-sub-block weight decode is shared by 4 token groups), 32 for Q6_K (registers)
+template <uint32_t T>
+__host__ __device__ constexpr int kq_groups() { return T == kQ4_K ? 4 : 2; }
 
 struct KqStage {
     alignas(16) uint8_t w0[64 * 128];      // Q4_K nibbles / Q6_K ql: row r piece p at slot r * 8 + (p ^ (r & 7))
     alignas(16) uint8_t wk[4096];          // Q4_K: p1 [64][16] then p2 [64][16]; Q6_K: qh, row r piece p at r * 4 + (p ^ (r & 3))
     alignas(16) uint32_t wm[384];          // Q6_K: the 20-byte meta of row r at dwords 5 r .. 5 r + 4
-    alignas(16) int8_t x[kKqTok * 256];    // token t piece p at slot t * 16 + (p ^ (t & 15))
-    alignas(16) int32_t bs[kKqTok * 16];   // bsums of token t at 16 t
+    alignas(16) int8_t x[kKqTokMax * 256];   // token t piece p at slot t * 16 + (p ^ (t & 15))
+    alignas(16) int32_t bs[kKqTokMax * 16];  // bsums of token t at 16 t
     alignas(16) float xd[64];              // Q8_K scale of token t (lanes 32..63: a copy)
 };
 
@@ -542,13 +545,14 @@ __device__ __forceinline__ void kq_copy(KqStage& st, const Packed& m, const ActP
         }
     }
     const size_t bss = x.stride / 16, ds = x.stride / 32;
+    constexpr int G = kq_groups<T>();
 #pragma unroll
-    for (int k = 0; k < 2; ++k) {  // 32 tokens x 16 pieces
+    for (int k = 0; k < G; ++k) {  // 16 G tokens x 16 pieces
         const int slot = k * kThreads + tid, t = slot >> 4, p = (slot & 15) ^ (t & 15);
         dma16(x.qs + tokc(t) * x.stride + c * 256 + p * 16, st.x + (k * kThreads + wave_first) * 16);
     }
-    if (wave < 2) dma16(x.bs + tokc(tid >> 2) * bss + c * 16 + (tid & 3) * 4, st.bs + wave_first * 4);  // 32 tokens x 4 pieces
-    if (wave == 0) dma4(x.d + tokc(tid & 31) * ds + c, st.xd);
+    if (T != kQ4_K && wave < G) dma16(x.bs + tokc(tid >> 2) * bss + c * 16 + (tid & 3) * 4, st.bs + wave_first * 4);  // 16 G tokens x 4 pieces (Q4_K folds them into the MFMAs)
+    if (wave == 0) dma4(x.d + tokc(tid & (16 * G - 1)) * ds + c, st.xd);
 }
 
 __device__ __forceinline__ uint64_t lds8(const uint8_t* p) { return *reinterpret_cast<const uint64_t*>(p); }
@@ -660,28 +664,317 @@ __device__ __forceinline__ void kq_compute(const KqStage& st, MmAcc<2>& acc) {
     }
 }
 
-template <uint32_t T, int MODE>
-__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(3, 8))) void k_mmk(MmArgs g) {
-    __shared__ KqStage st;
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    const uint32_t rt0 = blockIdx.x * 64;
-    const int t0 = blockIdx.y * kKqTok;
-    const int nc = static_cast<int>(g.m.cols / 256);
-    MmAcc<2> a;
+// LDS reads issued as inline assembly.  The compiler waits for every
+// outstanding global_load_lds before any LDS read it can see (it cannot tell
+// which LDS bytes the copies write), which would drain the next chunk's copies
+// before the current chunk is computed.  These reads it does not see; their
+// completion is waited for explicitly (lds_wait, which ties the destination
+// registers so no use moves above it).
+typedef __attribute__((address_space(3))) const void* lds_cvoid_ptr;
+__device__ __forceinline__ uint32_t lds_off(const void* p) { return static_cast<uint32_t>(reinterpret_cast<uintptr_t>((lds_cvoid_ptr)p)); }
+__device__ __forceinline__ uint64_t ds64(uint32_t a) {
+    uint64_t r;
+    asm volatile("ds_read_b64 %0, %1" : "=v"(r) : "v"(a));
+    return r;
+}
+__device__ __forceinline__ uint32_t ds32(uint32_t a) {
+    uint32_t r;
+    asm volatile("ds_read_b32 %0, %1" : "=v"(r) : "v"(a));
+    return r;
+}
+typedef unsigned v4u __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ v4u ds128v(uint32_t a) {
+    v4u r;
+    asm volatile("ds_read_b128 %0, %1" : "=v"(r) : "v"(a));
+    return r;
+}
+__device__ __forceinline__ uint4 ds128(uint32_t a) {
+    const v4u r = ds128v(a);
+    return make_uint4(r.x, r.y, r.z, r.w);
+}
+
+// One sub-block's fragments: weights (a; Q6_K also h), the two token groups'
+// activations (b0, b1) and, for Q4_K, their bsum pairs (p0, p1).
+struct KqFrag {
+    uint64_t a, h, b0, b1, b2, b3, p0, p1, p2, p3;
+};
+
+template <uint32_t T>
+__device__ __forceinline__ KqFrag kq_frag_issue(uint32_t base, int jj, int ar, int tl, int kq) {
+    KqFrag f;
+    const int off = kq & 15;
+    if (T == kQ4_K) {
+        const int p = 2 * (jj >> 1) + (kq >> 4);
+        f.a = ds64(base + offsetof(KqStage, w0) + (ar * 8 + (p ^ (ar & 7))) * 16 + off);
+        f.h = 0;
+    } else {
+        const int half = jj >> 2, quarter = jj & 3;
+        const int lb = half * 64 + (quarter & 1) * 32 + kq, lp = lb >> 4;
+        f.a = ds64(base + offsetof(KqStage, w0) + (ar * 8 + (lp ^ (ar & 7))) * 16 + off);
+        const int hb = half * 32 + kq, hp = hb >> 4;
+        f.h = ds64(base + offsetof(KqStage, wk) + (ar * 4 + (hp ^ (ar & 3))) * 16 + off);
+    }
+    const int p = 2 * jj + (kq >> 4);
+    auto bfrag = [&](int g) -> uint64_t {
+        const int t = 16 * g + tl;
+        return ds64(base + offsetof(KqStage, x) + (t * 16 + (p ^ (t & 15))) * 16 + off);
+    };
+    auto pfrag = [&](int g) -> uint64_t { return ds64(base + offsetof(KqStage, bs) + ((16 * g + tl) * 16 + 2 * jj) * 4); };
+    constexpr int G = kq_groups<T>();
+    f.b0 = bfrag(0);
+    f.b1 = bfrag(1);
+    f.b2 = G > 2 ? bfrag(2) : 0;
+    f.b3 = G > 2 ? bfrag(3) : 0;
+    if (T == kQ4_K) {
+        f.p0 = pfrag(0);
+        f.p1 = pfrag(1);
+        f.p2 = G > 2 ? pfrag(2) : 0;
+        f.p3 = G > 2 ? pfrag(3) : 0;
+    } else {
+        f.p0 = f.p1 = f.p2 = f.p3 = 0;
+    }
+    return f;
+}
+__device__ __forceinline__ void kq_frag_wait(KqFrag& f) {
+    asm volatile("s_waitcnt lgkmcnt(0)"
+                 : "+v"(f.a), "+v"(f.h), "+v"(f.b0), "+v"(f.b1), "+v"(f.b2), "+v"(f.b3), "+v"(f.p0), "+v"(f.p1), "+v"(f.p2),
+                   "+v"(f.p3));
+}
+
+// kq_compute from the stage at LDS offset `base`, reading only through the
+// assembly reads above; sub-block jj + 1's fragments are in flight while jj's
+// MFMAs and integer epilogue run.
+template <uint32_t T>
+__device__ __forceinline__ void kq_compute_asm(uint32_t base, MmAcc<kq_groups<T>()>& acc) {
+    constexpr int G = kq_groups<T>();
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, kq = (lane >> 4) * 8, tl = lane & 15;
+    const int ar = wave * 16 + tl, orow0 = wave * 16 + (lane >> 4) * 4;
+    const v4i zero = {0, 0, 0, 0};
+    // per-chunk operands: the 4 output rows' scales, the groups' activation scales
+    uint4 sc4[4];
+    uint32_t dd[4], xd[4];
 #pragma unroll
-    for (int gi = 0; gi < 2; ++gi)
+    for (int i = 0; i < 4; ++i) {
+        if (T == kQ4_K) {
+            sc4[i] = ds128(base + offsetof(KqStage, wk) + 1024 + (orow0 + i) * 16);
+            dd[i] = ds32(base + offsetof(KqStage, wk) + (orow0 + i) * 16);
+        } else {
+            const uint32_t mrow = base + offsetof(KqStage, wm) + (orow0 + i) * 20;  // 4-byte aligned: dword reads
+            sc4[i].x = ds32(mrow);
+            sc4[i].y = ds32(mrow + 4);
+            sc4[i].z = ds32(mrow + 8);
+            sc4[i].w = ds32(mrow + 12);
+            dd[i] = ds32(mrow + 16);
+        }
+        xd[i] = i < G ? ds32(base + offsetof(KqStage, xd) + (16 * i + tl) * 4) : 0u;
+    }
+    asm volatile("s_waitcnt lgkmcnt(0)"
+                 : "+v"(sc4[0].x), "+v"(sc4[0].y), "+v"(sc4[0].z), "+v"(sc4[0].w), "+v"(sc4[1].x), "+v"(sc4[1].y),
+                   "+v"(sc4[1].z), "+v"(sc4[1].w), "+v"(sc4[2].x), "+v"(sc4[2].y), "+v"(sc4[2].z), "+v"(sc4[2].w));
+    asm volatile("s_waitcnt lgkmcnt(0)"
+                 : "+v"(sc4[3].x), "+v"(sc4[3].y), "+v"(sc4[3].z), "+v"(sc4[3].w), "+v"(dd[0]), "+v"(dd[1]), "+v"(dd[2]),
+                   "+v"(dd[3]), "+v"(xd[0]), "+v"(xd[1]), "+v"(xd[2]), "+v"(xd[3]));
+    KqFrag cur = kq_frag_issue<T>(base, 0, ar, tl, kq);
+    kq_frag_wait(cur);
+    int wsum[G][4], osum[G][4];
+#pragma unroll
+    for (int g = 0; g < G; ++g)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) wsum[g][i] = osum[g][i] = 0;
+    const bool lo_half = lane < 32;  // Q6_K: lanes 0..31 hold k 0..15 of a sub-block, 32..63 hold k 16..31
+    // block dots are below 2^23 in magnitude and scales below 2^8: 24-bit multiplies are exact
+#pragma unroll
+    for (int jj = 0; jj < 8; ++jj) {
+        KqFrag nxt;
+        if (jj < 7) nxt = kq_frag_issue<T>(base, jj + 1, ar, tl, kq);
+        const uint64_t bq[4] = {cur.b0, cur.b1, cur.b2, cur.b3};
+        if (T == kQ4_K) {
+            const uint64_t a = (jj & 1) ? ((cur.a >> 4) & (0x0F * kB01)) : (cur.a & (0x0F * kB01));
+            const int sh = 8 * (jj & 3);
+            int sc[4], mn[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                sc[i] = static_cast<int>((((jj >> 2) ? sc4[i].y : sc4[i].x) >> sh) & 0xFF);
+                mn[i] = static_cast<int>((((jj >> 2) ? sc4[i].w : sc4[i].z) >> sh) & 0xFF);
+            }
+            const uint64_t pq[4] = {cur.p0, cur.p1, cur.p2, cur.p3};
+#pragma unroll
+            for (int g = 0; g < G; ++g) {
+                const v4i d = mfma(a, bq[g], zero);
+                const int pair = static_cast<int>(pq[g]) + static_cast<int>(pq[g] >> 32);
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    wsum[g][i] += __mul24(sc[i], d[i]);
+                    osum[g][i] += __mul24(mn[i], pair);
+                }
+            }
+        } else {
+            const int quarter = jj & 3;
+            const uint64_t nib = quarter >= 2 ? ((cur.a >> 4) & (0x0F * kB01)) : (cur.a & (0x0F * kB01));
+            const uint64_t u = nib | (((cur.h >> (2 * quarter)) & (0x03 * kB01)) << 4);  // 0..63
+            const uint64_t tq = u ^ (0x20 * kB01);                                       // 6-bit two's complement of u - 32
+            const uint64_t a = tq | ((tq & (0x20 * kB01)) * 0x06);
+            const uint64_t a0 = lo_half ? a : 0ull, a1 = lo_half ? 0ull : a;  // groups 2 jj and 2 jj + 1 of 16
+            const int sh = (jj & 1) * 16;
+            int s0[4], s1[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const uint32_t word = (jj >> 1) == 0 ? sc4[i].x : (jj >> 1) == 1 ? sc4[i].y : (jj >> 1) == 2 ? sc4[i].z : sc4[i].w;
+                s0[i] = static_cast<int8_t>((word >> sh) & 0xFF);
+                s1[i] = static_cast<int8_t>((word >> (sh + 8)) & 0xFF);
+            }
+#pragma unroll
+            for (int g = 0; g < G; ++g) {
+                const v4i e = mfma(a0, bq[g], zero), f = mfma(a1, bq[g], zero);
+#pragma unroll
+                for (int i = 0; i < 4; ++i) wsum[g][i] += __mul24(s0[i], e[i]) + __mul24(s1[i], f[i]);
+            }
+        }
+        if (jj < 7) {
+            kq_frag_wait(nxt);
+            cur = nxt;
+        }
+    }
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+        const float xg = __uint_as_float(xd[g]);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            if (T == kQ4_K) {
+                const float d = h2f(static_cast<uint16_t>(dd[i] & 0xFFFF)), dmin = h2f(static_cast<uint16_t>(dd[i] >> 16));
+                acc.s[g][i] += xg * (d * static_cast<float>(wsum[g][i]) - dmin * static_cast<float>(osum[g][i]));  // src/quant.cpp:500-521
+            } else {
+                const float d = h2f(static_cast<uint16_t>(dd[i] & 0xFFFF));
+                acc.s[g][i] += xg * d * static_cast<float>(wsum[g][i]);  // src/quant.cpp:549-563
+            }
+        }
+    }
+}
+
+// Q4_K with the scales folded into the MFMAs.  For sub-block j of a row,
+// weighted = sum_j sc_j dot_j and offsets = sum_j mn_j pair_j (dot_q4_k_q8_k,
+// src/quant.cpp:500-521) are exact integers; with sc_j = lo_j + 8 hi_j (3-bit
+// digits) and q in 0..15, q lo_j and q hi_j fit int8, so
+//   weighted = A_lo + 8 A_hi,  A_lo = sum_k (q_k lo_j(k)) x_k,  A_hi likewise,
+//   offsets  = sum_k mn_j(k) x_k   (pair_j is the sum of sub-block j's x),
+// three int32 MFMA chains over the super-block, with no per-sub-block integer
+// epilogue.  The float term per super-block is the reference's.
+// The MFMA is v_mfma_i32_16x16x64_i8 (CDNA4's full-rate int8 shape): lane l
+// holds 16 consecutive k of A row l % 16 and of B column l % 16, k = 16 (l / 16)
+// .. + 15 of the 64, so lanes 0..31 are sub-block 2 s and lanes 32..63
+// sub-block 2 s + 1 of step s, and each lane's digit is its own sub-block's.
+__device__ __forceinline__ v4i mfma64(const v4u& a, const v4u& b, v4i c) {
+    return __builtin_amdgcn_mfma_i32_16x16x64_i8(__builtin_bit_cast(v4i, a), __builtin_bit_cast(v4i, b), c, 0, 0, 0);
+}
+
+// Fragments read by kq_f64_issue; kq_f64_wait ties each as one 128-bit operand,
+// so no copy of a fragment register can be placed before the wait.
+struct KqF64 {
+    v4u a, b0, b1, b2, b3;
+};
+__device__ __forceinline__ KqF64 kq_f64_issue(uint32_t base, int s, int ar, int tl, int l16) {
+    KqF64 f;
+    const int pa = 2 * s + (l16 & 1);  // Q4_K: 32 bytes of nibbles a sub-block pair, low then high
+    f.a = ds128v(base + offsetof(KqStage, w0) + (ar * 8 + (pa ^ (ar & 7))) * 16);
+    const int pb = 4 * s + l16;
+    auto bfrag = [&](int g) -> v4u {
+        const int t = 16 * g + tl;
+        return ds128v(base + offsetof(KqStage, x) + (t * 16 + (pb ^ (t & 15))) * 16);
+    };
+    f.b0 = bfrag(0);
+    f.b1 = bfrag(1);
+    f.b2 = bfrag(2);
+    f.b3 = bfrag(3);
+    return f;
+}
+__device__ __forceinline__ void kq_f64_wait(KqF64& f) {
+    asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(f.a), "+v"(f.b0), "+v"(f.b1), "+v"(f.b2), "+v"(f.b3));
+}
+
+__device__ __forceinline__ void kq_compute_fold(uint32_t base, MmAcc<4>& acc) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, tl = lane & 15, l16 = lane >> 4;
+    const int ar = wave * 16 + tl, orow0 = wave * 16 + l16 * 4;
+    const v4i zero = {0, 0, 0, 0};
+    // the A row's decoded scales and mins (for the digits), the output rows' d / dmin, the groups' x scales
+    v4u scm = ds128v(base + offsetof(KqStage, wk) + 1024 + ar * 16);
+    uint32_t dd[4], xd[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        dd[i] = ds32(base + offsetof(KqStage, wk) + (orow0 + i) * 16);
+        xd[i] = ds32(base + offsetof(KqStage, xd) + (16 * i + tl) * 4);
+    }
+    asm volatile("s_waitcnt lgkmcnt(0)"
+                 : "+v"(scm), "+v"(dd[0]), "+v"(dd[1]), "+v"(dd[2]), "+v"(dd[3]), "+v"(xd[0]), "+v"(xd[1]), "+v"(xd[2]),
+                   "+v"(xd[3]));
+    KqF64 cur = kq_f64_issue(base, 0, ar, tl, l16);
+    kq_f64_wait(cur);
+    v4i alo[4], ahi[4], amn[4];
+#pragma unroll
+    for (int g = 0; g < 4; ++g) alo[g] = ahi[g] = amn[g] = zero;
+    const bool hi_nib = l16 >= 2;  // lanes 32..63: the odd sub-block of the pair (high nibbles)
+#pragma unroll
+    for (int st = 0; st < 4; ++st) {
+        KqF64 nxt;
+        if (st < 3) nxt = kq_f64_issue(base, st + 1, ar, tl, l16);
+        const int j = 2 * st + (l16 >> 1);  // this lane's sub-block
+        const uint32_t sc = ((j < 4 ? scm.x : scm.y) >> (8 * (j & 3))) & 0xFF;
+        const uint32_t mn = ((j < 4 ? scm.z : scm.w) >> (8 * (j & 3))) & 0xFF;
+        const uint32_t dlo = sc & 7, dhi = sc >> 3, m4 = mn * 0x01010101u;
+        const v4u qn = hi_nib ? ((cur.a >> 4) & 0x0F0F0F0Fu) : (cur.a & 0x0F0F0F0Fu);
+        const v4u qlo = qn * dlo;  // bytes 0..15 times 0..7: no carries between bytes
+        const v4u qhi = qn * dhi;
+        const v4u qmn = {m4, m4, m4, m4};
+        const v4u bq[4] = {cur.b0, cur.b1, cur.b2, cur.b3};
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+            alo[g] = mfma64(qlo, bq[g], alo[g]);
+            ahi[g] = mfma64(qhi, bq[g], ahi[g]);
+            amn[g] = mfma64(qmn, bq[g], amn[g]);
+        }
+        if (st < 3) {
+            kq_f64_wait(nxt);
+            cur = nxt;
+        }
+    }
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+        const float xg = __uint_as_float(xd[g]);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int weighted = alo[g][i] + 8 * ahi[g][i], offsets = amn[g][i];
+            const float d = h2f(static_cast<uint16_t>(dd[i] & 0xFFFF)), dmin = h2f(static_cast<uint16_t>(dd[i] >> 16));
+            acc.s[g][i] += xg * (d * static_cast<float>(weighted) - dmin * static_cast<float>(offsets));  // src/quant.cpp:500-521
+        }
+    }
+}
+
+template <uint32_t T, int MODE>
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 8))) void k_mmk(MmArgs g) {
+    __shared__ KqStage st[2];
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    constexpr int G = kq_groups<T>();
+    const uint32_t rt0 = blockIdx.x * 64;
+    const int t0 = blockIdx.y * (16 * G);
+    const int nc = static_cast<int>(g.m.cols / 256);
+    MmAcc<G> a;
+#pragma unroll
+    for (int gi = 0; gi < G; ++gi)
 #pragma unroll
         for (int i = 0; i < 4; ++i) a.s[gi][i] = 0.0f;
+    // two stages: chunk c + 1 is copied while chunk c is computed
+    kq_copy<T>(st[0], g.m, g.x, g.ntok, rt0, t0, 0);
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
     for (int c = 0; c < nc; ++c) {
-        if (c > 0) __syncthreads();  // the previous chunk is consumed
-        kq_copy<T>(st, g.m, g.x, g.ntok, rt0, t0, c);
-        __builtin_amdgcn_s_waitcnt(0);
-        __syncthreads();
-        kq_compute<T>(st, a);
+        if (c + 1 < nc) kq_copy<T>(st[(c + 1) & 1], g.m, g.x, g.ntok, rt0, t0, c + 1);
+        if constexpr (T == kQ4_K) kq_compute_fold(lds_off(&st[c & 1]), a);
+        else kq_compute_asm<T>(lds_off(&st[c & 1]), a);
+        __builtin_amdgcn_s_waitcnt(0);  // chunk c + 1 has landed (this wave's copies) ...
+        __syncthreads();                // ... everyone's, and stage c & 1 is consumed
     }
     const uint32_t rmax = g.m.rows - 1;
 #pragma unroll
-    for (int gi = 0; gi < 2; ++gi) {
+    for (int gi = 0; gi < G; ++gi) {
         const int t = t0 + 16 * gi + (lane & 15);
         if (t >= g.ntok) continue;
 #pragma unroll
@@ -942,7 +1235,8 @@ template <int MODE>
 static hipError_t mm_dispatch(const MmArgs& g, hipStream_t s) {
     const int tok = 16 * (g.m.type == kQ4_K || g.m.type == kQ6_K ? mm_groups<kQ4_K>() : mm_groups<kQ4_0>());
     const dim3 grid((g.m.rows + kRowsPerWg - 1) / kRowsPerWg, (g.ntok + tok - 1) / tok);
-    const dim3 kq_grid((g.m.rows + 63) / 64, (g.ntok + kKqTok - 1) / kKqTok);
+    const int kq_tok = 16 * (g.m.type == kQ4_K ? kq_groups<kQ4_K>() : kq_groups<kQ6_K>());
+    const dim3 kq_grid((g.m.rows + 63) / 64, (g.ntok + kq_tok - 1) / kq_tok);
     switch (g.m.type) {
         case kQ4_0: hipLaunchKernelGGL((k_mm<kQ4_0, MODE>), grid, dim3(kThreads), 0, s, g); break;
         case kQ8_0: hipLaunchKernelGGL((k_mm<kQ8_0, MODE>), grid, dim3(kThreads), 0, s, g); break;
