@@ -228,6 +228,7 @@ __device__ __forceinline__ bool run_tiles(int total, GemvLds& s, RowOf row_of, R
             if (!done(u, mu, r0, s.sums + off)) return false;
             off += Ru;
         }
+        pst(st, 5);
         grows = 0;
         return true;
     };
@@ -877,6 +878,7 @@ __device__ __forceinline__ bool phase_d(const LoopArgs& g, const LayerDev& L, in
                     tput(g.actt + r0 + r, out, tag);
                 }
             }
+            pst(st, 5);
             grows = 0;
             gfirst = tn;
         }

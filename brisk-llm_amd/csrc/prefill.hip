@@ -1047,13 +1047,13 @@ __global__ __launch_bounds__(kThreads) void k_pre_attn(PreAttnArgs p) {
 
 // Attention of a block of tokens over one key/value head, in the reference's
 // order per query row (the same arithmetic as attn_exact): a workgroup takes
-// kPaRows query rows (16 / hpk tokens x the hpk query heads of kv head
+// kPaRows query rows (8 / hpk tokens x the hpk query heads of kv head
 // blockIdx.y), so each staged key or value chunk serves all of them.  Scores
 // for every visible position go to LDS (causal: token t sees positions up to
 // pos0 + t), then softmax a row a wave, then value sums in position order, one
 // (row, dimension) chain a lane.  The cache holds every position (k_pre_rope
 // wrote this prompt's rows).
-constexpr int kPaRows = 16;
+constexpr int kPaRows = 8;
 constexpr int kPaMaxL = kExactMax;
 
 struct PaLds {
@@ -1184,7 +1184,7 @@ __device__ __forceinline__ void pa_values(const PreAttnArgs& p, PaLds& s, int ro
     }
 }
 
-__global__ __launch_bounds__(kThreads) void k_pre_attn_blk(PreAttnArgs p, int ntok) {
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 8))) void k_pre_attn_blk(PreAttnArgs p, int ntok) {
     __shared__ PaLds s;
     const AttnArgs& g = p.a;
     const int hpk = g.heads / g.kv_heads, hd = g.head_dim, kv = blockIdx.y;
