@@ -635,6 +635,30 @@ void Session::eval(const int32_t* tokens, size_t n, float* logits) {
 void Session::eval_all(const int32_t* tokens, size_t n, float* logits) {
     if (n == 0 || n > 64) throw Error(BRISK_HIP_EINVAL, "model: eval_all takes 1 to 64 tokens");
     validate(tokens, n);
+    if (use_prefill(n)) {
+        // every row through the batched layers, then output_norm and the output rows
+        // for all of them as one GEMM (the logits of eval_batch with all rows,
+        // src/model.cpp:712-714, :1195-1205); the last row's head also leaves the
+        // pending greedy pick, as eval does
+        ensure_prefill();
+        if (all_logits_ == nullptr) all_logits_ = static_cast<float*>(alloc(static_cast<size_t>(64) * cfg_.vocab * 4));
+        stage(tokens, n, position_ + n - 1);
+        const int T = static_cast<int>(n);
+        prefill_layers(position_, T);
+        prefill_quant(pre_h_, static_cast<int>(cfg_.embd), out_norm_, static_cast<int>(cfg_.embd), T, *out_);
+        MmArgs g{};
+        g.m = out_->p; g.x = pre_x_; g.ntok = T; g.out = all_logits_; g.ostride = static_cast<int>(cfg_.vocab);
+        check(launch_mm(g, kMmStore, stream_), "eval_all output");
+        HeadArgs ha{};
+        ha.m = out_->p; ha.x = pre_h_ + static_cast<size_t>(T - 1) * cfg_.embd; ha.normw = out_norm_;
+        ha.eps = cfg_.rms_epsilon; ha.logits = nullptr; ha.key = key_;
+        check(launch_head(ha, stream_), "output");
+        finish();
+        check(hipMemcpyAsync(logits, all_logits_, n * cfg_.vocab * 4, hipMemcpyDeviceToHost, stream_), "hipMemcpy(logits)");
+        check(hipStreamSynchronize(stream_), "eval_all sync");
+        position_ += n;
+        return;
+    }
     stage(tokens, n);
     for (size_t i = 0; i < n; ++i) {
         if (uses_loop()) {

@@ -121,6 +121,7 @@ private:
     bool prefill_on_ = true;
     float *pre_h_ = nullptr, *pre_q_ = nullptr, *pre_k_ = nullptr, *pre_v_ = nullptr, *pre_att_ = nullptr, *pre_act_ = nullptr;
     ActPlanar pre_x_{};
+    float* all_logits_ = nullptr;  // eval_all's [64][vocab] logits, allocated on first use
     hipGraphExec_t graph_layers_ = nullptr, graph_full_ = nullptr;
 };
 

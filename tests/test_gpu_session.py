@@ -68,6 +68,12 @@ def test_eval_all_and_rollback(pair):
     got, want = s.eval_all(toks), o.eval(toks, all_logits=True)
     assert got.shape == (5, cfg.vocab)
     assert np.abs(got - want).max() <= TOL
+    # the batched rows (prefill GEMMs, then the output rows for all of them) are the reference's to the bit
+    np.testing.assert_array_equal(got.view(np.uint32), want.view(np.uint32), err_msg=name)
+    # and decoding continues from the last row's pick
+    ids = s.decode(3)
+    o_ids, _ = o.generate([int(np.argmax(want[-1]))], 3)
+    np.testing.assert_array_equal(ids, o_ids, err_msg=name)
     # roll back to 2 and continue: the same as evaluating from there in one go
     s.rollback(2)
     o.rollback(2)
