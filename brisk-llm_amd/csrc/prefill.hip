@@ -491,9 +491,9 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 2))
 // the others' MFMAs.  The arithmetic is wchunk_compute's: exact int32 block
 // dots, the reference's float term and sum order.
 constexpr int kKqTokMax = 64;
-// tokens a workgroup: 64 for Q4_K (its per-sub-block weight decode is shared by 4 token groups), 32 for Q6_K (registers)
-template <uint32_t T>
-__host__ __device__ constexpr int kq_groups() { return T == kQ4_K ? 4 : 2; }
+constexpr int kKqCus = 256;  // MI355X compute units (the tile choice aims at a workgroup each)
+// tokens a workgroup: 16 G (G token groups share each weight fragment's decode); the
+// launcher takes the largest G that still gives a workgroup to every CU
 
 struct KqStage {
     alignas(16) uint8_t w0[64 * 128];      // Q4_K nibbles / Q6_K ql: row r piece p at slot r * 8 + (p ^ (r & 7))
@@ -513,7 +513,7 @@ __device__ __forceinline__ void dma4(const void* src, void* lds_wave_base) {
 
 // Copies chunk c of rows r0 .. r0 + 63 and tokens t0 .. t0 + 31 into the stage
 // (rows and tokens past the ends re-read the last one; their outputs are not stored).
-template <uint32_t T>
+template <uint32_t T, int G>
 __device__ __forceinline__ void kq_copy(KqStage& st, const Packed& m, const ActPlanar& x, int ntok, uint32_t r0, int t0, int c) {
     const int tid = threadIdx.x, wave = tid >> 6, wave_first = tid & ~63;
     const uint32_t nsb = m.cols / 256, rmax = m.rows - 1;
@@ -544,124 +544,13 @@ __device__ __forceinline__ void kq_copy(KqStage& st, const Packed& m, const ActP
             }
         }
     }
-    const size_t bss = x.stride / 16, ds = x.stride / 32;
-    constexpr int G = kq_groups<T>();
+    const size_t ds = x.stride / 32;
 #pragma unroll
-    for (int k = 0; k < G; ++k) {  // 16 G tokens x 16 pieces
+    for (int k = 0; k < G; ++k) {  // 16 G tokens x 16 pieces, G a thread
         const int slot = k * kThreads + tid, t = slot >> 4, p = (slot & 15) ^ (t & 15);
         dma16(x.qs + tokc(t) * x.stride + c * 256 + p * 16, st.x + (k * kThreads + wave_first) * 16);
     }
-    if (T != kQ4_K && wave < G) dma16(x.bs + tokc(tid >> 2) * bss + c * 16 + (tid & 3) * 4, st.bs + wave_first * 4);  // 16 G tokens x 4 pieces (Q4_K folds them into the MFMAs)
     if (wave == 0) dma4(x.d + tokc(tid & (16 * G - 1)) * ds + c, st.xd);
-}
-
-__device__ __forceinline__ uint64_t lds8(const uint8_t* p) { return *reinterpret_cast<const uint64_t*>(p); }
-
-// The chunk's contribution to the lane's outputs (tokens 16 g + l % 16, rows 16 w + 4 (l / 16) + i).
-template <uint32_t T>
-__device__ __forceinline__ void kq_compute(const KqStage& st, MmAcc<2>& acc) {
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, kq = (lane >> 4) * 8, tl = lane & 15;
-    const int ar = wave * 16 + tl;  // the A fragment's row within the tile
-    const v4i zero = {0, 0, 0, 0};
-    auto xfrag = [&](int g, int jj) -> uint64_t {
-        const int t = 16 * g + tl, byte = jj * 32 + kq, p = byte >> 4;
-        return lds8(reinterpret_cast<const uint8_t*>(st.x) + (t * 16 + (p ^ (t & 15))) * 16 + (byte & 15));
-    };
-    auto w0frag = [&](int byte) -> uint64_t {
-        const int p = byte >> 4;
-        return lds8(st.w0 + (ar * 8 + (p ^ (ar & 7))) * 16 + (byte & 15));
-    };
-    if (T == kQ4_K) {
-        uint4 scm[4];
-        uint32_t dd[4];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int orow = wave * 16 + (lane >> 4) * 4 + i;
-            scm[i] = *reinterpret_cast<const uint4*>(st.wk + 1024 + orow * 16);
-            dd[i] = *reinterpret_cast<const uint32_t*>(st.wk + orow * 16);
-        }
-        int wsum[2][4], osum[2][4];
-#pragma unroll
-        for (int g = 0; g < 2; ++g)
-#pragma unroll
-            for (int i = 0; i < 4; ++i) wsum[g][i] = osum[g][i] = 0;
-#pragma unroll
-        for (int jj = 0; jj < 8; ++jj) {
-            const uint64_t w = w0frag((jj >> 1) * 32 + kq);
-            const uint64_t a = (jj & 1) ? ((w >> 4) & (0x0F * kB01)) : (w & (0x0F * kB01));
-            const int sh = 8 * (jj & 3);
-            int sc[4], mn[4];
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                sc[i] = static_cast<int>((((jj >> 2) ? scm[i].y : scm[i].x) >> sh) & 0xFF);
-                mn[i] = static_cast<int>((((jj >> 2) ? scm[i].w : scm[i].z) >> sh) & 0xFF);
-            }
-#pragma unroll
-            for (int g = 0; g < 2; ++g) {
-                const int t = 16 * g + tl;
-                const v4i d = mfma(a, xfrag(g, jj), zero);
-                const int pair = st.bs[t * 16 + 2 * jj] + st.bs[t * 16 + 2 * jj + 1];
-#pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    wsum[g][i] += sc[i] * d[i];
-                    osum[g][i] += mn[i] * pair;
-                }
-            }
-        }
-#pragma unroll
-        for (int g = 0; g < 2; ++g) {
-            const float xd = st.xd[16 * g + tl];
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const float d = h2f(static_cast<uint16_t>(dd[i] & 0xFFFF)), dmin = h2f(static_cast<uint16_t>(dd[i] >> 16));
-                acc.s[g][i] += xd * (d * static_cast<float>(wsum[g][i]) - dmin * static_cast<float>(osum[g][i]));  // src/quant.cpp:500-521
-            }
-        }
-    } else {  // Q6_K
-        const bool lo_half = lane < 32;  // lanes 0..31 hold k 0..15 of a sub-block, 32..63 hold k 16..31
-        const int orow0 = wave * 16 + (lane >> 4) * 4;
-        int wsum[2][4];
-#pragma unroll
-        for (int g = 0; g < 2; ++g)
-#pragma unroll
-            for (int i = 0; i < 4; ++i) wsum[g][i] = 0;
-#pragma unroll 2
-        for (int jj = 0; jj < 8; ++jj) {
-            const int half = jj >> 2, quarter = jj & 3;
-            const uint64_t l = w0frag(half * 64 + (quarter & 1) * 32 + kq);
-            const int hb = half * 32 + kq, hp = hb >> 4;
-            const uint64_t h = lds8(st.wk + (ar * 4 + (hp ^ (ar & 3))) * 16 + (hb & 15));
-            const uint64_t nib = quarter >= 2 ? ((l >> 4) & (0x0F * kB01)) : (l & (0x0F * kB01));
-            const uint64_t u = nib | (((h >> (2 * quarter)) & (0x03 * kB01)) << 4);  // 0..63
-            const uint64_t tq = u ^ (0x20 * kB01);                                   // 6-bit two's complement of u - 32
-            const uint64_t a = tq | ((tq & (0x20 * kB01)) * 0x06);
-            const uint64_t a0 = lo_half ? a : 0ull, a1 = lo_half ? 0ull : a;  // groups 2 jj and 2 jj + 1 of 16
-            const int sh = (jj & 1) * 16;
-            int s0[4], s1[4];
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const uint32_t word = st.wm[(orow0 + i) * 5 + (jj >> 1)];
-                s0[i] = static_cast<int8_t>((word >> sh) & 0xFF);
-                s1[i] = static_cast<int8_t>((word >> (sh + 8)) & 0xFF);
-            }
-#pragma unroll
-            for (int g = 0; g < 2; ++g) {
-                const uint64_t b = xfrag(g, jj);
-                const v4i d0 = mfma(a0, b, zero), d1 = mfma(a1, b, zero);
-#pragma unroll
-                for (int i = 0; i < 4; ++i) wsum[g][i] += s0[i] * d0[i] + s1[i] * d1[i];
-            }
-        }
-#pragma unroll
-        for (int g = 0; g < 2; ++g) {
-            const float xd = st.xd[16 * g + tl];
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const float d = h2f(static_cast<uint16_t>(st.wm[(orow0 + i) * 5 + 4] & 0xFFFF));
-                acc.s[g][i] += xd * d * static_cast<float>(wsum[g][i]);  // src/quant.cpp:549-563
-            }
-        }
-    }
 }
 
 // LDS reads issued as inline assembly.  The compiler waits for every
@@ -693,164 +582,6 @@ __device__ __forceinline__ uint4 ds128(uint32_t a) {
     return make_uint4(r.x, r.y, r.z, r.w);
 }
 
-// One sub-block's fragments: weights (a; Q6_K also h), the two token groups'
-// activations (b0, b1) and, for Q4_K, their bsum pairs (p0, p1).
-struct KqFrag {
-    uint64_t a, h, b0, b1, b2, b3, p0, p1, p2, p3;
-};
-
-template <uint32_t T>
-__device__ __forceinline__ KqFrag kq_frag_issue(uint32_t base, int jj, int ar, int tl, int kq) {
-    KqFrag f;
-    const int off = kq & 15;
-    if (T == kQ4_K) {
-        const int p = 2 * (jj >> 1) + (kq >> 4);
-        f.a = ds64(base + offsetof(KqStage, w0) + (ar * 8 + (p ^ (ar & 7))) * 16 + off);
-        f.h = 0;
-    } else {
-        const int half = jj >> 2, quarter = jj & 3;
-        const int lb = half * 64 + (quarter & 1) * 32 + kq, lp = lb >> 4;
-        f.a = ds64(base + offsetof(KqStage, w0) + (ar * 8 + (lp ^ (ar & 7))) * 16 + off);
-        const int hb = half * 32 + kq, hp = hb >> 4;
-        f.h = ds64(base + offsetof(KqStage, wk) + (ar * 4 + (hp ^ (ar & 3))) * 16 + off);
-    }
-    const int p = 2 * jj + (kq >> 4);
-    auto bfrag = [&](int g) -> uint64_t {
-        const int t = 16 * g + tl;
-        return ds64(base + offsetof(KqStage, x) + (t * 16 + (p ^ (t & 15))) * 16 + off);
-    };
-    auto pfrag = [&](int g) -> uint64_t { return ds64(base + offsetof(KqStage, bs) + ((16 * g + tl) * 16 + 2 * jj) * 4); };
-    constexpr int G = kq_groups<T>();
-    f.b0 = bfrag(0);
-    f.b1 = bfrag(1);
-    f.b2 = G > 2 ? bfrag(2) : 0;
-    f.b3 = G > 2 ? bfrag(3) : 0;
-    if (T == kQ4_K) {
-        f.p0 = pfrag(0);
-        f.p1 = pfrag(1);
-        f.p2 = G > 2 ? pfrag(2) : 0;
-        f.p3 = G > 2 ? pfrag(3) : 0;
-    } else {
-        f.p0 = f.p1 = f.p2 = f.p3 = 0;
-    }
-    return f;
-}
-__device__ __forceinline__ void kq_frag_wait(KqFrag& f) {
-    asm volatile("s_waitcnt lgkmcnt(0)"
-                 : "+v"(f.a), "+v"(f.h), "+v"(f.b0), "+v"(f.b1), "+v"(f.b2), "+v"(f.b3), "+v"(f.p0), "+v"(f.p1), "+v"(f.p2),
-                   "+v"(f.p3));
-}
-
-// kq_compute from the stage at LDS offset `base`, reading only through the
-// assembly reads above; sub-block jj + 1's fragments are in flight while jj's
-// MFMAs and integer epilogue run.
-template <uint32_t T>
-__device__ __forceinline__ void kq_compute_asm(uint32_t base, MmAcc<kq_groups<T>()>& acc) {
-    constexpr int G = kq_groups<T>();
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, kq = (lane >> 4) * 8, tl = lane & 15;
-    const int ar = wave * 16 + tl, orow0 = wave * 16 + (lane >> 4) * 4;
-    const v4i zero = {0, 0, 0, 0};
-    // per-chunk operands: the 4 output rows' scales, the groups' activation scales
-    uint4 sc4[4];
-    uint32_t dd[4], xd[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        if (T == kQ4_K) {
-            sc4[i] = ds128(base + offsetof(KqStage, wk) + 1024 + (orow0 + i) * 16);
-            dd[i] = ds32(base + offsetof(KqStage, wk) + (orow0 + i) * 16);
-        } else {
-            const uint32_t mrow = base + offsetof(KqStage, wm) + (orow0 + i) * 20;  // 4-byte aligned: dword reads
-            sc4[i].x = ds32(mrow);
-            sc4[i].y = ds32(mrow + 4);
-            sc4[i].z = ds32(mrow + 8);
-            sc4[i].w = ds32(mrow + 12);
-            dd[i] = ds32(mrow + 16);
-        }
-        xd[i] = i < G ? ds32(base + offsetof(KqStage, xd) + (16 * i + tl) * 4) : 0u;
-    }
-    asm volatile("s_waitcnt lgkmcnt(0)"
-                 : "+v"(sc4[0].x), "+v"(sc4[0].y), "+v"(sc4[0].z), "+v"(sc4[0].w), "+v"(sc4[1].x), "+v"(sc4[1].y),
-                   "+v"(sc4[1].z), "+v"(sc4[1].w), "+v"(sc4[2].x), "+v"(sc4[2].y), "+v"(sc4[2].z), "+v"(sc4[2].w));
-    asm volatile("s_waitcnt lgkmcnt(0)"
-                 : "+v"(sc4[3].x), "+v"(sc4[3].y), "+v"(sc4[3].z), "+v"(sc4[3].w), "+v"(dd[0]), "+v"(dd[1]), "+v"(dd[2]),
-                   "+v"(dd[3]), "+v"(xd[0]), "+v"(xd[1]), "+v"(xd[2]), "+v"(xd[3]));
-    KqFrag cur = kq_frag_issue<T>(base, 0, ar, tl, kq);
-    kq_frag_wait(cur);
-    int wsum[G][4], osum[G][4];
-#pragma unroll
-    for (int g = 0; g < G; ++g)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) wsum[g][i] = osum[g][i] = 0;
-    const bool lo_half = lane < 32;  // Q6_K: lanes 0..31 hold k 0..15 of a sub-block, 32..63 hold k 16..31
-    // block dots are below 2^23 in magnitude and scales below 2^8: 24-bit multiplies are exact
-#pragma unroll
-    for (int jj = 0; jj < 8; ++jj) {
-        KqFrag nxt;
-        if (jj < 7) nxt = kq_frag_issue<T>(base, jj + 1, ar, tl, kq);
-        const uint64_t bq[4] = {cur.b0, cur.b1, cur.b2, cur.b3};
-        if (T == kQ4_K) {
-            const uint64_t a = (jj & 1) ? ((cur.a >> 4) & (0x0F * kB01)) : (cur.a & (0x0F * kB01));
-            const int sh = 8 * (jj & 3);
-            int sc[4], mn[4];
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                sc[i] = static_cast<int>((((jj >> 2) ? sc4[i].y : sc4[i].x) >> sh) & 0xFF);
-                mn[i] = static_cast<int>((((jj >> 2) ? sc4[i].w : sc4[i].z) >> sh) & 0xFF);
-            }
-            const uint64_t pq[4] = {cur.p0, cur.p1, cur.p2, cur.p3};
-#pragma unroll
-            for (int g = 0; g < G; ++g) {
-                const v4i d = mfma(a, bq[g], zero);
-                const int pair = static_cast<int>(pq[g]) + static_cast<int>(pq[g] >> 32);
-#pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    wsum[g][i] += __mul24(sc[i], d[i]);
-                    osum[g][i] += __mul24(mn[i], pair);
-                }
-            }
-        } else {
-            const int quarter = jj & 3;
-            const uint64_t nib = quarter >= 2 ? ((cur.a >> 4) & (0x0F * kB01)) : (cur.a & (0x0F * kB01));
-            const uint64_t u = nib | (((cur.h >> (2 * quarter)) & (0x03 * kB01)) << 4);  // 0..63
-            const uint64_t tq = u ^ (0x20 * kB01);                                       // 6-bit two's complement of u - 32
-            const uint64_t a = tq | ((tq & (0x20 * kB01)) * 0x06);
-            const uint64_t a0 = lo_half ? a : 0ull, a1 = lo_half ? 0ull : a;  // groups 2 jj and 2 jj + 1 of 16
-            const int sh = (jj & 1) * 16;
-            int s0[4], s1[4];
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const uint32_t word = (jj >> 1) == 0 ? sc4[i].x : (jj >> 1) == 1 ? sc4[i].y : (jj >> 1) == 2 ? sc4[i].z : sc4[i].w;
-                s0[i] = static_cast<int8_t>((word >> sh) & 0xFF);
-                s1[i] = static_cast<int8_t>((word >> (sh + 8)) & 0xFF);
-            }
-#pragma unroll
-            for (int g = 0; g < G; ++g) {
-                const v4i e = mfma(a0, bq[g], zero), f = mfma(a1, bq[g], zero);
-#pragma unroll
-                for (int i = 0; i < 4; ++i) wsum[g][i] += __mul24(s0[i], e[i]) + __mul24(s1[i], f[i]);
-            }
-        }
-        if (jj < 7) {
-            kq_frag_wait(nxt);
-            cur = nxt;
-        }
-    }
-#pragma unroll
-    for (int g = 0; g < G; ++g) {
-        const float xg = __uint_as_float(xd[g]);
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            if (T == kQ4_K) {
-                const float d = h2f(static_cast<uint16_t>(dd[i] & 0xFFFF)), dmin = h2f(static_cast<uint16_t>(dd[i] >> 16));
-                acc.s[g][i] += xg * (d * static_cast<float>(wsum[g][i]) - dmin * static_cast<float>(osum[g][i]));  // src/quant.cpp:500-521
-            } else {
-                const float d = h2f(static_cast<uint16_t>(dd[i] & 0xFFFF));
-                acc.s[g][i] += xg * d * static_cast<float>(wsum[g][i]);  // src/quant.cpp:549-563
-            }
-        }
-    }
-}
-
 // Q4_K with the scales folded into the MFMAs.  For sub-block j of a row,
 // weighted = sum_j sc_j dot_j and offsets = sum_j mn_j pair_j (dot_q4_k_q8_k,
 // src/quant.cpp:500-521) are exact integers; with sc_j = lo_j + 8 hi_j (3-bit
@@ -870,8 +601,9 @@ __device__ __forceinline__ v4i mfma64(const v4u& a, const v4u& b, v4i c) {
 // Fragments read by kq_f64_issue; kq_f64_wait ties each as one 128-bit operand,
 // so no copy of a fragment register can be placed before the wait.
 struct KqF64 {
-    v4u a, b0, b1, b2, b3;
+    v4u a, b0, b1, b2, b3;  // b0 .. b(G-1) used
 };
+template <int G>
 __device__ __forceinline__ KqF64 kq_f64_issue(uint32_t base, int s, int ar, int tl, int l16) {
     KqF64 f;
     const int pa = 2 * s + (l16 & 1);  // Q4_K: 32 bytes of nibbles a sub-block pair, low then high
@@ -881,17 +613,19 @@ __device__ __forceinline__ KqF64 kq_f64_issue(uint32_t base, int s, int ar, int 
         const int t = 16 * g + tl;
         return ds128v(base + offsetof(KqStage, x) + (t * 16 + (pb ^ (t & 15))) * 16);
     };
+    const v4u z = {0u, 0u, 0u, 0u};
     f.b0 = bfrag(0);
-    f.b1 = bfrag(1);
-    f.b2 = bfrag(2);
-    f.b3 = bfrag(3);
+    f.b1 = G > 1 ? bfrag(1) : z;
+    f.b2 = G > 2 ? bfrag(2) : z;
+    f.b3 = G > 3 ? bfrag(3) : z;
     return f;
 }
 __device__ __forceinline__ void kq_f64_wait(KqF64& f) {
     asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(f.a), "+v"(f.b0), "+v"(f.b1), "+v"(f.b2), "+v"(f.b3));
 }
 
-__device__ __forceinline__ void kq_compute_fold(uint32_t base, MmAcc<4>& acc) {
+template <int G>
+__device__ __forceinline__ void kq_compute_fold(uint32_t base, MmAcc<G>& acc) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, tl = lane & 15, l16 = lane >> 4;
     const int ar = wave * 16 + tl, orow0 = wave * 16 + l16 * 4;
     const v4i zero = {0, 0, 0, 0};
@@ -901,21 +635,21 @@ __device__ __forceinline__ void kq_compute_fold(uint32_t base, MmAcc<4>& acc) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
         dd[i] = ds32(base + offsetof(KqStage, wk) + (orow0 + i) * 16);
-        xd[i] = ds32(base + offsetof(KqStage, xd) + (16 * i + tl) * 4);
+        xd[i] = i < G ? ds32(base + offsetof(KqStage, xd) + (16 * i + tl) * 4) : 0u;
     }
     asm volatile("s_waitcnt lgkmcnt(0)"
                  : "+v"(scm), "+v"(dd[0]), "+v"(dd[1]), "+v"(dd[2]), "+v"(dd[3]), "+v"(xd[0]), "+v"(xd[1]), "+v"(xd[2]),
                    "+v"(xd[3]));
-    KqF64 cur = kq_f64_issue(base, 0, ar, tl, l16);
+    KqF64 cur = kq_f64_issue<G>(base, 0, ar, tl, l16);
     kq_f64_wait(cur);
     v4i alo[4], ahi[4], amn[4];
 #pragma unroll
-    for (int g = 0; g < 4; ++g) alo[g] = ahi[g] = amn[g] = zero;
+    for (int g = 0; g < G; ++g) alo[g] = ahi[g] = amn[g] = zero;
     const bool hi_nib = l16 >= 2;  // lanes 32..63: the odd sub-block of the pair (high nibbles)
 #pragma unroll
     for (int st = 0; st < 4; ++st) {
         KqF64 nxt;
-        if (st < 3) nxt = kq_f64_issue(base, st + 1, ar, tl, l16);
+        if (st < 3) nxt = kq_f64_issue<G>(base, st + 1, ar, tl, l16);
         const int j = 2 * st + (l16 >> 1);  // this lane's sub-block
         const uint32_t sc = ((j < 4 ? scm.x : scm.y) >> (8 * (j & 3))) & 0xFF;
         const uint32_t mn = ((j < 4 ? scm.z : scm.w) >> (8 * (j & 3))) & 0xFF;
@@ -926,7 +660,7 @@ __device__ __forceinline__ void kq_compute_fold(uint32_t base, MmAcc<4>& acc) {
         const v4u qmn = {m4, m4, m4, m4};
         const v4u bq[4] = {cur.b0, cur.b1, cur.b2, cur.b3};
 #pragma unroll
-        for (int g = 0; g < 4; ++g) {
+        for (int g = 0; g < G; ++g) {
             alo[g] = mfma64(qlo, bq[g], alo[g]);
             ahi[g] = mfma64(qhi, bq[g], ahi[g]);
             amn[g] = mfma64(qmn, bq[g], amn[g]);
@@ -937,7 +671,7 @@ __device__ __forceinline__ void kq_compute_fold(uint32_t base, MmAcc<4>& acc) {
         }
     }
 #pragma unroll
-    for (int g = 0; g < 4; ++g) {
+    for (int g = 0; g < G; ++g) {
         const float xg = __uint_as_float(xd[g]);
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
@@ -948,11 +682,133 @@ __device__ __forceinline__ void kq_compute_fold(uint32_t base, MmAcc<4>& acc) {
     }
 }
 
-template <uint32_t T, int MODE>
+// Q6_K with its signed 8-bit scales folded into the MFMAs.  Per 16-value
+// group g of a super-block, weighted = sum_g sc_g dot_g with dot_g = sum (q - 32) x
+// (dot_q6_k_q8_k, src/quant.cpp:549-563).  With sc_g + 128 = sum_i 4^i d_i,g
+// (base-4 digits, 0..3), sc_g = d_0 + 4 d_1 + 16 d_2 + 64 (d_3 - 2), and with
+// s = q - 32 in -32..31 every s d_i and s (d_3 - 2) fits int8, so
+//   weighted = A_0 + 4 A_1 + 16 A_2 + 64 A_3,  A_i = sum_k (s_k m_i,g(k)) x_k,
+// four exact int32 MFMA chains over the super-block.  Lane l of step st
+// (64 values) holds group 4 st + l / 16, so its multipliers are its own group's.
+// Bytes are signed: 2 s per byte is a masked shift, 3 s a carry-free byte add,
+// -s and -2 s carry-free byte subtractions from zero.
+__device__ __forceinline__ void kq_s23(unsigned w, unsigned& s2, unsigned& s3) {
+    s2 = (w << 1) & 0xFEFEFEFEu;
+    s3 = ((s2 & 0x7F7F7F7Fu) + (w & 0x7F7F7F7Fu)) ^ ((s2 ^ w) & 0x80808080u);
+}
+__device__ __forceinline__ unsigned kq_neg(unsigned x) { return (0x80808080u - (x & 0x7F7F7F7Fu)) ^ (~x & 0x80808080u); }
+
+struct Kq6F {
+    v4u l, h, b0, b1, b2, b3;  // b0 .. b(G-1) used
+};
+template <int G>
+__device__ __forceinline__ Kq6F kq6_issue(uint32_t base, int st, int ar, int tl, int l16) {
+    Kq6F f;
+    const int half = st >> 1;
+    const int lp = half * 4 + l16, hp = half * 2 + (l16 & 1);
+    f.l = ds128v(base + offsetof(KqStage, w0) + (ar * 8 + (lp ^ (ar & 7))) * 16);
+    f.h = ds128v(base + offsetof(KqStage, wk) + (ar * 4 + (hp ^ (ar & 3))) * 16);
+    const int pb = 4 * st + l16;
+    auto bfrag = [&](int g) -> v4u {
+        const int t = 16 * g + tl;
+        return ds128v(base + offsetof(KqStage, x) + (t * 16 + (pb ^ (t & 15))) * 16);
+    };
+    const v4u z = {0u, 0u, 0u, 0u};
+    f.b0 = bfrag(0);
+    f.b1 = G > 1 ? bfrag(1) : z;
+    f.b2 = G > 2 ? bfrag(2) : z;
+    f.b3 = G > 3 ? bfrag(3) : z;
+    return f;
+}
+__device__ __forceinline__ void kq6_wait(Kq6F& f) {
+    asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(f.l), "+v"(f.h), "+v"(f.b0), "+v"(f.b1), "+v"(f.b2), "+v"(f.b3));
+}
+
+template <int G>
+__device__ __forceinline__ void kq_compute_fold6(uint32_t base, MmAcc<G>& acc) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, tl = lane & 15, l16 = lane >> 4;
+    const int ar = wave * 16 + tl, orow0 = wave * 16 + l16 * 4;
+    const v4i zero = {0, 0, 0, 0};
+    // the A row's 16 int8 scales (four dwords of its meta), the output rows' d, the groups' x scales
+    const uint32_t arow = base + offsetof(KqStage, wm) + ar * 20;
+    uint32_t s0 = ds32(arow), s1 = ds32(arow + 4), s2 = ds32(arow + 8), s3 = ds32(arow + 12);
+    uint32_t dd[4], xd[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        dd[i] = ds32(base + offsetof(KqStage, wm) + (orow0 + i) * 20 + 16);
+        xd[i] = i < G ? ds32(base + offsetof(KqStage, xd) + (16 * i + tl) * 4) : 0u;
+    }
+    asm volatile("s_waitcnt lgkmcnt(0)"
+                 : "+v"(s0), "+v"(s1), "+v"(s2), "+v"(s3), "+v"(dd[0]), "+v"(dd[1]), "+v"(dd[2]), "+v"(dd[3]), "+v"(xd[0]),
+                   "+v"(xd[1]), "+v"(xd[2]), "+v"(xd[3]));
+    const uint32_t scw[4] = {s0, s1, s2, s3};
+    Kq6F cur = kq6_issue<G>(base, 0, ar, tl, l16);
+    kq6_wait(cur);
+    v4i a0[4], a1[4], a2[4], a3[4];
+#pragma unroll
+    for (int g = 0; g < G; ++g) a0[g] = a1[g] = a2[g] = a3[g] = zero;
+#pragma unroll
+    for (int st = 0; st < 4; ++st) {
+        Kq6F nxt;
+        if (st < 3) nxt = kq6_issue<G>(base, st + 1, ar, tl, l16);
+        // the lane's 16 values: nibbles of ql (high for odd steps), 2 bits of qh, minus 32
+        const int quarter = 2 * (st & 1) + (l16 >> 1);
+        const v4u nib = (st & 1) ? ((cur.l >> 4) & 0x0F0F0F0Fu) : (cur.l & 0x0F0F0F0Fu);
+        const v4u u = nib | (((cur.h >> (2 * quarter)) & 0x03030303u) << 4);  // 0..63
+        const v4u tq = u ^ 0x20202020u;                                         // 6-bit two's complement of u - 32
+        const v4u sv = tq | ((tq & 0x20202020u) * 0x06u);
+        const int gi = 4 * st + l16;                                            // this lane's group
+        const uint32_t scu = ((scw[gi >> 2] >> (8 * (gi & 3))) & 0xFF) ^ 0x80u;  // sc + 128 for int8 sc
+        v4u w2, w3;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            unsigned p2, p3;
+            kq_s23(sv[k], p2, p3);
+            w2[k] = p2;
+            w3[k] = p3;
+        }
+        v4u dg[4];
+#pragma unroll
+        for (int i = 0; i < 3; ++i) {
+            const uint32_t d = (scu >> (2 * i)) & 3;
+            dg[i] = (d & 2) ? ((d & 1) ? w3 : w2) : ((d & 1) ? sv : v4u{0u, 0u, 0u, 0u});
+        }
+        {  // the top digit less 2: -2, -1, 0 or 1 times s
+            const uint32_t d = scu >> 6;
+            v4u neg;
+#pragma unroll
+            for (int k = 0; k < 4; ++k) neg[k] = kq_neg((d & 1) ? sv[k] : w2[k]);
+            dg[3] = (d & 2) ? ((d & 1) ? sv : v4u{0u, 0u, 0u, 0u}) : neg;
+        }
+        const v4u bq[4] = {cur.b0, cur.b1, cur.b2, cur.b3};
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+            a0[g] = mfma64(dg[0], bq[g], a0[g]);
+            a1[g] = mfma64(dg[1], bq[g], a1[g]);
+            a2[g] = mfma64(dg[2], bq[g], a2[g]);
+            a3[g] = mfma64(dg[3], bq[g], a3[g]);
+        }
+        if (st < 3) {
+            kq6_wait(nxt);
+            cur = nxt;
+        }
+    }
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+        const float xg = __uint_as_float(xd[g]);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int weighted = a0[g][i] + 4 * a1[g][i] + 16 * a2[g][i] + 64 * a3[g][i];
+            const float d = h2f(static_cast<uint16_t>(dd[i] & 0xFFFF));
+            acc.s[g][i] += xg * d * static_cast<float>(weighted);  // src/quant.cpp:549-563
+        }
+    }
+}
+
+template <uint32_t T, int MODE, int G>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 8))) void k_mmk(MmArgs g) {
     __shared__ KqStage st[2];
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    constexpr int G = kq_groups<T>();
     const uint32_t rt0 = blockIdx.x * 64;
     const int t0 = blockIdx.y * (16 * G);
     const int nc = static_cast<int>(g.m.cols / 256);
@@ -961,14 +817,15 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 8))
     for (int gi = 0; gi < G; ++gi)
 #pragma unroll
         for (int i = 0; i < 4; ++i) a.s[gi][i] = 0.0f;
+    if (MODE == kMmGated) exp_tab_fill();  // ordered before the epilogue by the loop's barriers
     // two stages: chunk c + 1 is copied while chunk c is computed
-    kq_copy<T>(st[0], g.m, g.x, g.ntok, rt0, t0, 0);
+    kq_copy<T, G>(st[0], g.m, g.x, g.ntok, rt0, t0, 0);
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
     for (int c = 0; c < nc; ++c) {
-        if (c + 1 < nc) kq_copy<T>(st[(c + 1) & 1], g.m, g.x, g.ntok, rt0, t0, c + 1);
-        if constexpr (T == kQ4_K) kq_compute_fold(lds_off(&st[c & 1]), a);
-        else kq_compute_asm<T>(lds_off(&st[c & 1]), a);
+        if (c + 1 < nc) kq_copy<T, G>(st[(c + 1) & 1], g.m, g.x, g.ntok, rt0, t0, c + 1);
+        if constexpr (T == kQ4_K) kq_compute_fold<G>(lds_off(&st[c & 1]), a);
+        else kq_compute_fold6<G>(lds_off(&st[c & 1]), a);
         __builtin_amdgcn_s_waitcnt(0);  // chunk c + 1 has landed (this wave's copies) ...
         __syncthreads();                // ... everyone's, and stage c & 1 is consumed
     }
@@ -993,7 +850,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 8))
                     const float q = gv > 0.0f ? gv : 0.0f;
                     *o = q * q * v;  // src/model.cpp:1134-1138
                 } else {
-                    *o = gv / (1.0f + ref_expf(-gv)) * v;  // src/kernels_f32.cpp:287-289
+                    *o = gv / (1.0f + ref_expf_s(-gv)) * v;  // src/kernels_f32.cpp:287-289
                 }
             }
         }
@@ -1235,13 +1092,24 @@ template <int MODE>
 static hipError_t mm_dispatch(const MmArgs& g, hipStream_t s) {
     const int tok = 16 * (g.m.type == kQ4_K || g.m.type == kQ6_K ? mm_groups<kQ4_K>() : mm_groups<kQ4_0>());
     const dim3 grid((g.m.rows + kRowsPerWg - 1) / kRowsPerWg, (g.ntok + tok - 1) / tok);
-    const int kq_tok = 16 * (g.m.type == kQ4_K ? kq_groups<kQ4_K>() : kq_groups<kQ6_K>());
-    const dim3 kq_grid((g.m.rows + 63) / 64, (g.ntok + kq_tok - 1) / kq_tok);
+    // K-quants: the widest token tile (64, 32 or 16 tokens) that still gives a workgroup to every CU
+    const int row_tiles = static_cast<int>((g.m.rows + 63) / 64);
+    int kq_g = 4;
+    while (kq_g > 1 && row_tiles * ((g.ntok + 16 * kq_g - 1) / (16 * kq_g)) < kKqCus) kq_g /= 2;
+    const dim3 kq_grid(row_tiles, (g.ntok + 16 * kq_g - 1) / (16 * kq_g));
     switch (g.m.type) {
         case kQ4_0: hipLaunchKernelGGL((k_mm<kQ4_0, MODE>), grid, dim3(kThreads), 0, s, g); break;
         case kQ8_0: hipLaunchKernelGGL((k_mm<kQ8_0, MODE>), grid, dim3(kThreads), 0, s, g); break;
-        case kQ4_K: hipLaunchKernelGGL((k_mmk<kQ4_K, MODE>), kq_grid, dim3(kThreads), 0, s, g); break;
-        case kQ6_K: hipLaunchKernelGGL((k_mmk<kQ6_K, MODE>), kq_grid, dim3(kThreads), 0, s, g); break;
+        case kQ4_K:
+            if (kq_g == 4) hipLaunchKernelGGL((k_mmk<kQ4_K, MODE, 4>), kq_grid, dim3(kThreads), 0, s, g);
+            else if (kq_g == 2) hipLaunchKernelGGL((k_mmk<kQ4_K, MODE, 2>), kq_grid, dim3(kThreads), 0, s, g);
+            else hipLaunchKernelGGL((k_mmk<kQ4_K, MODE, 1>), kq_grid, dim3(kThreads), 0, s, g);
+            break;
+        case kQ6_K:
+            if (kq_g == 4) hipLaunchKernelGGL((k_mmk<kQ6_K, MODE, 4>), kq_grid, dim3(kThreads), 0, s, g);
+            else if (kq_g == 2) hipLaunchKernelGGL((k_mmk<kQ6_K, MODE, 2>), kq_grid, dim3(kThreads), 0, s, g);
+            else hipLaunchKernelGGL((k_mmk<kQ6_K, MODE, 1>), kq_grid, dim3(kThreads), 0, s, g);
+            break;
         case kTQ2_0: hipLaunchKernelGGL((k_mm<kTQ2_0, MODE>), grid, dim3(kThreads), 0, s, g); break;
         default: return hipErrorInvalidValue;
     }
