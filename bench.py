@@ -334,8 +334,31 @@ def main():
                                           "ops": ops},
                              "decode_after_prefill_tok_s": round(128 / dtd, 2)}
         log(f"prefill 512: {dtp * 1e3:.1f} ms -> {512 / dtp:.1f} tok/s; then 128 decode steps {128 / dtd:.1f} tok/s")
+        ls.rollback(0)
+        base = ls.eval(lp, logits=True)
         ls.close()
         del ls
+        # the same prompt with the opt-in MFMA attention (not order-exact)
+        os.environ["BRISK_HIP_PREFILL_ATTN"] = "mfma"
+        try:
+            ms_ = HipSession((lf, lcfg, ltable), max_context=1024)
+        finally:
+            del os.environ["BRISK_HIP_PREFILL_ATTN"]
+        ms_.eval(lp[:64], logits=False)
+        ms_.rollback(0)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        fast = ms_.eval(lp, logits=True)
+        dtf = time.perf_counter() - t0
+        ms_.close()
+        del ms_
+        result["prefill"]["mfma_attention"] = {
+            "note": "opt-in BRISK_HIP_PREFILL_ATTN=mfma: f16 MFMA attention (hi/lo operands), not order-exact",
+            "value": round(512 / dtf, 2), "unit": "tok/s", "ms": round(dtf * 1e3, 2),
+            "max_abs_logit_diff_vs_exact": float(np.abs(fast - base).max()),
+            "argmax_equal": bool(int(np.argmax(fast)) == int(np.argmax(base)))}
+        log(f"prefill 512 (mfma attention): {dtf * 1e3:.1f} ms -> {512 / dtf:.1f} tok/s, "
+            f"max |diff| vs exact {np.abs(fast - base).max():.3g}")
         torch.cuda.empty_cache()
 
     if not args.no_configs:

@@ -37,7 +37,13 @@ struct PreAttnArgs {
     float* out;      // [T][qstride] attention output
     int qstride, kvstride;
     int pos0;        // position of token 0
+    int mfma;        // 1: prompts of kFaMinTok tokens or more take the MFMA attention (not order-exact)
 };
+
+// Shapes the MFMA prefill attention (opt-in) takes: 64 query rows a workgroup.
+inline bool pre_attn_mfma_fits(int hpk, int head_dim) {
+    return hpk >= 1 && hpk <= 64 && 64 % hpk == 0 && (head_dim == 64 || head_dim == 128);
+}
 
 hipError_t launch_mm(const MmArgs& g, int mode, hipStream_t s);
 hipError_t launch_pre_quant(const float* x, int xstride, const float* w, float eps, int cols, int ntok, bool q8k, int bits,

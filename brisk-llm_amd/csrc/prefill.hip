@@ -20,6 +20,7 @@
 #include "phases.h"
 #include "prefill.h"
 
+
 namespace bh {
 
 typedef int v4i __attribute__((ext_vector_type(4)));
@@ -1086,6 +1087,220 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 8))
     else pa_values<kPaRows * 32 / kThreads>(p, s, rows, hpk, L, tb0, Ls, vbase, rv);
 }
 
+// ---------------------------------------------------------------- long-prompt attention on MFMA
+
+// Opt-in (BRISK_HIP_PREFILL_ATTN=mfma), for prompts of kFaMinTok tokens or
+// more: causal attention with the products on v_mfma_f32_16x16x32_f16, flash
+// style (a running max and sum per query row, so no score row is stored).
+// This is not the reference's summation order, so it is not bit-identical:
+// each f32 operand is carried as two halves, x = hi + lo / 4096 with
+// hi = f16(x) (probabilities scaled by 2^14 first, so small ones stay normal
+// f16: the MFMA reads f16 subnormals as zero), and the lo products go to their
+// own accumulators, so the products keep fp32 rounding.  The attention output
+// then differs from the reference's by fp32 reordering only, but the next
+// projection re-quantises it to int8, and one rounding that tips the other way
+// moves later layers by a quantisation step: on small random-weight models
+// logits can move by ~0.1.  The exact-order kernels above stay the default.
+//
+// A workgroup takes 64 query rows (64 / hpk tokens x the hpk query heads of kv
+// head blockIdx.y), 16 a wave, and walks the visible positions in chunks of 32
+// staged through LDS (keys row-major and XOR-swizzled, values transposed).
+// Per wave and chunk, with g = lane / 16 and lane l % 16 = the wave's row r:
+//   S^T = K Q^T:  A = keys (16 positions x head_dim), B = the query rows, so
+//                 D puts positions 4 g + i (+ 16) of row r in lane l: the row
+//                 is lane-local and its max needs two cross-lane steps.
+//   O^T += V^T P^T: A = values transposed (16 dims x 32 positions), B = P^T,
+//                 whose 8 k-slots per lane are exactly the 8 probabilities
+//                 the lane holds (positions 4 g .. + 3 and 16 + 4 g .. + 3),
+//                 so P never leaves registers; D puts dims 4 g + i of row r
+//                 in lane l.
+constexpr int kFaRows = 64;
+constexpr int kFaPos = 32;
+constexpr int kFaMinTok = 64;
+constexpr int kFaVtRow = kFaPos + 8;  // halves a transposed value row (80 bytes: conflict-free 16-row reads)
+constexpr float kFaPUp = 16384.0f;    // probabilities are scaled by this (<= 2^14) before the f16 split
+
+typedef _Float16 v8h __attribute__((ext_vector_type(8)));
+typedef float v4f __attribute__((ext_vector_type(4)));
+
+template <int HD>
+struct FaLds {
+    alignas(16) uint16_t k[2][kFaPos * HD];
+    alignas(16) uint16_t vt[2][HD * kFaVtRow];
+};
+
+// 16-byte piece p of key row `pos` in the staged chunk: XOR-swizzled so the 16
+// rows one A fragment reads fall in distinct banks
+template <int HD>
+__device__ __forceinline__ int fa_kslot(int pos, int p) {
+    constexpr int P = HD / 8, SH = HD >= 128 ? 0 : (HD == 64 ? 1 : 2);
+    return pos * P + (p ^ ((pos >> SH) & (P - 1)));
+}
+
+template <int HD>
+struct FaChunk {
+    static constexpr int N = kFaPos * HD / 8 / kThreads;  // 16-byte pieces a thread, keys and values each
+    uint4 k[N], v[N];
+};
+
+template <int HD>
+__device__ __forceinline__ void fa_load(FaChunk<HD>& r, const uint16_t* kb, const uint16_t* vb, int p0, int L) {
+    constexpr int P = HD / 8;
+#pragma unroll
+    for (int u = 0; u < FaChunk<HD>::N; ++u) {
+        const int j = u * kThreads + static_cast<int>(threadIdx.x), p = j % P;
+        // past the context: a copy of its last row (finite, and weighted by 0)
+        const int pos = p0 + j / P < L ? p0 + j / P : L - 1;
+        r.k[u] = *reinterpret_cast<const uint4*>(kb + static_cast<size_t>(pos) * HD + p * 8);
+        r.v[u] = *reinterpret_cast<const uint4*>(vb + static_cast<size_t>(pos) * HD + p * 8);
+    }
+}
+
+template <int HD>
+__device__ __forceinline__ void fa_store(const FaChunk<HD>& r, FaLds<HD>& s, int buf) {
+    constexpr int P = HD / 8;
+#pragma unroll
+    for (int u = 0; u < FaChunk<HD>::N; ++u) {
+        const int j = u * kThreads + static_cast<int>(threadIdx.x), pos = j / P, p = j % P;
+        reinterpret_cast<uint4*>(s.k[buf])[fa_kslot<HD>(pos, p)] = r.k[u];
+        const uint32_t w[4] = {r.v[u].x, r.v[u].y, r.v[u].z, r.v[u].w};
+        uint16_t* col = s.vt[buf] + (p * 8) * kFaVtRow + pos;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            col[(2 * e) * kFaVtRow] = static_cast<uint16_t>(w[e] & 0xFFFF);
+            col[(2 * e + 1) * kFaVtRow] = static_cast<uint16_t>(w[e] >> 16);
+        }
+    }
+}
+
+// x = hi + lo / 4096: the low half is scaled up so it stays a normal
+// f16 (the MFMA treats f16 subnormal inputs as zero) for all but tiny x
+constexpr float kFaLoUp = 4096.0f, kFaLoDown = 1.0f / 4096.0f;
+__device__ __forceinline__ void fa_split(const float* x, v8h& hi, v8h& lo) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        const _Float16 h = static_cast<_Float16>(x[j]);
+        hi[j] = h;
+        lo[j] = static_cast<_Float16>((x[j] - static_cast<float>(h)) * kFaLoUp);
+    }
+}
+
+__device__ __forceinline__ v4f fa_mfma(const v8h& a, const v8h& b, v4f c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+}
+
+template <int HD>
+__global__ __launch_bounds__(kThreads) void k_pre_attn_fa(PreAttnArgs p, int ntok) {
+    __shared__ FaLds<HD> s;
+    constexpr int KS = HD / 32, DT = HD / 16;
+    const AttnArgs& g = p.a;
+    const int hpk = g.heads / g.kv_heads, kv = blockIdx.y, tpb = kFaRows / hpk, tb0 = blockIdx.x * tpb;
+    const int ntb = ntok - tb0 < tpb ? ntok - tb0 : tpb;
+    const int L = p.pos0 + tb0 + ntb;  // positions the block's last token sees
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, r = lane & 15, gq4 = lane >> 4;
+    const int row = wave * 16 + r;
+    const int tt = row / hpk < ntb ? row / hpk : ntb - 1;  // past the prompt: a copy of its last token, not stored
+    const int head = kv * hpk + row % hpk;
+    const int lim = p.pos0 + tb0 + tt;  // the row sees positions 0 .. lim
+    const int wlast = p.pos0 + tb0 + ((wave * 16 + 15) / hpk < ntb ? (wave * 16 + 15) / hpk : ntb - 1);
+    const int wchunks = wlast / kFaPos + 1, nchunks = (L + kFaPos - 1) / kFaPos;
+
+    const uint16_t* kb = g.kcache + static_cast<size_t>(kv) * g.ctx * HD;
+    const uint16_t* vb = g.vcache + static_cast<size_t>(kv) * g.ctx * HD;
+    FaChunk<HD> ch;
+    fa_load<HD>(ch, kb, vb, 0, L);
+
+    // this lane's query row, d = 32 ks + 8 g .. + 7, as hi / lo halves
+    v8h qh[KS], ql[KS];
+    {
+        const float* q = p.q + static_cast<size_t>(tb0 + tt) * p.qstride + head * HD;
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) {
+            const float4 a = *reinterpret_cast<const float4*>(q + 32 * ks + 8 * gq4);
+            const float4 b = *reinterpret_cast<const float4*>(q + 32 * ks + 8 * gq4 + 4);
+            const float x[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+            fa_split(x, qh[ks], ql[ks]);
+        }
+    }
+    v4f o[DT];
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) o[dt] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+    float m = -INFINITY, lsum = 0.0f;
+    const float scale = g.scale;
+
+    for (int c = 0; c < nchunks; ++c) {
+        const int buf = c & 1;
+        fa_store<HD>(ch, s, buf);  // buffer c & 1 last held chunk c - 2, read before the barrier of chunk c - 1
+        if (c + 1 < nchunks) fa_load<HD>(ch, kb, vb, (c + 1) * kFaPos, L);
+        __syncthreads();
+        if (c >= wchunks) continue;  // every row of this wave is past this chunk
+        const int p0 = c * kFaPos;
+        // scores S^T: tile t covers positions p0 + 16 t .. + 15
+        v4f sc[2];
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+            v4f acc = {0.0f, 0.0f, 0.0f, 0.0f}, accl = acc;
+#pragma unroll
+            for (int ks = 0; ks < KS; ++ks) {
+                const v8h kf = *reinterpret_cast<const v8h*>(
+                    reinterpret_cast<const uint4*>(s.k[buf]) + fa_kslot<HD>(16 * t + r, 4 * ks + gq4));
+                acc = fa_mfma(kf, qh[ks], acc);
+                accl = fa_mfma(kf, ql[ks], accl);
+            }
+#pragma unroll
+            for (int i = 0; i < 4; ++i) sc[t][i] = acc[i] + accl[i] * kFaLoDown;
+        }
+        // online softmax over the row's 8 positions in this lane and the row's other 3 lanes
+        float sv[8];
+        float cmax = -INFINITY;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const int pos = p0 + 16 * (j >> 2) + 4 * gq4 + (j & 3);
+            sv[j] = pos <= lim ? sc[j >> 2][j & 3] * scale : -INFINITY;
+            cmax = fmaxf(cmax, sv[j]);
+        }
+        cmax = fmaxf(cmax, __shfl_xor(cmax, 16));
+        cmax = fmaxf(cmax, __shfl_xor(cmax, 32));
+        const float mn = fmaxf(m, cmax);  // finite: chunk 0 holds position 0, which every row sees
+        const float alpha = __expf(m - mn);
+        m = mn;
+        // probabilities scaled by 2^14 (<= 16384) so that small ones stay normal f16; the sum too
+        float pv[8], psum = 0.0f;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            pv[j] = __expf(sv[j] - mn) * kFaPUp;
+            psum += pv[j];
+        }
+        lsum = lsum * alpha + psum;
+        v8h ph, pl;
+        fa_split(pv, ph, pl);
+        // O^T += V^T P^T: A = values of dims 16 dt + r at positions 4 g .. + 3 and 16 + 4 g .. + 3
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt) {
+            const uint16_t* vr = s.vt[buf] + (16 * dt + r) * kFaVtRow + 4 * gq4;
+            const uint2 a0 = *reinterpret_cast<const uint2*>(vr);
+            const uint2 a1 = *reinterpret_cast<const uint2*>(vr + 16);
+            const v8h vf = __builtin_bit_cast(v8h, make_uint4(a0.x, a0.y, a1.x, a1.y));
+            v4f acc = o[dt] * alpha, accl = {0.0f, 0.0f, 0.0f, 0.0f};
+            acc = fa_mfma(vf, ph, acc);
+            accl = fa_mfma(vf, pl, accl);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) o[dt][i] = acc[i] + accl[i] * kFaLoDown;
+        }
+    }
+    lsum += __shfl_xor(lsum, 16);
+    lsum += __shfl_xor(lsum, 32);
+    if (row / hpk < ntb) {
+        const float inv = 1.0f / lsum;
+        float* out = p.out + static_cast<size_t>(tb0 + tt) * p.qstride + head * HD + 4 * gq4;
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt) {
+            const v4f v = o[dt] * inv;
+            *reinterpret_cast<float4*>(out + 16 * dt) = make_float4(v[0], v[1], v[2], v[3]);
+        }
+    }
+}
+
 // ---------------------------------------------------------------- launchers
 
 template <int MODE>
@@ -1159,13 +1374,21 @@ hipError_t launch_pre_attention(const PreAttnArgs& p, int ntok, hipStream_t s) {
     hipLaunchKernelGGL(k_pre_rope, grid, dim3(kThreads), 0, s, p);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    const int hpk = p.a.heads / p.a.kv_heads;
-    if (hpk <= kPaRows && (p.a.head_dim == 32 || p.a.head_dim == 64 || p.a.head_dim == 128) &&
+    const int hpk = p.a.heads / p.a.kv_heads, hd = p.a.head_dim;
+    const int L = p.pos0 + ntok;
+    const bool fa_ok = pre_attn_mfma_fits(hpk, hd);
+    if (p.mfma && fa_ok && (ntok >= kFaMinTok || L * hpk > kExactScores)) {
+        const dim3 fgrid((ntok + kFaRows / hpk - 1) / (kFaRows / hpk), p.a.kv_heads);
+        if (hd == 64) hipLaunchKernelGGL(k_pre_attn_fa<64>, fgrid, dim3(kThreads), 0, s, p, ntok);
+        else hipLaunchKernelGGL(k_pre_attn_fa<128>, fgrid, dim3(kThreads), 0, s, p, ntok);
+    } else if (hpk <= kPaRows && (p.a.head_dim == 32 || p.a.head_dim == 64 || p.a.head_dim == 128) &&
         p.pos0 + ntok <= kPaMaxL) {
         const int tpb = kPaRows / hpk;
         hipLaunchKernelGGL(k_pre_attn_blk, dim3((ntok + tpb - 1) / tpb, p.a.kv_heads), dim3(kThreads), 0, s, p, ntok);
-    } else {
+    } else if (L * hpk <= kExactScores) {
         hipLaunchKernelGGL(k_pre_attn, grid, dim3(kThreads), 0, s, p);
+    } else {
+        return hipErrorInvalidValue;  // no prefill attention for this shape (the session decodes it token by token)
     }
     return hipGetLastError();
 }

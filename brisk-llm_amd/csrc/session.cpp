@@ -192,6 +192,8 @@ Session::Session(const brisk_hip_config& cfg, const brisk_hip_tensor* tensors, s
     {
         const char* pf = std::getenv("BRISK_HIP_PREFILL");
         prefill_on_ = !(pf != nullptr && std::string(pf) == "0") && !debug_;
+        const char* pa = std::getenv("BRISK_HIP_PREFILL_ATTN");  // "mfma": long prompts' attention on f16 MFMA
+        prefill_mfma_ = pa != nullptr && std::string(pa) == "mfma";
     }
     setup_loop();
     use_graphs_ = std::getenv("BRISK_HIP_NO_GRAPH") == nullptr && !debug_;
@@ -524,7 +526,10 @@ void Session::stage(const int32_t* tokens, size_t n, size_t device_pos) {
 // Prompts of two or more tokens whose attention stays on the exact path go
 // through the batched prefill (BRISK_HIP_PREFILL=0 turns it off).
 bool Session::use_prefill(size_t n) const {
-    return prefill_on_ && n >= 2 && attn_is_exact(static_cast<int>(position_ + n), static_cast<int>(cfg_.heads / cfg_.kv_heads));
+    // the exact-order prefill attention keeps every score of a token's query heads in LDS
+    const bool exact_fits = (position_ + n) * (cfg_.heads / cfg_.kv_heads) <= static_cast<size_t>(kExactScores);
+    const bool mfma_fits = prefill_mfma_ && pre_attn_mfma_fits(static_cast<int>(cfg_.heads / cfg_.kv_heads), static_cast<int>(cfg_.head_dim));
+    return prefill_on_ && n >= 2 && (exact_fits || mfma_fits);
 }
 
 void Session::ensure_prefill() {
@@ -580,6 +585,7 @@ void Session::prefill_layers(size_t pos0, int T) {
         pa.a.scale = 1.0f / std::sqrt(static_cast<float>(cfg_.head_dim));  // src/model.cpp:978
         pa.q = pre_q_; pa.k = pre_k_; pa.v = pre_v_; pa.out = pre_att_;
         pa.qstride = qd; pa.kvstride = kvd; pa.pos0 = static_cast<int>(pos0);
+        pa.mfma = prefill_mfma_ ? 1 : 0;
         check(launch_pre_attention(pa, T, stream_), "prefill attention");
         // h += O (sub-normed) att (:1095-1111)
         prefill_quant(pre_att_, qd, L.attn_sub_norm, qd, T, L.o);
