@@ -169,10 +169,10 @@ int brisk_hip_expf(const float* x, float* y, size_t n, void* stream) {
 int brisk_hip_div_selftest(unsigned long long* mismatches) {
     return guarded([&] {
         unsigned long long* d = nullptr;
-        hip_check(hipMalloc(&d, 24), "hipMalloc");
-        hipError_t e = hipMemset(d, 0, 24);
+        hip_check(hipMalloc(&d, 32), "hipMalloc");
+        hipError_t e = hipMemset(d, 0, 32);
         if (e == hipSuccess) e = bh::launch_div_selftest(d, nullptr);
-        if (e == hipSuccess) e = hipMemcpy(mismatches, d, 24, hipMemcpyDeviceToHost);
+        if (e == hipSuccess) e = hipMemcpy(mismatches, d, 32, hipMemcpyDeviceToHost);
         hipFree(d);
         hip_check(e, "div selftest");
     });

@@ -27,6 +27,19 @@ constexpr int kTermCap = 8448;       // floats of LDS for the per-block terms of
 // IEEE half -> float; exact (src/quant.cpp:61-85 is the same conversion).
 __device__ __forceinline__ float h2f(uint16_t h) { return static_cast<float>(__builtin_bit_cast(_Float16, h)); }
 
+// RN(q * h), h being the low (Hi = false) or high half of `w` as an f16, in one
+// v_fma_mix_f32 (the half is widened inside the instruction): fma(q, h, -0) is
+// the rounded product for every input, the sign of a zero product included,
+// so it equals q * h2f(h) bit for bit (checked exhaustively over q by
+// brisk_hip_div_selftest).  Saves the separate conversion.
+template <bool Hi>
+__device__ __forceinline__ float mul_h(float q, uint32_t w) {
+    float r;
+    if (Hi) asm("v_fma_mix_f32 %0, %1, %2, %3 op_sel:[0,1,0] op_sel_hi:[0,1,0]" : "=v"(r) : "v"(q), "v"(w), "v"(-0.0f));
+    else asm("v_fma_mix_f32 %0, %1, %2, %3 op_sel_hi:[0,1,0]" : "=v"(r) : "v"(q), "v"(w), "v"(-0.0f));
+    return r;
+}
+
 // float -> IEEE half, round to nearest even, with the reference's handling of
 // overflow (infinity), underflow (signed zero) and NaN (quiet, payload
 // dropped): src/quant.cpp:87-113, written out on the bits.  f2h below is the

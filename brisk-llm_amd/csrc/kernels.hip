@@ -299,7 +299,8 @@ __global__ void k_expf(const float* __restrict__ x, float* __restrict__ y, size_
 // The short exact divisions of device.h against IEEE division, over every
 // input: bad[0] counts div127 mismatches (finite a >= 0), bad[1] rcp_rn
 // mismatches (finite d != 0), bad[2] hardware f2h against the bit-level
-// conversion (every float).
+// conversion (every float), bad[3] mul_h against the product of the widened
+// half (every float).
 __global__ void k_div_selftest(unsigned long long* bad) {
     const unsigned long long stride = static_cast<unsigned long long>(gridDim.x) * blockDim.x;
     unsigned long long n127 = 0, nrcp = 0;
@@ -318,6 +319,20 @@ __global__ void k_div_selftest(unsigned long long* bad) {
         if (f2h(x) != f2h_bits(x)) ++nh;
     }
     if (nh != 0) atomicAdd(bad + 2, nh);
+    // mul_h against the widened product: every float q, with a half drawn from
+    // q's bits (every half is met about 65536 times), low and high
+    unsigned long long nm = 0;
+    for (unsigned long long j = static_cast<unsigned long long>(blockIdx.x) * blockDim.x + threadIdx.x; j < (1ull << 32); j += stride) {
+        const uint32_t i = static_cast<uint32_t>(j);
+        const float q = __uint_as_float(i);
+        const uint32_t w = (i * 2654435761u) ^ (i >> 7);
+        const float lo = q * h2f(static_cast<uint16_t>(w & 0xFFFF)), hi = q * h2f(static_cast<uint16_t>(w >> 16));
+        const float mlo = mul_h<false>(q, w), mhi = mul_h<true>(q, w);
+        const bool nan = lo != lo;  // NaN payloads may differ; NaN must stay NaN
+        if (nan ? mlo == mlo : __float_as_uint(mlo) != __float_as_uint(lo)) ++nm;
+        if ((hi != hi) ? mhi == mhi : __float_as_uint(mhi) != __float_as_uint(hi)) ++nm;
+    }
+    if (nm != 0) atomicAdd(bad + 3, nm);
 }
 
 hipError_t launch_div_selftest(unsigned long long* bad, hipStream_t s) {

@@ -951,6 +951,32 @@ __device__ __forceinline__ void pa_chunk_store(const PaChunk& r, uint16_t* lds, 
     if (3 * kThreads + t < pieces) dst[3 * kThreads + t] = r.v3;
 }
 
+// score_lane's arithmetic (dot_f32, src/kernels_f32.cpp:229-246: 16 lane
+// partials, then their sum in order, times nothing yet) with each product q k
+// one mul_h, so the key halves need no separate conversion.
+template <int PER>
+__device__ __forceinline__ float pa_score(const float* q, const uint16_t* chunk, int p, int P, int mask) {
+    float lane[16];
+#pragma unroll
+    for (int j = 0; j < 16; ++j) lane[j] = 0.0f;
+    const uint4* rows = reinterpret_cast<const uint4*>(chunk);
+#pragma unroll
+    for (int m = 0; m < PER; ++m) {
+        const uint4 k0 = rows[p * P + ((2 * m) ^ (p & mask))];
+        const uint4 k1 = rows[p * P + ((2 * m + 1) ^ (p & mask))];
+        const float4* q4 = reinterpret_cast<const float4*>(q + 16 * m);
+        const float4 qa = q4[0], qb = q4[1], qc = q4[2], qd = q4[3];
+        const uint32_t kw[8] = {k0.x, k0.y, k0.z, k0.w, k1.x, k1.y, k1.z, k1.w};
+        const float qv[16] = {qa.x, qa.y, qa.z, qa.w, qb.x, qb.y, qb.z, qb.w, qc.x, qc.y, qc.z, qc.w, qd.x, qd.y, qd.z, qd.w};
+#pragma unroll
+        for (int j = 0; j < 16; ++j) lane[j] += (j & 1) ? mul_h<true>(qv[j], kw[j >> 1]) : mul_h<false>(qv[j], kw[j >> 1]);
+    }
+    float sum = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 16; ++j) sum += lane[j];
+    return sum;
+}
+
 template <int PER>
 __device__ __forceinline__ void pa_scores(const PreAttnArgs& p, PaLds& s, int rows, int tpb, int hpk, int L, int tb0, int Ls,
                                           const uint16_t* kbase) {
@@ -971,7 +997,7 @@ __device__ __forceinline__ void pa_scores(const PreAttnArgs& p, PaLds& s, int ro
         for (int i = threadIdx.x; i < rows * kSplit; i += kThreads) {
             const int row = i / kSplit, pp = i - row * kSplit, pos = p0 + pp;
             const int tpos = p.pos0 + tb0 + row / hpk;  // the row's token position: it sees 0 .. tpos
-            if (pos <= tpos && pos < L) s.sc[row * Ls + pos] = score_lane<PER>(s.q + row * hd, buf, pp, P, mask) * p.a.scale;
+            if (pos <= tpos && pos < L) s.sc[row * Ls + pos] = pa_score<PER>(s.q + row * hd, buf, pp, P, mask) * p.a.scale;
         }
     }
     __syncthreads();
@@ -1015,21 +1041,21 @@ __device__ __forceinline__ void pa_values(const PreAttnArgs& p, PaLds& s, int ro
         const int nany = lmax - q0 < 0 ? 0 : (lmax - q0 < kSplit ? lmax - q0 : kSplit);
         int q = 0;
         for (; q + 4 <= nall; q += 4) {
-            const float v0 = h2f(vcol[(q + 0) * hd]), v1 = h2f(vcol[(q + 1) * hd]);
-            const float v2 = h2f(vcol[(q + 2) * hd]), v3 = h2f(vcol[(q + 3) * hd]);
+            const uint32_t v0 = vcol[(q + 0) * hd], v1 = vcol[(q + 1) * hd];  // halves, widened by mul_h
+            const uint32_t v2 = vcol[(q + 2) * hd], v3 = vcol[(q + 3) * hd];
 #pragma unroll
             for (int k = 0; k < NCH; ++k) {
                 const float4 w4 = *reinterpret_cast<const float4*>(wrow[k] + q0 + q);
                 float a = acc[k];
-                a += w4.x * v0; a += w4.y * v1; a += w4.z * v2; a += w4.w * v3;
+                a += mul_h<false>(w4.x, v0); a += mul_h<false>(w4.y, v1); a += mul_h<false>(w4.z, v2); a += mul_h<false>(w4.w, v3);
                 acc[k] = a;
             }
         }
         for (; q < nany; ++q) {
-            const float v = h2f(vcol[q * hd]);
+            const uint32_t v = vcol[q * hd];
 #pragma unroll
             for (int k = 0; k < NCH; ++k)
-                if (q0 + q < lr[k]) acc[k] += wrow[k][q0 + q] * v;
+                if (q0 + q < lr[k]) acc[k] += mul_h<false>(wrow[k][q0 + q], v);
         }
     }
 #pragma unroll

@@ -119,7 +119,9 @@ int brisk_hip_expf(const float* x, float* y, size_t n, void* stream);
  * divisions of the activation quantisation (a / 127 for a >= 0, and 1 / d),
  * each compared with IEEE division on every finite input it can take, and the
  * hardware float-to-half conversion, compared with the reference's bit-level
- * conversion (src/quant.cpp:87-113) on every float.  mismatches[0..2] receive
+ * conversion (src/quant.cpp:87-113) on every float, and the mixed-precision
+ * multiply of a float by a half (the attention's q k and w v products) against
+ * the product of the widened half, on every float.  mismatches[0..3] receive
  * the counts (all 0 when the shortcuts are exact).  Test support; no
  * counterpart in the reference. */
 int brisk_hip_div_selftest(unsigned long long* mismatches);

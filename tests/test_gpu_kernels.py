@@ -187,8 +187,9 @@ def test_expf_matches_host_libm(lib, orc):
 
 def test_short_divisions_are_exact(lib):
     """div127 (a / 127, a >= 0) and rcp_rn (1 / d) equal IEEE division on every finite input, and the
-    hardware float-to-half conversion equals the reference's bit-level one on every float."""
+    hardware float-to-half conversion equals the reference's bit-level one on every float, and the
+    one-instruction float x half product equals the product of the widened half on every float."""
     import ctypes
-    bad = (ctypes.c_ulonglong * 3)()
+    bad = (ctypes.c_ulonglong * 4)()
     L.check(lib.brisk_hip_div_selftest(bad))
-    assert bad[0] == 0 and bad[1] == 0 and bad[2] == 0, f"div127: {bad[0]} mismatches, rcp_rn: {bad[1]}, f2h: {bad[2]}"
+    assert list(bad) == [0, 0, 0, 0], f"div127: {bad[0]} mismatches, rcp_rn: {bad[1]}, f2h: {bad[2]}, mul_h: {bad[3]}"
