@@ -37,6 +37,7 @@ struct PreAttnArgs {
     float* out;      // [T][qstride] attention output
     int qstride, kvstride;
     int pos0;        // position of token 0
+    int legacy;      // 1: the staged-chunk exact kernel (k_pre_attn_blk) in place of k_pre_attn_rows
     int mfma;        // 1: prompts of kFaMinTok tokens or more take the MFMA attention (not order-exact)
 };
 

@@ -1113,6 +1113,193 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 8))
     else pa_values<kPaRows * 32 / kThreads>(p, s, rows, hpk, L, tb0, Ls, vbase, rv);
 }
 
+// ---------------------------------------------------------------- exact attention, lane per position
+
+// The reference's attention for a block of tokens (the same arithmetic as
+// attn_exact), arranged so that no key or value is staged: a workgroup takes R
+// query rows (R / hpk tokens x the hpk query heads of kv head blockIdx.y).
+// Scores: a lane per position holds that position's key row in registers
+// (loaded from the cache directly) and takes every row's dot_f32 against it,
+// the query read as a broadcast; so a key is read once for all R rows and the
+// only per-score work is the 16-lane dot itself.  Softmax: a row a wave.
+// Values: a lane per (pair of dimensions, rows g, g + RG, ...), each value
+// pair read straight from the cache once for all of the lane's rows; every
+// chain adds its terms in position order, as weighted_sum_f32 does.
+constexpr int kPxRows = 16;
+
+// Causal attention blocks grow with their token index, and workgroups w,
+// w + kKqCus, ... share a compute unit when the grid is resident at once.  So
+// block ids are dealt heaviest first in a snake (round r of kKqCus ids takes
+// the next kKqCus blocks, reversed on odd rounds): each unit's blocks then sum
+// to about the same work.  Block k of the heavy-first order is token block
+// nx - 1 - k / ny of kv head k % ny.
+__device__ __forceinline__ void snake_block(int id, int nx, int ny, int& y, int& x) {
+    const int r = id / kKqCus, c = id - r * kKqCus;
+    const int k = r * kKqCus + ((r & 1) ? kKqCus - 1 - c : c);
+    const int n = nx * ny;
+    const int kk = k < n ? k : id;  // a partial last round: ids past n keep their own order
+    x = nx - 1 - kk / ny;
+    y = kk - (kk / ny) * ny;
+}
+template <int HD, int R, int LMAX>
+struct PxLds {
+    alignas(16) float q[R * HD];
+    alignas(16) float sc[R * (LMAX + 4)];
+};
+
+template <int HD, int R, int LMAX>
+__global__ __launch_bounds__(kThreads) void k_pre_attn_rows(PreAttnArgs p, int ntok) {
+    __shared__ PxLds<HD, R, LMAX> s;
+    constexpr int PER = HD / 16, NW = HD / 8;  // dot terms a lane partial; 16-byte pieces a key row
+    const AttnArgs& g = p.a;
+    const int hpk = g.heads / g.kv_heads, tpb = R / hpk;
+    int kv, xb;
+    snake_block(static_cast<int>(blockIdx.x), (ntok + tpb - 1) / tpb, g.kv_heads, kv, xb);
+    const int tb0 = xb * tpb;
+    const int ntb = ntok - tb0 < tpb ? ntok - tb0 : tpb, rows = ntb * hpk;
+    const int first = p.pos0 + tb0;  // the block's first token's position
+    const int L = first + ntb;       // positions the block's last token sees
+    const int Ls = (L + 3) & ~3;
+    const int t = threadIdx.x, wave = t >> 6, wl = t & 63;
+    exp_tab_fill();  // ordered before the softmax by the barriers between
+    for (int i = t; i < rows * HD; i += kThreads) {  // q rows: row = token * hpk + head
+        const int row = i / HD, d = i - row * HD, tt = row / hpk, gq = row - tt * hpk;
+        s.q[i] = p.q[static_cast<size_t>(tb0 + tt) * p.qstride + (kv * hpk + gq) * HD + d];
+    }
+    const uint16_t* kbase = g.kcache + static_cast<size_t>(kv) * g.ctx * HD;
+    const uint16_t* vbase = g.vcache + static_cast<size_t>(kv) * g.ctx * HD;
+    __syncthreads();
+    // ---- scores: score_p = dot_f32(q, k_p) * scale, a lane per position
+    for (int p0 = 0; p0 < L; p0 += kThreads) {
+        const int pos = p0 + t;
+        if (pos < L) {
+            uint32_t kw[HD / 2];
+            const uint4* krow = reinterpret_cast<const uint4*>(kbase + static_cast<size_t>(pos) * HD);
+#pragma unroll
+            for (int w = 0; w < NW; ++w) {
+                const uint4 v = krow[w];
+                kw[4 * w] = v.x; kw[4 * w + 1] = v.y; kw[4 * w + 2] = v.z; kw[4 * w + 3] = v.w;
+            }
+            // rows in token order: token tt sees positions 0 .. first + tt
+            for (int tt = (pos > first ? pos - first : 0); tt < ntb; ++tt) {
+                for (int gq = 0; gq < hpk; ++gq) {
+                    const int row = tt * hpk + gq;
+                    const float* q = s.q + row * HD;
+                    float lane[16];
+#pragma unroll
+                    for (int j = 0; j < 16; ++j) lane[j] = 0.0f;
+#pragma unroll
+                    for (int m = 0; m < PER; ++m) {
+                        const float4* q4 = reinterpret_cast<const float4*>(q + 16 * m);
+                        const float4 qa = q4[0], qb = q4[1], qc = q4[2], qd = q4[3];
+                        const float qv[16] = {qa.x, qa.y, qa.z, qa.w, qb.x, qb.y, qb.z, qb.w,
+                                              qc.x, qc.y, qc.z, qc.w, qd.x, qd.y, qd.z, qd.w};
+#pragma unroll
+                        for (int j = 0; j < 16; ++j)
+                            lane[j] += (j & 1) ? mul_h<true>(qv[j], kw[8 * m + (j >> 1)]) : mul_h<false>(qv[j], kw[8 * m + (j >> 1)]);
+                    }
+                    float sum = 0.0f;
+#pragma unroll
+                    for (int j = 0; j < 16; ++j) sum += lane[j];
+                    s.sc[row * Ls + pos] = sum * g.scale;
+                }
+            }
+        }
+    }
+    __syncthreads();
+    // ---- softmax, a row a wave: max, e = expf(s - max), double sum, w = e * (float)(1 / sum)
+    for (int row = wave; row < rows; row += kThreads / 64) {
+        const int Lr = first + row / hpk + 1;
+        float* sc = s.sc + row * Ls;
+        float m = -INFINITY;
+        for (int q = wl; q < Lr; q += 64) m = fmaxf(m, sc[q]);
+        m = wave_max(m);
+        double part = 0.0;
+        for (int q = wl; q < Lr; q += 64) {
+            const float e = ref_expf_s(sc[q] - m);
+            sc[q] = e;
+            part += static_cast<double>(e);
+        }
+        const float scale = static_cast<float>(1.0 / wave_sum(part));
+        for (int q = wl; q < Lr; q += 64) sc[q] *= scale;
+    }
+    __syncthreads();
+    // ---- value sums in position order: lane = (dimension pair dp, rows rg, rg + RG, ...)
+    constexpr int DP = HD / 2, RG = kThreads / DP, NR = R / RG;
+    const int dp = t % DP, rg = t / DP;
+    float acc0[NR], acc1[NR];
+    int lr[NR];
+    const float* wrow[NR];
+    int lmin = L, lmax = 0;
+#pragma unroll
+    for (int k = 0; k < NR; ++k) {
+        acc0[k] = acc1[k] = 0.0f;
+        const int row = rg + k * RG < rows ? rg + k * RG : rows - 1;  // past the block: a copy, not stored
+        lr[k] = first + row / hpk + 1;
+        wrow[k] = s.sc + row * Ls;
+        lmin = lr[k] < lmin ? lr[k] : lmin;
+        lmax = lr[k] > lmax ? lr[k] : lmax;
+    }
+    const uint32_t* vcol = reinterpret_cast<const uint32_t*>(vbase) + dp;  // value pair (2 dp, 2 dp + 1) of row 0
+    // positions every chain takes, in batches of B: the next batch's loads are
+    // issued before the current batch's adds (two register sets, ping-pong),
+    // so a batch waits for no load but the one issued a batch earlier
+    constexpr int B = 16;
+    const int nb = lmin / B;
+    uint32_t va[B], vb[B];
+    auto load = [&](uint32_t* v, int q0) {
+#pragma unroll
+        for (int u = 0; u < B; ++u) v[u] = vcol[static_cast<size_t>(q0 + u) * DP];
+    };
+    auto adds = [&](const uint32_t* v, int q0) {
+#pragma unroll
+        for (int k = 0; k < NR; ++k) {
+            float a0 = acc0[k], a1 = acc1[k];
+#pragma unroll
+            for (int u4 = 0; u4 < B; u4 += 4) {
+                const float4 w4 = *reinterpret_cast<const float4*>(wrow[k] + q0 + u4);
+                const float w[4] = {w4.x, w4.y, w4.z, w4.w};
+#pragma unroll
+                for (int u = 0; u < 4; ++u) {
+                    a0 += mul_h<false>(w[u], v[u4 + u]);
+                    a1 += mul_h<true>(w[u], v[u4 + u]);
+                }
+            }
+            acc0[k] = a0;
+            acc1[k] = a1;
+        }
+    };
+    if (nb > 0) load(va, 0);
+    int b = 0;
+    for (; b + 2 <= nb; b += 2) {
+        load(vb, (b + 1) * B);
+        adds(va, b * B);
+        if (b + 2 < nb) load(va, (b + 2) * B);
+        adds(vb, (b + 1) * B);
+    }
+    if (b < nb) adds(va, b * B);
+    int q = nb * B;
+    for (; q < lmax; ++q) {
+        const uint32_t v = vcol[static_cast<size_t>(q) * DP];
+#pragma unroll
+        for (int k = 0; k < NR; ++k)
+            if (q < lr[k]) {
+                const float w = wrow[k][q];
+                acc0[k] += mul_h<false>(w, v);
+                acc1[k] += mul_h<true>(w, v);
+            }
+    }
+#pragma unroll
+    for (int k = 0; k < NR; ++k) {
+        const int row = rg + k * RG;
+        if (row < rows) {
+            const int tt = row / hpk, gq = row - tt * hpk;
+            float* o = p.out + static_cast<size_t>(tb0 + tt) * p.qstride + (kv * hpk + gq) * HD + 2 * dp;
+            *reinterpret_cast<float2*>(o) = make_float2(acc0[k], acc1[k]);
+        }
+    }
+}
+
 // ---------------------------------------------------------------- long-prompt attention on MFMA
 
 // Opt-in (BRISK_HIP_PREFILL_ATTN=mfma), for prompts of kFaMinTok tokens or
@@ -1220,7 +1407,10 @@ __global__ __launch_bounds__(kThreads) void k_pre_attn_fa(PreAttnArgs p, int nto
     __shared__ FaLds<HD> s;
     constexpr int KS = HD / 32, DT = HD / 16;
     const AttnArgs& g = p.a;
-    const int hpk = g.heads / g.kv_heads, kv = blockIdx.y, tpb = kFaRows / hpk, tb0 = blockIdx.x * tpb;
+    const int hpk = g.heads / g.kv_heads, tpb = kFaRows / hpk;
+    int kv, xb;
+    snake_block(static_cast<int>(blockIdx.x), (ntok + tpb - 1) / tpb, g.kv_heads, kv, xb);
+    const int tb0 = xb * tpb;
     const int ntb = ntok - tb0 < tpb ? ntok - tb0 : tpb;
     const int L = p.pos0 + tb0 + ntb;  // positions the block's last token sees
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, r = lane & 15, gq4 = lane >> 4;
@@ -1404,9 +1594,13 @@ hipError_t launch_pre_attention(const PreAttnArgs& p, int ntok, hipStream_t s) {
     const int L = p.pos0 + ntok;
     const bool fa_ok = pre_attn_mfma_fits(hpk, hd);
     if (p.mfma && fa_ok && (ntok >= kFaMinTok || L * hpk > kExactScores)) {
-        const dim3 fgrid((ntok + kFaRows / hpk - 1) / (kFaRows / hpk), p.a.kv_heads);
+        const dim3 fgrid(((ntok + kFaRows / hpk - 1) / (kFaRows / hpk)) * p.a.kv_heads);
         if (hd == 64) hipLaunchKernelGGL(k_pre_attn_fa<64>, fgrid, dim3(kThreads), 0, s, p, ntok);
         else hipLaunchKernelGGL(k_pre_attn_fa<128>, fgrid, dim3(kThreads), 0, s, p, ntok);
+    } else if (!p.legacy && (hd == 64 || hd == 128) && hpk <= kPxRows && kPxRows % hpk == 0 && L <= kPaMaxL) {
+        const dim3 xgrid(((ntok + kPxRows / hpk - 1) / (kPxRows / hpk)) * p.a.kv_heads);
+        if (hd == 64) hipLaunchKernelGGL((k_pre_attn_rows<64, kPxRows, kPaMaxL>), xgrid, dim3(kThreads), 0, s, p, ntok);
+        else hipLaunchKernelGGL((k_pre_attn_rows<128, kPxRows, kPaMaxL>), xgrid, dim3(kThreads), 0, s, p, ntok);
     } else if (hpk <= kPaRows && (p.a.head_dim == 32 || p.a.head_dim == 64 || p.a.head_dim == 128) &&
         p.pos0 + ntok <= kPaMaxL) {
         const int tpb = kPaRows / hpk;

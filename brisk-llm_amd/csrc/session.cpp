@@ -194,6 +194,7 @@ Session::Session(const brisk_hip_config& cfg, const brisk_hip_tensor* tensors, s
         prefill_on_ = !(pf != nullptr && std::string(pf) == "0") && !debug_;
         const char* pa = std::getenv("BRISK_HIP_PREFILL_ATTN");  // "mfma": long prompts' attention on f16 MFMA
         prefill_mfma_ = pa != nullptr && std::string(pa) == "mfma";
+        prefill_legacy_ = pa != nullptr && std::string(pa) == "staged";
     }
     setup_loop();
     use_graphs_ = std::getenv("BRISK_HIP_NO_GRAPH") == nullptr && !debug_;
@@ -586,6 +587,7 @@ void Session::prefill_layers(size_t pos0, int T) {
         pa.q = pre_q_; pa.k = pre_k_; pa.v = pre_v_; pa.out = pre_att_;
         pa.qstride = qd; pa.kvstride = kvd; pa.pos0 = static_cast<int>(pos0);
         pa.mfma = prefill_mfma_ ? 1 : 0;
+        pa.legacy = prefill_legacy_ ? 1 : 0;
         check(launch_pre_attention(pa, T, stream_), "prefill attention");
         // h += O (sub-normed) att (:1095-1111)
         prefill_quant(pre_att_, qd, L.attn_sub_norm, qd, T, L.o);

@@ -119,7 +119,8 @@ private:
     // batched prefill (int8 MFMA), buffers for kPrefillTokens tokens, allocated on first use
     static constexpr int kPrefillTokens = 512;
     bool prefill_on_ = true;
-    bool prefill_mfma_ = false;  // BRISK_HIP_PREFILL_ATTN=mfma
+    bool prefill_mfma_ = false;    // BRISK_HIP_PREFILL_ATTN=mfma
+    bool prefill_legacy_ = false;  // BRISK_HIP_PREFILL_ATTN=staged
     float *pre_h_ = nullptr, *pre_q_ = nullptr, *pre_k_ = nullptr, *pre_v_ = nullptr, *pre_att_ = nullptr, *pre_act_ = nullptr;
     ActPlanar pre_x_{};
     float* all_logits_ = nullptr;  // eval_all's [64][vocab] logits, allocated on first use
