@@ -869,19 +869,42 @@ __global__ void k_pre_embed(Packed m, const int* __restrict__ seq, int pos0, flo
 }
 
 // Q/K norms, RoPE, and the K/V cache rows of token t (grid: tokens x kv heads);
-// the normed, rotated queries go back to q.
+// the normed, rotated queries go back to q.  The same steps as the token
+// path's attention prologue (attn_load_raw, attn_finish_prologue), with an LDS
+// footprint of this token's rows only, so many workgroups share a CU.
+constexpr int kRopeMaxHeads = 16;  // query heads a kv head (as the token path's AttnLds)
+struct RopeLds {
+    alignas(16) float q[kRopeMaxHeads * 128];
+    float kcur[128], vcur[128];
+};
 __global__ __launch_bounds__(kThreads) void k_pre_rope(PreAttnArgs p) {
-    __shared__ AttnLds s;
-    const int t = blockIdx.x, kv = blockIdx.y, pos = p.pos0 + t;
-    AttnArgs g = p.a;
-    g.q = p.q + static_cast<size_t>(t) * p.qstride;
-    g.k = p.k + static_cast<size_t>(t) * p.kvstride;
-    g.v = p.v + static_cast<size_t>(t) * p.kvstride;
-    attn_load_raw<PlainIO>(g, s, kv, true);
-    attn_finish_prologue<false>(g, s, kv, pos, true, true);
+    __shared__ RopeLds s;
+    const int t = blockIdx.x, kv = blockIdx.y, pos = p.pos0 + t, tid = threadIdx.x;
+    const AttnArgs& g = p.a;
     const int hpk = g.heads / g.kv_heads, hd = g.head_dim;
     float* q = p.q + static_cast<size_t>(t) * p.qstride + kv * hpk * hd;
-    for (int i = threadIdx.x; i < hpk * hd; i += kThreads) q[i] = s.q[i];
+    const float* k = p.k + static_cast<size_t>(t) * p.kvstride + kv * hd;
+    const float* v = p.v + static_cast<size_t>(t) * p.kvstride + kv * hd;
+    for (int i = tid; i < hpk * hd; i += kThreads) s.q[i] = q[i];
+    for (int i = tid; i < hd; i += kThreads) {
+        s.kcur[i] = k[i];
+        s.vcur[i] = v[i];
+    }
+    __syncthreads();
+    const float* rope = g.rope + static_cast<size_t>(pos) * hd;
+    for (int h = tid >> 6; h <= hpk; h += kThreads / 64) {  // a wave a head; the last is the key
+        if (h < hpk) head_norm_rope(s.q + h * hd, g.qnorm, rope, hd, g.neox, g.eps);
+        else head_norm_rope(s.kcur, g.knorm, rope, hd, g.neox, g.eps);
+    }
+    __syncthreads();
+    // the cache rows, fp16 (store_f16, src/kernels_f32.cpp:248-250)
+    uint16_t* kr = g.kcache + (static_cast<size_t>(kv) * g.ctx + pos) * hd;
+    uint16_t* vr = g.vcache + (static_cast<size_t>(kv) * g.ctx + pos) * hd;
+    for (int i = 2 * tid; i < hd; i += 2 * kThreads) {
+        *reinterpret_cast<uint32_t*>(kr + i) = f2h(s.kcur[i]) | (static_cast<uint32_t>(f2h(s.kcur[i + 1])) << 16);
+        *reinterpret_cast<uint32_t*>(vr + i) = f2h(s.vcur[i]) | (static_cast<uint32_t>(f2h(s.vcur[i + 1])) << 16);
+    }
+    for (int i = tid; i < hpk * hd; i += kThreads) q[i] = s.q[i];
 }
 
 // Attention of token t over positions 0 .. pos0 + t, in the reference's order.
@@ -1587,6 +1610,7 @@ hipError_t launch_pre_embed(const Packed& m, const int* seq, int pos0, int ntok,
 hipError_t launch_pre_attention(const PreAttnArgs& p, int ntok, hipStream_t s) {
     if (ntok <= 0) return hipSuccess;
     const dim3 grid(ntok, p.a.kv_heads);
+    if (p.a.heads / p.a.kv_heads > kRopeMaxHeads || p.a.head_dim > 128) return hipErrorInvalidValue;
     hipLaunchKernelGGL(k_pre_rope, grid, dim3(kThreads), 0, s, p);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
