@@ -883,7 +883,11 @@ struct Tile {
     uint32_t row0;
     int R;
 
-    // Issues the loads of every unit this thread owns.
+    // Issues the loads of every unit this thread owns.  Every thread issues all
+    // kMax, unconditionally (units past the tile or the matrix re-read its last
+    // unit and are never used), so the count of loads in flight is the same on
+    // every path and a later wait for this tile can leave the next tile's loads
+    // in flight (vmcnt(n) rather than vmcnt(0)).
     __device__ __forceinline__ void load(const Packed& m, uint32_t first_row, int rows_in_tile) {
         row0 = first_row;
         R = rows_in_tile;
@@ -891,11 +895,10 @@ struct Tile {
         const uint32_t total = static_cast<uint32_t>(R) * units;
 #pragma unroll
         for (int k = 0; k < kMax; ++k) {
-            const uint32_t i = threadIdx.x + k * kThreads;
-            if (i < total) {
-                const uint32_t r = i / units, b = i - r * units;
-                if (row0 + r < m.rows) u[k].load(m, static_cast<size_t>(row0 + r) * units + b);
-            }
+            const uint32_t i0 = threadIdx.x + k * kThreads, i = i0 < total ? i0 : total - 1;
+            const uint32_t r = i / units, b = i - r * units;
+            const uint32_t row = row0 + r < m.rows ? row0 + r : m.rows - 1;
+            u[k].load(m, static_cast<size_t>(row) * units + b);
         }
     }
 

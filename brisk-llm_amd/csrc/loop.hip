@@ -233,11 +233,11 @@ __device__ __forceinline__ bool run_tiles(int total, GemvLds& s, RowOf row_of, R
         return true;
     };
     auto fits = [&](int more) { return (grows + more) * static_cast<int>(stride) <= kTermCap && grows + more <= kGroupRows; };
+    // the next tile's loads are issued on every path (the last tile re-reads
+    // itself), so the wait for the current tile leaves them in flight
     while (true) {
-        if (t + G < total) {
-            row_of(t + G, mb, rb, Rb);
-            tb.load(mb, rb, Rb);
-        }
+        row_of(t + G < total ? t + G : t, mb, rb, Rb);
+        tb.load(mb, rb, Rb);
         ta.terms(ma, s.a, s.terms + grows * stride);
         grows += Ra;
         if (t + G >= total || !fits(Rb)) {
@@ -246,10 +246,8 @@ __device__ __forceinline__ bool run_tiles(int total, GemvLds& s, RowOf row_of, R
         }
         t += G;
         if (t >= total) break;
-        if (t + G < total) {
-            row_of(t + G, ma, ra, Ra);
-            ta.load(ma, ra, Ra);
-        }
+        row_of(t + G < total ? t + G : t, ma, ra, Ra);
+        ta.load(ma, ra, Ra);
         tb.terms(mb, s.a, s.terms + grows * stride);
         grows += Rb;
         if (t + G >= total || !fits(Ra)) {
