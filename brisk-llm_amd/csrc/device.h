@@ -883,22 +883,32 @@ struct Tile {
     uint32_t row0;
     int R;
 
-    // Issues the loads of every unit this thread owns.  Every thread issues all
-    // kMax, unconditionally (units past the tile or the matrix re-read its last
-    // unit and are never used), so the count of loads in flight is the same on
-    // every path and a later wait for this tile can leave the next tile's loads
-    // in flight (vmcnt(n) rather than vmcnt(0)).
+    // Issues the loads of every unit this thread owns.  Units past the tile or
+    // the matrix re-read its last unit (never used) rather than skip the load:
+    // with up to 4 units a thread (the persistent loop's tiles) every thread
+    // issues all of them on every path, so the count of loads in flight is the
+    // same everywhere and a later wait for this tile can leave the next tile's
+    // loads in flight (vmcnt(n) rather than vmcnt(0)).  Larger tiles do the
+    // same when the tile fills every unit of every thread (one straight run of
+    // loads); a partial one skips the rounds wholly past it (uniform branches).
     __device__ __forceinline__ void load(const Packed& m, uint32_t first_row, int rows_in_tile) {
         row0 = first_row;
         R = rows_in_tile;
         const uint32_t units = m.cols / Unit<T>::kElems;
         const uint32_t total = static_cast<uint32_t>(R) * units;
-#pragma unroll
-        for (int k = 0; k < kMax; ++k) {
+        auto one = [&](int k) {
             const uint32_t i0 = threadIdx.x + k * kThreads, i = i0 < total ? i0 : total - 1;
             const uint32_t r = i / units, b = i - r * units;
             const uint32_t row = row0 + r < m.rows ? row0 + r : m.rows - 1;
             u[k].load(m, static_cast<size_t>(row) * units + b);
+        };
+        if (kMax <= 4 || total >= static_cast<uint32_t>(kMax * kThreads)) {
+#pragma unroll
+            for (int k = 0; k < kMax; ++k) one(k);
+        } else {
+#pragma unroll
+            for (int k = 0; k < kMax; ++k)
+                if (static_cast<uint32_t>(k * kThreads) < total) one(k);
         }
     }
 
