@@ -1208,9 +1208,9 @@ __global__ __launch_bounds__(kThreads) void k_pre_attn_rows(PreAttnArgs p, int n
                 for (int gq = 0; gq < hpk; ++gq) {
                     const int row = tt * hpk + gq;
                     const float* q = s.q + row * HD;
+                    // the lane partials start at their first product, not at 0 + it: they
+                    // differ only by a zero's sign, which the 0 + ... of the final sum removes
                     float lane[16];
-#pragma unroll
-                    for (int j = 0; j < 16; ++j) lane[j] = 0.0f;
 #pragma unroll
                     for (int m = 0; m < PER; ++m) {
                         const float4* q4 = reinterpret_cast<const float4*>(q + 16 * m);
@@ -1218,8 +1218,10 @@ __global__ __launch_bounds__(kThreads) void k_pre_attn_rows(PreAttnArgs p, int n
                         const float qv[16] = {qa.x, qa.y, qa.z, qa.w, qb.x, qb.y, qb.z, qb.w,
                                               qc.x, qc.y, qc.z, qc.w, qd.x, qd.y, qd.z, qd.w};
 #pragma unroll
-                        for (int j = 0; j < 16; ++j)
-                            lane[j] += (j & 1) ? mul_h<true>(qv[j], kw[8 * m + (j >> 1)]) : mul_h<false>(qv[j], kw[8 * m + (j >> 1)]);
+                        for (int j = 0; j < 16; ++j) {
+                            const float pr = (j & 1) ? mul_h<true>(qv[j], kw[8 * m + (j >> 1)]) : mul_h<false>(qv[j], kw[8 * m + (j >> 1)]);
+                            lane[j] = m == 0 ? pr : lane[j] + pr;
+                        }
                     }
                     float sum = 0.0f;
 #pragma unroll
