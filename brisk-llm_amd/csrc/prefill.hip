@@ -496,13 +496,13 @@ constexpr int kKqCus = 256;  // MI355X compute units (the tile choice aims at a 
 // tokens a workgroup: 16 G (G token groups share each weight fragment's decode); the
 // launcher takes the largest G that still gives a workgroup to every CU
 
+template <uint32_t T>
 struct KqStage {
-    alignas(16) uint8_t w0[64 * 128];      // Q4_K nibbles / Q6_K ql: row r piece p at slot r * 8 + (p ^ (r & 7))
-    alignas(16) uint8_t wk[4096];          // Q4_K: p1 [64][16] then p2 [64][16]; Q6_K: qh, row r piece p at r * 4 + (p ^ (r & 3))
-    alignas(16) uint32_t wm[384];          // Q6_K: the 20-byte meta of row r at dwords 5 r .. 5 r + 4
-    alignas(16) int8_t x[kKqTokMax * 256];   // token t piece p at slot t * 16 + (p ^ (t & 15))
-    alignas(16) int32_t bs[kKqTokMax * 16];  // bsums of token t at 16 t
-    alignas(16) float xd[64];              // Q8_K scale of token t (lanes 32..63: a copy)
+    alignas(16) uint8_t w0[64 * 128];                  // Q4_K nibbles / Q6_K ql: row r piece p at slot r * 8 + (p ^ (r & 7))
+    alignas(16) uint8_t wk[T == kQ4_K ? 2048 : 4096];  // Q4_K: p1 [64][16] then p2 [64][16]; Q6_K: qh, row r piece p at r * 4 + (p ^ (r & 3))
+    alignas(16) uint32_t wm[T == kQ6_K ? 384 : 1];     // Q6_K: the 20-byte meta of row r at dwords 5 r .. 5 r + 4
+    alignas(16) int8_t x[kKqTokMax * 256];             // token t piece p at slot t * 16 + (p ^ (t & 15))
+    alignas(16) float xd[64];                          // Q8_K scale of token t (lanes 32..63: a copy)
 };
 
 __device__ __forceinline__ void dma16(const void* src, void* lds_wave_base) {
@@ -515,7 +515,7 @@ __device__ __forceinline__ void dma4(const void* src, void* lds_wave_base) {
 // Copies chunk c of rows r0 .. r0 + 63 and tokens t0 .. t0 + 31 into the stage
 // (rows and tokens past the ends re-read the last one; their outputs are not stored).
 template <uint32_t T, int G>
-__device__ __forceinline__ void kq_copy(KqStage& st, const Packed& m, const ActPlanar& x, int ntok, uint32_t r0, int t0, int c) {
+__device__ __forceinline__ void kq_copy(KqStage<T>& st, const Packed& m, const ActPlanar& x, int ntok, uint32_t r0, int t0, int c) {
     const int tid = threadIdx.x, wave = tid >> 6, wave_first = tid & ~63;
     const uint32_t nsb = m.cols / 256, rmax = m.rows - 1;
     auto rowc = [&](int r) -> size_t {
@@ -608,11 +608,11 @@ template <int G>
 __device__ __forceinline__ KqF64 kq_f64_issue(uint32_t base, int s, int ar, int tl, int l16) {
     KqF64 f;
     const int pa = 2 * s + (l16 & 1);  // Q4_K: 32 bytes of nibbles a sub-block pair, low then high
-    f.a = ds128v(base + offsetof(KqStage, w0) + (ar * 8 + (pa ^ (ar & 7))) * 16);
+    f.a = ds128v(base + offsetof(KqStage<kQ4_K>, w0) + (ar * 8 + (pa ^ (ar & 7))) * 16);
     const int pb = 4 * s + l16;
     auto bfrag = [&](int g) -> v4u {
         const int t = 16 * g + tl;
-        return ds128v(base + offsetof(KqStage, x) + (t * 16 + (pb ^ (t & 15))) * 16);
+        return ds128v(base + offsetof(KqStage<kQ4_K>, x) + (t * 16 + (pb ^ (t & 15))) * 16);
     };
     const v4u z = {0u, 0u, 0u, 0u};
     f.b0 = bfrag(0);
@@ -631,12 +631,12 @@ __device__ __forceinline__ void kq_compute_fold(uint32_t base, MmAcc<G>& acc) {
     const int ar = wave * 16 + tl, orow0 = wave * 16 + l16 * 4;
     const v4i zero = {0, 0, 0, 0};
     // the A row's decoded scales and mins (for the digits), the output rows' d / dmin, the groups' x scales
-    v4u scm = ds128v(base + offsetof(KqStage, wk) + 1024 + ar * 16);
+    v4u scm = ds128v(base + offsetof(KqStage<kQ4_K>, wk) + 1024 + ar * 16);
     uint32_t dd[4], xd[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-        dd[i] = ds32(base + offsetof(KqStage, wk) + (orow0 + i) * 16);
-        xd[i] = i < G ? ds32(base + offsetof(KqStage, xd) + (16 * i + tl) * 4) : 0u;
+        dd[i] = ds32(base + offsetof(KqStage<kQ4_K>, wk) + (orow0 + i) * 16);
+        xd[i] = i < G ? ds32(base + offsetof(KqStage<kQ4_K>, xd) + (16 * i + tl) * 4) : 0u;
     }
     asm volatile("s_waitcnt lgkmcnt(0)"
                  : "+v"(scm), "+v"(dd[0]), "+v"(dd[1]), "+v"(dd[2]), "+v"(dd[3]), "+v"(xd[0]), "+v"(xd[1]), "+v"(xd[2]),
@@ -707,12 +707,12 @@ __device__ __forceinline__ Kq6F kq6_issue(uint32_t base, int st, int ar, int tl,
     Kq6F f;
     const int half = st >> 1;
     const int lp = half * 4 + l16, hp = half * 2 + (l16 & 1);
-    f.l = ds128v(base + offsetof(KqStage, w0) + (ar * 8 + (lp ^ (ar & 7))) * 16);
-    f.h = ds128v(base + offsetof(KqStage, wk) + (ar * 4 + (hp ^ (ar & 3))) * 16);
+    f.l = ds128v(base + offsetof(KqStage<kQ6_K>, w0) + (ar * 8 + (lp ^ (ar & 7))) * 16);
+    f.h = ds128v(base + offsetof(KqStage<kQ6_K>, wk) + (ar * 4 + (hp ^ (ar & 3))) * 16);
     const int pb = 4 * st + l16;
     auto bfrag = [&](int g) -> v4u {
         const int t = 16 * g + tl;
-        return ds128v(base + offsetof(KqStage, x) + (t * 16 + (pb ^ (t & 15))) * 16);
+        return ds128v(base + offsetof(KqStage<kQ6_K>, x) + (t * 16 + (pb ^ (t & 15))) * 16);
     };
     const v4u z = {0u, 0u, 0u, 0u};
     f.b0 = bfrag(0);
@@ -731,13 +731,13 @@ __device__ __forceinline__ void kq_compute_fold6(uint32_t base, MmAcc<G>& acc) {
     const int ar = wave * 16 + tl, orow0 = wave * 16 + l16 * 4;
     const v4i zero = {0, 0, 0, 0};
     // the A row's 16 int8 scales (four dwords of its meta), the output rows' d, the groups' x scales
-    const uint32_t arow = base + offsetof(KqStage, wm) + ar * 20;
+    const uint32_t arow = base + offsetof(KqStage<kQ6_K>, wm) + ar * 20;
     uint32_t s0 = ds32(arow), s1 = ds32(arow + 4), s2 = ds32(arow + 8), s3 = ds32(arow + 12);
     uint32_t dd[4], xd[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-        dd[i] = ds32(base + offsetof(KqStage, wm) + (orow0 + i) * 20 + 16);
-        xd[i] = i < G ? ds32(base + offsetof(KqStage, xd) + (16 * i + tl) * 4) : 0u;
+        dd[i] = ds32(base + offsetof(KqStage<kQ6_K>, wm) + (orow0 + i) * 20 + 16);
+        xd[i] = i < G ? ds32(base + offsetof(KqStage<kQ6_K>, xd) + (16 * i + tl) * 4) : 0u;
     }
     asm volatile("s_waitcnt lgkmcnt(0)"
                  : "+v"(s0), "+v"(s1), "+v"(s2), "+v"(s3), "+v"(dd[0]), "+v"(dd[1]), "+v"(dd[2]), "+v"(dd[3]), "+v"(xd[0]),
@@ -808,7 +808,7 @@ __device__ __forceinline__ void kq_compute_fold6(uint32_t base, MmAcc<G>& acc) {
 
 template <uint32_t T, int MODE, int G>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 8))) void k_mmk(MmArgs g) {
-    __shared__ KqStage st[2];
+    __shared__ KqStage<T> st[2];
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const uint32_t rt0 = blockIdx.x * 64;
     const int t0 = blockIdx.y * (16 * G);
