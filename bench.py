@@ -353,11 +353,20 @@ def main():
         params = lcfg.layers * (2 * lcfg.embd * lcfg.heads * lcfg.head_dim + 2 * lcfg.embd * lcfg.kv_heads * lcfg.head_dim
                                 + 3 * lcfg.embd * lcfg.ff)
         ops = 2 * 512 * params
+        import ctypes as C
+        tops, tops32 = C.c_double(), C.c_double()
+        L.check(lib.brisk_hip_mfma_rate(0, C.byref(tops)))
+        L.check(lib.brisk_hip_mfma_rate(1, C.byref(tops32)))
+        log(f"int8 MFMA rate (register operands): v_mfma_i32_16x16x64_i8 {tops.value:.0f} TOP/s, "
+            f"v_mfma_i32_32x32x32_i8 {tops32.value:.0f} TOP/s")
         result["prefill"] = {"workload": "configs[2]: llama-3.2-1b-shape Q4_K_M, 512 random prompt ids (eval, last-token logits; median of 5)",
                              "value": round(512 / dtp, 2), "unit": "tok/s", "ms": round(dtp * 1e3, 2),
                              "roofline": {"bound": "mfma", "achieved": round(ops / dtp / 1e12, 2), "peak": 5000.0,
                                           "unit": "TOP/s (int8)", "frac": round(ops / dtp / 5.0e15, 5),
-                                          "ops": ops},
+                                          "ops": ops,
+                                          "mfma_int8_measured_tops": round(tops.value, 1),
+                                          "mfma_int8_32x32x32_measured_tops": round(tops32.value, 1),
+                                          "frac_of_measured": round(ops / dtp / 1e12 / tops.value, 5)},
                              "decode_after_prefill_tok_s": round(128 / dtd, 2)}
         log(f"prefill 512: {dtp * 1e3:.1f} ms -> {512 / dtp:.1f} tok/s; then 128 decode steps {128 / dtd:.1f} tok/s")
         ls.rollback(0)

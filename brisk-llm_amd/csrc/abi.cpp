@@ -178,6 +178,36 @@ int brisk_hip_div_selftest(unsigned long long* mismatches) {
     });
 }
 
+int brisk_hip_mfma_rate(int shape, double* int8_tops) {
+    return guarded([&] {
+        if (int8_tops == nullptr || shape < 0 || shape > 1) throw bh::Error(BRISK_HIP_EINVAL, "mfma rate: bad argument");
+        int dev = 0, cus = 0;
+        hip_check(hipGetDevice(&dev), "hipGetDevice");
+        hip_check(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev), "hipDeviceGetAttribute");
+        int* d = nullptr;
+        hip_check(hipMalloc(&d, 8), "hipMalloc");
+        hipEvent_t e0 = nullptr, e1 = nullptr;
+        const int blocks = 4 * cus, iters = 4096;
+        hipError_t e = hipEventCreate(&e0);
+        if (e == hipSuccess) e = hipEventCreate(&e1);
+        if (e == hipSuccess) e = bh::launch_mfma_rate(shape, blocks, 64, d, nullptr);  // warm-up
+        if (e == hipSuccess) e = hipEventRecord(e0, nullptr);
+        if (e == hipSuccess) e = bh::launch_mfma_rate(shape, blocks, iters, d, nullptr);
+        if (e == hipSuccess) e = hipEventRecord(e1, nullptr);
+        if (e == hipSuccess) e = hipEventSynchronize(e1);
+        float ms = 0.0f;
+        if (e == hipSuccess) e = hipEventElapsedTime(&ms, e0, e1);
+        if (e0) (void)hipEventDestroy(e0);
+        if (e1) (void)hipEventDestroy(e1);
+        (void)hipFree(d);
+        hip_check(e, "mfma rate");
+        // multiply-adds (2 ops each) per wave and iteration: 8 x 16x16x64 or 4 x 32x32x32
+        const double per_iter = shape == 0 ? 8.0 * 16 * 16 * 64 : 4.0 * 32 * 32 * 32;
+        const double ops = static_cast<double>(blocks) * (bh::kThreads / 64) * iters * per_iter * 2;
+        *int8_tops = ops / (ms * 1e-3) / 1e12;
+    });
+}
+
 int brisk_hip_session_create(const brisk_hip_config* config, const brisk_hip_tensor* tensors, size_t n_tensors, size_t max_context,
                              int device, brisk_hip_session** out) {
     return guarded([&] {

@@ -335,6 +335,51 @@ __global__ void k_div_selftest(unsigned long long* bad) {
     if (nm != 0) atomicAdd(bad + 3, nm);
 }
 
+// The int8 MFMA rate this device sustains: every wave runs independent
+// accumulator chains of one int8 MFMA shape (8 of v_mfma_i32_16x16x64_i8, the
+// prefill GEMMs' instruction, or 4 of v_mfma_i32_32x32x32_i8; 8192 multiply-adds
+// a chain step either way... the 32x32 shape does 32768) on register operands,
+// so nothing but the matrix cores bounds it.  out receives a checksum that
+// keeps the work alive.
+typedef int v4i_mb __attribute__((ext_vector_type(4)));
+typedef int v16i_mb __attribute__((ext_vector_type(16)));
+template <int kShape>  // 0: v_mfma_i32_16x16x64_i8, 1: v_mfma_i32_32x32x32_i8
+__global__ __launch_bounds__(kThreads) void k_mfma_rate(int iters, int* out) {
+    const int lane = threadIdx.x & 63;
+    const v4i_mb a = {lane, lane * 3, lane * 5, lane * 7}, b = {lane * 11, lane * 13, 17, lane};
+    int sum = 0;
+    if (kShape == 0) {
+        v4i_mb acc[8];
+#pragma unroll
+        for (int k = 0; k < 8; ++k) acc[k] = v4i_mb{k, 0, 0, 0};
+        for (int it = 0; it < iters; ++it)
+#pragma unroll
+            for (int k = 0; k < 8; ++k) acc[k] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, acc[k], 0, 0, 0);
+#pragma unroll
+        for (int k = 0; k < 8; ++k) sum += acc[k][0] + acc[k][1] + acc[k][2] + acc[k][3];
+    } else {
+        v16i_mb acc[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            acc[k] = v16i_mb{};
+            acc[k][0] = k;
+        }
+        for (int it = 0; it < iters; ++it)
+#pragma unroll
+            for (int k = 0; k < 4; ++k) acc[k] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b, acc[k], 0, 0, 0);
+#pragma unroll
+        for (int k = 0; k < 4; ++k) sum += acc[k][0] + acc[k][5] + acc[k][10] + acc[k][15];
+    }
+    if (sum == 0x7FFFFFFF) out[0] = sum;  // practically never: keeps the chains without a store per wave
+    if (threadIdx.x == 0 && blockIdx.x == 0) out[1] = sum;
+}
+
+hipError_t launch_mfma_rate(int shape, int blocks, int iters, int* out, hipStream_t s) {
+    if (shape == 0) hipLaunchKernelGGL(k_mfma_rate<0>, dim3(blocks), dim3(kThreads), 0, s, iters, out);
+    else hipLaunchKernelGGL(k_mfma_rate<1>, dim3(blocks), dim3(kThreads), 0, s, iters, out);
+    return hipGetLastError();
+}
+
 hipError_t launch_div_selftest(unsigned long long* bad, hipStream_t s) {
     hipLaunchKernelGGL(k_div_selftest, dim3(8192), dim3(256), 0, s, bad);
     return hipGetLastError();

@@ -92,6 +92,7 @@ hipError_t launch_head(HeadArgs g, hipStream_t s);
 hipError_t launch_advance(int* pos, hipStream_t s);
 hipError_t launch_expf(const float* x, float* y, size_t n, hipStream_t s);
 hipError_t launch_div_selftest(unsigned long long* bad, hipStream_t s);
+hipError_t launch_mfma_rate(int shape, int blocks, int iters, int* out, hipStream_t s);
 int attention_max_splits(int ctx);
 int pick_rows_per_tile(uint32_t type, size_t rows, size_t cols);
 

@@ -591,7 +591,8 @@ __device__ __forceinline__ uint4 ds128(uint32_t a) {
 //   offsets  = sum_k mn_j(k) x_k   (pair_j is the sum of sub-block j's x),
 // three int32 MFMA chains over the super-block, with no per-sub-block integer
 // epilogue.  The float term per super-block is the reference's.
-// The MFMA is v_mfma_i32_16x16x64_i8 (CDNA4's full-rate int8 shape): lane l
+// The MFMA is v_mfma_i32_16x16x64_i8 (measured at 2.5 POP/s on register operands,
+// against 4.2 for v_mfma_i32_32x32x32_i8: brisk_hip_mfma_rate): lane l
 // holds 16 consecutive k of A row l % 16 and of B column l % 16, k = 16 (l / 16)
 // .. + 15 of the 64, so lanes 0..31 are sub-block 2 s and lanes 32..63
 // sub-block 2 s + 1 of step s, and each lane's digit is its own sub-block's.

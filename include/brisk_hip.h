@@ -126,6 +126,14 @@ int brisk_hip_expf(const float* x, float* y, size_t n, void* stream);
  * counterpart in the reference. */
 int brisk_hip_div_selftest(unsigned long long* mismatches);
 
+/* The int8 matrix-core rate this device sustains (TOP/s): independent MFMA
+ * chains a wave on register operands, four workgroups a compute unit, timed
+ * with HIP events.  shape 0: v_mfma_i32_16x16x64_i8 (the prefill GEMMs'
+ * instruction), 1: v_mfma_i32_32x32x32_i8.  The measured ceiling the prefill
+ * GEMMs' MFMA fraction is read against.  Measurement support; no counterpart
+ * in the reference. */
+int brisk_hip_mfma_rate(int shape, double* int8_tops);
+
 /* ---------------------------------------------------------------- session level */
 
 /* Engine construction, as `MetalSession(model, file bytes, max_context)`
