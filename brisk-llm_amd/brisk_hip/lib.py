@@ -19,7 +19,7 @@ EXPORTS = (
     "brisk_hip_last_error", "brisk_hip_abi_version", "brisk_hip_device_count", "brisk_hip_packed_bytes", "brisk_hip_pack",
     "brisk_hip_quantize_q8_0", "brisk_hip_quantize_q8_k", "brisk_hip_matvec", "brisk_hip_matmul", "brisk_hip_gemv", "brisk_hip_expf",
     "brisk_hip_div_selftest", "brisk_hip_mfma_rate",
-    "brisk_hip_session_create", "brisk_hip_session_destroy", "brisk_hip_session_eval", "brisk_hip_session_eval_all",
+    "brisk_hip_session_estimate", "brisk_hip_device_memory", "brisk_hip_session_create", "brisk_hip_session_destroy", "brisk_hip_session_eval", "brisk_hip_session_eval_all",
     "brisk_hip_session_eval_greedy", "brisk_hip_session_generate", "brisk_hip_session_decode", "brisk_hip_session_rollback",
     "brisk_hip_session_position", "brisk_hip_session_max_context", "brisk_hip_session_kv_cache",
     "brisk_hip_session_set_position", "brisk_hip_session_stream", "brisk_hip_session_trace",
@@ -34,6 +34,10 @@ class HipConfig(C.Structure):
 
 class HipTensor(C.Structure):
     _fields_ = [("name", C.c_char_p), ("type", C.c_int), ("rows", C.c_uint64), ("cols", C.c_uint64), ("data", C.c_void_p)]
+
+
+class HipMemory(C.Structure):
+    _fields_ = [("weights", C.c_size_t), ("cache", C.c_size_t), ("scratch", C.c_size_t), ("total", C.c_size_t)]
 
 
 class BriskHipError(RuntimeError):
@@ -66,6 +70,8 @@ def load():
     L.brisk_hip_expf.argtypes = [_vp, _vp, _sz, _vp]
     L.brisk_hip_div_selftest.argtypes = [C.POINTER(C.c_ulonglong)]
     L.brisk_hip_mfma_rate.argtypes = [_i, C.POINTER(C.c_double)]
+    L.brisk_hip_session_estimate.argtypes = [C.POINTER(HipConfig), C.POINTER(HipTensor), _sz, _sz, C.POINTER(HipMemory)]
+    L.brisk_hip_device_memory.argtypes = [_i, C.POINTER(_sz), C.POINTER(_sz)]
     L.brisk_hip_session_create.argtypes = [C.POINTER(HipConfig), C.POINTER(HipTensor), _sz, _sz, _i, C.POINTER(_vp)]
     L.brisk_hip_session_destroy.argtypes = [_vp]
     L.brisk_hip_session_eval.argtypes = [_vp, _vp, _sz, _vp]

@@ -20,6 +20,37 @@ def _ptr(a: np.ndarray):
     return a.ctypes.data_as(C.c_void_p)
 
 
+def _c_args(c, table):
+    """The C ABI's config and tensor table for a ModelConfig and tensor list (plus what keeps them alive)."""
+    hc = _lib.HipConfig(c.arch, c.vocab, c.embd, c.layers, c.heads, c.kv_heads, c.head_dim, c.ff, c.context,
+                        c.rope_base, c.eps)
+    names = [t.name.encode() for t in table]
+    arr = (_lib.HipTensor * len(table))()
+    for i, t in enumerate(table):
+        arr[i] = _lib.HipTensor(names[i], t.type, t.rows, t.cols, t.data.ctypes.data)
+    return hc, arr, names
+
+
+def estimate(source, max_context: int = 0) -> dict:
+    """Device bytes a session would take (brisk_hip_session_estimate; nothing is allocated, no GPU needed)."""
+    L = _lib.load()
+    if isinstance(source, str):
+        source = _model.load(source)
+    _, c, table = source
+    hc, arr, keep = _c_args(c, table)
+    m = _lib.HipMemory()
+    _lib.check(L.brisk_hip_session_estimate(C.byref(hc), arr, len(table), max_context, C.byref(m)))
+    return {"weights": m.weights, "cache": m.cache, "scratch": m.scratch, "total": m.total}
+
+
+def device_memory(device: int = 0):
+    """(free, total) bytes of the device (brisk_hip_device_memory)."""
+    L = _lib.load()
+    f, t = C.c_size_t(), C.c_size_t()
+    _lib.check(L.brisk_hip_device_memory(device, C.byref(f), C.byref(t)))
+    return f.value, t.value
+
+
 class HipSession:
     """One sequence on one GPU.  ``source`` is a GGUF path or a (GgufFile, ModelConfig, table) triple."""
 
@@ -32,12 +63,7 @@ class HipSession:
             source = _model.load(source)
         self.file, self.config, table = source
         c = self.config
-        hc = _lib.HipConfig(c.arch, c.vocab, c.embd, c.layers, c.heads, c.kv_heads, c.head_dim, c.ff, c.context,
-                            c.rope_base, c.eps)
-        names = [t.name.encode() for t in table]
-        arr = (_lib.HipTensor * len(table))()
-        for i, t in enumerate(table):
-            arr[i] = _lib.HipTensor(names[i], t.type, t.rows, t.cols, t.data.ctypes.data)
+        hc, arr, keep = _c_args(c, table)
         h = C.c_void_p()
         _lib.check(L.brisk_hip_session_create(C.byref(hc), arr, len(table), max_context, device, C.byref(h)))
         self._h = h

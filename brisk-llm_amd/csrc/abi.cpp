@@ -208,6 +208,26 @@ int brisk_hip_mfma_rate(int shape, double* int8_tops) {
     });
 }
 
+int brisk_hip_session_estimate(const brisk_hip_config* config, const brisk_hip_tensor* tensors, size_t n_tensors,
+                               size_t max_context, brisk_hip_memory* out) {
+    return guarded([&] {
+        if (config == nullptr || out == nullptr || (tensors == nullptr && n_tensors != 0))
+            throw bh::Error(BRISK_HIP_EINVAL, "session: null argument");
+        *out = bh::estimate_session(*config, tensors, n_tensors, max_context);
+    });
+}
+
+int brisk_hip_device_memory(int device, size_t* free_bytes, size_t* total_bytes) {
+    return guarded([&] {
+        if (free_bytes == nullptr || total_bytes == nullptr) throw bh::Error(BRISK_HIP_EINVAL, "device memory: null argument");
+        int count = 0;
+        if (hipGetDeviceCount(&count) != hipSuccess || device < 0 || device >= count)
+            throw bh::Error(BRISK_HIP_ENODEV, "hip: no GPU device " + std::to_string(device));
+        hip_check(hipSetDevice(device), "hipSetDevice");
+        hip_check(hipMemGetInfo(free_bytes, total_bytes), "hipMemGetInfo");
+    });
+}
+
 int brisk_hip_session_create(const brisk_hip_config* config, const brisk_hip_tensor* tensors, size_t n_tensors, size_t max_context,
                              int device, brisk_hip_session** out) {
     return guarded([&] {

@@ -39,6 +39,44 @@ DeviceMatrix::~DeviceMatrix() {
     if (mem != nullptr) (void)hipFree(mem);
 }
 
+// The sizes the constructor (and the first prefill / eval_all) allocate, from the
+// shapes alone: estimate_memory's parts (src/memory.cpp:46-96) for this backend.
+brisk_hip_memory estimate_session(const brisk_hip_config& cfg, const brisk_hip_tensor* tensors, size_t n, size_t max_context) {
+    brisk_hip_memory m{};
+    size_t staging = 0;
+    for (size_t i = 0; i < n; ++i) {
+        const brisk_hip_tensor& t = tensors[i];
+        if (t.type == BRISK_HIP_F32) {
+            m.weights += t.rows * t.cols * 4;
+        } else if (block_elems(t.type) != 0) {
+            m.weights += packed_bytes(t.type, t.rows, t.cols);
+            staging = std::max<size_t>(staging, t.rows * (t.cols / block_elems(t.type)) * gguf_block_bytes(t.type));
+        }
+    }
+    const size_t ctx = max_context == 0 ? cfg.context_length : std::min<size_t>(max_context, cfg.context_length);
+    const size_t e = cfg.embd, hd = cfg.head_dim, qd = static_cast<size_t>(cfg.heads) * hd,
+                 kvd = static_cast<size_t>(cfg.kv_heads) * hd, ff = cfg.ff;
+    m.cache = 2 * static_cast<size_t>(cfg.layers) * kvd * ctx * 2;
+    const size_t splits = static_cast<size_t>(attention_max_splits(static_cast<int>(ctx)));
+    size_t sc = (e + 2 * qd + ff + cfg.vocab + 2 * kvd) * 4;              // token-path activations, logits
+    sc += static_cast<size_t>(cfg.heads) * splits * (hd + 2) * 4;          // attention partials
+    sc += (ctx + 1) * 4 + ctx * hd * 4;                                    // token sequence, RoPE table
+    sc += (e + 2 * qd + 2 * kvd + ff + static_cast<size_t>(cfg.heads) * splits * (hd + 2)) * 8;  // hand-off words
+    const size_t T = Session::kPrefillTokens, widest = std::max(std::max(e, qd), ff), stride = (widest + 255) / 256 * 256;
+    sc += T * (e + 2 * qd + 2 * kvd + ff) * 4 + T * stride * (1 + 4 / 32.0 + 4 / 16.0);  // prefill buffers
+    sc += static_cast<size_t>(64) * cfg.vocab * 4;                         // eval_all logits
+    sc += staging + (64 << 10);                                            // load staging, small state
+    m.scratch = sc;
+    m.total = m.weights + m.cache + m.scratch;
+    return m;
+}
+
+static std::string gb(size_t bytes) {
+    char buf[32];
+    std::snprintf(buf, sizeof(buf), "%.2f GB", static_cast<double>(bytes) / (1024.0 * 1024.0 * 1024.0));
+    return buf;
+}
+
 Session::Session(const brisk_hip_config& cfg, const brisk_hip_tensor* tensors, size_t n, size_t max_context, int device)
     : cfg_(cfg), device_(device) {
     int count = 0;
@@ -54,6 +92,21 @@ Session::Session(const brisk_hip_config& cfg, const brisk_hip_tensor* tensors, s
     if (cfg.head_dim == 0 || cfg.head_dim % 32 != 0 || cfg.head_dim > 128) model_fail("head size must be 32, 64, 96 or 128");
     if (cfg.embd > kMaxCols || cfg.ff > kMaxCols || cfg.heads * cfg.head_dim > kMaxCols) model_fail("a row wider than 8192 is not supported");
     check(hipSetDevice(device), "hipSetDevice");
+    if (std::getenv("BRISK_NO_MEMORY_CHECK") == nullptr) {  // check_memory (src/memory.cpp:118-135), for HBM
+        size_t free_b = 0, total_b = 0;
+        check(hipMemGetInfo(&free_b, &total_b), "hipMemGetInfo");
+        const brisk_hip_memory need = estimate_session(cfg, tensors, n, max_context);
+        constexpr size_t margin = size_t{256} << 20;
+        if (need.total + margin > free_b) {
+            std::string hint = "a smaller model or quantisation";
+            const size_t shortfall = need.total + margin - free_b;
+            if (shortfall <= need.cache * 7 / 8) hint = "a shorter context (the cache is " + gb(need.cache) + "), or " + hint;
+            throw Error(BRISK_HIP_ENOMEM, "hip: the session needs about " + gb(need.total) + " (" + gb(need.weights) + " weights, " +
+                                              gb(need.cache) + " cache, " + gb(need.scratch) + " scratch) but " + gb(free_b) +
+                                              " of device memory is free. Try " + hint +
+                                              ", or set BRISK_NO_MEMORY_CHECK=1 to proceed regardless.");
+        }
+    }
     check(hipStreamCreateWithFlags(&stream_, hipStreamNonBlocking), "hipStreamCreate");
     max_ctx_ = max_context == 0 ? cfg.context_length : std::min<size_t>(max_context, cfg.context_length);
 

@@ -40,8 +40,12 @@ struct Layer {
     const float* ffn_sub_norm = nullptr;
 };
 
+// Device bytes a session of these tensors would allocate (see Session's constructor).
+brisk_hip_memory estimate_session(const brisk_hip_config& cfg, const brisk_hip_tensor* tensors, size_t n, size_t max_context);
+
 class Session {
 public:
+    static constexpr int kPrefillTokens = 512;  // batched prefill: buffers for this many tokens, allocated on first use
     Session(const brisk_hip_config& cfg, const brisk_hip_tensor* tensors, size_t n, size_t max_context, int device);
     ~Session();
     Session(const Session&) = delete;
@@ -116,8 +120,6 @@ private:
     unsigned long long* trace_ = nullptr;
     static constexpr size_t kTraceSlots = 1 << 20;
     bool debug_ = false;
-    // batched prefill (int8 MFMA), buffers for kPrefillTokens tokens, allocated on first use
-    static constexpr int kPrefillTokens = 512;
     bool prefill_on_ = true;
     bool prefill_mfma_ = false;    // BRISK_HIP_PREFILL_ATTN=mfma
     bool prefill_legacy_ = false;  // BRISK_HIP_PREFILL_ATTN=staged

@@ -74,6 +74,14 @@ typedef struct {
 
 typedef struct brisk_hip_session brisk_hip_session;
 
+/* Device bytes a session takes, by part (MemoryEstimate, src/memory.h:13-20). */
+typedef struct {
+    size_t weights;  /* the repacked matrices and the norm vectors */
+    size_t cache;    /* the fp16 K/V caches for the context */
+    size_t scratch;  /* activations, hand-off words, attention partials, RoPE table, prefill buffers, logits */
+    size_t total;
+} brisk_hip_memory;
+
 const char* brisk_hip_last_error(void);
 int brisk_hip_abi_version(void);
 int brisk_hip_device_count(int* count);
@@ -136,9 +144,24 @@ int brisk_hip_mfma_rate(int shape, double* int8_tops);
 
 /* ---------------------------------------------------------------- session level */
 
+/* What a session of these tensors and context would take on the device
+ * (estimate_memory, src/memory.cpp:46-96, for HBM instead of host RAM):
+ * computed from the shapes alone, nothing is allocated.  max_context as for
+ * brisk_hip_session_create. */
+int brisk_hip_session_estimate(const brisk_hip_config* config, const brisk_hip_tensor* tensors, size_t n_tensors,
+                               size_t max_context, brisk_hip_memory* out);
+
+/* Free and total device memory of `device` (available_memory,
+ * src/memory.cpp:98-116, for HBM). */
+int brisk_hip_device_memory(int device, size_t* free_bytes, size_t* total_bytes);
+
 /* Engine construction, as `MetalSession(model, file bytes, max_context)`
  * (src/main.cpp:206): copies and repacks every tensor to the GPU `device`.
- * max_context 0 = the model's context length; otherwise min of both. */
+ * max_context 0 = the model's context length; otherwise min of both.
+ * Before allocating, the estimate (plus a 256 MB margin) is checked against
+ * the device's free memory, as check_memory (src/memory.cpp:118-135) does for
+ * RAM: BRISK_HIP_ENOMEM with a message naming the shortfall, unless
+ * BRISK_NO_MEMORY_CHECK is set. */
 int brisk_hip_session_create(const brisk_hip_config* config, const brisk_hip_tensor* tensors, size_t n_tensors,
                              size_t max_context, int device, brisk_hip_session** out);
 void brisk_hip_session_destroy(brisk_hip_session* s);

@@ -96,3 +96,22 @@ def test_errors(pair):
     s.rollback(0)
     with pytest.raises(BriskHipError, match="context length exceeded"):
         s.eval(np.zeros(257, np.int32))
+
+
+def test_memory_preflight():
+    """check_memory (src/memory.cpp:118-135) for HBM: a session whose estimate exceeds the free device
+    memory fails before allocating, naming the shortfall; BRISK_NO_MEMORY_CHECK is the reference's override."""
+    import dataclasses
+    from brisk_hip.session import device_memory, estimate
+    free, total = device_memory(0)
+    assert 0 < free <= total
+    f, cfg, table = model.load(synth.model_path("tiny-qwen3"))
+    huge = dataclasses.replace(cfg, context=1 << 31)  # a 2G-token context: terabytes of cache
+    need = estimate((f, huge, table), 0)
+    assert need["total"] > total
+    with pytest.raises(BriskHipError, match="needs about .* cache, .* of device memory is free. Try "):
+        HipSession((f, huge, table), max_context=0)
+    # the estimate of a real session fits, and the session works
+    assert estimate((f, cfg, table), 256)["total"] < free
+    with HipSession((f, cfg, table), max_context=256) as s:
+        assert s.eval_greedy(synth.prompt_ids(4, cfg.vocab)) >= 0

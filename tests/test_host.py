@@ -105,3 +105,23 @@ def test_model_config_parse(name):
     names = {t.name for t in table}
     assert "token_embd.weight" in names and "blk.0.ffn_down.weight" in names
     assert ("output.weight" in names) == (spec.out_fmt is not None)
+
+
+@pytest.mark.parametrize("name", ["tiny-qwen3", "tiny-llama", "tiny-bitnet"])
+def test_session_estimate(name):
+    """brisk_hip_session_estimate (HBM counterpart of estimate_memory, src/memory.cpp:46-96): shapes only, no GPU."""
+    from brisk_hip.session import estimate
+    import brisk_hip
+    lib = brisk_hip.load()
+    f, cfg, table = model.load(synth.model_path(name))
+    e1, e2 = estimate((f, cfg, table), 256), estimate((f, cfg, table), 512)
+    kvd = cfg.kv_heads * cfg.head_dim
+    assert e1["cache"] == 2 * cfg.layers * kvd * 256 * 2  # fp16 K and V for every position
+    assert e2["cache"] == 2 * e1["cache"]
+    packed = sum(lib.brisk_hip_packed_bytes(t.type, t.rows, t.cols) for t in table if t.type != 0)
+    vectors = sum(t.rows * t.cols * 4 for t in table if t.type == 0)
+    assert e1["weights"] == packed + vectors
+    assert e1["total"] == e1["weights"] + e1["cache"] + e1["scratch"]
+    assert e2["scratch"] > e1["scratch"]  # the RoPE table and sequence grow with the context
+    # max_context 0 is the model's own context length, and larger values are capped there
+    assert estimate((f, cfg, table), 0) == estimate((f, cfg, table), 10 * cfg.context)
