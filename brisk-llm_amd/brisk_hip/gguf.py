@@ -28,10 +28,11 @@ _SCALAR = {U8: "<B", I8: "<b", U16: "<H", I16: "<h", U32: "<I", I32: "<i", F32: 
 # Tensor types (ggml numbering, src/gguf.h:22-27) and their (elements, bytes) per block
 # (src/gguf.cpp:135-161).
 T_F32, T_F16, T_Q4_0, T_Q8_0, T_Q4_K, T_Q6_K, T_TQ2_0, T_BF16 = 0, 1, 2, 8, 12, 14, 35, 30
-BLOCK = {T_F32: (1, 4), T_F16: (1, 2), T_BF16: (1, 2), T_Q4_0: (32, 18), T_Q8_0: (32, 34),
-         T_Q4_K: (256, 144), T_Q6_K: (256, 210), T_TQ2_0: (256, 66)}
-TYPE_NAMES = {T_F32: "F32", T_F16: "F16", T_BF16: "BF16", T_Q4_0: "Q4_0", T_Q8_0: "Q8_0",
-              T_Q4_K: "Q4_K", T_Q6_K: "Q6_K", T_TQ2_0: "TQ2_0"}
+T_Q4_1, T_Q5_0, T_Q5_K = 3, 6, 13
+BLOCK = {T_F32: (1, 4), T_F16: (1, 2), T_BF16: (1, 2), T_Q4_0: (32, 18), T_Q4_1: (32, 20), T_Q5_0: (32, 22),
+         T_Q8_0: (32, 34), T_Q4_K: (256, 144), T_Q5_K: (256, 176), T_Q6_K: (256, 210), T_TQ2_0: (256, 66)}
+TYPE_NAMES = {T_F32: "F32", T_F16: "F16", T_BF16: "BF16", T_Q4_0: "Q4_0", T_Q4_1: "Q4_1", T_Q5_0: "Q5_0",
+              T_Q8_0: "Q8_0", T_Q4_K: "Q4_K", T_Q5_K: "Q5_K", T_Q6_K: "Q6_K", T_TQ2_0: "TQ2_0"}
 
 
 class GgufError(RuntimeError):

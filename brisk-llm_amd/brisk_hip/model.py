@@ -15,7 +15,7 @@ from . import gguf as G
 
 ARCH_QWEN3, ARCH_LLAMA, ARCH_BITNET = 0, 1, 2
 _ARCH = {"qwen3": ARCH_QWEN3, "llama": ARCH_LLAMA, "bitnet": ARCH_BITNET, "bitnet-b1.58": ARCH_BITNET}
-QUANT_TYPES = (G.T_Q4_0, G.T_Q8_0, G.T_Q4_K, G.T_Q6_K, G.T_TQ2_0)
+QUANT_TYPES = (G.T_Q4_0, G.T_Q4_1, G.T_Q5_0, G.T_Q8_0, G.T_Q4_K, G.T_Q5_K, G.T_Q6_K, G.T_TQ2_0)
 
 
 class ModelError(RuntimeError):

@@ -121,8 +121,35 @@ def tq2_0_blocks(seed: int, nblocks: int) -> np.ndarray:
     return out
 
 
+def q4_1_blocks(seed: int, nblocks: int) -> np.ndarray:
+    """{d, m, qs[16]}: d ~ U(0.001, 0.02), m ~ U(-0.15, 0) so that q d + m centres near zero."""
+    out = np.empty((nblocks, 20), np.uint8)
+    out[:, 0:2] = half_bits(random_uniform(seed, nblocks, 0.001, 0.02)).view(np.uint8).reshape(nblocks, 2)
+    out[:, 2:4] = half_bits(random_uniform(seed ^ 0x2, nblocks, -0.15, 0.0)).view(np.uint8).reshape(nblocks, 2)
+    out[:, 4:20] = random_bytes(seed ^ 0x5757, nblocks * 16).reshape(nblocks, 16)
+    return out
+
+
+def q5_0_blocks(seed: int, nblocks: int) -> np.ndarray:
+    """{d, qh[4], qs[16]}: d ~ U(0.001, 0.02), the 5-bit values uniform."""
+    out = np.empty((nblocks, 22), np.uint8)
+    out[:, 0:2] = half_bits(random_uniform(seed, nblocks, 0.001, 0.02)).view(np.uint8).reshape(nblocks, 2)
+    out[:, 2:22] = random_bytes(seed ^ 0x5858, nblocks * 20).reshape(nblocks, 20)
+    return out
+
+
+def q5_k_blocks(seed: int, nblocks: int) -> np.ndarray:
+    """{d, dmin, scales[12], qh[32], qs[128]}: d, dmin ~ U(0.0001, 0.001), scales and values uniform."""
+    out = np.empty((nblocks, 176), np.uint8)
+    out[:, 0:2] = half_bits(random_uniform(seed, nblocks, 0.0001, 0.001)).view(np.uint8).reshape(nblocks, 2)
+    out[:, 2:4] = half_bits(random_uniform(seed ^ 0x1, nblocks, 0.0001, 0.001)).view(np.uint8).reshape(nblocks, 2)
+    out[:, 4:176] = random_bytes(seed ^ 0x5959, nblocks * 172).reshape(nblocks, 172)
+    return out
+
+
 BLOCK_MAKERS = {G.T_Q4_0: q4_0_blocks, G.T_Q8_0: q8_0_blocks, G.T_Q4_K: q4_k_blocks,
-                G.T_Q6_K: q6_k_blocks, G.T_TQ2_0: tq2_0_blocks}
+                G.T_Q6_K: q6_k_blocks, G.T_TQ2_0: tq2_0_blocks,
+                G.T_Q4_1: q4_1_blocks, G.T_Q5_0: q5_0_blocks, G.T_Q5_K: q5_k_blocks}
 
 
 # --------------------------------------------------------------------------- models
@@ -203,6 +230,11 @@ SPECS = {
     "tiny-q8": ModelSpec("tiny-q8", "qwen3", 256, 2, 4, 2, 64, 512, 1000, 1e6, context=1024, fmt=_uniform4(G.T_Q8_0)),
     "tiny-bitnet": ModelSpec("tiny-bitnet", "bitnet-b1.58", 512, 2, 4, 1, 128, 768, 1000, 5e5, eps=1e-5, context=1024,
                              fmt=_uniform4(G.T_TQ2_0), embd_fmt=G.T_Q4_0, out_fmt=None),
+    # The loader's other formats (a Q5_K_M mix; Q5_0 with Q4_1), on the path's families.
+    "tiny-q5k": ModelSpec("tiny-q5k", "llama", 512, 2, 8, 2, 64, 768, 1000, 5e5, eps=1e-5, context=1024,
+                          fmt={**_uniform4(G.T_Q5_K), "v": G.T_Q6_K, "down": G.T_Q6_K}, embd_fmt=G.T_Q6_K, out_fmt=None),
+    "tiny-q5": ModelSpec("tiny-q5", "qwen3", 256, 2, 4, 2, 64, 512, 1000, 1e6, context=1024,
+                         fmt={**_uniform4(G.T_Q5_0), "o": G.T_Q4_1, "down": G.T_Q4_1}),
 }
 
 

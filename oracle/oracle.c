@@ -157,6 +157,47 @@ static float dot_q8_0(const uint8_t* w, const uint8_t* x, size_t blocks) {
     return sum;
 }
 
+/* src/quant.cpp:484-498.  Q4_1 = {u16 d, u16 m, u8 qs[16]}: weight = q d + m; the x block sum
+ * enters as m (dx xsum). */
+static float dot_q4_1(const uint8_t* w, const uint8_t* x, size_t blocks) {
+    float sum = 0.0f;
+    for (size_t b = 0; b < blocks; ++b) {
+        const uint8_t* wb = w + b * 20;
+        const uint8_t* xb = x + b * 34;
+        const int8_t* xq = (const int8_t*)(xb + 2);
+        int32_t acc = 0, xsum = 0;
+        for (int i = 0; i < 16; ++i) {
+            acc += (wb[4 + i] & 0x0F) * xq[i];
+            acc += (wb[4 + i] >> 4) * xq[i + 16];
+            xsum += xq[i] + xq[i + 16];
+        }
+        const float dx = or_half_to_float(rd16(xb));
+        sum += (float)acc * or_half_to_float(rd16(wb)) * dx + or_half_to_float(rd16(wb + 2)) * (dx * (float)xsum);
+    }
+    return sum;
+}
+
+/* src/quant.cpp:458-472.  Q5_0 = {u16 d, u8 qh[4], u8 qs[16]}: the fifth bit of element e is
+ * bit e of qh (little-endian word); weight = (q - 16) d. */
+static float dot_q5_0(const uint8_t* w, const uint8_t* x, size_t blocks) {
+    float sum = 0.0f;
+    for (size_t b = 0; b < blocks; ++b) {
+        const uint8_t* wb = w + b * 22;
+        const uint8_t* xb = x + b * 34;
+        const int8_t* xq = (const int8_t*)(xb + 2);
+        uint32_t qh;
+        memcpy(&qh, wb + 2, 4);
+        int32_t acc = 0;
+        for (int i = 0; i < 16; ++i) {
+            const int lo = ((wb[6 + i] & 0x0F) | (int)(((qh >> i) & 1) << 4)) - 16;
+            const int hi = ((wb[6 + i] >> 4) | (int)(((qh >> (i + 16)) & 1) << 4)) - 16;
+            acc += lo * xq[i] + hi * xq[i + 16];
+        }
+        sum += (float)acc * or_half_to_float(rd16(wb)) * or_half_to_float(rd16(xb));
+    }
+    return sum;
+}
+
 /* src/quant.h:256-264 */
 static void q4_k_scale_min(const uint8_t* scales, int j, uint8_t* scale, uint8_t* min) {
     if (j < 4) {
@@ -194,6 +235,35 @@ static float dot_q4_k(const uint8_t* w, const uint8_t* x, size_t blocks) {
             const int8_t* xq = xqs + sb * 32;
             int32_t dot = 0;
             for (int i = 0; i < 32; ++i) dot += ((sb % 2 == 0) ? (q[i] & 0xF) : (q[i] >> 4)) * xq[i];
+            weighted += scale * dot;
+            offsets += min * (q8k_bsum(xb, 2 * sb) + q8k_bsum(xb, 2 * sb + 1));
+        }
+        sum += q8k_d(xb) * (or_half_to_float(rd16(wb)) * (float)weighted - or_half_to_float(rd16(wb + 2)) * (float)offsets);
+    }
+    return sum;
+}
+
+/* src/quant.cpp:523-547.  Q5_K = {u16 d, u16 dmin, u8 scales[12], u8 qh[32], u8 qs[128]}: Q4_K
+ * with a fifth bit, bit sb of qh[i] for element i of sub-block sb. */
+static float dot_q5_k(const uint8_t* w, const uint8_t* x, size_t blocks) {
+    float sum = 0.0f;
+    for (size_t b = 0; b < blocks; ++b) {
+        const uint8_t* wb = w + b * 176;
+        const uint8_t* xb = x + b * 292;
+        const int8_t* xqs = (const int8_t*)(xb + 4);
+        const uint8_t* qh = wb + 16;
+        int32_t weighted = 0, offsets = 0;
+        for (int sb = 0; sb < 8; ++sb) {
+            uint8_t scale, min;
+            q4_k_scale_min(wb + 4, sb, &scale, &min);
+            const uint8_t* q = wb + 48 + (sb / 2) * 32;
+            const uint8_t bit = (uint8_t)(1u << sb);
+            const int8_t* xq = xqs + sb * 32;
+            int32_t dot = 0;
+            for (int i = 0; i < 32; ++i) {
+                const int v = ((sb % 2 == 0) ? (q[i] & 0xF) : (q[i] >> 4)) | ((qh[i] & bit) ? 16 : 0);
+                dot += v * xq[i];
+            }
             weighted += scale * dot;
             offsets += min * (q8k_bsum(xb, 2 * sb) + q8k_bsum(xb, 2 * sb + 1));
         }
@@ -281,7 +351,10 @@ float or_dot(int type, int lut16, const void* w, const void* x, size_t blocks) {
     switch (type) {
         case OR_Q4_0: return dot_q4_0((const uint8_t*)w, (const uint8_t*)x, blocks);
         case OR_Q8_0: return dot_q8_0((const uint8_t*)w, (const uint8_t*)x, blocks);
+        case OR_Q4_1: return dot_q4_1((const uint8_t*)w, (const uint8_t*)x, blocks);
+        case OR_Q5_0: return dot_q5_0((const uint8_t*)w, (const uint8_t*)x, blocks);
         case OR_Q4_K: return dot_q4_k((const uint8_t*)w, (const uint8_t*)x, blocks);
+        case OR_Q5_K: return dot_q5_k((const uint8_t*)w, (const uint8_t*)x, blocks);
         case OR_Q6_K: return dot_q6_k((const uint8_t*)w, (const uint8_t*)x, blocks);
         case OR_TQ2_0: return lut16 ? dot_tq2_0x16((const uint8_t*)w, (const uint8_t*)x, blocks)
                                     : dot_tq2_0((const uint8_t*)w, (const uint8_t*)x, blocks);
@@ -289,12 +362,17 @@ float or_dot(int type, int lut16, const void* w, const void* x, size_t blocks) {
     return NAN;
 }
 
-static size_t block_elems(int type) { return (type == OR_Q4_0 || type == OR_Q8_0) ? 32 : 256; }
+static size_t block_elems(int type) {
+    return (type == OR_Q4_0 || type == OR_Q8_0 || type == OR_Q4_1 || type == OR_Q5_0) ? 32 : 256;
+}
 static size_t block_bytes(int type) {
     switch (type) {
         case OR_Q4_0: return 18;
+        case OR_Q4_1: return 20;
+        case OR_Q5_0: return 22;
         case OR_Q8_0: return 34;
         case OR_Q4_K: return 144;
+        case OR_Q5_K: return 176;
         case OR_Q6_K: return 210;
         case OR_TQ2_0: return 66;
     }
@@ -304,7 +382,7 @@ static size_t block_bytes(int type) {
 /* src/model.cpp:496-503 + src/quant.cpp:144: on x86, TQ2_0 matrices with rows % 16 == 0 are
  * repacked to TQ2_0x16, whose kernels take 7-bit activations. */
 int or_activation_bits(int type, size_t rows) { return (type == OR_TQ2_0 && rows % 16 == 0) ? 7 : 8; }
-static int takes_q8_k(int type) { return type == OR_Q4_K || type == OR_Q6_K || type == OR_TQ2_0; }
+static int takes_q8_k(int type) { return type == OR_Q4_K || type == OR_Q5_K || type == OR_Q6_K || type == OR_TQ2_0; }
 
 /* matvec_generic (src/kernels.cpp:13-19) */
 void or_matvec(int type, const void* w, size_t rows, size_t cols, const void* x, float* out) {
@@ -332,6 +410,44 @@ void or_dequantize(int type, const void* blocks_, float* out, size_t count) {
             case OR_Q8_0: {
                 const float d = or_half_to_float(rd16(wb));
                 for (int i = 0; i < 32; ++i) y[i] = (float)((const int8_t*)(wb + 2))[i] * d;
+                break;
+            }
+            case OR_Q4_1: {  /* src/quant.cpp:207-217 */
+                const float d = or_half_to_float(rd16(wb)), m = or_half_to_float(rd16(wb + 2));
+                for (int i = 0; i < 16; ++i) {
+                    y[i] = (float)(wb[4 + i] & 0x0F) * d + m;
+                    y[i + 16] = (float)(wb[4 + i] >> 4) * d + m;
+                }
+                break;
+            }
+            case OR_Q5_0: {  /* src/quant.cpp:219-232 */
+                const float d = or_half_to_float(rd16(wb));
+                uint32_t qh;
+                memcpy(&qh, wb + 2, 4);
+                for (int i = 0; i < 16; ++i) {
+                    const int lo = (wb[6 + i] & 0x0F) | (int)(((qh >> i) & 1) << 4);
+                    const int hi = (wb[6 + i] >> 4) | (int)(((qh >> (i + 16)) & 1) << 4);
+                    y[i] = (float)(lo - 16) * d;
+                    y[i + 16] = (float)(hi - 16) * d;
+                }
+                break;
+            }
+            case OR_Q5_K: {  /* src/quant.cpp:263-283 */
+                const float d = or_half_to_float(rd16(wb)), dmin = or_half_to_float(rd16(wb + 2));
+                const uint8_t* qh = wb + 16;
+                for (int chunk = 0; chunk < 4; ++chunk) {
+                    uint8_t scale, min;
+                    q4_k_scale_min(wb + 4, 2 * chunk, &scale, &min);
+                    const float d1 = d * scale, m1 = dmin * min;
+                    q4_k_scale_min(wb + 4, 2 * chunk + 1, &scale, &min);
+                    const float d2 = d * scale, m2 = dmin * min;
+                    const uint8_t* q = wb + 48 + chunk * 32;
+                    const uint8_t lo_bit = (uint8_t)(1u << (2 * chunk)), hi_bit = (uint8_t)(lo_bit << 1);
+                    for (int i = 0; i < 32; ++i) {
+                        y[chunk * 64 + i] = d1 * (float)((q[i] & 0xF) | ((qh[i] & lo_bit) ? 16 : 0)) - m1;
+                        y[chunk * 64 + 32 + i] = d2 * (float)((q[i] >> 4) | ((qh[i] & hi_bit) ? 16 : 0)) - m2;
+                    }
+                }
                 break;
             }
             case OR_Q4_K: {

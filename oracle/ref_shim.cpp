@@ -150,8 +150,11 @@ void ref_quantize_q8_k(const float* x, void* out, size_t count, int bits) {
 static brisk::WeightFormat format_of(int type) {
     switch (type) {
         case 2: return brisk::WeightFormat::Q4_0;
+        case 3: return brisk::WeightFormat::Q4_1;
+        case 6: return brisk::WeightFormat::Q5_0;
         case 8: return brisk::WeightFormat::Q8_0;
         case 12: return brisk::WeightFormat::Q4_K;
+        case 13: return brisk::WeightFormat::Q5_K;
         case 14: return brisk::WeightFormat::Q6_K;
         case 35: return brisk::WeightFormat::TQ2_0;
         case 1016: return brisk::WeightFormat::TQ2_0x16;
@@ -178,6 +181,9 @@ int ref_dequantize(int type, const void* blocks, float* out, size_t count) {
         switch (format_of(type)) {
             case brisk::WeightFormat::Q4_0: brisk::dequantize_q4_0(static_cast<const brisk::BlockQ4_0*>(blocks), out, count); break;
             case brisk::WeightFormat::Q8_0: brisk::dequantize_q8_0(static_cast<const brisk::BlockQ8_0*>(blocks), out, count); break;
+            case brisk::WeightFormat::Q4_1: brisk::dequantize_q4_1(static_cast<const brisk::BlockQ4_1*>(blocks), out, count); break;
+            case brisk::WeightFormat::Q5_0: brisk::dequantize_q5_0(static_cast<const brisk::BlockQ5_0*>(blocks), out, count); break;
+            case brisk::WeightFormat::Q5_K: brisk::dequantize_q5_k(static_cast<const brisk::BlockQ5_K*>(blocks), out, count); break;
             case brisk::WeightFormat::Q4_K: brisk::dequantize_q4_k(static_cast<const brisk::BlockQ4_K*>(blocks), out, count); break;
             case brisk::WeightFormat::Q6_K: brisk::dequantize_q6_k(static_cast<const brisk::BlockQ6_K*>(blocks), out, count); break;
             case brisk::WeightFormat::TQ2_0: brisk::dequantize_tq2_0(static_cast<const brisk::BlockTQ2_0*>(blocks), out, count); break;

@@ -30,6 +30,8 @@ RUNS = {
     "tiny-llama": (12, 48),
     "tiny-q8": (12, 48),
     "tiny-bitnet": (12, 48),
+    "tiny-q5k": (12, 48),
+    "tiny-q5": (12, 48),
 }
 
 

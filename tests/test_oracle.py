@@ -24,8 +24,10 @@ from brisk_hip import gguf as G, model, synth
 HERE = os.path.dirname(os.path.abspath(__file__))
 needs_ref = pytest.mark.skipif(not pyoracle.ref_available(), reason="oracle/_ref is not built (no /root/reference)")
 
-TYPES = (G.T_Q4_0, G.T_Q8_0, G.T_Q4_K, G.T_Q6_K, G.T_TQ2_0)
-QK_BYTES = {G.T_Q4_0: 18, G.T_Q8_0: 34, G.T_Q4_K: 144, G.T_Q6_K: 210, G.T_TQ2_0: 66}
+TYPES = (G.T_Q4_0, G.T_Q8_0, G.T_Q4_K, G.T_Q6_K, G.T_TQ2_0, G.T_Q4_1, G.T_Q5_0, G.T_Q5_K)
+QK_BYTES = {G.T_Q4_0: 18, G.T_Q8_0: 34, G.T_Q4_K: 144, G.T_Q6_K: 210, G.T_TQ2_0: 66, G.T_Q4_1: 20, G.T_Q5_0: 22,
+            G.T_Q5_K: 176}
+SMALL = (G.T_Q4_0, G.T_Q8_0, G.T_Q4_1, G.T_Q5_0)  # 32-value blocks, Q8_0 activations
 
 
 @pytest.fixture(scope="module")
@@ -38,13 +40,13 @@ def rng_normal(seed, n):
 
 
 def q8_bytes(t):
-    return 34 if t in (G.T_Q4_0, G.T_Q8_0) else 292
+    return 34 if t in SMALL else 292
 
 
 def quantize(L, t, x, bits=8):
-    blocks = len(x) // (32 if t in (G.T_Q4_0, G.T_Q8_0) else 256)
+    blocks = len(x) // (32 if t in SMALL else 256)
     out = np.zeros(blocks * q8_bytes(t), np.uint8)
-    if t in (G.T_Q4_0, G.T_Q8_0):
+    if t in SMALL:
         L.or_quantize_q8_0(ptr(x), ptr(out), len(x))
     else:
         L.or_quantize_q8_k(ptr(x), ptr(out), len(x), bits)
@@ -154,7 +156,7 @@ def test_quantize_matches_reference(L, bits):
 # --------------------------------------------------------------------------- weights: dequant, dots
 
 def weights(t, rows, cols, seed):
-    be = 32 if t in (G.T_Q4_0, G.T_Q8_0) else 256
+    be = 32 if t in SMALL else 256
     return synth.BLOCK_MAKERS[t](seed, rows * cols // be).reshape(-1)
 
 
@@ -175,6 +177,25 @@ def test_dequantize_q4_0_and_q8_0_closed_form(L):
     d = w[:, 0:2].copy().view(np.float16).astype(np.float32)
     vals = w[:, 2:].view(np.int8).astype(np.float32)
     assert np.array_equal(dequant(L, G.T_Q8_0, w.reshape(-1), 256), (vals * d).reshape(-1))
+
+
+def test_dequantize_q4_1_and_q5_0_closed_form(L):
+    """Q4_1: q d + m; Q5_0: (nibble | fifth bit << 4) - 16, times d, the fifth bit of element e
+    at bit e of qh (src/quant.cpp:207-232)."""
+    w = weights(G.T_Q4_1, 4, 64, 11).reshape(-1, 20)
+    d = w[:, 0:2].copy().view(np.float16).astype(np.float32)
+    m = w[:, 2:4].copy().view(np.float16).astype(np.float32)
+    qs = w[:, 4:]
+    q = np.concatenate([(qs & 0xF), (qs >> 4)], axis=1).astype(np.float32)
+    assert np.array_equal(dequant(L, G.T_Q4_1, w.reshape(-1), 256), (q * d + m).astype(np.float32).reshape(-1))
+    w = weights(G.T_Q5_0, 4, 64, 12).reshape(-1, 22)
+    d = w[:, 0:2].copy().view(np.float16).astype(np.float32)
+    qh = w[:, 2:6].copy().view(np.uint32).astype(np.int64)
+    qs = w[:, 6:].astype(np.int64)
+    e = np.arange(32)
+    nib = np.concatenate([qs & 0xF, qs >> 4], axis=1)
+    q = nib | (((qh >> e) & 1) << 4)
+    assert np.array_equal(dequant(L, G.T_Q5_0, w.reshape(-1), 256), ((q - 16).astype(np.float32) * d).reshape(-1))
 
 
 def test_dequantize_tq2_0_is_ternary(L):
@@ -198,7 +219,7 @@ def test_dequantize_matches_reference(L, t):
 def int_block_dots(L, t, w, xq, cols):
     """Brute force: per block, the exact integer sum of (weight integer) x (activation integer),
     both recovered from dequantisation (weights) or the raw bytes (activations)."""
-    if t in (G.T_Q4_0, G.T_Q8_0):
+    if t in (G.T_Q4_0, G.T_Q8_0, G.T_Q5_0):
         nb = cols // 32
         wb = w.reshape(nb, -1)
         wd = wb[:, 0:2].copy().view(np.float16).astype(np.float32)
@@ -210,7 +231,7 @@ def int_block_dots(L, t, w, xq, cols):
     return None
 
 
-@pytest.mark.parametrize("t", [G.T_Q4_0, G.T_Q8_0])
+@pytest.mark.parametrize("t", [G.T_Q4_0, G.T_Q8_0, G.T_Q5_0])
 def test_block_dot_equals_brute_force(L, t):
     """or_dot = sequential fp32 sum of float(int block dot) * d_w * d_x (src/quant.cpp:445-482)."""
     cols = 1024
@@ -247,7 +268,8 @@ def test_matvec_within_reference_tolerance(L, t):
 
 @needs_ref
 @pytest.mark.parametrize("t,rows", [(G.T_Q4_0, 37), (G.T_Q8_0, 37), (G.T_Q4_K, 37), (G.T_Q6_K, 37),
-                                    (G.T_TQ2_0, 37), (G.T_TQ2_0, 48)])
+                                    (G.T_TQ2_0, 37), (G.T_TQ2_0, 48), (G.T_Q4_1, 37), (G.T_Q5_0, 37),
+                                    (G.T_Q5_K, 37)])
 def test_matvec_matches_reference_bitwise(L, t, rows):
     R = pyoracle.ref_lib()
     cols = 2048
@@ -367,7 +389,7 @@ def tiny(name):
     return path, f, cfg, table
 
 
-@pytest.mark.parametrize("name", ["tiny-qwen3", "tiny-llama", "tiny-q8", "tiny-bitnet"])
+@pytest.mark.parametrize("name", ["tiny-qwen3", "tiny-llama", "tiny-q8", "tiny-bitnet", "tiny-q5k", "tiny-q5"])
 def test_oracle_greedy_matches_reference_fixture(name):
     """tests/golden/<name>_greedy.json were written by the reference engine itself."""
     with open(os.path.join(HERE, "golden", f"{name}_greedy.json")) as fh:
@@ -396,7 +418,7 @@ def test_oracle_first_tokens_of_qwen3_0_6b_fixture():
 
 
 @needs_ref
-@pytest.mark.parametrize("name", ["tiny-qwen3", "tiny-llama", "tiny-bitnet"])
+@pytest.mark.parametrize("name", ["tiny-qwen3", "tiny-llama", "tiny-bitnet", "tiny-q5k", "tiny-q5"])
 def test_oracle_session_matches_reference_bitwise(name):
     """eval, eval_all and rollback of the restatement against the reference's Session."""
     path, f, cfg, table = tiny(name)
