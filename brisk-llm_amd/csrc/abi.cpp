@@ -42,8 +42,8 @@ void hip_check(hipError_t e, const char* what) {
 }
 
 bool known_type(int type) {
-    return type == BRISK_HIP_Q4_0 || type == BRISK_HIP_Q8_0 || type == BRISK_HIP_Q4_K || type == BRISK_HIP_Q6_K ||
-           type == BRISK_HIP_TQ2_0;
+    return type == BRISK_HIP_Q4_0 || type == BRISK_HIP_Q4_1 || type == BRISK_HIP_Q5_0 || type == BRISK_HIP_Q8_0 ||
+           type == BRISK_HIP_Q4_K || type == BRISK_HIP_Q5_K || type == BRISK_HIP_Q6_K || type == BRISK_HIP_TQ2_0;
 }
 
 bh::Packed packed_view(int type, int flags, const void* packed, size_t rows, size_t cols) {
@@ -173,7 +173,7 @@ int brisk_hip_div_selftest(unsigned long long* mismatches) {
         hipError_t e = hipMemset(d, 0, 32);
         if (e == hipSuccess) e = bh::launch_div_selftest(d, nullptr);
         if (e == hipSuccess) e = hipMemcpy(mismatches, d, 32, hipMemcpyDeviceToHost);
-        hipFree(d);
+        (void)hipFree(d);
         hip_check(e, "div selftest");
     });
 }

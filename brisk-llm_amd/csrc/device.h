@@ -688,6 +688,67 @@ template <> struct Unit<kQ4_0> {
     }
 };
 
+// dot_q4_1_q8_0 block term (src/quant.cpp:445-456 with the offset, :207-217):
+// acc = sum(q x) over the unsigned nibbles, exact; term = (float)acc * d_w * d_x
+// + m * (d_x * (float)sum(x)), the block sum coming with the activation.
+template <> struct Unit<kQ4_1> {
+    static constexpr uint32_t kElems = 32;
+    static constexpr int kMaxPerThread = 16;
+    uint4 q;
+    uint32_t d, m;
+    __device__ __forceinline__ void load(const Packed& mat, size_t blk) {
+        q = ld16(mat.p0 + blk * 16);
+        d = reinterpret_cast<const uint16_t*>(mat.p1)[blk];
+        m = reinterpret_cast<const uint16_t*>(mat.p2)[blk];
+    }
+    __device__ __forceinline__ float term(uint32_t b, const ActLds& a) const {
+        const int32_t* x = a.xs + b * 8;
+        int acc = 0;
+        const uint32_t qw[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            acc = dot4(static_cast<int>(qw[j] & 0x0F0F0F0Fu), x[j], acc);
+            acc = dot4(static_cast<int>((qw[j] >> 4) & 0x0F0F0F0Fu), x[4 + j], acc);
+        }
+        const float dx = a.xd[b];
+        return static_cast<float>(acc) * h2f(static_cast<uint16_t>(d)) * dx +
+               h2f(static_cast<uint16_t>(m)) * (dx * static_cast<float>(a.xsum[b]));
+    }
+};
+
+// Four bits of `v` (from bit `sh`) to bit 4 of four bytes: the product places
+// bit k at bit 8k (the shifted copies 7k apart never overlap, so no carries).
+__device__ __forceinline__ uint32_t spread4_hi(uint32_t v, int sh) {
+    return (((v >> sh) & 0xFu) * 0x00204081u & 0x01010101u) << 4;
+}
+
+// dot_q5_0_q8_0 block term (src/quant.cpp:458-472): value e = (nibble | bit e of
+// qh << 4) - 16; acc = sum(value x) = sum(q x) - 16 sum(x), exact; term =
+// (float)acc * d_w * d_x.
+template <> struct Unit<kQ5_0> {
+    static constexpr uint32_t kElems = 32;
+    static constexpr int kMaxPerThread = 16;
+    uint4 q;
+    uint32_t d, qh;
+    __device__ __forceinline__ void load(const Packed& m, size_t blk) {
+        q = ld16(m.p0 + blk * 16);
+        d = reinterpret_cast<const uint16_t*>(m.p1)[blk];
+        qh = reinterpret_cast<const uint32_t*>(m.p2)[blk];
+    }
+    __device__ __forceinline__ float term(uint32_t b, const ActLds& a) const {
+        const int32_t* x = a.xs + b * 8;
+        int acc = 0;
+        const uint32_t qw[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            acc = dot4(static_cast<int>((qw[j] & 0x0F0F0F0Fu) | spread4_hi(qh, 4 * j)), x[j], acc);
+            acc = dot4(static_cast<int>(((qw[j] >> 4) & 0x0F0F0F0Fu) | spread4_hi(qh, 16 + 4 * j)), x[4 + j], acc);
+        }
+        acc -= 16 * a.xsum[b];
+        return static_cast<float>(acc) * h2f(static_cast<uint16_t>(d)) * a.xd[b];
+    }
+};
+
 // dot_q8_0_q8_0 block term (src/quant.cpp:474-482).
 template <> struct Unit<kQ8_0> {
     static constexpr uint32_t kElems = 32;
@@ -745,6 +806,52 @@ template <> struct Unit<kQ4_K> {
             for (int j = 0; j < 8; ++j) {
                 lo = dot4(static_cast<int>(qw[j] & 0x0F0F0F0Fu), x[c * 16 + j], lo);
                 hi = dot4(static_cast<int>((qw[j] >> 4) & 0x0F0F0F0Fu), x[c * 16 + 8 + j], hi);
+            }
+            int s0, m0, s1, m1;
+            q4k_scale_min(mb + 4, 2 * c, s0, m0);
+            q4k_scale_min(mb + 4, 2 * c + 1, s1, m1);
+            weighted += s0 * lo + s1 * hi;
+            const int* bs = a.xsum + b * 16 + 4 * c;
+            offsets += m0 * (bs[0] + bs[1]) + m1 * (bs[2] + bs[3]);
+        }
+        const uint16_t d = static_cast<uint16_t>(meta.x & 0xFFFF), dmin = static_cast<uint16_t>(meta.x >> 16);
+        return a.xd[b] * (h2f(d) * static_cast<float>(weighted) - h2f(dmin) * static_cast<float>(offsets));
+    }
+};
+
+// dot_q5_k_q8_k super-block term (src/quant.cpp:523-547): Q4_K's with a fifth
+// bit, bit s of qh[i] for value i of sub-block s (values 0..31, still valid
+// signed bytes for sdot4); term = x.d * (d * weighted - dmin * offsets).
+template <> struct Unit<kQ5_K> {
+    static constexpr uint32_t kElems = 256;
+    static constexpr int kMaxPerThread = 4;
+    uint4 q[8];
+    uint4 meta;   // d, dmin, scales[12]
+    uint4 qh[2];  // qh[32]
+    __device__ __forceinline__ void load(const Packed& m, size_t blk) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) q[i] = ld16(m.p0 + blk * 128 + 16 * i);
+        meta = ld16(m.p1 + blk * 16);
+        qh[0] = ld16(m.p2 + blk * 48 + 16);
+        qh[1] = ld16(m.p2 + blk * 48 + 32);
+    }
+    __device__ __forceinline__ float term(uint32_t b, const ActLds& a) const {
+        const uint32_t mw[4] = {meta.x, meta.y, meta.z, meta.w};
+        const uint8_t* mb = reinterpret_cast<const uint8_t*>(mw);
+        const uint32_t hw[8] = {qh[0].x, qh[0].y, qh[0].z, qh[0].w, qh[1].x, qh[1].y, qh[1].z, qh[1].w};
+        const int32_t* x = a.xs + b * 64;
+        int weighted = 0, offsets = 0;
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {  // chunk c: 32 bytes, low nibbles = sub-block 2c, high = 2c+1
+            const uint32_t qw[8] = {q[2 * c].x, q[2 * c].y, q[2 * c].z, q[2 * c].w,
+                                    q[2 * c + 1].x, q[2 * c + 1].y, q[2 * c + 1].z, q[2 * c + 1].w};
+            int lo = 0, hi = 0;
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const uint32_t vl = (qw[j] & 0x0F0F0F0Fu) | (((hw[j] >> (2 * c)) & 0x01010101u) << 4);
+                const uint32_t vh = ((qw[j] >> 4) & 0x0F0F0F0Fu) | (((hw[j] >> (2 * c + 1)) & 0x01010101u) << 4);
+                lo = dot4(static_cast<int>(vl), x[c * 16 + j], lo);
+                hi = dot4(static_cast<int>(vh), x[c * 16 + 8 + j], hi);
             }
             int s0, m0, s1, m1;
             q4k_scale_min(mb + 4, 2 * c, s0, m0);

@@ -27,6 +27,20 @@ __global__ void k_pack(uint32_t type, const uint8_t* __restrict__ src, size_t bl
             for (int i = 0; i < 16; ++i) p0[b * 16 + i] = s[2 + i];
             break;
         }
+        case kQ4_1: {  // d, m, qs[16]
+            const uint8_t* s = src + b * 20;
+            p1[2 * b] = s[0]; p1[2 * b + 1] = s[1];
+            p2[2 * b] = s[2]; p2[2 * b + 1] = s[3];
+            for (int i = 0; i < 16; ++i) p0[b * 16 + i] = s[4 + i];
+            break;
+        }
+        case kQ5_0: {  // d, qh[4], qs[16]
+            const uint8_t* s = src + b * 22;
+            p1[2 * b] = s[0]; p1[2 * b + 1] = s[1];
+            for (int i = 0; i < 4; ++i) p2[b * 4 + i] = s[2 + i];
+            for (int i = 0; i < 16; ++i) p0[b * 16 + i] = s[6 + i];
+            break;
+        }
         case kQ8_0: {
             const uint8_t* s = src + b * 34;
             p1[2 * b] = s[0]; p1[2 * b + 1] = s[1];
@@ -43,6 +57,19 @@ __global__ void k_pack(uint32_t type, const uint8_t* __restrict__ src, size_t bl
                 p2[b * 16 + j] = static_cast<uint8_t>(sc);
                 p2[b * 16 + 8 + j] = static_cast<uint8_t>(mn);
             }
+            break;
+        }
+        case kQ5_K: {  // {d, dmin, scales[12]}, qh[32], qs[128]
+            const uint8_t* s = src + b * 176;
+            for (int i = 0; i < 16; ++i) p1[b * 16 + i] = s[i];
+            for (int i = 0; i < 128; ++i) p0[b * 128 + i] = s[48 + i];
+            for (int j = 0; j < 8; ++j) {
+                int sc, mn;
+                q4k_scale_min(s + 4, j, sc, mn);
+                p2[b * 48 + j] = static_cast<uint8_t>(sc);
+                p2[b * 48 + 8 + j] = static_cast<uint8_t>(mn);
+            }
+            for (int i = 0; i < 32; ++i) p2[b * 48 + 16 + i] = s[16 + i];
             break;
         }
         case kQ6_K: {  // ql[128], qh[64], scales[16], d
@@ -421,8 +448,11 @@ int pick_rows_per_tile(uint32_t type, size_t rows, size_t cols) {
     int max_per_thread = 0;
     switch (type) {
         case kQ4_0: max_per_thread = Unit<kQ4_0>::kMaxPerThread; break;
+        case kQ4_1: max_per_thread = Unit<kQ4_1>::kMaxPerThread; break;
+        case kQ5_0: max_per_thread = Unit<kQ5_0>::kMaxPerThread; break;
         case kQ8_0: max_per_thread = Unit<kQ8_0>::kMaxPerThread; break;
         case kQ4_K: max_per_thread = Unit<kQ4_K>::kMaxPerThread; break;
+        case kQ5_K: max_per_thread = Unit<kQ5_K>::kMaxPerThread; break;
         case kQ6_K: max_per_thread = Unit<kQ6_K>::kMaxPerThread; break;
         default: max_per_thread = Unit<kTQ2_0>::kMaxPerThread; break;
     }
@@ -439,8 +469,11 @@ int pick_rows_per_tile(uint32_t type, size_t rows, size_t cols) {
 #define BH_DISPATCH(type, K, ...)                                                           \
     switch (type) {                                                                        \
         case kQ4_0: hipLaunchKernelGGL(K<kQ4_0>, __VA_ARGS__); break;                       \
+        case kQ4_1: hipLaunchKernelGGL(K<kQ4_1>, __VA_ARGS__); break;                       \
+        case kQ5_0: hipLaunchKernelGGL(K<kQ5_0>, __VA_ARGS__); break;                       \
         case kQ8_0: hipLaunchKernelGGL(K<kQ8_0>, __VA_ARGS__); break;                       \
         case kQ4_K: hipLaunchKernelGGL(K<kQ4_K>, __VA_ARGS__); break;                       \
+        case kQ5_K: hipLaunchKernelGGL(K<kQ5_K>, __VA_ARGS__); break;                       \
         case kQ6_K: hipLaunchKernelGGL(K<kQ6_K>, __VA_ARGS__); break;                       \
         case kTQ2_0: hipLaunchKernelGGL(K<kTQ2_0>, __VA_ARGS__); break;                     \
         default: return hipErrorInvalidValue;                                              \

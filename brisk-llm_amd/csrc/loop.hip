@@ -187,7 +187,7 @@ __device__ __forceinline__ void embed_to_lds(const LoopArgs& g, int token, GemvL
 
 constexpr int kLoopUnits = 2;  // units per thread in the loop's tiles (the tile plan keeps to it)
 // ... in the output projection's tiles (fewer for the K-quant formats' larger units)
-__host__ __device__ constexpr int head_units(uint32_t type) { return (type == kQ4_K || type == kQ6_K) ? 2 : 4; }
+__host__ __device__ constexpr int head_units(uint32_t type) { return (type == kQ4_K || type == kQ5_K || type == kQ6_K) ? 2 : 4; }
 
 // The tiles t = blockIdx.x, + G, ... of a phase, streamed one ahead: a tile's
 // weights are requested before the phase's input has arrived and before the
@@ -722,7 +722,6 @@ __device__ __forceinline__ bool phase_b(const LoopArgs& g, const LayerDev& L, in
     const unsigned tin = tag_of(g, step, l, 1), tout = tag_of(g, step, l, 2);
     const AttnArgs a = attn_args(g, L, step, l);
     const TaggedOut o{g.attt, g.pacct, g.pmlt, tout, g.error, g.att_q8, g.heads * g.head_dim};
-    AttnLds& s = lds.att;
     if (attn_is_exact(Lc, hpk) && Lc <= kSplit * kPoolChunks && g.head_attn) {
         if (static_cast<int>(blockIdx.x) >= g.heads) return true;
         const int h = blockIdx.x;
@@ -1079,6 +1078,9 @@ const void* find_loop_kernel(uint32_t tq, uint32_t tv, uint32_t to, uint32_t tg,
     if (is(kQ8_0, kQ8_0, kQ8_0, kQ8_0, kQ8_0, kQ8_0)) return loop_kernel<kQ8_0, kQ8_0, kQ8_0, kQ8_0, kQ8_0, kQ8_0>();
     if (is(kQ4_K, kQ6_K, kQ4_K, kQ4_K, kQ6_K, kQ6_K)) return loop_kernel<kQ4_K, kQ6_K, kQ4_K, kQ4_K, kQ6_K, kQ6_K>();
     if (is(kTQ2_0, kTQ2_0, kTQ2_0, kTQ2_0, kTQ2_0, kQ4_0)) return loop_kernel<kTQ2_0, kTQ2_0, kTQ2_0, kTQ2_0, kTQ2_0, kQ4_0>();
+    // Q5_K_M (Q5_K with Q6_K for V, down and the output) and Q5_0 with Q4_1 on the O and down rows
+    if (is(kQ5_K, kQ6_K, kQ5_K, kQ5_K, kQ6_K, kQ6_K)) return loop_kernel<kQ5_K, kQ6_K, kQ5_K, kQ5_K, kQ6_K, kQ6_K>();
+    if (is(kQ5_0, kQ5_0, kQ4_1, kQ5_0, kQ4_1, kQ8_0)) return loop_kernel<kQ5_0, kQ5_0, kQ4_1, kQ5_0, kQ4_1, kQ8_0>();
     return nullptr;
 }
 

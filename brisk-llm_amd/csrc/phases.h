@@ -23,6 +23,35 @@ __device__ inline float dequant_elem(const Packed& m, uint32_t r, uint32_t e) {
             const uint8_t q = m.p0[blk * 16 + (i & 15)];
             return static_cast<float>((i < 16 ? (q & 0x0F) : (q >> 4)) - 8) * d;
         }
+        case kQ4_1: {  // q d + m (src/quant.cpp:207-217)
+            const size_t blk = static_cast<size_t>(r) * (cols / 32) + e / 32;
+            const float d = h2f(reinterpret_cast<const uint16_t*>(m.p1)[blk]);
+            const float mn = h2f(reinterpret_cast<const uint16_t*>(m.p2)[blk]);
+            const uint32_t i = e % 32;
+            const uint8_t q = m.p0[blk * 16 + (i & 15)];
+            return static_cast<float>(i < 16 ? (q & 0x0F) : (q >> 4)) * d + mn;
+        }
+        case kQ5_0: {  // ((nibble | bit e of qh << 4) - 16) d (src/quant.cpp:219-232)
+            const size_t blk = static_cast<size_t>(r) * (cols / 32) + e / 32;
+            const float d = h2f(reinterpret_cast<const uint16_t*>(m.p1)[blk]);
+            const uint32_t qh = reinterpret_cast<const uint32_t*>(m.p2)[blk];
+            const uint32_t i = e % 32;
+            const uint8_t q = m.p0[blk * 16 + (i & 15)];
+            const int v = (i < 16 ? (q & 0x0F) : (q >> 4)) | static_cast<int>(((qh >> i) & 1u) << 4);
+            return static_cast<float>(v - 16) * d;
+        }
+        case kQ5_K: {  // Q4_K's with bit s of qh[j] on value j of sub-block s (src/quant.cpp:263-283)
+            const size_t blk = static_cast<size_t>(r) * (cols / 256) + e / 256;
+            const uint8_t* meta = m.p1 + blk * 16;
+            const float d = h2f(static_cast<uint16_t>(meta[0] | (meta[1] << 8)));
+            const float dmin = h2f(static_cast<uint16_t>(meta[2] | (meta[3] << 8)));
+            const int i = e % 256, chunk = i / 64, hi = (i % 64) >= 32, j = i % 32, sb = 2 * chunk + hi;
+            const uint8_t* dec = m.p2 + blk * 48;
+            const float d1 = d * static_cast<float>(dec[sb]), m1 = dmin * static_cast<float>(dec[8 + sb]);
+            const uint8_t q = m.p0[blk * 128 + chunk * 32 + j];
+            const int v = (hi ? (q >> 4) : (q & 0xF)) | (((dec[16 + j] >> sb) & 1) << 4);
+            return d1 * static_cast<float>(v) - m1;
+        }
         case kQ4_K: {
             const size_t blk = static_cast<size_t>(r) * (cols / 256) + e / 256;
             const uint8_t* meta = m.p1 + blk * 16;

@@ -84,7 +84,9 @@ __global__ void k_pre_planar(const uint8_t* __restrict__ xq, int cols, int q8k, 
 
 // Eight consecutive weight values (k = kq .. kq + 7 of 32-value sub-block j) of
 // one row as signed int8, the A operand of one lane.  Q4_0: nibble - 8;
-// Q8_0: as stored; Q4_K: nibble 0..15 (the mins enter through the offsets);
+// Q4_1: nibble 0..15 (the offset m enters through the block sum); Q5_0: 5-bit
+// value - 16; Q8_0: as stored; Q4_K: nibble 0..15, Q5_K: 5-bit value 0..31
+// (the mins enter through the offsets);
 // Q6_K: 6-bit value - 32; TQ2_0: code - 1.  Sign extension is done per byte
 // (SWAR): for a field t of n bits, t | ((t & sign) * k) with k filling the
 // high bits.
@@ -103,11 +105,31 @@ __device__ __forceinline__ uint64_t frag_a(const Packed& m, uint32_t row, uint32
         const uint64_t nib = kq < 16 ? (w & (0x0F * kB01)) : ((w >> 4) & (0x0F * kB01));
         const uint64_t t = nib ^ (0x08 * kB01);             // 4-bit two's complement of nib - 8
         return t | ((t & (0x08 * kB01)) * 0x1E);             // sign-extend bit 3
+    } else if (T == kQ4_1) {
+        const uint32_t nsub = m.cols / 32;
+        const uint64_t w = ld8(m.p0 + (static_cast<size_t>(row) * nsub + j) * 16 + (kq & 15));
+        return kq < 16 ? (w & (0x0F * kB01)) : ((w >> 4) & (0x0F * kB01));
+    } else if (T == kQ5_0) {
+        const uint32_t nsub = m.cols / 32;
+        const size_t blk = static_cast<size_t>(row) * nsub + j;
+        const uint64_t w = ld8(m.p0 + blk * 16 + (kq & 15));
+        const uint32_t qh = reinterpret_cast<const uint32_t*>(m.p2)[blk] >> kq;  // bits of values kq .. kq + 7
+        const uint64_t hb = static_cast<uint64_t>(spread4_hi(qh, 0)) | (static_cast<uint64_t>(spread4_hi(qh, 4)) << 32);
+        const uint64_t u = (kq < 16 ? (w & (0x0F * kB01)) : ((w >> 4) & (0x0F * kB01))) | hb;  // 0..31
+        const uint64_t t = u ^ (0x10 * kB01);                                                // 5-bit two's complement of u - 16
+        return t | ((t & (0x10 * kB01)) * 0x0E);
     } else if (T == kQ4_K) {
         const uint32_t nsb = m.cols / 256, jj = j & 7;
         const size_t blk = static_cast<size_t>(row) * nsb + j / 8;
         const uint64_t w = ld8(m.p0 + blk * 128 + (jj >> 1) * 32 + kq);
         return (jj & 1) ? ((w >> 4) & (0x0F * kB01)) : (w & (0x0F * kB01));
+    } else if (T == kQ5_K) {
+        const uint32_t nsb = m.cols / 256, jj = j & 7;
+        const size_t blk = static_cast<size_t>(row) * nsb + j / 8;
+        const uint64_t w = ld8(m.p0 + blk * 128 + (jj >> 1) * 32 + kq);
+        const uint64_t h = ld8(m.p2 + blk * 48 + 16 + kq);
+        const uint64_t nib = (jj & 1) ? ((w >> 4) & (0x0F * kB01)) : (w & (0x0F * kB01));
+        return nib | (((h >> jj) & kB01) << 4);
     } else if (T == kQ6_K) {
         const uint32_t nsb = m.cols / 256, jj = j & 7, half = jj >> 2, quarter = jj & 3;
         const size_t blk = static_cast<size_t>(row) * nsb + j / 8;
@@ -145,13 +167,13 @@ constexpr int kBRow = kChunkCols + 16;  // LDS bytes per token row, padded off t
 // Token groups of 16 a workgroup: 4 (64 tokens), or 2 for the K-quants, whose
 // integer epilogue holds more state per output.
 template <uint32_t T>
-__host__ __device__ constexpr int mm_groups() { return (T == kQ4_K || T == kQ6_K) ? 2 : 4; }
+__host__ __device__ constexpr int mm_groups() { return (T == kQ4_K || T == kQ5_K || T == kQ6_K) ? 2 : 4; }
 
 template <int G>
 struct MmLds {
     alignas(16) int8_t b[16 * G][kBRow];
     float xd[16 * G][8];     // Q8_0: the chunk's 8 block scales; Q8_K: [0] the super-block's
-    int32_t bs[16 * G][16];  // Q8_K: the super-block's bsums
+    int32_t bs[16 * G][16];  // Q8_K: the super-block's bsums; Q8_0 (for Q4_1): [0..7] the 8 block sums
 };
 
 // One thread's share of a chunk's activations, in flight to LDS.
@@ -159,11 +181,12 @@ template <int G>
 struct ActStage {
     uint4 q[G];
     float d[2];
-    int32_t bs[4];
+    int32_t bs[4];  // Q8_0 with sums: [0..1] as d
 };
 
 template <int G>
-__device__ __forceinline__ void act_stage_load(ActStage<G>& st, const ActPlanar& x, int ntok, int t0, int c, bool q8k) {
+__device__ __forceinline__ void act_stage_load(ActStage<G>& st, const ActPlanar& x, int ntok, int t0, int c, bool q8k,
+                                               bool sums = false) {
     constexpr int kTok = 16 * G;
     const int tid = threadIdx.x;
 #pragma unroll
@@ -180,6 +203,7 @@ __device__ __forceinline__ void act_stage_load(ActStage<G>& st, const ActPlanar&
             if (tok < kTok) {
                 const int t = t0 + tok < ntok ? t0 + tok : ntok - 1;
                 st.d[k] = x.d[t * ds + c * 8 + blk];
+                if (sums) st.bs[k] = x.bs[t * bss + c * 8 + blk];
             }
         }
     } else {  // kTok tokens x 16 bsums, and kTok scales
@@ -197,7 +221,7 @@ __device__ __forceinline__ void act_stage_load(ActStage<G>& st, const ActPlanar&
 }
 
 template <int G>
-__device__ __forceinline__ void act_stage_store(const ActStage<G>& st, MmLds<G>& L, bool q8k) {
+__device__ __forceinline__ void act_stage_store(const ActStage<G>& st, MmLds<G>& L, bool q8k, bool sums = false) {
     constexpr int kTok = 16 * G;
     const int tid = threadIdx.x;
 #pragma unroll
@@ -209,7 +233,10 @@ __device__ __forceinline__ void act_stage_store(const ActStage<G>& st, MmLds<G>&
 #pragma unroll
         for (int k = 0; k < 2; ++k) {
             const int idx = k * kThreads + tid;
-            if ((idx >> 3) < kTok) L.xd[idx >> 3][idx & 7] = st.d[k];
+            if ((idx >> 3) < kTok) {
+                L.xd[idx >> 3][idx & 7] = st.d[k];
+                if (sums) L.bs[idx >> 3][idx & 7] = st.bs[k];
+            }
         }
     } else {
         if ((tid >> 2) < kTok) {
@@ -225,8 +252,9 @@ __device__ __forceinline__ void act_stage_store(const ActStage<G>& st, MmLds<G>&
 template <uint32_t T>
 struct WChunk {
     uint64_t a[8];
-    uint4 sc[4];     // Q4_0/Q8_0: 8 fp16 block scales a row; Q4_K: the decoded scales and mins; TQ2_0: .x = d
-    uint32_t s6[4];  // Q6_K: the fp16 d of each row (its int8 scales go in sc); Q4_K: {d, dmin}
+    uint4 sc[4];     // Q4_0/Q4_1/Q5_0/Q8_0: 8 fp16 block scales a row; Q4_K/Q5_K: the decoded scales and mins; TQ2_0: .x = d
+    uint32_t s6[4];  // Q6_K: the fp16 d of each row (its int8 scales go in sc); Q4_K/Q5_K: {d, dmin}
+    uint4 mn[4];     // Q4_1: 8 fp16 block offsets m a row
 };
 
 template <uint32_t T>
@@ -234,16 +262,20 @@ __device__ __forceinline__ void wchunk_load(WChunk<T>& w, const Packed& m, uint3
                                             int c, int kq) {
 #pragma unroll
     for (int jj = 0; jj < 8; ++jj) w.a[jj] = arow_ok ? frag_a<T>(m, arow, c * 8 + jj, kq) : 0ull;
-    if (T == kQ4_0 || T == kQ8_0) {
+    if (T == kQ4_0 || T == kQ4_1 || T == kQ5_0 || T == kQ8_0) {
         const uint32_t nsub = m.cols / 32;
 #pragma unroll
         for (int i = 0; i < 4; ++i) w.sc[i] = *reinterpret_cast<const uint4*>(m.p1 + (static_cast<size_t>(orow[i]) * nsub + c * 8) * 2);
-    } else if (T == kQ4_K) {
+        if (T == kQ4_1) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) w.mn[i] = *reinterpret_cast<const uint4*>(m.p2 + (static_cast<size_t>(orow[i]) * nsub + c * 8) * 2);
+        }
+    } else if (T == kQ4_K || T == kQ5_K) {
         const uint32_t nsb = m.cols / 256;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const size_t blk = static_cast<size_t>(orow[i]) * nsb + c;
-            w.sc[i] = *reinterpret_cast<const uint4*>(m.p2 + blk * 16);
+            w.sc[i] = *reinterpret_cast<const uint4*>(m.p2 + blk * (T == kQ5_K ? 48 : 16));
             w.s6[i] = *reinterpret_cast<const uint32_t*>(m.p1 + blk * 16);
         }
     } else if (T == kQ6_K) {
@@ -277,27 +309,37 @@ __device__ __forceinline__ void wchunk_compute(const WChunk<T>& w, const MmLds<G
     constexpr int kGroups = G;
     const int lane = threadIdx.x & 63, kq = (lane >> 4) * 8, tl = lane & 15;
     const v4i zero = {0, 0, 0, 0};
-    if (T == kQ4_0 || T == kQ8_0) {
+    if (T == kQ4_0 || T == kQ5_0 || T == kQ8_0 || T == kQ4_1) {
 #pragma unroll
         for (int jj = 0; jj < 8; ++jj) {
             v4i d[kGroups];
 #pragma unroll
             for (int g = 0; g < kGroups; ++g)
                 d[g] = mfma(w.a[jj], *reinterpret_cast<const uint64_t*>(&L.b[16 * g + tl][jj * 32 + kq]), zero);
-            float wd[4];
+            float wd[4], wm[4];
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 const uint32_t word = u4_word(w.sc[i], jj >> 1);
                 wd[i] = h2f(static_cast<uint16_t>((jj & 1) ? (word >> 16) : (word & 0xFFFF)));
+                if (T == kQ4_1) {
+                    const uint32_t mword = u4_word(w.mn[i], jj >> 1);
+                    wm[i] = h2f(static_cast<uint16_t>((jj & 1) ? (mword >> 16) : (mword & 0xFFFF)));
+                }
             }
 #pragma unroll
             for (int g = 0; g < kGroups; ++g) {
                 const float xd = L.xd[16 * g + tl][jj];
+                if (T == kQ4_1) {  // src/quant.cpp:445-456 with the offset term
+                    const float xs = xd * static_cast<float>(L.bs[16 * g + tl][jj]);
 #pragma unroll
-                for (int i = 0; i < 4; ++i) acc.s[g][i] += static_cast<float>(d[g][i]) * wd[i] * xd;  // src/quant.cpp:445-482
+                    for (int i = 0; i < 4; ++i) acc.s[g][i] += static_cast<float>(d[g][i]) * wd[i] * xd + wm[i] * xs;
+                } else {
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) acc.s[g][i] += static_cast<float>(d[g][i]) * wd[i] * xd;  // src/quant.cpp:445-482
+                }
             }
         }
-    } else if (T == kQ4_K) {
+    } else if (T == kQ4_K || T == kQ5_K) {
         int wsum[kGroups][4], osum[kGroups][4];
 #pragma unroll
         for (int g = 0; g < kGroups; ++g)
@@ -419,17 +461,18 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 2))
     const int nc = static_cast<int>(g.m.cols / kChunkCols);
     ActStage<kGroups> st;
     WChunk<T> w0, w1;  // two chunks in flight
-    act_stage_load(st, g.x, g.ntok, t0, 0, q8k);
+    constexpr bool kSums = T == kQ4_1;
+    act_stage_load(st, g.x, g.ntok, t0, 0, q8k, kSums);
     if (wave_ok) {
         wchunk_load<T>(w0, g.m, arow, arow_ok, orow, 0, kq);
     }
     for (int c = 0; c < nc; c += 2) {
         // chunk c (weights in w0/v0)
         __syncthreads();
-        act_stage_store(st, L, q8k);
+        act_stage_store(st, L, q8k, kSums);
         __syncthreads();
         if (c + 1 < nc) {
-            act_stage_load(st, g.x, g.ntok, t0, c + 1, q8k);
+            act_stage_load(st, g.x, g.ntok, t0, c + 1, q8k, kSums);
             if (wave_ok) {
                 wchunk_load<T>(w1, g.m, arow, arow_ok, orow, c + 1, kq);
             }
@@ -440,10 +483,10 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 2))
         if (c + 1 >= nc) break;
         // chunk c + 1 (weights in w1/v1)
         __syncthreads();
-        act_stage_store(st, L, q8k);
+        act_stage_store(st, L, q8k, kSums);
         __syncthreads();
         if (c + 2 < nc) {
-            act_stage_load(st, g.x, g.ntok, t0, c + 2, q8k);
+            act_stage_load(st, g.x, g.ntok, t0, c + 2, q8k, kSums);
             if (wave_ok) {
                 wchunk_load<T>(w0, g.m, arow, arow_ok, orow, c + 2, kq);
             }
@@ -1547,7 +1590,7 @@ __global__ __launch_bounds__(kThreads) void k_pre_attn_fa(PreAttnArgs p, int nto
 
 template <int MODE>
 static hipError_t mm_dispatch(const MmArgs& g, hipStream_t s) {
-    const int tok = 16 * (g.m.type == kQ4_K || g.m.type == kQ6_K ? mm_groups<kQ4_K>() : mm_groups<kQ4_0>());
+    const int tok = 16 * (g.m.type == kQ4_K || g.m.type == kQ5_K || g.m.type == kQ6_K ? mm_groups<kQ4_K>() : mm_groups<kQ4_0>());
     const dim3 grid((g.m.rows + kRowsPerWg - 1) / kRowsPerWg, (g.ntok + tok - 1) / tok);
     // K-quants: the widest token tile (64, 32 or 16 tokens) that still gives a workgroup to every CU
     const int row_tiles = static_cast<int>((g.m.rows + 63) / 64);
@@ -1556,7 +1599,10 @@ static hipError_t mm_dispatch(const MmArgs& g, hipStream_t s) {
     const dim3 kq_grid(row_tiles, (g.ntok + 16 * kq_g - 1) / (16 * kq_g));
     switch (g.m.type) {
         case kQ4_0: hipLaunchKernelGGL((k_mm<kQ4_0, MODE>), grid, dim3(kThreads), 0, s, g); break;
+        case kQ4_1: hipLaunchKernelGGL((k_mm<kQ4_1, MODE>), grid, dim3(kThreads), 0, s, g); break;
+        case kQ5_0: hipLaunchKernelGGL((k_mm<kQ5_0, MODE>), grid, dim3(kThreads), 0, s, g); break;
         case kQ8_0: hipLaunchKernelGGL((k_mm<kQ8_0, MODE>), grid, dim3(kThreads), 0, s, g); break;
+        case kQ5_K: hipLaunchKernelGGL((k_mm<kQ5_K, MODE>), grid, dim3(kThreads), 0, s, g); break;
         case kQ4_K:
             if (kq_g == 4) hipLaunchKernelGGL((k_mmk<kQ4_K, MODE, 4>), kq_grid, dim3(kThreads), 0, s, g);
             else if (kq_g == 2) hipLaunchKernelGGL((k_mmk<kQ4_K, MODE, 2>), kq_grid, dim3(kThreads), 0, s, g);

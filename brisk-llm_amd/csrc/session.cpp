@@ -449,7 +449,7 @@ void Session::setup_loop() {
     g.tiles_qkv[2] = tiles_of(L0.v.p, g.R_qkv[2]);
     g.R_o = loop_rows({&L0.o.p}, G);
     g.tiles_o = tiles_of(L0.o.p, g.R_o);
-    g.att_q8 = (L0.o.p.type == kQ4_0 || L0.o.p.type == kQ8_0) && L0.attn_sub_norm == nullptr &&
+    g.att_q8 = !takes_q8_k(L0.o.p.type) && L0.attn_sub_norm == nullptr &&
                ((cfg_.heads / cfg_.kv_heads) * cfg_.head_dim) % 32 == 0 ? 1 : 0;
     if (const char* e = std::getenv("BRISK_HIP_ATT_Q8")) g.att_q8 = g.att_q8 && std::string(e) != "0";
     g.R_gu = loop_rows({&L0.gate.p}, G);
@@ -462,7 +462,7 @@ void Session::setup_loop() {
         if (g.own_h) g.R_o = g.R_d = R;
     }
     g.tiles_o = tiles_of(L0.o.p, g.R_o);
-    g.att_q8 = (L0.o.p.type == kQ4_0 || L0.o.p.type == kQ8_0) && L0.attn_sub_norm == nullptr &&
+    g.att_q8 = !takes_q8_k(L0.o.p.type) && L0.attn_sub_norm == nullptr &&
                ((cfg_.heads / cfg_.kv_heads) * cfg_.head_dim) % 32 == 0 ? 1 : 0;
     if (const char* e = std::getenv("BRISK_HIP_ATT_Q8")) g.att_q8 = g.att_q8 && std::string(e) != "0";
     g.tiles_d = tiles_of(L0.down.p, g.R_d);

@@ -45,8 +45,11 @@ enum {
 enum {
     BRISK_HIP_F32 = 0,
     BRISK_HIP_Q4_0 = 2,
+    BRISK_HIP_Q4_1 = 3,
+    BRISK_HIP_Q5_0 = 6,
     BRISK_HIP_Q8_0 = 8,
     BRISK_HIP_Q4_K = 12,
+    BRISK_HIP_Q5_K = 13,
     BRISK_HIP_Q6_K = 14,
     BRISK_HIP_TQ2_0 = 35
 };

@@ -20,8 +20,10 @@ from brisk_hip import lib as L  # noqa: E402
 from brisk_hip import synth  # noqa: E402
 import pyoracle  # noqa: E402
 
-Q4_0, Q8_0, Q4_K, Q6_K, TQ2_0 = 2, 8, 12, 14, 35
-BLOCK = {Q4_0: (32, 18), Q8_0: (32, 34), Q4_K: (256, 144), Q6_K: (256, 210), TQ2_0: (256, 66)}
+Q4_0, Q4_1, Q5_0, Q8_0, Q4_K, Q5_K, Q6_K, TQ2_0 = 2, 3, 6, 8, 12, 13, 14, 35
+BLOCK = {Q4_0: (32, 18), Q4_1: (32, 20), Q5_0: (32, 22), Q8_0: (32, 34), Q4_K: (256, 144), Q5_K: (256, 176),
+         Q6_K: (256, 210), TQ2_0: (256, 66)}
+Q8K = (Q4_K, Q5_K, Q6_K, TQ2_0)
 
 
 def dev(a: np.ndarray):
@@ -110,6 +112,8 @@ CASES = [
     (Q4_K, 37, 1024), (Q4_K, 512, 2048), (Q4_K, 2048, 8192),
     (Q6_K, 37, 1024), (Q6_K, 512, 2048), (Q6_K, 2048, 8192),
     (TQ2_0, 48, 1024), (TQ2_0, 640, 2560), (TQ2_0, 37, 2560),
+    (Q4_1, 37, 1024), (Q4_1, 2048, 2048), (Q5_0, 37, 1024), (Q5_0, 1024, 3072),
+    (Q5_K, 37, 1024), (Q5_K, 512, 2048), (Q5_K, 2048, 8192),
 ]
 
 
@@ -117,7 +121,7 @@ CASES = [
 @pytest.mark.parametrize("type_,rows,cols", CASES)
 def test_matvec_matmul_bitexact(lib, orc, type_, rows, cols, n):
     w = weights(type_, rows, cols, rows * 7919 + cols)
-    q8k = type_ in (Q4_K, Q6_K, TQ2_0)
+    q8k = type_ in Q8K
     bits = orc.or_activation_bits(type_, rows)
     xs = [activations(cols, 100 + t) for t in range(n)]
     xq = np.concatenate([quant_ref(orc, x, q8k, bits) for x in xs])
@@ -138,7 +142,8 @@ def test_matvec_matmul_bitexact(lib, orc, type_, rows, cols, n):
 
 
 @pytest.mark.parametrize("type_,rows,cols", [(Q4_0, 2048, 1024), (Q8_0, 4096, 1024), (Q4_K, 256, 2048),
-                                              (Q6_K, 256, 8192), (TQ2_0, 640, 2560)])
+                                              (Q6_K, 256, 8192), (TQ2_0, 640, 2560), (Q4_1, 2048, 1024),
+                                              (Q5_0, 1024, 2048), (Q5_K, 256, 4096)])
 def test_gemv_fused_norm_bitexact(lib, orc, type_, rows, cols):
     """In-kernel rms_norm + quantisation + matvec equals the oracle's rms_norm -> quantize -> matvec."""
     w = weights(type_, rows, cols, rows + cols)
@@ -148,7 +153,7 @@ def test_gemv_fused_norm_bitexact(lib, orc, type_, rows, cols):
     normed = np.zeros(cols, np.float32)
     orc.or_rms_norm(pyoracle.ptr(x), pyoracle.ptr(nw), eps, pyoracle.ptr(normed), cols)
     bits = orc.or_activation_bits(type_, rows)
-    xq = quant_ref(orc, normed, type_ in (Q4_K, Q6_K, TQ2_0), bits)
+    xq = quant_ref(orc, normed, type_ in Q8K, bits)
     want = np.zeros(rows, np.float32)
     orc.or_matvec(type_, pyoracle.ptr(w), rows, cols, pyoracle.ptr(xq), pyoracle.ptr(want))
     flags = 1 if (type_ == TQ2_0 and rows % 16 == 0) else 0

@@ -39,7 +39,7 @@ def test_library_host_only_calls():
     assert L.brisk_hip_abi_version() == want
     # packed planes hold exactly the GGUF bytes of the matrix, each plane 256-byte aligned
     for t, (be, bb) in ((G.T_Q4_0, (32, 18)), (G.T_Q8_0, (32, 34)), (G.T_Q4_K, (256, 144)), (G.T_Q6_K, (256, 210)),
-                        (G.T_TQ2_0, (256, 66))):
+                        (G.T_TQ2_0, (256, 66)), (G.T_Q4_1, (32, 20)), (G.T_Q5_0, (32, 22)), (G.T_Q5_K, (256, 176))):
         rows, cols = 48, 2048
         n = L.brisk_hip_packed_bytes(t, rows, cols)
         gguf = rows * cols // be * bb
@@ -96,7 +96,7 @@ def test_spec_bytes_match_the_measurement_contract():
     assert s.output_bytes() == 165_306_368
 
 
-@pytest.mark.parametrize("name", ["tiny-qwen3", "tiny-llama", "tiny-bitnet"])
+@pytest.mark.parametrize("name", ["tiny-qwen3", "tiny-llama", "tiny-bitnet", "tiny-q5k", "tiny-q5"])
 def test_model_config_parse(name):
     spec = synth.SPECS[name]
     f, cfg, table = model.load(synth.model_path(name))
@@ -107,7 +107,7 @@ def test_model_config_parse(name):
     assert ("output.weight" in names) == (spec.out_fmt is not None)
 
 
-@pytest.mark.parametrize("name", ["tiny-qwen3", "tiny-llama", "tiny-bitnet"])
+@pytest.mark.parametrize("name", ["tiny-qwen3", "tiny-llama", "tiny-bitnet", "tiny-q5k", "tiny-q5"])
 def test_session_estimate(name):
     """brisk_hip_session_estimate (HBM counterpart of estimate_memory, src/memory.cpp:46-96): shapes only, no GPU."""
     from brisk_hip.session import estimate
