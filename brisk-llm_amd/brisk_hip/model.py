@@ -1,8 +1,8 @@
 """Model configuration and tensor table from a GGUF file (host side).
 
 Restates the part of the reference's loader the HIP session needs:
-``Model::parse_config`` (src/model.cpp:161-301) for the families on the
-benchmark path (qwen3, llama, bitnet), the tensor names and shapes of
+``Model::parse_config`` (src/model.cpp:161-301) for the families the HIP
+session runs (qwen3, llama, bitnet, qwen2, smollm3), the tensor names and shapes of
 ``Model::Model`` (src/model.cpp:303-423) and the tied output projection
 (src/model.cpp:328-330).  The session takes the weights as GGUF-layout bytes,
 as the reference's ``Model(file, repack = false)`` hands them to a GPU session.
@@ -13,8 +13,9 @@ from dataclasses import dataclass
 
 from . import gguf as G
 
-ARCH_QWEN3, ARCH_LLAMA, ARCH_BITNET = 0, 1, 2
-_ARCH = {"qwen3": ARCH_QWEN3, "llama": ARCH_LLAMA, "bitnet": ARCH_BITNET, "bitnet-b1.58": ARCH_BITNET}
+ARCH_QWEN3, ARCH_LLAMA, ARCH_BITNET, ARCH_QWEN2, ARCH_SMOLLM3 = 0, 1, 2, 3, 4
+_ARCH = {"qwen3": ARCH_QWEN3, "llama": ARCH_LLAMA, "bitnet": ARCH_BITNET, "bitnet-b1.58": ARCH_BITNET,
+         "qwen2": ARCH_QWEN2, "smollm3": ARCH_SMOLLM3}
 QUANT_TYPES = (G.T_Q4_0, G.T_Q4_1, G.T_Q5_0, G.T_Q8_0, G.T_Q4_K, G.T_Q5_K, G.T_Q6_K, G.T_TQ2_0)
 
 
@@ -43,7 +44,10 @@ class ModelConfig:
 
     @property
     def rope_neox(self) -> bool:  # src/model.cpp:167
-        return self.arch != ARCH_LLAMA
+        return self.arch not in (ARCH_LLAMA, ARCH_SMOLLM3)
+
+    def layer_has_rope(self, layer: int) -> bool:  # src/model.h:110; SmolLM3's step of 4, src/model.cpp:168
+        return not (self.arch == ARCH_SMOLLM3 and (layer + 1) % 4 == 0)
 
     @property
     def query_dim(self) -> int:
@@ -57,7 +61,7 @@ class ModelConfig:
 def parse_config(f: G.GgufFile) -> ModelConfig:
     name = f.get("general.architecture")
     if name not in _ARCH:
-        fail(f"unsupported architecture '{name}'; the HIP session runs qwen3, llama and bitnet")
+        fail(f"unsupported architecture '{name}'; the HIP session runs qwen3, qwen2, llama, smollm3 and bitnet")
     p = name + "."
 
     def u32(key):
@@ -144,6 +148,10 @@ def tensor_table(f: G.GgufFile, cfg: ModelConfig) -> list:
         if cfg.arch == ARCH_BITNET:
             vec(b + "attn_sub_norm.weight", e)
             vec(b + "ffn_sub_norm.weight", cfg.ff)
+        if f.tensor(b + "attn_q.bias") is not None:  # all or none (src/model.cpp:411-416)
+            vec(b + "attn_q.bias", qd)
+            vec(b + "attn_k.bias", kvd)
+            vec(b + "attn_v.bias", kvd)
         mat(b + "attn_output.weight", e, qd)
         vec(b + "ffn_norm.weight", e)
         mat(b + "ffn_gate.weight", cfg.ff, e)

@@ -233,6 +233,10 @@ SPECS = {
     # The loader's other formats (a Q5_K_M mix; Q5_0 with Q4_1), on the path's families.
     "tiny-q5k": ModelSpec("tiny-q5k", "llama", 512, 2, 8, 2, 64, 768, 1000, 5e5, eps=1e-5, context=1024,
                           fmt={**_uniform4(G.T_Q5_K), "v": G.T_Q6_K, "down": G.T_Q6_K}, embd_fmt=G.T_Q6_K, out_fmt=None),
+    # Qwen2 (projection biases, no Q/K norms) and SmolLM3 (Llama-shaped, layers 3 and 7 without RoPE).
+    "tiny-qwen2": ModelSpec("tiny-qwen2", "qwen2", 256, 2, 4, 2, 64, 512, 1000, 1e6, context=1024, fmt=_uniform4(G.T_Q4_0)),
+    "tiny-smollm3": ModelSpec("tiny-smollm3", "smollm3", 512, 8, 8, 2, 64, 768, 1000, 5e5, eps=1e-5, context=1024,
+                              fmt={**_uniform4(G.T_Q4_K), "v": G.T_Q6_K, "down": G.T_Q6_K}, embd_fmt=G.T_Q6_K, out_fmt=None),
     "tiny-q5": ModelSpec("tiny-q5", "qwen3", 256, 2, 4, 2, 64, 512, 1000, 1e6, context=1024,
                          fmt={**_uniform4(G.T_Q5_0), "o": G.T_Q4_1, "down": G.T_Q4_1}),
 }
@@ -248,6 +252,11 @@ def _matrix(w: G.GgufWriter, spec: ModelSpec, name: str, rows: int, cols: int, t
 def _vector(w: G.GgufWriter, spec: ModelSpec, name: str, n: int):
     seed = stream_seed(spec.seed, name)
     w.add_tensor(name, (n,), G.T_F32, lambda: random_uniform(seed, n, 0.8, 1.2).astype(np.float32).view(np.uint8))
+
+
+def _bias(w: G.GgufWriter, spec: ModelSpec, name: str, n: int):
+    seed = stream_seed(spec.seed, name)
+    w.add_tensor(name, (n,), G.T_F32, lambda: random_uniform(seed, n, -1.0, 1.0).astype(np.float32).view(np.uint8))
 
 
 def write_model(spec: ModelSpec, path: str) -> str:
@@ -284,6 +293,10 @@ def write_model(spec: ModelSpec, path: str) -> str:
         if a.startswith("bitnet"):
             _vector(w, spec, b + "attn_sub_norm.weight", spec.embd)
             _vector(w, spec, b + "ffn_sub_norm.weight", spec.ff)
+        if a == "qwen2":  # Q/K/V projection biases (src/model.cpp:411-416)
+            _bias(w, spec, b + "attn_q.bias", spec.query_dim)
+            _bias(w, spec, b + "attn_k.bias", spec.kv_dim)
+            _bias(w, spec, b + "attn_v.bias", spec.kv_dim)
         _matrix(w, spec, b + "attn_output.weight", spec.embd, spec.query_dim, spec.fmt["o"])
         _vector(w, spec, b + "ffn_norm.weight", spec.embd)
         _matrix(w, spec, b + "ffn_gate.weight", spec.ff, spec.embd, spec.fmt["gate"])

@@ -45,7 +45,10 @@ struct AttnArgs {
     const float* v;
     const float* qnorm;   // per-head q/k RMS weights (Qwen3) or null
     const float* knorm;
-    const float* rope;    // [max_context][head_dim] cos, sin pairs
+    const float* qbias;   // projection biases added to the raw q, k, v (Qwen2) or null
+    const float* kbias;   // ([heads][head_dim], [kv_heads][head_dim], ditto)
+    const float* vbias;
+    const float* rope;    // [max_context][head_dim] cos, sin pairs; null on a layer without RoPE (SmolLM3)
     float eps;
     int neox;
     uint16_t* kcache;     // this layer's [kv_heads][ctx][head_dim]

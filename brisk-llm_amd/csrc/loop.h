@@ -13,6 +13,10 @@ struct LayerDev {
     const float* attn_sub;
     const float* ffn_norm;
     const float* ffn_sub;
+    const float* q_bias;  // projection biases or null
+    const float* k_bias;
+    const float* v_bias;
+    int rope;             // 0: the layer attends without RoPE
     uint16_t* kc;  // [kv_heads][ctx][head_dim] fp16
     uint16_t* vc;
 };

@@ -199,11 +199,15 @@ struct TaggedOut {
     __device__ __forceinline__ bool get_pml(size_t i, float& v) const { return wait(part_ml + i, v); }
 };
 
-// RMS norm over one head (optional weight w) and RoPE, by one wave: the
-// per-head q_norm / k_norm and apply_rope of src/model.cpp:1026-1041, with
+// The projection bias (add_bias, src/model.cpp:117-119 and :1026-1030), an
+// RMS norm over one head (optional weight w) and RoPE (none when rope is
+// null), by one wave: the per-head steps of src/model.cpp:1021-1041, with
 // rms_norm's float squares summed in double (src/model.cpp:87-97).
-__device__ __forceinline__ void head_norm_rope(float* v, const float* w, const float* rope, int hd, int neox, float eps) {
+__device__ __forceinline__ void head_norm_rope(float* v, const float* bias, const float* w, const float* rope, int hd, int neox,
+                                               float eps) {
     const int lane = threadIdx.x & 63;
+    if (bias != nullptr)
+        for (int i = lane; i < hd; i += 64) v[i] = v[i] + bias[i];
     if (w != nullptr) {
         double s = 0.0;
         for (int i = lane; i < hd; i += 64) s += static_cast<double>(v[i] * v[i]);
@@ -211,6 +215,7 @@ __device__ __forceinline__ void head_norm_rope(float* v, const float* w, const f
         const float scale = rms_scale(s, hd, eps);
         for (int i = lane; i < hd; i += 64) v[i] = v[i] * scale * w[i];
     }
+    if (rope == nullptr) return;
     const int half = hd / 2;
     for (int i = lane; i < half; i += 64) {
         const float c = rope[2 * i], sn = rope[2 * i + 1];
@@ -263,17 +268,17 @@ template <bool kWriteThrough>
 __device__ __forceinline__ void attn_finish_prologue(const AttnArgs& g, AttnLds& s, int kv, int pos, bool writer,
                                                      bool store = true) {
     const int hd = g.head_dim, hpk = g.heads / g.kv_heads, t = threadIdx.x;
-    const float* rope = g.rope + static_cast<size_t>(pos) * hd;
+    const float* rope = g.rope != nullptr ? g.rope + static_cast<size_t>(pos) * hd : nullptr;
     const int wave = t >> 6;
     for (int h = wave; h < hpk + (writer ? 1 : 0); h += kThreads / 64) {
-        if (h < hpk) head_norm_rope(s.q + h * hd, g.qnorm, rope, hd, g.neox, g.eps);
-        else head_norm_rope(s.kcur, g.knorm, rope, hd, g.neox, g.eps);
+        if (h < hpk) head_norm_rope(s.q + h * hd, g.qbias != nullptr ? g.qbias + (kv * hpk + h) * hd : nullptr, g.qnorm, rope, hd, g.neox, g.eps);
+        else head_norm_rope(s.kcur, g.kbias != nullptr ? g.kbias + kv * hd : nullptr, g.knorm, rope, hd, g.neox, g.eps);
     }
     __syncthreads();
     if (writer) {
         for (int i = t; i < hd; i += kThreads) {
             s.kcur[i] = h2f(f2h(s.kcur[i]));
-            s.vcur[i] = h2f(f2h(s.vcur[i]));
+            s.vcur[i] = h2f(f2h(g.vbias != nullptr ? s.vcur[i] + g.vbias[kv * hd + i] : s.vcur[i]));
         }
         __syncthreads();
         if (store) {

@@ -932,13 +932,13 @@ __global__ __launch_bounds__(kThreads) void k_pre_rope(PreAttnArgs p) {
     for (int i = tid; i < hpk * hd; i += kThreads) s.q[i] = q[i];
     for (int i = tid; i < hd; i += kThreads) {
         s.kcur[i] = k[i];
-        s.vcur[i] = v[i];
+        s.vcur[i] = g.vbias != nullptr ? v[i] + g.vbias[kv * hd + i] : v[i];
     }
     __syncthreads();
-    const float* rope = g.rope + static_cast<size_t>(pos) * hd;
+    const float* rope = g.rope != nullptr ? g.rope + static_cast<size_t>(pos) * hd : nullptr;
     for (int h = tid >> 6; h <= hpk; h += kThreads / 64) {  // a wave a head; the last is the key
-        if (h < hpk) head_norm_rope(s.q + h * hd, g.qnorm, rope, hd, g.neox, g.eps);
-        else head_norm_rope(s.kcur, g.knorm, rope, hd, g.neox, g.eps);
+        if (h < hpk) head_norm_rope(s.q + h * hd, g.qbias != nullptr ? g.qbias + (kv * hpk + h) * hd : nullptr, g.qnorm, rope, hd, g.neox, g.eps);
+        else head_norm_rope(s.kcur, g.kbias != nullptr ? g.kbias + kv * hd : nullptr, g.knorm, rope, hd, g.neox, g.eps);
     }
     __syncthreads();
     // the cache rows, fp16 (store_f16, src/kernels_f32.cpp:248-250)

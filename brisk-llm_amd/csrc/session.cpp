@@ -77,12 +77,15 @@ static std::string gb(size_t bytes) {
     return buf;
 }
 
+// Rotate-half RoPE for every family but the adjacent-pair Llama and SmolLM3 (src/model.cpp:167).
+bool Session::neox() const { return cfg_.arch != BRISK_HIP_ARCH_LLAMA && cfg_.arch != BRISK_HIP_ARCH_SMOLLM3; }
+
 Session::Session(const brisk_hip_config& cfg, const brisk_hip_tensor* tensors, size_t n, size_t max_context, int device)
     : cfg_(cfg), device_(device) {
     int count = 0;
     if (hipGetDeviceCount(&count) != hipSuccess || count == 0) throw Error(BRISK_HIP_ENODEV, "hip: no GPU device available");
     if (device < 0 || device >= count) throw Error(BRISK_HIP_ENODEV, "hip: no GPU device " + std::to_string(device));
-    if (cfg.arch < BRISK_HIP_ARCH_QWEN3 || cfg.arch > BRISK_HIP_ARCH_BITNET) model_fail("unsupported architecture");
+    if (cfg.arch < BRISK_HIP_ARCH_QWEN3 || cfg.arch > BRISK_HIP_ARCH_SMOLLM3) model_fail("unsupported architecture");
     if (cfg.embd == 0 || cfg.layers == 0 || cfg.heads == 0 || cfg.kv_heads == 0 || cfg.ff == 0 || cfg.context_length == 0 ||
         cfg.vocab == 0)
         model_fail("a model dimension is zero");
@@ -185,6 +188,12 @@ Session::Session(const brisk_hip_config& cfg, const brisk_hip_tensor* tensors, s
             L.attn_sub_norm = load_vector(b + "attn_sub_norm.weight", e);
             L.ffn_sub_norm = load_vector(b + "ffn_sub_norm.weight", cfg.ff);
         }
+        if (find(b + "attn_q.bias") != nullptr) {  // src/model.cpp:411-416
+            L.q_bias = load_vector(b + "attn_q.bias", qd);
+            L.k_bias = load_vector(b + "attn_k.bias", kvd);
+            L.v_bias = load_vector(b + "attn_v.bias", kvd);
+        }
+        L.rope = !(cfg.arch == BRISK_HIP_ARCH_SMOLLM3 && (l + 1) % 4 == 0);  // layer_has_rope (src/model.h:110, :168)
         // one activation row feeds Q, K and V: they must take the same width (src/model.cpp:584-590)
         if (takes_q8_k(L.q.p.type) != takes_q8_k(L.k.p.type) || takes_q8_k(L.q.p.type) != takes_q8_k(L.v.p.type) ||
             act_bits(L.q.p) != act_bits(L.k.p) || act_bits(L.q.p) != act_bits(L.v.p) ||
@@ -301,8 +310,9 @@ void Session::record_step(bool full) {
         }
 
         AttnArgs aa{};
-        aa.q = q_; aa.k = k_; aa.v = v_; aa.qnorm = L.q_norm; aa.knorm = L.k_norm; aa.rope = rope_;
-        aa.eps = cfg_.rms_epsilon; aa.neox = cfg_.arch != BRISK_HIP_ARCH_LLAMA;  // src/model.cpp:167
+        aa.q = q_; aa.k = k_; aa.v = v_; aa.qnorm = L.q_norm; aa.knorm = L.k_norm; aa.rope = L.rope ? rope_ : nullptr;
+        aa.qbias = L.q_bias; aa.kbias = L.k_bias; aa.vbias = L.v_bias;
+        aa.eps = cfg_.rms_epsilon; aa.neox = neox();
         aa.kcache = kcache_[l]; aa.vcache = vcache_[l]; aa.pos = pos_;
         aa.ctx = static_cast<int>(max_ctx_); aa.head_dim = static_cast<int>(cfg_.head_dim);
         aa.heads = static_cast<int>(cfg_.heads); aa.kv_heads = static_cast<int>(cfg_.kv_heads);
@@ -385,7 +395,8 @@ void Session::setup_loop() {
     for (uint32_t l = 0; l < cfg_.layers; ++l) {
         const Layer& L = layers_[l];
         ld[l] = LayerDev{L.q.p, L.k.p, L.v.p, L.o.p, L.gate.p, L.up.p, L.down.p, L.attn_norm, L.q_norm, L.k_norm,
-                         L.attn_sub_norm, L.ffn_norm, L.ffn_sub_norm, kcache_[l], vcache_[l]};
+                         L.attn_sub_norm, L.ffn_norm, L.ffn_sub_norm, L.q_bias, L.k_bias, L.v_bias, L.rope ? 1 : 0,
+                         kcache_[l], vcache_[l]};
     }
     layers_dev_ = static_cast<LayerDev*>(alloc(ld.size() * sizeof(LayerDev)));
     check(hipMemcpy(layers_dev_, ld.data(), ld.size() * sizeof(LayerDev), hipMemcpyHostToDevice), "hipMemcpy(layers)");
@@ -421,7 +432,7 @@ void Session::setup_loop() {
     g.kv_heads = static_cast<int>(cfg_.kv_heads);
     g.head_dim = static_cast<int>(cfg_.head_dim);
     g.ff = static_cast<int>(cfg_.ff);
-    g.neox = cfg_.arch != BRISK_HIP_ARCH_LLAMA;
+    g.neox = neox();
     g.relu2 = cfg_.arch == BRISK_HIP_ARCH_BITNET;
     g.eps = cfg_.rms_epsilon;
     g.scale = 1.0f / std::sqrt(static_cast<float>(cfg_.head_dim));
@@ -631,8 +642,9 @@ void Session::prefill_layers(size_t pos0, int T) {
         check(launch_mm(g, kMmStore, stream_), "prefill v");
         // norms, RoPE, cache rows, attention (:1020-1093)
         PreAttnArgs pa{};
-        pa.a.qnorm = L.q_norm; pa.a.knorm = L.k_norm; pa.a.rope = rope_; pa.a.eps = cfg_.rms_epsilon;
-        pa.a.neox = cfg_.arch != BRISK_HIP_ARCH_LLAMA;  // src/model.cpp:167
+        pa.a.qnorm = L.q_norm; pa.a.knorm = L.k_norm; pa.a.rope = L.rope ? rope_ : nullptr; pa.a.eps = cfg_.rms_epsilon;
+        pa.a.qbias = L.q_bias; pa.a.kbias = L.k_bias; pa.a.vbias = L.v_bias;
+        pa.a.neox = neox();
         pa.a.kcache = kcache_[l]; pa.a.vcache = vcache_[l];
         pa.a.ctx = static_cast<int>(max_ctx_); pa.a.head_dim = static_cast<int>(cfg_.head_dim);
         pa.a.heads = static_cast<int>(cfg_.heads); pa.a.kv_heads = static_cast<int>(cfg_.kv_heads);

@@ -38,6 +38,10 @@ struct Layer {
     const float* attn_sub_norm = nullptr;
     const float* ffn_norm = nullptr;
     const float* ffn_sub_norm = nullptr;
+    const float* q_bias = nullptr;  // projection biases (Qwen2 and some Llama-shaped models), all or none
+    const float* k_bias = nullptr;
+    const float* v_bias = nullptr;
+    bool rope = true;               // false: the layer attends without RoPE (SmolLM3's every fourth)
 };
 
 // Device bytes a session of these tensors would allocate (see Session's constructor).
@@ -84,6 +88,7 @@ private:
     bool use_prefill(size_t n) const;
     void ensure_prefill();
     void prefill_layers(size_t pos0, int T);
+    bool neox() const;
     void prefill_quant(const float* x, int xstride, const float* w, int cols, int T, const DeviceMatrix& consumer);
 
     brisk_hip_config cfg_;

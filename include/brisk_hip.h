@@ -55,7 +55,13 @@ enum {
 };
 
 /* Model families on this path (Architecture, src/model.h:21-32). */
-enum { BRISK_HIP_ARCH_QWEN3 = 0, BRISK_HIP_ARCH_LLAMA = 1, BRISK_HIP_ARCH_BITNET = 2 };
+enum {
+    BRISK_HIP_ARCH_QWEN3 = 0,
+    BRISK_HIP_ARCH_LLAMA = 1,
+    BRISK_HIP_ARCH_BITNET = 2,
+    BRISK_HIP_ARCH_QWEN2 = 3,   /* Q/K/V projection biases, no Q/K norms */
+    BRISK_HIP_ARCH_SMOLLM3 = 4  /* Llama-shaped; every fourth layer attends without RoPE */
+};
 
 /* The fields of ModelConfig (src/model.h:36-60) this path reads. */
 typedef struct {

@@ -628,6 +628,7 @@ typedef struct {
 
 typedef struct {
     const float *attn_norm, *q_norm, *k_norm, *attn_sub_norm, *ffn_norm, *ffn_sub_norm;
+    const float *q_bias, *k_bias, *v_bias; /* all or none (src/model.cpp:411-416) */
     matrix q, k, v, o, gate, up, down;
 } layer_t;
 
@@ -691,6 +692,11 @@ oracle_session* or_session_create(const oracle_config* cfg, const oracle_tensor*
         if (c->arch == OR_BITNET) {
             GETV(L->attn_sub_norm, LN("attn_sub_norm.weight"));
             GETV(L->ffn_sub_norm, LN("ffn_sub_norm.weight"));
+        }
+        if (find(t, n, LN("attn_q.bias"))) {
+            GETV(L->q_bias, LN("attn_q.bias"));
+            GETV(L->k_bias, LN("attn_k.bias"));
+            GETV(L->v_bias, LN("attn_v.bias"));
         }
     }
     {
@@ -770,7 +776,7 @@ static void forward_token(oracle_session* s, int32_t token, float* logits) {
     const oracle_config* c = &s->c;
     const size_t embd = c->embd, hd = c->head_dim, qd = (size_t)c->heads * hd, kvd = (size_t)c->kv_heads * hd;
     const size_t hpk = (size_t)(c->heads / c->kv_heads), pos = s->position, ctx = (size_t)c->max_context;
-    const int neox = c->arch != OR_LLAMA; /* src/model.cpp:167 */
+    const int neox = c->arch != OR_LLAMA && c->arch != OR_SMOLLM3; /* src/model.cpp:167 */
     const float attention_scale = 1.0f / sqrtf((float)hd);
 
     /* build_rope (src/model.cpp:880-894), scale 1, attn factor 1, no factors */
@@ -791,16 +797,23 @@ static void forward_token(oracle_session* s, int32_t token, float* logits) {
         multiply(s, &L->q, s->normed, s->q);
         multiply(s, &L->k, s->normed, s->k);
         multiply(s, &L->v, s->normed, s->v);
+        /* SmolLM3: every fourth layer has no RoPE (layer_has_rope, src/model.h:110; step 4, src/model.cpp:168) */
+        const size_t rope_dim = (c->arch == OR_SMOLLM3 && (l + 1) % 4 == 0) ? 0 : hd;
+        if (L->q_bias) { /* add_bias (src/model.cpp:117-119, :1026-1030) */
+            for (size_t i = 0; i < qd; ++i) s->q[i] += L->q_bias[i];
+            for (size_t i = 0; i < kvd; ++i) s->k[i] += L->k_bias[i];
+            for (size_t i = 0; i < kvd; ++i) s->v[i] += L->v_bias[i];
+        }
         for (int h = 0; h < c->heads; ++h) {
             float* q = s->q + h * hd;
             if (L->q_norm) or_rms_norm(q, L->q_norm, c->eps, q, hd);
-            apply_rope(q, s->rope, hd, neox);
+            apply_rope(q, s->rope, rope_dim, neox);
         }
         for (int h = 0; h < c->kv_heads; ++h) {
             float* k = s->k + h * hd;
             const float* v = s->v + h * hd;
             if (L->k_norm) or_rms_norm(k, L->k_norm, c->eps, k, hd);
-            apply_rope(k, s->rope, hd, neox);
+            apply_rope(k, s->rope, rope_dim, neox);
             uint16_t* kr = s->kcache[l] + ((size_t)h * ctx + pos) * hd;
             uint16_t* vr = s->vcache[l] + ((size_t)h * ctx + pos) * hd;
             for (size_t i = 0; i < hd; ++i) {

@@ -25,7 +25,7 @@ extern "C" {
 /* ggml tensor types (src/gguf.h:22-27). */
 enum { OR_F32 = 0, OR_Q4_0 = 2, OR_Q4_1 = 3, OR_Q5_0 = 6, OR_Q8_0 = 8, OR_Q4_K = 12, OR_Q5_K = 13, OR_Q6_K = 14, OR_TQ2_0 = 35 };
 /* Architectures of src/model.h:21-32 that the configs use. */
-enum { OR_QWEN3 = 0, OR_LLAMA = 1, OR_BITNET = 2 };
+enum { OR_QWEN3 = 0, OR_LLAMA = 1, OR_BITNET = 2, OR_QWEN2 = 3, OR_SMOLLM3 = 4 };
 
 typedef struct {
     int arch;

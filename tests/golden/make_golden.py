@@ -32,6 +32,8 @@ RUNS = {
     "tiny-bitnet": (12, 48),
     "tiny-q5k": (12, 48),
     "tiny-q5": (12, 48),
+    "tiny-qwen2": (12, 48),
+    "tiny-smollm3": (12, 48),
 }
 
 

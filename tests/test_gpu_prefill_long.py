@@ -27,7 +27,7 @@ from brisk_hip import HipSession, model, synth  # noqa: E402
 import pyoracle  # noqa: E402
 
 TOL = 2e-2
-FAMILIES = ["tiny-qwen3", "tiny-llama", "tiny-q8", "tiny-bitnet", "tiny-q5k", "tiny-q5"]
+FAMILIES = ["tiny-qwen3", "tiny-llama", "tiny-q8", "tiny-bitnet", "tiny-q5k", "tiny-q5", "tiny-qwen2", "tiny-smollm3"]
 
 
 def _session(src, ctx, mfma):
@@ -61,7 +61,8 @@ def test_long_prompt_exact(name, first, second):
         np.testing.assert_array_equal(ids, o_ids, err_msg=f"gaps {gaps}")
 
 
-@pytest.mark.parametrize("name", FAMILIES)
+# two-layer models: every extra layer re-quantises once more, so deeper stacks give fewer bit-identical prompts
+@pytest.mark.parametrize("name", [n for n in FAMILIES if synth.SPECS[n].layers == 2])
 def test_mfma_attention_tiny(name):
     """Eight prompts each of 64, 100 and 300 tokens: most give the oracle's logits
     bit for bit (the reordered sums round the same way after re-quantisation);
