@@ -131,11 +131,33 @@ def other_configs(torch, HipSession, model, synth):
     """configs[3] (Qwen3-1.7B Q8_0, KV pre-filled to 4096 with fp16 N(0,1), 128 decode steps) and
     configs[4] (BitNet-2B TQ2_0, 64-id prompt, 256 greedy steps): decode tok/s."""
     import ctypes as C
+    import numpy as np
     out = {}
     hip = C.CDLL("libamdhip64.so")
     hip.hipMemcpy.argtypes = [C.c_void_p, C.c_void_p, C.c_size_t, C.c_int]
     f, cfg, table = model.load(synth.model_path("qwen3-1.7b"))
-    s = HipSession((f, cfg, table), max_context=4096 + 160)
+    gguf_bytes = sum(t.data.nbytes for t in table)
+    for t in table:                    # the file's pages resident, as after the reference's mmap + first touch
+        int(np.asarray(t.data[::4096], dtype=np.uint64).sum())
+    load = {}
+    for mode in ("pageable", "pinned"):  # session creation: upload + repack of every tensor
+        if mode == "pageable":
+            os.environ["BRISK_HIP_PAGEABLE_UPLOAD"] = "1"
+        t0 = time.perf_counter()
+        s = HipSession((f, cfg, table), max_context=4096 + 160)
+        torch.cuda.synchronize()
+        load[mode] = time.perf_counter() - t0
+        os.environ.pop("BRISK_HIP_PAGEABLE_UPLOAD", None)
+        if mode == "pageable":
+            s.close()
+            del s
+    out["load_qwen3-1.7b"] = {"workload": "session creation of configs[3] (upload of the GGUF bytes, repack to planes, "
+                                          "caches for 4256 positions)", "gguf_bytes": gguf_bytes,
+                              "seconds": round(load["pinned"], 4), "gb_s": round(gguf_bytes / load["pinned"] / 1e9, 2),
+                              "pageable_seconds": round(load["pageable"], 4),
+                              "pageable_gb_s": round(gguf_bytes / load["pageable"] / 1e9, 2)}
+    log(f"configs[3] load: {load['pinned']:.3f}s pinned staging, {load['pageable']:.3f}s pageable "
+        f"({gguf_bytes / 1e9:.2f} GB)")
     gen = torch.Generator(device="cuda").manual_seed(7)
     for layer in range(cfg.layers):
         for value in (False, True):

@@ -180,8 +180,10 @@ __device__ __forceinline__ void prologue_lds(const Packed& m, ActRegs& ar, const
 }
 
 // The embedding row of `token` (embedding_row, src/model.cpp:27-70) into s.x.
+// The loop is built for an embedding of its output's format (find_loop_kernel checks it).
+template <uint32_t TE>
 __device__ __forceinline__ void embed_to_lds(const LoopArgs& g, int token, GemvLds& s) {
-    for (uint32_t e = threadIdx.x; e < g.embd.cols; e += kThreads) s.x[e] = dequant_elem(g.embd, static_cast<uint32_t>(token), e);
+    for (uint32_t e = threadIdx.x; e < g.embd.cols; e += kThreads) s.x[e] = dequant_elem<TE>(g.embd, static_cast<uint32_t>(token), e);
     __syncthreads();
 }
 
@@ -263,7 +265,7 @@ __device__ __forceinline__ bool run_tiles(int total, GemvLds& s, RowOf row_of, R
 // ---------------------------------------------------------------- phases
 
 // A: Q, K, V rows (one format, or Q/K's and then V's).
-template <uint32_t TQ, uint32_t TV>
+template <uint32_t TQ, uint32_t TV, uint32_t TE>
 __device__ __forceinline__ bool phase_a(const LoopArgs& g, const LayerDev& L, int step, int l, int token, GemvLds& s) {
     const int nq = g.tiles_qkv[0] + g.tiles_qkv[1];
     const int total = nq + g.tiles_qkv[2];
@@ -271,7 +273,7 @@ __device__ __forceinline__ bool phase_a(const LoopArgs& g, const LayerDev& L, in
     const Stamps st = pst_ptr(g, step, l, 0);
     auto input = [&]() -> bool {
         if (l == 0) {
-            embed_to_lds(g, token, s);
+            embed_to_lds<TE>(g, token, s);
             return true;
         }
         const bool ok = tget_vec(g, g.ht, tag_of(g, step, l - 1, 5), s.x, g.embd_dim);
@@ -1024,7 +1026,7 @@ __global__ __launch_bounds__(kThreads) void k_loop(LoopArgs g) {
             const LayerDev& L = g.layers[l];
             if (g.trace != nullptr && blockIdx.x == 0 && threadIdx.x == 0) g.trace[1 + (step * g.n_layers + l) * 5] = wall_clock64();
             pst(pst_ptr(g, step, l, 0), 0);
-            if (!phase_a<TQ, TV>(g, L, step, l, token, lds.g)) return;
+            if (!phase_a<TQ, TV, TH>(g, L, step, l, token, lds.g)) return;
             pst(pst_ptr(g, step, l, 0), 7);
             __syncthreads();
             if (g.trace != nullptr && blockIdx.x == 0 && threadIdx.x == 0) g.trace[2 + (step * g.n_layers + l) * 5] = wall_clock64();

@@ -8,9 +8,11 @@ namespace bh {
 
 // Element e of row r of a packed matrix, dequantised as embedding_row does
 // (src/model.cpp:27-70, src/quant.cpp:196-239).
+// T: the format, known at compile time (kF32: read m.type at run time).
+template <uint32_t T = kF32>
 __device__ inline float dequant_elem(const Packed& m, uint32_t r, uint32_t e) {
     const uint32_t cols = m.cols;
-    switch (m.type) {
+    switch (T != kF32 ? T : m.type) {
         case kQ8_0: {
             const size_t blk = static_cast<size_t>(r) * (cols / 32) + e / 32;
             const float d = h2f(reinterpret_cast<const uint16_t*>(m.p1)[blk]);

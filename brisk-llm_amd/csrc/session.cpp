@@ -18,6 +18,7 @@
 #include <cstdlib>
 #include <cstring>
 #include <string>
+#include <thread>
 #include <vector>
 
 namespace bh {
@@ -32,6 +33,86 @@ void check(hipError_t e, const char* what) {
                     std::string("hip: ") + what + ": " + hipGetErrorString(e));
     }
 }
+
+// Host -> device uploads of the model's bytes through two pinned chunks.  The
+// host copies chunk i + 1 out of the caller's (usually memory-mapped) tensor
+// bytes while the DMA engine moves chunk i, so the transfer overlaps the host
+// reads instead of going through the runtime's pageable path, one blocking
+// copy at a time.  The host copy of a chunk is split over a few threads (a
+// single thread's memcpy from the page cache is slower than the link).  The
+// reference's loader maps the file and reads the tensors in place
+// (src/mapped_file.cpp:88-102); this is the device-side counterpart.
+class Uploader {
+public:
+    static constexpr size_t kChunk = size_t{32} << 20;
+    explicit Uploader(hipStream_t s) : s_(s) {
+        for (int k = 0; k < 2; ++k) {
+            if (hipHostMalloc(&buf_[k], kChunk, hipHostMallocDefault) != hipSuccess) buf_[k] = nullptr;
+            if (hipEventCreateWithFlags(&ev_[k], hipEventDisableTiming) != hipSuccess) ev_[k] = nullptr;
+        }
+        // BRISK_HIP_PAGEABLE_UPLOAD=1: the runtime's pageable copies (for comparison)
+        pinned_ = buf_[0] != nullptr && buf_[1] != nullptr && ev_[0] != nullptr && ev_[1] != nullptr &&
+                  std::getenv("BRISK_HIP_PAGEABLE_UPLOAD") == nullptr;
+        const unsigned hw = std::thread::hardware_concurrency();
+        threads_ = static_cast<int>(std::min(8u, std::max(1u, hw)));
+    }
+    ~Uploader() {
+        (void)hipStreamSynchronize(s_);
+        for (int k = 0; k < 2; ++k) {
+            if (buf_[k] != nullptr) (void)hipHostFree(buf_[k]);
+            if (ev_[k] != nullptr) (void)hipEventDestroy(ev_[k]);
+        }
+    }
+    Uploader(const Uploader&) = delete;
+    Uploader& operator=(const Uploader&) = delete;
+
+    // Enqueues dst[0, bytes) = src[0, bytes) on the stream; src may be reused on return.
+    void copy(void* dst, const void* src, size_t bytes) {
+        if (!pinned_) {  // no pinned memory: the runtime's blocking pageable copy
+            check(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, s_), "hipMemcpy(upload)");
+            check(hipStreamSynchronize(s_), "upload sync");
+            return;
+        }
+        for (size_t off = 0; off < bytes; off += kChunk) {
+            const size_t n = std::min(kChunk, bytes - off);
+            const int k = next_;
+            next_ ^= 1;
+            if (used_[k]) check(hipEventSynchronize(ev_[k]), "upload wait");  // the chunk's previous DMA is done
+            host_copy(buf_[k], static_cast<const uint8_t*>(src) + off, n);
+            check(hipMemcpyAsync(static_cast<uint8_t*>(dst) + off, buf_[k], n, hipMemcpyHostToDevice, s_), "hipMemcpy(upload)");
+            check(hipEventRecord(ev_[k], s_), "hipEventRecord(upload)");
+            used_[k] = true;
+        }
+    }
+    bool pinned() const { return pinned_; }
+
+private:
+    void host_copy(void* dst, const uint8_t* src, size_t n) const {
+        constexpr size_t kMinPerThread = size_t{2} << 20;
+        const int t = static_cast<int>(std::min<size_t>(threads_, std::max<size_t>(1, n / kMinPerThread)));
+        if (t <= 1) {
+            std::memcpy(dst, src, n);
+            return;
+        }
+        const size_t per = (n / t + 63) & ~static_cast<size_t>(63);
+        std::vector<std::thread> pool;
+        pool.reserve(t - 1);
+        for (int i = 1; i < t; ++i) {
+            const size_t a = std::min(n, per * i), b = std::min(n, per * (i + 1));
+            if (a < b) pool.emplace_back([=] { std::memcpy(static_cast<uint8_t*>(dst) + a, src + a, b - a); });
+        }
+        std::memcpy(dst, src, std::min(n, per));
+        for (auto& th : pool) th.join();
+    }
+
+    hipStream_t s_;
+    void* buf_[2] = {nullptr, nullptr};
+    hipEvent_t ev_[2] = {nullptr, nullptr};
+    bool used_[2] = {false, false};
+    int next_ = 0;
+    int threads_ = 1;
+    bool pinned_ = false;
+};
 
 }  // namespace
 
@@ -126,6 +207,8 @@ Session::Session(const brisk_hip_config& cfg, const brisk_hip_tensor* tensors, s
     }
     void* staging = nullptr;
     if (staging_bytes) check(hipMalloc(&staging, staging_bytes), "hipMalloc(staging)");
+    // stream order keeps a matrix's upload after the previous matrix's repack out of `staging`
+    Uploader up(stream_);
 
     auto load_matrix = [&](const std::string& name, size_t rows, size_t cols, DeviceMatrix& m) {
         const brisk_hip_tensor* t = find(name);
@@ -143,9 +226,8 @@ Session::Session(const brisk_hip_config& cfg, const brisk_hip_tensor* tensors, s
         // x86's load-time TQ2_0x16 layout (rows % 16 == 0) takes 7-bit activations (src/model.cpp:496-503)
         if (type == kTQ2_0 && rows % 16 == 0) m.p.flags |= kFlagLut16;
         const size_t bytes = rows * (cols / block_elems(type)) * gguf_block_bytes(type);
-        check(hipMemcpyAsync(staging, t->data, bytes, hipMemcpyHostToDevice, stream_), "hipMemcpy(weights)");
+        up.copy(staging, t->data, bytes);
         check(launch_pack(type, staging, rows, cols, m.p, stream_), "pack");
-        check(hipStreamSynchronize(stream_), "pack sync");
         weight_bytes_ += bytes;
     };
     auto load_vector = [&](const std::string& name, size_t count) -> float* {
@@ -154,7 +236,7 @@ Session::Session(const brisk_hip_config& cfg, const brisk_hip_tensor* tensors, s
         if (t->rows * t->cols != count) model_fail("tensor '" + name + "' has an unexpected size");
         if (t->type != BRISK_HIP_F32) model_fail("tensor '" + name + "' is not F32");
         float* p = static_cast<float*>(alloc(count * sizeof(float)));
-        check(hipMemcpyAsync(p, t->data, count * sizeof(float), hipMemcpyHostToDevice, stream_), "hipMemcpy(vector)");
+        up.copy(p, t->data, count * sizeof(float));
         return p;
     };
 
@@ -200,6 +282,7 @@ Session::Session(const brisk_hip_config& cfg, const brisk_hip_tensor* tensors, s
             takes_q8_k(L.gate.p.type) != takes_q8_k(L.up.p.type) || act_bits(L.gate.p) != act_bits(L.up.p))
             model_fail("fused multiply mixes activation widths");
     }
+    check(hipStreamSynchronize(stream_), "upload sync");
     if (staging) check(hipFree(staging), "hipFree(staging)");
 
     // activations and state
@@ -374,6 +457,7 @@ void Session::setup_loop() {
     if (debug_) return;
     // the loop's split attention merges at most 4 outputs a thread (heads per kv head x head size <= 1024)
     if ((cfg_.heads / cfg_.kv_heads) * cfg_.head_dim > 4 * kThreads) return;
+    if (embd_.p.type != out_->p.type) return;  // the loop reads the embedding in its output's format
     const Layer& L0 = layers_[0];
     const void* k = find_loop_kernel(L0.q.p.type, L0.v.p.type, L0.o.p.type, L0.gate.p.type, L0.down.p.type, out_->p.type);
     if (k == nullptr) return;
