@@ -2,7 +2,7 @@
 
 Restates the part of the reference's loader the HIP session needs:
 ``Model::parse_config`` (src/model.cpp:161-301) for the families the HIP
-session runs (qwen3, llama, bitnet, qwen2, smollm3), the tensor names and shapes of
+session runs (qwen3, llama, bitnet, qwen2, smollm3, gemma3), the tensor names and shapes of
 ``Model::Model`` (src/model.cpp:303-423) and the tied output projection
 (src/model.cpp:328-330).  The session takes the weights as GGUF-layout bytes,
 as the reference's ``Model(file, repack = false)`` hands them to a GPU session.
@@ -11,11 +11,13 @@ from __future__ import annotations
 
 from dataclasses import dataclass
 
+import numpy as np
+
 from . import gguf as G
 
-ARCH_QWEN3, ARCH_LLAMA, ARCH_BITNET, ARCH_QWEN2, ARCH_SMOLLM3 = 0, 1, 2, 3, 4
+ARCH_QWEN3, ARCH_LLAMA, ARCH_BITNET, ARCH_QWEN2, ARCH_SMOLLM3, ARCH_GEMMA3 = 0, 1, 2, 3, 4, 5
 _ARCH = {"qwen3": ARCH_QWEN3, "llama": ARCH_LLAMA, "bitnet": ARCH_BITNET, "bitnet-b1.58": ARCH_BITNET,
-         "qwen2": ARCH_QWEN2, "smollm3": ARCH_SMOLLM3}
+         "qwen2": ARCH_QWEN2, "smollm3": ARCH_SMOLLM3, "gemma3": ARCH_GEMMA3}
 QUANT_TYPES = (G.T_Q4_0, G.T_Q4_1, G.T_Q5_0, G.T_Q8_0, G.T_Q4_K, G.T_Q5_K, G.T_Q6_K, G.T_TQ2_0)
 
 
@@ -41,6 +43,11 @@ class ModelConfig:
     context: int
     rope_base: float
     eps: float
+    # Gemma 3 (src/model.cpp:170-176); zero for the other families
+    sliding_window: int = 0
+    rope_base_local: float = 0.0
+    rope_scale: float = 0.0
+    final_softcap: float = 0.0
 
     @property
     def rope_neox(self) -> bool:  # src/model.cpp:167
@@ -61,7 +68,7 @@ class ModelConfig:
 def parse_config(f: G.GgufFile) -> ModelConfig:
     name = f.get("general.architecture")
     if name not in _ARCH:
-        fail(f"unsupported architecture '{name}'; the HIP session runs qwen3, qwen2, llama, smollm3 and bitnet")
+        fail(f"unsupported architecture '{name}'; the HIP session runs qwen3, qwen2, llama, smollm3, gemma3 and bitnet")
     p = name + "."
 
     def u32(key):
@@ -92,8 +99,14 @@ def parse_config(f: G.GgufFile) -> ModelConfig:
     emb = f.tensor("token_embd.weight")
     if emb is None or len(emb.dims) != 2 or emb.dims[0] != embd:
         fail("missing or misshapen token_embd.weight")
-    return ModelConfig(_ARCH[name], name, int(emb.dims[1]), embd, layers, heads, kv, head_dim, ff, ctx,
-                       f32("rope.freq_base"), f32("attention.layer_norm_rms_epsilon"))
+    cfg = ModelConfig(_ARCH[name], name, int(emb.dims[1]), embd, layers, heads, kv, head_dim, ff, ctx,
+                      f32("rope.freq_base"), f32("attention.layer_norm_rms_epsilon"))
+    if cfg.arch == ARCH_GEMMA3:
+        cfg.sliding_window = int(f.get(p + "attention.sliding_window", 0))
+        cfg.rope_base_local = float(f.get(p + "rope.freq_base_swa", 10000.0))
+        cfg.rope_scale = float(np.float32(1.0) / np.float32(f.get(p + "rope.scaling.factor", 1.0)))  # in float
+        cfg.final_softcap = float(f.get(p + "final_logit_softcapping", 0.0))
+    return cfg
 
 
 @dataclass
@@ -142,9 +155,12 @@ def tensor_table(f: G.GgufFile, cfg: ModelConfig) -> list:
         mat(b + "attn_q.weight", qd, e)
         mat(b + "attn_k.weight", kvd, e)
         mat(b + "attn_v.weight", kvd, e)
-        if cfg.arch == ARCH_QWEN3:
+        if cfg.arch in (ARCH_QWEN3, ARCH_GEMMA3):
             vec(b + "attn_q_norm.weight", cfg.head_dim)
             vec(b + "attn_k_norm.weight", cfg.head_dim)
+        if cfg.arch == ARCH_GEMMA3:
+            vec(b + "post_attention_norm.weight", e)
+            vec(b + "post_ffw_norm.weight", e)
         if cfg.arch == ARCH_BITNET:
             vec(b + "attn_sub_norm.weight", e)
             vec(b + "ffn_sub_norm.weight", cfg.ff)

@@ -172,6 +172,7 @@ class ModelSpec:
     embd_fmt: int = G.T_Q8_0
     out_fmt: int | None = G.T_Q8_0            # None: tied to token_embd (src/model.cpp:328-330)
     seed: int = 1
+    extra: dict = field(default_factory=dict)  # further "<arch>.<key>" metadata: key -> (GGUF type, value)
 
     @property
     def query_dim(self):
@@ -237,6 +238,12 @@ SPECS = {
     "tiny-qwen2": ModelSpec("tiny-qwen2", "qwen2", 256, 2, 4, 2, 64, 512, 1000, 1e6, context=1024, fmt=_uniform4(G.T_Q4_0)),
     "tiny-smollm3": ModelSpec("tiny-smollm3", "smollm3", 512, 8, 8, 2, 64, 768, 1000, 5e5, eps=1e-5, context=1024,
                               fmt={**_uniform4(G.T_Q4_K), "v": G.T_Q6_K, "down": G.T_Q6_K}, embd_fmt=G.T_Q6_K, out_fmt=None),
+    # Gemma 3: layers 0-4 and 6 slide over the last 8 positions (local RoPE base), 5 is global with
+    # positions scaled by 1/2; logits soft-capped at 30; the Q8_0 embedding rows scaled by sqrt(embd).
+    "tiny-gemma3": ModelSpec("tiny-gemma3", "gemma3", 256, 7, 4, 1, 64, 512, 1000, 1e6, context=1024,
+                             fmt=_uniform4(G.T_Q8_0),
+                             extra={"attention.sliding_window": (G.U32, 8), "rope.freq_base_swa": (G.F32, 10000.0),
+                                    "rope.scaling.factor": (G.F32, 2.0), "final_logit_softcapping": (G.F32, 30.0)}),
     "tiny-q5": ModelSpec("tiny-q5", "qwen3", 256, 2, 4, 2, 64, 512, 1000, 1e6, context=1024,
                          fmt={**_uniform4(G.T_Q5_0), "o": G.T_Q4_1, "down": G.T_Q4_1}),
 }
@@ -277,6 +284,8 @@ def write_model(spec: ModelSpec, path: str) -> str:
     w.add(f"{a}.context_length", G.U32, spec.context)
     w.add(f"{a}.rope.freq_base", G.F32, spec.rope_base)
     w.add(f"{a}.attention.layer_norm_rms_epsilon", G.F32, spec.eps)
+    for key, (vtype, value) in spec.extra.items():
+        w.add(f"{a}.{key}", vtype, value)
     _matrix(w, spec, "token_embd.weight", spec.vocab, spec.embd, spec.embd_fmt)
     _vector(w, spec, "output_norm.weight", spec.embd)
     if spec.out_fmt is not None:
@@ -287,9 +296,12 @@ def write_model(spec: ModelSpec, path: str) -> str:
         _matrix(w, spec, b + "attn_q.weight", spec.query_dim, spec.embd, spec.fmt["q"])
         _matrix(w, spec, b + "attn_k.weight", spec.kv_dim, spec.embd, spec.fmt["k"])
         _matrix(w, spec, b + "attn_v.weight", spec.kv_dim, spec.embd, spec.fmt["v"])
-        if a == "qwen3":
+        if a in ("qwen3", "gemma3"):
             _vector(w, spec, b + "attn_q_norm.weight", spec.head_dim)
             _vector(w, spec, b + "attn_k_norm.weight", spec.head_dim)
+        if a == "gemma3":
+            _vector(w, spec, b + "post_attention_norm.weight", spec.embd)
+            _vector(w, spec, b + "post_ffw_norm.weight", spec.embd)
         if a.startswith("bitnet"):
             _vector(w, spec, b + "attn_sub_norm.weight", spec.embd)
             _vector(w, spec, b + "ffn_sub_norm.weight", spec.ff)

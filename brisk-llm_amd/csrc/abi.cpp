@@ -166,6 +166,10 @@ int brisk_hip_expf(const float* x, float* y, size_t n, void* stream) {
     return guarded([&] { hip_check(bh::launch_expf(x, y, n, static_cast<hipStream_t>(stream)), "expf"); });
 }
 
+int brisk_hip_tanhf(const float* x, float* y, size_t n, void* stream) {
+    return guarded([&] { hip_check(bh::launch_tanhf(x, y, n, static_cast<hipStream_t>(stream)), "tanhf"); });
+}
+
 int brisk_hip_div_selftest(unsigned long long* mismatches) {
     return guarded([&] {
         unsigned long long* d = nullptr;

@@ -137,6 +137,110 @@ __device__ __forceinline__ float ref_expf_impl(float x) {
 __device__ inline float ref_expf(float x) { return ref_expf_impl<false>(x); }
 __device__ __forceinline__ float ref_expf_s(float x) { return ref_expf_impl<true>(x); }
 
+// ---------------------------------------------------------------- tanh
+
+// tanhf and expm1f as the reference's host libm computes them (std::tanh on a
+// float: gelu_mul_f32, src/kernels_f32.cpp:291-296, and the final softcap,
+// src/model.cpp:1206-1209).  glibc 2.35 builds both from fdlibm's s_tanhf.c
+// and s_expm1f.c (Sun Microsystems' freely distributable fdlibm 5.3; no FMA
+// variant on x86-64): expm1 reduces x by k ln2 split in a hi and a lo part,
+// takes a rational form in the reduced argument with five scaled
+// coefficients, and puts k back into the exponent; tanh is 1 - 2 / (expm1(2|x|)
+// + 2) for |x| >= 1 and -expm1(-2|x|) / (expm1(-2|x|) + 2) below.  This
+// restatement gives glibc's result for every one of the 2^32 float inputs
+// (checked exhaustively on the host).
+__device__ __forceinline__ float bits_to_f(uint32_t u) { return __uint_as_float(u); }
+
+__device__ inline float ref_expm1f(float x) {
+    const float one = 1.0f, huge = 1.0e+30f, tiny = 1.0e-30f, o_threshold = 8.8721679688e+01f;
+    const float ln2_hi = 6.9313812256e-01f, ln2_lo = 9.0580006145e-06f, invln2 = 1.4426950216e+00f;
+    const float Q1 = -3.3333335072e-02f, Q2 = 1.5873016091e-03f, Q3 = -7.9365076090e-05f, Q4 = 4.0082177293e-06f,
+                Q5 = -2.0109921195e-07f;
+    float y, hi, lo, c = 0.0f, t, e;
+    int k;
+    uint32_t hx = __float_as_uint(x);
+    const uint32_t xsb = hx & 0x80000000u;
+    hx &= 0x7fffffffu;
+    if (hx >= 0x4195b844u) {  // |x| >= 27 ln2
+        if (hx >= 0x42b17218u) {
+            if (hx > 0x7f800000u) return x + x;
+            if (hx == 0x7f800000u) return xsb == 0 ? x : -1.0f;
+            if (x > o_threshold) return huge * huge;
+        }
+        if (xsb != 0) return tiny - one;
+    }
+    if (hx > 0x3eb17218u) {  // |x| > ln2 / 2
+        if (hx < 0x3F851592u) {  // and < 3 ln2 / 2
+            if (xsb == 0) { hi = x - ln2_hi; lo = ln2_lo; k = 1; }
+            else { hi = x + ln2_hi; lo = -ln2_lo; k = -1; }
+        } else {
+            k = static_cast<int>(invln2 * x + (xsb == 0 ? 0.5f : -0.5f));
+            t = static_cast<float>(k);
+            hi = x - t * ln2_hi;
+            lo = t * ln2_lo;
+        }
+        x = hi - lo;
+        c = (hi - x) - lo;
+    } else if (hx < 0x33000000u) {  // |x| < 2^-25
+        t = huge + x;
+        return x - (t - (huge + x));
+    } else {
+        k = 0;
+    }
+    const float hfx = 0.5f * x, hxs = x * hfx;
+    const float r1 = one + hxs * (Q1 + hxs * (Q2 + hxs * (Q3 + hxs * (Q4 + hxs * Q5))));
+    t = 3.0f - r1 * hfx;
+    e = hxs * ((r1 - t) / (6.0f - x * t));
+    if (k == 0) return x - (x * e - hxs);
+    e = (x * (e - c) - c);
+    e -= hxs;
+    if (k == -1) return 0.5f * (x - e) - 0.5f;
+    if (k == 1) {
+        if (x < -0.25f) return -2.0f * (e - (x + 0.5f));
+        return one + 2.0f * (x - e);
+    }
+    if (k <= -2 || k > 56) {
+        y = one - (e - x);
+        return bits_to_f(__float_as_uint(y) + (static_cast<uint32_t>(k) << 23)) - one;
+    }
+    if (k < 23) {
+        t = bits_to_f(0x3f800000u - (0x1000000u >> k));
+        y = t - (e - x);
+    } else {
+        t = bits_to_f(static_cast<uint32_t>(0x7f - k) << 23);
+        y = x - (e + t);
+        y += one;
+    }
+    return bits_to_f(__float_as_uint(y) + (static_cast<uint32_t>(k) << 23));
+}
+
+__device__ inline float ref_tanhf(float x) {
+    const float one = 1.0f, two = 2.0f, tiny = 1.0e-30f;
+    const uint32_t jx = __float_as_uint(x), ix = jx & 0x7fffffffu;
+    float z;
+    if (ix >= 0x7f800000u) return (jx & 0x80000000u) == 0 ? one / x + one : one / x - one;
+    if (ix < 0x41b00000u) {  // |x| < 22
+        if (ix == 0) return x;
+        if (ix < 0x24000000u) return x * (one + x);
+        if (ix >= 0x3f800000u) {
+            const float t = ref_expm1f(two * fabsf(x));
+            z = one - two / (t + two);
+        } else {
+            const float t = ref_expm1f(-two * fabsf(x));
+            z = -t / (t + two);
+        }
+    } else {
+        z = one - tiny;
+    }
+    return (jx & 0x80000000u) == 0 ? z : -z;
+}
+
+// gelu_mul_f32's gate (src/kernels_f32.cpp:291-296): 0.5 x (1 + tanh(sqrt(2/pi) (x + 0.044715 x^3))),
+// in its left-to-right order, times up.
+__device__ __forceinline__ float gelu_mul(float x, float up) {
+    return 0.5f * x * (1.0f + ref_tanhf(0.7978845608f * (x + 0.044715f * x * x * x))) * up;
+}
+
 __device__ __forceinline__ int dot4(int a, int b, int c) { return __builtin_amdgcn_sdot4(a, b, c, false); }
 
 // ---------------------------------------------------------------- reductions

@@ -212,6 +212,8 @@ __global__ __launch_bounds__(kThreads) void k_gateup(GateUpArgs g) {
         if (g.relu2) {
             const float q = gv > 0.0f ? gv : 0.0f;
             out = q * q * uv;
+        } else if (g.gelu) {
+            out = gelu_mul(gv, uv);
         } else {
             out = gv / (1.0f + ref_expf(-gv)) * uv;
         }
@@ -242,7 +244,8 @@ __global__ __launch_bounds__(kThreads) void k_head(HeadArgs g) {
     if (threadIdx.x < 64) {  // R <= 64: the first wave holds the tile's rows
         unsigned long long key = 0;
         if (r < static_cast<uint32_t>(g.R) && row < g.m.rows) {
-            const float v = sums[r];
+            float v = sums[r];
+            if (g.softcap != 0.0f) v = g.softcap * ref_tanhf(v / g.softcap);  // src/model.cpp:1206-1209
             if (g.logits != nullptr) g.logits[row] = v;
             key = pick_key(v, row);
         }
@@ -282,7 +285,16 @@ __global__ __launch_bounds__(kThreads) void k_attn(AttnArgs g) {
     __shared__ AttnLds s;
     __shared__ bool last;
     const int kv = blockIdx.x, split = blockIdx.y;
-    const int pos = *g.pos, L = pos + 1;
+    // A sliding layer sees positions start .. pos (src/model.cpp:1084-1085): the cache
+    // rows and the RoPE table are taken from `start` on, and positions counted from there.
+    const int pos_abs = *g.pos, start = g.window > 0 && pos_abs + 1 > g.window ? pos_abs + 1 - g.window : 0;
+    if (start > 0) {
+        const size_t shift = static_cast<size_t>(start) * g.head_dim;
+        g.kcache += shift;
+        g.vcache += shift;
+        if (g.rope != nullptr) g.rope += shift;
+    }
+    const int pos = pos_abs - start, L = pos + 1;
     const bool exact = attn_is_exact(L, g.heads / g.kv_heads);
     if (exact ? split != 0 : split * kSplit >= L) return;
     attn_prologue<PlainIO>(g, s, kv, pos, exact || split == pos / kSplit);
@@ -309,12 +321,30 @@ __global__ __launch_bounds__(kThreads) void k_attn(AttnArgs g) {
 // embedding_row (src/model.cpp:27-70): dequantise row *token of the packed embedding.
 // Starts a step: finalizes the previous step's pick, if one is pending, then
 // dequantises the row of token seq[pos].
-__global__ __launch_bounds__(kThreads) void k_embed(Packed m, PickState ps, float* __restrict__ h) {
+// Gemma's rows are then multiplied by sqrt(embd) (src/model.cpp:899-901; scale 1 elsewhere).
+__global__ __launch_bounds__(kThreads) void k_embed(Packed m, PickState ps, float* __restrict__ h, float scale) {
     __shared__ int tok;
     if (threadIdx.x == 0) tok = ps.seq[finalize_pick(ps)];
     __syncthreads();
     const uint32_t r = static_cast<uint32_t>(tok);
-    for (uint32_t e = threadIdx.x; e < m.cols; e += kThreads) h[e] = dequant_elem(m, r, e);
+    for (uint32_t e = threadIdx.x; e < m.cols; e += kThreads) {
+        const float v = dequant_elem(m, r, e);
+        h[e] = scale != 1.0f ? v * scale : v;
+    }
+}
+
+// h += rms_norm(p, w) (src/model.cpp:1113-1121, :1153-1160): one workgroup.
+__global__ __launch_bounds__(kThreads) void k_post_add(float* __restrict__ h, const float* __restrict__ p,
+                                                       const float* __restrict__ w, float eps, int n) {
+    __shared__ double red[4];
+    const float scale = rms_scale(block_sumsq(p, n, red), n, eps);
+    for (int i = threadIdx.x; i < n; i += kThreads) h[i] = h[i] + p[i] * scale * w[i];
+}
+
+// tanhf as the Gemma epilogues compute it (ref_tanhf), for the parity tests.
+__global__ void k_tanhf(const float* __restrict__ x, float* __restrict__ y, size_t n) {
+    const size_t i = static_cast<size_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (i < n) y[i] = ref_tanhf(x[i]);
 }
 
 // expf as the token loop computes it (ref_expf), for the parity tests.
@@ -519,8 +549,19 @@ hipError_t launch_attention(const AttnArgs& g, hipStream_t s) {
 
 int attention_max_splits(int ctx) { return (ctx + kSplit - 1) / kSplit; }
 
-hipError_t launch_embed(const Packed& m, const PickState& ps, float* h, hipStream_t s) {
-    hipLaunchKernelGGL(k_embed, dim3(1), dim3(kThreads), 0, s, m, ps, h);
+hipError_t launch_post_add(float* h, const float* p, const float* w, float eps, int n, hipStream_t s) {
+    hipLaunchKernelGGL(k_post_add, dim3(1), dim3(kThreads), 0, s, h, p, w, eps, n);
+    return hipGetLastError();
+}
+
+hipError_t launch_tanhf(const float* x, float* y, size_t n, hipStream_t s) {
+    if (n == 0) return hipSuccess;
+    hipLaunchKernelGGL(k_tanhf, dim3(static_cast<unsigned>((n + 255) / 256)), dim3(256), 0, s, x, y, n);
+    return hipGetLastError();
+}
+
+hipError_t launch_embed(const Packed& m, const PickState& ps, float* h, float scale, hipStream_t s) {
+    hipLaunchKernelGGL(k_embed, dim3(1), dim3(kThreads), 0, s, m, ps, h, scale);
     return hipGetLastError();
 }
 

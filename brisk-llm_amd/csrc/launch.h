@@ -36,6 +36,7 @@ struct GateUpArgs {
     const float* normw;   // ffn_norm
     float eps;
     int relu2;            // BitNet squared-ReLU gate
+    int gelu;             // Gemma GELU (tanh form) gate
     float* act;
 };
 
@@ -51,6 +52,7 @@ struct AttnArgs {
     const float* rope;    // [max_context][head_dim] cos, sin pairs; null on a layer without RoPE (SmolLM3)
     float eps;
     int neox;
+    int window;           // a sliding layer's last `window` positions (Gemma 3); 0: every position
     uint16_t* kcache;     // this layer's [kv_heads][ctx][head_dim]
     uint16_t* vcache;
     const int* pos;
@@ -81,6 +83,7 @@ struct HeadArgs {
     float eps;
     float* logits;        // or null
     unsigned long long* key;   // the step's pick key (PickState::key)
+    float softcap;        // logits = c tanh(logits / c) before the pick (Gemma); 0: none
 };
 
 hipError_t launch_pack(uint32_t type, const void* src, size_t rows, size_t cols, const Packed& dst, hipStream_t s);
@@ -89,11 +92,14 @@ hipError_t launch_matvec_q8(const Packed& m, const void* xq, size_t n, float* ou
 hipError_t launch_gemv(GemvArgs g, hipStream_t s);
 hipError_t launch_gateup(GateUpArgs g, hipStream_t s);
 hipError_t launch_attention(const AttnArgs& g, hipStream_t s);
-hipError_t launch_embed(const Packed& m, const PickState& ps, float* h, hipStream_t s);
+hipError_t launch_embed(const Packed& m, const PickState& ps, float* h, float scale, hipStream_t s);
+// h += rms_norm(p, w) over n values (Gemma's post-attention / post-feed-forward norm).
+hipError_t launch_post_add(float* h, const float* p, const float* w, float eps, int n, hipStream_t s);
 hipError_t launch_finalize(const PickState& ps, hipStream_t s);
 hipError_t launch_head(HeadArgs g, hipStream_t s);
 hipError_t launch_advance(int* pos, hipStream_t s);
 hipError_t launch_expf(const float* x, float* y, size_t n, hipStream_t s);
+hipError_t launch_tanhf(const float* x, float* y, size_t n, hipStream_t s);
 hipError_t launch_div_selftest(unsigned long long* bad, hipStream_t s);
 hipError_t launch_mfma_rate(int shape, int blocks, int iters, int* out, hipStream_t s);
 int attention_max_splits(int ctx);

@@ -142,6 +142,7 @@ brisk_hip_memory estimate_session(const brisk_hip_config& cfg, const brisk_hip_t
     size_t sc = (e + 2 * qd + ff + cfg.vocab + 2 * kvd) * 4;              // token-path activations, logits
     sc += static_cast<size_t>(cfg.heads) * splits * (hd + 2) * 4;          // attention partials
     sc += (ctx + 1) * 4 + ctx * hd * 4;                                    // token sequence, RoPE table
+    if (cfg.arch == BRISK_HIP_ARCH_GEMMA3) sc += ctx * hd * 4 + e * 4;     // local RoPE table, post-norm input
     sc += (e + 2 * qd + 2 * kvd + ff + static_cast<size_t>(cfg.heads) * splits * (hd + 2)) * 8;  // hand-off words
     const size_t T = Session::kPrefillTokens, widest = std::max(std::max(e, qd), ff), stride = (widest + 255) / 256 * 256;
     sc += T * (e + 2 * qd + 2 * kvd + ff) * 4 + T * stride * (1 + 4 / 32.0 + 4 / 16.0);  // prefill buffers
@@ -166,7 +167,7 @@ Session::Session(const brisk_hip_config& cfg, const brisk_hip_tensor* tensors, s
     int count = 0;
     if (hipGetDeviceCount(&count) != hipSuccess || count == 0) throw Error(BRISK_HIP_ENODEV, "hip: no GPU device available");
     if (device < 0 || device >= count) throw Error(BRISK_HIP_ENODEV, "hip: no GPU device " + std::to_string(device));
-    if (cfg.arch < BRISK_HIP_ARCH_QWEN3 || cfg.arch > BRISK_HIP_ARCH_SMOLLM3) model_fail("unsupported architecture");
+    if (cfg.arch < BRISK_HIP_ARCH_QWEN3 || cfg.arch > BRISK_HIP_ARCH_GEMMA3) model_fail("unsupported architecture");
     if (cfg.embd == 0 || cfg.layers == 0 || cfg.heads == 0 || cfg.kv_heads == 0 || cfg.ff == 0 || cfg.context_length == 0 ||
         cfg.vocab == 0)
         model_fail("a model dimension is zero");
@@ -262,7 +263,7 @@ Session::Session(const brisk_hip_config& cfg, const brisk_hip_tensor* tensors, s
         load_matrix(b + "ffn_gate.weight", cfg.ff, e, L.gate);
         load_matrix(b + "ffn_up.weight", cfg.ff, e, L.up);
         load_matrix(b + "ffn_down.weight", e, cfg.ff, L.down);
-        if (cfg.arch == BRISK_HIP_ARCH_QWEN3) {
+        if (cfg.arch == BRISK_HIP_ARCH_QWEN3 || cfg.arch == BRISK_HIP_ARCH_GEMMA3) {
             L.q_norm = load_vector(b + "attn_q_norm.weight", hd);
             L.k_norm = load_vector(b + "attn_k_norm.weight", hd);
         }
@@ -276,6 +277,11 @@ Session::Session(const brisk_hip_config& cfg, const brisk_hip_tensor* tensors, s
             L.v_bias = load_vector(b + "attn_v.bias", kvd);
         }
         L.rope = !(cfg.arch == BRISK_HIP_ARCH_SMOLLM3 && (l + 1) % 4 == 0);  // layer_has_rope (src/model.h:110, :168)
+        if (cfg.arch == BRISK_HIP_ARCH_GEMMA3) {  // src/model.cpp:399-402; layer_slides, src/model.h:87-90
+            L.attn_post_norm = load_vector(b + "post_attention_norm.weight", e);
+            L.ffn_post_norm = load_vector(b + "post_ffw_norm.weight", e);
+            L.slides = cfg.sliding_window != 0 && l % 6 != 5;
+        }
         // one activation row feeds Q, K and V: they must take the same width (src/model.cpp:584-590)
         if (takes_q8_k(L.q.p.type) != takes_q8_k(L.k.p.type) || takes_q8_k(L.q.p.type) != takes_q8_k(L.v.p.type) ||
             act_bits(L.q.p) != act_bits(L.k.p) || act_bits(L.q.p) != act_bits(L.v.p) ||
@@ -317,11 +323,13 @@ Session::Session(const brisk_hip_config& cfg, const brisk_hip_tensor* tensors, s
 
     // RoPE table, built on the host exactly as build_rope does (src/model.cpp:880-894):
     // theta_scale = base^(-2/dim); theta = pos * scale, multiplied by theta_scale per pair.
-    {
+    // Gemma 3: the global layers' positions are scaled by 1 / rope.scaling.factor, the
+    // sliding layers take their own base at scale 1 (src/model.cpp:893-894).
+    auto rope_table = [&](float base, float scale) {
         std::vector<float> rope(max_ctx_ * hd);
-        const float theta_scale = std::pow(cfg.rope_base, -2.0f / static_cast<float>(hd));
+        const float theta_scale = std::pow(base, -2.0f / static_cast<float>(hd));
         for (size_t p = 0; p < max_ctx_; ++p) {
-            float theta = static_cast<float>(p) * 1.0f;
+            float theta = static_cast<float>(p) * scale;
             float* r = rope.data() + p * hd;
             for (size_t i = 0; i < hd / 2; ++i) {
                 r[2 * i] = std::cos(theta) * 1.0f;
@@ -329,8 +337,15 @@ Session::Session(const brisk_hip_config& cfg, const brisk_hip_tensor* tensors, s
                 theta *= theta_scale;
             }
         }
-        rope_ = static_cast<float*>(alloc(rope.size() * 4));
-        check(hipMemcpy(rope_, rope.data(), rope.size() * 4, hipMemcpyHostToDevice), "hipMemcpy(rope)");
+        float* d = static_cast<float*>(alloc(rope.size() * 4));
+        check(hipMemcpy(d, rope.data(), rope.size() * 4, hipMemcpyHostToDevice), "hipMemcpy(rope)");
+        return d;
+    };
+    rope_ = rope_table(cfg.rope_base, gemma() && cfg.rope_scale != 0.0f ? cfg.rope_scale : 1.0f);
+    if (gemma()) {
+        if (cfg.sliding_window != 0) rope_local_ = rope_table(cfg.rope_base_local, 1.0f);
+        proj_ = static_cast<float*>(alloc(e * 4));
+        embd_scale_ = std::sqrt(static_cast<float>(cfg.embd));
     }
     check(hipStreamSynchronize(stream_), "init sync");
     debug_ = std::getenv("BRISK_HIP_DEBUG") != nullptr;
@@ -366,7 +381,7 @@ void* Session::alloc(size_t bytes) {
 // One decode step at *pos_: embed seq[*pos_], every layer, then either the
 // output projection + greedy pick (which advances *pos_) or a bare advance.
 void Session::record_step(bool full) {
-    check(launch_embed(embd_.p, pick_state(), h_, stream_), "embed");
+    check(launch_embed(embd_.p, pick_state(), h_, embd_scale_, stream_), "embed");
     const float scale = 1.0f / std::sqrt(static_cast<float>(cfg_.head_dim));  // src/model.cpp:978
     for (uint32_t l = 0; l < cfg_.layers; ++l) {
         const Layer& L = layers_[l];
@@ -393,7 +408,9 @@ void Session::record_step(bool full) {
         }
 
         AttnArgs aa{};
-        aa.q = q_; aa.k = k_; aa.v = v_; aa.qnorm = L.q_norm; aa.knorm = L.k_norm; aa.rope = L.rope ? rope_ : nullptr;
+        aa.q = q_; aa.k = k_; aa.v = v_; aa.qnorm = L.q_norm; aa.knorm = L.k_norm;
+        aa.rope = !L.rope ? nullptr : L.slides ? rope_local_ : rope_;
+        aa.window = L.slides ? static_cast<int>(cfg_.sliding_window) : 0;
         aa.qbias = L.q_bias; aa.kbias = L.k_bias; aa.vbias = L.v_bias;
         aa.eps = cfg_.rms_epsilon; aa.neox = neox();
         aa.kcache = kcache_[l]; aa.vcache = vcache_[l]; aa.pos = pos_;
@@ -403,26 +420,29 @@ void Session::record_step(bool full) {
         aa.tickets = ticket_ + 4; aa.out = att_;
         check(launch_attention(aa, stream_), "attention");
 
+        // h += W_o att, or with a post-norm h += rms_norm(W_o att) (src/model.cpp:1113-1121)
         GemvArgs oa{};
-        oa.n = 1; oa.t[0].m = L.o.p; oa.t[0].out = h_;
-        oa.x = att_; oa.normw = L.attn_sub_norm; oa.eps = cfg_.rms_epsilon; oa.add = 1;
+        oa.n = 1; oa.t[0].m = L.o.p; oa.t[0].out = L.attn_post_norm ? proj_ : h_;
+        oa.x = att_; oa.normw = L.attn_sub_norm; oa.eps = cfg_.rms_epsilon; oa.add = L.attn_post_norm ? 0 : 1;
         check(launch_gemv(oa, stream_), "attn_output");
+        if (L.attn_post_norm) check(launch_post_add(h_, proj_, L.attn_post_norm, cfg_.rms_epsilon, static_cast<int>(cfg_.embd), stream_), "post norm");
 
         GateUpArgs ga{};
         ga.gate = L.gate.p; ga.up = L.up.p; ga.x = h_; ga.normw = L.ffn_norm; ga.eps = cfg_.rms_epsilon;
-        ga.relu2 = cfg_.arch == BRISK_HIP_ARCH_BITNET; ga.act = act_;
+        ga.relu2 = cfg_.arch == BRISK_HIP_ARCH_BITNET; ga.gelu = gemma(); ga.act = act_;
         check(launch_gateup(ga, stream_), "gate_up");
 
         GemvArgs da{};
-        da.n = 1; da.t[0].m = L.down.p; da.t[0].out = h_;
-        da.x = act_; da.normw = L.ffn_sub_norm; da.eps = cfg_.rms_epsilon; da.add = 1;
+        da.n = 1; da.t[0].m = L.down.p; da.t[0].out = L.ffn_post_norm ? proj_ : h_;
+        da.x = act_; da.normw = L.ffn_sub_norm; da.eps = cfg_.rms_epsilon; da.add = L.ffn_post_norm ? 0 : 1;
         check(launch_gemv(da, stream_), "ffn_down");
+        if (L.ffn_post_norm) check(launch_post_add(h_, proj_, L.ffn_post_norm, cfg_.rms_epsilon, static_cast<int>(cfg_.embd), stream_), "post norm");
         if (debug_) debug_layer(l);
     }
     if (full) {
         HeadArgs ha{};
         ha.m = out_->p; ha.x = h_; ha.normw = out_norm_; ha.eps = cfg_.rms_epsilon; ha.logits = logits_;
-        ha.key = key_;
+        ha.key = key_; ha.softcap = gemma() ? cfg_.final_softcap : 0.0f;
         check(launch_head(ha, stream_), "output");
     } else {
         check(launch_advance(pos_, stream_), "advance");
@@ -458,6 +478,7 @@ void Session::setup_loop() {
     // the loop's split attention merges at most 4 outputs a thread (heads per kv head x head size <= 1024)
     if ((cfg_.heads / cfg_.kv_heads) * cfg_.head_dim > 4 * kThreads) return;
     if (embd_.p.type != out_->p.type) return;  // the loop reads the embedding in its output's format
+    if (gemma()) return;  // post-norms, sliding windows and the softcap are phases of the graph path only
     const Layer& L0 = layers_[0];
     const void* k = find_loop_kernel(L0.q.p.type, L0.v.p.type, L0.o.p.type, L0.gate.p.type, L0.down.p.type, out_->p.type);
     if (k == nullptr) return;
@@ -678,7 +699,7 @@ bool Session::use_prefill(size_t n) const {
     // the exact-order prefill attention keeps every score of a token's query heads in LDS
     const bool exact_fits = (position_ + n) * (cfg_.heads / cfg_.kv_heads) <= static_cast<size_t>(kExactScores);
     const bool mfma_fits = prefill_mfma_ && pre_attn_mfma_fits(static_cast<int>(cfg_.heads / cfg_.kv_heads), static_cast<int>(cfg_.head_dim));
-    return prefill_on_ && n >= 2 && (exact_fits || mfma_fits);
+    return prefill_on_ && !gemma() && n >= 2 && (exact_fits || mfma_fits);
 }
 
 void Session::ensure_prefill() {

@@ -42,6 +42,9 @@ struct Layer {
     const float* k_bias = nullptr;
     const float* v_bias = nullptr;
     bool rope = true;               // false: the layer attends without RoPE (SmolLM3's every fourth)
+    const float* attn_post_norm = nullptr;  // Gemma: norms of the attention and feed-forward outputs
+    const float* ffn_post_norm = nullptr;
+    bool slides = false;            // Gemma 3: a sliding-window layer (local RoPE base)
 };
 
 // Device bytes a session of these tensors would allocate (see Session's constructor).
@@ -89,6 +92,7 @@ private:
     void ensure_prefill();
     void prefill_layers(size_t pos0, int T);
     bool neox() const;
+    bool gemma() const { return cfg_.arch == BRISK_HIP_ARCH_GEMMA3; }
     void prefill_quant(const float* x, int xstride, const float* w, int cols, int T, const DeviceMatrix& consumer);
 
     brisk_hip_config cfg_;
@@ -106,6 +110,9 @@ private:
     size_t kv_bytes_ = 0;
     float *h_ = nullptr, *q_ = nullptr, *att_ = nullptr, *act_ = nullptr, *logits_ = nullptr, *rope_ = nullptr;
     float *part_acc_ = nullptr, *part_ml_ = nullptr, *k_ = nullptr, *v_ = nullptr;
+    float* rope_local_ = nullptr;  // Gemma 3 sliding layers' RoPE table
+    float* proj_ = nullptr;        // Gemma: a projection's output before its post-norm
+    float embd_scale_ = 1.0f;      // Gemma: sqrt(embd) (src/model.cpp:286)
     unsigned long long* key_ = nullptr;
     unsigned* ticket_ = nullptr;
     int* pos_ = nullptr;

@@ -31,7 +31,7 @@
 extern "C" {
 #endif
 
-#define BRISK_HIP_ABI_VERSION 1
+#define BRISK_HIP_ABI_VERSION 2
 
 enum {
     BRISK_HIP_OK = 0,
@@ -60,7 +60,8 @@ enum {
     BRISK_HIP_ARCH_LLAMA = 1,
     BRISK_HIP_ARCH_BITNET = 2,
     BRISK_HIP_ARCH_QWEN2 = 3,   /* Q/K/V projection biases, no Q/K norms */
-    BRISK_HIP_ARCH_SMOLLM3 = 4  /* Llama-shaped; every fourth layer attends without RoPE */
+    BRISK_HIP_ARCH_SMOLLM3 = 4, /* Llama-shaped; every fourth layer attends without RoPE */
+    BRISK_HIP_ARCH_GEMMA3 = 5   /* Q/K norms, post-norms, GELU gate, sliding-window layers, scaled embeddings */
 };
 
 /* The fields of ModelConfig (src/model.h:36-60) this path reads. */
@@ -68,6 +69,11 @@ typedef struct {
     int arch;
     uint32_t vocab, embd, layers, heads, kv_heads, head_dim, ff, context_length;
     float rope_base, rms_epsilon;
+    /* Gemma 3 (zero for the other families; ModelConfig, src/model.h:63-71): */
+    uint32_t sliding_window; /* layers with l % 6 != 5 see only the last this-many positions; 0: none */
+    float rope_base_local;   /* those layers' RoPE base (rope.freq_base_swa) */
+    float rope_scale;        /* the other layers' position scale, 1 / rope.scaling.factor; 0 reads as 1 */
+    float final_softcap;     /* logits = c tanh(logits / c); 0: none */
 } brisk_hip_config;
 
 /* One model tensor in GGUF layout (host memory, e.g. the file's mmap):
@@ -131,6 +137,12 @@ int brisk_hip_gemv(int type, int flags, const void* packed, size_t rows, size_t 
  * softmax_f32 and silu_mul_f32 call: src/kernels_f32.cpp:276-289); the token
  * loop's softmax and SiLU use the same device routine.  y[i] = expf(x[i]). */
 int brisk_hip_expf(const float* x, float* y, size_t n, void* stream);
+
+/* tanhf exactly as the reference's host libm computes it (glibc 2.35's, which
+ * gelu_mul_f32 and the final logit softcap call: src/kernels_f32.cpp:291-296,
+ * src/model.cpp:1206-1209); the Gemma epilogues use the same device routine.
+ * y[i] = tanhf(x[i]). */
+int brisk_hip_tanhf(const float* x, float* y, size_t n, void* stream);
 
 /* Self-test of the shortcuts the device arithmetic takes: the two short
  * divisions of the activation quantisation (a / 127 for a >= 0, and 1 / d),

@@ -618,6 +618,113 @@ uint64_t or_expf_check(uint32_t stride, uint64_t* checked) {
     return bad;
 }
 
+/* glibc's tanhf, as the reference calls it (std::tanh on float: gelu_mul_f32 and the
+ * final softcap, src/kernels_f32.cpp:291-296, src/model.cpp:1206-1209). */
+void or_tanhf_batch(const float* x, float* y, size_t n) {
+    for (size_t i = 0; i < n; ++i) y[i] = tanhf(x[i]);
+}
+
+/* The restatement of glibc 2.35's tanhf that the HIP Gemma epilogues run: fdlibm's
+ * s_tanhf.c over its s_expm1f.c (argument reduction by k ln2 in a hi and a lo part,
+ * a rational form with five scaled coefficients, k put back into the exponent).
+ * or_tanhf_check compares it with the host's tanhf on every `stride`-th 32-bit
+ * pattern and returns the number of differing results. */
+static inline uint32_t fbits(float f) { uint32_t u; memcpy(&u, &f, 4); return u; }
+static inline float ffrom(uint32_t u) { float f; memcpy(&f, &u, 4); return f; }
+static float expm1f_restated(float x) {
+    const float one = 1.0f, huge = 1.0e+30f, tiny = 1.0e-30f, o_threshold = 8.8721679688e+01f;
+    const float ln2_hi = 6.9313812256e-01f, ln2_lo = 9.0580006145e-06f, invln2 = 1.4426950216e+00f;
+    const float Q1 = -3.3333335072e-02f, Q2 = 1.5873016091e-03f, Q3 = -7.9365076090e-05f, Q4 = 4.0082177293e-06f, Q5 = -2.0109921195e-07f;
+    float y, hi, lo, c = 0, t, e, hxs, hfx, r1;
+    int32_t k;
+    uint32_t hx = fbits(x);
+    const uint32_t xsb = hx & 0x80000000u;
+    hx &= 0x7fffffffu;
+    if (hx >= 0x4195b844u) {
+        if (hx >= 0x42b17218u) {
+            if (hx > 0x7f800000u) return x + x;
+            if (hx == 0x7f800000u) return xsb == 0 ? x : -1.0f;
+            if (x > o_threshold) return huge * huge;
+        }
+        if (xsb != 0) return tiny - one;
+    }
+    if (hx > 0x3eb17218u) {
+        if (hx < 0x3F851592u) {
+            if (xsb == 0) { hi = x - ln2_hi; lo = ln2_lo; k = 1; }
+            else { hi = x + ln2_hi; lo = -ln2_lo; k = -1; }
+        } else {
+            k = (int32_t)(invln2 * x + (xsb == 0 ? 0.5f : -0.5f));
+            t = (float)k;
+            hi = x - t * ln2_hi;
+            lo = t * ln2_lo;
+        }
+        x = hi - lo;
+        c = (hi - x) - lo;
+    } else if (hx < 0x33000000u) {
+        t = huge + x;
+        return x - (t - (huge + x));
+    } else k = 0;
+    hfx = 0.5f * x;
+    hxs = x * hfx;
+    r1 = one + hxs * (Q1 + hxs * (Q2 + hxs * (Q3 + hxs * (Q4 + hxs * Q5))));
+    t = 3.0f - r1 * hfx;
+    e = hxs * ((r1 - t) / (6.0f - x * t));
+    if (k == 0) return x - (x * e - hxs);
+    e = (x * (e - c) - c);
+    e -= hxs;
+    if (k == -1) return 0.5f * (x - e) - 0.5f;
+    if (k == 1) {
+        if (x < -0.25f) return -2.0f * (e - (x + 0.5f));
+        return one + 2.0f * (x - e);
+    }
+    if (k <= -2 || k > 56) {
+        y = one - (e - x);
+        return ffrom(fbits(y) + ((uint32_t)k << 23)) - one;
+    }
+    if (k < 23) {
+        t = ffrom(0x3f800000u - (0x1000000u >> k));
+        y = t - (e - x);
+        y = ffrom(fbits(y) + ((uint32_t)k << 23));
+    } else {
+        t = ffrom((uint32_t)(0x7f - k) << 23);
+        y = x - (e + t);
+        y += one;
+        y = ffrom(fbits(y) + ((uint32_t)k << 23));
+    }
+    return y;
+}
+static float tanhf_restated(float x) {
+    const float one = 1.0f, two = 2.0f, tiny = 1.0e-30f;
+    float t, z;
+    const uint32_t jx = fbits(x), ix = jx & 0x7fffffffu;
+    if (ix >= 0x7f800000u) return (jx & 0x80000000u) == 0 ? one / x + one : one / x - one;
+    if (ix < 0x41b00000u) {
+        if (ix == 0) return x;
+        if (ix < 0x24000000u) return x * (one + x);
+        if (ix >= 0x3f800000u) {
+            t = expm1f_restated(two * fabsf(x));
+            z = one - two / (t + two);
+        } else {
+            t = expm1f_restated(-two * fabsf(x));
+            z = -t / (t + two);
+        }
+    } else z = one - tiny;
+    return (jx & 0x80000000u) == 0 ? z : -z;
+}
+
+uint64_t or_tanhf_check(uint32_t stride, uint64_t* checked) {
+    uint64_t bad = 0, n = 0;
+    for (uint64_t b = 0; b <= 0xFFFFFFFFull; b += stride) {
+        const float x = ffrom((uint32_t)b);
+        if (isnan(x)) continue;
+        const float a = tanhf(x), e = tanhf_restated(x);
+        bad += fbits(a) != fbits(e);
+        ++n;
+    }
+    if (checked) *checked = n;
+    return bad;
+}
+
 /* ------------------------------------------------------------------ session */
 
 typedef struct {
@@ -629,6 +736,7 @@ typedef struct {
 typedef struct {
     const float *attn_norm, *q_norm, *k_norm, *attn_sub_norm, *ffn_norm, *ffn_sub_norm;
     const float *q_bias, *k_bias, *v_bias; /* all or none (src/model.cpp:411-416) */
+    const float *attn_post_norm, *ffn_post_norm; /* Gemma (src/model.cpp:399-402) */
     matrix q, k, v, o, gate, up, down;
 } layer_t;
 
@@ -640,7 +748,7 @@ struct oracle_session {
     uint16_t **kcache, **vcache;
     size_t position;
     /* scratch */
-    float *h, *normed, *q, *k, *v, *att, *proj, *gate, *up, *scores, *rope;
+    float *h, *normed, *q, *k, *v, *att, *proj, *gate, *up, *scores, *rope, *rope_local;
     uint8_t* xq;
 };
 
@@ -685,7 +793,11 @@ oracle_session* or_session_create(const oracle_config* cfg, const oracle_tensor*
         GETM(L->gate, LN("ffn_gate.weight"));
         GETM(L->up, LN("ffn_up.weight"));
         GETM(L->down, LN("ffn_down.weight"));
-        if (c->arch == OR_QWEN3) {
+        if (c->arch == OR_GEMMA3) {
+            GETV(L->attn_post_norm, LN("post_attention_norm.weight"));
+            GETV(L->ffn_post_norm, LN("post_ffw_norm.weight"));
+        }
+        if (c->arch == OR_QWEN3 || c->arch == OR_GEMMA3) {
             GETV(L->q_norm, LN("attn_q_norm.weight"));
             GETV(L->k_norm, LN("attn_k_norm.weight"));
         }
@@ -720,6 +832,7 @@ oracle_session* or_session_create(const oracle_config* cfg, const oracle_tensor*
         s->up = (float*)calloc(c->ff, 4);
         s->scores = (float*)calloc((size_t)c->max_context, 4);
         s->rope = (float*)calloc(c->head_dim, 4);
+        s->rope_local = (float*)calloc(c->head_dim, 4);
         s->xq = (uint8_t*)calloc(wide / 32 * 34 + wide / 256 * 292 + 1024, 1);
     }
     return s;
@@ -741,7 +854,7 @@ void or_session_destroy(oracle_session* s) {
     free(s->vcache);
     free(s->layers);
     free(s->h); free(s->normed); free(s->q); free(s->k); free(s->v); free(s->att);
-    free(s->proj); free(s->gate); free(s->up); free(s->scores); free(s->rope); free(s->xq);
+    free(s->proj); free(s->gate); free(s->up); free(s->scores); free(s->rope); free(s->rope_local); free(s->xq);
     free(s);
 }
 
@@ -779,17 +892,33 @@ static void forward_token(oracle_session* s, int32_t token, float* logits) {
     const int neox = c->arch != OR_LLAMA && c->arch != OR_SMOLLM3; /* src/model.cpp:167 */
     const float attention_scale = 1.0f / sqrtf((float)hd);
 
-    /* build_rope (src/model.cpp:880-894), scale 1, attn factor 1, no factors */
+    const int gemma = c->arch == OR_GEMMA3;
+    /* build_rope (src/model.cpp:880-894), attn factor 1, no factors; Gemma 3: the global
+     * table at scale 1 / rope.scaling.factor, the sliding layers' at their own base, scale 1 */
     {
+        const float scale = gemma && c->rope_scale != 0.0f ? c->rope_scale : 1.0f;
         const float theta_scale = powf(c->rope_base, -2.0f / (float)hd);
-        float theta = (float)pos * 1.0f;
+        float theta = (float)pos * scale;
         for (size_t i = 0; i < hd / 2; ++i) {
             s->rope[2 * i] = cosf(theta) * 1.0f;
             s->rope[2 * i + 1] = sinf(theta) * 1.0f;
             theta *= theta_scale;
         }
+        if (gemma && c->sliding_window != 0) {
+            const float ts = powf(c->rope_base_local, -2.0f / (float)hd);
+            float th = (float)pos * 1.0f;
+            for (size_t i = 0; i < hd / 2; ++i) {
+                s->rope_local[2 * i] = cosf(th) * 1.0f;
+                s->rope_local[2 * i + 1] = sinf(th) * 1.0f;
+                th *= ts;
+            }
+        }
     }
     embedding_row(&s->embd, (size_t)token, s->h);
+    if (gemma) { /* src/model.cpp:286, :899-901 */
+        const float es = sqrtf((float)embd);
+        for (size_t i = 0; i < embd; ++i) s->h[i] *= es;
+    }
 
     for (int l = 0; l < c->layers; ++l) {
         const layer_t* L = &s->layers[l];
@@ -799,6 +928,9 @@ static void forward_token(oracle_session* s, int32_t token, float* logits) {
         multiply(s, &L->v, s->normed, s->v);
         /* SmolLM3: every fourth layer has no RoPE (layer_has_rope, src/model.h:110; step 4, src/model.cpp:168) */
         const size_t rope_dim = (c->arch == OR_SMOLLM3 && (l + 1) % 4 == 0) ? 0 : hd;
+        /* Gemma 3: layers with l % 6 != 5 slide (layer_slides, src/model.h:87-90) */
+        const int slides = gemma && c->sliding_window != 0 && l % 6 != 5;
+        const float* rope = slides ? s->rope_local : s->rope;
         if (L->q_bias) { /* add_bias (src/model.cpp:117-119, :1026-1030) */
             for (size_t i = 0; i < qd; ++i) s->q[i] += L->q_bias[i];
             for (size_t i = 0; i < kvd; ++i) s->k[i] += L->k_bias[i];
@@ -807,13 +939,13 @@ static void forward_token(oracle_session* s, int32_t token, float* logits) {
         for (int h = 0; h < c->heads; ++h) {
             float* q = s->q + h * hd;
             if (L->q_norm) or_rms_norm(q, L->q_norm, c->eps, q, hd);
-            apply_rope(q, s->rope, rope_dim, neox);
+            apply_rope(q, rope, rope_dim, neox);
         }
         for (int h = 0; h < c->kv_heads; ++h) {
             float* k = s->k + h * hd;
             const float* v = s->v + h * hd;
             if (L->k_norm) or_rms_norm(k, L->k_norm, c->eps, k, hd);
-            apply_rope(k, s->rope, rope_dim, neox);
+            apply_rope(k, rope, rope_dim, neox);
             uint16_t* kr = s->kcache[l] + ((size_t)h * ctx + pos) * hd;
             uint16_t* vr = s->vcache[l] + ((size_t)h * ctx + pos) * hd;
             for (size_t i = 0; i < hd; ++i) {
@@ -824,19 +956,21 @@ static void forward_token(oracle_session* s, int32_t token, float* logits) {
         /* attention (src/model.cpp:1050-1093, src/kernels_f32.cpp:256-284) */
         {
             const size_t visible = pos + 1;
+            /* a sliding layer sees the last sliding_window positions (src/model.cpp:1084-1085) */
+            const size_t start = slides && visible > (size_t)c->sliding_window ? visible - (size_t)c->sliding_window : 0;
             float* key = s->proj; /* free until the output projection */
             for (int h = 0; h < c->heads; ++h) {
                 const size_t kv = (size_t)h / hpk;
                 const float* q = s->q + h * hd;
-                for (size_t p = 0; p < visible; ++p) {
+                for (size_t p = start; p < visible; ++p) {
                     const uint16_t* kr = s->kcache[l] + (kv * ctx + p) * hd;
                     for (size_t i = 0; i < hd; ++i) key[i] = or_half_to_float(kr[i]);
                     s->scores[p] = or_dot_f32(q, key, hd) * attention_scale;
                 }
-                or_softmax(s->scores, visible);
+                or_softmax(s->scores + start, visible - start);
                 float* out = s->att + h * hd;
                 for (size_t i = 0; i < hd; ++i) out[i] = 0.0f;
-                for (size_t p = 0; p < visible; ++p) {
+                for (size_t p = start; p < visible; ++p) {
                     const uint16_t* vr = s->vcache[l] + (kv * ctx + p) * hd;
                     const float w = s->scores[p];
                     for (size_t i = 0; i < hd; ++i) out[i] += w * or_half_to_float(vr[i]);
@@ -845,6 +979,7 @@ static void forward_token(oracle_session* s, int32_t token, float* logits) {
         }
         if (L->attn_sub_norm) or_rms_norm(s->att, L->attn_sub_norm, c->eps, s->att, qd);
         multiply(s, &L->o, s->att, s->proj);
+        if (L->attn_post_norm) or_rms_norm(s->proj, L->attn_post_norm, c->eps, s->proj, embd); /* :1116-1119 */
         for (size_t i = 0; i < embd; ++i) s->h[i] += s->proj[i];
         or_rms_norm(s->h, L->ffn_norm, c->eps, s->normed, embd);
         multiply(s, &L->gate, s->normed, s->gate);
@@ -854,12 +989,15 @@ static void forward_token(oracle_session* s, int32_t token, float* logits) {
             if (c->arch == OR_BITNET) {
                 const float r = g > 0.0f ? g : 0.0f;
                 s->gate[i] = r * r * s->up[i];
+            } else if (gemma) { /* gelu_mul_f32, src/kernels_f32.cpp:291-296 */
+                s->gate[i] = 0.5f * g * (1.0f + tanhf(0.7978845608f * (g + 0.044715f * g * g * g))) * s->up[i];
             } else {
                 s->gate[i] = g / (1.0f + expf(-g)) * s->up[i];
             }
         }
         if (L->ffn_sub_norm) or_rms_norm(s->gate, L->ffn_sub_norm, c->eps, s->gate, c->ff);
         multiply(s, &L->down, s->gate, s->proj);
+        if (L->ffn_post_norm) or_rms_norm(s->proj, L->ffn_post_norm, c->eps, s->proj, embd); /* :1156-1159 */
         for (size_t i = 0; i < embd; ++i) s->h[i] += s->proj[i];
         (void)kvd;
         if (getenv("BRISK_CPU_DEBUG") != NULL) { /* the reference's per-layer line, src/model.cpp:1183-1192 */
@@ -876,6 +1014,10 @@ static void forward_token(oracle_session* s, int32_t token, float* logits) {
     if (logits) {
         or_rms_norm(s->h, s->out_norm, c->eps, s->normed, embd);
         multiply(s, &s->out, s->normed, logits);
+        if (gemma && c->final_softcap != 0.0f) { /* src/model.cpp:1206-1209 */
+            const float cap = c->final_softcap;
+            for (int i = 0; i < c->vocab; ++i) logits[i] = cap * tanhf(logits[i] / cap);
+        }
     }
     s->position += 1;
 }

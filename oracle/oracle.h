@@ -25,13 +25,16 @@ extern "C" {
 /* ggml tensor types (src/gguf.h:22-27). */
 enum { OR_F32 = 0, OR_Q4_0 = 2, OR_Q4_1 = 3, OR_Q5_0 = 6, OR_Q8_0 = 8, OR_Q4_K = 12, OR_Q5_K = 13, OR_Q6_K = 14, OR_TQ2_0 = 35 };
 /* Architectures of src/model.h:21-32 that the configs use. */
-enum { OR_QWEN3 = 0, OR_LLAMA = 1, OR_BITNET = 2, OR_QWEN2 = 3, OR_SMOLLM3 = 4 };
+enum { OR_QWEN3 = 0, OR_LLAMA = 1, OR_BITNET = 2, OR_QWEN2 = 3, OR_SMOLLM3 = 4, OR_GEMMA3 = 5 };
 
 typedef struct {
     int arch;
     int embd, layers, heads, kv_heads, head_dim, ff, vocab;
     float rope_base, eps;
     int max_context;
+    /* Gemma 3 (src/model.cpp:170-176, :286); zero elsewhere */
+    int sliding_window;
+    float rope_base_local, rope_scale, final_softcap;
 } oracle_config;
 
 /* One tensor of the model: `rows` x `cols` (vectors: rows = 1), GGUF bytes. */
@@ -58,6 +61,8 @@ void or_rms_norm(const float* x, const float* w, float eps, float* out, size_t n
 /* glibc expf over a batch, and the check of the HIP loop's restatement of it. */
 void or_expf_batch(const float* x, float* y, size_t n);
 uint64_t or_expf_check(uint32_t stride, uint64_t* checked);
+void or_tanhf_batch(const float* x, float* y, size_t n);
+uint64_t or_tanhf_check(uint32_t stride, uint64_t* checked);
 /* Activation bits a matrix of `type` with `rows` rows takes on x86 (src/model.cpp:496-503, src/quant.cpp:144). */
 int or_activation_bits(int type, size_t rows);
 

@@ -22,7 +22,9 @@ _vp, _sz, _i, _f, _u16 = C.c_void_p, C.c_size_t, C.c_int, C.c_float, C.c_uint16
 class OracleConfig(C.Structure):
     _fields_ = [("arch", C.c_int), ("embd", C.c_int), ("layers", C.c_int), ("heads", C.c_int),
                 ("kv_heads", C.c_int), ("head_dim", C.c_int), ("ff", C.c_int), ("vocab", C.c_int),
-                ("rope_base", C.c_float), ("eps", C.c_float), ("max_context", C.c_int)]
+                ("rope_base", C.c_float), ("eps", C.c_float), ("max_context", C.c_int),
+                ("sliding_window", C.c_int), ("rope_base_local", C.c_float), ("rope_scale", C.c_float),
+                ("final_softcap", C.c_float)]
 
 
 class OracleTensor(C.Structure):
@@ -68,6 +70,9 @@ def oracle_lib():
         L.or_expf_batch.argtypes = [_vp, _vp, _sz]
         L.or_expf_check.argtypes = [C.c_uint32, C.POINTER(C.c_uint64)]
         L.or_expf_check.restype = C.c_uint64
+        L.or_tanhf_batch.argtypes = [_vp, _vp, _sz]
+        L.or_tanhf_check.argtypes = [C.c_uint32, C.POINTER(C.c_uint64)]
+        L.or_tanhf_check.restype = C.c_uint64
         L.or_activation_bits.argtypes = [_i, _sz]
         L.or_activation_bits.restype = _i
         L.or_session_create.argtypes = [C.POINTER(OracleConfig), C.POINTER(OracleTensor), _sz]
@@ -129,7 +134,8 @@ class Oracle:
         L = oracle_lib()
         self.L, self.cfg, self.max_context = L, cfg, max_context
         c = OracleConfig(cfg.arch, cfg.embd, cfg.layers, cfg.heads, cfg.kv_heads, cfg.head_dim, cfg.ff, cfg.vocab,
-                         cfg.rope_base, cfg.eps, max_context)
+                         cfg.rope_base, cfg.eps, max_context, cfg.sliding_window, cfg.rope_base_local, cfg.rope_scale,
+                         cfg.final_softcap)
         self._names = [t.name.encode() for t in table]
         arr = (OracleTensor * len(table))()
         for i, t in enumerate(table):

@@ -34,6 +34,7 @@ RUNS = {
     "tiny-q5": (12, 48),
     "tiny-qwen2": (12, 48),
     "tiny-smollm3": (12, 48),
+    "tiny-gemma3": (12, 48),
 }
 
 

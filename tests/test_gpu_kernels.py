@@ -190,6 +190,21 @@ def test_expf_matches_host_libm(lib, orc):
     assert len(bad) == 0, f"{len(bad)} of {len(x)} differ, e.g. x={x[bad[:3]]} got={got[bad[:3]]} want={want[bad[:3]]}"
 
 
+def test_tanhf_matches_host_libm(lib, orc):
+    """The device tanhf used by the GELU gate and the logit softcap equals glibc's tanhf (the reference's std::tanh)."""
+    bits = np.arange(0, 1 << 32, 251, dtype=np.uint64).astype(np.uint32)
+    x = bits.view(np.float32)
+    x = x[~np.isnan(x)]
+    want = np.empty_like(x)
+    orc.or_tanhf_batch(pyoracle.ptr(x), pyoracle.ptr(want), len(x))
+    xd = dev(x)
+    out = torch.zeros(len(x), dtype=torch.float32, device="cuda")
+    L.check(lib.brisk_hip_tanhf(p(xd), p(out), len(x), None))
+    got = host(out, np.float32)
+    bad = np.flatnonzero(got.view(np.uint32) != want.view(np.uint32))
+    assert len(bad) == 0, f"{len(bad)} of {len(x)} differ, e.g. x={x[bad[:3]]} got={got[bad[:3]]} want={want[bad[:3]]}"
+
+
 def test_short_divisions_are_exact(lib):
     """div127 (a / 127, a >= 0) and rcp_rn (1 / d) equal IEEE division on every finite input, and the
     hardware float-to-half conversion equals the reference's bit-level one on every float, and the

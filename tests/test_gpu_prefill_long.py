@@ -27,7 +27,7 @@ from brisk_hip import HipSession, model, synth  # noqa: E402
 import pyoracle  # noqa: E402
 
 TOL = 2e-2
-FAMILIES = ["tiny-qwen3", "tiny-llama", "tiny-q8", "tiny-bitnet", "tiny-q5k", "tiny-q5", "tiny-qwen2", "tiny-smollm3"]
+FAMILIES = ["tiny-qwen3", "tiny-llama", "tiny-q8", "tiny-bitnet", "tiny-q5k", "tiny-q5", "tiny-qwen2", "tiny-smollm3", "tiny-gemma3"]
 
 
 def _session(src, ctx, mfma):
@@ -43,6 +43,9 @@ def _session(src, ctx, mfma):
 @pytest.mark.parametrize("first,second", [(64, 0), (200, 0), (30, 150), (700, 0)], ids=["64", "200", "30+150", "700"])
 def test_long_prompt_exact(name, first, second):
     f, cfg, table = model.load(synth.model_path(name))
+    if cfg.arch == model.ARCH_GEMMA3 and first + second > 512:
+        pytest.skip("Gemma 3 evaluates prompts token by token; its attention over more positions than the exact "
+                    "form holds is the split-K one, held to tolerance in test_gpu_long_context.py")
     ctx = first + second + 16
     print(f"[prefill] {name}: {first} + {second} prompt ids", flush=True)
     prompt = synth.prompt_ids(first + second, cfg.vocab, seed=11)

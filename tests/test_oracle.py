@@ -381,6 +381,17 @@ def test_expf_restatement_matches_libm():
     assert bad == 0
 
 
+def test_tanhf_restatement_matches_libm():
+    """The Gemma epilogues' tanhf restatement (fdlibm's tanhf over expm1f, as glibc 2.35 builds it) against the
+    host libm, on a strided sweep of every float bit pattern (every pattern when run with stride 1)."""
+    import ctypes as C
+    L = pyoracle.oracle_lib()
+    checked = C.c_uint64()
+    bad = L.or_tanhf_check(997, C.byref(checked))
+    assert checked.value > 4_000_000
+    assert bad == 0
+
+
 # --------------------------------------------------------------------------- whole models
 
 def tiny(name):
@@ -389,7 +400,7 @@ def tiny(name):
     return path, f, cfg, table
 
 
-@pytest.mark.parametrize("name", ["tiny-qwen3", "tiny-llama", "tiny-q8", "tiny-bitnet", "tiny-q5k", "tiny-q5", "tiny-qwen2", "tiny-smollm3"])
+@pytest.mark.parametrize("name", ["tiny-qwen3", "tiny-llama", "tiny-q8", "tiny-bitnet", "tiny-q5k", "tiny-q5", "tiny-qwen2", "tiny-smollm3", "tiny-gemma3"])
 def test_oracle_greedy_matches_reference_fixture(name):
     """tests/golden/<name>_greedy.json were written by the reference engine itself."""
     with open(os.path.join(HERE, "golden", f"{name}_greedy.json")) as fh:
@@ -418,7 +429,7 @@ def test_oracle_first_tokens_of_qwen3_0_6b_fixture():
 
 
 @needs_ref
-@pytest.mark.parametrize("name", ["tiny-qwen3", "tiny-llama", "tiny-bitnet", "tiny-q5k", "tiny-q5", "tiny-qwen2", "tiny-smollm3"])
+@pytest.mark.parametrize("name", ["tiny-qwen3", "tiny-llama", "tiny-bitnet", "tiny-q5k", "tiny-q5", "tiny-qwen2", "tiny-smollm3", "tiny-gemma3"])
 def test_oracle_session_matches_reference_bitwise(name):
     """eval, eval_all and rollback of the restatement against the reference's Session."""
     path, f, cfg, table = tiny(name)
