@@ -2,7 +2,7 @@
 
 Restates the part of the reference's loader the HIP session needs:
 ``Model::parse_config`` (src/model.cpp:161-301) for the families the HIP
-session runs (qwen3, llama, bitnet, qwen2, smollm3, gemma3), the tensor names and shapes of
+session runs (qwen3, llama, bitnet, qwen2, smollm3, gemma3, phi3), the tensor names and shapes of
 ``Model::Model`` (src/model.cpp:303-423) and the tied output projection
 (src/model.cpp:328-330).  The session takes the weights as GGUF-layout bytes,
 as the reference's ``Model(file, repack = false)`` hands them to a GPU session.
@@ -15,9 +15,9 @@ import numpy as np
 
 from . import gguf as G
 
-ARCH_QWEN3, ARCH_LLAMA, ARCH_BITNET, ARCH_QWEN2, ARCH_SMOLLM3, ARCH_GEMMA3 = 0, 1, 2, 3, 4, 5
+ARCH_QWEN3, ARCH_LLAMA, ARCH_BITNET, ARCH_QWEN2, ARCH_SMOLLM3, ARCH_GEMMA3, ARCH_PHI3 = 0, 1, 2, 3, 4, 5, 6
 _ARCH = {"qwen3": ARCH_QWEN3, "llama": ARCH_LLAMA, "bitnet": ARCH_BITNET, "bitnet-b1.58": ARCH_BITNET,
-         "qwen2": ARCH_QWEN2, "smollm3": ARCH_SMOLLM3, "gemma3": ARCH_GEMMA3}
+         "qwen2": ARCH_QWEN2, "smollm3": ARCH_SMOLLM3, "gemma3": ARCH_GEMMA3, "phi3": ARCH_PHI3}
 QUANT_TYPES = (G.T_Q4_0, G.T_Q4_1, G.T_Q5_0, G.T_Q8_0, G.T_Q4_K, G.T_Q5_K, G.T_Q6_K, G.T_TQ2_0)
 
 
@@ -48,6 +48,10 @@ class ModelConfig:
     rope_base_local: float = 0.0
     rope_scale: float = 0.0
     final_softcap: float = 0.0
+    # Phi-3 (src/model.cpp:177-187); zero for the other families
+    rope_dim: int = 0
+    rope_attn_factor: float = 0.0
+    rope_original_context: int = 0
 
     @property
     def rope_neox(self) -> bool:  # src/model.cpp:167
@@ -68,7 +72,8 @@ class ModelConfig:
 def parse_config(f: G.GgufFile) -> ModelConfig:
     name = f.get("general.architecture")
     if name not in _ARCH:
-        fail(f"unsupported architecture '{name}'; the HIP session runs qwen3, qwen2, llama, smollm3, gemma3 and bitnet")
+        fail(f"unsupported architecture '{name}'; the HIP session runs qwen3, qwen2, llama, smollm3, gemma3, phi3 "
+             "and bitnet")
     p = name + "."
 
     def u32(key):
@@ -106,6 +111,10 @@ def parse_config(f: G.GgufFile) -> ModelConfig:
         cfg.rope_base_local = float(f.get(p + "rope.freq_base_swa", 10000.0))
         cfg.rope_scale = float(np.float32(1.0) / np.float32(f.get(p + "rope.scaling.factor", 1.0)))  # in float
         cfg.final_softcap = float(f.get(p + "final_logit_softcapping", 0.0))
+    if cfg.arch == ARCH_PHI3:
+        cfg.rope_dim = int(f.get(p + "rope.dimension_count", 0))
+        cfg.rope_attn_factor = float(f.get(p + "rope.scaling.attn_factor", 1.0))
+        cfg.rope_original_context = int(f.get(p + "rope.scaling.original_context_length", 0))
     return cfg
 
 
@@ -146,15 +155,24 @@ def tensor_table(f: G.GgufFile, cfg: ModelConfig) -> list:
 
     e, qd, kvd = cfg.embd, cfg.query_dim, cfg.kv_dim
     mat("token_embd.weight", cfg.vocab, e)
+    rd = cfg.rope_dim or cfg.head_dim
+    if f.tensor("rope_freqs.weight") is not None:  # Llama 3's per-frequency factors (src/model.cpp:314-318)
+        vec("rope_freqs.weight", cfg.head_dim // 2)
+    if cfg.arch == ARCH_PHI3 and f.tensor("rope_factors_short.weight") is not None:  # LongRoPE (src/model.cpp:181-186)
+        vec("rope_factors_short.weight", rd // 2)
+        vec("rope_factors_long.weight", rd // 2)
     vec("output_norm.weight", e)
     if f.tensor("output.weight") is not None:
         mat("output.weight", cfg.vocab, e)
     for l in range(cfg.layers):
         b = f"blk.{l}."
         vec(b + "attn_norm.weight", e)
-        mat(b + "attn_q.weight", qd, e)
-        mat(b + "attn_k.weight", kvd, e)
-        mat(b + "attn_v.weight", kvd, e)
+        if cfg.arch == ARCH_PHI3:  # fused Q|K|V and gate|up (src/model.cpp:370-380)
+            mat(b + "attn_qkv.weight", qd + 2 * kvd, e)
+        else:
+            mat(b + "attn_q.weight", qd, e)
+            mat(b + "attn_k.weight", kvd, e)
+            mat(b + "attn_v.weight", kvd, e)
         if cfg.arch in (ARCH_QWEN3, ARCH_GEMMA3):
             vec(b + "attn_q_norm.weight", cfg.head_dim)
             vec(b + "attn_k_norm.weight", cfg.head_dim)
@@ -170,8 +188,11 @@ def tensor_table(f: G.GgufFile, cfg: ModelConfig) -> list:
             vec(b + "attn_v.bias", kvd)
         mat(b + "attn_output.weight", e, qd)
         vec(b + "ffn_norm.weight", e)
-        mat(b + "ffn_gate.weight", cfg.ff, e)
-        mat(b + "ffn_up.weight", cfg.ff, e)
+        if cfg.arch == ARCH_PHI3:
+            mat(b + "ffn_up.weight", 2 * cfg.ff, e)
+        else:
+            mat(b + "ffn_gate.weight", cfg.ff, e)
+            mat(b + "ffn_up.weight", cfg.ff, e)
         mat(b + "ffn_down.weight", e, cfg.ff)
     return out
 

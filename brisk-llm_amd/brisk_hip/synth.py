@@ -173,6 +173,7 @@ class ModelSpec:
     out_fmt: int | None = G.T_Q8_0            # None: tied to token_embd (src/model.cpp:328-330)
     seed: int = 1
     extra: dict = field(default_factory=dict)  # further "<arch>.<key>" metadata: key -> (GGUF type, value)
+    factors: dict = field(default_factory=dict)  # RoPE factor tensors: name -> length
 
     @property
     def query_dim(self):
@@ -244,6 +245,17 @@ SPECS = {
                              fmt=_uniform4(G.T_Q8_0),
                              extra={"attention.sliding_window": (G.U32, 8), "rope.freq_base_swa": (G.F32, 10000.0),
                                     "rope.scaling.factor": (G.F32, 2.0), "final_logit_softcapping": (G.F32, 30.0)}),
+    # Phi-3: fused tensors, 32 of 64 head dimensions rotated, LongRoPE short factors up to a
+    # 512-position context and long ones past it, cos/sin times 1.19.
+    "tiny-phi3": ModelSpec("tiny-phi3", "phi3", 256, 2, 4, 4, 64, 512, 1000, 1e4, eps=1e-5, context=2048,
+                           fmt=_uniform4(G.T_Q4_0),
+                           extra={"rope.dimension_count": (G.U32, 32), "rope.scaling.attn_factor": (G.F32, 1.1902381),
+                                  "rope.scaling.original_context_length": (G.U32, 512)},
+                           factors={"rope_factors_short.weight": 16, "rope_factors_long.weight": 16}),
+    # Llama 3.x's rope_freqs factors (src/model.cpp:314-318) on the tiny Llama shape.
+    "tiny-llama32": ModelSpec("tiny-llama32", "llama", 512, 2, 8, 2, 64, 768, 1000, 5e5, eps=1e-5, context=1024,
+                              fmt={**_uniform4(G.T_Q4_K), "v": G.T_Q6_K, "down": G.T_Q6_K}, embd_fmt=G.T_Q6_K,
+                              out_fmt=None, factors={"rope_freqs.weight": 32}),
     "tiny-q5": ModelSpec("tiny-q5", "qwen3", 256, 2, 4, 2, 64, 512, 1000, 1e6, context=1024,
                          fmt={**_uniform4(G.T_Q5_0), "o": G.T_Q4_1, "down": G.T_Q4_1}),
 }
@@ -287,15 +299,21 @@ def write_model(spec: ModelSpec, path: str) -> str:
     for key, (vtype, value) in spec.extra.items():
         w.add(f"{a}.{key}", vtype, value)
     _matrix(w, spec, "token_embd.weight", spec.vocab, spec.embd, spec.embd_fmt)
+    for name, n in spec.factors.items():  # per-frequency RoPE factors in [1, 8], as Llama 3's and LongRoPE's
+        seed = stream_seed(spec.seed, name)
+        w.add_tensor(name, (n,), G.T_F32, lambda seed=seed, n=n: random_uniform(seed, n, 1.0, 8.0).astype(np.float32).view(np.uint8))
     _vector(w, spec, "output_norm.weight", spec.embd)
     if spec.out_fmt is not None:
         _matrix(w, spec, "output.weight", spec.vocab, spec.embd, spec.out_fmt)
     for l in range(spec.layers):
         b = f"blk.{l}."
         _vector(w, spec, b + "attn_norm.weight", spec.embd)
-        _matrix(w, spec, b + "attn_q.weight", spec.query_dim, spec.embd, spec.fmt["q"])
-        _matrix(w, spec, b + "attn_k.weight", spec.kv_dim, spec.embd, spec.fmt["k"])
-        _matrix(w, spec, b + "attn_v.weight", spec.kv_dim, spec.embd, spec.fmt["v"])
+        if a == "phi3":  # fused Q|K|V (src/model.cpp:370-376)
+            _matrix(w, spec, b + "attn_qkv.weight", spec.query_dim + 2 * spec.kv_dim, spec.embd, spec.fmt["q"])
+        else:
+            _matrix(w, spec, b + "attn_q.weight", spec.query_dim, spec.embd, spec.fmt["q"])
+            _matrix(w, spec, b + "attn_k.weight", spec.kv_dim, spec.embd, spec.fmt["k"])
+            _matrix(w, spec, b + "attn_v.weight", spec.kv_dim, spec.embd, spec.fmt["v"])
         if a in ("qwen3", "gemma3"):
             _vector(w, spec, b + "attn_q_norm.weight", spec.head_dim)
             _vector(w, spec, b + "attn_k_norm.weight", spec.head_dim)
@@ -311,8 +329,11 @@ def write_model(spec: ModelSpec, path: str) -> str:
             _bias(w, spec, b + "attn_v.bias", spec.kv_dim)
         _matrix(w, spec, b + "attn_output.weight", spec.embd, spec.query_dim, spec.fmt["o"])
         _vector(w, spec, b + "ffn_norm.weight", spec.embd)
-        _matrix(w, spec, b + "ffn_gate.weight", spec.ff, spec.embd, spec.fmt["gate"])
-        _matrix(w, spec, b + "ffn_up.weight", spec.ff, spec.embd, spec.fmt["up"])
+        if a == "phi3":  # fused gate|up (src/model.cpp:377-379)
+            _matrix(w, spec, b + "ffn_up.weight", 2 * spec.ff, spec.embd, spec.fmt["up"])
+        else:
+            _matrix(w, spec, b + "ffn_gate.weight", spec.ff, spec.embd, spec.fmt["gate"])
+            _matrix(w, spec, b + "ffn_up.weight", spec.ff, spec.embd, spec.fmt["up"])
         _matrix(w, spec, b + "ffn_down.weight", spec.embd, spec.ff, spec.fmt["down"])
     tmp = path + ".part"
     w.write(tmp)

@@ -292,7 +292,7 @@ __global__ __launch_bounds__(kThreads) void k_attn(AttnArgs g) {
         const size_t shift = static_cast<size_t>(start) * g.head_dim;
         g.kcache += shift;
         g.vcache += shift;
-        if (g.rope != nullptr) g.rope += shift;
+        if (g.rope != nullptr) g.rope += static_cast<size_t>(start) * g.rope_dim;
     }
     const int pos = pos_abs - start, L = pos + 1;
     const bool exact = attn_is_exact(L, g.heads / g.kv_heads);

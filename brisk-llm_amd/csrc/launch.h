@@ -49,7 +49,8 @@ struct AttnArgs {
     const float* qbias;   // projection biases added to the raw q, k, v (Qwen2) or null
     const float* kbias;   // ([heads][head_dim], [kv_heads][head_dim], ditto)
     const float* vbias;
-    const float* rope;    // [max_context][head_dim] cos, sin pairs; null on a layer without RoPE (SmolLM3)
+    const float* rope;    // [max_context][rope_dim] cos, sin pairs; null on a layer without RoPE (SmolLM3)
+    int rope_dim;         // dimensions rotated (the head's first rope_dim; Phi-3 rotates part of it)
     float eps;
     int neox;
     int window;           // a sliding layer's last `window` positions (Gemma 3); 0: every position

@@ -28,7 +28,8 @@ struct LoopArgs {
     const float* out_norm;
     int embd_dim, heads, kv_heads, head_dim, ff, neox, relu2;
     float eps, scale;
-    const float* rope;       // [ctx][head_dim]
+    const float* rope;       // [ctx][rope_dim]
+    int rope_dim;
     int ctx;
     // tagged hand-off words: (tag << 32) | float bits
     unsigned long long *ht, *qt, *kt, *vt, *attt, *actt, *pacct, *pmlt;

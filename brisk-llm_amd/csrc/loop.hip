@@ -339,7 +339,7 @@ __device__ __forceinline__ bool phase_a(const LoopArgs& g, const LayerDev& L, in
 __device__ __forceinline__ AttnArgs attn_args(const LoopArgs& g, const LayerDev& L, int step, int l) {
     AttnArgs a{};
     a.qnorm = L.q_norm; a.knorm = L.k_norm; a.rope = L.rope ? g.rope : nullptr; a.eps = g.eps; a.neox = g.neox;
-    a.qbias = L.q_bias; a.kbias = L.k_bias; a.vbias = L.v_bias;
+    a.qbias = L.q_bias; a.kbias = L.k_bias; a.vbias = L.v_bias; a.rope_dim = g.rope_dim;
     a.kcache = L.kc; a.vcache = L.vc; a.ctx = g.ctx; a.head_dim = g.head_dim; a.heads = g.heads;
     a.kv_heads = g.kv_heads; a.scale = g.scale; a.max_splits = g.max_splits;
     a.stamps = g.trace != nullptr ? g.trace + 65536 + (static_cast<size_t>(step * g.n_layers + l) * 8 + 1) * 8 : nullptr;
@@ -602,10 +602,10 @@ __device__ __forceinline__ bool attn_head_pool(const LoopArgs& lg, const AttnArg
     }
     attn_stamp(g, h, 1);
     // q_norm / k_norm and RoPE (src/model.cpp:1026-1041), k and v rounded to fp16 as the cache holds them
-    const float* rope = g.rope != nullptr ? g.rope + static_cast<size_t>(pos) * hd : nullptr;
-    if (wave == 0) head_norm_rope(s.q, g.qbias != nullptr ? g.qbias + h * hd : nullptr, g.qnorm, rope, hd, g.neox, g.eps);
+    const float* rope = g.rope != nullptr ? g.rope + static_cast<size_t>(pos) * g.rope_dim : nullptr;
+    if (wave == 0) head_norm_rope(s.q, g.qbias != nullptr ? g.qbias + h * hd : nullptr, g.qnorm, rope, hd, g.rope_dim, g.neox, g.eps);
     else if (wave == 1) {
-        head_norm_rope(s.kcur, g.kbias != nullptr ? g.kbias + kv * hd : nullptr, g.knorm, rope, hd, g.neox, g.eps);
+        head_norm_rope(s.kcur, g.kbias != nullptr ? g.kbias + kv * hd : nullptr, g.knorm, rope, hd, g.rope_dim, g.neox, g.eps);
         for (int i = lane; i < hd; i += 64) s.kcur[i] = h2f(f2h(s.kcur[i]));
     } else if (wave == 2) {
         for (int i = lane; i < hd; i += 64) s.vcur[i] = h2f(f2h(g.vbias != nullptr ? s.vcur[i] + g.vbias[kv * hd + i] : s.vcur[i]));

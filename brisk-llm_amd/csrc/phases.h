@@ -205,8 +205,8 @@ struct TaggedOut {
 // RMS norm over one head (optional weight w) and RoPE (none when rope is
 // null), by one wave: the per-head steps of src/model.cpp:1021-1041, with
 // rms_norm's float squares summed in double (src/model.cpp:87-97).
-__device__ __forceinline__ void head_norm_rope(float* v, const float* bias, const float* w, const float* rope, int hd, int neox,
-                                               float eps) {
+__device__ __forceinline__ void head_norm_rope(float* v, const float* bias, const float* w, const float* rope, int hd, int rd,
+                                               int neox, float eps) {
     const int lane = threadIdx.x & 63;
     if (bias != nullptr)
         for (int i = lane; i < hd; i += 64) v[i] = v[i] + bias[i];
@@ -218,7 +218,7 @@ __device__ __forceinline__ void head_norm_rope(float* v, const float* bias, cons
         for (int i = lane; i < hd; i += 64) v[i] = v[i] * scale * w[i];
     }
     if (rope == nullptr) return;
-    const int half = hd / 2;
+    const int half = rd / 2;  // only the first rd dimensions rotate (apply_rope, src/model.cpp:100-115)
     for (int i = lane; i < half; i += 64) {
         const float c = rope[2 * i], sn = rope[2 * i + 1];
         const int ia = neox ? i : 2 * i, ib = neox ? i + half : 2 * i + 1;
@@ -270,11 +270,11 @@ template <bool kWriteThrough>
 __device__ __forceinline__ void attn_finish_prologue(const AttnArgs& g, AttnLds& s, int kv, int pos, bool writer,
                                                      bool store = true) {
     const int hd = g.head_dim, hpk = g.heads / g.kv_heads, t = threadIdx.x;
-    const float* rope = g.rope != nullptr ? g.rope + static_cast<size_t>(pos) * hd : nullptr;
+    const float* rope = g.rope != nullptr ? g.rope + static_cast<size_t>(pos) * g.rope_dim : nullptr;
     const int wave = t >> 6;
     for (int h = wave; h < hpk + (writer ? 1 : 0); h += kThreads / 64) {
-        if (h < hpk) head_norm_rope(s.q + h * hd, g.qbias != nullptr ? g.qbias + (kv * hpk + h) * hd : nullptr, g.qnorm, rope, hd, g.neox, g.eps);
-        else head_norm_rope(s.kcur, g.kbias != nullptr ? g.kbias + kv * hd : nullptr, g.knorm, rope, hd, g.neox, g.eps);
+        if (h < hpk) head_norm_rope(s.q + h * hd, g.qbias != nullptr ? g.qbias + (kv * hpk + h) * hd : nullptr, g.qnorm, rope, hd, g.rope_dim, g.neox, g.eps);
+        else head_norm_rope(s.kcur, g.kbias != nullptr ? g.kbias + kv * hd : nullptr, g.knorm, rope, hd, g.rope_dim, g.neox, g.eps);
     }
     __syncthreads();
     if (writer) {

@@ -935,10 +935,10 @@ __global__ __launch_bounds__(kThreads) void k_pre_rope(PreAttnArgs p) {
         s.vcur[i] = g.vbias != nullptr ? v[i] + g.vbias[kv * hd + i] : v[i];
     }
     __syncthreads();
-    const float* rope = g.rope != nullptr ? g.rope + static_cast<size_t>(pos) * hd : nullptr;
+    const float* rope = g.rope != nullptr ? g.rope + static_cast<size_t>(pos) * g.rope_dim : nullptr;
     for (int h = tid >> 6; h <= hpk; h += kThreads / 64) {  // a wave a head; the last is the key
-        if (h < hpk) head_norm_rope(s.q + h * hd, g.qbias != nullptr ? g.qbias + (kv * hpk + h) * hd : nullptr, g.qnorm, rope, hd, g.neox, g.eps);
-        else head_norm_rope(s.kcur, g.kbias != nullptr ? g.kbias + kv * hd : nullptr, g.knorm, rope, hd, g.neox, g.eps);
+        if (h < hpk) head_norm_rope(s.q + h * hd, g.qbias != nullptr ? g.qbias + (kv * hpk + h) * hd : nullptr, g.qnorm, rope, hd, g.rope_dim, g.neox, g.eps);
+        else head_norm_rope(s.kcur, g.kbias != nullptr ? g.kbias + kv * hd : nullptr, g.knorm, rope, hd, g.rope_dim, g.neox, g.eps);
     }
     __syncthreads();
     // the cache rows, fp16 (store_f16, src/kernels_f32.cpp:248-250)

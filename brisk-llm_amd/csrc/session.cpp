@@ -167,7 +167,8 @@ Session::Session(const brisk_hip_config& cfg, const brisk_hip_tensor* tensors, s
     int count = 0;
     if (hipGetDeviceCount(&count) != hipSuccess || count == 0) throw Error(BRISK_HIP_ENODEV, "hip: no GPU device available");
     if (device < 0 || device >= count) throw Error(BRISK_HIP_ENODEV, "hip: no GPU device " + std::to_string(device));
-    if (cfg.arch < BRISK_HIP_ARCH_QWEN3 || cfg.arch > BRISK_HIP_ARCH_GEMMA3) model_fail("unsupported architecture");
+    if (cfg.arch < BRISK_HIP_ARCH_QWEN3 || cfg.arch > BRISK_HIP_ARCH_PHI3) model_fail("unsupported architecture");
+    if (cfg.rope_dim > cfg.head_dim || cfg.rope_dim % 2 != 0) model_fail("rope dimension count must be even and at most the head size");
     if (cfg.embd == 0 || cfg.layers == 0 || cfg.heads == 0 || cfg.kv_heads == 0 || cfg.ff == 0 || cfg.context_length == 0 ||
         cfg.vocab == 0)
         model_fail("a model dimension is zero");
@@ -211,10 +212,12 @@ Session::Session(const brisk_hip_config& cfg, const brisk_hip_tensor* tensors, s
     // stream order keeps a matrix's upload after the previous matrix's repack out of `staging`
     Uploader up(stream_);
 
-    auto load_matrix = [&](const std::string& name, size_t rows, size_t cols, DeviceMatrix& m) {
+    // rows [row0, row0 + rows) of a matrix of `total` rows (Phi-3's fused tensors, load_matrix_rows,
+    // src/model.cpp:370-380; a whole matrix otherwise)
+    auto load_rows = [&](const std::string& name, size_t row0, size_t rows, size_t total, size_t cols, DeviceMatrix& m) {
         const brisk_hip_tensor* t = find(name);
         if (t == nullptr) model_fail("missing tensor '" + name + "'");
-        if (t->rows != rows || t->cols != cols) model_fail("tensor '" + name + "' has an unexpected shape");
+        if (t->rows != total || t->cols != cols) model_fail("tensor '" + name + "' has an unexpected shape");
         const uint32_t type = static_cast<uint32_t>(t->type);
         if (gguf_block_bytes(type) == 0) model_fail("tensor '" + name + "' has a type the HIP session does not take");
         if (cols % block_elems(type) != 0) model_fail("tensor '" + name + "' row length is not a multiple of its block size");
@@ -226,10 +229,13 @@ Session::Session(const brisk_hip_config& cfg, const brisk_hip_tensor* tensors, s
                      static_cast<uint32_t>(rows), static_cast<uint32_t>(cols), type, 0u};
         // x86's load-time TQ2_0x16 layout (rows % 16 == 0) takes 7-bit activations (src/model.cpp:496-503)
         if (type == kTQ2_0 && rows % 16 == 0) m.p.flags |= kFlagLut16;
-        const size_t bytes = rows * (cols / block_elems(type)) * gguf_block_bytes(type);
-        up.copy(staging, t->data, bytes);
+        const size_t row_bytes = (cols / block_elems(type)) * gguf_block_bytes(type), bytes = rows * row_bytes;
+        up.copy(staging, static_cast<const uint8_t*>(t->data) + row0 * row_bytes, bytes);
         check(launch_pack(type, staging, rows, cols, m.p, stream_), "pack");
         weight_bytes_ += bytes;
+    };
+    auto load_matrix = [&](const std::string& name, size_t rows, size_t cols, DeviceMatrix& m) {
+        load_rows(name, 0, rows, rows, cols, m);
     };
     auto load_vector = [&](const std::string& name, size_t count) -> float* {
         const brisk_hip_tensor* t = find(name);
@@ -255,13 +261,21 @@ Session::Session(const brisk_hip_config& cfg, const brisk_hip_tensor* tensors, s
         const std::string b = "blk." + std::to_string(l) + ".";
         Layer& L = layers_[l];
         L.attn_norm = load_vector(b + "attn_norm.weight", e);
-        load_matrix(b + "attn_q.weight", qd, e, L.q);
-        load_matrix(b + "attn_k.weight", kvd, e, L.k);
-        load_matrix(b + "attn_v.weight", kvd, e, L.v);
+        if (cfg.arch == BRISK_HIP_ARCH_PHI3) {  // Q|K|V rows of attn_qkv, gate|up rows of ffn_up
+            load_rows(b + "attn_qkv.weight", 0, qd, qd + 2 * kvd, e, L.q);
+            load_rows(b + "attn_qkv.weight", qd, kvd, qd + 2 * kvd, e, L.k);
+            load_rows(b + "attn_qkv.weight", qd + kvd, kvd, qd + 2 * kvd, e, L.v);
+            load_rows(b + "ffn_up.weight", 0, cfg.ff, 2 * static_cast<size_t>(cfg.ff), e, L.gate);
+            load_rows(b + "ffn_up.weight", cfg.ff, cfg.ff, 2 * static_cast<size_t>(cfg.ff), e, L.up);
+        } else {
+            load_matrix(b + "attn_q.weight", qd, e, L.q);
+            load_matrix(b + "attn_k.weight", kvd, e, L.k);
+            load_matrix(b + "attn_v.weight", kvd, e, L.v);
+            load_matrix(b + "ffn_gate.weight", cfg.ff, e, L.gate);
+            load_matrix(b + "ffn_up.weight", cfg.ff, e, L.up);
+        }
         load_matrix(b + "attn_output.weight", e, qd, L.o);
         L.ffn_norm = load_vector(b + "ffn_norm.weight", e);
-        load_matrix(b + "ffn_gate.weight", cfg.ff, e, L.gate);
-        load_matrix(b + "ffn_up.weight", cfg.ff, e, L.up);
         load_matrix(b + "ffn_down.weight", e, cfg.ff, L.down);
         if (cfg.arch == BRISK_HIP_ARCH_QWEN3 || cfg.arch == BRISK_HIP_ARCH_GEMMA3) {
             L.q_norm = load_vector(b + "attn_q_norm.weight", hd);
@@ -325,15 +339,35 @@ Session::Session(const brisk_hip_config& cfg, const brisk_hip_tensor* tensors, s
     // theta_scale = base^(-2/dim); theta = pos * scale, multiplied by theta_scale per pair.
     // Gemma 3: the global layers' positions are scaled by 1 / rope.scaling.factor, the
     // sliding layers take their own base at scale 1 (src/model.cpp:893-894).
-    auto rope_table = [&](float base, float scale) {
-        std::vector<float> rope(max_ctx_ * hd);
-        const float theta_scale = std::pow(base, -2.0f / static_cast<float>(hd));
+    // Per-frequency factors divide the angle (Llama 3's rope_freqs, Phi-3's LongRoPE short or,
+    // past the original context, long factors: src/model.cpp:312-318, :691-694, :886-888) and
+    // Phi-3's attention factor scales cos and sin; only the first rope_dim dimensions rotate.
+    const size_t rd = cfg.rope_dim != 0 ? cfg.rope_dim : hd;
+    rope_dim_ = static_cast<int>(rd);
+    const float attn_factor = cfg.rope_attn_factor != 0.0f ? cfg.rope_attn_factor : 1.0f;
+    const float* factors = nullptr;
+    {
+        std::vector<const char*> names = {"rope_freqs.weight"};
+        if (cfg.arch == BRISK_HIP_ARCH_PHI3)
+            names = {cfg.rope_original_context != 0 && max_ctx_ > cfg.rope_original_context ? "rope_factors_long.weight"
+                                                                                            : "rope_factors_short.weight"};
+        for (const char* nm : names) {
+            const brisk_hip_tensor* t = find(nm);
+            if (t == nullptr) continue;
+            if (t->type != BRISK_HIP_F32 || t->rows * t->cols < rd / 2) model_fail(std::string("tensor '") + nm + "' has an unexpected size");
+            factors = static_cast<const float*>(t->data);
+        }
+    }
+    auto rope_table = [&](float base, float scale, size_t dim, const float* fac, float af) {
+        std::vector<float> rope(max_ctx_ * dim);
+        const float theta_scale = std::pow(base, -2.0f / static_cast<float>(dim));
         for (size_t p = 0; p < max_ctx_; ++p) {
             float theta = static_cast<float>(p) * scale;
-            float* r = rope.data() + p * hd;
-            for (size_t i = 0; i < hd / 2; ++i) {
-                r[2 * i] = std::cos(theta) * 1.0f;
-                r[2 * i + 1] = std::sin(theta) * 1.0f;
+            float* r = rope.data() + p * dim;
+            for (size_t i = 0; i < dim / 2; ++i) {
+                const float angle = fac != nullptr ? theta / fac[i] : theta;
+                r[2 * i] = std::cos(angle) * af;
+                r[2 * i + 1] = std::sin(angle) * af;
                 theta *= theta_scale;
             }
         }
@@ -341,9 +375,9 @@ Session::Session(const brisk_hip_config& cfg, const brisk_hip_tensor* tensors, s
         check(hipMemcpy(d, rope.data(), rope.size() * 4, hipMemcpyHostToDevice), "hipMemcpy(rope)");
         return d;
     };
-    rope_ = rope_table(cfg.rope_base, gemma() && cfg.rope_scale != 0.0f ? cfg.rope_scale : 1.0f);
+    rope_ = rope_table(cfg.rope_base, gemma() && cfg.rope_scale != 0.0f ? cfg.rope_scale : 1.0f, rd, factors, attn_factor);
     if (gemma()) {
-        if (cfg.sliding_window != 0) rope_local_ = rope_table(cfg.rope_base_local, 1.0f);
+        if (cfg.sliding_window != 0) rope_local_ = rope_table(cfg.rope_base_local, 1.0f, hd, nullptr, 1.0f);
         proj_ = static_cast<float*>(alloc(e * 4));
         embd_scale_ = std::sqrt(static_cast<float>(cfg.embd));
     }
@@ -411,6 +445,7 @@ void Session::record_step(bool full) {
         aa.q = q_; aa.k = k_; aa.v = v_; aa.qnorm = L.q_norm; aa.knorm = L.k_norm;
         aa.rope = !L.rope ? nullptr : L.slides ? rope_local_ : rope_;
         aa.window = L.slides ? static_cast<int>(cfg_.sliding_window) : 0;
+        aa.rope_dim = L.slides ? static_cast<int>(cfg_.head_dim) : rope_dim_;
         aa.qbias = L.q_bias; aa.kbias = L.k_bias; aa.vbias = L.v_bias;
         aa.eps = cfg_.rms_epsilon; aa.neox = neox();
         aa.kcache = kcache_[l]; aa.vcache = vcache_[l]; aa.pos = pos_;
@@ -542,6 +577,7 @@ void Session::setup_loop() {
     g.eps = cfg_.rms_epsilon;
     g.scale = 1.0f / std::sqrt(static_cast<float>(cfg_.head_dim));
     g.rope = rope_;
+    g.rope_dim = rope_dim_;
     g.ctx = static_cast<int>(max_ctx_);
     g.logits = logits_;
     g.max_splits = max_splits_;
@@ -748,6 +784,7 @@ void Session::prefill_layers(size_t pos0, int T) {
         // norms, RoPE, cache rows, attention (:1020-1093)
         PreAttnArgs pa{};
         pa.a.qnorm = L.q_norm; pa.a.knorm = L.k_norm; pa.a.rope = L.rope ? rope_ : nullptr; pa.a.eps = cfg_.rms_epsilon;
+        pa.a.rope_dim = rope_dim_;
         pa.a.qbias = L.q_bias; pa.a.kbias = L.k_bias; pa.a.vbias = L.v_bias;
         pa.a.neox = neox();
         pa.a.kcache = kcache_[l]; pa.a.vcache = vcache_[l];

@@ -113,6 +113,7 @@ private:
     float* rope_local_ = nullptr;  // Gemma 3 sliding layers' RoPE table
     float* proj_ = nullptr;        // Gemma: a projection's output before its post-norm
     float embd_scale_ = 1.0f;      // Gemma: sqrt(embd) (src/model.cpp:286)
+    int rope_dim_ = 0;             // dimensions the RoPE table rotates (its row stride)
     unsigned long long* key_ = nullptr;
     unsigned* ticket_ = nullptr;
     int* pos_ = nullptr;

@@ -61,7 +61,8 @@ enum {
     BRISK_HIP_ARCH_BITNET = 2,
     BRISK_HIP_ARCH_QWEN2 = 3,   /* Q/K/V projection biases, no Q/K norms */
     BRISK_HIP_ARCH_SMOLLM3 = 4, /* Llama-shaped; every fourth layer attends without RoPE */
-    BRISK_HIP_ARCH_GEMMA3 = 5   /* Q/K norms, post-norms, GELU gate, sliding-window layers, scaled embeddings */
+    BRISK_HIP_ARCH_GEMMA3 = 5,  /* Q/K norms, post-norms, GELU gate, sliding-window layers, scaled embeddings */
+    BRISK_HIP_ARCH_PHI3 = 6     /* fused QKV and gate/up tensors, partial rotary, LongRoPE factors */
 };
 
 /* The fields of ModelConfig (src/model.h:36-60) this path reads. */
@@ -74,6 +75,10 @@ typedef struct {
     float rope_base_local;   /* those layers' RoPE base (rope.freq_base_swa) */
     float rope_scale;        /* the other layers' position scale, 1 / rope.scaling.factor; 0 reads as 1 */
     float final_softcap;     /* logits = c tanh(logits / c); 0: none */
+    /* RoPE details (src/model.h:48-62); zero reads as the default: */
+    uint32_t rope_dim;       /* dimensions rotated, the first of each head (Phi-3); 0: the head size */
+    float rope_attn_factor;  /* cos and sin scaled by it (Phi-3 LongRoPE); 0 reads as 1 */
+    uint32_t rope_original_context; /* past it, rope_factors_long.weight replaces rope_factors_short.weight */
 } brisk_hip_config;
 
 /* One model tensor in GGUF layout (host memory, e.g. the file's mmap):

@@ -749,6 +749,7 @@ struct oracle_session {
     size_t position;
     /* scratch */
     float *h, *normed, *q, *k, *v, *att, *proj, *gate, *up, *scores, *rope, *rope_local;
+    const float* rope_factors; /* rope_freqs, or Phi-3's short / long factors; NULL: none */
     uint8_t* xq;
 };
 
@@ -780,18 +781,41 @@ oracle_session* or_session_create(const oracle_config* cfg, const oracle_tensor*
     if (find(t, n, "output.weight")) GETM(s->out, "output.weight");
     else s->out = s->embd;  /* src/model.cpp:328-330 */
     GETV(s->out_norm, "output_norm.weight");
+    /* per-frequency factors (src/model.cpp:312-318) and LongRoPE's choice (:691-694) */
+    {
+        const oracle_tensor* f = find(t, n, "rope_freqs.weight");
+        if (c->arch == OR_PHI3 && find(t, n, "rope_factors_short.weight"))
+            f = find(t, n, c->rope_original_context != 0 && c->max_context > c->rope_original_context ? "rope_factors_long.weight"
+                                                                                                       : "rope_factors_short.weight");
+        s->rope_factors = f ? (const float*)f->data : NULL;
+    }
     s->layers = (layer_t*)calloc((size_t)c->layers, sizeof(layer_t));
     for (int l = 0; l < c->layers; ++l) {
         layer_t* L = &s->layers[l];
 #define LN(sfx) (snprintf(name, sizeof name, "blk.%d.%s", l, sfx), name)
         GETV(L->attn_norm, LN("attn_norm.weight"));
-        GETM(L->q, LN("attn_q.weight"));
-        GETM(L->k, LN("attn_k.weight"));
-        GETM(L->v, LN("attn_v.weight"));
+        if (c->arch == OR_PHI3) { /* rows of the fused tensors (load_matrix_rows, src/model.cpp:370-380) */
+            const size_t qd = (size_t)c->heads * c->head_dim, kvd = (size_t)c->kv_heads * c->head_dim;
+            GETM(L->q, LN("attn_qkv.weight"));
+            L->k = L->q;
+            L->v = L->q;
+            const size_t rb = block_bytes(L->q.type) * (L->q.cols / block_elems(L->q.type));
+            L->q.rows = qd;
+            L->k.rows = kvd; L->k.data += qd * rb;
+            L->v.rows = kvd; L->v.data += (qd + kvd) * rb;
+            GETM(L->gate, LN("ffn_up.weight"));
+            L->up = L->gate;
+            L->gate.rows = (size_t)c->ff;
+            L->up.rows = (size_t)c->ff; L->up.data += (size_t)c->ff * rb;
+        } else {
+            GETM(L->q, LN("attn_q.weight"));
+            GETM(L->k, LN("attn_k.weight"));
+            GETM(L->v, LN("attn_v.weight"));
+            GETM(L->gate, LN("ffn_gate.weight"));
+            GETM(L->up, LN("ffn_up.weight"));
+        }
         GETM(L->o, LN("attn_output.weight"));
         GETV(L->ffn_norm, LN("ffn_norm.weight"));
-        GETM(L->gate, LN("ffn_gate.weight"));
-        GETM(L->up, LN("ffn_up.weight"));
         GETM(L->down, LN("ffn_down.weight"));
         if (c->arch == OR_GEMMA3) {
             GETV(L->attn_post_norm, LN("post_attention_norm.weight"));
@@ -897,11 +921,14 @@ static void forward_token(oracle_session* s, int32_t token, float* logits) {
      * table at scale 1 / rope.scaling.factor, the sliding layers' at their own base, scale 1 */
     {
         const float scale = gemma && c->rope_scale != 0.0f ? c->rope_scale : 1.0f;
-        const float theta_scale = powf(c->rope_base, -2.0f / (float)hd);
+        const float af = c->rope_attn_factor != 0.0f ? c->rope_attn_factor : 1.0f;
+        const size_t rd = c->rope_dim ? (size_t)c->rope_dim : hd;
+        const float theta_scale = powf(c->rope_base, -2.0f / (float)rd);
         float theta = (float)pos * scale;
-        for (size_t i = 0; i < hd / 2; ++i) {
-            s->rope[2 * i] = cosf(theta) * 1.0f;
-            s->rope[2 * i + 1] = sinf(theta) * 1.0f;
+        for (size_t i = 0; i < rd / 2; ++i) {
+            const float angle = s->rope_factors ? theta / s->rope_factors[i] : theta;
+            s->rope[2 * i] = cosf(angle) * af;
+            s->rope[2 * i + 1] = sinf(angle) * af;
             theta *= theta_scale;
         }
         if (gemma && c->sliding_window != 0) {
@@ -927,9 +954,10 @@ static void forward_token(oracle_session* s, int32_t token, float* logits) {
         multiply(s, &L->k, s->normed, s->k);
         multiply(s, &L->v, s->normed, s->v);
         /* SmolLM3: every fourth layer has no RoPE (layer_has_rope, src/model.h:110; step 4, src/model.cpp:168) */
-        const size_t rope_dim = (c->arch == OR_SMOLLM3 && (l + 1) % 4 == 0) ? 0 : hd;
         /* Gemma 3: layers with l % 6 != 5 slide (layer_slides, src/model.h:87-90) */
         const int slides = gemma && c->sliding_window != 0 && l % 6 != 5;
+        /* the rotated width (src/model.cpp:1024): none, the head, or the partial rotary dimension */
+        const size_t rope_dim = (c->arch == OR_SMOLLM3 && (l + 1) % 4 == 0) ? 0 : slides ? hd : (c->rope_dim ? (size_t)c->rope_dim : hd);
         const float* rope = slides ? s->rope_local : s->rope;
         if (L->q_bias) { /* add_bias (src/model.cpp:117-119, :1026-1030) */
             for (size_t i = 0; i < qd; ++i) s->q[i] += L->q_bias[i];

@@ -25,7 +25,7 @@ extern "C" {
 /* ggml tensor types (src/gguf.h:22-27). */
 enum { OR_F32 = 0, OR_Q4_0 = 2, OR_Q4_1 = 3, OR_Q5_0 = 6, OR_Q8_0 = 8, OR_Q4_K = 12, OR_Q5_K = 13, OR_Q6_K = 14, OR_TQ2_0 = 35 };
 /* Architectures of src/model.h:21-32 that the configs use. */
-enum { OR_QWEN3 = 0, OR_LLAMA = 1, OR_BITNET = 2, OR_QWEN2 = 3, OR_SMOLLM3 = 4, OR_GEMMA3 = 5 };
+enum { OR_QWEN3 = 0, OR_LLAMA = 1, OR_BITNET = 2, OR_QWEN2 = 3, OR_SMOLLM3 = 4, OR_GEMMA3 = 5, OR_PHI3 = 6 };
 
 typedef struct {
     int arch;
@@ -35,6 +35,11 @@ typedef struct {
     /* Gemma 3 (src/model.cpp:170-176, :286); zero elsewhere */
     int sliding_window;
     float rope_base_local, rope_scale, final_softcap;
+    /* RoPE details (src/model.h:48-62): rotated dims (0: head size), cos/sin factor (0: 1), and
+     * Phi-3's LongRoPE switch-over context */
+    int rope_dim;
+    float rope_attn_factor;
+    int rope_original_context;
 } oracle_config;
 
 /* One tensor of the model: `rows` x `cols` (vectors: rows = 1), GGUF bytes. */

@@ -35,6 +35,8 @@ RUNS = {
     "tiny-qwen2": (12, 48),
     "tiny-smollm3": (12, 48),
     "tiny-gemma3": (12, 48),
+    "tiny-phi3": (12, 48),
+    "tiny-llama32": (12, 48),
 }
 
 

@@ -44,7 +44,8 @@ def _h2d(dst_ptr, host, nbytes):
 
 
 # tiny-gemma3: its sliding layers see only the last 8 of the 900 positions, its global layer all of them
-@pytest.mark.parametrize("name,n_pos,steps", [("tiny-qwen3", 900, 6), ("tiny-llama", 700, 6), ("tiny-gemma3", 900, 6)])
+@pytest.mark.parametrize("name,n_pos,steps", [("tiny-qwen3", 900, 6), ("tiny-llama", 700, 6), ("tiny-gemma3", 900, 6),
+                                                 ("tiny-phi3", 900, 6)])
 def test_split_attention_tiny(name, n_pos, steps):
     f, cfg, table = model.load(synth.model_path(name))
     print(f"[long] {name}: KV pre-filled to {n_pos}", flush=True)

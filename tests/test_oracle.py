@@ -400,7 +400,7 @@ def tiny(name):
     return path, f, cfg, table
 
 
-@pytest.mark.parametrize("name", ["tiny-qwen3", "tiny-llama", "tiny-q8", "tiny-bitnet", "tiny-q5k", "tiny-q5", "tiny-qwen2", "tiny-smollm3", "tiny-gemma3"])
+@pytest.mark.parametrize("name", ["tiny-qwen3", "tiny-llama", "tiny-q8", "tiny-bitnet", "tiny-q5k", "tiny-q5", "tiny-qwen2", "tiny-smollm3", "tiny-gemma3", "tiny-phi3", "tiny-llama32"])
 def test_oracle_greedy_matches_reference_fixture(name):
     """tests/golden/<name>_greedy.json were written by the reference engine itself."""
     with open(os.path.join(HERE, "golden", f"{name}_greedy.json")) as fh:
@@ -429,7 +429,7 @@ def test_oracle_first_tokens_of_qwen3_0_6b_fixture():
 
 
 @needs_ref
-@pytest.mark.parametrize("name", ["tiny-qwen3", "tiny-llama", "tiny-bitnet", "tiny-q5k", "tiny-q5", "tiny-qwen2", "tiny-smollm3", "tiny-gemma3"])
+@pytest.mark.parametrize("name", ["tiny-qwen3", "tiny-llama", "tiny-bitnet", "tiny-q5k", "tiny-q5", "tiny-qwen2", "tiny-smollm3", "tiny-gemma3", "tiny-phi3", "tiny-llama32"])
 def test_oracle_session_matches_reference_bitwise(name):
     """eval, eval_all and rollback of the restatement against the reference's Session."""
     path, f, cfg, table = tiny(name)
@@ -446,6 +446,23 @@ def test_oracle_session_matches_reference_bitwise(name):
     assert o.position == r.position == 12
     o.close()
     r.close()
+
+
+@needs_ref
+def test_oracle_longrope_matches_reference_bitwise():
+    """Phi-3 with a context past rope.scaling.original_context_length takes the long factors
+    (src/model.cpp:691-694): the restatement against the reference's Session at 600 positions."""
+    path, f, cfg, table = tiny("tiny-phi3")
+    prompt = synth.prompt_ids(20, cfg.vocab, seed=3)
+    o = pyoracle.Oracle(cfg, table, max_context=600)
+    r = pyoracle.Reference(path, threads=2, max_context=600)
+    a, b = o.eval(prompt), r.eval(prompt)
+    assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+    short = pyoracle.Oracle(cfg, table, max_context=64)
+    assert not np.array_equal(short.eval(prompt), a)  # the factors differ, so the logits do
+    o.close()
+    r.close()
+    short.close()
 
 
 def test_oracle_rejects_bad_input():
