@@ -2,7 +2,7 @@
 
 Restates the part of the reference's loader the HIP session needs:
 ``Model::parse_config`` (src/model.cpp:161-301) for the families the HIP
-session runs (qwen3, llama, bitnet, qwen2, smollm3, gemma3, phi3), the tensor names and shapes of
+session runs (qwen3, llama, bitnet, qwen2, smollm3, gemma3, phi3, lfm2), the tensor names and shapes of
 ``Model::Model`` (src/model.cpp:303-423) and the tied output projection
 (src/model.cpp:328-330).  The session takes the weights as GGUF-layout bytes,
 as the reference's ``Model(file, repack = false)`` hands them to a GPU session.
@@ -15,9 +15,10 @@ import numpy as np
 
 from . import gguf as G
 
-ARCH_QWEN3, ARCH_LLAMA, ARCH_BITNET, ARCH_QWEN2, ARCH_SMOLLM3, ARCH_GEMMA3, ARCH_PHI3 = 0, 1, 2, 3, 4, 5, 6
+ARCH_QWEN3, ARCH_LLAMA, ARCH_BITNET, ARCH_QWEN2, ARCH_SMOLLM3, ARCH_GEMMA3, ARCH_PHI3, ARCH_LFM2 = range(8)
 _ARCH = {"qwen3": ARCH_QWEN3, "llama": ARCH_LLAMA, "bitnet": ARCH_BITNET, "bitnet-b1.58": ARCH_BITNET,
-         "qwen2": ARCH_QWEN2, "smollm3": ARCH_SMOLLM3, "gemma3": ARCH_GEMMA3, "phi3": ARCH_PHI3}
+         "qwen2": ARCH_QWEN2, "smollm3": ARCH_SMOLLM3, "gemma3": ARCH_GEMMA3, "phi3": ARCH_PHI3,
+         "lfm2": ARCH_LFM2}
 QUANT_TYPES = (G.T_Q4_0, G.T_Q4_1, G.T_Q5_0, G.T_Q8_0, G.T_Q4_K, G.T_Q5_K, G.T_Q6_K, G.T_TQ2_0)
 
 
@@ -52,6 +53,9 @@ class ModelConfig:
     rope_dim: int = 0
     rope_attn_factor: float = 0.0
     rope_original_context: int = 0
+    # LFM2 (src/model.cpp:229-253): convolution width; layers whose head_count_kv entry is 0 convolve
+    conv_taps: int = 0
+    conv_layers: tuple = ()
 
     @property
     def rope_neox(self) -> bool:  # src/model.cpp:167
@@ -72,8 +76,8 @@ class ModelConfig:
 def parse_config(f: G.GgufFile) -> ModelConfig:
     name = f.get("general.architecture")
     if name not in _ARCH:
-        fail(f"unsupported architecture '{name}'; the HIP session runs qwen3, qwen2, llama, smollm3, gemma3, phi3 "
-             "and bitnet")
+        fail(f"unsupported architecture '{name}'; the HIP session runs qwen3, qwen2, llama, smollm3, gemma3, phi3, "
+             "lfm2 and bitnet")
     p = name + "."
 
     def u32(key):
@@ -89,7 +93,12 @@ def parse_config(f: G.GgufFile) -> ModelConfig:
         return float(v)
 
     embd, layers, heads = u32("embedding_length"), u32("block_count"), u32("attention.head_count")
-    kv, ff, ctx = u32("attention.head_count_kv"), u32("feed_forward_length"), u32("context_length")
+    kv_raw = f.get(p + "attention.head_count_kv")
+    per_layer_kv = list(kv_raw) if isinstance(kv_raw, (list, tuple)) else None  # per layer (src/model.cpp:229-238)
+    if per_layer_kv is not None and len(per_layer_kv) != layers:
+        fail("head_count_kv array length")
+    kv = max(per_layer_kv) if per_layer_kv is not None else u32("attention.head_count_kv")
+    ff, ctx = u32("feed_forward_length"), u32("context_length")
     if 0 in (embd, layers, heads, kv, ff, ctx):
         fail("a model dimension is zero")
     if heads % kv:
@@ -111,6 +120,13 @@ def parse_config(f: G.GgufFile) -> ModelConfig:
         cfg.rope_base_local = float(f.get(p + "rope.freq_base_swa", 10000.0))
         cfg.rope_scale = float(np.float32(1.0) / np.float32(f.get(p + "rope.scaling.factor", 1.0)))  # in float
         cfg.final_softcap = float(f.get(p + "final_logit_softcapping", 0.0))
+    if cfg.arch == ARCH_LFM2:
+        cfg.conv_taps = int(f.get(p + "shortconv.l_cache", 0))
+        if not 2 <= cfg.conv_taps <= 8:
+            fail("unsupported short-convolution width")
+        cfg.conv_layers = tuple(l for l in range(layers) if per_layer_kv is not None and per_layer_kv[l] == 0)
+    elif per_layer_kv is not None and min(per_layer_kv) != kv:
+        fail("per-layer key/value head counts are not supported for this family")
     if cfg.arch == ARCH_PHI3:
         cfg.rope_dim = int(f.get(p + "rope.dimension_count", 0))
         cfg.rope_attn_factor = float(f.get(p + "rope.scaling.attn_factor", 1.0))
@@ -161,19 +177,28 @@ def tensor_table(f: G.GgufFile, cfg: ModelConfig) -> list:
     if cfg.arch == ARCH_PHI3 and f.tensor("rope_factors_short.weight") is not None:  # LongRoPE (src/model.cpp:181-186)
         vec("rope_factors_short.weight", rd // 2)
         vec("rope_factors_long.weight", rd // 2)
-    vec("output_norm.weight", e)
+    vec("token_embd_norm.weight" if cfg.arch == ARCH_LFM2 else "output_norm.weight", e)  # src/model.cpp:331
     if f.tensor("output.weight") is not None:
         mat("output.weight", cfg.vocab, e)
     for l in range(cfg.layers):
         b = f"blk.{l}."
         vec(b + "attn_norm.weight", e)
+        if l in cfg.conv_layers:  # LFM2 short convolution (src/model.cpp:360-364)
+            mat(b + "shortconv.in_proj.weight", 3 * e, e)
+            mat(b + "shortconv.out_proj.weight", e, e)
+            vec(b + "shortconv.conv.weight", cfg.conv_taps * e)
+            vec(b + "ffn_norm.weight", e)
+            mat(b + "ffn_gate.weight", cfg.ff, e)
+            mat(b + "ffn_up.weight", cfg.ff, e)
+            mat(b + "ffn_down.weight", e, cfg.ff)
+            continue
         if cfg.arch == ARCH_PHI3:  # fused Q|K|V and gate|up (src/model.cpp:370-380)
             mat(b + "attn_qkv.weight", qd + 2 * kvd, e)
         else:
             mat(b + "attn_q.weight", qd, e)
             mat(b + "attn_k.weight", kvd, e)
             mat(b + "attn_v.weight", kvd, e)
-        if cfg.arch in (ARCH_QWEN3, ARCH_GEMMA3):
+        if cfg.arch in (ARCH_QWEN3, ARCH_GEMMA3, ARCH_LFM2):
             vec(b + "attn_q_norm.weight", cfg.head_dim)
             vec(b + "attn_k_norm.weight", cfg.head_dim)
         if cfg.arch == ARCH_GEMMA3:

@@ -24,7 +24,7 @@ def _c_args(c, table):
     """The C ABI's config and tensor table for a ModelConfig and tensor list (plus what keeps them alive)."""
     hc = _lib.HipConfig(c.arch, c.vocab, c.embd, c.layers, c.heads, c.kv_heads, c.head_dim, c.ff, c.context,
                         c.rope_base, c.eps, c.sliding_window, c.rope_base_local, c.rope_scale, c.final_softcap,
-                        c.rope_dim, c.rope_attn_factor, c.rope_original_context)
+                        c.rope_dim, c.rope_attn_factor, c.rope_original_context, c.conv_taps)
     names = [t.name.encode() for t in table]
     arr = (_lib.HipTensor * len(table))()
     for i, t in enumerate(table):

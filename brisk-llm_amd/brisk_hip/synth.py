@@ -174,6 +174,7 @@ class ModelSpec:
     seed: int = 1
     extra: dict = field(default_factory=dict)  # further "<arch>.<key>" metadata: key -> (GGUF type, value)
     factors: dict = field(default_factory=dict)  # RoPE factor tensors: name -> length
+    conv_layers: tuple = ()                      # LFM2: layers that convolve (head_count_kv entry 0)
 
     @property
     def query_dim(self):
@@ -256,6 +257,11 @@ SPECS = {
     "tiny-llama32": ModelSpec("tiny-llama32", "llama", 512, 2, 8, 2, 64, 768, 1000, 5e5, eps=1e-5, context=1024,
                               fmt={**_uniform4(G.T_Q4_K), "v": G.T_Q6_K, "down": G.T_Q6_K}, embd_fmt=G.T_Q6_K,
                               out_fmt=None, factors={"rope_freqs.weight": 32}),
+    # LFM2: layers 0, 1 and 3 are 3-tap short convolutions, layer 2 attends.
+    "tiny-lfm2": ModelSpec("tiny-lfm2", "lfm2", 256, 4, 4, 2, 64, 512, 1000, 1e6, eps=1e-5, context=1024,
+                           fmt=_uniform4(G.T_Q8_0), conv_layers=(0, 1, 3),
+                           extra={"shortconv.l_cache": (G.U32, 3),
+                                  "attention.head_count_kv": (G.ARRAY, (G.U32, [0, 0, 2, 0]))}),
     "tiny-q5": ModelSpec("tiny-q5", "qwen3", 256, 2, 4, 2, 64, 512, 1000, 1e6, context=1024,
                          fmt={**_uniform4(G.T_Q5_0), "o": G.T_Q4_1, "down": G.T_Q4_1}),
 }
@@ -289,7 +295,8 @@ def write_model(spec: ModelSpec, path: str) -> str:
     w.add(f"{a}.embedding_length", G.U32, spec.embd)
     w.add(f"{a}.block_count", G.U32, spec.layers)
     w.add(f"{a}.attention.head_count", G.U32, spec.heads)
-    w.add(f"{a}.attention.head_count_kv", G.U32, spec.kv_heads)
+    if "attention.head_count_kv" not in spec.extra:
+        w.add(f"{a}.attention.head_count_kv", G.U32, spec.kv_heads)
     w.add(f"{a}.attention.key_length", G.U32, spec.head_dim)
     w.add(f"{a}.attention.value_length", G.U32, spec.head_dim)
     w.add(f"{a}.feed_forward_length", G.U32, spec.ff)
@@ -302,19 +309,31 @@ def write_model(spec: ModelSpec, path: str) -> str:
     for name, n in spec.factors.items():  # per-frequency RoPE factors in [1, 8], as Llama 3's and LongRoPE's
         seed = stream_seed(spec.seed, name)
         w.add_tensor(name, (n,), G.T_F32, lambda seed=seed, n=n: random_uniform(seed, n, 1.0, 8.0).astype(np.float32).view(np.uint8))
-    _vector(w, spec, "output_norm.weight", spec.embd)
+    _vector(w, spec, "token_embd_norm.weight" if a == "lfm2" else "output_norm.weight", spec.embd)
     if spec.out_fmt is not None:
         _matrix(w, spec, "output.weight", spec.vocab, spec.embd, spec.out_fmt)
     for l in range(spec.layers):
         b = f"blk.{l}."
         _vector(w, spec, b + "attn_norm.weight", spec.embd)
+        if l in spec.conv_layers:  # LFM2 short convolution (src/model.cpp:360-364)
+            taps = spec.extra["shortconv.l_cache"][1]
+            _matrix(w, spec, b + "shortconv.in_proj.weight", 3 * spec.embd, spec.embd, spec.fmt["q"])
+            _matrix(w, spec, b + "shortconv.out_proj.weight", spec.embd, spec.embd, spec.fmt["o"])
+            seed = stream_seed(spec.seed, b + "conv")
+            w.add_tensor(b + "shortconv.conv.weight", (taps, spec.embd), G.T_F32,
+                         lambda seed=seed, n=taps * spec.embd: random_uniform(seed, n, -1.0, 1.0).astype(np.float32).view(np.uint8))
+            _vector(w, spec, b + "ffn_norm.weight", spec.embd)
+            _matrix(w, spec, b + "ffn_gate.weight", spec.ff, spec.embd, spec.fmt["gate"])
+            _matrix(w, spec, b + "ffn_up.weight", spec.ff, spec.embd, spec.fmt["up"])
+            _matrix(w, spec, b + "ffn_down.weight", spec.embd, spec.ff, spec.fmt["down"])
+            continue
         if a == "phi3":  # fused Q|K|V (src/model.cpp:370-376)
             _matrix(w, spec, b + "attn_qkv.weight", spec.query_dim + 2 * spec.kv_dim, spec.embd, spec.fmt["q"])
         else:
             _matrix(w, spec, b + "attn_q.weight", spec.query_dim, spec.embd, spec.fmt["q"])
             _matrix(w, spec, b + "attn_k.weight", spec.kv_dim, spec.embd, spec.fmt["k"])
             _matrix(w, spec, b + "attn_v.weight", spec.kv_dim, spec.embd, spec.fmt["v"])
-        if a in ("qwen3", "gemma3"):
+        if a in ("qwen3", "gemma3", "lfm2"):
             _vector(w, spec, b + "attn_q_norm.weight", spec.head_dim)
             _vector(w, spec, b + "attn_k_norm.weight", spec.head_dim)
         if a == "gemma3":

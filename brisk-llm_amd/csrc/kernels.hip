@@ -341,6 +341,25 @@ __global__ __launch_bounds__(kThreads) void k_post_add(float* __restrict__ h, co
     for (int i = threadIdx.x; i < n; i += kThreads) h[i] = h[i] + p[i] * scale * w[i];
 }
 
+// LFM2 short convolution (src/model.cpp:935-969): bx = b * x, kept per position as
+// fp16 (store_f16); out = c * sum over the last `taps` positions, oldest first, of
+// w[d][k] * bx (read back from the fp16 cache; positions before 0 are zero state).
+// One thread per channel: the thread that stores bx[pos][d] is the one that reads it.
+__global__ __launch_bounds__(kThreads) void k_conv(const float* __restrict__ bcx, uint16_t* __restrict__ cache,
+                                                   const float* __restrict__ w, int taps, const int* __restrict__ pos_p,
+                                                   int n, float* __restrict__ out) {
+    const int d = blockIdx.x * kThreads + threadIdx.x;
+    if (d >= n) return;
+    const int pos = *pos_p;
+    cache[static_cast<size_t>(pos) * n + d] = f2h(bcx[2 * n + d] * bcx[d]);
+    float acc = 0.0f;
+    for (int k = 0; k < taps; ++k) {
+        if (pos + k + 1 < taps) continue;
+        acc += w[d * taps + k] * h2f(cache[static_cast<size_t>(pos + k + 1 - taps) * n + d]);
+    }
+    out[d] = acc * bcx[n + d];
+}
+
 // tanhf as the Gemma epilogues compute it (ref_tanhf), for the parity tests.
 __global__ void k_tanhf(const float* __restrict__ x, float* __restrict__ y, size_t n) {
     const size_t i = static_cast<size_t>(blockIdx.x) * blockDim.x + threadIdx.x;
@@ -551,6 +570,13 @@ int attention_max_splits(int ctx) { return (ctx + kSplit - 1) / kSplit; }
 
 hipError_t launch_post_add(float* h, const float* p, const float* w, float eps, int n, hipStream_t s) {
     hipLaunchKernelGGL(k_post_add, dim3(1), dim3(kThreads), 0, s, h, p, w, eps, n);
+    return hipGetLastError();
+}
+
+hipError_t launch_conv(const float* bcx, uint16_t* cache, const float* w, int taps, const int* pos, int n, float* out,
+                       hipStream_t s) {
+    hipLaunchKernelGGL(k_conv, dim3(static_cast<unsigned>((n + kThreads - 1) / kThreads)), dim3(kThreads), 0, s, bcx, cache, w,
+                       taps, pos, n, out);
     return hipGetLastError();
 }
 

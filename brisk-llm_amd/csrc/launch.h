@@ -101,6 +101,10 @@ hipError_t launch_head(HeadArgs g, hipStream_t s);
 hipError_t launch_advance(int* pos, hipStream_t s);
 hipError_t launch_expf(const float* x, float* y, size_t n, hipStream_t s);
 hipError_t launch_tanhf(const float* x, float* y, size_t n, hipStream_t s);
+// LFM2's short convolution of the token at *pos: bc = [b | c | x] rows, cache [ctx][n] fp16,
+// w [n][taps]; out = c * sum_k w[d][k] bx[pos + k + 1 - taps] with bx = b * x stored at pos.
+hipError_t launch_conv(const float* bcx, uint16_t* cache, const float* w, int taps, const int* pos, int n, float* out,
+                       hipStream_t s);
 hipError_t launch_div_selftest(unsigned long long* bad, hipStream_t s);
 hipError_t launch_mfma_rate(int shape, int blocks, int iters, int* out, hipStream_t s);
 int attention_max_splits(int ctx);

@@ -143,6 +143,7 @@ brisk_hip_memory estimate_session(const brisk_hip_config& cfg, const brisk_hip_t
     sc += static_cast<size_t>(cfg.heads) * splits * (hd + 2) * 4;          // attention partials
     sc += (ctx + 1) * 4 + ctx * hd * 4;                                    // token sequence, RoPE table
     if (cfg.arch == BRISK_HIP_ARCH_GEMMA3) sc += ctx * hd * 4 + e * 4;     // local RoPE table, post-norm input
+    if (cfg.arch == BRISK_HIP_ARCH_LFM2) sc += 3 * e * 4 + static_cast<size_t>(cfg.layers) * ctx * e * 2;  // conv rows, bx caches
     sc += (e + 2 * qd + 2 * kvd + ff + static_cast<size_t>(cfg.heads) * splits * (hd + 2)) * 8;  // hand-off words
     const size_t T = Session::kPrefillTokens, widest = std::max(std::max(e, qd), ff), stride = (widest + 255) / 256 * 256;
     sc += T * (e + 2 * qd + 2 * kvd + ff) * 4 + T * stride * (1 + 4 / 32.0 + 4 / 16.0);  // prefill buffers
@@ -167,7 +168,8 @@ Session::Session(const brisk_hip_config& cfg, const brisk_hip_tensor* tensors, s
     int count = 0;
     if (hipGetDeviceCount(&count) != hipSuccess || count == 0) throw Error(BRISK_HIP_ENODEV, "hip: no GPU device available");
     if (device < 0 || device >= count) throw Error(BRISK_HIP_ENODEV, "hip: no GPU device " + std::to_string(device));
-    if (cfg.arch < BRISK_HIP_ARCH_QWEN3 || cfg.arch > BRISK_HIP_ARCH_PHI3) model_fail("unsupported architecture");
+    if (cfg.arch < BRISK_HIP_ARCH_QWEN3 || cfg.arch > BRISK_HIP_ARCH_LFM2) model_fail("unsupported architecture");
+    if (cfg.arch == BRISK_HIP_ARCH_LFM2 && (cfg.conv_taps < 2 || cfg.conv_taps > 8)) model_fail("unsupported short-convolution width");
     if (cfg.rope_dim > cfg.head_dim || cfg.rope_dim % 2 != 0) model_fail("rope dimension count must be even and at most the head size");
     if (cfg.embd == 0 || cfg.layers == 0 || cfg.heads == 0 || cfg.kv_heads == 0 || cfg.ff == 0 || cfg.context_length == 0 ||
         cfg.vocab == 0)
@@ -255,12 +257,22 @@ Session::Session(const brisk_hip_config& cfg, const brisk_hip_tensor* tensors, s
     } else {
         out_ = &embd_;  // tied (src/model.cpp:328-330)
     }
-    out_norm_ = load_vector("output_norm.weight", e);
+    out_norm_ = load_vector(cfg.arch == BRISK_HIP_ARCH_LFM2 ? "token_embd_norm.weight" : "output_norm.weight", e);  // src/model.cpp:331
     layers_.resize(cfg.layers);
     for (uint32_t l = 0; l < cfg.layers; ++l) {
         const std::string b = "blk." + std::to_string(l) + ".";
         Layer& L = layers_[l];
         L.attn_norm = load_vector(b + "attn_norm.weight", e);
+        if (cfg.arch == BRISK_HIP_ARCH_LFM2 && find(b + "shortconv.in_proj.weight") != nullptr) {  // src/model.cpp:360-364
+            load_matrix(b + "shortconv.in_proj.weight", 3 * e, e, L.conv_in);
+            load_matrix(b + "shortconv.out_proj.weight", e, e, L.conv_out);
+            L.conv_w = load_vector(b + "shortconv.conv.weight", static_cast<size_t>(cfg.conv_taps) * e);
+            L.ffn_norm = load_vector(b + "ffn_norm.weight", e);
+            load_matrix(b + "ffn_gate.weight", cfg.ff, e, L.gate);
+            load_matrix(b + "ffn_up.weight", cfg.ff, e, L.up);
+            load_matrix(b + "ffn_down.weight", e, cfg.ff, L.down);
+            continue;
+        }
         if (cfg.arch == BRISK_HIP_ARCH_PHI3) {  // Q|K|V rows of attn_qkv, gate|up rows of ffn_up
             load_rows(b + "attn_qkv.weight", 0, qd, qd + 2 * kvd, e, L.q);
             load_rows(b + "attn_qkv.weight", qd, kvd, qd + 2 * kvd, e, L.k);
@@ -277,7 +289,7 @@ Session::Session(const brisk_hip_config& cfg, const brisk_hip_tensor* tensors, s
         load_matrix(b + "attn_output.weight", e, qd, L.o);
         L.ffn_norm = load_vector(b + "ffn_norm.weight", e);
         load_matrix(b + "ffn_down.weight", e, cfg.ff, L.down);
-        if (cfg.arch == BRISK_HIP_ARCH_QWEN3 || cfg.arch == BRISK_HIP_ARCH_GEMMA3) {
+        if (cfg.arch == BRISK_HIP_ARCH_QWEN3 || cfg.arch == BRISK_HIP_ARCH_GEMMA3 || cfg.arch == BRISK_HIP_ARCH_LFM2) {
             L.q_norm = load_vector(b + "attn_q_norm.weight", hd);
             L.k_norm = load_vector(b + "attn_k_norm.weight", hd);
         }
@@ -307,6 +319,11 @@ Session::Session(const brisk_hip_config& cfg, const brisk_hip_tensor* tensors, s
 
     // activations and state
     h_ = static_cast<float*>(alloc(e * 4));
+    if (lfm2()) {
+        conv_buf_ = static_cast<float*>(alloc(3 * e * 4));
+        for (Layer& L : layers_)
+            if (L.conv_w != nullptr) L.conv_cache = static_cast<uint16_t*>(alloc(max_ctx_ * e * 2));
+    }
     q_ = static_cast<float*>(alloc(qd * 4));
     att_ = static_cast<float*>(alloc(qd * 4));
     act_ = static_cast<float*>(alloc(static_cast<size_t>(cfg.ff) * 4));
@@ -419,8 +436,20 @@ void Session::record_step(bool full) {
     const float scale = 1.0f / std::sqrt(static_cast<float>(cfg_.head_dim));  // src/model.cpp:978
     for (uint32_t l = 0; l < cfg_.layers; ++l) {
         const Layer& L = layers_[l];
+        if (L.conv_w != nullptr) {  // LFM2 short convolution in place of attention (src/model.cpp:935-969)
+            GemvArgs ca{};
+            ca.n = 1; ca.t[0].m = L.conv_in.p; ca.t[0].out = conv_buf_;
+            ca.x = h_; ca.normw = L.attn_norm; ca.eps = cfg_.rms_epsilon; ca.add = 0;
+            check(launch_gemv(ca, stream_), "conv in_proj");
+            check(launch_conv(conv_buf_, L.conv_cache, L.conv_w, static_cast<int>(cfg_.conv_taps), pos_,
+                              static_cast<int>(cfg_.embd), att_, stream_), "conv");
+            GemvArgs co{};
+            co.n = 1; co.t[0].m = L.conv_out.p; co.t[0].out = h_;
+            co.x = att_; co.normw = nullptr; co.eps = cfg_.rms_epsilon; co.add = 1;
+            check(launch_gemv(co, stream_), "conv out_proj");
+        }
         // Q, K, V rows from attn_norm(h) (src/model.cpp:996-1015): one launch per weight format
-        {
+        if (L.conv_w == nullptr) {
             const DeviceMatrix* mats[3] = {&L.q, &L.k, &L.v};
             float* outs[3] = {q_, k_, v_};
             GemvArgs qa{};
@@ -441,6 +470,7 @@ void Session::record_step(bool full) {
             }
         }
 
+        if (L.conv_w == nullptr) {
         AttnArgs aa{};
         aa.q = q_; aa.k = k_; aa.v = v_; aa.qnorm = L.q_norm; aa.knorm = L.k_norm;
         aa.rope = !L.rope ? nullptr : L.slides ? rope_local_ : rope_;
@@ -461,6 +491,7 @@ void Session::record_step(bool full) {
         oa.x = att_; oa.normw = L.attn_sub_norm; oa.eps = cfg_.rms_epsilon; oa.add = L.attn_post_norm ? 0 : 1;
         check(launch_gemv(oa, stream_), "attn_output");
         if (L.attn_post_norm) check(launch_post_add(h_, proj_, L.attn_post_norm, cfg_.rms_epsilon, static_cast<int>(cfg_.embd), stream_), "post norm");
+        }
 
         GateUpArgs ga{};
         ga.gate = L.gate.p; ga.up = L.up.p; ga.x = h_; ga.normw = L.ffn_norm; ga.eps = cfg_.rms_epsilon;
@@ -513,7 +544,7 @@ void Session::setup_loop() {
     // the loop's split attention merges at most 4 outputs a thread (heads per kv head x head size <= 1024)
     if ((cfg_.heads / cfg_.kv_heads) * cfg_.head_dim > 4 * kThreads) return;
     if (embd_.p.type != out_->p.type) return;  // the loop reads the embedding in its output's format
-    if (gemma()) return;  // post-norms, sliding windows and the softcap are phases of the graph path only
+    if (gemma() || lfm2()) return;  // post-norms, windows, softcap and convolutions are graph-path phases only
     const Layer& L0 = layers_[0];
     const void* k = find_loop_kernel(L0.q.p.type, L0.v.p.type, L0.o.p.type, L0.gate.p.type, L0.down.p.type, out_->p.type);
     if (k == nullptr) return;
@@ -735,7 +766,7 @@ bool Session::use_prefill(size_t n) const {
     // the exact-order prefill attention keeps every score of a token's query heads in LDS
     const bool exact_fits = (position_ + n) * (cfg_.heads / cfg_.kv_heads) <= static_cast<size_t>(kExactScores);
     const bool mfma_fits = prefill_mfma_ && pre_attn_mfma_fits(static_cast<int>(cfg_.heads / cfg_.kv_heads), static_cast<int>(cfg_.head_dim));
-    return prefill_on_ && !gemma() && n >= 2 && (exact_fits || mfma_fits);
+    return prefill_on_ && !gemma() && !lfm2() && n >= 2 && (exact_fits || mfma_fits);
 }
 
 void Session::ensure_prefill() {

@@ -45,6 +45,9 @@ struct Layer {
     const float* attn_post_norm = nullptr;  // Gemma: norms of the attention and feed-forward outputs
     const float* ffn_post_norm = nullptr;
     bool slides = false;            // Gemma 3: a sliding-window layer (local RoPE base)
+    DeviceMatrix conv_in, conv_out; // LFM2 short-convolution layer: in_proj (3 embd rows), out_proj
+    const float* conv_w = nullptr;  // [embd][taps]; non-null marks a convolution layer
+    uint16_t* conv_cache = nullptr; // bx per position, fp16 [ctx][embd]
 };
 
 // Device bytes a session of these tensors would allocate (see Session's constructor).
@@ -93,6 +96,7 @@ private:
     void prefill_layers(size_t pos0, int T);
     bool neox() const;
     bool gemma() const { return cfg_.arch == BRISK_HIP_ARCH_GEMMA3; }
+    bool lfm2() const { return cfg_.arch == BRISK_HIP_ARCH_LFM2; }
     void prefill_quant(const float* x, int xstride, const float* w, int cols, int T, const DeviceMatrix& consumer);
 
     brisk_hip_config cfg_;
@@ -112,6 +116,7 @@ private:
     float *part_acc_ = nullptr, *part_ml_ = nullptr, *k_ = nullptr, *v_ = nullptr;
     float* rope_local_ = nullptr;  // Gemma 3 sliding layers' RoPE table
     float* proj_ = nullptr;        // Gemma: a projection's output before its post-norm
+    float* conv_buf_ = nullptr;    // LFM2: in_proj's [b | c | x] rows
     float embd_scale_ = 1.0f;      // Gemma: sqrt(embd) (src/model.cpp:286)
     int rope_dim_ = 0;             // dimensions the RoPE table rotates (its row stride)
     unsigned long long* key_ = nullptr;

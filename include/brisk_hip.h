@@ -62,7 +62,8 @@ enum {
     BRISK_HIP_ARCH_QWEN2 = 3,   /* Q/K/V projection biases, no Q/K norms */
     BRISK_HIP_ARCH_SMOLLM3 = 4, /* Llama-shaped; every fourth layer attends without RoPE */
     BRISK_HIP_ARCH_GEMMA3 = 5,  /* Q/K norms, post-norms, GELU gate, sliding-window layers, scaled embeddings */
-    BRISK_HIP_ARCH_PHI3 = 6     /* fused QKV and gate/up tensors, partial rotary, LongRoPE factors */
+    BRISK_HIP_ARCH_PHI3 = 6,    /* fused QKV and gate/up tensors, partial rotary, LongRoPE factors */
+    BRISK_HIP_ARCH_LFM2 = 7     /* short-convolution layers (those with blk.N.shortconv.* tensors) between attention layers */
 };
 
 /* The fields of ModelConfig (src/model.h:36-60) this path reads. */
@@ -79,6 +80,7 @@ typedef struct {
     uint32_t rope_dim;       /* dimensions rotated, the first of each head (Phi-3); 0: the head size */
     float rope_attn_factor;  /* cos and sin scaled by it (Phi-3 LongRoPE); 0 reads as 1 */
     uint32_t rope_original_context; /* past it, rope_factors_long.weight replaces rope_factors_short.weight */
+    uint32_t conv_taps;      /* LFM2's short-convolution width (shortconv.l_cache), 2 to 8; 0 elsewhere */
 } brisk_hip_config;
 
 /* One model tensor in GGUF layout (host memory, e.g. the file's mmap):

@@ -738,6 +738,9 @@ typedef struct {
     const float *q_bias, *k_bias, *v_bias; /* all or none (src/model.cpp:411-416) */
     const float *attn_post_norm, *ffn_post_norm; /* Gemma (src/model.cpp:399-402) */
     matrix q, k, v, o, gate, up, down;
+    matrix conv_in, conv_out;  /* LFM2 short convolution (src/model.cpp:360-364) */
+    const float* conv_w;       /* [embd][taps]; non-NULL marks a convolution layer */
+    uint16_t* conv_cache;      /* bx per position, fp16 [max_context][embd] */
 } layer_t;
 
 struct oracle_session {
@@ -748,7 +751,7 @@ struct oracle_session {
     uint16_t **kcache, **vcache;
     size_t position;
     /* scratch */
-    float *h, *normed, *q, *k, *v, *att, *proj, *gate, *up, *scores, *rope, *rope_local;
+    float *h, *normed, *q, *k, *v, *att, *proj, *gate, *up, *scores, *rope, *rope_local, *conv;
     const float* rope_factors; /* rope_freqs, or Phi-3's short / long factors; NULL: none */
     uint8_t* xq;
 };
@@ -780,7 +783,7 @@ oracle_session* or_session_create(const oracle_config* cfg, const oracle_tensor*
     GETM(s->embd, "token_embd.weight");
     if (find(t, n, "output.weight")) GETM(s->out, "output.weight");
     else s->out = s->embd;  /* src/model.cpp:328-330 */
-    GETV(s->out_norm, "output_norm.weight");
+    GETV(s->out_norm, c->arch == OR_LFM2 ? "token_embd_norm.weight" : "output_norm.weight"); /* src/model.cpp:331 */
     /* per-frequency factors (src/model.cpp:312-318) and LongRoPE's choice (:691-694) */
     {
         const oracle_tensor* f = find(t, n, "rope_freqs.weight");
@@ -794,6 +797,17 @@ oracle_session* or_session_create(const oracle_config* cfg, const oracle_tensor*
         layer_t* L = &s->layers[l];
 #define LN(sfx) (snprintf(name, sizeof name, "blk.%d.%s", l, sfx), name)
         GETV(L->attn_norm, LN("attn_norm.weight"));
+        if (c->arch == OR_LFM2 && find(t, n, LN("shortconv.in_proj.weight"))) {
+            GETM(L->conv_in, LN("shortconv.in_proj.weight"));
+            GETM(L->conv_out, LN("shortconv.out_proj.weight"));
+            GETV(L->conv_w, LN("shortconv.conv.weight"));
+            GETV(L->ffn_norm, LN("ffn_norm.weight"));
+            GETM(L->gate, LN("ffn_gate.weight"));
+            GETM(L->up, LN("ffn_up.weight"));
+            GETM(L->down, LN("ffn_down.weight"));
+            L->conv_cache = (uint16_t*)calloc((size_t)c->max_context * (size_t)c->embd, 2);
+            continue;
+        }
         if (c->arch == OR_PHI3) { /* rows of the fused tensors (load_matrix_rows, src/model.cpp:370-380) */
             const size_t qd = (size_t)c->heads * c->head_dim, kvd = (size_t)c->kv_heads * c->head_dim;
             GETM(L->q, LN("attn_qkv.weight"));
@@ -821,7 +835,7 @@ oracle_session* or_session_create(const oracle_config* cfg, const oracle_tensor*
             GETV(L->attn_post_norm, LN("post_attention_norm.weight"));
             GETV(L->ffn_post_norm, LN("post_ffw_norm.weight"));
         }
-        if (c->arch == OR_QWEN3 || c->arch == OR_GEMMA3) {
+        if (c->arch == OR_QWEN3 || c->arch == OR_GEMMA3 || c->arch == OR_LFM2) { /* src/model.cpp:394-397 */
             GETV(L->q_norm, LN("attn_q_norm.weight"));
             GETV(L->k_norm, LN("attn_k_norm.weight"));
         }
@@ -857,6 +871,7 @@ oracle_session* or_session_create(const oracle_config* cfg, const oracle_tensor*
         s->scores = (float*)calloc((size_t)c->max_context, 4);
         s->rope = (float*)calloc(c->head_dim, 4);
         s->rope_local = (float*)calloc(c->head_dim, 4);
+        s->conv = (float*)calloc(3 * (size_t)c->embd, 4);
         s->xq = (uint8_t*)calloc(wide / 32 * 34 + wide / 256 * 292 + 1024, 1);
     }
     return s;
@@ -876,9 +891,10 @@ void or_session_destroy(oracle_session* s) {
         for (int l = 0; l < s->c.layers; ++l) free(s->vcache[l]);
     free(s->kcache);
     free(s->vcache);
+    for (int l = 0; s->layers && l < s->c.layers; ++l) free(s->layers[l].conv_cache);
     free(s->layers);
     free(s->h); free(s->normed); free(s->q); free(s->k); free(s->v); free(s->att);
-    free(s->proj); free(s->gate); free(s->up); free(s->scores); free(s->rope); free(s->rope_local); free(s->xq);
+    free(s->proj); free(s->gate); free(s->up); free(s->scores); free(s->rope); free(s->rope_local); free(s->conv); free(s->xq);
     free(s);
 }
 
@@ -950,6 +966,25 @@ static void forward_token(oracle_session* s, int32_t token, float* logits) {
     for (int l = 0; l < c->layers; ++l) {
         const layer_t* L = &s->layers[l];
         or_rms_norm(s->h, L->attn_norm, c->eps, s->normed, embd);
+        if (L->conv_w) { /* LFM2 short convolution (src/model.cpp:935-969) */
+            const size_t taps = (size_t)c->conv_taps;
+            float* bcx = s->conv;
+            multiply(s, &L->conv_in, s->normed, bcx);
+            for (size_t d = 0; d < embd; ++d) {
+                bcx[2 * embd + d] *= bcx[d];
+                L->conv_cache[pos * embd + d] = or_float_to_half(bcx[2 * embd + d]);
+            }
+            for (size_t d = 0; d < embd; ++d) s->att[d] = 0.0f;
+            for (size_t k = 0; k < taps; ++k) {
+                if (pos + k + 1 < taps) continue;
+                const uint16_t* row = L->conv_cache + (pos + k + 1 - taps) * embd;
+                for (size_t d = 0; d < embd; ++d) s->att[d] += L->conv_w[d * taps + k] * or_half_to_float(row[d]);
+            }
+            for (size_t d = 0; d < embd; ++d) s->att[d] *= bcx[embd + d];
+            multiply(s, &L->conv_out, s->att, s->proj);
+            for (size_t i = 0; i < embd; ++i) s->h[i] += s->proj[i];
+            goto ffn;
+        }
         multiply(s, &L->q, s->normed, s->q);
         multiply(s, &L->k, s->normed, s->k);
         multiply(s, &L->v, s->normed, s->v);
@@ -1009,6 +1044,7 @@ static void forward_token(oracle_session* s, int32_t token, float* logits) {
         multiply(s, &L->o, s->att, s->proj);
         if (L->attn_post_norm) or_rms_norm(s->proj, L->attn_post_norm, c->eps, s->proj, embd); /* :1116-1119 */
         for (size_t i = 0; i < embd; ++i) s->h[i] += s->proj[i];
+    ffn:
         or_rms_norm(s->h, L->ffn_norm, c->eps, s->normed, embd);
         multiply(s, &L->gate, s->normed, s->gate);
         multiply(s, &L->up, s->normed, s->up);

@@ -25,7 +25,7 @@ extern "C" {
 /* ggml tensor types (src/gguf.h:22-27). */
 enum { OR_F32 = 0, OR_Q4_0 = 2, OR_Q4_1 = 3, OR_Q5_0 = 6, OR_Q8_0 = 8, OR_Q4_K = 12, OR_Q5_K = 13, OR_Q6_K = 14, OR_TQ2_0 = 35 };
 /* Architectures of src/model.h:21-32 that the configs use. */
-enum { OR_QWEN3 = 0, OR_LLAMA = 1, OR_BITNET = 2, OR_QWEN2 = 3, OR_SMOLLM3 = 4, OR_GEMMA3 = 5, OR_PHI3 = 6 };
+enum { OR_QWEN3 = 0, OR_LLAMA = 1, OR_BITNET = 2, OR_QWEN2 = 3, OR_SMOLLM3 = 4, OR_GEMMA3 = 5, OR_PHI3 = 6, OR_LFM2 = 7 };
 
 typedef struct {
     int arch;
@@ -40,6 +40,7 @@ typedef struct {
     int rope_dim;
     float rope_attn_factor;
     int rope_original_context;
+    int conv_taps; /* LFM2 short-convolution width */
 } oracle_config;
 
 /* One tensor of the model: `rows` x `cols` (vectors: rows = 1), GGUF bytes. */

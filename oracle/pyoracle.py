@@ -25,7 +25,7 @@ class OracleConfig(C.Structure):
                 ("rope_base", C.c_float), ("eps", C.c_float), ("max_context", C.c_int),
                 ("sliding_window", C.c_int), ("rope_base_local", C.c_float), ("rope_scale", C.c_float),
                 ("final_softcap", C.c_float), ("rope_dim", C.c_int), ("rope_attn_factor", C.c_float),
-                ("rope_original_context", C.c_int)]
+                ("rope_original_context", C.c_int), ("conv_taps", C.c_int)]
 
 
 class OracleTensor(C.Structure):
@@ -136,7 +136,7 @@ class Oracle:
         self.L, self.cfg, self.max_context = L, cfg, max_context
         c = OracleConfig(cfg.arch, cfg.embd, cfg.layers, cfg.heads, cfg.kv_heads, cfg.head_dim, cfg.ff, cfg.vocab,
                          cfg.rope_base, cfg.eps, max_context, cfg.sliding_window, cfg.rope_base_local, cfg.rope_scale,
-                         cfg.final_softcap, cfg.rope_dim, cfg.rope_attn_factor, cfg.rope_original_context)
+                         cfg.final_softcap, cfg.rope_dim, cfg.rope_attn_factor, cfg.rope_original_context, cfg.conv_taps)
         self._names = [t.name.encode() for t in table]
         arr = (OracleTensor * len(table))()
         for i, t in enumerate(table):

@@ -37,6 +37,7 @@ RUNS = {
     "tiny-gemma3": (12, 48),
     "tiny-phi3": (12, 48),
     "tiny-llama32": (12, 48),
+    "tiny-lfm2": (12, 48),
 }
 
 

@@ -27,7 +27,7 @@ from brisk_hip import HipSession, model, synth  # noqa: E402
 import pyoracle  # noqa: E402
 
 TOL = 2e-2
-FAMILIES = ["tiny-qwen3", "tiny-llama", "tiny-q8", "tiny-bitnet", "tiny-q5k", "tiny-q5", "tiny-qwen2", "tiny-smollm3", "tiny-gemma3", "tiny-phi3", "tiny-llama32"]
+FAMILIES = ["tiny-qwen3", "tiny-llama", "tiny-q8", "tiny-bitnet", "tiny-q5k", "tiny-q5", "tiny-qwen2", "tiny-smollm3", "tiny-gemma3", "tiny-phi3", "tiny-llama32", "tiny-lfm2"]
 
 
 def _session(src, ctx, mfma):

@@ -96,7 +96,7 @@ def test_spec_bytes_match_the_measurement_contract():
     assert s.output_bytes() == 165_306_368
 
 
-@pytest.mark.parametrize("name", ["tiny-qwen3", "tiny-llama", "tiny-bitnet", "tiny-q5k", "tiny-q5", "tiny-qwen2", "tiny-smollm3", "tiny-gemma3", "tiny-phi3", "tiny-llama32"])
+@pytest.mark.parametrize("name", ["tiny-qwen3", "tiny-llama", "tiny-bitnet", "tiny-q5k", "tiny-q5", "tiny-qwen2", "tiny-smollm3", "tiny-gemma3", "tiny-phi3", "tiny-llama32", "tiny-lfm2"])
 def test_model_config_parse(name):
     spec = synth.SPECS[name]
     f, cfg, table = model.load(synth.model_path(name))
@@ -107,7 +107,7 @@ def test_model_config_parse(name):
     assert ("output.weight" in names) == (spec.out_fmt is not None)
 
 
-@pytest.mark.parametrize("name", ["tiny-qwen3", "tiny-llama", "tiny-bitnet", "tiny-q5k", "tiny-q5", "tiny-qwen2", "tiny-smollm3", "tiny-gemma3", "tiny-phi3", "tiny-llama32"])
+@pytest.mark.parametrize("name", ["tiny-qwen3", "tiny-llama", "tiny-bitnet", "tiny-q5k", "tiny-q5", "tiny-qwen2", "tiny-smollm3", "tiny-gemma3", "tiny-phi3", "tiny-llama32", "tiny-lfm2"])
 def test_session_estimate(name):
     """brisk_hip_session_estimate (HBM counterpart of estimate_memory, src/memory.cpp:46-96): shapes only, no GPU."""
     from brisk_hip.session import estimate

@@ -400,7 +400,7 @@ def tiny(name):
     return path, f, cfg, table
 
 
-@pytest.mark.parametrize("name", ["tiny-qwen3", "tiny-llama", "tiny-q8", "tiny-bitnet", "tiny-q5k", "tiny-q5", "tiny-qwen2", "tiny-smollm3", "tiny-gemma3", "tiny-phi3", "tiny-llama32"])
+@pytest.mark.parametrize("name", ["tiny-qwen3", "tiny-llama", "tiny-q8", "tiny-bitnet", "tiny-q5k", "tiny-q5", "tiny-qwen2", "tiny-smollm3", "tiny-gemma3", "tiny-phi3", "tiny-llama32", "tiny-lfm2"])
 def test_oracle_greedy_matches_reference_fixture(name):
     """tests/golden/<name>_greedy.json were written by the reference engine itself."""
     with open(os.path.join(HERE, "golden", f"{name}_greedy.json")) as fh:
@@ -429,7 +429,7 @@ def test_oracle_first_tokens_of_qwen3_0_6b_fixture():
 
 
 @needs_ref
-@pytest.mark.parametrize("name", ["tiny-qwen3", "tiny-llama", "tiny-bitnet", "tiny-q5k", "tiny-q5", "tiny-qwen2", "tiny-smollm3", "tiny-gemma3", "tiny-phi3", "tiny-llama32"])
+@pytest.mark.parametrize("name", ["tiny-qwen3", "tiny-llama", "tiny-bitnet", "tiny-q5k", "tiny-q5", "tiny-qwen2", "tiny-smollm3", "tiny-gemma3", "tiny-phi3", "tiny-llama32", "tiny-lfm2"])
 def test_oracle_session_matches_reference_bitwise(name):
     """eval, eval_all and rollback of the restatement against the reference's Session."""
     path, f, cfg, table = tiny(name)
