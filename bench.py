@@ -247,7 +247,7 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU; --gpus {args.gpus} is not supported "
-              "(the token loop is single-device; see the multi-GPU note in DESIGN.md)", file=sys.stderr)
+              "(the token loop runs on a single device; a multi-GPU run would shard the layers' rows per GPU)", file=sys.stderr)
         sys.exit(2)
 
     if args.copy_calibration:
