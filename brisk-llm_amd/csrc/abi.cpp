@@ -2,6 +2,7 @@
 #include <hip/hip_runtime.h>
 
 #include <exception>
+#include <mutex>
 #include <new>
 #include <string>
 
@@ -13,6 +14,12 @@ struct brisk_hip_session {
     template <typename... A>
     explicit brisk_hip_session(A&&... a) : impl(static_cast<A&&>(a)...) {}
 };
+
+// The no-alloc matmul's staging: the planar int8 activation rows (values,
+// scales, sums) that brisk_hip_matmul otherwise hipMallocs per call.  One copy
+// per GPU, held until the process ends; every no-alloc call on a GPU reuses it.
+constexpr size_t kNoAllocScratch = size_t{4} << 20;
+static __device__ __align__(256) unsigned char scratch[kNoAllocScratch];
 
 namespace {
 
@@ -61,6 +68,25 @@ bh::Packed packed_view(int type, int flags, const void* packed, size_t rows, siz
                  static_cast<uint32_t>(flags) & bh::kFlagLut16};
     if (type != BRISK_HIP_TQ2_0) p.flags = 0;
     return p;
+}
+
+// The device address of `scratch` on the current device.  The array's name is
+// only a host-side handle: its address differs per GPU and comes from
+// hipGetSymbolAddress, looked up once per device with that device current.
+void* noalloc_scratch() {
+    constexpr int kMaxDevices = 64;
+    static std::mutex mu;
+    static void* ptrs[kMaxDevices] = {};
+    int dev = 0;
+    hip_check(hipGetDevice(&dev), "hipGetDevice");
+    if (dev < 0 || dev >= kMaxDevices) throw bh::Error(BRISK_HIP_ENODEV, "kernels: device index out of range");
+    std::lock_guard<std::mutex> lock(mu);
+    if (ptrs[dev] == nullptr) {
+        void* ptr = nullptr;
+        hip_check(hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)), "hipGetSymbolAddress");
+        ptrs[dev] = ptr;
+    }
+    return ptrs[dev];
 }
 
 }  // namespace
@@ -144,6 +170,39 @@ int brisk_hip_matmul(int type, int flags, const void* packed, size_t rows, size_
         (void)hipFree(mem);
         hip_check(e, "matmul");
         hip_check(e2, "matmul sync");
+    });
+}
+
+int brisk_hip_matmul_noalloc(int type, int flags, const void* packed, size_t rows, size_t cols, const void* xq, size_t n,
+                             float* out, size_t out_stride, void* stream) {
+    return guarded([&] {
+        const bh::Packed p = packed_view(type, flags, packed, rows, cols);
+        if (n == 0 || n > 65535) throw bh::Error(BRISK_HIP_EINVAL, "kernels: n must be 1..65535");
+        if (out_stride < rows) throw bh::Error(BRISK_HIP_EINVAL, "kernels: out_stride < rows");
+        const hipStream_t st = static_cast<hipStream_t>(stream);
+        if (n == 1) {  // the matvec takes no scratch
+            hip_check(bh::launch_matvec_q8(p, xq, n, out, out_stride, st), "matmul");
+            return;
+        }
+        const int stride = static_cast<int>((cols + 255) / 256 * 256);
+        const size_t qb = n * static_cast<size_t>(stride), db = n * static_cast<size_t>(stride / 32) * 4,
+                     bb = n * static_cast<size_t>(stride / 16) * 4;
+        if (qb + db + bb > kNoAllocScratch)
+            throw bh::Error(BRISK_HIP_EINVAL, "kernels: " + std::to_string(n) + " rows of " + std::to_string(cols) +
+                                                  " columns need " + std::to_string(qb + db + bb) +
+                                                  " bytes of scratch; the no-alloc matmul holds " +
+                                                  std::to_string(kNoAllocScratch));
+        char* mem = static_cast<char*>(noalloc_scratch());
+        bh::ActPlanar x{};
+        x.stride = stride;
+        x.qs = reinterpret_cast<int8_t*>(mem);
+        x.d = reinterpret_cast<float*>(mem + qb);
+        x.bs = reinterpret_cast<int32_t*>(mem + qb + db);
+        hip_check(bh::launch_pre_planar(xq, static_cast<int>(cols), static_cast<int>(n), bh::takes_q8_k(p.type), x, st),
+                  "matmul");
+        bh::MmArgs g{};
+        g.m = p; g.x = x; g.ntok = static_cast<int>(n); g.out = out; g.ostride = static_cast<int>(out_stride);
+        hip_check(bh::launch_mm(g, bh::kMmStore, st), "matmul");
     });
 }
 

@@ -134,6 +134,18 @@ int brisk_hip_matvec(int type, int flags, const void* packed, size_t rows, size_
 int brisk_hip_matmul(int type, int flags, const void* packed, size_t rows, size_t cols, const void* xq, size_t n,
                      float* out, size_t out_stride, void* stream);
 
+/* brisk_hip_matmul without any device allocation.  No counterpart in the
+ * reference: it is for callers that cannot allocate (code under HIP graph
+ * capture, tight serving loops, hosts that forbid hipMalloc).  For n > 1 the
+ * batch's activation rows are staged in a static device buffer of 4 MiB, one
+ * per GPU, held until the process ends (n x ceil(cols / 256) x 256 x 1.375
+ * bytes must fit, e.g. 372 rows of 8192 columns; larger requests fail with
+ * BRISK_HIP_EINVAL).  Outputs are identical to brisk_hip_matmul's.  The call
+ * does not synchronise: the buffer is reused by the next call on that GPU, so
+ * calls on one GPU that overlap (other streams, other threads) race. */
+int brisk_hip_matmul_noalloc(int type, int flags, const void* packed, size_t rows, size_t cols, const void* xq, size_t n,
+                             float* out, size_t out_stride, void* stream);
+
 /* The decode GEMV of the token loop: quantises the f32 row x in-kernel (after
  * rms_norm with weight `norm_w` and `eps` when norm_w is non-null), then
  * out = W x, or out += W x when `accumulate` (the residual update). */
