@@ -106,7 +106,9 @@ def cpu_baseline(path, prompt, n_gen):
     import pyoracle
     if not pyoracle.ref_available():
         return None
-    threads = max(1, min(16, os.cpu_count() or 1))
+    # `-t $(nproc)` as BASELINE.md runs the reference: nproc counts the cores this process may run on
+    nproc = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else (os.cpu_count() or 1)
+    threads = max(1, min(128, nproc))
     ref = pyoracle.Reference(path, threads=threads, max_context=len(prompt) + n_gen + 8)
     ids, gaps, pre_s, gen_s = ref.generate(prompt, n_gen)
     ref.close()
@@ -123,7 +125,7 @@ def cpu_baseline(path, prompt, n_gen):
             "sample": f"the full decode workload: qwen3-0.6b-shape, {len(prompt)}-id prompt then {n_gen} greedy tokens "
                       f"(generation tok/s = (tokens - 1) / generation seconds, as src/main.cpp:312-318; {threads} threads "
                       f"of {model or 'host CPU'}); prompt {len(prompt) / pre_s:.1f} tok/s",
-            "one_thread_tok_s": round(7 / gen1, 3),
+            "one_thread_tok_s": round(7 / gen1, 3), "nproc": nproc, "cpu_count": os.cpu_count(),
             "ids": ids}
 
 
@@ -211,14 +213,15 @@ def other_configs(torch, HipSession, model, synth):
 
 
 def profiled_traffic(steps):
-    """HBM bytes of the decode launch measured by rocprofv3 (FETCH_SIZE + WRITE_SIZE, each scaled by a plain
-    copy's reading) for the default 256-step workload; None for other step counts or without the summary."""
+    """HBM bytes of a `steps`-step decode launch measured by rocprofv3 (FETCH_SIZE + WRITE_SIZE, each scaled by a
+    plain copy's reading), from the summary's `traffic_bytes_per_launch_K<steps>:` line (profiled for K = 256,
+    the default, and K = 20, the driver's); None for a step count that was not profiled."""
     p = os.path.join(ROOT, "profiles", "k_loop_qwen3-0.6b_decode.md")
-    if steps != 256 or not os.path.exists(p):
+    if not os.path.exists(p):
         return None
     with open(p) as fh:
         for line in fh:
-            if line.startswith("traffic_bytes_per_launch:"):
+            if line.startswith(f"traffic_bytes_per_launch_K{steps}:"):
                 return int(line.split(":")[1])
     return None
 
@@ -269,7 +272,7 @@ def main():
     prompt = synth.prompt_ids(32, cfg.vocab)
     K, W = args.steps, args.warmup
     t0 = time.time()
-    s = HipSession((f, cfg, table), max_context=len(prompt) + max(K, W) + 64)
+    s = HipSession((f, cfg, table), max_context=len(prompt) + max(K, W, 256) + 64)
     log(f"session load {time.time() - t0:.1f}s")
 
     # warmup: prompt + W steps, then back to the start of the workload
@@ -295,6 +298,22 @@ def main():
     mean_bytes = launch_bytes / K
     log(f"decode: {K} steps in {dt * 1e3:.1f} ms (k_loop {loop_ms:.1f} ms by events) -> {tok_s:.1f} tok/s, "
         f"{ms_step * 1e3:.1f} us/step, {mean_bytes / 1e6:.1f} MB/step -> {launch_bytes / (loop_ms * 1e-3) / 1e9:.1f} GB/s")
+    # the whole configs[1] workload (256 steps after the prompt), whatever K is: its rate and its 256 ids
+    FULL = 256
+    if K == FULL:
+        full_s, full_ids = dt, ids
+    else:
+        s.rollback(0)
+        ffirst = s.eval_greedy(prompt)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        full_ids = s.decode(FULL)
+        torch.cuda.synchronize()
+        full_s = time.perf_counter() - t0
+        gen_full = np.concatenate([[ffirst], full_ids])
+    full_gen = gen if K == FULL else gen_full
+    full_bytes = int(sum(spec.decode_bytes(len(prompt) + i) for i in range(FULL)))
+    log(f"full workload: {FULL} steps in {full_s * 1e3:.1f} ms -> {FULL / full_s:.1f} tok/s")
     s.close()
     del s
     torch.cuda.empty_cache()
@@ -316,12 +335,18 @@ def main():
     if traffic is not None:
         result["roofline"]["traffic"] = traffic
         result["roofline"]["traffic_source"] = "profiles/k_loop_qwen3-0.6b_decode.md (rocprofv3 FETCH_SIZE + WRITE_SIZE, copy-calibrated)"
+    else:
+        result["roofline"]["traffic_note"] = f"no rocprofv3 FETCH_SIZE/WRITE_SIZE pass on file for a {K}-step launch"
+    result["full_workload"] = {"workload": "configs[1] as specified: 32-id prompt, then 256 greedy decode steps in one launch",
+                               "value": round(FULL / full_s, 2), "unit": "tok/s", "ms_per_step": round(full_s / FULL * 1e3, 4),
+                               "achieved_gb_s": round(full_bytes / full_s / 1e9, 2),
+                               "frac": round(full_bytes / full_s / HBM_PEAK, 4)}
     golden = os.path.join(ROOT, "tests", "golden", "qwen3-0.6b_greedy.json")
     if os.path.exists(golden):
         with open(golden) as fh:
             want = json.load(fh)["ids"]
-        n = min(len(gen), len(want))
-        result["greedy_matches_reference"] = bool(list(map(int, gen[:n])) == want[:n])
+        n = min(len(full_gen), len(want))
+        result["greedy_matches_reference"] = bool(list(map(int, full_gen[:n])) == want[:n])
         result["greedy_compared"] = n
 
     if not args.no_kernels:
@@ -429,7 +454,10 @@ def main():
         cb = cpu_baseline(path, prompt, 256)
         if cb is not None:
             ref_ids = cb.pop("ids")
-            cb["greedy_matches_gpu"] = bool(np.array_equal(ref_ids, gen[:len(ref_ids)]))
+            # the common prefix of the reference's 256 ids and the timed run's K + 1
+            nc = min(len(ref_ids), len(full_gen))
+            cb["greedy_matches_gpu"] = bool(np.array_equal(np.asarray(ref_ids[:nc]), full_gen[:nc]))
+            cb["greedy_compared"] = int(nc)
             result["cpu_baseline"] = cb
             log(f"cpu baseline ({time.time() - t0:.1f}s): {cb['value']} tok/s on {cb['cores']} threads")
         else:

@@ -33,6 +33,9 @@ struct LoopArgs {
     int ctx;
     // tagged hand-off words: (tag << 32) | float bits
     unsigned long long *ht, *qt, *kt, *vt, *attt, *actt, *pacct, *pmlt;
+    unsigned long long* sct;   // the spread attention's scores: [kv head][head][position], packed by length
+    // exact attention spread over the grid (stage 1 by position chunks, stage 2 by 32-wide value slices)
+    int spread;
     unsigned tag_base;
     float* logits;
     int max_splits;
@@ -51,6 +54,9 @@ struct LoopArgs {
     // O and down tiles cover the same rows of h on the same workgroup, which
     // then keeps its rows of h in LDS for the residual adds
     int own_h;
+    // the O and down tiles (phases C and F) go to workgroups c_first, c_first + 1, ...: with the
+    // spread attention the workgroups of its second stage, which finish phase B last, take none
+    int c_first;
     // the attention output is handed to phase C quantised (Q8_0 O matrix, no sub-norm)
     int att_q8;
     // exact attention one workgroup per query head (else one per key/value head)
@@ -60,6 +66,8 @@ struct LoopArgs {
 constexpr int kOwnRows = 256;  // rows of h one workgroup can keep
 
 int loop_units_per_thread(uint32_t type, bool head);
+// Whether the spread exact attention takes this shape on a grid of `grid` workgroups.
+bool loop_spread_fits(int heads, int kv_heads, int head_dim, int rope_dim, int grid);
 
 const void* find_loop_kernel(uint32_t tq, uint32_t tv, uint32_t to, uint32_t tg, uint32_t td, uint32_t th);
 hipError_t launch_loop(const void* kernel, const LoopArgs& g, int grid, hipStream_t s);

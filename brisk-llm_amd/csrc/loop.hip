@@ -138,10 +138,32 @@ struct GemvLds {
     double red[4];
     float x[kMaxCols];  // the phase's input vector
 };
+// The spread exact attention (phase_b_spread): stage 1 scores a chunk of
+// positions, stage 2 turns a head's scores into weights and sums one 32-wide
+// slice of the values.
+constexpr int kSpreadSlice = 32;                 // value dimensions a stage-2 task (one Q8_0 block a head)
+constexpr int kSpreadHpk = 8;                    // query heads a key/value head, at most
+constexpr int kSpreadChunk = 64;                 // positions a stage-1 task, at most
+constexpr int kVtStride = kExactMax + 8;         // halves a transposed value row (16-byte aligned, banks staggered)
+struct SpreadLds {
+    alignas(16) float q[kSpreadHpk * 128];       // stage 1: the query heads, normed and rotated
+    alignas(16) float kcur[128];                 // stage 1 (writer): this token's key
+    alignas(16) float vcur[kSpreadSlice];        // stage 2: this token's values of the slice
+    alignas(16) float rope[128];                 // stage 1: the rotation row of this position
+    alignas(16) float qn[128];                   // stage 1: q_norm / k_norm weights
+    alignas(16) float kn[128];
+    alignas(16) float sc[kSpreadHpk * kExactMax];   // stage 2: scores [head][position]
+    alignas(16) float wt[kSpreadHpk * kExactMax];   // stage 2: weights [head][position, padded to 8]
+    alignas(16) uint16_t kst[kSpreadChunk * 128];   // stage 1: the chunk's cached keys [position][dim]
+    alignas(16) uint16_t vraw[kExactMax * kSpreadSlice];  // stage 2: cached values of the slice [position][dim]
+    alignas(16) uint16_t vt[kSpreadSlice * kVtStride];    // stage 2: the same, transposed [dim][position]
+};
+
 union LoopLds {
     GemvLds g;
     AttnLds att;
     AttnPoolLds pool;
+    SpreadLds spread;
 };
 
 // Trace: workgroup 0's wall clock at point `pt` of phase `ph` of every (step,
@@ -197,12 +219,14 @@ __host__ __device__ constexpr int head_units(uint32_t type) { return (type == kQ
 // `row_of(t, m, R)` maps a tile to (matrix, first row); `done(t, sums)` is the
 // epilogue.  `ready()` waits for the input and prepares the activation; it runs
 // once, after the first tile's loads are issued.  Returns false when abandoning.
+// The tiles go to workgroups first, first + 1, ... (first > 0 keeps the first
+// workgroups, busy elsewhere, out of the phase).
 template <uint32_t T, int M, class RowOf, class Ready, class Done>
 __device__ __forceinline__ bool run_tiles(int total, GemvLds& s, RowOf row_of, Ready ready, Done done,
-                                          Stamps st = Stamps{nullptr, nullptr}) {
-    const int G = static_cast<int>(gridDim.x);
-    int t = static_cast<int>(blockIdx.x);
-    if (t >= total) return true;
+                                          Stamps st = Stamps{nullptr, nullptr}, int first = 0) {
+    const int G = static_cast<int>(gridDim.x) - first;
+    int t = static_cast<int>(blockIdx.x) - first;
+    if (t < 0 || t >= total) return true;
     Tile<T, M> ta, tb;
     Packed ma, mb;  // by value: a pointer to a kernel-argument member would force a private copy
     uint32_t ra, rb = 0;
@@ -719,12 +743,299 @@ __device__ __forceinline__ bool attn_head_pool(const LoopArgs& lg, const AttnArg
     return true;
 }
 
+// ---------------------------------------------------------------- spread exact attention
+
+// Attention in the reference's order (src/model.cpp:1050-1093, src/kernels_f32.cpp:256-284),
+// spread over the grid so that no workgroup streams a whole head's cache:
+//
+//  stage 1, task (kv, c) on workgroup n2 + kv * per_kv + c: the query heads of
+//    key/value head kv (bias, q_norm, RoPE), then their scores against the
+//    positions of chunk c, each dot_f32(q, k) * scale (16 lane sums, then the
+//    lanes added in order).  The task holding this token's position also
+//    normalises and rotates its key, rounds it to fp16 and stores the cache row.
+//    Scores go out as tagged words, [kv][head][position] packed by length L.
+//  stage 2, task (kv, slice) on workgroup kv * slices + slice: every score of
+//    the group's heads, softmax (max, expf, double sum, multiply by the float of
+//    1 / sum), then out[h][d] = sum over positions in order of w[h][p] v[p][d]
+//    (each product rounded, then added) for the slice's 32 dimensions, one
+//    chain a lane.  It also rounds this token's values of the slice to fp16 and
+//    stores them into the cache row.
+//
+// A stage-1 task reads its chunk's keys and a stage-2 task its slice's values;
+// both are requested before the task's inputs are awaited.  Every cache row a
+// task stores is in memory before the task publishes (s_waitcnt), so later
+// steps, which depend on what it published, see it.
+// The rotation pair of lane `lane` in a head of hd values rotated whole
+// (apply_rope, src/model.cpp:100-115): (i, i + hd / 2) in the NeoX layout,
+// (2 i, 2 i + 1) otherwise; lanes from hd / 2 on hold none.
+struct Pair {
+    int ia, ib;
+    bool live;
+};
+__device__ __forceinline__ Pair rope_pair(int lane, int hd, int neox) {
+    Pair p;
+    p.live = lane < hd / 2;
+    p.ia = neox ? lane : 2 * lane;
+    p.ib = neox ? lane + hd / 2 : 2 * lane + 1;
+    if (!p.live) p.ia = p.ib = 0;
+    return p;
+}
+
+// The per-lane constants of a head's norm and rotation, fetched before the inputs arrive.
+struct PairConst {
+    float wa, wb, c, sn;
+};
+__device__ __forceinline__ PairConst pair_const(const Pair& p, const float* w, const float* rope_row) {
+    PairConst k{1.0f, 1.0f, 1.0f, 0.0f};
+    if (p.live) {
+        if (w != nullptr) { k.wa = w[p.ia]; k.wb = w[p.ib]; }
+        if (rope_row != nullptr) {
+            const int i = static_cast<int>(threadIdx.x & 63);
+            k.c = rope_row[2 * i];
+            k.sn = rope_row[2 * i + 1];
+        }
+    }
+    return k;
+}
+
+// Bias, RMS norm (float squares summed in double, src/model.cpp:87-97) and
+// rotation of one head in LDS (v), by one wave, each lane on its pair in registers.
+__device__ __forceinline__ void pair_norm_rope(float* v, const Pair& p, const PairConst& k, const float* bias, bool norm,
+                                               bool rope, int hd, float eps) {
+    float a = p.live ? v[p.ia] : 0.0f, b = p.live ? v[p.ib] : 0.0f;
+    if (bias != nullptr && p.live) {
+        a = a + bias[p.ia];
+        b = b + bias[p.ib];
+    }
+    if (norm) {
+        double s2 = static_cast<double>(a * a);
+        s2 += static_cast<double>(b * b);
+        const float scale = rms_scale(wave_sum(s2), hd, eps);
+        a = a * scale * k.wa;
+        b = b * scale * k.wb;
+    }
+    if (rope) {
+        const float x0 = a, x1 = b;
+        a = x0 * k.c - x1 * k.sn;
+        b = x0 * k.sn + x1 * k.c;
+    }
+    if (p.live) {
+        v[p.ia] = a;
+        v[p.ib] = b;
+    }
+}
+
+__device__ __forceinline__ bool spread_stage1(const LoopArgs& g, const AttnArgs& a, SpreadLds& s, int kv, int p0, int p1,
+                                              int pos, unsigned tin, unsigned tsc, const Stamps& st) {
+    const int hd = a.head_dim, hpk = a.heads / a.kv_heads, t = threadIdx.x, wave = t >> 6, Lc = pos + 1;
+    const bool writer = p1 == Lc;
+    const int cached = (writer ? pos : p1) - p0;
+    const float* rope_row = a.rope != nullptr ? a.rope + static_cast<size_t>(pos) * a.rope_dim : nullptr;
+    const Pair pr = rope_pair(t & 63, hd, a.neox);
+    // the norm and rotation constants of the head(s) this wave will take (queries: q_norm, the writer's key: k_norm)
+    const PairConst kq = pair_const(pr, a.qnorm, rope_row), kk = pair_const(pr, a.knorm, rope_row);
+    bool fail = false;
+    if (wave == 0) {  // this token's query heads (and, for the writer, key) while the others stage the keys
+        fail = !wget_segs<8>(g, tin, TSeg{g.qt + kv * hpk * hd, s.q, hpk * hd},
+                             writer ? TSeg{g.kt + kv * hd, s.kcur, hd} : TSeg{nullptr, nullptr, 0}, TSeg{nullptr, nullptr, 0});
+    } else if (cached > 0) {
+        chunk_issue_by(s.kst, a.kcache + static_cast<size_t>(kv) * a.ctx * hd, p0, cached, hd, false, t - 64, kThreads - 64);
+    }
+    __builtin_amdgcn_s_waitcnt(0);
+    if (__syncthreads_or(fail)) return false;
+    pst(st, 1);
+    // q_norm / k_norm and RoPE (src/model.cpp:1026-1041); the key rounded to fp16 as the cache holds it
+    for (int h = wave; h < hpk + (writer ? 1 : 0); h += kThreads / 64) {
+        if (h < hpk)
+            pair_norm_rope(s.q + h * hd, pr, kq, a.qbias != nullptr ? a.qbias + (kv * hpk + h) * hd : nullptr, a.qnorm != nullptr,
+                           rope_row != nullptr, hd, a.eps);
+        else {
+            pair_norm_rope(s.kcur, pr, kk, a.kbias != nullptr ? a.kbias + kv * hd : nullptr, a.knorm != nullptr, rope_row != nullptr,
+                           hd, a.eps);
+            for (int i = t & 63; i < hd; i += 64) s.kst[(pos - p0) * hd + i] = f2h(s.kcur[i]);
+        }
+    }
+    __syncthreads();
+    pst(st, 2);
+    // scores: 4 threads a (head, position), thread r holding dot_f32's lanes 4 r .. 4 r + 3; the
+    // lanes are added in order (0 + lane 0 + ... + lane 15), each thread adding its four to the
+    // running sum it takes from the thread before it
+    const int n = p1 - p0, items = hpk * n, per = hd / 16, r = t & 3;
+    for (int base = 0; base < items; base += kThreads / 4) {
+        const int it = base + (t >> 2);
+        const bool live = it < items;
+        const int h = live ? it / n : 0, p = live ? it - h * n : 0;
+        float l0 = 0.0f, l1 = 0.0f, l2 = 0.0f, l3 = 0.0f;
+        const float* q = s.q + h * hd + 4 * r;
+        const uint16_t* k = s.kst + p * hd + 4 * r;
+        for (int m = 0; m < per; ++m) {
+            const float4 qv = *reinterpret_cast<const float4*>(q + 16 * m);
+            const uint2 kw = *reinterpret_cast<const uint2*>(k + 16 * m);
+            l0 += mul_h<false>(qv.x, kw.x);
+            l1 += mul_h<true>(qv.y, kw.x);
+            l2 += mul_h<false>(qv.z, kw.y);
+            l3 += mul_h<true>(qv.w, kw.y);
+        }
+        float sum = 0.0f;
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const float prev = __shfl_up(sum, 1, 4);
+            if (r == u) sum = ((((u == 0 ? 0.0f : prev) + l0) + l1) + l2) + l3;
+        }
+        if (live && r == 3)
+            tput(g.sct + static_cast<size_t>(kv * hpk + h) * Lc + p0 + p, sum * a.scale, tsc);
+    }
+    pst(st, 3);
+    return true;
+}
+
+template <class O>
+__device__ __forceinline__ bool spread_stage2(const LoopArgs& g, const AttnArgs& a, SpreadLds& s, int kv, int d0, int pos,
+                                              unsigned tin, unsigned tsc, const O& o, const Stamps& st) {
+    const int hd = a.head_dim, hpk = a.heads / a.kv_heads, t = threadIdx.x, wave = t >> 6, lane = t & 63, Lc = pos + 1;
+    const float* rope_row = a.rope != nullptr ? a.rope + static_cast<size_t>(pos) * a.rope_dim : nullptr;
+    bool fail = false;
+    if (wave == 0) {
+        // this token's key (all of it: its norm spans the head) and values of the slice; the key
+        // normalised and rotated, then the slice of both rows rounded to fp16 into the cache rows
+        // (store_f16, src/kernels_f32.cpp:248-250) and the values into position pos of the slice
+        const Pair pr = rope_pair(lane, hd, a.neox);
+        const PairConst kk = pair_const(pr, a.knorm, rope_row);
+        fail = !wget_segs<4>(g, tin, TSeg{g.kt + kv * hd, s.kcur, hd}, TSeg{g.vt + kv * hd + d0, s.vcur, kSpreadSlice},
+                             TSeg{nullptr, nullptr, 0});
+        if (!fail) {
+            pair_norm_rope(s.kcur, pr, kk, a.kbias != nullptr ? a.kbias + kv * hd : nullptr, a.knorm != nullptr, rope_row != nullptr,
+                           hd, a.eps);
+            if (lane < kSpreadSlice / 2) {
+                const int d = 2 * lane;
+                uint16_t* kr = a.kcache + (static_cast<size_t>(kv) * a.ctx + pos) * hd + d0;
+                uint16_t* vr = a.vcache + (static_cast<size_t>(kv) * a.ctx + pos) * hd + d0;
+                const uint16_t k0 = f2h(s.kcur[d0 + d]), k1 = f2h(s.kcur[d0 + d + 1]);
+                const float b0 = a.vbias != nullptr ? a.vbias[kv * hd + d0 + d] : 0.0f;
+                const float b1 = a.vbias != nullptr ? a.vbias[kv * hd + d0 + d + 1] : 0.0f;
+                const uint16_t v0 = f2h(a.vbias != nullptr ? s.vcur[d] + b0 : s.vcur[d]);
+                const uint16_t v1 = f2h(a.vbias != nullptr ? s.vcur[d + 1] + b1 : s.vcur[d + 1]);
+                s.vt[d * kVtStride + pos] = v0;
+                s.vt[(d + 1) * kVtStride + pos] = v1;
+                __hip_atomic_store(reinterpret_cast<uint32_t*>(kr + d), k0 | (static_cast<uint32_t>(k1) << 16), __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_SYSTEM);
+                __hip_atomic_store(reinterpret_cast<uint32_t*>(vr + d), v0 | (static_cast<uint32_t>(v1) << 16), __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_SYSTEM);
+            }
+        }
+    } else {
+        // the slice's cached values, 4 pieces of 16 bytes a position: each of waves 1-3 stages
+        // its pieces into [position][32] and transposes them to [dim][position] once they land
+        const uint8_t* src = reinterpret_cast<const uint8_t*>(a.vcache + static_cast<size_t>(kv) * a.ctx * hd + d0);
+        uint8_t* dst = reinterpret_cast<uint8_t*>(s.vraw);
+        const int r = t - 64, nt = kThreads - 64, pieces = pos * 4, wave_first = r & ~63;
+        for (int k = 0; k * nt < pieces; ++k) {
+            const int i = k * nt + r;
+            if (i < pieces)
+                __builtin_amdgcn_global_load_lds((global_cvoid_ptr)(src + static_cast<size_t>(i >> 2) * hd * 2 + (i & 3) * 16),
+                                                 (lds_void_ptr)(dst + (k * nt + wave_first) * 16), 16, 0, 0);
+        }
+        __builtin_amdgcn_s_waitcnt(0);
+        for (int k = 0; k * nt < pieces; ++k) {
+            const int i = k * nt + r;
+            if (i < pieces) {
+                const int p = i >> 2, c = (i & 3) * 8;
+                const uint4 w = *reinterpret_cast<const uint4*>(s.vraw + p * kSpreadSlice + c);
+                const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    s.vt[(c + 2 * e) * kVtStride + p] = static_cast<uint16_t>(ws[e]);
+                    s.vt[(c + 2 * e + 1) * kVtStride + p] = static_cast<uint16_t>(ws[e] >> 16);
+                }
+            }
+        }
+    }
+    if (__syncthreads_or(fail)) {
+        __builtin_amdgcn_s_waitcnt(0);
+        return false;
+    }
+    // every score of the group
+    if (!tget_vec(g, g.sct + static_cast<size_t>(kv) * hpk * Lc, tsc, s.sc, hpk * Lc)) {
+        __builtin_amdgcn_s_waitcnt(0);
+        return false;
+    }
+    pst(st, 4);
+    // softmax of each head's row (softmax_f32, src/kernels_f32.cpp:275-285), a wave a head
+    const int Ls = (Lc + 7) & ~7;
+    for (int h = wave; h < hpk; h += kThreads / 64) {
+        const float* sc = s.sc + h * Lc;
+        float* wt = s.wt + h * Ls;
+        float m = -INFINITY;
+        for (int p = lane; p < Lc; p += 64) m = fmaxf(m, sc[p]);
+        m = wave_max(m);
+        double part = 0.0;
+        for (int p = lane; p < Lc; p += 64) {
+            const float e = ref_expf_s(sc[p] - m);
+            wt[p] = e;
+            part += static_cast<double>(e);
+        }
+        const float scale = static_cast<float>(1.0 / wave_sum(part));
+        for (int p = lane; p < Lc; p += 64) wt[p] *= scale;
+    }
+    __syncthreads();
+    pst(st, 5);
+    // value sums, one (head, dimension) chain a lane, positions in order (weighted_sum_f32, :265-273)
+    if (t < hpk * kSpreadSlice) {
+        const int h = t / kSpreadSlice, d = t - h * kSpreadSlice;
+        const float* w = s.wt + h * Ls;
+        const uint16_t* vrow = s.vt + d * kVtStride;
+        float acc = 0.0f;
+        const int full = Lc & ~7;
+        int p = 0;
+        if (full > 0) {  // eight positions a round, the next round's weights and values read a round ahead
+            float4 w0 = *reinterpret_cast<const float4*>(w), w1 = *reinterpret_cast<const float4*>(w + 4);
+            uint4 vv = *reinterpret_cast<const uint4*>(vrow);
+            for (; p < full; p += 8) {
+                const int pn = p + 8 < full ? p + 8 : p;
+                const float4 n0 = *reinterpret_cast<const float4*>(w + pn), n1 = *reinterpret_cast<const float4*>(w + pn + 4);
+                const uint4 nv = *reinterpret_cast<const uint4*>(vrow + pn);
+                acc += mul_h<false>(w0.x, vv.x); acc += mul_h<true>(w0.y, vv.x);
+                acc += mul_h<false>(w0.z, vv.y); acc += mul_h<true>(w0.w, vv.y);
+                acc += mul_h<false>(w1.x, vv.z); acc += mul_h<true>(w1.y, vv.z);
+                acc += mul_h<false>(w1.z, vv.w); acc += mul_h<true>(w1.w, vv.w);
+                w0 = n0; w1 = n1; vv = nv;
+            }
+        }
+        for (; p < Lc; ++p) acc += mul_h<false>(w[p], vrow[p]);
+        if (t < kSpreadSlice / 2) __builtin_amdgcn_s_waitcnt(0);  // the cache rows are in memory before any output
+        o.att((kv * hpk + h) * hd + d0 + d, acc);
+    }
+    pst(st, 6);
+    return true;
+}
+
+// B, spread: the tasks of both stages; a workgroup with neither goes on to phase C.
+__device__ __forceinline__ bool phase_b_spread(const LoopArgs& g, const LayerDev& L, int step, int l, int pos, SpreadLds& s) {
+    const int kvh = g.kv_heads, hd = g.head_dim, Lc = pos + 1, G = static_cast<int>(gridDim.x);
+    const int slices = hd / kSpreadSlice, n2 = kvh * slices, per_kv = (G - n2) / kvh;
+    int P1 = (Lc + per_kv - 1) / per_kv;
+    P1 = P1 < 4 ? 4 : P1;
+    const int chunks = (Lc + P1 - 1) / P1;
+    const unsigned tin = tag_of(g, step, l, 1), tsc = tag_of(g, step, l, 6), tout = tag_of(g, step, l, 2);
+    const AttnArgs a = attn_args(g, L, step, l);
+    const int b = static_cast<int>(blockIdx.x);
+    if (b < n2) {
+        const TaggedOut o{g.attt, g.pacct, g.pmlt, tout, g.error, g.att_q8, g.heads * g.head_dim};
+        return spread_stage2(g, a, s, b / slices, (b % slices) * kSpreadSlice, pos, tin, tsc, o, pst_ptr(g, step, l, 1));
+    }
+    const int task = b - n2, kv = task / per_kv, c = task - kv * per_kv;
+    if (kv >= kvh || c >= chunks) return true;
+    const int p0 = c * P1, p1 = p0 + P1 < Lc ? p0 + P1 : Lc;
+    return spread_stage1(g, a, s, kv, p0, p1, pos, tin, tsc, pst_ptr(g, step, l, 1));
+}
+
 // B: attention, exact (one workgroup per key/value head) or split over (kv, split) slots.
 __device__ __forceinline__ bool phase_b(const LoopArgs& g, const LayerDev& L, int step, int l, int pos, LoopLds& lds) {
     const int kvh = g.kv_heads, hpk = g.heads / kvh, hd = g.head_dim, Lc = pos + 1;
     const unsigned tin = tag_of(g, step, l, 1), tout = tag_of(g, step, l, 2);
     const AttnArgs a = attn_args(g, L, step, l);
     const TaggedOut o{g.attt, g.pacct, g.pmlt, tout, g.error, g.att_q8, g.heads * g.head_dim};
+    if (g.spread && attn_is_exact(Lc, hpk)) return phase_b_spread(g, L, step, l, pos, lds.spread);
     if (attn_is_exact(Lc, hpk) && Lc <= kSplit * kPoolChunks && g.head_attn) {
         if (static_cast<int>(blockIdx.x) >= g.heads) return true;
         const int h = blockIdx.x;
@@ -785,7 +1096,7 @@ template <uint32_t TO>
 __device__ __forceinline__ bool phase_c(const LoopArgs& g, const LayerDev& L, int step, int l, int token, GemvLds& s,
                                         float* hown) {
     const unsigned tag = tag_of(g, step, l, 3), tprev = tag_of(g, step, l - 1, 5);
-    const int G = static_cast<int>(gridDim.x);
+    const int G = static_cast<int>(gridDim.x) - g.c_first;
     const Stamps st = pst_ptr(g, step, l, 2);
     auto row_of = [&](int t, Packed& m, uint32_t& row0, int& R) {
         m = L.o;
@@ -812,7 +1123,7 @@ __device__ __forceinline__ bool phase_c(const LoopArgs& g, const LayerDev& L, in
         bool ok = true;
         if (r < static_cast<uint32_t>(g.R_o) && row < m.rows) {
             float prev = 0.0f;
-            const int slot = (t - static_cast<int>(blockIdx.x)) / G * g.R_o + static_cast<int>(r);
+            const int slot = (t - (static_cast<int>(blockIdx.x) - g.c_first)) / G * g.R_o + static_cast<int>(r);
             if (g.own_h) prev = hown[slot];
             else if (l == 0) prev = dequant_elem(g.embd, static_cast<uint32_t>(token), row);
             else ok = tget_one(g, g.ht + row, tprev, prev);
@@ -822,7 +1133,7 @@ __device__ __forceinline__ bool phase_c(const LoopArgs& g, const LayerDev& L, in
         }
         return g.own_h || !__syncthreads_or(!ok);
     };
-    return run_tiles<TO, kLoopUnits>(g.tiles_o, s, row_of, ready, done, st);
+    return run_tiles<TO, kLoopUnits>(g.tiles_o, s, row_of, ready, done, st, g.c_first);
 }
 
 // D: gate/up rows of ffn_norm(h), the gated activation.  A tile is R gate rows
@@ -892,7 +1203,7 @@ __device__ __forceinline__ bool phase_d(const LoopArgs& g, const LayerDev& L, in
 template <uint32_t TD>
 __device__ __forceinline__ bool phase_f(const LoopArgs& g, const LayerDev& L, int step, int l, GemvLds& s, float* hown) {
     const unsigned tag = tag_of(g, step, l, 5), tprev = tag_of(g, step, l, 3);
-    const int G = static_cast<int>(gridDim.x);
+    const int G = static_cast<int>(gridDim.x) - g.c_first;
     auto row_of = [&](int t, Packed& m, uint32_t& row0, int& R) {
         m = L.down;
         R = g.R_d;
@@ -902,7 +1213,8 @@ __device__ __forceinline__ bool phase_f(const LoopArgs& g, const LayerDev& L, in
     auto ready = [&]() -> bool {
         ActRegs ar;
         act_issue_w(ar, L.ffn_sub, g.ff);
-        if (!tget_vec(g, g.actt, tag_of(g, step, l, 4), s.x, g.ff)) return false;
+        // the whole input in one round of loads (3072 words: 12 a thread)
+        if (!tget_segs<12>(g, tag_of(g, step, l, 4), TSeg{g.actt, s.x, g.ff})) return false;
         pst(st, 1);
         prologue_lds<TD>(L.down, ar, L.ffn_sub, g.eps, s);
         pst(st, 2);
@@ -913,7 +1225,7 @@ __device__ __forceinline__ bool phase_f(const LoopArgs& g, const LayerDev& L, in
         bool ok = true;
         if (r < static_cast<uint32_t>(g.R_d) && row < m.rows) {
             float prev = 0.0f;
-            const int slot = (t - static_cast<int>(blockIdx.x)) / G * g.R_d + static_cast<int>(r);
+            const int slot = (t - (static_cast<int>(blockIdx.x) - g.c_first)) / G * g.R_d + static_cast<int>(r);
             if (g.own_h) prev = hown[slot];
             else ok = tget_one(g, g.ht + row, tprev, prev);
             const float h = prev + sums[r];  // h += proj (src/model.cpp:1162)
@@ -922,7 +1234,7 @@ __device__ __forceinline__ bool phase_f(const LoopArgs& g, const LayerDev& L, in
         }
         return g.own_h || !__syncthreads_or(!ok);
     };
-    return run_tiles<TD, kLoopUnits>(g.tiles_d, s, row_of, ready, done, st);
+    return run_tiles<TD, kLoopUnits>(g.tiles_d, s, row_of, ready, done, st, g.c_first);
 }
 
 // H: output rows of output_norm(h) -> logits; the workgroup's best key folded
@@ -1016,7 +1328,8 @@ __global__ __launch_bounds__(kThreads) void k_loop(LoopArgs g) {
         if (!s_ok) return;
         const int token = s_token;
         if (g.own_h) {  // this workgroup's rows of h: the embedding row (embedding_row, src/model.cpp:27-70)
-            for (int t = blockIdx.x, k = 0; t < g.tiles_o; t += gridDim.x, ++k)
+            for (int t = static_cast<int>(blockIdx.x) - g.c_first, k = 0; t >= 0 && t < g.tiles_o;
+                 t += static_cast<int>(gridDim.x) - g.c_first, ++k)
                 for (int r = threadIdx.x; r < g.R_o; r += kThreads) {
                     const uint32_t row = static_cast<uint32_t>(t * g.R_o + r);
                     if (row < g.embd.cols) hown[k * g.R_o + r] = dequant_elem(g.embd, static_cast<uint32_t>(token), row);
@@ -1088,6 +1401,15 @@ const void* find_loop_kernel(uint32_t tq, uint32_t tv, uint32_t to, uint32_t tg,
 }
 
 int loop_units_per_thread(uint32_t type, bool head) { return head ? head_units(type) : kLoopUnits; }
+
+bool loop_spread_fits(int heads, int kv_heads, int head_dim, int rope_dim, int grid) {
+    if (kv_heads <= 0 || heads % kv_heads != 0 || heads / kv_heads > kSpreadHpk) return false;
+    if (head_dim % kSpreadSlice != 0 || head_dim > 128) return false;
+    if (rope_dim != head_dim) return false;  // the rotation pairs span the head (no partial rotary)
+    const int n2 = kv_heads * (head_dim / kSpreadSlice);
+    // at least kExactMax / kSpreadChunk stage-1 tasks a key/value head, so a chunk never exceeds kSpreadChunk
+    return grid - n2 >= kv_heads * (kExactMax / kSpreadChunk);
+}
 
 hipError_t launch_loop(const void* kernel, const LoopArgs& g, int grid, hipStream_t s) {
     void* args[] = {const_cast<LoopArgs*>(&g)};

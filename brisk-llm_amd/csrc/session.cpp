@@ -144,7 +144,8 @@ brisk_hip_memory estimate_session(const brisk_hip_config& cfg, const brisk_hip_t
     sc += (ctx + 1) * 4 + ctx * hd * 4;                                    // token sequence, RoPE table
     if (cfg.arch == BRISK_HIP_ARCH_GEMMA3) sc += ctx * hd * 4 + e * 4;     // local RoPE table, post-norm input
     if (cfg.arch == BRISK_HIP_ARCH_LFM2) sc += 3 * e * 4 + static_cast<size_t>(cfg.layers) * ctx * e * 2;  // conv rows, bx caches
-    sc += (e + 2 * qd + 2 * kvd + ff + static_cast<size_t>(cfg.heads) * splits * (hd + 2)) * 8;  // hand-off words
+    sc += (e + 2 * qd + 2 * kvd + ff + static_cast<size_t>(cfg.heads) * splits * (hd + 2) +
+           static_cast<size_t>(cfg.heads) * kExactMax) * 8;                // hand-off words (with the spread scores)
     const size_t T = Session::kPrefillTokens, widest = std::max(std::max(e, qd), ff), stride = (widest + 255) / 256 * 256;
     sc += T * (e + 2 * qd + 2 * kvd + ff) * 4 + T * stride * (1 + 4 / 32.0 + 4 / 16.0);  // prefill buffers
     sc += static_cast<size_t>(64) * cfg.vocab * 4;                         // eval_all logits
@@ -576,7 +577,8 @@ void Session::setup_loop() {
     {
         const size_t qd = static_cast<size_t>(cfg_.heads) * cfg_.head_dim, kvd = static_cast<size_t>(cfg_.kv_heads) * cfg_.head_dim;
         const size_t parts = static_cast<size_t>(cfg_.heads) * max_splits_;
-        tagged_words_ = cfg_.embd + qd + 2 * kvd + qd + cfg_.ff + parts * cfg_.head_dim + parts * 2;
+        tagged_words_ = cfg_.embd + qd + 2 * kvd + qd + cfg_.ff + parts * cfg_.head_dim + parts * 2 +
+                        static_cast<size_t>(cfg_.heads) * kExactMax;
         unsigned long long* w = static_cast<unsigned long long*>(alloc(tagged_words_ * 8));
         tagged_ = w;
         check(hipMemset(w, 0, tagged_words_ * 8), "memset(tagged)");
@@ -587,7 +589,8 @@ void Session::setup_loop() {
         loop_.attt = w; w += qd;
         loop_.actt = w; w += cfg_.ff;
         loop_.pacct = w; w += parts * cfg_.head_dim;
-        loop_.pmlt = w;
+        loop_.pmlt = w; w += parts * 2;
+        loop_.sct = w;
     }
     if (std::getenv("BRISK_HIP_TRACE") != nullptr) trace_ = static_cast<unsigned long long*>(alloc(kTraceSlots * 8));
     check(hipMemset(loop_error_, 0, 64), "memset");
@@ -630,18 +633,25 @@ void Session::setup_loop() {
     g.tiles_qkv[0] = tiles_of(L0.q.p, g.R_qkv[0]);
     g.tiles_qkv[1] = tiles_of(L0.k.p, g.R_qkv[1]);
     g.tiles_qkv[2] = tiles_of(L0.v.p, g.R_qkv[2]);
-    g.R_o = loop_rows({&L0.o.p}, G);
+    // with the spread attention, its stage-2 workgroups take no O or down tiles
+    g.spread = loop_spread_fits(static_cast<int>(cfg_.heads), static_cast<int>(cfg_.kv_heads), static_cast<int>(cfg_.head_dim), rope_dim_, G) ? 1 : 0;
+    if (const char* e = std::getenv("BRISK_HIP_SPREAD")) g.spread = g.spread && std::string(e) != "0";
+    // (only when every position of the context takes it: beyond kExactMax the split attention runs)
+    g.c_first = g.spread && max_ctx_ <= static_cast<size_t>(kExactMax) ? static_cast<int>(cfg_.kv_heads * (cfg_.head_dim / 32)) : 0;
+    if (const char* e = std::getenv("BRISK_HIP_C_FIRST")) g.c_first = g.spread && std::string(e) != "0" ? g.c_first : 0;
+    const int Gc = G - g.c_first;
+    g.R_o = loop_rows({&L0.o.p}, Gc);
     g.tiles_o = tiles_of(L0.o.p, g.R_o);
     g.att_q8 = !takes_q8_k(L0.o.p.type) && L0.attn_sub_norm == nullptr &&
                ((cfg_.heads / cfg_.kv_heads) * cfg_.head_dim) % 32 == 0 ? 1 : 0;
     if (const char* e = std::getenv("BRISK_HIP_ATT_Q8")) g.att_q8 = g.att_q8 && std::string(e) != "0";
     g.R_gu = loop_rows({&L0.gate.p}, G);
     g.tiles_gu = tiles_of(L0.gate.p, g.R_gu);
-    g.R_d = loop_rows({&L0.down.p}, G);
+    g.R_d = loop_rows({&L0.down.p}, Gc);
     {
         const int R = std::min(g.R_o, g.R_d);
         const int tiles = tiles_of(L0.o.p, R);
-        g.own_h = ((tiles + G - 1) / G) * R <= kOwnRows ? 1 : 0;
+        g.own_h = ((tiles + Gc - 1) / Gc) * R <= kOwnRows ? 1 : 0;
         if (g.own_h) g.R_o = g.R_d = R;
     }
     g.tiles_o = tiles_of(L0.o.p, g.R_o);
