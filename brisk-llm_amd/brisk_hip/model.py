@@ -97,6 +97,9 @@ def parse_config(f: G.GgufFile) -> ModelConfig:
     per_layer_kv = list(kv_raw) if isinstance(kv_raw, (list, tuple)) else None  # per layer (src/model.cpp:229-238)
     if per_layer_kv is not None and len(per_layer_kv) != layers:
         fail("head_count_kv array length")
+    if per_layer_kv is not None and len({k for k in per_layer_kv if k != 0}) > 1:
+        # the session applies one head count to every attention layer (kv_head_count_of, src/model.h:91)
+        fail("attention layers with different key/value head counts are not supported")
     kv = max(per_layer_kv) if per_layer_kv is not None else u32("attention.head_count_kv")
     ff, ctx = u32("feed_forward_length"), u32("context_length")
     if 0 in (embd, layers, heads, kv, ff, ctx):

@@ -149,6 +149,15 @@ __device__ __forceinline__ float ref_expf_s(float x) { return ref_expf_impl<true
 // + 2) for |x| >= 1 and -expm1(-2|x|) / (expm1(-2|x|) + 2) below.  This
 // restatement gives glibc's result for every one of the 2^32 float inputs
 // (checked exhaustively on the host).
+//
+// ref_expm1f and ref_tanhf restate fdlibm's s_expm1f.c and s_tanhf.c, whose
+// notice follows:
+//   Copyright (C) 1993 by Sun Microsystems, Inc. All rights reserved.
+//   Developed at SunPro, a Sun Microsystems, Inc. business.
+//   Permission to use, copy, modify, and distribute this
+//   software is freely granted, provided that this notice
+//   is preserved.
+//   (Conversion to float by Ian Lance Taylor, Cygnus Support, ian@cygnus.com.)
 __device__ __forceinline__ float bits_to_f(uint32_t u) { return __uint_as_float(u); }
 
 __device__ inline float ref_expm1f(float x) {

@@ -70,6 +70,6 @@ int loop_units_per_thread(uint32_t type, bool head);
 bool loop_spread_fits(int heads, int kv_heads, int head_dim, int rope_dim, int grid);
 
 const void* find_loop_kernel(uint32_t tq, uint32_t tv, uint32_t to, uint32_t tg, uint32_t td, uint32_t th);
-hipError_t launch_loop(const void* kernel, const LoopArgs& g, int grid, hipStream_t s);
+hipError_t launch_loop(const void* kernel, const LoopArgs& g, int grid, hipStream_t s, bool cooperative);
 
 }  // namespace bh

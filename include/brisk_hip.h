@@ -31,7 +31,7 @@
 extern "C" {
 #endif
 
-#define BRISK_HIP_ABI_VERSION 2
+#define BRISK_HIP_ABI_VERSION 3
 
 enum {
     BRISK_HIP_OK = 0,
@@ -236,7 +236,8 @@ size_t brisk_hip_session_max_context(const brisk_hip_session* s);
 /* Device pointer and size of layer `layer`'s fp16 key (value = 0) or value (1)
  * cache, laid out [kv_head][max_context][head_dim] as the reference's
  * (src/model.cpp:984-991).  With brisk_hip_session_set_position it lets a
- * caller install a pre-filled cache (no Engine counterpart). */
+ * caller install a pre-filled cache (no Engine counterpart).  BRISK_HIP_EINVAL
+ * for a layer without one (an LFM2 short-convolution layer). */
 int brisk_hip_session_kv_cache(brisk_hip_session* s, int layer, int value, void** device_ptr, size_t* bytes);
 int brisk_hip_session_set_position(brisk_hip_session* s, size_t position);
 

@@ -115,3 +115,23 @@ def test_memory_preflight():
     assert estimate((f, cfg, table), 256)["total"] < free
     with HipSession((f, cfg, table), max_context=256) as s:
         assert s.eval_greedy(synth.prompt_ids(4, cfg.vocab)) >= 0
+
+
+def test_cooperative_loop_launch():
+    """BRISK_HIP_COOPERATIVE=1: the token loop launched cooperatively (the runtime places the whole grid
+    or refuses it) gives the same greedy ids as the oracle."""
+    f, cfg, table = model.load(synth.model_path("tiny-qwen3"))
+    os.environ["BRISK_HIP_COOPERATIVE"] = "1"
+    try:
+        s = HipSession((f, cfg, table), max_context=128)
+    finally:
+        del os.environ["BRISK_HIP_COOPERATIVE"]
+    o = pyoracle.Oracle(cfg, table, 128)
+    prompt = synth.prompt_ids(12, cfg.vocab)
+    got, want = s.eval(prompt), o.eval(prompt)
+    np.testing.assert_array_equal(got.view(np.uint32), want.view(np.uint32))
+    ids = s.generate([int(np.argmax(got))], 24)
+    o_ids, _ = o.generate([int(np.argmax(want))], 24)
+    np.testing.assert_array_equal(ids, o_ids)
+    s.close()
+    o.close()

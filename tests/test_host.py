@@ -116,7 +116,11 @@ def test_session_estimate(name):
     f, cfg, table = model.load(synth.model_path(name))
     e1, e2 = estimate((f, cfg, table), 256), estimate((f, cfg, table), 512)
     kvd = cfg.kv_heads * cfg.head_dim
-    assert e1["cache"] == 2 * cfg.layers * kvd * 256 * 2  # fp16 K and V for every position
+    # fp16 K and V for every position of an attention layer; an LFM2 short-convolution layer
+    # (blk.N.shortconv.*) holds its bx rows instead (estimate_memory, src/memory.cpp:59-68)
+    conv = sum(1 for t in table if t.name.endswith(".shortconv.in_proj.weight"))
+    assert (conv > 0) == (name == "tiny-lfm2")
+    assert e1["cache"] == 2 * (cfg.layers - conv) * kvd * 256 * 2 + conv * 256 * cfg.embd * 2
     assert e2["cache"] == 2 * e1["cache"]
     packed = sum(lib.brisk_hip_packed_bytes(t.type, t.rows, t.cols) for t in table if t.type != 0)
     vectors = sum(t.rows * t.cols * 4 for t in table if t.type == 0)
@@ -125,3 +129,53 @@ def test_session_estimate(name):
     assert e2["scratch"] > e1["scratch"]  # the RoPE table and sequence grow with the context
     # max_context 0 is the model's own context length, and larger values are capped there
     assert estimate((f, cfg, table), 0) == estimate((f, cfg, table), 10 * cfg.context)
+
+
+def test_header_structs_match_the_ctypes_binding(tmp_path):
+    """sizeof and field offsets of include/brisk_hip.h's structs, compiled by the C compiler, equal the
+    ctypes declarations (a caller built against another header version would pass another layout)."""
+    import shutil
+    import subprocess
+    if shutil.which("gcc") is None:
+        pytest.skip("no C compiler")
+    structs = {"brisk_hip_config": hiplib.HipConfig, "brisk_hip_tensor": hiplib.HipTensor, "brisk_hip_memory": hiplib.HipMemory}
+    lines = ["#include <stdio.h>", "#include <stddef.h>", '#include "brisk_hip.h"', "int main(void) {"]
+    for cname, ct in structs.items():
+        lines.append(f'printf("{cname} size %zu\\n", sizeof({cname}));')
+        for fname, _ in ct._fields_:
+            lines.append(f'printf("{cname} {fname} %zu\\n", offsetof({cname}, {fname}));')
+    lines.append("return 0; }")
+    src = tmp_path / "layout.c"
+    src.write_text("\n".join(lines) + "\n")
+    exe = tmp_path / "layout"
+    subprocess.run(["gcc", "-std=c11", "-I", os.path.join(ROOT, "include"), str(src), "-o", str(exe)], check=True)
+    out = subprocess.run([str(exe)], check=True, capture_output=True, text=True).stdout.split("\n")
+    got = {tuple(l.split()[:2]): int(l.split()[2]) for l in out if l.strip()}
+    for cname, ct in structs.items():
+        assert got[(cname, "size")] == C.sizeof(ct), cname
+        for fname, _ in ct._fields_:
+            assert got[(cname, fname)] == getattr(ct, fname).offset, (cname, fname)
+
+
+def test_lfm2_layers_must_share_one_kv_head_count(tmp_path):
+    """The session applies one key/value head count to every attention layer, so a model whose
+    attention layers differ (head_count_kv per layer, src/model.cpp:229-238) is refused at load."""
+    src = G.GgufFile(synth.model_path("tiny-lfm2"))
+    kv = list(src.metadata["lfm2.attention.head_count_kv"])
+    nz = [i for i, k in enumerate(kv) if k != 0]
+    z = [i for i, k in enumerate(kv) if k == 0]
+    assert nz and z
+    kv[z[0]] = int(kv[nz[0]]) * 2  # a second attention layer with twice the key/value heads
+    md = dict(src.metadata)
+    md["lfm2.attention.head_count_kv"] = kv
+    with pytest.raises(model.ModelError, match="different key/value head counts"):
+        model.parse_config(_MetaOnly(md))
+
+
+class _MetaOnly:
+    """A GGUF stand-in carrying only metadata, for the config parser."""
+    def __init__(self, metadata):
+        self.metadata = metadata
+
+    def get(self, key, default=None):
+        return self.metadata.get(key, default)
