@@ -32,7 +32,8 @@ class HipConfig(C.Structure):
                 ("context_length", C.c_uint32), ("rope_base", C.c_float), ("rms_epsilon", C.c_float),
                 ("sliding_window", C.c_uint32), ("rope_base_local", C.c_float), ("rope_scale", C.c_float),
                 ("final_softcap", C.c_float), ("rope_dim", C.c_uint32), ("rope_attn_factor", C.c_float),
-                ("rope_original_context", C.c_uint32), ("conv_taps", C.c_uint32)]
+                ("rope_original_context", C.c_uint32), ("conv_taps", C.c_uint32), ("rope_neox", C.c_int32),
+                ("no_rope_step", C.c_uint32), ("embedding_scale", C.c_float), ("gelu", C.c_int32)]
 
 
 class HipTensor(C.Structure):

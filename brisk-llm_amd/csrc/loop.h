@@ -68,6 +68,8 @@ constexpr int kOwnRows = 256;  // rows of h one workgroup can keep
 int loop_units_per_thread(uint32_t type, bool head);
 // Whether the spread exact attention takes this shape on a grid of `grid` workgroups.
 bool loop_spread_fits(int heads, int kv_heads, int head_dim, int rope_dim, int grid);
+// Whether it takes every position of a context of `positions` (longer ones take the split attention).
+bool loop_spread_covers(int heads, int kv_heads, int head_dim, int grid, int positions);
 
 const void* find_loop_kernel(uint32_t tq, uint32_t tv, uint32_t to, uint32_t tg, uint32_t td, uint32_t th);
 hipError_t launch_loop(const void* kernel, const LoopArgs& g, int grid, hipStream_t s, bool cooperative);

@@ -140,23 +140,38 @@ struct GemvLds {
 };
 // The spread exact attention (phase_b_spread): stage 1 scores a chunk of
 // positions, stage 2 turns a head's scores into weights and sums one 32-wide
-// slice of the values.
+// slice of the values, streaming the cached values in chunks of positions.
 constexpr int kSpreadSlice = 32;                 // value dimensions a stage-2 task (one Q8_0 block a head)
-constexpr int kSpreadHpk = 8;                    // query heads a key/value head, at most
-constexpr int kSpreadChunk = 64;                 // positions a stage-1 task, at most
-constexpr int kVtStride = kExactMax + 8;         // halves a transposed value row (16-byte aligned, banks staggered)
-struct SpreadLds {
-    alignas(16) float q[kSpreadHpk * 128];       // stage 1: the query heads, normed and rotated
-    alignas(16) float kcur[128];                 // stage 1 (writer): this token's key
-    alignas(16) float vcur[kSpreadSlice];        // stage 2: this token's values of the slice
-    alignas(16) float rope[128];                 // stage 1: the rotation row of this position
-    alignas(16) float qn[128];                   // stage 1: q_norm / k_norm weights
-    alignas(16) float kn[128];
-    alignas(16) float sc[kSpreadHpk * kExactMax];   // stage 2: scores [head][position]
-    alignas(16) float wt[kSpreadHpk * kExactMax];   // stage 2: weights [head][position, padded to 8]
-    alignas(16) uint16_t kst[kSpreadChunk * 128];   // stage 1: the chunk's cached keys [position][dim]
-    alignas(16) uint16_t vraw[kExactMax * kSpreadSlice];  // stage 2: cached values of the slice [position][dim]
-    alignas(16) uint16_t vt[kSpreadSlice * kVtStride];    // stage 2: the same, transposed [dim][position]
+constexpr int kSpreadHpk = 4;                    // query heads a key/value head, at most
+constexpr int kSpreadChunk = 320;                // positions a stage-1 task, at most
+constexpr int kSpreadScores = 16384;             // heads-per-kv x positions (padded to 8), at most
+constexpr int kSpreadStage = 256;                // positions a stage-2 chunk
+constexpr int kVtStride = kSpreadStage + 8;      // halves a transposed value row (16-byte aligned, banks staggered)
+// s_waitcnt vmcnt(N), other counters unconstrained (gfx9 encoding: vmcnt bits 3:0 and 15:14,
+// expcnt 6:4, lgkmcnt 11:8)
+template <int N>
+__device__ __forceinline__ void wait_vm_le() {
+    static_assert(N >= 0 && N < 16, "vmcnt immediate");
+    __builtin_amdgcn_s_waitcnt(0x0F70 | N);
+}
+
+struct SpreadStage1 {
+    alignas(16) float q[kSpreadHpk * 128];       // the query heads, normed and rotated
+    alignas(16) float kcur[128];                 // (writer) this token's key
+    alignas(16) uint16_t kst[kSpreadChunk * 128];   // the chunk's keys [position][dim]
+};
+struct SpreadStage2 {
+    alignas(16) float kcur[128];                 // this token's key (its cache row)
+    alignas(16) float vcur[kSpreadSlice];        // this token's values of the slice
+    alignas(16) float sc[kSpreadScores];         // scores, then weights: [head][position, rows padded to 8]
+    alignas(16) uint16_t vraw[2][kSpreadStage * kSpreadSlice];  // cached values of two chunks [position][dim]
+    alignas(16) uint16_t vt[2][kSpreadSlice * kVtStride];       // the same, transposed [dim][position]
+    float mx[4];
+    double red[4];
+};
+union SpreadLds {
+    SpreadStage1 s1;
+    SpreadStage2 s2;
 };
 
 union LoopLds {
@@ -825,7 +840,7 @@ __device__ __forceinline__ void pair_norm_rope(float* v, const Pair& p, const Pa
     }
 }
 
-__device__ __forceinline__ bool spread_stage1(const LoopArgs& g, const AttnArgs& a, SpreadLds& s, int kv, int p0, int p1,
+__device__ __forceinline__ bool spread_stage1(const LoopArgs& g, const AttnArgs& a, SpreadStage1& s, int kv, int p0, int p1,
                                               int pos, unsigned tin, unsigned tsc, const Stamps& st) {
     const int hd = a.head_dim, hpk = a.heads / a.kv_heads, t = threadIdx.x, wave = t >> 6, Lc = pos + 1;
     const bool writer = p1 == Lc;
@@ -890,15 +905,68 @@ __device__ __forceinline__ bool spread_stage1(const LoopArgs& g, const AttnArgs&
 }
 
 template <class O>
-__device__ __forceinline__ bool spread_stage2(const LoopArgs& g, const AttnArgs& a, SpreadLds& s, int kv, int d0, int pos,
+__device__ __forceinline__ bool spread_stage2(const LoopArgs& g, const AttnArgs& a, SpreadStage2& s, int kv, int d0, int pos,
                                               unsigned tin, unsigned tsc, const O& o, const Stamps& st) {
     const int hd = a.head_dim, hpk = a.heads / a.kv_heads, t = threadIdx.x, wave = t >> 6, lane = t & 63, Lc = pos + 1;
+    const int Ls = (Lc + 7) & ~7, chunks = (Lc + kSpreadStage - 1) / kSpreadStage, chains = hpk * kSpreadSlice;
+    // chain waves hold one (head, dimension) chain a lane; the others stage the cached values
+    const int cw = (chains + 63) / 64, r = t - 64 * cw, nt = kThreads - 64 * cw, wave_first = r & ~63;
     const float* rope_row = a.rope != nullptr ? a.rope + static_cast<size_t>(pos) * a.rope_dim : nullptr;
+    const uint8_t* vsrc = reinterpret_cast<const uint8_t*>(a.vcache + static_cast<size_t>(kv) * a.ctx * hd + d0);
+    // chunk c's cached rows of the slice (4 pieces of 16 bytes a position) into vraw[c & 1], by the staging waves
+    auto issue = [&](int c) {
+        const int p0 = c * kSpreadStage, np = (pos < p0 + kSpreadStage ? pos : p0 + kSpreadStage) - p0, pieces = np * 4;
+        uint8_t* dst = reinterpret_cast<uint8_t*>(s.vraw[c & 1]);
+        for (int k = 0; k * nt < pieces; ++k) {
+            const int i = k * nt + r;
+            if (i < pieces)
+                __builtin_amdgcn_global_load_lds((global_cvoid_ptr)(vsrc + static_cast<size_t>(p0 + (i >> 2)) * hd * 2 + (i & 3) * 16),
+                                                 (lds_void_ptr)(dst + (k * nt + wave_first) * 16), 16, 0, 0);
+        }
+    };
+    // ... transposed to [dim][position] in vt[c & 1] (each staging wave its own pieces: whole 8 x 8
+    // blocks of 8 positions by 8 dimensions in registers, the rest a half at a time); the last chunk
+    // also takes this token's values of the slice, rounded to fp16 with the bias, at position pos
+    auto transpose = [&](int c) {
+        const int p0 = c * kSpreadStage, np = (pos < p0 + kSpreadStage ? pos : p0 + kSpreadStage) - p0;
+        const uint16_t* raw = s.vraw[c & 1];
+        uint16_t* vt = s.vt[c & 1];
+        const int blocks = (np >> 3) * (kSpreadSlice / 8);
+        for (int bi = r; bi < blocks; bi += nt) {
+            const int pb = (bi >> 2) * 8, c8 = (bi & 3) * 8;
+            uint32_t in[8][4];
+#pragma unroll
+            for (int q = 0; q < 8; ++q) {
+                const uint4 w = *reinterpret_cast<const uint4*>(raw + (pb + q) * kSpreadSlice + c8);
+                in[q][0] = w.x; in[q][1] = w.y; in[q][2] = w.z; in[q][3] = w.w;
+            }
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                // byte selectors: the low (even j) or high (odd j) half of each of two words
+                const uint32_t sel = (j & 1) ? 0x07060302u : 0x05040100u;
+                uint4 o4;
+                o4.x = __builtin_amdgcn_perm(in[1][j >> 1], in[0][j >> 1], sel);
+                o4.y = __builtin_amdgcn_perm(in[3][j >> 1], in[2][j >> 1], sel);
+                o4.z = __builtin_amdgcn_perm(in[5][j >> 1], in[4][j >> 1], sel);
+                o4.w = __builtin_amdgcn_perm(in[7][j >> 1], in[6][j >> 1], sel);
+                *reinterpret_cast<uint4*>(vt + (c8 + j) * kVtStride + pb) = o4;
+            }
+        }
+        const int tail0 = np & ~7, tail = (np - tail0) * kSpreadSlice;
+        for (int i = r; i < tail; i += nt) {
+            const int p = tail0 + i / kSpreadSlice, dd = i % kSpreadSlice;
+            vt[dd * kVtStride + p] = raw[p * kSpreadSlice + dd];
+        }
+        if (c == chunks - 1 && r < kSpreadSlice) {
+            const float v = a.vbias != nullptr ? s.vcur[r] + a.vbias[kv * hd + d0 + r] : s.vcur[r];
+            vt[r * kVtStride + pos - p0] = f2h(v);
+        }
+    };
     bool fail = false;
     if (wave == 0) {
         // this token's key (all of it: its norm spans the head) and values of the slice; the key
         // normalised and rotated, then the slice of both rows rounded to fp16 into the cache rows
-        // (store_f16, src/kernels_f32.cpp:248-250) and the values into position pos of the slice
+        // (store_f16, src/kernels_f32.cpp:248-250)
         const Pair pr = rope_pair(lane, hd, a.neox);
         const PairConst kk = pair_const(pr, a.knorm, rope_row);
         fail = !wget_segs<4>(g, tin, TSeg{g.kt + kv * hd, s.kcur, hd}, TSeg{g.vt + kv * hd + d0, s.vcur, kSpreadSlice},
@@ -915,93 +983,116 @@ __device__ __forceinline__ bool spread_stage2(const LoopArgs& g, const AttnArgs&
                 const float b1 = a.vbias != nullptr ? a.vbias[kv * hd + d0 + d + 1] : 0.0f;
                 const uint16_t v0 = f2h(a.vbias != nullptr ? s.vcur[d] + b0 : s.vcur[d]);
                 const uint16_t v1 = f2h(a.vbias != nullptr ? s.vcur[d + 1] + b1 : s.vcur[d + 1]);
-                s.vt[d * kVtStride + pos] = v0;
-                s.vt[(d + 1) * kVtStride + pos] = v1;
                 __hip_atomic_store(reinterpret_cast<uint32_t*>(kr + d), k0 | (static_cast<uint32_t>(k1) << 16), __ATOMIC_RELAXED,
                                    __HIP_MEMORY_SCOPE_SYSTEM);
                 __hip_atomic_store(reinterpret_cast<uint32_t*>(vr + d), v0 | (static_cast<uint32_t>(v1) << 16), __ATOMIC_RELAXED,
                                    __HIP_MEMORY_SCOPE_SYSTEM);
             }
         }
-    } else {
-        // the slice's cached values, 4 pieces of 16 bytes a position: each of waves 1-3 stages
-        // its pieces into [position][32] and transposes them to [dim][position] once they land
-        const uint8_t* src = reinterpret_cast<const uint8_t*>(a.vcache + static_cast<size_t>(kv) * a.ctx * hd + d0);
-        uint8_t* dst = reinterpret_cast<uint8_t*>(s.vraw);
-        const int r = t - 64, nt = kThreads - 64, pieces = pos * 4, wave_first = r & ~63;
-        for (int k = 0; k * nt < pieces; ++k) {
-            const int i = k * nt + r;
-            if (i < pieces)
-                __builtin_amdgcn_global_load_lds((global_cvoid_ptr)(src + static_cast<size_t>(i >> 2) * hd * 2 + (i & 3) * 16),
-                                                 (lds_void_ptr)(dst + (k * nt + wave_first) * 16), 16, 0, 0);
-        }
-        __builtin_amdgcn_s_waitcnt(0);
-        for (int k = 0; k * nt < pieces; ++k) {
-            const int i = k * nt + r;
-            if (i < pieces) {
-                const int p = i >> 2, c = (i & 3) * 8;
-                const uint4 w = *reinterpret_cast<const uint4*>(s.vraw + p * kSpreadSlice + c);
-                const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    s.vt[(c + 2 * e) * kVtStride + p] = static_cast<uint16_t>(ws[e]);
-                    s.vt[(c + 2 * e + 1) * kVtStride + p] = static_cast<uint16_t>(ws[e] >> 16);
-                }
-            }
-        }
+    } else if (wave >= cw) {
+        issue(0);
+        if (chunks > 1) issue(1);
     }
     if (__syncthreads_or(fail)) {
         __builtin_amdgcn_s_waitcnt(0);
         return false;
     }
-    // every score of the group
-    if (!tget_vec(g, g.sct + static_cast<size_t>(kv) * hpk * Lc, tsc, s.sc, hpk * Lc)) {
+    if (wave >= cw) {  // the first chunk transposed, the third requested
+        __builtin_amdgcn_s_waitcnt(0);
+        transpose(0);
+        if (chunks > 2) issue(2);
+    }
+    // every score of the group, a head a padded row
+    bool ok = true;
+    for (int h0 = 0; h0 < hpk && ok; h0 += 3) {
+        auto seg = [&](int h) {
+            return h < hpk ? TSeg{g.sct + static_cast<size_t>(kv * hpk + h) * Lc, s.sc + h * Ls, Lc} : TSeg{nullptr, nullptr, 0};
+        };
+        ok = tget_segs<8>(g, tsc, seg(h0), seg(h0 + 1), seg(h0 + 2));
+    }
+    if (!ok) {
         __builtin_amdgcn_s_waitcnt(0);
         return false;
     }
     pst(st, 4);
-    // softmax of each head's row (softmax_f32, src/kernels_f32.cpp:275-285), a wave a head
-    const int Ls = (Lc + 7) & ~7;
-    for (int h = wave; h < hpk; h += kThreads / 64) {
-        const float* sc = s.sc + h * Lc;
-        float* wt = s.wt + h * Ls;
-        float m = -INFINITY;
-        for (int p = lane; p < Lc; p += 64) m = fmaxf(m, sc[p]);
-        m = wave_max(m);
-        double part = 0.0;
-        for (int p = lane; p < Lc; p += 64) {
-            const float e = ref_expf_s(sc[p] - m);
-            wt[p] = e;
-            part += static_cast<double>(e);
+    // softmax of each head's row (softmax_f32, src/kernels_f32.cpp:275-285): a wave a head on short
+    // rows (no barriers), the whole workgroup on a head on long ones
+    if (Lc <= 1024) {
+        for (int h = wave; h < hpk; h += kThreads / 64) {
+            float* sc = s.sc + h * Ls;
+            float m = -INFINITY;
+            for (int p = lane; p < Lc; p += 64) m = fmaxf(m, sc[p]);
+            m = wave_max(m);
+            double part = 0.0;
+            for (int p = lane; p < Lc; p += 64) {
+                const float e = ref_expf_s(sc[p] - m);
+                sc[p] = e;
+                part += static_cast<double>(e);
+            }
+            const float scale = static_cast<float>(1.0 / wave_sum(part));
+            for (int p = lane; p < Lc; p += 64) sc[p] *= scale;
         }
-        const float scale = static_cast<float>(1.0 / wave_sum(part));
-        for (int p = lane; p < Lc; p += 64) wt[p] *= scale;
+    } else {
+        for (int h = 0; h < hpk; ++h) {
+            float* sc = s.sc + h * Ls;
+            float m = -INFINITY;
+            for (int p = t; p < Lc; p += kThreads) m = fmaxf(m, sc[p]);
+            m = wave_max(m);
+            if (lane == 0) s.mx[wave] = m;
+            __syncthreads();
+            m = fmaxf(fmaxf(s.mx[0], s.mx[1]), fmaxf(s.mx[2], s.mx[3]));
+            double part = 0.0;
+            for (int p = t; p < Lc; p += kThreads) {
+                const float e = ref_expf_s(sc[p] - m);
+                sc[p] = e;
+                part += static_cast<double>(e);
+            }
+            part = wave_sum(part);
+            if (lane == 0) s.red[wave] = part;
+            __syncthreads();
+            const float scale = static_cast<float>(1.0 / (((s.red[0] + s.red[1]) + s.red[2]) + s.red[3]));
+            for (int p = t; p < Lc; p += kThreads) sc[p] *= scale;
+            __syncthreads();
+        }
     }
     __syncthreads();
     pst(st, 5);
-    // value sums, one (head, dimension) chain a lane, positions in order (weighted_sum_f32, :265-273)
-    if (t < hpk * kSpreadSlice) {
-        const int h = t / kSpreadSlice, d = t - h * kSpreadSlice;
-        const float* w = s.wt + h * Ls;
-        const uint16_t* vrow = s.vt + d * kVtStride;
-        float acc = 0.0f;
-        const int full = Lc & ~7;
-        int p = 0;
-        if (full > 0) {  // eight positions a round, the next round's weights and values read a round ahead
-            float4 w0 = *reinterpret_cast<const float4*>(w), w1 = *reinterpret_cast<const float4*>(w + 4);
-            uint4 vv = *reinterpret_cast<const uint4*>(vrow);
-            for (; p < full; p += 8) {
-                const int pn = p + 8 < full ? p + 8 : p;
-                const float4 n0 = *reinterpret_cast<const float4*>(w + pn), n1 = *reinterpret_cast<const float4*>(w + pn + 4);
-                const uint4 nv = *reinterpret_cast<const uint4*>(vrow + pn);
-                acc += mul_h<false>(w0.x, vv.x); acc += mul_h<true>(w0.y, vv.x);
-                acc += mul_h<false>(w0.z, vv.y); acc += mul_h<true>(w0.w, vv.y);
-                acc += mul_h<false>(w1.x, vv.z); acc += mul_h<true>(w1.y, vv.z);
-                acc += mul_h<false>(w1.z, vv.w); acc += mul_h<true>(w1.w, vv.w);
-                w0 = n0; w1 = n1; vv = nv;
+    // value sums, one (head, dimension) chain a lane, positions in order (weighted_sum_f32, :265-273),
+    // chunk by chunk; while the chain waves sum chunk c, the staging waves transpose chunk c + 1 and
+    // request chunk c + 3 (into the raw buffer chunk c + 1 leaves)
+    const bool chain = t < chains;
+    const int h = chain ? t / kSpreadSlice : 0, d = t - h * kSpreadSlice;
+    const float* w = s.sc + h * Ls;
+    float acc = 0.0f;
+    for (int c = 0; c < chunks; ++c) {
+        if (chain) {
+            const int p0 = c * kSpreadStage, pe = Lc < p0 + kSpreadStage ? Lc : p0 + kSpreadStage;
+            const uint16_t* vrow = s.vt[c & 1] + d * kVtStride - p0;
+            const int full = p0 + ((pe - p0) & ~7);
+            int p = p0;
+            if (full > p0) {  // eight positions a round, the next round's weights and values read a round ahead
+                float4 w0 = *reinterpret_cast<const float4*>(w + p), w1 = *reinterpret_cast<const float4*>(w + p + 4);
+                uint4 vv = *reinterpret_cast<const uint4*>(vrow + p);
+                for (; p < full; p += 8) {
+                    const int pn = p + 8 < full ? p + 8 : p;
+                    const float4 n0 = *reinterpret_cast<const float4*>(w + pn), n1 = *reinterpret_cast<const float4*>(w + pn + 4);
+                    const uint4 nv = *reinterpret_cast<const uint4*>(vrow + pn);
+                    acc += mul_h<false>(w0.x, vv.x); acc += mul_h<true>(w0.y, vv.x);
+                    acc += mul_h<false>(w0.z, vv.y); acc += mul_h<true>(w0.w, vv.y);
+                    acc += mul_h<false>(w1.x, vv.z); acc += mul_h<true>(w1.y, vv.z);
+                    acc += mul_h<false>(w1.z, vv.w); acc += mul_h<true>(w1.w, vv.w);
+                    w0 = n0; w1 = n1; vv = nv;
+                }
             }
+            for (; p < pe; ++p) acc += mul_h<false>(w[p], vrow[p]);
+        } else if (wave >= cw && c + 1 < chunks) {
+            __builtin_amdgcn_s_waitcnt(0);
+            transpose(c + 1);
+            if (c + 3 < chunks) issue(c + 3);
         }
-        for (; p < Lc; ++p) acc += mul_h<false>(w[p], vrow[p]);
+        __syncthreads();
+    }
+    if (chain) {
         if (t < kSpreadSlice / 2) __builtin_amdgcn_s_waitcnt(0);  // the cache rows are in memory before any output
         o.att((kv * hpk + h) * hd + d0 + d, acc);
     }
@@ -1021,12 +1112,19 @@ __device__ __forceinline__ bool phase_b_spread(const LoopArgs& g, const LayerDev
     const int b = static_cast<int>(blockIdx.x);
     if (b < n2) {
         const TaggedOut o{g.attt, g.pacct, g.pmlt, tout, g.error, g.att_q8, g.heads * g.head_dim};
-        return spread_stage2(g, a, s, b / slices, (b % slices) * kSpreadSlice, pos, tin, tsc, o, pst_ptr(g, step, l, 1));
+        return spread_stage2(g, a, s.s2, b / slices, (b % slices) * kSpreadSlice, pos, tin, tsc, o, pst_ptr(g, step, l, 1));
     }
     const int task = b - n2, kv = task / per_kv, c = task - kv * per_kv;
     if (kv >= kvh || c >= chunks) return true;
     const int p0 = c * P1, p1 = p0 + P1 < Lc ? p0 + P1 : Lc;
-    return spread_stage1(g, a, s, kv, p0, p1, pos, tin, tsc, pst_ptr(g, step, l, 1));
+    return spread_stage1(g, a, s.s1, kv, p0, p1, pos, tin, tsc, pst_ptr(g, step, l, 1));
+}
+
+// Whether the spread attention takes a context of L positions (on a grid of G workgroups).
+__device__ __forceinline__ bool spread_takes(const LoopArgs& g, int L) {
+    const int hpk = g.heads / g.kv_heads, n2 = g.kv_heads * (g.head_dim / kSpreadSlice);
+    const int per_kv = (static_cast<int>(gridDim.x) - n2) / g.kv_heads;
+    return hpk * ((L + 7) & ~7) <= kSpreadScores && (L + per_kv - 1) / per_kv <= kSpreadChunk;
 }
 
 // B: attention, exact (one workgroup per key/value head) or split over (kv, split) slots.
@@ -1035,7 +1133,7 @@ __device__ __forceinline__ bool phase_b(const LoopArgs& g, const LayerDev& L, in
     const unsigned tin = tag_of(g, step, l, 1), tout = tag_of(g, step, l, 2);
     const AttnArgs a = attn_args(g, L, step, l);
     const TaggedOut o{g.attt, g.pacct, g.pmlt, tout, g.error, g.att_q8, g.heads * g.head_dim};
-    if (g.spread && attn_is_exact(Lc, hpk)) return phase_b_spread(g, L, step, l, pos, lds.spread);
+    if (g.spread && spread_takes(g, Lc)) return phase_b_spread(g, L, step, l, pos, lds.spread);
     if (attn_is_exact(Lc, hpk) && Lc <= kSplit * kPoolChunks && g.head_attn) {
         if (static_cast<int>(blockIdx.x) >= g.heads) return true;
         const int h = blockIdx.x;
@@ -1406,9 +1504,12 @@ bool loop_spread_fits(int heads, int kv_heads, int head_dim, int rope_dim, int g
     if (kv_heads <= 0 || heads % kv_heads != 0 || heads / kv_heads > kSpreadHpk) return false;
     if (head_dim % kSpreadSlice != 0 || head_dim > 128) return false;
     if (rope_dim != head_dim) return false;  // the rotation pairs span the head (no partial rotary)
-    const int n2 = kv_heads * (head_dim / kSpreadSlice);
-    // at least kExactMax / kSpreadChunk stage-1 tasks a key/value head, so a chunk never exceeds kSpreadChunk
-    return grid - n2 >= kv_heads * (kExactMax / kSpreadChunk);
+    return grid - kv_heads * (head_dim / kSpreadSlice) >= kv_heads;  // a stage-1 task a key/value head at least
+}
+
+bool loop_spread_covers(int heads, int kv_heads, int head_dim, int grid, int positions) {
+    const int per_kv = (grid - kv_heads * (head_dim / kSpreadSlice)) / kv_heads;
+    return (heads / kv_heads) * ((positions + 7) & ~7) <= kSpreadScores && (positions + per_kv - 1) / per_kv <= kSpreadChunk;
 }
 
 // cooperative: the runtime either places the whole grid at once or fails the

@@ -156,7 +156,7 @@ brisk_hip_memory estimate_session(const brisk_hip_config& cfg, const brisk_hip_t
     if (cfg.arch == BRISK_HIP_ARCH_GEMMA3) sc += ctx * hd * 4 + e * 4;     // local RoPE table, post-norm input
     if (cfg.arch == BRISK_HIP_ARCH_LFM2) sc += 3 * e * 4;                  // conv rows
     sc += (e + 2 * qd + 2 * kvd + ff + static_cast<size_t>(cfg.heads) * splits * (hd + 2) +
-           static_cast<size_t>(cfg.heads) * kExactMax) * 8;                // hand-off words (with the spread scores)
+           static_cast<size_t>(cfg.heads) * ctx) * 8;                      // hand-off words (with the spread scores)
     const size_t T = Session::kPrefillTokens, widest = std::max(std::max(e, qd), ff), stride = (widest + 255) / 256 * 256;
     sc += T * (e + 2 * qd + 2 * kvd + ff) * 4 + T * stride * (1 + 4 / 32.0 + 4 / 16.0);  // prefill buffers
     sc += static_cast<size_t>(64) * cfg.vocab * 4;                         // eval_all logits
@@ -173,7 +173,10 @@ static std::string gb(size_t bytes) {
 }
 
 // Rotate-half RoPE for every family but the adjacent-pair Llama and SmolLM3 (src/model.cpp:167).
-bool Session::neox() const { return cfg_.arch != BRISK_HIP_ARCH_LLAMA && cfg_.arch != BRISK_HIP_ARCH_SMOLLM3; }
+bool Session::neox() const {
+    if (cfg_.rope_neox != 0) return cfg_.rope_neox == 1;  // the caller's ModelConfig::rope_neox
+    return cfg_.arch != BRISK_HIP_ARCH_LLAMA && cfg_.arch != BRISK_HIP_ARCH_SMOLLM3;
+}
 
 Session::Session(const brisk_hip_config& cfg, const brisk_hip_tensor* tensors, size_t n, size_t max_context, int device)
     : cfg_(cfg), device_(device) {
@@ -262,6 +265,12 @@ Session::Session(const brisk_hip_config& cfg, const brisk_hip_tensor* tensors, s
     };
 
     const size_t e = cfg.embd, hd = cfg.head_dim, qd = static_cast<size_t>(cfg.heads) * hd, kvd = static_cast<size_t>(cfg.kv_heads) * hd;
+    // ModelConfig's flags: the caller's values where given, else the family's (src/model.cpp:161-301)
+    const uint32_t no_rope_step = cfg.no_rope_step == 0xFFFFFFFFu ? 0 : cfg.no_rope_step != 0 ? cfg.no_rope_step
+                                : cfg.arch == BRISK_HIP_ARCH_SMOLLM3 ? 4 : 0;
+    if (cfg.gelu != 0 && (cfg.gelu == 1) != (cfg.arch == BRISK_HIP_ARCH_GEMMA3)) model_fail("GELU gating outside Gemma is not supported");
+    if (cfg.embedding_scale != 0.0f && cfg.arch != BRISK_HIP_ARCH_GEMMA3 && cfg.embedding_scale != 1.0f)
+        model_fail("scaled embeddings outside Gemma are not supported");
     load_matrix("token_embd.weight", cfg.vocab, e, embd_);
     if (find("output.weight") != nullptr) {
         load_matrix("output.weight", cfg.vocab, e, out_own_);
@@ -285,7 +294,7 @@ Session::Session(const brisk_hip_config& cfg, const brisk_hip_tensor* tensors, s
             load_matrix(b + "ffn_down.weight", e, cfg.ff, L.down);
             continue;
         }
-        if (cfg.arch == BRISK_HIP_ARCH_PHI3) {  // Q|K|V rows of attn_qkv, gate|up rows of ffn_up
+        if (cfg.arch == BRISK_HIP_ARCH_PHI3 && find(b + "attn_qkv.weight") != nullptr) {  // Q|K|V rows of attn_qkv, gate|up rows of ffn_up
             load_rows(b + "attn_qkv.weight", 0, qd, qd + 2 * kvd, e, L.q);
             load_rows(b + "attn_qkv.weight", qd, kvd, qd + 2 * kvd, e, L.k);
             load_rows(b + "attn_qkv.weight", qd + kvd, kvd, qd + 2 * kvd, e, L.v);
@@ -314,7 +323,7 @@ Session::Session(const brisk_hip_config& cfg, const brisk_hip_tensor* tensors, s
             L.k_bias = load_vector(b + "attn_k.bias", kvd);
             L.v_bias = load_vector(b + "attn_v.bias", kvd);
         }
-        L.rope = !(cfg.arch == BRISK_HIP_ARCH_SMOLLM3 && (l + 1) % 4 == 0);  // layer_has_rope (src/model.h:110, :168)
+        L.rope = no_rope_step == 0 || (l + 1) % no_rope_step != 0;  // layer_has_rope (src/model.h:110, src/model.cpp:168)
         if (cfg.arch == BRISK_HIP_ARCH_GEMMA3) {  // src/model.cpp:399-402; layer_slides, src/model.h:87-90
             L.attn_post_norm = load_vector(b + "post_attention_norm.weight", e);
             L.ffn_post_norm = load_vector(b + "post_ffw_norm.weight", e);
@@ -409,7 +418,7 @@ Session::Session(const brisk_hip_config& cfg, const brisk_hip_tensor* tensors, s
     if (gemma()) {
         if (cfg.sliding_window != 0) rope_local_ = rope_table(cfg.rope_base_local, 1.0f, hd, nullptr, 1.0f);
         proj_ = static_cast<float*>(alloc(e * 4));
-        embd_scale_ = std::sqrt(static_cast<float>(cfg.embd));
+        embd_scale_ = cfg.embedding_scale != 0.0f ? cfg.embedding_scale : std::sqrt(static_cast<float>(cfg.embd));
     }
     check(hipStreamSynchronize(stream_), "init sync");
     debug_ = std::getenv("BRISK_HIP_DEBUG") != nullptr;
@@ -600,7 +609,7 @@ void Session::setup_loop() {
         const size_t qd = static_cast<size_t>(cfg_.heads) * cfg_.head_dim, kvd = static_cast<size_t>(cfg_.kv_heads) * cfg_.head_dim;
         const size_t parts = static_cast<size_t>(cfg_.heads) * max_splits_;
         tagged_words_ = cfg_.embd + qd + 2 * kvd + qd + cfg_.ff + parts * cfg_.head_dim + parts * 2 +
-                        static_cast<size_t>(cfg_.heads) * kExactMax;
+                        static_cast<size_t>(cfg_.heads) * max_ctx_;
         unsigned long long* w = static_cast<unsigned long long*>(alloc(tagged_words_ * 8));
         tagged_ = w;
         check(hipMemset(w, 0, tagged_words_ * 8), "memset(tagged)");
@@ -658,8 +667,10 @@ void Session::setup_loop() {
     // with the spread attention, its stage-2 workgroups take no O or down tiles
     g.spread = loop_spread_fits(static_cast<int>(cfg_.heads), static_cast<int>(cfg_.kv_heads), static_cast<int>(cfg_.head_dim), rope_dim_, G) ? 1 : 0;
     if (const char* e = std::getenv("BRISK_HIP_SPREAD")) g.spread = g.spread && std::string(e) != "0";
-    // (only when every position of the context takes it: beyond kExactMax the split attention runs)
-    g.c_first = g.spread && max_ctx_ <= static_cast<size_t>(kExactMax) ? static_cast<int>(cfg_.kv_heads * (cfg_.head_dim / 32)) : 0;
+    // (only when every position of the context takes it: longer contexts run the split attention)
+    g.c_first = g.spread && loop_spread_covers(static_cast<int>(cfg_.heads), static_cast<int>(cfg_.kv_heads), static_cast<int>(cfg_.head_dim),
+                                               G, static_cast<int>(max_ctx_))
+                    ? static_cast<int>(cfg_.kv_heads * (cfg_.head_dim / 32)) : 0;
     if (const char* e = std::getenv("BRISK_HIP_C_FIRST")) g.c_first = g.spread && std::string(e) != "0" ? g.c_first : 0;
     const int Gc = G - g.c_first;
     g.R_o = loop_rows({&L0.o.p}, Gc);

@@ -81,6 +81,11 @@ typedef struct {
     float rope_attn_factor;  /* cos and sin scaled by it (Phi-3 LongRoPE); 0 reads as 1 */
     uint32_t rope_original_context; /* past it, rope_factors_long.weight replaces rope_factors_short.weight */
     uint32_t conv_taps;      /* LFM2's short-convolution width (shortconv.l_cache), 2 to 8; 0 elsewhere */
+    /* ModelConfig's flags (src/model.h:45-110); zero reads as the family's value: */
+    int32_t rope_neox;       /* 1: RoPE pairs (i, i + rotated / 2) ("NeoX"); 2: adjacent pairs (2 i, 2 i + 1) */
+    uint32_t no_rope_step;   /* every no_rope_step-th layer attends without RoPE (SmolLM3: 4); 0xFFFFFFFF: none */
+    float embedding_scale;   /* the embedding rows are multiplied by it (Gemma: sqrt(embd)) */
+    int32_t gelu;            /* 1: GELU (tanh) gating (Gemma); 2: SiLU / the family's */
 } brisk_hip_config;
 
 /* One model tensor in GGUF layout (host memory, e.g. the file's mmap):

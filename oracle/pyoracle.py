@@ -109,6 +109,7 @@ def ref_lib():
         L.ref_rollback.argtypes = [_vp, _sz]
         L.ref_eval.argtypes = [_vp, _vp, _sz, _vp]
         L.ref_eval_all.argtypes = [_vp, _vp, _sz, _vp]
+        L.ref_log_likelihood.argtypes = [_vp, _vp, _sz, C.POINTER(C.c_double)]
         L.ref_generate.argtypes = [_vp, _vp, _sz, _sz, _vp, _vp, C.POINTER(C.c_double), C.POINTER(C.c_double)]
         L.ref_last_error.restype = C.c_char_p
         L.ref_half_to_float.argtypes = [_u16]
@@ -236,6 +237,13 @@ class Reference:
         if self.L.ref_rollback(self.h, p) != 0:
             raise RuntimeError(self.L.ref_last_error().decode())
 
+    def log_likelihood(self, tokens) -> float:
+        tokens = np.ascontiguousarray(tokens, dtype=np.int32)
+        out = C.c_double()
+        if self.L.ref_log_likelihood(self.h, ptr(tokens), len(tokens), C.byref(out)) != 0:
+            raise RuntimeError(self.L.ref_last_error().decode())
+        return out.value
+
     def generate(self, prompt, n_gen: int):
         prompt = np.ascontiguousarray(prompt, dtype=np.int32)
         ids = np.zeros(n_gen, np.int32)
@@ -244,3 +252,115 @@ class Reference:
         if self.L.ref_generate(self.h, ptr(prompt), len(prompt), n_gen, ptr(ids), ptr(gaps), C.byref(a), C.byref(b)) != 0:
             raise RuntimeError(self.L.ref_last_error().decode())
         return ids, gaps, a.value, b.value
+
+
+# ---------------------------------------------------------------- the drop-in binding, driven as the reference drives an Engine
+
+HIP_ENGINE_PATH = os.path.join(HERE, "_ref", "libhip_engine.so")
+HIP_ENGINE_EXPORTS = ("he_last_error", "he_open", "he_close", "he_position", "he_rollback", "he_eval", "he_eval_all",
+                      "he_generate", "he_generate_greedy", "he_speculative", "he_serve_warmup", "he_serve_prefill",
+                      "he_serve_extend", "he_log_likelihood")
+
+
+def hip_engine_available() -> bool:
+    return os.path.exists(HIP_ENGINE_PATH)
+
+
+def hip_engine_lib():
+    L = C.CDLL(HIP_ENGINE_PATH)
+    vp, sz = C.c_void_p, C.c_size_t
+    L.he_last_error.restype = C.c_char_p
+    L.he_open.argtypes = [C.c_char_p, sz]
+    L.he_open.restype = vp
+    L.he_close.argtypes = [vp]
+    L.he_position.argtypes = [vp]
+    L.he_position.restype = sz
+    L.he_rollback.argtypes = [vp, sz]
+    for f in (L.he_eval, L.he_eval_all, L.he_serve_extend):
+        f.argtypes = [vp, vp, sz, vp]
+    for f in (L.he_generate, L.he_generate_greedy):
+        f.argtypes = [vp, vp, sz, sz, vp]
+    L.he_speculative.argtypes = [vp, C.c_char_p, C.c_int, vp, sz, sz, sz, vp, vp]
+    L.he_serve_warmup.argtypes = [vp, C.c_int32]
+    L.he_serve_prefill.argtypes = [vp, vp, sz, vp, C.POINTER(sz)]
+    L.he_log_likelihood.argtypes = [vp, vp, sz, C.POINTER(C.c_double)]
+    return L
+
+
+class HipEngine:
+    """HipSession : Engine (brisk-llm_amd/binding/hip_session.h) over Model(file, repack = false), through
+    oracle/_ref/libhip_engine.so: the calls the reference's CLI, server and speculative driver make."""
+
+    def __init__(self, path: str, max_context: int, vocab: int):
+        self.L = hip_engine_lib()
+        self.vocab = vocab
+        self.h = self.L.he_open(path.encode(), max_context)
+        if not self.h:
+            raise RuntimeError(self.L.he_last_error().decode())
+
+    def _check(self, rc):
+        if rc != 0:
+            raise RuntimeError(self.L.he_last_error().decode())
+
+    def close(self):
+        if self.h:
+            self.L.he_close(self.h)
+            self.h = None
+
+    __del__ = close
+
+    @property
+    def position(self) -> int:
+        return self.L.he_position(self.h)
+
+    def rollback(self, p: int):
+        self._check(self.L.he_rollback(self.h, p))
+
+    def eval(self, tokens) -> np.ndarray:
+        t = np.ascontiguousarray(tokens, dtype=np.int32)
+        out = np.empty(self.vocab, np.float32)
+        self._check(self.L.he_eval(self.h, ptr(t), len(t), ptr(out)))
+        return out
+
+    def eval_all(self, tokens) -> np.ndarray:
+        t = np.ascontiguousarray(tokens, dtype=np.int32)
+        out = np.empty((len(t), self.vocab), np.float32)
+        self._check(self.L.he_eval_all(self.h, ptr(t), len(t), ptr(out)))
+        return out
+
+    def generate(self, prompt, n_gen: int, on_device: bool = False) -> np.ndarray:
+        p = np.ascontiguousarray(prompt, dtype=np.int32)
+        out = np.zeros(n_gen, np.int32)
+        f = self.L.he_generate_greedy if on_device else self.L.he_generate
+        self._check(f(self.h, ptr(p), len(p), n_gen, ptr(out)))
+        return out
+
+    def speculative(self, prompt, n_gen: int, draft_tokens: int, draft_path=None, threads: int = 1):
+        p = np.ascontiguousarray(prompt, dtype=np.int32)
+        out = np.zeros(n_gen, np.int32)
+        stats = np.zeros(4, np.uint64)
+        self._check(self.L.he_speculative(self.h, draft_path.encode() if draft_path else None, threads, ptr(p), len(p), n_gen,
+                                          draft_tokens, ptr(out), ptr(stats)))
+        return out, dict(zip(("rounds", "plain", "drafted", "accepted"), map(int, stats)))
+
+    def serve_warmup(self, first: int):
+        self._check(self.L.he_serve_warmup(self.h, first))
+
+    def serve_prefill(self, prompt):
+        p = np.ascontiguousarray(prompt, dtype=np.int32)
+        out = np.empty(self.vocab, np.float32)
+        reused = C.c_size_t()
+        self._check(self.L.he_serve_prefill(self.h, ptr(p), len(p), ptr(out), C.byref(reused)))
+        return out, reused.value
+
+    def serve_extend(self, tokens) -> np.ndarray:
+        t = np.ascontiguousarray(tokens, dtype=np.int32)
+        out = np.empty(self.vocab, np.float32)
+        self._check(self.L.he_serve_extend(self.h, ptr(t), len(t), ptr(out)))
+        return out
+
+    def log_likelihood(self, tokens) -> float:
+        t = np.ascontiguousarray(tokens, dtype=np.int32)
+        out = C.c_double()
+        self._check(self.L.he_log_likelihood(self.h, ptr(t), len(t), C.byref(out)))
+        return out.value

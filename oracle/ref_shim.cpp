@@ -91,6 +91,11 @@ int ref_eval(void* handle, const int32_t* tokens, size_t n, float* out) {
 }
 
 // All n rows of eval_all(tokens) into out[n * vocab].
+// Engine::log_likelihood (src/engine.cpp:10-33) on the CPU Session.
+int ref_log_likelihood(void* handle, const int32_t* tokens, size_t n, double* out) {
+    return guarded([&] { *out = static_cast<RefHandle*>(handle)->session->log_likelihood(std::span<const brisk::Token>(tokens, n)); });
+}
+
 int ref_eval_all(void* handle, const int32_t* tokens, size_t n, float* out) {
     return guarded([&] {
         auto* h = static_cast<RefHandle*>(handle);

@@ -1,0 +1,100 @@
+"""Every benchmark config's full workload against reference-written fixtures, with the
+logits held to the north-star tolerance (max-abs 2e-2) at every step.
+
+tests/golden/*_steps.json were written by tests/golden/make_golden.py: the reference's
+CPU engine (oracle/_ref) for configs[1], [2] and [4]; the oracle (oracle/oracle.c, pinned
+to oracle/_ref) for configs[3], whose K/V caches are pre-filled with seeded fp16 N(0,1)
+values.  Each step holds the greedy pick, the top 8 logits and a strided sample.
+
+Two checks a config: the session's own greedy run (prompt, then one persistent-loop
+launch for all steps) picks the reference's ids; and, teacher-forced on the reference's
+ids one eval at a time, every step's logits sample is within 2e-2 of the reference's.
+"""
+import json
+import os
+
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+torch = pytest.importorskip("torch")
+
+from brisk_hip import HipSession, model, synth  # noqa: E402
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+TOL = 2e-2
+
+
+def fixture(name):
+    with open(os.path.join(HERE, "golden", name)) as fh:
+        return json.load(fh)
+
+
+def check_step(logits, want, stride, step):
+    idx = np.array(want["top_idx"])
+    err_top = np.abs(logits[idx] - np.array(want["top_val"], np.float32)).max()
+    err_strided = np.abs(logits[::stride] - np.array(want["strided"], np.float32)).max()
+    assert max(err_top, err_strided) <= TOL, f"step {step}: max |logit diff| {max(err_top, err_strided):.4g}"
+    return max(err_top, err_strided)
+
+
+def teacher_forced(s, first_tokens, ids, steps, stride):
+    """eval(prompt), then eval(reference pick) a step at a time; every step's logits checked."""
+    logits = s.eval(first_tokens)
+    worst = 0.0
+    for i, want in enumerate(steps):
+        worst = max(worst, check_step(logits, want, stride, i))
+        assert int(np.argmax(logits)) == ids[i], f"step {i}: pick {int(np.argmax(logits))}, reference {ids[i]}"
+        if i + 1 < len(steps):
+            logits = s.eval([ids[i]])
+    return worst
+
+
+@pytest.mark.parametrize("name", ["qwen3-0.6b", "llama-3.2-1b", "bitnet-2b"])
+def test_config_full_workload(name):
+    g = fixture(f"{name}_steps.json")
+    prompt = np.array(g["prompt"], np.int32)
+    n = len(g["ids"])
+    print(f"[config] {name}: {len(prompt)} prompt ids, {n} greedy steps", flush=True)
+    with HipSession(synth.model_path(name), max_context=len(prompt) + n + 8) as s:
+        first = int(np.argmax(s.eval(prompt)))
+        ids = np.concatenate([[first], s.decode(n - 1)])
+        mism = np.flatnonzero(ids != np.array(g["ids"]))
+        assert len(mism) == 0, f"first divergence at step {mism[0]}"
+        s.rollback(0)
+        worst = teacher_forced(s, prompt, g["ids"], g["steps"], g["stride"])
+        print(f"  {n} ids identical; worst per-step logit diff {worst:.3g}", flush=True)
+
+
+def _h2d(dst_ptr, host, nbytes):
+    import ctypes as C
+    hip = C.CDLL("libamdhip64.so")
+    hip.hipMemcpy.argtypes = [C.c_void_p, C.c_void_p, C.c_size_t, C.c_int]
+    assert hip.hipMemcpy(C.c_void_p(dst_ptr), C.c_void_p(host.ctypes.data), nbytes, 1) == 0  # hipMemcpyHostToDevice
+
+
+def test_config3_long_context():
+    """Qwen3-1.7B-shape Q8_0, K/V pre-filled to 4096 positions (the fixture's seeded values,
+    regenerated here layer by layer, key then value), then 32 greedy steps (split-K attention)."""
+    g = fixture("qwen3-1.7b_kv4096_steps.json")
+    f, cfg, table = model.load(synth.model_path(g["model"]))
+    n_pos, n = g["kv_positions"], len(g["ids"])
+    print(f"[config] qwen3-1.7b: KV pre-filled to {n_pos}, {n} greedy steps", flush=True)
+    with HipSession((f, cfg, table), max_context=n_pos + n + 8) as s:
+        rng = np.random.default_rng(g["kv_seed"])
+        for layer in range(cfg.layers):
+            for value in (False, True):
+                vals = rng.standard_normal((cfg.kv_heads, n_pos, cfg.head_dim)).astype(np.float16).view(np.uint16)
+                ptr, nbytes = s.kv_cache(layer, value)
+                cache = np.zeros((cfg.kv_heads, nbytes // (2 * cfg.kv_heads * cfg.head_dim), cfg.head_dim), np.uint16)
+                cache[:, :n_pos, :] = vals
+                _h2d(ptr, cache, nbytes)
+        s.set_position(n_pos)
+        first = int(np.argmax(s.eval([g["token"]])))
+        ids = np.concatenate([[first], s.decode(n - 1)])
+        mism = np.flatnonzero(ids != np.array(g["ids"]))
+        assert len(mism) == 0, f"first divergence at step {mism[0]}"
+        s.set_position(n_pos)
+        worst = teacher_forced(s, [g["token"]], g["ids"], g["steps"], g["stride"])
+        print(f"  {n} ids identical; worst per-step logit diff {worst:.3g}", flush=True)
