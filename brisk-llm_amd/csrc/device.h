@@ -18,6 +18,30 @@
 
 namespace bh {
 
+// Global-memory views of generic pointers: accesses through them are global
+// (not flat) instructions, counted by the vector memory counter only.  A flat
+// access also counts against lgkmcnt, so every wait for an LDS or scalar
+// result would wait for it too (the weight loads issued ahead among them).
+template <class T>
+__device__ __forceinline__ const __attribute__((address_space(1))) T* gmem(const T* p) {
+    return (const __attribute__((address_space(1))) T*)p;
+}
+template <class T>
+__device__ __forceinline__ __attribute__((address_space(1))) T* gmem(T* p) {
+    return (__attribute__((address_space(1))) T*)p;
+}
+// Four floats at p (16-byte aligned, global memory).
+__device__ __forceinline__ float4 gld4(const float* p) {
+    typedef float v4f __attribute__((ext_vector_type(4)));
+    const v4f v = *gmem(reinterpret_cast<const v4f*>(p));
+    return make_float4(v.x, v.y, v.z, v.w);
+}
+// Element i of a T array at p (global memory).
+template <class T>
+__device__ __forceinline__ T gld(const void* p, size_t i) {
+    return gmem(static_cast<const T*>(p))[i];
+}
+
 constexpr int kThreads = 256;        // every token-loop kernel runs 256-thread workgroups (4 waves of 64)
 constexpr int kMaxCols = 8192;       // widest activation row a matvec takes (Llama-3.2-1B FFN)
 constexpr int kTermCap = 8448;       // floats of LDS for the per-block terms of one tile
@@ -409,7 +433,7 @@ __device__ __forceinline__ float rms_scale(double sum, int n, float eps) {
 // counter-based barrier and no cache writeback/invalidate.
 struct PlainIO {
     static __device__ __forceinline__ float ld(const float* p) { return *p; }
-    static __device__ __forceinline__ float4 ld4(const float* p) { return *reinterpret_cast<const float4*>(p); }
+    static __device__ __forceinline__ float4 ld4(const float* p) { return *reinterpret_cast<const float4*>(p); }  // generic: x may be in LDS
     static __device__ __forceinline__ void st(float* p, float v) { *p = v; }
 };
 
@@ -527,7 +551,7 @@ struct ActRegs {
     float4 w[kActRegChunks];
 };
 
-__device__ __forceinline__ float4 ld4(const float* p) { return *reinterpret_cast<const float4*>(p); }
+__device__ __forceinline__ float4 ld4(const float* p) { return gld4(p); }
 
 // The norm weight's chunks alone (before the input is ready), then the input's.
 __device__ __forceinline__ void act_issue_w(ActRegs& r, const float* w, int cols) {
@@ -771,7 +795,11 @@ __device__ inline void act_from_q8_k(const uint8_t* xq, int cols, ActLds& a) {
 // issue every load of a thread before any term (and before the activation
 // prologue), so the memory latency is paid once per tile, not once per block.
 
-__device__ __forceinline__ uint4 ld16(const uint8_t* p) { return *reinterpret_cast<const uint4*>(p); }
+__device__ __forceinline__ uint4 ld16(const uint8_t* p) {
+    typedef unsigned v4u __attribute__((ext_vector_type(4)));
+    const v4u v = *gmem(reinterpret_cast<const v4u*>(p));
+    return make_uint4(v.x, v.y, v.z, v.w);
+}
 
 template <uint32_t T> struct Unit;
 
@@ -785,7 +813,7 @@ template <> struct Unit<kQ4_0> {
     uint32_t d;
     __device__ __forceinline__ void load(const Packed& m, size_t blk) {
         q = ld16(m.p0 + blk * 16);
-        d = reinterpret_cast<const uint16_t*>(m.p1)[blk];
+        d = gld<uint16_t>(m.p1, blk);
     }
     __device__ __forceinline__ float term(uint32_t b, const ActLds& a) const {
         const int32_t* x = a.xs + b * 8;
@@ -811,8 +839,8 @@ template <> struct Unit<kQ4_1> {
     uint32_t d, m;
     __device__ __forceinline__ void load(const Packed& mat, size_t blk) {
         q = ld16(mat.p0 + blk * 16);
-        d = reinterpret_cast<const uint16_t*>(mat.p1)[blk];
-        m = reinterpret_cast<const uint16_t*>(mat.p2)[blk];
+        d = gld<uint16_t>(mat.p1, blk);
+        m = gld<uint16_t>(mat.p2, blk);
     }
     __device__ __forceinline__ float term(uint32_t b, const ActLds& a) const {
         const int32_t* x = a.xs + b * 8;
@@ -845,8 +873,8 @@ template <> struct Unit<kQ5_0> {
     uint32_t d, qh;
     __device__ __forceinline__ void load(const Packed& m, size_t blk) {
         q = ld16(m.p0 + blk * 16);
-        d = reinterpret_cast<const uint16_t*>(m.p1)[blk];
-        qh = reinterpret_cast<const uint32_t*>(m.p2)[blk];
+        d = gld<uint16_t>(m.p1, blk);
+        qh = gld<uint32_t>(m.p2, blk);
     }
     __device__ __forceinline__ float term(uint32_t b, const ActLds& a) const {
         const int32_t* x = a.xs + b * 8;
@@ -871,7 +899,7 @@ template <> struct Unit<kQ8_0> {
     __device__ __forceinline__ void load(const Packed& m, size_t blk) {
         q0 = ld16(m.p0 + blk * 32);
         q1 = ld16(m.p0 + blk * 32 + 16);
-        d = reinterpret_cast<const uint16_t*>(m.p1)[blk];
+        d = gld<uint16_t>(m.p1, blk);
     }
     __device__ __forceinline__ float term(uint32_t b, const ActLds& a) const {
         const int32_t* x = a.xs + b * 8;
@@ -883,7 +911,8 @@ template <> struct Unit<kQ8_0> {
 };
 
 // q4_k_scale_min (src/quant.h:256-264)
-__device__ __forceinline__ void q4k_scale_min(const uint8_t* s, int j, int& scale, int& min) {
+template <class P>
+__device__ __forceinline__ void q4k_scale_min(P s, int j, int& scale, int& min) {
     if (j < 4) {
         scale = s[j] & 63;
         min = s[j + 4] & 63;
@@ -991,7 +1020,7 @@ template <> struct Unit<kQ6_K> {
         for (int i = 0; i < 8; ++i) ql[i] = ld16(m.p0 + blk * 128 + 16 * i);
 #pragma unroll
         for (int i = 0; i < 4; ++i) qh[i] = ld16(m.p1 + blk * 64 + 16 * i);
-        const uint32_t* mp = reinterpret_cast<const uint32_t*>(m.p2 + blk * 20);
+        const auto mp = gmem(reinterpret_cast<const uint32_t*>(m.p2 + blk * 20));
 #pragma unroll
         for (int i = 0; i < 5; ++i) meta[i] = mp[i];
     }
@@ -1047,7 +1076,7 @@ template <> struct Unit<kTQ2_0> {
     __device__ __forceinline__ void load(const Packed& m, size_t blk) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) q[i] = ld16(m.p0 + blk * 64 + 16 * i);
-        d = reinterpret_cast<const uint16_t*>(m.p1)[blk];
+        d = gld<uint16_t>(m.p1, blk);
         lut16 = (m.flags & kFlagLut16) != 0;
     }
     __device__ __forceinline__ float term(uint32_t b, const ActLds& a) const {
@@ -1137,6 +1166,21 @@ struct Tile {
         const uint32_t units = m.cols / Unit<T>::kElems;
         const uint32_t stride = term_stride(units);
         const uint32_t total = static_cast<uint32_t>(R) * units;
+        if (kThreads % units == 0) {
+            // every unit of this thread is the same block b of a different row, so the
+            // activation block is read from LDS once for all of them: all terms are
+            // formed in registers (no LDS store between the reads), then stored
+            const uint32_t b = threadIdx.x % units, r0 = threadIdx.x / units, step = kThreads / units;
+            float tv[kMax];
+#pragma unroll
+            for (int k = 0; k < kMax; ++k) tv[k] = u[k].term(b, a);
+#pragma unroll
+            for (int k = 0; k < kMax; ++k) {
+                const uint32_t r = r0 + k * step;
+                if (r < static_cast<uint32_t>(R) && row0 + r < m.rows) terms[r * stride + b] = tv[k];
+            }
+            return;
+        }
 #pragma unroll
         for (int k = 0; k < kMax; ++k) {
             const uint32_t i = threadIdx.x + k * kThreads;

@@ -483,6 +483,39 @@ hipError_t launch_pack(uint32_t type, const void* src, size_t rows, size_t cols,
     return hipGetLastError();
 }
 
+// Unit (row r, block b) of a packed 32-value-block matrix to unit (b, r) of
+// `dst`: the same planes, block-major ([cols/32][rows] units), so the units of
+// one block column across every row are contiguous.  Value runs and scales are
+// copied unchanged (Q4_0, Q4_1, Q5_0, Q8_0).
+__global__ void k_unit_transpose(Packed src, uint8_t* __restrict__ p0, uint8_t* __restrict__ p1, uint8_t* __restrict__ p2,
+                                 uint32_t run, uint32_t extra) {
+    const size_t units = src.cols / 32, total = static_cast<size_t>(src.rows) * units;
+    for (size_t i = static_cast<size_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < total; i += static_cast<size_t>(gridDim.x) * blockDim.x) {
+        const size_t r = i / units, b = i - r * units, o = b * src.rows + r;
+        for (uint32_t k = 0; k < run; k += 16)
+            *reinterpret_cast<uint4*>(p0 + o * run + k) = *reinterpret_cast<const uint4*>(src.p0 + i * run + k);
+        reinterpret_cast<uint16_t*>(p1)[o] = reinterpret_cast<const uint16_t*>(src.p1)[i];
+        if (extra == 2) reinterpret_cast<uint16_t*>(p2)[o] = reinterpret_cast<const uint16_t*>(src.p2)[i];
+        if (extra == 4) reinterpret_cast<uint32_t*>(p2)[o] = reinterpret_cast<const uint32_t*>(src.p2)[i];
+    }
+}
+
+hipError_t launch_unit_transpose(const Packed& src, const Packed& dst, hipStream_t s) {
+    uint32_t run = 0, extra = 0;
+    switch (src.type) {
+        case kQ4_0: run = 16; break;
+        case kQ4_1: run = 16; extra = 2; break;
+        case kQ5_0: run = 16; extra = 4; break;
+        case kQ8_0: run = 32; break;
+        default: return hipErrorInvalidValue;
+    }
+    const size_t total = static_cast<size_t>(src.rows) * (src.cols / 32);
+    if (total == 0) return hipSuccess;
+    hipLaunchKernelGGL(k_unit_transpose, dim3(static_cast<unsigned>(cdiv(total, 256) < 4096 ? cdiv(total, 256) : 4096)), dim3(256), 0, s,
+                       src, const_cast<uint8_t*>(dst.p0), const_cast<uint8_t*>(dst.p1), const_cast<uint8_t*>(dst.p2), run, extra);
+    return hipGetLastError();
+}
+
 hipError_t launch_quantize(int kind, const float* x, void* out, size_t count, int bits, hipStream_t s) {
     if (count == 0) return hipSuccess;
     if (kind == 0) hipLaunchKernelGGL(k_quant_q8_0, dim3(cdiv(count, kMaxCols)), dim3(kThreads), 0, s, x, static_cast<uint8_t*>(out), count);

@@ -88,6 +88,8 @@ struct HeadArgs {
 };
 
 hipError_t launch_pack(uint32_t type, const void* src, size_t rows, size_t cols, const Packed& dst, hipStream_t s);
+// Block-major copy of a packed Q4_0 / Q4_1 / Q5_0 / Q8_0 matrix (dst planes sized as src's).
+hipError_t launch_unit_transpose(const Packed& src, const Packed& dst, hipStream_t s);
 hipError_t launch_quantize(int kind, const float* x, void* out, size_t count, int bits, hipStream_t s);
 hipError_t launch_matvec_q8(const Packed& m, const void* xq, size_t n, float* out, size_t out_stride, hipStream_t s);
 hipError_t launch_gemv(GemvArgs g, hipStream_t s);

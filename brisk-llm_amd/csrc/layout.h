@@ -41,7 +41,7 @@ struct Packed {
     uint32_t rows, cols, type, flags;
 };
 
-__host__ __device__ inline uint32_t block_elems(uint32_t type) {
+__host__ __device__ constexpr inline uint32_t block_elems(uint32_t type) {
     return (type == kQ4_0 || type == kQ4_1 || type == kQ5_0 || type == kQ8_0) ? 32u : 256u;
 }
 __host__ __device__ inline bool takes_q8_k(uint32_t type) {

@@ -19,6 +19,7 @@ struct LayerDev {
     int rope;             // 0: the layer attends without RoPE
     uint16_t* kc;  // [kv_heads][ctx][head_dim] fp16
     uint16_t* vc;
+    Packed down_t;  // with push_ffn: the down matrix block-major (launch_unit_transpose)
 };
 
 struct LoopArgs {
@@ -57,10 +58,17 @@ struct LoopArgs {
     // the O and down tiles (phases C and F) go to workgroups c_first, c_first + 1, ...: with the
     // spread attention the workgroups of its second stage, which finish phase B last, take none
     int c_first;
+    int n_c;  // ... and to n_c workgroups from there (round-robin)
     // the attention output is handed to phase C quantised (Q8_0 O matrix, no sub-norm)
     int att_q8;
     // exact attention one workgroup per query head (else one per key/value head)
     int head_attn;
+    // the feed-forward block pushed to its consumers: the workgroup of activation block j
+    // (gate/up rows 32 j .. 32 j + 31) quantises that block and writes the down matrix's
+    // term of block j for every row, dtt[j][row]; the owners of h's rows add them in block
+    // order (phase F).  Tasks go to workgroups d_first, d_first + 1, ... (mod the grid).
+    int push_ffn, d_first;
+    unsigned long long* dtt;
 };
 
 constexpr int kOwnRows = 256;  // rows of h one workgroup can keep

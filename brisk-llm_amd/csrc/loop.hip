@@ -29,6 +29,37 @@ namespace bh {
 
 constexpr unsigned kSpinLimit = 1u << 24;
 
+// A field of a layer descriptor (read-only for the launch) by a scalar load.
+// Scalar loads go through the scalar cache and are counted by lgkmcnt, so the
+// read does not wait for the vector memory operations in flight (weight loads
+// issued ahead, hand-off stores): a vector load of it would, as the vector
+// memory counter retires in order.  The load stays where it is written
+// (volatile), so its result is not held in registers across the phases.
+template <class T>
+__device__ __forceinline__ T sld(const T* p) {
+    static_assert(sizeof(T) == 4 || sizeof(T) == 8 || sizeof(T) == 40, "sld: 4, 8 or 40 bytes");
+    if constexpr (sizeof(T) == 4) {
+        uint32_t v;
+        asm volatile("s_load_dword %0, %1, 0x0\n\ts_waitcnt lgkmcnt(0)" : "=s"(v) : "s"(p));
+        return __builtin_bit_cast(T, v);
+    } else if constexpr (sizeof(T) == 8) {
+        uint64_t v;
+        asm volatile("s_load_dwordx2 %0, %1, 0x0\n\ts_waitcnt lgkmcnt(0)" : "=s"(v) : "s"(p));
+        return __builtin_bit_cast(T, v);
+    } else {
+        typedef unsigned u32x8 __attribute__((ext_vector_type(8)));
+        u32x8 a;
+        uint64_t b;
+        asm volatile("s_load_dwordx8 %0, %2, 0x0\n\ts_load_dwordx2 %1, %2, 0x20\n\ts_waitcnt lgkmcnt(0)" : "=s"(a), "=s"(b) : "s"(p));
+        unsigned char buf[40];
+        __builtin_memcpy(buf, &a, 32);
+        __builtin_memcpy(buf + 32, &b, 8);
+        T r;
+        __builtin_memcpy(&r, buf, 40);
+        return r;
+    }
+}
+
 __device__ __forceinline__ bool loop_failed(const LoopArgs& g) {
     return __hip_atomic_load(g.error, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0;
 }
@@ -41,26 +72,27 @@ struct TSeg {
     int n;
 };
 
-template <int kGetPer = 4>
-__device__ __forceinline__ bool tget_segs(const LoopArgs& g, unsigned tag, TSeg s0, TSeg s1 = TSeg{nullptr, nullptr, 0},
-                                          TSeg s2 = TSeg{nullptr, nullptr, 0}) {
-    // kGetPer words a thread (kGetPer * kThreads a round) are requested before
-    // any is checked, so a round costs one memory round trip
-    const int n01 = s0.n + s1.n, n = n01 + s2.n;
-    auto at = [&](int i, const unsigned long long*& src, float*& dst) {
-        if (i < s0.n) { src = s0.src + i; dst = s0.dst + i; }
-        else if (i < n01) { src = s1.src + (i - s0.n); dst = s1.dst + (i - s0.n); }
-        else { src = s2.src + (i - n01); dst = s2.dst + (i - n01); }
-    };
+// Tagged values into LDS: word i of n at at(i) -> (src, dst), by the whole
+// workgroup (kWg, ends with a barrier) or by one wave (no barrier).  Each thread
+// requests kGetPer words before checking any, so a round costs one memory round
+// trip.  While words are missing, each wave polls a single word (the first
+// missing word of its lowest lane still waiting, the same address in every
+// lane, one memory request), then fetches its missing words again: polling
+// traffic stays at one request a wave, so it does not queue the weight and
+// cache loads of the compute units behind it.  False when abandoning.
+template <int kGetPer, bool kWg, class At>
+__device__ __forceinline__ bool tgather(const LoopArgs& g, unsigned tag, int n, At at) {
+    const int nt = kWg ? kThreads : 64, me = kWg ? static_cast<int>(threadIdx.x) : static_cast<int>(threadIdx.x & 63);
     bool fail = false;
-    for (int base = threadIdx.x; base < n && !fail; base += kGetPer * kThreads) {
+    for (int base0 = 0; base0 < n && !fail; base0 += kGetPer * nt) {
+        const int base = base0 + me;
         unsigned long long w[kGetPer];
         const unsigned long long* src[kGetPer];
         float* dst[kGetPer];
         bool have[kGetPer];
 #pragma unroll
         for (int u = 0; u < kGetPer; ++u) {
-            const int i = base + u * kThreads;
+            const int i = base + u * nt;
             have[u] = i >= n;
             at(i < n ? i : n - 1, src[u], dst[u]);  // unconditional loads (no branches between them)
             w[u] = tload(src[u]);
@@ -68,24 +100,27 @@ __device__ __forceinline__ bool tget_segs(const LoopArgs& g, unsigned tag, TSeg 
         unsigned spins = 0;
         while (true) {
             bool all = true;
-            const unsigned long long* first = nullptr;  // the first word still missing
+            const unsigned long long* first = src[0];
 #pragma unroll
-            for (int u = 0; u < kGetPer; ++u) {
+            for (int u = kGetPer - 1; u >= 0; --u) {
                 if (!have[u]) {
                     if (static_cast<unsigned>(w[u] >> 32) == tag) {
                         *dst[u] = __uint_as_float(static_cast<unsigned>(w[u]));
                         have[u] = true;
                     } else {
-                        if (all) first = src[u];
+                        first = src[u];
                         all = false;
                     }
                 }
             }
-            if (all) break;
-            // poll only that word (one load per round keeps the polling traffic
-            // low while producers are still running), then fetch the rest again
-            unsigned long long f;
-            while (static_cast<unsigned>((f = tload(first)) >> 32) != tag) {
+            const unsigned long long miss = __ballot(!all);
+            if (miss == 0) break;
+            const int leader = __ffsll(static_cast<long long>(miss)) - 1;
+            const uintptr_t fa = reinterpret_cast<uintptr_t>(first);
+            const uint32_t lo = __builtin_amdgcn_readlane(static_cast<uint32_t>(fa), leader);
+            const uint32_t hi = __builtin_amdgcn_readlane(static_cast<uint32_t>(fa >> 32), leader);
+            const unsigned long long* poll = reinterpret_cast<const unsigned long long*>((static_cast<uintptr_t>(hi) << 32) | lo);
+            while (static_cast<unsigned>(tload(poll) >> 32) != tag) {
                 if (++spins > kSpinLimit) {
                     atomicExch(g.error, 1);
                     fail = true;
@@ -103,7 +138,19 @@ __device__ __forceinline__ bool tget_segs(const LoopArgs& g, unsigned tag, TSeg 
                 if (!have[u]) w[u] = tload(src[u]);
         }
     }
-    return !__syncthreads_or(fail);
+    if (kWg) return !__syncthreads_or(fail);
+    return !fail;
+}
+
+template <int kGetPer = 4>
+__device__ __forceinline__ bool tget_segs(const LoopArgs& g, unsigned tag, TSeg s0, TSeg s1 = TSeg{nullptr, nullptr, 0},
+                                          TSeg s2 = TSeg{nullptr, nullptr, 0}) {
+    const int n01 = s0.n + s1.n, n = n01 + s2.n;
+    return tgather<kGetPer, true>(g, tag, n, [&](int i, const unsigned long long*& src, float*& dst) {
+        if (i < s0.n) { src = s0.src + i; dst = s0.dst + i; }
+        else if (i < n01) { src = s1.src + (i - s0.n); dst = s1.dst + (i - s0.n); }
+        else { src = s2.src + (i - n01); dst = s2.dst + (i - n01); }
+    });
 }
 
 __device__ __forceinline__ bool tget_vec(const LoopArgs& g, const unsigned long long* src, unsigned tag, float* dst, int n) {
@@ -126,12 +173,18 @@ __device__ __forceinline__ bool tget_one(const LoopArgs& g, const unsigned long 
     return true;
 }
 
+template <int kGetPer, class At>
+__device__ __forceinline__ bool tget_fn(const LoopArgs& g, unsigned tag, int n, At at) {
+    return tgather<kGetPer, true>(g, tag, n, at);
+}
+
 // ---------------------------------------------------------------- shared memory
 
 constexpr int kGroupRows = kThreads;  // rows of one tile group (one summing lane each)
 
 struct GemvLds {
     ActLds a;
+    ActLds a2;  // the pushed phase D's activation block (block 0)
     alignas(16) float terms[kTermCap];
     float sums[kGroupRows];
     float sums2[64];
@@ -199,7 +252,10 @@ __device__ __forceinline__ void pst(const Stamps& st, int pt) {
     if (threadIdx.x == 0 && (st.w0 != nullptr || st.all != nullptr)) {
         const unsigned long long t = wall_clock64();
         if (st.w0 != nullptr) st.w0[pt] = t;
-        if (st.all != nullptr) st.all[pt * 1024 + blockIdx.x] = t;
+        if (st.all != nullptr) {
+            st.all[pt * 1024 + blockIdx.x] = t;
+            st.all[65536 + pt * 1024 + blockIdx.x] = clock64();
+        }
     }
 }
 
@@ -238,10 +294,10 @@ __host__ __device__ constexpr int head_units(uint32_t type) { return (type == kQ
 // workgroups, busy elsewhere, out of the phase).
 template <uint32_t T, int M, class RowOf, class Ready, class Done>
 __device__ __forceinline__ bool run_tiles(int total, GemvLds& s, RowOf row_of, Ready ready, Done done,
-                                          Stamps st = Stamps{nullptr, nullptr}, int first = 0) {
-    const int G = static_cast<int>(gridDim.x) - first;
+                                          Stamps st = Stamps{nullptr, nullptr}, int first = 0, int count = 0) {
+    const int G = count > 0 ? count : static_cast<int>(gridDim.x) - first;
     int t = static_cast<int>(blockIdx.x) - first;
-    if (t < 0 || t >= total) return true;
+    if (t < 0 || t >= total || t >= G) return true;
     Tile<T, M> ta, tb;
     Packed ma, mb;  // by value: a pointer to a kernel-argument member would force a private copy
     uint32_t ra, rb = 0;
@@ -306,6 +362,10 @@ __device__ __forceinline__ bool run_tiles(int total, GemvLds& s, RowOf row_of, R
 // A: Q, K, V rows (one format, or Q/K's and then V's).
 template <uint32_t TQ, uint32_t TV, uint32_t TE>
 __device__ __forceinline__ bool phase_a(const LoopArgs& g, const LayerDev& L, int step, int l, int token, GemvLds& s) {
+    const Packed L_q = sld(&L.q);
+    const Packed L_k = sld(&L.k);
+    const Packed L_v = sld(&L.v);
+    const float* L_attn_norm = sld(&L.attn_norm);
     const int nq = g.tiles_qkv[0] + g.tiles_qkv[1];
     const int total = nq + g.tiles_qkv[2];
     const unsigned tag = tag_of(g, step, l, 1);
@@ -322,7 +382,7 @@ __device__ __forceinline__ bool phase_a(const LoopArgs& g, const LayerDev& L, in
     auto row_of = [&](int t, Packed& m, uint32_t& row0, int& R) {
         const int i = t < g.tiles_qkv[0] ? 0 : t < nq ? 1 : 2;
         const int tt = i == 0 ? t : i == 1 ? t - g.tiles_qkv[0] : t - nq;
-        m = i == 0 ? L.q : i == 1 ? L.k : L.v;
+        m = i == 0 ? L_q : i == 1 ? L_k : L_v;
         R = g.R_qkv[i];
         row0 = static_cast<uint32_t>(tt) * R;
     };
@@ -336,9 +396,9 @@ __device__ __forceinline__ bool phase_a(const LoopArgs& g, const LayerDev& L, in
     if (TQ == TV) {
         return run_tiles<TQ, kLoopUnits>(total, s, row_of, [&]() -> bool {
             ActRegs ar;
-            act_issue_w(ar, L.attn_norm, static_cast<int>(L.q.cols));
+            act_issue_w(ar, L_attn_norm, static_cast<int>(L_q.cols));
             if (!input()) return false;
-            prologue_lds<TQ>(L.q, ar, L.attn_norm, g.eps, s);
+            prologue_lds<TQ>(L_q, ar, L_attn_norm, g.eps, s);
             pst(st, 2);
             return true;
         }, done, st);
@@ -348,10 +408,10 @@ __device__ __forceinline__ bool phase_a(const LoopArgs& g, const LayerDev& L, in
     bool have_input = false;
     if (!run_tiles<TQ, kLoopUnits>(nq, s, row_of, [&]() -> bool {
             ActRegs ar;
-            act_issue_w(ar, L.attn_norm, static_cast<int>(L.q.cols));
+            act_issue_w(ar, L_attn_norm, static_cast<int>(L_q.cols));
             if (!input()) return false;
             have_input = true;
-            prologue_lds<TQ>(L.q, ar, L.attn_norm, g.eps, s);
+            prologue_lds<TQ>(L_q, ar, L_attn_norm, g.eps, s);
             return true;
         }, done))
         return false;
@@ -362,24 +422,32 @@ __device__ __forceinline__ bool phase_a(const LoopArgs& g, const LayerDev& L, in
     if (me >= g.tiles_qkv[2]) return true;
     {
         ActRegs ar;
-        act_issue_w(ar, L.attn_norm, static_cast<int>(L.v.cols));
-        prologue_lds<TV>(L.v, ar, L.attn_norm, g.eps, s);
+        act_issue_w(ar, L_attn_norm, static_cast<int>(L_v.cols));
+        prologue_lds<TV>(L_v, ar, L_attn_norm, g.eps, s);
     }
     for (int t = me; t < g.tiles_qkv[2]; t += G) {
         const uint32_t row0 = static_cast<uint32_t>(t) * g.R_qkv[2];
         Tile<TV, kLoopUnits> tile;
-        tile.load(L.v, row0, g.R_qkv[2]);
-        tile.sums(L.v, s.a, s.terms, s.sums);
-        done(nq + t, L.v, row0, s.sums);
+        tile.load(L_v, row0, g.R_qkv[2]);
+        tile.sums(L_v, s.a, s.terms, s.sums);
+        done(nq + t, L_v, row0, s.sums);
     }
     return true;
 }
 
 __device__ __forceinline__ AttnArgs attn_args(const LoopArgs& g, const LayerDev& L, int step, int l) {
+    const float* L_q_norm = sld(&L.q_norm);
+    const float* L_k_norm = sld(&L.k_norm);
+    const int L_rope = sld(&L.rope);
+    const float* L_q_bias = sld(&L.q_bias);
+    const float* L_k_bias = sld(&L.k_bias);
+    const float* L_v_bias = sld(&L.v_bias);
+    uint16_t* L_kc = sld(&L.kc);
+    uint16_t* L_vc = sld(&L.vc);
     AttnArgs a{};
-    a.qnorm = L.q_norm; a.knorm = L.k_norm; a.rope = L.rope ? g.rope : nullptr; a.eps = g.eps; a.neox = g.neox;
-    a.qbias = L.q_bias; a.kbias = L.k_bias; a.vbias = L.v_bias; a.rope_dim = g.rope_dim;
-    a.kcache = L.kc; a.vcache = L.vc; a.ctx = g.ctx; a.head_dim = g.head_dim; a.heads = g.heads;
+    a.qnorm = L_q_norm; a.knorm = L_k_norm; a.rope = L_rope ? g.rope : nullptr; a.eps = g.eps; a.neox = g.neox;
+    a.qbias = L_q_bias; a.kbias = L_k_bias; a.vbias = L_v_bias; a.rope_dim = g.rope_dim;
+    a.kcache = L_kc; a.vcache = L_vc; a.ctx = g.ctx; a.head_dim = g.head_dim; a.heads = g.heads;
     a.kv_heads = g.kv_heads; a.scale = g.scale; a.max_splits = g.max_splits;
     a.stamps = g.trace != nullptr ? g.trace + 65536 + (static_cast<size_t>(step * g.n_layers + l) * 8 + 1) * 8 : nullptr;
     return a;
@@ -530,56 +598,15 @@ __device__ __forceinline__ bool attn_slot_merge(const LoopArgs& lg, const AttnAr
 
 // ---------------------------------------------------------------- per-head exact attention
 
-// Tagged values into LDS by one wave (no barrier): up to K words a lane in
-// flight, every missing word re-polled each round; false when abandoning.
+// Tagged values into LDS by one wave (no barrier); false when abandoning.
 template <int K>
 __device__ __forceinline__ bool wget_segs(const LoopArgs& g, unsigned tag, TSeg s0, TSeg s1, TSeg s2) {
-    const int lane = static_cast<int>(threadIdx.x & 63);
     const int n01 = s0.n + s1.n, n = n01 + s2.n;
-    auto at = [&](int i, const unsigned long long*& src, float*& dst) {
+    return tgather<K, false>(g, tag, n, [&](int i, const unsigned long long*& src, float*& dst) {
         if (i < s0.n) { src = s0.src + i; dst = s0.dst + i; }
         else if (i < n01) { src = s1.src + (i - s0.n); dst = s1.dst + (i - s0.n); }
         else { src = s2.src + (i - n01); dst = s2.dst + (i - n01); }
-    };
-    for (int base = lane; base < n; base += K * 64) {
-        unsigned long long w[K];
-        const unsigned long long* src[K];
-        float* dst[K];
-        bool have[K];
-#pragma unroll
-        for (int u = 0; u < K; ++u) {
-            const int i = base + u * 64;
-            have[u] = i >= n;
-            at(i < n ? i : n - 1, src[u], dst[u]);
-            w[u] = tload(src[u]);
-        }
-        unsigned spins = 0;
-        while (true) {
-            bool all = true;
-#pragma unroll
-            for (int u = 0; u < K; ++u) {
-                if (!have[u]) {
-                    if (static_cast<unsigned>(w[u] >> 32) == tag) {
-                        *dst[u] = __uint_as_float(static_cast<unsigned>(w[u]));
-                        have[u] = true;
-                    } else {
-                        all = false;
-                    }
-                }
-            }
-            if (all) break;
-            if (++spins > kSpinLimit) {
-                atomicExch(g.error, 1);
-                return false;
-            }
-            if ((spins & 63) == 0 && loop_failed(g)) return false;
-            __builtin_amdgcn_s_sleep(1);
-#pragma unroll
-            for (int u = 0; u < K; ++u)
-                if (!have[u]) w[u] = tload(src[u]);
-        }
-    }
-    return true;
+    });
 }
 
 // chunk_issue by the `nt` threads of rank 0 .. nt - 1 (nt a multiple of 64).
@@ -647,7 +674,7 @@ __device__ __forceinline__ bool attn_head_pool(const LoopArgs& lg, const AttnArg
         head_norm_rope(s.kcur, g.kbias != nullptr ? g.kbias + kv * hd : nullptr, g.knorm, rope, hd, g.rope_dim, g.neox, g.eps);
         for (int i = lane; i < hd; i += 64) s.kcur[i] = h2f(f2h(s.kcur[i]));
     } else if (wave == 2) {
-        for (int i = lane; i < hd; i += 64) s.vcur[i] = h2f(f2h(g.vbias != nullptr ? s.vcur[i] + g.vbias[kv * hd + i] : s.vcur[i]));
+        for (int i = lane; i < hd; i += 64) s.vcur[i] = h2f(f2h(g.vbias != nullptr ? s.vcur[i] + gmem(g.vbias)[kv * hd + i] : s.vcur[i]));
     }
     __builtin_amdgcn_s_waitcnt(0);  // waves 1-3: the staged keys (and values) have landed
     __syncthreads();
@@ -661,8 +688,8 @@ __device__ __forceinline__ bool attn_head_pool(const LoopArgs& lg, const AttnArg
             uint16_t* vr = g.vcache + (static_cast<size_t>(kv) * g.ctx + pos) * hd;
             const uint32_t kw = f2h(s.kcur[i]) | (static_cast<uint32_t>(f2h(s.kcur[i + 1])) << 16);
             const uint32_t vw = f2h(s.vcur[i]) | (static_cast<uint32_t>(f2h(s.vcur[i + 1])) << 16);
-            __hip_atomic_store(reinterpret_cast<uint32_t*>(kr + i), kw, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
-            __hip_atomic_store(reinterpret_cast<uint32_t*>(vr + i), vw, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+            __hip_atomic_store(gmem(reinterpret_cast<uint32_t*>(kr + i)), kw, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+            __hip_atomic_store(gmem(reinterpret_cast<uint32_t*>(vr + i)), vw, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
         }
     }
     __syncthreads();
@@ -803,7 +830,7 @@ struct PairConst {
 __device__ __forceinline__ PairConst pair_const(const Pair& p, const float* w, const float* rope_row) {
     PairConst k{1.0f, 1.0f, 1.0f, 0.0f};
     if (p.live) {
-        if (w != nullptr) { k.wa = w[p.ia]; k.wb = w[p.ib]; }
+        if (w != nullptr) { k.wa = gmem(w)[p.ia]; k.wb = gmem(w)[p.ib]; }
         if (rope_row != nullptr) {
             const int i = static_cast<int>(threadIdx.x & 63);
             k.c = rope_row[2 * i];
@@ -819,8 +846,8 @@ __device__ __forceinline__ void pair_norm_rope(float* v, const Pair& p, const Pa
                                                bool rope, int hd, float eps) {
     float a = p.live ? v[p.ia] : 0.0f, b = p.live ? v[p.ib] : 0.0f;
     if (bias != nullptr && p.live) {
-        a = a + bias[p.ia];
-        b = b + bias[p.ib];
+        a = a + gmem(bias)[p.ia];
+        b = b + gmem(bias)[p.ib];
     }
     if (norm) {
         double s2 = static_cast<double>(a * a);
@@ -958,7 +985,7 @@ __device__ __forceinline__ bool spread_stage2(const LoopArgs& g, const AttnArgs&
             vt[dd * kVtStride + p] = raw[p * kSpreadSlice + dd];
         }
         if (c == chunks - 1 && r < kSpreadSlice) {
-            const float v = a.vbias != nullptr ? s.vcur[r] + a.vbias[kv * hd + d0 + r] : s.vcur[r];
+            const float v = a.vbias != nullptr ? s.vcur[r] + gmem(a.vbias)[kv * hd + d0 + r] : s.vcur[r];
             vt[r * kVtStride + pos - p0] = f2h(v);
         }
     };
@@ -979,13 +1006,13 @@ __device__ __forceinline__ bool spread_stage2(const LoopArgs& g, const AttnArgs&
                 uint16_t* kr = a.kcache + (static_cast<size_t>(kv) * a.ctx + pos) * hd + d0;
                 uint16_t* vr = a.vcache + (static_cast<size_t>(kv) * a.ctx + pos) * hd + d0;
                 const uint16_t k0 = f2h(s.kcur[d0 + d]), k1 = f2h(s.kcur[d0 + d + 1]);
-                const float b0 = a.vbias != nullptr ? a.vbias[kv * hd + d0 + d] : 0.0f;
-                const float b1 = a.vbias != nullptr ? a.vbias[kv * hd + d0 + d + 1] : 0.0f;
+                const float b0 = a.vbias != nullptr ? gmem(a.vbias)[kv * hd + d0 + d] : 0.0f;
+                const float b1 = a.vbias != nullptr ? gmem(a.vbias)[kv * hd + d0 + d + 1] : 0.0f;
                 const uint16_t v0 = f2h(a.vbias != nullptr ? s.vcur[d] + b0 : s.vcur[d]);
                 const uint16_t v1 = f2h(a.vbias != nullptr ? s.vcur[d + 1] + b1 : s.vcur[d + 1]);
-                __hip_atomic_store(reinterpret_cast<uint32_t*>(kr + d), k0 | (static_cast<uint32_t>(k1) << 16), __ATOMIC_RELAXED,
+                __hip_atomic_store(gmem(reinterpret_cast<uint32_t*>(kr + d)), k0 | (static_cast<uint32_t>(k1) << 16), __ATOMIC_RELAXED,
                                    __HIP_MEMORY_SCOPE_SYSTEM);
-                __hip_atomic_store(reinterpret_cast<uint32_t*>(vr + d), v0 | (static_cast<uint32_t>(v1) << 16), __ATOMIC_RELAXED,
+                __hip_atomic_store(gmem(reinterpret_cast<uint32_t*>(vr + d)), v0 | (static_cast<uint32_t>(v1) << 16), __ATOMIC_RELAXED,
                                    __HIP_MEMORY_SCOPE_SYSTEM);
             }
         }
@@ -1193,11 +1220,13 @@ __device__ __forceinline__ bool phase_b(const LoopArgs& g, const LayerDev& L, in
 template <uint32_t TO>
 __device__ __forceinline__ bool phase_c(const LoopArgs& g, const LayerDev& L, int step, int l, int token, GemvLds& s,
                                         float* hown) {
+    const Packed L_o = sld(&L.o);
+    const float* L_attn_sub = sld(&L.attn_sub);
     const unsigned tag = tag_of(g, step, l, 3), tprev = tag_of(g, step, l - 1, 5);
-    const int G = static_cast<int>(gridDim.x) - g.c_first;
+    const int G = g.n_c;
     const Stamps st = pst_ptr(g, step, l, 2);
     auto row_of = [&](int t, Packed& m, uint32_t& row0, int& R) {
-        m = L.o;
+        m = L_o;
         R = g.R_o;
         row0 = static_cast<uint32_t>(t) * R;
     };
@@ -1211,9 +1240,9 @@ __device__ __forceinline__ bool phase_c(const LoopArgs& g, const LayerDev& L, in
             return ok;
         }
         ActRegs ar;
-        act_issue_w(ar, L.attn_sub, n);
+        act_issue_w(ar, L_attn_sub, n);
         if (!tget_vec(g, g.attt, tag_of(g, step, l, 2), s.x, n)) return false;
-        prologue_lds<TO>(L.o, ar, L.attn_sub, g.eps, s);
+        prologue_lds<TO>(L_o, ar, L_attn_sub, g.eps, s);
         return true;
     };
     auto done = [&](int t, const Packed& m, uint32_t row0, const float* sums) -> bool {
@@ -1231,7 +1260,7 @@ __device__ __forceinline__ bool phase_c(const LoopArgs& g, const LayerDev& L, in
         }
         return g.own_h || !__syncthreads_or(!ok);
     };
-    return run_tiles<TO, kLoopUnits>(g.tiles_o, s, row_of, ready, done, st, g.c_first);
+    return run_tiles<TO, kLoopUnits>(g.tiles_o, s, row_of, ready, done, st, g.c_first, g.n_c);
 }
 
 // D: gate/up rows of ffn_norm(h), the gated activation.  A tile is R gate rows
@@ -1239,33 +1268,36 @@ __device__ __forceinline__ bool phase_c(const LoopArgs& g, const LayerDev& L, in
 // up terms, a tile after the other).
 template <uint32_t TG>
 __device__ __forceinline__ bool phase_d(const LoopArgs& g, const LayerDev& L, int step, int l, GemvLds& s) {
+    const Packed L_gate = sld(&L.gate);
+    const Packed L_up = sld(&L.up);
+    const float* L_ffn_norm = sld(&L.ffn_norm);
     if (static_cast<int>(blockIdx.x) >= g.tiles_gu) return true;
     const unsigned tag = tag_of(g, step, l, 4);
     const int G = static_cast<int>(gridDim.x), R = g.R_gu;
-    const uint32_t units = L.gate.cols / Unit<TG>::kElems, stride = term_stride(units);
+    const uint32_t units = L_gate.cols / Unit<TG>::kElems, stride = term_stride(units);
     Tile<TG, kLoopUnits> tg, tu;
     int t = blockIdx.x;
     uint32_t row0 = static_cast<uint32_t>(t) * R;
-    tg.load(L.gate, row0, R);
-    tu.load(L.up, row0, R);
+    tg.load(L_gate, row0, R);
+    tu.load(L_up, row0, R);
     const Stamps st = pst_ptr(g, step, l, 3);
     ActRegs ar;
-    act_issue_w(ar, L.ffn_norm, g.embd_dim);
+    act_issue_w(ar, L_ffn_norm, g.embd_dim);
     if (!tget_vec(g, g.ht, tag_of(g, step, l, 3), s.x, g.embd_dim)) return false;
     pst(st, 1);
-    prologue_lds<TG>(L.gate, ar, L.ffn_norm, g.eps, s);
+    prologue_lds<TG>(L_gate, ar, L_ffn_norm, g.eps, s);
     pst(st, 2);
     int gfirst = t, grows = 0;
     while (true) {
-        tg.terms(L.gate, s.a, s.terms + grows * stride);
-        tu.terms(L.up, s.a, s.terms + (grows + R) * stride);
+        tg.terms(L_gate, s.a, s.terms + grows * stride);
+        tu.terms(L_up, s.a, s.terms + (grows + R) * stride);
         grows += 2 * R;
         const int tn = t + G;
         const bool last = tn >= g.tiles_gu;
         if (!last) {  // the next tile's weights stream in while this group finishes
             row0 = static_cast<uint32_t>(tn) * R;
-            tg.load(L.gate, row0, R);
-            tu.load(L.up, row0, R);
+            tg.load(L_gate, row0, R);
+            tu.load(L_up, row0, R);
         }
         if (last || (grows + 2 * R) * static_cast<int>(stride) > kTermCap || grows + 2 * R > kGroupRows) {
             pst(st, 3);
@@ -1275,7 +1307,7 @@ __device__ __forceinline__ bool phase_d(const LoopArgs& g, const LayerDev& L, in
             pst(st, 4);
             for (int u = gfirst, off = 0; off < grows; u += G, off += 2 * R) {
                 const uint32_t r = threadIdx.x, r0 = static_cast<uint32_t>(u) * R;
-                if (r < static_cast<uint32_t>(R) && r0 + r < L.gate.rows) {
+                if (r < static_cast<uint32_t>(R) && r0 + r < L_gate.rows) {
                     const float gv = s.sums[off + r], uv = s.sums[off + R + r];
                     float out;
                     if (g.relu2) {
@@ -1300,21 +1332,23 @@ __device__ __forceinline__ bool phase_d(const LoopArgs& g, const LayerDev& L, in
 // F: down rows of act, h += down act (residual rows from the own copy with own_h).
 template <uint32_t TD>
 __device__ __forceinline__ bool phase_f(const LoopArgs& g, const LayerDev& L, int step, int l, GemvLds& s, float* hown) {
+    const Packed L_down = sld(&L.down);
+    const float* L_ffn_sub = sld(&L.ffn_sub);
     const unsigned tag = tag_of(g, step, l, 5), tprev = tag_of(g, step, l, 3);
-    const int G = static_cast<int>(gridDim.x) - g.c_first;
+    const int G = g.n_c;
     auto row_of = [&](int t, Packed& m, uint32_t& row0, int& R) {
-        m = L.down;
+        m = L_down;
         R = g.R_d;
         row0 = static_cast<uint32_t>(t) * R;
     };
     const Stamps st = pst_ptr(g, step, l, 4);
     auto ready = [&]() -> bool {
         ActRegs ar;
-        act_issue_w(ar, L.ffn_sub, g.ff);
+        act_issue_w(ar, L_ffn_sub, g.ff);
         // the whole input in one round of loads (3072 words: 12 a thread)
         if (!tget_segs<12>(g, tag_of(g, step, l, 4), TSeg{g.actt, s.x, g.ff})) return false;
         pst(st, 1);
-        prologue_lds<TD>(L.down, ar, L.ffn_sub, g.eps, s);
+        prologue_lds<TD>(L_down, ar, L_ffn_sub, g.eps, s);
         pst(st, 2);
         return true;
     };
@@ -1332,7 +1366,191 @@ __device__ __forceinline__ bool phase_f(const LoopArgs& g, const LayerDev& L, in
         }
         return g.own_h || !__syncthreads_or(!ok);
     };
-    return run_tiles<TD, kLoopUnits>(g.tiles_d, s, row_of, ready, done, st, g.c_first);
+    return run_tiles<TD, kLoopUnits>(g.tiles_d, s, row_of, ready, done, st, g.c_first, g.n_c);
+}
+
+// ---------------------------------------------------------------- the pushed feed-forward block
+
+// Gate/up rows a tile of the pushed phase D: the largest power of two up to 32
+// whose units fit 4 a thread.
+__device__ __forceinline__ int push_tile_rows(uint32_t units) {
+    int r = 32;
+    while (r > 1 && static_cast<uint32_t>(r) * units > static_cast<uint32_t>(4 * kThreads)) r >>= 1;
+    return r;
+}
+
+// quantize_q8_0 (src/quant.cpp:115-142) of one 32-value block held one value a
+// lane by lanes 0..31 of a wave (lanes 32..63 run along on their own values,
+// results unused) into block 0 of `a`.
+__device__ __forceinline__ void quant_block_lanes(float v, ActLds& a) {
+    const int lane = threadIdx.x & 63;
+    float amax = group_reduce<16>(fabsf(v), [](float x, float y) { return nnmax(x, y); });
+    amax = nnmax(amax, __shfl_xor(amax, 16, 64));
+    const float d = div127(amax);
+    const float inv = d != 0.0f ? rcp_rn(d) : 0.0f;
+    const int q = static_cast<int>(rintf(v * inv));
+    int sum = group_reduce<16>(q, [](int x, int y) { return x + y; });
+    sum += __shfl_xor(sum, 16, 64);
+    const int q1 = __shfl_down(q, 1, 64), q2 = __shfl_down(q, 2, 64), q3 = __shfl_down(q, 3, 64);
+    if (lane < 32 && (lane & 3) == 0)
+        a.xs[lane / 4] = (q & 0xFF) | ((q1 & 0xFF) << 8) | ((q2 & 0xFF) << 16) | (static_cast<uint32_t>(q3) << 24);
+    if (lane == 0) {
+        a.xd[0] = h2f(f2h(d));
+        a.xsum[0] = sum;
+    }
+}
+
+#ifdef BRISK_NO_PUSH
+constexpr bool kPushBuilt = false;
+#else
+constexpr bool kPushBuilt = true;
+#endif
+constexpr int kPushDown = 4;    // down rows a thread a chunk
+constexpr int kPushChunks = 4;  // chunks at most (rows of h up to 4096)
+
+// D, pushed (src/model.cpp:1111-1162 with the down projection split by its
+// input blocks): task j computes gate/up rows 32 j .. 32 j + 31 of
+// ffn_norm(h) (each row sum in block order), the gated activation of those 32
+// rows (silu(gate) * up, src/kernels_f32.cpp:287-289), its Q8_0 block (the
+// block the reference's quantize_q8_0 of the whole activation makes), and the
+// down matrix's term of block j for every row: term = (float)acc * d_w * d_x,
+// as dot_*_q8_0 forms it.  The terms go out as tagged words dtt[j][row].
+// Loads are issued before any store of the task (on gfx9 a wait for a load
+// also waits for every store issued before it).
+template <uint32_t TG, uint32_t TD>
+__device__ __forceinline__ bool phase_d_push(const LoopArgs& g, const LayerDev& L, int step, int l, GemvLds& s) {
+    const Packed L_gate = sld(&L.gate);
+    const Packed L_up = sld(&L.up);
+    const Packed L_down_t = sld(&L.down_t);
+    const float* L_ffn_norm = sld(&L.ffn_norm);
+    const int G = static_cast<int>(gridDim.x), nb = g.ff / 32, rows = g.embd_dim;
+    const int first = (static_cast<int>(blockIdx.x) - g.d_first + G) % G;
+    if (first >= nb) return true;
+    const unsigned tag = tag_of(g, step, l, 4);
+    const Stamps st = pst_ptr(g, step, l, 3);
+    const uint32_t units = L_gate.cols / Unit<TG>::kElems, stride = term_stride(units);
+    const int R = push_tile_rows(units), per = 32 / R, tiles = 2 * per;  // gate tiles, then up tiles
+    auto tile_load = [&](Tile<TG, 4>& t, int j, int k) {
+        t.load(k < per ? L_gate : L_up, static_cast<uint32_t>(32 * j + (k % per) * R), R);
+    };
+    auto tile_terms = [&](const Tile<TG, 4>& t, int k) { t.terms(k < per ? L_gate : L_up, s.a, s.terms + k * R * stride); };
+    // the down units of chunk c (every thread issues every load; rows past the matrix re-read its last row)
+    auto down_load = [&](Unit<TD> (&u)[kPushDown], int j, int c) {
+#pragma unroll
+        for (int k = 0; k < kPushDown; ++k) {
+            int r = (c * kPushDown + k) * kThreads + static_cast<int>(threadIdx.x);
+            r = r < rows ? r : rows - 1;
+            u[k].load(L_down_t, static_cast<size_t>(j) * rows + r);
+        }
+    };
+    const int dchunks = (rows + kPushDown * kThreads - 1) / (kPushDown * kThreads);
+    bool have_input = false;
+    for (int j = first; j < nb; j += G) {
+        Unit<TD> du[kPushDown];
+        down_load(du, j, 0);
+        Tile<TG, 4> t0, t1;
+        tile_load(t0, j, 0);
+        tile_load(t1, j, 1);
+        if (!have_input) {
+            ActRegs ar;
+            act_issue_w(ar, L_ffn_norm, g.embd_dim);
+            if (!tget_vec(g, g.ht, tag_of(g, step, l, 3), s.x, g.embd_dim)) return false;
+            pst(st, 1);
+            prologue_lds<TG>(L_gate, ar, L_ffn_norm, g.eps, s);
+            pst(st, 2);
+            have_input = true;
+        }
+        // two tiles in flight: tile k + 2 is requested once tile k's terms are out
+        tile_terms(t0, 0);
+        if (tiles > 2) tile_load(t0, j, 2);
+        tile_terms(t1, 1);
+        for (int k = 2; k < tiles; k += 2) {
+            if (k + 1 < tiles) tile_load(t1, j, k + 1);
+            tile_terms(t0, k);
+            if (k + 2 < tiles) tile_load(t0, j, k + 2);
+            if (k + 1 < tiles) tile_terms(t1, k + 1);
+        }
+        __syncthreads();
+        row_sums(s.terms, stride, units, 64, s.sums);
+        __syncthreads();
+        pst(st, 3);
+        // the gated activation of the block, quantised by wave 0 into block 0 of s.a2
+        if (threadIdx.x < 64) {
+            const int r = threadIdx.x & 31;
+            const float gv = s.sums[r], uv = s.sums[32 + r];
+            float out;
+            if (g.relu2) {
+                const float q = gv > 0.0f ? gv : 0.0f;
+                out = q * q * uv;  // src/model.cpp:1134-1138
+            } else {
+                out = gv / (1.0f + ref_expf_s(-gv)) * uv;  // src/kernels_f32.cpp:287-289
+            }
+            quant_block_lanes(out, s.a2);
+        }
+        __syncthreads();
+        pst(st, 4);
+        // every down term of the task in registers, then the stores
+        float dt[kPushChunks][kPushDown];
+#pragma unroll
+        for (int c = 0; c < kPushChunks; ++c) {
+            if (c < dchunks) {
+                if (c > 0) down_load(du, j, c);
+#pragma unroll
+                for (int k = 0; k < kPushDown; ++k) dt[c][k] = du[k].term(0, s.a2);
+            }
+        }
+#pragma unroll
+        for (int c = 0; c < kPushChunks; ++c) {
+            if (c < dchunks) {
+#pragma unroll
+                for (int k = 0; k < kPushDown; ++k) {
+                    const int r = (c * kPushDown + k) * kThreads + static_cast<int>(threadIdx.x);
+                    if (r < rows) tput(g.dtt + static_cast<size_t>(j) * rows + r, dt[c][k], tag);
+                }
+            }
+        }
+        pst(st, 5);
+        __syncthreads();  // s.a2 and s.terms are rewritten by the next task
+    }
+    return true;
+}
+
+// F, pushed: the rows of h this workgroup owns (phase C's tiles), each h += the
+// sum of its terms dtt[0..nb)[row] in block order (as the reference's
+// sequential `sum +=`), residual from the own copy.
+template <uint32_t TD>
+__device__ __forceinline__ bool phase_f_push(const LoopArgs& g, int step, int l, GemvLds& s, float* hown) {
+    const int Gc = g.n_c, me = static_cast<int>(blockIdx.x) - g.c_first;
+    if (me < 0 || me >= g.tiles_o || me >= Gc) return true;
+    const int nb = g.ff / 32, rows = g.embd_dim, R = g.R_o;
+    const uint32_t stride = term_stride(static_cast<uint32_t>(nb));
+    const unsigned tag = tag_of(g, step, l, 5);
+    const Stamps st = pst_ptr(g, step, l, 4);
+    // owned rows: slot k * R + r is row (me + k Gc) R + r
+    const int ntiles = (g.tiles_o - me + Gc - 1) / Gc, nrows = ntiles * R;
+    const int n = nrows * nb;
+    const bool ok = tget_fn<4>(g, tag_of(g, step, l, 4), n, [&](int i, const unsigned long long*& src, float*& dst) {
+        const int slot = i % nrows, j = i / nrows;
+        int row = (me + (slot / R) * Gc) * R + slot % R;
+        row = row < rows ? row : rows - 1;
+        src = g.dtt + static_cast<size_t>(j) * rows + row;
+        dst = s.terms + slot * stride + j;
+    });
+    if (!ok) return false;
+    pst(st, 1);
+    row_sums(s.terms, stride, static_cast<uint32_t>(nb), nrows, s.sums);
+    __syncthreads();
+    pst(st, 4);
+    for (int slot = threadIdx.x; slot < nrows; slot += kThreads) {
+        const int row = (me + (slot / R) * Gc) * R + slot % R;
+        if (row < rows) {
+            const float h = hown[slot] + s.sums[slot];  // h += proj (src/model.cpp:1162)
+            tput(g.ht + row, h, tag);
+            hown[slot] = h;
+        }
+    }
+    pst(st, 5);
+    return true;
 }
 
 // H: output rows of output_norm(h) -> logits; the workgroup's best key folded
@@ -1397,26 +1615,38 @@ __device__ __forceinline__ bool wait_pick(const LoopArgs& g, int step, int& toke
     return true;
 }
 
+// The launch's arguments (the kernel's only argument, at the start of the kernel
+// argument segment), re-addressed through an opaque copy of the segment pointer
+// at each use: the compiler then reads the fields it needs with scalar loads
+// where they are used, instead of holding every value derived from them in
+// registers across the whole step loop (which spills).
+__device__ __forceinline__ const LoopArgs& lg() {
+    const __attribute__((address_space(4))) LoopArgs* p = (const __attribute__((address_space(4))) LoopArgs*)__builtin_amdgcn_kernarg_segment_ptr();
+    asm volatile("" : "+s"(p));
+    return *(const LoopArgs*)p;
+}
+
 template <uint32_t TQ, uint32_t TV, uint32_t TO, uint32_t TG, uint32_t TD, uint32_t TH>
-__global__ __launch_bounds__(kThreads) void k_loop(LoopArgs g) {
+__global__ __launch_bounds__(kThreads) void k_loop(LoopArgs g_arg) {
+    (void)g_arg;  // read through lg(), re-addressed at each use
     __shared__ LoopLds lds;
     __shared__ float hown[kOwnRows];
     __shared__ int s_token, s_ok;
     exp_tab_fill();  // ordered before its first use by the barrier after the first token
-    for (int step = 0; step < g.n_steps; ++step) {
-        const int pos = g.pos0 + step;
-        const bool full = step >= g.first_full;
+    for (int step = 0; step < lg().n_steps; ++step) {
+        const int pos = lg().pos0 + step;
+        const bool full = step >= lg().first_full;
         // the token of this step: the caller's, or the previous step's pick
         if (threadIdx.x == 0) {
-            int token = g.seq[pos];
+            int token = lg().seq[pos];
             bool ok = true;
-            if (step > 0 && pos >= g.fixed) ok = wait_pick(g, step - 1, token);
+            if (step > 0 && pos >= lg().fixed) ok = wait_pick(lg(), step - 1, token);
             if (ok && blockIdx.x == 0) {
-                if (step > 0 && pos >= g.fixed) g.seq[pos] = token;
+                if (step > 0 && pos >= lg().fixed) lg().seq[pos] = token;
                 // re-arm the key this step's phase H uses: its last readers (the
                 // previous step's starts) are all done, since this step's pick
                 // waits on the previous step's phase H, which needed their outputs
-                if (step >= 2) __hip_atomic_store(g.keys + (step & 1), 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                if (step >= 2) __hip_atomic_store(lg().keys + (step & 1), 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                 __builtin_amdgcn_s_waitcnt(0);
             }
             s_token = token;
@@ -1425,55 +1655,71 @@ __global__ __launch_bounds__(kThreads) void k_loop(LoopArgs g) {
         __syncthreads();
         if (!s_ok) return;
         const int token = s_token;
-        if (g.own_h) {  // this workgroup's rows of h: the embedding row (embedding_row, src/model.cpp:27-70)
-            for (int t = static_cast<int>(blockIdx.x) - g.c_first, k = 0; t >= 0 && t < g.tiles_o;
-                 t += static_cast<int>(gridDim.x) - g.c_first, ++k)
-                for (int r = threadIdx.x; r < g.R_o; r += kThreads) {
-                    const uint32_t row = static_cast<uint32_t>(t * g.R_o + r);
-                    if (row < g.embd.cols) hown[k * g.R_o + r] = dequant_elem(g.embd, static_cast<uint32_t>(token), row);
+        if (lg().own_h) {  // this workgroup's rows of h: the embedding row (embedding_row, src/model.cpp:27-70)
+            const int me = static_cast<int>(blockIdx.x) - lg().c_first;
+            for (int t = me, k = 0; me >= 0 && me < lg().n_c && t < lg().tiles_o; t += lg().n_c, ++k)
+                for (int r = threadIdx.x; r < lg().R_o; r += kThreads) {
+                    const uint32_t row = static_cast<uint32_t>(t * lg().R_o + r);
+                    if (row < lg().embd.cols) hown[k * lg().R_o + r] = dequant_elem(lg().embd, static_cast<uint32_t>(token), row);
                 }
         }
-        for (int l = 0; l < g.n_layers; ++l) {
-            const LayerDev& L = g.layers[l];
-            if (g.trace != nullptr && blockIdx.x == 0 && threadIdx.x == 0) g.trace[1 + (step * g.n_layers + l) * 5] = wall_clock64();
-            pst(pst_ptr(g, step, l, 0), 0);
-            if (!phase_a<TQ, TV, TH>(g, L, step, l, token, lds.g)) return;
-            pst(pst_ptr(g, step, l, 0), 7);
+        for (int l = 0; l < lg().n_layers; ++l) {
+            const LayerDev& L = lg().layers[l];
+            if (lg().trace != nullptr && blockIdx.x == 0 && threadIdx.x == 0) lg().trace[1 + (step * lg().n_layers + l) * 5] = wall_clock64();
+            pst(pst_ptr(lg(), step, l, 0), 0);
+            if (!phase_a<TQ, TV, TH>(lg(), L, step, l, token, lds.g)) return;
+            pst(pst_ptr(lg(), step, l, 0), 7);
             __syncthreads();
-            if (g.trace != nullptr && blockIdx.x == 0 && threadIdx.x == 0) g.trace[2 + (step * g.n_layers + l) * 5] = wall_clock64();
-            pst(pst_ptr(g, step, l, 1), 0);
-            if (!phase_b(g, L, step, l, pos, lds)) return;
-            pst(pst_ptr(g, step, l, 1), 7);
+            if (lg().trace != nullptr && blockIdx.x == 0 && threadIdx.x == 0) lg().trace[2 + (step * lg().n_layers + l) * 5] = wall_clock64();
+            pst(pst_ptr(lg(), step, l, 1), 0);
+            if (!phase_b(lg(), L, step, l, pos, lds)) return;
+            pst(pst_ptr(lg(), step, l, 1), 7);
             __syncthreads();
-            if (g.trace != nullptr && blockIdx.x == 0 && threadIdx.x == 0) g.trace[3 + (step * g.n_layers + l) * 5] = wall_clock64();
-            pst(pst_ptr(g, step, l, 2), 0);
-            if (!phase_c<TO>(g, L, step, l, token, lds.g, hown)) return;
-            pst(pst_ptr(g, step, l, 2), 7);
+            if (lg().trace != nullptr && blockIdx.x == 0 && threadIdx.x == 0) lg().trace[3 + (step * lg().n_layers + l) * 5] = wall_clock64();
+            pst(pst_ptr(lg(), step, l, 2), 0);
+            if (!phase_c<TO>(lg(), L, step, l, token, lds.g, hown)) return;
+            pst(pst_ptr(lg(), step, l, 2), 7);
             __syncthreads();
-            if (g.trace != nullptr && blockIdx.x == 0 && threadIdx.x == 0) g.trace[4 + (step * g.n_layers + l) * 5] = wall_clock64();
-            pst(pst_ptr(g, step, l, 3), 0);
-            if (!phase_d<TG>(g, L, step, l, lds.g)) return;
-            pst(pst_ptr(g, step, l, 3), 7);
+            if (lg().trace != nullptr && blockIdx.x == 0 && threadIdx.x == 0) lg().trace[4 + (step * lg().n_layers + l) * 5] = wall_clock64();
+            pst(pst_ptr(lg(), step, l, 3), 0);
+            if constexpr (block_elems(TD) == 32 && kPushBuilt) {
+                if (lg().push_ffn) {
+                    if (!phase_d_push<TG, TD>(lg(), L, step, l, lds.g)) return;
+                } else if (!phase_d<TG>(lg(), L, step, l, lds.g)) {
+                    return;
+                }
+            } else if (!phase_d<TG>(lg(), L, step, l, lds.g)) {
+                return;
+            }
+            pst(pst_ptr(lg(), step, l, 3), 7);
             __syncthreads();
-            if (g.trace != nullptr && blockIdx.x == 0 && threadIdx.x == 0) g.trace[5 + (step * g.n_layers + l) * 5] = wall_clock64();
-            pst(pst_ptr(g, step, l, 4), 0);
-            if (!phase_f<TD>(g, L, step, l, lds.g, hown)) return;
-            pst(pst_ptr(g, step, l, 4), 7);
+            if (lg().trace != nullptr && blockIdx.x == 0 && threadIdx.x == 0) lg().trace[5 + (step * lg().n_layers + l) * 5] = wall_clock64();
+            pst(pst_ptr(lg(), step, l, 4), 0);
+            if constexpr (block_elems(TD) == 32 && kPushBuilt) {
+                if (lg().push_ffn) {
+                    if (!phase_f_push<TD>(lg(), step, l, lds.g, hown)) return;
+                } else if (!phase_f<TD>(lg(), L, step, l, lds.g, hown)) {
+                    return;
+                }
+            } else if (!phase_f<TD>(lg(), L, step, l, lds.g, hown)) {
+                return;
+            }
+            pst(pst_ptr(lg(), step, l, 4), 7);
             __syncthreads();
         }
-        if (full && !phase_h<TH>(g, step, lds.g)) return;
+        if (full && !phase_h<TH>(lg(), step, lds.g)) return;
         __syncthreads();
     }
     if (blockIdx.x != 0 || threadIdx.x != 0) return;
     // the last step's pick becomes seq[end]; the device position follows
-    const int end = g.pos0 + g.n_steps;
-    if (g.n_steps > g.first_full && end < g.seq_len && end >= g.fixed) {
+    const int end = lg().pos0 + lg().n_steps;
+    if (lg().n_steps > lg().first_full && end < lg().seq_len && end >= lg().fixed) {
         int token = 0;
-        if (!wait_pick(g, g.n_steps - 1, token)) return;
-        g.seq[end] = token;
+        if (!wait_pick(lg(), lg().n_steps - 1, token)) return;
+        lg().seq[end] = token;
     }
-    *g.pos_out = end;
-    if (g.trace != nullptr) g.trace[0] = wall_clock64();
+    *lg().pos_out = end;
+    if (lg().trace != nullptr) lg().trace[0] = wall_clock64();
 }
 
 // ---------------------------------------------------------------- host side

@@ -15,63 +15,63 @@ __device__ inline float dequant_elem(const Packed& m, uint32_t r, uint32_t e) {
     switch (T != kF32 ? T : m.type) {
         case kQ8_0: {
             const size_t blk = static_cast<size_t>(r) * (cols / 32) + e / 32;
-            const float d = h2f(reinterpret_cast<const uint16_t*>(m.p1)[blk]);
-            return static_cast<float>(static_cast<int8_t>(m.p0[blk * 32 + e % 32])) * d;
+            const float d = h2f(gld<uint16_t>(m.p1, blk));
+            return static_cast<float>(static_cast<int8_t>(gmem(m.p0)[blk * 32 + e % 32])) * d;
         }
         case kQ4_0: {
             const size_t blk = static_cast<size_t>(r) * (cols / 32) + e / 32;
-            const float d = h2f(reinterpret_cast<const uint16_t*>(m.p1)[blk]);
+            const float d = h2f(gld<uint16_t>(m.p1, blk));
             const uint32_t i = e % 32;
-            const uint8_t q = m.p0[blk * 16 + (i & 15)];
+            const uint8_t q = gmem(m.p0)[blk * 16 + (i & 15)];
             return static_cast<float>((i < 16 ? (q & 0x0F) : (q >> 4)) - 8) * d;
         }
         case kQ4_1: {  // q d + m (src/quant.cpp:207-217)
             const size_t blk = static_cast<size_t>(r) * (cols / 32) + e / 32;
-            const float d = h2f(reinterpret_cast<const uint16_t*>(m.p1)[blk]);
-            const float mn = h2f(reinterpret_cast<const uint16_t*>(m.p2)[blk]);
+            const float d = h2f(gld<uint16_t>(m.p1, blk));
+            const float mn = h2f(gld<uint16_t>(m.p2, blk));
             const uint32_t i = e % 32;
-            const uint8_t q = m.p0[blk * 16 + (i & 15)];
+            const uint8_t q = gmem(m.p0)[blk * 16 + (i & 15)];
             return static_cast<float>(i < 16 ? (q & 0x0F) : (q >> 4)) * d + mn;
         }
         case kQ5_0: {  // ((nibble | bit e of qh << 4) - 16) d (src/quant.cpp:219-232)
             const size_t blk = static_cast<size_t>(r) * (cols / 32) + e / 32;
-            const float d = h2f(reinterpret_cast<const uint16_t*>(m.p1)[blk]);
-            const uint32_t qh = reinterpret_cast<const uint32_t*>(m.p2)[blk];
+            const float d = h2f(gld<uint16_t>(m.p1, blk));
+            const uint32_t qh = gld<uint32_t>(m.p2, blk);
             const uint32_t i = e % 32;
-            const uint8_t q = m.p0[blk * 16 + (i & 15)];
+            const uint8_t q = gmem(m.p0)[blk * 16 + (i & 15)];
             const int v = (i < 16 ? (q & 0x0F) : (q >> 4)) | static_cast<int>(((qh >> i) & 1u) << 4);
             return static_cast<float>(v - 16) * d;
         }
         case kQ5_K: {  // Q4_K's with bit s of qh[j] on value j of sub-block s (src/quant.cpp:263-283)
             const size_t blk = static_cast<size_t>(r) * (cols / 256) + e / 256;
-            const uint8_t* meta = m.p1 + blk * 16;
+            const auto meta = gmem(m.p1 + blk * 16);
             const float d = h2f(static_cast<uint16_t>(meta[0] | (meta[1] << 8)));
             const float dmin = h2f(static_cast<uint16_t>(meta[2] | (meta[3] << 8)));
             const int i = e % 256, chunk = i / 64, hi = (i % 64) >= 32, j = i % 32, sb = 2 * chunk + hi;
-            const uint8_t* dec = m.p2 + blk * 48;
+            const auto dec = gmem(m.p2 + blk * 48);
             const float d1 = d * static_cast<float>(dec[sb]), m1 = dmin * static_cast<float>(dec[8 + sb]);
-            const uint8_t q = m.p0[blk * 128 + chunk * 32 + j];
+            const uint8_t q = gmem(m.p0)[blk * 128 + chunk * 32 + j];
             const int v = (hi ? (q >> 4) : (q & 0xF)) | (((dec[16 + j] >> sb) & 1) << 4);
             return d1 * static_cast<float>(v) - m1;
         }
         case kQ4_K: {
             const size_t blk = static_cast<size_t>(r) * (cols / 256) + e / 256;
-            const uint8_t* meta = m.p1 + blk * 16;
+            const auto meta = gmem(m.p1 + blk * 16);
             const float d = h2f(static_cast<uint16_t>(meta[0] | (meta[1] << 8)));
             const float dmin = h2f(static_cast<uint16_t>(meta[2] | (meta[3] << 8)));
             const int i = e % 256, chunk = i / 64, hi = (i % 64) >= 32, j = i % 32;
             int sc, mn;
             q4k_scale_min(meta + 4, 2 * chunk + hi, sc, mn);
             const float d1 = d * static_cast<float>(sc), m1 = dmin * static_cast<float>(mn);
-            const uint8_t q = m.p0[blk * 128 + chunk * 32 + j];
+            const uint8_t q = gmem(m.p0)[blk * 128 + chunk * 32 + j];
             return d1 * static_cast<float>(hi ? (q >> 4) : (q & 0xF)) - m1;
         }
         case kQ6_K: {
             const size_t blk = static_cast<size_t>(r) * (cols / 256) + e / 256;
             const int i = e % 256, half = i / 128, w = i % 128, quarter = w / 32, l = w % 32;
-            const uint8_t* ql = m.p0 + blk * 128 + half * 64;
-            const uint8_t* qh = m.p1 + blk * 64 + half * 32;
-            const uint8_t* meta = m.p2 + blk * 20;
+            const auto ql = gmem(m.p0 + blk * 128 + half * 64);
+            const auto qh = gmem(m.p1 + blk * 64 + half * 32);
+            const auto meta = gmem(m.p2 + blk * 20);
             const int lo = (quarter & 1) ? ql[l + 32] : ql[l];
             const int nib = quarter >= 2 ? (lo >> 4) : (lo & 0xF);
             const int q = (nib | (((qh[l] >> (2 * quarter)) & 3) << 4)) - 32;
@@ -81,8 +81,8 @@ __device__ inline float dequant_elem(const Packed& m, uint32_t r, uint32_t e) {
         default: {  // TQ2_0
             const size_t blk = static_cast<size_t>(r) * (cols / 256) + e / 256;
             const int i = e % 256;
-            const int c = (m.p0[blk * 64 + (i / 128) * 32 + i % 32] >> (2 * ((i % 128) / 32))) & 3;
-            return static_cast<float>(c - 1) * h2f(reinterpret_cast<const uint16_t*>(m.p1)[blk]);
+            const int c = (gmem(m.p0)[blk * 64 + (i / 128) * 32 + i % 32] >> (2 * ((i % 128) / 32))) & 3;
+            return static_cast<float>(c - 1) * h2f(gld<uint16_t>(m.p1, blk));
         }
     }
 }
@@ -124,11 +124,11 @@ struct AttnPoolLds {
 // A 64-bit word holding a float and the tag of the step that produced it,
 // written and read with system-scope accesses (past the per-XCD L2s).
 __device__ __forceinline__ void tput(unsigned long long* p, float v, unsigned tag) {
-    __hip_atomic_store(p, (static_cast<unsigned long long>(tag) << 32) | __float_as_uint(v), __ATOMIC_RELAXED,
+    __hip_atomic_store(gmem(p), (static_cast<unsigned long long>(tag) << 32) | __float_as_uint(v), __ATOMIC_RELAXED,
                        __HIP_MEMORY_SCOPE_SYSTEM);
 }
 __device__ __forceinline__ unsigned long long tload(const unsigned long long* p) {
-    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+    return __hip_atomic_load(gmem(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
 }
 
 // Where attention puts its results: plain floats (one kernel per phase) ...
@@ -209,13 +209,13 @@ __device__ __forceinline__ void head_norm_rope(float* v, const float* bias, cons
                                                int neox, float eps) {
     const int lane = threadIdx.x & 63;
     if (bias != nullptr)
-        for (int i = lane; i < hd; i += 64) v[i] = v[i] + bias[i];
+        for (int i = lane; i < hd; i += 64) v[i] = v[i] + gmem(bias)[i];
     if (w != nullptr) {
         double s = 0.0;
         for (int i = lane; i < hd; i += 64) s += static_cast<double>(v[i] * v[i]);
         s = wave_sum(s);
         const float scale = rms_scale(s, hd, eps);
-        for (int i = lane; i < hd; i += 64) v[i] = v[i] * scale * w[i];
+        for (int i = lane; i < hd; i += 64) v[i] = v[i] * scale * gmem(w)[i];
     }
     if (rope == nullptr) return;
     const int half = rd / 2;  // only the first rd dimensions rotate (apply_rope, src/model.cpp:100-115)
@@ -254,8 +254,8 @@ __device__ __forceinline__ void attn_store_rows(const AttnArgs& g, const AttnLds
         const uint32_t kw = f2h(s.kcur[i]) | (static_cast<uint32_t>(f2h(s.kcur[i + 1])) << 16);
         const uint32_t vw = f2h(s.vcur[i]) | (static_cast<uint32_t>(f2h(s.vcur[i + 1])) << 16);
         if (kWriteThrough) {
-            __hip_atomic_store(reinterpret_cast<uint32_t*>(kr + i), kw, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
-            __hip_atomic_store(reinterpret_cast<uint32_t*>(vr + i), vw, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+            __hip_atomic_store(gmem(reinterpret_cast<uint32_t*>(kr + i)), kw, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+            __hip_atomic_store(gmem(reinterpret_cast<uint32_t*>(vr + i)), vw, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
         } else {
             *reinterpret_cast<uint32_t*>(kr + i) = kw;
             *reinterpret_cast<uint32_t*>(vr + i) = vw;
@@ -280,7 +280,7 @@ __device__ __forceinline__ void attn_finish_prologue(const AttnArgs& g, AttnLds&
     if (writer) {
         for (int i = t; i < hd; i += kThreads) {
             s.kcur[i] = h2f(f2h(s.kcur[i]));
-            s.vcur[i] = h2f(f2h(g.vbias != nullptr ? s.vcur[i] + g.vbias[kv * hd + i] : s.vcur[i]));
+            s.vcur[i] = h2f(f2h(g.vbias != nullptr ? s.vcur[i] + gmem(g.vbias)[kv * hd + i] : s.vcur[i]));
         }
         __syncthreads();
         if (store) {

@@ -161,6 +161,25 @@ brisk_hip_memory estimate_session(const brisk_hip_config& cfg, const brisk_hip_t
     sc += T * (e + 2 * qd + 2 * kvd + ff) * 4 + T * stride * (1 + 4 / 32.0 + 4 / 16.0);  // prefill buffers
     sc += static_cast<size_t>(64) * cfg.vocab * 4;                         // eval_all logits
     sc += staging + (64 << 10);                                            // load staging, small state
+    {  // the token loop's block-major down copies and their term words (Session::setup_loop's push)
+        size_t down_bytes = 0;
+        bool fmt = cfg.ff % 32 == 0 && cfg.embd <= 4096 && cfg.arch != BRISK_HIP_ARCH_BITNET && cfg.arch != BRISK_HIP_ARCH_GEMMA3 &&
+                   cfg.arch != BRISK_HIP_ARCH_LFM2;
+        for (size_t i = 0; i < n && fmt; ++i) {
+            const std::string name = tensors[i].name != nullptr ? tensors[i].name : "";
+            const auto ends = [&](const std::string& suffix) {
+                return name.size() > suffix.size() && name.compare(name.size() - suffix.size(), suffix.size(), suffix) == 0;
+            };
+            const uint32_t ty = static_cast<uint32_t>(tensors[i].type);
+            if (ends(".ffn_sub_norm.weight")) fmt = false;
+            if (ends(".ffn_gate.weight") && takes_q8_k(ty)) fmt = false;
+            if (ends(".ffn_down.weight")) {
+                if (ty != kQ4_0 && ty != kQ4_1 && ty != kQ5_0 && ty != kQ8_0) fmt = false;
+                else down_bytes += packed_bytes(ty, tensors[i].rows, tensors[i].cols);
+            }
+        }
+        if (fmt) sc += down_bytes + static_cast<size_t>(cfg.ff / 32) * e * 8;
+    }
     m.scratch = sc;
     m.total = m.weights + m.cache + m.scratch;
     return m;
@@ -594,12 +613,33 @@ void Session::setup_loop() {
     loop_grid_ = cus;  // one resident workgroup per CU: the barrier needs every workgroup resident
     loop_kernel_ = k;
 
+    // the pushed feed-forward block (phase D writes the down terms of its activation block, phase F
+    // adds them): down rows in a Q8_0-activation format, no ffn_sub norm, rows of at most 4096
+    const uint32_t td = L0.down.p.type;
+    const bool push_fmt = (td == kQ4_0 || td == kQ4_1 || td == kQ5_0 || td == kQ8_0) && !takes_q8_k(L0.gate.p.type) &&
+                          L0.ffn_sub_norm == nullptr && cfg_.ff % 32 == 0 && cfg_.embd <= 4096 && cfg_.arch != BRISK_HIP_ARCH_BITNET;
+    const char* push_env = std::getenv("BRISK_HIP_PUSH_FFN");
+    const bool push = push_fmt && (push_env == nullptr || std::string(push_env) != "0");
+    std::vector<Packed> down_t(cfg_.layers);
+    if (push) {
+        for (uint32_t l = 0; l < cfg_.layers; ++l) {
+            const Packed& d = layers_[l].down.p;
+            size_t planes[3];
+            plane_bytes(d.type, d.rows, d.cols, planes);
+            uint8_t* base = static_cast<uint8_t*>(alloc(packed_bytes(d.type, d.rows, d.cols)));
+            down_t[l] = Packed{base, base + align256(planes[0]), base + align256(planes[0]) + align256(planes[1]), d.rows, d.cols, d.type,
+                               d.flags};
+            check(launch_unit_transpose(d, down_t[l], stream_), "transpose(down)");
+        }
+        check(hipStreamSynchronize(stream_), "transpose(down)");
+    }
+
     std::vector<LayerDev> ld(cfg_.layers);
     for (uint32_t l = 0; l < cfg_.layers; ++l) {
         const Layer& L = layers_[l];
         ld[l] = LayerDev{L.q.p, L.k.p, L.v.p, L.o.p, L.gate.p, L.up.p, L.down.p, L.attn_norm, L.q_norm, L.k_norm,
                          L.attn_sub_norm, L.ffn_norm, L.ffn_sub_norm, L.q_bias, L.k_bias, L.v_bias, L.rope ? 1 : 0,
-                         kcache_[l], vcache_[l]};
+                         kcache_[l], vcache_[l], down_t[l]};
     }
     layers_dev_ = static_cast<LayerDev*>(alloc(ld.size() * sizeof(LayerDev)));
     check(hipMemcpy(layers_dev_, ld.data(), ld.size() * sizeof(LayerDev), hipMemcpyHostToDevice), "hipMemcpy(layers)");
@@ -608,8 +648,9 @@ void Session::setup_loop() {
     {
         const size_t qd = static_cast<size_t>(cfg_.heads) * cfg_.head_dim, kvd = static_cast<size_t>(cfg_.kv_heads) * cfg_.head_dim;
         const size_t parts = static_cast<size_t>(cfg_.heads) * max_splits_;
+        const size_t dterms = push ? static_cast<size_t>(cfg_.ff / 32) * cfg_.embd : 0;
         tagged_words_ = cfg_.embd + qd + 2 * kvd + qd + cfg_.ff + parts * cfg_.head_dim + parts * 2 +
-                        static_cast<size_t>(cfg_.heads) * max_ctx_;
+                        static_cast<size_t>(cfg_.heads) * max_ctx_ + dterms;
         unsigned long long* w = static_cast<unsigned long long*>(alloc(tagged_words_ * 8));
         tagged_ = w;
         check(hipMemset(w, 0, tagged_words_ * 8), "memset(tagged)");
@@ -621,7 +662,8 @@ void Session::setup_loop() {
         loop_.actt = w; w += cfg_.ff;
         loop_.pacct = w; w += parts * cfg_.head_dim;
         loop_.pmlt = w; w += parts * 2;
-        loop_.sct = w;
+        loop_.sct = w; w += static_cast<size_t>(cfg_.heads) * max_ctx_;
+        loop_.dtt = dterms ? w : nullptr;
     }
     if (std::getenv("BRISK_HIP_TRACE") != nullptr) trace_ = static_cast<unsigned long long*>(alloc(kTraceSlots * 8));
     check(hipMemset(loop_error_, 0, 64), "memset");
@@ -672,7 +714,12 @@ void Session::setup_loop() {
                                                G, static_cast<int>(max_ctx_))
                     ? static_cast<int>(cfg_.kv_heads * (cfg_.head_dim / 32)) : 0;
     if (const char* e = std::getenv("BRISK_HIP_C_FIRST")) g.c_first = g.spread && std::string(e) != "0" ? g.c_first : 0;
-    const int Gc = G - g.c_first;
+    // with the pushed feed-forward block, its tasks get workgroups of their own (the stage-2
+    // workgroups, then the last ones), so they request their weights while phase C runs
+    const int tasks = push ? static_cast<int>(cfg_.ff / 32) : 0;
+    g.n_c = G - g.c_first;
+    if (push && tasks > g.c_first) g.n_c = std::max(G - tasks, std::min(G - g.c_first, 64));
+    const int Gc = g.n_c;
     g.R_o = loop_rows({&L0.o.p}, Gc);
     g.tiles_o = tiles_of(L0.o.p, g.R_o);
     g.att_q8 = !takes_q8_k(L0.o.p.type) && L0.attn_sub_norm == nullptr &&
@@ -692,6 +739,8 @@ void Session::setup_loop() {
                ((cfg_.heads / cfg_.kv_heads) * cfg_.head_dim) % 32 == 0 ? 1 : 0;
     if (const char* e = std::getenv("BRISK_HIP_ATT_Q8")) g.att_q8 = g.att_q8 && std::string(e) != "0";
     g.tiles_d = tiles_of(L0.down.p, g.R_d);
+    g.push_ffn = push && g.own_h ? 1 : 0;
+    g.d_first = (g.c_first + g.n_c) % G;
     g.head_attn = static_cast<int>(cfg_.heads) <= G ? 1 : 0;
     if (const char* e = std::getenv("BRISK_HIP_HEAD_ATTN")) g.head_attn = g.head_attn && std::string(e) != "0";
     g.R_h = loop_rows({&out_->p}, G, true);
