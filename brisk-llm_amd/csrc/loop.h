@@ -37,6 +37,9 @@ struct LoopArgs {
     unsigned long long* sct;   // the spread attention's scores: [kv head][head][position], packed by length
     // exact attention spread over the grid (stage 1 by position chunks, stage 2 by 32-wide value slices)
     int spread;
+    // its launch constants: value slices a head, stage-2 workgroups, stage-1 workgroups a key/value
+    // head; sp_all: it takes every position of the session's context
+    int sp_slices, sp_n2, sp_per_kv, sp_all, sp_hpk;
     unsigned tag_base;
     float* logits;
     int max_splits;

@@ -29,35 +29,22 @@ namespace bh {
 
 constexpr unsigned kSpinLimit = 1u << 24;
 
-// A field of a layer descriptor (read-only for the launch) by a scalar load.
-// Scalar loads go through the scalar cache and are counted by lgkmcnt, so the
-// read does not wait for the vector memory operations in flight (weight loads
-// issued ahead, hand-off stores): a vector load of it would, as the vector
-// memory counter retires in order.  The load stays where it is written
-// (volatile), so its result is not held in registers across the phases.
+// A field of a layer descriptor (read-only for the launch), read through the
+// constant address space: the compiler reads it with scalar loads, which go
+// through the scalar cache and are counted by lgkmcnt, so the read does not
+// wait for the vector memory operations in flight (weight loads issued ahead,
+// hand-off stores); a vector load of it would, as the vector memory counter
+// retires in order.
 template <class T>
 __device__ __forceinline__ T sld(const T* p) {
-    static_assert(sizeof(T) == 4 || sizeof(T) == 8 || sizeof(T) == 40, "sld: 4, 8 or 40 bytes");
-    if constexpr (sizeof(T) == 4) {
-        uint32_t v;
-        asm volatile("s_load_dword %0, %1, 0x0\n\ts_waitcnt lgkmcnt(0)" : "=s"(v) : "s"(p));
-        return __builtin_bit_cast(T, v);
-    } else if constexpr (sizeof(T) == 8) {
-        uint64_t v;
-        asm volatile("s_load_dwordx2 %0, %1, 0x0\n\ts_waitcnt lgkmcnt(0)" : "=s"(v) : "s"(p));
-        return __builtin_bit_cast(T, v);
-    } else {
-        typedef unsigned u32x8 __attribute__((ext_vector_type(8)));
-        u32x8 a;
-        uint64_t b;
-        asm volatile("s_load_dwordx8 %0, %2, 0x0\n\ts_load_dwordx2 %1, %2, 0x20\n\ts_waitcnt lgkmcnt(0)" : "=s"(a), "=s"(b) : "s"(p));
-        unsigned char buf[40];
-        __builtin_memcpy(buf, &a, 32);
-        __builtin_memcpy(buf + 32, &b, 8);
-        T r;
-        __builtin_memcpy(&r, buf, 40);
-        return r;
-    }
+    static_assert(sizeof(T) % 4 == 0 && alignof(T) >= 4, "sld: whole dwords");
+    typedef const __attribute__((address_space(4))) uint32_t* cptr;
+    uint32_t w[sizeof(T) / 4];
+#pragma unroll
+    for (size_t i = 0; i < sizeof(T) / 4; ++i) w[i] = ((cptr)p)[i];
+    T v;
+    __builtin_memcpy(&v, w, sizeof(T));
+    return v;
 }
 
 __device__ __forceinline__ bool loop_failed(const LoopArgs& g) {
@@ -869,25 +856,33 @@ __device__ __forceinline__ void pair_norm_rope(float* v, const Pair& p, const Pa
 
 __device__ __forceinline__ bool spread_stage1(const LoopArgs& g, const AttnArgs& a, SpreadStage1& s, int kv, int p0, int p1,
                                               int pos, unsigned tin, unsigned tsc, const Stamps& st) {
-    const int hd = a.head_dim, hpk = a.heads / a.kv_heads, t = threadIdx.x, wave = t >> 6, Lc = pos + 1;
+    const int hd = a.head_dim, hpk = g.sp_hpk, t = threadIdx.x, wave = t >> 6, Lc = pos + 1;
     const bool writer = p1 == Lc;
     const int cached = (writer ? pos : p1) - p0;
     const float* rope_row = a.rope != nullptr ? a.rope + static_cast<size_t>(pos) * a.rope_dim : nullptr;
     const Pair pr = rope_pair(t & 63, hd, a.neox);
-    // the norm and rotation constants of the head(s) this wave will take (queries: q_norm, the writer's key: k_norm)
-    const PairConst kq = pair_const(pr, a.qnorm, rope_row), kk = pair_const(pr, a.knorm, rope_row);
+    // the norm and rotation constants of the head(s) this wave will take (queries: q_norm, the writer's key:
+    // k_norm).  Wave 0 only polls: a load issued before its poll would hold the poll's results back
+    // until it returned (a wave's loads complete in order).
+    PairConst kq{1.0f, 1.0f, 1.0f, 0.0f}, kk{1.0f, 1.0f, 1.0f, 0.0f};
+    if (wave != 0) {
+        kq = pair_const(pr, a.qnorm, rope_row);
+        kk = pair_const(pr, a.knorm, rope_row);
+    }
     bool fail = false;
     if (wave == 0) {  // this token's query heads (and, for the writer, key) while the others stage the keys
+        pst(st, 4);
         fail = !wget_segs<8>(g, tin, TSeg{g.qt + kv * hpk * hd, s.q, hpk * hd},
                              writer ? TSeg{g.kt + kv * hd, s.kcur, hd} : TSeg{nullptr, nullptr, 0}, TSeg{nullptr, nullptr, 0});
+        pst(st, 6);
     } else if (cached > 0) {
         chunk_issue_by(s.kst, a.kcache + static_cast<size_t>(kv) * a.ctx * hd, p0, cached, hd, false, t - 64, kThreads - 64);
     }
     __builtin_amdgcn_s_waitcnt(0);
     if (__syncthreads_or(fail)) return false;
     pst(st, 1);
-    // q_norm / k_norm and RoPE (src/model.cpp:1026-1041); the key rounded to fp16 as the cache holds it
-    for (int h = wave; h < hpk + (writer ? 1 : 0); h += kThreads / 64) {
+    // q_norm / k_norm and RoPE (src/model.cpp:1026-1041) by waves 1..3; the key rounded to fp16 as the cache holds it
+    for (int h = wave - 1; wave > 0 && h < hpk + (writer ? 1 : 0); h += kThreads / 64 - 1) {
         if (h < hpk)
             pair_norm_rope(s.q + h * hd, pr, kq, a.qbias != nullptr ? a.qbias + (kv * hpk + h) * hd : nullptr, a.qnorm != nullptr,
                            rope_row != nullptr, hd, a.eps);
@@ -995,9 +990,11 @@ __device__ __forceinline__ bool spread_stage2(const LoopArgs& g, const AttnArgs&
         // normalised and rotated, then the slice of both rows rounded to fp16 into the cache rows
         // (store_f16, src/kernels_f32.cpp:248-250)
         const Pair pr = rope_pair(lane, hd, a.neox);
-        const PairConst kk = pair_const(pr, a.knorm, rope_row);
         fail = !wget_segs<4>(g, tin, TSeg{g.kt + kv * hd, s.kcur, hd}, TSeg{g.vt + kv * hd + d0, s.vcur, kSpreadSlice},
                              TSeg{nullptr, nullptr, 0});
+        // (the norm and rotation constants requested after the poll: loads issued before it would hold
+        // its results back)
+        const PairConst kk = pair_const(pr, a.knorm, rope_row);
         if (!fail) {
             pair_norm_rope(s.kcur, pr, kk, a.kbias != nullptr ? a.kbias + kv * hd : nullptr, a.knorm != nullptr, rope_row != nullptr,
                            hd, a.eps);
@@ -1127,24 +1124,41 @@ __device__ __forceinline__ bool spread_stage2(const LoopArgs& g, const AttnArgs&
     return true;
 }
 
-// B, spread: the tasks of both stages; a workgroup with neither goes on to phase C.
-__device__ __forceinline__ bool phase_b_spread(const LoopArgs& g, const LayerDev& L, int step, int l, int pos, SpreadLds& s) {
-    const int kvh = g.kv_heads, hd = g.head_dim, Lc = pos + 1, G = static_cast<int>(gridDim.x);
-    const int slices = hd / kSpreadSlice, n2 = kvh * slices, per_kv = (G - n2) / kvh;
+// This workgroup's part of the spread attention at one context length: a
+// stage-2 task (kv2, slice at d0; kv = -1), or stage-1 positions [p0, p1) of
+// key/value head kv (empty when the length leaves the chunk out).
+struct SpreadGeo {
+    int kv, p0, p1, kv2, d0;
+};
+__device__ __forceinline__ SpreadGeo spread_geo(const LoopArgs& g, int pos) {
+    SpreadGeo geo{-1, 0, 0, 0, 0};
+    if (!g.spread) return geo;
+    const int Lc = pos + 1, b = static_cast<int>(blockIdx.x), per_kv = g.sp_per_kv;
+    if (b < g.sp_n2) {
+        geo.kv2 = b / g.sp_slices;
+        geo.d0 = (b - geo.kv2 * g.sp_slices) * kSpreadSlice;
+        return geo;
+    }
     int P1 = (Lc + per_kv - 1) / per_kv;
     P1 = P1 < 4 ? 4 : P1;
-    const int chunks = (Lc + P1 - 1) / P1;
+    const int task = b - g.sp_n2, kv = task / per_kv, c = task - kv * per_kv;
+    geo.kv = kv < g.kv_heads ? kv : g.kv_heads;  // past the last head: no task
+    geo.p0 = kv < g.kv_heads ? c * P1 : 0;
+    geo.p1 = kv < g.kv_heads ? (geo.p0 + P1 < Lc ? geo.p0 + P1 : Lc) : 0;
+    if (geo.p0 >= Lc) geo.p1 = geo.p0;
+    return geo;
+}
+
+// B, spread: the tasks of both stages; a workgroup with neither goes on to phase C.
+__device__ __forceinline__ bool phase_b_spread(const LoopArgs& g, const AttnArgs& a, int step, int l, int pos, SpreadLds& s,
+                                               const SpreadGeo& geo) {
     const unsigned tin = tag_of(g, step, l, 1), tsc = tag_of(g, step, l, 6), tout = tag_of(g, step, l, 2);
-    const AttnArgs a = attn_args(g, L, step, l);
-    const int b = static_cast<int>(blockIdx.x);
-    if (b < n2) {
+    if (geo.kv < 0) {  // stage 2: (key/value head, slice)
         const TaggedOut o{g.attt, g.pacct, g.pmlt, tout, g.error, g.att_q8, g.heads * g.head_dim};
-        return spread_stage2(g, a, s.s2, b / slices, (b % slices) * kSpreadSlice, pos, tin, tsc, o, pst_ptr(g, step, l, 1));
+        return spread_stage2(g, a, s.s2, geo.kv2, geo.d0, pos, tin, tsc, o, pst_ptr(g, step, l, 1));
     }
-    const int task = b - n2, kv = task / per_kv, c = task - kv * per_kv;
-    if (kv >= kvh || c >= chunks) return true;
-    const int p0 = c * P1, p1 = p0 + P1 < Lc ? p0 + P1 : Lc;
-    return spread_stage1(g, a, s.s1, kv, p0, p1, pos, tin, tsc, pst_ptr(g, step, l, 1));
+    if (geo.p0 >= geo.p1) return true;  // no chunk at this length
+    return spread_stage1(g, a, s.s1, geo.kv, geo.p0, geo.p1, pos, tin, tsc, pst_ptr(g, step, l, 1));
 }
 
 // Whether the spread attention takes a context of L positions (on a grid of G workgroups).
@@ -1155,12 +1169,12 @@ __device__ __forceinline__ bool spread_takes(const LoopArgs& g, int L) {
 }
 
 // B: attention, exact (one workgroup per key/value head) or split over (kv, split) slots.
-__device__ __forceinline__ bool phase_b(const LoopArgs& g, const LayerDev& L, int step, int l, int pos, LoopLds& lds) {
-    const int kvh = g.kv_heads, hpk = g.heads / kvh, hd = g.head_dim, Lc = pos + 1;
+__device__ __forceinline__ bool phase_b(const LoopArgs& g, const LayerDev& L, int step, int l, int pos, LoopLds& lds, const SpreadGeo& geo) {
+    const int kvh = g.kv_heads, hpk = g.sp_hpk, hd = g.head_dim, Lc = pos + 1;
     const unsigned tin = tag_of(g, step, l, 1), tout = tag_of(g, step, l, 2);
     const AttnArgs a = attn_args(g, L, step, l);
     const TaggedOut o{g.attt, g.pacct, g.pmlt, tout, g.error, g.att_q8, g.heads * g.head_dim};
-    if (g.spread && spread_takes(g, Lc)) return phase_b_spread(g, L, step, l, pos, lds.spread);
+    if (g.spread && (g.sp_all || spread_takes(g, Lc))) return phase_b_spread(g, a, step, l, pos, lds.spread, geo);
     if (attn_is_exact(Lc, hpk) && Lc <= kSplit * kPoolChunks && g.head_attn) {
         if (static_cast<int>(blockIdx.x) >= g.heads) return true;
         const int h = blockIdx.x;
@@ -1632,6 +1646,7 @@ __global__ __launch_bounds__(kThreads) void k_loop(LoopArgs g_arg) {
     __shared__ LoopLds lds;
     __shared__ float hown[kOwnRows];
     __shared__ int s_token, s_ok;
+    __shared__ SpreadGeo s_geo;
     exp_tab_fill();  // ordered before its first use by the barrier after the first token
     for (int step = 0; step < lg().n_steps; ++step) {
         const int pos = lg().pos0 + step;
@@ -1652,6 +1667,7 @@ __global__ __launch_bounds__(kThreads) void k_loop(LoopArgs g_arg) {
             s_token = token;
             s_ok = ok;
         }
+        if (threadIdx.x == 0) s_geo = spread_geo(lg(), pos);
         __syncthreads();
         if (!s_ok) return;
         const int token = s_token;
@@ -1668,11 +1684,15 @@ __global__ __launch_bounds__(kThreads) void k_loop(LoopArgs g_arg) {
             if (lg().trace != nullptr && blockIdx.x == 0 && threadIdx.x == 0) lg().trace[1 + (step * lg().n_layers + l) * 5] = wall_clock64();
             pst(pst_ptr(lg(), step, l, 0), 0);
             if (!phase_a<TQ, TV, TH>(lg(), L, step, l, token, lds.g)) return;
+            if (lg().trace != nullptr) {
+                __builtin_amdgcn_s_waitcnt(0);
+                pst(pst_ptr(lg(), step, l, 0), 6);
+            }
             pst(pst_ptr(lg(), step, l, 0), 7);
             __syncthreads();
             if (lg().trace != nullptr && blockIdx.x == 0 && threadIdx.x == 0) lg().trace[2 + (step * lg().n_layers + l) * 5] = wall_clock64();
             pst(pst_ptr(lg(), step, l, 1), 0);
-            if (!phase_b(lg(), L, step, l, pos, lds)) return;
+            if (!phase_b(lg(), L, step, l, pos, lds, s_geo)) return;
             pst(pst_ptr(lg(), step, l, 1), 7);
             __syncthreads();
             if (lg().trace != nullptr && blockIdx.x == 0 && threadIdx.x == 0) lg().trace[3 + (step * lg().n_layers + l) * 5] = wall_clock64();

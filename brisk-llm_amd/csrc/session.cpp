@@ -709,6 +709,12 @@ void Session::setup_loop() {
     // with the spread attention, its stage-2 workgroups take no O or down tiles
     g.spread = loop_spread_fits(static_cast<int>(cfg_.heads), static_cast<int>(cfg_.kv_heads), static_cast<int>(cfg_.head_dim), rope_dim_, G) ? 1 : 0;
     if (const char* e = std::getenv("BRISK_HIP_SPREAD")) g.spread = g.spread && std::string(e) != "0";
+    g.sp_slices = static_cast<int>(cfg_.head_dim) / 32;
+    g.sp_hpk = static_cast<int>(cfg_.heads / cfg_.kv_heads);
+    g.sp_n2 = static_cast<int>(cfg_.kv_heads) * g.sp_slices;
+    g.sp_per_kv = (G - g.sp_n2) / static_cast<int>(cfg_.kv_heads);
+    g.sp_all = g.spread && loop_spread_covers(static_cast<int>(cfg_.heads), static_cast<int>(cfg_.kv_heads), static_cast<int>(cfg_.head_dim),
+                                              G, static_cast<int>(max_ctx_)) ? 1 : 0;
     // (only when every position of the context takes it: longer contexts run the split attention)
     g.c_first = g.spread && loop_spread_covers(static_cast<int>(cfg_.heads), static_cast<int>(cfg_.kv_heads), static_cast<int>(cfg_.head_dim),
                                                G, static_cast<int>(max_ctx_))
