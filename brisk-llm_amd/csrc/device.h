@@ -1174,10 +1174,17 @@ struct Tile {
             float tv[kMax];
 #pragma unroll
             for (int k = 0; k < kMax; ++k) tv[k] = u[k].term(b, a);
+            if (total == static_cast<uint32_t>(kMax * kThreads) && row0 + static_cast<uint32_t>(R) <= m.rows) {
+                // every unit of the tile is in the matrix (a uniform test): stores without
+                // per-unit branches, so the units' independent chains interleave
 #pragma unroll
-            for (int k = 0; k < kMax; ++k) {
-                const uint32_t r = r0 + k * step;
-                if (r < static_cast<uint32_t>(R) && row0 + r < m.rows) terms[r * stride + b] = tv[k];
+                for (int k = 0; k < kMax; ++k) terms[(r0 + k * step) * stride + b] = tv[k];
+            } else {
+#pragma unroll
+                for (int k = 0; k < kMax; ++k) {
+                    const uint32_t r = r0 + k * step;
+                    if (r < static_cast<uint32_t>(R) && row0 + r < m.rows) terms[r * stride + b] = tv[k];
+                }
             }
             return;
         }

@@ -1484,6 +1484,7 @@ __device__ __forceinline__ bool phase_d_push(const LoopArgs& g, const LayerDev& 
             if (k + 2 < tiles) tile_load(t0, j, k + 2);
             if (k + 1 < tiles) tile_terms(t1, k + 1);
         }
+        pst(st, 6);
         __syncthreads();
         row_sums(s.terms, stride, units, 64, s.sums);
         __syncthreads();

@@ -573,6 +573,9 @@ static int loop_rows(const std::vector<const Packed*>& ms, int grid, bool head =
     cap = std::max<size_t>(cap, 1);
     const size_t g = static_cast<size_t>(grid);
     const size_t rounds = (rows + g * cap - 1) / (g * cap);
+    // full tiles when they take no more rounds: every unit of a full tile is in the matrix, so
+    // its terms are formed without per-unit branches
+    if ((rows + cap - 1) / cap <= g * rounds && rows % cap == 0) return static_cast<int>(cap);
     return static_cast<int>(std::max<size_t>(1, (rows + g * rounds - 1) / (g * rounds)));
 }
 
@@ -733,7 +736,7 @@ void Session::setup_loop() {
     if (const char* e = std::getenv("BRISK_HIP_ATT_Q8")) g.att_q8 = g.att_q8 && std::string(e) != "0";
     g.R_gu = loop_rows({&L0.gate.p}, G);
     g.tiles_gu = tiles_of(L0.gate.p, g.R_gu);
-    g.R_d = loop_rows({&L0.down.p}, Gc);
+    g.R_d = push ? g.R_o : loop_rows({&L0.down.p}, Gc);  // the pushed phase F takes phase C's rows
     {
         const int R = std::min(g.R_o, g.R_d);
         const int tiles = tiles_of(L0.o.p, R);
@@ -746,7 +749,13 @@ void Session::setup_loop() {
     if (const char* e = std::getenv("BRISK_HIP_ATT_Q8")) g.att_q8 = g.att_q8 && std::string(e) != "0";
     g.tiles_d = tiles_of(L0.down.p, g.R_d);
     g.push_ffn = push && g.own_h ? 1 : 0;
-    g.d_first = (g.c_first + g.n_c) % G;
+    {
+        // the pushed phase D's tasks on the workgroups past those with O tiles, if there are enough
+        // (the stage-2 attention workgroups, which finish phase B last, then take none); else from
+        // the end of the grid round to the stage-2 workgroups
+        const int c_wgs = std::min(g.tiles_o, g.n_c);
+        g.d_first = G - g.c_first - c_wgs >= tasks ? g.c_first + c_wgs : (g.c_first + g.n_c) % G;
+    }
     g.head_attn = static_cast<int>(cfg_.heads) <= G ? 1 : 0;
     if (const char* e = std::getenv("BRISK_HIP_HEAD_ATTN")) g.head_attn = g.head_attn && std::string(e) != "0";
     g.R_h = loop_rows({&out_->p}, G, true);
