@@ -125,6 +125,7 @@ def ref_lib():
         L.ref_softmax.argtypes = [_vp, _sz]
         L.ref_dot_f32.argtypes = [_vp, _vp, _sz]
         L.ref_dot_f32.restype = _f
+        L.ref_config.argtypes = [_vp, C.POINTER(RefConfig)]
         _ref = L
     return _ref
 
@@ -197,6 +198,22 @@ def _gap(logits, best):
     return float(logits[best] - second)
 
 
+class RefConfig(C.Structure):
+    """ref_shim.cpp's RefConfig: the reference's ModelConfig (src/model.h:34-125) as parsed from a file."""
+    _fields_ = [(n, C.c_uint32) for n in ("arch", "vocab", "embd", "layers", "heads", "kv_heads", "head_dim", "ff", "context")] + [
+        ("rope_base", C.c_float), ("eps", C.c_float), ("rope_neox", C.c_int32), ("rope_dim", C.c_uint32),
+        ("rope_original_context", C.c_uint32), ("rope_attn_factor", C.c_float), ("sliding_window", C.c_uint32),
+        ("rope_base_local", C.c_float), ("rope_scale", C.c_float), ("embedding_scale", C.c_float),
+        ("final_softcap", C.c_float), ("gelu", C.c_int32), ("conv_taps", C.c_uint32), ("no_rope_step", C.c_uint32),
+        ("n_rope_factors", C.c_uint32), ("n_factors_short", C.c_uint32), ("n_factors_long", C.c_uint32),
+        ("conv_layers", C.c_uint64)]
+
+
+# the reference's Architecture enumerators (src/model.h:20-31), by GGUF architecture name
+REF_ARCH = {"qwen3": 0, "qwen2": 1, "llama": 2, "gemma3": 3, "gemma4": 4, "bitnet": 5, "bitnet-b1.58": 5, "phi3": 6,
+            "lfm2": 7, "smollm3": 8, "qwen35": 9}
+
+
 class Reference:
     """The reference's own CPU Session (oracle/_ref), opened on a GGUF path."""
 
@@ -214,6 +231,12 @@ class Reference:
             self.h = None
 
     __del__ = close
+
+    def config(self) -> RefConfig:
+        out = RefConfig()
+        if self.L.ref_config(self.h, C.byref(out)) != 0:
+            raise RuntimeError(self.L.ref_last_error().decode())
+        return out
 
     def eval(self, tokens) -> np.ndarray:
         tokens = np.ascontiguousarray(tokens, dtype=np.int32)

@@ -75,6 +75,43 @@ void ref_close(void* handle) { delete static_cast<RefHandle*>(handle); }
 
 uint32_t ref_vocab(void* handle) { return static_cast<RefHandle*>(handle)->model->config().vocab_size; }
 
+// The reference's parse of the file's metadata (ModelConfig, src/model.h:34-125, filled by
+// src/model.cpp:161-301), for pinning the Python binding's own parse against it.
+struct RefConfig {
+    uint32_t arch, vocab, embd, layers, heads, kv_heads, head_dim, ff, context;
+    float rope_base, eps;
+    int32_t rope_neox;
+    uint32_t rope_dim, rope_original_context;
+    float rope_attn_factor;
+    uint32_t sliding_window;
+    float rope_base_local, rope_scale, embedding_scale, final_softcap;
+    int32_t gelu;
+    uint32_t conv_taps, no_rope_step;
+    uint32_t n_rope_factors, n_factors_short, n_factors_long;
+    uint64_t conv_layers;  // bit l: layer l is a short-convolution layer (layers 0..63)
+};
+
+int ref_config(void* handle, RefConfig* out) {
+    return guarded([&] {
+        const brisk::ModelConfig& c = static_cast<RefHandle*>(handle)->model->config();
+        RefConfig r{};
+        r.arch = static_cast<uint32_t>(c.architecture);
+        r.vocab = c.vocab_size; r.embd = c.embedding_dim; r.layers = c.layer_count; r.heads = c.head_count;
+        r.kv_heads = c.kv_head_count; r.head_dim = c.head_dim; r.ff = c.feed_forward_dim; r.context = c.context_length;
+        r.rope_base = c.rope_base; r.eps = c.rms_epsilon; r.rope_neox = c.rope_neox ? 1 : 0;
+        r.rope_dim = c.rope_dim_of(); r.rope_original_context = c.rope_original_context; r.rope_attn_factor = c.rope_attn_factor;
+        r.sliding_window = c.sliding_window; r.rope_base_local = c.rope_base_local; r.rope_scale = c.rope_scale;
+        r.embedding_scale = c.embedding_scale; r.final_softcap = c.final_softcap; r.gelu = c.gelu ? 1 : 0;
+        r.conv_taps = c.conv_taps; r.no_rope_step = c.no_rope_step;
+        r.n_rope_factors = static_cast<uint32_t>(c.rope_factors.size());
+        r.n_factors_short = static_cast<uint32_t>(c.rope_factors_short.size());
+        r.n_factors_long = static_cast<uint32_t>(c.rope_factors_long.size());
+        for (std::size_t l = 0; l < c.layer_count && l < 64; ++l)
+            if (c.layer_is_conv(l)) r.conv_layers |= uint64_t{1} << l;
+        *out = r;
+    });
+}
+
 size_t ref_position(void* handle) { return static_cast<RefHandle*>(handle)->session->position(); }
 
 int ref_rollback(void* handle, size_t position) {

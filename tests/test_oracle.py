@@ -465,6 +465,44 @@ def test_oracle_longrope_matches_reference_bitwise():
     short.close()
 
 
+@needs_ref
+@pytest.mark.parametrize("name", ["tiny-qwen3", "tiny-llama", "tiny-bitnet", "tiny-q5k", "tiny-q5", "tiny-qwen2", "tiny-smollm3", "tiny-gemma3", "tiny-phi3", "tiny-llama32", "tiny-lfm2"])
+def test_model_config_matches_reference(name):
+    """brisk_hip.model.parse_config against the reference's own ModelConfig parse (src/model.cpp:140-260)
+    of the same file, field by field. The Python config keeps 0 for a field its family does not use;
+    the reference holds its default there (src/model.h:34-125), so those map through the defaults."""
+    path, f, cfg, table = tiny(name)
+    r = pyoracle.Reference(path, threads=1, max_context=16)
+    c = r.config()
+    r.close()
+    assert c.arch == pyoracle.REF_ARCH[cfg.arch_name]
+    assert (c.vocab, c.embd, c.layers, c.heads, c.kv_heads, c.head_dim, c.ff, c.context) == \
+        (cfg.vocab, cfg.embd, cfg.layers, cfg.heads, cfg.kv_heads, cfg.head_dim, cfg.ff, cfg.context)
+    f32 = lambda x: np.float32(x).view(np.uint32)  # noqa: E731
+    assert f32(c.rope_base) == f32(cfg.rope_base) and f32(c.eps) == f32(cfg.eps)
+    assert bool(c.rope_neox) == cfg.rope_neox
+    assert c.rope_dim == (cfg.rope_dim or cfg.head_dim)
+    assert c.rope_original_context == cfg.rope_original_context
+    assert f32(c.rope_attn_factor) == f32(cfg.rope_attn_factor or 1.0)
+    assert c.sliding_window == cfg.sliding_window
+    gemma = cfg.arch == model.ARCH_GEMMA3
+    assert f32(c.rope_base_local) == f32(cfg.rope_base_local if gemma else 10000.0)
+    assert f32(c.rope_scale) == f32(cfg.rope_scale if gemma else 1.0)
+    assert f32(c.final_softcap) == f32(cfg.final_softcap)
+    # Gemma's sqrt(embedding_dim) input scale and GELU activation follow from the family in the session
+    assert f32(c.embedding_scale) == f32(np.sqrt(np.float32(cfg.embd)) if gemma else 1.0)
+    assert bool(c.gelu) == gemma
+    assert c.conv_taps == cfg.conv_taps
+    assert c.conv_layers == sum(1 << l for l in cfg.conv_layers)
+    assert c.no_rope_step == (4 if cfg.arch == model.ARCH_SMOLLM3 else 0)
+    assert [l for l in range(cfg.layers) if not cfg.layer_has_rope(l)] == \
+        ([l for l in range(cfg.layers) if (l + 1) % c.no_rope_step == 0] if c.no_rope_step else [])
+    names = {t.name for t in table}
+    # Phi-3 starts from its short LongRoPE factors (src/model.cpp:186)
+    assert (c.n_rope_factors > 0) == ("rope_freqs.weight" in names or "rope_factors_short.weight" in names)
+    assert (c.n_factors_short > 0) == (c.n_factors_long > 0) == ("rope_factors_short.weight" in names)
+
+
 def test_oracle_rejects_bad_input():
     path, f, cfg, table = tiny("tiny-qwen3")
     o = pyoracle.Oracle(cfg, table, max_context=8)
