@@ -156,13 +156,17 @@ int brisk_hip_matmul(int type, int flags, const void* packed, size_t rows, size_
         void* mem = nullptr;
         const size_t qb = n * static_cast<size_t>(stride), db = n * static_cast<size_t>(stride / 32) * 4,
                      bb = n * static_cast<size_t>(stride / 16) * 4;
-        hip_check(hipMalloc(&mem, qb + db + bb), "hipMalloc");
+        // a Q6_K matrix is expanded there too, as a session's prefill holds it (launch_q6x_expand)
+        const size_t xb = p.type == bh::kQ6_K ? bh::q6x_bytes(p.rows, p.cols) : 0;
+        const size_t ab = bh::align256(qb + db + bb);
+        hip_check(hipMalloc(&mem, ab + xb), "hipMalloc");
         x.qs = static_cast<int8_t*>(mem);
         x.d = reinterpret_cast<float*>(static_cast<char*>(mem) + qb);
         x.bs = reinterpret_cast<int32_t*>(static_cast<char*>(mem) + qb + db);
+        bh::MmArgs g{};
         hipError_t e = bh::launch_pre_planar(xq, static_cast<int>(cols), static_cast<int>(n), bh::takes_q8_k(p.type), x, st);
+        if (e == hipSuccess && xb != 0) e = bh::launch_q6x_expand(p, static_cast<char*>(mem) + ab, &g.qx, &g.qxd, st);
         if (e == hipSuccess) {
-            bh::MmArgs g{};
             g.m = p; g.x = x; g.ntok = static_cast<int>(n); g.out = out; g.ostride = static_cast<int>(out_stride);
             e = bh::launch_mm(g, bh::kMmStore, st);
         }

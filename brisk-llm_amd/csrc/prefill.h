@@ -27,7 +27,19 @@ struct MmArgs {
     float* out;      // out[t * ostride + r]
     int ostride;
     int relu2;       // kMmPair: BitNet's squared-ReLU gate instead of SiLU
+    // Q6_K: the expanded planes of m (and m2) from launch_q6x_expand, or null (the packed-plane GEMM)
+    const int8_t* qx;
+    const float* qxd;
+    const int8_t* qx2;
+    const float* qxd2;
 };
+
+// Rows a workgroup of the expanded-Q6_K GEMM computes; the expanded planes pad rows to it.
+constexpr int kMxRows = 128;
+// Bytes of a Q6_K matrix's expanded planes (int8 lo and hi weights, float scales).
+size_t q6x_bytes(uint32_t rows, uint32_t cols);
+// Writes the expanded planes of Q6_K matrix m into mem (q6x_bytes of it); *q and *d point into mem.
+hipError_t launch_q6x_expand(const Packed& m, void* mem, const int8_t** q, const float** d, hipStream_t s);
 
 struct PreAttnArgs {
     AttnArgs a;      // layer, shape and cache (a.q/k/v/pos/out unused)

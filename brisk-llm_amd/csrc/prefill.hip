@@ -20,6 +20,8 @@
 #include "phases.h"
 #include "prefill.h"
 
+#include <cstdlib>
+
 
 namespace bh {
 
@@ -850,6 +852,223 @@ __device__ __forceinline__ void kq_compute_fold6(uint32_t base, MmAcc<G>& acc) {
     }
 }
 
+// ---------------------------------------------------------------- Q6_K, expanded
+
+// Q6_K matrices the batched prefill multiplies are also held expanded (once, at
+// the first prefill): per 16-value group g of a super-block the exact integer
+// weight w = sc_g (q - 32) (|w| <= 4096) is split as w = lo + 128 hi with lo in
+// -64..63 and hi in -32..32, both int8.  Then dot_q6_k_q8_k's weighted sum
+// (src/quant.cpp:549-563) is A_lo + 128 A_hi, A = sum_k w_k x_k, two int32 MFMA
+// chains over the super-block with no decoding in the GEMM.
+//
+// The planes are in the fragment order of v_mfma_i32_32x32x32_i8: for 32-row
+// group rg, super-block c, 32-value step s and plane p (lo, hi), 64 lanes x 16
+// bytes, lane l holding row 32 rg + l % 32, values 32 s + 16 (l / 32) .. + 15
+// of the super-block.  A wave's operand for one step is one coalesced 1 KB load.
+// The scales follow as floats: d[(rg * nsb + c) * 32 + r % 32] = h2f(d of row r).
+// Rows are padded to a multiple of kMxRows with zero weights.
+__global__ void k_q6x_expand(Packed m, int8_t* __restrict__ q, float* __restrict__ dq, uint32_t row_groups) {
+    const size_t gid = static_cast<size_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    const uint32_t nsb = m.cols / 256;
+    const int lane = static_cast<int>(gid & 63), s = static_cast<int>((gid >> 6) & 7);
+    const size_t rest = gid >> 9;
+    const uint32_t c = static_cast<uint32_t>(rest % nsb), rg = static_cast<uint32_t>(rest / nsb);
+    if (rg >= row_groups) return;
+    const uint32_t row = rg * 32 + (lane & 31);
+    const int kin = s * 32 + (lane >> 5) * 16;  // first value of the lane's group within the super-block
+    uint32_t lo[4] = {0, 0, 0, 0}, hi[4] = {0, 0, 0, 0};
+    float d = 0.0f;
+    if (row < m.rows) {
+        const size_t blk = static_cast<size_t>(row) * nsb + c;
+        const uint8_t* ql = m.p0 + blk * 128;
+        const uint8_t* qh = m.p1 + blk * 64;
+        const uint8_t* meta = m.p2 + blk * 20;
+        const int sc = static_cast<int8_t>(meta[kin / 16]);
+        d = h2f(static_cast<uint16_t>(meta[16] | (meta[17] << 8)));
+        for (int b = 0; b < 16; ++b) {  // block_q6_K element order (dequantize_row_q6_K)
+            const int k = kin + b, n = k >> 7, j = k & 127, which = j >> 5, l = j & 31;
+            const int qlb = ql[n * 64 + l + (which & 1) * 32];
+            const int nib = which >= 2 ? qlb >> 4 : qlb & 15;
+            const int u = nib | (((qh[n * 32 + l] >> (2 * which)) & 3) << 4);
+            const int w = sc * (u - 32);
+            const int wl = ((w + 64) & 127) - 64, wh = (w - wl) >> 7;
+            lo[b >> 2] |= static_cast<uint32_t>(wl & 0xFF) << (8 * (b & 3));
+            hi[b >> 2] |= static_cast<uint32_t>(wh & 0xFF) << (8 * (b & 3));
+        }
+    }
+    uint8_t* o = reinterpret_cast<uint8_t*>(q) + ((((static_cast<size_t>(rg) * nsb + c) * 8 + s) * 2) * 64 + lane) * 16;
+    *reinterpret_cast<uint4*>(o) = make_uint4(lo[0], lo[1], lo[2], lo[3]);
+    *reinterpret_cast<uint4*>(o + 1024) = make_uint4(hi[0], hi[1], hi[2], hi[3]);
+    if (s == 0 && lane < 32) dq[(static_cast<size_t>(rg) * nsb + c) * 32 + lane] = d;
+}
+
+typedef int v16i __attribute__((ext_vector_type(16)));
+__device__ __forceinline__ v16i mfma32(const v4u& a, const v4u& b, v16i c) {
+    return __builtin_amdgcn_mfma_i32_32x32x32_i8(__builtin_bit_cast(v4i, a), __builtin_bit_cast(v4i, b), c, 0, 0, 0);
+}
+
+// 32 G tokens' activations of one super-block (token t piece p at slot t * 16 + (p ^ (t & 15))) and their scales.
+template <int G>
+struct MxStage {
+    alignas(16) int8_t x[32 * G * 256];
+    alignas(16) float xd[64];  // G = 1: lanes 32..63 hold a copy
+};
+
+template <int G>
+__device__ __forceinline__ void mx_copy(MxStage<G>& st, const ActPlanar& x, int ntok, int t0, int c) {
+    const int tid = threadIdx.x, wave = tid >> 6, wave_first = tid & ~63;
+    auto tokc = [&](int t) -> size_t { return static_cast<size_t>(t0 + t < ntok ? t0 + t : ntok - 1); };
+#pragma unroll
+    for (int k = 0; k < 2 * G; ++k) {
+        const int slot = k * kThreads + tid, t = slot >> 4, p = (slot & 15) ^ (t & 15);
+        dma16(x.qs + tokc(t) * x.stride + c * 256 + p * 16, st.x + (k * kThreads + wave_first) * 16);
+    }
+    if (wave == 0) dma4(x.d + tokc(tid & (32 * G - 1)) * (x.stride / 32) + c, st.xd);
+}
+
+// A wave's operands for one super-block: 8 steps x (lo, hi) fragments and the 16 output rows' scales.
+struct MxA {
+    v4u f[16];
+    float4 d[4];
+};
+__device__ __forceinline__ void mx_load(MxA& a, const int8_t* qw, const float* dw, int lane) {
+    const auto* p = gmem(reinterpret_cast<const v4u*>(qw) + lane);
+#pragma unroll
+    for (int i = 0; i < 16; ++i) a.f[i] = p[i * 64];
+    const float* pd = dw + (lane >> 5) * 4;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) a.d[q] = gld4(pd + q * 8);
+}
+
+// acc[gb] (lane: token 32 gb + l % 32, rows 8 (i / 4) + 4 (l / 32) + i % 4) += this super-block's
+// terms, in the reference's term order (dot_q6_k_q8_k, src/quant.cpp:549-563: d_x d_w weighted).
+template <int G>
+__device__ __forceinline__ void mx_compute(uint32_t base, const MxA& a, float (&acc)[G][16]) {
+    const int lane = threadIdx.x & 63, h = lane >> 5;
+#pragma unroll
+    for (int gb = 0; gb < G; ++gb) {
+        const int t = 32 * gb + (lane & 31);
+        v4u b[8];
+#pragma unroll
+        for (int s = 0; s < 8; ++s) {
+            const int p = 2 * s + h;
+            b[s] = ds128v(base + offsetof(MxStage<G>, x) + (t * 16 + (p ^ (t & 15))) * 16);
+        }
+        uint32_t xd = ds32(base + offsetof(MxStage<G>, xd) + (G == 1 ? lane : t) * 4);
+        asm volatile("s_waitcnt lgkmcnt(0)"
+                     : "+v"(b[0]), "+v"(b[1]), "+v"(b[2]), "+v"(b[3]), "+v"(b[4]), "+v"(b[5]), "+v"(b[6]), "+v"(b[7]), "+v"(xd));
+        v16i lo = {}, hi = {};
+#pragma unroll
+        for (int s = 0; s < 8; ++s) {
+            lo = mfma32(a.f[2 * s], b[s], lo);
+            hi = mfma32(a.f[2 * s + 1], b[s], hi);
+        }
+        const float xg = __uint_as_float(xd);
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            const int weighted = lo[i] + 128 * hi[i];
+            const float4 dq = a.d[i >> 2];
+            const float d = (i & 3) == 0 ? dq.x : (i & 3) == 1 ? dq.y : (i & 3) == 2 ? dq.z : dq.w;
+            acc[gb][i] += xg * d * static_cast<float>(weighted);
+        }
+    }
+}
+
+// The expanded-Q6_K GEMM: a workgroup computes kMxRows rows (32 a wave) x 32 G tokens.  The
+// activations are staged in LDS (two stages, global_load_lds); each wave's weight
+// fragments are its own and come straight from global memory a super-block ahead.
+// Workgroup b runs on XCD b % 8; when the row tiles divide by 8, each XCD takes whole
+// row tiles (every token tile of them), so a row tile's weights are read through one L2.
+// s_waitcnt vmcnt(n), the other counters not waited: every vector memory load but the last n has landed.
+constexpr int mx_wait_imm(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8); }
+constexpr int kMxLoads = 20;  // global loads of one mx_load (16 fragments, 4 scale rows)
+#ifndef BRISK_MX_BUFS
+#define BRISK_MX_BUFS 3
+#endif
+constexpr int kMxBufs = BRISK_MX_BUFS;  // fragment buffers in flight (unified VGPR/AGPR file: one wave a SIMD)
+
+template <int MODE, int G>
+__global__ __launch_bounds__(kThreads) void k_mmx(MmArgs g) {
+    __shared__ MxStage<G> st[2];
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int nsb = static_cast<int>(g.m.cols / 256);
+    const int rtiles = static_cast<int>((g.m.rows + kMxRows - 1) / kMxRows), ttiles = (g.ntok + 32 * G - 1) / (32 * G);
+    const int b = blockIdx.x;
+    int rt, tt;
+    if (rtiles % 8 == 0) {
+        const int j = b >> 3;
+        rt = (b & 7) + 8 * (j / ttiles);
+        tt = j % ttiles;
+    } else {
+        rt = b % rtiles;
+        tt = b / rtiles;
+    }
+    const int t0 = tt * 32 * G;
+    const size_t rg = static_cast<size_t>(rt) * (kMxRows / 32) + wave;
+    const int8_t* qw = g.qx + rg * nsb * 16384;
+    const float* dw = g.qxd + rg * nsb * 32;
+    float acc[G][16];
+#pragma unroll
+    for (int gb = 0; gb < G; ++gb)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) acc[gb][i] = 0.0f;
+    if (MODE == kMmGated) exp_tab_fill();  // ordered before the epilogue by the loop's barriers
+    // kMxBufs fragment buffers: a super-block's fragments are loaded kMxBufs - 1 super-blocks
+    // ahead, its activations one ahead.  Each step issues stage (c + 1)'s copies, then the loads
+    // of super-block c + kMxBufs - 1, computes c, and waits for everything but the loads still
+    // ahead of c + 1 (so c + 1 has landed).  A bare barrier: __syncthreads' fence would wait for
+    // all of them.
+    MxA a[kMxBufs];
+    mx_copy<G>(st[0], g.x, g.ntok, t0, 0);
+#pragma unroll
+    for (int k = 0; k < kMxBufs - 1; ++k) {
+        const int n = min(k, nsb - 1);  // past the end: the last super-block again, so the count stays exact
+        mx_load(a[k], qw + static_cast<size_t>(n) * 16384, dw + n * 32, lane);
+    }
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    for (int c0 = 0; c0 < nsb; c0 += kMxBufs) {
+#pragma unroll
+        for (int k = 0; k < kMxBufs; ++k) {
+            const int c = c0 + k;
+            if (c >= nsb) break;
+            if (c + 1 < nsb) mx_copy<G>(st[(c + 1) & 1], g.x, g.ntok, t0, c + 1);
+            const int n = min(c + kMxBufs - 1, nsb - 1);
+            mx_load(a[(k + kMxBufs - 1) % kMxBufs], qw + static_cast<size_t>(n) * 16384, dw + n * 32, lane);
+            mx_compute<G>(lds_off(&st[c & 1]), a[k], acc);
+            __builtin_amdgcn_s_waitcnt(mx_wait_imm(kMxLoads * (kMxBufs - 2)));
+            __builtin_amdgcn_s_barrier();
+        }
+    }
+    __builtin_amdgcn_s_waitcnt(0);
+    const uint32_t rmax = g.m.rows - 1;
+#pragma unroll
+    for (int gb = 0; gb < G; ++gb) {
+        const int t = t0 + 32 * gb + (lane & 31);
+        if (t >= g.ntok) continue;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            const uint32_t r = static_cast<uint32_t>(rt) * kMxRows + wave * 32 + (i >> 2) * 8 + (lane >> 5) * 4 + (i & 3);
+            if (r > rmax) continue;
+            float* o = g.out + static_cast<size_t>(t) * g.ostride + r;
+            const float v = acc[gb][i];
+            if (MODE == kMmStore) {
+                *o = v;
+            } else if (MODE == kMmAdd) {
+                *o = *o + v;  // h += proj (src/model.cpp:1111, :1162)
+            } else {  // kMmGated: out holds the gate row, this is up
+                const float gv = *o;
+                if (g.relu2) {
+                    const float q = gv > 0.0f ? gv : 0.0f;
+                    *o = q * q * v;  // src/model.cpp:1134-1138
+                } else {
+                    *o = gv / (1.0f + ref_expf_s(-gv)) * v;  // src/kernels_f32.cpp:287-289
+                }
+            }
+        }
+    }
+}
+
 template <uint32_t T, int MODE, int G>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 8))) void k_mmk(MmArgs g) {
     __shared__ KqStage<T> st[2];
@@ -1609,6 +1828,11 @@ static hipError_t mm_dispatch(const MmArgs& g, hipStream_t s) {
             else hipLaunchKernelGGL((k_mmk<kQ4_K, MODE, 1>), kq_grid, dim3(kThreads), 0, s, g);
             break;
         case kQ6_K:
+            if (g.qx != nullptr) {
+                const int rtiles = static_cast<int>((g.m.rows + kMxRows - 1) / kMxRows);
+                hipLaunchKernelGGL((k_mmx<MODE, 1>), dim3(rtiles * ((g.ntok + 31) / 32)), dim3(kThreads), 0, s, g);
+                break;
+            }
             if (kq_g == 4) hipLaunchKernelGGL((k_mmk<kQ6_K, MODE, 4>), kq_grid, dim3(kThreads), 0, s, g);
             else if (kq_g == 2) hipLaunchKernelGGL((k_mmk<kQ6_K, MODE, 2>), kq_grid, dim3(kThreads), 0, s, g);
             else hipLaunchKernelGGL((k_mmk<kQ6_K, MODE, 1>), kq_grid, dim3(kThreads), 0, s, g);
@@ -1631,10 +1855,30 @@ hipError_t launch_mm(const MmArgs& g, int mode, hipStream_t s) {
             if (e != hipSuccess) return e;
             MmArgs up = g;
             up.m = g.m2;
+            up.qx = g.qx2;
+            up.qxd = g.qxd2;
             return mm_dispatch<kMmGated>(up, s);
         }
         default: return hipErrorInvalidValue;
     }
+}
+
+size_t q6x_bytes(uint32_t rows, uint32_t cols) {
+    const size_t rp = (rows + kMxRows - 1) / kMxRows * kMxRows;
+    return rp * cols * 2 + align256(rp * (cols / 256) * 4);
+}
+
+hipError_t launch_q6x_expand(const Packed& m, void* mem, const int8_t** q, const float** d, hipStream_t s) {
+    if (m.type != kQ6_K || m.cols % 256 != 0) return hipErrorInvalidValue;
+    const size_t rp = (m.rows + kMxRows - 1) / kMxRows * kMxRows;
+    int8_t* qq = static_cast<int8_t*>(mem);
+    float* dd = reinterpret_cast<float*>(qq + rp * m.cols * 2);
+    const size_t threads = rp / 32 * (m.cols / 256) * 512;
+    hipLaunchKernelGGL(k_q6x_expand, dim3(static_cast<unsigned>((threads + 255) / 256)), dim3(256), 0, s, m, qq, dd,
+                       static_cast<uint32_t>(rp / 32));
+    *q = qq;
+    *d = dd;
+    return hipGetLastError();
 }
 
 hipError_t launch_pre_quant(const float* x, int xstride, const float* w, float eps, int cols, int ntok, bool q8k, int bits,

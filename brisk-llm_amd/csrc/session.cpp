@@ -118,6 +118,7 @@ private:
 
 DeviceMatrix::~DeviceMatrix() {
     if (mem != nullptr) (void)hipFree(mem);
+    if (xmem != nullptr) (void)hipFree(xmem);
 }
 
 // The sizes the constructor (and the first prefill / eval_all) allocate, from the
@@ -160,6 +161,10 @@ brisk_hip_memory estimate_session(const brisk_hip_config& cfg, const brisk_hip_t
     const size_t T = Session::kPrefillTokens, widest = std::max(std::max(e, qd), ff), stride = (widest + 255) / 256 * 256;
     sc += T * (e + 2 * qd + 2 * kvd + ff) * 4 + T * stride * (1 + 4 / 32.0 + 4 / 16.0);  // prefill buffers
     sc += static_cast<size_t>(64) * cfg.vocab * 4;                         // eval_all logits
+    if (cfg.arch != BRISK_HIP_ARCH_GEMMA3 && cfg.arch != BRISK_HIP_ARCH_LFM2)  // the prefill's expanded Q6_K layer matrices
+        for (size_t i = 0; i < n; ++i)
+            if (tensors[i].type == BRISK_HIP_Q6_K && tensors[i].name != nullptr && std::strncmp(tensors[i].name, "blk.", 4) == 0)
+                sc += q6x_bytes(static_cast<uint32_t>(tensors[i].rows), static_cast<uint32_t>(tensors[i].cols));
     sc += staging + (64 << 10);                                            // load staging, small state
     {  // the token loop's block-major down copies and their term words (Session::setup_loop's push)
         size_t down_bytes = 0;
@@ -891,6 +896,14 @@ void Session::ensure_prefill() {
     pre_x_.qs = static_cast<int8_t*>(alloc(T * pre_x_.stride));
     pre_x_.d = static_cast<float*>(alloc(T * (pre_x_.stride / 32) * 4));
     pre_x_.bs = static_cast<int32_t*>(alloc(T * (pre_x_.stride / 16) * 4));
+    const char* qx = std::getenv("BRISK_HIP_PREFILL_Q6X");  // "0": Q6_K through the packed-plane GEMM
+    if (qx != nullptr && std::string(qx) == "0") return;
+    for (Layer& L : layers_)
+        for (DeviceMatrix* m : {&L.q, &L.k, &L.v, &L.o, &L.gate, &L.up, &L.down})
+            if (m->p.type == kQ6_K && m->xmem == nullptr) {
+                check(hipMalloc(&m->xmem, q6x_bytes(m->p.rows, m->p.cols)), "hipMalloc(expanded Q6_K)");
+                check(launch_q6x_expand(m->p, m->xmem, &m->xq, &m->xd, stream_), "expand Q6_K");
+            }
 }
 
 // T rows of x (rms_norm'd by w when given), quantised for `consumer`'s activation format.
@@ -913,11 +926,11 @@ void Session::prefill_layers(size_t pos0, int T) {
         g.ntok = T;
         // Q, K, V of attn_norm(h) (src/model.cpp:996-1015)
         prefill_quant(pre_h_, e, L.attn_norm, e, T, L.q);
-        g.m = L.q.p; g.out = pre_q_; g.ostride = qd;
+        g.m = L.q.p; g.qx = L.q.xq; g.qxd = L.q.xd; g.out = pre_q_; g.ostride = qd;
         check(launch_mm(g, kMmStore, stream_), "prefill q");
-        g.m = L.k.p; g.out = pre_k_; g.ostride = kvd;
+        g.m = L.k.p; g.qx = L.k.xq; g.qxd = L.k.xd; g.out = pre_k_; g.ostride = kvd;
         check(launch_mm(g, kMmStore, stream_), "prefill k");
-        g.m = L.v.p; g.out = pre_v_; g.ostride = kvd;
+        g.m = L.v.p; g.qx = L.v.xq; g.qxd = L.v.xd; g.out = pre_v_; g.ostride = kvd;
         check(launch_mm(g, kMmStore, stream_), "prefill v");
         // norms, RoPE, cache rows, attention (:1020-1093)
         PreAttnArgs pa{};
@@ -936,15 +949,15 @@ void Session::prefill_layers(size_t pos0, int T) {
         check(launch_pre_attention(pa, T, stream_), "prefill attention");
         // h += O (sub-normed) att (:1095-1111)
         prefill_quant(pre_att_, qd, L.attn_sub_norm, qd, T, L.o);
-        g.m = L.o.p; g.out = pre_h_; g.ostride = e;
+        g.m = L.o.p; g.qx = L.o.xq; g.qxd = L.o.xd; g.out = pre_h_; g.ostride = e;
         check(launch_mm(g, kMmAdd, stream_), "prefill o");
         // act = silu(gate) * up of ffn_norm(h) (:1111-1143)
         prefill_quant(pre_h_, e, L.ffn_norm, e, T, L.gate);
-        g.m = L.gate.p; g.m2 = L.up.p; g.out = pre_act_; g.ostride = ff; g.relu2 = cfg_.arch == BRISK_HIP_ARCH_BITNET;
+        g.m = L.gate.p; g.m2 = L.up.p; g.qx = L.gate.xq; g.qxd = L.gate.xd; g.qx2 = L.up.xq; g.qxd2 = L.up.xd; g.out = pre_act_; g.ostride = ff; g.relu2 = cfg_.arch == BRISK_HIP_ARCH_BITNET;
         check(launch_mm(g, kMmPair, stream_), "prefill gate/up");
         // h += down (sub-normed) act (:1144-1162)
         prefill_quant(pre_act_, ff, L.ffn_sub_norm, ff, T, L.down);
-        g.m = L.down.p; g.out = pre_h_; g.ostride = e; g.relu2 = 0;
+        g.m = L.down.p; g.qx = L.down.xq; g.qxd = L.down.xd; g.out = pre_h_; g.ostride = e; g.relu2 = 0;
         check(launch_mm(g, kMmAdd, stream_), "prefill down");
     }
 }

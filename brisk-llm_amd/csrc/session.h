@@ -23,10 +23,17 @@ struct Error : std::runtime_error {
 struct DeviceMatrix {
     Packed p{};
     void* mem = nullptr;
+    // Q6_K: the batched prefill's expanded planes (launch_q6x_expand), made at the first prefill
+    void* xmem = nullptr;
+    const int8_t* xq = nullptr;
+    const float* xd = nullptr;
     DeviceMatrix() = default;
     DeviceMatrix(const DeviceMatrix&) = delete;
     DeviceMatrix& operator=(const DeviceMatrix&) = delete;
-    DeviceMatrix(DeviceMatrix&& o) noexcept : p(o.p), mem(o.mem) { o.mem = nullptr; }
+    DeviceMatrix(DeviceMatrix&& o) noexcept : p(o.p), mem(o.mem), xmem(o.xmem), xq(o.xq), xd(o.xd) {
+        o.mem = nullptr;
+        o.xmem = nullptr;
+    }
     ~DeviceMatrix();
 };
 

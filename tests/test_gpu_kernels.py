@@ -110,7 +110,7 @@ CASES = [
     (Q4_0, 37, 1024), (Q4_0, 2048, 2048), (Q4_0, 1024, 3072), (Q4_0, 3072, 1024),
     (Q8_0, 37, 1024), (Q8_0, 2048, 6144), (Q8_0, 300, 2048),
     (Q4_K, 37, 1024), (Q4_K, 512, 2048), (Q4_K, 2048, 8192),
-    (Q6_K, 37, 1024), (Q6_K, 512, 2048), (Q6_K, 2048, 8192),
+    (Q6_K, 37, 1024), (Q6_K, 512, 2048), (Q6_K, 2048, 8192), (Q6_K, 200, 256), (Q6_K, 130, 512), (Q6_K, 300, 1280),
     (TQ2_0, 48, 1024), (TQ2_0, 640, 2560), (TQ2_0, 37, 2560),
     (Q4_1, 37, 1024), (Q4_1, 2048, 2048), (Q5_0, 37, 1024), (Q5_0, 1024, 3072),
     (Q5_K, 37, 1024), (Q5_K, 512, 2048), (Q5_K, 2048, 8192),
