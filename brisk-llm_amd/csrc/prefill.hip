@@ -914,14 +914,14 @@ struct MxStage {
     alignas(16) float xd[64];  // G = 1: lanes 32..63 hold a copy
 };
 
-template <int G>
+template <int G, int W>
 __device__ __forceinline__ void mx_copy(MxStage<G>& st, const ActPlanar& x, int ntok, int t0, int c) {
     const int tid = threadIdx.x, wave = tid >> 6, wave_first = tid & ~63;
     auto tokc = [&](int t) -> size_t { return static_cast<size_t>(t0 + t < ntok ? t0 + t : ntok - 1); };
 #pragma unroll
-    for (int k = 0; k < 2 * G; ++k) {
-        const int slot = k * kThreads + tid, t = slot >> 4, p = (slot & 15) ^ (t & 15);
-        dma16(x.qs + tokc(t) * x.stride + c * 256 + p * 16, st.x + (k * kThreads + wave_first) * 16);
+    for (int k = 0; k < 8 * G / W; ++k) {  // 32 G tokens x 16 pieces, over W waves
+        const int slot = k * 64 * W + tid, t = slot >> 4, p = (slot & 15) ^ (t & 15);
+        dma16(x.qs + tokc(t) * x.stride + c * 256 + p * 16, st.x + (k * 64 * W + wave_first) * 16);
     }
     if (wave == 0) dma4(x.d + tokc(tid & (32 * G - 1)) * (x.stride / 32) + c, st.xd);
 }
@@ -974,7 +974,7 @@ __device__ __forceinline__ void mx_compute(uint32_t base, const MxA& a, float (&
     }
 }
 
-// The expanded-Q6_K GEMM: a workgroup computes kMxRows rows (32 a wave) x 32 G tokens.  The
+// The expanded-Q6_K GEMM: a workgroup of W waves computes 32 W rows (32 a wave) x 32 G tokens.  The
 // activations are staged in LDS (two stages, global_load_lds); each wave's weight
 // fragments are its own and come straight from global memory a super-block ahead.
 // Workgroup b runs on XCD b % 8; when the row tiles divide by 8, each XCD takes whole
@@ -987,12 +987,12 @@ constexpr int kMxLoads = 20;  // global loads of one mx_load (16 fragments, 4 sc
 #endif
 constexpr int kMxBufs = BRISK_MX_BUFS;  // fragment buffers in flight (unified VGPR/AGPR file: one wave a SIMD)
 
-template <int MODE, int G>
-__global__ __launch_bounds__(kThreads) void k_mmx(MmArgs g) {
+template <int MODE, int G, int W>
+__global__ __launch_bounds__(64 * W) void k_mmx(MmArgs g) {
     __shared__ MxStage<G> st[2];
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int nsb = static_cast<int>(g.m.cols / 256);
-    const int rtiles = static_cast<int>((g.m.rows + kMxRows - 1) / kMxRows), ttiles = (g.ntok + 32 * G - 1) / (32 * G);
+    const int rtiles = static_cast<int>((g.m.rows + 32 * W - 1) / (32 * W)), ttiles = (g.ntok + 32 * G - 1) / (32 * G);
     const int b = blockIdx.x;
     int rt, tt;
     if (rtiles % 8 == 0) {
@@ -1004,7 +1004,7 @@ __global__ __launch_bounds__(kThreads) void k_mmx(MmArgs g) {
         tt = b / rtiles;
     }
     const int t0 = tt * 32 * G;
-    const size_t rg = static_cast<size_t>(rt) * (kMxRows / 32) + wave;
+    const size_t rg = static_cast<size_t>(rt) * W + wave;
     const int8_t* qw = g.qx + rg * nsb * 16384;
     const float* dw = g.qxd + rg * nsb * 32;
     float acc[G][16];
@@ -1019,7 +1019,7 @@ __global__ __launch_bounds__(kThreads) void k_mmx(MmArgs g) {
     // ahead of c + 1 (so c + 1 has landed).  A bare barrier: __syncthreads' fence would wait for
     // all of them.
     MxA a[kMxBufs];
-    mx_copy<G>(st[0], g.x, g.ntok, t0, 0);
+    mx_copy<G, W>(st[0], g.x, g.ntok, t0, 0);
 #pragma unroll
     for (int k = 0; k < kMxBufs - 1; ++k) {
         const int n = min(k, nsb - 1);  // past the end: the last super-block again, so the count stays exact
@@ -1032,7 +1032,7 @@ __global__ __launch_bounds__(kThreads) void k_mmx(MmArgs g) {
         for (int k = 0; k < kMxBufs; ++k) {
             const int c = c0 + k;
             if (c >= nsb) break;
-            if (c + 1 < nsb) mx_copy<G>(st[(c + 1) & 1], g.x, g.ntok, t0, c + 1);
+            if (c + 1 < nsb) mx_copy<G, W>(st[(c + 1) & 1], g.x, g.ntok, t0, c + 1);
             const int n = min(c + kMxBufs - 1, nsb - 1);
             mx_load(a[(k + kMxBufs - 1) % kMxBufs], qw + static_cast<size_t>(n) * 16384, dw + n * 32, lane);
             mx_compute<G>(lds_off(&st[c & 1]), a[k], acc);
@@ -1048,7 +1048,7 @@ __global__ __launch_bounds__(kThreads) void k_mmx(MmArgs g) {
         if (t >= g.ntok) continue;
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
-            const uint32_t r = static_cast<uint32_t>(rt) * kMxRows + wave * 32 + (i >> 2) * 8 + (lane >> 5) * 4 + (i & 3);
+            const uint32_t r = static_cast<uint32_t>(rt) * (32 * W) + wave * 32 + (i >> 2) * 8 + (lane >> 5) * 4 + (i & 3);
             if (r > rmax) continue;
             float* o = g.out + static_cast<size_t>(t) * g.ostride + r;
             const float v = acc[gb][i];
@@ -1829,8 +1829,12 @@ static hipError_t mm_dispatch(const MmArgs& g, hipStream_t s) {
             break;
         case kQ6_K:
             if (g.qx != nullptr) {
-                const int rtiles = static_cast<int>((g.m.rows + kMxRows - 1) / kMxRows);
-                hipLaunchKernelGGL((k_mmx<MODE, 1>), dim3(rtiles * ((g.ntok + 31) / 32)), dim3(kThreads), 0, s, g);
+                // 4 waves (128 rows) a workgroup, fewer where that leaves compute units without one
+                const int tt = (g.ntok + 31) / 32;
+                auto tiles = [&](int w) { return static_cast<int>((g.m.rows + 32 * w - 1) / (32 * w)) * tt; };
+                if (tiles(4) >= kKqCus) hipLaunchKernelGGL((k_mmx<MODE, 1, 4>), dim3(tiles(4)), dim3(256), 0, s, g);
+                else if (tiles(2) >= kKqCus) hipLaunchKernelGGL((k_mmx<MODE, 1, 2>), dim3(tiles(2)), dim3(128), 0, s, g);
+                else hipLaunchKernelGGL((k_mmx<MODE, 1, 1>), dim3(tiles(1)), dim3(64), 0, s, g);
                 break;
             }
             if (kq_g == 4) hipLaunchKernelGGL((k_mmk<kQ6_K, MODE, 4>), kq_grid, dim3(kThreads), 0, s, g);
