@@ -671,6 +671,17 @@ __device__ __forceinline__ void kq_f64_wait(KqF64& f) {
     asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(f.a), "+v"(f.b0), "+v"(f.b1), "+v"(f.b2), "+v"(f.b3));
 }
 
+// Each byte of q (0..15) times d (0..7), as two 16-bit lanes a dword (v_pk_mul_lo_u16, full rate,
+// where a 32-bit v_mul_lo_u32 is quarter rate): a byte's product is at most 105, so none carries.
+typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint32_t mul_bytes1(uint32_t q, u16x2 dd) {
+    return __builtin_bit_cast(uint32_t, __builtin_bit_cast(u16x2, q) * dd);
+}
+__device__ __forceinline__ v4u mul_bytes(const v4u& q, uint32_t d) {
+    const u16x2 dd = {static_cast<unsigned short>(d), static_cast<unsigned short>(d)};
+    return v4u{mul_bytes1(q.x, dd), mul_bytes1(q.y, dd), mul_bytes1(q.z, dd), mul_bytes1(q.w, dd)};
+}
+
 template <int G>
 __device__ __forceinline__ void kq_compute_fold(uint32_t base, MmAcc<G>& acc) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, tl = lane & 15, l16 = lane >> 4;
@@ -702,8 +713,8 @@ __device__ __forceinline__ void kq_compute_fold(uint32_t base, MmAcc<G>& acc) {
         const uint32_t mn = ((j < 4 ? scm.z : scm.w) >> (8 * (j & 3))) & 0xFF;
         const uint32_t dlo = sc & 7, dhi = sc >> 3, m4 = mn * 0x01010101u;
         const v4u qn = hi_nib ? ((cur.a >> 4) & 0x0F0F0F0Fu) : (cur.a & 0x0F0F0F0Fu);
-        const v4u qlo = qn * dlo;  // bytes 0..15 times 0..7: no carries between bytes
-        const v4u qhi = qn * dhi;
+        const v4u qlo = mul_bytes(qn, dlo);  // bytes 0..15 times 0..7: no carries between bytes
+        const v4u qhi = mul_bytes(qn, dhi);
         const v4u qmn = {m4, m4, m4, m4};
         const v4u bq[4] = {cur.b0, cur.b1, cur.b2, cur.b3};
 #pragma unroll
