@@ -27,6 +27,7 @@ struct MmArgs {
     float* out;      // out[t * ostride + r]
     int ostride;
     int relu2;       // kMmPair: BitNet's squared-ReLU gate instead of SiLU
+    int gelu;        // kMmPair: Gemma's GELU (tanh form) gate instead of SiLU
     // Q6_K: the expanded planes of m (and m2) from launch_q6x_expand, or null (the packed-plane GEMM)
     const int8_t* qx;
     const float* qxd;
@@ -62,7 +63,11 @@ hipError_t launch_mm(const MmArgs& g, int mode, hipStream_t s);
 hipError_t launch_pre_quant(const float* x, int xstride, const float* w, float eps, int cols, int ntok, bool q8k, int bits,
                             const ActPlanar& out, hipStream_t s);
 hipError_t launch_pre_planar(const void* xq, int cols, int ntok, bool q8k, const ActPlanar& out, hipStream_t s);
-hipError_t launch_pre_embed(const Packed& m, const int* seq, int pos0, int ntok, float* h, hipStream_t s);
+hipError_t launch_pre_embed(const Packed& m, const int* seq, int pos0, int ntok, float* h, float scale, hipStream_t s);
+// h[t] += rms_norm(p[t], w) for the ntok rows of n values (Gemma's post-norms)
+hipError_t launch_pre_post_add(float* h, const float* p, const float* w, float eps, int n, int ntok, hipStream_t s);
+// x[i] = cap tanh(x[i] / cap) (Gemma's final logit soft-capping)
+hipError_t launch_softcap(float* x, size_t n, float cap, hipStream_t s);
 hipError_t launch_pre_attention(const PreAttnArgs& p, int ntok, hipStream_t s);
 
 }  // namespace bh

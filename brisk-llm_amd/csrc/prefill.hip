@@ -517,6 +517,8 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 2))
                 if (g.relu2) {
                     const float q = gv > 0.0f ? gv : 0.0f;
                     *o = q * q * v;  // src/model.cpp:1134-1138
+                } else if (g.gelu) {
+                    *o = gelu_mul(gv, v);  // src/kernels_f32.cpp:291-296
                 } else {
                     *o = gv / (1.0f + ref_expf(-gv)) * v;  // src/kernels_f32.cpp:287-289
                 }
@@ -1072,6 +1074,8 @@ __global__ __launch_bounds__(64 * W) void k_mmx(MmArgs g) {
                 if (g.relu2) {
                     const float q = gv > 0.0f ? gv : 0.0f;
                     *o = q * q * v;  // src/model.cpp:1134-1138
+                } else if (g.gelu) {
+                    *o = gelu_mul(gv, v);  // src/kernels_f32.cpp:291-296
                 } else {
                     *o = gv / (1.0f + ref_expf_s(-gv)) * v;  // src/kernels_f32.cpp:287-289
                 }
@@ -1124,6 +1128,8 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 8))
                 if (g.relu2) {
                     const float q = gv > 0.0f ? gv : 0.0f;
                     *o = q * q * v;  // src/model.cpp:1134-1138
+                } else if (g.gelu) {
+                    *o = gelu_mul(gv, v);  // src/kernels_f32.cpp:291-296
                 } else {
                     *o = gv / (1.0f + ref_expf_s(-gv)) * v;  // src/kernels_f32.cpp:287-289
                 }
@@ -1135,11 +1141,32 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 8))
 // ---------------------------------------------------------------- per-token work
 
 // Embedding rows of seq[pos0 + t] (embedding_row, src/model.cpp:27-70).
-__global__ void k_pre_embed(Packed m, const int* __restrict__ seq, int pos0, float* __restrict__ h) {
+// Gemma's rows are then multiplied by sqrt(embd) (src/model.cpp:899-901; scale 1 elsewhere).
+__global__ void k_pre_embed(Packed m, const int* __restrict__ seq, int pos0, float* __restrict__ h, float scale) {
     const int t = blockIdx.x;
     const uint32_t tok = static_cast<uint32_t>(seq[pos0 + t]);
     float* row = h + static_cast<size_t>(t) * m.cols;
-    for (uint32_t e = threadIdx.x; e < m.cols; e += blockDim.x) row[e] = dequant_elem(m, tok, e);
+    for (uint32_t e = threadIdx.x; e < m.cols; e += blockDim.x) {
+        const float v = dequant_elem(m, tok, e);
+        row[e] = scale != 1.0f ? v * scale : v;
+    }
+}
+
+// h[t] += rms_norm(p[t], w) for every row t (src/model.cpp:1113-1121, :1153-1160): a workgroup a row.
+__global__ __launch_bounds__(kThreads) void k_pre_post_add(float* __restrict__ h, const float* __restrict__ p,
+                                                           const float* __restrict__ w, float eps, int n) {
+    __shared__ double red[4];
+    const size_t off = static_cast<size_t>(blockIdx.x) * n;
+    h += off;
+    p += off;
+    const float scale = rms_scale(block_sumsq(p, n, red), n, eps);
+    for (int i = threadIdx.x; i < n; i += kThreads) h[i] = h[i] + p[i] * scale * w[i];
+}
+
+// logits = cap * tanh(logits / cap) (src/model.cpp:1206-1208).
+__global__ void k_softcap(float* __restrict__ x, size_t n, float cap) {
+    const size_t i = static_cast<size_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (i < n) x[i] = cap * ref_tanhf(x[i] / cap);
 }
 
 // Q/K norms, RoPE, and the K/V cache rows of token t (grid: tokens x kv heads);
@@ -1197,7 +1224,16 @@ __global__ __launch_bounds__(kThreads) void k_pre_attn(PreAttnArgs p) {
     }
     __syncthreads();
     const PlainOut o{p.out + static_cast<size_t>(t) * p.qstride, nullptr, nullptr};
-    attn_exact(g, s, kv, pos + 1, o);
+    // a sliding layer sees positions start .. pos (src/model.cpp:1084-1085): its cache rows from start on
+    const int start = g.window > 0 && pos + 1 > g.window ? pos + 1 - g.window : 0;
+    if (start == 0) {
+        attn_exact(g, s, kv, pos + 1, o);
+        return;
+    }
+    AttnArgs gw = g;
+    gw.kcache += static_cast<size_t>(start) * hd;
+    gw.vcache += static_cast<size_t>(start) * hd;
+    attn_exact(gw, s, kv, pos + 1 - start, o);
 }
 
 // Attention of a block of tokens over one key/value head, in the reference's
@@ -1507,20 +1543,25 @@ __global__ __launch_bounds__(kThreads) void k_pre_attn_rows(PreAttnArgs p, int n
     }
     __syncthreads();
     // ---- softmax, a row a wave: max, e = expf(s - max), double sum, w = e * (float)(1 / sum)
+    // A sliding layer's row sees positions start .. Lr - 1 (src/model.cpp:1084-1088): the weights
+    // before start are set to zero, so the value sums below add +0 until start and then the
+    // same terms in the same order as from start.
     for (int row = wave; row < rows; row += kThreads / 64) {
         const int Lr = first + row / hpk + 1;
+        const int start = g.window > 0 && Lr > g.window ? Lr - g.window : 0;
         float* sc = s.sc + row * Ls;
         float m = -INFINITY;
-        for (int q = wl; q < Lr; q += 64) m = fmaxf(m, sc[q]);
+        for (int q = start + wl; q < Lr; q += 64) m = fmaxf(m, sc[q]);
         m = wave_max(m);
         double part = 0.0;
-        for (int q = wl; q < Lr; q += 64) {
+        for (int q = start + wl; q < Lr; q += 64) {
             const float e = ref_expf_s(sc[q] - m);
             sc[q] = e;
             part += static_cast<double>(e);
         }
         const float scale = static_cast<float>(1.0 / wave_sum(part));
-        for (int q = wl; q < Lr; q += 64) sc[q] *= scale;
+        for (int q = start + wl; q < Lr; q += 64) sc[q] *= scale;
+        for (int q = wl; q < start; q += 64) sc[q] = 0.0f;
     }
     __syncthreads();
     // ---- value sums in position order: lane = (dimension pair dp, rows rg, rg + RG, ...)
@@ -1909,9 +1950,21 @@ hipError_t launch_pre_planar(const void* xq, int cols, int ntok, bool q8k, const
     return hipGetLastError();
 }
 
-hipError_t launch_pre_embed(const Packed& m, const int* seq, int pos0, int ntok, float* h, hipStream_t s) {
+hipError_t launch_pre_embed(const Packed& m, const int* seq, int pos0, int ntok, float* h, float scale, hipStream_t s) {
     if (ntok <= 0) return hipSuccess;
-    hipLaunchKernelGGL(k_pre_embed, dim3(ntok), dim3(kThreads), 0, s, m, seq, pos0, h);
+    hipLaunchKernelGGL(k_pre_embed, dim3(ntok), dim3(kThreads), 0, s, m, seq, pos0, h, scale);
+    return hipGetLastError();
+}
+
+hipError_t launch_pre_post_add(float* h, const float* p, const float* w, float eps, int n, int ntok, hipStream_t s) {
+    if (ntok <= 0) return hipSuccess;
+    hipLaunchKernelGGL(k_pre_post_add, dim3(ntok), dim3(kThreads), 0, s, h, p, w, eps, n);
+    return hipGetLastError();
+}
+
+hipError_t launch_softcap(float* x, size_t n, float cap, hipStream_t s) {
+    if (n == 0) return hipSuccess;
+    hipLaunchKernelGGL(k_softcap, dim3(static_cast<unsigned>((n + 255) / 256)), dim3(256), 0, s, x, n, cap);
     return hipGetLastError();
 }
 
@@ -1925,7 +1978,7 @@ hipError_t launch_pre_attention(const PreAttnArgs& p, int ntok, hipStream_t s) {
     const int hpk = p.a.heads / p.a.kv_heads, hd = p.a.head_dim;
     const int L = p.pos0 + ntok;
     const bool fa_ok = pre_attn_mfma_fits(hpk, hd);
-    if (p.mfma && fa_ok && (ntok >= kFaMinTok || L * hpk > kExactScores)) {
+    if (p.mfma && p.a.window == 0 && fa_ok && (ntok >= kFaMinTok || L * hpk > kExactScores)) {
         const dim3 fgrid(((ntok + kFaRows / hpk - 1) / (kFaRows / hpk)) * p.a.kv_heads);
         if (hd == 64) hipLaunchKernelGGL(k_pre_attn_fa<64>, fgrid, dim3(kThreads), 0, s, p, ntok);
         else hipLaunchKernelGGL(k_pre_attn_fa<128>, fgrid, dim3(kThreads), 0, s, p, ntok);
@@ -1933,7 +1986,7 @@ hipError_t launch_pre_attention(const PreAttnArgs& p, int ntok, hipStream_t s) {
         const dim3 xgrid(((ntok + kPxRows / hpk - 1) / (kPxRows / hpk)) * p.a.kv_heads);
         if (hd == 64) hipLaunchKernelGGL((k_pre_attn_rows<64, kPxRows, kPaMaxL>), xgrid, dim3(kThreads), 0, s, p, ntok);
         else hipLaunchKernelGGL((k_pre_attn_rows<128, kPxRows, kPaMaxL>), xgrid, dim3(kThreads), 0, s, p, ntok);
-    } else if (hpk <= kPaRows && (p.a.head_dim == 32 || p.a.head_dim == 64 || p.a.head_dim == 128) &&
+    } else if (p.a.window == 0 && hpk <= kPaRows && (p.a.head_dim == 32 || p.a.head_dim == 64 || p.a.head_dim == 128) &&
         p.pos0 + ntok <= kPaMaxL) {
         const int tpb = kPaRows / hpk;
         hipLaunchKernelGGL(k_pre_attn_blk, dim3((ntok + tpb - 1) / tpb, p.a.kv_heads), dim3(kThreads), 0, s, p, ntok);

@@ -160,6 +160,7 @@ brisk_hip_memory estimate_session(const brisk_hip_config& cfg, const brisk_hip_t
            static_cast<size_t>(cfg.heads) * ctx) * 8;                      // hand-off words (with the spread scores)
     const size_t T = Session::kPrefillTokens, widest = std::max(std::max(e, qd), ff), stride = (widest + 255) / 256 * 256;
     sc += T * (e + 2 * qd + 2 * kvd + ff) * 4 + T * stride * (1 + 4 / 32.0 + 4 / 16.0);  // prefill buffers
+    if (cfg.arch == BRISK_HIP_ARCH_GEMMA3) sc += T * e * 4;                 // prefill projections before post-norms
     sc += static_cast<size_t>(64) * cfg.vocab * 4;                         // eval_all logits
     if (cfg.arch != BRISK_HIP_ARCH_GEMMA3 && cfg.arch != BRISK_HIP_ARCH_LFM2)  // the prefill's expanded Q6_K layer matrices
         for (size_t i = 0; i < n; ++i)
@@ -878,7 +879,9 @@ bool Session::use_prefill(size_t n) const {
     // the exact-order prefill attention keeps every score of a token's query heads in LDS
     const bool exact_fits = (position_ + n) * (cfg_.heads / cfg_.kv_heads) <= static_cast<size_t>(kExactScores);
     const bool mfma_fits = prefill_mfma_ && pre_attn_mfma_fits(static_cast<int>(cfg_.heads / cfg_.kv_heads), static_cast<int>(cfg_.head_dim));
-    return prefill_on_ && !gemma() && !lfm2() && n >= 2 && (exact_fits || mfma_fits);
+    // Gemma 3 (sliding layers, post-norms, GELU, soft-capped logits) takes the exact attention only
+    if (gemma()) return prefill_on_ && n >= 2 && exact_fits && cfg_.head_dim <= 128;
+    return prefill_on_ && !lfm2() && n >= 2 && (exact_fits || mfma_fits);
 }
 
 void Session::ensure_prefill() {
@@ -891,6 +894,7 @@ void Session::ensure_prefill() {
     pre_v_ = static_cast<float*>(alloc(T * kvd * 4));
     pre_att_ = static_cast<float*>(alloc(T * qd * 4));
     pre_act_ = static_cast<float*>(alloc(T * ff * 4));
+    if (gemma()) pre_proj_ = static_cast<float*>(alloc(T * e * 4));  // projections before their post-norms
     const size_t widest = std::max(std::max(e, qd), ff);
     pre_x_.stride = static_cast<int>((widest + 255) / 256 * 256);
     pre_x_.qs = static_cast<int8_t*>(alloc(T * pre_x_.stride));
@@ -918,7 +922,7 @@ void Session::prefill_quant(const float* x, int xstride, const float* w, int col
 void Session::prefill_layers(size_t pos0, int T) {
     const int e = static_cast<int>(cfg_.embd), qd = static_cast<int>(cfg_.heads * cfg_.head_dim),
               kvd = static_cast<int>(cfg_.kv_heads * cfg_.head_dim), ff = static_cast<int>(cfg_.ff);
-    check(launch_pre_embed(embd_.p, seq_, static_cast<int>(pos0), T, pre_h_, stream_), "prefill embed");
+    check(launch_pre_embed(embd_.p, seq_, static_cast<int>(pos0), T, pre_h_, embd_scale_, stream_), "prefill embed");
     for (uint32_t l = 0; l < cfg_.layers; ++l) {
         const Layer& L = layers_[l];
         MmArgs g{};
@@ -934,7 +938,9 @@ void Session::prefill_layers(size_t pos0, int T) {
         check(launch_mm(g, kMmStore, stream_), "prefill v");
         // norms, RoPE, cache rows, attention (:1020-1093)
         PreAttnArgs pa{};
-        pa.a.qnorm = L.q_norm; pa.a.knorm = L.k_norm; pa.a.rope = L.rope ? rope_ : nullptr; pa.a.eps = cfg_.rms_epsilon;
+        pa.a.qnorm = L.q_norm; pa.a.knorm = L.k_norm; pa.a.eps = cfg_.rms_epsilon;
+        pa.a.rope = !L.rope ? nullptr : L.slides ? rope_local_ : rope_;  // Gemma 3's sliding layers: the local base
+        pa.a.window = L.slides ? static_cast<int>(cfg_.sliding_window) : 0;
         pa.a.rope_dim = rope_dim_;
         pa.a.qbias = L.q_bias; pa.a.kbias = L.k_bias; pa.a.vbias = L.v_bias;
         pa.a.neox = neox();
@@ -949,16 +955,22 @@ void Session::prefill_layers(size_t pos0, int T) {
         check(launch_pre_attention(pa, T, stream_), "prefill attention");
         // h += O (sub-normed) att (:1095-1111)
         prefill_quant(pre_att_, qd, L.attn_sub_norm, qd, T, L.o);
-        g.m = L.o.p; g.qx = L.o.xq; g.qxd = L.o.xd; g.out = pre_h_; g.ostride = e;
-        check(launch_mm(g, kMmAdd, stream_), "prefill o");
+        g.m = L.o.p; g.qx = L.o.xq; g.qxd = L.o.xd; g.out = L.attn_post_norm ? pre_proj_ : pre_h_; g.ostride = e;
+        check(launch_mm(g, L.attn_post_norm ? kMmStore : kMmAdd, stream_), "prefill o");
+        if (L.attn_post_norm)  // h += rms_norm(O att, post_attention_norm) (:1113-1121)
+            check(launch_pre_post_add(pre_h_, pre_proj_, L.attn_post_norm, cfg_.rms_epsilon, e, T, stream_), "prefill post norm");
         // act = silu(gate) * up of ffn_norm(h) (:1111-1143)
         prefill_quant(pre_h_, e, L.ffn_norm, e, T, L.gate);
         g.m = L.gate.p; g.m2 = L.up.p; g.qx = L.gate.xq; g.qxd = L.gate.xd; g.qx2 = L.up.xq; g.qxd2 = L.up.xd; g.out = pre_act_; g.ostride = ff; g.relu2 = cfg_.arch == BRISK_HIP_ARCH_BITNET;
+        g.gelu = gemma();
         check(launch_mm(g, kMmPair, stream_), "prefill gate/up");
         // h += down (sub-normed) act (:1144-1162)
         prefill_quant(pre_act_, ff, L.ffn_sub_norm, ff, T, L.down);
-        g.m = L.down.p; g.qx = L.down.xq; g.qxd = L.down.xd; g.out = pre_h_; g.ostride = e; g.relu2 = 0;
-        check(launch_mm(g, kMmAdd, stream_), "prefill down");
+        g.m = L.down.p; g.qx = L.down.xq; g.qxd = L.down.xd; g.out = L.ffn_post_norm ? pre_proj_ : pre_h_; g.ostride = e;
+        g.relu2 = 0; g.gelu = 0;
+        check(launch_mm(g, L.ffn_post_norm ? kMmStore : kMmAdd, stream_), "prefill down");
+        if (L.ffn_post_norm)  // h += rms_norm(down act, post_ffw_norm) (:1153-1160)
+            check(launch_pre_post_add(pre_h_, pre_proj_, L.ffn_post_norm, cfg_.rms_epsilon, e, T, stream_), "prefill post norm");
     }
 }
 
@@ -975,7 +987,7 @@ void Session::eval(const int32_t* tokens, size_t n, float* logits) {
         }
         HeadArgs ha{};  // output_norm + output rows of the last token (src/model.cpp:1195-1205)
         ha.m = out_->p; ha.x = pre_h_ + static_cast<size_t>(T - 1) * cfg_.embd; ha.normw = out_norm_;
-        ha.eps = cfg_.rms_epsilon; ha.logits = logits_; ha.key = key_;
+        ha.eps = cfg_.rms_epsilon; ha.logits = logits_; ha.key = key_; ha.softcap = gemma() ? cfg_.final_softcap : 0.0f;
         check(launch_head(ha, stream_), "output");
         finish();
         if (logits != nullptr)
@@ -1015,9 +1027,11 @@ void Session::eval_all(const int32_t* tokens, size_t n, float* logits) {
         MmArgs g{};
         g.m = out_->p; g.x = pre_x_; g.ntok = T; g.out = all_logits_; g.ostride = static_cast<int>(cfg_.vocab);
         check(launch_mm(g, kMmStore, stream_), "eval_all output");
+        if (gemma() && cfg_.final_softcap != 0.0f)  // every row's logits soft-capped (src/model.cpp:1206-1208)
+            check(launch_softcap(all_logits_, n * cfg_.vocab, cfg_.final_softcap, stream_), "eval_all softcap");
         HeadArgs ha{};
         ha.m = out_->p; ha.x = pre_h_ + static_cast<size_t>(T - 1) * cfg_.embd; ha.normw = out_norm_;
-        ha.eps = cfg_.rms_epsilon; ha.logits = nullptr; ha.key = key_;
+        ha.eps = cfg_.rms_epsilon; ha.logits = nullptr; ha.key = key_; ha.softcap = gemma() ? cfg_.final_softcap : 0.0f;
         check(launch_head(ha, stream_), "output");
         finish();
         check(hipMemcpyAsync(logits, all_logits_, n * cfg_.vocab * 4, hipMemcpyDeviceToHost, stream_), "hipMemcpy(logits)");

@@ -150,6 +150,7 @@ private:
     bool prefill_mfma_ = false;    // BRISK_HIP_PREFILL_ATTN=mfma
     bool prefill_legacy_ = false;  // BRISK_HIP_PREFILL_ATTN=staged
     float *pre_h_ = nullptr, *pre_q_ = nullptr, *pre_k_ = nullptr, *pre_v_ = nullptr, *pre_att_ = nullptr, *pre_act_ = nullptr;
+    float* pre_proj_ = nullptr;  // Gemma: a projection's rows before their post-norm
     ActPlanar pre_x_{};
     float* all_logits_ = nullptr;  // eval_all's [64][vocab] logits, allocated on first use
     hipGraphExec_t graph_layers_ = nullptr, graph_full_ = nullptr;

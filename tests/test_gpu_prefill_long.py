@@ -2,7 +2,9 @@
 
 Default path: the exact-order attention kernels (k_pre_attn_blk up to 512
 positions, k_pre_attn beyond), so logits are bit-identical to the oracle's at
-every prompt length, also for a prompt that continues an existing context.
+every prompt length, also for a prompt that continues an existing context.  Gemma 3
+runs here too: its sliding layers see the last `sliding_window` positions
+(src/model.cpp:1084-1088), its projections pass their post-norms, its gate is GELU.
 
 Opt-in path (BRISK_HIP_PREFILL_ATTN=mfma): from 64 tokens on, the causal
 attention runs flash style on v_mfma_f32_16x16x32_f16 with hi/lo f16 operands
@@ -43,9 +45,6 @@ def _session(src, ctx, mfma):
 @pytest.mark.parametrize("first,second", [(64, 0), (200, 0), (30, 150), (700, 0)], ids=["64", "200", "30+150", "700"])
 def test_long_prompt_exact(name, first, second):
     f, cfg, table = model.load(synth.model_path(name))
-    if cfg.arch == model.ARCH_GEMMA3 and first + second > 512:
-        pytest.skip("Gemma 3 evaluates prompts token by token; its attention over more positions than the exact "
-                    "form holds is the split-K one, held to tolerance in test_gpu_long_context.py")
     ctx = first + second + 16
     print(f"[prefill] {name}: {first} + {second} prompt ids", flush=True)
     prompt = synth.prompt_ids(first + second, cfg.vocab, seed=11)
