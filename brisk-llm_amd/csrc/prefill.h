@@ -66,6 +66,9 @@ hipError_t launch_pre_planar(const void* xq, int cols, int ntok, bool q8k, const
 hipError_t launch_pre_embed(const Packed& m, const int* seq, int pos0, int ntok, float* h, float scale, hipStream_t s);
 // h[t] += rms_norm(p[t], w) for the ntok rows of n values (Gemma's post-norms)
 hipError_t launch_pre_post_add(float* h, const float* p, const float* w, float eps, int n, int ntok, hipStream_t s);
+// LFM2's short convolution for ntok tokens at positions pos0 ..: bcx [ntok][3 n] in, out [ntok][n]
+hipError_t launch_pre_conv(const float* bcx, uint16_t* cache, const float* w, int taps, int pos0, int n, int ntok, float* out,
+                           hipStream_t s);
 // x[i] = cap tanh(x[i] / cap) (Gemma's final logit soft-capping)
 hipError_t launch_softcap(float* x, size_t n, float cap, hipStream_t s);
 hipError_t launch_pre_attention(const PreAttnArgs& p, int ntok, hipStream_t s);

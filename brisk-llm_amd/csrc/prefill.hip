@@ -1163,6 +1163,29 @@ __global__ __launch_bounds__(kThreads) void k_pre_post_add(float* __restrict__ h
     for (int i = threadIdx.x; i < n; i += kThreads) h[i] = h[i] + p[i] * scale * w[i];
 }
 
+// LFM2 short convolution over ntok tokens at positions pos0 .. (src/model.cpp:935-969): for each
+// token in order, bx = b * x is stored (fp16) at its position, then out = c * sum over the last
+// `taps` positions, oldest first, of w[d][k] * bx (positions before 0 are zero state).  A thread
+// a channel walks the tokens in order, so each bx it reads was stored before (by itself or by an
+// earlier call).  bcx rows are [b | c | x], 3 n values each.
+__global__ __launch_bounds__(kThreads) void k_pre_conv(const float* __restrict__ bcx, uint16_t* __restrict__ cache,
+                                                       const float* __restrict__ w, int taps, int pos0, int n, int ntok,
+                                                       float* __restrict__ out) {
+    const int d = blockIdx.x * kThreads + threadIdx.x;
+    if (d >= n) return;
+    for (int t = 0; t < ntok; ++t) {
+        const float* r = bcx + static_cast<size_t>(t) * 3 * n;
+        const int pos = pos0 + t;
+        cache[static_cast<size_t>(pos) * n + d] = f2h(r[2 * n + d] * r[d]);
+        float acc = 0.0f;
+        for (int k = 0; k < taps; ++k) {
+            if (pos + k + 1 < taps) continue;
+            acc += w[d * taps + k] * h2f(cache[static_cast<size_t>(pos + k + 1 - taps) * n + d]);
+        }
+        out[static_cast<size_t>(t) * n + d] = acc * r[n + d];
+    }
+}
+
 // logits = cap * tanh(logits / cap) (src/model.cpp:1206-1208).
 __global__ void k_softcap(float* __restrict__ x, size_t n, float cap) {
     const size_t i = static_cast<size_t>(blockIdx.x) * blockDim.x + threadIdx.x;
@@ -1959,6 +1982,14 @@ hipError_t launch_pre_embed(const Packed& m, const int* seq, int pos0, int ntok,
 hipError_t launch_pre_post_add(float* h, const float* p, const float* w, float eps, int n, int ntok, hipStream_t s) {
     if (ntok <= 0) return hipSuccess;
     hipLaunchKernelGGL(k_pre_post_add, dim3(ntok), dim3(kThreads), 0, s, h, p, w, eps, n);
+    return hipGetLastError();
+}
+
+hipError_t launch_pre_conv(const float* bcx, uint16_t* cache, const float* w, int taps, int pos0, int n, int ntok, float* out,
+                           hipStream_t s) {
+    if (ntok <= 0) return hipSuccess;
+    hipLaunchKernelGGL(k_pre_conv, dim3(static_cast<unsigned>((n + kThreads - 1) / kThreads)), dim3(kThreads), 0, s, bcx, cache,
+                       w, taps, pos0, n, ntok, out);
     return hipGetLastError();
 }
 

@@ -160,7 +160,8 @@ brisk_hip_memory estimate_session(const brisk_hip_config& cfg, const brisk_hip_t
            static_cast<size_t>(cfg.heads) * ctx) * 8;                      // hand-off words (with the spread scores)
     const size_t T = Session::kPrefillTokens, widest = std::max(std::max(e, qd), ff), stride = (widest + 255) / 256 * 256;
     sc += T * (e + 2 * qd + 2 * kvd + ff) * 4 + T * stride * (1 + 4 / 32.0 + 4 / 16.0);  // prefill buffers
-    if (cfg.arch == BRISK_HIP_ARCH_GEMMA3) sc += T * e * 4;                 // prefill projections before post-norms
+    if (cfg.arch == BRISK_HIP_ARCH_GEMMA3 || cfg.arch == BRISK_HIP_ARCH_LFM2) sc += T * e * 4;  // post-norm inputs, conv outputs
+    if (cfg.arch == BRISK_HIP_ARCH_LFM2) sc += T * 3 * e * 4;                                   // prefill conv rows
     sc += static_cast<size_t>(64) * cfg.vocab * 4;                         // eval_all logits
     if (cfg.arch != BRISK_HIP_ARCH_GEMMA3 && cfg.arch != BRISK_HIP_ARCH_LFM2)  // the prefill's expanded Q6_K layer matrices
         for (size_t i = 0; i < n; ++i)
@@ -879,9 +880,10 @@ bool Session::use_prefill(size_t n) const {
     // the exact-order prefill attention keeps every score of a token's query heads in LDS
     const bool exact_fits = (position_ + n) * (cfg_.heads / cfg_.kv_heads) <= static_cast<size_t>(kExactScores);
     const bool mfma_fits = prefill_mfma_ && pre_attn_mfma_fits(static_cast<int>(cfg_.heads / cfg_.kv_heads), static_cast<int>(cfg_.head_dim));
-    // Gemma 3 (sliding layers, post-norms, GELU, soft-capped logits) takes the exact attention only
-    if (gemma()) return prefill_on_ && n >= 2 && exact_fits && cfg_.head_dim <= 128;
-    return prefill_on_ && !lfm2() && n >= 2 && (exact_fits || mfma_fits);
+    // Gemma 3 (sliding layers, post-norms, GELU, soft-capped logits) and LFM2 (short convolutions)
+    // take the exact attention only
+    if (gemma() || lfm2()) return prefill_on_ && n >= 2 && exact_fits && cfg_.head_dim <= 128;
+    return prefill_on_ && n >= 2 && (exact_fits || mfma_fits);
 }
 
 void Session::ensure_prefill() {
@@ -894,7 +896,8 @@ void Session::ensure_prefill() {
     pre_v_ = static_cast<float*>(alloc(T * kvd * 4));
     pre_att_ = static_cast<float*>(alloc(T * qd * 4));
     pre_act_ = static_cast<float*>(alloc(T * ff * 4));
-    if (gemma()) pre_proj_ = static_cast<float*>(alloc(T * e * 4));  // projections before their post-norms
+    if (gemma() || lfm2()) pre_proj_ = static_cast<float*>(alloc(T * e * 4));  // post-norm inputs; conv outputs
+    if (lfm2()) pre_conv_ = static_cast<float*>(alloc(T * 3 * e * 4));           // LFM2's [b | c | x] rows
     const size_t widest = std::max(std::max(e, qd), ff);
     pre_x_.stride = static_cast<int>((widest + 255) / 256 * 256);
     pre_x_.qs = static_cast<int8_t*>(alloc(T * pre_x_.stride));
@@ -903,7 +906,7 @@ void Session::ensure_prefill() {
     const char* qx = std::getenv("BRISK_HIP_PREFILL_Q6X");  // "0": Q6_K through the packed-plane GEMM
     if (qx != nullptr && std::string(qx) == "0") return;
     for (Layer& L : layers_)
-        for (DeviceMatrix* m : {&L.q, &L.k, &L.v, &L.o, &L.gate, &L.up, &L.down})
+        for (DeviceMatrix* m : {&L.q, &L.k, &L.v, &L.o, &L.gate, &L.up, &L.down, &L.conv_in, &L.conv_out})
             if (m->p.type == kQ6_K && m->xmem == nullptr) {
                 check(hipMalloc(&m->xmem, q6x_bytes(m->p.rows, m->p.cols)), "hipMalloc(expanded Q6_K)");
                 check(launch_q6x_expand(m->p, m->xmem, &m->xq, &m->xd, stream_), "expand Q6_K");
@@ -928,37 +931,48 @@ void Session::prefill_layers(size_t pos0, int T) {
         MmArgs g{};
         g.x = pre_x_;
         g.ntok = T;
-        // Q, K, V of attn_norm(h) (src/model.cpp:996-1015)
-        prefill_quant(pre_h_, e, L.attn_norm, e, T, L.q);
-        g.m = L.q.p; g.qx = L.q.xq; g.qxd = L.q.xd; g.out = pre_q_; g.ostride = qd;
-        check(launch_mm(g, kMmStore, stream_), "prefill q");
-        g.m = L.k.p; g.qx = L.k.xq; g.qxd = L.k.xd; g.out = pre_k_; g.ostride = kvd;
-        check(launch_mm(g, kMmStore, stream_), "prefill k");
-        g.m = L.v.p; g.qx = L.v.xq; g.qxd = L.v.xd; g.out = pre_v_; g.ostride = kvd;
-        check(launch_mm(g, kMmStore, stream_), "prefill v");
-        // norms, RoPE, cache rows, attention (:1020-1093)
-        PreAttnArgs pa{};
-        pa.a.qnorm = L.q_norm; pa.a.knorm = L.k_norm; pa.a.eps = cfg_.rms_epsilon;
-        pa.a.rope = !L.rope ? nullptr : L.slides ? rope_local_ : rope_;  // Gemma 3's sliding layers: the local base
-        pa.a.window = L.slides ? static_cast<int>(cfg_.sliding_window) : 0;
-        pa.a.rope_dim = rope_dim_;
-        pa.a.qbias = L.q_bias; pa.a.kbias = L.k_bias; pa.a.vbias = L.v_bias;
-        pa.a.neox = neox();
-        pa.a.kcache = kcache_[l]; pa.a.vcache = vcache_[l];
-        pa.a.ctx = static_cast<int>(max_ctx_); pa.a.head_dim = static_cast<int>(cfg_.head_dim);
-        pa.a.heads = static_cast<int>(cfg_.heads); pa.a.kv_heads = static_cast<int>(cfg_.kv_heads);
-        pa.a.scale = 1.0f / std::sqrt(static_cast<float>(cfg_.head_dim));  // src/model.cpp:978
-        pa.q = pre_q_; pa.k = pre_k_; pa.v = pre_v_; pa.out = pre_att_;
-        pa.qstride = qd; pa.kvstride = kvd; pa.pos0 = static_cast<int>(pos0);
-        pa.mfma = prefill_mfma_ ? 1 : 0;
-        pa.legacy = prefill_legacy_ ? 1 : 0;
-        check(launch_pre_attention(pa, T, stream_), "prefill attention");
-        // h += O (sub-normed) att (:1095-1111)
-        prefill_quant(pre_att_, qd, L.attn_sub_norm, qd, T, L.o);
-        g.m = L.o.p; g.qx = L.o.xq; g.qxd = L.o.xd; g.out = L.attn_post_norm ? pre_proj_ : pre_h_; g.ostride = e;
-        check(launch_mm(g, L.attn_post_norm ? kMmStore : kMmAdd, stream_), "prefill o");
-        if (L.attn_post_norm)  // h += rms_norm(O att, post_attention_norm) (:1113-1121)
-            check(launch_pre_post_add(pre_h_, pre_proj_, L.attn_post_norm, cfg_.rms_epsilon, e, T, stream_), "prefill post norm");
+        if (L.conv_w != nullptr) {  // LFM2 short convolution in place of attention (src/model.cpp:935-969)
+            prefill_quant(pre_h_, e, L.attn_norm, e, T, L.conv_in);
+            g.m = L.conv_in.p; g.qx = L.conv_in.xq; g.qxd = L.conv_in.xd; g.out = pre_conv_; g.ostride = 3 * e;
+            check(launch_mm(g, kMmStore, stream_), "prefill conv in_proj");
+            check(launch_pre_conv(pre_conv_, L.conv_cache, L.conv_w, static_cast<int>(cfg_.conv_taps), static_cast<int>(pos0), e, T,
+                                  pre_proj_, stream_), "prefill conv");
+            prefill_quant(pre_proj_, e, nullptr, e, T, L.conv_out);
+            g.m = L.conv_out.p; g.qx = L.conv_out.xq; g.qxd = L.conv_out.xd; g.out = pre_h_; g.ostride = e;
+            check(launch_mm(g, kMmAdd, stream_), "prefill conv out_proj");
+        } else {
+            // Q, K, V of attn_norm(h) (src/model.cpp:996-1015)
+            prefill_quant(pre_h_, e, L.attn_norm, e, T, L.q);
+            g.m = L.q.p; g.qx = L.q.xq; g.qxd = L.q.xd; g.out = pre_q_; g.ostride = qd;
+            check(launch_mm(g, kMmStore, stream_), "prefill q");
+            g.m = L.k.p; g.qx = L.k.xq; g.qxd = L.k.xd; g.out = pre_k_; g.ostride = kvd;
+            check(launch_mm(g, kMmStore, stream_), "prefill k");
+            g.m = L.v.p; g.qx = L.v.xq; g.qxd = L.v.xd; g.out = pre_v_; g.ostride = kvd;
+            check(launch_mm(g, kMmStore, stream_), "prefill v");
+            // norms, RoPE, cache rows, attention (:1020-1093)
+            PreAttnArgs pa{};
+            pa.a.qnorm = L.q_norm; pa.a.knorm = L.k_norm; pa.a.eps = cfg_.rms_epsilon;
+            pa.a.rope = !L.rope ? nullptr : L.slides ? rope_local_ : rope_;  // Gemma 3's sliding layers: the local base
+            pa.a.window = L.slides ? static_cast<int>(cfg_.sliding_window) : 0;
+            pa.a.rope_dim = L.slides ? static_cast<int>(cfg_.head_dim) : rope_dim_;
+            pa.a.qbias = L.q_bias; pa.a.kbias = L.k_bias; pa.a.vbias = L.v_bias;
+            pa.a.neox = neox();
+            pa.a.kcache = kcache_[l]; pa.a.vcache = vcache_[l];
+            pa.a.ctx = static_cast<int>(max_ctx_); pa.a.head_dim = static_cast<int>(cfg_.head_dim);
+            pa.a.heads = static_cast<int>(cfg_.heads); pa.a.kv_heads = static_cast<int>(cfg_.kv_heads);
+            pa.a.scale = 1.0f / std::sqrt(static_cast<float>(cfg_.head_dim));  // src/model.cpp:978
+            pa.q = pre_q_; pa.k = pre_k_; pa.v = pre_v_; pa.out = pre_att_;
+            pa.qstride = qd; pa.kvstride = kvd; pa.pos0 = static_cast<int>(pos0);
+            pa.mfma = prefill_mfma_ ? 1 : 0;
+            pa.legacy = prefill_legacy_ ? 1 : 0;
+            check(launch_pre_attention(pa, T, stream_), "prefill attention");
+            // h += O (sub-normed) att (:1095-1111)
+            prefill_quant(pre_att_, qd, L.attn_sub_norm, qd, T, L.o);
+            g.m = L.o.p; g.qx = L.o.xq; g.qxd = L.o.xd; g.out = L.attn_post_norm ? pre_proj_ : pre_h_; g.ostride = e;
+            check(launch_mm(g, L.attn_post_norm ? kMmStore : kMmAdd, stream_), "prefill o");
+            if (L.attn_post_norm)  // h += rms_norm(O att, post_attention_norm) (:1113-1121)
+                check(launch_pre_post_add(pre_h_, pre_proj_, L.attn_post_norm, cfg_.rms_epsilon, e, T, stream_), "prefill post norm");
+        }
         // act = silu(gate) * up of ffn_norm(h) (:1111-1143)
         prefill_quant(pre_h_, e, L.ffn_norm, e, T, L.gate);
         g.m = L.gate.p; g.m2 = L.up.p; g.qx = L.gate.xq; g.qxd = L.gate.xd; g.qx2 = L.up.xq; g.qxd2 = L.up.xd; g.out = pre_act_; g.ostride = ff; g.relu2 = cfg_.arch == BRISK_HIP_ARCH_BITNET;

@@ -150,7 +150,8 @@ private:
     bool prefill_mfma_ = false;    // BRISK_HIP_PREFILL_ATTN=mfma
     bool prefill_legacy_ = false;  // BRISK_HIP_PREFILL_ATTN=staged
     float *pre_h_ = nullptr, *pre_q_ = nullptr, *pre_k_ = nullptr, *pre_v_ = nullptr, *pre_att_ = nullptr, *pre_act_ = nullptr;
-    float* pre_proj_ = nullptr;  // Gemma: a projection's rows before their post-norm
+    float* pre_proj_ = nullptr;  // Gemma: a projection's rows before their post-norm; LFM2: conv outputs
+    float* pre_conv_ = nullptr;  // LFM2: in_proj rows [b | c | x]
     ActPlanar pre_x_{};
     float* all_logits_ = nullptr;  // eval_all's [64][vocab] logits, allocated on first use
     hipGraphExec_t graph_layers_ = nullptr, graph_full_ = nullptr;
