@@ -156,8 +156,8 @@ int brisk_hip_matmul(int type, int flags, const void* packed, size_t rows, size_
         void* mem = nullptr;
         const size_t qb = n * static_cast<size_t>(stride), db = n * static_cast<size_t>(stride / 32) * 4,
                      bb = n * static_cast<size_t>(stride / 16) * 4;
-        // a Q6_K matrix is expanded there too, as a session's prefill holds it (launch_q6x_expand)
-        const size_t xb = p.type == bh::kQ6_K ? bh::q6x_bytes(p.rows, p.cols) : 0;
+        // a matrix the session's prefill holds expanded is expanded there too (launch_mx_expand)
+        const size_t xb = bh::mx_expanded(p.type) ? bh::mx_bytes(p.type, p.rows, p.cols) : 0;
         const size_t ab = bh::align256(qb + db + bb);
         hip_check(hipMalloc(&mem, ab + xb), "hipMalloc");
         x.qs = static_cast<int8_t*>(mem);
@@ -165,7 +165,11 @@ int brisk_hip_matmul(int type, int flags, const void* packed, size_t rows, size_
         x.bs = reinterpret_cast<int32_t*>(static_cast<char*>(mem) + qb + db);
         bh::MmArgs g{};
         hipError_t e = bh::launch_pre_planar(xq, static_cast<int>(cols), static_cast<int>(n), bh::takes_q8_k(p.type), x, st);
-        if (e == hipSuccess && xb != 0) e = bh::launch_q6x_expand(p, static_cast<char*>(mem) + ab, &g.qx, &g.qxd, st);
+        if (e == hipSuccess && xb != 0) {
+            bh::MxPlanes xp{};
+            e = bh::launch_mx_expand(p, static_cast<char*>(mem) + ab, &xp, st);
+            g.qx = xp.q; g.qxd = xp.d; g.qxm = xp.mn;
+        }
         if (e == hipSuccess) {
             g.m = p; g.x = x; g.ntok = static_cast<int>(n); g.out = out; g.ostride = static_cast<int>(out_stride);
             e = bh::launch_mm(g, bh::kMmStore, st);

@@ -28,19 +28,33 @@ struct MmArgs {
     int ostride;
     int relu2;       // kMmPair: BitNet's squared-ReLU gate instead of SiLU
     int gelu;        // kMmPair: Gemma's GELU (tanh form) gate instead of SiLU
-    // Q6_K: the expanded planes of m (and m2) from launch_q6x_expand, or null (the packed-plane GEMM)
+    // Q6_K / Q4_K / Q5_K: the expanded planes of m (and m2) from launch_mx_expand, or null (the
+    // packed-plane GEMMs)
     const int8_t* qx;
     const float* qxd;
+    const uint8_t* qxm;
     const int8_t* qx2;
     const float* qxd2;
+    const uint8_t* qxm2;
 };
 
-// Rows a workgroup of the expanded-Q6_K GEMM computes; the expanded planes pad rows to it.
+// A matrix's expanded planes: int8 lo and hi weights, float scales (and dmins), and the
+// K-quants' sub-block mins (null for Q6_K).
+struct MxPlanes {
+    const int8_t* q = nullptr;
+    const float* d = nullptr;
+    const uint8_t* mn = nullptr;
+};
+
+// Rows the widest workgroup of the expanded-plane GEMM computes; the planes pad rows to it.
 constexpr int kMxRows = 128;
-// Bytes of a Q6_K matrix's expanded planes (int8 lo and hi weights, float scales).
-size_t q6x_bytes(uint32_t rows, uint32_t cols);
-// Writes the expanded planes of Q6_K matrix m into mem (q6x_bytes of it); *q and *d point into mem.
-hipError_t launch_q6x_expand(const Packed& m, void* mem, const int8_t** q, const float** d, hipStream_t s);
+// Formats the prefill multiplies from expanded planes: Q6_K and Q5_K; Q4_K when
+// BRISK_HIP_PREFILL_Q4X=1 (its packed-plane GEMM folds the scales without them).
+bool mx_expanded(uint32_t type);
+// Bytes of a Q6_K, Q4_K or Q5_K matrix's expanded planes.
+size_t mx_bytes(uint32_t type, uint32_t rows, uint32_t cols);
+// Writes the expanded planes of m into mem (mx_bytes of it); *out points into mem.
+hipError_t launch_mx_expand(const Packed& m, void* mem, MxPlanes* out, hipStream_t s);
 
 struct PreAttnArgs {
     AttnArgs a;      // layer, shape and cache (a.q/k/v/pos/out unused)

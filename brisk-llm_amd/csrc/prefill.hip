@@ -21,6 +21,7 @@
 #include "prefill.h"
 
 #include <cstdlib>
+#include <string>
 
 
 namespace bh {
@@ -915,6 +916,58 @@ __global__ void k_q6x_expand(Packed m, int8_t* __restrict__ q, float* __restrict
     if (s == 0 && lane < 32) dq[(static_cast<size_t>(rg) * nsb + c) * 32 + lane] = d;
 }
 
+// Q4_K and Q5_K expanded the same way: per 32-value sub-block j the exact integer weight
+// w = sc_j q (q in 0..15 or 0..31, sc_j 6-bit: w <= 1953) is split as w = lo + 128 hi (lo 0..127,
+// hi 0..15), and dot_q4_k_q8_k / dot_q5_k_q8_k's (src/quant.cpp:500-547)
+//   weighted = A_lo + 128 A_hi,  offsets = sum_j mn_j pair_j = sum_k mn_j(k) x_k,
+// the offsets a third chain against the sub-block's min byte repeated over the step (a step is
+// one sub-block).  Per (rg, c) the scales are 64 floats (the 32 rows' d, then their dmin) and the
+// mins 32 rows x 8 bytes.
+__global__ void k_kmx_expand(Packed m, int8_t* __restrict__ q, float* __restrict__ dq, uint8_t* __restrict__ mq,
+                             uint32_t row_groups) {
+    const size_t gid = static_cast<size_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    const uint32_t nsb = m.cols / 256;
+    const int lane = static_cast<int>(gid & 63), s = static_cast<int>((gid >> 6) & 7);
+    const size_t rest = gid >> 9;
+    const uint32_t c = static_cast<uint32_t>(rest % nsb), rg = static_cast<uint32_t>(rest / nsb);
+    if (rg >= row_groups) return;
+    const uint32_t row = rg * 32 + (lane & 31);
+    const int h = lane >> 5;  // values 16 h .. 16 h + 15 of sub-block s
+    const bool q5 = m.type == kQ5_K;
+    uint32_t lo[4] = {0, 0, 0, 0}, hi[4] = {0, 0, 0, 0};
+    float d = 0.0f, dmin = 0.0f;
+    int mn = 0;
+    if (row < m.rows) {
+        const size_t blk = static_cast<size_t>(row) * nsb + c;
+        const uint8_t* qs = m.p0 + blk * 128 + (s >> 1) * 32;
+        const uint8_t* meta = m.p1 + blk * 16;
+        const uint8_t* dec = m.p2 + blk * (q5 ? 48 : 16);  // decoded scales, mins (then Q5_K's qh)
+        const int sc = dec[s];
+        mn = dec[8 + s];
+        d = h2f(static_cast<uint16_t>(meta[0] | (meta[1] << 8)));
+        dmin = h2f(static_cast<uint16_t>(meta[2] | (meta[3] << 8)));
+        for (int b = 0; b < 16; ++b) {
+            const int i = 16 * h + b;
+            int v = (s & 1) ? qs[i] >> 4 : qs[i] & 15;
+            if (q5 && (dec[16 + i] >> s) & 1) v |= 16;
+            const int w = sc * v, wl = w & 127, wh = w >> 7;
+            lo[b >> 2] |= static_cast<uint32_t>(wl) << (8 * (b & 3));
+            hi[b >> 2] |= static_cast<uint32_t>(wh) << (8 * (b & 3));
+        }
+    }
+    const size_t rc = static_cast<size_t>(rg) * nsb + c;
+    uint8_t* o = reinterpret_cast<uint8_t*>(q) + (((rc * 8 + s) * 2) * 64 + lane) * 16;
+    *reinterpret_cast<uint4*>(o) = make_uint4(lo[0], lo[1], lo[2], lo[3]);
+    *reinterpret_cast<uint4*>(o + 1024) = make_uint4(hi[0], hi[1], hi[2], hi[3]);
+    if (lane < 32) {
+        mq[(rc * 32 + lane) * 8 + s] = static_cast<uint8_t>(mn);
+        if (s == 0) {
+            dq[rc * 64 + lane] = d;
+            dq[rc * 64 + 32 + lane] = dmin;
+        }
+    }
+}
+
 typedef int v16i __attribute__((ext_vector_type(16)));
 __device__ __forceinline__ v16i mfma32(const v4u& a, const v4u& b, v16i c) {
     return __builtin_amdgcn_mfma_i32_32x32x32_i8(__builtin_bit_cast(v4i, a), __builtin_bit_cast(v4i, b), c, 0, 0, 0);
@@ -939,24 +992,38 @@ __device__ __forceinline__ void mx_copy(MxStage<G>& st, const ActPlanar& x, int 
     if (wave == 0) dma4(x.d + tokc(tid & (32 * G - 1)) * (x.stride / 32) + c, st.xd);
 }
 
-// A wave's operands for one super-block: 8 steps x (lo, hi) fragments and the 16 output rows' scales.
+// A wave's operands for one super-block: 8 steps x (lo, hi) fragments, the 16 output rows'
+// scales and, for Q4_K / Q5_K (KM), their dmins and the A row's 8 sub-block mins.
+template <bool KM>
 struct MxA {
     v4u f[16];
     float4 d[4];
+    float4 dm[KM ? 4 : 1];
+    uint32_t mn[KM ? 2 : 1];
 };
-__device__ __forceinline__ void mx_load(MxA& a, const int8_t* qw, const float* dw, int lane) {
+template <bool KM>
+__device__ __forceinline__ void mx_load(MxA<KM>& a, const int8_t* qw, const float* dw, const uint8_t* mw, int lane) {
     const auto* p = gmem(reinterpret_cast<const v4u*>(qw) + lane);
 #pragma unroll
     for (int i = 0; i < 16; ++i) a.f[i] = p[i * 64];
     const float* pd = dw + (lane >> 5) * 4;
 #pragma unroll
     for (int q = 0; q < 4; ++q) a.d[q] = gld4(pd + q * 8);
+    if constexpr (KM) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) a.dm[q] = gld4(pd + 32 + q * 8);
+        const uint32_t* pm = reinterpret_cast<const uint32_t*>(mw + (lane & 31) * 8);
+        a.mn[0] = gld<uint32_t>(pm, 0);
+        a.mn[1] = gld<uint32_t>(pm, 1);
+    }
 }
+__device__ __forceinline__ float f4_at(const float4& v, int i) { return i == 0 ? v.x : i == 1 ? v.y : i == 2 ? v.z : v.w; }
 
 // acc[gb] (lane: token 32 gb + l % 32, rows 8 (i / 4) + 4 (l / 32) + i % 4) += this super-block's
-// terms, in the reference's term order (dot_q6_k_q8_k, src/quant.cpp:549-563: d_x d_w weighted).
-template <int G>
-__device__ __forceinline__ void mx_compute(uint32_t base, const MxA& a, float (&acc)[G][16]) {
+// terms, in the reference's term order: Q6_K d_x d_w weighted (dot_q6_k_q8_k, src/quant.cpp:549-563);
+// Q4_K / Q5_K d_x (d weighted - dmin offsets) (dot_q4_k_q8_k / dot_q5_k_q8_k, :500-547).
+template <int G, bool KM>
+__device__ __forceinline__ void mx_compute(uint32_t base, const MxA<KM>& a, float (&acc)[G][16]) {
     const int lane = threadIdx.x & 63, h = lane >> 5;
 #pragma unroll
     for (int gb = 0; gb < G; ++gb) {
@@ -970,19 +1037,27 @@ __device__ __forceinline__ void mx_compute(uint32_t base, const MxA& a, float (&
         uint32_t xd = ds32(base + offsetof(MxStage<G>, xd) + (G == 1 ? lane : t) * 4);
         asm volatile("s_waitcnt lgkmcnt(0)"
                      : "+v"(b[0]), "+v"(b[1]), "+v"(b[2]), "+v"(b[3]), "+v"(b[4]), "+v"(b[5]), "+v"(b[6]), "+v"(b[7]), "+v"(xd));
-        v16i lo = {}, hi = {};
+        v16i lo = {}, hi = {}, mo = {};
 #pragma unroll
         for (int s = 0; s < 8; ++s) {
             lo = mfma32(a.f[2 * s], b[s], lo);
             hi = mfma32(a.f[2 * s + 1], b[s], hi);
+            if constexpr (KM) {
+                const uint32_t m4 = ((a.mn[s >> 2] >> (8 * (s & 3))) & 0xFF) * 0x01010101u;
+                mo = mfma32(v4u{m4, m4, m4, m4}, b[s], mo);
+            }
         }
         const float xg = __uint_as_float(xd);
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
             const int weighted = lo[i] + 128 * hi[i];
-            const float4 dq = a.d[i >> 2];
-            const float d = (i & 3) == 0 ? dq.x : (i & 3) == 1 ? dq.y : (i & 3) == 2 ? dq.z : dq.w;
-            acc[gb][i] += xg * d * static_cast<float>(weighted);
+            const float d = f4_at(a.d[i >> 2], i & 3);
+            if constexpr (KM) {
+                const float dmin = f4_at(a.dm[i >> 2], i & 3);
+                acc[gb][i] += xg * (d * static_cast<float>(weighted) - dmin * static_cast<float>(mo[i]));
+            } else {
+                acc[gb][i] += xg * d * static_cast<float>(weighted);
+            }
         }
     }
 }
@@ -994,13 +1069,14 @@ __device__ __forceinline__ void mx_compute(uint32_t base, const MxA& a, float (&
 // row tiles (every token tile of them), so a row tile's weights are read through one L2.
 // s_waitcnt vmcnt(n), the other counters not waited: every vector memory load but the last n has landed.
 constexpr int mx_wait_imm(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8); }
-constexpr int kMxLoads = 20;  // global loads of one mx_load (16 fragments, 4 scale rows)
+constexpr int kMxLoads = 20;    // global loads of one mx_load (16 fragments, 4 scale rows)
+constexpr int kMxLoadsKm = 26;  // ... with 4 dmin rows and 2 min words
 #ifndef BRISK_MX_BUFS
 #define BRISK_MX_BUFS 3
 #endif
 constexpr int kMxBufs = BRISK_MX_BUFS;  // fragment buffers in flight (unified VGPR/AGPR file: one wave a SIMD)
 
-template <int MODE, int G, int W>
+template <int MODE, int G, int W, bool KM>
 __global__ __launch_bounds__(64 * W) void k_mmx(MmArgs g) {
     __shared__ MxStage<G> st[2];
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
@@ -1018,8 +1094,10 @@ __global__ __launch_bounds__(64 * W) void k_mmx(MmArgs g) {
     }
     const int t0 = tt * 32 * G;
     const size_t rg = static_cast<size_t>(rt) * W + wave;
+    constexpr int DW = KM ? 64 : 32;  // scale floats per (row group, super-block)
     const int8_t* qw = g.qx + rg * nsb * 16384;
-    const float* dw = g.qxd + rg * nsb * 32;
+    const float* dw = g.qxd + rg * nsb * DW;
+    const uint8_t* mw = KM ? g.qxm + rg * nsb * 256 : nullptr;
     float acc[G][16];
 #pragma unroll
     for (int gb = 0; gb < G; ++gb)
@@ -1031,13 +1109,12 @@ __global__ __launch_bounds__(64 * W) void k_mmx(MmArgs g) {
     // of super-block c + kMxBufs - 1, computes c, and waits for everything but the loads still
     // ahead of c + 1 (so c + 1 has landed).  A bare barrier: __syncthreads' fence would wait for
     // all of them.
-    MxA a[kMxBufs];
+    MxA<KM> a[kMxBufs];
+    auto load = [&](MxA<KM>& dst, int n) { mx_load<KM>(dst, qw + static_cast<size_t>(n) * 16384, dw + n * DW, KM ? mw + n * 256 : nullptr, lane); };
     mx_copy<G, W>(st[0], g.x, g.ntok, t0, 0);
 #pragma unroll
-    for (int k = 0; k < kMxBufs - 1; ++k) {
-        const int n = min(k, nsb - 1);  // past the end: the last super-block again, so the count stays exact
-        mx_load(a[k], qw + static_cast<size_t>(n) * 16384, dw + n * 32, lane);
-    }
+    for (int k = 0; k < kMxBufs - 1; ++k) load(a[k], min(k, nsb - 1));  // past the end: the last super-block again,
+                                                                          // so the load count stays exact
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
     for (int c0 = 0; c0 < nsb; c0 += kMxBufs) {
@@ -1046,10 +1123,9 @@ __global__ __launch_bounds__(64 * W) void k_mmx(MmArgs g) {
             const int c = c0 + k;
             if (c >= nsb) break;
             if (c + 1 < nsb) mx_copy<G, W>(st[(c + 1) & 1], g.x, g.ntok, t0, c + 1);
-            const int n = min(c + kMxBufs - 1, nsb - 1);
-            mx_load(a[(k + kMxBufs - 1) % kMxBufs], qw + static_cast<size_t>(n) * 16384, dw + n * 32, lane);
-            mx_compute<G>(lds_off(&st[c & 1]), a[k], acc);
-            __builtin_amdgcn_s_waitcnt(mx_wait_imm(kMxLoads * (kMxBufs - 2)));
+            load(a[(k + kMxBufs - 1) % kMxBufs], min(c + kMxBufs - 1, nsb - 1));
+            mx_compute<G, KM>(lds_off(&st[c & 1]), a[k], acc);
+            __builtin_amdgcn_s_waitcnt(mx_wait_imm((KM ? kMxLoadsKm : kMxLoads) * (kMxBufs - 2)));
             __builtin_amdgcn_s_barrier();
         }
     }
@@ -1882,6 +1958,16 @@ __global__ __launch_bounds__(kThreads) void k_pre_attn_fa(PreAttnArgs p, int nto
 
 // ---------------------------------------------------------------- launchers
 
+// The expanded-plane GEMM: 4 waves (128 rows) a workgroup, fewer where that leaves compute units without one.
+template <int MODE, bool KM>
+static void mmx_launch(const MmArgs& g, hipStream_t s) {
+    const int tt = (g.ntok + 31) / 32;
+    auto tiles = [&](int w) { return static_cast<int>((g.m.rows + 32 * w - 1) / (32 * w)) * tt; };
+    if (tiles(4) >= kKqCus) hipLaunchKernelGGL((k_mmx<MODE, 1, 4, KM>), dim3(tiles(4)), dim3(256), 0, s, g);
+    else if (tiles(2) >= kKqCus) hipLaunchKernelGGL((k_mmx<MODE, 1, 2, KM>), dim3(tiles(2)), dim3(128), 0, s, g);
+    else hipLaunchKernelGGL((k_mmx<MODE, 1, 1, KM>), dim3(tiles(1)), dim3(64), 0, s, g);
+}
+
 template <int MODE>
 static hipError_t mm_dispatch(const MmArgs& g, hipStream_t s) {
     const int tok = 16 * (g.m.type == kQ4_K || g.m.type == kQ5_K || g.m.type == kQ6_K ? mm_groups<kQ4_K>() : mm_groups<kQ4_0>());
@@ -1896,20 +1982,22 @@ static hipError_t mm_dispatch(const MmArgs& g, hipStream_t s) {
         case kQ4_1: hipLaunchKernelGGL((k_mm<kQ4_1, MODE>), grid, dim3(kThreads), 0, s, g); break;
         case kQ5_0: hipLaunchKernelGGL((k_mm<kQ5_0, MODE>), grid, dim3(kThreads), 0, s, g); break;
         case kQ8_0: hipLaunchKernelGGL((k_mm<kQ8_0, MODE>), grid, dim3(kThreads), 0, s, g); break;
-        case kQ5_K: hipLaunchKernelGGL((k_mm<kQ5_K, MODE>), grid, dim3(kThreads), 0, s, g); break;
+        case kQ5_K:
+            if (g.qx != nullptr) mmx_launch<MODE, true>(g, s);
+            else hipLaunchKernelGGL((k_mm<kQ5_K, MODE>), grid, dim3(kThreads), 0, s, g);
+            break;
         case kQ4_K:
+            if (g.qx != nullptr) {
+                mmx_launch<MODE, true>(g, s);
+                break;
+            }
             if (kq_g == 4) hipLaunchKernelGGL((k_mmk<kQ4_K, MODE, 4>), kq_grid, dim3(kThreads), 0, s, g);
             else if (kq_g == 2) hipLaunchKernelGGL((k_mmk<kQ4_K, MODE, 2>), kq_grid, dim3(kThreads), 0, s, g);
             else hipLaunchKernelGGL((k_mmk<kQ4_K, MODE, 1>), kq_grid, dim3(kThreads), 0, s, g);
             break;
         case kQ6_K:
             if (g.qx != nullptr) {
-                // 4 waves (128 rows) a workgroup, fewer where that leaves compute units without one
-                const int tt = (g.ntok + 31) / 32;
-                auto tiles = [&](int w) { return static_cast<int>((g.m.rows + 32 * w - 1) / (32 * w)) * tt; };
-                if (tiles(4) >= kKqCus) hipLaunchKernelGGL((k_mmx<MODE, 1, 4>), dim3(tiles(4)), dim3(256), 0, s, g);
-                else if (tiles(2) >= kKqCus) hipLaunchKernelGGL((k_mmx<MODE, 1, 2>), dim3(tiles(2)), dim3(128), 0, s, g);
-                else hipLaunchKernelGGL((k_mmx<MODE, 1, 1>), dim3(tiles(1)), dim3(64), 0, s, g);
+                mmx_launch<MODE, false>(g, s);
                 break;
             }
             if (kq_g == 4) hipLaunchKernelGGL((k_mmk<kQ6_K, MODE, 4>), kq_grid, dim3(kThreads), 0, s, g);
@@ -1936,27 +2024,44 @@ hipError_t launch_mm(const MmArgs& g, int mode, hipStream_t s) {
             up.m = g.m2;
             up.qx = g.qx2;
             up.qxd = g.qxd2;
+            up.qxm = g.qxm2;
             return mm_dispatch<kMmGated>(up, s);
         }
         default: return hipErrorInvalidValue;
     }
 }
 
-size_t q6x_bytes(uint32_t rows, uint32_t cols) {
-    const size_t rp = (rows + kMxRows - 1) / kMxRows * kMxRows;
-    return rp * cols * 2 + align256(rp * (cols / 256) * 4);
+static bool mx_km(uint32_t type) { return type == kQ4_K || type == kQ5_K; }
+
+bool mx_expanded(uint32_t type) {
+    if (type == kQ6_K || type == kQ5_K) return true;
+    const char* e = std::getenv("BRISK_HIP_PREFILL_Q4X");
+    return type == kQ4_K && e != nullptr && std::string(e) == "1";
 }
 
-hipError_t launch_q6x_expand(const Packed& m, void* mem, const int8_t** q, const float** d, hipStream_t s) {
-    if (m.type != kQ6_K || m.cols % 256 != 0) return hipErrorInvalidValue;
-    const size_t rp = (m.rows + kMxRows - 1) / kMxRows * kMxRows;
+size_t mx_bytes(uint32_t type, uint32_t rows, uint32_t cols) {
+    const size_t rp = (rows + kMxRows - 1) / kMxRows * kMxRows, nsb = cols / 256;
+    const size_t q = rp * cols * 2, d = align256(rp * nsb * (mx_km(type) ? 2 : 1) * 4);
+    return q + d + (mx_km(type) ? align256(rp * nsb * 8) : 0);
+}
+
+hipError_t launch_mx_expand(const Packed& m, void* mem, MxPlanes* out, hipStream_t s) {
+    if ((m.type != kQ6_K && !mx_km(m.type)) || m.cols % 256 != 0) return hipErrorInvalidValue;
+    const size_t rp = (m.rows + kMxRows - 1) / kMxRows * kMxRows, nsb = m.cols / 256;
     int8_t* qq = static_cast<int8_t*>(mem);
     float* dd = reinterpret_cast<float*>(qq + rp * m.cols * 2);
-    const size_t threads = rp / 32 * (m.cols / 256) * 512;
-    hipLaunchKernelGGL(k_q6x_expand, dim3(static_cast<unsigned>((threads + 255) / 256)), dim3(256), 0, s, m, qq, dd,
-                       static_cast<uint32_t>(rp / 32));
-    *q = qq;
-    *d = dd;
+    uint8_t* mm = reinterpret_cast<uint8_t*>(dd) + align256(rp * nsb * 2 * 4);
+    const size_t threads = rp / 32 * nsb * 512;
+    const dim3 grid(static_cast<unsigned>((threads + 255) / 256));
+    if (m.type == kQ6_K) {
+        hipLaunchKernelGGL(k_q6x_expand, grid, dim3(256), 0, s, m, qq, dd, static_cast<uint32_t>(rp / 32));
+        mm = nullptr;
+    } else {
+        hipLaunchKernelGGL(k_kmx_expand, grid, dim3(256), 0, s, m, qq, dd, mm, static_cast<uint32_t>(rp / 32));
+    }
+    out->q = qq;
+    out->d = dd;
+    out->mn = mm;
     return hipGetLastError();
 }
 

@@ -23,6 +23,14 @@
 
 namespace bh {
 
+// The expanded planes of m (or nulls) as a GEMM's first / second matrix.
+static void set_mx(MmArgs& g, const DeviceMatrix& m) {
+    g.qx = m.x.q; g.qxd = m.x.d; g.qxm = m.x.mn;
+}
+static void set_mx2(MmArgs& g, const DeviceMatrix& m) {
+    g.qx2 = m.x.q; g.qxd2 = m.x.d; g.qxm2 = m.x.mn;
+}
+
 namespace {
 
 [[noreturn]] void model_fail(const std::string& what) { throw Error(BRISK_HIP_EINVAL, "model: " + what); }
@@ -163,10 +171,11 @@ brisk_hip_memory estimate_session(const brisk_hip_config& cfg, const brisk_hip_t
     if (cfg.arch == BRISK_HIP_ARCH_GEMMA3 || cfg.arch == BRISK_HIP_ARCH_LFM2) sc += T * e * 4;  // post-norm inputs, conv outputs
     if (cfg.arch == BRISK_HIP_ARCH_LFM2) sc += T * 3 * e * 4;                                   // prefill conv rows
     sc += static_cast<size_t>(64) * cfg.vocab * 4;                         // eval_all logits
-    if (cfg.arch != BRISK_HIP_ARCH_GEMMA3 && cfg.arch != BRISK_HIP_ARCH_LFM2)  // the prefill's expanded Q6_K layer matrices
-        for (size_t i = 0; i < n; ++i)
-            if (tensors[i].type == BRISK_HIP_Q6_K && tensors[i].name != nullptr && std::strncmp(tensors[i].name, "blk.", 4) == 0)
-                sc += q6x_bytes(static_cast<uint32_t>(tensors[i].rows), static_cast<uint32_t>(tensors[i].cols));
+    for (size_t i = 0; i < n; ++i)  // the prefill's expanded layer matrices
+        if (mx_expanded(static_cast<uint32_t>(tensors[i].type)) && tensors[i].name != nullptr &&
+            std::strncmp(tensors[i].name, "blk.", 4) == 0 && tensors[i].rows > 1)
+            sc += mx_bytes(static_cast<uint32_t>(tensors[i].type), static_cast<uint32_t>(tensors[i].rows),
+                           static_cast<uint32_t>(tensors[i].cols));
     sc += staging + (64 << 10);                                            // load staging, small state
     {  // the token loop's block-major down copies and their term words (Session::setup_loop's push)
         size_t down_bytes = 0;
@@ -903,13 +912,13 @@ void Session::ensure_prefill() {
     pre_x_.qs = static_cast<int8_t*>(alloc(T * pre_x_.stride));
     pre_x_.d = static_cast<float*>(alloc(T * (pre_x_.stride / 32) * 4));
     pre_x_.bs = static_cast<int32_t*>(alloc(T * (pre_x_.stride / 16) * 4));
-    const char* qx = std::getenv("BRISK_HIP_PREFILL_Q6X");  // "0": Q6_K through the packed-plane GEMM
+    const char* qx = std::getenv("BRISK_HIP_PREFILL_MX");  // "0": every format through the packed-plane GEMMs
     if (qx != nullptr && std::string(qx) == "0") return;
     for (Layer& L : layers_)
         for (DeviceMatrix* m : {&L.q, &L.k, &L.v, &L.o, &L.gate, &L.up, &L.down, &L.conv_in, &L.conv_out})
-            if (m->p.type == kQ6_K && m->xmem == nullptr) {
-                check(hipMalloc(&m->xmem, q6x_bytes(m->p.rows, m->p.cols)), "hipMalloc(expanded Q6_K)");
-                check(launch_q6x_expand(m->p, m->xmem, &m->xq, &m->xd, stream_), "expand Q6_K");
+            if (m->mem != nullptr && mx_expanded(m->p.type) && m->xmem == nullptr) {
+                check(hipMalloc(&m->xmem, mx_bytes(m->p.type, m->p.rows, m->p.cols)), "hipMalloc(expanded planes)");
+                check(launch_mx_expand(m->p, m->xmem, &m->x, stream_), "expand planes");
             }
 }
 
@@ -933,21 +942,21 @@ void Session::prefill_layers(size_t pos0, int T) {
         g.ntok = T;
         if (L.conv_w != nullptr) {  // LFM2 short convolution in place of attention (src/model.cpp:935-969)
             prefill_quant(pre_h_, e, L.attn_norm, e, T, L.conv_in);
-            g.m = L.conv_in.p; g.qx = L.conv_in.xq; g.qxd = L.conv_in.xd; g.out = pre_conv_; g.ostride = 3 * e;
+            g.m = L.conv_in.p; set_mx(g, L.conv_in); g.out = pre_conv_; g.ostride = 3 * e;
             check(launch_mm(g, kMmStore, stream_), "prefill conv in_proj");
             check(launch_pre_conv(pre_conv_, L.conv_cache, L.conv_w, static_cast<int>(cfg_.conv_taps), static_cast<int>(pos0), e, T,
                                   pre_proj_, stream_), "prefill conv");
             prefill_quant(pre_proj_, e, nullptr, e, T, L.conv_out);
-            g.m = L.conv_out.p; g.qx = L.conv_out.xq; g.qxd = L.conv_out.xd; g.out = pre_h_; g.ostride = e;
+            g.m = L.conv_out.p; set_mx(g, L.conv_out); g.out = pre_h_; g.ostride = e;
             check(launch_mm(g, kMmAdd, stream_), "prefill conv out_proj");
         } else {
             // Q, K, V of attn_norm(h) (src/model.cpp:996-1015)
             prefill_quant(pre_h_, e, L.attn_norm, e, T, L.q);
-            g.m = L.q.p; g.qx = L.q.xq; g.qxd = L.q.xd; g.out = pre_q_; g.ostride = qd;
+            g.m = L.q.p; set_mx(g, L.q); g.out = pre_q_; g.ostride = qd;
             check(launch_mm(g, kMmStore, stream_), "prefill q");
-            g.m = L.k.p; g.qx = L.k.xq; g.qxd = L.k.xd; g.out = pre_k_; g.ostride = kvd;
+            g.m = L.k.p; set_mx(g, L.k); g.out = pre_k_; g.ostride = kvd;
             check(launch_mm(g, kMmStore, stream_), "prefill k");
-            g.m = L.v.p; g.qx = L.v.xq; g.qxd = L.v.xd; g.out = pre_v_; g.ostride = kvd;
+            g.m = L.v.p; set_mx(g, L.v); g.out = pre_v_; g.ostride = kvd;
             check(launch_mm(g, kMmStore, stream_), "prefill v");
             // norms, RoPE, cache rows, attention (:1020-1093)
             PreAttnArgs pa{};
@@ -968,19 +977,19 @@ void Session::prefill_layers(size_t pos0, int T) {
             check(launch_pre_attention(pa, T, stream_), "prefill attention");
             // h += O (sub-normed) att (:1095-1111)
             prefill_quant(pre_att_, qd, L.attn_sub_norm, qd, T, L.o);
-            g.m = L.o.p; g.qx = L.o.xq; g.qxd = L.o.xd; g.out = L.attn_post_norm ? pre_proj_ : pre_h_; g.ostride = e;
+            g.m = L.o.p; set_mx(g, L.o); g.out = L.attn_post_norm ? pre_proj_ : pre_h_; g.ostride = e;
             check(launch_mm(g, L.attn_post_norm ? kMmStore : kMmAdd, stream_), "prefill o");
             if (L.attn_post_norm)  // h += rms_norm(O att, post_attention_norm) (:1113-1121)
                 check(launch_pre_post_add(pre_h_, pre_proj_, L.attn_post_norm, cfg_.rms_epsilon, e, T, stream_), "prefill post norm");
         }
         // act = silu(gate) * up of ffn_norm(h) (:1111-1143)
         prefill_quant(pre_h_, e, L.ffn_norm, e, T, L.gate);
-        g.m = L.gate.p; g.m2 = L.up.p; g.qx = L.gate.xq; g.qxd = L.gate.xd; g.qx2 = L.up.xq; g.qxd2 = L.up.xd; g.out = pre_act_; g.ostride = ff; g.relu2 = cfg_.arch == BRISK_HIP_ARCH_BITNET;
+        g.m = L.gate.p; g.m2 = L.up.p; set_mx(g, L.gate); set_mx2(g, L.up); g.out = pre_act_; g.ostride = ff; g.relu2 = cfg_.arch == BRISK_HIP_ARCH_BITNET;
         g.gelu = gemma();
         check(launch_mm(g, kMmPair, stream_), "prefill gate/up");
         // h += down (sub-normed) act (:1144-1162)
         prefill_quant(pre_act_, ff, L.ffn_sub_norm, ff, T, L.down);
-        g.m = L.down.p; g.qx = L.down.xq; g.qxd = L.down.xd; g.out = L.ffn_post_norm ? pre_proj_ : pre_h_; g.ostride = e;
+        g.m = L.down.p; set_mx(g, L.down); g.out = L.ffn_post_norm ? pre_proj_ : pre_h_; g.ostride = e;
         g.relu2 = 0; g.gelu = 0;
         check(launch_mm(g, L.ffn_post_norm ? kMmStore : kMmAdd, stream_), "prefill down");
         if (L.ffn_post_norm)  // h += rms_norm(down act, post_ffw_norm) (:1153-1160)

@@ -23,14 +23,14 @@ struct Error : std::runtime_error {
 struct DeviceMatrix {
     Packed p{};
     void* mem = nullptr;
-    // Q6_K: the batched prefill's expanded planes (launch_q6x_expand), made at the first prefill
+    // Q6_K, Q5_K (Q4_K on request): the batched prefill's expanded planes (launch_mx_expand), made at
+    // the first prefill
     void* xmem = nullptr;
-    const int8_t* xq = nullptr;
-    const float* xd = nullptr;
+    MxPlanes x{};
     DeviceMatrix() = default;
     DeviceMatrix(const DeviceMatrix&) = delete;
     DeviceMatrix& operator=(const DeviceMatrix&) = delete;
-    DeviceMatrix(DeviceMatrix&& o) noexcept : p(o.p), mem(o.mem), xmem(o.xmem), xq(o.xq), xd(o.xd) {
+    DeviceMatrix(DeviceMatrix&& o) noexcept : p(o.p), mem(o.mem), xmem(o.xmem), x(o.x) {
         o.mem = nullptr;
         o.xmem = nullptr;
     }
