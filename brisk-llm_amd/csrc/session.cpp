@@ -476,7 +476,21 @@ Session::~Session() {
     if (graph_layers_) (void)hipGraphExecDestroy(graph_layers_);
     if (graph_full_) (void)hipGraphExecDestroy(graph_full_);
     for (void* p : owned_) (void)hipFree(p);
+    if (host_io_) (void)hipHostFree(host_io_);
     if (stream_) (void)hipStreamDestroy(stream_);
+}
+
+// Pinned host staging for the token and logits copies: a pageable copy goes through the
+// runtime's own staging, a few hundred microseconds more for a row of logits.  Grown on demand.
+void* Session::host_buf(size_t bytes) {
+    if (bytes > host_io_bytes_) {
+        if (host_io_) (void)hipHostFree(host_io_);
+        host_io_ = nullptr;
+        host_io_bytes_ = 0;
+        check(hipHostMalloc(&host_io_, bytes, hipHostMallocDefault), "hipHostMalloc(staging)");
+        host_io_bytes_ = bytes;
+    }
+    return host_io_;
 }
 
 void* Session::alloc(size_t bytes) {
@@ -874,13 +888,25 @@ void Session::validate(const int32_t* tokens, size_t n) const {
 
 // Writes tokens to seq[position_ ..], syncs the device position to the host's and
 // marks seq[0, position_ + n) as caller tokens (pos_[1]).
+// rows x vocab logits from the device into out (when given) through the pinned staging; waits for the stream.
+void Session::fetch_logits(float* out, const float* dev, size_t rows) {
+    const size_t bytes = rows * static_cast<size_t>(cfg_.vocab) * 4;
+    void* hb = out != nullptr ? host_buf(bytes) : nullptr;
+    if (out != nullptr) check(hipMemcpyAsync(hb, dev, bytes, hipMemcpyDeviceToHost, stream_), "hipMemcpy(logits)");
+    check(hipStreamSynchronize(stream_), "eval sync");
+    if (out != nullptr) std::memcpy(out, hb, bytes);
+}
+
 void Session::stage(const int32_t* tokens, size_t n) { stage(tokens, n, position_); }
 
 void Session::stage(const int32_t* tokens, size_t n, size_t device_pos) {
-    check(hipMemcpyAsync(seq_ + position_, tokens, n * 4, hipMemcpyHostToDevice, stream_), "hipMemcpy(tokens)");
-    const int p[2] = {static_cast<int>(device_pos), static_cast<int>(position_ + n)};
-    check(hipMemcpyAsync(pos_, p, 8, hipMemcpyHostToDevice, stream_), "hipMemcpy(pos)");
-    check(hipStreamSynchronize(stream_), "stage sync");  // the host copies above read stack memory
+    int32_t* pin = static_cast<int32_t*>(host_buf(std::max<size_t>((n + 2) * 4, static_cast<size_t>(cfg_.vocab) * 4)));
+    std::memcpy(pin, tokens, n * 4);
+    pin[n] = static_cast<int32_t>(device_pos);
+    pin[n + 1] = static_cast<int32_t>(position_ + n);
+    check(hipMemcpyAsync(seq_ + position_, pin, n * 4, hipMemcpyHostToDevice, stream_), "hipMemcpy(tokens)");
+    check(hipMemcpyAsync(pos_, pin + n, 8, hipMemcpyHostToDevice, stream_), "hipMemcpy(pos)");
+    check(hipStreamSynchronize(stream_), "stage sync");  // the staging buffer is reused by the next copy
 }
 
 // Prompts of two or more tokens whose attention stays on the exact path go
@@ -1013,9 +1039,7 @@ void Session::eval(const int32_t* tokens, size_t n, float* logits) {
         ha.eps = cfg_.rms_epsilon; ha.logits = logits_; ha.key = key_; ha.softcap = gemma() ? cfg_.final_softcap : 0.0f;
         check(launch_head(ha, stream_), "output");
         finish();
-        if (logits != nullptr)
-            check(hipMemcpyAsync(logits, logits_, static_cast<size_t>(cfg_.vocab) * 4, hipMemcpyDeviceToHost, stream_), "hipMemcpy(logits)");
-        check(hipStreamSynchronize(stream_), "eval sync");
+        fetch_logits(logits, logits_, 1);
         position_ += n;
         return;
     }
@@ -1027,8 +1051,7 @@ void Session::eval(const int32_t* tokens, size_t n, float* logits) {
         step(true);
         finish();
     }
-    if (logits != nullptr) check(hipMemcpyAsync(logits, logits_, static_cast<size_t>(cfg_.vocab) * 4, hipMemcpyDeviceToHost, stream_), "hipMemcpy(logits)");
-    check(hipStreamSynchronize(stream_), "eval sync");
+    fetch_logits(logits, logits_, 1);
     check_loop_error();
     position_ += n;
 }
@@ -1057,12 +1080,13 @@ void Session::eval_all(const int32_t* tokens, size_t n, float* logits) {
         ha.eps = cfg_.rms_epsilon; ha.logits = nullptr; ha.key = key_; ha.softcap = gemma() ? cfg_.final_softcap : 0.0f;
         check(launch_head(ha, stream_), "output");
         finish();
-        check(hipMemcpyAsync(logits, all_logits_, n * cfg_.vocab * 4, hipMemcpyDeviceToHost, stream_), "hipMemcpy(logits)");
-        check(hipStreamSynchronize(stream_), "eval_all sync");
+        fetch_logits(logits, all_logits_, n);
         position_ += n;
         return;
     }
     stage(tokens, n);
+    const size_t row = static_cast<size_t>(cfg_.vocab) * 4;
+    char* hb = static_cast<char*>(host_buf(n * row));
     for (size_t i = 0; i < n; ++i) {
         if (uses_loop()) {
             run_loop(position_ + i, 1, 0, position_ + n);
@@ -1070,10 +1094,10 @@ void Session::eval_all(const int32_t* tokens, size_t n, float* logits) {
             step(true);
             if (i + 1 == n) finish();
         }
-        check(hipMemcpyAsync(logits + i * cfg_.vocab, logits_, static_cast<size_t>(cfg_.vocab) * 4, hipMemcpyDeviceToHost, stream_),
-              "hipMemcpy(logits)");
+        check(hipMemcpyAsync(hb + i * row, logits_, row, hipMemcpyDeviceToHost, stream_), "hipMemcpy(logits)");
     }
     check(hipStreamSynchronize(stream_), "eval_all sync");
+    std::memcpy(logits, hb, n * row);
     check_loop_error();
     position_ += n;
 }

@@ -150,6 +150,10 @@ private:
     bool prefill_mfma_ = false;    // BRISK_HIP_PREFILL_ATTN=mfma
     bool prefill_legacy_ = false;  // BRISK_HIP_PREFILL_ATTN=staged
     float *pre_h_ = nullptr, *pre_q_ = nullptr, *pre_k_ = nullptr, *pre_v_ = nullptr, *pre_att_ = nullptr, *pre_act_ = nullptr;
+    void* host_io_ = nullptr;  // pinned staging for token and logits copies (host_buf)
+    size_t host_io_bytes_ = 0;
+    void* host_buf(size_t bytes);
+    void fetch_logits(float* out, const float* dev, size_t rows);
     float* pre_proj_ = nullptr;  // Gemma: a projection's rows before their post-norm; LFM2: conv outputs
     float* pre_conv_ = nullptr;  // LFM2: in_proj rows [b | c | x]
     ActPlanar pre_x_{};
