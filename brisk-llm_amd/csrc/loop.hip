@@ -1094,19 +1094,35 @@ __device__ __forceinline__ bool spread_stage2(const LoopArgs& g, const AttnArgs&
             const uint16_t* vrow = s.vt[c & 1] + d * kVtStride - p0;
             const int full = p0 + ((pe - p0) & ~7);
             int p = p0;
-            if (full > p0) {  // eight positions a round, the next round's weights and values read a round ahead
-                float4 w0 = *reinterpret_cast<const float4*>(w + p), w1 = *reinterpret_cast<const float4*>(w + p + 4);
-                uint4 vv = *reinterpret_cast<const uint4*>(vrow + p);
-                for (; p < full; p += 8) {
-                    const int pn = p + 8 < full ? p + 8 : p;
-                    const float4 n0 = *reinterpret_cast<const float4*>(w + pn), n1 = *reinterpret_cast<const float4*>(w + pn + 4);
-                    const uint4 nv = *reinterpret_cast<const uint4*>(vrow + pn);
-                    acc += mul_h<false>(w0.x, vv.x); acc += mul_h<true>(w0.y, vv.x);
-                    acc += mul_h<false>(w0.z, vv.y); acc += mul_h<true>(w0.w, vv.y);
-                    acc += mul_h<false>(w1.x, vv.z); acc += mul_h<true>(w1.y, vv.z);
-                    acc += mul_h<false>(w1.z, vv.w); acc += mul_h<true>(w1.w, vv.w);
-                    w0 = n0; w1 = n1; vv = nv;
+            if (full > p0) {  // eight positions a round, each round's weights and values read two rounds ahead
+                struct Round {
+                    float4 w0, w1;
+                    uint4 v;
+                };
+                auto rd = [&](int q) {
+                    const int qc = q < full ? q : full - 8;  // past the end: the last round again (unused)
+                    return Round{*reinterpret_cast<const float4*>(w + qc), *reinterpret_cast<const float4*>(w + qc + 4),
+                                 *reinterpret_cast<const uint4*>(vrow + qc)};
+                };
+                auto sum = [&](const Round& r) {
+                    acc += mul_h<false>(r.w0.x, r.v.x); acc += mul_h<true>(r.w0.y, r.v.x);
+                    acc += mul_h<false>(r.w0.z, r.v.y); acc += mul_h<true>(r.w0.w, r.v.y);
+                    acc += mul_h<false>(r.w1.x, r.v.z); acc += mul_h<true>(r.w1.y, r.v.z);
+                    acc += mul_h<false>(r.w1.z, r.v.w); acc += mul_h<true>(r.w1.w, r.v.w);
+                };
+                // rounds at p, p + 8, ...: ra and rb hold the next two; three rounds an iteration,
+                // the names rotated rather than copied
+                Round ra = rd(p), rb = rd(p + 8);
+                for (; p + 24 <= full; p += 24) {
+                    const Round rc = rd(p + 16);
+                    sum(ra);
+                    ra = rd(p + 24);
+                    sum(rb);
+                    rb = rd(p + 32);
+                    sum(rc);
                 }
+                if (p < full) { sum(ra); p += 8; }
+                if (p < full) { sum(rb); p += 8; }
             }
             for (; p < pe; ++p) acc += mul_h<false>(w[p], vrow[p]);
         } else if (wave >= cw && c + 1 < chunks) {
