@@ -133,7 +133,10 @@ int brisk_hip_quantize_q8_k(const float* x, void* out, size_t count, int bits, v
  * dot(row r, activation row t) over a packed matrix and pre-quantised
  * activations (Q8_0 rows for Q4_0/Q8_0, Q8_K rows for Q4_K/Q6_K/TQ2_0).  Each
  * output is bit-identical to the reference's generic kernels. `flags`: bit 0
- * selects, for TQ2_0, the x86 TQ2_0x16 arithmetic (src/quant.cpp:789-802). */
+ * selects, for TQ2_0, the x86 TQ2_0x16 arithmetic (src/quant.cpp:789-802).
+ * For n > 1, matmul allocates a scratch block for the call: the planar
+ * activation rows, and for Q6_K and Q5_K the matrix's expanded weight planes
+ * (about 2 bytes a weight), as a session's batched prefill holds them. */
 int brisk_hip_matvec(int type, int flags, const void* packed, size_t rows, size_t cols, const void* xq, float* out,
                      void* stream);
 int brisk_hip_matmul(int type, int flags, const void* packed, size_t rows, size_t cols, const void* xq, size_t n,
