@@ -648,20 +648,30 @@ __device__ __forceinline__ v4i mfma64(const v4u& a, const v4u& b, v4i c) {
     return __builtin_amdgcn_mfma_i32_16x16x64_i8(__builtin_bit_cast(v4i, a), __builtin_bit_cast(v4i, b), c, 0, 0, 0);
 }
 
+// LDS addresses of a Q4_K stage's parts: the nibble rows, the {d, dmin, scales} and decoded
+// scale/min rows (wk, then wk + 1024), the activations and their scales.
+struct KqBases {
+    uint32_t w0, wk, x, xd;
+};
+__device__ __forceinline__ KqBases kq_bases(uint32_t base) {
+    return KqBases{base + static_cast<uint32_t>(offsetof(KqStage<kQ4_K>, w0)), base + static_cast<uint32_t>(offsetof(KqStage<kQ4_K>, wk)),
+                   base + static_cast<uint32_t>(offsetof(KqStage<kQ4_K>, x)), base + static_cast<uint32_t>(offsetof(KqStage<kQ4_K>, xd))};
+}
+
 // Fragments read by kq_f64_issue; kq_f64_wait ties each as one 128-bit operand,
 // so no copy of a fragment register can be placed before the wait.
 struct KqF64 {
     v4u a, b0, b1, b2, b3;  // b0 .. b(G-1) used
 };
 template <int G>
-__device__ __forceinline__ KqF64 kq_f64_issue(uint32_t base, int s, int ar, int tl, int l16) {
+__device__ __forceinline__ KqF64 kq_f64_issue(const KqBases& b, int s, int ar, int tl, int l16) {
     KqF64 f;
     const int pa = 2 * s + (l16 & 1);  // Q4_K: 32 bytes of nibbles a sub-block pair, low then high
-    f.a = ds128v(base + offsetof(KqStage<kQ4_K>, w0) + (ar * 8 + (pa ^ (ar & 7))) * 16);
+    f.a = ds128v(b.w0 + (ar * 8 + (pa ^ (ar & 7))) * 16);
     const int pb = 4 * s + l16;
     auto bfrag = [&](int g) -> v4u {
         const int t = 16 * g + tl;
-        return ds128v(base + offsetof(KqStage<kQ4_K>, x) + (t * 16 + (pb ^ (t & 15))) * 16);
+        return ds128v(b.x + (t * 16 + (pb ^ (t & 15))) * 16);
     };
     const v4u z = {0u, 0u, 0u, 0u};
     f.b0 = bfrag(0);
@@ -686,17 +696,17 @@ __device__ __forceinline__ v4u mul_bytes(const v4u& q, uint32_t d) {
 }
 
 template <int G>
-__device__ __forceinline__ void kq_compute_fold(uint32_t base, MmAcc<G>& acc) {
+__device__ __forceinline__ void kq_compute_fold(const KqBases& base, MmAcc<G>& acc) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, tl = lane & 15, l16 = lane >> 4;
     const int ar = wave * 16 + tl, orow0 = wave * 16 + l16 * 4;
     const v4i zero = {0, 0, 0, 0};
     // the A row's decoded scales and mins (for the digits), the output rows' d / dmin, the groups' x scales
-    v4u scm = ds128v(base + offsetof(KqStage<kQ4_K>, wk) + 1024 + ar * 16);
+    v4u scm = ds128v(base.wk + 1024 + ar * 16);
     uint32_t dd[4], xd[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-        dd[i] = ds32(base + offsetof(KqStage<kQ4_K>, wk) + (orow0 + i) * 16);
-        xd[i] = i < G ? ds32(base + offsetof(KqStage<kQ4_K>, xd) + (16 * i + tl) * 4) : 0u;
+        dd[i] = ds32(base.wk + (orow0 + i) * 16);
+        xd[i] = i < G ? ds32(base.xd + (16 * i + tl) * 4) : 0u;
     }
     asm volatile("s_waitcnt lgkmcnt(0)"
                  : "+v"(scm), "+v"(dd[0]), "+v"(dd[1]), "+v"(dd[2]), "+v"(dd[3]), "+v"(xd[0]), "+v"(xd[1]), "+v"(xd[2]),
@@ -1179,7 +1189,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 8))
     __syncthreads();
     for (int c = 0; c < nc; ++c) {
         if (c + 1 < nc) kq_copy<T, G>(st[(c + 1) & 1], g.m, g.x, g.ntok, rt0, t0, c + 1);
-        if constexpr (T == kQ4_K) kq_compute_fold<G>(lds_off(&st[c & 1]), a);
+        if constexpr (T == kQ4_K) kq_compute_fold<G>(kq_bases(lds_off(&st[c & 1])), a);
         else kq_compute_fold6<G>(lds_off(&st[c & 1]), a);
         __builtin_amdgcn_s_waitcnt(0);  // chunk c + 1 has landed (this wave's copies) ...
         __syncthreads();                // ... everyone's, and stage c & 1 is consumed
@@ -1209,6 +1219,104 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 8))
                 } else {
                     *o = gv / (1.0f + ref_expf_s(-gv)) * v;  // src/kernels_f32.cpp:287-289
                 }
+            }
+        }
+    }
+}
+
+// ---------------------------------------------------------------- Q4_K gate and up, fused
+
+// The gate and up projections of one row tile in one workgroup: both matrices' chunks are
+// staged beside one copy of the activations, and the epilogue applies the gate to the up
+// sums in registers (the pair's two launches stored the gate rows and read them back).
+// Each sum is the one k_mmk computes, in its term order, so the outputs are the same bits.
+struct KqPairStage {
+    alignas(16) uint8_t w0[64 * 128];  // gate: as KqStage<kQ4_K>
+    alignas(16) uint8_t wk[2048];
+    alignas(16) uint8_t u0[64 * 128];  // up
+    alignas(16) uint8_t uk[2048];
+    alignas(16) int8_t x[kKqTokMax * 256];
+    alignas(16) float xd[64];
+};
+
+__device__ __forceinline__ void kq_copy_w4k(uint8_t* w0, uint8_t* wk, const Packed& m, uint32_t r0, int c) {
+    const int tid = threadIdx.x, wave = tid >> 6, wave_first = tid & ~63;
+    const uint32_t nsb = m.cols / 256, rmax = m.rows - 1;
+    auto rowc = [&](int r) -> size_t {
+        const uint32_t rr = r0 + r <= rmax ? r0 + r : rmax;
+        return static_cast<size_t>(rr) * nsb + c;
+    };
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {  // 64 rows x 8 pieces
+        const int slot = k * kThreads + tid, r = slot >> 3, p = (slot & 7) ^ (r & 7);
+        dma16(m.p0 + rowc(r) * 128 + p * 16, w0 + (k * kThreads + wave_first) * 16);
+    }
+    if (wave < 2) {  // wave 0: the p1 rows, wave 1: the p2 rows
+        const int r = tid & 63;
+        dma16((wave ? m.p2 : m.p1) + rowc(r) * 16, wk + wave_first * 16);
+    }
+}
+
+template <int G>
+__device__ __forceinline__ void kq_copy_x(int8_t* xs, float* xd, const ActPlanar& x, int ntok, int t0, int c) {
+    const int tid = threadIdx.x, wave = tid >> 6, wave_first = tid & ~63;
+    auto tokc = [&](int t) -> size_t { return static_cast<size_t>(t0 + t < ntok ? t0 + t : ntok - 1); };
+    const size_t ds = x.stride / 32;
+#pragma unroll
+    for (int k = 0; k < G; ++k) {  // 16 G tokens x 16 pieces, G a thread
+        const int slot = k * kThreads + tid, t = slot >> 4, p = (slot & 15) ^ (t & 15);
+        dma16(x.qs + tokc(t) * x.stride + c * 256 + p * 16, xs + (k * kThreads + wave_first) * 16);
+    }
+    if (wave == 0) dma4(x.d + tokc(tid & (16 * G - 1)) * ds + c, xd);
+}
+
+template <int G>
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 8))) void k_mmk_pair(MmArgs g) {
+    __shared__ KqPairStage st[2];
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const uint32_t rt0 = blockIdx.x * 64;
+    const int t0 = blockIdx.y * (16 * G);
+    const int nc = static_cast<int>(g.m.cols / 256);
+    MmAcc<G> ag, au;
+#pragma unroll
+    for (int gi = 0; gi < G; ++gi)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) ag.s[gi][i] = au.s[gi][i] = 0.0f;
+    exp_tab_fill();  // ordered before the epilogue by the loop's barriers
+    auto copy = [&](KqPairStage& d, int c) {
+        kq_copy_w4k(d.w0, d.wk, g.m, rt0, c);
+        kq_copy_w4k(d.u0, d.uk, g.m2, rt0, c);
+        kq_copy_x<G>(d.x, d.xd, g.x, g.ntok, t0, c);
+    };
+    copy(st[0], 0);
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    for (int c = 0; c < nc; ++c) {
+        if (c + 1 < nc) copy(st[(c + 1) & 1], c + 1);
+        KqPairStage& cur = st[c & 1];
+        kq_compute_fold<G>(KqBases{lds_off(cur.w0), lds_off(cur.wk), lds_off(cur.x), lds_off(cur.xd)}, ag);
+        kq_compute_fold<G>(KqBases{lds_off(cur.u0), lds_off(cur.uk), lds_off(cur.x), lds_off(cur.xd)}, au);
+        __builtin_amdgcn_s_waitcnt(0);  // chunk c + 1 has landed (this wave's copies) ...
+        __syncthreads();                // ... everyone's, and stage c & 1 is consumed
+    }
+    const uint32_t rmax = g.m.rows - 1;
+#pragma unroll
+    for (int gi = 0; gi < G; ++gi) {
+        const int t = t0 + 16 * gi + (lane & 15);
+        if (t >= g.ntok) continue;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const uint32_t r = rt0 + wave * 16 + (lane >> 4) * 4 + i;
+            if (r > rmax) continue;
+            float* o = g.out + static_cast<size_t>(t) * g.ostride + r;
+            const float gv = ag.s[gi][i], v = au.s[gi][i];
+            if (g.relu2) {
+                const float q = gv > 0.0f ? gv : 0.0f;
+                *o = q * q * v;  // src/model.cpp:1134-1138
+            } else if (g.gelu) {
+                *o = gelu_mul(gv, v);  // src/kernels_f32.cpp:291-296
+            } else {
+                *o = gv / (1.0f + ref_expf_s(-gv)) * v;  // src/kernels_f32.cpp:287-289
             }
         }
     }
@@ -2010,6 +2118,12 @@ static hipError_t mm_dispatch(const MmArgs& g, hipStream_t s) {
     return hipGetLastError();
 }
 
+// BRISK_HIP_PAIR_SPLIT=1: Q4_K gate and up as two launches (the gate rows stored, then read back).
+static bool pair_split() {
+    const char* e = std::getenv("BRISK_HIP_PAIR_SPLIT");
+    return e != nullptr && std::string(e) == "1";
+}
+
 hipError_t launch_mm(const MmArgs& g, int mode, hipStream_t s) {
     if (g.ntok <= 0) return hipSuccess;
     if (g.m.cols % kChunkCols != 0 || g.x.stride % kChunkCols != 0) return hipErrorInvalidValue;
@@ -2017,7 +2131,18 @@ hipError_t launch_mm(const MmArgs& g, int mode, hipStream_t s) {
     switch (mode) {
         case kMmStore: return mm_dispatch<kMmStore>(g, s);
         case kMmAdd: return mm_dispatch<kMmAdd>(g, s);
-        case kMmPair: {  // the gate rows into out, then up with the gated epilogue
+        case kMmPair: {
+            if (g.m.type == kQ4_K && g.qx == nullptr && g.qx2 == nullptr && !pair_split()) {  // one fused launch
+                const int row_tiles = static_cast<int>((g.m.rows + 63) / 64);
+                int kq_g = 4;
+                while (kq_g > 1 && row_tiles * ((g.ntok + 16 * kq_g - 1) / (16 * kq_g)) < kKqCus) kq_g /= 2;
+                const dim3 grid(row_tiles, (g.ntok + 16 * kq_g - 1) / (16 * kq_g));
+                if (kq_g == 4) hipLaunchKernelGGL(k_mmk_pair<4>, grid, dim3(kThreads), 0, s, g);
+                else if (kq_g == 2) hipLaunchKernelGGL(k_mmk_pair<2>, grid, dim3(kThreads), 0, s, g);
+                else hipLaunchKernelGGL(k_mmk_pair<1>, grid, dim3(kThreads), 0, s, g);
+                return hipGetLastError();
+            }
+            // the gate rows into out, then up with the gated epilogue
             const hipError_t e = mm_dispatch<kMmStore>(g, s);
             if (e != hipSuccess) return e;
             MmArgs up = g;
