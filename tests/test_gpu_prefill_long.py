@@ -108,3 +108,30 @@ def test_mfma_attention_llama_512():
         else:
             np.testing.assert_array_equal(got.view(np.uint32), want.view(np.uint32))
         assert int(np.argmax(got)) == int(np.argmax(want))
+
+
+@pytest.mark.parametrize("name", ["tiny-llama", "tiny-q5k"])
+@pytest.mark.parametrize("env", [{}, {"BRISK_HIP_PAIR_SPLIT": "1"}, {"BRISK_HIP_PREFILL_MX": "0"}, {"BRISK_HIP_PREFILL_Q4X": "1"}],
+                         ids=["default", "pair-split", "packed-planes", "q4k-expanded"])
+def test_prefill_gemm_variants_exact(name, env):
+    """Every GEMM form of the prefill gives the oracle's logits to the bit: the fused Q4_K gate/up
+    (default) and its two-launch form, the expanded-plane GEMM (default for Q6_K / Q5_K) and the
+    packed-plane ones, and the expanded form for Q4_K."""
+    f, cfg, table = model.load(synth.model_path(name))
+    prompt = synth.prompt_ids(200, cfg.vocab, seed=5)
+    o = pyoracle.Oracle(cfg, table, 216)
+    want = o.eval(prompt)
+    o.close()
+    print(f"[prefill variants] {name} {env}", flush=True)
+    old = {k: os.environ.get(k) for k in env}
+    os.environ.update(env)
+    try:
+        with HipSession((f, cfg, table), max_context=216) as s:
+            got = s.eval(prompt)
+    finally:
+        for k, v in old.items():
+            if v is None:
+                os.environ.pop(k, None)
+            else:
+                os.environ[k] = v
+    np.testing.assert_array_equal(got.view(np.uint32), want.view(np.uint32))
