@@ -49,7 +49,8 @@ struct MxPlanes {
 // Rows the widest workgroup of the expanded-plane GEMM computes; the planes pad rows to it.
 constexpr int kMxRows = 128;
 // Formats the prefill multiplies from expanded planes: Q6_K and Q5_K; Q4_K when
-// BRISK_HIP_PREFILL_Q4X=1 (its packed-plane GEMM folds the scales without them).
+// BRISK_HIP_PREFILL_Q4X=1 (its packed-plane GEMM folds the scales without them); none when
+// BRISK_HIP_PREFILL_MX=0.
 bool mx_expanded(uint32_t type);
 // Bytes of a Q6_K, Q4_K or Q5_K matrix's expanded planes.
 size_t mx_bytes(uint32_t type, uint32_t rows, uint32_t cols);

@@ -2159,6 +2159,8 @@ hipError_t launch_mm(const MmArgs& g, int mode, hipStream_t s) {
 static bool mx_km(uint32_t type) { return type == kQ4_K || type == kQ5_K; }
 
 bool mx_expanded(uint32_t type) {
+    const char* off = std::getenv("BRISK_HIP_PREFILL_MX");  // "0": every format on the packed-plane GEMMs
+    if (off != nullptr && std::string(off) == "0") return false;
     if (type == kQ6_K || type == kQ5_K) return true;
     const char* e = std::getenv("BRISK_HIP_PREFILL_Q4X");
     return type == kQ4_K && e != nullptr && std::string(e) == "1";

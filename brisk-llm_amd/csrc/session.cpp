@@ -941,8 +941,6 @@ void Session::ensure_prefill() {
     pre_x_.qs = static_cast<int8_t*>(alloc(T * pre_x_.stride));
     pre_x_.d = static_cast<float*>(alloc(T * (pre_x_.stride / 32) * 4));
     pre_x_.bs = static_cast<int32_t*>(alloc(T * (pre_x_.stride / 16) * 4));
-    const char* qx = std::getenv("BRISK_HIP_PREFILL_MX");  // "0": every format through the packed-plane GEMMs
-    if (qx != nullptr && std::string(qx) == "0") return;
     for (Layer& L : layers_)
         for (DeviceMatrix* m : {&L.q, &L.k, &L.v, &L.o, &L.gate, &L.up, &L.down, &L.conv_in, &L.conv_out})
             if (m->mem != nullptr && mx_expanded(m->p.type) && m->xmem == nullptr) {

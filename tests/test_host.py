@@ -179,3 +179,45 @@ class _MetaOnly:
 
     def get(self, key, default=None):
         return self.metadata.get(key, default)
+
+
+def _mx_bytes(type_, rows, cols):
+    """The expanded planes a batched prefill holds for one matrix: int8 lo and hi weights (rows padded
+    to 128), float scales (Q4_K/Q5_K: d and dmin), and the K-quants' 8 sub-block mins a row."""
+    align = lambda n: (n + 255) // 256 * 256  # noqa: E731
+    rp, nsb = (rows + 127) // 128 * 128, cols // 256
+    km = type_ in (G.T_Q4_K, G.T_Q5_K)
+    return rp * cols * 2 + align(rp * nsb * (2 if km else 1) * 4) + (align(rp * nsb * 8) if km else 0)
+
+
+@pytest.mark.parametrize("name", ["tiny-llama", "tiny-q5k"])
+def test_session_estimate_counts_expanded_planes(name, monkeypatch):
+    """The estimate charges the prefill's expanded planes: switching Q4_K expansion on
+    (BRISK_HIP_PREFILL_Q4X=1) adds exactly their bytes for every Q4_K layer matrix."""
+    from brisk_hip.session import estimate
+    f, cfg, table = model.load(synth.model_path(name))
+    monkeypatch.delenv("BRISK_HIP_PREFILL_Q4X", raising=False)
+    base = estimate((f, cfg, table), 256)
+    monkeypatch.setenv("BRISK_HIP_PREFILL_Q4X", "1")
+    more = estimate((f, cfg, table), 256)
+    want = sum(_mx_bytes(t.type, t.rows, t.cols) for t in table if t.type == G.T_Q4_K and t.name.startswith("blk."))
+    assert more["scratch"] - base["scratch"] == want
+    assert (want > 0) == (name == "tiny-llama")
+    assert more["weights"] == base["weights"] and more["cache"] == base["cache"]
+
+
+@pytest.mark.parametrize("name", ["tiny-llama", "tiny-q5k"])
+def test_session_estimate_without_expanded_planes(name, monkeypatch):
+    """BRISK_HIP_PREFILL_MX=0 (every format on the packed-plane GEMMs) drops exactly the Q6_K and
+    Q5_K layer matrices' expanded planes from the estimate."""
+    from brisk_hip.session import estimate
+    f, cfg, table = model.load(synth.model_path(name))
+    monkeypatch.delenv("BRISK_HIP_PREFILL_Q4X", raising=False)
+    monkeypatch.delenv("BRISK_HIP_PREFILL_MX", raising=False)
+    base = estimate((f, cfg, table), 256)
+    monkeypatch.setenv("BRISK_HIP_PREFILL_MX", "0")
+    less = estimate((f, cfg, table), 256)
+    want = sum(_mx_bytes(t.type, t.rows, t.cols) for t in table
+               if t.type in (G.T_Q6_K, G.T_Q5_K) and t.name.startswith("blk.") and t.rows > 1)
+    assert want > 0
+    assert base["scratch"] - less["scratch"] == want
