@@ -2066,13 +2066,16 @@ __global__ __launch_bounds__(kThreads) void k_pre_attn_fa(PreAttnArgs p, int nto
 
 // ---------------------------------------------------------------- launchers
 
-// The expanded-plane GEMM: 4 waves (128 rows) a workgroup, fewer where that leaves compute units without one.
+// The expanded-plane GEMM: 4 waves (128 rows) a workgroup when that still gives every compute unit
+// two workgroups, else 2 waves, else 1.  At one wave a SIMD a CU holds four waves either way; smaller
+// workgroups couple fewer waves at each super-block's barrier (down on configs[2]: 59 us with 4
+// waves a workgroup, 50 with 2 or 1).
 template <int MODE, bool KM>
 static void mmx_launch(const MmArgs& g, hipStream_t s) {
     const int tt = (g.ntok + 31) / 32;
     auto tiles = [&](int w) { return static_cast<int>((g.m.rows + 32 * w - 1) / (32 * w)) * tt; };
-    if (tiles(4) >= kKqCus) hipLaunchKernelGGL((k_mmx<MODE, 1, 4, KM>), dim3(tiles(4)), dim3(256), 0, s, g);
-    else if (tiles(2) >= kKqCus) hipLaunchKernelGGL((k_mmx<MODE, 1, 2, KM>), dim3(tiles(2)), dim3(128), 0, s, g);
+    if (tiles(4) >= 2 * kKqCus) hipLaunchKernelGGL((k_mmx<MODE, 1, 4, KM>), dim3(tiles(4)), dim3(256), 0, s, g);
+    else if (tiles(2) >= 2 * kKqCus) hipLaunchKernelGGL((k_mmx<MODE, 1, 2, KM>), dim3(tiles(2)), dim3(128), 0, s, g);
     else hipLaunchKernelGGL((k_mmx<MODE, 1, 1, KM>), dim3(tiles(1)), dim3(64), 0, s, g);
 }
 
