@@ -630,18 +630,15 @@ void Session::setup_loop() {
             return;
     }
     // Every workgroup of the loop waits on others, so all of them must be resident at once: one
-    // workgroup a compute unit, within the occupancy (below).  The launch is cooperative, so the
-    // runtime refuses a grid it cannot place whole (a device shared with other work) instead of
-    // starting part of it; a device without cooperative launches takes the one-kernel-per-phase
-    // path.  BRISK_HIP_COOPERATIVE=0 makes it a plain launch, whose bounded waits then report an
-    // unplaceable grid as an error.
+    // workgroup a compute unit, within the occupancy (below).  BRISK_HIP_COOPERATIVE=1 makes the
+    // launch cooperative, so the runtime refuses a grid it cannot place whole (a device shared with
+    // other work); by default a plain launch, whose bounded waits report such a case as an error.
     int cus = 0, per_cu = 0;
-    {
-        const char* e = std::getenv("BRISK_HIP_COOPERATIVE");
-        loop_cooperative_ = e == nullptr || std::string(e) != "0";
+    if (const char* e = std::getenv("BRISK_HIP_COOPERATIVE")) {
         int coop = 0;
         check(hipDeviceGetAttribute(&coop, hipDeviceAttributeCooperativeLaunch, device_), "hipDeviceGetAttribute");
-        if (loop_cooperative_ && coop == 0) return;
+        loop_cooperative_ = std::string(e) != "0";
+        if (loop_cooperative_ && coop == 0) return;  // no cooperative launches: the one-kernel-per-phase path
     }
     check(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device_), "hipDeviceGetAttribute");
     check(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, k, kThreads, 0), "hipOccupancy");

@@ -135,7 +135,7 @@ private:
     // persistent loop
     const void* loop_kernel_ = nullptr;
     int loop_grid_ = 0;
-    bool loop_cooperative_ = true;  // the loop's launch is cooperative (BRISK_HIP_COOPERATIVE=0: plain)
+    bool loop_cooperative_ = false;  // BRISK_HIP_COOPERATIVE: launch the loop cooperatively
     LoopArgs loop_{};
     LayerDev* layers_dev_ = nullptr;
     unsigned* loop_done_ = nullptr;

@@ -117,11 +117,11 @@ def test_memory_preflight():
         assert s.eval_greedy(synth.prompt_ids(4, cfg.vocab)) >= 0
 
 
-def test_plain_loop_launch():
-    """BRISK_HIP_COOPERATIVE=0: the token loop launched as a plain kernel (the default launch is
-    cooperative: the runtime places the whole grid or refuses it) gives the same greedy ids as the oracle."""
+def test_cooperative_loop_launch():
+    """BRISK_HIP_COOPERATIVE=1: the token loop launched cooperatively (the runtime places the whole grid
+    or refuses it) gives the same greedy ids as the oracle."""
     f, cfg, table = model.load(synth.model_path("tiny-qwen3"))
-    os.environ["BRISK_HIP_COOPERATIVE"] = "0"
+    os.environ["BRISK_HIP_COOPERATIVE"] = "1"
     try:
         s = HipSession((f, cfg, table), max_context=128)
     finally:
