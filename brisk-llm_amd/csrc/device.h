@@ -801,19 +801,6 @@ __device__ __forceinline__ uint4 ld16(const uint8_t* p) {
     return make_uint4(v.x, v.y, v.z, v.w);
 }
 
-// Weight loads: each weight byte is read once a token, so the loads are
-// non-temporal (streamed through the L2 without displacing what is reused: the
-// layer descriptors, norm vectors, RoPE rows and hand-off words).
-__device__ __forceinline__ uint4 wld16(const uint8_t* p) {
-    typedef unsigned v4u __attribute__((ext_vector_type(4)));
-    const v4u v = __builtin_nontemporal_load(gmem(reinterpret_cast<const v4u*>(p)));
-    return make_uint4(v.x, v.y, v.z, v.w);
-}
-template <class T>
-__device__ __forceinline__ T wld(const void* p, size_t i) {
-    return __builtin_nontemporal_load(gmem(static_cast<const T*>(p)) + i);
-}
-
 template <uint32_t T> struct Unit;
 
 // dot_q4_0_q8_0 block term (src/quant.cpp:445-456): acc = sum((q - 8) x), exact;
@@ -825,8 +812,8 @@ template <> struct Unit<kQ4_0> {
     uint4 q;
     uint32_t d;
     __device__ __forceinline__ void load(const Packed& m, size_t blk) {
-        q = wld16(m.p0 + blk * 16);
-        d = wld<uint16_t>(m.p1, blk);
+        q = ld16(m.p0 + blk * 16);
+        d = gld<uint16_t>(m.p1, blk);
     }
     __device__ __forceinline__ float term(uint32_t b, const ActLds& a) const {
         const int32_t* x = a.xs + b * 8;
@@ -851,9 +838,9 @@ template <> struct Unit<kQ4_1> {
     uint4 q;
     uint32_t d, m;
     __device__ __forceinline__ void load(const Packed& mat, size_t blk) {
-        q = wld16(mat.p0 + blk * 16);
-        d = wld<uint16_t>(mat.p1, blk);
-        m = wld<uint16_t>(mat.p2, blk);
+        q = ld16(mat.p0 + blk * 16);
+        d = gld<uint16_t>(mat.p1, blk);
+        m = gld<uint16_t>(mat.p2, blk);
     }
     __device__ __forceinline__ float term(uint32_t b, const ActLds& a) const {
         const int32_t* x = a.xs + b * 8;
@@ -885,9 +872,9 @@ template <> struct Unit<kQ5_0> {
     uint4 q;
     uint32_t d, qh;
     __device__ __forceinline__ void load(const Packed& m, size_t blk) {
-        q = wld16(m.p0 + blk * 16);
-        d = wld<uint16_t>(m.p1, blk);
-        qh = wld<uint32_t>(m.p2, blk);
+        q = ld16(m.p0 + blk * 16);
+        d = gld<uint16_t>(m.p1, blk);
+        qh = gld<uint32_t>(m.p2, blk);
     }
     __device__ __forceinline__ float term(uint32_t b, const ActLds& a) const {
         const int32_t* x = a.xs + b * 8;
@@ -910,9 +897,9 @@ template <> struct Unit<kQ8_0> {
     uint4 q0, q1;
     uint32_t d;
     __device__ __forceinline__ void load(const Packed& m, size_t blk) {
-        q0 = wld16(m.p0 + blk * 32);
-        q1 = wld16(m.p0 + blk * 32 + 16);
-        d = wld<uint16_t>(m.p1, blk);
+        q0 = ld16(m.p0 + blk * 32);
+        q1 = ld16(m.p0 + blk * 32 + 16);
+        d = gld<uint16_t>(m.p1, blk);
     }
     __device__ __forceinline__ float term(uint32_t b, const ActLds& a) const {
         const int32_t* x = a.xs + b * 8;
@@ -944,8 +931,8 @@ template <> struct Unit<kQ4_K> {
     uint4 meta;  // d, dmin, scales[12]
     __device__ __forceinline__ void load(const Packed& m, size_t blk) {
 #pragma unroll
-        for (int i = 0; i < 8; ++i) q[i] = wld16(m.p0 + blk * 128 + 16 * i);
-        meta = wld16(m.p1 + blk * 16);
+        for (int i = 0; i < 8; ++i) q[i] = ld16(m.p0 + blk * 128 + 16 * i);
+        meta = ld16(m.p1 + blk * 16);
     }
     __device__ __forceinline__ float term(uint32_t b, const ActLds& a) const {
         const uint32_t mw[4] = {meta.x, meta.y, meta.z, meta.w};
@@ -985,10 +972,10 @@ template <> struct Unit<kQ5_K> {
     uint4 qh[2];  // qh[32]
     __device__ __forceinline__ void load(const Packed& m, size_t blk) {
 #pragma unroll
-        for (int i = 0; i < 8; ++i) q[i] = wld16(m.p0 + blk * 128 + 16 * i);
-        meta = wld16(m.p1 + blk * 16);
-        qh[0] = wld16(m.p2 + blk * 48 + 16);
-        qh[1] = wld16(m.p2 + blk * 48 + 32);
+        for (int i = 0; i < 8; ++i) q[i] = ld16(m.p0 + blk * 128 + 16 * i);
+        meta = ld16(m.p1 + blk * 16);
+        qh[0] = ld16(m.p2 + blk * 48 + 16);
+        qh[1] = ld16(m.p2 + blk * 48 + 32);
     }
     __device__ __forceinline__ float term(uint32_t b, const ActLds& a) const {
         const uint32_t mw[4] = {meta.x, meta.y, meta.z, meta.w};
@@ -1030,9 +1017,9 @@ template <> struct Unit<kQ6_K> {
     uint32_t meta[5];  // int8 scales[16], u16 d, pad
     __device__ __forceinline__ void load(const Packed& m, size_t blk) {
 #pragma unroll
-        for (int i = 0; i < 8; ++i) ql[i] = wld16(m.p0 + blk * 128 + 16 * i);
+        for (int i = 0; i < 8; ++i) ql[i] = ld16(m.p0 + blk * 128 + 16 * i);
 #pragma unroll
-        for (int i = 0; i < 4; ++i) qh[i] = wld16(m.p1 + blk * 64 + 16 * i);
+        for (int i = 0; i < 4; ++i) qh[i] = ld16(m.p1 + blk * 64 + 16 * i);
         const auto mp = gmem(reinterpret_cast<const uint32_t*>(m.p2 + blk * 20));
 #pragma unroll
         for (int i = 0; i < 5; ++i) meta[i] = mp[i];
@@ -1088,8 +1075,8 @@ template <> struct Unit<kTQ2_0> {
     bool lut16;
     __device__ __forceinline__ void load(const Packed& m, size_t blk) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) q[i] = wld16(m.p0 + blk * 64 + 16 * i);
-        d = wld<uint16_t>(m.p1, blk);
+        for (int i = 0; i < 4; ++i) q[i] = ld16(m.p0 + blk * 64 + 16 * i);
+        d = gld<uint16_t>(m.p1, blk);
         lut16 = (m.flags & kFlagLut16) != 0;
     }
     __device__ __forceinline__ float term(uint32_t b, const ActLds& a) const {
