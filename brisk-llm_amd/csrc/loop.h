@@ -72,6 +72,11 @@ struct LoopArgs {
     // order (phase F).  Tasks go to workgroups d_first, d_first + 1, ... (mod the grid).
     int push_ffn, d_first;
     unsigned long long* dtt;
+    // resident attention for contexts up to kResMax positions: the workgroups of the spread
+    // attention's second stage (task (kv head, 32-wide value slice)) hold the layer's cached keys
+    // and their value slice in LDS, loaded while the other phases run, and take the whole
+    // attention (no stage 1); phase A's tiles then go to the other workgroups
+    int res_ok;
 };
 
 constexpr int kOwnRows = 256;  // rows of h one workgroup can keep
@@ -81,6 +86,8 @@ int loop_units_per_thread(uint32_t type, bool head);
 bool loop_spread_fits(int heads, int kv_heads, int head_dim, int rope_dim, int grid);
 // Whether it takes every position of a context of `positions` (longer ones take the split attention).
 bool loop_spread_covers(int heads, int kv_heads, int head_dim, int grid, int positions);
+// Positions the resident attention takes (the context of a step, this token's included).
+int loop_resident_max();
 
 const void* find_loop_kernel(uint32_t tq, uint32_t tv, uint32_t to, uint32_t tg, uint32_t td, uint32_t th);
 hipError_t launch_loop(const void* kernel, const LoopArgs& g, int grid, hipStream_t s, bool cooperative);

@@ -786,6 +786,23 @@ void Session::setup_loop() {
         const int c_wgs = std::min(g.tiles_o, g.n_c);
         g.d_first = G - g.c_first - c_wgs >= tasks ? g.c_first + c_wgs : (g.c_first + g.n_c) % G;
     }
+    {
+        // the resident attention: its workgroups (the spread attention's stage-2 tasks, the first
+        // sp_n2) take no tiles of phases A, C, D and F, so their LDS holds the next layer's keys and
+        // values between attentions; phase A's tiles are planned over the other workgroups
+        const int n2 = g.sp_n2, hpk = static_cast<int>(cfg_.heads / cfg_.kv_heads);
+        bool ok = g.spread && g.c_first == n2 && hpk <= 4 && (cfg_.head_dim == 64 || cfg_.head_dim == 128) && L0.q.p.type == L0.v.p.type &&
+                  L0.q.p.type == L0.k.p.type && g.push_ffn && g.d_first >= n2 && g.d_first + tasks <= G && G - n2 >= 64;
+        if (const char* e = std::getenv("BRISK_HIP_RESIDENT")) ok = ok && std::string(e) != "0";
+        g.res_ok = ok ? 1 : 0;
+        if (ok) {
+            const int R = loop_rows({&L0.q.p, &L0.k.p, &L0.v.p}, G - n2);
+            for (int i = 0; i < 3; ++i) g.R_qkv[i] = R;
+            g.tiles_qkv[0] = tiles_of(L0.q.p, R);
+            g.tiles_qkv[1] = tiles_of(L0.k.p, R);
+            g.tiles_qkv[2] = tiles_of(L0.v.p, R);
+        }
+    }
     g.head_attn = static_cast<int>(cfg_.heads) <= G ? 1 : 0;
     if (const char* e = std::getenv("BRISK_HIP_HEAD_ATTN")) g.head_attn = g.head_attn && std::string(e) != "0";
     g.R_h = loop_rows({&out_->p}, G, true);
