@@ -72,11 +72,11 @@ struct LoopArgs {
     // order (phase F).  Tasks go to workgroups d_first, d_first + 1, ... (mod the grid).
     int push_ffn, d_first;
     unsigned long long* dtt;
-    // resident attention for contexts up to kResMax positions: the workgroups of the spread
-    // attention's second stage (task (kv head, 32-wide value slice)) hold the layer's cached keys
-    // and their value slice in LDS, loaded while the other phases run, and take the whole
-    // attention (no stage 1); phase A's tiles then go to the other workgroups
-    int res_ok;
+    // resident attention for contexts up to loop_resident_max() positions: workgroups
+    // 0 .. res_n - 1 (task: query head, 64-wide value slice) hold the layer's cached keys and
+    // their value slice in LDS, loaded while the other phases run, and take the whole attention;
+    // they take no tiles of phases A, C, D and F
+    int res_ok, res_n;
 };
 
 constexpr int kOwnRows = 256;  // rows of h one workgroup can keep

@@ -214,22 +214,24 @@ union SpreadLds {
     SpreadStage2 s2;
 };
 
-// The resident attention (short contexts): a stage-2 workgroup (kv head, value
-// slice) holds the layer's cached keys (whole heads) and its value slice,
+// The resident attention (short contexts): workgroup b < heads * (head_dim / 64)
+// takes query head b / (head_dim / 64) and a 64-wide slice of its values.  It
+// holds the layer's cached keys of that head's kv head and its value slice,
 // transposed, in LDS.  They are loaded after the workgroup's attention of the
 // layer before (at the start of a step for layer 0), while the other phases
 // run, so the attention itself waits only for this token's q, k and v.
-constexpr int kResMax = 384;                     // positions (this token's included)
+constexpr int kResMax = 320;                     // positions (this token's included)
+constexpr int kResSlice = 64;                    // value dimensions a task (one wave of chains)
 constexpr int kResVt = kResMax + 8;              // halves a transposed value row (16-byte aligned)
 constexpr int kResStage = 128;                   // value rows staged at a time for the transpose
 struct ResLds {
-    alignas(16) uint16_t keys[kResMax * 128];    // [position][dim]
-    alignas(16) uint16_t vt[kSpreadSlice * kResVt];             // [dim][position]
-    alignas(16) uint16_t vstage[kResStage * kSpreadSlice];      // value rows [position][dim]
-    alignas(16) float sc[kSpreadHpk * kResVt];   // scores, then weights [head][position]
-    alignas(16) float q[kSpreadHpk * 128];
+    alignas(16) uint16_t keys[kResMax * 128];    // [position][dim], 16-byte pieces swizzled by position
+    alignas(16) uint16_t vt[kResSlice * kResVt];                // [dim][position]
+    alignas(16) uint16_t vstage[kResStage * kResSlice];         // value rows [position][dim]
+    alignas(16) float sc[kResVt];                // scores, then weights
+    alignas(16) float q[128];
     alignas(16) float kcur[128];
-    alignas(16) float vcur[kSpreadSlice];
+    alignas(16) float vcur[kResSlice];
     float mx[4];
     double red[4];
 };
@@ -403,7 +405,7 @@ __device__ __forceinline__ bool phase_a(const LoopArgs& g, const LayerDev& L, in
     };
     if (TQ == TV) {
         // with the resident attention its workgroups (the first sp_n2) take no tiles
-        const int first = g.res_ok ? g.sp_n2 : 0;
+        const int first = g.res_ok ? g.res_n : 0;
         return run_tiles<TQ, kLoopUnits>(total, s, row_of, [&]() -> bool {
             ActRegs ar;
             act_issue_w(ar, L_attn_norm, static_cast<int>(L_q.cols));
@@ -1165,13 +1167,22 @@ __device__ __forceinline__ bool spread_stage2(const LoopArgs& g, const AttnArgs&
 
 // ---------------------------------------------------------------- resident attention
 
+// The resident attention's task of workgroup b: query head h, kv head kv, value slice at d0.
+struct ResTask {
+    int h, kv, d0;
+};
+__device__ __forceinline__ ResTask res_task(const LoopArgs& g, int b) {
+    const int ns = g.head_dim / kResSlice, h = b / ns;
+    return ResTask{h, h / g.sp_hpk, (b - h * ns) * kResSlice};
+}
+
 // Rows [0, n) of kv head kv's key cache (whole heads) and of the value slice at
 // d0, the values transposed to [dim][position], into LDS; by the whole
-// workgroup, ends with a barrier.  Keys go straight in by global_load_lds
-// (the LDS rows are the cache rows); values through a staging buffer.
-__device__ __forceinline__ void res_preload(const AttnArgs& a, ResLds& s, int kv, int d0, int n) {
+// workgroup, ends with a barrier.  Keys go straight in by global_load_lds;
+// values through a staging buffer.
+__device__ __forceinline__ void res_preload(const AttnArgs& a, ResLds& s, const ResTask& k, int n) {
     const int hd = a.head_dim, t = threadIdx.x, P = hd / 8;
-    const uint8_t* ksrc = reinterpret_cast<const uint8_t*>(a.kcache + static_cast<size_t>(kv) * a.ctx * hd);
+    const uint8_t* ksrc = reinterpret_cast<const uint8_t*>(a.kcache + static_cast<size_t>(k.kv) * a.ctx * hd);
     uint8_t* kdst = reinterpret_cast<uint8_t*>(s.keys);
     // LDS slot c of key row p holds the row's 16-byte piece c ^ (p & (P - 1)), so the score
     // loop's reads (consecutive positions at one piece) spread over the banks
@@ -1181,26 +1192,27 @@ __device__ __forceinline__ void res_preload(const AttnArgs& a, ResLds& s, int kv
             __builtin_amdgcn_global_load_lds((global_cvoid_ptr)(ksrc + (static_cast<size_t>(p) * P + c) * 16),
                                              (lds_void_ptr)(kdst + (base + (t & ~63)) * 16), 16, 0, 0);
     }
-    const uint8_t* vsrc = reinterpret_cast<const uint8_t*>(a.vcache + static_cast<size_t>(kv) * a.ctx * hd + d0);
+    constexpr int VP = kResSlice / 8;  // 16-byte pieces a value row of the slice
+    const uint8_t* vsrc = reinterpret_cast<const uint8_t*>(a.vcache + static_cast<size_t>(k.kv) * a.ctx * hd + k.d0);
     uint8_t* vdst = reinterpret_cast<uint8_t*>(s.vstage);
     for (int c0 = 0; c0 < n; c0 += kResStage) {
-        const int np = n - c0 < kResStage ? n - c0 : kResStage, pieces = np * 4;
+        const int np = n - c0 < kResStage ? n - c0 : kResStage, pieces = np * VP;
         for (int base = 0; base < pieces; base += kThreads) {
             const int i = base + t;
             if (i < pieces)
-                __builtin_amdgcn_global_load_lds((global_cvoid_ptr)(vsrc + static_cast<size_t>(c0 + (i >> 2)) * hd * 2 + (i & 3) * 16),
+                __builtin_amdgcn_global_load_lds((global_cvoid_ptr)(vsrc + static_cast<size_t>(c0 + i / VP) * hd * 2 + (i % VP) * 16),
                                                  (lds_void_ptr)(vdst + (base + (t & ~63)) * 16), 16, 0, 0);
         }
         __builtin_amdgcn_s_waitcnt(0);
         __syncthreads();
         // 8 x 8 blocks (8 positions by 8 dimensions) transposed in registers, the rest a half at a time
-        const int blocks = (np >> 3) * (kSpreadSlice / 8);
+        const int blocks = (np >> 3) * VP;
         for (int bi = t; bi < blocks; bi += kThreads) {
-            const int pb = (bi >> 2) * 8, c8 = (bi & 3) * 8;
+            const int pb = (bi / VP) * 8, c8 = (bi % VP) * 8;
             uint32_t in[8][4];
 #pragma unroll
             for (int q = 0; q < 8; ++q) {
-                const uint4 w = *reinterpret_cast<const uint4*>(s.vstage + (pb + q) * kSpreadSlice + c8);
+                const uint4 w = *reinterpret_cast<const uint4*>(s.vstage + (pb + q) * kResSlice + c8);
                 in[q][0] = w.x; in[q][1] = w.y; in[q][2] = w.z; in[q][3] = w.w;
             }
 #pragma unroll
@@ -1214,10 +1226,10 @@ __device__ __forceinline__ void res_preload(const AttnArgs& a, ResLds& s, int kv
                 *reinterpret_cast<uint4*>(s.vt + (c8 + j) * kResVt + c0 + pb) = o4;
             }
         }
-        const int tail0 = np & ~7, tail = (np - tail0) * kSpreadSlice;
+        const int tail0 = np & ~7, tail = (np - tail0) * kResSlice;
         for (int i = t; i < tail; i += kThreads) {
-            const int p = tail0 + i / kSpreadSlice, dd = i % kSpreadSlice;
-            s.vt[dd * kResVt + c0 + p] = s.vstage[p * kSpreadSlice + dd];
+            const int p = tail0 + i / kResSlice, dd = i % kResSlice;
+            s.vt[dd * kResVt + c0 + p] = s.vstage[p * kResSlice + dd];
         }
         __syncthreads();
     }
@@ -1226,20 +1238,19 @@ __device__ __forceinline__ void res_preload(const AttnArgs& a, ResLds& s, int kv
 }
 
 // Scores of the resident attention (dot_f32, src/kernels_f32.cpp:256-262, times
-// the scale) for every position: 4 threads a (head, position), thread r holding
-// dot_f32's lanes 4 r .. 4 r + 3 over the PER 16-value steps of the head; each
-// quad keeps one head, its query values in registers, and walks positions
-// g / hpk, + 64 / hpk, ...; the lanes are added in order along the quad (each
-// thread adding its four to the running sum broadcast from the thread before).
+// the scale) for every position: 4 threads a position, thread r holding
+// dot_f32's lanes 4 r .. 4 r + 3 over the PER 16-value steps of the head, its
+// query values in registers; quad g walks positions g, g + 64, ...; the lanes
+// are added in order along the quad (each thread adding its four to the
+// running sum broadcast from the thread before).
 template <int PER>
-__device__ __forceinline__ void res_scores(ResLds& s, int hpk, int Lc, int Ls, float scale) {
+__device__ __forceinline__ void res_scores(ResLds& s, int Lc, float scale) {
     constexpr int hd = PER * 16, P = hd / 8;
-    const int t = threadIdx.x, r = t & 3, g = t >> 2, h = g % hpk, step = (kThreads / 4) / hpk, p0 = g / hpk;
-    if (p0 >= step) return;  // (hpk = 3: the last quad has no head)
+    const int t = threadIdx.x, r = t & 3, g = t >> 2;
     float4 qr[PER];
 #pragma unroll
-    for (int m = 0; m < PER; ++m) qr[m] = *reinterpret_cast<const float4*>(s.q + h * hd + 16 * m + 4 * r);
-    for (int p = p0; p < Lc; p += step) {
+    for (int m = 0; m < PER; ++m) qr[m] = *reinterpret_cast<const float4*>(s.q + 16 * m + 4 * r);
+    for (int p = g; p < Lc; p += kThreads / 4) {
         const uint16_t* k = s.keys + p * hd + 4 * (r & 1);
         uint2 kw[PER];
 #pragma unroll
@@ -1258,59 +1269,56 @@ __device__ __forceinline__ void res_scores(ResLds& s, int hpk, int Lc, int Ls, f
         prev = dpp<0x55>(sum);
         if (r == 2) sum = (((prev + l0) + l1) + l2) + l3;
         prev = dpp<0xAA>(sum);
-        if (r == 3) s.sc[h * Ls + p] = ((((prev + l0) + l1) + l2) + l3) * scale;
+        if (r == 3) s.sc[p] = ((((prev + l0) + l1) + l2) + l3) * scale;
     }
 }
 
-// The whole attention of kv head kv's query heads for value slice d0 at
-// position pos (src/model.cpp:1020-1093), in the reference's order: wave 0
-// awaits this token's q, k and v slice; waves 1-3 normalise and rotate the
-// query heads and the key (pair_norm_rope); this token's cache rows of the
-// slice are stored; scores by dot_f32's 16 lanes in order over every position
-// (4 threads a score); softmax (max, glibc expf, double sum, multiply by the
-// float reciprocal); value sums one (head, dimension) chain a lane in
+// The attention of query head k.h for value slice k.d0 at position pos
+// (src/model.cpp:1020-1093), in the reference's order: wave 0 awaits this
+// token's q head, k and v slice; waves 1 and 2 normalise and rotate the query
+// head and the key (pair_norm_rope); the first query head of a kv head stores
+// this token's cache rows of the slice; scores by dot_f32's 16 lanes in order
+// (4 threads a score); softmax over the four waves (max, glibc expf, double sum,
+// multiply by the float reciprocal); value sums one dimension chain a lane in
 // position order; the outputs quantised for the O projection.
 template <class O>
-__device__ __forceinline__ bool res_attend(const LoopArgs& g, const AttnArgs& a, ResLds& s, int kv, int d0, int pos, unsigned tin,
+__device__ __forceinline__ bool res_attend(const LoopArgs& g, const AttnArgs& a, ResLds& s, const ResTask& k, int pos, unsigned tin,
                                            const O& o, const Stamps& st) {
-    const int hd = a.head_dim, hpk = g.sp_hpk, t = threadIdx.x, wave = t >> 6, lane = t & 63, Lc = pos + 1;
-    const int Ls = (Lc + 7) & ~7;
+    const int hd = a.head_dim, t = threadIdx.x, wave = t >> 6, lane = t & 63, Lc = pos + 1;
+    const int d0 = k.d0, kv = k.kv;
     const float* rope_row = a.rope != nullptr ? a.rope + static_cast<size_t>(pos) * a.rope_dim : nullptr;
     const Pair pr = rope_pair(lane, hd, a.neox);
-    PairConst kq{1.0f, 1.0f, 1.0f, 0.0f}, kk{1.0f, 1.0f, 1.0f, 0.0f};
-    if (wave != 0) {  // (wave 0 polls: a load issued before its poll would hold the poll's results back)
-        kq = pair_const(pr, a.qnorm, rope_row);
-        kk = pair_const(pr, a.knorm, rope_row);
-    }
+    PairConst kc{1.0f, 1.0f, 1.0f, 0.0f};
+    if (wave == 1) kc = pair_const(pr, a.qnorm, rope_row);  // (wave 0 polls: a load issued before its poll would
+    if (wave == 2) kc = pair_const(pr, a.knorm, rope_row);  //  hold the poll's results back)
     bool fail = false;
     if (wave == 0) {
         pst(st, 1);
-        fail = !wget_segs<8>(g, tin, TSeg{g.qt + kv * hpk * hd, s.q, hpk * hd}, TSeg{g.kt + kv * hd, s.kcur, hd},
-                             TSeg{g.vt + kv * hd + d0, s.vcur, kSpreadSlice});
+        fail = !wget_segs<4>(g, tin, TSeg{g.qt + k.h * hd, s.q, hd}, TSeg{g.kt + kv * hd, s.kcur, hd},
+                             TSeg{g.vt + kv * hd + d0, s.vcur, kResSlice});
     }
     if (__syncthreads_or(fail)) {
         __builtin_amdgcn_s_waitcnt(0);
         return false;
     }
     pst(st, 2);
-    for (int h = wave - 1; wave > 0 && h <= hpk; h += kThreads / 64 - 1) {
-        if (h < hpk)
-            pair_norm_rope(s.q + h * hd, pr, kq, a.qbias != nullptr ? a.qbias + (kv * hpk + h) * hd : nullptr, a.qnorm != nullptr,
-                           rope_row != nullptr, hd, a.eps);
-        else
-            pair_norm_rope(s.kcur, pr, kk, a.kbias != nullptr ? a.kbias + kv * hd : nullptr, a.knorm != nullptr, rope_row != nullptr,
-                           hd, a.eps);
-    }
+    if (wave == 1)
+        pair_norm_rope(s.q, pr, kc, a.qbias != nullptr ? a.qbias + k.h * hd : nullptr, a.qnorm != nullptr, rope_row != nullptr, hd, a.eps);
+    if (wave == 2)
+        pair_norm_rope(s.kcur, pr, kc, a.kbias != nullptr ? a.kbias + kv * hd : nullptr, a.knorm != nullptr, rope_row != nullptr, hd,
+                       a.eps);
     __syncthreads();
     // this token's key (fp16, as the cache holds it) and value slice join the LDS copies; the
-    // slice of both cache rows is stored (store_f16, src/kernels_f32.cpp:248-250)
+    // first query head of the kv head stores the slice of both cache rows (store_f16,
+    // src/kernels_f32.cpp:248-250)
     const int P = hd / 8;  // 16-byte pieces a key row, swizzled as res_preload stores them
     for (int i = t; i < hd; i += kThreads) s.keys[pos * hd + (((i >> 3) ^ (pos & (P - 1))) << 3) + (i & 7)] = f2h(s.kcur[i]);
-    if (t < kSpreadSlice) {
-        const float v = a.vbias != nullptr ? s.vcur[t] + gmem(a.vbias)[kv * hd + d0 + t] : s.vcur[t];
-        s.vt[t * kResVt + pos] = f2h(v);
+    if (t >= 64 && t < 64 + kResSlice) {
+        const int d = t - 64;
+        const float v = a.vbias != nullptr ? s.vcur[d] + gmem(a.vbias)[kv * hd + d0 + d] : s.vcur[d];
+        s.vt[d * kResVt + pos] = f2h(v);
     }
-    if (t < kSpreadSlice / 2) {  // wave 0, whose output lanes wait for these stores
+    if (t < kResSlice / 2 && k.h % g.sp_hpk == 0) {  // wave 0, whose output lanes wait for these stores
         const int d = 2 * t;
         uint16_t* kr = a.kcache + (static_cast<size_t>(kv) * a.ctx + pos) * hd + d0;
         uint16_t* vr = a.vcache + (static_cast<size_t>(kv) * a.ctx + pos) * hd + d0;
@@ -1326,34 +1334,39 @@ __device__ __forceinline__ bool res_attend(const LoopArgs& g, const AttnArgs& a,
     }
     __syncthreads();
     pst(st, 3);
-    if (hd == 128) res_scores<8>(s, hpk, Lc, Ls, a.scale);
-    else res_scores<4>(s, hpk, Lc, Ls, a.scale);
+    if (hd == 128) res_scores<8>(s, Lc, a.scale);
+    else res_scores<4>(s, Lc, a.scale);
     __syncthreads();
     pst(st, 4);
-    // softmax of each head's row (softmax_f32, src/kernels_f32.cpp:275-285), a wave a head
-    for (int h = wave; h < hpk; h += kThreads / 64) {
-        float* sc = s.sc + h * Ls;
+    // softmax (softmax_f32, src/kernels_f32.cpp:275-285) over the four waves: the max, the
+    // exponentials with their double sum (a double sum of floats is exact in any grouping over the
+    // range here), then every weight times the float reciprocal of the sum
+    {
         float m = -INFINITY;
-        for (int p = lane; p < Lc; p += 64) m = fmaxf(m, sc[p]);
+        for (int p = t; p < Lc; p += kThreads) m = fmaxf(m, s.sc[p]);
         m = wave_max(m);
+        if (lane == 0) s.mx[wave] = m;
+        __syncthreads();
+        m = fmaxf(fmaxf(s.mx[0], s.mx[1]), fmaxf(s.mx[2], s.mx[3]));
         double part = 0.0;
-        for (int p = lane; p < Lc; p += 64) {
-            const float e = ref_expf_s(sc[p] - m);
-            sc[p] = e;
+        for (int p = t; p < Lc; p += kThreads) {
+            const float e = ref_expf_s(s.sc[p] - m);
+            s.sc[p] = e;
             part += static_cast<double>(e);
         }
-        const float scale = static_cast<float>(1.0 / wave_sum(part));
-        for (int p = lane; p < Lc; p += 64) sc[p] *= scale;
+        part = wave_sum(part);
+        if (lane == 0) s.red[wave] = part;
+        __syncthreads();
+        const float scale = static_cast<float>(1.0 / (((s.red[0] + s.red[1]) + s.red[2]) + s.red[3]));
+        for (int p = t; p < Lc; p += kThreads) s.sc[p] *= scale;
     }
     __syncthreads();
     pst(st, 5);
-    // value sums (weighted_sum_f32, :265-273): one (head, dimension) chain a lane, positions in order,
-    // eight a round, each round's weights and values read two rounds ahead
-    const int chains = hpk * kSpreadSlice;
-    if (t < chains) {
-        const int h = t / kSpreadSlice, d = t - h * kSpreadSlice;
-        const float* w = s.sc + h * Ls;
-        const uint16_t* vrow = s.vt + d * kResVt;
+    // value sums (weighted_sum_f32, :265-273): one dimension chain a lane of wave 0, positions in
+    // order, eight a round, each round's weights and values read two rounds ahead
+    if (wave == 0) {
+        const float* w = s.sc;
+        const uint16_t* vrow = s.vt + lane * kResVt;
         const int full = Lc & ~7;
         float acc = 0.0f;
         int p = 0;
@@ -1388,7 +1401,7 @@ __device__ __forceinline__ bool res_attend(const LoopArgs& g, const AttnArgs& a,
         for (; p < Lc; ++p) acc += mul_h<false>(w[p], vrow[p]);
         __builtin_amdgcn_s_waitcnt(0);  // the cache rows are in memory before any output
         pst(st, 6);
-        o.att((kv * hpk + h) * hd + d0 + d, acc);
+        o.att(k.h * hd + d0 + lane, acc);
     }
     return true;
 }
@@ -1444,8 +1457,8 @@ __device__ __forceinline__ bool phase_b(const LoopArgs& g, const LayerDev& L, in
     const AttnArgs a = attn_args(g, L, step, l);
     const TaggedOut o{g.attt, g.pacct, g.pmlt, tout, g.error, g.att_q8, g.heads * g.head_dim};
     if (g.res_ok && Lc <= kResMax) {
-        if (geo.kv >= 0) return true;  // (a stage-1 workgroup of the spread geometry: no task)
-        return res_attend(g, a, lds.res, geo.kv2, geo.d0, pos, tin, o, pst_ptr(g, step, l, 1));
+        if (static_cast<int>(blockIdx.x) >= g.res_n) return true;
+        return res_attend(g, a, lds.res, res_task(g, blockIdx.x), pos, tin, o, pst_ptr(g, step, l, 1));
     }
     if (g.spread && (g.sp_all || spread_takes(g, Lc))) return phase_b_spread(g, a, step, l, pos, lds.spread, geo);
     if (attn_is_exact(Lc, hpk) && Lc <= kSplit * kPoolChunks && g.head_attn) {
@@ -1954,8 +1967,8 @@ __global__ __launch_bounds__(kThreads) void k_loop(LoopArgs g_arg) {
                 }
         }
         // the resident attention's workgroups load layer 0's keys and values
-        const bool res = lg().res_ok && pos + 1 <= kResMax && s_geo.kv < 0;
-        if (res) res_preload(attn_args(lg(), lg().layers[0], step, 0), lds.res, s_geo.kv2, s_geo.d0, pos);
+        const bool res = lg().res_ok && pos + 1 <= kResMax && static_cast<int>(blockIdx.x) < lg().res_n;
+        if (res) res_preload(attn_args(lg(), lg().layers[0], step, 0), lds.res, res_task(lg(), blockIdx.x), pos);
         for (int l = 0; l < lg().n_layers; ++l) {
             const LayerDev& L = lg().layers[l];
             if (lg().trace != nullptr && blockIdx.x == 0 && threadIdx.x == 0) lg().trace[1 + (step * lg().n_layers + l) * 5] = wall_clock64();
@@ -1973,7 +1986,7 @@ __global__ __launch_bounds__(kThreads) void k_loop(LoopArgs g_arg) {
             pst(pst_ptr(lg(), step, l, 1), 7);
             __syncthreads();
             // ... and, their attention of this layer done, the next layer's
-            if (res && l + 1 < lg().n_layers) res_preload(attn_args(lg(), lg().layers[l + 1], step, l + 1), lds.res, s_geo.kv2, s_geo.d0, pos);
+            if (res && l + 1 < lg().n_layers) res_preload(attn_args(lg(), lg().layers[l + 1], step, l + 1), lds.res, res_task(lg(), blockIdx.x), pos);
             if (lg().trace != nullptr && blockIdx.x == 0 && threadIdx.x == 0) lg().trace[3 + (step * lg().n_layers + l) * 5] = wall_clock64();
             pst(pst_ptr(lg(), step, l, 2), 0);
             if (!phase_c<TO>(lg(), L, step, l, token, lds.g, hown)) return;

@@ -790,11 +790,14 @@ void Session::setup_loop() {
         // the resident attention: its workgroups (the spread attention's stage-2 tasks, the first
         // sp_n2) take no tiles of phases A, C, D and F, so their LDS holds the next layer's keys and
         // values between attentions; phase A's tiles are planned over the other workgroups
-        const int n2 = g.sp_n2, hpk = static_cast<int>(cfg_.heads / cfg_.kv_heads);
-        bool ok = g.spread && g.c_first == n2 && hpk <= 4 && (cfg_.head_dim == 64 || cfg_.head_dim == 128) && L0.q.p.type == L0.v.p.type &&
-                  L0.q.p.type == L0.k.p.type && g.push_ffn && g.d_first >= n2 && g.d_first + tasks <= G && G - n2 >= 64;
+        const int hpk = static_cast<int>(cfg_.heads / cfg_.kv_heads);
+        const int n2 = static_cast<int>(cfg_.heads) * std::max(1, static_cast<int>(cfg_.head_dim) / 64);
+        bool ok = g.spread && n2 <= g.c_first && (cfg_.head_dim == 64 || cfg_.head_dim == 128) && hpk <= 4 &&
+                  L0.q.p.type == L0.v.p.type && L0.q.p.type == L0.k.p.type && g.push_ffn && g.d_first >= n2 &&
+                  g.d_first + tasks <= G && G - n2 >= 64;
         if (const char* e = std::getenv("BRISK_HIP_RESIDENT")) ok = ok && std::string(e) != "0";
         g.res_ok = ok ? 1 : 0;
+        g.res_n = ok ? n2 : 0;
         if (ok) {
             const int R = loop_rows({&L0.q.p, &L0.k.p, &L0.v.p}, G - n2);
             for (int i = 0; i < 3; ++i) g.R_qkv[i] = R;
