@@ -8,7 +8,9 @@ Errors raise ``BriskHipError`` (a RuntimeError) with the reference's messages.
 """
 from __future__ import annotations
 
+import atexit
 import ctypes as C
+import weakref
 
 import numpy as np
 
@@ -57,6 +59,11 @@ class HipSession:
 
     max_scored_tokens = 64  # Engine::kMaxScoredTokens
 
+    # Sessions still open when the interpreter exits are closed by an atexit hook, which runs
+    # before the HIP runtime's own exit handlers (a session destroyed after them would free
+    # streams and pinned buffers of a runtime already torn down).
+    _live = weakref.WeakSet()
+
     def __init__(self, source, max_context: int = 0, device: int = 0):
         L = _lib.load()
         self._L = L
@@ -69,6 +76,7 @@ class HipSession:
         _lib.check(L.brisk_hip_session_create(C.byref(hc), arr, len(table), max_context, device, C.byref(h)))
         self._h = h
         self.vocab = c.vocab
+        HipSession._live.add(self)
 
     def close(self):
         if getattr(self, "_h", None):
@@ -159,3 +167,9 @@ class HipSession:
                 mx = row.max()
                 total += (row[t[begin + i + 1]] - mx) - np.log(np.exp(row - mx).sum())
         return total
+
+
+@atexit.register
+def _close_live_sessions():
+    for s in list(HipSession._live):
+        s.close()

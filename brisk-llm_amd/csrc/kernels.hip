@@ -295,7 +295,8 @@ __global__ __launch_bounds__(kThreads) void k_attn(AttnArgs g) {
         if (g.rope != nullptr) g.rope += static_cast<size_t>(start) * g.rope_dim;
     }
     const int pos = pos_abs - start, L = pos + 1;
-    const bool exact = attn_is_exact(L, g.heads / g.kv_heads);
+    // exact-order attention at every length when the global score buffer is given
+    const bool exact = attn_is_exact(L, g.heads / g.kv_heads) || g.gsc != nullptr;
     if (exact ? split != 0 : split * kSplit >= L) return;
     attn_prologue<PlainIO>(g, s, kv, pos, exact || split == pos / kSplit);
     const PlainOut o{g.out, g.part_acc, g.part_ml};

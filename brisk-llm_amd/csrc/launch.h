@@ -63,6 +63,9 @@ struct AttnArgs {
     float* part_ml;       // [heads][max_splits][2]
     int max_splits;
     unsigned* tickets;    // [kv_heads], zero between launches (the merging workgroup re-arms its own)
+    // exact attention past the LDS score limit: the scores in global memory, [kv_heads][hpk][ctx]
+    // (null: such contexts take the split attention)
+    float* gsc;
     float* out;           // [heads][head_dim]
     unsigned long long* stamps;  // optional profiling: key/value head 0's wall clock at sub-phase ends
 };

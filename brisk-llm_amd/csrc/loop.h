@@ -86,6 +86,8 @@ int loop_units_per_thread(uint32_t type, bool head);
 bool loop_spread_fits(int heads, int kv_heads, int head_dim, int rope_dim, int grid);
 // Whether it takes every position of a context of `positions` (longer ones take the split attention).
 bool loop_spread_covers(int heads, int kv_heads, int head_dim, int grid, int positions);
+// Whether the pooled exact attention takes every length of a context of `positions`.
+bool loop_pool_covers(int hpk, int positions);
 // Positions the resident attention takes (the context of a step, this token's included).
 int loop_resident_max();
 

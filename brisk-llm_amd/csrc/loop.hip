@@ -465,149 +465,6 @@ __device__ __forceinline__ AttnArgs attn_args(const LoopArgs& g, const LayerDev&
     return a;
 }
 
-// ---------------------------------------------------------------- split attention (long contexts)
-
-constexpr int kSlotPos = 4 * kSplit;  // positions a split slot: four chunks of keys and four of values in the pool
-
-// Word offsets of slot `slot` of kv head `kv` in the partial buffers:
-// values [kv][slot][head][hd], (max, sum) [kv][slot][head][2].
-__device__ __forceinline__ size_t slot_acc(const AttnArgs& a, int kv, int slot) {
-    return static_cast<size_t>(kv * a.max_splits + slot) * (a.heads / a.kv_heads) * a.head_dim;
-}
-__device__ __forceinline__ size_t slot_ml(const AttnArgs& a, int kv, int slot) {
-    return static_cast<size_t>(kv * a.max_splits + slot) * (a.heads / a.kv_heads) * 2;
-}
-
-// Issues the cached key and value rows of the slot's chunks into pool chunks 0..3 and 4..7.
-__device__ __forceinline__ void attn_slot_issue(const AttnArgs& g, AttnPoolLds& s, int kv, int slot, int L) {
-    const int hd = g.head_dim;
-    const uint16_t* kbase = g.kcache + static_cast<size_t>(kv) * g.ctx * hd;
-    const uint16_t* vbase = g.vcache + static_cast<size_t>(kv) * g.ctx * hd;
-    for (int c = 0; c < 4; ++c) {
-        const int gc = slot * 4 + c, nn = chunk_cached(gc, L);
-        if (nn > 0) {
-            chunk_issue(s.chunk(c), kbase, gc * kSplit, nn, hd, true);
-            chunk_issue(s.chunk(4 + c), vbase, gc * kSplit, nn, hd, false);
-        }
-    }
-}
-
-// The slot's partial attention for each query head of the group: m = max score,
-// l = sum of exp(score - m), acc = sum of exp(score - m) v (flash-decoding).
-// The writer (the slot holding position L - 1) also stores the new cache rows.
-template <class O>
-__device__ __forceinline__ void attn_slot_partial(const AttnArgs& g, AttnPoolLds& sp, int kv, int slot, int L, bool writer,
-                                                  const O& o) {
-    AttnLds& s = sp.a;
-    const int hd = g.head_dim, hpk = g.heads / g.kv_heads, t = threadIdx.x, per = hd / 16;
-    const int P0 = slot * kSlotPos, n = L - P0 < kSlotPos ? L - P0 : kSlotPos, Ls = (n + 3) & ~3;
-    __builtin_amdgcn_s_waitcnt(0);
-    if (writer) {
-        const int r = L - 1 - P0;
-        pool_put_current(sp.chunk(r / kSplit), s.kcur, (r % kSplit) + 1, hd, true);
-        pool_put_current(sp.chunk(4 + r / kSplit), s.vcur, (r % kSplit) + 1, hd, false);
-    }
-    __syncthreads();
-    if (writer) attn_store_rows<true>(g, s, kv, L - 1);
-    const int P = kv_pieces(hd), mask = kv_mask(hd);
-    for (int i = t; i < hpk * n; i += kThreads) {
-        const int gq = i / n, p = i - gq * n;
-        const float* q = s.q + gq * hd;
-        const uint16_t* buf = sp.chunk(p / kSplit);
-        const int pr = p % kSplit;
-        const float v = per == 8 ? score_lane<8>(q, buf, pr, P, mask) : per == 6 ? score_lane<6>(q, buf, pr, P, mask)
-                      : per == 4 ? score_lane<4>(q, buf, pr, P, mask) : score_lane<2>(q, buf, pr, P, mask);
-        s.sc[gq * Ls + p] = v * g.scale;
-    }
-    __syncthreads();
-    const int wave = t >> 6, wl = t & 63;
-    for (int gq = wave; gq < hpk; gq += kThreads / 64) {
-        float* sc = s.sc + gq * Ls;
-        float m = -INFINITY;
-        for (int p = wl; p < n; p += 64) m = fmaxf(m, sc[p]);
-        m = wave_max(m);
-        double part = 0.0;
-        for (int p = wl; p < n; p += 64) {
-            const float e = ref_expf_s(sc[p] - m);
-            sc[p] = e;
-            part += static_cast<double>(e);
-        }
-        const double l = wave_sum(part);
-        if (writer) __builtin_amdgcn_s_waitcnt(0);  // the new cache rows are in memory before any output
-        if (wl == 0) {
-            const size_t ml = slot_ml(g, kv, slot) + gq * 2;
-            o.pml(ml, m);
-            o.pml(ml + 1, static_cast<float>(l));
-        }
-    }
-    __syncthreads();
-    const int chains = hpk * hd;
-    for (int ch = t; ch < chains; ch += kThreads) {
-        const int gq = ch / hd, d = ch % hd;
-        const float* w = s.sc + gq * Ls;
-        float acc = 0.0f;
-        int p = 0;
-        for (; p + 8 <= n; p += 8) {
-            float wv[8], vf[8];
-#pragma unroll
-            for (int u = 0; u < 8; ++u) {
-                wv[u] = w[p + u];
-                vf[u] = h2f(sp.chunk(4 + (p + u) / kSplit)[((p + u) % kSplit) * hd + d]);
-            }
-#pragma unroll
-            for (int u = 0; u < 8; ++u) acc += wv[u] * vf[u];
-        }
-        for (; p < n; ++p) acc += w[p] * h2f(sp.chunk(4 + p / kSplit)[(p % kSplit) * hd + d]);
-        o.pacc(slot_acc(g, kv, slot) + ch, acc);
-    }
-}
-
-// Merges kv head kv's ns slots: out = sum_s acc_s e^(m_s - M) / sum_s l_s e^(m_s - M), M = max_s m_s.
-// The partials are fetched in bulk (batches of slots into the pool) before any arithmetic.
-template <class O>
-__device__ __forceinline__ bool attn_slot_merge(const LoopArgs& lg, const AttnArgs& g, AttnPoolLds& sp, int kv, int ns,
-                                                unsigned tag, const O& o) {
-    const int hd = g.head_dim, hpk = g.heads / g.kv_heads, chains = hpk * hd, t = threadIdx.x;
-    float* buf = reinterpret_cast<float*>(sp.chunk(0));  // the pool as floats
-    constexpr int kPoolFloats = kPoolChunks * kSplit * 128 / 2;
-    const int per_slot = chains + 2 * hpk;
-    const int batch = kPoolFloats / per_slot;
-    // running merge for the outputs this thread owns (chains t, t + 256, ...; at most 4)
-    float M[4], num[4], den[4];
-#pragma unroll
-    for (int k = 0; k < 4; ++k) { M[k] = -INFINITY; num[k] = 0.0f; den[k] = 0.0f; }
-    for (int s0 = 0; s0 < ns; s0 += batch) {
-        const int nb = ns - s0 < batch ? ns - s0 : batch;
-        __syncthreads();
-        if (!tget_segs<16>(lg, tag, TSeg{lg.pacct + slot_acc(g, kv, s0), buf, nb * chains},
-                           TSeg{lg.pmlt + slot_ml(g, kv, s0), buf + nb * chains, nb * 2 * hpk}))
-            return false;
-        const float* ml = buf + nb * chains;
-#pragma unroll
-        for (int k = 0; k < 4; ++k) {
-            const int ch = t + k * kThreads;
-            if (ch >= chains) continue;
-            const int gq = ch / hd;
-            float Mn = M[k];
-            for (int j = 0; j < nb; ++j) Mn = fmaxf(Mn, ml[(j * hpk + gq) * 2]);
-            const float r = M[k] == -INFINITY ? 0.0f : ref_expf_s(M[k] - Mn);
-            float nu = num[k] * r, de = den[k] * r;
-            for (int j = 0; j < nb; ++j) {
-                const float f = ref_expf_s(ml[(j * hpk + gq) * 2] - Mn);
-                de += ml[(j * hpk + gq) * 2 + 1] * f;
-                nu += buf[j * chains + ch] * f;
-            }
-            M[k] = Mn; num[k] = nu; den[k] = de;
-        }
-    }
-#pragma unroll
-    for (int k = 0; k < 4; ++k) {
-        const int ch = t + k * kThreads;
-        if (ch < chains) o.att(kv * chains + ch, num[k] / den[k]);
-    }
-    return true;
-}
-
 // ---------------------------------------------------------------- per-head exact attention
 
 // Tagged values into LDS by one wave (no barrier); false when abandoning.
@@ -1488,30 +1345,10 @@ __device__ __forceinline__ bool phase_b(const LoopArgs& g, const LayerDev& L, in
         else attn_exact_pool<0>(a, sp, kv, Lc, o);
         return true;
     }
-    // split-K: slots of kSlotPos positions a (kv head, slot) task, then one merge a kv head
-    const int ns = (Lc + kSlotPos - 1) / kSlotPos, tasks = ns * kvh, G = static_cast<int>(gridDim.x);
-    AttnPoolLds& sp = lds.pool;
-    for (int task = blockIdx.x; task < tasks; task += G) {
-        const int kv = task % kvh, slot = task / kvh;
-        const bool writer = slot == pos / kSlotPos;
-        attn_slot_issue(a, sp, kv, slot, Lc);  // the slot's cached keys and values stream in while q/k/v are awaited
-        if (!tget_segs<>(g, tin, TSeg{g.qt + kv * hpk * hd, sp.a.q, hpk * hd},
-                         writer ? TSeg{g.kt + kv * hd, sp.a.kcur, hd} : TSeg{nullptr, nullptr, 0},
-                         writer ? TSeg{g.vt + kv * hd, sp.a.vcur, hd} : TSeg{nullptr, nullptr, 0})) {
-            __builtin_amdgcn_s_waitcnt(0);
-            return false;
-        }
-        attn_finish_prologue<true>(a, sp.a, kv, pos, writer, false);
-        attn_slot_partial(a, sp, kv, slot, Lc, writer, o);
-        __syncthreads();
-    }
-    // the merge of kv head k runs on workgroup G - 1 - k when that one had no slot task
-    for (int kv = 0; kv < kvh; ++kv) {
-        const int wg = G - 1 - kv >= tasks ? G - 1 - kv : kv;
-        if (static_cast<int>(blockIdx.x) != wg) continue;
-        if (!attn_slot_merge(g, a, sp, kv, ns, tout, o)) return false;
-    }
-    return true;
+    // no other case reaches the loop: the session takes the one-kernel-per-phase path for a
+    // context that neither the spread nor the pooled exact attention takes whole
+    atomicExch(g.error, 1);
+    return false;
 }
 
 // C: O rows of att, h += O att.  With own_h the residual rows come from the
@@ -2066,6 +1903,8 @@ bool loop_spread_fits(int heads, int kv_heads, int head_dim, int rope_dim, int g
 }
 
 int loop_resident_max() { return kResMax; }
+
+bool loop_pool_covers(int hpk, int positions) { return attn_is_exact(positions, hpk) && positions <= kSplit * kPoolChunks; }
 
 bool loop_spread_covers(int heads, int kv_heads, int head_dim, int grid, int positions) {
     const int per_kv = (grid - kv_heads * (head_dim / kSpreadSlice)) / kv_heads;

@@ -417,6 +417,8 @@ template <class O>
 __device__ __forceinline__ void attn_exact(const AttnArgs& g, AttnLds& s, int kv, int L, const O& o, bool k0_issued = false,
                                            bool store_rows = false) {
     const int hd = g.head_dim, hpk = g.heads / g.kv_heads, t = threadIdx.x, per = hd / 16;
+    // the scores in LDS when they fit it, else in the global buffer (same order of every operation)
+    float* const scores = L * hpk <= kExactScores ? s.sc : g.gsc + static_cast<size_t>(kv) * hpk * g.ctx;
     const int nchunks = (L + kSplit - 1) / kSplit;
     const uint16_t* kbase = g.kcache + static_cast<size_t>(kv) * g.ctx * hd;
     const uint16_t* vbase = g.vcache + static_cast<size_t>(kv) * g.ctx * hd;
@@ -433,7 +435,7 @@ __device__ __forceinline__ void attn_exact(const AttnArgs& g, AttnLds& s, int kv
             const float* q = s.q + gq * hd;
             const float v = per == 8 ? score_lane<8>(q, kvb, p, P, mask) : per == 6 ? score_lane<6>(q, kvb, p, P, mask)
                           : per == 4 ? score_lane<4>(q, kvb, p, P, mask) : score_lane<2>(q, kvb, p, P, mask);
-            s.sc[gq * L + p0 + p] = v * g.scale;
+            scores[gq * L + p0 + p] = v * g.scale;
         }
     }
     // the first value chunk streams in while the softmax runs
@@ -447,7 +449,7 @@ __device__ __forceinline__ void attn_exact(const AttnArgs& g, AttnLds& s, int kv
     // ---- softmax, a wave per head
     const int wave = t >> 6, wl = t & 63;
     for (int gq = wave; gq < hpk; gq += kThreads / 64) {
-        float* sc = s.sc + gq * L;
+        float* sc = scores + gq * L;
         float m = -INFINITY;
         for (int p = wl; p < L; p += 64) m = fmaxf(m, sc[p]);
         m = wave_max(m);
@@ -474,7 +476,7 @@ __device__ __forceinline__ void attn_exact(const AttnArgs& g, AttnLds& s, int kv
             const int ch = t + k * kThreads;
             if (ch < chains) {
                 const int gq = ch / hd, d = ch % hd;
-                const float* w = s.sc + gq * L + p0;
+                const float* w = scores + gq * L + p0;
                 const uint16_t* vv = kvb + d;
                 float a = acc[k];
                 int p = 0;

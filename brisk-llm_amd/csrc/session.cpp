@@ -473,6 +473,9 @@ Session::Session(const brisk_hip_config& cfg, const brisk_hip_tensor* tensors, s
 }
 
 Session::~Session() {
+    // the stream's work (a loop launch, copies into the pinned staging buffer) is done before any
+    // graph, allocation or the stream itself is released
+    if (stream_) (void)hipStreamSynchronize(stream_);
     if (graph_layers_) (void)hipGraphExecDestroy(graph_layers_);
     if (graph_full_) (void)hipGraphExecDestroy(graph_full_);
     for (void* p : owned_) (void)hipFree(p);
@@ -554,6 +557,9 @@ void Session::record_step(bool full) {
         aa.heads = static_cast<int>(cfg_.heads); aa.kv_heads = static_cast<int>(cfg_.kv_heads);
         aa.scale = scale; aa.part_acc = part_acc_; aa.part_ml = part_ml_; aa.max_splits = max_splits_;
         aa.tickets = ticket_ + 4; aa.out = att_;
+        // scores past the LDS limit go to the split buffers: heads x ctx floats fit them
+        // (heads x max_splits x head_dim, head_dim >= the split length)
+        aa.gsc = cfg_.head_dim >= static_cast<uint32_t>(kSplit) ? part_acc_ : nullptr;
         check(launch_attention(aa, stream_), "attention");
 
         // h += W_o att, or with a post-norm h += rms_norm(W_o att) (src/model.cpp:1113-1121)
@@ -615,7 +621,7 @@ void Session::setup_loop() {
     const char* path = std::getenv("BRISK_HIP_PATH");
     if (path != nullptr && std::string(path) == "graph") return;
     if (debug_) return;
-    // the loop's split attention merges at most 4 outputs a thread (heads per kv head x head size <= 1024)
+    // the loop's exact attentions hold at most 4 outputs a thread (heads per kv head x head size <= 1024)
     if ((cfg_.heads / cfg_.kv_heads) * cfg_.head_dim > 4 * kThreads) return;
     if (embd_.p.type != out_->p.type) return;  // the loop reads the embedding in its output's format
     if (gemma() || lfm2()) return;  // post-norms, windows, softcap and convolutions are graph-path phases only
@@ -643,6 +649,17 @@ void Session::setup_loop() {
     check(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device_), "hipDeviceGetAttribute");
     check(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, k, kThreads, 0), "hipOccupancy");
     if (cus <= 0 || per_cu < 1 || cus < static_cast<int>(cfg_.kv_heads)) return;
+    {
+        // the loop only where its attention keeps the reference's order at every length of the
+        // context: the spread attention takes all of it, or the pooled exact attention does.  Other
+        // sessions take the one-kernel-per-phase path, whose attention is order-exact at any length.
+        const int heads = static_cast<int>(cfg_.heads), kvh = static_cast<int>(cfg_.kv_heads), hd = static_cast<int>(cfg_.head_dim);
+        const int ctx = static_cast<int>(max_ctx_);
+        bool spread_ok = loop_spread_fits(heads, kvh, hd, rope_dim_, cus) && loop_spread_covers(heads, kvh, hd, cus, ctx);
+        if (const char* e = std::getenv("BRISK_HIP_SPREAD")) spread_ok = spread_ok && std::string(e) != "0";
+        const bool pool_ok = loop_pool_covers(heads / kvh, ctx);
+        if (!spread_ok && !pool_ok) return;
+    }
     loop_grid_ = cus;  // one resident workgroup per CU: the barrier needs every workgroup resident
     loop_kernel_ = k;
 
@@ -778,7 +795,14 @@ void Session::setup_loop() {
                ((cfg_.heads / cfg_.kv_heads) * cfg_.head_dim) % 32 == 0 ? 1 : 0;
     if (const char* e = std::getenv("BRISK_HIP_ATT_Q8")) g.att_q8 = g.att_q8 && std::string(e) != "0";
     g.tiles_d = tiles_of(L0.down.p, g.R_d);
-    g.push_ffn = push && g.own_h ? 1 : 0;
+    // the pushed phase F sums every owned row's ff / 32 terms in LDS: they must fit the term buffer
+    const bool push_fits = static_cast<size_t>((g.tiles_o + Gc - 1) / Gc) * g.R_o * term_stride(cfg_.ff / 32) <= kTermCap;
+    g.push_ffn = push && g.own_h && push_fits ? 1 : 0;
+    if (!g.push_ffn && push) {  // not pushed after all: phase F tiles the down rows on their own
+        g.R_d = loop_rows({&L0.down.p}, Gc);
+        g.tiles_d = tiles_of(L0.down.p, g.R_d);
+        g.own_h = 0;
+    }
     {
         // the pushed phase D's tasks on the workgroups past those with O tiles, if there are enough
         // (the stage-2 attention workgroups, which finish phase B last, then take none); else from

@@ -76,7 +76,8 @@ def _h2d(dst_ptr, host, nbytes):
 
 def test_config3_long_context():
     """Qwen3-1.7B-shape Q8_0, K/V pre-filled to 4096 positions (the fixture's seeded values,
-    regenerated here layer by layer, key then value), then 32 greedy steps (split-K attention)."""
+    regenerated here layer by layer, key then value), then the fixture's greedy steps (the loop's
+    exact spread attention)."""
     g = fixture("qwen3-1.7b_kv4096_steps.json")
     f, cfg, table = model.load(synth.model_path(g["model"]))
     n_pos, n = g["kv_positions"], len(g["ids"])

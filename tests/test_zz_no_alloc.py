@@ -19,9 +19,9 @@ from brisk_hip import lib as L  # noqa: E402
 from brisk_hip import synth  # noqa: E402
 import pyoracle  # noqa: E402
 
-Q4_0, Q8_0, Q4_K, Q6_K, TQ2_0 = 2, 8, 12, 14, 35
-BLOCK = {Q4_0: (32, 18), Q8_0: (32, 34), Q4_K: (256, 144), Q6_K: (256, 210), TQ2_0: (256, 66)}
-Q8K = (Q4_K, Q6_K, TQ2_0)
+Q4_0, Q8_0, Q4_K, Q5_K, Q6_K, TQ2_0 = 2, 8, 12, 13, 14, 35
+BLOCK = {Q4_0: (32, 18), Q8_0: (32, 34), Q4_K: (256, 144), Q5_K: (256, 176), Q6_K: (256, 210), TQ2_0: (256, 66)}
+Q8K = (Q4_K, Q5_K, Q6_K, TQ2_0)
 
 
 def dev(a):
@@ -54,7 +54,7 @@ def quantised_rows(orc, type_, rows, cols, n, seed):
 
 
 @pytest.mark.parametrize("type_,rows,cols", [(Q4_0, 1024, 2048), (Q8_0, 300, 1024), (Q4_K, 512, 2048),
-                                              (Q6_K, 256, 8192), (TQ2_0, 640, 2560)])
+                                              (Q5_K, 512, 2048), (Q6_K, 256, 8192), (TQ2_0, 640, 2560)])
 def test_noalloc_matmul_matches_matmul(lib, type_, rows, cols):
     orc = pyoracle.oracle_lib()
     be, _ = BLOCK[type_]
