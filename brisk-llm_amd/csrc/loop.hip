@@ -808,6 +808,56 @@ __device__ __forceinline__ bool spread_stage1(const LoopArgs& g, const AttnArgs&
     return true;
 }
 
+// A value chain of the exact attention over positions [p, full) (full - p a multiple of 8):
+// acc += w[q] * v[q] in position order, w the float weights and v the fp16 values of one
+// dimension (transposed rows), both in LDS.  Eight positions a round, each round's three LDS
+// reads issued two rounds ahead as inline assembly with counted waits (the compiler would wait
+// for every read before the first use); the products are v_fma_mix_f32's rounded float products.
+__device__ __forceinline__ float value_chain(const float* w, const uint16_t* vrow, int p, int full, float acc) {
+    typedef float f4 __attribute__((ext_vector_type(4)));
+    typedef unsigned u4 __attribute__((ext_vector_type(4)));
+    struct Round {
+        f4 w0, w1;
+        u4 v;
+    };
+    typedef __attribute__((address_space(3))) const void* lds_cptr;
+    const uint32_t wb = static_cast<uint32_t>(reinterpret_cast<uintptr_t>((lds_cptr)w));
+    const uint32_t vb = static_cast<uint32_t>(reinterpret_cast<uintptr_t>((lds_cptr)vrow));
+    auto rd = [&](int q) {
+        const int qc = q < full ? q : full - 8;  // past the end: the last round again (unused)
+        Round r;
+        asm volatile("ds_read_b128 %0, %1" : "=v"(r.w0) : "v"(wb + 4 * qc));
+        asm volatile("ds_read_b128 %0, %1 offset:16" : "=v"(r.w1) : "v"(wb + 4 * qc));
+        asm volatile("ds_read_b128 %0, %1" : "=v"(r.v) : "v"(vb + 2 * qc));
+        return r;
+    };
+    auto sum = [&](const Round& r) {
+        acc += mul_h<false>(r.w0.x, r.v.x); acc += mul_h<true>(r.w0.y, r.v.x);
+        acc += mul_h<false>(r.w0.z, r.v.y); acc += mul_h<true>(r.w0.w, r.v.y);
+        acc += mul_h<false>(r.w1.x, r.v.z); acc += mul_h<true>(r.w1.y, r.v.z);
+        acc += mul_h<false>(r.w1.z, r.v.w); acc += mul_h<true>(r.w1.w, r.v.w);
+    };
+    if (full <= p) return acc;
+    // rounds at p, p + 8, ...: ra and rb hold the next two; three rounds an iteration, the names
+    // rotated rather than copied; each wait leaves the later round's three reads in flight
+    Round ra = rd(p), rb = rd(p + 8), rc;
+    for (; p + 24 <= full; p += 24) {
+        asm volatile("s_waitcnt lgkmcnt(3)" : "+v"(ra.w0), "+v"(ra.w1), "+v"(ra.v));
+        rc = rd(p + 16);
+        sum(ra);
+        asm volatile("s_waitcnt lgkmcnt(3)" : "+v"(rb.w0), "+v"(rb.w1), "+v"(rb.v));
+        ra = rd(p + 24);
+        sum(rb);
+        asm volatile("s_waitcnt lgkmcnt(3)" : "+v"(rc.w0), "+v"(rc.w1), "+v"(rc.v));
+        rb = rd(p + 32);
+        sum(rc);
+    }
+    asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(ra.w0), "+v"(ra.w1), "+v"(ra.v), "+v"(rb.w0), "+v"(rb.w1), "+v"(rb.v));
+    if (p < full) { sum(ra); p += 8; }
+    if (p < full) sum(rb);
+    return acc;
+}
+
 template <class O>
 __device__ __forceinline__ bool spread_stage2(const LoopArgs& g, const AttnArgs& a, SpreadStage2& s, int kv, int d0, int pos,
                                               unsigned tin, unsigned tsc, const O& o, const Stamps& st) {
@@ -976,36 +1026,8 @@ __device__ __forceinline__ bool spread_stage2(const LoopArgs& g, const AttnArgs&
             const uint16_t* vrow = s.vt[c & 1] + d * kVtStride - p0;
             const int full = p0 + ((pe - p0) & ~7);
             int p = p0;
-            if (full > p0) {  // eight positions a round, each round's weights and values read two rounds ahead
-                struct Round {
-                    float4 w0, w1;
-                    uint4 v;
-                };
-                auto rd = [&](int q) {
-                    const int qc = q < full ? q : full - 8;  // past the end: the last round again (unused)
-                    return Round{*reinterpret_cast<const float4*>(w + qc), *reinterpret_cast<const float4*>(w + qc + 4),
-                                 *reinterpret_cast<const uint4*>(vrow + qc)};
-                };
-                auto sum = [&](const Round& r) {
-                    acc += mul_h<false>(r.w0.x, r.v.x); acc += mul_h<true>(r.w0.y, r.v.x);
-                    acc += mul_h<false>(r.w0.z, r.v.y); acc += mul_h<true>(r.w0.w, r.v.y);
-                    acc += mul_h<false>(r.w1.x, r.v.z); acc += mul_h<true>(r.w1.y, r.v.z);
-                    acc += mul_h<false>(r.w1.z, r.v.w); acc += mul_h<true>(r.w1.w, r.v.w);
-                };
-                // rounds at p, p + 8, ...: ra and rb hold the next two; three rounds an iteration,
-                // the names rotated rather than copied
-                Round ra = rd(p), rb = rd(p + 8);
-                for (; p + 24 <= full; p += 24) {
-                    const Round rc = rd(p + 16);
-                    sum(ra);
-                    ra = rd(p + 24);
-                    sum(rb);
-                    rb = rd(p + 32);
-                    sum(rc);
-                }
-                if (p < full) { sum(ra); p += 8; }
-                if (p < full) { sum(rb); p += 8; }
-            }
+            acc = value_chain(w, vrow, p0, full, acc);
+            p = full;
             for (; p < pe; ++p) acc += mul_h<false>(w[p], vrow[p]);
         } else if (wave >= cw && c + 1 < chunks) {
             __builtin_amdgcn_s_waitcnt(0);
@@ -1225,36 +1247,8 @@ __device__ __forceinline__ bool res_attend(const LoopArgs& g, const AttnArgs& a,
         const float* w = s.sc;
         const uint16_t* vrow = s.vt + lane * kResVt;
         const int full = Lc & ~7;
-        float acc = 0.0f;
-        int p = 0;
-        if (full > 0) {
-            struct Round {
-                float4 w0, w1;
-                uint4 v;
-            };
-            auto rd = [&](int q) {
-                const int qc = q < full ? q : full - 8;  // past the end: the last round again (unused)
-                return Round{*reinterpret_cast<const float4*>(w + qc), *reinterpret_cast<const float4*>(w + qc + 4),
-                             *reinterpret_cast<const uint4*>(vrow + qc)};
-            };
-            auto sum = [&](const Round& rr) {
-                acc += mul_h<false>(rr.w0.x, rr.v.x); acc += mul_h<true>(rr.w0.y, rr.v.x);
-                acc += mul_h<false>(rr.w0.z, rr.v.y); acc += mul_h<true>(rr.w0.w, rr.v.y);
-                acc += mul_h<false>(rr.w1.x, rr.v.z); acc += mul_h<true>(rr.w1.y, rr.v.z);
-                acc += mul_h<false>(rr.w1.z, rr.v.w); acc += mul_h<true>(rr.w1.w, rr.v.w);
-            };
-            Round ra = rd(0), rb = rd(8);
-            for (; p + 24 <= full; p += 24) {
-                const Round rc = rd(p + 16);
-                sum(ra);
-                ra = rd(p + 24);
-                sum(rb);
-                rb = rd(p + 32);
-                sum(rc);
-            }
-            if (p < full) { sum(ra); p += 8; }
-            if (p < full) { sum(rb); p += 8; }
-        }
+        float acc = value_chain(w, vrow, 0, full, 0.0f);
+        int p = full;
         for (; p < Lc; ++p) acc += mul_h<false>(w[p], vrow[p]);
         __builtin_amdgcn_s_waitcnt(0);  // the cache rows are in memory before any output
         pst(st, 6);

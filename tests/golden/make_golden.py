@@ -100,7 +100,7 @@ def steps_fixture(name):
     print(f"{name}: {n_gen} steps in {time.time() - t0:.1f}s -> {dst}", flush=True)
 
 
-def long_context_fixture(n_pos=4096, n_gen=32, kv_seed=7, token=11):
+def long_context_fixture(n_pos=4096, n_gen=128, kv_seed=7, token=11):
     """Qwen3-1.7B-shape Q8_0 with every layer's K and V cache pre-filled to n_pos positions
     with seeded fp16 N(0,1) values (numpy default_rng(kv_seed), layer by layer, key then value), then
     greedy steps from `token`.  Run by the oracle (the C restatement, which takes a pre-filled cache)."""
