@@ -404,16 +404,16 @@ __device__ __forceinline__ bool phase_a(const LoopArgs& g, const LayerDev& L, in
         return true;
     };
     if (TQ == TV) {
-        // with the resident attention its workgroups (the first sp_n2) take no tiles
-        const int first = g.res_ok ? g.res_n : 0;
-        return run_tiles<TQ, kLoopUnits>(total, s, row_of, [&]() -> bool {
+        auto ready = [&]() -> bool {
             ActRegs ar;
             act_issue_w(ar, L_attn_norm, static_cast<int>(L_q.cols));
             if (!input()) return false;
             prologue_lds<TQ>(L_q, ar, L_attn_norm, g.eps, s);
             pst(st, 2);
             return true;
-        }, done, st, first);
+        };
+        // with the resident attention its workgroups (the first res_n) take no tiles
+        return run_tiles<TQ, kLoopUnits>(total, s, row_of, ready, done, st, g.res_ok ? g.res_n : 0);
     }
     // Q and K in their format, then V's tiles (same activation family, its own width)
     if (static_cast<int>(blockIdx.x) >= total) return true;
@@ -1124,6 +1124,7 @@ __device__ __forceinline__ void res_preload(const AttnArgs& a, ResLds& s, const 
 // running sum broadcast from the thread before).
 template <int PER>
 __device__ __forceinline__ void res_scores(ResLds& s, int Lc, float scale) {
+    float mx = -INFINITY;  // the scores' max, for the softmax: each wave's into s.mx
     constexpr int hd = PER * 16, P = hd / 8;
     const int t = threadIdx.x, r = t & 3, g = t >> 2;
     float4 qr[PER];
@@ -1148,8 +1149,14 @@ __device__ __forceinline__ void res_scores(ResLds& s, int Lc, float scale) {
         prev = dpp<0x55>(sum);
         if (r == 2) sum = (((prev + l0) + l1) + l2) + l3;
         prev = dpp<0xAA>(sum);
-        if (r == 3) s.sc[p] = ((((prev + l0) + l1) + l2) + l3) * scale;
+        if (r == 3) {
+            const float v = ((((prev + l0) + l1) + l2) + l3) * scale;
+            s.sc[p] = v;
+            mx = fmaxf(mx, v);
+        }
     }
+    mx = wave_max(mx);
+    if ((threadIdx.x & 63) == 0) s.mx[threadIdx.x >> 6] = mx;
 }
 
 // The attention of query head k.h for value slice k.d0 at position pos
@@ -1221,12 +1228,7 @@ __device__ __forceinline__ bool res_attend(const LoopArgs& g, const AttnArgs& a,
     // exponentials with their double sum (a double sum of floats is exact in any grouping over the
     // range here), then every weight times the float reciprocal of the sum
     {
-        float m = -INFINITY;
-        for (int p = t; p < Lc; p += kThreads) m = fmaxf(m, s.sc[p]);
-        m = wave_max(m);
-        if (lane == 0) s.mx[wave] = m;
-        __syncthreads();
-        m = fmaxf(fmaxf(s.mx[0], s.mx[1]), fmaxf(s.mx[2], s.mx[3]));
+        const float m = fmaxf(fmaxf(s.mx[0], s.mx[1]), fmaxf(s.mx[2], s.mx[3]));  // (res_scores' wave maxima)
         double part = 0.0;
         for (int p = t; p < Lc; p += kThreads) {
             const float e = ref_expf_s(s.sc[p] - m);

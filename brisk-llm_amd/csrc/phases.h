@@ -164,14 +164,17 @@ struct TaggedOut {
     // then total / 32 block sums.  One value a lane: lanes 32 k .. 32 k + 31 hold
     // a block, and all of them call together.
     __device__ __forceinline__ void att_q8_0(int i, float v) const {
+        // the two 16-lane rows of a block combined through scalar reads of their first lanes (no
+        // LDS round trip); the quad's bytes gathered by DPP quad broadcasts
+        const bool upper = (threadIdx.x & 63) >= 32;
         float amax = group_reduce<16>(fabsf(v), [](float a, float b) { return nnmax(a, b); });
-        amax = nnmax(amax, __shfl_xor(amax, 16, 64));
+        amax = upper ? nnmax(readlane(amax, 32), readlane(amax, 48)) : nnmax(readlane(amax, 0), readlane(amax, 16));
         const float d = div127(amax);
         const float inv = d != 0.0f ? rcp_rn(d) : 0.0f;
         const int q = static_cast<int>(rintf(v * inv));
         int sum = group_reduce<16>(q, [](int a, int b) { return a + b; });
-        sum += __shfl_xor(sum, 16, 64);
-        const int q1 = __shfl_down(q, 1, 64), q2 = __shfl_down(q, 2, 64), q3 = __shfl_down(q, 3, 64);
+        sum = upper ? readlane(sum, 32) + readlane(sum, 48) : readlane(sum, 0) + readlane(sum, 16);
+        const int q1 = dpp<0x55>(q), q2 = dpp<0xAA>(q), q3 = dpp<0xFF>(q);
         if ((i & 3) == 0) {
             const uint32_t w = (q & 0xFF) | ((q1 & 0xFF) << 8) | ((q2 & 0xFF) << 16) | (static_cast<uint32_t>(q3) << 24);
             tput(out + i / 4, __uint_as_float(w), tag);
