@@ -2,7 +2,7 @@
 
 Restates the part of the reference's loader the HIP session needs:
 ``Model::parse_config`` (src/model.cpp:161-301) for the families the HIP
-session runs (qwen3, llama, bitnet, qwen2, smollm3, gemma3, phi3, lfm2), the tensor names and shapes of
+session runs (qwen3, llama, bitnet, qwen2, smollm3, gemma3, phi3, lfm2, qwen35), the tensor names and shapes of
 ``Model::Model`` (src/model.cpp:303-423) and the tied output projection
 (src/model.cpp:328-330).  The session takes the weights as GGUF-layout bytes,
 as the reference's ``Model(file, repack = false)`` hands them to a GPU session.
@@ -15,10 +15,10 @@ import numpy as np
 
 from . import gguf as G
 
-ARCH_QWEN3, ARCH_LLAMA, ARCH_BITNET, ARCH_QWEN2, ARCH_SMOLLM3, ARCH_GEMMA3, ARCH_PHI3, ARCH_LFM2 = range(8)
+ARCH_QWEN3, ARCH_LLAMA, ARCH_BITNET, ARCH_QWEN2, ARCH_SMOLLM3, ARCH_GEMMA3, ARCH_PHI3, ARCH_LFM2, ARCH_QWEN35 = range(9)
 _ARCH = {"qwen3": ARCH_QWEN3, "llama": ARCH_LLAMA, "bitnet": ARCH_BITNET, "bitnet-b1.58": ARCH_BITNET,
          "qwen2": ARCH_QWEN2, "smollm3": ARCH_SMOLLM3, "gemma3": ARCH_GEMMA3, "phi3": ARCH_PHI3,
-         "lfm2": ARCH_LFM2}
+         "lfm2": ARCH_LFM2, "qwen35": ARCH_QWEN35}
 QUANT_TYPES = (G.T_Q4_0, G.T_Q4_1, G.T_Q5_0, G.T_Q8_0, G.T_Q4_K, G.T_Q5_K, G.T_Q6_K, G.T_TQ2_0)
 
 
@@ -56,6 +56,18 @@ class ModelConfig:
     # LFM2 (src/model.cpp:229-253): convolution width; layers whose head_count_kv entry is 0 convolve
     conv_taps: int = 0
     conv_layers: tuple = ()
+    # Qwen3.5 (src/model.cpp:254-274): Gated DeltaNet state size, key/value heads, inner width and
+    # conv width; layers whose head_count_kv entry is 0 (every layer but each interval-th) are recurrent
+    ssm_state: int = 0
+    ssm_k_heads: int = 0
+    ssm_v_heads: int = 0
+    ssm_inner: int = 0
+    ssm_conv: int = 0
+    recurrent_layers: tuple = ()
+
+    @property
+    def ssm_qkv_dim(self) -> int:  # src/model.h:108
+        return 2 * self.ssm_k_heads * self.ssm_state + self.ssm_inner
 
     @property
     def rope_neox(self) -> bool:  # src/model.cpp:167
@@ -77,7 +89,7 @@ def parse_config(f: G.GgufFile) -> ModelConfig:
     name = f.get("general.architecture")
     if name not in _ARCH:
         fail(f"unsupported architecture '{name}'; the HIP session runs qwen3, qwen2, llama, smollm3, gemma3, phi3, "
-             "lfm2 and bitnet")
+             "lfm2, qwen35 and bitnet")
     p = name + "."
 
     def u32(key):
@@ -95,6 +107,11 @@ def parse_config(f: G.GgufFile) -> ModelConfig:
     embd, layers, heads = u32("embedding_length"), u32("block_count"), u32("attention.head_count")
     kv_raw = f.get(p + "attention.head_count_kv")
     per_layer_kv = list(kv_raw) if isinstance(kv_raw, (list, tuple)) else None  # per layer (src/model.cpp:229-238)
+    if name == "qwen35" and per_layer_kv is None:  # every interval-th layer attends (src/model.cpp:255-271)
+        interval = int(f.get(p + "full_attention_interval", 0))
+        if interval == 0:
+            fail("qwen35: full_attention_interval is missing")
+        per_layer_kv = [int(kv_raw or 0) if (l + 1) % interval == 0 else 0 for l in range(layers)]
     if per_layer_kv is not None and len(per_layer_kv) != layers:
         fail("head_count_kv array length")
     if per_layer_kv is not None and len({k for k in per_layer_kv if k != 0}) > 1:
@@ -128,6 +145,16 @@ def parse_config(f: G.GgufFile) -> ModelConfig:
         if not 2 <= cfg.conv_taps <= 8:
             fail("unsupported short-convolution width")
         cfg.conv_layers = tuple(l for l in range(layers) if per_layer_kv is not None and per_layer_kv[l] == 0)
+    elif cfg.arch == ARCH_QWEN35:
+        cfg.ssm_state, cfg.ssm_k_heads, cfg.ssm_v_heads = u32("ssm.state_size"), u32("ssm.group_count"), u32("ssm.time_step_rank")
+        cfg.ssm_inner, cfg.ssm_conv = u32("ssm.inner_size"), u32("ssm.conv_kernel")
+        if (cfg.ssm_v_heads == 0 or cfg.ssm_inner % cfg.ssm_v_heads or cfg.ssm_inner // cfg.ssm_v_heads != cfg.ssm_state
+                or cfg.ssm_k_heads != cfg.ssm_v_heads or not 2 <= cfg.ssm_conv <= 8):
+            fail("qwen35: unsupported DeltaNet shape (equal key and value heads of state_size values are supported)")
+        if cfg.ssm_state > 256:
+            fail("qwen35: a DeltaNet state wider than 256 is not supported")
+        cfg.recurrent_layers = tuple(l for l in range(layers) if per_layer_kv[l] == 0)
+        cfg.rope_dim = int(f.get(p + "rope.dimension_count", 0))
     elif per_layer_kv is not None and min(per_layer_kv) != kv:
         fail("per-layer key/value head counts are not supported for this family")
     if cfg.arch == ARCH_PHI3:
@@ -186,6 +213,21 @@ def tensor_table(f: G.GgufFile, cfg: ModelConfig) -> list:
     for l in range(cfg.layers):
         b = f"blk.{l}."
         vec(b + "attn_norm.weight", e)
+        if l in cfg.recurrent_layers:  # Qwen3.5 Gated DeltaNet (src/model.cpp:343-358)
+            mat(b + "attn_qkv.weight", cfg.ssm_qkv_dim, e)
+            mat(b + "attn_gate.weight", cfg.ssm_inner, e)
+            mat(b + "ssm_alpha.weight", cfg.ssm_v_heads, e)
+            mat(b + "ssm_beta.weight", cfg.ssm_v_heads, e)
+            vec(b + "ssm_a", cfg.ssm_v_heads)
+            vec(b + "ssm_dt.bias", cfg.ssm_v_heads)
+            vec(b + "ssm_conv1d.weight", cfg.ssm_conv * cfg.ssm_qkv_dim)
+            vec(b + "ssm_norm.weight", cfg.ssm_state)
+            mat(b + "ssm_out.weight", e, cfg.ssm_inner)
+            vec(b + "post_attention_norm.weight", e)
+            mat(b + "ffn_gate.weight", cfg.ff, e)
+            mat(b + "ffn_up.weight", cfg.ff, e)
+            mat(b + "ffn_down.weight", e, cfg.ff)
+            continue
         if l in cfg.conv_layers:  # LFM2 short convolution (src/model.cpp:360-364)
             mat(b + "shortconv.in_proj.weight", 3 * e, e)
             mat(b + "shortconv.out_proj.weight", e, e)
@@ -197,11 +239,11 @@ def tensor_table(f: G.GgufFile, cfg: ModelConfig) -> list:
             continue
         if cfg.arch == ARCH_PHI3:  # fused Q|K|V and gate|up (src/model.cpp:370-380)
             mat(b + "attn_qkv.weight", qd + 2 * kvd, e)
-        else:
-            mat(b + "attn_q.weight", qd, e)
+        else:  # Qwen3.5: each head's query rows followed by its gate rows (src/model.cpp:383-384)
+            mat(b + "attn_q.weight", 2 * qd if cfg.arch == ARCH_QWEN35 else qd, e)
             mat(b + "attn_k.weight", kvd, e)
             mat(b + "attn_v.weight", kvd, e)
-        if cfg.arch in (ARCH_QWEN3, ARCH_GEMMA3, ARCH_LFM2):
+        if cfg.arch in (ARCH_QWEN3, ARCH_GEMMA3, ARCH_LFM2, ARCH_QWEN35):
             vec(b + "attn_q_norm.weight", cfg.head_dim)
             vec(b + "attn_k_norm.weight", cfg.head_dim)
         if cfg.arch == ARCH_GEMMA3:
@@ -215,7 +257,7 @@ def tensor_table(f: G.GgufFile, cfg: ModelConfig) -> list:
             vec(b + "attn_k.bias", kvd)
             vec(b + "attn_v.bias", kvd)
         mat(b + "attn_output.weight", e, qd)
-        vec(b + "ffn_norm.weight", e)
+        vec(b + ("post_attention_norm.weight" if cfg.arch == ARCH_QWEN35 else "ffn_norm.weight"), e)  # src/model.cpp:418
         if cfg.arch == ARCH_PHI3:
             mat(b + "ffn_up.weight", 2 * cfg.ff, e)
         else:

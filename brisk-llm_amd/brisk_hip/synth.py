@@ -175,6 +175,7 @@ class ModelSpec:
     extra: dict = field(default_factory=dict)  # further "<arch>.<key>" metadata: key -> (GGUF type, value)
     factors: dict = field(default_factory=dict)  # RoPE factor tensors: name -> length
     conv_layers: tuple = ()                      # LFM2: layers that convolve (head_count_kv entry 0)
+    recurrent_layers: tuple = ()                 # Qwen3.5: Gated DeltaNet layers (all but every interval-th)
 
     @property
     def query_dim(self):
@@ -262,6 +263,22 @@ SPECS = {
                            fmt=_uniform4(G.T_Q8_0), conv_layers=(0, 1, 3),
                            extra={"shortconv.l_cache": (G.U32, 3),
                                   "attention.head_count_kv": (G.ARRAY, (G.U32, [0, 0, 2, 0]))}),
+    # Qwen3.5: layers 0, 1, 3 and 4 are Gated DeltaNet recurrences (4 heads of a 64 x 64 state, 4-tap
+    # conv), layers 2 and 5 attend with a sigmoid gate per query row and 16 of 64 head dimensions
+    # rotated; head 1's dt bias of 20 puts its softplus on both sides of the reference's cut-over.
+    "tiny-qwen35": ModelSpec("tiny-qwen35", "qwen35", 256, 6, 4, 2, 64, 512, 1000, 1e7, context=1024,
+                             fmt=_uniform4(G.T_Q8_0), recurrent_layers=(0, 1, 3, 4),
+                             extra={"full_attention_interval": (G.U32, 3), "rope.dimension_count": (G.U32, 16),
+                                    "ssm.state_size": (G.U32, 64), "ssm.group_count": (G.U32, 4),
+                                    "ssm.time_step_rank": (G.U32, 4), "ssm.inner_size": (G.U32, 256),
+                                    "ssm.conv_kernel": (G.U32, 4)}),
+    # The same family at a 128 x 128 state and head size, Q4_0 layers, a 3-tap conv.
+    "tiny-qwen35w": ModelSpec("tiny-qwen35w", "qwen35", 512, 4, 4, 1, 128, 768, 1000, 1e7, context=1024,
+                              fmt=_uniform4(G.T_Q4_0), recurrent_layers=(0, 1, 2),
+                              extra={"full_attention_interval": (G.U32, 4), "rope.dimension_count": (G.U32, 32),
+                                     "ssm.state_size": (G.U32, 128), "ssm.group_count": (G.U32, 4),
+                                     "ssm.time_step_rank": (G.U32, 4), "ssm.inner_size": (G.U32, 512),
+                                     "ssm.conv_kernel": (G.U32, 3)}),
     "tiny-q5": ModelSpec("tiny-q5", "qwen3", 256, 2, 4, 2, 64, 512, 1000, 1e6, context=1024,
                          fmt={**_uniform4(G.T_Q5_0), "o": G.T_Q4_1, "down": G.T_Q4_1}),
 }
@@ -315,6 +332,32 @@ def write_model(spec: ModelSpec, path: str) -> str:
     for l in range(spec.layers):
         b = f"blk.{l}."
         _vector(w, spec, b + "attn_norm.weight", spec.embd)
+        if l in spec.recurrent_layers:  # Qwen3.5 Gated DeltaNet (src/model.cpp:343-358)
+            ex = spec.extra
+            state, heads, inner, taps = (ex[k][1] for k in ("ssm.state_size", "ssm.time_step_rank", "ssm.inner_size",
+                                                            "ssm.conv_kernel"))
+            qkv = 2 * ex["ssm.group_count"][1] * state + inner
+            _matrix(w, spec, b + "attn_qkv.weight", qkv, spec.embd, spec.fmt["q"])
+            _matrix(w, spec, b + "attn_gate.weight", inner, spec.embd, spec.fmt["q"])
+            _matrix(w, spec, b + "ssm_alpha.weight", heads, spec.embd, spec.fmt["k"])
+            _matrix(w, spec, b + "ssm_beta.weight", heads, spec.embd, spec.fmt["k"])
+            seed = stream_seed(spec.seed, b + "ssm_a")  # A = -exp(A_log) < 0: every decay below 1
+            w.add_tensor(b + "ssm_a", (heads,), G.T_F32,
+                         lambda seed=seed, n=heads: random_uniform(seed, n, -4.0, -0.5).astype(np.float32).view(np.uint8))
+            seed = stream_seed(spec.seed, b + "ssm_dt")
+            dt = random_uniform(seed, heads, -1.0, 1.0)
+            dt[1] = 20.0
+            w.add_tensor(b + "ssm_dt.bias", (heads,), G.T_F32, lambda dt=dt: dt.astype(np.float32).view(np.uint8))
+            seed = stream_seed(spec.seed, b + "ssm_conv1d")
+            w.add_tensor(b + "ssm_conv1d.weight", (taps, qkv), G.T_F32,
+                         lambda seed=seed, n=taps * qkv: random_uniform(seed, n, -1.0, 1.0).astype(np.float32).view(np.uint8))
+            _vector(w, spec, b + "ssm_norm.weight", state)
+            _matrix(w, spec, b + "ssm_out.weight", spec.embd, inner, spec.fmt["o"])
+            _vector(w, spec, b + "post_attention_norm.weight", spec.embd)
+            _matrix(w, spec, b + "ffn_gate.weight", spec.ff, spec.embd, spec.fmt["gate"])
+            _matrix(w, spec, b + "ffn_up.weight", spec.ff, spec.embd, spec.fmt["up"])
+            _matrix(w, spec, b + "ffn_down.weight", spec.embd, spec.ff, spec.fmt["down"])
+            continue
         if l in spec.conv_layers:  # LFM2 short convolution (src/model.cpp:360-364)
             taps = spec.extra["shortconv.l_cache"][1]
             _matrix(w, spec, b + "shortconv.in_proj.weight", 3 * spec.embd, spec.embd, spec.fmt["q"])
@@ -330,10 +373,10 @@ def write_model(spec: ModelSpec, path: str) -> str:
         if a == "phi3":  # fused Q|K|V (src/model.cpp:370-376)
             _matrix(w, spec, b + "attn_qkv.weight", spec.query_dim + 2 * spec.kv_dim, spec.embd, spec.fmt["q"])
         else:
-            _matrix(w, spec, b + "attn_q.weight", spec.query_dim, spec.embd, spec.fmt["q"])
+            _matrix(w, spec, b + "attn_q.weight", (2 if a == "qwen35" else 1) * spec.query_dim, spec.embd, spec.fmt["q"])
             _matrix(w, spec, b + "attn_k.weight", spec.kv_dim, spec.embd, spec.fmt["k"])
             _matrix(w, spec, b + "attn_v.weight", spec.kv_dim, spec.embd, spec.fmt["v"])
-        if a in ("qwen3", "gemma3", "lfm2"):
+        if a in ("qwen3", "gemma3", "lfm2", "qwen35"):
             _vector(w, spec, b + "attn_q_norm.weight", spec.head_dim)
             _vector(w, spec, b + "attn_k_norm.weight", spec.head_dim)
         if a == "gemma3":
@@ -347,7 +390,7 @@ def write_model(spec: ModelSpec, path: str) -> str:
             _bias(w, spec, b + "attn_k.bias", spec.kv_dim)
             _bias(w, spec, b + "attn_v.bias", spec.kv_dim)
         _matrix(w, spec, b + "attn_output.weight", spec.embd, spec.query_dim, spec.fmt["o"])
-        _vector(w, spec, b + "ffn_norm.weight", spec.embd)
+        _vector(w, spec, b + ("post_attention_norm.weight" if a == "qwen35" else "ffn_norm.weight"), spec.embd)
         if a == "phi3":  # fused gate|up (src/model.cpp:377-379)
             _matrix(w, spec, b + "ffn_up.weight", 2 * spec.ff, spec.embd, spec.fmt["up"])
         else:

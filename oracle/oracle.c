@@ -725,6 +725,95 @@ uint64_t or_tanhf_check(uint32_t stride, uint64_t* checked) {
     return bad;
 }
 
+/* glibc's log1pf, as the reference calls it (std::log1p on float: the softplus of Qwen3.5's
+ * recurrence, src/model.cpp:827). */
+void or_log1pf_batch(const float* x, float* y, size_t n) {
+    for (size_t i = 0; i < n; ++i) y[i] = log1pf(x[i]);
+}
+
+/* The restatement of glibc 2.35's log1pf that the HIP recurrence runs: fdlibm's s_log1pf.c
+ * (1 + x split as 2^k (1 + f) with a correction term c for the rounding of 1 + x, then
+ * log(1 + f) = f - hfsq + s (hfsq + R(s^2)), s = f / (2 + f), R a degree-7 polynomial in
+ * s^2, plus k ln2 in a hi and a lo part).  or_log1pf_check compares it with the host's
+ * log1pf on every `stride`-th 32-bit pattern and returns the number of differing results. */
+static float log1pf_restated(float x) {
+    const float ln2_hi = 6.9313812256e-01f, ln2_lo = 9.0580006145e-06f, two25 = 3.355443200e+07f;
+    const float Lp1 = 6.6666668653e-01f, Lp2 = 4.0000000596e-01f, Lp3 = 2.8571429849e-01f, Lp4 = 2.2222198546e-01f,
+                Lp5 = 1.8183572590e-01f, Lp6 = 1.5313838422e-01f, Lp7 = 1.4798198640e-01f;
+    float hfsq, f = 0.0f, c = 0.0f, s, z, R, u;
+    const int32_t hx = (int32_t)fbits(x), ax = hx & 0x7fffffff;
+    int32_t k = 1, hu = 0;
+    if (hx < 0x3ed413d7) { /* x < 0.41422 */
+        if (ax >= 0x3f800000) { /* x <= -1 */
+            if (x == -1.0f) return -two25 / 0.0f;
+            return (x - x) / (x - x);
+        }
+        if (ax < 0x31000000) { /* |x| < 2^-29 */
+            if (ax < 0x24800000) return x;
+            return x - x * x * 0.5f;
+        }
+        if (hx > 0 || hx <= (int32_t)0xbe95f61f) { /* -0.2929 < x < 0.41422 */
+            k = 0;
+            f = x;
+            hu = 1;
+        }
+    } else if (hx >= 0x7f800000) {
+        return x + x;
+    }
+    if (k != 0) {
+        if (hx < 0x5a000000) {
+            u = 1.0f + x;
+            hu = (int32_t)fbits(u);
+            k = (hu >> 23) - 127;
+            c = k > 0 ? 1.0f - (u - x) : x - (u - 1.0f); /* the rounding error of 1 + x */
+            c /= u;
+        } else {
+            u = x;
+            hu = (int32_t)fbits(u);
+            k = (hu >> 23) - 127;
+            c = 0.0f;
+        }
+        hu &= 0x007fffff;
+        if (hu < 0x3504f7) {
+            u = ffrom((uint32_t)hu | 0x3f800000u);
+        } else {
+            k += 1;
+            u = ffrom((uint32_t)hu | 0x3f000000u);
+            hu = (0x00800000 - hu) >> 2;
+        }
+        f = u - 1.0f;
+    }
+    hfsq = 0.5f * f * f;
+    if (hu == 0) { /* |f| < 2^-20 */
+        if (f == 0.0f) {
+            if (k == 0) return 0.0f;
+            c += k * ln2_lo;
+            return k * ln2_hi + c;
+        }
+        R = hfsq * (1.0f - 0.66666666666666666f * f);
+        if (k == 0) return f - R;
+        return k * ln2_hi - ((R - (k * ln2_lo + c)) - f);
+    }
+    s = f / (2.0f + f);
+    z = s * s;
+    R = z * (Lp1 + z * (Lp2 + z * (Lp3 + z * (Lp4 + z * (Lp5 + z * (Lp6 + z * Lp7))))));
+    if (k == 0) return f - (hfsq - s * (hfsq + R));
+    return k * ln2_hi - ((hfsq - (s * (hfsq + R) + (k * ln2_lo + c))) - f);
+}
+
+uint64_t or_log1pf_check(uint32_t stride, uint64_t* checked) {
+    uint64_t bad = 0, n = 0;
+    for (uint64_t b = 0; b <= 0xFFFFFFFFull; b += stride) {
+        const float x = ffrom((uint32_t)b);
+        if (isnan(x)) continue;
+        const float a = log1pf(x), e = log1pf_restated(x);
+        bad += fbits(a) != fbits(e) && !(isnan(a) && isnan(e));
+        ++n;
+    }
+    if (checked) *checked = n;
+    return bad;
+}
+
 /* ------------------------------------------------------------------ session */
 
 typedef struct {
@@ -741,6 +830,11 @@ typedef struct {
     matrix conv_in, conv_out;  /* LFM2 short convolution (src/model.cpp:360-364) */
     const float* conv_w;       /* [embd][taps]; non-NULL marks a convolution layer */
     uint16_t* conv_cache;      /* bx per position, fp16 [max_context][embd] */
+    /* Qwen3.5 Gated DeltaNet layer (src/model.cpp:343-358); ssm_a non-NULL marks it */
+    matrix ssm_qkv, ssm_gate, ssm_alpha, ssm_beta, ssm_out;
+    const float *ssm_a, *ssm_dt, *ssm_conv_w, *ssm_norm;
+    float *state, *ring;           /* S[head][j][i] (value j, key i); the conv's last ssm_conv - 1 inputs */
+    float *snap_state, *snap_ring; /* both as they were before the last evaluated token */
 } layer_t;
 
 struct oracle_session {
@@ -754,6 +848,10 @@ struct oracle_session {
     float *h, *normed, *q, *k, *v, *att, *proj, *gate, *up, *scores, *rope, *rope_local, *conv;
     const float* rope_factors; /* rope_freqs, or Phi-3's short / long factors; NULL: none */
     uint8_t* xq;
+    /* Qwen3.5: the query|gate rows, the gates, the recurrence's projections and conv outputs */
+    float *qg, *agate, *sqkv, *sconv, *sz, *sab;
+    int snap_valid;
+    size_t snap_pos;
 };
 
 static const oracle_tensor* find(const oracle_tensor* t, size_t n, const char* name) {
@@ -797,6 +895,28 @@ oracle_session* or_session_create(const oracle_config* cfg, const oracle_tensor*
         layer_t* L = &s->layers[l];
 #define LN(sfx) (snprintf(name, sizeof name, "blk.%d.%s", l, sfx), name)
         GETV(L->attn_norm, LN("attn_norm.weight"));
+        if (c->arch == OR_QWEN35 && find(t, n, LN("ssm_a"))) { /* src/model.cpp:343-358 */
+            const size_t qkv = 2 * (size_t)c->ssm_k_heads * c->ssm_state + (size_t)c->ssm_inner;
+            GETM(L->ssm_qkv, LN("attn_qkv.weight"));
+            GETM(L->ssm_gate, LN("attn_gate.weight"));
+            GETM(L->ssm_alpha, LN("ssm_alpha.weight"));
+            GETM(L->ssm_beta, LN("ssm_beta.weight"));
+            GETV(L->ssm_a, LN("ssm_a"));
+            GETV(L->ssm_dt, LN("ssm_dt.bias"));
+            GETV(L->ssm_conv_w, LN("ssm_conv1d.weight"));
+            GETV(L->ssm_norm, LN("ssm_norm.weight"));
+            GETM(L->ssm_out, LN("ssm_out.weight"));
+            GETV(L->ffn_norm, LN("post_attention_norm.weight"));
+            GETM(L->gate, LN("ffn_gate.weight"));
+            GETM(L->up, LN("ffn_up.weight"));
+            GETM(L->down, LN("ffn_down.weight"));
+            const size_t st = (size_t)c->ssm_v_heads * c->ssm_state * c->ssm_state, rg = (size_t)(c->ssm_conv - 1) * qkv;
+            L->state = (float*)calloc(st, 4);
+            L->snap_state = (float*)calloc(st, 4);
+            L->ring = (float*)calloc(rg, 4);
+            L->snap_ring = (float*)calloc(rg, 4);
+            continue;
+        }
         if (c->arch == OR_LFM2 && find(t, n, LN("shortconv.in_proj.weight"))) {
             GETM(L->conv_in, LN("shortconv.in_proj.weight"));
             GETM(L->conv_out, LN("shortconv.out_proj.weight"));
@@ -829,13 +949,13 @@ oracle_session* or_session_create(const oracle_config* cfg, const oracle_tensor*
             GETM(L->up, LN("ffn_up.weight"));
         }
         GETM(L->o, LN("attn_output.weight"));
-        GETV(L->ffn_norm, LN("ffn_norm.weight"));
+        GETV(L->ffn_norm, LN(c->arch == OR_QWEN35 ? "post_attention_norm.weight" : "ffn_norm.weight")); /* src/model.cpp:418 */
         GETM(L->down, LN("ffn_down.weight"));
         if (c->arch == OR_GEMMA3) {
             GETV(L->attn_post_norm, LN("post_attention_norm.weight"));
             GETV(L->ffn_post_norm, LN("post_ffw_norm.weight"));
         }
-        if (c->arch == OR_QWEN3 || c->arch == OR_GEMMA3 || c->arch == OR_LFM2) { /* src/model.cpp:394-397 */
+        if (c->arch == OR_QWEN3 || c->arch == OR_GEMMA3 || c->arch == OR_LFM2 || c->arch == OR_QWEN35) { /* src/model.cpp:394-398 */
             GETV(L->q_norm, LN("attn_q_norm.weight"));
             GETV(L->k_norm, LN("attn_k_norm.weight"));
         }
@@ -864,7 +984,16 @@ oracle_session* or_session_create(const oracle_config* cfg, const oracle_tensor*
         s->q = (float*)calloc(qd, 4);
         s->k = (float*)calloc(kvd, 4);
         s->v = (float*)calloc(kvd, 4);
-        s->att = (float*)calloc(qd, 4);
+        s->att = (float*)calloc(qd > (size_t)c->ssm_inner ? qd : (size_t)c->ssm_inner, 4);
+        if (c->arch == OR_QWEN35) {
+            const size_t qkv = 2 * (size_t)c->ssm_k_heads * c->ssm_state + (size_t)c->ssm_inner;
+            s->qg = (float*)calloc(2 * qd, 4);
+            s->agate = (float*)calloc(qd, 4);
+            s->sqkv = (float*)calloc(qkv, 4);
+            s->sconv = (float*)calloc(qkv, 4);
+            s->sz = (float*)calloc((size_t)c->ssm_inner, 4);
+            s->sab = (float*)calloc(2 * (size_t)c->ssm_v_heads, 4);
+        }
         s->proj = (float*)calloc(c->embd, 4);
         s->gate = (float*)calloc(c->ff, 4);
         s->up = (float*)calloc(c->ff, 4);
@@ -891,7 +1020,11 @@ void or_session_destroy(oracle_session* s) {
         for (int l = 0; l < s->c.layers; ++l) free(s->vcache[l]);
     free(s->kcache);
     free(s->vcache);
-    for (int l = 0; s->layers && l < s->c.layers; ++l) free(s->layers[l].conv_cache);
+    for (int l = 0; s->layers && l < s->c.layers; ++l) {
+        layer_t* L = &s->layers[l];
+        free(L->conv_cache); free(L->state); free(L->ring); free(L->snap_state); free(L->snap_ring);
+    }
+    free(s->qg); free(s->agate); free(s->sqkv); free(s->sconv); free(s->sz); free(s->sab);
     free(s->layers);
     free(s->h); free(s->normed); free(s->q); free(s->k); free(s->v); free(s->att);
     free(s->proj); free(s->gate); free(s->up); free(s->scores); free(s->rope); free(s->rope_local); free(s->conv); free(s->xq);
@@ -902,8 +1035,40 @@ size_t or_session_position(const oracle_session* s) { return s->position; }
 void or_session_set_position(oracle_session* s, size_t p) { s->position = p; }
 uint16_t* or_session_kv(oracle_session* s, int layer, int value) { return value ? s->vcache[layer] : s->kcache[layer]; }
 
+/* Qwen3.5's recurrent layers back to zero (Session::reset_recurrent, src/model.cpp:729-733). */
+static void reset_recurrent(oracle_session* s) {
+    const oracle_config* c = &s->c;
+    const size_t qkv = 2 * (size_t)c->ssm_k_heads * c->ssm_state + (size_t)c->ssm_inner;
+    for (int l = 0; l < c->layers; ++l) {
+        layer_t* L = &s->layers[l];
+        if (!L->ssm_a) continue;
+        memset(L->state, 0, (size_t)c->ssm_v_heads * c->ssm_state * c->ssm_state * 4);
+        memset(L->ring, 0, (size_t)(c->ssm_conv - 1) * qkv * 4);
+    }
+    s->snap_valid = 0;
+}
+
+/* Session::rollback (src/model.cpp:735-752): the caches keep their rows; Qwen3.5's recurrent
+ * states step back only to the snapshot before the last evaluated token, any other earlier
+ * position restarts them at position 0. */
 int or_session_rollback(oracle_session* s, size_t position) {
     if (position > s->position) return fail("model: cannot roll forward"); /* src/model.cpp:736 */
+    if (s->c.arch == OR_QWEN35 && position != s->position) {
+        const oracle_config* c = &s->c;
+        const size_t qkv = 2 * (size_t)c->ssm_k_heads * c->ssm_state + (size_t)c->ssm_inner;
+        if (s->snap_valid && s->snap_pos == position) {
+            for (int l = 0; l < c->layers; ++l) {
+                layer_t* L = &s->layers[l];
+                if (!L->ssm_a) continue;
+                memcpy(L->state, L->snap_state, (size_t)c->ssm_v_heads * c->ssm_state * c->ssm_state * 4);
+                memcpy(L->ring, L->snap_ring, (size_t)(c->ssm_conv - 1) * qkv * 4);
+            }
+            s->snap_valid = 0;
+        } else {
+            reset_recurrent(s);
+            position = 0;
+        }
+    }
     s->position = position;
     return 0;
 }
@@ -966,6 +1131,68 @@ static void forward_token(oracle_session* s, int32_t token, float* logits) {
     for (int l = 0; l < c->layers; ++l) {
         const layer_t* L = &s->layers[l];
         or_rms_norm(s->h, L->attn_norm, c->eps, s->normed, embd);
+        if (L->ssm_a) { /* Qwen3.5 Gated DeltaNet, Session::forward_recurrent (src/model.cpp:754-865) for one token */
+            const size_t heads = (size_t)c->ssm_v_heads, dim = (size_t)c->ssm_state, taps = (size_t)c->ssm_conv;
+            const size_t k_off = (size_t)c->ssm_k_heads * dim, v_off = 2 * k_off, qkv = 2 * k_off + (size_t)c->ssm_inner;
+            multiply(s, &L->ssm_qkv, s->normed, s->sqkv);
+            multiply(s, &L->ssm_gate, s->normed, s->sz);
+            multiply(s, &L->ssm_alpha, s->normed, s->sab);
+            multiply(s, &L->ssm_beta, s->normed, s->sab + heads);
+            /* the causal conv over the ring's taps - 1 inputs (oldest first) and this one, then SiLU */
+            for (size_t ch = 0; ch < qkv; ++ch) s->sconv[ch] = 0.0f;
+            for (size_t i = 0; i < taps; ++i) {
+                const float* in = i + 1 < taps ? L->ring + i * qkv : s->sqkv;
+                for (size_t ch = 0; ch < qkv; ++ch) s->sconv[ch] += L->ssm_conv_w[ch * taps + i] * in[ch];
+            }
+            for (size_t ch = 0; ch < qkv; ++ch) s->sconv[ch] = s->sconv[ch] / (1.0f + expf(-s->sconv[ch]));
+            const float q_scale = 1.0f / sqrtf((float)dim);
+            for (size_t hh = 0; hh < heads; ++hh) {
+                float q[256], k[256], d[256];
+                const float* row = s->sconv;
+                for (int which = 0; which < 2; ++which) { /* L2 norms of q (times 1/sqrt(dim)) and k */
+                    const float* src = row + (which ? k_off : 0) + hh * dim;
+                    float* dst = which ? k : q;
+                    float sum = 0.0f;
+                    for (size_t i = 0; i < dim; ++i) sum += src[i] * src[i];
+                    const float inv = (which ? 1.0f : q_scale) / sqrtf(sum + c->eps);
+                    for (size_t i = 0; i < dim; ++i) dst[i] = src[i] * inv;
+                }
+                const float* v = row + v_off + hh * dim;
+                const float alpha = s->sab[hh] + L->ssm_dt[hh];
+                const float softplus = alpha > 20.0f ? alpha : log1pf(expf(alpha));
+                const float decay = expf(softplus * L->ssm_a[hh]);
+                const float beta = 1.0f / (1.0f + expf(-s->sab[heads + hh]));
+                float* S = L->state + hh * dim * dim;
+                for (size_t j = 0; j < dim; ++j) {
+                    float* Sj = S + j * dim;
+                    float sk = 0.0f;
+                    for (size_t i = 0; i < dim; ++i) {
+                        Sj[i] *= decay;
+                        sk += Sj[i] * k[i];
+                    }
+                    d[j] = (v[j] - sk) * beta;
+                }
+                float* o = s->att + hh * dim;
+                for (size_t j = 0; j < dim; ++j) {
+                    float* Sj = S + j * dim;
+                    float oj = 0.0f;
+                    for (size_t i = 0; i < dim; ++i) {
+                        Sj[i] += k[i] * d[j];
+                        oj += Sj[i] * q[i];
+                    }
+                    o[j] = oj;
+                }
+                or_rms_norm(o, L->ssm_norm, c->eps, o, dim); /* the gated norm */
+                const float* z = s->sz + hh * dim;
+                for (size_t j = 0; j < dim; ++j) o[j] *= z[j] / (1.0f + expf(-z[j]));
+            }
+            /* the ring: the last taps - 1 inputs */
+            for (size_t i = 0; i + 2 < taps; ++i) memcpy(L->ring + i * qkv, L->ring + (i + 1) * qkv, qkv * 4);
+            memcpy(L->ring + (taps - 2) * qkv, s->sqkv, qkv * 4);
+            multiply(s, &L->ssm_out, s->att, s->proj);
+            for (size_t i = 0; i < embd; ++i) s->h[i] += s->proj[i];
+            goto ffn;
+        }
         if (L->conv_w) { /* LFM2 short convolution (src/model.cpp:935-969) */
             const size_t taps = (size_t)c->conv_taps;
             float* bcx = s->conv;
@@ -985,7 +1212,15 @@ static void forward_token(oracle_session* s, int32_t token, float* logits) {
             for (size_t i = 0; i < embd; ++i) s->h[i] += s->proj[i];
             goto ffn;
         }
-        multiply(s, &L->q, s->normed, s->q);
+        if (c->arch == OR_QWEN35) { /* each head's query followed by its gate (src/model.cpp:1002-1012) */
+            multiply(s, &L->q, s->normed, s->qg);
+            for (int h = 0; h < c->heads; ++h) {
+                memcpy(s->q + h * hd, s->qg + 2 * h * hd, hd * 4);
+                memcpy(s->agate + h * hd, s->qg + 2 * h * hd + hd, hd * 4);
+            }
+        } else {
+            multiply(s, &L->q, s->normed, s->q);
+        }
         multiply(s, &L->k, s->normed, s->k);
         multiply(s, &L->v, s->normed, s->v);
         /* SmolLM3: every fourth layer has no RoPE (layer_has_rope, src/model.h:110; step 4, src/model.cpp:168) */
@@ -1041,6 +1276,8 @@ static void forward_token(oracle_session* s, int32_t token, float* logits) {
             }
         }
         if (L->attn_sub_norm) or_rms_norm(s->att, L->attn_sub_norm, c->eps, s->att, qd);
+        if (c->arch == OR_QWEN35) /* the sigmoid gate (src/model.cpp:1102-1108) */
+            for (size_t i = 0; i < qd; ++i) s->att[i] *= 1.0f / (1.0f + expf(-s->agate[i]));
         multiply(s, &L->o, s->att, s->proj);
         if (L->attn_post_norm) or_rms_norm(s->proj, L->attn_post_norm, c->eps, s->proj, embd); /* :1116-1119 */
         for (size_t i = 0; i < embd; ++i) s->h[i] += s->proj[i];
@@ -1091,8 +1328,20 @@ int or_session_eval(oracle_session* s, const int32_t* tokens, size_t n, int all_
     for (size_t i = 0; i < n; ++i)
         if (tokens[i] < 0 || tokens[i] >= s->c.vocab) return fail("model: token id out of range");
     if (n > (size_t)s->c.max_context - s->position) return fail("model: context length exceeded");
+    const oracle_config* c = &s->c;
+    const size_t qkv = 2 * (size_t)c->ssm_k_heads * c->ssm_state + (size_t)c->ssm_inner;
     for (size_t i = 0; i < n; ++i) {
         float* row = all_logits ? out + i * (size_t)s->c.vocab : (i + 1 == n ? out : NULL);
+        if (c->arch == OR_QWEN35 && i + 1 == n) { /* the snapshot before the last token (src/model.cpp:798-812) */
+            for (int l = 0; l < c->layers; ++l) {
+                layer_t* L = &s->layers[l];
+                if (!L->ssm_a) continue;
+                memcpy(L->snap_state, L->state, (size_t)c->ssm_v_heads * c->ssm_state * c->ssm_state * 4);
+                memcpy(L->snap_ring, L->ring, (size_t)(c->ssm_conv - 1) * qkv * 4);
+            }
+            s->snap_pos = s->position;
+            s->snap_valid = 1;
+        }
         forward_token(s, tokens[i], row);
     }
     return 0;

@@ -25,7 +25,7 @@ extern "C" {
 /* ggml tensor types (src/gguf.h:22-27). */
 enum { OR_F32 = 0, OR_Q4_0 = 2, OR_Q4_1 = 3, OR_Q5_0 = 6, OR_Q8_0 = 8, OR_Q4_K = 12, OR_Q5_K = 13, OR_Q6_K = 14, OR_TQ2_0 = 35 };
 /* Architectures of src/model.h:21-32 that the configs use. */
-enum { OR_QWEN3 = 0, OR_LLAMA = 1, OR_BITNET = 2, OR_QWEN2 = 3, OR_SMOLLM3 = 4, OR_GEMMA3 = 5, OR_PHI3 = 6, OR_LFM2 = 7 };
+enum { OR_QWEN3 = 0, OR_LLAMA = 1, OR_BITNET = 2, OR_QWEN2 = 3, OR_SMOLLM3 = 4, OR_GEMMA3 = 5, OR_PHI3 = 6, OR_LFM2 = 7, OR_QWEN35 = 8 };
 
 typedef struct {
     int arch;
@@ -41,6 +41,9 @@ typedef struct {
     float rope_attn_factor;
     int rope_original_context;
     int conv_taps; /* LFM2 short-convolution width */
+    /* Qwen3.5 Gated DeltaNet layers (src/model.h:100-109): state size, key and value heads,
+     * inner width (value heads x state), conv width; the layers with blk.N.ssm_a are recurrent */
+    int ssm_state, ssm_k_heads, ssm_v_heads, ssm_inner, ssm_conv;
 } oracle_config;
 
 /* One tensor of the model: `rows` x `cols` (vectors: rows = 1), GGUF bytes. */
@@ -69,13 +72,19 @@ void or_expf_batch(const float* x, float* y, size_t n);
 uint64_t or_expf_check(uint32_t stride, uint64_t* checked);
 void or_tanhf_batch(const float* x, float* y, size_t n);
 uint64_t or_tanhf_check(uint32_t stride, uint64_t* checked);
+/* glibc log1pf over a batch, and the check of the HIP recurrence's restatement of it. */
+void or_log1pf_batch(const float* x, float* y, size_t n);
+uint64_t or_log1pf_check(uint32_t stride, uint64_t* checked);
 /* Activation bits a matrix of `type` with `rows` rows takes on x86 (src/model.cpp:496-503, src/quant.cpp:144). */
 int or_activation_bits(int type, size_t rows);
 
 typedef struct oracle_session oracle_session;
 oracle_session* or_session_create(const oracle_config* cfg, const oracle_tensor* tensors, size_t n_tensors);
 void or_session_destroy(oracle_session* s);
-/* eval / eval_all of src/model.cpp:704-727: logits of the last token (all_logits = 0) or of every token. */
+/* eval / eval_all of src/model.cpp:704-727: logits of the last token (all_logits = 0) or of every token.
+ * Qwen3.5: each call leaves the snapshot of the recurrent states before its last token
+ * (src/model.cpp:798-812), which or_session_rollback restores or, for any other earlier
+ * position, replaces by a restart at position 0 (src/model.cpp:735-751). */
 int or_session_eval(oracle_session* s, const int32_t* tokens, size_t n, int all_logits, float* out);
 size_t or_session_position(const oracle_session* s);
 int or_session_rollback(oracle_session* s, size_t position);

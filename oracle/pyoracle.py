@@ -25,7 +25,8 @@ class OracleConfig(C.Structure):
                 ("rope_base", C.c_float), ("eps", C.c_float), ("max_context", C.c_int),
                 ("sliding_window", C.c_int), ("rope_base_local", C.c_float), ("rope_scale", C.c_float),
                 ("final_softcap", C.c_float), ("rope_dim", C.c_int), ("rope_attn_factor", C.c_float),
-                ("rope_original_context", C.c_int), ("conv_taps", C.c_int)]
+                ("rope_original_context", C.c_int), ("conv_taps", C.c_int), ("ssm_state", C.c_int),
+                ("ssm_k_heads", C.c_int), ("ssm_v_heads", C.c_int), ("ssm_inner", C.c_int), ("ssm_conv", C.c_int)]
 
 
 class OracleTensor(C.Structure):
@@ -74,6 +75,9 @@ def oracle_lib():
         L.or_tanhf_batch.argtypes = [_vp, _vp, _sz]
         L.or_tanhf_check.argtypes = [C.c_uint32, C.POINTER(C.c_uint64)]
         L.or_tanhf_check.restype = C.c_uint64
+        L.or_log1pf_batch.argtypes = [_vp, _vp, _sz]
+        L.or_log1pf_check.argtypes = [C.c_uint32, C.POINTER(C.c_uint64)]
+        L.or_log1pf_check.restype = C.c_uint64
         L.or_activation_bits.argtypes = [_i, _sz]
         L.or_activation_bits.restype = _i
         L.or_session_create.argtypes = [C.POINTER(OracleConfig), C.POINTER(OracleTensor), _sz]
@@ -138,7 +142,8 @@ class Oracle:
         self.L, self.cfg, self.max_context = L, cfg, max_context
         c = OracleConfig(cfg.arch, cfg.embd, cfg.layers, cfg.heads, cfg.kv_heads, cfg.head_dim, cfg.ff, cfg.vocab,
                          cfg.rope_base, cfg.eps, max_context, cfg.sliding_window, cfg.rope_base_local, cfg.rope_scale,
-                         cfg.final_softcap, cfg.rope_dim, cfg.rope_attn_factor, cfg.rope_original_context, cfg.conv_taps)
+                         cfg.final_softcap, cfg.rope_dim, cfg.rope_attn_factor, cfg.rope_original_context, cfg.conv_taps,
+                         cfg.ssm_state, cfg.ssm_k_heads, cfg.ssm_v_heads, cfg.ssm_inner, cfg.ssm_conv)
         self._names = [t.name.encode() for t in table]
         arr = (OracleTensor * len(table))()
         for i, t in enumerate(table):
@@ -206,7 +211,9 @@ class RefConfig(C.Structure):
         ("rope_base_local", C.c_float), ("rope_scale", C.c_float), ("embedding_scale", C.c_float),
         ("final_softcap", C.c_float), ("gelu", C.c_int32), ("conv_taps", C.c_uint32), ("no_rope_step", C.c_uint32),
         ("n_rope_factors", C.c_uint32), ("n_factors_short", C.c_uint32), ("n_factors_long", C.c_uint32),
-        ("conv_layers", C.c_uint64)]
+        ("conv_layers", C.c_uint64), ("ssm_state", C.c_uint32), ("ssm_k_heads", C.c_uint32),
+        ("ssm_v_heads", C.c_uint32), ("ssm_inner", C.c_uint32), ("ssm_conv", C.c_uint32), ("attention_gate", C.c_int32),
+        ("recurrent_layers", C.c_uint64)]
 
 
 # the reference's Architecture enumerators (src/model.h:20-31), by GGUF architecture name

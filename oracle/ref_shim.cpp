@@ -89,6 +89,9 @@ struct RefConfig {
     uint32_t conv_taps, no_rope_step;
     uint32_t n_rope_factors, n_factors_short, n_factors_long;
     uint64_t conv_layers;  // bit l: layer l is a short-convolution layer (layers 0..63)
+    uint32_t ssm_state, ssm_k_heads, ssm_v_heads, ssm_inner, ssm_conv;
+    int32_t attention_gate;
+    uint64_t recurrent_layers;  // bit l: layer l is a Gated DeltaNet layer (layers 0..63)
 };
 
 int ref_config(void* handle, RefConfig* out) {
@@ -108,6 +111,10 @@ int ref_config(void* handle, RefConfig* out) {
         r.n_factors_long = static_cast<uint32_t>(c.rope_factors_long.size());
         for (std::size_t l = 0; l < c.layer_count && l < 64; ++l)
             if (c.layer_is_conv(l)) r.conv_layers |= uint64_t{1} << l;
+        r.ssm_state = c.ssm_state; r.ssm_k_heads = c.ssm_k_heads; r.ssm_v_heads = c.ssm_v_heads;
+        r.ssm_inner = c.ssm_inner; r.ssm_conv = c.ssm_conv; r.attention_gate = c.attention_gate ? 1 : 0;
+        for (std::size_t l = 0; l < c.layer_count && l < 64; ++l)
+            if (c.layer_is_recurrent(l)) r.recurrent_layers |= uint64_t{1} << l;
         *out = r;
     });
 }

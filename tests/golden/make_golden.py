@@ -45,6 +45,8 @@ RUNS = {
     "tiny-phi3": (12, 48),
     "tiny-llama32": (12, 48),
     "tiny-lfm2": (12, 48),
+    "tiny-qwen35": (12, 48),
+    "tiny-qwen35w": (12, 48),
 }
 
 

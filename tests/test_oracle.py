@@ -392,6 +392,30 @@ def test_tanhf_restatement_matches_libm():
     assert bad == 0
 
 
+def test_log1pf_restatement_matches_libm():
+    """The Qwen3.5 recurrence's log1pf restatement (fdlibm's s_log1pf.c, as glibc 2.35 builds it) against the
+    host libm, on a strided sweep of every float bit pattern (every pattern agrees when run with stride 1)."""
+    import ctypes as C
+    L = pyoracle.oracle_lib()
+    checked = C.c_uint64()
+    bad = L.or_log1pf_check(97, C.byref(checked))
+    assert checked.value > 40_000_000
+    assert bad == 0
+
+
+def test_log1pf_closed_forms():
+    """log1p at its special points and where it reduces to a textbook value: log1p(0) = 0, log1p(e - 1) = 1,
+    log1p(-1) = -inf, log1p(x) = x for tiny x, log1p(2^k - 1) = k ln 2."""
+    import ctypes as C
+    L = pyoracle.oracle_lib()
+    x = np.array([0.0, np.e - 1, -1.0, 1e-30, 1.0, 3.0, 7.0, 1023.0], np.float32)
+    y = np.empty_like(x)
+    L.or_log1pf_batch(pyoracle.ptr(x), pyoracle.ptr(y), len(x))
+    assert y[0] == 0.0 and abs(y[1] - 1.0) <= 1.2e-7 and y[2] == -np.inf and y[3] == np.float32(1e-30)
+    for i, k in ((4, 1), (5, 2), (6, 3), (7, 10)):
+        assert abs(float(y[i]) - k * np.log(2.0)) <= 1e-6 * k
+
+
 # --------------------------------------------------------------------------- whole models
 
 def tiny(name):
@@ -400,7 +424,7 @@ def tiny(name):
     return path, f, cfg, table
 
 
-@pytest.mark.parametrize("name", ["tiny-qwen3", "tiny-llama", "tiny-q8", "tiny-bitnet", "tiny-q5k", "tiny-q5", "tiny-qwen2", "tiny-smollm3", "tiny-gemma3", "tiny-phi3", "tiny-llama32", "tiny-lfm2"])
+@pytest.mark.parametrize("name", ["tiny-qwen3", "tiny-llama", "tiny-q8", "tiny-bitnet", "tiny-q5k", "tiny-q5", "tiny-qwen2", "tiny-smollm3", "tiny-gemma3", "tiny-phi3", "tiny-llama32", "tiny-lfm2", "tiny-qwen35", "tiny-qwen35w"])
 def test_oracle_greedy_matches_reference_fixture(name):
     """tests/golden/<name>_greedy.json were written by the reference engine itself."""
     with open(os.path.join(HERE, "golden", f"{name}_greedy.json")) as fh:
@@ -429,7 +453,7 @@ def test_oracle_first_tokens_of_qwen3_0_6b_fixture():
 
 
 @needs_ref
-@pytest.mark.parametrize("name", ["tiny-qwen3", "tiny-llama", "tiny-bitnet", "tiny-q5k", "tiny-q5", "tiny-qwen2", "tiny-smollm3", "tiny-gemma3", "tiny-phi3", "tiny-llama32", "tiny-lfm2"])
+@pytest.mark.parametrize("name", ["tiny-qwen3", "tiny-llama", "tiny-bitnet", "tiny-q5k", "tiny-q5", "tiny-qwen2", "tiny-smollm3", "tiny-gemma3", "tiny-phi3", "tiny-llama32", "tiny-lfm2", "tiny-qwen35", "tiny-qwen35w"])
 def test_oracle_session_matches_reference_bitwise(name):
     """eval, eval_all and rollback of the restatement against the reference's Session."""
     path, f, cfg, table = tiny(name)
@@ -443,7 +467,46 @@ def test_oracle_session_matches_reference_bitwise(name):
     a = o.eval(prompt[7:12], all_logits=True)
     b = r.eval_all(prompt[7:12])
     assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
-    assert o.position == r.position == 12
+    # Qwen3.5's recurrent states cannot step back to 7: the rollback restarted them at 0
+    assert o.position == r.position == (5 if cfg.arch == model.ARCH_QWEN35 else 12)
+    o.close()
+    r.close()
+
+
+@needs_ref
+@pytest.mark.parametrize("name", ["tiny-qwen35", "tiny-qwen35w"])
+def test_oracle_recurrent_snapshot_matches_reference_bitwise(name):
+    """Qwen3.5's rollback (src/model.cpp:735-752): one step back restores the snapshot taken before the last
+    token, whether that token came alone or at the end of a longer call; a second step back, or any other
+    earlier position, restarts at 0; rolling back to the current position changes nothing."""
+    path, f, cfg, table = tiny(name)
+    prompt = synth.prompt_ids(20, cfg.vocab, seed=5)
+    o = pyoracle.Oracle(cfg, table, max_context=64)
+    r = pyoracle.Reference(path, threads=2, max_context=64)
+    same = lambda a, b: np.array_equal(a.view(np.uint32), b.view(np.uint32))  # noqa: E731
+    first = o.eval(prompt[:10])
+    assert same(first, r.eval(prompt[:10]))
+    for h in (o, r):
+        h.rollback(10)  # the current position: nothing happens
+        h.rollback(9)   # the snapshot before the call's last token
+    assert o.position == r.position == 9
+    a, b = o.eval(prompt[9:10]), r.eval(prompt[9:10])
+    assert same(a, b) and same(a, first)  # the token again from the restored state
+    a, b = o.eval(prompt[10:11]), r.eval(prompt[10:11])
+    assert same(a, b)
+    for h in (o, r):
+        h.rollback(10)
+    again = o.eval(prompt[10:11])
+    assert same(again, r.eval(prompt[10:11])) and same(again, a)
+    for h in (o, r):
+        h.rollback(10)
+        h.rollback(9)   # the snapshot was used: a restart
+    assert o.position == r.position == 0
+    a, b = o.eval(prompt[:4], all_logits=True), r.eval_all(prompt[:4])
+    assert same(a, b)
+    for h in (o, r):
+        h.rollback(1)   # not the snapshot's position (3): a restart
+    assert o.position == r.position == 0
     o.close()
     r.close()
 
@@ -466,7 +529,7 @@ def test_oracle_longrope_matches_reference_bitwise():
 
 
 @needs_ref
-@pytest.mark.parametrize("name", ["tiny-qwen3", "tiny-llama", "tiny-bitnet", "tiny-q5k", "tiny-q5", "tiny-qwen2", "tiny-smollm3", "tiny-gemma3", "tiny-phi3", "tiny-llama32", "tiny-lfm2"])
+@pytest.mark.parametrize("name", ["tiny-qwen3", "tiny-llama", "tiny-bitnet", "tiny-q5k", "tiny-q5", "tiny-qwen2", "tiny-smollm3", "tiny-gemma3", "tiny-phi3", "tiny-llama32", "tiny-lfm2", "tiny-qwen35", "tiny-qwen35w"])
 def test_model_config_matches_reference(name):
     """brisk_hip.model.parse_config against the reference's own ModelConfig parse (src/model.cpp:140-260)
     of the same file, field by field. The Python config keeps 0 for a field its family does not use;
@@ -493,7 +556,13 @@ def test_model_config_matches_reference(name):
     assert f32(c.embedding_scale) == f32(np.sqrt(np.float32(cfg.embd)) if gemma else 1.0)
     assert bool(c.gelu) == gemma
     assert c.conv_taps == cfg.conv_taps
-    assert c.conv_layers == sum(1 << l for l in cfg.conv_layers)
+    # layer_is_conv (src/model.h:95) holds for every layer without key/value heads, Qwen3.5's recurrent
+    # ones included; eval_batch asks layer_is_recurrent first (src/model.cpp:932-934)
+    assert c.conv_layers == sum(1 << l for l in cfg.conv_layers + cfg.recurrent_layers)
+    assert c.recurrent_layers == sum(1 << l for l in cfg.recurrent_layers)
+    assert (c.ssm_state, c.ssm_k_heads, c.ssm_v_heads, c.ssm_inner, c.ssm_conv) == \
+        (cfg.ssm_state, cfg.ssm_k_heads, cfg.ssm_v_heads, cfg.ssm_inner, cfg.ssm_conv)
+    assert bool(c.attention_gate) == (cfg.arch == model.ARCH_QWEN35)
     assert c.no_rope_step == (4 if cfg.arch == model.ARCH_SMOLLM3 else 0)
     assert [l for l in range(cfg.layers) if not cfg.layer_has_rope(l)] == \
         ([l for l in range(cfg.layers) if (l + 1) % c.no_rope_step == 0] if c.no_rope_step else [])
