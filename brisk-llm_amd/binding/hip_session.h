@@ -38,6 +38,7 @@ public:
             case Architecture::Gemma3: cfg.arch = BRISK_HIP_ARCH_GEMMA3; break;
             case Architecture::Phi3: cfg.arch = BRISK_HIP_ARCH_PHI3; break;
             case Architecture::LFM2: cfg.arch = BRISK_HIP_ARCH_LFM2; break;
+            case Architecture::Qwen35: cfg.arch = BRISK_HIP_ARCH_QWEN35; break;
             default: throw std::runtime_error("hip: this architecture is not on the GPU path");
         }
         // ModelConfig (src/model.h:36-125)
@@ -63,6 +64,11 @@ public:
         cfg.no_rope_step = c.no_rope_step == 0 ? 0xFFFFFFFFu : c.no_rope_step;
         cfg.embedding_scale = c.embedding_scale;
         cfg.gelu = c.gelu ? 1 : 2;
+        cfg.ssm_state = c.ssm_state;
+        cfg.ssm_k_heads = c.ssm_k_heads;
+        cfg.ssm_v_heads = c.ssm_v_heads;
+        cfg.ssm_inner = c.ssm_inner;
+        cfg.ssm_conv = c.ssm_conv;
         for (std::size_t l = 0; l < c.layer_count; ++l)
             if (c.kv_head_count_of(l) != 0 && c.kv_head_count_of(l) != c.kv_head_count)
                 throw std::runtime_error("hip: attention layers with different key/value head counts are not on the GPU path");
@@ -82,7 +88,17 @@ public:
             const Model::Layer& L = model.layers()[l];
             const std::string b = "blk." + std::to_string(l) + ".";
             add_vector(b + "attn_norm.weight", L.attention_norm);
-            if (c.layer_is_conv(l)) {  // LFM2 short convolution
+            if (c.layer_is_recurrent(l)) {  // Qwen3.5 Gated DeltaNet
+                add_matrix(b + "attn_qkv.weight", L.ssm_qkv);
+                add_matrix(b + "attn_gate.weight", L.ssm_gate);
+                add_matrix(b + "ssm_alpha.weight", L.ssm_alpha);
+                add_matrix(b + "ssm_beta.weight", L.ssm_beta);
+                add_vector(b + "ssm_a", L.ssm_a);
+                add_vector(b + "ssm_dt.bias", L.ssm_dt_bias);
+                add_vector(b + "ssm_conv1d.weight", L.ssm_conv_weight);
+                add_vector(b + "ssm_norm.weight", L.ssm_norm);
+                add_matrix(b + "ssm_out.weight", L.ssm_out);
+            } else if (c.layer_is_conv(l)) {  // LFM2 short convolution
                 add_matrix(b + "shortconv.in_proj.weight", L.conv_in);
                 add_matrix(b + "shortconv.out_proj.weight", L.conv_out);
                 add_vector(b + "shortconv.conv.weight", L.conv_weight);
@@ -99,7 +115,9 @@ public:
                 add_matrix(b + "attn_output.weight", L.attention_output);
                 add_vector(b + "post_attention_norm.weight", L.attention_post_norm);
             }
-            add_vector(b + "ffn_norm.weight", L.feed_forward_norm);
+            // Qwen3.5 names the feed-forward norm post_attention_norm (src/model.cpp:418)
+            add_vector(b + (c.architecture == Architecture::Qwen35 ? "post_attention_norm.weight" : "ffn_norm.weight"),
+                       L.feed_forward_norm);
             add_matrix(b + "ffn_gate.weight", L.gate);  // Phi-3: row views of ffn_up
             add_matrix(b + "ffn_up.weight", L.up);
             add_vector(b + "ffn_sub_norm.weight", L.feed_forward_sub_norm);

@@ -17,7 +17,7 @@ _vp, _sz, _i, _f = C.c_void_p, C.c_size_t, C.c_int, C.c_float
 # Expected exports of include/brisk_hip.h (checked by tests/test_abi.py).
 EXPORTS = (
     "brisk_hip_last_error", "brisk_hip_abi_version", "brisk_hip_device_count", "brisk_hip_packed_bytes", "brisk_hip_pack",
-    "brisk_hip_quantize_q8_0", "brisk_hip_quantize_q8_k", "brisk_hip_matvec", "brisk_hip_matmul", "brisk_hip_matmul_noalloc", "brisk_hip_gemv", "brisk_hip_expf", "brisk_hip_tanhf",
+    "brisk_hip_quantize_q8_0", "brisk_hip_quantize_q8_k", "brisk_hip_matvec", "brisk_hip_matmul", "brisk_hip_matmul_noalloc", "brisk_hip_gemv", "brisk_hip_expf", "brisk_hip_tanhf", "brisk_hip_log1pf",
     "brisk_hip_div_selftest", "brisk_hip_mfma_rate",
     "brisk_hip_session_estimate", "brisk_hip_device_memory", "brisk_hip_session_create", "brisk_hip_session_destroy", "brisk_hip_session_eval", "brisk_hip_session_eval_all",
     "brisk_hip_session_eval_greedy", "brisk_hip_session_generate", "brisk_hip_session_decode", "brisk_hip_session_rollback",
@@ -33,7 +33,9 @@ class HipConfig(C.Structure):
                 ("sliding_window", C.c_uint32), ("rope_base_local", C.c_float), ("rope_scale", C.c_float),
                 ("final_softcap", C.c_float), ("rope_dim", C.c_uint32), ("rope_attn_factor", C.c_float),
                 ("rope_original_context", C.c_uint32), ("conv_taps", C.c_uint32), ("rope_neox", C.c_int32),
-                ("no_rope_step", C.c_uint32), ("embedding_scale", C.c_float), ("gelu", C.c_int32)]
+                ("no_rope_step", C.c_uint32), ("embedding_scale", C.c_float), ("gelu", C.c_int32),
+                ("ssm_state", C.c_uint32), ("ssm_k_heads", C.c_uint32), ("ssm_v_heads", C.c_uint32),
+                ("ssm_inner", C.c_uint32), ("ssm_conv", C.c_uint32)]
 
 
 class HipTensor(C.Structure):
@@ -74,6 +76,7 @@ def load():
     L.brisk_hip_gemv.argtypes = [_i, _i, _vp, _sz, _sz, _vp, _vp, _f, _vp, _i, _vp]
     L.brisk_hip_expf.argtypes = [_vp, _vp, _sz, _vp]
     L.brisk_hip_tanhf.argtypes = [_vp, _vp, _sz, _vp]
+    L.brisk_hip_log1pf.argtypes = [_vp, _vp, _sz, _vp]
     L.brisk_hip_div_selftest.argtypes = [C.POINTER(C.c_ulonglong)]
     L.brisk_hip_mfma_rate.argtypes = [_i, C.POINTER(C.c_double)]
     L.brisk_hip_session_estimate.argtypes = [C.POINTER(HipConfig), C.POINTER(HipTensor), _sz, _sz, C.POINTER(HipMemory)]

@@ -27,6 +27,8 @@ def _c_args(c, table):
     hc = _lib.HipConfig(c.arch, c.vocab, c.embd, c.layers, c.heads, c.kv_heads, c.head_dim, c.ff, c.context,
                         c.rope_base, c.eps, c.sliding_window, c.rope_base_local, c.rope_scale, c.final_softcap,
                         c.rope_dim, c.rope_attn_factor, c.rope_original_context, c.conv_taps)
+    hc.ssm_state, hc.ssm_k_heads, hc.ssm_v_heads = c.ssm_state, c.ssm_k_heads, c.ssm_v_heads
+    hc.ssm_inner, hc.ssm_conv = c.ssm_inner, c.ssm_conv
     names = [t.name.encode() for t in table]
     arr = (_lib.HipTensor * len(table))()
     for i, t in enumerate(table):

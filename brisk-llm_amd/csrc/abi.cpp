@@ -237,6 +237,10 @@ int brisk_hip_tanhf(const float* x, float* y, size_t n, void* stream) {
     return guarded([&] { hip_check(bh::launch_tanhf(x, y, n, static_cast<hipStream_t>(stream)), "tanhf"); });
 }
 
+int brisk_hip_log1pf(const float* x, float* y, size_t n, void* stream) {
+    return guarded([&] { hip_check(bh::launch_log1pf(x, y, n, static_cast<hipStream_t>(stream)), "log1pf"); });
+}
+
 int brisk_hip_div_selftest(unsigned long long* mismatches) {
     return guarded([&] {
         unsigned long long* d = nullptr;

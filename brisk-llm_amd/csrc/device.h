@@ -268,6 +268,69 @@ __device__ inline float ref_tanhf(float x) {
     return (jx & 0x80000000u) == 0 ? z : -z;
 }
 
+// ---------------------------------------------------------------- log1p
+
+// log1pf as the reference's host libm computes it (std::log1p on a float: the
+// softplus of Qwen3.5's recurrence, src/model.cpp:827).  glibc 2.35 builds it
+// from fdlibm's s_log1pf.c (no FMA variant on x86-64): 1 + x is split as
+// 2^k (1 + f), with a correction term c for the rounding of 1 + x when k != 0;
+// log(1 + f) = f - hfsq + s (hfsq + R(s^2)) with s = f / (2 + f), hfsq = f^2 / 2
+// and R a degree-7 polynomial in s^2; k ln2 is added back in a hi and a lo part.
+// This restatement gives glibc's result for every one of the 2^32 float inputs
+// (checked exhaustively on the host).
+__device__ inline float ref_log1pf(float x) {
+    const float ln2_hi = 6.9313812256e-01f, ln2_lo = 9.0580006145e-06f, two25 = 3.355443200e+07f;
+    const float Lp1 = 6.6666668653e-01f, Lp2 = 4.0000000596e-01f, Lp3 = 2.8571429849e-01f, Lp4 = 2.2222198546e-01f,
+                Lp5 = 1.8183572590e-01f, Lp6 = 1.5313838422e-01f, Lp7 = 1.4798198640e-01f;
+    float f = 0.0f, c = 0.0f, u;
+    const int32_t hx = static_cast<int32_t>(__float_as_uint(x)), ax = hx & 0x7fffffff;
+    int32_t k = 1, hu = 0;
+    if (hx < 0x3ed413d7) {  // x < 0.41422
+        if (ax >= 0x3f800000) return x == -1.0f ? -two25 / 0.0f : (x - x) / (x - x);  // x <= -1
+        if (ax < 0x31000000) return ax < 0x24800000 ? x : x - x * x * 0.5f;          // |x| < 2^-29
+        if (hx > 0 || hx <= static_cast<int32_t>(0xbe95f61fu)) {  // -0.2929 < x < 0.41422
+            k = 0;
+            f = x;
+            hu = 1;
+        }
+    } else if (hx >= 0x7f800000) {
+        return x + x;
+    }
+    if (k != 0) {
+        if (hx < 0x5a000000) {
+            u = 1.0f + x;
+            hu = static_cast<int32_t>(__float_as_uint(u));
+            k = (hu >> 23) - 127;
+            c = k > 0 ? 1.0f - (u - x) : x - (u - 1.0f);  // the rounding error of 1 + x
+            c /= u;
+        } else {
+            u = x;
+            hu = static_cast<int32_t>(__float_as_uint(u));
+            k = (hu >> 23) - 127;
+            c = 0.0f;
+        }
+        hu &= 0x007fffff;
+        if (hu < 0x3504f7) {
+            u = __uint_as_float(static_cast<uint32_t>(hu) | 0x3f800000u);
+        } else {
+            k += 1;
+            u = __uint_as_float(static_cast<uint32_t>(hu) | 0x3f000000u);
+            hu = (0x00800000 - hu) >> 2;
+        }
+        f = u - 1.0f;
+    }
+    const float hfsq = 0.5f * f * f;
+    const float fk = static_cast<float>(k);
+    if (hu == 0) {  // |f| < 2^-20
+        if (f == 0.0f) return k == 0 ? 0.0f : fk * ln2_hi + (c + fk * ln2_lo);
+        const float R = hfsq * (1.0f - 0.66666666666666666f * f);
+        return k == 0 ? f - R : fk * ln2_hi - ((R - (fk * ln2_lo + c)) - f);
+    }
+    const float s = f / (2.0f + f), z = s * s;
+    const float R = z * (Lp1 + z * (Lp2 + z * (Lp3 + z * (Lp4 + z * (Lp5 + z * (Lp6 + z * Lp7))))));
+    return k == 0 ? f - (hfsq - s * (hfsq + R)) : fk * ln2_hi - ((hfsq - (s * (hfsq + R) + (fk * ln2_lo + c))) - f);
+}
+
 // gelu_mul_f32's gate (src/kernels_f32.cpp:291-296): 0.5 x (1 + tanh(sqrt(2/pi) (x + 0.044715 x^3))),
 // in its left-to-right order, times up.
 __device__ __forceinline__ float gelu_mul(float x, float up) {

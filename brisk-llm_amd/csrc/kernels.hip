@@ -361,6 +361,117 @@ __global__ __launch_bounds__(kThreads) void k_conv(const float* __restrict__ bcx
     out[d] = acc * bcx[n + d];
 }
 
+// Qwen3.5 Gated DeltaNet, Session::forward_recurrent (src/model.cpp:754-865) for one
+// token: one workgroup per head h, thread j owning channel j of the head's q, k and v
+// and row j (value j) of its state.
+//   conv: x_c = SiLU(sum over taps i, oldest first, of w[c][i] in_i[c]), in_taps-1 the
+//         token's own attn_qkv row, the others the ring's (zero before position 0);
+//   q = x_q q_scale / sqrt(sum x_q^2 + eps), k = x_k / sqrt(sum x_k^2 + eps), each sum
+//         float and sequential (one lane each);
+//   decay = exp(softplus(alpha + dt) a), beta = sigmoid(beta);
+//   S[j][i] = S[j][i] decay; d_j = (v_j - sum_i S[j][i] k_i) beta;
+//   S[j][i] += k_i d_j; o_j = sum_i S[j][i] q_i   (both sums sequential in i);
+//   out = rms_norm(o, ssm_norm) SiLU(z).
+// The state is key-major ([i][j]), so a step of i reads and writes one contiguous row
+// across the lanes; it lives in two halves by position parity, so the half a token read
+// is still the state before that token (the reference's snapshot, src/model.cpp:798-812).
+__global__ __launch_bounds__(kThreads) void k_ssm(SsmArgs g) {
+    __shared__ float qs[kThreads], ks[kThreads];
+    __shared__ float inv[2];
+    __shared__ double red[4];
+    const int h = blockIdx.x, j = threadIdx.x, dim = g.dim, taps = g.taps, qkv = g.qkv_dim;
+    const int pos = *g.pos, k_off = g.heads * dim;
+    float v = 0.0f;
+    if (j < dim) {
+        for (int c = 0; c < 3; ++c) {  // q, k, v channels of head h
+            const int ch = c * k_off + h * dim + j;
+            const float cur = g.qkv[ch];
+            const float* w = g.conv_w + static_cast<size_t>(ch) * taps;
+            float acc = 0.0f;
+            for (int i = 0; i < taps; ++i) {
+                const int p = pos - (taps - 1) + i;
+                const float in = i == taps - 1 ? cur : p < 0 ? 0.0f : g.ring[static_cast<size_t>(p % taps) * qkv + ch];
+                acc = acc + w[i] * in;
+            }
+            g.ring[static_cast<size_t>(pos % taps) * qkv + ch] = cur;  // the slot of position pos - taps, read by no one
+            const float x = acc / (1.0f + ref_expf(-acc));
+            if (c == 0) qs[j] = x;
+            else if (c == 1) ks[j] = x;
+            else v = x;
+        }
+    }
+    __syncthreads();
+    if (j == 0 || j == 64) {  // the two L2 sums, one lane of two waves
+        const float* src = j == 0 ? qs : ks;
+        float sum = 0.0f;
+        for (int i = 0; i < dim; ++i) sum += src[i] * src[i];
+        inv[j == 0 ? 0 : 1] = (j == 0 ? g.q_scale : 1.0f) / sqrtf(sum + g.eps);
+    }
+    __syncthreads();
+    if (j < dim) {
+        qs[j] = qs[j] * inv[0];
+        ks[j] = ks[j] * inv[1];
+    }
+    const float alpha = g.ab[h] + g.dt[h];
+    const float softplus = alpha > 20.0f ? alpha : ref_log1pf(ref_expf(alpha));
+    const float decay = ref_expf(softplus * g.a[h]);
+    const float beta = 1.0f / (1.0f + ref_expf(-g.ab[g.heads + h]));
+    __syncthreads();
+    float o = 0.0f;
+    if (j < dim) {
+        const size_t plane = static_cast<size_t>(dim) * dim;
+        const float* sin = g.state + (static_cast<size_t>(pos & 1) * g.heads + h) * plane + j;
+        float* sout = g.state + (static_cast<size_t>((pos + 1) & 1) * g.heads + h) * plane + j;
+        const bool fresh = pos == 0;  // the zero state of a new or restarted sequence
+        float sk = 0.0f;
+#pragma unroll 8
+        for (int i = 0; i < dim; ++i) {
+            const float si = (fresh ? 0.0f : sin[static_cast<size_t>(i) * dim]) * decay;
+            sk = sk + si * ks[i];
+        }
+        const float d = (v - sk) * beta;
+#pragma unroll 8
+        for (int i = 0; i < dim; ++i) {
+            float si = (fresh ? 0.0f : sin[static_cast<size_t>(i) * dim]) * decay;
+            si = si + ks[i] * d;
+            sout[static_cast<size_t>(i) * dim] = si;
+            o = o + si * qs[i];
+        }
+    }
+    double sq = j < dim ? static_cast<double>(o * o) : 0.0;
+    sq = wave_sum(sq);
+    if ((j & 63) == 0) red[j >> 6] = sq;
+    __syncthreads();
+    const float scale = rms_scale(((red[0] + red[1]) + red[2]) + red[3], dim, g.eps);
+    if (j < dim) {
+        const float z = g.z[h * dim + j];
+        const float gate = z / (1.0f + ref_expf(-z));
+        g.out[h * dim + j] = o * scale * g.norm[j] * gate;
+    }
+}
+
+// Qwen3.5's query projection holds each head's query rows followed by its gate rows
+// (src/model.cpp:1002-1012).
+__global__ void k_qgate_split(const float* __restrict__ qg, float* __restrict__ q, float* __restrict__ gate, int hd, int n) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    const int h = i / hd, d = i - h * hd;
+    q[i] = qg[2 * h * hd + d];
+    gate[i] = qg[2 * h * hd + hd + d];
+}
+
+// att *= 1 / (1 + exp(-gate)) (src/model.cpp:1102-1108).
+__global__ void k_sigmoid_gate(float* __restrict__ att, const float* __restrict__ gate, int n) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) att[i] = att[i] * (1.0f / (1.0f + ref_expf(-gate[i])));
+}
+
+// log1pf as the recurrence computes it (ref_log1pf), for the parity tests.
+__global__ void k_log1pf(const float* __restrict__ x, float* __restrict__ y, size_t n) {
+    const size_t i = static_cast<size_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (i < n) y[i] = ref_log1pf(x[i]);
+}
+
 // tanhf as the Gemma epilogues compute it (ref_tanhf), for the parity tests.
 __global__ void k_tanhf(const float* __restrict__ x, float* __restrict__ y, size_t n) {
     const size_t i = static_cast<size_t>(blockIdx.x) * blockDim.x + threadIdx.x;
@@ -604,6 +715,32 @@ int attention_max_splits(int ctx) { return (ctx + kSplit - 1) / kSplit; }
 
 hipError_t launch_post_add(float* h, const float* p, const float* w, float eps, int n, hipStream_t s) {
     hipLaunchKernelGGL(k_post_add, dim3(1), dim3(kThreads), 0, s, h, p, w, eps, n);
+    return hipGetLastError();
+}
+
+hipError_t launch_ssm(const SsmArgs& g, hipStream_t s) {
+    if (g.dim < 1 || g.dim > kThreads || g.heads < 1 || g.taps < 2 || g.taps > 8 || g.qkv_dim != 3 * g.heads * g.dim)
+        return hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_ssm, dim3(static_cast<unsigned>(g.heads)), dim3(kThreads), 0, s, g);
+    return hipGetLastError();
+}
+
+hipError_t launch_qgate_split(const float* qg, float* q, float* gate, int heads, int hd, hipStream_t s) {
+    const int n = heads * hd;
+    hipLaunchKernelGGL(k_qgate_split, dim3(static_cast<unsigned>((n + kThreads - 1) / kThreads)), dim3(kThreads), 0, s, qg, q,
+                       gate, hd, n);
+    return hipGetLastError();
+}
+
+hipError_t launch_sigmoid_gate(float* att, const float* gate, int n, hipStream_t s) {
+    hipLaunchKernelGGL(k_sigmoid_gate, dim3(static_cast<unsigned>((n + kThreads - 1) / kThreads)), dim3(kThreads), 0, s, att,
+                       gate, n);
+    return hipGetLastError();
+}
+
+hipError_t launch_log1pf(const float* x, float* y, size_t n, hipStream_t s) {
+    if (n == 0) return hipSuccess;
+    hipLaunchKernelGGL(k_log1pf, dim3(static_cast<unsigned>((n + 255) / 256)), dim3(256), 0, s, x, y, n);
     return hipGetLastError();
 }
 

@@ -21,7 +21,7 @@ struct GemvTarget {
 };
 
 struct GemvArgs {
-    GemvTarget t[3];
+    GemvTarget t[4];
     int n;                // targets
     const float* x;       // activation row (f32)
     const float* normw;   // rms_norm weight applied to x first, or null
@@ -70,6 +70,23 @@ struct AttnArgs {
     unsigned long long* stamps;  // optional profiling: key/value head 0's wall clock at sub-phase ends
 };
 
+// One token of a Qwen3.5 Gated DeltaNet layer after its projections (src/model.cpp:754-865).
+struct SsmArgs {
+    const float* qkv;     // this token's attn_qkv rows [q | k | v] before the conv (qkv_dim)
+    const float* z;       // attn_gate rows [heads][dim]
+    const float* ab;      // ssm_alpha rows [heads], then ssm_beta rows [heads]
+    const float* conv_w;  // ssm_conv1d [qkv_dim][taps]
+    const float* a;       // ssm_a [heads]
+    const float* dt;      // ssm_dt.bias [heads]
+    const float* norm;    // ssm_norm [dim]
+    float* ring;          // [taps][qkv_dim]: slot p % taps holds position p's attn_qkv rows
+    float* state;         // [2][heads][dim (key i)][dim (value j)]: position p reads half p & 1, writes the other
+    const int* pos;
+    float* out;           // [heads][dim]
+    int heads, dim, taps, qkv_dim;
+    float eps, q_scale;
+};
+
 // The pending greedy pick and the sequence state it updates.
 struct PickState {
     unsigned long long* key;   // 0 = no pick pending; else the ordered (logit, index) key of the best row
@@ -110,6 +127,12 @@ hipError_t launch_tanhf(const float* x, float* y, size_t n, hipStream_t s);
 // w [n][taps]; out = c * sum_k w[d][k] bx[pos + k + 1 - taps] with bx = b * x stored at pos.
 hipError_t launch_conv(const float* bcx, uint16_t* cache, const float* w, int taps, const int* pos, int n, float* out,
                        hipStream_t s);
+// Qwen3.5: one recurrent layer's conv, delta-rule state update and gated norm (one workgroup a head).
+hipError_t launch_ssm(const SsmArgs& g, hipStream_t s);
+// Qwen3.5 attention: [heads][q | gate] rows split into q and gate; att *= sigmoid(gate).
+hipError_t launch_qgate_split(const float* qg, float* q, float* gate, int heads, int hd, hipStream_t s);
+hipError_t launch_sigmoid_gate(float* att, const float* gate, int n, hipStream_t s);
+hipError_t launch_log1pf(const float* x, float* y, size_t n, hipStream_t s);
 hipError_t launch_div_selftest(unsigned long long* bad, hipStream_t s);
 hipError_t launch_mfma_rate(int shape, int blocks, int iters, int* out, hipStream_t s);
 int attention_max_splits(int ctx);

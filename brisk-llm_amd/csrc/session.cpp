@@ -157,13 +157,27 @@ brisk_hip_memory estimate_session(const brisk_hip_config& cfg, const brisk_hip_t
             if (name.size() > suffix.size() && name.compare(name.size() - suffix.size(), suffix.size(), suffix) == 0) ++conv_layers;
         }
     conv_layers = std::min<size_t>(conv_layers, cfg.layers);
-    m.cache = 2 * (static_cast<size_t>(cfg.layers) - conv_layers) * kvd * ctx * 2 + conv_layers * ctx * e * 2;
+    // a Qwen3.5 Gated DeltaNet layer (one with blk.N.ssm_a) holds its state in two halves and
+    // the conv's last inputs (src/memory.cpp:62-63)
+    size_t rec_layers = 0;
+    const size_t ssm_qkv = 3 * static_cast<size_t>(cfg.ssm_v_heads) * cfg.ssm_state;
+    if (cfg.arch == BRISK_HIP_ARCH_QWEN35)
+        for (size_t i = 0; i < n; ++i) {
+            const std::string name = tensors[i].name != nullptr ? tensors[i].name : "";
+            const std::string suffix = ".ssm_a";
+            if (name.size() > suffix.size() && name.compare(name.size() - suffix.size(), suffix.size(), suffix) == 0) ++rec_layers;
+        }
+    rec_layers = std::min<size_t>(rec_layers, cfg.layers - conv_layers);
+    m.cache = 2 * (static_cast<size_t>(cfg.layers) - conv_layers - rec_layers) * kvd * ctx * 2 + conv_layers * ctx * e * 2 +
+              rec_layers * (2 * static_cast<size_t>(cfg.ssm_v_heads) * cfg.ssm_state * cfg.ssm_state + cfg.ssm_conv * ssm_qkv) * 4;
     const size_t splits = static_cast<size_t>(attention_max_splits(static_cast<int>(ctx)));
     size_t sc = (e + 2 * qd + ff + cfg.vocab + 2 * kvd) * 4;              // token-path activations, logits
     sc += static_cast<size_t>(cfg.heads) * splits * (hd + 2) * 4;          // attention partials
     sc += (ctx + 1) * 4 + ctx * hd * 4;                                    // token sequence, RoPE table
     if (cfg.arch == BRISK_HIP_ARCH_GEMMA3) sc += ctx * hd * 4 + e * 4;     // local RoPE table, post-norm input
     if (cfg.arch == BRISK_HIP_ARCH_LFM2) sc += 3 * e * 4;                  // conv rows
+    if (cfg.arch == BRISK_HIP_ARCH_QWEN35)                                 // recurrence rows, query|gate rows, gates
+        sc += (ssm_qkv + 2 * static_cast<size_t>(cfg.ssm_inner) + 2 * cfg.ssm_v_heads + 3 * qd) * 4;
     sc += (e + 2 * qd + 2 * kvd + ff + static_cast<size_t>(cfg.heads) * splits * (hd + 2) +
            static_cast<size_t>(cfg.heads) * ctx) * 8;                      // hand-off words (with the spread scores)
     const size_t T = Session::kPrefillTokens, widest = std::max(std::max(e, qd), ff), stride = (widest + 255) / 256 * 256;
@@ -218,7 +232,14 @@ Session::Session(const brisk_hip_config& cfg, const brisk_hip_tensor* tensors, s
     int count = 0;
     if (hipGetDeviceCount(&count) != hipSuccess || count == 0) throw Error(BRISK_HIP_ENODEV, "hip: no GPU device available");
     if (device < 0 || device >= count) throw Error(BRISK_HIP_ENODEV, "hip: no GPU device " + std::to_string(device));
-    if (cfg.arch < BRISK_HIP_ARCH_QWEN3 || cfg.arch > BRISK_HIP_ARCH_LFM2) model_fail("unsupported architecture");
+    if (cfg.arch < BRISK_HIP_ARCH_QWEN3 || cfg.arch > BRISK_HIP_ARCH_QWEN35) model_fail("unsupported architecture");
+    if (cfg.arch == BRISK_HIP_ARCH_QWEN35) {  // src/model.cpp:262-265, :675
+        if (cfg.ssm_v_heads == 0 || cfg.ssm_inner % cfg.ssm_v_heads != 0 || cfg.ssm_inner / cfg.ssm_v_heads != cfg.ssm_state ||
+            cfg.ssm_k_heads != cfg.ssm_v_heads || cfg.ssm_conv < 2 || cfg.ssm_conv > 8)
+            model_fail("qwen35: unsupported DeltaNet shape (equal key and value heads of state_size values are supported)");
+        if (cfg.ssm_state > 256) model_fail("qwen35: a DeltaNet state wider than 256 is not supported");
+        if (cfg.ssm_inner > kMaxCols) model_fail("a row wider than 8192 is not supported");
+    }
     if (cfg.arch == BRISK_HIP_ARCH_LFM2 && (cfg.conv_taps < 2 || cfg.conv_taps > 8)) model_fail("unsupported short-convolution width");
     if (cfg.rope_dim > cfg.head_dim || cfg.rope_dim % 2 != 0) model_fail("rope dimension count must be even and at most the head size");
     if (cfg.embd == 0 || cfg.layers == 0 || cfg.heads == 0 || cfg.kv_heads == 0 || cfg.ff == 0 || cfg.context_length == 0 ||
@@ -319,6 +340,25 @@ Session::Session(const brisk_hip_config& cfg, const brisk_hip_tensor* tensors, s
         const std::string b = "blk." + std::to_string(l) + ".";
         Layer& L = layers_[l];
         L.attn_norm = load_vector(b + "attn_norm.weight", e);
+        if (cfg.arch == BRISK_HIP_ARCH_QWEN35 && find(b + "ssm_a") != nullptr) {  // src/model.cpp:343-358
+            const size_t qkv = 3 * static_cast<size_t>(cfg.ssm_v_heads) * cfg.ssm_state;
+            load_matrix(b + "attn_qkv.weight", qkv, e, L.ssm_qkv);
+            load_matrix(b + "attn_gate.weight", cfg.ssm_inner, e, L.ssm_gate);
+            load_matrix(b + "ssm_alpha.weight", cfg.ssm_v_heads, e, L.ssm_alpha);
+            load_matrix(b + "ssm_beta.weight", cfg.ssm_v_heads, e, L.ssm_beta);
+            L.ssm_a = load_vector(b + "ssm_a", cfg.ssm_v_heads);
+            L.ssm_dt = load_vector(b + "ssm_dt.bias", cfg.ssm_v_heads);
+            L.ssm_conv_w = load_vector(b + "ssm_conv1d.weight", static_cast<size_t>(cfg.ssm_conv) * qkv);
+            L.ssm_norm = load_vector(b + "ssm_norm.weight", cfg.ssm_state);
+            load_matrix(b + "ssm_out.weight", e, cfg.ssm_inner, L.ssm_out);
+            L.ffn_norm = load_vector(b + "post_attention_norm.weight", e);
+            load_matrix(b + "ffn_gate.weight", cfg.ff, e, L.gate);
+            load_matrix(b + "ffn_up.weight", cfg.ff, e, L.up);
+            load_matrix(b + "ffn_down.weight", e, cfg.ff, L.down);
+            if (takes_q8_k(L.gate.p.type) != takes_q8_k(L.up.p.type) || act_bits(L.gate.p) != act_bits(L.up.p))
+                model_fail("fused multiply mixes activation widths");
+            continue;
+        }
         if (cfg.arch == BRISK_HIP_ARCH_LFM2 && find(b + "shortconv.in_proj.weight") != nullptr) {  // src/model.cpp:360-364
             load_matrix(b + "shortconv.in_proj.weight", 3 * e, e, L.conv_in);
             load_matrix(b + "shortconv.out_proj.weight", e, e, L.conv_out);
@@ -336,16 +376,16 @@ Session::Session(const brisk_hip_config& cfg, const brisk_hip_tensor* tensors, s
             load_rows(b + "ffn_up.weight", 0, cfg.ff, 2 * static_cast<size_t>(cfg.ff), e, L.gate);
             load_rows(b + "ffn_up.weight", cfg.ff, cfg.ff, 2 * static_cast<size_t>(cfg.ff), e, L.up);
         } else {
-            load_matrix(b + "attn_q.weight", qd, e, L.q);
+            load_matrix(b + "attn_q.weight", qwen35() ? 2 * qd : qd, e, L.q);  // Qwen3.5: each head's query, then its gate
             load_matrix(b + "attn_k.weight", kvd, e, L.k);
             load_matrix(b + "attn_v.weight", kvd, e, L.v);
             load_matrix(b + "ffn_gate.weight", cfg.ff, e, L.gate);
             load_matrix(b + "ffn_up.weight", cfg.ff, e, L.up);
         }
         load_matrix(b + "attn_output.weight", e, qd, L.o);
-        L.ffn_norm = load_vector(b + "ffn_norm.weight", e);
+        L.ffn_norm = load_vector(b + (qwen35() ? "post_attention_norm.weight" : "ffn_norm.weight"), e);  // src/model.cpp:418
         load_matrix(b + "ffn_down.weight", e, cfg.ff, L.down);
-        if (cfg.arch == BRISK_HIP_ARCH_QWEN3 || cfg.arch == BRISK_HIP_ARCH_GEMMA3 || cfg.arch == BRISK_HIP_ARCH_LFM2) {
+        if (cfg.arch == BRISK_HIP_ARCH_QWEN3 || cfg.arch == BRISK_HIP_ARCH_GEMMA3 || cfg.arch == BRISK_HIP_ARCH_LFM2 || qwen35()) {
             L.q_norm = load_vector(b + "attn_q_norm.weight", hd);
             L.k_norm = load_vector(b + "attn_k_norm.weight", hd);
         }
@@ -380,8 +420,25 @@ Session::Session(const brisk_hip_config& cfg, const brisk_hip_tensor* tensors, s
         for (Layer& L : layers_)
             if (L.conv_w != nullptr) L.conv_cache = static_cast<uint16_t*>(alloc(max_ctx_ * e * 2));
     }
+    if (qwen35()) {
+        const size_t qkv = 3 * static_cast<size_t>(cfg.ssm_v_heads) * cfg.ssm_state;
+        ssm_qkv_ = static_cast<float*>(alloc(qkv * 4));
+        ssm_z_ = static_cast<float*>(alloc(static_cast<size_t>(cfg.ssm_inner) * 4));
+        ssm_ab_ = static_cast<float*>(alloc(2 * static_cast<size_t>(cfg.ssm_v_heads) * 4));
+        qg_ = static_cast<float*>(alloc(2 * qd * 4));
+        agate_ = static_cast<float*>(alloc(qd * 4));
+        for (Layer& L : layers_) {
+            if (L.ssm_a == nullptr) continue;
+            const size_t ring = static_cast<size_t>(cfg.ssm_conv) * qkv * 4,
+                         state = 2 * static_cast<size_t>(cfg.ssm_v_heads) * cfg.ssm_state * cfg.ssm_state * 4;
+            L.ssm_ring = static_cast<float*>(alloc(ring));
+            L.ssm_state = static_cast<float*>(alloc(state));
+            check(hipMemsetAsync(L.ssm_ring, 0, ring, stream_), "memset");
+            check(hipMemsetAsync(L.ssm_state, 0, state, stream_), "memset");
+        }
+    }
     q_ = static_cast<float*>(alloc(qd * 4));
-    att_ = static_cast<float*>(alloc(qd * 4));
+    att_ = static_cast<float*>(alloc(std::max<size_t>(qd, cfg.ssm_inner) * 4));
     act_ = static_cast<float*>(alloc(static_cast<size_t>(cfg.ff) * 4));
     logits_ = static_cast<float*>(alloc(static_cast<size_t>(cfg.vocab) * 4));
     max_splits_ = attention_max_splits(static_cast<int>(max_ctx_));
@@ -402,6 +459,7 @@ Session::Session(const brisk_hip_config& cfg, const brisk_hip_tensor* tensors, s
     vcache_.assign(cfg.layers, nullptr);
     for (uint32_t l = 0; l < cfg.layers; ++l) {
         if (layers_[l].conv_w != nullptr) continue;  // a short-convolution layer keeps its bx rows instead (LFM2)
+        if (layers_[l].ssm_a != nullptr) continue;   // a recurrent layer keeps its state instead (Qwen3.5)
         kcache_[l] = static_cast<uint16_t*>(alloc(kv_bytes));
         vcache_[l] = static_cast<uint16_t*>(alloc(kv_bytes));
         check(hipMemsetAsync(kcache_[l], 0, kv_bytes, stream_), "memset");
@@ -522,10 +580,42 @@ void Session::record_step(bool full) {
             co.x = att_; co.normw = nullptr; co.eps = cfg_.rms_epsilon; co.add = 1;
             check(launch_gemv(co, stream_), "conv out_proj");
         }
+        if (L.ssm_a != nullptr) {  // Qwen3.5 Gated DeltaNet in place of attention (src/model.cpp:754-865)
+            // attn_qkv, attn_gate, ssm_alpha and ssm_beta rows from attn_norm(h): one launch per weight format
+            const DeviceMatrix* mats[4] = {&L.ssm_qkv, &L.ssm_gate, &L.ssm_alpha, &L.ssm_beta};
+            float* outs[4] = {ssm_qkv_, ssm_z_, ssm_ab_, ssm_ab_ + cfg_.ssm_v_heads};
+            GemvArgs ia{};
+            ia.x = h_; ia.normw = L.attn_norm; ia.eps = cfg_.rms_epsilon; ia.add = 0;
+            bool done[4] = {false, false, false, false};
+            for (int i = 0; i < 4; ++i) {
+                if (done[i]) continue;
+                ia.n = 0;
+                for (int j = i; j < 4; ++j) {
+                    if (!done[j] && mats[j]->p.type == mats[i]->p.type) {
+                        ia.t[ia.n].m = mats[j]->p;
+                        ia.t[ia.n].out = outs[j];
+                        ++ia.n;
+                        done[j] = true;
+                    }
+                }
+                check(launch_gemv(ia, stream_), "recurrence projections");
+            }
+            SsmArgs sa{};
+            sa.qkv = ssm_qkv_; sa.z = ssm_z_; sa.ab = ssm_ab_; sa.conv_w = L.ssm_conv_w; sa.a = L.ssm_a; sa.dt = L.ssm_dt;
+            sa.norm = L.ssm_norm; sa.ring = L.ssm_ring; sa.state = L.ssm_state; sa.pos = pos_; sa.out = att_;
+            sa.heads = static_cast<int>(cfg_.ssm_v_heads); sa.dim = static_cast<int>(cfg_.ssm_state);
+            sa.taps = static_cast<int>(cfg_.ssm_conv); sa.qkv_dim = 3 * sa.heads * sa.dim;
+            sa.eps = cfg_.rms_epsilon; sa.q_scale = 1.0f / std::sqrt(static_cast<float>(cfg_.ssm_state));  // src/model.cpp:813
+            check(launch_ssm(sa, stream_), "recurrence");
+            GemvArgs so{};
+            so.n = 1; so.t[0].m = L.ssm_out.p; so.t[0].out = h_;
+            so.x = att_; so.normw = nullptr; so.eps = cfg_.rms_epsilon; so.add = 1;
+            check(launch_gemv(so, stream_), "ssm_out");
+        }
         // Q, K, V rows from attn_norm(h) (src/model.cpp:996-1015): one launch per weight format
-        if (L.conv_w == nullptr) {
+        if (L.conv_w == nullptr && L.ssm_a == nullptr) {
             const DeviceMatrix* mats[3] = {&L.q, &L.k, &L.v};
-            float* outs[3] = {q_, k_, v_};
+            float* outs[3] = {qwen35() ? qg_ : q_, k_, v_};
             GemvArgs qa{};
             qa.x = h_; qa.normw = L.attn_norm; qa.eps = cfg_.rms_epsilon; qa.add = 0;
             bool done[3] = {false, false, false};
@@ -542,9 +632,10 @@ void Session::record_step(bool full) {
                 }
                 check(launch_gemv(qa, stream_), "qkv");
             }
+            if (qwen35()) check(launch_qgate_split(qg_, q_, agate_, static_cast<int>(cfg_.heads), static_cast<int>(cfg_.head_dim), stream_), "query gate");
         }
 
-        if (L.conv_w == nullptr) {
+        if (L.conv_w == nullptr && L.ssm_a == nullptr) {
         AttnArgs aa{};
         aa.q = q_; aa.k = k_; aa.v = v_; aa.qnorm = L.q_norm; aa.knorm = L.k_norm;
         aa.rope = !L.rope ? nullptr : L.slides ? rope_local_ : rope_;
@@ -561,6 +652,7 @@ void Session::record_step(bool full) {
         // (heads x max_splits x head_dim, head_dim >= the split length)
         aa.gsc = cfg_.head_dim >= static_cast<uint32_t>(kSplit) ? part_acc_ : nullptr;
         check(launch_attention(aa, stream_), "attention");
+        if (qwen35()) check(launch_sigmoid_gate(att_, agate_, static_cast<int>(cfg_.heads * cfg_.head_dim), stream_), "attention gate");
 
         // h += W_o att, or with a post-norm h += rms_norm(W_o att) (src/model.cpp:1113-1121)
         GemvArgs oa{};
@@ -624,7 +716,7 @@ void Session::setup_loop() {
     // the loop's exact attentions hold at most 4 outputs a thread (heads per kv head x head size <= 1024)
     if ((cfg_.heads / cfg_.kv_heads) * cfg_.head_dim > 4 * kThreads) return;
     if (embd_.p.type != out_->p.type) return;  // the loop reads the embedding in its output's format
-    if (gemma() || lfm2()) return;  // post-norms, windows, softcap and convolutions are graph-path phases only
+    if (gemma() || lfm2() || qwen35()) return;  // post-norms, windows, softcap, convolutions, recurrences: graph-path phases only
     const Layer& L0 = layers_[0];
     const void* k = find_loop_kernel(L0.q.p.type, L0.v.p.type, L0.o.p.type, L0.gate.p.type, L0.down.p.type, out_->p.type);
     if (k == nullptr) return;
@@ -962,6 +1054,7 @@ bool Session::use_prefill(size_t n) const {
     // Gemma 3 (sliding layers, post-norms, GELU, soft-capped logits) and LFM2 (short convolutions)
     // take the exact attention only
     if (gemma() || lfm2()) return prefill_on_ && n >= 2 && exact_fits && cfg_.head_dim <= 128;
+    if (qwen35()) return false;  // the recurrence takes its tokens one at a time
     return prefill_on_ && n >= 2 && (exact_fits || mfma_fits);
 }
 
@@ -1083,6 +1176,7 @@ void Session::eval(const int32_t* tokens, size_t n, float* logits) {
         finish();
         fetch_logits(logits, logits_, 1);
         position_ += n;
+        evaluated();
         return;
     }
     stage(tokens, n);
@@ -1096,6 +1190,7 @@ void Session::eval(const int32_t* tokens, size_t n, float* logits) {
     fetch_logits(logits, logits_, 1);
     check_loop_error();
     position_ += n;
+    evaluated();
 }
 
 void Session::eval_all(const int32_t* tokens, size_t n, float* logits) {
@@ -1124,6 +1219,7 @@ void Session::eval_all(const int32_t* tokens, size_t n, float* logits) {
         finish();
         fetch_logits(logits, all_logits_, n);
         position_ += n;
+        evaluated();
         return;
     }
     stage(tokens, n);
@@ -1142,6 +1238,7 @@ void Session::eval_all(const int32_t* tokens, size_t n, float* logits) {
     std::memcpy(logits, hb, n * row);
     check_loop_error();
     position_ += n;
+    evaluated();
 }
 
 int32_t Session::picked() {
@@ -1172,6 +1269,7 @@ void Session::generate(const int32_t* prompt, size_t n_prompt, size_t n_gen, int
     check(hipStreamSynchronize(stream_), "generate sync");
     check_loop_error();
     position_ += n_gen - 1;
+    evaluated();
 }
 
 void Session::decode(size_t n, int32_t* out) {
@@ -1193,16 +1291,34 @@ void Session::decode(size_t n, int32_t* out) {
     check(hipStreamSynchronize(stream_), "decode sync");
     check_loop_error();
     position_ += n;
+    evaluated();
+}
+
+// After a call that evaluated tokens up to position_ - 1: the recurrent layers' input state of that
+// last token is still held (the half of its parity), so rollback can step back to it, as it can to
+// the reference's snapshot taken before a batch's last token (src/model.cpp:798-812).
+void Session::evaluated() {
+    snap_ok_ = qwen35() && position_ > 0;
+    snap_pos_ = position_ - 1;
 }
 
 void Session::rollback(size_t position) {
     if (position > position_) throw Error(BRISK_HIP_EINVAL, "model: cannot roll forward");  // src/model.cpp:736
+    if (qwen35() && position != position_) {
+        // The recurrent states absorb every token: they step back to the last evaluated token's
+        // input state, or start over at 0 (src/model.cpp:737-750).  At position 0 the recurrence
+        // reads a zero state and the conv zero inputs, whatever the buffers hold.
+        if (!(snap_ok_ && position == snap_pos_)) position = 0;
+        snap_ok_ = false;
+    }
     position_ = position;  // the caches keep their storage; later entries are overwritten
 }
 
 void Session::set_position(size_t position) {
     if (position > max_ctx_) throw Error(BRISK_HIP_EINVAL, "model: context length exceeded");
+    if (qwen35() && position != 0) throw Error(BRISK_HIP_EINVAL, "model: a recurrent model cannot start past position 0");
     position_ = position;
+    snap_ok_ = false;
 }
 
 void Session::kv_cache(int layer, int value, void** ptr, size_t* bytes) {

@@ -55,6 +55,14 @@ struct Layer {
     DeviceMatrix conv_in, conv_out; // LFM2 short-convolution layer: in_proj (3 embd rows), out_proj
     const float* conv_w = nullptr;  // [embd][taps]; non-null marks a convolution layer
     uint16_t* conv_cache = nullptr; // bx per position, fp16 [ctx][embd]
+    // Qwen3.5 Gated DeltaNet layer (src/model.cpp:343-358); ssm_a non-null marks it
+    DeviceMatrix ssm_qkv, ssm_gate, ssm_alpha, ssm_beta, ssm_out;
+    const float* ssm_a = nullptr;
+    const float* ssm_dt = nullptr;
+    const float* ssm_conv_w = nullptr;  // [qkv_dim][conv]
+    const float* ssm_norm = nullptr;
+    float* ssm_ring = nullptr;          // [conv][qkv_dim]: slot p % conv holds position p's attn_qkv rows
+    float* ssm_state = nullptr;         // [2][heads][state (key)][state (value)], halves by position parity
 };
 
 // Device bytes a session of these tensors would allocate (see Session's constructor).
@@ -104,6 +112,8 @@ private:
     bool neox() const;
     bool gemma() const { return cfg_.arch == BRISK_HIP_ARCH_GEMMA3; }
     bool lfm2() const { return cfg_.arch == BRISK_HIP_ARCH_LFM2; }
+    bool qwen35() const { return cfg_.arch == BRISK_HIP_ARCH_QWEN35; }
+    void evaluated();
     void prefill_quant(const float* x, int xstride, const float* w, int cols, int T, const DeviceMatrix& consumer);
 
     brisk_hip_config cfg_;
@@ -124,6 +134,12 @@ private:
     float* rope_local_ = nullptr;  // Gemma 3 sliding layers' RoPE table
     float* proj_ = nullptr;        // Gemma: a projection's output before its post-norm
     float* conv_buf_ = nullptr;    // LFM2: in_proj's [b | c | x] rows
+    // Qwen3.5: the recurrent layers' projections, the attention layers' query|gate rows and gates
+    float *ssm_qkv_ = nullptr, *ssm_z_ = nullptr, *ssm_ab_ = nullptr, *qg_ = nullptr, *agate_ = nullptr;
+    // Qwen3.5: the recurrent states can step back to snap_pos_ (the last evaluated token's
+    // position, whose input state is still held) while snap_ok_
+    bool snap_ok_ = false;
+    size_t snap_pos_ = 0;
     float embd_scale_ = 1.0f;      // Gemma: sqrt(embd) (src/model.cpp:286)
     int rope_dim_ = 0;             // dimensions the RoPE table rotates (its row stride)
     unsigned long long* key_ = nullptr;

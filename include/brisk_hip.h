@@ -63,7 +63,8 @@ enum {
     BRISK_HIP_ARCH_SMOLLM3 = 4, /* Llama-shaped; every fourth layer attends without RoPE */
     BRISK_HIP_ARCH_GEMMA3 = 5,  /* Q/K norms, post-norms, GELU gate, sliding-window layers, scaled embeddings */
     BRISK_HIP_ARCH_PHI3 = 6,    /* fused QKV and gate/up tensors, partial rotary, LongRoPE factors */
-    BRISK_HIP_ARCH_LFM2 = 7     /* short-convolution layers (those with blk.N.shortconv.* tensors) between attention layers */
+    BRISK_HIP_ARCH_LFM2 = 7,    /* short-convolution layers (those with blk.N.shortconv.* tensors) between attention layers */
+    BRISK_HIP_ARCH_QWEN35 = 8   /* Gated DeltaNet layers (those with blk.N.ssm_a) between gated attention layers */
 };
 
 /* The fields of ModelConfig (src/model.h:36-60) this path reads. */
@@ -86,6 +87,12 @@ typedef struct {
     uint32_t no_rope_step;   /* every no_rope_step-th layer attends without RoPE (SmolLM3: 4); 0xFFFFFFFF: none */
     float embedding_scale;   /* the embedding rows are multiplied by it (Gemma: sqrt(embd)) */
     int32_t gelu;            /* 1: GELU (tanh) gating (Gemma); 2: SiLU / the family's */
+    /* Qwen3.5's Gated DeltaNet layers (ModelConfig, src/model.h:100-109); zero elsewhere: */
+    uint32_t ssm_state;      /* ssm.state_size: a head's state is ssm_state x ssm_state, at most 256 */
+    uint32_t ssm_k_heads;    /* ssm.group_count */
+    uint32_t ssm_v_heads;    /* ssm.time_step_rank (equal to ssm_k_heads) */
+    uint32_t ssm_inner;      /* ssm.inner_size = ssm_v_heads x ssm_state */
+    uint32_t ssm_conv;       /* ssm.conv_kernel: the causal conv's width, 2 to 8 */
 } brisk_hip_config;
 
 /* One model tensor in GGUF layout (host memory, e.g. the file's mmap):
@@ -170,6 +177,12 @@ int brisk_hip_expf(const float* x, float* y, size_t n, void* stream);
  * src/model.cpp:1206-1209); the Gemma epilogues use the same device routine.
  * y[i] = tanhf(x[i]). */
 int brisk_hip_tanhf(const float* x, float* y, size_t n, void* stream);
+
+/* log1pf exactly as the reference's host libm computes it (glibc 2.35's, the
+ * softplus of Qwen3.5's recurrence, src/model.cpp:827).  No counterpart in the
+ * reference's API: it exposes the device routine for parity tests.
+ * y[i] = log1pf(x[i]). */
+int brisk_hip_log1pf(const float* x, float* y, size_t n, void* stream);
 
 /* Self-test of the shortcuts the device arithmetic takes: the two short
  * divisions of the activation quantisation (a / 127 for a >= 0, and 1 / d),

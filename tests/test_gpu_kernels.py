@@ -205,6 +205,25 @@ def test_tanhf_matches_host_libm(lib, orc):
     assert len(bad) == 0, f"{len(bad)} of {len(x)} differ, e.g. x={x[bad[:3]]} got={got[bad[:3]]} want={want[bad[:3]]}"
 
 
+def test_log1pf_matches_host_libm(lib, orc):
+    """The device log1pf of the Qwen3.5 recurrence's softplus equals glibc's log1pf (the reference's std::log1p):
+    a strided sweep of every float pattern, and every float of [1, 2) and of [2^20, 2^21) (exp of the softplus
+    inputs below its cut-over at 20 reaches 4.9e8)."""
+    bits = np.concatenate([np.arange(0, 1 << 32, 251, dtype=np.uint64).astype(np.uint32),
+                           np.arange(0x3F800000, 0x40000000, dtype=np.uint32),
+                           np.arange(0x49800000, 0x4A000000, dtype=np.uint32)])
+    x = bits.view(np.float32)
+    x = x[~np.isnan(x)]
+    want = np.empty_like(x)
+    orc.or_log1pf_batch(pyoracle.ptr(x), pyoracle.ptr(want), len(x))
+    xd = dev(x)
+    out = torch.zeros(len(x), dtype=torch.float32, device="cuda")
+    L.check(lib.brisk_hip_log1pf(p(xd), p(out), len(x), None))
+    got = host(out, np.float32)
+    bad = np.flatnonzero((got.view(np.uint32) != want.view(np.uint32)) & ~(np.isnan(got) & np.isnan(want)))
+    assert len(bad) == 0, f"{len(bad)} of {len(x)} differ, e.g. x={x[bad[:3]]} got={got[bad[:3]]} want={want[bad[:3]]}"
+
+
 def test_short_divisions_are_exact(lib):
     """div127 (a / 127, a >= 0) and rcp_rn (1 / d) equal IEEE division on every finite input, and the
     hardware float-to-half conversion equals the reference's bit-level one on every float, and the

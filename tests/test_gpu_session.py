@@ -17,7 +17,7 @@ from brisk_hip import BriskHipError, HipSession, model, synth  # noqa: E402
 import pyoracle  # noqa: E402
 
 TOL = 2e-2
-FAMILIES = ["tiny-qwen3", "tiny-llama", "tiny-q8", "tiny-bitnet", "tiny-q5k", "tiny-q5", "tiny-qwen2", "tiny-smollm3", "tiny-gemma3", "tiny-phi3", "tiny-llama32", "tiny-lfm2"]
+FAMILIES = ["tiny-qwen3", "tiny-llama", "tiny-q8", "tiny-bitnet", "tiny-q5k", "tiny-q5", "tiny-qwen2", "tiny-smollm3", "tiny-gemma3", "tiny-phi3", "tiny-llama32", "tiny-lfm2", "tiny-qwen35", "tiny-qwen35w"]
 
 
 # the persistent token loop, one kernel per phase replayed from hipGraphs (both with the
@@ -74,12 +74,16 @@ def test_eval_all_and_rollback(pair):
     ids = s.decode(3)
     o_ids, _ = o.generate([int(np.argmax(want[-1]))], 3)
     np.testing.assert_array_equal(ids, o_ids, err_msg=name)
-    # roll back to 2 and continue: the same as evaluating from there in one go
+    # roll back to 2 and continue: the same as evaluating from there in one go (Qwen3.5's recurrent
+    # states cannot step back to 2: both restart at 0, src/model.cpp:737-750)
     s.rollback(2)
     o.rollback(2)
+    assert s.position == o.position == (0 if cfg.arch == model.ARCH_QWEN35 else 2)
     g2, w2 = s.eval(toks[2:]), o.eval(toks[2:])
     assert np.abs(g2 - w2).max() <= TOL
-    assert np.abs(g2 - got[-1]).max() <= 1e-5
+    np.testing.assert_array_equal(g2.view(np.uint32), w2.view(np.uint32), err_msg=name)
+    if cfg.arch != model.ARCH_QWEN35:
+        assert np.abs(g2 - got[-1]).max() <= 1e-5
     assert s.eval_greedy([7]) == int(np.argmax(o.eval([7])))
 
 
