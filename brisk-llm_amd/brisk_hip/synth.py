@@ -279,6 +279,13 @@ SPECS = {
                                      "ssm.state_size": (G.U32, 128), "ssm.group_count": (G.U32, 4),
                                      "ssm.time_step_rank": (G.U32, 4), "ssm.inner_size": (G.U32, 512),
                                      "ssm.conv_kernel": (G.U32, 3)}),
+    # Qwen3.5's own attention shape: 256-wide heads with a quarter of each rotated (the plain attention).
+    "tiny-qwen35h": ModelSpec("tiny-qwen35h", "qwen35", 256, 4, 4, 2, 256, 512, 1000, 1e7, context=1024,
+                              fmt=_uniform4(G.T_Q8_0), recurrent_layers=(0, 1, 2),
+                              extra={"full_attention_interval": (G.U32, 4), "rope.dimension_count": (G.U32, 64),
+                                     "ssm.state_size": (G.U32, 64), "ssm.group_count": (G.U32, 4),
+                                     "ssm.time_step_rank": (G.U32, 4), "ssm.inner_size": (G.U32, 256),
+                                     "ssm.conv_kernel": (G.U32, 4)}),
     "tiny-q5": ModelSpec("tiny-q5", "qwen3", 256, 2, 4, 2, 64, 512, 1000, 1e6, context=1024,
                          fmt={**_uniform4(G.T_Q5_0), "o": G.T_Q4_1, "down": G.T_Q4_1}),
 }

@@ -472,6 +472,138 @@ __global__ void k_log1pf(const float* __restrict__ x, float* __restrict__ y, siz
     if (i < n) y[i] = ref_log1pf(x[i]);
 }
 
+// ---------------------------------------------------------------- plain attention
+//
+// The reference's attention for one token (src/model.cpp:1019-1093 with the portable
+// kernels of src/kernels_f32.cpp:229-284) in four kernels, for head sizes the LDS-resident
+// attention does not take (up to 512) and for layers that read another layer's cache:
+//   prologue (a workgroup per key/value head): q heads and k bias, RMS norm and RoPE, v
+//            bias (and Gemma 4's weightless V norm), the fp16 K/V rows at pos;
+//   scores   (a lane per position): dot_f32(q, k_p) * scale, 16 lane partials over
+//            i = j (mod 16) in order, then 0 + lane 0 + ... + lane 15;
+//   softmax  (a workgroup per head): max, e_p = expf(s_p - max), their sum in double,
+//            w_p = e_p * (float)(1 / sum);
+//   values   (a lane per output dimension): 0 + w_0 v_0 + w_1 v_1 + ... in position order.
+// A sliding layer's token sees positions [L - window, L) (src/model.cpp:1084-1085).
+
+__device__ __forceinline__ int plain_start(const AttnArgs& g, int L) { return g.window > 0 && L > g.window ? L - g.window : 0; }
+
+__global__ __launch_bounds__(kThreads) void k_plain_prologue(AttnArgs g) {
+    __shared__ float qs[16 * kPlainMaxHead], kc[kPlainMaxHead], vc[kPlainMaxHead];
+    __shared__ double red[4];
+    const int kv = blockIdx.x, hd = g.head_dim, hpk = g.heads / g.kv_heads, t = threadIdx.x, pos = *g.pos;
+    const bool own = g.no_kv == 0;
+    for (int i = t; i < hpk * hd; i += kThreads) qs[i] = g.q[kv * hpk * hd + i];
+    if (own)
+        for (int i = t; i < hd; i += kThreads) {
+            kc[i] = g.k[kv * hd + i];
+            vc[i] = g.vbias != nullptr ? g.v[kv * hd + i] + g.vbias[kv * hd + i] : g.v[kv * hd + i];
+        }
+    __syncthreads();
+    const float* rope = g.rope != nullptr ? g.rope + static_cast<size_t>(pos) * g.rope_dim : nullptr;
+    for (int h = t >> 6; h < hpk + (own ? 1 : 0); h += kThreads / 64) {
+        if (h < hpk) head_norm_rope(qs + h * hd, g.qbias != nullptr ? g.qbias + (kv * hpk + h) * hd : nullptr, g.qnorm, rope, hd, g.rope_dim, g.neox, g.eps);
+        else head_norm_rope(kc, g.kbias != nullptr ? g.kbias + kv * hd : nullptr, g.knorm, rope, hd, g.rope_dim, g.neox, g.eps);
+    }
+    if (own && g.vnorm) {  // rms_norm(v) with no weight (src/model.cpp:1041)
+        double sq = 0.0;
+        for (int i = t; i < hd; i += kThreads) sq += static_cast<double>(vc[i] * vc[i]);
+        sq = wave_sum(sq);
+        if ((t & 63) == 0) red[t >> 6] = sq;
+        __syncthreads();
+        const float scale = rms_scale(((red[0] + red[1]) + red[2]) + red[3], hd, g.eps);
+        __syncthreads();
+        for (int i = t; i < hd; i += kThreads) vc[i] = vc[i] * scale;
+    }
+    __syncthreads();
+    for (int i = t; i < hpk * hd; i += kThreads) g.qn[kv * hpk * hd + i] = qs[i];
+    if (own) {
+        uint16_t* kr = g.kcache + (static_cast<size_t>(kv) * g.ctx + pos) * hd;
+        uint16_t* vr = g.vcache + (static_cast<size_t>(kv) * g.ctx + pos) * hd;
+        for (int i = t; i < hd; i += kThreads) {
+            kr[i] = f2h(kc[i]);
+            vr[i] = f2h(vc[i]);
+        }
+    }
+}
+
+__global__ __launch_bounds__(kThreads) void k_plain_scores(AttnArgs g) {
+    __shared__ float qs[16 * kPlainMaxHead];
+    const int kv = blockIdx.x, hd = g.head_dim, hpk = g.heads / g.kv_heads, t = threadIdx.x;
+    const int L = *g.pos + 1, start = plain_start(g, L);
+    if (start + static_cast<int>(blockIdx.y) * kThreads >= L) return;  // the grid covers the longest context
+    for (int i = t; i < hpk * hd; i += kThreads) qs[i] = g.qn[kv * hpk * hd + i];
+    __syncthreads();
+    const int p = start + static_cast<int>(blockIdx.y) * kThreads + t;
+    if (p >= L) return;
+    const uint16_t* kr = g.kcache + (static_cast<size_t>(kv) * g.ctx + p) * hd;
+    for (int gq = 0; gq < hpk; ++gq) {
+        const float* q = qs + gq * hd;
+        float lane[16];
+#pragma unroll
+        for (int j = 0; j < 16; ++j) lane[j] = 0.0f;
+        for (int b = 0; b < hd; b += 16) {
+            const uint4 k0 = *reinterpret_cast<const uint4*>(kr + b), k1 = *reinterpret_cast<const uint4*>(kr + b + 8);
+            const uint32_t kw[8] = {k0.x, k0.y, k0.z, k0.w, k1.x, k1.y, k1.z, k1.w};
+#pragma unroll
+            for (int j = 0; j < 16; ++j) {
+                const uint16_t h = static_cast<uint16_t>((j & 1) ? (kw[j >> 1] >> 16) : (kw[j >> 1] & 0xFFFF));
+                lane[j] += q[b + j] * h2f(h);
+            }
+        }
+        float sum = 0.0f;
+#pragma unroll
+        for (int j = 0; j < 16; ++j) sum += lane[j];
+        g.gsc[static_cast<size_t>(kv * hpk + gq) * g.ctx + p] = sum * g.scale;
+    }
+}
+
+__global__ __launch_bounds__(kThreads) void k_plain_softmax(AttnArgs g) {
+    __shared__ float mred[4];
+    __shared__ double red[4];
+    const int h = blockIdx.x, t = threadIdx.x, L = *g.pos + 1, start = plain_start(g, L);
+    float* sc = g.gsc + static_cast<size_t>(h) * g.ctx;
+    float m = -INFINITY;
+    for (int p = start + t; p < L; p += kThreads) m = fmaxf(m, sc[p]);
+    m = wave_max(m);
+    if ((t & 63) == 0) mred[t >> 6] = m;
+    __syncthreads();
+    m = fmaxf(fmaxf(mred[0], mred[1]), fmaxf(mred[2], mred[3]));
+    double part = 0.0;
+    for (int p = start + t; p < L; p += kThreads) {
+        const float e = ref_expf(sc[p] - m);
+        sc[p] = e;
+        part += static_cast<double>(e);
+    }
+    part = wave_sum(part);
+    if ((t & 63) == 0) red[t >> 6] = part;
+    __syncthreads();
+    const float scale = static_cast<float>(1.0 / (((red[0] + red[1]) + red[2]) + red[3]));
+    for (int p = start + t; p < L; p += kThreads) sc[p] *= scale;
+}
+
+__global__ __launch_bounds__(kThreads) void k_plain_values(AttnArgs g) {
+    const int h = blockIdx.x, hd = g.head_dim, hpk = g.heads / g.kv_heads, kv = h / hpk;
+    const int d = static_cast<int>(blockIdx.y) * kThreads + threadIdx.x, L = *g.pos + 1, start = plain_start(g, L);
+    if (d >= hd) return;
+    const float* w = g.gsc + static_cast<size_t>(h) * g.ctx;
+    const uint16_t* vv = g.vcache + static_cast<size_t>(kv) * g.ctx * hd + d;
+    float a = 0.0f;
+    int p = start;
+    for (; p + 8 <= L; p += 8) {  // loads first, then the adds in position order
+        float wv[8], vf[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            wv[u] = w[p + u];
+            vf[u] = h2f(vv[static_cast<size_t>(p + u) * hd]);
+        }
+#pragma unroll
+        for (int u = 0; u < 8; ++u) a += wv[u] * vf[u];
+    }
+    for (; p < L; ++p) a += w[p] * h2f(vv[static_cast<size_t>(p) * hd]);
+    g.out[h * hd + d] = a;
+}
+
 // tanhf as the Gemma epilogues compute it (ref_tanhf), for the parity tests.
 __global__ void k_tanhf(const float* __restrict__ x, float* __restrict__ y, size_t n) {
     const size_t i = static_cast<size_t>(blockIdx.x) * blockDim.x + threadIdx.x;
@@ -708,6 +840,20 @@ hipError_t launch_head(HeadArgs g, hipStream_t s) {
 
 hipError_t launch_attention(const AttnArgs& g, hipStream_t s) {
     hipLaunchKernelGGL(k_attn, dim3(g.kv_heads, g.max_splits), dim3(kThreads), 0, s, g);
+    return hipGetLastError();
+}
+
+hipError_t launch_attention_plain(const AttnArgs& g, hipStream_t s) {
+    const int hpk = g.kv_heads > 0 ? g.heads / g.kv_heads : 0;
+    if (g.head_dim < 16 || g.head_dim > kPlainMaxHead || g.head_dim % 16 != 0 || hpk < 1 || hpk > 16 ||
+        hpk * g.kv_heads != g.heads || g.qn == nullptr || g.gsc == nullptr)
+        return hipErrorInvalidValue;
+    const unsigned pos_blocks = static_cast<unsigned>((g.ctx + kThreads - 1) / kThreads);  // the most any position needs
+    hipLaunchKernelGGL(k_plain_prologue, dim3(g.kv_heads), dim3(kThreads), 0, s, g);
+    hipLaunchKernelGGL(k_plain_scores, dim3(g.kv_heads, pos_blocks), dim3(kThreads), 0, s, g);
+    hipLaunchKernelGGL(k_plain_softmax, dim3(g.heads), dim3(kThreads), 0, s, g);
+    hipLaunchKernelGGL(k_plain_values, dim3(g.heads, static_cast<unsigned>((g.head_dim + kThreads - 1) / kThreads)), dim3(kThreads),
+                       0, s, g);
     return hipGetLastError();
 }
 

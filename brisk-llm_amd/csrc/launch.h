@@ -67,6 +67,10 @@ struct AttnArgs {
     // (null: such contexts take the split attention)
     float* gsc;
     float* out;           // [heads][head_dim]
+    // the plain attention (launch_attention_plain) only:
+    float* qn;            // [heads][head_dim]: the normed and rotated queries
+    int vnorm;            // V RMS-normalised without weight before the cache (Gemma 4)
+    int no_kv;            // the layer reads another layer's cache and stores no rows (Gemma 4's shared K/V)
     unsigned long long* stamps;  // optional profiling: key/value head 0's wall clock at sub-phase ends
 };
 
@@ -115,6 +119,11 @@ hipError_t launch_matvec_q8(const Packed& m, const void* xq, size_t n, float* ou
 hipError_t launch_gemv(GemvArgs g, hipStream_t s);
 hipError_t launch_gateup(GateUpArgs g, hipStream_t s);
 hipError_t launch_attention(const AttnArgs& g, hipStream_t s);
+// The reference's attention for one token by four plain kernels (prologue, scores, softmax,
+// values), for any head size up to 512 (a multiple of 16): scores and weights in gsc
+// ([heads][ctx]), the queries in qn.
+hipError_t launch_attention_plain(const AttnArgs& g, hipStream_t s);
+constexpr int kPlainMaxHead = 512;
 hipError_t launch_embed(const Packed& m, const PickState& ps, float* h, float scale, hipStream_t s);
 // h += rms_norm(p, w) over n values (Gemma's post-attention / post-feed-forward norm).
 hipError_t launch_post_add(float* h, const float* p, const float* w, float eps, int n, hipStream_t s);

@@ -174,6 +174,7 @@ brisk_hip_memory estimate_session(const brisk_hip_config& cfg, const brisk_hip_t
     size_t sc = (e + 2 * qd + ff + cfg.vocab + 2 * kvd) * 4;              // token-path activations, logits
     sc += static_cast<size_t>(cfg.heads) * splits * (hd + 2) * 4;          // attention partials
     sc += (ctx + 1) * 4 + ctx * hd * 4;                                    // token sequence, RoPE table
+    if (hd > 128) sc += (qd + static_cast<size_t>(cfg.heads) * ctx) * 4;  // the plain attention's queries and scores
     if (cfg.arch == BRISK_HIP_ARCH_GEMMA3) sc += ctx * hd * 4 + e * 4;     // local RoPE table, post-norm input
     if (cfg.arch == BRISK_HIP_ARCH_LFM2) sc += 3 * e * 4;                  // conv rows
     if (cfg.arch == BRISK_HIP_ARCH_QWEN35)                                 // recurrence rows, query|gate rows, gates
@@ -248,8 +249,13 @@ Session::Session(const brisk_hip_config& cfg, const brisk_hip_tensor* tensors, s
     if (cfg.heads % cfg.kv_heads != 0) model_fail("head_count is not a multiple of head_count_kv");
     if (cfg.heads / cfg.kv_heads > 16) model_fail("more than 16 query heads per key/value head is not supported");
     if (cfg.kv_heads > 1000) model_fail("more than 1000 key/value heads is not supported");  // ticket slots
-    if (cfg.head_dim == 0 || cfg.head_dim % 32 != 0 || cfg.head_dim > 128) model_fail("head size must be 32, 64, 96 or 128");
+    if (cfg.head_dim == 0 || cfg.head_dim % 32 != 0 || cfg.head_dim > static_cast<uint32_t>(kPlainMaxHead))
+        model_fail("head size must be a non-zero multiple of 32 up to 512");
     if (cfg.embd > kMaxCols || cfg.ff > kMaxCols || cfg.heads * cfg.head_dim > kMaxCols) model_fail("a row wider than 8192 is not supported");
+    {
+        const char* at = std::getenv("BRISK_HIP_ATTN");
+        plain_attn_ = cfg.head_dim > 128 || (at != nullptr && std::string(at) == "plain");
+    }
     check(hipSetDevice(device), "hipSetDevice");
     if (std::getenv("BRISK_NO_MEMORY_CHECK") == nullptr) {  // check_memory (src/memory.cpp:118-135), for HBM
         size_t free_b = 0, total_b = 0;
@@ -442,6 +448,10 @@ Session::Session(const brisk_hip_config& cfg, const brisk_hip_tensor* tensors, s
     act_ = static_cast<float*>(alloc(static_cast<size_t>(cfg.ff) * 4));
     logits_ = static_cast<float*>(alloc(static_cast<size_t>(cfg.vocab) * 4));
     max_splits_ = attention_max_splits(static_cast<int>(max_ctx_));
+    if (plain_attn_) {
+        plain_q_ = static_cast<float*>(alloc(qd * 4));
+        plain_sc_ = static_cast<float*>(alloc(static_cast<size_t>(cfg.heads) * max_ctx_ * 4));
+    }
     part_acc_ = static_cast<float*>(alloc(static_cast<size_t>(cfg.heads) * max_splits_ * hd * 4));
     part_ml_ = static_cast<float*>(alloc(static_cast<size_t>(cfg.heads) * max_splits_ * 2 * 4));
     k_ = static_cast<float*>(alloc(kvd * 4));
@@ -651,7 +661,13 @@ void Session::record_step(bool full) {
         // scores past the LDS limit go to the split buffers: heads x ctx floats fit them
         // (heads x max_splits x head_dim, head_dim >= the split length)
         aa.gsc = cfg_.head_dim >= static_cast<uint32_t>(kSplit) ? part_acc_ : nullptr;
-        check(launch_attention(aa, stream_), "attention");
+        if (plain_attn_) {
+            aa.gsc = plain_sc_;
+            aa.qn = plain_q_;
+            check(launch_attention_plain(aa, stream_), "attention");
+        } else {
+            check(launch_attention(aa, stream_), "attention");
+        }
         if (qwen35()) check(launch_sigmoid_gate(att_, agate_, static_cast<int>(cfg_.heads * cfg_.head_dim), stream_), "attention gate");
 
         // h += W_o att, or with a post-norm h += rms_norm(W_o att) (src/model.cpp:1113-1121)
@@ -717,6 +733,7 @@ void Session::setup_loop() {
     if ((cfg_.heads / cfg_.kv_heads) * cfg_.head_dim > 4 * kThreads) return;
     if (embd_.p.type != out_->p.type) return;  // the loop reads the embedding in its output's format
     if (gemma() || lfm2() || qwen35()) return;  // post-norms, windows, softcap, convolutions, recurrences: graph-path phases only
+    if (plain_attn_) return;                    // the plain attention is a graph-path phase
     const Layer& L0 = layers_[0];
     const void* k = find_loop_kernel(L0.q.p.type, L0.v.p.type, L0.o.p.type, L0.gate.p.type, L0.down.p.type, out_->p.type);
     if (k == nullptr) return;
@@ -1055,6 +1072,7 @@ bool Session::use_prefill(size_t n) const {
     // take the exact attention only
     if (gemma() || lfm2()) return prefill_on_ && n >= 2 && exact_fits && cfg_.head_dim <= 128;
     if (qwen35()) return false;  // the recurrence takes its tokens one at a time
+    if (plain_attn_) return false;  // the batched attention holds heads of at most 128
     return prefill_on_ && n >= 2 && (exact_fits || mfma_fits);
 }
 

@@ -140,6 +140,9 @@ private:
     // position, whose input state is still held) while snap_ok_
     bool snap_ok_ = false;
     size_t snap_pos_ = 0;
+    // the plain attention (launch_attention_plain): head sizes past 128, or BRISK_HIP_ATTN=plain
+    bool plain_attn_ = false;
+    float *plain_q_ = nullptr, *plain_sc_ = nullptr;
     float embd_scale_ = 1.0f;      // Gemma: sqrt(embd) (src/model.cpp:286)
     int rope_dim_ = 0;             // dimensions the RoPE table rotates (its row stride)
     unsigned long long* key_ = nullptr;

@@ -47,6 +47,7 @@ RUNS = {
     "tiny-lfm2": (12, 48),
     "tiny-qwen35": (12, 48),
     "tiny-qwen35w": (12, 48),
+    "tiny-qwen35h": (12, 48),
 }
 
 

@@ -19,7 +19,7 @@ torch = pytest.importorskip("torch")
 from brisk_hip import BriskHipError, HipSession, model, synth  # noqa: E402
 import pyoracle  # noqa: E402
 
-NAMES = ["tiny-qwen35", "tiny-qwen35w"]
+NAMES = ["tiny-qwen35", "tiny-qwen35w", "tiny-qwen35h"]
 
 
 def same(a, b, what):

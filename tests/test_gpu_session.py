@@ -17,12 +17,12 @@ from brisk_hip import BriskHipError, HipSession, model, synth  # noqa: E402
 import pyoracle  # noqa: E402
 
 TOL = 2e-2
-FAMILIES = ["tiny-qwen3", "tiny-llama", "tiny-q8", "tiny-bitnet", "tiny-q5k", "tiny-q5", "tiny-qwen2", "tiny-smollm3", "tiny-gemma3", "tiny-phi3", "tiny-llama32", "tiny-lfm2", "tiny-qwen35", "tiny-qwen35w"]
+FAMILIES = ["tiny-qwen3", "tiny-llama", "tiny-q8", "tiny-bitnet", "tiny-q5k", "tiny-q5", "tiny-qwen2", "tiny-smollm3", "tiny-gemma3", "tiny-phi3", "tiny-llama32", "tiny-lfm2", "tiny-qwen35", "tiny-qwen35w", "tiny-qwen35h"]
 
 
 # the persistent token loop, one kernel per phase replayed from hipGraphs (both with the
 # batched MFMA prefill for prompts), and the loop with prompts evaluated token by token
-PATHS = ["loop", "graph", "tokenwise"]
+PATHS = ["loop", "graph", "tokenwise", "plain"]
 
 
 @pytest.fixture(scope="module", params=[(f, p) for p in PATHS for f in FAMILIES], ids=lambda fp: f"{fp[0]}-{fp[1]}")
@@ -31,7 +31,7 @@ def pair(request):
     name, path = request.param
     f, cfg, table = model.load(synth.model_path(name))
     print(f"[session] {name} ({path})", flush=True)
-    env = {"BRISK_HIP_PATH": path} if path != "tokenwise" else {"BRISK_HIP_PREFILL": "0"}
+    env = {"tokenwise": {"BRISK_HIP_PREFILL": "0"}, "plain": {"BRISK_HIP_ATTN": "plain"}}.get(path, {"BRISK_HIP_PATH": path})
     os.environ.update(env)
     try:
         s = HipSession((f, cfg, table), max_context=256)

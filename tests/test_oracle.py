@@ -424,7 +424,7 @@ def tiny(name):
     return path, f, cfg, table
 
 
-@pytest.mark.parametrize("name", ["tiny-qwen3", "tiny-llama", "tiny-q8", "tiny-bitnet", "tiny-q5k", "tiny-q5", "tiny-qwen2", "tiny-smollm3", "tiny-gemma3", "tiny-phi3", "tiny-llama32", "tiny-lfm2", "tiny-qwen35", "tiny-qwen35w"])
+@pytest.mark.parametrize("name", ["tiny-qwen3", "tiny-llama", "tiny-q8", "tiny-bitnet", "tiny-q5k", "tiny-q5", "tiny-qwen2", "tiny-smollm3", "tiny-gemma3", "tiny-phi3", "tiny-llama32", "tiny-lfm2", "tiny-qwen35", "tiny-qwen35w", "tiny-qwen35h"])
 def test_oracle_greedy_matches_reference_fixture(name):
     """tests/golden/<name>_greedy.json were written by the reference engine itself."""
     with open(os.path.join(HERE, "golden", f"{name}_greedy.json")) as fh:
@@ -453,7 +453,7 @@ def test_oracle_first_tokens_of_qwen3_0_6b_fixture():
 
 
 @needs_ref
-@pytest.mark.parametrize("name", ["tiny-qwen3", "tiny-llama", "tiny-bitnet", "tiny-q5k", "tiny-q5", "tiny-qwen2", "tiny-smollm3", "tiny-gemma3", "tiny-phi3", "tiny-llama32", "tiny-lfm2", "tiny-qwen35", "tiny-qwen35w"])
+@pytest.mark.parametrize("name", ["tiny-qwen3", "tiny-llama", "tiny-bitnet", "tiny-q5k", "tiny-q5", "tiny-qwen2", "tiny-smollm3", "tiny-gemma3", "tiny-phi3", "tiny-llama32", "tiny-lfm2", "tiny-qwen35", "tiny-qwen35w", "tiny-qwen35h"])
 def test_oracle_session_matches_reference_bitwise(name):
     """eval, eval_all and rollback of the restatement against the reference's Session."""
     path, f, cfg, table = tiny(name)
@@ -474,7 +474,7 @@ def test_oracle_session_matches_reference_bitwise(name):
 
 
 @needs_ref
-@pytest.mark.parametrize("name", ["tiny-qwen35", "tiny-qwen35w"])
+@pytest.mark.parametrize("name", ["tiny-qwen35", "tiny-qwen35w", "tiny-qwen35h"])
 def test_oracle_recurrent_snapshot_matches_reference_bitwise(name):
     """Qwen3.5's rollback (src/model.cpp:735-752): one step back restores the snapshot taken before the last
     token, whether that token came alone or at the end of a longer call; a second step back, or any other
@@ -529,7 +529,7 @@ def test_oracle_longrope_matches_reference_bitwise():
 
 
 @needs_ref
-@pytest.mark.parametrize("name", ["tiny-qwen3", "tiny-llama", "tiny-bitnet", "tiny-q5k", "tiny-q5", "tiny-qwen2", "tiny-smollm3", "tiny-gemma3", "tiny-phi3", "tiny-llama32", "tiny-lfm2", "tiny-qwen35", "tiny-qwen35w"])
+@pytest.mark.parametrize("name", ["tiny-qwen3", "tiny-llama", "tiny-bitnet", "tiny-q5k", "tiny-q5", "tiny-qwen2", "tiny-smollm3", "tiny-gemma3", "tiny-phi3", "tiny-llama32", "tiny-lfm2", "tiny-qwen35", "tiny-qwen35w", "tiny-qwen35h"])
 def test_model_config_matches_reference(name):
     """brisk_hip.model.parse_config against the reference's own ModelConfig parse (src/model.cpp:140-260)
     of the same file, field by field. The Python config keeps 0 for a field its family does not use;
