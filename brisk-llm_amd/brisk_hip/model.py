@@ -2,7 +2,7 @@
 
 Restates the part of the reference's loader the HIP session needs:
 ``Model::parse_config`` (src/model.cpp:161-301) for the families the HIP
-session runs (qwen3, llama, bitnet, qwen2, smollm3, gemma3, phi3, lfm2, qwen35), the tensor names and shapes of
+session runs (qwen3, llama, bitnet, qwen2, smollm3, gemma3, gemma4, phi3, lfm2, qwen35), the tensor names and shapes of
 ``Model::Model`` (src/model.cpp:303-423) and the tied output projection
 (src/model.cpp:328-330).  The session takes the weights as GGUF-layout bytes,
 as the reference's ``Model(file, repack = false)`` hands them to a GPU session.
@@ -15,10 +15,10 @@ import numpy as np
 
 from . import gguf as G
 
-ARCH_QWEN3, ARCH_LLAMA, ARCH_BITNET, ARCH_QWEN2, ARCH_SMOLLM3, ARCH_GEMMA3, ARCH_PHI3, ARCH_LFM2, ARCH_QWEN35 = range(9)
+ARCH_QWEN3, ARCH_LLAMA, ARCH_BITNET, ARCH_QWEN2, ARCH_SMOLLM3, ARCH_GEMMA3, ARCH_PHI3, ARCH_LFM2, ARCH_QWEN35, ARCH_GEMMA4 = range(10)
 _ARCH = {"qwen3": ARCH_QWEN3, "llama": ARCH_LLAMA, "bitnet": ARCH_BITNET, "bitnet-b1.58": ARCH_BITNET,
          "qwen2": ARCH_QWEN2, "smollm3": ARCH_SMOLLM3, "gemma3": ARCH_GEMMA3, "phi3": ARCH_PHI3,
-         "lfm2": ARCH_LFM2, "qwen35": ARCH_QWEN35}
+         "lfm2": ARCH_LFM2, "qwen35": ARCH_QWEN35, "gemma4": ARCH_GEMMA4}
 QUANT_TYPES = (G.T_Q4_0, G.T_Q4_1, G.T_Q5_0, G.T_Q8_0, G.T_Q4_K, G.T_Q5_K, G.T_Q6_K, G.T_TQ2_0)
 
 
@@ -64,6 +64,36 @@ class ModelConfig:
     ssm_inner: int = 0
     ssm_conv: int = 0
     recurrent_layers: tuple = ()
+    # Gemma 4 (src/model.cpp:189-226): the sliding layers' head size (0: head_dim), the first layer
+    # that reads an earlier layer's K/V (0: none), the per-layer embedding width, the score scale
+    # (0: 1 / sqrt(head size)), V's weightless norm; per-layer tables (empty: the rule / the scalar)
+    head_dim_local: int = 0
+    kv_from_start: int = 0
+    ple_dim: int = 0
+    attention_scale: float = 0.0
+    value_norm: int = 0
+    sliding_pattern: tuple = ()
+    ff_dims: tuple = ()
+    kv_head_counts: tuple = ()
+
+    def layer_slides(self, layer: int) -> bool:  # src/model.h:87-90
+        if self.sliding_pattern:
+            return bool(self.sliding_pattern[layer])
+        return self.sliding_window != 0 and layer % 6 != 5
+
+    def head_dim_of(self, layer: int) -> int:  # src/model.h:111-113
+        return self.head_dim_local if self.head_dim_local and self.layer_slides(layer) else self.head_dim
+
+    def kv_heads_of(self, layer: int) -> int:  # src/model.h:91-93
+        return int(self.kv_head_counts[layer]) if self.kv_head_counts else self.kv_heads
+
+    def ff_of(self, layer: int) -> int:  # src/model.h:118
+        return int(self.ff_dims[layer]) if self.ff_dims else self.ff
+
+    def kv_layer_of(self, layer: int) -> int:  # src/model.h:114-117
+        if self.kv_from_start == 0 or layer < self.kv_from_start:
+            return layer
+        return self.kv_from_start - (2 if self.layer_slides(layer) else 1)
 
     @property
     def ssm_qkv_dim(self) -> int:  # src/model.h:108
@@ -88,8 +118,8 @@ class ModelConfig:
 def parse_config(f: G.GgufFile) -> ModelConfig:
     name = f.get("general.architecture")
     if name not in _ARCH:
-        fail(f"unsupported architecture '{name}'; the HIP session runs qwen3, qwen2, llama, smollm3, gemma3, phi3, "
-             "lfm2, qwen35 and bitnet")
+        fail(f"unsupported architecture '{name}'; the HIP session runs qwen3, qwen2, llama, smollm3, gemma3, gemma4, "
+             "phi3, lfm2, qwen35 and bitnet")
     p = name + "."
 
     def u32(key):
@@ -114,17 +144,31 @@ def parse_config(f: G.GgufFile) -> ModelConfig:
         per_layer_kv = [int(kv_raw or 0) if (l + 1) % interval == 0 else 0 for l in range(layers)]
     if per_layer_kv is not None and len(per_layer_kv) != layers:
         fail("head_count_kv array length")
-    if per_layer_kv is not None and len({k for k in per_layer_kv if k != 0}) > 1:
-        # the session applies one head count to every attention layer (kv_head_count_of, src/model.h:91)
+    if per_layer_kv is not None and len({k for k in per_layer_kv if k != 0}) > 1 and name != "gemma4":
+        # one head count for every attention layer but Gemma 4's (kv_head_count_of, src/model.h:91)
         fail("attention layers with different key/value head counts are not supported")
-    kv = max(per_layer_kv) if per_layer_kv is not None else u32("attention.head_count_kv")
-    ff, ctx = u32("feed_forward_length"), u32("context_length")
+    kv = int(max(per_layer_kv)) if per_layer_kv is not None else u32("attention.head_count_kv")
+    ff_raw = f.get(p + "feed_forward_length")
+    ff_dims = ()
+    if name == "gemma4" and isinstance(ff_raw, (list, tuple)):  # per layer (src/model.cpp:202-212)
+        if any(int(w) <= 0 for w in ff_raw):
+            fail("non-positive feed-forward width")
+        ff_dims = tuple(int(w) for w in ff_raw)
+        if len(ff_dims) != layers:
+            fail("feed_forward_length array length")
+        ff = max(ff_dims)
+    else:
+        ff = u32("feed_forward_length")
+    ctx = u32("context_length")
     if 0 in (embd, layers, heads, kv, ff, ctx):
         fail("a model dimension is zero")
-    if heads % kv:
-        fail("head_count is not a multiple of head_count_kv")
-    if heads // kv > 16:
-        fail("more than 16 query heads per key/value head is not supported")
+    for k in (per_layer_kv if per_layer_kv is not None else [kv]):  # src/model.cpp:275-280
+        if k == 0 and name in ("lfm2", "qwen35"):
+            continue
+        if k == 0 or heads % k:
+            fail("head_count is not a multiple of head_count_kv")
+        if heads // k > 16:
+            fail("more than 16 query heads per key/value head is not supported")
     head_dim = int(f.get(p + "attention.key_length", embd // heads))
     if head_dim == 0 or head_dim % 32:
         fail("head size must be a non-zero multiple of 32")
@@ -135,7 +179,27 @@ def parse_config(f: G.GgufFile) -> ModelConfig:
         fail("missing or misshapen token_embd.weight")
     cfg = ModelConfig(_ARCH[name], name, int(emb.dims[1]), embd, layers, heads, kv, head_dim, ff, ctx,
                       f32("rope.freq_base"), f32("attention.layer_norm_rms_epsilon"))
-    if cfg.arch == ARCH_GEMMA3:
+    cfg.ff_dims = ff_dims
+    if cfg.arch == ARCH_GEMMA4:  # src/model.cpp:189-226
+        pattern = f.get(p + "attention.sliding_window_pattern")
+        if pattern is not None:
+            cfg.sliding_pattern = tuple(1 if b else 0 for b in pattern)
+            if len(cfg.sliding_pattern) != layers:
+                fail("sliding window pattern length")
+        cfg.head_dim_local = int(f.get(p + "attention.key_length_swa", 0))
+        if cfg.head_dim_local and (cfg.head_dim_local % 32 or cfg.head_dim_local > head_dim):
+            fail("the sliding layers' head size must be a multiple of 32 no larger than the global one")
+        shared = int(f.get(p + "attention.shared_kv_layers", 0))
+        if shared:
+            if shared + 2 > layers:
+                fail("more shared K/V layers than layers")
+            cfg.kv_from_start = layers - shared
+        cfg.ple_dim = int(f.get(p + "embedding_length_per_layer_input", 0))
+        cfg.attention_scale = 1.0
+        cfg.value_norm = 1
+        if per_layer_kv is not None:
+            cfg.kv_head_counts = tuple(int(k) for k in per_layer_kv)
+    if cfg.arch in (ARCH_GEMMA3, ARCH_GEMMA4):
         cfg.sliding_window = int(f.get(p + "attention.sliding_window", 0))
         cfg.rope_base_local = float(f.get(p + "rope.freq_base_swa", 10000.0))
         cfg.rope_scale = float(np.float32(1.0) / np.float32(f.get(p + "rope.scaling.factor", 1.0)))  # in float
@@ -155,7 +219,7 @@ def parse_config(f: G.GgufFile) -> ModelConfig:
             fail("qwen35: a DeltaNet state wider than 256 is not supported")
         cfg.recurrent_layers = tuple(l for l in range(layers) if per_layer_kv[l] == 0)
         cfg.rope_dim = int(f.get(p + "rope.dimension_count", 0))
-    elif per_layer_kv is not None and min(per_layer_kv) != kv:
+    elif per_layer_kv is not None and min(per_layer_kv) != kv and cfg.arch != ARCH_GEMMA4:
         fail("per-layer key/value head counts are not supported for this family")
     if cfg.arch == ARCH_PHI3:
         cfg.rope_dim = int(f.get(p + "rope.dimension_count", 0))
@@ -208,6 +272,11 @@ def tensor_table(f: G.GgufFile, cfg: ModelConfig) -> list:
         vec("rope_factors_short.weight", rd // 2)
         vec("rope_factors_long.weight", rd // 2)
     vec("token_embd_norm.weight" if cfg.arch == ARCH_LFM2 else "output_norm.weight", e)  # src/model.cpp:331
+    if cfg.ple_dim:  # Gemma 4's per-layer embeddings (src/model.cpp:319-324)
+        pall = cfg.ple_dim * cfg.layers
+        mat("per_layer_token_embd.weight", cfg.vocab, pall)
+        mat("per_layer_model_proj.weight", pall, e)
+        vec("per_layer_proj_norm.weight", cfg.ple_dim)
     if f.tensor("output.weight") is not None:
         mat("output.weight", cfg.vocab, e)
     for l in range(cfg.layers):
@@ -237,33 +306,45 @@ def tensor_table(f: G.GgufFile, cfg: ModelConfig) -> list:
             mat(b + "ffn_up.weight", cfg.ff, e)
             mat(b + "ffn_down.weight", e, cfg.ff)
             continue
+        # the layer's head size, key/value heads, width and K/V source (Gemma 4, src/model.cpp:337-341)
+        hdl, ffl = cfg.head_dim_of(l), cfg.ff_of(l)
+        qdl, kvdl, own = cfg.heads * hdl, cfg.kv_heads_of(l) * hdl, cfg.kv_layer_of(l) == l
         if cfg.arch == ARCH_PHI3:  # fused Q|K|V and gate|up (src/model.cpp:370-380)
             mat(b + "attn_qkv.weight", qd + 2 * kvd, e)
         else:  # Qwen3.5: each head's query rows followed by its gate rows (src/model.cpp:383-384)
-            mat(b + "attn_q.weight", 2 * qd if cfg.arch == ARCH_QWEN35 else qd, e)
-            mat(b + "attn_k.weight", kvd, e)
-            mat(b + "attn_v.weight", kvd, e)
-        if cfg.arch in (ARCH_QWEN3, ARCH_GEMMA3, ARCH_LFM2, ARCH_QWEN35):
-            vec(b + "attn_q_norm.weight", cfg.head_dim)
-            vec(b + "attn_k_norm.weight", cfg.head_dim)
-        if cfg.arch == ARCH_GEMMA3:
+            mat(b + "attn_q.weight", 2 * qdl if cfg.arch == ARCH_QWEN35 else qdl, e)
+            if own:
+                mat(b + "attn_k.weight", kvdl, e)
+                if cfg.arch != ARCH_GEMMA4 or f.tensor(b + "attn_v.weight") is not None:  # Gemma 4: K may serve as V
+                    mat(b + "attn_v.weight", kvdl, e)
+        if cfg.arch in (ARCH_QWEN3, ARCH_GEMMA3, ARCH_LFM2, ARCH_QWEN35, ARCH_GEMMA4):
+            vec(b + "attn_q_norm.weight", hdl)
+            if own:
+                vec(b + "attn_k_norm.weight", hdl)
+        if cfg.arch in (ARCH_GEMMA3, ARCH_GEMMA4):
             vec(b + "post_attention_norm.weight", e)
             vec(b + "post_ffw_norm.weight", e)
         if cfg.arch == ARCH_BITNET:
             vec(b + "attn_sub_norm.weight", e)
             vec(b + "ffn_sub_norm.weight", cfg.ff)
+        if cfg.ple_dim:  # src/model.cpp:403-407
+            mat(b + "inp_gate.weight", cfg.ple_dim, e)
+            mat(b + "proj.weight", e, cfg.ple_dim)
+            vec(b + "post_norm.weight", e)
+        if f.tensor(b + "layer_output_scale.weight") is not None:  # src/model.cpp:408-410
+            vec(b + "layer_output_scale.weight", 1)
         if f.tensor(b + "attn_q.bias") is not None:  # all or none (src/model.cpp:411-416)
             vec(b + "attn_q.bias", qd)
             vec(b + "attn_k.bias", kvd)
             vec(b + "attn_v.bias", kvd)
-        mat(b + "attn_output.weight", e, qd)
+        mat(b + "attn_output.weight", e, qdl)
         vec(b + ("post_attention_norm.weight" if cfg.arch == ARCH_QWEN35 else "ffn_norm.weight"), e)  # src/model.cpp:418
         if cfg.arch == ARCH_PHI3:
             mat(b + "ffn_up.weight", 2 * cfg.ff, e)
         else:
-            mat(b + "ffn_gate.weight", cfg.ff, e)
-            mat(b + "ffn_up.weight", cfg.ff, e)
-        mat(b + "ffn_down.weight", e, cfg.ff)
+            mat(b + "ffn_gate.weight", ffl, e)
+            mat(b + "ffn_up.weight", ffl, e)
+        mat(b + "ffn_down.weight", e, ffl)
     return out
 
 

@@ -286,6 +286,20 @@ SPECS = {
                                      "ssm.state_size": (G.U32, 64), "ssm.group_count": (G.U32, 4),
                                      "ssm.time_step_rank": (G.U32, 4), "ssm.inner_size": (G.U32, 256),
                                      "ssm.conv_kernel": (G.U32, 4)}),
+    # Gemma 4: sliding layers 0-2 and 4 (64-wide heads, 2 key/value heads) and global layers 3 and 5
+    # (128-wide heads, 1 key/value head, proportional RoPE factors); layers 4 and 5 read the caches
+    # of layers 2 and 3; layer 3 has no V projection (K serves as V); per-layer feed-forward widths,
+    # 64-wide per-layer embeddings and per-layer output scales.
+    "tiny-gemma4": ModelSpec("tiny-gemma4", "gemma4", 256, 6, 4, 2, 128, 768, 1000, 1e6, context=1024,
+                             fmt=_uniform4(G.T_Q8_0), factors={"rope_freqs.weight": 64},
+                             extra={"attention.sliding_window": (G.U32, 8), "rope.freq_base_swa": (G.F32, 10000.0),
+                                    "final_logit_softcapping": (G.F32, 30.0),
+                                    "attention.sliding_window_pattern": (G.ARRAY, (G.BOOL, [1, 1, 1, 0, 1, 0])),
+                                    "attention.key_length_swa": (G.U32, 64),
+                                    "attention.shared_kv_layers": (G.U32, 2),
+                                    "embedding_length_per_layer_input": (G.U32, 64),
+                                    "feed_forward_length": (G.ARRAY, (G.I32, [512, 512, 768, 768, 512, 512])),
+                                    "attention.head_count_kv": (G.ARRAY, (G.U32, [2, 2, 2, 1, 2, 1]))}),
     "tiny-q5": ModelSpec("tiny-q5", "qwen3", 256, 2, 4, 2, 64, 512, 1000, 1e6, context=1024,
                          fmt={**_uniform4(G.T_Q5_0), "o": G.T_Q4_1, "down": G.T_Q4_1}),
 }
@@ -308,6 +322,35 @@ def _bias(w: G.GgufWriter, spec: ModelSpec, name: str, n: int):
     w.add_tensor(name, (n,), G.T_F32, lambda: random_uniform(seed, n, -1.0, 1.0).astype(np.float32).view(np.uint8))
 
 
+class _Gemma4Layers:
+    """Per-layer shapes of a Gemma 4 spec, from its metadata (ModelConfig's accessors, src/model.h:87-118)."""
+
+    def __init__(self, spec: ModelSpec):
+        ex = spec.extra
+        self.spec = spec
+        self.pattern = list(ex["attention.sliding_window_pattern"][1][1])
+        self.hd_local = ex.get("attention.key_length_swa", (None, 0))[1]
+        self.shared = ex.get("attention.shared_kv_layers", (None, 0))[1]
+        self.ple = ex.get("embedding_length_per_layer_input", (None, 0))[1]
+        self.ffs = list(ex["feed_forward_length"][1][1]) if "feed_forward_length" in ex else [spec.ff] * spec.layers
+        self.kvs = list(ex["attention.head_count_kv"][1][1]) if "attention.head_count_kv" in ex else [spec.kv_heads] * spec.layers
+
+    def head_dim(self, l):
+        return self.hd_local if self.hd_local and self.pattern[l] else self.spec.head_dim
+
+    def kv(self, l):
+        return self.kvs[l]
+
+    def ff(self, l):
+        return self.ffs[l]
+
+    def kv_layer(self, l):
+        start = self.spec.layers - self.shared if self.shared else 0
+        if start == 0 or l < start:
+            return l
+        return start - (2 if self.pattern[l] else 1)
+
+
 def write_model(spec: ModelSpec, path: str) -> str:
     """Writes ``spec`` as a GGUF file at ``path`` (skipped when the file already exists)."""
     if os.path.exists(path):
@@ -323,7 +366,8 @@ def write_model(spec: ModelSpec, path: str) -> str:
         w.add(f"{a}.attention.head_count_kv", G.U32, spec.kv_heads)
     w.add(f"{a}.attention.key_length", G.U32, spec.head_dim)
     w.add(f"{a}.attention.value_length", G.U32, spec.head_dim)
-    w.add(f"{a}.feed_forward_length", G.U32, spec.ff)
+    if "feed_forward_length" not in spec.extra:
+        w.add(f"{a}.feed_forward_length", G.U32, spec.ff)
     w.add(f"{a}.context_length", G.U32, spec.context)
     w.add(f"{a}.rope.freq_base", G.F32, spec.rope_base)
     w.add(f"{a}.attention.layer_norm_rms_epsilon", G.F32, spec.eps)
@@ -334,6 +378,11 @@ def write_model(spec: ModelSpec, path: str) -> str:
         seed = stream_seed(spec.seed, name)
         w.add_tensor(name, (n,), G.T_F32, lambda seed=seed, n=n: random_uniform(seed, n, 1.0, 8.0).astype(np.float32).view(np.uint8))
     _vector(w, spec, "token_embd_norm.weight" if a == "lfm2" else "output_norm.weight", spec.embd)
+    g4 = _Gemma4Layers(spec) if a == "gemma4" else None
+    if g4 is not None and g4.ple:  # per-layer embeddings (src/model.cpp:319-324)
+        _matrix(w, spec, "per_layer_token_embd.weight", spec.vocab, g4.ple * spec.layers, spec.embd_fmt)
+        _matrix(w, spec, "per_layer_model_proj.weight", g4.ple * spec.layers, spec.embd, spec.fmt["q"])
+        _vector(w, spec, "per_layer_proj_norm.weight", g4.ple)
     if spec.out_fmt is not None:
         _matrix(w, spec, "output.weight", spec.vocab, spec.embd, spec.out_fmt)
     for l in range(spec.layers):
@@ -376,6 +425,31 @@ def write_model(spec: ModelSpec, path: str) -> str:
             _matrix(w, spec, b + "ffn_gate.weight", spec.ff, spec.embd, spec.fmt["gate"])
             _matrix(w, spec, b + "ffn_up.weight", spec.ff, spec.embd, spec.fmt["up"])
             _matrix(w, spec, b + "ffn_down.weight", spec.embd, spec.ff, spec.fmt["down"])
+            continue
+        if g4 is not None:  # src/model.cpp:337-410
+            hd, kvh, ff, own = g4.head_dim(l), g4.kv(l), g4.ff(l), g4.kv_layer(l) == l
+            _matrix(w, spec, b + "attn_q.weight", spec.heads * hd, spec.embd, spec.fmt["q"])
+            if own:
+                _matrix(w, spec, b + "attn_k.weight", kvh * hd, spec.embd, spec.fmt["k"])
+                if l != 3:  # layer 3: K serves as V (src/model.cpp:386-388)
+                    _matrix(w, spec, b + "attn_v.weight", kvh * hd, spec.embd, spec.fmt["v"])
+            _vector(w, spec, b + "attn_q_norm.weight", hd)
+            if own:
+                _vector(w, spec, b + "attn_k_norm.weight", hd)
+            _vector(w, spec, b + "post_attention_norm.weight", spec.embd)
+            _vector(w, spec, b + "post_ffw_norm.weight", spec.embd)
+            if g4.ple:
+                _matrix(w, spec, b + "inp_gate.weight", g4.ple, spec.embd, spec.fmt["gate"])
+                _matrix(w, spec, b + "proj.weight", spec.embd, g4.ple, spec.fmt["down"])
+                _vector(w, spec, b + "post_norm.weight", spec.embd)
+            seed = stream_seed(spec.seed, b + "out_scale")
+            w.add_tensor(b + "layer_output_scale.weight", (1,), G.T_F32,
+                         lambda seed=seed: random_uniform(seed, 1, 0.5, 1.5).astype(np.float32).view(np.uint8))
+            _matrix(w, spec, b + "attn_output.weight", spec.embd, spec.heads * hd, spec.fmt["o"])
+            _vector(w, spec, b + "ffn_norm.weight", spec.embd)
+            _matrix(w, spec, b + "ffn_gate.weight", ff, spec.embd, spec.fmt["gate"])
+            _matrix(w, spec, b + "ffn_up.weight", ff, spec.embd, spec.fmt["up"])
+            _matrix(w, spec, b + "ffn_down.weight", spec.embd, ff, spec.fmt["down"])
             continue
         if a == "phi3":  # fused Q|K|V (src/model.cpp:370-376)
             _matrix(w, spec, b + "attn_qkv.weight", spec.query_dim + 2 * spec.kv_dim, spec.embd, spec.fmt["q"])

@@ -539,6 +539,10 @@ void or_rms_norm(const float* x, const float* w, float eps, float* out, size_t n
     for (size_t i = 0; i < n; ++i) sum += (double)(x[i] * x[i]);
     const float mean = (float)(sum / (double)n);
     const float scale = 1.0f / sqrtf(mean + eps);
+    if (!w) { /* no weight: plain normalisation (Gemma 4's V) */
+        for (size_t i = 0; i < n; ++i) out[i] = x[i] * scale;
+        return;
+    }
     for (size_t i = 0; i < n; ++i) out[i] = x[i] * scale * w[i];
 }
 
@@ -835,6 +839,10 @@ typedef struct {
     const float *ssm_a, *ssm_dt, *ssm_conv_w, *ssm_norm;
     float *state, *ring;           /* S[head][j][i] (value j, key i); the conv's last ssm_conv - 1 inputs */
     float *snap_state, *snap_ring; /* both as they were before the last evaluated token */
+    /* Gemma 4: the per-layer embedding's gate and projection and its norm; the output scale */
+    matrix ple_gate, ple_proj;
+    const float* ple_post_norm;
+    float out_scale;
 } layer_t;
 
 struct oracle_session {
@@ -852,7 +860,27 @@ struct oracle_session {
     float *qg, *agate, *sqkv, *sconv, *sz, *sab;
     int snap_valid;
     size_t snap_pos;
+    /* Gemma 4's per-layer embeddings (src/model.cpp:319-324): table, projection, its norm; the
+     * token's inputs [layers][ple_dim], its table row and the gate */
+    matrix ple_tok, ple_model_proj;
+    const float* ple_proj_norm;
+    float *ple, *ple_row, *ple_g;
 };
+
+/* ModelConfig's per-layer accessors (src/model.h:87-118). */
+static int layer_slides(const oracle_config* c, int l) {
+    if (c->sliding_pattern) return c->sliding_pattern[l] != 0;
+    return c->sliding_window != 0 && l % 6 != 5;
+}
+static size_t head_dim_of(const oracle_config* c, int l) {
+    return c->head_dim_local != 0 && layer_slides(c, l) ? (size_t)c->head_dim_local : (size_t)c->head_dim;
+}
+static size_t kv_heads_of(const oracle_config* c, int l) { return c->kv_head_counts ? (size_t)c->kv_head_counts[l] : (size_t)c->kv_heads; }
+static size_t ff_of(const oracle_config* c, int l) { return c->ff_dims ? (size_t)c->ff_dims[l] : (size_t)c->ff; }
+static int kv_layer_of(const oracle_config* c, int l) {
+    if (c->kv_from_start == 0 || l < c->kv_from_start) return l;
+    return c->kv_from_start - (layer_slides(c, l) ? 2 : 1);
+}
 
 static const oracle_tensor* find(const oracle_tensor* t, size_t n, const char* name) {
     for (size_t i = 0; i < n; ++i)
@@ -882,6 +910,11 @@ oracle_session* or_session_create(const oracle_config* cfg, const oracle_tensor*
     if (find(t, n, "output.weight")) GETM(s->out, "output.weight");
     else s->out = s->embd;  /* src/model.cpp:328-330 */
     GETV(s->out_norm, c->arch == OR_LFM2 ? "token_embd_norm.weight" : "output_norm.weight"); /* src/model.cpp:331 */
+    if (c->ple_dim != 0) { /* src/model.cpp:319-324 */
+        GETM(s->ple_tok, "per_layer_token_embd.weight");
+        GETM(s->ple_model_proj, "per_layer_model_proj.weight");
+        GETV(s->ple_proj_norm, "per_layer_proj_norm.weight");
+    }
     /* per-frequency factors (src/model.cpp:312-318) and LongRoPE's choice (:691-694) */
     {
         const oracle_tensor* f = find(t, n, "rope_freqs.weight");
@@ -895,6 +928,7 @@ oracle_session* or_session_create(const oracle_config* cfg, const oracle_tensor*
         layer_t* L = &s->layers[l];
 #define LN(sfx) (snprintf(name, sizeof name, "blk.%d.%s", l, sfx), name)
         GETV(L->attn_norm, LN("attn_norm.weight"));
+        L->out_scale = 1.0f;
         if (c->arch == OR_QWEN35 && find(t, n, LN("ssm_a"))) { /* src/model.cpp:343-358 */
             const size_t qkv = 2 * (size_t)c->ssm_k_heads * c->ssm_state + (size_t)c->ssm_inner;
             GETM(L->ssm_qkv, LN("attn_qkv.weight"));
@@ -943,21 +977,35 @@ oracle_session* or_session_create(const oracle_config* cfg, const oracle_tensor*
             L->up.rows = (size_t)c->ff; L->up.data += (size_t)c->ff * rb;
         } else {
             GETM(L->q, LN("attn_q.weight"));
-            GETM(L->k, LN("attn_k.weight"));
-            GETM(L->v, LN("attn_v.weight"));
+            if (kv_layer_of(c, l) == l) {
+                GETM(L->k, LN("attn_k.weight"));
+                /* Gemma 4 global layers may have no V projection: K serves as V (src/model.cpp:386-388) */
+                if (find(t, n, LN("attn_v.weight"))) GETM(L->v, LN("attn_v.weight"));
+                else L->v = L->k;
+            }
             GETM(L->gate, LN("ffn_gate.weight"));
             GETM(L->up, LN("ffn_up.weight"));
         }
         GETM(L->o, LN("attn_output.weight"));
         GETV(L->ffn_norm, LN(c->arch == OR_QWEN35 ? "post_attention_norm.weight" : "ffn_norm.weight")); /* src/model.cpp:418 */
         GETM(L->down, LN("ffn_down.weight"));
-        if (c->arch == OR_GEMMA3) {
+        if (c->arch == OR_GEMMA3 || c->arch == OR_GEMMA4) {
             GETV(L->attn_post_norm, LN("post_attention_norm.weight"));
             GETV(L->ffn_post_norm, LN("post_ffw_norm.weight"));
         }
-        if (c->arch == OR_QWEN3 || c->arch == OR_GEMMA3 || c->arch == OR_LFM2 || c->arch == OR_QWEN35) { /* src/model.cpp:394-398 */
+        if (c->arch == OR_QWEN3 || c->arch == OR_GEMMA3 || c->arch == OR_LFM2 || c->arch == OR_QWEN35 || c->arch == OR_GEMMA4) { /* src/model.cpp:394-398 */
             GETV(L->q_norm, LN("attn_q_norm.weight"));
-            GETV(L->k_norm, LN("attn_k_norm.weight"));
+            if (kv_layer_of(c, l) == l) GETV(L->k_norm, LN("attn_k_norm.weight"));
+        }
+        if (c->ple_dim != 0) { /* src/model.cpp:403-407 */
+            GETM(L->ple_gate, LN("inp_gate.weight"));
+            GETM(L->ple_proj, LN("proj.weight"));
+            GETV(L->ple_post_norm, LN("post_norm.weight"));
+        }
+        if (find(t, n, LN("layer_output_scale.weight"))) { /* src/model.cpp:408-410 */
+            const float* os;
+            GETV(os, LN("layer_output_scale.weight"));
+            L->out_scale = os[0];
         }
         if (c->arch == OR_BITNET) {
             GETV(L->attn_sub_norm, LN("attn_sub_norm.weight"));
@@ -970,12 +1018,19 @@ oracle_session* or_session_create(const oracle_config* cfg, const oracle_tensor*
         }
     }
     {
-        const size_t kvsz = (size_t)c->kv_heads * c->max_context * c->head_dim;
         s->kcache = (uint16_t**)calloc((size_t)c->layers, sizeof(uint16_t*));
         s->vcache = (uint16_t**)calloc((size_t)c->layers, sizeof(uint16_t*));
         for (int l = 0; l < c->layers; ++l) {
+            if (kv_layer_of(c, l) != l) continue;
+            const size_t kvsz = kv_heads_of(c, l) * c->max_context * head_dim_of(c, l);
             s->kcache[l] = (uint16_t*)calloc(kvsz, 2);
             s->vcache[l] = (uint16_t*)calloc(kvsz, 2);
+        }
+        if (c->ple_dim != 0) {
+            const size_t pall = (size_t)c->ple_dim * c->layers;
+            s->ple = (float*)calloc(pall, 4);
+            s->ple_row = (float*)calloc(pall, 4);
+            s->ple_g = (float*)calloc((size_t)c->ple_dim, 4);
         }
         const size_t qd = (size_t)c->heads * c->head_dim, kvd = (size_t)c->kv_heads * c->head_dim;
         const size_t wide = (size_t)(c->embd > c->ff ? c->embd : c->ff) + qd;
@@ -1015,9 +1070,10 @@ bad:
 void or_session_destroy(oracle_session* s) {
     if (!s) return;
     if (s->kcache)
-        for (int l = 0; l < s->c.layers; ++l) free(s->kcache[l]);
+        for (int l = 0; l < s->c.layers; ++l) free(s->kcache[l]);  /* shared layers hold NULL */
     if (s->vcache)
         for (int l = 0; l < s->c.layers; ++l) free(s->vcache[l]);
+    free(s->ple); free(s->ple_row); free(s->ple_g);
     free(s->kcache);
     free(s->vcache);
     for (int l = 0; s->layers && l < s->c.layers; ++l) {
@@ -1092,12 +1148,10 @@ static void embedding_row(const matrix* m, size_t r, float* out) {
  * attention rows only see their own visible range), so a batch equals its tokens in order. */
 static void forward_token(oracle_session* s, int32_t token, float* logits) {
     const oracle_config* c = &s->c;
-    const size_t embd = c->embd, hd = c->head_dim, qd = (size_t)c->heads * hd, kvd = (size_t)c->kv_heads * hd;
-    const size_t hpk = (size_t)(c->heads / c->kv_heads), pos = s->position, ctx = (size_t)c->max_context;
+    const size_t embd = c->embd, hd = c->head_dim, pos = s->position, ctx = (size_t)c->max_context;
     const int neox = c->arch != OR_LLAMA && c->arch != OR_SMOLLM3; /* src/model.cpp:167 */
-    const float attention_scale = 1.0f / sqrtf((float)hd);
-
-    const int gemma = c->arch == OR_GEMMA3;
+    const int gemma = c->arch == OR_GEMMA3 || c->arch == OR_GEMMA4;
+    const size_t hd_local = c->head_dim_local != 0 ? (size_t)c->head_dim_local : hd;
     /* build_rope (src/model.cpp:880-894), attn factor 1, no factors; Gemma 3: the global
      * table at scale 1 / rope.scaling.factor, the sliding layers' at their own base, scale 1 */
     {
@@ -1112,10 +1166,10 @@ static void forward_token(oracle_session* s, int32_t token, float* logits) {
             s->rope[2 * i + 1] = sinf(angle) * af;
             theta *= theta_scale;
         }
-        if (gemma && c->sliding_window != 0) {
-            const float ts = powf(c->rope_base_local, -2.0f / (float)hd);
+        if (gemma && c->sliding_window != 0) { /* the sliding layers' head size (src/model.cpp:875, :894) */
+            const float ts = powf(c->rope_base_local, -2.0f / (float)hd_local);
             float th = (float)pos * 1.0f;
-            for (size_t i = 0; i < hd / 2; ++i) {
+            for (size_t i = 0; i < hd_local / 2; ++i) {
                 s->rope_local[2 * i] = cosf(th) * 1.0f;
                 s->rope_local[2 * i + 1] = sinf(th) * 1.0f;
                 th *= ts;
@@ -1126,6 +1180,19 @@ static void forward_token(oracle_session* s, int32_t token, float* logits) {
     if (gemma) { /* src/model.cpp:286, :899-901 */
         const float es = sqrtf((float)embd);
         for (size_t i = 0; i < embd; ++i) s->h[i] *= es;
+    }
+    if (c->ple_dim != 0) { /* Gemma 4's per-layer embedding inputs (src/model.cpp:905-925) */
+        const size_t pd = (size_t)c->ple_dim;
+        multiply(s, &s->ple_model_proj, s->h, s->ple);
+        const float proj_scale = 1.0f / sqrtf((float)embd);
+        const float table_scale = sqrtf((float)pd);
+        embedding_row(&s->ple_tok, (size_t)token, s->ple_row);
+        for (int l = 0; l < c->layers; ++l) {
+            float* slice = s->ple + (size_t)l * pd;
+            for (size_t i = 0; i < pd; ++i) slice[i] *= proj_scale;
+            or_rms_norm(slice, s->ple_proj_norm, c->eps, slice, pd);
+            for (size_t i = 0; i < pd; ++i) slice[i] = (slice[i] + s->ple_row[(size_t)l * pd + i] * table_scale) * 0.70710678f;
+        }
     }
 
     for (int l = 0; l < c->layers; ++l) {
@@ -1212,72 +1279,85 @@ static void forward_token(oracle_session* s, int32_t token, float* logits) {
             for (size_t i = 0; i < embd; ++i) s->h[i] += s->proj[i];
             goto ffn;
         }
+        /* the layer's head size, key/value heads and cache (Gemma 4: sliding layers' smaller heads,
+         * per-layer key/value heads, later layers reading an earlier layer's cache; src/model.h:111-117) */
+        const size_t hdl = head_dim_of(c, l), qdl = (size_t)c->heads * hdl, kvh = kv_heads_of(c, l), kvdl = kvh * hdl;
+        const size_t hpkl = (size_t)c->heads / kvh;
+        const int src = kv_layer_of(c, l), own_kv = src == l;
+        const float attention_scale = c->attention_scale != 0.0f ? c->attention_scale : 1.0f / sqrtf((float)hdl);
         if (c->arch == OR_QWEN35) { /* each head's query followed by its gate (src/model.cpp:1002-1012) */
             multiply(s, &L->q, s->normed, s->qg);
             for (int h = 0; h < c->heads; ++h) {
-                memcpy(s->q + h * hd, s->qg + 2 * h * hd, hd * 4);
-                memcpy(s->agate + h * hd, s->qg + 2 * h * hd + hd, hd * 4);
+                memcpy(s->q + h * hdl, s->qg + 2 * h * hdl, hdl * 4);
+                memcpy(s->agate + h * hdl, s->qg + 2 * h * hdl + hdl, hdl * 4);
             }
         } else {
             multiply(s, &L->q, s->normed, s->q);
         }
-        multiply(s, &L->k, s->normed, s->k);
-        multiply(s, &L->v, s->normed, s->v);
+        if (own_kv) {
+            multiply(s, &L->k, s->normed, s->k);
+            multiply(s, &L->v, s->normed, s->v);
+        }
         /* SmolLM3: every fourth layer has no RoPE (layer_has_rope, src/model.h:110; step 4, src/model.cpp:168) */
-        /* Gemma 3: layers with l % 6 != 5 slide (layer_slides, src/model.h:87-90) */
-        const int slides = gemma && c->sliding_window != 0 && l % 6 != 5;
+        /* Gemma: the sliding layers (layer_slides, src/model.h:87-90) */
+        const int slides = gemma && layer_slides(c, l);
         /* the rotated width (src/model.cpp:1024): none, the head, or the partial rotary dimension */
-        const size_t rope_dim = (c->arch == OR_SMOLLM3 && (l + 1) % 4 == 0) ? 0 : slides ? hd : (c->rope_dim ? (size_t)c->rope_dim : hd);
+        const size_t rd_g = c->rope_dim ? (size_t)c->rope_dim : hd;
+        const size_t rope_dim = (c->arch == OR_SMOLLM3 && (l + 1) % 4 == 0) ? 0 : slides ? hdl : (rd_g < hdl ? rd_g : hdl);
         const float* rope = slides ? s->rope_local : s->rope;
         if (L->q_bias) { /* add_bias (src/model.cpp:117-119, :1026-1030) */
-            for (size_t i = 0; i < qd; ++i) s->q[i] += L->q_bias[i];
-            for (size_t i = 0; i < kvd; ++i) s->k[i] += L->k_bias[i];
-            for (size_t i = 0; i < kvd; ++i) s->v[i] += L->v_bias[i];
+            for (size_t i = 0; i < qdl; ++i) s->q[i] += L->q_bias[i];
+            for (size_t i = 0; i < kvdl; ++i) s->k[i] += L->k_bias[i];
+            for (size_t i = 0; i < kvdl; ++i) s->v[i] += L->v_bias[i];
         }
         for (int h = 0; h < c->heads; ++h) {
-            float* q = s->q + h * hd;
-            if (L->q_norm) or_rms_norm(q, L->q_norm, c->eps, q, hd);
+            float* q = s->q + h * hdl;
+            if (L->q_norm) or_rms_norm(q, L->q_norm, c->eps, q, hdl);
             apply_rope(q, rope, rope_dim, neox);
         }
-        for (int h = 0; h < c->kv_heads; ++h) {
-            float* k = s->k + h * hd;
-            const float* v = s->v + h * hd;
-            if (L->k_norm) or_rms_norm(k, L->k_norm, c->eps, k, hd);
-            apply_rope(k, rope, rope_dim, neox);
-            uint16_t* kr = s->kcache[l] + ((size_t)h * ctx + pos) * hd;
-            uint16_t* vr = s->vcache[l] + ((size_t)h * ctx + pos) * hd;
-            for (size_t i = 0; i < hd; ++i) {
-                kr[i] = or_float_to_half(k[i]);
-                vr[i] = or_float_to_half(v[i]);
+        if (own_kv)
+            for (size_t h = 0; h < kvh; ++h) {
+                float* k = s->k + h * hdl;
+                float* v = s->v + h * hdl;
+                if (L->k_norm) or_rms_norm(k, L->k_norm, c->eps, k, hdl);
+                if (c->value_norm) or_rms_norm(v, NULL, c->eps, v, hdl); /* Gemma 4: V normalised, no weight (:1041) */
+                apply_rope(k, rope, rope_dim, neox);
+                uint16_t* kr = s->kcache[l] + (h * ctx + pos) * hdl;
+                uint16_t* vr = s->vcache[l] + (h * ctx + pos) * hdl;
+                for (size_t i = 0; i < hdl; ++i) {
+                    kr[i] = or_float_to_half(k[i]);
+                    vr[i] = or_float_to_half(v[i]);
+                }
             }
-        }
-        /* attention (src/model.cpp:1050-1093, src/kernels_f32.cpp:256-284) */
+        /* attention (src/model.cpp:1050-1093, src/kernels_f32.cpp:256-284) over the cache of layer src */
         {
             const size_t visible = pos + 1;
             /* a sliding layer sees the last sliding_window positions (src/model.cpp:1084-1085) */
             const size_t start = slides && visible > (size_t)c->sliding_window ? visible - (size_t)c->sliding_window : 0;
+            const uint16_t* kc = s->kcache[src];
+            const uint16_t* vc = s->vcache[src];
             float* key = s->proj; /* free until the output projection */
             for (int h = 0; h < c->heads; ++h) {
-                const size_t kv = (size_t)h / hpk;
-                const float* q = s->q + h * hd;
+                const size_t kv = (size_t)h / hpkl;
+                const float* q = s->q + h * hdl;
                 for (size_t p = start; p < visible; ++p) {
-                    const uint16_t* kr = s->kcache[l] + (kv * ctx + p) * hd;
-                    for (size_t i = 0; i < hd; ++i) key[i] = or_half_to_float(kr[i]);
-                    s->scores[p] = or_dot_f32(q, key, hd) * attention_scale;
+                    const uint16_t* kr = kc + (kv * ctx + p) * hdl;
+                    for (size_t i = 0; i < hdl; ++i) key[i] = or_half_to_float(kr[i]);
+                    s->scores[p] = or_dot_f32(q, key, hdl) * attention_scale;
                 }
                 or_softmax(s->scores + start, visible - start);
-                float* out = s->att + h * hd;
-                for (size_t i = 0; i < hd; ++i) out[i] = 0.0f;
+                float* out = s->att + h * hdl;
+                for (size_t i = 0; i < hdl; ++i) out[i] = 0.0f;
                 for (size_t p = start; p < visible; ++p) {
-                    const uint16_t* vr = s->vcache[l] + (kv * ctx + p) * hd;
+                    const uint16_t* vr = vc + (kv * ctx + p) * hdl;
                     const float w = s->scores[p];
-                    for (size_t i = 0; i < hd; ++i) out[i] += w * or_half_to_float(vr[i]);
+                    for (size_t i = 0; i < hdl; ++i) out[i] += w * or_half_to_float(vr[i]);
                 }
             }
         }
-        if (L->attn_sub_norm) or_rms_norm(s->att, L->attn_sub_norm, c->eps, s->att, qd);
+        if (L->attn_sub_norm) or_rms_norm(s->att, L->attn_sub_norm, c->eps, s->att, qdl);
         if (c->arch == OR_QWEN35) /* the sigmoid gate (src/model.cpp:1102-1108) */
-            for (size_t i = 0; i < qd; ++i) s->att[i] *= 1.0f / (1.0f + expf(-s->agate[i]));
+            for (size_t i = 0; i < qdl; ++i) s->att[i] *= 1.0f / (1.0f + expf(-s->agate[i]));
         multiply(s, &L->o, s->att, s->proj);
         if (L->attn_post_norm) or_rms_norm(s->proj, L->attn_post_norm, c->eps, s->proj, embd); /* :1116-1119 */
         for (size_t i = 0; i < embd; ++i) s->h[i] += s->proj[i];
@@ -1285,7 +1365,8 @@ static void forward_token(oracle_session* s, int32_t token, float* logits) {
         or_rms_norm(s->h, L->ffn_norm, c->eps, s->normed, embd);
         multiply(s, &L->gate, s->normed, s->gate);
         multiply(s, &L->up, s->normed, s->up);
-        for (int i = 0; i < c->ff; ++i) { /* src/model.cpp:1128-1143, src/kernels_f32.cpp:287-289 */
+        const size_t ffl = ff_of(c, l); /* Gemma 4: the layer's width (ff_dim_of, src/model.h:118) */
+        for (size_t i = 0; i < ffl; ++i) { /* src/model.cpp:1128-1143, src/kernels_f32.cpp:287-289 */
             const float g = s->gate[i];
             if (c->arch == OR_BITNET) {
                 const float r = g > 0.0f ? g : 0.0f;
@@ -1296,11 +1377,25 @@ static void forward_token(oracle_session* s, int32_t token, float* logits) {
                 s->gate[i] = g / (1.0f + expf(-g)) * s->up[i];
             }
         }
-        if (L->ffn_sub_norm) or_rms_norm(s->gate, L->ffn_sub_norm, c->eps, s->gate, c->ff);
+        if (L->ffn_sub_norm) or_rms_norm(s->gate, L->ffn_sub_norm, c->eps, s->gate, ffl);
         multiply(s, &L->down, s->gate, s->proj);
         if (L->ffn_post_norm) or_rms_norm(s->proj, L->ffn_post_norm, c->eps, s->proj, embd); /* :1156-1159 */
         for (size_t i = 0; i < embd; ++i) s->h[i] += s->proj[i];
-        (void)kvd;
+        if (c->ple_dim != 0) { /* h = (h + norm(proj(gelu(gate h) * ple_input[l]))) * scale (src/model.cpp:1163-1177) */
+            const size_t pd = (size_t)c->ple_dim;
+            multiply(s, &L->ple_gate, s->h, s->ple_g);
+            const float* in = s->ple + (size_t)l * pd;
+            for (size_t i = 0; i < pd; ++i) {
+                const float g = s->ple_g[i];
+                s->ple_g[i] = 0.5f * g * (1.0f + tanhf(0.7978845608f * (g + 0.044715f * g * g * g))) * in[i];
+            }
+            multiply(s, &L->ple_proj, s->ple_g, s->proj);
+            or_rms_norm(s->proj, L->ple_post_norm, c->eps, s->proj, embd);
+            for (size_t i = 0; i < embd; ++i) s->h[i] = (s->h[i] + s->proj[i]) * L->out_scale;
+        } else if (L->out_scale != 1.0f) {
+            for (size_t i = 0; i < embd; ++i) s->h[i] *= L->out_scale;
+        }
+
         if (getenv("BRISK_CPU_DEBUG") != NULL) { /* the reference's per-layer line, src/model.cpp:1183-1192 */
             double sum = 0.0;
             float peak = 0.0f;

@@ -25,7 +25,7 @@ extern "C" {
 /* ggml tensor types (src/gguf.h:22-27). */
 enum { OR_F32 = 0, OR_Q4_0 = 2, OR_Q4_1 = 3, OR_Q5_0 = 6, OR_Q8_0 = 8, OR_Q4_K = 12, OR_Q5_K = 13, OR_Q6_K = 14, OR_TQ2_0 = 35 };
 /* Architectures of src/model.h:21-32 that the configs use. */
-enum { OR_QWEN3 = 0, OR_LLAMA = 1, OR_BITNET = 2, OR_QWEN2 = 3, OR_SMOLLM3 = 4, OR_GEMMA3 = 5, OR_PHI3 = 6, OR_LFM2 = 7, OR_QWEN35 = 8 };
+enum { OR_QWEN3 = 0, OR_LLAMA = 1, OR_BITNET = 2, OR_QWEN2 = 3, OR_SMOLLM3 = 4, OR_GEMMA3 = 5, OR_PHI3 = 6, OR_LFM2 = 7, OR_QWEN35 = 8, OR_GEMMA4 = 9 };
 
 typedef struct {
     int arch;
@@ -44,6 +44,15 @@ typedef struct {
     /* Qwen3.5 Gated DeltaNet layers (src/model.h:100-109): state size, key and value heads,
      * inner width (value heads x state), conv width; the layers with blk.N.ssm_a are recurrent */
     int ssm_state, ssm_k_heads, ssm_v_heads, ssm_inner, ssm_conv;
+    /* Gemma 4 (src/model.cpp:189-226, src/model.h:76-118); zero / NULL elsewhere: the sliding
+     * layers' head size (0: head_dim), the first layer reading another's K/V (0: none), the
+     * per-layer embedding width, the score scale (0: 1 / sqrt(head size)), V's weightless norm,
+     * and per-layer tables (NULL: every sixth layer global; ff and kv_heads everywhere) */
+    int head_dim_local, kv_from_start, ple_dim, value_norm;
+    float attention_scale;
+    const uint8_t* sliding_pattern;
+    const int32_t* ff_dims;
+    const int32_t* kv_head_counts;
 } oracle_config;
 
 /* One tensor of the model: `rows` x `cols` (vectors: rows = 1), GGUF bytes. */

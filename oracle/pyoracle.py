@@ -26,7 +26,10 @@ class OracleConfig(C.Structure):
                 ("sliding_window", C.c_int), ("rope_base_local", C.c_float), ("rope_scale", C.c_float),
                 ("final_softcap", C.c_float), ("rope_dim", C.c_int), ("rope_attn_factor", C.c_float),
                 ("rope_original_context", C.c_int), ("conv_taps", C.c_int), ("ssm_state", C.c_int),
-                ("ssm_k_heads", C.c_int), ("ssm_v_heads", C.c_int), ("ssm_inner", C.c_int), ("ssm_conv", C.c_int)]
+                ("ssm_k_heads", C.c_int), ("ssm_v_heads", C.c_int), ("ssm_inner", C.c_int), ("ssm_conv", C.c_int),
+                ("head_dim_local", C.c_int), ("kv_from_start", C.c_int), ("ple_dim", C.c_int), ("value_norm", C.c_int),
+                ("attention_scale", C.c_float), ("sliding_pattern", C.c_void_p), ("ff_dims", C.c_void_p),
+                ("kv_head_counts", C.c_void_p)]
 
 
 class OracleTensor(C.Structure):
@@ -144,6 +147,15 @@ class Oracle:
                          cfg.rope_base, cfg.eps, max_context, cfg.sliding_window, cfg.rope_base_local, cfg.rope_scale,
                          cfg.final_softcap, cfg.rope_dim, cfg.rope_attn_factor, cfg.rope_original_context, cfg.conv_taps,
                          cfg.ssm_state, cfg.ssm_k_heads, cfg.ssm_v_heads, cfg.ssm_inner, cfg.ssm_conv)
+        c.head_dim_local, c.kv_from_start, c.ple_dim = cfg.head_dim_local, cfg.kv_from_start, cfg.ple_dim
+        c.value_norm, c.attention_scale = cfg.value_norm, cfg.attention_scale
+        self._tables = []
+        for field, vals, dt in (("sliding_pattern", cfg.sliding_pattern, np.uint8), ("ff_dims", cfg.ff_dims, np.int32),
+                                ("kv_head_counts", cfg.kv_head_counts, np.int32)):
+            if len(vals):
+                a = np.ascontiguousarray(vals, dtype=dt)
+                self._tables.append(a)
+                setattr(c, field, a.ctypes.data)
         self._names = [t.name.encode() for t in table]
         arr = (OracleTensor * len(table))()
         for i, t in enumerate(table):
@@ -213,7 +225,10 @@ class RefConfig(C.Structure):
         ("n_rope_factors", C.c_uint32), ("n_factors_short", C.c_uint32), ("n_factors_long", C.c_uint32),
         ("conv_layers", C.c_uint64), ("ssm_state", C.c_uint32), ("ssm_k_heads", C.c_uint32),
         ("ssm_v_heads", C.c_uint32), ("ssm_inner", C.c_uint32), ("ssm_conv", C.c_uint32), ("attention_gate", C.c_int32),
-        ("recurrent_layers", C.c_uint64)]
+        ("recurrent_layers", C.c_uint64), ("head_dim_local", C.c_uint32), ("kv_from_start", C.c_uint32),
+        ("ple_dim", C.c_uint32), ("attention_scale", C.c_float), ("value_norm", C.c_int32), ("sliding_layers", C.c_uint64),
+        ("head_dim_of", C.c_uint32 * 64), ("kv_heads_of", C.c_uint32 * 64), ("ff_of", C.c_uint32 * 64),
+        ("kv_layer_of", C.c_uint32 * 64)]
 
 
 # the reference's Architecture enumerators (src/model.h:20-31), by GGUF architecture name

@@ -92,6 +92,11 @@ struct RefConfig {
     uint32_t ssm_state, ssm_k_heads, ssm_v_heads, ssm_inner, ssm_conv;
     int32_t attention_gate;
     uint64_t recurrent_layers;  // bit l: layer l is a Gated DeltaNet layer (layers 0..63)
+    uint32_t head_dim_local, kv_from_start, ple_dim;
+    float attention_scale;
+    int32_t value_norm;
+    uint64_t sliding_layers;    // bit l: layer_slides(l) (layers 0..63)
+    uint32_t head_dim_of[64], kv_heads_of[64], ff_of[64], kv_layer_of[64];
 };
 
 int ref_config(void* handle, RefConfig* out) {
@@ -115,6 +120,15 @@ int ref_config(void* handle, RefConfig* out) {
         r.ssm_inner = c.ssm_inner; r.ssm_conv = c.ssm_conv; r.attention_gate = c.attention_gate ? 1 : 0;
         for (std::size_t l = 0; l < c.layer_count && l < 64; ++l)
             if (c.layer_is_recurrent(l)) r.recurrent_layers |= uint64_t{1} << l;
+        r.head_dim_local = c.head_dim_local; r.kv_from_start = c.kv_from_start; r.ple_dim = c.ple_dim;
+        r.attention_scale = c.attention_scale; r.value_norm = c.value_norm ? 1 : 0;
+        for (std::size_t l = 0; l < c.layer_count && l < 64; ++l) {
+            if (c.layer_slides(l)) r.sliding_layers |= uint64_t{1} << l;
+            r.head_dim_of[l] = c.head_dim_of(l);
+            r.kv_heads_of[l] = c.kv_head_count_of(l);
+            r.ff_of[l] = c.ff_dim_of(l);
+            r.kv_layer_of[l] = static_cast<uint32_t>(c.kv_layer_of(l));
+        }
         *out = r;
     });
 }

@@ -48,6 +48,7 @@ RUNS = {
     "tiny-qwen35": (12, 48),
     "tiny-qwen35w": (12, 48),
     "tiny-qwen35h": (12, 48),
+    "tiny-gemma4": (12, 48),
 }
 
 

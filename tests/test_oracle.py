@@ -424,7 +424,7 @@ def tiny(name):
     return path, f, cfg, table
 
 
-@pytest.mark.parametrize("name", ["tiny-qwen3", "tiny-llama", "tiny-q8", "tiny-bitnet", "tiny-q5k", "tiny-q5", "tiny-qwen2", "tiny-smollm3", "tiny-gemma3", "tiny-phi3", "tiny-llama32", "tiny-lfm2", "tiny-qwen35", "tiny-qwen35w", "tiny-qwen35h"])
+@pytest.mark.parametrize("name", ["tiny-qwen3", "tiny-llama", "tiny-q8", "tiny-bitnet", "tiny-q5k", "tiny-q5", "tiny-qwen2", "tiny-smollm3", "tiny-gemma3", "tiny-phi3", "tiny-llama32", "tiny-lfm2", "tiny-qwen35", "tiny-qwen35w", "tiny-qwen35h", "tiny-gemma4"])
 def test_oracle_greedy_matches_reference_fixture(name):
     """tests/golden/<name>_greedy.json were written by the reference engine itself."""
     with open(os.path.join(HERE, "golden", f"{name}_greedy.json")) as fh:
@@ -453,7 +453,7 @@ def test_oracle_first_tokens_of_qwen3_0_6b_fixture():
 
 
 @needs_ref
-@pytest.mark.parametrize("name", ["tiny-qwen3", "tiny-llama", "tiny-bitnet", "tiny-q5k", "tiny-q5", "tiny-qwen2", "tiny-smollm3", "tiny-gemma3", "tiny-phi3", "tiny-llama32", "tiny-lfm2", "tiny-qwen35", "tiny-qwen35w", "tiny-qwen35h"])
+@pytest.mark.parametrize("name", ["tiny-qwen3", "tiny-llama", "tiny-bitnet", "tiny-q5k", "tiny-q5", "tiny-qwen2", "tiny-smollm3", "tiny-gemma3", "tiny-phi3", "tiny-llama32", "tiny-lfm2", "tiny-qwen35", "tiny-qwen35w", "tiny-qwen35h", "tiny-gemma4"])
 def test_oracle_session_matches_reference_bitwise(name):
     """eval, eval_all and rollback of the restatement against the reference's Session."""
     path, f, cfg, table = tiny(name)
@@ -529,7 +529,7 @@ def test_oracle_longrope_matches_reference_bitwise():
 
 
 @needs_ref
-@pytest.mark.parametrize("name", ["tiny-qwen3", "tiny-llama", "tiny-bitnet", "tiny-q5k", "tiny-q5", "tiny-qwen2", "tiny-smollm3", "tiny-gemma3", "tiny-phi3", "tiny-llama32", "tiny-lfm2", "tiny-qwen35", "tiny-qwen35w", "tiny-qwen35h"])
+@pytest.mark.parametrize("name", ["tiny-qwen3", "tiny-llama", "tiny-bitnet", "tiny-q5k", "tiny-q5", "tiny-qwen2", "tiny-smollm3", "tiny-gemma3", "tiny-phi3", "tiny-llama32", "tiny-lfm2", "tiny-qwen35", "tiny-qwen35w", "tiny-qwen35h", "tiny-gemma4"])
 def test_model_config_matches_reference(name):
     """brisk_hip.model.parse_config against the reference's own ModelConfig parse (src/model.cpp:140-260)
     of the same file, field by field. The Python config keeps 0 for a field its family does not use;
@@ -548,7 +548,7 @@ def test_model_config_matches_reference(name):
     assert c.rope_original_context == cfg.rope_original_context
     assert f32(c.rope_attn_factor) == f32(cfg.rope_attn_factor or 1.0)
     assert c.sliding_window == cfg.sliding_window
-    gemma = cfg.arch == model.ARCH_GEMMA3
+    gemma = cfg.arch in (model.ARCH_GEMMA3, model.ARCH_GEMMA4)
     assert f32(c.rope_base_local) == f32(cfg.rope_base_local if gemma else 10000.0)
     assert f32(c.rope_scale) == f32(cfg.rope_scale if gemma else 1.0)
     assert f32(c.final_softcap) == f32(cfg.final_softcap)
@@ -563,6 +563,16 @@ def test_model_config_matches_reference(name):
     assert (c.ssm_state, c.ssm_k_heads, c.ssm_v_heads, c.ssm_inner, c.ssm_conv) == \
         (cfg.ssm_state, cfg.ssm_k_heads, cfg.ssm_v_heads, cfg.ssm_inner, cfg.ssm_conv)
     assert bool(c.attention_gate) == (cfg.arch == model.ARCH_QWEN35)
+    # Gemma 4's per-layer shapes (src/model.h:76-118)
+    assert (c.head_dim_local, c.kv_from_start, c.ple_dim, bool(c.value_norm)) == \
+        (cfg.head_dim_local, cfg.kv_from_start, cfg.ple_dim, bool(cfg.value_norm))
+    assert f32(c.attention_scale) == f32(cfg.attention_scale)
+    for l in range(cfg.layers):
+        assert bool(c.sliding_layers >> l & 1) == (cfg.layer_slides(l) if cfg.arch in (model.ARCH_GEMMA3, model.ARCH_GEMMA4)
+                                                   else False), l
+        assert (c.head_dim_of[l], c.ff_of[l], c.kv_layer_of[l]) == (cfg.head_dim_of(l), cfg.ff_of(l), cfg.kv_layer_of(l)), l
+        if l not in cfg.conv_layers + cfg.recurrent_layers:
+            assert c.kv_heads_of[l] == cfg.kv_heads_of(l), l
     assert c.no_rope_step == (4 if cfg.arch == model.ARCH_SMOLLM3 else 0)
     assert [l for l in range(cfg.layers) if not cfg.layer_has_rope(l)] == \
         ([l for l in range(cfg.layers) if (l + 1) % c.no_rope_step == 0] if c.no_rope_step else [])
