@@ -39,6 +39,7 @@ public:
             case Architecture::Phi3: cfg.arch = BRISK_HIP_ARCH_PHI3; break;
             case Architecture::LFM2: cfg.arch = BRISK_HIP_ARCH_LFM2; break;
             case Architecture::Qwen35: cfg.arch = BRISK_HIP_ARCH_QWEN35; break;
+            case Architecture::Gemma4: cfg.arch = BRISK_HIP_ARCH_GEMMA4; break;
             default: throw std::runtime_error("hip: this architecture is not on the GPU path");
         }
         // ModelConfig (src/model.h:36-125)
@@ -69,7 +70,15 @@ public:
         cfg.ssm_v_heads = c.ssm_v_heads;
         cfg.ssm_inner = c.ssm_inner;
         cfg.ssm_conv = c.ssm_conv;
-        for (std::size_t l = 0; l < c.layer_count; ++l)
+        cfg.head_dim_local = c.head_dim_local;
+        cfg.kv_from_start = c.kv_from_start;
+        cfg.ple_dim = c.ple_dim;
+        cfg.attention_scale = c.attention_scale;
+        cfg.value_norm = c.value_norm ? 1 : 0;
+        cfg.sliding_pattern = c.sliding_pattern.empty() ? nullptr : c.sliding_pattern.data();
+        cfg.ff_dims = c.ff_dims.empty() ? nullptr : c.ff_dims.data();
+        cfg.kv_head_counts = c.architecture != Architecture::Gemma4 || c.kv_head_counts.empty() ? nullptr : c.kv_head_counts.data();
+        for (std::size_t l = 0; l < c.layer_count && c.architecture != Architecture::Gemma4; ++l)
             if (c.kv_head_count_of(l) != 0 && c.kv_head_count_of(l) != c.kv_head_count)
                 throw std::runtime_error("hip: attention layers with different key/value head counts are not on the GPU path");
 
@@ -84,6 +93,11 @@ public:
         add_vector("rope_freqs.weight", c.rope_factors);
         add_vector("rope_factors_short.weight", c.rope_factors_short);
         add_vector("rope_factors_long.weight", c.rope_factors_long);
+        if (c.ple_dim != 0) {  // Gemma 4's per-layer embeddings
+            add_matrix("per_layer_token_embd.weight", model.ple_token_embedding());
+            add_matrix("per_layer_model_proj.weight", model.ple_model_proj());
+            add_vector("per_layer_proj_norm.weight", model.ple_proj_norm());
+        }
         for (std::size_t l = 0; l < c.layer_count; ++l) {
             const Model::Layer& L = model.layers()[l];
             const std::string b = "blk." + std::to_string(l) + ".";
@@ -123,6 +137,10 @@ public:
             add_vector(b + "ffn_sub_norm.weight", L.feed_forward_sub_norm);
             add_matrix(b + "ffn_down.weight", L.down);
             add_vector(b + "post_ffw_norm.weight", L.feed_forward_post_norm);
+            add_matrix(b + "inp_gate.weight", L.ple_gate);
+            add_matrix(b + "proj.weight", L.ple_proj);
+            add_vector(b + "post_norm.weight", L.ple_post_norm);
+            if (L.out_scale != 1.0f) add_vector(b + "layer_output_scale.weight", std::span<const float>(&L.out_scale, 1));
         }
         for (std::size_t i = 0; i < table_.size(); ++i) table_[i].name = names_[i].c_str();
         check(brisk_hip_session_create(&cfg, table_.data(), table_.size(), max_context, device, &s_));

@@ -35,7 +35,10 @@ class HipConfig(C.Structure):
                 ("rope_original_context", C.c_uint32), ("conv_taps", C.c_uint32), ("rope_neox", C.c_int32),
                 ("no_rope_step", C.c_uint32), ("embedding_scale", C.c_float), ("gelu", C.c_int32),
                 ("ssm_state", C.c_uint32), ("ssm_k_heads", C.c_uint32), ("ssm_v_heads", C.c_uint32),
-                ("ssm_inner", C.c_uint32), ("ssm_conv", C.c_uint32)]
+                ("ssm_inner", C.c_uint32), ("ssm_conv", C.c_uint32), ("head_dim_local", C.c_uint32),
+                ("kv_from_start", C.c_uint32), ("ple_dim", C.c_uint32), ("attention_scale", C.c_float),
+                ("value_norm", C.c_int32), ("sliding_pattern", C.c_void_p), ("ff_dims", C.c_void_p),
+                ("kv_head_counts", C.c_void_p)]
 
 
 class HipTensor(C.Structure):

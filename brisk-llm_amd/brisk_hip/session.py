@@ -29,11 +29,20 @@ def _c_args(c, table):
                         c.rope_dim, c.rope_attn_factor, c.rope_original_context, c.conv_taps)
     hc.ssm_state, hc.ssm_k_heads, hc.ssm_v_heads = c.ssm_state, c.ssm_k_heads, c.ssm_v_heads
     hc.ssm_inner, hc.ssm_conv = c.ssm_inner, c.ssm_conv
+    hc.head_dim_local, hc.kv_from_start, hc.ple_dim = c.head_dim_local, c.kv_from_start, c.ple_dim
+    hc.attention_scale, hc.value_norm = c.attention_scale, c.value_norm
+    keep = []
+    for field, vals, dt in (("sliding_pattern", c.sliding_pattern, np.uint8), ("ff_dims", c.ff_dims, np.uint32),
+                            ("kv_head_counts", c.kv_head_counts, np.uint32)):
+        if len(vals):
+            a = np.ascontiguousarray(vals, dtype=dt)
+            keep.append(a)
+            setattr(hc, field, a.ctypes.data)
     names = [t.name.encode() for t in table]
     arr = (_lib.HipTensor * len(table))()
     for i, t in enumerate(table):
         arr[i] = _lib.HipTensor(names[i], t.type, t.rows, t.cols, t.data.ctypes.data)
-    return hc, arr, names
+    return hc, arr, (names, keep)
 
 
 def estimate(source, max_context: int = 0) -> dict:

@@ -334,12 +334,44 @@ __global__ __launch_bounds__(kThreads) void k_embed(Packed m, PickState ps, floa
     }
 }
 
-// h += rms_norm(p, w) (src/model.cpp:1113-1121, :1153-1160): one workgroup.
+// h = (h + rms_norm(p, w)) * out_scale (src/model.cpp:1113-1121, :1153-1160, :1172-1176; x * 1.0f
+// is x, so out_scale 1 is the plain residual add): one workgroup.
 __global__ __launch_bounds__(kThreads) void k_post_add(float* __restrict__ h, const float* __restrict__ p,
-                                                       const float* __restrict__ w, float eps, int n) {
+                                                       const float* __restrict__ w, float eps, int n, float out_scale) {
     __shared__ double red[4];
     const float scale = rms_scale(block_sumsq(p, n, red), n, eps);
-    for (int i = threadIdx.x; i < n; i += kThreads) h[i] = h[i] + p[i] * scale * w[i];
+    for (int i = threadIdx.x; i < n; i += kThreads) h[i] = (h[i] + p[i] * scale * w[i]) * out_scale;
+}
+
+// h *= out_scale (src/model.cpp:1178-1181).
+__global__ void k_scale(float* __restrict__ h, float out_scale, int n) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) h[i] *= out_scale;
+}
+
+// Gemma 4's per-layer embedding inputs (src/model.cpp:905-925), one workgroup per layer's slice:
+// the slice scaled by 1/sqrt(embd) (stored, as the reference scales it in place), RMS-normed with
+// per_layer_proj_norm, plus the token's row of per_layer_token_embd times sqrt(dim), times 0.70710678.
+__global__ __launch_bounds__(kThreads) void k_ple_inputs(float* __restrict__ in, Packed table, const float* __restrict__ norm,
+                                                         const int* __restrict__ seq, const int* __restrict__ pos, int dim,
+                                                         float proj_scale, float table_scale, float eps) {
+    __shared__ double red[4];
+    const int l = blockIdx.x;
+    float* slice = in + static_cast<size_t>(l) * dim;
+    const uint32_t tok = static_cast<uint32_t>(seq[*pos]);
+    for (int i = threadIdx.x; i < dim; i += kThreads) slice[i] = slice[i] * proj_scale;
+    __syncthreads();
+    const float scale = rms_scale(block_sumsq(slice, dim, red), dim, eps);
+    for (int i = threadIdx.x; i < dim; i += kThreads) {
+        const float row = dequant_elem(table, tok, static_cast<uint32_t>(l * dim + i));
+        slice[i] = (slice[i] * scale * norm[i] + row * table_scale) * 0.70710678f;
+    }
+}
+
+// g = gelu(g) * in (gelu_mul_f32, src/kernels_f32.cpp:291-296).
+__global__ void k_gelu_mul(float* __restrict__ g, const float* __restrict__ in, int n) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) g[i] = gelu_mul(g[i], in[i]);
 }
 
 // LFM2 short convolution (src/model.cpp:935-969): bx = b * x, kept per position as
@@ -859,8 +891,26 @@ hipError_t launch_attention_plain(const AttnArgs& g, hipStream_t s) {
 
 int attention_max_splits(int ctx) { return (ctx + kSplit - 1) / kSplit; }
 
-hipError_t launch_post_add(float* h, const float* p, const float* w, float eps, int n, hipStream_t s) {
-    hipLaunchKernelGGL(k_post_add, dim3(1), dim3(kThreads), 0, s, h, p, w, eps, n);
+hipError_t launch_post_add(float* h, const float* p, const float* w, float eps, int n, hipStream_t s, float out_scale) {
+    hipLaunchKernelGGL(k_post_add, dim3(1), dim3(kThreads), 0, s, h, p, w, eps, n, out_scale);
+    return hipGetLastError();
+}
+
+hipError_t launch_scale(float* h, float out_scale, int n, hipStream_t s) {
+    hipLaunchKernelGGL(k_scale, dim3(static_cast<unsigned>((n + kThreads - 1) / kThreads)), dim3(kThreads), 0, s, h, out_scale, n);
+    return hipGetLastError();
+}
+
+hipError_t launch_ple_inputs(float* in, const Packed& table, const float* norm, const int* seq, const int* pos, int layers,
+                             int dim, float proj_scale, float table_scale, float eps, hipStream_t s) {
+    if (layers < 1 || dim < 1 || static_cast<size_t>(layers) * dim != table.cols) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_ple_inputs, dim3(static_cast<unsigned>(layers)), dim3(kThreads), 0, s, in, table, norm, seq, pos, dim,
+                       proj_scale, table_scale, eps);
+    return hipGetLastError();
+}
+
+hipError_t launch_gelu_mul(float* g, const float* in, int n, hipStream_t s) {
+    hipLaunchKernelGGL(k_gelu_mul, dim3(static_cast<unsigned>((n + kThreads - 1) / kThreads)), dim3(kThreads), 0, s, g, in, n);
     return hipGetLastError();
 }
 

@@ -125,8 +125,18 @@ hipError_t launch_attention(const AttnArgs& g, hipStream_t s);
 hipError_t launch_attention_plain(const AttnArgs& g, hipStream_t s);
 constexpr int kPlainMaxHead = 512;
 hipError_t launch_embed(const Packed& m, const PickState& ps, float* h, float scale, hipStream_t s);
-// h += rms_norm(p, w) over n values (Gemma's post-attention / post-feed-forward norm).
-hipError_t launch_post_add(float* h, const float* p, const float* w, float eps, int n, hipStream_t s);
+// h = (h + rms_norm(p, w)) * out_scale over n values (Gemma's post-attention / post-feed-forward
+// norm with out_scale 1; Gemma 4's per-layer embedding with the layer's output scale).
+hipError_t launch_post_add(float* h, const float* p, const float* w, float eps, int n, hipStream_t s, float out_scale = 1.0f);
+// h *= out_scale (Gemma 4's layer output scale without per-layer embeddings).
+hipError_t launch_scale(float* h, float out_scale, int n, hipStream_t s);
+// Gemma 4's per-layer embedding inputs of the token seq[*pos] (src/model.cpp:905-925): for each
+// layer l, slice l of in (the per_layer_model_proj rows of the scaled embedding) becomes
+// (rms_norm(slice * proj_scale, norm) + table[tok][l * dim ..] * table_scale) * 0.70710678.
+hipError_t launch_ple_inputs(float* in, const Packed& table, const float* norm, const int* seq, const int* pos, int layers,
+                             int dim, float proj_scale, float table_scale, float eps, hipStream_t s);
+// g = gelu(g) * in over n values (gelu_mul_f32, src/kernels_f32.cpp:291-296).
+hipError_t launch_gelu_mul(float* g, const float* in, int n, hipStream_t s);
 hipError_t launch_finalize(const PickState& ps, hipStream_t s);
 hipError_t launch_head(HeadArgs g, hipStream_t s);
 hipError_t launch_advance(int* pos, hipStream_t s);

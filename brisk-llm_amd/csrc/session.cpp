@@ -170,12 +170,24 @@ brisk_hip_memory estimate_session(const brisk_hip_config& cfg, const brisk_hip_t
     rec_layers = std::min<size_t>(rec_layers, cfg.layers - conv_layers);
     m.cache = 2 * (static_cast<size_t>(cfg.layers) - conv_layers - rec_layers) * kvd * ctx * 2 + conv_layers * ctx * e * 2 +
               rec_layers * (2 * static_cast<size_t>(cfg.ssm_v_heads) * cfg.ssm_state * cfg.ssm_state + cfg.ssm_conv * ssm_qkv) * 4;
+    if (cfg.arch == BRISK_HIP_ARCH_GEMMA4) {  // the layers' own caches at their own shapes (src/memory.cpp:59-68)
+        m.cache = 0;
+        for (uint32_t l = 0; l < cfg.layers; ++l) {
+            const bool slides = cfg.sliding_pattern != nullptr ? cfg.sliding_pattern[l] != 0 : cfg.sliding_window != 0 && l % 6 != 5;
+            if (cfg.kv_from_start != 0 && l >= cfg.kv_from_start) continue;
+            const size_t hdl = cfg.head_dim_local != 0 && slides ? cfg.head_dim_local : hd;
+            const size_t kvh = cfg.kv_head_counts != nullptr ? cfg.kv_head_counts[l] : cfg.kv_heads;
+            m.cache += 2 * kvh * hdl * ctx * 2;
+        }
+    }
     const size_t splits = static_cast<size_t>(attention_max_splits(static_cast<int>(ctx)));
     size_t sc = (e + 2 * qd + ff + cfg.vocab + 2 * kvd) * 4;              // token-path activations, logits
     sc += static_cast<size_t>(cfg.heads) * splits * (hd + 2) * 4;          // attention partials
     sc += (ctx + 1) * 4 + ctx * hd * 4;                                    // token sequence, RoPE table
     if (hd > 128) sc += (qd + static_cast<size_t>(cfg.heads) * ctx) * 4;  // the plain attention's queries and scores
-    if (cfg.arch == BRISK_HIP_ARCH_GEMMA3) sc += ctx * hd * 4 + e * 4;     // local RoPE table, post-norm input
+    if (cfg.arch == BRISK_HIP_ARCH_GEMMA3 || cfg.arch == BRISK_HIP_ARCH_GEMMA4) sc += ctx * hd * 4 + e * 4;  // local RoPE, post-norm input
+    if (cfg.arch == BRISK_HIP_ARCH_GEMMA4)  // the plain attention, the per-layer embedding inputs and gate
+        sc += (qd + static_cast<size_t>(cfg.heads) * ctx + static_cast<size_t>(cfg.ple_dim) * (cfg.layers + 1)) * 4;
     if (cfg.arch == BRISK_HIP_ARCH_LFM2) sc += 3 * e * 4;                  // conv rows
     if (cfg.arch == BRISK_HIP_ARCH_QWEN35)                                 // recurrence rows, query|gate rows, gates
         sc += (ssm_qkv + 2 * static_cast<size_t>(cfg.ssm_inner) + 2 * cfg.ssm_v_heads + 3 * qd) * 4;
@@ -195,6 +207,7 @@ brisk_hip_memory estimate_session(const brisk_hip_config& cfg, const brisk_hip_t
     {  // the token loop's block-major down copies and their term words (Session::setup_loop's push)
         size_t down_bytes = 0;
         bool fmt = cfg.ff % 32 == 0 && cfg.embd <= 4096 && cfg.arch != BRISK_HIP_ARCH_BITNET && cfg.arch != BRISK_HIP_ARCH_GEMMA3 &&
+                   cfg.arch != BRISK_HIP_ARCH_GEMMA4 && cfg.arch != BRISK_HIP_ARCH_QWEN35 &&
                    cfg.arch != BRISK_HIP_ARCH_LFM2;
         for (size_t i = 0; i < n && fmt; ++i) {
             const std::string name = tensors[i].name != nullptr ? tensors[i].name : "";
@@ -233,7 +246,23 @@ Session::Session(const brisk_hip_config& cfg, const brisk_hip_tensor* tensors, s
     int count = 0;
     if (hipGetDeviceCount(&count) != hipSuccess || count == 0) throw Error(BRISK_HIP_ENODEV, "hip: no GPU device available");
     if (device < 0 || device >= count) throw Error(BRISK_HIP_ENODEV, "hip: no GPU device " + std::to_string(device));
-    if (cfg.arch < BRISK_HIP_ARCH_QWEN3 || cfg.arch > BRISK_HIP_ARCH_QWEN35) model_fail("unsupported architecture");
+    if (cfg.arch < BRISK_HIP_ARCH_QWEN3 || cfg.arch > BRISK_HIP_ARCH_GEMMA4) model_fail("unsupported architecture");
+    if (cfg.arch == BRISK_HIP_ARCH_GEMMA4) {  // src/model.cpp:219-227, :275-291
+        if (cfg.kv_from_start != 0 && cfg.kv_from_start < 2) model_fail("more shared K/V layers than layers");
+        if (cfg.head_dim_local != 0 && (cfg.head_dim_local % 32 != 0 || cfg.head_dim_local > cfg.head_dim))
+            model_fail("the sliding layers' head size must be a multiple of 32 no larger than the global one");
+        for (uint32_t l = 0; l < cfg.layers; ++l) {
+            const uint32_t kvh = cfg.kv_head_counts != nullptr ? cfg.kv_head_counts[l] : cfg.kv_heads;
+            if (kvh == 0 || cfg.heads % kvh != 0) model_fail("head_count is not a multiple of head_count_kv");
+            if (cfg.heads / kvh > 16) model_fail("more than 16 query heads per key/value head is not supported");
+            if (kvh > cfg.kv_heads) model_fail("kv_heads must be the largest of the layers' key/value heads");
+            if (cfg.ff_dims != nullptr && (cfg.ff_dims[l] == 0 || cfg.ff_dims[l] > cfg.ff))
+                model_fail("ff must be the largest of the layers' feed-forward widths");
+        }
+    } else if (cfg.sliding_pattern != nullptr || cfg.ff_dims != nullptr || cfg.kv_head_counts != nullptr || cfg.ple_dim != 0 ||
+               cfg.kv_from_start != 0 || cfg.head_dim_local != 0) {
+        model_fail("per-layer shapes, shared K/V and per-layer embeddings are Gemma 4's only");
+    }
     if (cfg.arch == BRISK_HIP_ARCH_QWEN35) {  // src/model.cpp:262-265, :675
         if (cfg.ssm_v_heads == 0 || cfg.ssm_inner % cfg.ssm_v_heads != 0 || cfg.ssm_inner / cfg.ssm_v_heads != cfg.ssm_state ||
             cfg.ssm_k_heads != cfg.ssm_v_heads || cfg.ssm_conv < 2 || cfg.ssm_conv > 8)
@@ -254,7 +283,8 @@ Session::Session(const brisk_hip_config& cfg, const brisk_hip_tensor* tensors, s
     if (cfg.embd > kMaxCols || cfg.ff > kMaxCols || cfg.heads * cfg.head_dim > kMaxCols) model_fail("a row wider than 8192 is not supported");
     {
         const char* at = std::getenv("BRISK_HIP_ATTN");
-        plain_attn_ = cfg.head_dim > 128 || (at != nullptr && std::string(at) == "plain");
+        // Gemma 4's layers differ in head size and may read another layer's cache: the plain attention
+        plain_attn_ = cfg.head_dim > 128 || cfg.arch == BRISK_HIP_ARCH_GEMMA4 || (at != nullptr && std::string(at) == "plain");
     }
     check(hipSetDevice(device), "hipSetDevice");
     if (std::getenv("BRISK_NO_MEMORY_CHECK") == nullptr) {  // check_memory (src/memory.cpp:118-135), for HBM
@@ -330,8 +360,8 @@ Session::Session(const brisk_hip_config& cfg, const brisk_hip_tensor* tensors, s
     // ModelConfig's flags: the caller's values where given, else the family's (src/model.cpp:161-301)
     const uint32_t no_rope_step = cfg.no_rope_step == 0xFFFFFFFFu ? 0 : cfg.no_rope_step != 0 ? cfg.no_rope_step
                                 : cfg.arch == BRISK_HIP_ARCH_SMOLLM3 ? 4 : 0;
-    if (cfg.gelu != 0 && (cfg.gelu == 1) != (cfg.arch == BRISK_HIP_ARCH_GEMMA3)) model_fail("GELU gating outside Gemma is not supported");
-    if (cfg.embedding_scale != 0.0f && cfg.arch != BRISK_HIP_ARCH_GEMMA3 && cfg.embedding_scale != 1.0f)
+    if (cfg.gelu != 0 && (cfg.gelu == 1) != gemma()) model_fail("GELU gating outside Gemma is not supported");
+    if (cfg.embedding_scale != 0.0f && !gemma() && cfg.embedding_scale != 1.0f)
         model_fail("scaled embeddings outside Gemma are not supported");
     load_matrix("token_embd.weight", cfg.vocab, e, embd_);
     if (find("output.weight") != nullptr) {
@@ -341,11 +371,23 @@ Session::Session(const brisk_hip_config& cfg, const brisk_hip_tensor* tensors, s
         out_ = &embd_;  // tied (src/model.cpp:328-330)
     }
     out_norm_ = load_vector(cfg.arch == BRISK_HIP_ARCH_LFM2 ? "token_embd_norm.weight" : "output_norm.weight", e);  // src/model.cpp:331
+    if (cfg.ple_dim != 0) {  // Gemma 4's per-layer embeddings (src/model.cpp:319-324)
+        const size_t pall = static_cast<size_t>(cfg.ple_dim) * cfg.layers;
+        load_matrix("per_layer_token_embd.weight", cfg.vocab, pall, ple_tok_);
+        load_matrix("per_layer_model_proj.weight", pall, e, ple_proj_);
+        ple_norm_ = load_vector("per_layer_proj_norm.weight", cfg.ple_dim);
+    }
     layers_.resize(cfg.layers);
     for (uint32_t l = 0; l < cfg.layers; ++l) {
         const std::string b = "blk." + std::to_string(l) + ".";
         Layer& L = layers_[l];
         L.attn_norm = load_vector(b + "attn_norm.weight", e);
+        // ModelConfig's per-layer accessors (src/model.h:87-118)
+        L.slides = gemma() && (cfg.sliding_pattern != nullptr ? cfg.sliding_pattern[l] != 0 : cfg.sliding_window != 0 && l % 6 != 5);
+        L.hd = static_cast<int>(cfg.head_dim_local != 0 && L.slides ? cfg.head_dim_local : cfg.head_dim);
+        L.kvh = static_cast<int>(cfg.kv_head_counts != nullptr ? cfg.kv_head_counts[l] : cfg.kv_heads);
+        L.ff = static_cast<int>(cfg.ff_dims != nullptr ? cfg.ff_dims[l] : cfg.ff);
+        L.kv_src = static_cast<int>(cfg.kv_from_start == 0 || l < cfg.kv_from_start ? l : cfg.kv_from_start - (L.slides ? 2 : 1));
         if (cfg.arch == BRISK_HIP_ARCH_QWEN35 && find(b + "ssm_a") != nullptr) {  // src/model.cpp:343-358
             const size_t qkv = 3 * static_cast<size_t>(cfg.ssm_v_heads) * cfg.ssm_state;
             load_matrix(b + "attn_qkv.weight", qkv, e, L.ssm_qkv);
@@ -382,18 +424,32 @@ Session::Session(const brisk_hip_config& cfg, const brisk_hip_tensor* tensors, s
             load_rows(b + "ffn_up.weight", 0, cfg.ff, 2 * static_cast<size_t>(cfg.ff), e, L.gate);
             load_rows(b + "ffn_up.weight", cfg.ff, cfg.ff, 2 * static_cast<size_t>(cfg.ff), e, L.up);
         } else {
-            load_matrix(b + "attn_q.weight", qwen35() ? 2 * qd : qd, e, L.q);  // Qwen3.5: each head's query, then its gate
-            load_matrix(b + "attn_k.weight", kvd, e, L.k);
-            load_matrix(b + "attn_v.weight", kvd, e, L.v);
-            load_matrix(b + "ffn_gate.weight", cfg.ff, e, L.gate);
-            load_matrix(b + "ffn_up.weight", cfg.ff, e, L.up);
+            const size_t qdl = static_cast<size_t>(cfg.heads) * L.hd, kvdl = static_cast<size_t>(L.kvh) * L.hd;
+            load_matrix(b + "attn_q.weight", qwen35() ? 2 * qdl : qdl, e, L.q);  // Qwen3.5: each head's query, then its gate
+            if (L.kv_src == static_cast<int>(l)) {
+                load_matrix(b + "attn_k.weight", kvdl, e, L.k);
+                // Gemma 4 global layers may have no V projection: K serves as V (src/model.cpp:386-388)
+                L.v_is_k = gemma4() && find(b + "attn_v.weight") == nullptr;
+                if (!L.v_is_k) load_matrix(b + "attn_v.weight", kvdl, e, L.v);
+            }
+            load_matrix(b + "ffn_gate.weight", L.ff, e, L.gate);
+            load_matrix(b + "ffn_up.weight", L.ff, e, L.up);
         }
-        load_matrix(b + "attn_output.weight", e, qd, L.o);
+        load_matrix(b + "attn_output.weight", e, static_cast<size_t>(cfg.heads) * L.hd, L.o);
         L.ffn_norm = load_vector(b + (qwen35() ? "post_attention_norm.weight" : "ffn_norm.weight"), e);  // src/model.cpp:418
-        load_matrix(b + "ffn_down.weight", e, cfg.ff, L.down);
-        if (cfg.arch == BRISK_HIP_ARCH_QWEN3 || cfg.arch == BRISK_HIP_ARCH_GEMMA3 || cfg.arch == BRISK_HIP_ARCH_LFM2 || qwen35()) {
-            L.q_norm = load_vector(b + "attn_q_norm.weight", hd);
-            L.k_norm = load_vector(b + "attn_k_norm.weight", hd);
+        load_matrix(b + "ffn_down.weight", e, L.ff, L.down);
+        if (cfg.arch == BRISK_HIP_ARCH_QWEN3 || gemma() || cfg.arch == BRISK_HIP_ARCH_LFM2 || qwen35()) {
+            L.q_norm = load_vector(b + "attn_q_norm.weight", L.hd);
+            if (L.kv_src == static_cast<int>(l)) L.k_norm = load_vector(b + "attn_k_norm.weight", L.hd);
+        }
+        if (cfg.ple_dim != 0) {  // src/model.cpp:403-407
+            load_matrix(b + "inp_gate.weight", cfg.ple_dim, e, L.ple_gate);
+            load_matrix(b + "proj.weight", e, cfg.ple_dim, L.ple_proj);
+            L.ple_post_norm = load_vector(b + "post_norm.weight", e);
+        }
+        if (const brisk_hip_tensor* os = find(b + "layer_output_scale.weight")) {  // src/model.cpp:408-410
+            if (os->type != BRISK_HIP_F32 || os->rows * os->cols != 1) model_fail("tensor '" + b + "layer_output_scale.weight' has an unexpected size");
+            L.out_scale = *static_cast<const float*>(os->data);
         }
         if (cfg.arch == BRISK_HIP_ARCH_BITNET) {
             L.attn_sub_norm = load_vector(b + "attn_sub_norm.weight", e);
@@ -405,14 +461,15 @@ Session::Session(const brisk_hip_config& cfg, const brisk_hip_tensor* tensors, s
             L.v_bias = load_vector(b + "attn_v.bias", kvd);
         }
         L.rope = no_rope_step == 0 || (l + 1) % no_rope_step != 0;  // layer_has_rope (src/model.h:110, src/model.cpp:168)
-        if (cfg.arch == BRISK_HIP_ARCH_GEMMA3) {  // src/model.cpp:399-402; layer_slides, src/model.h:87-90
+        if (gemma()) {  // src/model.cpp:399-402
             L.attn_post_norm = load_vector(b + "post_attention_norm.weight", e);
             L.ffn_post_norm = load_vector(b + "post_ffw_norm.weight", e);
-            L.slides = cfg.sliding_window != 0 && l % 6 != 5;
         }
         // one activation row feeds Q, K and V: they must take the same width (src/model.cpp:584-590)
-        if (takes_q8_k(L.q.p.type) != takes_q8_k(L.k.p.type) || takes_q8_k(L.q.p.type) != takes_q8_k(L.v.p.type) ||
-            act_bits(L.q.p) != act_bits(L.k.p) || act_bits(L.q.p) != act_bits(L.v.p) ||
+        const Packed& kp = L.k.mem != nullptr ? L.k.p : L.q.p;  // a shared layer projects Q only
+        const Packed& vp = L.v.mem != nullptr ? L.v.p : kp;     // K serving as V
+        if (takes_q8_k(L.q.p.type) != takes_q8_k(kp.type) || takes_q8_k(L.q.p.type) != takes_q8_k(vp.type) ||
+            act_bits(L.q.p) != act_bits(kp) || act_bits(L.q.p) != act_bits(vp) ||
             takes_q8_k(L.gate.p.type) != takes_q8_k(L.up.p.type) || act_bits(L.gate.p) != act_bits(L.up.p))
             model_fail("fused multiply mixes activation widths");
     }
@@ -464,18 +521,30 @@ Session::Session(const brisk_hip_config& cfg, const brisk_hip_tensor* tensors, s
     check(hipMemsetAsync(ticket_, 0, 4096, stream_), "memset");
     check(hipMemsetAsync(pos_, 0, 64, stream_), "memset");
     check(hipMemsetAsync(seq_, 0, (max_ctx_ + 1) * 4, stream_), "memset");
-    const size_t kv_bytes = static_cast<size_t>(cfg.kv_heads) * max_ctx_ * hd * 2;
     kcache_.assign(cfg.layers, nullptr);
     vcache_.assign(cfg.layers, nullptr);
+    kv_bytes_.assign(cfg.layers, 0);
     for (uint32_t l = 0; l < cfg.layers; ++l) {
-        if (layers_[l].conv_w != nullptr) continue;  // a short-convolution layer keeps its bx rows instead (LFM2)
-        if (layers_[l].ssm_a != nullptr) continue;   // a recurrent layer keeps its state instead (Qwen3.5)
+        const Layer& L = layers_[l];
+        if (L.conv_w != nullptr) continue;  // a short-convolution layer keeps its bx rows instead (LFM2)
+        if (L.ssm_a != nullptr) continue;   // a recurrent layer keeps its state instead (Qwen3.5)
+        if (L.kv_src != static_cast<int>(l)) {  // Gemma 4: the cache of an earlier layer of its kind (src/model.cpp:979-983)
+            kcache_[l] = kcache_[L.kv_src];
+            vcache_[l] = vcache_[L.kv_src];
+            kv_bytes_[l] = kv_bytes_[L.kv_src];
+            continue;
+        }
+        const size_t kv_bytes = static_cast<size_t>(L.kvh) * max_ctx_ * L.hd * 2;
         kcache_[l] = static_cast<uint16_t*>(alloc(kv_bytes));
         vcache_[l] = static_cast<uint16_t*>(alloc(kv_bytes));
         check(hipMemsetAsync(kcache_[l], 0, kv_bytes, stream_), "memset");
         check(hipMemsetAsync(vcache_[l], 0, kv_bytes, stream_), "memset");
+        kv_bytes_[l] = kv_bytes;
     }
-    kv_bytes_ = kv_bytes;
+    if (cfg.ple_dim != 0) {
+        ple_in_ = static_cast<float*>(alloc(static_cast<size_t>(cfg.ple_dim) * cfg.layers * 4));
+        ple_g_ = static_cast<float*>(alloc(static_cast<size_t>(cfg.ple_dim) * 4));
+    }
 
     // RoPE table, built on the host exactly as build_rope does (src/model.cpp:880-894):
     // theta_scale = base^(-2/dim); theta = pos * scale, multiplied by theta_scale per pair.
@@ -519,7 +588,9 @@ Session::Session(const brisk_hip_config& cfg, const brisk_hip_tensor* tensors, s
     };
     rope_ = rope_table(cfg.rope_base, gemma() && cfg.rope_scale != 0.0f ? cfg.rope_scale : 1.0f, rd, factors, attn_factor);
     if (gemma()) {
-        if (cfg.sliding_window != 0) rope_local_ = rope_table(cfg.rope_base_local, 1.0f, hd, nullptr, 1.0f);
+        // the sliding layers' table at their own head size (Gemma 4's are narrower, src/model.cpp:875, :894)
+        if (cfg.sliding_window != 0)
+            rope_local_ = rope_table(cfg.rope_base_local, 1.0f, cfg.head_dim_local != 0 ? cfg.head_dim_local : hd, nullptr, 1.0f);
         proj_ = static_cast<float*>(alloc(e * 4));
         embd_scale_ = cfg.embedding_scale != 0.0f ? cfg.embedding_scale : std::sqrt(static_cast<float>(cfg.embd));
     }
@@ -575,7 +646,17 @@ void* Session::alloc(size_t bytes) {
 // output projection + greedy pick (which advances *pos_) or a bare advance.
 void Session::record_step(bool full) {
     check(launch_embed(embd_.p, pick_state(), h_, embd_scale_, stream_), "embed");
-    const float scale = 1.0f / std::sqrt(static_cast<float>(cfg_.head_dim));  // src/model.cpp:978
+    const int e = static_cast<int>(cfg_.embd);
+    if (cfg_.ple_dim != 0) {  // Gemma 4's per-layer embedding inputs (src/model.cpp:905-925)
+        GemvArgs pa{};
+        pa.n = 1; pa.t[0].m = ple_proj_.p; pa.t[0].out = ple_in_;
+        pa.x = h_; pa.normw = nullptr; pa.eps = cfg_.rms_epsilon; pa.add = 0;
+        check(launch_gemv(pa, stream_), "per-layer projection");
+        check(launch_ple_inputs(ple_in_, ple_tok_.p, ple_norm_, seq_, pos_, static_cast<int>(cfg_.layers), static_cast<int>(cfg_.ple_dim),
+                                1.0f / std::sqrt(static_cast<float>(cfg_.embd)), std::sqrt(static_cast<float>(cfg_.ple_dim)),
+                                cfg_.rms_epsilon, stream_),
+              "per-layer inputs");
+    }
     for (uint32_t l = 0; l < cfg_.layers; ++l) {
         const Layer& L = layers_[l];
         if (L.conv_w != nullptr) {  // LFM2 short convolution in place of attention (src/model.cpp:935-969)
@@ -623,16 +704,19 @@ void Session::record_step(bool full) {
             check(launch_gemv(so, stream_), "ssm_out");
         }
         // Q, K, V rows from attn_norm(h) (src/model.cpp:996-1015): one launch per weight format
+        const bool own_kv = L.kv_src == static_cast<int>(l);
         if (L.conv_w == nullptr && L.ssm_a == nullptr) {
+            // a shared layer (Gemma 4) projects Q only; K serving as V is projected once
             const DeviceMatrix* mats[3] = {&L.q, &L.k, &L.v};
             float* outs[3] = {qwen35() ? qg_ : q_, k_, v_};
+            const int nm = !own_kv ? 1 : L.v_is_k ? 2 : 3;
             GemvArgs qa{};
             qa.x = h_; qa.normw = L.attn_norm; qa.eps = cfg_.rms_epsilon; qa.add = 0;
             bool done[3] = {false, false, false};
-            for (int i = 0; i < 3; ++i) {
+            for (int i = 0; i < nm; ++i) {
                 if (done[i]) continue;
                 qa.n = 0;
-                for (int j = i; j < 3; ++j) {
+                for (int j = i; j < nm; ++j) {
                     if (!done[j] && mats[j]->p.type == mats[i]->p.type) {
                         qa.t[qa.n].m = mats[j]->p;
                         qa.t[qa.n].out = outs[j];
@@ -647,16 +731,20 @@ void Session::record_step(bool full) {
 
         if (L.conv_w == nullptr && L.ssm_a == nullptr) {
         AttnArgs aa{};
-        aa.q = q_; aa.k = k_; aa.v = v_; aa.qnorm = L.q_norm; aa.knorm = L.k_norm;
+        aa.q = q_; aa.k = k_; aa.v = L.v_is_k ? k_ : v_; aa.qnorm = L.q_norm; aa.knorm = L.k_norm;
         aa.rope = !L.rope ? nullptr : L.slides ? rope_local_ : rope_;
         aa.window = L.slides ? static_cast<int>(cfg_.sliding_window) : 0;
-        aa.rope_dim = L.slides ? static_cast<int>(cfg_.head_dim) : rope_dim_;
+        // the rotated width (src/model.cpp:1024): the sliding layer's head, else the rotary dimension within the head
+        aa.rope_dim = L.slides ? L.hd : std::min(rope_dim_, L.hd);
         aa.qbias = L.q_bias; aa.kbias = L.k_bias; aa.vbias = L.v_bias;
         aa.eps = cfg_.rms_epsilon; aa.neox = neox();
         aa.kcache = kcache_[l]; aa.vcache = vcache_[l]; aa.pos = pos_;
-        aa.ctx = static_cast<int>(max_ctx_); aa.head_dim = static_cast<int>(cfg_.head_dim);
-        aa.heads = static_cast<int>(cfg_.heads); aa.kv_heads = static_cast<int>(cfg_.kv_heads);
-        aa.scale = scale; aa.part_acc = part_acc_; aa.part_ml = part_ml_; aa.max_splits = max_splits_;
+        aa.ctx = static_cast<int>(max_ctx_); aa.head_dim = L.hd;
+        aa.heads = static_cast<int>(cfg_.heads); aa.kv_heads = L.kvh;
+        aa.vnorm = cfg_.value_norm; aa.no_kv = own_kv ? 0 : 1;
+        // src/model.cpp:978: the family's scale, else 1 / sqrt(the layer's head size)
+        aa.scale = cfg_.attention_scale != 0.0f ? cfg_.attention_scale : 1.0f / std::sqrt(static_cast<float>(L.hd));
+        aa.part_acc = part_acc_; aa.part_ml = part_ml_; aa.max_splits = max_splits_;
         aa.tickets = ticket_ + 4; aa.out = att_;
         // scores past the LDS limit go to the split buffers: heads x ctx floats fit them
         // (heads x max_splits x head_dim, head_dim >= the split length)
@@ -688,6 +776,21 @@ void Session::record_step(bool full) {
         da.x = act_; da.normw = L.ffn_sub_norm; da.eps = cfg_.rms_epsilon; da.add = L.ffn_post_norm ? 0 : 1;
         check(launch_gemv(da, stream_), "ffn_down");
         if (L.ffn_post_norm) check(launch_post_add(h_, proj_, L.ffn_post_norm, cfg_.rms_epsilon, static_cast<int>(cfg_.embd), stream_), "post norm");
+        if (cfg_.ple_dim != 0) {  // h = (h + norm(proj(gelu(gate h) * input l))) * scale (src/model.cpp:1163-1177)
+            GemvArgs pg{};
+            pg.n = 1; pg.t[0].m = L.ple_gate.p; pg.t[0].out = ple_g_;
+            pg.x = h_; pg.normw = nullptr; pg.eps = cfg_.rms_epsilon; pg.add = 0;
+            check(launch_gemv(pg, stream_), "per-layer gate");
+            check(launch_gelu_mul(ple_g_, ple_in_ + static_cast<size_t>(l) * cfg_.ple_dim, static_cast<int>(cfg_.ple_dim), stream_),
+                  "per-layer gelu");
+            GemvArgs pp{};
+            pp.n = 1; pp.t[0].m = L.ple_proj.p; pp.t[0].out = proj_;
+            pp.x = ple_g_; pp.normw = nullptr; pp.eps = cfg_.rms_epsilon; pp.add = 0;
+            check(launch_gemv(pp, stream_), "per-layer projection");
+            check(launch_post_add(h_, proj_, L.ple_post_norm, cfg_.rms_epsilon, e, stream_, L.out_scale), "per-layer norm");
+        } else if (L.out_scale != 1.0f) {
+            check(launch_scale(h_, L.out_scale, e, stream_), "layer scale");
+        }
         if (debug_) debug_layer(l);
     }
     if (full) {
@@ -1070,9 +1173,9 @@ bool Session::use_prefill(size_t n) const {
     const bool mfma_fits = prefill_mfma_ && pre_attn_mfma_fits(static_cast<int>(cfg_.heads / cfg_.kv_heads), static_cast<int>(cfg_.head_dim));
     // Gemma 3 (sliding layers, post-norms, GELU, soft-capped logits) and LFM2 (short convolutions)
     // take the exact attention only
+    if (qwen35()) return false;     // the recurrence takes its tokens one at a time
+    if (plain_attn_) return false;  // the batched attention holds heads of at most 128, one shape for all layers
     if (gemma() || lfm2()) return prefill_on_ && n >= 2 && exact_fits && cfg_.head_dim <= 128;
-    if (qwen35()) return false;  // the recurrence takes its tokens one at a time
-    if (plain_attn_) return false;  // the batched attention holds heads of at most 128
     return prefill_on_ && n >= 2 && (exact_fits || mfma_fits);
 }
 
@@ -1343,7 +1446,7 @@ void Session::kv_cache(int layer, int value, void** ptr, size_t* bytes) {
     if (layer < 0 || static_cast<uint32_t>(layer) >= cfg_.layers) throw Error(BRISK_HIP_EINVAL, "model: layer out of range");
     if (kcache_[layer] == nullptr) throw Error(BRISK_HIP_EINVAL, "model: layer has no key/value cache");
     *ptr = value ? static_cast<void*>(vcache_[layer]) : static_cast<void*>(kcache_[layer]);
-    *bytes = kv_bytes_;
+    *bytes = kv_bytes_[layer];
 }
 
 }  // namespace bh

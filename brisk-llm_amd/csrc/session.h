@@ -51,7 +51,14 @@ struct Layer {
     bool rope = true;               // false: the layer attends without RoPE (SmolLM3's every fourth)
     const float* attn_post_norm = nullptr;  // Gemma: norms of the attention and feed-forward outputs
     const float* ffn_post_norm = nullptr;
-    bool slides = false;            // Gemma 3: a sliding-window layer (local RoPE base)
+    bool slides = false;            // Gemma: a sliding-window layer (local RoPE base)
+    // the layer's head size, key/value heads and width (Gemma 4 varies them per layer), and the
+    // layer whose K/V cache it reads (itself, or for Gemma 4's shared layers an earlier one)
+    int hd = 0, kvh = 0, ff = 0, kv_src = 0;
+    bool v_is_k = false;            // Gemma 4: no V projection, K's raw rows serve as V
+    DeviceMatrix ple_gate, ple_proj; // Gemma 4's per-layer embedding (src/model.cpp:403-407)
+    const float* ple_post_norm = nullptr;
+    float out_scale = 1.0f;         // layer_output_scale
     DeviceMatrix conv_in, conv_out; // LFM2 short-convolution layer: in_proj (3 embd rows), out_proj
     const float* conv_w = nullptr;  // [embd][taps]; non-null marks a convolution layer
     uint16_t* conv_cache = nullptr; // bx per position, fp16 [ctx][embd]
@@ -110,9 +117,10 @@ private:
     void ensure_prefill();
     void prefill_layers(size_t pos0, int T);
     bool neox() const;
-    bool gemma() const { return cfg_.arch == BRISK_HIP_ARCH_GEMMA3; }
+    bool gemma() const { return cfg_.arch == BRISK_HIP_ARCH_GEMMA3 || cfg_.arch == BRISK_HIP_ARCH_GEMMA4; }
     bool lfm2() const { return cfg_.arch == BRISK_HIP_ARCH_LFM2; }
     bool qwen35() const { return cfg_.arch == BRISK_HIP_ARCH_QWEN35; }
+    bool gemma4() const { return cfg_.arch == BRISK_HIP_ARCH_GEMMA4; }
     void evaluated();
     void prefill_quant(const float* x, int xstride, const float* w, int cols, int T, const DeviceMatrix& consumer);
 
@@ -128,7 +136,7 @@ private:
     const float* out_norm_ = nullptr;
     std::vector<Layer> layers_;
     std::vector<uint16_t*> kcache_, vcache_;
-    size_t kv_bytes_ = 0;
+    std::vector<size_t> kv_bytes_;  // per layer (0: no cache of its own)
     float *h_ = nullptr, *q_ = nullptr, *att_ = nullptr, *act_ = nullptr, *logits_ = nullptr, *rope_ = nullptr;
     float *part_acc_ = nullptr, *part_ml_ = nullptr, *k_ = nullptr, *v_ = nullptr;
     float* rope_local_ = nullptr;  // Gemma 3 sliding layers' RoPE table
@@ -143,6 +151,10 @@ private:
     // the plain attention (launch_attention_plain): head sizes past 128, or BRISK_HIP_ATTN=plain
     bool plain_attn_ = false;
     float *plain_q_ = nullptr, *plain_sc_ = nullptr;
+    // Gemma 4's per-layer embeddings: table, projection of the embedding, its norm; the token's inputs
+    DeviceMatrix ple_tok_, ple_proj_;
+    const float* ple_norm_ = nullptr;
+    float *ple_in_ = nullptr, *ple_g_ = nullptr;
     float embd_scale_ = 1.0f;      // Gemma: sqrt(embd) (src/model.cpp:286)
     int rope_dim_ = 0;             // dimensions the RoPE table rotates (its row stride)
     unsigned long long* key_ = nullptr;

@@ -64,7 +64,8 @@ enum {
     BRISK_HIP_ARCH_GEMMA3 = 5,  /* Q/K norms, post-norms, GELU gate, sliding-window layers, scaled embeddings */
     BRISK_HIP_ARCH_PHI3 = 6,    /* fused QKV and gate/up tensors, partial rotary, LongRoPE factors */
     BRISK_HIP_ARCH_LFM2 = 7,    /* short-convolution layers (those with blk.N.shortconv.* tensors) between attention layers */
-    BRISK_HIP_ARCH_QWEN35 = 8   /* Gated DeltaNet layers (those with blk.N.ssm_a) between gated attention layers */
+    BRISK_HIP_ARCH_QWEN35 = 8,  /* Gated DeltaNet layers (those with blk.N.ssm_a) between gated attention layers */
+    BRISK_HIP_ARCH_GEMMA4 = 9   /* Gemma 3 plus per-layer embeddings, K/V sharing, wider global heads, unscaled scores */
 };
 
 /* The fields of ModelConfig (src/model.h:36-60) this path reads. */
@@ -93,6 +94,16 @@ typedef struct {
     uint32_t ssm_v_heads;    /* ssm.time_step_rank (equal to ssm_k_heads) */
     uint32_t ssm_inner;      /* ssm.inner_size = ssm_v_heads x ssm_state */
     uint32_t ssm_conv;       /* ssm.conv_kernel: the causal conv's width, 2 to 8 */
+    /* Gemma 4 (ModelConfig, src/model.h:76-118); zero / NULL elsewhere.  head_dim, kv_heads and
+     * ff hold the largest of the layers' values; the tables are read during create only: */
+    uint32_t head_dim_local;        /* the sliding layers' head size; 0: head_dim */
+    uint32_t kv_from_start;         /* layers from this one on read an earlier layer's K/V (kv_layer_of); 0: none */
+    uint32_t ple_dim;               /* the per-layer embedding width; 0: none */
+    float attention_scale;          /* the score scale; 0: 1 / sqrt(the layer's head size) */
+    int32_t value_norm;             /* 1: V is RMS-normalised, without weight, before the cache */
+    const uint8_t* sliding_pattern; /* [layers], 1 = sliding; NULL: with sliding_window, every layer but each sixth */
+    const uint32_t* ff_dims;        /* [layers] feed-forward widths; NULL: ff everywhere */
+    const uint32_t* kv_head_counts; /* [layers] key/value heads; NULL: kv_heads everywhere */
 } brisk_hip_config;
 
 /* One model tensor in GGUF layout (host memory, e.g. the file's mmap):

@@ -27,7 +27,7 @@ import pyoracle  # noqa: E402
 HERE = os.path.dirname(os.path.abspath(__file__))
 TOL = 2e-2
 FAMILIES = ["tiny-qwen3", "tiny-llama", "tiny-q8", "tiny-bitnet", "tiny-q5k", "tiny-q5", "tiny-qwen2", "tiny-smollm3",
-            "tiny-gemma3", "tiny-phi3", "tiny-llama32", "tiny-lfm2", "tiny-qwen35", "tiny-qwen35w", "tiny-qwen35h"]
+            "tiny-gemma3", "tiny-phi3", "tiny-llama32", "tiny-lfm2", "tiny-qwen35", "tiny-qwen35w", "tiny-qwen35h", "tiny-gemma4"]
 
 
 @pytest.fixture(scope="module", autouse=True)
