@@ -475,6 +475,10 @@ Session::Session(const brisk_hip_config& cfg, const brisk_hip_tensor* tensors, s
     }
     check(hipStreamSynchronize(stream_), "upload sync");
     if (staging) check(hipFree(staging), "hipFree(staging)");
+    // the per-layer tables live in the layers now; the caller's arrays are not kept
+    cfg_.sliding_pattern = nullptr;
+    cfg_.ff_dims = nullptr;
+    cfg_.kv_head_counts = nullptr;
 
     // activations and state
     h_ = static_cast<float*>(alloc(e * 4));
