@@ -176,6 +176,7 @@ class ModelSpec:
     factors: dict = field(default_factory=dict)  # RoPE factor tensors: name -> length
     conv_layers: tuple = ()                      # LFM2: layers that convolve (head_count_kv entry 0)
     recurrent_layers: tuple = ()                 # Qwen3.5: Gated DeltaNet layers (all but every interval-th)
+    no_v_layers: tuple = ()                      # Gemma 4: layers without attn_v (K serves as V)
 
     @property
     def query_dim(self):
@@ -291,7 +292,7 @@ SPECS = {
     # of layers 2 and 3; layer 3 has no V projection (K serves as V); per-layer feed-forward widths,
     # 64-wide per-layer embeddings and per-layer output scales.
     "tiny-gemma4": ModelSpec("tiny-gemma4", "gemma4", 256, 6, 4, 2, 128, 768, 1000, 1e6, context=1024,
-                             fmt=_uniform4(G.T_Q8_0), factors={"rope_freqs.weight": 64},
+                             fmt=_uniform4(G.T_Q8_0), factors={"rope_freqs.weight": 64}, no_v_layers=(3,),
                              extra={"attention.sliding_window": (G.U32, 8), "rope.freq_base_swa": (G.F32, 10000.0),
                                     "final_logit_softcapping": (G.F32, 30.0),
                                     "attention.sliding_window_pattern": (G.ARRAY, (G.BOOL, [1, 1, 1, 0, 1, 0])),
@@ -300,6 +301,35 @@ SPECS = {
                                     "embedding_length_per_layer_input": (G.U32, 64),
                                     "feed_forward_length": (G.ARRAY, (G.I32, [512, 512, 768, 768, 512, 512])),
                                     "attention.head_count_kv": (G.ARRAY, (G.U32, [2, 2, 2, 1, 2, 1]))}),
+    # Full-size shapes of the graph-path families, for bench.py's decode lines (synthetic weights):
+    # Gemma-3-1B (256-wide heads: the plain attention; 512-position windows, five of six layers),
+    # LFM2-1.2B (10 convolution layers, 6 attention layers), a Qwen3.5 shape (18 recurrent layers of
+    # 16 128-wide heads, 6 attention layers of 256-wide heads) and a Gemma 4 shape (256/512-wide
+    # heads, 15 shared K/V layers, 256-wide per-layer embeddings; its vocabulary cut to 65536 to
+    # bound the per-layer table's size).
+    "gemma3-1b": ModelSpec("gemma3-1b", "gemma3", 1152, 26, 4, 1, 256, 6912, 262144, 1e6, context=32768,
+                           fmt=_uniform4(G.T_Q4_0),
+                           extra={"attention.sliding_window": (G.U32, 512), "rope.freq_base_swa": (G.F32, 10000.0)}),
+    "lfm2-1.2b": ModelSpec("lfm2-1.2b", "lfm2", 2048, 16, 32, 8, 64, 8192, 65536, 1e6, eps=1e-5, context=32768,
+                           fmt=_uniform4(G.T_Q4_0), conv_layers=(0, 1, 3, 4, 6, 7, 9, 11, 13, 15),
+                           extra={"shortconv.l_cache": (G.U32, 3),
+                                  "attention.head_count_kv": (G.ARRAY, (G.U32, [0 if l in (0, 1, 3, 4, 6, 7, 9, 11, 13, 15)
+                                                                                else 8 for l in range(16)]))}),
+    "qwen35-0.8b": ModelSpec("qwen35-0.8b", "qwen35", 1024, 24, 8, 2, 256, 3584, 151936, 1e7, context=32768,
+                             fmt=_uniform4(G.T_Q4_0), recurrent_layers=tuple(l for l in range(24) if (l + 1) % 4),
+                             extra={"full_attention_interval": (G.U32, 4), "rope.dimension_count": (G.U32, 64),
+                                    "ssm.state_size": (G.U32, 128), "ssm.group_count": (G.U32, 16),
+                                    "ssm.time_step_rank": (G.U32, 16), "ssm.inner_size": (G.U32, 2048),
+                                    "ssm.conv_kernel": (G.U32, 4)}),
+    "gemma4-e2b": ModelSpec("gemma4-e2b", "gemma4", 1536, 35, 8, 1, 512, 6144, 65536, 1e6, context=32768,
+                            fmt=_uniform4(G.T_Q4_0), embd_fmt=G.T_Q4_0,
+                            extra={"attention.sliding_window": (G.U32, 512), "rope.freq_base_swa": (G.F32, 10000.0),
+                                   "final_logit_softcapping": (G.F32, 30.0),
+                                   "attention.sliding_window_pattern": (G.ARRAY, (G.BOOL, [0 if l % 5 == 4 else 1
+                                                                                          for l in range(35)])),
+                                   "attention.key_length_swa": (G.U32, 256),
+                                   "attention.shared_kv_layers": (G.U32, 15),
+                                   "embedding_length_per_layer_input": (G.U32, 256)}),
     "tiny-q5": ModelSpec("tiny-q5", "qwen3", 256, 2, 4, 2, 64, 512, 1000, 1e6, context=1024,
                          fmt={**_uniform4(G.T_Q5_0), "o": G.T_Q4_1, "down": G.T_Q4_1}),
 }
@@ -431,7 +461,7 @@ def write_model(spec: ModelSpec, path: str) -> str:
             _matrix(w, spec, b + "attn_q.weight", spec.heads * hd, spec.embd, spec.fmt["q"])
             if own:
                 _matrix(w, spec, b + "attn_k.weight", kvh * hd, spec.embd, spec.fmt["k"])
-                if l != 3:  # layer 3: K serves as V (src/model.cpp:386-388)
+                if l not in spec.no_v_layers:  # else K serves as V (src/model.cpp:386-388)
                     _matrix(w, spec, b + "attn_v.weight", kvh * hd, spec.embd, spec.fmt["v"])
             _vector(w, spec, b + "attn_q_norm.weight", hd)
             if own:
