@@ -407,12 +407,27 @@ __global__ __launch_bounds__(kThreads) void k_conv(const float* __restrict__ bcx
 // The state is key-major ([i][j]), so a step of i reads and writes one contiguous row
 // across the lanes; it lives in two halves by position parity, so the half a token read
 // is still the state before that token (the reference's snapshot, src/model.cpp:798-812).
+// DIM: the state size when it is 64 or 128, so the thread's state row is held in registers,
+// loaded by one batch of loads and reused by the second sum; 0: any size (256 would spill), read
+// twice from memory.
+template <int DIM>
 __global__ __launch_bounds__(kThreads) void k_ssm(SsmArgs g) {
     __shared__ float qs[kThreads], ks[kThreads];
     __shared__ float inv[2];
     __shared__ double red[4];
-    const int h = blockIdx.x, j = threadIdx.x, dim = g.dim, taps = g.taps, qkv = g.qkv_dim;
+    const int h = blockIdx.x, j = threadIdx.x, dim = DIM != 0 ? DIM : g.dim, taps = g.taps, qkv = g.qkv_dim;
     const int pos = *g.pos, k_off = g.heads * dim;
+    const size_t plane = static_cast<size_t>(dim) * dim;
+    const float* sin = g.state + (static_cast<size_t>(pos & 1) * g.heads + h) * plane + j;
+    float* sout = g.state + (static_cast<size_t>((pos + 1) & 1) * g.heads + h) * plane + j;
+    const bool fresh = pos == 0;  // the zero state of a new or restarted sequence
+    // the state row first: its loads are in flight during the conv and the norms
+    constexpr int kRow = DIM != 0 ? DIM : 1;
+    float row[kRow];
+    if (DIM != 0 && j < dim) {
+#pragma unroll
+        for (int i = 0; i < kRow; ++i) row[i] = fresh ? 0.0f : sin[static_cast<size_t>(i) * dim];
+    }
     float v = 0.0f;
     if (j < dim) {
         for (int c = 0; c < 3; ++c) {  // q, k, v channels of head h
@@ -451,23 +466,34 @@ __global__ __launch_bounds__(kThreads) void k_ssm(SsmArgs g) {
     __syncthreads();
     float o = 0.0f;
     if (j < dim) {
-        const size_t plane = static_cast<size_t>(dim) * dim;
-        const float* sin = g.state + (static_cast<size_t>(pos & 1) * g.heads + h) * plane + j;
-        float* sout = g.state + (static_cast<size_t>((pos + 1) & 1) * g.heads + h) * plane + j;
-        const bool fresh = pos == 0;  // the zero state of a new or restarted sequence
         float sk = 0.0f;
+        if (DIM != 0) {
+#pragma unroll
+            for (int i = 0; i < kRow; ++i) {
+                row[i] = row[i] * decay;
+                sk = sk + row[i] * ks[i];
+            }
+            const float d = (v - sk) * beta;
+#pragma unroll
+            for (int i = 0; i < kRow; ++i) {
+                const float si = row[i] + ks[i] * d;
+                sout[static_cast<size_t>(i) * dim] = si;
+                o = o + si * qs[i];
+            }
+        } else {
 #pragma unroll 8
-        for (int i = 0; i < dim; ++i) {
-            const float si = (fresh ? 0.0f : sin[static_cast<size_t>(i) * dim]) * decay;
-            sk = sk + si * ks[i];
-        }
-        const float d = (v - sk) * beta;
+            for (int i = 0; i < dim; ++i) {
+                const float si = (fresh ? 0.0f : sin[static_cast<size_t>(i) * dim]) * decay;
+                sk = sk + si * ks[i];
+            }
+            const float d = (v - sk) * beta;
 #pragma unroll 8
-        for (int i = 0; i < dim; ++i) {
-            float si = (fresh ? 0.0f : sin[static_cast<size_t>(i) * dim]) * decay;
-            si = si + ks[i] * d;
-            sout[static_cast<size_t>(i) * dim] = si;
-            o = o + si * qs[i];
+            for (int i = 0; i < dim; ++i) {
+                float si = (fresh ? 0.0f : sin[static_cast<size_t>(i) * dim]) * decay;
+                si = si + ks[i] * d;
+                sout[static_cast<size_t>(i) * dim] = si;
+                o = o + si * qs[i];
+            }
         }
     }
     double sq = j < dim ? static_cast<double>(o * o) : 0.0;
@@ -917,7 +943,10 @@ hipError_t launch_gelu_mul(float* g, const float* in, int n, hipStream_t s) {
 hipError_t launch_ssm(const SsmArgs& g, hipStream_t s) {
     if (g.dim < 1 || g.dim > kThreads || g.heads < 1 || g.taps < 2 || g.taps > 8 || g.qkv_dim != 3 * g.heads * g.dim)
         return hipErrorInvalidValue;
-    hipLaunchKernelGGL(k_ssm, dim3(static_cast<unsigned>(g.heads)), dim3(kThreads), 0, s, g);
+    const dim3 grid(static_cast<unsigned>(g.heads)), block(kThreads);
+    if (g.dim == 64) hipLaunchKernelGGL(k_ssm<64>, grid, block, 0, s, g);
+    else if (g.dim == 128) hipLaunchKernelGGL(k_ssm<128>, grid, block, 0, s, g);
+    else hipLaunchKernelGGL(k_ssm<0>, grid, block, 0, s, g);
     return hipGetLastError();
 }
 
