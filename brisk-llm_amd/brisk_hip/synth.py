@@ -230,6 +230,9 @@ SPECS = {
                            fmt=_uniform4(G.T_TQ2_0), embd_fmt=G.T_Q4_0, out_fmt=None),
     # Small shapes of each family for the parity tests (the oracle finishes them in well under a second).
     "tiny-qwen3": ModelSpec("tiny-qwen3", "qwen3", 256, 2, 4, 2, 64, 512, 1000, 1e6, context=1024, fmt=_uniform4(G.T_Q4_0)),
+    # tiny-qwen3's shape with a 16384-position context, for long pre-filled caches
+    "tiny-qwen3-long": ModelSpec("tiny-qwen3-long", "qwen3", 256, 2, 4, 2, 64, 512, 1000, 1e6, context=16384,
+                                 fmt=_uniform4(G.T_Q4_0)),
     "tiny-llama": ModelSpec("tiny-llama", "llama", 512, 2, 8, 2, 64, 768, 1000, 5e5, eps=1e-5, context=1024,
                             fmt={**_uniform4(G.T_Q4_K), "v": G.T_Q6_K, "down": G.T_Q6_K}, embd_fmt=G.T_Q6_K, out_fmt=None),
     "tiny-q8": ModelSpec("tiny-q8", "qwen3", 256, 2, 4, 2, 64, 512, 1000, 1e6, context=1024, fmt=_uniform4(G.T_Q8_0)),

@@ -533,132 +533,134 @@ __global__ void k_log1pf(const float* __restrict__ x, float* __restrict__ y, siz
 // ---------------------------------------------------------------- plain attention
 //
 // The reference's attention for one token (src/model.cpp:1019-1093 with the portable
-// kernels of src/kernels_f32.cpp:229-284) in four kernels, for head sizes the LDS-resident
+// kernels of src/kernels_f32.cpp:229-284) in three kernels, for head sizes the LDS-resident
 // attention does not take (up to 512) and for layers that read another layer's cache:
-//   prologue (a workgroup per key/value head): q heads and k bias, RMS norm and RoPE, v
-//            bias (and Gemma 4's weightless V norm), the fp16 K/V rows at pos;
-//   scores   (a lane per position): dot_f32(q, k_p) * scale, 16 lane partials over
-//            i = j (mod 16) in order, then 0 + lane 0 + ... + lane 15;
-//   softmax  (a workgroup per head): max, e_p = expf(s_p - max), their sum in double,
-//            w_p = e_p * (float)(1 / sum);
-//   values   (a lane per output dimension): 0 + w_0 v_0 + w_1 v_1 + ... in position order.
+//   prologue (a wave per query head and per key/value head): bias, RMS norm and RoPE of each
+//            query head into qn; of each key head, V's bias (and Gemma 4's weightless V norm),
+//            and the fp16 K/V rows at pos;
+//   scores   (a workgroup per query head and 64 positions, a lane per position):
+//            dot_f32(q, k_p) * scale, 16 lane partials over i = j (mod 16) in order, then
+//            0 + lane 0 + ... + lane 15;
+//   values   (a wave per head and 64 output dimensions): the head's softmax (max,
+//            e_p = expf(s_p - max), their sum in double, w_p = e_p * (float)(1 / sum)), then
+//            for each output dimension 0 + w_0 v_0 + w_1 v_1 + ... in position order.
 // A sliding layer's token sees positions [L - window, L) (src/model.cpp:1084-1085).
 
 __device__ __forceinline__ int plain_start(const AttnArgs& g, int L) { return g.window > 0 && L > g.window ? L - g.window : 0; }
 
-__global__ __launch_bounds__(kThreads) void k_plain_prologue(AttnArgs g) {
-    __shared__ float qs[16 * kPlainMaxHead], kc[kPlainMaxHead], vc[kPlainMaxHead];
-    __shared__ double red[4];
-    const int kv = blockIdx.x, hd = g.head_dim, hpk = g.heads / g.kv_heads, t = threadIdx.x, pos = *g.pos;
-    const bool own = g.no_kv == 0;
-    for (int i = t; i < hpk * hd; i += kThreads) qs[i] = g.q[kv * hpk * hd + i];
-    if (own)
-        for (int i = t; i < hd; i += kThreads) {
-            kc[i] = g.k[kv * hd + i];
-            vc[i] = g.vbias != nullptr ? g.v[kv * hd + i] + g.vbias[kv * hd + i] : g.v[kv * hd + i];
-        }
-    __syncthreads();
+// One wave a head: wave h < heads forms query head h (bias, norm, RoPE) into qn; wave heads + kv
+// forms key/value head kv (bias, norm, RoPE; V's bias and weightless norm) and stores its fp16 rows.
+// A query head's raw rows are q[h * q_stride ..] (q_stride 2 * head_dim: Qwen3.5's query|gate rows).
+__global__ __launch_bounds__(64) void k_plain_prologue(AttnArgs g) {
+    __shared__ float a[kPlainMaxHead], b[kPlainMaxHead];
+    const int hd = g.head_dim, lane = threadIdx.x, pos = *g.pos;
+    const int qs = g.q_stride != 0 ? g.q_stride : hd;
     const float* rope = g.rope != nullptr ? g.rope + static_cast<size_t>(pos) * g.rope_dim : nullptr;
-    for (int h = t >> 6; h < hpk + (own ? 1 : 0); h += kThreads / 64) {
-        if (h < hpk) head_norm_rope(qs + h * hd, g.qbias != nullptr ? g.qbias + (kv * hpk + h) * hd : nullptr, g.qnorm, rope, hd, g.rope_dim, g.neox, g.eps);
-        else head_norm_rope(kc, g.kbias != nullptr ? g.kbias + kv * hd : nullptr, g.knorm, rope, hd, g.rope_dim, g.neox, g.eps);
+    const int w = blockIdx.x;
+    if (w < g.heads) {
+        for (int i = lane; i < hd; i += 64) a[i] = g.q[static_cast<size_t>(w) * qs + i];
+        head_norm_rope(a, g.qbias != nullptr ? g.qbias + w * hd : nullptr, g.qnorm, rope, hd, g.rope_dim, g.neox, g.eps);
+        for (int i = lane; i < hd; i += 64) g.qn[w * hd + i] = a[i];
+        return;
     }
-    if (own && g.vnorm) {  // rms_norm(v) with no weight (src/model.cpp:1041)
+    const int kv = w - g.heads;
+    for (int i = lane; i < hd; i += 64) {
+        a[i] = g.k[kv * hd + i];
+        b[i] = g.vbias != nullptr ? g.v[kv * hd + i] + g.vbias[kv * hd + i] : g.v[kv * hd + i];
+    }
+    head_norm_rope(a, g.kbias != nullptr ? g.kbias + kv * hd : nullptr, g.knorm, rope, hd, g.rope_dim, g.neox, g.eps);
+    if (g.vnorm) {  // rms_norm(v) with no weight (src/model.cpp:1041)
         double sq = 0.0;
-        for (int i = t; i < hd; i += kThreads) sq += static_cast<double>(vc[i] * vc[i]);
-        sq = wave_sum(sq);
-        if ((t & 63) == 0) red[t >> 6] = sq;
-        __syncthreads();
-        const float scale = rms_scale(((red[0] + red[1]) + red[2]) + red[3], hd, g.eps);
-        __syncthreads();
-        for (int i = t; i < hd; i += kThreads) vc[i] = vc[i] * scale;
+        for (int i = lane; i < hd; i += 64) sq += static_cast<double>(b[i] * b[i]);
+        const float scale = rms_scale(wave_sum(sq), hd, g.eps);
+        for (int i = lane; i < hd; i += 64) b[i] = b[i] * scale;
     }
-    __syncthreads();
-    for (int i = t; i < hpk * hd; i += kThreads) g.qn[kv * hpk * hd + i] = qs[i];
-    if (own) {
-        uint16_t* kr = g.kcache + (static_cast<size_t>(kv) * g.ctx + pos) * hd;
-        uint16_t* vr = g.vcache + (static_cast<size_t>(kv) * g.ctx + pos) * hd;
-        for (int i = t; i < hd; i += kThreads) {
-            kr[i] = f2h(kc[i]);
-            vr[i] = f2h(vc[i]);
-        }
+    uint16_t* kr = g.kcache + (static_cast<size_t>(kv) * g.ctx + pos) * hd;
+    uint16_t* vr = g.vcache + (static_cast<size_t>(kv) * g.ctx + pos) * hd;
+    for (int i = lane; i < hd; i += 64) {
+        kr[i] = f2h(a[i]);
+        vr[i] = f2h(b[i]);
     }
 }
 
-__global__ __launch_bounds__(kThreads) void k_plain_scores(AttnArgs g) {
-    __shared__ float qs[16 * kPlainMaxHead];
-    const int kv = blockIdx.x, hd = g.head_dim, hpk = g.heads / g.kv_heads, t = threadIdx.x;
+// A workgroup per (query head, 64 positions), a lane per position.
+__global__ __launch_bounds__(64) void k_plain_scores(AttnArgs g) {
+    __shared__ float q[kPlainMaxHead];
+    const int h = blockIdx.x, hd = g.head_dim, hpk = g.heads / g.kv_heads, kv = h / hpk, lane = threadIdx.x;
     const int L = *g.pos + 1, start = plain_start(g, L);
-    if (start + static_cast<int>(blockIdx.y) * kThreads >= L) return;  // the grid covers the longest context
-    for (int i = t; i < hpk * hd; i += kThreads) qs[i] = g.qn[kv * hpk * hd + i];
+    const int p0 = start + static_cast<int>(blockIdx.y) * 64;
+    if (p0 >= L) return;  // the grid covers the longest context
+    for (int i = lane; i < hd; i += 64) q[i] = g.qn[h * hd + i];
     __syncthreads();
-    const int p = start + static_cast<int>(blockIdx.y) * kThreads + t;
+    const int p = p0 + lane;
     if (p >= L) return;
     const uint16_t* kr = g.kcache + (static_cast<size_t>(kv) * g.ctx + p) * hd;
-    for (int gq = 0; gq < hpk; ++gq) {
-        const float* q = qs + gq * hd;
-        float lane[16];
+    float acc[16];
 #pragma unroll
-        for (int j = 0; j < 16; ++j) lane[j] = 0.0f;
-        for (int b = 0; b < hd; b += 16) {
-            const uint4 k0 = *reinterpret_cast<const uint4*>(kr + b), k1 = *reinterpret_cast<const uint4*>(kr + b + 8);
-            const uint32_t kw[8] = {k0.x, k0.y, k0.z, k0.w, k1.x, k1.y, k1.z, k1.w};
+    for (int j = 0; j < 16; ++j) acc[j] = 0.0f;
+    for (int b0 = 0; b0 < hd; b0 += 128) {  // eight 16-wide blocks' loads issued together
+        uint4 kk[16];
+#pragma unroll
+        for (int u = 0; u < 16; ++u) kk[u] = b0 + 8 * u < hd ? *reinterpret_cast<const uint4*>(kr + b0 + 8 * u) : make_uint4(0, 0, 0, 0);
+#pragma unroll
+        for (int blk = 0; blk < 8; ++blk) {
+            if (b0 + 16 * blk >= hd) break;
+            const uint32_t kw[8] = {kk[2 * blk].x, kk[2 * blk].y, kk[2 * blk].z, kk[2 * blk].w,
+                                    kk[2 * blk + 1].x, kk[2 * blk + 1].y, kk[2 * blk + 1].z, kk[2 * blk + 1].w};
 #pragma unroll
             for (int j = 0; j < 16; ++j) {
-                const uint16_t h = static_cast<uint16_t>((j & 1) ? (kw[j >> 1] >> 16) : (kw[j >> 1] & 0xFFFF));
-                lane[j] += q[b + j] * h2f(h);
+                const uint16_t hv = static_cast<uint16_t>((j & 1) ? (kw[j >> 1] >> 16) : (kw[j >> 1] & 0xFFFF));
+                acc[j] += q[b0 + 16 * blk + j] * h2f(hv);
             }
         }
-        float sum = 0.0f;
-#pragma unroll
-        for (int j = 0; j < 16; ++j) sum += lane[j];
-        g.gsc[static_cast<size_t>(kv * hpk + gq) * g.ctx + p] = sum * g.scale;
     }
+    float sum = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 16; ++j) sum += acc[j];
+    g.gsc[static_cast<size_t>(h) * g.ctx + p] = sum * g.scale;
 }
 
-__global__ __launch_bounds__(kThreads) void k_plain_softmax(AttnArgs g) {
-    __shared__ float mred[4];
-    __shared__ double red[4];
-    const int h = blockIdx.x, t = threadIdx.x, L = *g.pos + 1, start = plain_start(g, L);
-    float* sc = g.gsc + static_cast<size_t>(h) * g.ctx;
+// A wave per (head, 64 output dimensions): the head's softmax (each wave of the head computes the
+// same weights: max, e_p = expf(s_p - max), their double sum, e_p * (float)(1 / sum)), held in LDS
+// when the window fits it and recomputed per position otherwise; then a lane per output dimension
+// sums w_p v_p[d] in position order, its loads issued 32 positions at a time.  Qwen3.5's sigmoid
+// gate (src/model.cpp:1102-1108) is applied to the sums.
+constexpr int kPlainLdsW = 8192;
+__global__ __launch_bounds__(64) void k_plain_values(AttnArgs g) {
+    __shared__ float wl[kPlainLdsW];
+    const int h = blockIdx.x, hd = g.head_dim, hpk = g.heads / g.kv_heads, kv = h / hpk, lane = threadIdx.x;
+    const int L = *g.pos + 1, start = plain_start(g, L), n = L - start;
+    const float* sc = g.gsc + static_cast<size_t>(h) * g.ctx + start;
     float m = -INFINITY;
-    for (int p = start + t; p < L; p += kThreads) m = fmaxf(m, sc[p]);
+    for (int p = lane; p < n; p += 64) m = fmaxf(m, sc[p]);
     m = wave_max(m);
-    if ((t & 63) == 0) mred[t >> 6] = m;
-    __syncthreads();
-    m = fmaxf(fmaxf(mred[0], mred[1]), fmaxf(mred[2], mred[3]));
+    const bool in_lds = n <= kPlainLdsW;
     double part = 0.0;
-    for (int p = start + t; p < L; p += kThreads) {
+    for (int p = lane; p < n; p += 64) {
         const float e = ref_expf(sc[p] - m);
-        sc[p] = e;
+        if (in_lds) wl[p] = e;
         part += static_cast<double>(e);
     }
-    part = wave_sum(part);
-    if ((t & 63) == 0) red[t >> 6] = part;
+    const float scale = static_cast<float>(1.0 / wave_sum(part));
+    if (in_lds)
+        for (int p = lane; p < n; p += 64) wl[p] = wl[p] * scale;
     __syncthreads();
-    const float scale = static_cast<float>(1.0 / (((red[0] + red[1]) + red[2]) + red[3]));
-    for (int p = start + t; p < L; p += kThreads) sc[p] *= scale;
-}
-
-__global__ __launch_bounds__(kThreads) void k_plain_values(AttnArgs g) {
-    const int h = blockIdx.x, hd = g.head_dim, hpk = g.heads / g.kv_heads, kv = h / hpk;
-    const int d = static_cast<int>(blockIdx.y) * kThreads + threadIdx.x, L = *g.pos + 1, start = plain_start(g, L);
+    const int d = static_cast<int>(blockIdx.y) * 64 + lane;
     if (d >= hd) return;
-    const float* w = g.gsc + static_cast<size_t>(h) * g.ctx;
-    const uint16_t* vv = g.vcache + static_cast<size_t>(kv) * g.ctx * hd + d;
+    const uint16_t* vv = g.vcache + static_cast<size_t>(kv) * g.ctx * hd + static_cast<size_t>(start) * hd + d;
+    auto weight = [&](int p) { return in_lds ? wl[p] : ref_expf(sc[p] - m) * scale; };
+    constexpr int kB = 32;
     float a = 0.0f;
-    int p = start;
-    for (; p + 8 <= L; p += 8) {  // loads first, then the adds in position order
-        float wv[8], vf[8];
+    int p = 0;
+    for (; p + kB <= n; p += kB) {  // loads first, then the adds in position order
+        float vf[kB];
 #pragma unroll
-        for (int u = 0; u < 8; ++u) {
-            wv[u] = w[p + u];
-            vf[u] = h2f(vv[static_cast<size_t>(p + u) * hd]);
-        }
+        for (int u = 0; u < kB; ++u) vf[u] = h2f(vv[static_cast<size_t>(p + u) * hd]);
 #pragma unroll
-        for (int u = 0; u < 8; ++u) a += wv[u] * vf[u];
+        for (int u = 0; u < kB; ++u) a += weight(p + u) * vf[u];
     }
-    for (; p < L; ++p) a += w[p] * h2f(vv[static_cast<size_t>(p) * hd]);
+    for (; p < n; ++p) a += weight(p) * h2f(vv[static_cast<size_t>(p) * hd]);
+    if (g.gate != nullptr) a = a * (1.0f / (1.0f + ref_expf(-g.gate[static_cast<size_t>(h) * g.gate_stride + d])));
     g.out[h * hd + d] = a;
 }
 
@@ -906,12 +908,11 @@ hipError_t launch_attention_plain(const AttnArgs& g, hipStream_t s) {
     if (g.head_dim < 16 || g.head_dim > kPlainMaxHead || g.head_dim % 16 != 0 || hpk < 1 || hpk > 16 ||
         hpk * g.kv_heads != g.heads || g.qn == nullptr || g.gsc == nullptr)
         return hipErrorInvalidValue;
-    const unsigned pos_blocks = static_cast<unsigned>((g.ctx + kThreads - 1) / kThreads);  // the most any position needs
-    hipLaunchKernelGGL(k_plain_prologue, dim3(g.kv_heads), dim3(kThreads), 0, s, g);
-    hipLaunchKernelGGL(k_plain_scores, dim3(g.kv_heads, pos_blocks), dim3(kThreads), 0, s, g);
-    hipLaunchKernelGGL(k_plain_softmax, dim3(g.heads), dim3(kThreads), 0, s, g);
-    hipLaunchKernelGGL(k_plain_values, dim3(g.heads, static_cast<unsigned>((g.head_dim + kThreads - 1) / kThreads)), dim3(kThreads),
-                       0, s, g);
+    const unsigned pos_blocks = static_cast<unsigned>((g.ctx + 63) / 64);  // the most any position needs
+    hipLaunchKernelGGL(k_plain_prologue, dim3(static_cast<unsigned>(g.heads + (g.no_kv ? 0 : g.kv_heads))), dim3(64), 0, s, g);
+    hipLaunchKernelGGL(k_plain_scores, dim3(static_cast<unsigned>(g.heads), pos_blocks), dim3(64), 0, s, g);
+    hipLaunchKernelGGL(k_plain_values, dim3(static_cast<unsigned>(g.heads), static_cast<unsigned>(g.head_dim / 64 + (g.head_dim % 64 != 0))),
+                       dim3(64), 0, s, g);
     return hipGetLastError();
 }
 

@@ -71,6 +71,9 @@ struct AttnArgs {
     float* qn;            // [heads][head_dim]: the normed and rotated queries
     int vnorm;            // V RMS-normalised without weight before the cache (Gemma 4)
     int no_kv;            // the layer reads another layer's cache and stores no rows (Gemma 4's shared K/V)
+    int q_stride;         // floats from one query head's raw rows to the next (0: head_dim)
+    const float* gate;    // the output times sigmoid(gate[h * gate_stride + d]) (Qwen3.5), or null
+    int gate_stride;
     unsigned long long* stamps;  // optional profiling: key/value head 0's wall clock at sub-phase ends
 };
 
@@ -119,7 +122,7 @@ hipError_t launch_matvec_q8(const Packed& m, const void* xq, size_t n, float* ou
 hipError_t launch_gemv(GemvArgs g, hipStream_t s);
 hipError_t launch_gateup(GateUpArgs g, hipStream_t s);
 hipError_t launch_attention(const AttnArgs& g, hipStream_t s);
-// The reference's attention for one token by four plain kernels (prologue, scores, softmax,
+// The reference's attention for one token by three plain kernels (prologue, scores, softmax with
 // values), for any head size up to 512 (a multiple of 16): scores and weights in gsc
 // ([heads][ctx]), the queries in qn.
 hipError_t launch_attention_plain(const AttnArgs& g, hipStream_t s);

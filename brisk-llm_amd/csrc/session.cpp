@@ -730,7 +730,9 @@ void Session::record_step(bool full) {
                 }
                 check(launch_gemv(qa, stream_), "qkv");
             }
-            if (qwen35()) check(launch_qgate_split(qg_, q_, agate_, static_cast<int>(cfg_.heads), static_cast<int>(cfg_.head_dim), stream_), "query gate");
+            // Qwen3.5: the plain attention reads the query and gate rows in place; the others take them split
+            if (qwen35() && !plain_attn_)
+                check(launch_qgate_split(qg_, q_, agate_, static_cast<int>(cfg_.heads), static_cast<int>(cfg_.head_dim), stream_), "query gate");
         }
 
         if (L.conv_w == nullptr && L.ssm_a == nullptr) {
@@ -756,11 +758,17 @@ void Session::record_step(bool full) {
         if (plain_attn_) {
             aa.gsc = plain_sc_;
             aa.qn = plain_q_;
+            if (qwen35()) {  // each head's query rows, then its gate rows (src/model.cpp:1002-1012)
+                aa.q = qg_;
+                aa.q_stride = 2 * L.hd;
+                aa.gate = qg_ + L.hd;
+                aa.gate_stride = 2 * L.hd;
+            }
             check(launch_attention_plain(aa, stream_), "attention");
         } else {
             check(launch_attention(aa, stream_), "attention");
+            if (qwen35()) check(launch_sigmoid_gate(att_, agate_, static_cast<int>(cfg_.heads * cfg_.head_dim), stream_), "attention gate");
         }
-        if (qwen35()) check(launch_sigmoid_gate(att_, agate_, static_cast<int>(cfg_.heads * cfg_.head_dim), stream_), "attention gate");
 
         // h += W_o att, or with a post-norm h += rms_norm(W_o att) (src/model.cpp:1113-1121)
         GemvArgs oa{};

@@ -68,6 +68,29 @@ def test_long_attention_tiny(name, n_pos, steps):
         o.close()
 
 
+@pytest.mark.parametrize("n_pos", [300, 9000])
+def test_long_plain_attention(n_pos):
+    """The plain attention (BRISK_HIP_ATTN=plain) at 300 positions (weights in LDS) and at 9000 (past its
+    8192-position LDS window: the weights recomputed per position), bit-identical to the oracle."""
+    import os
+    f, cfg, table = model.load(synth.model_path("tiny-qwen3-long"))
+    print(f"[long] tiny-qwen3-long plain attention: KV pre-filled to {n_pos}", flush=True)
+    os.environ["BRISK_HIP_ATTN"] = "plain"
+    try:
+        s = HipSession((f, cfg, table), max_context=n_pos + 16)
+    finally:
+        del os.environ["BRISK_HIP_ATTN"]
+    with s:
+        o = pyoracle.Oracle(cfg, table, n_pos + 16)
+        prefill_kv(s, o, cfg, n_pos, seed=9)
+        got, want = s.eval([23]), o.eval([23])
+        np.testing.assert_array_equal(got.view(np.uint32), want.view(np.uint32))
+        ids = s.generate([int(np.argmax(got))], 4)
+        o_ids, gaps = o.generate([int(np.argmax(want))], 4)
+        np.testing.assert_array_equal(ids, o_ids, err_msg=f"gaps {gaps}")
+        o.close()
+
+
 @pytest.mark.slow
 def test_qwen3_1_7b_at_4096():
     """configs[3] at full size: Qwen3-1.7B-shape Q8_0, 4096 pre-filled positions, then decode."""
