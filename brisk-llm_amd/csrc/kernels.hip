@@ -181,7 +181,8 @@ __global__ __launch_bounds__(kThreads) void k_gemv(GemvArgs g) {
     tile.sums(tg.m, a, terms, sums);
     const uint32_t r = threadIdx.x, row = tile.row0 + r;
     if (r < static_cast<uint32_t>(tg.R) && row < tg.m.rows) {
-        if (g.add) tg.out[row] += sums[r];
+        if (g.gelu_in != nullptr) tg.out[row] = gelu_mul(sums[r], g.gelu_in[row]);
+        else if (g.add) tg.out[row] += sums[r];
         else tg.out[row] = sums[r];
     }
 }
@@ -368,11 +369,6 @@ __global__ __launch_bounds__(kThreads) void k_ple_inputs(float* __restrict__ in,
     }
 }
 
-// g = gelu(g) * in (gelu_mul_f32, src/kernels_f32.cpp:291-296).
-__global__ void k_gelu_mul(float* __restrict__ g, const float* __restrict__ in, int n) {
-    const int i = blockIdx.x * blockDim.x + threadIdx.x;
-    if (i < n) g[i] = gelu_mul(g[i], in[i]);
-}
 
 // LFM2 short convolution (src/model.cpp:935-969): bx = b * x, kept per position as
 // fp16 (store_f16); out = c * sum over the last `taps` positions, oldest first, of
@@ -873,6 +869,7 @@ hipError_t launch_matvec_q8(const Packed& m, const void* xq, size_t n, float* ou
 }
 
 hipError_t launch_gemv(GemvArgs g, hipStream_t s) {
+    if (g.gelu_in != nullptr && (g.n != 1 || g.add)) return hipErrorInvalidValue;
     unsigned tiles = 0;
     for (int i = 0; i < g.n; ++i) {
         if (g.t[i].m.type != g.t[0].m.type) return hipErrorInvalidValue;
@@ -933,11 +930,6 @@ hipError_t launch_ple_inputs(float* in, const Packed& table, const float* norm, 
     if (layers < 1 || dim < 1 || static_cast<size_t>(layers) * dim != table.cols) return hipErrorInvalidValue;
     hipLaunchKernelGGL(k_ple_inputs, dim3(static_cast<unsigned>(layers)), dim3(kThreads), 0, s, in, table, norm, seq, pos, dim,
                        proj_scale, table_scale, eps);
-    return hipGetLastError();
-}
-
-hipError_t launch_gelu_mul(float* g, const float* in, int n, hipStream_t s) {
-    hipLaunchKernelGGL(k_gelu_mul, dim3(static_cast<unsigned>((n + kThreads - 1) / kThreads)), dim3(kThreads), 0, s, g, in, n);
     return hipGetLastError();
 }
 

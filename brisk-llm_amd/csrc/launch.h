@@ -27,6 +27,7 @@ struct GemvArgs {
     const float* normw;   // rms_norm weight applied to x first, or null
     float eps;
     int add;              // 1: out += W x (residual), 0: out = W x
+    const float* gelu_in; // non-null: out[r] = gelu(W x)[r] * gelu_in[r] (gelu_mul_f32; Gemma 4's per-layer gate)
 };
 
 struct GateUpArgs {
@@ -138,8 +139,6 @@ hipError_t launch_scale(float* h, float out_scale, int n, hipStream_t s);
 // (rms_norm(slice * proj_scale, norm) + table[tok][l * dim ..] * table_scale) * 0.70710678.
 hipError_t launch_ple_inputs(float* in, const Packed& table, const float* norm, const int* seq, const int* pos, int layers,
                              int dim, float proj_scale, float table_scale, float eps, hipStream_t s);
-// g = gelu(g) * in over n values (gelu_mul_f32, src/kernels_f32.cpp:291-296).
-hipError_t launch_gelu_mul(float* g, const float* in, int n, hipStream_t s);
 hipError_t launch_finalize(const PickState& ps, hipStream_t s);
 hipError_t launch_head(HeadArgs g, hipStream_t s);
 hipError_t launch_advance(int* pos, hipStream_t s);

@@ -789,12 +789,11 @@ void Session::record_step(bool full) {
         check(launch_gemv(da, stream_), "ffn_down");
         if (L.ffn_post_norm) check(launch_post_add(h_, proj_, L.ffn_post_norm, cfg_.rms_epsilon, static_cast<int>(cfg_.embd), stream_), "post norm");
         if (cfg_.ple_dim != 0) {  // h = (h + norm(proj(gelu(gate h) * input l))) * scale (src/model.cpp:1163-1177)
-            GemvArgs pg{};
+            GemvArgs pg{};  // gelu(gate h) * input l, in the GEMV's epilogue
             pg.n = 1; pg.t[0].m = L.ple_gate.p; pg.t[0].out = ple_g_;
             pg.x = h_; pg.normw = nullptr; pg.eps = cfg_.rms_epsilon; pg.add = 0;
+            pg.gelu_in = ple_in_ + static_cast<size_t>(l) * cfg_.ple_dim;
             check(launch_gemv(pg, stream_), "per-layer gate");
-            check(launch_gelu_mul(ple_g_, ple_in_ + static_cast<size_t>(l) * cfg_.ple_dim, static_cast<int>(cfg_.ple_dim), stream_),
-                  "per-layer gelu");
             GemvArgs pp{};
             pp.n = 1; pp.t[0].m = L.ple_proj.p; pp.t[0].out = proj_;
             pp.x = ple_g_; pp.normw = nullptr; pp.eps = cfg_.rms_epsilon; pp.add = 0;
