@@ -225,8 +225,9 @@ FAMILY_SHAPES = (
 
 
 def families(torch, HipSession, model, synth):
-    """Decode tok/s of each graph-path family: a 32-id prompt, then 128 greedy steps.  hbm_frac counts the
+    """Decode tok/s of each graph-path family: a 32-id prompt, then 128 greedy steps; and a 512-id prompt.  hbm_frac counts the
     bytes of the weight matrices a token reads (each layer's, the output's, one embedding row) at HBM peak."""
+    import numpy as np
     out = {}
     for name, desc in FAMILY_SHAPES:
         f, cfg, table = model.load(synth.model_path(name))
@@ -248,6 +249,23 @@ def families(torch, HipSession, model, synth):
                      "value": round(128 / dt, 2), "unit": "tok/s", "weight_bytes_per_token": int(wbytes),
                      "hbm_frac": round(wbytes * 128 / dt / HBM_PEAK, 4)}
         log(f"{name} decode: {128 / dt:.1f} tok/s")
+        s.close()
+        del s
+        # a 512-id prompt (eval, last-token logits; median of 3): batched where the family has a
+        # prefill (LFM2, Gemma 3, Qwen3.5), token by token otherwise (Gemma 4)
+        lp = synth.prompt_ids(512, cfg.vocab, seed=11)
+        s = HipSession((f, cfg, table), max_context=512 + 16)
+        s.eval(lp[:64], logits=False)  # warm-up
+        times = []
+        for _ in range(3):
+            s.rollback(0)
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            s.eval(lp, logits=True)
+            times.append(time.perf_counter() - t0)
+        dtp = float(np.median(times))
+        out[name]["prompt_512_tok_s"] = round(512 / dtp, 1)
+        log(f"{name} 512-id prompt: {dtp * 1e3:.1f} ms -> {512 / dtp:.0f} tok/s")
         s.close()
         del s
         torch.cuda.empty_cache()

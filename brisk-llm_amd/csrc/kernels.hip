@@ -403,27 +403,212 @@ __global__ __launch_bounds__(kThreads) void k_conv(const float* __restrict__ bcx
 // The state is key-major ([i][j]), so a step of i reads and writes one contiguous row
 // across the lanes; it lives in two halves by position parity, so the half a token read
 // is still the state before that token (the reference's snapshot, src/model.cpp:798-812).
-// DIM: the state size when it is 64 or 128, so the thread's state row is held in registers,
-// loaded by one batch of loads and reused by the second sum; 0: any size (256 would spill), read
-// twice from memory.
+
+// The LDS of one recurrence workgroup.
+struct SsmLds {
+    float qs[kThreads], ks[kThreads];
+    float inv[2];
+    double red[4];
+};
+
+// A thread's conv state for its q, k and v channels, held in registers and right-aligned in
+// fixed slots (every index a constant): the taps' weights at w[c][8 - taps ..], oldest first (the
+// newest, for the token's own rows, at slot 7), and the last taps - 1 inputs at win[c][8 - taps ..],
+// oldest first (zero before position 0).
+constexpr int kSsmMaxTaps = 8;
+struct SsmConv {
+    float w[3][kSsmMaxTaps];
+    float win[3][kSsmMaxTaps - 1];
+};
+
+// The conv state of thread j (a channel of head h) before the token at pos, from the weights and
+// the ring (slot p % taps holds position p's rows).
+template <int DIM>
+__device__ __forceinline__ void ssm_conv_load(const SsmArgs& g, int h, int pos, SsmConv& cv) {
+    const int j = threadIdx.x, taps = g.taps;
+    if (j >= DIM) return;
+#pragma unroll
+    for (int c = 0; c < 3; ++c) {
+        const int ch = c * g.heads * DIM + h * DIM + j;
+#pragma unroll
+        for (int k = 0; k < kSsmMaxTaps; ++k) {
+            const int i = k - (kSsmMaxTaps - taps);  // the tap in slot k
+            cv.w[c][k] = i >= 0 ? g.conv_w[static_cast<size_t>(ch) * taps + i] : 0.0f;
+        }
+#pragma unroll
+        for (int k = 0; k < kSsmMaxTaps - 1; ++k) {
+            const int i = k - (kSsmMaxTaps - taps), p = pos - (taps - 1) + i;  // input i, at position p
+            cv.win[c][k] = i >= 0 && p >= 0 ? g.ring[static_cast<size_t>(p % taps) * g.qkv_dim + ch] : 0.0f;
+        }
+    }
+}
+
+// One token of head h (a step of Session::forward_recurrent) whose attn_qkv rows for thread j's
+// channels are cur[] and gate row z: the conv over the window and cur (which then joins the
+// window), the norms, the delta update of the thread's state row (row[], in place) and the gated
+// norm; returns the output of channel j (0 for threads j >= DIM).  Every thread of the workgroup
+// calls it (it holds barriers).
+template <int DIM>
+__device__ __forceinline__ float ssm_step(const SsmArgs& g, SsmLds& s, int h, const float (&cur)[3], SsmConv& cv, float z,
+                                          float alpha_in, float beta_in, float (&row)[DIM]) {
+    const int j = threadIdx.x, taps = g.taps;
+    float v = 0.0f;
+    if (j < DIM) {
+#pragma unroll
+        for (int c = 0; c < 3; ++c) {  // q, k, v channels of head h
+            float acc = 0.0f;  // the taps in order, oldest first (the slots before the first tap skipped)
+#pragma unroll
+            for (int k = 0; k < kSsmMaxTaps - 1; ++k)
+                if (k >= kSsmMaxTaps - taps) acc = acc + cv.w[c][k] * cv.win[c][k];
+            acc = acc + cv.w[c][kSsmMaxTaps - 1] * cur[c];
+#pragma unroll
+            for (int k = 0; k < kSsmMaxTaps - 2; ++k) cv.win[c][k] = cv.win[c][k + 1];  // the window moves on
+            cv.win[c][kSsmMaxTaps - 2] = cur[c];
+            const float x = acc / (1.0f + ref_expf(-acc));
+            if (c == 0) s.qs[j] = x;
+            else if (c == 1) s.ks[j] = x;
+            else v = x;
+        }
+    }
+    __syncthreads();
+    if (j == 0 || j == 64) {  // the two L2 sums, one lane of two waves
+        const float* src = j == 0 ? s.qs : s.ks;
+        float sum = 0.0f;
+        for (int i = 0; i < DIM; ++i) sum += src[i] * src[i];
+        s.inv[j == 0 ? 0 : 1] = (j == 0 ? g.q_scale : 1.0f) / sqrtf(sum + g.eps);
+    }
+    __syncthreads();
+    if (j < DIM) {
+        s.qs[j] = s.qs[j] * s.inv[0];
+        s.ks[j] = s.ks[j] * s.inv[1];
+    }
+    const float alpha = alpha_in + g.dt[h];
+    const float softplus = alpha > 20.0f ? alpha : ref_log1pf(ref_expf(alpha));
+    const float decay = ref_expf(softplus * g.a[h]);
+    const float beta = 1.0f / (1.0f + ref_expf(-beta_in));
+    __syncthreads();
+    float o = 0.0f;
+    if (j < DIM) {
+        float sk = 0.0f;
+#pragma unroll
+        for (int i = 0; i < DIM; ++i) {
+            row[i] = row[i] * decay;
+            sk = sk + row[i] * s.ks[i];
+        }
+        const float d = (v - sk) * beta;
+#pragma unroll
+        for (int i = 0; i < DIM; ++i) {
+            row[i] = row[i] + s.ks[i] * d;
+            o = o + row[i] * s.qs[i];
+        }
+    }
+    double sq = j < DIM ? static_cast<double>(o * o) : 0.0;
+    sq = wave_sum(sq);
+    if ((j & 63) == 0) s.red[j >> 6] = sq;
+    __syncthreads();
+    const float scale = rms_scale(((s.red[0] + s.red[1]) + s.red[2]) + s.red[3], DIM, g.eps);
+    float out = 0.0f;
+    if (j < DIM) {
+        const float gate = z / (1.0f + ref_expf(-z));
+        out = o * scale * g.norm[j] * gate;
+    }
+    __syncthreads();  // the LDS is the next token's
+    return out;
+}
+
+// The attn_qkv rows of thread j's three channels of head h, from a token's row.
+template <int DIM>
+__device__ __forceinline__ void ssm_cur(const SsmArgs& g, int h, const float* qkv_t, float (&cur)[3]) {
+    const int j = threadIdx.x < DIM ? threadIdx.x : 0;
+#pragma unroll
+    for (int c = 0; c < 3; ++c) cur[c] = qkv_t[c * g.heads * DIM + h * DIM + j];
+}
+
+// The state row of thread j in half `half`, or zero at position 0 (a new or restarted sequence).
+template <int DIM>
+__device__ __forceinline__ void ssm_row_load(const SsmArgs& g, int h, int half, bool fresh, float (&row)[DIM]) {
+    const int j = threadIdx.x;
+    const float* src = g.state + (static_cast<size_t>(half) * g.heads + h) * DIM * DIM + j;
+#pragma unroll
+    for (int i = 0; i < DIM; ++i) row[i] = fresh || j >= DIM ? 0.0f : src[static_cast<size_t>(i) * DIM];
+}
+template <int DIM>
+__device__ __forceinline__ void ssm_row_store(const SsmArgs& g, int h, int half, const float (&row)[DIM]) {
+    const int j = threadIdx.x;
+    if (j >= DIM) return;
+    float* dst = g.state + (static_cast<size_t>(half) * g.heads + h) * DIM * DIM + j;
+#pragma unroll
+    for (int i = 0; i < DIM; ++i) dst[static_cast<size_t>(i) * DIM] = row[i];
+}
+
+// Decode, state sizes 64 and 128: the thread's state row in registers, loaded by one batch of
+// loads (in flight during the conv and the norms), the token at *pos read from half pos & 1 and
+// written to the other.
 template <int DIM>
 __global__ __launch_bounds__(kThreads) void k_ssm(SsmArgs g) {
+    __shared__ SsmLds s;
+    const int h = blockIdx.x, pos = *g.pos, j = threadIdx.x;
+    float row[DIM];
+    ssm_row_load<DIM>(g, h, pos & 1, pos == 0, row);
+    SsmConv cv;
+    ssm_conv_load<DIM>(g, h, pos, cv);
+    float cur[3];
+    ssm_cur<DIM>(g, h, g.qkv, cur);
+    const float z = g.z[h * DIM + (j < DIM ? j : 0)];
+    const float out = ssm_step<DIM>(g, s, h, cur, cv, z, g.ab[h], g.ab[g.heads + h], row);
+    ssm_row_store<DIM>(g, h, (pos + 1) & 1, row);
+    if (j < DIM) {
+        g.out[h * DIM + j] = out;
+#pragma unroll
+        for (int c = 0; c < 3; ++c) g.ring[static_cast<size_t>(pos % g.taps) * g.qkv_dim + c * g.heads * DIM + h * DIM + j] = cur[c];
+    }
+}
+
+// Prefill, state sizes 64 and 128: the ntok tokens at positions pos0 .. in order, the state row in
+// registers throughout.  Token t's rows are qkv[t * qkv_dim ..], z[t * heads * DIM ..], alpha
+// ab[t * ab_stride + h] and beta ab[t * ab_stride + heads + h]; outputs out[t * heads * DIM ..].
+// The half of the last token's parity keeps the state before it (the reference's snapshot,
+// src/model.cpp:798-812), the other half the state after it.
+template <int DIM>
+__global__ __launch_bounds__(kThreads) void k_pre_ssm(SsmArgs g, int pos0, int ntok, int ab_stride) {
+    __shared__ SsmLds s;
+    const int h = blockIdx.x, inner = g.heads * DIM, j = threadIdx.x, taps = g.taps;
+    float row[DIM];
+    ssm_row_load<DIM>(g, h, pos0 & 1, pos0 == 0, row);
+    SsmConv cv;
+    ssm_conv_load<DIM>(g, h, pos0, cv);
+    for (int t = 0; t < ntok; ++t) {
+        const int pos = pos0 + t;
+        if (t + 1 == ntok) ssm_row_store<DIM>(g, h, pos & 1, row);
+        float cur[3];
+        ssm_cur<DIM>(g, h, g.qkv + static_cast<size_t>(t) * g.qkv_dim, cur);
+        const float z = g.z[static_cast<size_t>(t) * inner + h * DIM + (j < DIM ? j : 0)];
+        const float* ab = g.ab + static_cast<size_t>(t) * ab_stride;
+        const float out = ssm_step<DIM>(g, s, h, cur, cv, z, ab[h], ab[g.heads + h], row);
+        if (j < DIM) g.out[static_cast<size_t>(t) * inner + h * DIM + j] = out;
+    }
+    ssm_row_store<DIM>(g, h, (pos0 + ntok) & 1, row);
+    // the ring: the batch's last taps positions' rows (older slots keep theirs)
+    if (j < DIM)
+        for (int t = ntok - taps > 0 ? ntok - taps : 0; t < ntok; ++t)
+#pragma unroll
+            for (int c = 0; c < 3; ++c) {
+                const int ch = c * inner + h * DIM + j;
+                g.ring[static_cast<size_t>((pos0 + t) % taps) * g.qkv_dim + ch] = g.qkv[static_cast<size_t>(t) * g.qkv_dim + ch];
+            }
+}
+
+// Decode, any state size up to 256: the state read twice from memory.
+__global__ __launch_bounds__(kThreads) void k_ssm_any(SsmArgs g) {
     __shared__ float qs[kThreads], ks[kThreads];
     __shared__ float inv[2];
     __shared__ double red[4];
-    const int h = blockIdx.x, j = threadIdx.x, dim = DIM != 0 ? DIM : g.dim, taps = g.taps, qkv = g.qkv_dim;
+    const int h = blockIdx.x, j = threadIdx.x, dim = g.dim, taps = g.taps, qkv = g.qkv_dim;
     const int pos = *g.pos, k_off = g.heads * dim;
     const size_t plane = static_cast<size_t>(dim) * dim;
     const float* sin = g.state + (static_cast<size_t>(pos & 1) * g.heads + h) * plane + j;
     float* sout = g.state + (static_cast<size_t>((pos + 1) & 1) * g.heads + h) * plane + j;
     const bool fresh = pos == 0;  // the zero state of a new or restarted sequence
-    // the state row first: its loads are in flight during the conv and the norms
-    constexpr int kRow = DIM != 0 ? DIM : 1;
-    float row[kRow];
-    if (DIM != 0 && j < dim) {
-#pragma unroll
-        for (int i = 0; i < kRow; ++i) row[i] = fresh ? 0.0f : sin[static_cast<size_t>(i) * dim];
-    }
     float v = 0.0f;
     if (j < dim) {
         for (int c = 0; c < 3; ++c) {  // q, k, v channels of head h
@@ -463,33 +648,18 @@ __global__ __launch_bounds__(kThreads) void k_ssm(SsmArgs g) {
     float o = 0.0f;
     if (j < dim) {
         float sk = 0.0f;
-        if (DIM != 0) {
-#pragma unroll
-            for (int i = 0; i < kRow; ++i) {
-                row[i] = row[i] * decay;
-                sk = sk + row[i] * ks[i];
-            }
-            const float d = (v - sk) * beta;
-#pragma unroll
-            for (int i = 0; i < kRow; ++i) {
-                const float si = row[i] + ks[i] * d;
-                sout[static_cast<size_t>(i) * dim] = si;
-                o = o + si * qs[i];
-            }
-        } else {
 #pragma unroll 8
-            for (int i = 0; i < dim; ++i) {
-                const float si = (fresh ? 0.0f : sin[static_cast<size_t>(i) * dim]) * decay;
-                sk = sk + si * ks[i];
-            }
-            const float d = (v - sk) * beta;
+        for (int i = 0; i < dim; ++i) {
+            const float si = (fresh ? 0.0f : sin[static_cast<size_t>(i) * dim]) * decay;
+            sk = sk + si * ks[i];
+        }
+        const float d = (v - sk) * beta;
 #pragma unroll 8
-            for (int i = 0; i < dim; ++i) {
-                float si = (fresh ? 0.0f : sin[static_cast<size_t>(i) * dim]) * decay;
-                si = si + ks[i] * d;
-                sout[static_cast<size_t>(i) * dim] = si;
-                o = o + si * qs[i];
-            }
+        for (int i = 0; i < dim; ++i) {
+            float si = (fresh ? 0.0f : sin[static_cast<size_t>(i) * dim]) * decay;
+            si = si + ks[i] * d;
+            sout[static_cast<size_t>(i) * dim] = si;
+            o = o + si * qs[i];
         }
     }
     double sq = j < dim ? static_cast<double>(o * o) : 0.0;
@@ -621,7 +791,6 @@ __global__ __launch_bounds__(64) void k_plain_scores(AttnArgs g) {
 // when the window fits it and recomputed per position otherwise; then a lane per output dimension
 // sums w_p v_p[d] in position order, its loads issued 32 positions at a time.  Qwen3.5's sigmoid
 // gate (src/model.cpp:1102-1108) is applied to the sums.
-constexpr int kPlainLdsW = 8192;
 __global__ __launch_bounds__(64) void k_plain_values(AttnArgs g) {
     __shared__ float wl[kPlainLdsW];
     const int h = blockIdx.x, hd = g.head_dim, hpk = g.heads / g.kv_heads, kv = h / hpk, lane = threadIdx.x;
@@ -658,6 +827,113 @@ __global__ __launch_bounds__(64) void k_plain_values(AttnArgs g) {
     for (; p < n; ++p) a += weight(p) * h2f(vv[static_cast<size_t>(p) * hd]);
     if (g.gate != nullptr) a = a * (1.0f / (1.0f + ref_expf(-g.gate[static_cast<size_t>(h) * g.gate_stride + d])));
     g.out[h * hd + d] = a;
+}
+
+// The plain attention for the ntok tokens of a prompt (positions pos0 ..), each token's steps
+// those of the decode kernels above: a prologue wave per (token, head), then a workgroup per
+// (token, query head) that forms the scores of every visible position in LDS (a thread per
+// position), runs the softmax on one wave (the decode kernels' grouping) and sums the values (a
+// thread per output dimension).  Contexts up to kPlainLdsW positions.
+__global__ __launch_bounds__(64) void k_pre_plain_prologue(PrePlainArgs p) {
+    __shared__ float a[kPlainMaxHead], b[kPlainMaxHead];
+    const AttnArgs& g = p.a;
+    const int t = blockIdx.x, w = blockIdx.y, hd = g.head_dim, lane = threadIdx.x, pos = p.pos0 + t;
+    const int qs = g.q_stride != 0 ? g.q_stride : hd;
+    const float* rope = g.rope != nullptr ? g.rope + static_cast<size_t>(pos) * g.rope_dim : nullptr;
+    if (w < g.heads) {
+        const float* q = g.q + static_cast<size_t>(t) * p.q_tok + static_cast<size_t>(w) * qs;
+        for (int i = lane; i < hd; i += 64) a[i] = q[i];
+        head_norm_rope(a, g.qbias != nullptr ? g.qbias + w * hd : nullptr, g.qnorm, rope, hd, g.rope_dim, g.neox, g.eps);
+        for (int i = lane; i < hd; i += 64) g.qn[(static_cast<size_t>(t) * g.heads + w) * hd + i] = a[i];
+        return;
+    }
+    const int kv = w - g.heads;
+    const float* k = g.k + static_cast<size_t>(t) * p.kv_tok + kv * hd;
+    const float* v = g.v + static_cast<size_t>(t) * p.kv_tok + kv * hd;
+    for (int i = lane; i < hd; i += 64) {
+        a[i] = k[i];
+        b[i] = g.vbias != nullptr ? v[i] + g.vbias[kv * hd + i] : v[i];
+    }
+    head_norm_rope(a, g.kbias != nullptr ? g.kbias + kv * hd : nullptr, g.knorm, rope, hd, g.rope_dim, g.neox, g.eps);
+    if (g.vnorm) {
+        double sq = 0.0;
+        for (int i = lane; i < hd; i += 64) sq += static_cast<double>(b[i] * b[i]);
+        const float scale = rms_scale(wave_sum(sq), hd, g.eps);
+        for (int i = lane; i < hd; i += 64) b[i] = b[i] * scale;
+    }
+    uint16_t* kr = g.kcache + (static_cast<size_t>(kv) * g.ctx + pos) * hd;
+    uint16_t* vr = g.vcache + (static_cast<size_t>(kv) * g.ctx + pos) * hd;
+    for (int i = lane; i < hd; i += 64) {
+        kr[i] = f2h(a[i]);
+        vr[i] = f2h(b[i]);
+    }
+}
+
+__global__ __launch_bounds__(kThreads) void k_pre_plain_attn(PrePlainArgs p) {
+    __shared__ float q[kPlainMaxHead];
+    __shared__ float wl[kPlainLdsW];
+    const AttnArgs& g = p.a;
+    const int t = blockIdx.x, h = blockIdx.y, hd = g.head_dim, hpk = g.heads / g.kv_heads, kv = h / hpk, tid = threadIdx.x;
+    const int L = p.pos0 + t + 1, start = plain_start(g, L), n = L - start;
+    for (int i = tid; i < hd; i += kThreads) q[i] = g.qn[(static_cast<size_t>(t) * g.heads + h) * hd + i];
+    __syncthreads();
+    const uint16_t* kbase = g.kcache + (static_cast<size_t>(kv) * g.ctx + start) * hd;
+    for (int pp = tid; pp < n; pp += kThreads) {  // dot_f32 order: 16 lane partials, then their sum
+        const uint16_t* kr = kbase + static_cast<size_t>(pp) * hd;
+        float acc[16];
+#pragma unroll
+        for (int j = 0; j < 16; ++j) acc[j] = 0.0f;
+        for (int b0 = 0; b0 < hd; b0 += 16) {
+            const uint4 k0 = *reinterpret_cast<const uint4*>(kr + b0), k1 = *reinterpret_cast<const uint4*>(kr + b0 + 8);
+            const uint32_t kw[8] = {k0.x, k0.y, k0.z, k0.w, k1.x, k1.y, k1.z, k1.w};
+#pragma unroll
+            for (int j = 0; j < 16; ++j) {
+                const uint16_t hv = static_cast<uint16_t>((j & 1) ? (kw[j >> 1] >> 16) : (kw[j >> 1] & 0xFFFF));
+                acc[j] += q[b0 + j] * h2f(hv);
+            }
+        }
+        float sum = 0.0f;
+#pragma unroll
+        for (int j = 0; j < 16; ++j) sum += acc[j];
+        wl[pp] = sum * g.scale;
+    }
+    __syncthreads();
+    if (tid < 64) {  // the softmax on one wave, as k_plain_values runs it
+        float m = -INFINITY;
+        for (int pp = tid; pp < n; pp += 64) m = fmaxf(m, wl[pp]);
+        m = wave_max(m);
+        double part = 0.0;
+        for (int pp = tid; pp < n; pp += 64) {
+            const float e = ref_expf(wl[pp] - m);
+            wl[pp] = e;
+            part += static_cast<double>(e);
+        }
+        const float scale = static_cast<float>(1.0 / wave_sum(part));
+        for (int pp = tid; pp < n; pp += 64) wl[pp] = wl[pp] * scale;
+    }
+    __syncthreads();
+    constexpr int kChains = kPlainMaxHead / kThreads;
+    const uint16_t* vbase = g.vcache + (static_cast<size_t>(kv) * g.ctx + start) * hd;
+#pragma unroll
+    for (int c = 0; c < kChains; ++c) {
+        const int d = tid + c * kThreads;
+        if (d >= hd) break;
+        const uint16_t* vv = vbase + d;
+        constexpr int kB = 32;
+        float acc = 0.0f;
+        int pp = 0;
+        for (; pp + kB <= n; pp += kB) {  // loads first, then the adds in position order
+            float vf[kB];
+#pragma unroll
+            for (int u = 0; u < kB; ++u) vf[u] = h2f(vv[static_cast<size_t>(pp + u) * hd]);
+#pragma unroll
+            for (int u = 0; u < kB; ++u) acc += wl[pp + u] * vf[u];
+        }
+        for (; pp < n; ++pp) acc += wl[pp] * h2f(vv[static_cast<size_t>(pp) * hd]);
+        if (g.gate != nullptr)
+            acc = acc * (1.0f / (1.0f + ref_expf(-g.gate[static_cast<size_t>(t) * p.q_tok + static_cast<size_t>(h) * g.gate_stride + d])));
+        g.out[static_cast<size_t>(t) * g.heads * hd + h * hd + d] = acc;
+    }
 }
 
 // tanhf as the Gemma epilogues compute it (ref_tanhf), for the parity tests.
@@ -913,6 +1189,18 @@ hipError_t launch_attention_plain(const AttnArgs& g, hipStream_t s) {
     return hipGetLastError();
 }
 
+hipError_t launch_pre_attention_plain(const PrePlainArgs& p, hipStream_t s) {
+    const AttnArgs& g = p.a;
+    const int hpk = g.kv_heads > 0 ? g.heads / g.kv_heads : 0;
+    if (g.head_dim < 16 || g.head_dim > kPlainMaxHead || g.head_dim % 16 != 0 || hpk < 1 || hpk > 16 ||
+        hpk * g.kv_heads != g.heads || g.qn == nullptr || g.no_kv || p.ntok < 1 || p.pos0 < 0 || !pre_plain_fits(p.pos0 + p.ntok))
+        return hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_pre_plain_prologue, dim3(static_cast<unsigned>(p.ntok), static_cast<unsigned>(g.heads + g.kv_heads)), dim3(64),
+                       0, s, p);
+    hipLaunchKernelGGL(k_pre_plain_attn, dim3(static_cast<unsigned>(p.ntok), static_cast<unsigned>(g.heads)), dim3(kThreads), 0, s, p);
+    return hipGetLastError();
+}
+
 int attention_max_splits(int ctx) { return (ctx + kSplit - 1) / kSplit; }
 
 hipError_t launch_post_add(float* h, const float* p, const float* w, float eps, int n, hipStream_t s, float out_scale) {
@@ -939,7 +1227,16 @@ hipError_t launch_ssm(const SsmArgs& g, hipStream_t s) {
     const dim3 grid(static_cast<unsigned>(g.heads)), block(kThreads);
     if (g.dim == 64) hipLaunchKernelGGL(k_ssm<64>, grid, block, 0, s, g);
     else if (g.dim == 128) hipLaunchKernelGGL(k_ssm<128>, grid, block, 0, s, g);
-    else hipLaunchKernelGGL(k_ssm<0>, grid, block, 0, s, g);
+    else hipLaunchKernelGGL(k_ssm_any, grid, block, 0, s, g);
+    return hipGetLastError();
+}
+
+hipError_t launch_pre_ssm(const SsmArgs& g, int pos0, int ntok, int ab_stride, hipStream_t s) {
+    if (!pre_ssm_fits(g.dim) || g.heads < 1 || g.taps < 2 || g.taps > 8 || g.qkv_dim != 3 * g.heads * g.dim || ntok < 1 || pos0 < 0)
+        return hipErrorInvalidValue;
+    const dim3 grid(static_cast<unsigned>(g.heads)), block(kThreads);
+    if (g.dim == 64) hipLaunchKernelGGL(k_pre_ssm<64>, grid, block, 0, s, g, pos0, ntok, ab_stride);
+    else hipLaunchKernelGGL(k_pre_ssm<128>, grid, block, 0, s, g, pos0, ntok, ab_stride);
     return hipGetLastError();
 }
 

@@ -128,6 +128,16 @@ hipError_t launch_attention(const AttnArgs& g, hipStream_t s);
 // ([heads][ctx]), the queries in qn.
 hipError_t launch_attention_plain(const AttnArgs& g, hipStream_t s);
 constexpr int kPlainMaxHead = 512;
+constexpr int kPlainLdsW = 8192;  // the weights a plain-attention softmax keeps in LDS
+// The plain attention for a prompt's ntok tokens at positions pos0 .. (every token's rows and
+// outputs at the strides below; the queries' gate, when given, at a.gate + t * q_tok).
+struct PrePlainArgs {
+    AttnArgs a;    // a.q, a.k, a.v: token 0's raw rows; a.qn: [ntok][heads][head_dim]; a.out: [ntok][heads * head_dim]
+    int pos0, ntok;
+    int q_tok, kv_tok;  // floats from one token's raw query (key/value) rows to the next
+};
+inline bool pre_plain_fits(int positions) { return positions <= kPlainLdsW; }
+hipError_t launch_pre_attention_plain(const PrePlainArgs& p, hipStream_t s);
 hipError_t launch_embed(const Packed& m, const PickState& ps, float* h, float scale, hipStream_t s);
 // h = (h + rms_norm(p, w)) * out_scale over n values (Gemma's post-attention / post-feed-forward
 // norm with out_scale 1; Gemma 4's per-layer embedding with the layer's output scale).
@@ -150,6 +160,11 @@ hipError_t launch_conv(const float* bcx, uint16_t* cache, const float* w, int ta
                        hipStream_t s);
 // Qwen3.5: one recurrent layer's conv, delta-rule state update and gated norm (one workgroup a head).
 hipError_t launch_ssm(const SsmArgs& g, hipStream_t s);
+// Qwen3.5 prefill: the recurrence over ntok tokens at positions pos0 .. in one launch (state sizes
+// 64 and 128): g.qkv [ntok][qkv_dim], g.z [ntok][heads * dim], alpha and beta of token t at
+// g.ab[t * ab_stride + h] and g.ab[t * ab_stride + heads + h], out [ntok][heads * dim].
+hipError_t launch_pre_ssm(const SsmArgs& g, int pos0, int ntok, int ab_stride, hipStream_t s);
+inline bool pre_ssm_fits(int dim) { return dim == 64 || dim == 128; }
 // Qwen3.5 attention: [heads][q | gate] rows split into q and gate; att *= sigmoid(gate).
 hipError_t launch_qgate_split(const float* qg, float* q, float* gate, int heads, int hd, hipStream_t s);
 hipError_t launch_sigmoid_gate(float* att, const float* gate, int n, hipStream_t s);

@@ -75,6 +75,8 @@ inline bool pre_attn_mfma_fits(int hpk, int head_dim) {
 }
 
 hipError_t launch_mm(const MmArgs& g, int mode, hipStream_t s);
+// The GEMMs take rows whose length is a multiple of this many values (one staged chunk).
+constexpr int kMmChunkCols = 256;
 hipError_t launch_pre_quant(const float* x, int xstride, const float* w, float eps, int cols, int ntok, bool q8k, int bits,
                             const ActPlanar& out, hipStream_t s);
 hipError_t launch_pre_planar(const void* xq, int cols, int ntok, bool q8k, const ActPlanar& out, hipStream_t s);

@@ -165,7 +165,7 @@ __device__ __forceinline__ v4i mfma(uint64_t a, uint64_t b, v4i c) {
 // fragments and row scales in registers; both are loaded one chunk ahead, so
 // memory latency overlaps the MFMAs and the float epilogue.
 constexpr int kRowsPerWg = 64;
-constexpr int kChunkCols = 256;
+constexpr int kChunkCols = kMmChunkCols;
 constexpr int kBRow = kChunkCols + 16;  // LDS bytes per token row, padded off the bank period
 // Token groups of 16 a workgroup: 4 (64 tokens), or 2 for the K-quants, whose
 // integer epilogue holds more state per output.

@@ -197,6 +197,8 @@ brisk_hip_memory estimate_session(const brisk_hip_config& cfg, const brisk_hip_t
     sc += T * (e + 2 * qd + 2 * kvd + ff) * 4 + T * stride * (1 + 4 / 32.0 + 4 / 16.0);  // prefill buffers
     if (cfg.arch == BRISK_HIP_ARCH_GEMMA3 || cfg.arch == BRISK_HIP_ARCH_LFM2) sc += T * e * 4;  // post-norm inputs, conv outputs
     if (cfg.arch == BRISK_HIP_ARCH_LFM2) sc += T * 3 * e * 4;                                   // prefill conv rows
+    if (cfg.arch == BRISK_HIP_ARCH_QWEN35)  // prefill recurrence rows, query|gate rows, the wider attention output
+        sc += T * (5 * static_cast<size_t>(cfg.ssm_inner) + 2 * cfg.ssm_v_heads + 2 * qd) * 4;
     sc += static_cast<size_t>(64) * cfg.vocab * 4;                         // eval_all logits
     for (size_t i = 0; i < n; ++i)  // the prefill's expanded layer matrices
         if (mx_expanded(static_cast<uint32_t>(tensors[i].type)) && tensors[i].name != nullptr &&
@@ -603,6 +605,12 @@ Session::Session(const brisk_hip_config& cfg, const brisk_hip_tensor* tensors, s
     {
         const char* pf = std::getenv("BRISK_HIP_PREFILL");
         prefill_on_ = !(pf != nullptr && std::string(pf) == "0") && !debug_;
+        for (const Layer& L : layers_)  // the batched GEMMs stage their rows in 256-value chunks
+            for (const DeviceMatrix* m : {&L.q, &L.k, &L.v, &L.o, &L.gate, &L.up, &L.down, &L.conv_in, &L.conv_out, &L.ssm_qkv,
+                                          &L.ssm_gate, &L.ssm_alpha, &L.ssm_beta, &L.ssm_out})
+                if (m->mem != nullptr && m->p.cols % kMmChunkCols != 0) prefill_shapes_ = false;
+        if (out_->p.cols % kMmChunkCols != 0) prefill_shapes_ = false;
+        prefill_on_ = prefill_on_ && prefill_shapes_;
         const char* pa = std::getenv("BRISK_HIP_PREFILL_ATTN");  // "mfma": long prompts' attention on f16 MFMA
         prefill_mfma_ = pa != nullptr && std::string(pa) == "mfma";
         prefill_legacy_ = pa != nullptr && std::string(pa) == "staged";
@@ -1184,8 +1192,13 @@ bool Session::use_prefill(size_t n) const {
     const bool mfma_fits = prefill_mfma_ && pre_attn_mfma_fits(static_cast<int>(cfg_.heads / cfg_.kv_heads), static_cast<int>(cfg_.head_dim));
     // Gemma 3 (sliding layers, post-norms, GELU, soft-capped logits) and LFM2 (short convolutions)
     // take the exact attention only
-    if (qwen35()) return false;     // the recurrence takes its tokens one at a time
-    if (plain_attn_) return false;  // the batched attention holds heads of at most 128, one shape for all layers
+    // Qwen3.5: the projections batched, the recurrence over the tokens in one launch (state sizes 64
+    // and 128), the plain attention batched (contexts of its LDS window)
+    if (qwen35())
+        return prefill_on_ && n >= 2 && pre_ssm_fits(static_cast<int>(cfg_.ssm_state)) && pre_plain_fits(static_cast<int>(position_ + n));
+    // the plain attention batched (contexts of its LDS window); Gemma 4's per-layer shapes and
+    // per-layer embeddings take their prompts token by token
+    if (plain_attn_) return prefill_on_ && n >= 2 && !gemma4() && pre_plain_fits(static_cast<int>(position_ + n));
     if (gemma() || lfm2()) return prefill_on_ && n >= 2 && exact_fits && cfg_.head_dim <= 128;
     return prefill_on_ && n >= 2 && (exact_fits || mfma_fits);
 }
@@ -1198,17 +1211,25 @@ void Session::ensure_prefill() {
     pre_q_ = static_cast<float*>(alloc(T * qd * 4));
     pre_k_ = static_cast<float*>(alloc(T * kvd * 4));
     pre_v_ = static_cast<float*>(alloc(T * kvd * 4));
-    pre_att_ = static_cast<float*>(alloc(T * qd * 4));
+    pre_att_ = static_cast<float*>(alloc(T * std::max<size_t>(qd, cfg_.ssm_inner) * 4));
     pre_act_ = static_cast<float*>(alloc(T * ff * 4));
     if (gemma() || lfm2()) pre_proj_ = static_cast<float*>(alloc(T * e * 4));  // post-norm inputs; conv outputs
     if (lfm2()) pre_conv_ = static_cast<float*>(alloc(T * 3 * e * 4));           // LFM2's [b | c | x] rows
-    const size_t widest = std::max(std::max(e, qd), ff);
+    if (qwen35()) {
+        const size_t inner = cfg_.ssm_inner, heads = cfg_.ssm_v_heads;
+        pre_sqkv_ = static_cast<float*>(alloc(T * 3 * inner * 4));
+        pre_sz_ = static_cast<float*>(alloc(T * inner * 4));
+        pre_sab_ = static_cast<float*>(alloc(T * 2 * heads * 4));
+        pre_qg_ = static_cast<float*>(alloc(T * 2 * qd * 4));
+    }
+    const size_t widest = std::max(std::max(std::max(e, qd), ff), static_cast<size_t>(cfg_.ssm_inner));
     pre_x_.stride = static_cast<int>((widest + 255) / 256 * 256);
     pre_x_.qs = static_cast<int8_t*>(alloc(T * pre_x_.stride));
     pre_x_.d = static_cast<float*>(alloc(T * (pre_x_.stride / 32) * 4));
     pre_x_.bs = static_cast<int32_t*>(alloc(T * (pre_x_.stride / 16) * 4));
     for (Layer& L : layers_)
-        for (DeviceMatrix* m : {&L.q, &L.k, &L.v, &L.o, &L.gate, &L.up, &L.down, &L.conv_in, &L.conv_out})
+        for (DeviceMatrix* m : {&L.q, &L.k, &L.v, &L.o, &L.gate, &L.up, &L.down, &L.conv_in, &L.conv_out, &L.ssm_qkv, &L.ssm_gate,
+                                &L.ssm_alpha, &L.ssm_beta, &L.ssm_out})
             if (m->mem != nullptr && mx_expanded(m->p.type) && m->xmem == nullptr) {
                 check(hipMalloc(&m->xmem, mx_bytes(m->p.type, m->p.rows, m->p.cols)), "hipMalloc(expanded planes)");
                 check(launch_mx_expand(m->p, m->xmem, &m->x, stream_), "expand planes");
@@ -1233,7 +1254,54 @@ void Session::prefill_layers(size_t pos0, int T) {
         MmArgs g{};
         g.x = pre_x_;
         g.ntok = T;
-        if (L.conv_w != nullptr) {  // LFM2 short convolution in place of attention (src/model.cpp:935-969)
+        if (L.ssm_a != nullptr) {  // Qwen3.5 Gated DeltaNet (src/model.cpp:754-865)
+            const int heads = static_cast<int>(cfg_.ssm_v_heads), inner = static_cast<int>(cfg_.ssm_inner), qkv = 3 * inner;
+            const DeviceMatrix* mats[4] = {&L.ssm_qkv, &L.ssm_gate, &L.ssm_alpha, &L.ssm_beta};
+            float* outs[4] = {pre_sqkv_, pre_sz_, pre_sab_, pre_sab_ + heads};
+            const int strides[4] = {qkv, inner, 2 * heads, 2 * heads};
+            const DeviceMatrix* quantised_for = nullptr;
+            for (int i = 0; i < 4; ++i) {  // attn_norm(h) quantised once per activation format
+                const DeviceMatrix& m = *mats[i];
+                if (quantised_for == nullptr || takes_q8_k(m.p.type) != takes_q8_k(quantised_for->p.type) ||
+                    act_bits(m.p) != act_bits(quantised_for->p)) {
+                    prefill_quant(pre_h_, e, L.attn_norm, e, T, m);
+                    quantised_for = &m;
+                }
+                g.m = m.p; set_mx(g, m); g.out = outs[i]; g.ostride = strides[i];
+                check(launch_mm(g, kMmStore, stream_), "prefill recurrence projections");
+            }
+            SsmArgs sa{};
+            sa.qkv = pre_sqkv_; sa.z = pre_sz_; sa.ab = pre_sab_; sa.conv_w = L.ssm_conv_w; sa.a = L.ssm_a; sa.dt = L.ssm_dt;
+            sa.norm = L.ssm_norm; sa.ring = L.ssm_ring; sa.state = L.ssm_state; sa.pos = pos_; sa.out = pre_att_;
+            sa.heads = heads; sa.dim = static_cast<int>(cfg_.ssm_state); sa.taps = static_cast<int>(cfg_.ssm_conv); sa.qkv_dim = qkv;
+            sa.eps = cfg_.rms_epsilon; sa.q_scale = 1.0f / std::sqrt(static_cast<float>(cfg_.ssm_state));  // src/model.cpp:813
+            check(launch_pre_ssm(sa, static_cast<int>(pos0), T, 2 * heads, stream_), "prefill recurrence");
+            prefill_quant(pre_att_, inner, nullptr, inner, T, L.ssm_out);
+            g.m = L.ssm_out.p; set_mx(g, L.ssm_out); g.out = pre_h_; g.ostride = e;
+            check(launch_mm(g, kMmAdd, stream_), "prefill ssm_out");
+        } else if (qwen35()) {  // Qwen3.5's gated attention: each head's query rows, then its gate rows
+            prefill_quant(pre_h_, e, L.attn_norm, e, T, L.q);
+            g.m = L.q.p; set_mx(g, L.q); g.out = pre_qg_; g.ostride = 2 * qd;
+            check(launch_mm(g, kMmStore, stream_), "prefill q");
+            g.m = L.k.p; set_mx(g, L.k); g.out = pre_k_; g.ostride = kvd;
+            check(launch_mm(g, kMmStore, stream_), "prefill k");
+            g.m = L.v.p; set_mx(g, L.v); g.out = pre_v_; g.ostride = kvd;
+            check(launch_mm(g, kMmStore, stream_), "prefill v");
+            PrePlainArgs pp{};
+            AttnArgs& aa = pp.a;
+            aa.q = pre_qg_; aa.k = pre_k_; aa.v = pre_v_; aa.qnorm = L.q_norm; aa.knorm = L.k_norm;
+            aa.rope = rope_; aa.rope_dim = std::min(rope_dim_, L.hd); aa.eps = cfg_.rms_epsilon; aa.neox = neox();
+            aa.kcache = kcache_[l]; aa.vcache = vcache_[l]; aa.ctx = static_cast<int>(max_ctx_); aa.head_dim = L.hd;
+            aa.heads = static_cast<int>(cfg_.heads); aa.kv_heads = L.kvh;
+            aa.scale = 1.0f / std::sqrt(static_cast<float>(L.hd));  // src/model.cpp:978
+            aa.qn = pre_q_; aa.out = pre_att_;
+            aa.q_stride = 2 * L.hd; aa.gate = pre_qg_ + L.hd; aa.gate_stride = 2 * L.hd;
+            pp.pos0 = static_cast<int>(pos0); pp.ntok = T; pp.q_tok = 2 * qd; pp.kv_tok = kvd;
+            check(launch_pre_attention_plain(pp, stream_), "prefill attention");
+            prefill_quant(pre_att_, qd, nullptr, qd, T, L.o);
+            g.m = L.o.p; set_mx(g, L.o); g.out = pre_h_; g.ostride = e;
+            check(launch_mm(g, kMmAdd, stream_), "prefill o");
+        } else if (L.conv_w != nullptr) {  // LFM2 short convolution in place of attention (src/model.cpp:935-969)
             prefill_quant(pre_h_, e, L.attn_norm, e, T, L.conv_in);
             g.m = L.conv_in.p; set_mx(g, L.conv_in); g.out = pre_conv_; g.ostride = 3 * e;
             check(launch_mm(g, kMmStore, stream_), "prefill conv in_proj");
@@ -1252,6 +1320,23 @@ void Session::prefill_layers(size_t pos0, int T) {
             g.m = L.v.p; set_mx(g, L.v); g.out = pre_v_; g.ostride = kvd;
             check(launch_mm(g, kMmStore, stream_), "prefill v");
             // norms, RoPE, cache rows, attention (:1020-1093)
+            if (plain_attn_) {  // heads past 128 (or BRISK_HIP_ATTN=plain): the plain attention batched
+                PrePlainArgs pp{};
+                AttnArgs& aa = pp.a;
+                aa.q = pre_q_; aa.k = pre_k_; aa.v = pre_v_; aa.qnorm = L.q_norm; aa.knorm = L.k_norm;
+                aa.rope = !L.rope ? nullptr : L.slides ? rope_local_ : rope_;
+                aa.window = L.slides ? static_cast<int>(cfg_.sliding_window) : 0;
+                aa.rope_dim = L.slides ? L.hd : std::min(rope_dim_, L.hd);
+                aa.qbias = L.q_bias; aa.kbias = L.k_bias; aa.vbias = L.v_bias;
+                aa.eps = cfg_.rms_epsilon; aa.neox = neox();
+                aa.kcache = kcache_[l]; aa.vcache = vcache_[l]; aa.ctx = static_cast<int>(max_ctx_); aa.head_dim = L.hd;
+                aa.heads = static_cast<int>(cfg_.heads); aa.kv_heads = L.kvh;
+                aa.scale = 1.0f / std::sqrt(static_cast<float>(L.hd));  // src/model.cpp:978
+                // the queries normed in place (one wave owns each token's head, reading it whole first)
+                aa.qn = pre_q_; aa.out = pre_att_;
+                pp.pos0 = static_cast<int>(pos0); pp.ntok = T; pp.q_tok = qd; pp.kv_tok = kvd;
+                check(launch_pre_attention_plain(pp, stream_), "prefill attention");
+            } else {
             PreAttnArgs pa{};
             pa.a.qnorm = L.q_norm; pa.a.knorm = L.k_norm; pa.a.eps = cfg_.rms_epsilon;
             pa.a.rope = !L.rope ? nullptr : L.slides ? rope_local_ : rope_;  // Gemma 3's sliding layers: the local base
@@ -1268,6 +1353,7 @@ void Session::prefill_layers(size_t pos0, int T) {
             pa.mfma = prefill_mfma_ ? 1 : 0;
             pa.legacy = prefill_legacy_ ? 1 : 0;
             check(launch_pre_attention(pa, T, stream_), "prefill attention");
+            }
             // h += O (sub-normed) att (:1095-1111)
             prefill_quant(pre_att_, qd, L.attn_sub_norm, qd, T, L.o);
             g.m = L.o.p; set_mx(g, L.o); g.out = L.attn_post_norm ? pre_proj_ : pre_h_; g.ostride = e;

@@ -178,6 +178,7 @@ private:
     static constexpr size_t kTraceSlots = 1 << 20;
     bool debug_ = false;
     bool prefill_on_ = true;
+    bool prefill_shapes_ = true;   // every matrix's rows a whole number of the batched GEMM's chunks
     bool prefill_mfma_ = false;    // BRISK_HIP_PREFILL_ATTN=mfma
     bool prefill_legacy_ = false;  // BRISK_HIP_PREFILL_ATTN=staged
     float *pre_h_ = nullptr, *pre_q_ = nullptr, *pre_k_ = nullptr, *pre_v_ = nullptr, *pre_att_ = nullptr, *pre_act_ = nullptr;
@@ -187,6 +188,8 @@ private:
     void fetch_logits(float* out, const float* dev, size_t rows);
     float* pre_proj_ = nullptr;  // Gemma: a projection's rows before their post-norm; LFM2: conv outputs
     float* pre_conv_ = nullptr;  // LFM2: in_proj rows [b | c | x]
+    // Qwen3.5: the recurrence's projections [T][qkv], [T][inner], [T][alpha | beta]; the query|gate rows
+    float *pre_sqkv_ = nullptr, *pre_sz_ = nullptr, *pre_sab_ = nullptr, *pre_qg_ = nullptr;
     ActPlanar pre_x_{};
     float* all_logits_ = nullptr;  // eval_all's [64][vocab] logits, allocated on first use
     hipGraphExec_t graph_layers_ = nullptr, graph_full_ = nullptr;
