@@ -293,7 +293,7 @@ SPECS = {
     # Gemma 4: sliding layers 0-2 and 4 (64-wide heads, 2 key/value heads) and global layers 3 and 5
     # (128-wide heads, 1 key/value head, proportional RoPE factors); layers 4 and 5 read the caches
     # of layers 2 and 3; layer 3 has no V projection (K serves as V); per-layer feed-forward widths,
-    # 64-wide per-layer embeddings and per-layer output scales.
+    # 256-wide per-layer embeddings and per-layer output scales.
     "tiny-gemma4": ModelSpec("tiny-gemma4", "gemma4", 256, 6, 4, 2, 128, 768, 1000, 1e6, context=1024,
                              fmt=_uniform4(G.T_Q8_0), factors={"rope_freqs.weight": 64}, no_v_layers=(3,),
                              extra={"attention.sliding_window": (G.U32, 8), "rope.freq_base_swa": (G.F32, 10000.0),
@@ -301,7 +301,7 @@ SPECS = {
                                     "attention.sliding_window_pattern": (G.ARRAY, (G.BOOL, [1, 1, 1, 0, 1, 0])),
                                     "attention.key_length_swa": (G.U32, 64),
                                     "attention.shared_kv_layers": (G.U32, 2),
-                                    "embedding_length_per_layer_input": (G.U32, 64),
+                                    "embedding_length_per_layer_input": (G.U32, 256),
                                     "feed_forward_length": (G.ARRAY, (G.I32, [512, 512, 768, 768, 512, 512])),
                                     "attention.head_count_kv": (G.ARRAY, (G.U32, [2, 2, 2, 1, 2, 1]))}),
     # Full-size shapes of the graph-path families, for bench.py's decode lines (synthetic weights):

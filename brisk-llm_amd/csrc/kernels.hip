@@ -1193,10 +1193,11 @@ hipError_t launch_pre_attention_plain(const PrePlainArgs& p, hipStream_t s) {
     const AttnArgs& g = p.a;
     const int hpk = g.kv_heads > 0 ? g.heads / g.kv_heads : 0;
     if (g.head_dim < 16 || g.head_dim > kPlainMaxHead || g.head_dim % 16 != 0 || hpk < 1 || hpk > 16 ||
-        hpk * g.kv_heads != g.heads || g.qn == nullptr || g.no_kv || p.ntok < 1 || p.pos0 < 0 || !pre_plain_fits(p.pos0 + p.ntok))
+        hpk * g.kv_heads != g.heads || g.qn == nullptr || p.ntok < 1 || p.pos0 < 0 || !pre_plain_fits(p.pos0 + p.ntok))
         return hipErrorInvalidValue;
-    hipLaunchKernelGGL(k_pre_plain_prologue, dim3(static_cast<unsigned>(p.ntok), static_cast<unsigned>(g.heads + g.kv_heads)), dim3(64),
-                       0, s, p);
+    // a layer reading another layer's cache (no_kv) forms its queries only
+    hipLaunchKernelGGL(k_pre_plain_prologue, dim3(static_cast<unsigned>(p.ntok), static_cast<unsigned>(g.heads + (g.no_kv ? 0 : g.kv_heads))),
+                       dim3(64), 0, s, p);
     hipLaunchKernelGGL(k_pre_plain_attn, dim3(static_cast<unsigned>(p.ntok), static_cast<unsigned>(g.heads)), dim3(kThreads), 0, s, p);
     return hipGetLastError();
 }

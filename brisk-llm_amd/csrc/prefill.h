@@ -82,7 +82,16 @@ hipError_t launch_pre_quant(const float* x, int xstride, const float* w, float e
 hipError_t launch_pre_planar(const void* xq, int cols, int ntok, bool q8k, const ActPlanar& out, hipStream_t s);
 hipError_t launch_pre_embed(const Packed& m, const int* seq, int pos0, int ntok, float* h, float scale, hipStream_t s);
 // h[t] += rms_norm(p[t], w) for the ntok rows of n values (Gemma's post-norms)
-hipError_t launch_pre_post_add(float* h, const float* p, const float* w, float eps, int n, int ntok, hipStream_t s);
+// h[t] = (h[t] + rms_norm(p[t], w)) * out_scale (Gemma 4's per-layer embedding with its output scale)
+hipError_t launch_pre_post_add(float* h, const float* p, const float* w, float eps, int n, int ntok, hipStream_t s,
+                               float out_scale = 1.0f);
+// h *= out_scale over ntok rows of n values
+hipError_t launch_pre_scale(float* h, float out_scale, int n, int ntok, hipStream_t s);
+// Gemma 4's per-layer embedding inputs of tokens seq[pos0 ..] (src/model.cpp:905-925): in is [ntok][layers][dim]
+hipError_t launch_pre_ple_inputs(float* in, const Packed& table, const float* norm, const int* seq, int pos0, int ntok, int layers,
+                                 int dim, float proj_scale, float table_scale, float eps, hipStream_t s);
+// g[t][i] = gelu(g[t][i]) * in[t * in_stride + i], ntok rows of n
+hipError_t launch_pre_gelu_mul(float* g, const float* in, int n, int in_stride, int ntok, hipStream_t s);
 // LFM2's short convolution for ntok tokens at positions pos0 ..: bcx [ntok][3 n] in, out [ntok][n]
 hipError_t launch_pre_conv(const float* bcx, uint16_t* cache, const float* w, int taps, int pos0, int n, int ntok, float* out,
                            hipStream_t s);

@@ -1338,13 +1338,48 @@ __global__ void k_pre_embed(Packed m, const int* __restrict__ seq, int pos0, flo
 
 // h[t] += rms_norm(p[t], w) for every row t (src/model.cpp:1113-1121, :1153-1160): a workgroup a row.
 __global__ __launch_bounds__(kThreads) void k_pre_post_add(float* __restrict__ h, const float* __restrict__ p,
-                                                           const float* __restrict__ w, float eps, int n) {
+                                                           const float* __restrict__ w, float eps, int n, float out_scale) {
     __shared__ double red[4];
     const size_t off = static_cast<size_t>(blockIdx.x) * n;
     h += off;
     p += off;
     const float scale = rms_scale(block_sumsq(p, n, red), n, eps);
-    for (int i = threadIdx.x; i < n; i += kThreads) h[i] = h[i] + p[i] * scale * w[i];
+    // (x * 1.0f is x: out_scale 1 is the plain residual add)
+    for (int i = threadIdx.x; i < n; i += kThreads) h[i] = (h[i] + p[i] * scale * w[i]) * out_scale;
+}
+
+// h *= out_scale over ntok rows of n values (Gemma 4's layer output scale, src/model.cpp:1178-1181).
+__global__ void k_pre_scale(float* __restrict__ h, float out_scale, size_t count) {
+    const size_t i = static_cast<size_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (i < count) h[i] *= out_scale;
+}
+
+// Gemma 4's per-layer embedding inputs of token t (src/model.cpp:905-925), a workgroup per
+// (layer, token): slice (l, t) of in ([ntok][layers][dim], the per_layer_model_proj rows of the
+// scaled embedding) scaled by proj_scale, RMS-normed with norm, plus the token's row of the
+// per-layer table times table_scale, times 0.70710678.
+__global__ __launch_bounds__(kThreads) void k_pre_ple_inputs(float* __restrict__ in, Packed table, const float* __restrict__ norm,
+                                                             const int* __restrict__ seq, int pos0, int layers, int dim,
+                                                             float proj_scale, float table_scale, float eps) {
+    __shared__ double red[4];
+    const int l = blockIdx.x, t = blockIdx.y;
+    float* slice = in + (static_cast<size_t>(t) * layers + l) * dim;
+    const uint32_t tok = static_cast<uint32_t>(seq[pos0 + t]);
+    for (int i = threadIdx.x; i < dim; i += kThreads) slice[i] = slice[i] * proj_scale;
+    __syncthreads();
+    const float scale = rms_scale(block_sumsq(slice, dim, red), dim, eps);
+    for (int i = threadIdx.x; i < dim; i += kThreads) {
+        const float row = dequant_elem(table, tok, static_cast<uint32_t>(l * dim + i));
+        slice[i] = (slice[i] * scale * norm[i] + row * table_scale) * 0.70710678f;
+    }
+}
+
+// g[t][i] = gelu(g[t][i]) * in[t * in_stride + i] over ntok rows of n (gelu_mul_f32, src/kernels_f32.cpp:291-296).
+__global__ void k_pre_gelu_mul(float* __restrict__ g, const float* __restrict__ in, int n, int in_stride, int ntok) {
+    const size_t i = static_cast<size_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (i >= static_cast<size_t>(n) * ntok) return;
+    const size_t t = i / n, c = i - t * n;
+    g[i] = gelu_mul(g[i], in[t * in_stride + c]);
 }
 
 // LFM2 short convolution over ntok tokens at positions pos0 .. (src/model.cpp:935-969): for each
@@ -2214,9 +2249,34 @@ hipError_t launch_pre_embed(const Packed& m, const int* seq, int pos0, int ntok,
     return hipGetLastError();
 }
 
-hipError_t launch_pre_post_add(float* h, const float* p, const float* w, float eps, int n, int ntok, hipStream_t s) {
+hipError_t launch_pre_post_add(float* h, const float* p, const float* w, float eps, int n, int ntok, hipStream_t s, float out_scale) {
     if (ntok <= 0) return hipSuccess;
-    hipLaunchKernelGGL(k_pre_post_add, dim3(ntok), dim3(kThreads), 0, s, h, p, w, eps, n);
+    hipLaunchKernelGGL(k_pre_post_add, dim3(ntok), dim3(kThreads), 0, s, h, p, w, eps, n, out_scale);
+    return hipGetLastError();
+}
+
+hipError_t launch_pre_scale(float* h, float out_scale, int n, int ntok, hipStream_t s) {
+    const size_t count = static_cast<size_t>(n) * ntok;
+    if (count == 0) return hipSuccess;
+    hipLaunchKernelGGL(k_pre_scale, dim3(static_cast<unsigned>((count + kThreads - 1) / kThreads)), dim3(kThreads), 0, s, h, out_scale,
+                       count);
+    return hipGetLastError();
+}
+
+hipError_t launch_pre_ple_inputs(float* in, const Packed& table, const float* norm, const int* seq, int pos0, int ntok, int layers,
+                                 int dim, float proj_scale, float table_scale, float eps, hipStream_t s) {
+    if (ntok <= 0) return hipSuccess;
+    if (layers < 1 || dim < 1 || static_cast<size_t>(layers) * dim != table.cols) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_pre_ple_inputs, dim3(static_cast<unsigned>(layers), static_cast<unsigned>(ntok)), dim3(kThreads), 0, s, in,
+                       table, norm, seq, pos0, layers, dim, proj_scale, table_scale, eps);
+    return hipGetLastError();
+}
+
+hipError_t launch_pre_gelu_mul(float* g, const float* in, int n, int in_stride, int ntok, hipStream_t s) {
+    const size_t count = static_cast<size_t>(n) * ntok;
+    if (count == 0) return hipSuccess;
+    hipLaunchKernelGGL(k_pre_gelu_mul, dim3(static_cast<unsigned>((count + kThreads - 1) / kThreads)), dim3(kThreads), 0, s, g, in, n,
+                       in_stride, ntok);
     return hipGetLastError();
 }
 

@@ -197,6 +197,8 @@ brisk_hip_memory estimate_session(const brisk_hip_config& cfg, const brisk_hip_t
     sc += T * (e + 2 * qd + 2 * kvd + ff) * 4 + T * stride * (1 + 4 / 32.0 + 4 / 16.0);  // prefill buffers
     if (cfg.arch == BRISK_HIP_ARCH_GEMMA3 || cfg.arch == BRISK_HIP_ARCH_LFM2) sc += T * e * 4;  // post-norm inputs, conv outputs
     if (cfg.arch == BRISK_HIP_ARCH_LFM2) sc += T * 3 * e * 4;                                   // prefill conv rows
+    if (cfg.arch == BRISK_HIP_ARCH_GEMMA4)  // prefill per-layer embedding inputs and gate rows
+        sc += T * static_cast<size_t>(cfg.ple_dim) * (cfg.layers + 1) * 4;
     if (cfg.arch == BRISK_HIP_ARCH_QWEN35)  // prefill recurrence rows, query|gate rows, the wider attention output
         sc += T * (5 * static_cast<size_t>(cfg.ssm_inner) + 2 * cfg.ssm_v_heads + 2 * qd) * 4;
     sc += static_cast<size_t>(64) * cfg.vocab * 4;                         // eval_all logits
@@ -607,9 +609,10 @@ Session::Session(const brisk_hip_config& cfg, const brisk_hip_tensor* tensors, s
         prefill_on_ = !(pf != nullptr && std::string(pf) == "0") && !debug_;
         for (const Layer& L : layers_)  // the batched GEMMs stage their rows in 256-value chunks
             for (const DeviceMatrix* m : {&L.q, &L.k, &L.v, &L.o, &L.gate, &L.up, &L.down, &L.conv_in, &L.conv_out, &L.ssm_qkv,
-                                          &L.ssm_gate, &L.ssm_alpha, &L.ssm_beta, &L.ssm_out})
+                                          &L.ssm_gate, &L.ssm_alpha, &L.ssm_beta, &L.ssm_out, &L.ple_gate, &L.ple_proj})
                 if (m->mem != nullptr && m->p.cols % kMmChunkCols != 0) prefill_shapes_ = false;
         if (out_->p.cols % kMmChunkCols != 0) prefill_shapes_ = false;
+        if (ple_proj_.mem != nullptr && ple_proj_.p.cols % kMmChunkCols != 0) prefill_shapes_ = false;
         prefill_on_ = prefill_on_ && prefill_shapes_;
         const char* pa = std::getenv("BRISK_HIP_PREFILL_ATTN");  // "mfma": long prompts' attention on f16 MFMA
         prefill_mfma_ = pa != nullptr && std::string(pa) == "mfma";
@@ -1198,7 +1201,7 @@ bool Session::use_prefill(size_t n) const {
         return prefill_on_ && n >= 2 && pre_ssm_fits(static_cast<int>(cfg_.ssm_state)) && pre_plain_fits(static_cast<int>(position_ + n));
     // the plain attention batched (contexts of its LDS window); Gemma 4's per-layer shapes and
     // per-layer embeddings take their prompts token by token
-    if (plain_attn_) return prefill_on_ && n >= 2 && !gemma4() && pre_plain_fits(static_cast<int>(position_ + n));
+    if (plain_attn_) return prefill_on_ && n >= 2 && pre_plain_fits(static_cast<int>(position_ + n));
     if (gemma() || lfm2()) return prefill_on_ && n >= 2 && exact_fits && cfg_.head_dim <= 128;
     return prefill_on_ && n >= 2 && (exact_fits || mfma_fits);
 }
@@ -1215,6 +1218,10 @@ void Session::ensure_prefill() {
     pre_act_ = static_cast<float*>(alloc(T * ff * 4));
     if (gemma() || lfm2()) pre_proj_ = static_cast<float*>(alloc(T * e * 4));  // post-norm inputs; conv outputs
     if (lfm2()) pre_conv_ = static_cast<float*>(alloc(T * 3 * e * 4));           // LFM2's [b | c | x] rows
+    if (cfg_.ple_dim != 0) {  // Gemma 4's per-layer embedding inputs [T][layers][ple_dim] and gate rows
+        pre_ple_ = static_cast<float*>(alloc(T * cfg_.ple_dim * cfg_.layers * 4));
+        pre_pleg_ = static_cast<float*>(alloc(T * cfg_.ple_dim * 4));
+    }
     if (qwen35()) {
         const size_t inner = cfg_.ssm_inner, heads = cfg_.ssm_v_heads;
         pre_sqkv_ = static_cast<float*>(alloc(T * 3 * inner * 4));
@@ -1229,7 +1236,7 @@ void Session::ensure_prefill() {
     pre_x_.bs = static_cast<int32_t*>(alloc(T * (pre_x_.stride / 16) * 4));
     for (Layer& L : layers_)
         for (DeviceMatrix* m : {&L.q, &L.k, &L.v, &L.o, &L.gate, &L.up, &L.down, &L.conv_in, &L.conv_out, &L.ssm_qkv, &L.ssm_gate,
-                                &L.ssm_alpha, &L.ssm_beta, &L.ssm_out})
+                                &L.ssm_alpha, &L.ssm_beta, &L.ssm_out, &L.ple_gate, &L.ple_proj})
             if (m->mem != nullptr && mx_expanded(m->p.type) && m->xmem == nullptr) {
                 check(hipMalloc(&m->xmem, mx_bytes(m->p.type, m->p.rows, m->p.cols)), "hipMalloc(expanded planes)");
                 check(launch_mx_expand(m->p, m->xmem, &m->x, stream_), "expand planes");
@@ -1249,6 +1256,17 @@ void Session::prefill_layers(size_t pos0, int T) {
     const int e = static_cast<int>(cfg_.embd), qd = static_cast<int>(cfg_.heads * cfg_.head_dim),
               kvd = static_cast<int>(cfg_.kv_heads * cfg_.head_dim), ff = static_cast<int>(cfg_.ff);
     check(launch_pre_embed(embd_.p, seq_, static_cast<int>(pos0), T, pre_h_, embd_scale_, stream_), "prefill embed");
+    if (cfg_.ple_dim != 0) {  // Gemma 4's per-layer embedding inputs (src/model.cpp:905-925)
+        prefill_quant(pre_h_, e, nullptr, e, T, ple_proj_);
+        MmArgs pg{};
+        pg.x = pre_x_; pg.ntok = T; pg.m = ple_proj_.p; set_mx(pg, ple_proj_); pg.out = pre_ple_;
+        pg.ostride = static_cast<int>(cfg_.ple_dim * cfg_.layers);
+        check(launch_mm(pg, kMmStore, stream_), "prefill per-layer projection of the embedding");
+        check(launch_pre_ple_inputs(pre_ple_, ple_tok_.p, ple_norm_, seq_, static_cast<int>(pos0), T, static_cast<int>(cfg_.layers),
+                                    static_cast<int>(cfg_.ple_dim), 1.0f / std::sqrt(static_cast<float>(cfg_.embd)),
+                                    std::sqrt(static_cast<float>(cfg_.ple_dim)), cfg_.rms_epsilon, stream_),
+              "prefill per-layer inputs");
+    }
     for (uint32_t l = 0; l < cfg_.layers; ++l) {
         const Layer& L = layers_[l];
         MmArgs g{};
@@ -1311,19 +1329,26 @@ void Session::prefill_layers(size_t pos0, int T) {
             g.m = L.conv_out.p; set_mx(g, L.conv_out); g.out = pre_h_; g.ostride = e;
             check(launch_mm(g, kMmAdd, stream_), "prefill conv out_proj");
         } else {
-            // Q, K, V of attn_norm(h) (src/model.cpp:996-1015)
+            // Q, K, V of attn_norm(h) (src/model.cpp:996-1015), at the layer's head size and key/value
+            // heads (Gemma 4: a shared layer projects Q only; K may serve as V)
+            const int qdl = static_cast<int>(cfg_.heads) * L.hd, kvdl = L.kvh * L.hd;
+            const bool own_kv = L.kv_src == static_cast<int>(l);
             prefill_quant(pre_h_, e, L.attn_norm, e, T, L.q);
-            g.m = L.q.p; set_mx(g, L.q); g.out = pre_q_; g.ostride = qd;
+            g.m = L.q.p; set_mx(g, L.q); g.out = pre_q_; g.ostride = qdl;
             check(launch_mm(g, kMmStore, stream_), "prefill q");
-            g.m = L.k.p; set_mx(g, L.k); g.out = pre_k_; g.ostride = kvd;
-            check(launch_mm(g, kMmStore, stream_), "prefill k");
-            g.m = L.v.p; set_mx(g, L.v); g.out = pre_v_; g.ostride = kvd;
-            check(launch_mm(g, kMmStore, stream_), "prefill v");
+            if (own_kv) {
+                g.m = L.k.p; set_mx(g, L.k); g.out = pre_k_; g.ostride = kvdl;
+                check(launch_mm(g, kMmStore, stream_), "prefill k");
+                if (!L.v_is_k) {
+                    g.m = L.v.p; set_mx(g, L.v); g.out = pre_v_; g.ostride = kvdl;
+                    check(launch_mm(g, kMmStore, stream_), "prefill v");
+                }
+            }
             // norms, RoPE, cache rows, attention (:1020-1093)
             if (plain_attn_) {  // heads past 128 (or BRISK_HIP_ATTN=plain): the plain attention batched
                 PrePlainArgs pp{};
                 AttnArgs& aa = pp.a;
-                aa.q = pre_q_; aa.k = pre_k_; aa.v = pre_v_; aa.qnorm = L.q_norm; aa.knorm = L.k_norm;
+                aa.q = pre_q_; aa.k = pre_k_; aa.v = L.v_is_k ? pre_k_ : pre_v_; aa.qnorm = L.q_norm; aa.knorm = L.k_norm;
                 aa.rope = !L.rope ? nullptr : L.slides ? rope_local_ : rope_;
                 aa.window = L.slides ? static_cast<int>(cfg_.sliding_window) : 0;
                 aa.rope_dim = L.slides ? L.hd : std::min(rope_dim_, L.hd);
@@ -1331,10 +1356,12 @@ void Session::prefill_layers(size_t pos0, int T) {
                 aa.eps = cfg_.rms_epsilon; aa.neox = neox();
                 aa.kcache = kcache_[l]; aa.vcache = vcache_[l]; aa.ctx = static_cast<int>(max_ctx_); aa.head_dim = L.hd;
                 aa.heads = static_cast<int>(cfg_.heads); aa.kv_heads = L.kvh;
-                aa.scale = 1.0f / std::sqrt(static_cast<float>(L.hd));  // src/model.cpp:978
+                aa.vnorm = cfg_.value_norm; aa.no_kv = own_kv ? 0 : 1;
+                // src/model.cpp:978: the family's scale, else 1 / sqrt(the layer's head size)
+                aa.scale = cfg_.attention_scale != 0.0f ? cfg_.attention_scale : 1.0f / std::sqrt(static_cast<float>(L.hd));
                 // the queries normed in place (one wave owns each token's head, reading it whole first)
                 aa.qn = pre_q_; aa.out = pre_att_;
-                pp.pos0 = static_cast<int>(pos0); pp.ntok = T; pp.q_tok = qd; pp.kv_tok = kvd;
+                pp.pos0 = static_cast<int>(pos0); pp.ntok = T; pp.q_tok = qdl; pp.kv_tok = kvdl;
                 check(launch_pre_attention_plain(pp, stream_), "prefill attention");
             } else {
             PreAttnArgs pa{};
@@ -1355,7 +1382,7 @@ void Session::prefill_layers(size_t pos0, int T) {
             check(launch_pre_attention(pa, T, stream_), "prefill attention");
             }
             // h += O (sub-normed) att (:1095-1111)
-            prefill_quant(pre_att_, qd, L.attn_sub_norm, qd, T, L.o);
+            prefill_quant(pre_att_, qdl, L.attn_sub_norm, qdl, T, L.o);
             g.m = L.o.p; set_mx(g, L.o); g.out = L.attn_post_norm ? pre_proj_ : pre_h_; g.ostride = e;
             check(launch_mm(g, L.attn_post_norm ? kMmStore : kMmAdd, stream_), "prefill o");
             if (L.attn_post_norm)  // h += rms_norm(O att, post_attention_norm) (:1113-1121)
@@ -1366,13 +1393,27 @@ void Session::prefill_layers(size_t pos0, int T) {
         g.m = L.gate.p; g.m2 = L.up.p; set_mx(g, L.gate); set_mx2(g, L.up); g.out = pre_act_; g.ostride = ff; g.relu2 = cfg_.arch == BRISK_HIP_ARCH_BITNET;
         g.gelu = gemma();
         check(launch_mm(g, kMmPair, stream_), "prefill gate/up");
-        // h += down (sub-normed) act (:1144-1162)
-        prefill_quant(pre_act_, ff, L.ffn_sub_norm, ff, T, L.down);
+        // h += down (sub-normed) act (:1144-1162); Gemma 4's rows are the layer's width at stride ff
+        prefill_quant(pre_act_, ff, L.ffn_sub_norm, L.ff, T, L.down);
         g.m = L.down.p; set_mx(g, L.down); g.out = L.ffn_post_norm ? pre_proj_ : pre_h_; g.ostride = e;
         g.relu2 = 0; g.gelu = 0;
         check(launch_mm(g, L.ffn_post_norm ? kMmStore : kMmAdd, stream_), "prefill down");
         if (L.ffn_post_norm)  // h += rms_norm(down act, post_ffw_norm) (:1153-1160)
             check(launch_pre_post_add(pre_h_, pre_proj_, L.ffn_post_norm, cfg_.rms_epsilon, e, T, stream_), "prefill post norm");
+        if (cfg_.ple_dim != 0) {  // h = (h + norm(proj(gelu(gate h) * input l))) * scale (src/model.cpp:1163-1177)
+            const int pd = static_cast<int>(cfg_.ple_dim), pall = pd * static_cast<int>(cfg_.layers);
+            prefill_quant(pre_h_, e, nullptr, e, T, L.ple_gate);
+            g.m = L.ple_gate.p; set_mx(g, L.ple_gate); g.out = pre_pleg_; g.ostride = pd;
+            check(launch_mm(g, kMmStore, stream_), "prefill per-layer gate");
+            check(launch_pre_gelu_mul(pre_pleg_, pre_ple_ + static_cast<size_t>(l) * pd, pd, pall, T, stream_), "prefill per-layer gelu");
+            prefill_quant(pre_pleg_, pd, nullptr, pd, T, L.ple_proj);
+            g.m = L.ple_proj.p; set_mx(g, L.ple_proj); g.out = pre_proj_; g.ostride = e;
+            check(launch_mm(g, kMmStore, stream_), "prefill per-layer projection");
+            check(launch_pre_post_add(pre_h_, pre_proj_, L.ple_post_norm, cfg_.rms_epsilon, e, T, stream_, L.out_scale),
+                  "prefill per-layer norm");
+        } else if (L.out_scale != 1.0f) {
+            check(launch_pre_scale(pre_h_, L.out_scale, e, T, stream_), "prefill layer scale");
+        }
     }
 }
 

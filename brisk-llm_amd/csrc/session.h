@@ -190,6 +190,7 @@ private:
     float* pre_conv_ = nullptr;  // LFM2: in_proj rows [b | c | x]
     // Qwen3.5: the recurrence's projections [T][qkv], [T][inner], [T][alpha | beta]; the query|gate rows
     float *pre_sqkv_ = nullptr, *pre_sz_ = nullptr, *pre_sab_ = nullptr, *pre_qg_ = nullptr;
+    float *pre_ple_ = nullptr, *pre_pleg_ = nullptr;  // Gemma 4: per-layer embedding inputs and gate rows
     ActPlanar pre_x_{};
     float* all_logits_ = nullptr;  // eval_all's [64][vocab] logits, allocated on first use
     hipGraphExec_t graph_layers_ = nullptr, graph_full_ = nullptr;
