@@ -831,11 +831,30 @@ __device__ __forceinline__ float value_chain(const float* w, const uint16_t* vro
         asm volatile("ds_read_b128 %0, %1" : "=v"(r.v) : "v"(vb + 2 * qc));
         return r;
     };
+    // one round: the eight products (v_fma_mix_f32, as mul_h) issued ahead of their adds, in one
+    // asm block so each add's product is formed while the add before it completes
     auto sum = [&](const Round& r) {
-        acc += mul_h<false>(r.w0.x, r.v.x); acc += mul_h<true>(r.w0.y, r.v.x);
-        acc += mul_h<false>(r.w0.z, r.v.y); acc += mul_h<true>(r.w0.w, r.v.y);
-        acc += mul_h<false>(r.w1.x, r.v.z); acc += mul_h<true>(r.w1.y, r.v.z);
-        acc += mul_h<false>(r.w1.z, r.v.w); acc += mul_h<true>(r.w1.w, r.v.w);
+        float p0, p1, p2, p3, p4, p5, p6, p7;
+        asm volatile(
+            "v_fma_mix_f32 %1, %9, %17, %19 op_sel_hi:[0,1,0]\n\t"
+            "v_fma_mix_f32 %2, %10, %17, %19 op_sel:[0,1,0] op_sel_hi:[0,1,0]\n\t"
+            "v_fma_mix_f32 %3, %11, %18, %19 op_sel_hi:[0,1,0]\n\t"
+            "v_add_f32 %0, %0, %1\n\t"
+            "v_fma_mix_f32 %4, %12, %18, %19 op_sel:[0,1,0] op_sel_hi:[0,1,0]\n\t"
+            "v_add_f32 %0, %0, %2\n\t"
+            "v_fma_mix_f32 %5, %13, %20, %19 op_sel_hi:[0,1,0]\n\t"
+            "v_add_f32 %0, %0, %3\n\t"
+            "v_fma_mix_f32 %6, %14, %20, %19 op_sel:[0,1,0] op_sel_hi:[0,1,0]\n\t"
+            "v_add_f32 %0, %0, %4\n\t"
+            "v_fma_mix_f32 %7, %15, %21, %19 op_sel_hi:[0,1,0]\n\t"
+            "v_add_f32 %0, %0, %5\n\t"
+            "v_fma_mix_f32 %8, %16, %21, %19 op_sel:[0,1,0] op_sel_hi:[0,1,0]\n\t"
+            "v_add_f32 %0, %0, %6\n\t"
+            "v_add_f32 %0, %0, %7\n\t"
+            "v_add_f32 %0, %0, %8"
+            : "+v"(acc), "=&v"(p0), "=&v"(p1), "=&v"(p2), "=&v"(p3), "=&v"(p4), "=&v"(p5), "=&v"(p6), "=&v"(p7)
+            : "v"(r.w0.x), "v"(r.w0.y), "v"(r.w0.z), "v"(r.w0.w), "v"(r.w1.x), "v"(r.w1.y), "v"(r.w1.z), "v"(r.w1.w),
+              "v"(r.v.x), "v"(r.v.y), "v"(-0.0f), "v"(r.v.z), "v"(r.v.w));
     };
     if (full <= p) return acc;
     // rounds at p, p + 8, ...: ra and rb hold the next two; three rounds an iteration, the names
