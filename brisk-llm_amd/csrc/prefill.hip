@@ -48,6 +48,112 @@ __global__ __launch_bounds__(kThreads) void k_pre_quant(const float* __restrict_
     for (int i = threadIdx.x; i < cols / 16; i += kThreads) bs[i] = a.xsum[i];
 }
 
+// quantize_q8_k / quantize_q8_0 (src/quant.cpp:115-194) of 256-value block b of token t's row,
+// by one wave: lane l holds values 4 l .. 4 l + 3 of the block (the mapping, and so every
+// operation, of quant_piece_q8_k / quant_piece_q8_0), straight into the planar layout.
+template <bool Q8K>
+__device__ __forceinline__ void pre_quant_block(const float (&v)[4], int t, int b, int bits, const ActPlanar& out) {
+    const int lane = threadIdx.x & 63, base = b * 256 + 4 * lane;
+    int q[4];
+    if constexpr (Q8K) {
+        float amax = -1.0f, sel = 0.0f;
+        int idx = 0;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const float av = fabsf(v[i]);
+            if (av > amax) { amax = av; idx = lane * 4 + i; sel = v[i]; }
+        }
+        {
+            const AbsMax m = wave_absmax(AbsMax{amax, idx, sel});
+            amax = m.amax; sel = m.sel;
+        }
+        float d;
+        if (amax == 0.0f) {
+            d = 0.0f;
+            q[0] = q[1] = q[2] = q[3] = 0;
+        } else {
+            const float extreme = bits == 7 ? 63.0f : 127.0f;
+            const float inv = -extreme / sel;
+            d = rcp_rn(inv);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) q[i] = static_cast<int>(fminf(127.0f, rintf(inv * v[i])));
+        }
+        int sm = q[0] + q[1] + q[2] + q[3];
+        sm = group_reduce<4>(sm, [](int a, int c) { return a + c; });
+        if ((lane & 3) == 0) out.bs[static_cast<size_t>(t) * (out.stride / 16) + base / 16] = static_cast<int16_t>(sm);  // bsums are int16
+        if (lane == 0) out.d[static_cast<size_t>(t) * (out.stride / 32) + b] = d;
+    } else {
+        float amax = nnmax(nnmax(fabsf(v[0]), fabsf(v[1])), nnmax(fabsf(v[2]), fabsf(v[3])));
+        amax = group_reduce<8>(amax, [](float a, float c) { return nnmax(a, c); });
+        const float d = div127(amax);
+        const float inv = d != 0.0f ? rcp_rn(d) : 0.0f;
+        int sm = 0;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            q[i] = static_cast<int>(rintf(v[i] * inv));
+            sm += q[i];
+        }
+        sm = group_reduce<8>(sm, [](int a, int c) { return a + c; });
+        if ((lane & 7) == 0) {
+            out.d[static_cast<size_t>(t) * (out.stride / 32) + base / 32] = h2f(f2h(d));
+            out.bs[static_cast<size_t>(t) * (out.stride / 16) + base / 32] = sm;
+        }
+    }
+    *reinterpret_cast<int32_t*>(out.qs + static_cast<size_t>(t) * out.stride + base) =
+        (q[0] & 0xFF) | ((q[1] & 0xFF) << 8) | ((q[2] & 0xFF) << 16) | (q[3] << 24);
+}
+
+// Rows with no norm: a wave per (token, 256-value block), four a workgroup.
+template <bool Q8K>
+__global__ __launch_bounds__(kThreads) void k_pre_quant_blocks(const float* __restrict__ x, int xstride, int cols, int bits, ActPlanar out,
+                                                                int ntok) {
+    const int nb = cols / 256, g = blockIdx.x * 4 + (threadIdx.x >> 6), t = g / nb, b = g - t * nb;
+    if (t >= ntok) return;
+    const float4 xv = gld4(x + static_cast<size_t>(t) * xstride + b * 256 + 4 * (threadIdx.x & 63));
+    const float v[4] = {xv.x, xv.y, xv.z, xv.w};
+    pre_quant_block<Q8K>(v, t, b, bits, out);
+}
+
+// rms_norm'd rows (src/model.cpp:87-97): a workgroup per token, wave k taking blocks k, k + 4, ...
+// The double sum of squares is grouped as the token path's act_finish groups it (thread 64 k + l
+// sums its four values of each of those blocks in order; each wave's sums reduced over the wave,
+// then the four added in order), so the scale, and every output, is that path's.  The outputs go
+// straight to the planar layout; no width limit (a multiple of 256).
+template <bool Q8K>
+__global__ __launch_bounds__(kThreads) void k_pre_quant_norm(const float* __restrict__ x, int xstride, const float* __restrict__ w,
+                                                              float eps, int cols, int bits, ActPlanar out) {
+    __shared__ double red[4];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, t = blockIdx.x, nb = cols / 256;
+    const float* row = x + static_cast<size_t>(t) * xstride;
+    constexpr int kHeld = 4;  // blocks a wave keeps in registers between the two passes (rows up to 4096 values)
+    float4 held[kHeld];
+    double sq = 0.0;
+#pragma unroll
+    for (int k = 0; k < kHeld; ++k) {
+        const int b = wave + 4 * k;
+        if (b < nb) {
+            held[k] = gld4(row + b * 256 + 4 * lane);
+            sq += static_cast<double>(held[k].x * held[k].x); sq += static_cast<double>(held[k].y * held[k].y);
+            sq += static_cast<double>(held[k].z * held[k].z); sq += static_cast<double>(held[k].w * held[k].w);
+        }
+    }
+    for (int b = wave + 4 * kHeld; b < nb; b += 4) {
+        const float4 v = gld4(row + b * 256 + 4 * lane);
+        sq += static_cast<double>(v.x * v.x); sq += static_cast<double>(v.y * v.y);
+        sq += static_cast<double>(v.z * v.z); sq += static_cast<double>(v.w * v.w);
+    }
+    sq = wave_sum(sq);
+    if (lane == 0) red[wave] = sq;
+    __syncthreads();
+    const float scale = rms_scale(((red[0] + red[1]) + red[2]) + red[3], cols, eps);
+    for (int k = 0, b = wave; b < nb; ++k, b += 4) {
+        const float4 xv = k < kHeld ? held[k < kHeld ? k : 0] : gld4(row + b * 256 + 4 * lane);
+        const float4 wv = gld4(w + b * 256 + 4 * lane);
+        const float v[4] = {xv.x * scale * wv.x, xv.y * scale * wv.y, xv.z * scale * wv.z, xv.w * scale * wv.w};
+        pre_quant_block<Q8K>(v, t, b, bits, out);
+    }
+}
+
 // GGUF BlockQ8_0 / BlockQ8_K rows (the kernel-level ABI's activation format) into the planar layout.
 __global__ void k_pre_planar(const uint8_t* __restrict__ xq, int cols, int q8k, ActPlanar out) {
     const int t = blockIdx.x;
@@ -2233,7 +2339,19 @@ hipError_t launch_mx_expand(const Packed& m, void* mem, MxPlanes* out, hipStream
 hipError_t launch_pre_quant(const float* x, int xstride, const float* w, float eps, int cols, int ntok, bool q8k, int bits,
                             const ActPlanar& out, hipStream_t s) {
     if (ntok <= 0) return hipSuccess;
-    hipLaunchKernelGGL(k_pre_quant, dim3(ntok), dim3(kThreads), 0, s, x, xstride, w, eps, cols, q8k ? 1 : 0, bits, out);
+    if (cols % 256 != 0) {  // a workgroup a row (rows of whole 32-value blocks, up to kMaxCols)
+        hipLaunchKernelGGL(k_pre_quant, dim3(ntok), dim3(kThreads), 0, s, x, xstride, w, eps, cols, q8k ? 1 : 0, bits, out);
+        return hipGetLastError();
+    }
+    if (w != nullptr) {
+        if (q8k) hipLaunchKernelGGL(k_pre_quant_norm<true>, dim3(ntok), dim3(kThreads), 0, s, x, xstride, w, eps, cols, bits, out);
+        else hipLaunchKernelGGL(k_pre_quant_norm<false>, dim3(ntok), dim3(kThreads), 0, s, x, xstride, w, eps, cols, bits, out);
+    } else {
+        const size_t waves = static_cast<size_t>(ntok) * (cols / 256);
+        const dim3 grid(static_cast<unsigned>((waves + 3) / 4));
+        if (q8k) hipLaunchKernelGGL(k_pre_quant_blocks<true>, grid, dim3(kThreads), 0, s, x, xstride, cols, bits, out, ntok);
+        else hipLaunchKernelGGL(k_pre_quant_blocks<false>, grid, dim3(kThreads), 0, s, x, xstride, cols, bits, out, ntok);
+    }
     return hipGetLastError();
 }
 
