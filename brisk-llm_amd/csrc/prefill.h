@@ -75,6 +75,9 @@ inline bool pre_attn_mfma_fits(int hpk, int head_dim) {
 }
 
 hipError_t launch_mm(const MmArgs& g, int mode, hipStream_t s);
+// Two store GEMMs of one activation (Q and K): one launch when both are packed-plane Q4_K of one
+// width, else launch_mm of each.
+hipError_t launch_mm_two(const MmArgs& a, const MmArgs& b, hipStream_t s);
 // The GEMMs take rows whose length is a multiple of this many values (one staged chunk).
 constexpr int kMmChunkCols = 256;
 hipError_t launch_pre_quant(const float* x, int xstride, const float* w, float eps, int cols, int ntok, bool q8k, int bits,

@@ -1276,11 +1276,21 @@ __global__ __launch_bounds__(64 * W) void k_mmx(MmArgs g) {
     }
 }
 
-template <uint32_t T, int MODE, int G>
-__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 8))) void k_mmk(MmArgs g) {
+// TWO: one launch for two store GEMMs of one activation (the same format and width; Q and K):
+// row tiles 0 .. of ga's rows, then gb's, each workgroup writing its own matrix's output.
+template <uint32_t T, int MODE, int G, bool TWO = false>
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 8))) void k_mmk(MmArgs ga, MmArgs gb) {
     __shared__ KqStage<T> st[2];
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    const uint32_t rt0 = blockIdx.x * 64;
+    const uint32_t rta = (ga.m.rows + 63) / 64;
+    const bool second = TWO && blockIdx.x >= rta;
+    MmArgs g = ga;
+    if (second) {
+        g.m = gb.m;
+        g.out = gb.out;
+        g.ostride = gb.ostride;
+    }
+    const uint32_t rt0 = (second ? blockIdx.x - rta : blockIdx.x) * 64;
     const int t0 = blockIdx.y * (16 * G);
     const int nc = static_cast<int>(g.m.cols / 256);
     MmAcc<G> a;
@@ -2243,18 +2253,18 @@ static hipError_t mm_dispatch(const MmArgs& g, hipStream_t s) {
                 mmx_launch<MODE, true>(g, s);
                 break;
             }
-            if (kq_g == 4) hipLaunchKernelGGL((k_mmk<kQ4_K, MODE, 4>), kq_grid, dim3(kThreads), 0, s, g);
-            else if (kq_g == 2) hipLaunchKernelGGL((k_mmk<kQ4_K, MODE, 2>), kq_grid, dim3(kThreads), 0, s, g);
-            else hipLaunchKernelGGL((k_mmk<kQ4_K, MODE, 1>), kq_grid, dim3(kThreads), 0, s, g);
+            if (kq_g == 4) hipLaunchKernelGGL((k_mmk<kQ4_K, MODE, 4>), kq_grid, dim3(kThreads), 0, s, g, g);
+            else if (kq_g == 2) hipLaunchKernelGGL((k_mmk<kQ4_K, MODE, 2>), kq_grid, dim3(kThreads), 0, s, g, g);
+            else hipLaunchKernelGGL((k_mmk<kQ4_K, MODE, 1>), kq_grid, dim3(kThreads), 0, s, g, g);
             break;
         case kQ6_K:
             if (g.qx != nullptr) {
                 mmx_launch<MODE, false>(g, s);
                 break;
             }
-            if (kq_g == 4) hipLaunchKernelGGL((k_mmk<kQ6_K, MODE, 4>), kq_grid, dim3(kThreads), 0, s, g);
-            else if (kq_g == 2) hipLaunchKernelGGL((k_mmk<kQ6_K, MODE, 2>), kq_grid, dim3(kThreads), 0, s, g);
-            else hipLaunchKernelGGL((k_mmk<kQ6_K, MODE, 1>), kq_grid, dim3(kThreads), 0, s, g);
+            if (kq_g == 4) hipLaunchKernelGGL((k_mmk<kQ6_K, MODE, 4>), kq_grid, dim3(kThreads), 0, s, g, g);
+            else if (kq_g == 2) hipLaunchKernelGGL((k_mmk<kQ6_K, MODE, 2>), kq_grid, dim3(kThreads), 0, s, g, g);
+            else hipLaunchKernelGGL((k_mmk<kQ6_K, MODE, 1>), kq_grid, dim3(kThreads), 0, s, g, g);
             break;
         case kTQ2_0: hipLaunchKernelGGL((k_mm<kTQ2_0, MODE>), grid, dim3(kThreads), 0, s, g); break;
         default: return hipErrorInvalidValue;
@@ -2298,6 +2308,25 @@ hipError_t launch_mm(const MmArgs& g, int mode, hipStream_t s) {
         }
         default: return hipErrorInvalidValue;
     }
+}
+
+hipError_t launch_mm_two(const MmArgs& a, const MmArgs& b, hipStream_t s) {
+    if (a.ntok <= 0) return hipSuccess;
+    const bool fuse = a.m.type == kQ4_K && b.m.type == kQ4_K && a.m.cols == b.m.cols && a.qx == nullptr && b.qx == nullptr &&
+                      a.ntok == b.ntok && a.x.qs == b.x.qs && a.m.cols % kChunkCols == 0 && a.x.stride % kChunkCols == 0;
+    if (!fuse) {
+        const hipError_t e = launch_mm(a, kMmStore, s);
+        return e != hipSuccess ? e : launch_mm(b, kMmStore, s);
+    }
+    // the widest token tile that still gives a workgroup to every CU, over both matrices' row tiles
+    const int row_tiles = static_cast<int>((a.m.rows + 63) / 64 + (b.m.rows + 63) / 64);
+    int kq_g = 4;
+    while (kq_g > 1 && row_tiles * ((a.ntok + 16 * kq_g - 1) / (16 * kq_g)) < kKqCus) kq_g /= 2;
+    const dim3 grid(row_tiles, (a.ntok + 16 * kq_g - 1) / (16 * kq_g));
+    if (kq_g == 4) hipLaunchKernelGGL((k_mmk<kQ4_K, kMmStore, 4, true>), grid, dim3(kThreads), 0, s, a, b);
+    else if (kq_g == 2) hipLaunchKernelGGL((k_mmk<kQ4_K, kMmStore, 2, true>), grid, dim3(kThreads), 0, s, a, b);
+    else hipLaunchKernelGGL((k_mmk<kQ4_K, kMmStore, 1, true>), grid, dim3(kThreads), 0, s, a, b);
+    return hipGetLastError();
 }
 
 static bool mx_km(uint32_t type) { return type == kQ4_K || type == kQ5_K; }

@@ -1335,14 +1335,16 @@ void Session::prefill_layers(size_t pos0, int T) {
             const bool own_kv = L.kv_src == static_cast<int>(l);
             prefill_quant(pre_h_, e, L.attn_norm, e, T, L.q);
             g.m = L.q.p; set_mx(g, L.q); g.out = pre_q_; g.ostride = qdl;
-            check(launch_mm(g, kMmStore, stream_), "prefill q");
-            if (own_kv) {
-                g.m = L.k.p; set_mx(g, L.k); g.out = pre_k_; g.ostride = kvdl;
-                check(launch_mm(g, kMmStore, stream_), "prefill k");
+            if (own_kv) {  // Q and K in one launch where their formats allow
+                MmArgs gk = g;
+                gk.m = L.k.p; set_mx(gk, L.k); gk.out = pre_k_; gk.ostride = kvdl;
+                check(launch_mm_two(g, gk, stream_), "prefill q, k");
                 if (!L.v_is_k) {
                     g.m = L.v.p; set_mx(g, L.v); g.out = pre_v_; g.ostride = kvdl;
                     check(launch_mm(g, kMmStore, stream_), "prefill v");
                 }
+            } else {
+                check(launch_mm(g, kMmStore, stream_), "prefill q");
             }
             // norms, RoPE, cache rows, attention (:1020-1093)
             if (plain_attn_) {  // heads past 128 (or BRISK_HIP_ATTN=plain): the plain attention batched
