@@ -77,6 +77,10 @@ struct LoopArgs {
     // their value slice in LDS, loaded while the other phases run, and take the whole attention;
     // they take no tiles of phases A, C, D and F
     int res_ok, res_n;
+    // a_touch: before phase F, each h-row owner with a phase-A tile in the next layer loads that
+    // tile's bytes once (into L2), so its phase-A weight loads, and the input poll behind them,
+    // do not wait for HBM
+    int a_touch;
 };
 
 constexpr int kOwnRows = 256;  // rows of h one workgroup can keep

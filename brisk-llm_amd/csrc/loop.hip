@@ -369,6 +369,71 @@ __device__ __forceinline__ bool run_tiles(int total, GemvLds& s, RowOf row_of, R
 
 // ---------------------------------------------------------------- phases
 
+// Bytes a block takes in each of a matrix's planes (plane_bytes for one block).
+__device__ __forceinline__ void block_plane_bytes(uint32_t type, uint32_t (&b)[3]) {
+    b[0] = b[1] = b[2] = 0;
+    switch (type) {
+        case kQ4_0: b[0] = 16; b[1] = 2; break;
+        case kQ4_1: b[0] = 16; b[1] = 2; b[2] = 2; break;
+        case kQ5_0: b[0] = 16; b[1] = 2; b[2] = 4; break;
+        case kQ8_0: b[0] = 32; b[1] = 2; break;
+        case kQ4_K: b[0] = 128; b[1] = 16; b[2] = 16; break;
+        case kQ5_K: b[0] = 128; b[1] = 16; b[2] = 48; break;
+        case kQ6_K: b[0] = 128; b[1] = 64; b[2] = 20; break;
+        case kTQ2_0: b[0] = 64; b[1] = 2; break;
+        default: break;
+    }
+}
+
+// Rows [row0, row0 + R) of m, every plane, one dword a 128-byte line (a line a thread, up to four
+// a thread), loaded and waited for in one asm block (no register receives data after it ends).
+__device__ __forceinline__ void touch_rows(const Packed& m, uint32_t row0, int R) {
+    uint32_t b[3];
+    block_plane_bytes(m.type, b);
+    const size_t nb = m.cols / block_elems(m.type);
+    const uint8_t* planes[3] = {m.p0, m.p1, m.p2};
+    const uint8_t* addr[4];
+    int n = 0;
+    size_t line = threadIdx.x;
+    for (int k = 0; k < 3 && n < 4; ++k) {
+        if (b[k] == 0) continue;
+        const size_t off = static_cast<size_t>(row0) * nb * b[k], len = static_cast<size_t>(R) * nb * b[k];
+        const size_t lines = (len + 127) / 128;
+        while (line < lines && n < 4) {
+            addr[n++] = planes[k] + off + line * 128;
+            line += kThreads;
+        }
+        line -= lines;  // this thread's line index in the next plane
+    }
+    if (n == 0) return;
+    for (int i = n; i < 4; ++i) addr[i] = addr[0];
+    uint32_t d0, d1, d2, d3;
+    asm volatile(
+        "global_load_dword %0, %4, off\n\t"
+        "global_load_dword %1, %5, off\n\t"
+        "global_load_dword %2, %6, off\n\t"
+        "global_load_dword %3, %7, off\n\t"
+        "s_waitcnt vmcnt(0)"
+        : "=&v"(d0), "=&v"(d1), "=&v"(d2), "=&v"(d3)
+        : "v"(addr[0]), "v"(addr[1]), "v"(addr[2]), "v"(addr[3])
+        : "memory");
+}
+
+// The phase-A tile workgroup b takes in the layer of L (one-format Q/K/V, the plan run_tiles
+// follows), touched into L2 by touch_rows.
+__device__ __forceinline__ void a_touch(const LoopArgs& g, const LayerDev& L) {
+    const int first = g.res_ok ? g.res_n : 0, G = static_cast<int>(gridDim.x) - first;
+    const int nq = g.tiles_qkv[0] + g.tiles_qkv[1], total = nq + g.tiles_qkv[2];
+    const int t = static_cast<int>(blockIdx.x) - first;  // the first tile: the loads run_tiles issues before its input wait
+    if (t < 0 || t >= total || t >= G) return;
+    const int i = t < g.tiles_qkv[0] ? 0 : t < nq ? 1 : 2;
+    const int tt = i == 0 ? t : i == 1 ? t - g.tiles_qkv[0] : t - nq;
+    const Packed m = i == 0 ? sld(&L.q) : i == 1 ? sld(&L.k) : sld(&L.v);
+    const int R = g.R_qkv[i];
+    const uint32_t row0 = static_cast<uint32_t>(tt) * R;
+    touch_rows(m, row0, row0 + R <= m.rows ? R : static_cast<int>(m.rows - row0));
+}
+
 // A: Q, K, V rows (one format, or Q/K's and then V's).
 template <uint32_t TQ, uint32_t TV, uint32_t TE>
 __device__ __forceinline__ bool phase_a(const LoopArgs& g, const LayerDev& L, int step, int l, int token, GemvLds& s) {
@@ -1859,6 +1924,10 @@ __global__ __launch_bounds__(kThreads) void k_loop(LoopArgs g_arg) {
             __syncthreads();
             if (lg().trace != nullptr && blockIdx.x == 0 && threadIdx.x == 0) lg().trace[5 + (step * lg().n_layers + l) * 5] = wall_clock64();
             pst(pst_ptr(lg(), step, l, 4), 0);
+            if constexpr (TQ == TV) {
+                const int me = static_cast<int>(blockIdx.x) - lg().c_first;
+                if (lg().a_touch && l + 1 < lg().n_layers && lg().own_h && me >= 0 && me < lg().n_c) a_touch(lg(), lg().layers[l + 1]);
+            }
             if constexpr (block_elems(TD) == 32 && kPushBuilt) {
                 if (lg().push_ffn) {
                     if (!phase_f_push<TD>(lg(), step, l, lds.g, hown)) return;

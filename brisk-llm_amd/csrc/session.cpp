@@ -1056,7 +1056,13 @@ void Session::setup_loop() {
         if (const char* e = std::getenv("BRISK_HIP_RESIDENT")) ok = ok && std::string(e) != "0";
         g.res_ok = ok ? 1 : 0;
         g.res_n = ok ? n2 : 0;
+        g.a_touch = 0;
         if (ok) {
+            // an h-row owner finishes phase F last; its phase-A tile's weight loads, issued then,
+            // would hold its input poll back (loads complete in order), so it touches that tile
+            // into L2 at the start of phase F, where it waits for the pushed terms anyway
+            g.a_touch = g.own_h && g.push_ffn ? 1 : 0;
+            if (const char* e = std::getenv("BRISK_HIP_A_TOUCH")) g.a_touch = g.a_touch && std::string(e) != "0";
             const int R = loop_rows({&L0.q.p, &L0.k.p, &L0.v.p}, G - n2);
             for (int i = 0; i < 3; ++i) g.R_qkv[i] = R;
             g.tiles_qkv[0] = tiles_of(L0.q.p, R);
