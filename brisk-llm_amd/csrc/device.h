@@ -426,6 +426,28 @@ __device__ __forceinline__ AbsMax wave_absmax(AbsMax v) {
     return absmax_op(absmax_op(absmax_op(row(0), row(16)), row(32)), row(48));
 }
 
+// The value of largest magnitude of a wave's 256-value block (lane l holding values 4 l .. 4 l + 3),
+// the first one in index order on ties, as quantize_q8_k's `ax > amax` scan picks it (NaNs never
+// picked), and that magnitude; 0 when every value is 0 or NaN.  The magnitude is a plain wave
+// max; the value comes from the first lane holding it (a ballot) and, in that lane, its first
+// such value.
+__device__ __forceinline__ float block_first_absmax(const float v[4], float& amax) {
+    float am = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
+    am = wave_max(am);
+    amax = am > 0.0f ? am : 0.0f;
+    if (!(am > 0.0f)) return 0.0f;
+    float mine = 0.0f;
+    bool has = false;
+#pragma unroll
+    for (int i = 3; i >= 0; --i)
+        if (fabsf(v[i]) == am) {
+            mine = v[i];
+            has = true;
+        }
+    const unsigned long long hit = __builtin_amdgcn_ballot_w64(has);
+    return readlane(mine, __builtin_ctzll(hit));
+}
+
 // Sum of float squares in double over a workgroup (the accumulator of rms_norm,
 // src/model.cpp:89-90).  The double sum of float squares is exact unless the
 // squares span more than ~29 binades, so the grouping rarely matters; every
@@ -568,19 +590,9 @@ __device__ inline void act_q8_k(const float* x, const float* w, float scale, int
             v[0] = v[0] * scale * wv.x; v[1] = v[1] * scale * wv.y;
             v[2] = v[2] * scale * wv.z; v[3] = v[3] * scale * wv.w;
         }
-        // first index of the largest |v|
-        float amax = -1.0f;
-        int idx = 0;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const float av = fabsf(v[i]);
-            if (av > amax) { amax = av; idx = lane * 4 + i; }
-        }
-        float sel = v[idx - lane * 4 < 0 ? 0 : (idx & 3)];
-        {
-            const AbsMax m = wave_absmax(AbsMax{amax, idx, sel});
-            amax = m.amax; idx = m.idx; sel = m.sel;
-        }
+        // the first value of the largest |v|
+        float amax;
+        const float sel = block_first_absmax(v, amax);
         int q[4];
         float d;
         if (amax == 0.0f) {
@@ -716,17 +728,8 @@ __device__ __forceinline__ void quant_pieces_q8_0(const float (&v)[N][4], const 
 // 256-value block; the scale comes from the first value of largest magnitude.
 __device__ __forceinline__ void quant_piece_q8_k(const float v[4], int base, int bits, ActLds& a) {
     const int lane = threadIdx.x & 63;
-    float amax = -1.0f, sel = 0.0f;
-    int idx = 0;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const float av = fabsf(v[i]);
-        if (av > amax) { amax = av; idx = lane * 4 + i; sel = v[i]; }
-    }
-    {
-        const AbsMax m = wave_absmax(AbsMax{amax, idx, sel});
-        amax = m.amax; idx = m.idx; sel = m.sel;
-    }
+    float amax;
+    const float sel = block_first_absmax(v, amax);
     int q[4];
     float d;
     if (amax == 0.0f) {

@@ -56,17 +56,8 @@ __device__ __forceinline__ void pre_quant_block(const float (&v)[4], int t, int 
     const int lane = threadIdx.x & 63, base = b * 256 + 4 * lane;
     int q[4];
     if constexpr (Q8K) {
-        float amax = -1.0f, sel = 0.0f;
-        int idx = 0;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const float av = fabsf(v[i]);
-            if (av > amax) { amax = av; idx = lane * 4 + i; sel = v[i]; }
-        }
-        {
-            const AbsMax m = wave_absmax(AbsMax{amax, idx, sel});
-            amax = m.amax; sel = m.sel;
-        }
+        float amax;
+        const float sel = block_first_absmax(v, amax);
         float d;
         if (amax == 0.0f) {
             d = 0.0f;
