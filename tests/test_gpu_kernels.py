@@ -97,6 +97,26 @@ def test_quantize_q8_k_bitexact(lib, orc, n, bits):
     np.testing.assert_array_equal(host(out, np.uint8), want)
 
 
+@pytest.mark.parametrize("bits", [8, 7])
+def test_quantize_q8_k_special_blocks(lib, orc, bits):
+    """Blocks whose scale value the wave search must pick as the reference's scan does: all NaN
+    (the scan never picks a NaN, so the block is zeros), equal magnitudes in different lanes (the
+    first, negative, sets the scale), zeros with -0.0, and an ordinary block."""
+    x = activations(1024, 40 + bits)
+    x[:256] = np.nan
+    x[256:512] *= 0.01
+    x[256 + 7] = -5.0
+    x[256 + 100] = 5.0
+    x[256 + 201] = -5.0
+    x[512:768] = 0.0
+    x[512 + 3::17] = -0.0
+    want = quant_ref(orc, x, True, bits)
+    xd = dev(x)
+    out = torch.zeros(len(want), dtype=torch.uint8, device="cuda")
+    L.check(lib.brisk_hip_quantize_q8_k(p(xd), p(out), 1024, bits, None))
+    np.testing.assert_array_equal(host(out, np.uint8), want)
+
+
 def packed(lib, type_, w, rows, cols):
     nbytes = lib.brisk_hip_packed_bytes(type_, rows, cols)
     assert nbytes > 0

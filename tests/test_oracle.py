@@ -151,6 +151,15 @@ def test_quantize_matches_reference(L, bits):
     a = np.ones(2 * 292, np.uint8)
     L.or_quantize_q8_k(ptr(z), ptr(a), 512, bits)
     assert not a.any()
+    # an all-NaN block (the scan never picks a NaN: zeros) and equal magnitudes, the first negative
+    x = rng_normal(9, 512) * 0.01
+    x[:256] = np.nan
+    x[256 + 7], x[256 + 100] = -5.0, 5.0
+    a = np.zeros(2 * 292, np.uint8)
+    b = np.zeros_like(a)
+    L.or_quantize_q8_k(ptr(x), ptr(a), 512, bits)
+    R.ref_quantize_q8_k(ptr(x), ptr(b), 512, bits)
+    assert np.array_equal(a, b) and not a[:292].any()
 
 
 # --------------------------------------------------------------------------- weights: dequant, dots
