@@ -235,6 +235,11 @@ SPECS = {
                                  fmt=_uniform4(G.T_Q4_0)),
     "tiny-llama": ModelSpec("tiny-llama", "llama", 512, 2, 8, 2, 64, 768, 1000, 5e5, eps=1e-5, context=1024,
                             fmt={**_uniform4(G.T_Q4_K), "v": G.T_Q6_K, "down": G.T_Q6_K}, embd_fmt=G.T_Q6_K, out_fmt=None),
+    # Feed-forward rows wider than the GEMV's activation buffer (8192): 4B-class widths.
+    "tiny-wide": ModelSpec("tiny-wide", "llama", 256, 2, 4, 2, 64, 9728, 1000, 5e5, eps=1e-5, context=1024,
+                           fmt={**_uniform4(G.T_Q4_K), "v": G.T_Q6_K, "down": G.T_Q6_K}, embd_fmt=G.T_Q6_K, out_fmt=None),
+    "tiny-wide-q4": ModelSpec("tiny-wide-q4", "qwen3", 256, 2, 4, 2, 64, 14336, 1000, 1e6, context=1024,
+                              fmt=_uniform4(G.T_Q4_0)),
     "tiny-q8": ModelSpec("tiny-q8", "qwen3", 256, 2, 4, 2, 64, 512, 1000, 1e6, context=1024, fmt=_uniform4(G.T_Q8_0)),
     "tiny-bitnet": ModelSpec("tiny-bitnet", "bitnet-b1.58", 512, 2, 4, 1, 128, 768, 1000, 5e5, eps=1e-5, context=1024,
                              fmt=_uniform4(G.T_TQ2_0), embd_fmt=G.T_Q4_0, out_fmt=None),

@@ -57,7 +57,8 @@ bh::Packed packed_view(int type, int flags, const void* packed, size_t rows, siz
     if (!known_type(type)) throw bh::Error(BRISK_HIP_EINVAL, "kernels: unsupported weight type " + std::to_string(type));
     if (cols == 0 || cols % bh::block_elems(static_cast<uint32_t>(type)) != 0)
         throw bh::Error(BRISK_HIP_EINVAL, "kernels: cols must be a non-zero multiple of the block size");
-    if (cols > static_cast<size_t>(bh::kMaxCols)) throw bh::Error(BRISK_HIP_EINVAL, "kernels: rows wider than 8192 are not supported");
+    if (cols > static_cast<size_t>(bh::kMaxCols) && cols % 256 != 0)
+        throw bh::Error(BRISK_HIP_EINVAL, "kernels: rows wider than 8192 must be whole 256-value blocks");
     if (rows == 0 || rows > 0xFFFFFFFFu) throw bh::Error(BRISK_HIP_EINVAL, "kernels: bad row count");
     if (packed == nullptr) throw bh::Error(BRISK_HIP_EINVAL, "kernels: null weights");
     size_t planes[3];
@@ -144,12 +145,13 @@ int brisk_hip_matmul(int type, int flags, const void* packed, size_t rows, size_
         if (n == 0 || n > 65535) throw bh::Error(BRISK_HIP_EINVAL, "kernels: n must be 1..65535");
         if (out_stride < rows) throw bh::Error(BRISK_HIP_EINVAL, "kernels: out_stride < rows");
         const hipStream_t st = static_cast<hipStream_t>(stream);
-        if (n == 1) {
+        if (n == 1 && cols <= static_cast<size_t>(bh::kMaxCols)) {  // the GEMV holds the row in LDS
             hip_check(bh::launch_matvec_q8(p, xq, n, out, out_stride, st), "matmul");
             return;
         }
-        // batches take the int8 MFMA path of the prefill: the GGUF activation rows are
-        // converted to its planar layout in a scratch allocation, released when done
+        // batches (and rows wider than the GEMV's buffer) take the int8 MFMA path of the prefill:
+        // the GGUF activation rows are converted to its planar layout in a scratch allocation,
+        // released when done
         const int stride = static_cast<int>((cols + 255) / 256 * 256);
         bh::ActPlanar x{};
         x.stride = stride;
@@ -188,7 +190,7 @@ int brisk_hip_matmul_noalloc(int type, int flags, const void* packed, size_t row
         if (n == 0 || n > 65535) throw bh::Error(BRISK_HIP_EINVAL, "kernels: n must be 1..65535");
         if (out_stride < rows) throw bh::Error(BRISK_HIP_EINVAL, "kernels: out_stride < rows");
         const hipStream_t st = static_cast<hipStream_t>(stream);
-        if (n == 1) {  // the matvec takes no scratch
+        if (n == 1 && cols <= static_cast<size_t>(bh::kMaxCols)) {  // the matvec takes no scratch
             hip_check(bh::launch_matvec_q8(p, xq, n, out, out_stride, st), "matmul");
             return;
         }
@@ -217,6 +219,8 @@ int brisk_hip_matmul_noalloc(int type, int flags, const void* packed, size_t row
 int brisk_hip_gemv(int type, int flags, const void* packed, size_t rows, size_t cols, const float* x, const float* norm_w, float eps,
                    float* out, int accumulate, void* stream) {
     return guarded([&] {
+        if (cols > static_cast<size_t>(bh::kMaxCols))  // the fused norm reads the whole row from LDS
+            throw bh::Error(BRISK_HIP_EINVAL, "kernels: gemv rows wider than 8192 are not supported (quantise, then matvec)");
         bh::GemvArgs g{};
         g.n = 1;
         g.t[0].m = packed_view(type, flags, packed, rows, cols);

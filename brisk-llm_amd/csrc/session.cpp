@@ -201,6 +201,7 @@ brisk_hip_memory estimate_session(const brisk_hip_config& cfg, const brisk_hip_t
         sc += T * static_cast<size_t>(cfg.ple_dim) * (cfg.layers + 1) * 4;
     if (cfg.arch == BRISK_HIP_ARCH_QWEN35)  // prefill recurrence rows, query|gate rows, the wider attention output
         sc += T * (5 * static_cast<size_t>(cfg.ssm_inner) + 2 * cfg.ssm_v_heads + 2 * qd) * 4;
+    if (ff > static_cast<size_t>(kMaxCols)) sc += (ff + 255) / 256 * 256 * (1 + 4 / 32.0 + 4 / 16.0);  // wide down input
     sc += static_cast<size_t>(64) * cfg.vocab * 4;                         // eval_all logits
     for (size_t i = 0; i < n; ++i)  // the prefill's expanded layer matrices
         if (mx_expanded(static_cast<uint32_t>(tensors[i].type)) && tensors[i].name != nullptr &&
@@ -284,7 +285,11 @@ Session::Session(const brisk_hip_config& cfg, const brisk_hip_tensor* tensors, s
     if (cfg.kv_heads > 1000) model_fail("more than 1000 key/value heads is not supported");  // ticket slots
     if (cfg.head_dim == 0 || cfg.head_dim % 32 != 0 || cfg.head_dim > static_cast<uint32_t>(kPlainMaxHead))
         model_fail("head size must be a non-zero multiple of 32 up to 512");
-    if (cfg.embd > kMaxCols || cfg.ff > kMaxCols || cfg.heads * cfg.head_dim > kMaxCols) model_fail("a row wider than 8192 is not supported");
+    if (cfg.embd > kMaxCols || cfg.heads * cfg.head_dim > kMaxCols) model_fail("a row wider than 8192 is not supported");
+    // feed-forward rows past kMaxCols: the down projection runs as a one-token GEMM over 256-value
+    // chunks (its input quantised to a global buffer), which has no width limit
+    if (cfg.ff > kMaxCols && cfg.ff % kMmChunkCols != 0)
+        model_fail("a feed-forward row wider than 8192 must be whole 256-value blocks");
     {
         const char* at = std::getenv("BRISK_HIP_ATTN");
         // Gemma 4's layers differ in head size and may read another layer's cache: the plain attention
@@ -511,6 +516,12 @@ Session::Session(const brisk_hip_config& cfg, const brisk_hip_tensor* tensors, s
     q_ = static_cast<float*>(alloc(qd * 4));
     att_ = static_cast<float*>(alloc(std::max<size_t>(qd, cfg.ssm_inner) * 4));
     act_ = static_cast<float*>(alloc(static_cast<size_t>(cfg.ff) * 4));
+    if (cfg.ff > kMaxCols) {  // the wide down projection's quantised input, one token
+        wide_x_.stride = static_cast<int>((cfg.ff + kMmChunkCols - 1) / kMmChunkCols * kMmChunkCols);
+        wide_x_.qs = static_cast<int8_t*>(alloc(wide_x_.stride));
+        wide_x_.d = static_cast<float*>(alloc((wide_x_.stride / 32) * 4));
+        wide_x_.bs = static_cast<int32_t*>(alloc((wide_x_.stride / 16) * 4));
+    }
     logits_ = static_cast<float*>(alloc(static_cast<size_t>(cfg.vocab) * 4));
     max_splits_ = attention_max_splits(static_cast<int>(max_ctx_));
     if (plain_attn_) {
@@ -794,10 +805,19 @@ void Session::record_step(bool full) {
         ga.relu2 = cfg_.arch == BRISK_HIP_ARCH_BITNET; ga.gelu = gemma(); ga.act = act_;
         check(launch_gateup(ga, stream_), "gate_up");
 
-        GemvArgs da{};
-        da.n = 1; da.t[0].m = L.down.p; da.t[0].out = L.ffn_post_norm ? proj_ : h_;
-        da.x = act_; da.normw = L.ffn_sub_norm; da.eps = cfg_.rms_epsilon; da.add = L.ffn_post_norm ? 0 : 1;
-        check(launch_gemv(da, stream_), "ffn_down");
+        if (L.ff > kMaxCols) {  // wider than the GEMV's activation buffer: quantised to wide_x_, then a one-token GEMM
+            check(launch_pre_quant(act_, L.ff, L.ffn_sub_norm, cfg_.rms_epsilon, L.ff, 1, takes_q8_k(L.down.p.type), act_bits(L.down.p),
+                                   wide_x_, stream_),
+                  "ffn_down input");
+            MmArgs dm{};
+            dm.m = L.down.p; dm.x = wide_x_; dm.ntok = 1; dm.out = L.ffn_post_norm ? proj_ : h_; dm.ostride = e;
+            check(launch_mm(dm, L.ffn_post_norm ? kMmStore : kMmAdd, stream_), "ffn_down");
+        } else {
+            GemvArgs da{};
+            da.n = 1; da.t[0].m = L.down.p; da.t[0].out = L.ffn_post_norm ? proj_ : h_;
+            da.x = act_; da.normw = L.ffn_sub_norm; da.eps = cfg_.rms_epsilon; da.add = L.ffn_post_norm ? 0 : 1;
+            check(launch_gemv(da, stream_), "ffn_down");
+        }
         if (L.ffn_post_norm) check(launch_post_add(h_, proj_, L.ffn_post_norm, cfg_.rms_epsilon, static_cast<int>(cfg_.embd), stream_), "post norm");
         if (cfg_.ple_dim != 0) {  // h = (h + norm(proj(gelu(gate h) * input l))) * scale (src/model.cpp:1163-1177)
             GemvArgs pg{};  // gelu(gate h) * input l, in the GEMV's epilogue
@@ -859,6 +879,7 @@ void Session::setup_loop() {
     if (embd_.p.type != out_->p.type) return;  // the loop reads the embedding in its output's format
     if (gemma() || lfm2() || qwen35()) return;  // post-norms, windows, softcap, convolutions, recurrences: graph-path phases only
     if (plain_attn_) return;                    // the plain attention is a graph-path phase
+    if (wide_x_.qs != nullptr) return;          // feed-forward rows past kMaxCols: the graph path's one-token GEMM
     const Layer& L0 = layers_[0];
     const void* k = find_loop_kernel(L0.q.p.type, L0.v.p.type, L0.o.p.type, L0.gate.p.type, L0.down.p.type, out_->p.type);
     if (k == nullptr) return;

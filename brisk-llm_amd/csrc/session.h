@@ -192,6 +192,7 @@ private:
     float *pre_sqkv_ = nullptr, *pre_sz_ = nullptr, *pre_sab_ = nullptr, *pre_qg_ = nullptr;
     float *pre_ple_ = nullptr, *pre_pleg_ = nullptr;  // Gemma 4: per-layer embedding inputs and gate rows
     ActPlanar pre_x_{};
+    ActPlanar wide_x_{};  // feed-forward rows past kMaxCols: the down projection's quantised input (one token)
     float* all_logits_ = nullptr;  // eval_all's [64][vocab] logits, allocated on first use
     hipGraphExec_t graph_layers_ = nullptr, graph_full_ = nullptr;
 };

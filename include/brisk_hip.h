@@ -152,9 +152,11 @@ int brisk_hip_quantize_q8_k(const float* x, void* out, size_t count, int bits, v
  * activations (Q8_0 rows for Q4_0/Q8_0, Q8_K rows for Q4_K/Q6_K/TQ2_0).  Each
  * output is bit-identical to the reference's generic kernels. `flags`: bit 0
  * selects, for TQ2_0, the x86 TQ2_0x16 arithmetic (src/quant.cpp:789-802).
- * For n > 1, matmul allocates a scratch block for the call: the planar
- * activation rows, and for Q6_K and Q5_K the matrix's expanded weight planes
- * (about 2 bytes a weight), as a session's batched prefill holds them. */
+ * Rows of any width (src/kernels.cpp:13-30); rows wider than 8192 must be
+ * whole 256-value blocks.  For n > 1, and for rows wider than 8192, matmul
+ * allocates a scratch block for the call: the planar activation rows, and for
+ * Q6_K and Q5_K the matrix's expanded weight planes (about 2 bytes a weight),
+ * as a session's batched prefill holds them. */
 int brisk_hip_matvec(int type, int flags, const void* packed, size_t rows, size_t cols, const void* xq, float* out,
                      void* stream);
 int brisk_hip_matmul(int type, int flags, const void* packed, size_t rows, size_t cols, const void* xq, size_t n,
@@ -162,8 +164,8 @@ int brisk_hip_matmul(int type, int flags, const void* packed, size_t rows, size_
 
 /* brisk_hip_matmul without any device allocation.  No counterpart in the
  * reference: it is for callers that cannot allocate (code under HIP graph
- * capture, tight serving loops, hosts that forbid hipMalloc).  For n > 1 the
- * batch's activation rows are staged in a static device buffer of 4 MiB, one
+ * capture, tight serving loops, hosts that forbid hipMalloc).  For n > 1 (or
+ * rows wider than 8192) the activation rows are staged in a static device buffer of 4 MiB, one
  * per GPU, held until the process ends (n x ceil(cols / 256) x 256 x 1.375
  * bytes must fit, e.g. 372 rows of 8192 columns; larger requests fail with
  * BRISK_HIP_EINVAL).  Outputs are identical to brisk_hip_matmul's.  The call
@@ -174,7 +176,8 @@ int brisk_hip_matmul_noalloc(int type, int flags, const void* packed, size_t row
 
 /* The decode GEMV of the token loop: quantises the f32 row x in-kernel (after
  * rms_norm with weight `norm_w` and `eps` when norm_w is non-null), then
- * out = W x, or out += W x when `accumulate` (the residual update). */
+ * out = W x, or out += W x when `accumulate` (the residual update).  Rows of
+ * at most 8192 values (the row is held in LDS). */
 int brisk_hip_gemv(int type, int flags, const void* packed, size_t rows, size_t cols, const float* x,
                    const float* norm_w, float eps, float* out, int accumulate, void* stream);
 

@@ -134,6 +134,9 @@ CASES = [
     (TQ2_0, 48, 1024), (TQ2_0, 640, 2560), (TQ2_0, 37, 2560),
     (Q4_1, 37, 1024), (Q4_1, 2048, 2048), (Q5_0, 37, 1024), (Q5_0, 1024, 3072),
     (Q5_K, 37, 1024), (Q5_K, 512, 2048), (Q5_K, 2048, 8192),
+    # rows wider than the GEMV's LDS row (4B-class feed-forward widths): the planar GEMM path, n = 1 too
+    (Q4_0, 64, 14336), (Q8_0, 48, 9728), (Q4_K, 64, 9728), (Q6_K, 48, 14336), (TQ2_0, 48, 9728),
+    (Q4_1, 37, 9728), (Q5_0, 37, 14336), (Q5_K, 37, 9728),
 ]
 
 
@@ -159,6 +162,23 @@ def test_matvec_matmul_bitexact(lib, orc, type_, rows, cols, n):
     L.check(lib.brisk_hip_matmul(type_, flags, p(wd), rows, cols, p(xd), n, p(out2), rows + 3, None))
     got = host(out2, np.float32).reshape(n, rows + 3)[:, :rows]
     np.testing.assert_array_equal(got, want)
+
+
+def test_wide_rows_need_whole_chunks(lib):
+    """Rows wider than 8192 go through 256-value chunks: a width that is not whole chunks is refused
+    with an error (no launch); the fused-norm GEMV, which holds the row in LDS, refuses any wider row."""
+    rows, cols = 37, 8192 + 32
+    w = weights(Q4_0, rows, cols, 5)
+    nbytes = lib.brisk_hip_packed_bytes(Q4_0, rows, cols)
+    wd = torch.zeros(nbytes, dtype=torch.uint8, device="cuda")
+    assert lib.brisk_hip_pack(Q4_0, p(dev(w)), rows, cols, p(wd), None) != 0
+    assert b"256-value blocks" in lib.brisk_hip_last_error()
+    cols = 9728
+    x = torch.zeros(cols, dtype=torch.float32, device="cuda")
+    out = torch.zeros(rows, dtype=torch.float32, device="cuda")
+    wd = torch.zeros(lib.brisk_hip_packed_bytes(Q4_0, rows, cols), dtype=torch.uint8, device="cuda")
+    assert lib.brisk_hip_gemv(Q4_0, 0, p(wd), rows, cols, p(x), None, 1e-6, p(out), 0, None) != 0
+    assert b"wider than 8192" in lib.brisk_hip_last_error()
 
 
 @pytest.mark.parametrize("type_,rows,cols", [(Q4_0, 2048, 1024), (Q8_0, 4096, 1024), (Q4_K, 256, 2048),
