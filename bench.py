@@ -251,8 +251,7 @@ def families(torch, HipSession, model, synth):
         log(f"{name} decode: {128 / dt:.1f} tok/s")
         s.close()
         del s
-        # a 512-id prompt (eval, last-token logits; median of 3): batched where the family has a
-        # prefill (LFM2, Gemma 3, Qwen3.5), token by token otherwise (Gemma 4)
+        # a 512-id prompt (eval, last-token logits; median of 3), through the batched prefill
         lp = synth.prompt_ids(512, cfg.vocab, seed=11)
         s = HipSession((f, cfg, table), max_context=512 + 16)
         s.eval(lp[:64], logits=False)  # warm-up

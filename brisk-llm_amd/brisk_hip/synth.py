@@ -252,6 +252,13 @@ SPECS = {
                               fmt={**_uniform4(G.T_Q4_K), "v": G.T_Q6_K, "down": G.T_Q6_K}, embd_fmt=G.T_Q6_K, out_fmt=None),
     # Gemma 3: layers 0-4 and 6 slide over the last 8 positions (local RoPE base), 5 is global with
     # positions scaled by 1/2; logits soft-capped at 30; the Q8_0 embedding rows scaled by sqrt(embd).
+    # Rows of 32-value blocks that end inside a 256-value chunk (Gemma-3-1B's 1152): 352 = 11 blocks,
+    # 1184 = 37 blocks, so the batched GEMMs' last chunk holds 3 and 5 blocks.
+    "tiny-gemma3w": ModelSpec("tiny-gemma3w", "gemma3", 352, 3, 4, 1, 64, 1184, 1000, 1e6, context=1024,
+                              fmt=_uniform4(G.T_Q4_0),
+                              extra={"attention.sliding_window": (G.U32, 8), "rope.freq_base_swa": (G.F32, 10000.0),
+                                     "final_logit_softcapping": (G.F32, 30.0)}),
+    "tiny-q8w": ModelSpec("tiny-q8w", "qwen3", 352, 2, 4, 2, 64, 1184, 1000, 1e6, context=1024, fmt=_uniform4(G.T_Q8_0)),
     "tiny-gemma3": ModelSpec("tiny-gemma3", "gemma3", 256, 7, 4, 1, 64, 512, 1000, 1e6, context=1024,
                              fmt=_uniform4(G.T_Q8_0),
                              extra={"attention.sliding_window": (G.U32, 8), "rope.freq_base_swa": (G.F32, 10000.0),

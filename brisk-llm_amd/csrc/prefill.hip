@@ -357,18 +357,30 @@ struct WChunk {
     uint4 mn[4];     // Q4_1: 8 fp16 block offsets m a row
 };
 
+// The 8 fp16 values of a row's plane at element e0 (a chunk's block scales), or its first nb of
+// them (the rest 0) when the row ends inside the chunk: nothing past the row is read.
+__device__ __forceinline__ uint4 chunk_halves(const uint8_t* plane, size_t e0, int nb) {
+    if (nb >= 8) return *reinterpret_cast<const uint4*>(plane + e0 * 2);
+    const uint16_t* h = reinterpret_cast<const uint16_t*>(plane) + e0;
+    uint32_t wd[4] = {0u, 0u, 0u, 0u};
+    for (int k = 0; k < nb; ++k) wd[k >> 1] |= static_cast<uint32_t>(h[k]) << (16 * (k & 1));
+    return make_uint4(wd[0], wd[1], wd[2], wd[3]);
+}
+
+// Chunk c's weights; nb of its 8 sub-blocks lie in the row (fewer than 8 only in the last chunk
+// of a row of 32-value blocks that is not whole 256-value chunks): the others are not read.
 template <uint32_t T>
 __device__ __forceinline__ void wchunk_load(WChunk<T>& w, const Packed& m, uint32_t arow, bool arow_ok, const uint32_t orow[4],
-                                            int c, int kq) {
+                                            int c, int kq, int nb = 8) {
 #pragma unroll
-    for (int jj = 0; jj < 8; ++jj) w.a[jj] = arow_ok ? frag_a<T>(m, arow, c * 8 + jj, kq) : 0ull;
+    for (int jj = 0; jj < 8; ++jj) w.a[jj] = arow_ok && jj < nb ? frag_a<T>(m, arow, c * 8 + jj, kq) : 0ull;
     if (T == kQ4_0 || T == kQ4_1 || T == kQ5_0 || T == kQ8_0) {
         const uint32_t nsub = m.cols / 32;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) w.sc[i] = *reinterpret_cast<const uint4*>(m.p1 + (static_cast<size_t>(orow[i]) * nsub + c * 8) * 2);
+        for (int i = 0; i < 4; ++i) w.sc[i] = chunk_halves(m.p1, static_cast<size_t>(orow[i]) * nsub + c * 8, nb);
         if (T == kQ4_1) {
 #pragma unroll
-            for (int i = 0; i < 4; ++i) w.mn[i] = *reinterpret_cast<const uint4*>(m.p2 + (static_cast<size_t>(orow[i]) * nsub + c * 8) * 2);
+            for (int i = 0; i < 4; ++i) w.mn[i] = chunk_halves(m.p2, static_cast<size_t>(orow[i]) * nsub + c * 8, nb);
         }
     } else if (T == kQ4_K || T == kQ5_K) {
         const uint32_t nsb = m.cols / 256;
@@ -405,13 +417,14 @@ struct MmAcc {
 // The chunk's contribution to the lane's outputs (tokens 16 g + l % 16, rows 4 (l / 16) + i),
 // in the reference's term and sum order.
 template <uint32_t T, int G>
-__device__ __forceinline__ void wchunk_compute(const WChunk<T>& w, const MmLds<G>& L, MmAcc<G>& acc, bool lut16) {
+__device__ __forceinline__ void wchunk_compute(const WChunk<T>& w, const MmLds<G>& L, MmAcc<G>& acc, bool lut16, int nb = 8) {
     constexpr int kGroups = G;
     const int lane = threadIdx.x & 63, kq = (lane >> 4) * 8, tl = lane & 15;
     const v4i zero = {0, 0, 0, 0};
     if (T == kQ4_0 || T == kQ5_0 || T == kQ8_0 || T == kQ4_1) {
 #pragma unroll
         for (int jj = 0; jj < 8; ++jj) {
+            if (jj >= nb) break;  // past the row (a partial last chunk): no term
             v4i d[kGroups];
 #pragma unroll
             for (int g = 0; g < kGroups; ++g)
@@ -558,13 +571,16 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 2))
     for (int gi = 0; gi < kGroups; ++gi)
 #pragma unroll
         for (int i = 0; i < 4; ++i) a.s[gi][i] = 0.0f;
-    const int nc = static_cast<int>(g.m.cols / kChunkCols);
+    // chunks of 256 values; a row of 32-value blocks may end inside its last chunk (nb_of < 8
+    // blocks there; its activation reads stay inside the planar rows, whose stride is whole chunks)
+    const int nc = static_cast<int>((g.m.cols + kChunkCols - 1) / kChunkCols), nsub = static_cast<int>(g.m.cols / 32);
+    auto nb_of = [&](int c) { return nsub - 8 * c < 8 ? nsub - 8 * c : 8; };
     ActStage<kGroups> st;
     WChunk<T> w0, w1;  // two chunks in flight
     constexpr bool kSums = T == kQ4_1;
     act_stage_load(st, g.x, g.ntok, t0, 0, q8k, kSums);
     if (wave_ok) {
-        wchunk_load<T>(w0, g.m, arow, arow_ok, orow, 0, kq);
+        wchunk_load<T>(w0, g.m, arow, arow_ok, orow, 0, kq, nb_of(0));
     }
     for (int c = 0; c < nc; c += 2) {
         // chunk c (weights in w0/v0)
@@ -574,11 +590,11 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 2))
         if (c + 1 < nc) {
             act_stage_load(st, g.x, g.ntok, t0, c + 1, q8k, kSums);
             if (wave_ok) {
-                wchunk_load<T>(w1, g.m, arow, arow_ok, orow, c + 1, kq);
+                wchunk_load<T>(w1, g.m, arow, arow_ok, orow, c + 1, kq, nb_of(c + 1));
             }
         }
         if (wave_ok) {
-            wchunk_compute<T>(w0, L, a, lut16);
+            wchunk_compute<T>(w0, L, a, lut16, nb_of(c));
         }
         if (c + 1 >= nc) break;
         // chunk c + 1 (weights in w1/v1)
@@ -588,11 +604,11 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 2))
         if (c + 2 < nc) {
             act_stage_load(st, g.x, g.ntok, t0, c + 2, q8k, kSums);
             if (wave_ok) {
-                wchunk_load<T>(w0, g.m, arow, arow_ok, orow, c + 2, kq);
+                wchunk_load<T>(w0, g.m, arow, arow_ok, orow, c + 2, kq, nb_of(c + 2));
             }
         }
         if (wave_ok) {
-            wchunk_compute<T>(w1, L, a, lut16);
+            wchunk_compute<T>(w1, L, a, lut16, nb_of(c + 1));
         }
     }
     if (!wave_ok) return;
@@ -2271,7 +2287,11 @@ static bool pair_split() {
 
 hipError_t launch_mm(const MmArgs& g, int mode, hipStream_t s) {
     if (g.ntok <= 0) return hipSuccess;
-    if (g.m.cols % kChunkCols != 0 || g.x.stride % kChunkCols != 0) return hipErrorInvalidValue;
+    // rows of whole 256-value chunks; the 32-value-block formats (k_mm) also take a partial last chunk
+    const bool small_blocks = g.m.type == kQ4_0 || g.m.type == kQ4_1 || g.m.type == kQ5_0 || g.m.type == kQ8_0;
+    if ((g.m.cols % kChunkCols != 0 && !(small_blocks && g.m.cols % 32 == 0)) || g.x.stride % kChunkCols != 0 ||
+        static_cast<size_t>(g.x.stride) < g.m.cols)
+        return hipErrorInvalidValue;
     if (mode == kMmPair && (g.m2.type != g.m.type || g.m2.rows != g.m.rows || g.m2.cols != g.m.cols)) return hipErrorInvalidValue;
     switch (mode) {
         case kMmStore: return mm_dispatch<kMmStore>(g, s);

@@ -618,12 +618,18 @@ Session::Session(const brisk_hip_config& cfg, const brisk_hip_tensor* tensors, s
     {
         const char* pf = std::getenv("BRISK_HIP_PREFILL");
         prefill_on_ = !(pf != nullptr && std::string(pf) == "0") && !debug_;
-        for (const Layer& L : layers_)  // the batched GEMMs stage their rows in 256-value chunks
+        // the batched GEMMs stage their rows in 256-value chunks; rows of 32-value blocks may end
+        // inside the last one
+        auto chunked = [](const Packed& p) {
+            const bool small = p.type == kQ4_0 || p.type == kQ4_1 || p.type == kQ5_0 || p.type == kQ8_0;
+            return p.cols % kMmChunkCols == 0 || (small && p.cols % 32 == 0 && p.cols <= static_cast<uint32_t>(kMaxCols));
+        };
+        for (const Layer& L : layers_)
             for (const DeviceMatrix* m : {&L.q, &L.k, &L.v, &L.o, &L.gate, &L.up, &L.down, &L.conv_in, &L.conv_out, &L.ssm_qkv,
                                           &L.ssm_gate, &L.ssm_alpha, &L.ssm_beta, &L.ssm_out, &L.ple_gate, &L.ple_proj})
-                if (m->mem != nullptr && m->p.cols % kMmChunkCols != 0) prefill_shapes_ = false;
-        if (out_->p.cols % kMmChunkCols != 0) prefill_shapes_ = false;
-        if (ple_proj_.mem != nullptr && ple_proj_.p.cols % kMmChunkCols != 0) prefill_shapes_ = false;
+                if (m->mem != nullptr && !chunked(m->p)) prefill_shapes_ = false;
+        if (!chunked(out_->p)) prefill_shapes_ = false;
+        if (ple_proj_.mem != nullptr && !chunked(ple_proj_.p)) prefill_shapes_ = false;
         prefill_on_ = prefill_on_ && prefill_shapes_;
         const char* pa = std::getenv("BRISK_HIP_PREFILL_ATTN");  // "mfma": long prompts' attention on f16 MFMA
         prefill_mfma_ = pa != nullptr && std::string(pa) == "mfma";
