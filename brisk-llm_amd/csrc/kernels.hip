@@ -448,9 +448,23 @@ __device__ __forceinline__ void ssm_conv_load(const SsmArgs& g, int h, int pos, 
 // window), the norms, the delta update of the thread's state row (row[], in place) and the gated
 // norm; returns the output of channel j (0 for threads j >= DIM).  Every thread of the workgroup
 // calls it (it holds barriers).
+// The step's per-head constants (dt bias, A, the gated norm's weight of channel j), read once
+// ahead of a token loop.
+struct SsmConst {
+    float dt, a, norm;
+};
+template <int DIM>
+__device__ __forceinline__ SsmConst ssm_const(const SsmArgs& g, int h) {
+    return SsmConst{g.dt[h], g.a[h], g.norm[threadIdx.x < DIM ? threadIdx.x : 0]};
+}
+
+// A workgroup barrier that orders LDS only (the step's threads share nothing else): loads of
+// global memory issued before it (the next token's rows) stay in flight.
+__device__ __forceinline__ void ssm_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
 template <int DIM>
 __device__ __forceinline__ float ssm_step(const SsmArgs& g, SsmLds& s, int h, const float (&cur)[3], SsmConv& cv, float z,
-                                          float alpha_in, float beta_in, float (&row)[DIM]) {
+                                          float alpha_in, float beta_in, float (&row)[DIM], const SsmConst& kc) {
     const int j = threadIdx.x, taps = g.taps;
     float v = 0.0f;
     if (j < DIM) {
@@ -470,23 +484,23 @@ __device__ __forceinline__ float ssm_step(const SsmArgs& g, SsmLds& s, int h, co
             else v = x;
         }
     }
-    __syncthreads();
+    ssm_barrier();
     if (j == 0 || j == 64) {  // the two L2 sums, one lane of two waves
         const float* src = j == 0 ? s.qs : s.ks;
         float sum = 0.0f;
         for (int i = 0; i < DIM; ++i) sum += src[i] * src[i];
         s.inv[j == 0 ? 0 : 1] = (j == 0 ? g.q_scale : 1.0f) / sqrtf(sum + g.eps);
     }
-    __syncthreads();
+    ssm_barrier();
     if (j < DIM) {
         s.qs[j] = s.qs[j] * s.inv[0];
         s.ks[j] = s.ks[j] * s.inv[1];
     }
-    const float alpha = alpha_in + g.dt[h];
+    const float alpha = alpha_in + kc.dt;
     const float softplus = alpha > 20.0f ? alpha : ref_log1pf(ref_expf(alpha));
-    const float decay = ref_expf(softplus * g.a[h]);
+    const float decay = ref_expf(softplus * kc.a);
     const float beta = 1.0f / (1.0f + ref_expf(-beta_in));
-    __syncthreads();
+    ssm_barrier();
     float o = 0.0f;
     if (j < DIM) {
         float sk = 0.0f;
@@ -505,14 +519,14 @@ __device__ __forceinline__ float ssm_step(const SsmArgs& g, SsmLds& s, int h, co
     double sq = j < DIM ? static_cast<double>(o * o) : 0.0;
     sq = wave_sum(sq);
     if ((j & 63) == 0) s.red[j >> 6] = sq;
-    __syncthreads();
+    ssm_barrier();
     const float scale = rms_scale(((s.red[0] + s.red[1]) + s.red[2]) + s.red[3], DIM, g.eps);
     float out = 0.0f;
     if (j < DIM) {
         const float gate = z / (1.0f + ref_expf(-z));
-        out = o * scale * g.norm[j] * gate;
+        out = o * scale * kc.norm * gate;
     }
-    __syncthreads();  // the LDS is the next token's
+    ssm_barrier();  // the LDS is the next token's
     return out;
 }
 
@@ -555,7 +569,7 @@ __global__ __launch_bounds__(kThreads) void k_ssm(SsmArgs g) {
     float cur[3];
     ssm_cur<DIM>(g, h, g.qkv, cur);
     const float z = g.z[h * DIM + (j < DIM ? j : 0)];
-    const float out = ssm_step<DIM>(g, s, h, cur, cv, z, g.ab[h], g.ab[g.heads + h], row);
+    const float out = ssm_step<DIM>(g, s, h, cur, cv, z, g.ab[h], g.ab[g.heads + h], row, ssm_const<DIM>(g, h));
     ssm_row_store<DIM>(g, h, (pos + 1) & 1, row);
     if (j < DIM) {
         g.out[h * DIM + j] = out;
@@ -577,15 +591,28 @@ __global__ __launch_bounds__(kThreads) void k_pre_ssm(SsmArgs g, int pos0, int n
     ssm_row_load<DIM>(g, h, pos0 & 1, pos0 == 0, row);
     SsmConv cv;
     ssm_conv_load<DIM>(g, h, pos0, cv);
+    const SsmConst kc = ssm_const<DIM>(g, h);
+    // token t's rows, z and gates, loaded while token t - 1 steps (the step's barriers leave them in flight)
+    struct In {
+        float cur[3], z, a, b;
+    };
+    auto load_in = [&](int t, In& in) {
+        ssm_cur<DIM>(g, h, g.qkv + static_cast<size_t>(t) * g.qkv_dim, in.cur);
+        in.z = g.z[static_cast<size_t>(t) * inner + h * DIM + (j < DIM ? j : 0)];
+        const float* ab = g.ab + static_cast<size_t>(t) * ab_stride;
+        in.a = ab[h];
+        in.b = ab[g.heads + h];
+    };
+    In in;
+    load_in(0, in);
     for (int t = 0; t < ntok; ++t) {
         const int pos = pos0 + t;
         if (t + 1 == ntok) ssm_row_store<DIM>(g, h, pos & 1, row);
-        float cur[3];
-        ssm_cur<DIM>(g, h, g.qkv + static_cast<size_t>(t) * g.qkv_dim, cur);
-        const float z = g.z[static_cast<size_t>(t) * inner + h * DIM + (j < DIM ? j : 0)];
-        const float* ab = g.ab + static_cast<size_t>(t) * ab_stride;
-        const float out = ssm_step<DIM>(g, s, h, cur, cv, z, ab[h], ab[g.heads + h], row);
+        In next = in;
+        if (t + 1 < ntok) load_in(t + 1, next);
+        const float out = ssm_step<DIM>(g, s, h, in.cur, cv, in.z, in.a, in.b, row, kc);
         if (j < DIM) g.out[static_cast<size_t>(t) * inner + h * DIM + j] = out;
+        in = next;
     }
     ssm_row_store<DIM>(g, h, (pos0 + ntok) & 1, row);
     // the ring: the batch's last taps positions' rows (older slots keep theirs)
