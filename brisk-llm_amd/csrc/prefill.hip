@@ -1542,6 +1542,7 @@ constexpr int kRopeMaxHeads = 16;  // query heads a kv head (as the token path's
 struct RopeLds {
     alignas(16) float q[kRopeMaxHeads * 128];
     float kcur[128], vcur[128];
+    float rope[128];  // this position's RoPE row, loaded with the rows
 };
 __global__ __launch_bounds__(kThreads) void k_pre_rope(PreAttnArgs p) {
     __shared__ RopeLds s;
@@ -1556,8 +1557,11 @@ __global__ __launch_bounds__(kThreads) void k_pre_rope(PreAttnArgs p) {
         s.kcur[i] = k[i];
         s.vcur[i] = g.vbias != nullptr ? v[i] + g.vbias[kv * hd + i] : v[i];
     }
+    const float* rope_row = g.rope != nullptr ? g.rope + static_cast<size_t>(pos) * g.rope_dim : nullptr;
+    if (rope_row != nullptr)  // the table row beside the rows: one round trip, not two
+        for (int i = tid; i < g.rope_dim; i += kThreads) s.rope[i] = rope_row[i];
     __syncthreads();
-    const float* rope = g.rope != nullptr ? g.rope + static_cast<size_t>(pos) * g.rope_dim : nullptr;
+    const float* rope = rope_row != nullptr ? s.rope : nullptr;
     for (int h = tid >> 6; h <= hpk; h += kThreads / 64) {  // a wave a head; the last is the key
         if (h < hpk) head_norm_rope(s.q + h * hd, g.qbias != nullptr ? g.qbias + (kv * hpk + h) * hd : nullptr, g.qnorm, rope, hd, g.rope_dim, g.neox, g.eps);
         else head_norm_rope(s.kcur, g.kbias != nullptr ? g.kbias + kv * hd : nullptr, g.knorm, rope, hd, g.rope_dim, g.neox, g.eps);
@@ -2455,7 +2459,7 @@ hipError_t launch_softcap(float* x, size_t n, float cap, hipStream_t s) {
 hipError_t launch_pre_attention(const PreAttnArgs& p, int ntok, hipStream_t s) {
     if (ntok <= 0) return hipSuccess;
     const dim3 grid(ntok, p.a.kv_heads);
-    if (p.a.heads / p.a.kv_heads > kRopeMaxHeads || p.a.head_dim > 128) return hipErrorInvalidValue;
+    if (p.a.heads / p.a.kv_heads > kRopeMaxHeads || p.a.head_dim > 128 || p.a.rope_dim > 128) return hipErrorInvalidValue;
     hipLaunchKernelGGL(k_pre_rope, grid, dim3(kThreads), 0, s, p);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
