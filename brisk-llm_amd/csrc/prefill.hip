@@ -829,16 +829,19 @@ __device__ __forceinline__ void kq_compute_fold(const KqBases& base, MmAcc<G>& a
     v4i alo[4], ahi[4], amn[4];
 #pragma unroll
     for (int g = 0; g < G; ++g) alo[g] = ahi[g] = amn[g] = zero;
-    const bool hi_nib = l16 >= 2;  // lanes 32..63: the odd sub-block of the pair (high nibbles)
+    // lanes 32..63 take the odd sub-block of the pair (high nibbles): a shift by 4, not a select
+    const uint32_t nib_shift = l16 >= 2 ? 4u : 0u;
+    const uint32_t lane_byte = static_cast<uint32_t>(l16 >> 1) * 0x01010101u;
 #pragma unroll
     for (int st = 0; st < 4; ++st) {
         KqF64 nxt;
         if (st < 3) nxt = kq_f64_issue<G>(base, st + 1, ar, tl, l16);
-        const int j = 2 * st + (l16 >> 1);  // this lane's sub-block
-        const uint32_t sc = ((j < 4 ? scm.x : scm.y) >> (8 * (j & 3))) & 0xFF;
-        const uint32_t mn = ((j < 4 ? scm.z : scm.w) >> (8 * (j & 3))) & 0xFF;
-        const uint32_t dlo = sc & 7, dhi = sc >> 3, m4 = mn * 0x01010101u;
-        const v4u qn = hi_nib ? ((cur.a >> 4) & 0x0F0F0F0Fu) : (cur.a & 0x0F0F0F0Fu);
+        const int j = 2 * st + (l16 >> 1);  // this lane's sub-block (j < 4 exactly when st < 2)
+        const uint32_t sc = ((st < 2 ? scm.x : scm.y) >> (8 * (j & 3))) & 0xFF;
+        // the min byte of sub-block j in all four bytes (v_perm_b32: byte j & 3 of the word, four times)
+        const uint32_t m4 = __builtin_amdgcn_perm(0u, st < 2 ? scm.z : scm.w, lane_byte + static_cast<uint32_t>((2 * st) & 3) * 0x01010101u);
+        const uint32_t dlo = sc & 7, dhi = sc >> 3;
+        const v4u qn = (cur.a >> nib_shift) & 0x0F0F0F0Fu;
         const v4u qlo = mul_bytes(qn, dlo);  // bytes 0..15 times 0..7: no carries between bytes
         const v4u qhi = mul_bytes(qn, dhi);
         const v4u qmn = {m4, m4, m4, m4};
@@ -1166,7 +1169,7 @@ __device__ __forceinline__ void mx_compute(uint32_t base, const MxA<KM>& a, floa
             lo = mfma32(a.f[2 * s], b[s], lo);
             hi = mfma32(a.f[2 * s + 1], b[s], hi);
             if constexpr (KM) {
-                const uint32_t m4 = ((a.mn[s >> 2] >> (8 * (s & 3))) & 0xFF) * 0x01010101u;
+                const uint32_t m4 = __builtin_amdgcn_perm(0u, a.mn[s >> 2], static_cast<uint32_t>(s & 3) * 0x01010101u);  // byte s & 3, four times
                 mo = mfma32(v4u{m4, m4, m4, m4}, b[s], mo);
             }
         }
