@@ -206,8 +206,8 @@ struct SpreadStage2 {
     alignas(16) float sc[kSpreadScores];         // scores, then weights: [head][position, rows padded to 8]
     alignas(16) uint16_t vraw[2][kSpreadStage * kSpreadSlice];  // cached values of two chunks [position][dim]
     alignas(16) uint16_t vt[2][kSpreadSlice * kVtStride];       // the same, transposed [dim][position]
-    float mx[4];
-    double red[4];
+    float mx[kSpreadHpk][4];     // [head][wave]
+    double red[kSpreadHpk][4];
 };
 union SpreadLds {
     SpreadStage1 s1;
@@ -942,6 +942,52 @@ __device__ __forceinline__ float value_chain(const float* w, const uint16_t* vro
     return acc;
 }
 
+// The whole workgroup's softmax of H heads' long rows, all heads in each pass: one barrier a
+// pass for all of them, and the heads' exp chains interleaved.  Each head's max, exps, partial
+// sums (thread t: positions t, t + 256, ..; then the wave sum; then the four waves in order)
+// and scale are what it gets on its own.
+template <int H>
+__device__ __forceinline__ void spread_softmax_long(SpreadStage2& s, int Ls, int Lc) {
+    const int t = threadIdx.x, wave = t >> 6, lane = t & 63;
+    float m[H];
+#pragma unroll
+    for (int h = 0; h < H; ++h) m[h] = -INFINITY;
+    for (int p = t; p < Lc; p += kThreads)
+#pragma unroll
+        for (int h = 0; h < H; ++h) m[h] = fmaxf(m[h], s.sc[h * Ls + p]);
+#pragma unroll
+    for (int h = 0; h < H; ++h) {
+        m[h] = wave_max(m[h]);
+        if (lane == 0) s.mx[h][wave] = m[h];
+    }
+    __syncthreads();
+    double part[H];
+#pragma unroll
+    for (int h = 0; h < H; ++h) {
+        m[h] = fmaxf(fmaxf(s.mx[h][0], s.mx[h][1]), fmaxf(s.mx[h][2], s.mx[h][3]));
+        part[h] = 0.0;
+    }
+    for (int p = t; p < Lc; p += kThreads)
+#pragma unroll
+        for (int h = 0; h < H; ++h) {
+            const float e = ref_expf_s(s.sc[h * Ls + p] - m[h]);
+            s.sc[h * Ls + p] = e;
+            part[h] += static_cast<double>(e);
+        }
+#pragma unroll
+    for (int h = 0; h < H; ++h) {
+        part[h] = wave_sum(part[h]);
+        if (lane == 0) s.red[h][wave] = part[h];
+    }
+    __syncthreads();
+    float scale[H];
+#pragma unroll
+    for (int h = 0; h < H; ++h) scale[h] = static_cast<float>(1.0 / (((s.red[h][0] + s.red[h][1]) + s.red[h][2]) + s.red[h][3]));
+    for (int p = t; p < Lc; p += kThreads)
+#pragma unroll
+        for (int h = 0; h < H; ++h) s.sc[h * Ls + p] *= scale[h];
+}
+
 template <class O>
 __device__ __forceinline__ bool spread_stage2(const LoopArgs& g, const AttnArgs& a, SpreadStage2& s, int kv, int d0, int pos,
                                               unsigned tin, unsigned tsc, const O& o, const Stamps& st) {
@@ -1073,26 +1119,11 @@ __device__ __forceinline__ bool spread_stage2(const LoopArgs& g, const AttnArgs&
             for (int p = lane; p < Lc; p += 64) sc[p] *= scale;
         }
     } else {
-        for (int h = 0; h < hpk; ++h) {
-            float* sc = s.sc + h * Ls;
-            float m = -INFINITY;
-            for (int p = t; p < Lc; p += kThreads) m = fmaxf(m, sc[p]);
-            m = wave_max(m);
-            if (lane == 0) s.mx[wave] = m;
-            __syncthreads();
-            m = fmaxf(fmaxf(s.mx[0], s.mx[1]), fmaxf(s.mx[2], s.mx[3]));
-            double part = 0.0;
-            for (int p = t; p < Lc; p += kThreads) {
-                const float e = ref_expf_s(sc[p] - m);
-                sc[p] = e;
-                part += static_cast<double>(e);
-            }
-            part = wave_sum(part);
-            if (lane == 0) s.red[wave] = part;
-            __syncthreads();
-            const float scale = static_cast<float>(1.0 / (((s.red[0] + s.red[1]) + s.red[2]) + s.red[3]));
-            for (int p = t; p < Lc; p += kThreads) sc[p] *= scale;
-            __syncthreads();
+        switch (hpk) {
+            case 1: spread_softmax_long<1>(s, Ls, Lc); break;
+            case 2: spread_softmax_long<2>(s, Ls, Lc); break;
+            case 3: spread_softmax_long<3>(s, Ls, Lc); break;
+            default: spread_softmax_long<4>(s, Ls, Lc); break;
         }
     }
     __syncthreads();
