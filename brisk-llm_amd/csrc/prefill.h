@@ -67,6 +67,12 @@ struct PreAttnArgs {
     int pos0;        // position of token 0
     int legacy;      // 1: the staged-chunk exact kernel (k_pre_attn_blk) in place of k_pre_attn_rows
     int mfma;        // 1: prompts of kFaMinTok tokens or more take the MFMA attention (not order-exact)
+    // When qout.qs is set and the launch takes k_pre_attn_rows with heads-per-kv x head_dim = 256,
+    // that kernel also writes each (token, kv head)'s output as the 256-value activation block kv of
+    // qout (Q8_K when q8k, else Q8_0; qbits as act_bits), and launch_pre_attention reports it in
+    // *quantised.  Otherwise qout is untouched and the caller quantises out itself.
+    ActPlanar qout;
+    int q8k, qbits;
 };
 
 // Shapes the MFMA prefill attention (opt-in) takes: 64 query rows a workgroup.
@@ -100,6 +106,6 @@ hipError_t launch_pre_conv(const float* bcx, uint16_t* cache, const float* w, in
                            hipStream_t s);
 // x[i] = cap tanh(x[i] / cap) (Gemma's final logit soft-capping)
 hipError_t launch_softcap(float* x, size_t n, float cap, hipStream_t s);
-hipError_t launch_pre_attention(const PreAttnArgs& p, int ntok, hipStream_t s);
+hipError_t launch_pre_attention(const PreAttnArgs& p, int ntok, hipStream_t s, bool* quantised = nullptr);
 
 }  // namespace bh

@@ -2010,6 +2010,24 @@ __global__ __launch_bounds__(kThreads) void k_pre_attn_rows(PreAttnArgs p, int n
             *reinterpret_cast<float2*>(o) = make_float2(acc0[k], acc1[k]);
         }
     }
+    // The O projection's activation blocks: token tt's hpk heads of this kv head are values
+    // kv * 256 .. kv * 256 + 255 of its row, one whole block, quantised here (as k_pre_quant_blocks
+    // does from the stored rows) instead of by a separate launch.  s.q is free: its last reads
+    // (the scores) are behind the softmax's barriers.
+    if (p.qout.qs != nullptr && hpk * HD == 256) {
+#pragma unroll
+        for (int k = 0; k < NR; ++k) {
+            const int row = rg + k * RG;
+            if (row < rows) *reinterpret_cast<float2*>(s.q + row * HD + 2 * dp) = make_float2(acc0[k], acc1[k]);
+        }
+        __syncthreads();
+        for (int tt = wave; tt < ntb; tt += kThreads / 64) {
+            const float4 x = *reinterpret_cast<const float4*>(s.q + tt * 256 + 4 * wl);
+            const float v[4] = {x.x, x.y, x.z, x.w};
+            if (p.q8k) pre_quant_block<true>(v, tb0 + tt, kv, p.qbits, p.qout);
+            else pre_quant_block<false>(v, tb0 + tt, kv, p.qbits, p.qout);
+        }
+    }
 }
 
 // ---------------------------------------------------------------- long-prompt attention on MFMA
@@ -2459,7 +2477,8 @@ hipError_t launch_softcap(float* x, size_t n, float cap, hipStream_t s) {
     return hipGetLastError();
 }
 
-hipError_t launch_pre_attention(const PreAttnArgs& p, int ntok, hipStream_t s) {
+hipError_t launch_pre_attention(const PreAttnArgs& p, int ntok, hipStream_t s, bool* quantised) {
+    if (quantised != nullptr) *quantised = false;
     if (ntok <= 0) return hipSuccess;
     const dim3 grid(ntok, p.a.kv_heads);
     if (p.a.heads / p.a.kv_heads > kRopeMaxHeads || p.a.head_dim > 128 || p.a.rope_dim > 128) return hipErrorInvalidValue;
@@ -2477,6 +2496,7 @@ hipError_t launch_pre_attention(const PreAttnArgs& p, int ntok, hipStream_t s) {
         const dim3 xgrid(((ntok + kPxRows / hpk - 1) / (kPxRows / hpk)) * p.a.kv_heads);
         if (hd == 64) hipLaunchKernelGGL((k_pre_attn_rows<64, kPxRows, kPaMaxL>), xgrid, dim3(kThreads), 0, s, p, ntok);
         else hipLaunchKernelGGL((k_pre_attn_rows<128, kPxRows, kPaMaxL>), xgrid, dim3(kThreads), 0, s, p, ntok);
+        if (quantised != nullptr) *quantised = p.qout.qs != nullptr && hpk * hd == 256;
     } else if (p.a.window == 0 && hpk <= kPaRows && (p.a.head_dim == 32 || p.a.head_dim == 64 || p.a.head_dim == 128) &&
         p.pos0 + ntok <= kPaMaxL) {
         const int tpb = kPaRows / hpk;

@@ -1365,6 +1365,7 @@ void Session::prefill_layers(size_t pos0, int T) {
             // Q, K, V of attn_norm(h) (src/model.cpp:996-1015), at the layer's head size and key/value
             // heads (Gemma 4: a shared layer projects Q only; K may serve as V)
             const int qdl = static_cast<int>(cfg_.heads) * L.hd, kvdl = L.kvh * L.hd;
+            bool o_quantised = false;  // the attention wrote O's activation blocks
             const bool own_kv = L.kv_src == static_cast<int>(l);
             prefill_quant(pre_h_, e, L.attn_norm, e, T, L.q);
             g.m = L.q.p; set_mx(g, L.q); g.out = pre_q_; g.ostride = qdl;
@@ -1414,10 +1415,13 @@ void Session::prefill_layers(size_t pos0, int T) {
             pa.qstride = qd; pa.kvstride = kvd; pa.pos0 = static_cast<int>(pos0);
             pa.mfma = prefill_mfma_ ? 1 : 0;
             pa.legacy = prefill_legacy_ ? 1 : 0;
-            check(launch_pre_attention(pa, T, stream_), "prefill attention");
+            if (L.attn_sub_norm == nullptr && qdl == qd) {  // the attention may quantise O's input itself
+                pa.qout = pre_x_; pa.q8k = takes_q8_k(L.o.p.type) ? 1 : 0; pa.qbits = act_bits(L.o.p);
+            }
+            check(launch_pre_attention(pa, T, stream_, &o_quantised), "prefill attention");
             }
             // h += O (sub-normed) att (:1095-1111)
-            prefill_quant(pre_att_, qdl, L.attn_sub_norm, qdl, T, L.o);
+            if (!o_quantised) prefill_quant(pre_att_, qdl, L.attn_sub_norm, qdl, T, L.o);
             g.m = L.o.p; set_mx(g, L.o); g.out = L.attn_post_norm ? pre_proj_ : pre_h_; g.ostride = e;
             check(launch_mm(g, L.attn_post_norm ? kMmStore : kMmAdd, stream_), "prefill o");
             if (L.attn_post_norm)  // h += rms_norm(O att, post_attention_norm) (:1113-1121)
